@@ -1,0 +1,110 @@
+/*
+ * lizard_hip.h -- C ABI of the MI355X (gfx950) Lizard attention hot path.
+ *
+ * Library: lizard_reproduction_amd/_lib/liblizard_hip.so (hipcc --offload-arch=gfx950).
+ *
+ * Conventions for every entry point:
+ *   - tensors are device pointers to contiguous row-major buffers;
+ *     [BH, L, X] means batch*heads rows of length*X elements, the layout of a
+ *     contiguous torch tensor of shape [B, H, L, X];
+ *   - "bf16" buffers hold bfloat16, "f32" buffers float;
+ *   - the library never allocates device memory: outputs, saved tensors and
+ *     workspaces are owned by the caller (the reference's autograd Functions
+ *     own theirs the same way, src/kernels/gla.py:221-225, swa.py:144-146);
+ *   - work is enqueued on `stream` (a hipStream_t; NULL = default stream) and
+ *     the call returns without synchronising;
+ *   - return value 0 = success; otherwise an error code, with a message
+ *     available from lz_last_error() on the calling thread.
+ *
+ * The reference (mahdikhashan/lizard-reproduction) is pure Python + Triton; the
+ * functions below replace its Triton launches.  Each comment names the
+ * reference code the entry point stands in for.
+ */
+#ifndef LIZARD_HIP_H
+#define LIZARD_HIP_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LZ_ABI_VERSION 1
+
+/* ABI version of the loaded library (LZ_ABI_VERSION). */
+int lz_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* lz_last_error(void);
+
+/*
+ * GLA forward.  Replaces kernels.gla's forward: the gate cumsum and head
+ * expand (src/kernels/gla.py:259-263) and the two launches of _GLA.forward,
+ * _gla_fwd_h + _gla_fwd_o (src/kernels/gla.py:213-234).
+ *   fq, fk      bf16 [BH, L, nf]      feature-mapped queries / keys
+ *   v           bf16 [BH, L, nd]
+ *   log_gamma   f32  [B, L] (gate_per_head = 0) or [B, H, L] (gate_per_head = 1);
+ *               log of the gate (<= 0), NOT its cumsum
+ *   y           bf16 [BH, L, nd]      output
+ *   chunk       tiling hint of the reference API (power of two >= 16); the
+ *               kernels always walk 64-token chunks, results are
+ *               chunk-independent up to rounding
+ * Supported sizes: nf <= 256, nd <= 128, and nd <= 64 when nf > 128.
+ * Nothing is saved for the backward: lz_gla_bwd recomputes what it needs, so
+ * the output is the same with and without autograd (tests/test_kernels.py:102-107).
+ */
+int lz_gla_fwd(const void* fq, const void* fk, const void* v, const float* log_gamma, void* y,
+               int batch, int heads, int length, int nf, int nd, int gate_per_head, int chunk,
+               void* stream);
+
+/* Workspace bytes lz_gla_bwd needs for these sizes. */
+size_t lz_gla_bwd_workspace_bytes(int batch, int heads, int length, int nf, int nd,
+                                  int gate_per_head, int chunk);
+
+/*
+ * GLA backward.  Replaces _GLA.backward (src/kernels/gla.py:236-256): delta,
+ * _gla_bwd_dh, _gla_bwd_dqkv, the dg reduction, and the autograd steps of
+ * the gate path (expand-sum over heads, reverse cumsum, gla.py:260-262).
+ *   dy          bf16 [BH, L, nd]      upstream gradient
+ *   dfq, dfk    [BH, L, nf], dv [BH, L, nd]: bf16 if grad_bf16 else f32
+ *   dlog_gamma  f32, same shape as log_gamma
+ * The other arguments are those of lz_gla_fwd.
+ */
+int lz_gla_bwd(const void* fq, const void* fk, const void* v, const float* log_gamma,
+               const void* dy, void* dfq, void* dfk, void* dv, float* dlog_gamma, int grad_bf16,
+               int batch, int heads, int length, int nf, int nd, int gate_per_head, int chunk,
+               void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * SWA forward.  Replaces _SWA.forward / _swa_fwd (src/kernels/swa.py:136-156,
+ * 19-59).
+ *   q, k, v     bf16 [BH, L, dim]  (RoPE already applied to q and k)
+ *   meta        f32 [n_meta] sink logits (n_meta may be 0; at most 64)
+ *   y           bf16 [BH, L, dim] output;  lse  f32 [BH, L] (saved for backward)
+ *   window      keys i-window < t <= i;  scale  usually 1/sqrt(dim)
+ * Supported sizes: dim <= 256.
+ */
+int lz_swa_fwd(const void* q, const void* k, const void* v, const float* meta, int n_meta,
+               void* y, float* lse, int batch, int heads, int length, int dim, int window,
+               float scale, void* stream);
+
+/* Workspace bytes lz_swa_bwd needs for these sizes. */
+size_t lz_swa_bwd_workspace_bytes(int batch, int heads, int length, int dim, int n_meta);
+
+/*
+ * SWA backward.  Replaces _SWA.backward (src/kernels/swa.py:158-179): delta,
+ * _swa_bwd_q, _swa_bwd_kv and the dmeta reduction.
+ *   y, lse      from lz_swa_fwd;  dy  bf16 [BH, L, dim]
+ *   dq, dk, dv  [BH, L, dim]: bf16 if grad_bf16 else f32
+ *   dmeta       f32 [n_meta] (untouched when n_meta == 0)
+ */
+int lz_swa_bwd(const void* q, const void* k, const void* v, const float* meta, int n_meta,
+               const void* y, const float* lse, const void* dy, void* dq, void* dk, void* dv,
+               float* dmeta, int grad_bf16, int batch, int heads, int length, int dim,
+               int window, float scale, void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LIZARD_HIP_H */

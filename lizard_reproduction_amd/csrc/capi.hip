@@ -1,0 +1,165 @@
+// extern "C" entry points of liblizard_hip.so; declarations and the
+// reference code each one replaces are in include/lizard_hip.h.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <string>
+
+#include "../../include/lizard_hip.h"
+#include "common.hpp"
+
+namespace lz {
+hipError_t launch_gla_fwd(const void* fq, const void* fk, const void* v, const float* lg, void* y,
+                          int B, int H, int L, int F, int D, int gate_per_head, hipStream_t st);
+hipError_t launch_gla_bwd(const void* fq, const void* fk, const void* v, const float* lg,
+                          const void* dy, void* dfq, void* dfk, void* dv, float* dlg,
+                          bool grad_bf16, int B, int H, int L, int F, int D, int gate_per_head,
+                          float* ws, hipStream_t st);
+size_t gla_bwd_workspace(int B, int H, int L);
+bool gla_dims_supported(int F, int D);
+int swa_padded_dim(int d);
+hipError_t launch_swa_fwd(const void* q, const void* k, const void* v, const float* meta,
+                          int n_meta, void* y, float* lse, int BH, int L, int d, int W, float scale,
+                          hipStream_t st);
+hipError_t launch_swa_bwd(const void* q, const void* k, const void* v, const float* meta,
+                          int n_meta, const void* y, const float* lse, const void* dy, void* dq,
+                          void* dk, void* dv, bool grad_bf16, float* dmeta_part, int BH, int L,
+                          int d, int W, float scale, hipStream_t st);
+constexpr int MAX_META = 64;
+
+// Sum of the per-block dmeta partials [rows, n_meta] in a fixed order.
+__global__ void dmeta_reduce_kernel(const float* __restrict__ part, float* __restrict__ dmeta,
+                                    int rows, int n_meta) {
+  const int j = threadIdx.x;
+  if (j >= n_meta) return;
+  float s = 0.f;
+  for (int r = 0; r < rows; ++r) s += part[(size_t)r * n_meta + j];
+  dmeta[j] = s;
+}
+}  // namespace lz
+
+static thread_local std::string g_err;
+
+static int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+static int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+static int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) {
+    g_err.clear();
+    return 0;
+  }
+  return fail((int)e, "%s: HIP error %d (%s)", what, (int)e, hipGetErrorString(e));
+}
+
+static bool pow2_at_least_16(int c) { return c >= 16 && (c & (c - 1)) == 0; }
+
+extern "C" int lz_abi_version(void) { return LZ_ABI_VERSION; }
+
+extern "C" const char* lz_last_error(void) { return g_err.c_str(); }
+
+static int check_gla(const void* fq, const void* fk, const void* v, const float* lg, int batch,
+                     int heads, int length, int nf, int nd, int chunk) {
+  if (!fq || !fk || !v || !lg) return fail(1, "gla: null input pointer");
+  if (batch <= 0 || heads <= 0 || length <= 0 || nf <= 0 || nd <= 0)
+    return fail(1, "gla: sizes must be positive (B=%d H=%d L=%d F=%d D=%d)", batch, heads,
+                length, nf, nd);
+  if (!pow2_at_least_16(chunk)) return fail(1, "gla: chunk must be a power of two >= 16, got %d", chunk);
+  if (!lz::gla_dims_supported(nf, nd))
+    return fail(1, "gla: unsupported feature/value dims F=%d D=%d (need F<=256, D<=128, "
+                   "and D<=64 when F>128)", nf, nd);
+  return 0;
+}
+
+extern "C" int lz_gla_fwd(const void* fq, const void* fk, const void* v, const float* log_gamma,
+                          void* y, int batch, int heads, int length, int nf, int nd,
+                          int gate_per_head, int chunk, void* stream) {
+  if (int rc = check_gla(fq, fk, v, log_gamma, batch, heads, length, nf, nd, chunk)) return rc;
+  if (!y) return fail(1, "gla_fwd: null output pointer");
+  return hip_status(lz::launch_gla_fwd(fq, fk, v, log_gamma, y, batch, heads, length, nf, nd,
+                                       gate_per_head ? 1 : 0, (hipStream_t)stream),
+                    "gla_fwd");
+}
+
+extern "C" size_t lz_gla_bwd_workspace_bytes(int batch, int heads, int length, int nf, int nd,
+                                             int gate_per_head, int chunk) {
+  (void)nf; (void)nd; (void)gate_per_head; (void)chunk;
+  if (batch <= 0 || heads <= 0 || length <= 0) return 0;
+  return lz::gla_bwd_workspace(batch, heads, length);
+}
+
+extern "C" int lz_gla_bwd(const void* fq, const void* fk, const void* v, const float* log_gamma,
+                          const void* dy, void* dfq, void* dfk, void* dv, float* dlog_gamma,
+                          int grad_bf16, int batch, int heads, int length, int nf, int nd,
+                          int gate_per_head, int chunk, void* workspace, size_t workspace_bytes,
+                          void* stream) {
+  if (int rc = check_gla(fq, fk, v, log_gamma, batch, heads, length, nf, nd, chunk)) return rc;
+  if (!dy || !dfq || !dfk || !dv || !dlog_gamma) return fail(1, "gla_bwd: null pointer");
+  const size_t need = lz::gla_bwd_workspace(batch, heads, length);
+  if (!workspace || workspace_bytes < need)
+    return fail(1, "gla_bwd: workspace of %zu bytes given, %zu needed", workspace_bytes, need);
+  return hip_status(lz::launch_gla_bwd(fq, fk, v, log_gamma, dy, dfq, dfk, dv, dlog_gamma,
+                                       grad_bf16 != 0, batch, heads, length, nf, nd,
+                                       gate_per_head ? 1 : 0, (float*)workspace,
+                                       (hipStream_t)stream),
+                    "gla_bwd");
+}
+
+static int check_swa(const void* q, const void* k, const void* v, const float* meta, int n_meta,
+                     int batch, int heads, int length, int dim, int window) {
+  if (!q || !k || !v) return fail(1, "swa: null input pointer");
+  if (n_meta < 0 || n_meta > lz::MAX_META)
+    return fail(1, "swa: n_meta must be in [0, %d], got %d", lz::MAX_META, n_meta);
+  if (n_meta > 0 && !meta) return fail(1, "swa: null meta pointer");
+  if (batch <= 0 || heads <= 0 || length <= 0 || dim <= 0)
+    return fail(1, "swa: sizes must be positive (B=%d H=%d L=%d d=%d)", batch, heads, length, dim);
+  if (window <= 0) return fail(1, "swa: window must be positive, got %d", window);
+  if (lz::swa_padded_dim(dim) < 0) return fail(1, "swa: head dim %d > 256 unsupported", dim);
+  return 0;
+}
+
+extern "C" int lz_swa_fwd(const void* q, const void* k, const void* v, const float* meta,
+                          int n_meta, void* y, float* lse, int batch, int heads, int length,
+                          int dim, int window, float scale, void* stream) {
+  if (int rc = check_swa(q, k, v, meta, n_meta, batch, heads, length, dim, window)) return rc;
+  if (!y || !lse) return fail(1, "swa_fwd: null output pointer");
+  return hip_status(lz::launch_swa_fwd(q, k, v, meta, n_meta, y, lse, batch * heads, length, dim,
+                                       window, scale, (hipStream_t)stream),
+                    "swa_fwd");
+}
+
+extern "C" size_t lz_swa_bwd_workspace_bytes(int batch, int heads, int length, int dim,
+                                             int n_meta) {
+  (void)dim;
+  if (batch <= 0 || heads <= 0 || length <= 0 || n_meta <= 0) return 0;
+  const size_t nb = (size_t)(length + 127) / 128;
+  return (size_t)batch * heads * nb * n_meta * sizeof(float);
+}
+
+extern "C" int lz_swa_bwd(const void* q, const void* k, const void* v, const float* meta,
+                          int n_meta, const void* y, const float* lse, const void* dy, void* dq,
+                          void* dk, void* dv, float* dmeta, int grad_bf16, int batch, int heads,
+                          int length, int dim, int window, float scale, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+  if (int rc = check_swa(q, k, v, meta, n_meta, batch, heads, length, dim, window)) return rc;
+  if (!y || !lse || !dy || !dq || !dk || !dv) return fail(1, "swa_bwd: null pointer");
+  if (n_meta > 0 && !dmeta) return fail(1, "swa_bwd: null dmeta pointer");
+  const size_t need = lz_swa_bwd_workspace_bytes(batch, heads, length, dim, n_meta);
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(1, "swa_bwd: workspace of %zu bytes given, %zu needed", workspace_bytes, need);
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e = lz::launch_swa_bwd(q, k, v, meta, n_meta, y, lse, dy, dq, dk, dv, grad_bf16 != 0,
+                                    (float*)workspace, batch * heads, length, dim, window, scale, st);
+  if (e != hipSuccess || n_meta == 0) return hip_status(e, "swa_bwd");
+  const int rows = batch * heads * ((length + 127) / 128);
+  hipLaunchKernelGGL(lz::dmeta_reduce_kernel, dim3(1), dim3(64), 0, st, (const float*)workspace,
+                     dmeta, rows, n_meta);
+  return hip_status(hipGetLastError(), "swa_bwd dmeta");
+}

@@ -1,0 +1,128 @@
+// Shared device helpers for the Lizard attention kernels (gfx950 / CDNA4).
+//
+// Every contraction is a bf16 MFMA v_mfma_f32_32x32x16_bf16 with fp32
+// accumulation.  Operand layout of that instruction (lane l of a 64-wide
+// wave, h = l / 32):
+//   A (32 x 16):  lane holds row  l % 32, k-slots j = 0..7
+//   B (16 x 32):  lane holds col  l % 32, k-slots j = 0..7
+//   D (32 x 32):  lane holds col  l % 32, register r holds row acc_row(r, h)
+// The hardware pairs k-slot j of A with k-slot j of B; which k index a slot
+// carries is a free choice as long as A and B agree.  This code uses
+//   slot j of lane half h  <->  k = 8*(j/4) + 4*h + (j%4)   (within a 16-block)
+// because that is exactly the row order of an accumulator: registers
+// 8*kb .. 8*kb+7 of a 32x32 accumulator are the A/B operand of the k-block kb
+// of a following product that contracts over the accumulator's rows.  So
+// scores never leave registers on their way to P*V, and the GLA state never
+// leaves registers on its way to Q~ S.
+//
+// LDS tiles store each 16-element k-block in "slot order" (storage position
+// pidx(k), bits 2 and 3 of k swapped), so one 16-byte read at storage offset
+// 16*kb + 8*h yields the operand of k-block kb for lane half h.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace lz {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int WAVE = 64;
+constexpr float TINY = 1.1754943508222875e-38f;   // FLT_MIN, the reference's clamp
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr float LN2 = 0.6931471805599453f;
+constexpr float NEG_INF = -__builtin_huge_valf();
+
+__device__ __forceinline__ f32x16 mfma(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// Row (M index) held by accumulator register r in lane half h.
+__host__ __device__ __forceinline__ constexpr int acc_row(int r, int h) {
+  return ((r >> 2) << 3) + (h << 2) + (r & 3);
+}
+
+// Storage position of k inside its 16-block: swap bits 2 and 3 (an involution).
+__host__ __device__ __forceinline__ constexpr int pidx(int k) {
+  return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1);
+}
+
+__device__ __forceinline__ float fexp(float x) { return __builtin_amdgcn_exp2f(x * LOG2E); }
+__device__ __forceinline__ float flog(float x) { return __builtin_amdgcn_logf(x) * LN2; }
+
+__device__ __forceinline__ bf16 to_bf16(float x) { return static_cast<bf16>(x); }
+__device__ __forceinline__ float to_f32(bf16 x) { return static_cast<float>(x); }
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.f;
+  return z;
+}
+
+__device__ __forceinline__ bf16x8 zero_bf8() {
+  bf16x8 z;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) z[i] = to_bf16(0.f);
+  return z;
+}
+
+// Registers 8*kb .. 8*kb+7 of an accumulator as a bf16 operand.
+__device__ __forceinline__ bf16x8 acc_operand(const f32x16& acc, int kb) {
+  bf16x8 o;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) o[j] = to_bf16(acc[8 * kb + j]);
+  return o;
+}
+
+// Elements [c, c+4) of row `row` of a row-major [nrows x ncols] bf16 matrix,
+// zero outside it.  Vector path when the row pitch keeps 8-byte alignment.
+__device__ __forceinline__ bf16x4 load4(const bf16* __restrict__ p, int row, int c,
+                                        int nrows, int ncols) {
+  bf16x4 out;
+  if (row < nrows && c + 3 < ncols && (ncols & 3) == 0) {
+    out = *reinterpret_cast<const bf16x4*>(p + (size_t)row * ncols + c);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      out[e] = (row < nrows && c + e < ncols) ? p[(size_t)row * ncols + c + e] : to_bf16(0.f);
+  }
+  return out;
+}
+
+// Store 4 consecutive fp32 values as OutT (bf16 or float) at [row][c..c+4),
+// clipped to ncols.
+template <typename OutT>
+__device__ __forceinline__ void store4(OutT* __restrict__ p, int row, int c, int ncols,
+                                       float a, float b, float cc, float d) {
+  float v[4] = {a, b, cc, d};
+  OutT* q = p + (size_t)row * ncols + c;
+  if (c + 3 < ncols && (ncols & 3) == 0) {
+    if constexpr (sizeof(OutT) == 2) {
+      bf16x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = to_bf16(v[e]);
+      *reinterpret_cast<bf16x4*>(q) = o;
+    } else {
+      f32x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = v[e];
+      *reinterpret_cast<f32x4*>(q) = o;
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (c + e < ncols) {
+        if constexpr (sizeof(OutT) == 2) q[e] = to_bf16(v[e]);
+        else q[e] = v[e];
+      }
+  }
+}
+
+// Exchange with the other half of the wave (lane ^ 32).
+__device__ __forceinline__ float xhalf(float x) { return __shfl_xor(x, 32); }
+
+}  // namespace lz

@@ -1,0 +1,207 @@
+"""Operator API of the Lizard attention hot path on MI355X (gfx950).
+
+Drop-in for the reference's ``kernels`` package (``src/kernels/__init__.py``):
+
+* ``gla(fq, fk, v, log_gamma, chunk=64)``  -- ``src/kernels/gla.py:259-263``
+* ``swa(q, k, v, meta, window, fwd_blocks=(64, 64), bwd_blocks=(64, 64))``
+  -- ``src/kernels/swa.py:182-183``
+
+Same signatures, shapes and conventions: tensors are ``[B, H, L, .]``; inputs
+of any float dtype are cast to bf16; outputs are bf16; gradients come back in
+each input's dtype; the gate is ``[B, L]`` (one per token, shared by heads) or
+``[B, H, L]`` (one per head).  ``chunk`` and ``*_blocks`` are tiling hints in
+the reference; results do not depend on them beyond rounding, and the HIP
+kernels always use their own tiles (64-token GLA chunks, 32-row SWA tiles).
+
+Every call goes through the C ABI of ``liblizard_hip.so`` on the current HIP
+stream; there is no CPU or PyTorch fallback.
+"""
+import math
+
+import torch
+
+from . import _lib
+
+CHUNK = 64
+FWD_BLOCKS = (64, 64)
+BWD_BLOCKS = (64, 64)
+
+
+def _stream(t):
+    return ctypes_ptr(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def ctypes_ptr(x):
+    return x if isinstance(x, int) else int(x)
+
+
+def _ptr(t):
+    return t.data_ptr() if t is not None and t.numel() else None
+
+
+def _require_gpu(*tensors):
+    for t in tensors:
+        if not t.is_cuda:
+            raise ValueError("lizard_reproduction_amd kernels need tensors on a ROCm GPU "
+                             f"(got a tensor on {t.device})")
+
+
+def _bf16(t):
+    return t.to(torch.bfloat16).contiguous()
+
+
+# ---------------------------------------------------------------------------
+# gated linear attention
+# ---------------------------------------------------------------------------
+
+def _check_gla(fq, fk, v, log_gamma, chunk):
+    if fq.dim() != 4 or fk.shape != fq.shape:
+        raise ValueError(f"gla: fq and fk must be [B, H, L, F] of one shape, got "
+                         f"{tuple(fq.shape)} and {tuple(fk.shape)}")
+    if v.dim() != 4 or v.shape[:3] != fq.shape[:3]:
+        raise ValueError(f"gla: v must be [B, H, L, D] matching fq, got {tuple(v.shape)}")
+    b, h, length, _ = fq.shape
+    if tuple(log_gamma.shape) not in ((b, length), (b, h, length)):
+        raise ValueError(f"gla: log_gamma must be [B, L] or [B, H, L], got "
+                         f"{tuple(log_gamma.shape)} for fq {tuple(fq.shape)}")
+    if not isinstance(chunk, int) or chunk < 16 or chunk & (chunk - 1):
+        raise ValueError(f"gla: chunk must be a power of two >= 16, got {chunk!r}")
+    _require_gpu(fq, fk, v, log_gamma)
+
+
+class _GLA(torch.autograd.Function):
+    """Autograd node of ``gla``; mirrors ``_GLA`` (src/kernels/gla.py:213-256),
+    but takes log_gamma itself: its cumsum, head expand and their gradients
+    run inside the kernels."""
+
+    @staticmethod
+    def forward(ctx, fq, fk, v, log_gamma, chunk):
+        ctx.dtypes = (fq.dtype, fk.dtype, v.dtype, log_gamma.dtype)
+        fq, fk, v = _bf16(fq), _bf16(fk), _bf16(v)
+        lg = log_gamma.float().contiguous()
+        b, h, length, nf = fq.shape
+        nd = v.shape[-1]
+        y = torch.empty_like(v)
+        if y.numel():
+            lib = _lib.load()
+            rc = lib.lz_gla_fwd(_ptr(fq), _ptr(fk), _ptr(v), _ptr(lg), _ptr(y), b, h, length,
+                                nf, nd, int(lg.dim() == 3), chunk, _stream(fq))
+            _lib.check(rc, "lz_gla_fwd")
+        if any(ctx.needs_input_grad[:4]):
+            ctx.save_for_backward(fq, fk, v, lg)
+        ctx.chunk = chunk
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        fq, fk, v, lg = ctx.saved_tensors
+        b, h, length, nf = fq.shape
+        nd = v.shape[-1]
+        dy = _bf16(dy)
+        gdt = torch.bfloat16 if all(d == torch.bfloat16 for d in ctx.dtypes[:3]) else torch.float32
+        dfq = torch.empty(fq.shape, device=fq.device, dtype=gdt)
+        dfk = torch.empty_like(dfq)
+        dv = torch.empty(v.shape, device=v.device, dtype=gdt)
+        dlg = torch.empty_like(lg)
+        if dy.numel():
+            lib = _lib.load()
+            per_head = int(lg.dim() == 3)
+            nbytes = lib.lz_gla_bwd_workspace_bytes(b, h, length, nf, nd, per_head, ctx.chunk)
+            ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=fq.device)
+            rc = lib.lz_gla_bwd(_ptr(fq), _ptr(fk), _ptr(v), _ptr(lg), _ptr(dy), _ptr(dfq),
+                                _ptr(dfk), _ptr(dv), _ptr(dlg), int(gdt == torch.bfloat16), b,
+                                h, length, nf, nd, per_head, ctx.chunk, _ptr(ws), ws.numel(),
+                                _stream(fq))
+            _lib.check(rc, "lz_gla_bwd")
+        else:
+            dfq.zero_(), dfk.zero_(), dv.zero_(), dlg.zero_()
+        grads = tuple(g.to(d) for g, d in zip((dfq, dfk, dv, dlg), ctx.dtypes))
+        return grads + (None,)
+
+
+def gla(fq, fk, v, log_gamma, chunk=CHUNK):
+    """Chunked gated linear attention (``src/kernels/gla.py:259-263``).
+
+    y_i = sum_{t<=i} w_it v_t / max(sum_{t<=i} w_it, FLT_MIN) with
+    w_it = (fq_i . fk_t) exp(G_i - G_t), G = cumsum(log_gamma) along L.
+    Returns bf16 ``[B, H, L, D]``.
+    """
+    _check_gla(fq, fk, v, log_gamma, chunk)
+    return _GLA.apply(fq, fk, v, log_gamma, chunk)
+
+
+# ---------------------------------------------------------------------------
+# sliding-window softmax with sinks
+# ---------------------------------------------------------------------------
+
+def _check_swa(q, k, v, meta, window, fwd_blocks, bwd_blocks):
+    if q.dim() != 4 or k.shape != q.shape or v.shape != q.shape:
+        raise ValueError(f"swa: q, k, v must be [B, H, L, d] of one shape, got "
+                         f"{tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
+    if meta.dim() != 1:
+        raise ValueError(f"swa: meta must be 1-D, got {tuple(meta.shape)}")
+    if not isinstance(window, int) or window < 1:
+        raise ValueError(f"swa: window must be a positive int, got {window!r}")
+    for blocks in (fwd_blocks, bwd_blocks):
+        if len(tuple(blocks)) != 2 or any(int(x) < 1 for x in blocks):
+            raise ValueError(f"swa: blocks must be two positive ints, got {blocks!r}")
+    _require_gpu(q, k, v)
+    if meta.numel():
+        _require_gpu(meta)
+
+
+class _SWA(torch.autograd.Function):
+    """Autograd node of ``swa``; mirrors ``_SWA`` (src/kernels/swa.py:136-179)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, meta, window, fwd_blocks, bwd_blocks):
+        ctx.dtypes = (q.dtype, k.dtype, v.dtype, meta.dtype)
+        q, k, v = _bf16(q), _bf16(k), _bf16(v)
+        meta = meta.float().contiguous()
+        b, h, length, d = q.shape
+        scale = 1.0 / math.sqrt(d)
+        y = torch.empty_like(v)
+        lse = torch.empty(b, h, length, device=v.device, dtype=torch.float32)
+        if y.numel():
+            lib = _lib.load()
+            rc = lib.lz_swa_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(meta), meta.numel(), _ptr(y),
+                                _ptr(lse), b, h, length, d, window, scale, _stream(q))
+            _lib.check(rc, "lz_swa_fwd")
+        ctx.save_for_backward(q, k, v, meta, y, lse)
+        ctx.window, ctx.scale = window, scale
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        q, k, v, meta, y, lse = ctx.saved_tensors
+        b, h, length, d = q.shape
+        dy = _bf16(dy)
+        gdt = torch.bfloat16 if all(x == torch.bfloat16 for x in ctx.dtypes[:3]) else torch.float32
+        dq = torch.empty(q.shape, device=q.device, dtype=gdt)
+        dk = torch.empty_like(dq)
+        dv = torch.empty_like(dq)
+        dmeta = torch.zeros(meta.shape, device=q.device, dtype=torch.float32)
+        if dy.numel():
+            lib = _lib.load()
+            n_meta = meta.numel()
+            nbytes = lib.lz_swa_bwd_workspace_bytes(b, h, length, d, n_meta)
+            ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
+            rc = lib.lz_swa_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(meta), n_meta, _ptr(y),
+                                _ptr(lse), _ptr(dy), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dmeta),
+                                int(gdt == torch.bfloat16), b, h, length, d, ctx.window,
+                                ctx.scale, _ptr(ws), ws.numel(), _stream(q))
+            _lib.check(rc, "lz_swa_bwd")
+        else:
+            dq.zero_(), dk.zero_(), dv.zero_()
+        grads = tuple(g.to(dt) for g, dt in zip((dq, dk, dv, dmeta), ctx.dtypes))
+        return grads + (None, None, None)
+
+
+def swa(q, k, v, meta, window, fwd_blocks=FWD_BLOCKS, bwd_blocks=BWD_BLOCKS):
+    """Sliding-window softmax attention with sink logits (``src/kernels/swa.py:182-183``).
+
+    y_i = sum_{i-W<t<=i} e^{s_it} v_t / (sum_j e^{meta_j} + sum_t e^{s_it}),
+    s_it = q_i . k_t / sqrt(d).  Returns bf16 ``[B, H, L, d]``.
+    """
+    _check_swa(q, k, v, meta, window, fwd_blocks, bwd_blocks)
+    return _SWA.apply(q, k, v, meta, window, tuple(fwd_blocks), tuple(bwd_blocks))

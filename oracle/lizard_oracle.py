@@ -1,0 +1,296 @@
+"""CPU oracle for the Lizard attention hot path -- TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` may import this module, and only as the checker (or as the timed
+CPU baseline).  The product (``lizard_reproduction_amd``) never imports it and
+has no CPU fallback: without the HIP library it raises.
+
+It restates, in plain PyTorch on the CPU, the math of the reference's dense
+PyTorch functions (``src/lizard_attention.py:9-44`` of
+mahdikhashan/lizard-reproduction) and the reference kernels' operator API
+(``src/kernels/gla.py:259-263``, ``src/kernels/swa.py:182-183``), plus
+
+* closed-form loop/recurrent versions of every formula (the reference's own
+  ground truth, ``tests/test_lizard.py:22-69``), written from the formulas;
+* a chunked restatement of the 64-token chunk algorithm the HIP kernels run
+  (``src/kernels/gla.py:19-101`` conventions: gates measured from the chunk
+  boundary, every absorbed factor <= 1), optionally emulating the bf16
+  roundings of the kernel's MFMA operands.
+
+How each function is pinned (all in ``tests/test_oracle.py``):
+
+==================  =======================================================
+function            pinned by
+==================  =======================================================
+window_mask         brute-force predicate on small sizes
+gate_products       brute-force products; gla_loop / gla_recurrent
+gla                 gla_loop, gla_recurrent (fp64, 1e-10); gate 0 -> v;
+                    constant v stays constant; gate 1 -> normalised causal
+                    linear attention; gradcheck
+awa / sink_softmax  awa_loop (fp64, 1e-10); no sinks + huge window ==
+                    torch SDPA(is_causal=True); many sinks == one logsumexp
+                    sink; gradcheck
+hedgehog            hedgehog_loop; halves are softmaxes (sum to one)
+gla_kernel_api      gla on exp(log_gamma), per-head folding as the
+                    reference's tests do (tests/test_kernels.py:61-70)
+swa_kernel_api      awa; empty meta == meta of -1e4 (tests/test_kernels.py:
+                    127-134)
+gla_chunked         == dense gla in fp64 for chunk 16/64, L in {1,77,150},
+                    per-token and per-head gates, strong decay
+rope                rope_loop; relative-position invariance of q.k
+==================  =======================================================
+
+The loops are deliberately independent code paths (explicit Python loops over
+tokens), so a dropped term, a wrong sign, an off-by-one in the window or a
+transposed operand in the vectorised functions fails a check.
+"""
+import math
+
+import torch
+
+TINY = torch.finfo(torch.float32).tiny
+
+
+# ---------------------------------------------------------------------------
+# Dense math (src/lizard_attention.py:9-44)
+# ---------------------------------------------------------------------------
+
+def hedgehog(x, weight):
+    """Hedgehog feature map, ``src/lizard_attention.py:9-11``.
+
+    phi(x) = [softmax(x W^T), softmax(-x W^T)] along the last dim, so the
+    feature dimension is twice ``weight.shape[0]``.
+    """
+    proj = torch.matmul(x, weight.transpose(0, 1))
+    return torch.cat([torch.softmax(proj, dim=-1),
+                      torch.softmax(-proj, dim=-1)], dim=-1)
+
+
+def window_mask(length, window, device=None):
+    """Boolean [L, L] mask of the keys t a query i sees,
+    ``src/lizard_attention.py:14-17``: t <= i and i - t < window (so the
+    window holds ``window`` keys including the query itself)."""
+    rows = torch.arange(length, device=device).unsqueeze(1)
+    cols = torch.arange(length, device=device).unsqueeze(0)
+    return (cols <= rows) & ((rows - cols) < window)
+
+
+def gate_products(gamma):
+    """Decay matrix D[..., i, t] = prod_{s=t+1..i} gamma_s for t <= i, else 0.
+
+    Follows ``src/lizard_attention.py:20-25``: it works on gamma itself (not
+    log gamma), so gamma == 0 is exact.  For row i the factors
+    u_i[s] = gamma_s (s <= i) or 1 (s > i) are multiplied over s > t with a
+    suffix product.
+    """
+    length = gamma.shape[-1]
+    causal = window_mask(length, length, gamma.device)
+    factors = torch.where(causal, gamma.unsqueeze(-2), torch.ones((), dtype=gamma.dtype))
+    # inclusive suffix product over s >= t, then shift by one to get s > t
+    suffix = torch.flip(torch.cumprod(torch.flip(factors, [-1]), dim=-1), [-1])
+    exclusive = torch.cat([suffix[..., 1:], torch.ones_like(suffix[..., :1])], dim=-1)
+    return exclusive * causal
+
+
+def gla(fq, fk, v, gamma):
+    """Dense gated linear attention, ``src/lizard_attention.py:28-31``.
+
+    fq, fk: [B, H, L, F]; v: [B, H, L, D]; gamma: [B, L] (shared by heads).
+    y_i = sum_t w_it v_t / max(sum_t w_it, tiny), w_it = (fq_i . fk_t) D_it.
+    """
+    weights = torch.matmul(fq, fk.transpose(-1, -2)) * gate_products(gamma).unsqueeze(1)
+    tiny = torch.finfo(weights.dtype).tiny
+    return torch.matmul(weights, v) / weights.sum(-1, keepdim=True).clamp_min(tiny)
+
+
+def sink_softmax(scores, meta):
+    """Softmax over the last dim with learned sink logits in the denominator
+    only, ``src/lizard_attention.py:34-38``.  The shift m (row max, also over
+    the sinks) is detached, as in the reference.  ``meta`` may be empty."""
+    m = scores.amax(-1, keepdim=True)
+    if meta.numel():
+        m = torch.maximum(m, meta.max())
+    m = m.detach()
+    e = torch.exp(scores - m)
+    den = e.sum(-1, keepdim=True)
+    if meta.numel():
+        den = den + torch.exp(meta - m).sum(-1, keepdim=True)
+    return e / den
+
+
+def awa(q, k, v, meta, window):
+    """Dense sliding-window softmax with sinks, ``src/lizard_attention.py:41-44``.
+    Scores are scaled by 1/sqrt(head_dim) and masked to the window."""
+    mask = window_mask(q.shape[-2], window, q.device)
+    scores = torch.matmul(q, k.transpose(-1, -2)) / math.sqrt(q.shape[-1])
+    scores = scores.masked_fill(~mask, float("-inf"))
+    return torch.matmul(sink_softmax(scores, meta), v)
+
+
+# ---------------------------------------------------------------------------
+# Kernel operator API semantics (src/kernels/gla.py:259-263, swa.py:182-183)
+# ---------------------------------------------------------------------------
+
+def gla_kernel_api(fq, fk, v, log_gamma, dtype=torch.float32):
+    """What ``kernels.gla(fq, fk, v, log_gamma)`` computes, in ``dtype``.
+
+    log_gamma is [B, L] (one gate per token, shared by heads) or [B, H, L]
+    (one gate per head); gamma = exp(log_gamma).  Per-head gates fold B*H into
+    the batch, as the reference's tests do (``tests/test_kernels.py:61-70``).
+    """
+    batch, heads, length, _ = fq.shape
+    gamma = torch.exp(log_gamma.to(dtype))
+    if log_gamma.dim() == 2:
+        return gla(fq.to(dtype), fk.to(dtype), v.to(dtype), gamma)
+
+    def fold(t):
+        return t.to(dtype).reshape(batch * heads, 1, length, -1)
+    y = gla(fold(fq), fold(fk), fold(v), gamma.reshape(batch * heads, length))
+    return y.reshape(batch, heads, length, -1)
+
+
+def swa_kernel_api(q, k, v, meta, window, dtype=torch.float32):
+    """What ``kernels.swa(q, k, v, meta, window)`` computes, in ``dtype``."""
+    return awa(q.to(dtype), k.to(dtype), v.to(dtype), meta.to(dtype), window)
+
+
+# ---------------------------------------------------------------------------
+# Closed forms (tests/test_lizard.py:22-69), written as explicit loops
+# ---------------------------------------------------------------------------
+
+def hedgehog_loop(x, weight):
+    proj = x @ weight.T
+    pos, neg = torch.exp(proj), torch.exp(-proj)
+    return torch.cat([pos / pos.sum(-1, keepdim=True),
+                      neg / neg.sum(-1, keepdim=True)], dim=-1)
+
+
+def gla_loop(fq, fk, v, gamma):
+    """y_i = sum_{t<=i} w_it v_t / sum_{t<=i} w_it with
+    w_it = (fq_i . fk_t) * prod_{s=t+1..i} gamma_s; gamma is [B, L]."""
+    out = torch.zeros_like(v)
+    for i in range(fq.shape[2]):
+        num = torch.zeros_like(v[:, :, 0])
+        den = torch.zeros_like(v[:, :, 0, :1])
+        for t in range(i + 1):
+            decay = torch.ones_like(gamma[:, 0])
+            for s in range(t + 1, i + 1):
+                decay = decay * gamma[:, s]
+            w = decay[:, None, None] * (fq[:, :, i] * fk[:, :, t]).sum(-1, keepdim=True)
+            num = num + w * v[:, :, t]
+            den = den + w
+        out[:, :, i] = num / den
+    return out
+
+
+def gla_recurrent(fq, fk, v, gamma):
+    """Recurrent form: S_i = gamma_i S_{i-1} + fk_i v_i^T, z_i = gamma_i z_{i-1}
+    + fk_i, y_i = fq_i S_i / (fq_i . z_i)."""
+    b, h, n, f = fq.shape
+    state = torch.zeros(b, h, f, v.shape[-1], dtype=fq.dtype)
+    norm = torch.zeros(b, h, f, dtype=fq.dtype)
+    outs = []
+    for i in range(n):
+        g = gamma[:, i].view(b, 1, 1)
+        state = g[..., None] * state + fk[:, :, i, :, None] * v[:, :, i, None, :]
+        norm = g * norm + fk[:, :, i]
+        num = (fq[:, :, i, :, None] * state).sum(-2)
+        outs.append(num / (fq[:, :, i] * norm).sum(-1, keepdim=True))
+    return torch.stack(outs, dim=2)
+
+
+def awa_loop(q, k, v, meta, window):
+    """y_i = sum_{i-W<t<=i} e^{s_it} v_t / (sum_j e^{meta_j} + sum_t e^{s_it}),
+    s_it = q_i . k_t / sqrt(d)."""
+    out = torch.zeros_like(v)
+    for i in range(q.shape[2]):
+        lo = max(0, i - window + 1)
+        scores = (q[:, :, i, None] * k[:, :, lo:i + 1]).sum(-1) / math.sqrt(q.shape[-1])
+        e = torch.exp(scores)
+        num = (e[..., None] * v[:, :, lo:i + 1]).sum(-2)
+        sinks = meta.exp().sum() if meta.numel() else 0.0
+        out[:, :, i] = num / (sinks + e.sum(-1, keepdim=True))
+    return out
+
+
+def rope_loop(x, cos, sin):
+    """rotate_half RoPE: x*cos + [-x2, x1]*sin, cos/sin [L, d]."""
+    half = x.shape[-1] // 2
+    out = torch.empty_like(x)
+    for j in range(x.shape[-1]):
+        partner = -x[..., j + half] if j < half else x[..., j - half]
+        out[..., j] = x[..., j] * cos[:, j] + partner * sin[:, j]
+    return out
+
+
+def rope_cos_sin(length, dim, theta=500000.0, dtype=torch.float64):
+    """Default (unscaled) RoPE tables [L, d] with the rotate_half convention,
+    as transformers' Llama rotary embedding builds them."""
+    inv = 1.0 / (theta ** (torch.arange(0, dim, 2, dtype=torch.float64) / dim))
+    pos = torch.arange(length, dtype=torch.float64)
+    ang = torch.outer(pos, inv)
+    emb = torch.cat([ang, ang], dim=-1)
+    return emb.cos().to(dtype), emb.sin().to(dtype)
+
+
+def rope(x, cos, sin):
+    """Vectorised rotate_half RoPE, pinned by ``rope_loop``."""
+    half = x.shape[-1] // 2
+    rotated = torch.cat([-x[..., half:], x[..., :half]], dim=-1)
+    return x * cos + rotated * sin
+
+
+# ---------------------------------------------------------------------------
+# Chunked restatement of the kernel algorithm (src/kernels/gla.py:19-101)
+# ---------------------------------------------------------------------------
+
+def _bf16(t):
+    return t.to(torch.bfloat16).to(t.dtype)
+
+
+def gla_chunked(fq, fk, v, log_gamma, chunk=64, round_bf16=False, dtype=torch.float64):
+    """Chunkwise GLA with gates measured from each chunk's boundary.
+
+    Within chunk n (tokens [nC, nC+C)), lg_j is the inclusive sum of
+    log_gamma over the chunk up to token j, lg_end its last value:
+
+    * Q~_i = fq_i exp(lg_i) and K~_t = fk_t exp(lg_end - lg_t)  (both <= 1);
+    * o_i = Q~_i S_n + sum_{t<=i} a_it v_t, a_it = (fq_i . fk_t) exp(lg_i - lg_t);
+    * den_i = Q~_i . z_n + sum_{t<=i} a_it;  y_i = o_i / max(den_i, tiny);
+    * S_{n+1} = exp(lg_end) S_n + K~^T V,  z_{n+1} = exp(lg_end) z_n + sum_t K~_t.
+
+    The reference measures the same differences from a global cumsum
+    (start = G[nC-1], end = G[last]); here they are chunk-local sums, which is
+    what the HIP kernels do.  With ``round_bf16`` the kernel's bf16 MFMA
+    operands (Q~, K~, a and the state used by Q~ S) are rounded as the kernel
+    rounds them.  log_gamma: [B, L] or [B, H, L].  Returns [B, H, L, D].
+    """
+    batch, heads, length, nf = fq.shape
+    nd = v.shape[-1]
+    fq, fk, v = fq.to(dtype), fk.to(dtype), v.to(dtype)
+    lgam = log_gamma.to(dtype)
+    if lgam.dim() == 2:
+        lgam = lgam[:, None, :].expand(batch, heads, length)
+    rnd = _bf16 if round_bf16 else (lambda t: t)
+    state = torch.zeros(batch, heads, nf, nd, dtype=dtype)
+    norm = torch.zeros(batch, heads, nf, dtype=dtype)
+    out = torch.empty(batch, heads, length, nd, dtype=dtype)
+    for c0 in range(0, length, chunk):
+        c1 = min(c0 + chunk, length)
+        lg = torch.cumsum(lgam[..., c0:c1], dim=-1)           # [B,H,c]
+        lg_end = lg[..., -1:]
+        q, k, vv = fq[:, :, c0:c1], fk[:, :, c0:c1], v[:, :, c0:c1]
+        qt = rnd(q * torch.exp(lg)[..., None])
+        kt = rnd(k * torch.exp(lg_end - lg)[..., None])
+        n = c1 - c0
+        causal = torch.ones(n, n, dtype=torch.bool).tril()
+        diff = lg[..., :, None] - lg[..., None, :]
+        decay = torch.exp(torch.where(causal, diff, torch.full_like(diff, -math.inf)))
+        a = rnd(torch.matmul(q, k.transpose(-1, -2)) * decay)
+        o = torch.matmul(qt, rnd(state)) + torch.matmul(a, vv)
+        den = (qt * norm[:, :, None, :]).sum(-1) + a.sum(-1)
+        out[:, :, c0:c1] = o / den.clamp_min(TINY)[..., None]
+        r = torch.exp(lg_end)[..., None]                       # [B,H,1,1]
+        state = state * r + torch.matmul(kt.transpose(-1, -2), vv)
+        norm = norm * r[..., 0] + kt.sum(-2)
+    return out

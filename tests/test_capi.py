@@ -1,0 +1,109 @@
+"""CPU tests of the boundary: the C-ABI library builds, loads, exports every
+symbol include/lizard_hip.h declares, rejects bad arguments with a message
+(without touching a GPU), and the product never reaches the oracle."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from lizard_reproduction_amd import _lib, kernels
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "lizard_hip.h")
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_lib.LIB_PATH):
+        from lizard_reproduction_amd import build
+        build.build(verbose=False)
+    return _lib.load()
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(lz_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_bound_symbols():
+    assert declared_symbols() == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    raw = ctypes.CDLL(_lib.LIB_PATH)
+    for name in declared_symbols():
+        assert hasattr(raw, name), name
+
+
+def test_abi_version_and_error_string(lib):
+    assert lib.lz_abi_version() == _lib.ABI_VERSION
+    assert isinstance(lib.lz_last_error(), bytes)
+
+
+def test_null_pointers_are_rejected_with_a_message(lib):
+    rc = lib.lz_gla_fwd(None, None, None, None, None, 1, 1, 8, 16, 16, 0, 64, None)
+    assert rc != 0 and b"null" in lib.lz_last_error()
+    rc = lib.lz_swa_fwd(None, None, None, None, 0, None, None, 1, 1, 8, 16, 4, 0.25, None)
+    assert rc != 0 and b"null" in lib.lz_last_error()
+
+
+def test_bad_sizes_are_rejected_before_any_launch(lib):
+    p = ctypes.c_void_p(16)   # never dereferenced: validation fails first
+    rc = lib.lz_gla_fwd(p, p, p, p, p, 1, 1, 8, 300, 16, 0, 64, None)
+    assert rc != 0 and b"unsupported" in lib.lz_last_error()
+    rc = lib.lz_gla_fwd(p, p, p, p, p, 1, 1, 8, 16, 16, 0, 48, None)
+    assert rc != 0 and b"chunk" in lib.lz_last_error()
+    rc = lib.lz_swa_fwd(p, p, p, p, 65, p, p, 1, 1, 8, 16, 4, 0.25, None)
+    assert rc != 0 and b"n_meta" in lib.lz_last_error()
+    rc = lib.lz_swa_fwd(p, p, p, p, 0, p, p, 1, 1, 8, 512, 4, 0.25, None)
+    assert rc != 0 and b"dim" in lib.lz_last_error()
+    rc = lib.lz_swa_fwd(p, p, p, p, 0, p, p, 1, 1, 8, 16, 0, 0.25, None)
+    assert rc != 0 and b"window" in lib.lz_last_error()
+    ws = lib.lz_gla_bwd_workspace_bytes(2, 3, 100, 24, 20, 0, 64)
+    rc = lib.lz_gla_bwd(p, p, p, p, p, p, p, p, p, 0, 2, 3, 100, 24, 20, 0, 64, p, ws - 1, None)
+    assert rc != 0 and b"workspace" in lib.lz_last_error()
+
+
+def test_workspace_sizes(lib):
+    assert lib.lz_gla_bwd_workspace_bytes(2, 3, 100, 24, 20, 0, 64) == 4 * 2 * 3 * 100 * 4
+    assert lib.lz_swa_bwd_workspace_bytes(1, 32, 2048, 64, 4) == 32 * 16 * 4 * 4
+    assert lib.lz_swa_bwd_workspace_bytes(1, 32, 2048, 64, 0) == 0
+
+
+def test_python_api_validates_shapes():
+    x = torch.zeros(1, 2, 8, 16)
+    with pytest.raises(ValueError):
+        kernels.gla(x, torch.zeros(1, 2, 8, 12), x, torch.zeros(1, 8))
+    with pytest.raises(ValueError):
+        kernels.gla(x, x, x, torch.zeros(1, 3, 8))
+    with pytest.raises(ValueError):
+        kernels.gla(x, x, x, torch.zeros(1, 8), chunk=48)
+    with pytest.raises(ValueError):
+        kernels.swa(x, x, x, torch.zeros(4), 0)
+    with pytest.raises(ValueError):
+        kernels.swa(x, x, torch.zeros(1, 2, 8, 8), torch.zeros(4), 4)
+
+
+def test_python_api_refuses_cpu_tensors():
+    x = torch.zeros(1, 2, 8, 16)
+    with pytest.raises(ValueError, match="ROCm GPU"):
+        kernels.gla(x, x, x, torch.zeros(1, 8))
+    with pytest.raises(ValueError, match="ROCm GPU"):
+        kernels.swa(x, x, x, torch.zeros(4), 4)
+
+
+def test_missing_library_raises(tmp_path, monkeypatch):
+    monkeypatch.setattr(_lib, "_lib", None)
+    with pytest.raises(RuntimeError, match="missing"):
+        _lib.load(str(tmp_path / "nope.so"))
+
+
+def test_product_never_imports_the_oracle():
+    pkg = os.path.join(ROOT, "lizard_reproduction_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".hip", ".hpp", ".cpp")):
+                text = open(os.path.join(dirpath, f)).read()
+                assert not re.search(r"^\s*(from|import)\s+oracle", text, re.M), f

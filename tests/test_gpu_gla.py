@@ -1,0 +1,120 @@
+"""GPU parity of the HIP GLA path against the CPU oracle.
+
+Mirrors the reference's kernel tests (tests/test_kernels.py:55-107): same
+inputs, lengths, chunk sizes, per-head gates, strong decay and the
+no-grad/grad bitwise check, with the north-star bar (max-abs error relative
+to the fp32 oracle's max-abs: <= 1e-2 outputs, <= 2e-2 gradients) on top of
+the reference's own norm bar.  The BASELINE shapes are checked against the
+dense oracle where it fits and against the chunked oracle beyond.
+"""
+import pytest
+import torch
+import torch.nn.functional as F
+
+from lizard_reproduction_amd import kernels
+from oracle import lizard_oracle as lo
+from tests.helpers import (GRAD_TOL, OUT_TOL, baseline_gla_inputs, compare, gla_inputs,
+                           max_rel)
+
+pytestmark = pytest.mark.gpu
+
+
+def gla_kernel(chunk):
+    def kernel(fq, fk, v, z):
+        return kernels.gla(fq, fk, v, F.logsigmoid(z), chunk)
+    return kernel
+
+
+def gla_reference(fq, fk, v, z):
+    return lo.gla_kernel_api(fq, fk, v, F.logsigmoid(z), dtype=torch.float32)
+
+
+@pytest.mark.parametrize("length, chunk", [(1, 16), (77, 16), (150, 64), (64, 64), (129, 64)])
+def test_gla_matches_oracle(length, chunk):
+    inputs = gla_inputs(length)
+    grad = torch.randn(inputs[2].shape, generator=torch.Generator().manual_seed(1))
+    compare(gla_kernel(chunk), gla_reference, inputs, grad, label=f"L={length}")
+
+
+def test_gla_with_a_gate_per_head_matches_oracle():
+    inputs = gla_inputs(100, gates=(3,))
+    grad = torch.randn(inputs[2].shape, generator=torch.Generator().manual_seed(1))
+    compare(gla_kernel(16), gla_reference, inputs, grad, label="per-head")
+
+
+def test_gla_with_strong_decay_matches_oracle():
+    inputs = gla_inputs(200, shift=-6.0)
+    assert F.logsigmoid(inputs[3]).sum(-1).max() < -1000
+    grad = torch.randn(inputs[2].shape, generator=torch.Generator().manual_seed(1))
+    compare(gla_kernel(16), gla_reference, inputs, grad, label="strong decay")
+
+
+@pytest.mark.parametrize("features, dim", [(64, 64), (128, 128), (256, 64), (32, 128), (128, 32),
+                                           (40, 72)])
+def test_gla_feature_and_value_dims(features, dim):
+    inputs = gla_inputs(150, batch=1, heads=2, features=features, dim=dim)
+    grad = torch.randn(inputs[2].shape, generator=torch.Generator().manual_seed(1))
+    compare(gla_kernel(64), gla_reference, inputs, grad, label=f"F={features} D={dim}")
+
+
+def test_gla_without_grad_gives_the_same_output():
+    fq, fk, v, z = (t.cuda() for t in gla_inputs(70))
+    y = kernels.gla(fq, fk, v.requires_grad_(), F.logsigmoid(z), 16)
+    with torch.no_grad():
+        assert torch.equal(kernels.gla(fq, fk, v, F.logsigmoid(z), 16), y)
+
+
+def test_gla_is_deterministic():
+    fq, fk, v, z = (t.cuda().requires_grad_() for t in gla_inputs(150, gates=(3,)))
+    outs = []
+    for _ in range(2):
+        y = kernels.gla(fq, fk, v, F.logsigmoid(z))
+        y.backward(torch.ones_like(y))
+        outs.append([y.detach().clone()] + [t.grad.clone() for t in (fq, fk, v, z)])
+        for t in (fq, fk, v, z):
+            t.grad = None
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+
+
+def test_gla_fp32_inputs_give_fp32_grads():
+    fq, fk, v, z = gla_inputs(50)
+    leaves = [t.float().cuda().requires_grad_() for t in (fq, fk, v)]
+    lg = F.logsigmoid(z).cuda().requires_grad_()
+    y = kernels.gla(*leaves, lg)
+    y.float().sum().backward()
+    assert y.dtype == torch.bfloat16
+    assert all(t.grad.dtype == torch.float32 for t in leaves + [lg])
+
+
+def _baseline_case(batch, heads, length, dim, per_head, gate_mean, gate_std, oracle):
+    fq, fk, v, lg, dy = baseline_gla_inputs(batch, heads, length, dim, per_head,
+                                            gate_mean, gate_std)
+    ours = [t.cuda().requires_grad_() for t in (fq, fk, v, lg)]
+    y = kernels.gla(*ours)
+    y.backward(dy.cuda())
+    theirs = [t.clone().requires_grad_() for t in (fq, fk, v, lg)]
+    ref = oracle(*theirs)
+    ref.backward(dy.float())
+    errs = [max_rel(y, ref)] + [max_rel(a.grad, b.grad) for a, b in zip(ours, theirs)]
+    print(f"GLA B={batch} H={heads} L={length} d={dim} per_head={per_head}: "
+          f"out {errs[0]:.2e} grads " + " ".join(f"{e:.2e}" for e in errs[1:]), flush=True)
+    assert errs[0] <= OUT_TOL, errs
+    assert max(errs[1:]) <= GRAD_TOL, errs
+
+
+def test_gla_baseline_config1_dense():
+    _baseline_case(1, 4, 256, 64, False, 3.0, 1.0,
+                   lambda *a: lo.gla_kernel_api(*a, dtype=torch.float32))
+
+
+def test_gla_baseline_config2_training_shape_dense():
+    _baseline_case(1, 32, 2048, 64, False, 3.0, 1.0,
+                   lambda *a: lo.gla_kernel_api(*a, dtype=torch.float32))
+
+
+def test_gla_baseline_config4_per_head_d128_chunked():
+    # B=1, L=2048 of the config-4 sweep; oracle = chunked restatement in fp32
+    # (pinned against the dense oracle in tests/test_oracle.py)
+    _baseline_case(1, 4, 2048, 128, True, 2.0, 1.5,
+                   lambda *a: lo.gla_chunked(*a, chunk=64, dtype=torch.float32))
