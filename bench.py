@@ -1,0 +1,328 @@
+#!/usr/bin/env python3
+"""Benchmark of the Lizard attention hot path on one MI355X (gfx950).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sweep] [--no-cpu-baseline]
+
+Headline (the step that ``value`` and ``ms_per_step`` time): one GLA forward,
+``kernels.gla(fq, fk, v, log_gamma)``, at the shape the reference's Table-3
+benchmark and the north-star target use (src/benchmark.py:28-41,113-141):
+B=16, H=32, L=2048, F=D=128, per-head gate log_gamma = logsigmoid(N(2, 1.5)),
+fq, fk = softplus(N(0,1)), v = N(0,1), all bf16 and resident in HBM before
+the timed region.  The step is exactly one kernel launch, so the event-timed
+average is also the kernel's average duration, the basis of ``roofline``.
+
+Beside it (``extra``), each timed as the median of per-iteration HIP events
+after warm-up, like triton.testing.do_bench(return_mode="median") in the
+reference (src/benchmark.py:57-66):
+  * GLA fwd+bwd at the headline shape (grads reset each iteration);
+  * BASELINE config 2, GLA fwd and fwd+bwd at the training shape (B=1, H=32,
+    L=2048, d=64, per-token gate logsigmoid(N(3,1)));
+  * BASELINE config 3, SWA fwd and fwd+bwd (B=1, H=32, L=2048, d=64, W=64,
+    4 sink logits, RoPE'd q and k);
+  * BASELINE config 4 sweep, GLA fwd and fwd+bwd, B in {1,4,16},
+    L in {2K,4K,8K,16K}, d=128, per-head gate (skip with --no-sweep).
+
+``cpu_baseline`` times the dense fp32 PyTorch restatement of the reference's
+torch backend (oracle.lizard_oracle.gla_kernel_api, the math of
+src/lizard_attention.py:20-31) on the host cores, on a bounded sample of the
+headline workload (a few (b, h) slices at the full L), scaled linearly to all
+B*H slices (the dense algorithm is independent per slice).
+
+Only one GPU is supported: --gpus N with N > 1 exits with a message.
+"""
+import argparse
+import json
+import math
+import os
+import platform
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = ("GLA fwd & fwd+bwd ms + MFMA util% (H=32,d=128,L=2K–16K); "
+          "SWA fwd+bwd ms")
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, vendor figure
+MFMA_BF16_PEAK_TFS = 2516.6    # MI355X dense bf16 MFMA, vendor figure
+CHUNK = 64
+
+
+def gla_fwd_flops(bh, length, nf, nd):
+    """4FD + 2CF + 2CD per token and head: K~^T V, Q~ S, fq fk^T, A V."""
+    return bh * length * (4 * nf * nd + 2 * CHUNK * nf + 2 * CHUNK * nd)
+
+
+def gla_fwd_bwd_flops(bh, length, nf, nd):
+    """12FD + 8CF + 6CD per token and head (forward plus the reference's
+    backward algorithm, src/kernels/gla.py:104-194)."""
+    return bh * length * (12 * nf * nd + 8 * CHUNK * nf + 6 * CHUNK * nd)
+
+
+def gla_fwd_bytes(bh, length, nf, nd, per_head):
+    """Algorithmic HBM bytes of one forward: read fq, fk (F bf16 each), v
+    (D bf16), the gate (fp32, per head or shared by the heads of a token),
+    write y (D bf16)."""
+    gate = 4 if per_head else 0
+    return bh * length * (2 * nf + 2 * nf + 2 * nd + 2 * nd + gate)
+
+
+def swa_weff(length, window):
+    return sum(min(i + 1, window) for i in range(length)) / length
+
+
+def swa_flops(bh, length, d, window, backward):
+    return (14 if backward else 4) * d * swa_weff(length, window) * bh * length
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--no-sweep", action="store_true", help="skip the config-4 sweep")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=12.0,
+                   help="target CPU time of the cpu_baseline sample")
+    return p.parse_args()
+
+
+def gla_inputs(torch, batch, heads, length, dim, per_head, mean, std, seed=0):
+    import torch.nn.functional as F
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    shape = (batch, heads, length, dim)
+    fq = F.softplus(torch.randn(shape, device="cuda", generator=g)).bfloat16()
+    fk = F.softplus(torch.randn(shape, device="cuda", generator=g)).bfloat16()
+    v = torch.randn(shape, device="cuda", generator=g).bfloat16()
+    gshape = (batch, heads, length) if per_head else (batch, length)
+    lg = F.logsigmoid(mean + std * torch.randn(gshape, device="cuda", generator=g))
+    dy = torch.randn(shape, device="cuda", generator=g).bfloat16()
+    return fq, fk, v, lg, dy
+
+
+def swa_inputs(torch, batch, heads, length, dim, sinks=4, seed=0):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    shape = (batch, heads, length, dim)
+    q, k, v = (torch.randn(shape, device="cuda", generator=g) for _ in range(3))
+    inv = 1.0 / (500000.0 ** (torch.arange(0, dim, 2, device="cuda", dtype=torch.float64) / dim))
+    ang = torch.outer(torch.arange(length, device="cuda", dtype=torch.float64), inv)
+    emb = torch.cat([ang, ang], dim=-1)
+    cos, sin = emb.cos(), emb.sin()
+    half = dim // 2
+
+    def rope(x):
+        rot = torch.cat([-x[..., half:], x[..., :half]], dim=-1)
+        return (x.double() * cos + rot.double() * sin).bfloat16()
+    meta = torch.randn(sinks, device="cuda", generator=g)
+    dy = torch.randn(shape, device="cuda", generator=g).bfloat16()
+    return rope(q), rope(k), v.bfloat16(), meta, dy
+
+
+def median_ms(torch, fn, iters, warmup, reset=None):
+    """Median of per-iteration event timings (ms) on the current stream."""
+    for _ in range(warmup):
+        fn()
+        if reset:
+            reset()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(iters):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        fn()
+        end.record()
+        if reset:
+            reset()
+        times.append((start, end))
+    torch.cuda.synchronize()
+    return statistics.median(s.elapsed_time(e) for s, e in times)
+
+
+def fwd_bwd_fn(torch, op, inputs, dy, extra=()):
+    leaves = [t.detach().clone().requires_grad_() for t in inputs]
+
+    def run():
+        y = op(*leaves, *extra)
+        y.backward(dy)
+
+    def reset():
+        for t in leaves:
+            t.grad = None
+    return run, reset
+
+
+def cpu_baseline(torch, fq, fk, v, lg, target_s):
+    """Dense fp32 torch restatement (the reference's torch backend) on the host
+    cores, on whole (b, h) slices of the headline inputs; returns the time
+    scaled to all B*H slices."""
+    from oracle import lizard_oracle as lo
+    cores = max(1, min(16, len(os.sched_getaffinity(0))))
+    torch.set_num_threads(cores)
+    batch, heads = fq.shape[:2]
+    flat = [t.reshape(batch * heads, 1, *t.shape[2:]) for t in (fq, fk, v)]
+    lgf = lg.reshape(batch * heads, 1, lg.shape[-1])
+
+    def run(n):
+        ins = [t[:n].cpu() for t in flat] + [lgf[:n].cpu()]
+        t0 = time.perf_counter()
+        with torch.no_grad():
+            lo.gla_kernel_api(*ins, dtype=torch.float32)
+        return time.perf_counter() - t0
+    run(1)                                   # warm-up
+    per = run(2) / 2
+    n = int(max(1, min(batch * heads, target_s / max(per, 1e-6))))
+    elapsed = run(n)
+    full_ms = elapsed / n * batch * heads * 1e3
+    cpu = platform.processor() or platform.machine()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": round(full_ms, 3), "unit": "ms", "cores": cores, "kind": "port",
+            "sample": (f"dense fp32 oracle gla_kernel_api (torch backend math) on {n} of "
+                       f"{batch * heads} (b,h) slices at L={fq.shape[2]}, F=D={fq.shape[3]}, "
+                       f"{elapsed:.1f} s, scaled x{batch * heads / n:.1f} to the full workload; "
+                       f"host CPU {cpu}")}
+
+
+def main():
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, "
+              f"WORLD_SIZE={world}); the Lizard hot path here has no multi-GPU build.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from lizard_reproduction_amd import _lib, kernels
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(1)
+    _lib.load()
+    torch.manual_seed(0)
+
+    # ---- headline: GLA forward, B=16 H=32 L=2048 F=D=128, per-head gate -----
+    B, H, L, D = 16, 32, 2048, 128
+    fq, fk, v, lg, dy = gla_inputs(torch, B, H, L, D, True, 2.0, 1.5)
+    with torch.no_grad():
+        for _ in range(args.warmup):
+            kernels.gla(fq, fk, v, lg)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(args.steps):
+            kernels.gla(fq, fk, v, lg)
+        end.record()
+        torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    flops = gla_fwd_flops(B * H, L, D, D)
+    nbytes = gla_fwd_bytes(B * H, L, D, D, True)
+    achieved_gbs = nbytes / (ms * 1e-3) / 1e9
+    tflops = flops / (ms * 1e-3) / 1e12
+    attainable = min(MFMA_BF16_PEAK_TFS, flops / nbytes * HBM_PEAK_GBS / 1e3)
+    print(f"[bench] GLA fwd B={B} H={H} L={L} d={D}: {ms:.4f} ms, {tflops:.1f} TFLOP/s, "
+          f"{achieved_gbs:.0f} GB/s", file=sys.stderr, flush=True)
+
+    extra = {"headline_gla_fwd": {
+        "ms": round(ms, 4), "tflops": round(tflops, 2), "gbs": round(achieved_gbs, 1),
+        "mfma_peak_frac": round(tflops / MFMA_BF16_PEAK_TFS, 4),
+        "attainable_tflops": round(attainable, 1),
+        "attainable_frac": round(tflops / attainable, 4),
+        "flops": flops, "bytes": nbytes}}
+
+    iters = 50
+    run, reset = fwd_bwd_fn(torch, kernels.gla, (fq, fk, v, lg), dy)
+    t = median_ms(torch, run, iters, 5, reset)
+    f = gla_fwd_bwd_flops(B * H, L, D, D)
+    extra["headline_gla_fwd_bwd"] = {"ms": round(t, 4), "tflops": round(f / t / 1e9, 2),
+                                     "mfma_peak_frac": round(f / t / 1e9 / MFMA_BF16_PEAK_TFS, 4)}
+    print(f"[bench] GLA fwd+bwd headline: {t:.4f} ms", file=sys.stderr, flush=True)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(torch, fq, fk, v, lg, args.cpu_seconds)
+        print(f"[bench] cpu baseline: {cpu}", file=sys.stderr, flush=True)
+    del fq, fk, v, lg, dy, run, reset
+    torch.cuda.empty_cache()
+
+    # ---- config 2: GLA training shape, per-token gate -----------------------
+    fq, fk, v, lg, dy = gla_inputs(torch, 1, 32, 2048, 64, False, 3.0, 1.0)
+    with torch.no_grad():
+        t_f = median_ms(torch, lambda: kernels.gla(fq, fk, v, lg), 100, 10)
+    run, reset = fwd_bwd_fn(torch, kernels.gla, (fq, fk, v, lg), dy)
+    t_fb = median_ms(torch, run, 100, 10, reset)
+    extra["config2_gla_train"] = {
+        "shape": "B=1 H=32 L=2048 F=D=64 per-token gate", "fwd_ms": round(t_f, 4),
+        "fwd_bwd_ms": round(t_fb, 4),
+        "fwd_tflops": round(gla_fwd_flops(32, 2048, 64, 64) / t_f / 1e9, 2),
+        "fwd_bwd_tflops": round(gla_fwd_bwd_flops(32, 2048, 64, 64) / t_fb / 1e9, 2)}
+    print(f"[bench] config2: {extra['config2_gla_train']}", file=sys.stderr, flush=True)
+    del fq, fk, v, lg, dy, run, reset
+
+    # ---- config 3: SWA with sinks -------------------------------------------
+    q, k, v, meta, dy = swa_inputs(torch, 1, 32, 2048, 64)
+    with torch.no_grad():
+        t_f = median_ms(torch, lambda: kernels.swa(q, k, v, meta, 64), 100, 10)
+    run, reset = fwd_bwd_fn(torch, kernels.swa, (q, k, v, meta), dy, (64,))
+    t_fb = median_ms(torch, run, 100, 10, reset)
+    swa_bytes = 32 * 2048 * (8 * 64 + 4)
+    extra["config3_swa"] = {
+        "shape": "B=1 H=32 L=2048 d=64 W=64 4 sinks", "fwd_ms": round(t_f, 4),
+        "fwd_bwd_ms": round(t_fb, 4),
+        "fwd_tflops": round(swa_flops(32, 2048, 64, 64, False) / t_f / 1e9, 2),
+        "fwd_bwd_tflops": round(swa_flops(32, 2048, 64, 64, True) / t_fb / 1e9, 2),
+        "fwd_gbs": round(swa_bytes / t_f / 1e6, 1)}
+    print(f"[bench] config3: {extra['config3_swa']}", file=sys.stderr, flush=True)
+    del q, k, v, meta, dy, run, reset
+    torch.cuda.empty_cache()
+
+    # ---- config 4 sweep -----------------------------------------------------
+    if not args.no_sweep:
+        sweep = []
+        for b in (1, 4, 16):
+            for length in (2048, 4096, 8192, 16384):
+                fq, fk, v, lg, dy = gla_inputs(torch, b, 32, length, 128, True, 2.0, 1.5)
+                with torch.no_grad():
+                    t_f = median_ms(torch, lambda: kernels.gla(fq, fk, v, lg), 20, 3)
+                run, reset = fwd_bwd_fn(torch, kernels.gla, (fq, fk, v, lg), dy)
+                t_fb = median_ms(torch, run, 10, 2, reset)
+                ff = gla_fwd_flops(b * 32, length, 128, 128)
+                fb = gla_fwd_bwd_flops(b * 32, length, 128, 128)
+                row = {"B": b, "L": length, "fwd_ms": round(t_f, 4), "fwd_bwd_ms": round(t_fb, 4),
+                       "fwd_tflops": round(ff / t_f / 1e9, 1),
+                       "fwd_mfma_frac": round(ff / t_f / 1e9 / MFMA_BF16_PEAK_TFS, 4),
+                       "fwd_bwd_tflops": round(fb / t_fb / 1e9, 1)}
+                sweep.append(row)
+                print(f"[bench] sweep {row}", file=sys.stderr, flush=True)
+                del fq, fk, v, lg, dy, run, reset
+                torch.cuda.empty_cache()
+        extra["config4_sweep"] = sweep
+
+    line = {
+        "metric": METRIC, "value": round(ms, 4), "unit": "ms", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded; distributions of BASELINE configs 2-4)",
+        "config": {"workload": "GLA forward, per-head gate, B=16 H=32 L=2048 F=D=128, "
+                               "chunk 64 (BASELINE config 4 headline point)",
+                   "batch": B, "heads": H, "seq_len": L, "feature_dim": D, "value_dim": D,
+                   "gate": "per-head logsigmoid(N(2,1.5))", "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": None, "kernel": "gla_fwd_kernel<128,128>",
+                     "algorithmic_bytes": nbytes},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define LZ_ABI_VERSION 1
+#define LZ_ABI_VERSION 2
 
 /* ABI version of the loaded library (LZ_ABI_VERSION). */
 int lz_abi_version(void);
@@ -80,26 +80,31 @@ int lz_gla_bwd(const void* fq, const void* fk, const void* v, const float* log_g
  * 19-59).
  *   q, k, v     bf16 [BH, L, dim]  (RoPE already applied to q and k)
  *   meta        f32 [n_meta] sink logits (n_meta may be 0; at most 64)
- *   y           bf16 [BH, L, dim] output;  lse  f32 [BH, L] (saved for backward)
+ *   y           bf16 [BH, L, dim] output
+ *   y32         f32 [BH, L, dim] the same output before rounding, saved for
+ *               lz_swa_bwd's delta = dy . y; may be NULL when no backward follows
+ *               (y is bitwise the same either way)
+ *   lse         f32 [BH, L] log of each row's softmax denominator (saved for backward)
  *   window      keys i-window < t <= i;  scale  usually 1/sqrt(dim)
  * Supported sizes: dim <= 256.
  */
 int lz_swa_fwd(const void* q, const void* k, const void* v, const float* meta, int n_meta,
-               void* y, float* lse, int batch, int heads, int length, int dim, int window,
-               float scale, void* stream);
+               void* y, float* y32, float* lse, int batch, int heads, int length, int dim,
+               int window, float scale, void* stream);
 
 /* Workspace bytes lz_swa_bwd needs for these sizes. */
 size_t lz_swa_bwd_workspace_bytes(int batch, int heads, int length, int dim, int n_meta);
 
 /*
  * SWA backward.  Replaces _SWA.backward (src/kernels/swa.py:158-179): delta,
- * _swa_bwd_q, _swa_bwd_kv and the dmeta reduction.
- *   y, lse      from lz_swa_fwd;  dy  bf16 [BH, L, dim]
+ * _swa_bwd_q, _swa_bwd_kv and the dmeta reduction.  delta = dy . y32 (the
+ * reference uses the bf16 y, swa.py:164; fp32 y halves the sink-gradient error).
+ *   y32, lse    from lz_swa_fwd;  dy  bf16 [BH, L, dim]
  *   dq, dk, dv  [BH, L, dim]: bf16 if grad_bf16 else f32
  *   dmeta       f32 [n_meta] (untouched when n_meta == 0)
  */
 int lz_swa_bwd(const void* q, const void* k, const void* v, const float* meta, int n_meta,
-               const void* y, const float* lse, const void* dy, void* dq, void* dk, void* dv,
+               const float* y32, const float* lse, const void* dy, void* dq, void* dk, void* dv,
                float* dmeta, int grad_bf16, int batch, int heads, int length, int dim,
                int window, float scale, void* workspace, size_t workspace_bytes, void* stream);
 

@@ -19,10 +19,10 @@ size_t gla_bwd_workspace(int B, int H, int L);
 bool gla_dims_supported(int F, int D);
 int swa_padded_dim(int d);
 hipError_t launch_swa_fwd(const void* q, const void* k, const void* v, const float* meta,
-                          int n_meta, void* y, float* lse, int BH, int L, int d, int W, float scale,
-                          hipStream_t st);
+                          int n_meta, void* y, float* y32, float* lse, int BH, int L, int d, int W,
+                          float scale, hipStream_t st);
 hipError_t launch_swa_bwd(const void* q, const void* k, const void* v, const float* meta,
-                          int n_meta, const void* y, const float* lse, const void* dy, void* dq,
+                          int n_meta, const float* y32, const float* lse, const void* dy, void* dq,
                           void* dk, void* dv, bool grad_bf16, float* dmeta_part, int BH, int L,
                           int d, int W, float scale, hipStream_t st);
 constexpr int MAX_META = 64;
@@ -126,12 +126,12 @@ static int check_swa(const void* q, const void* k, const void* v, const float* m
 }
 
 extern "C" int lz_swa_fwd(const void* q, const void* k, const void* v, const float* meta,
-                          int n_meta, void* y, float* lse, int batch, int heads, int length,
-                          int dim, int window, float scale, void* stream) {
+                          int n_meta, void* y, float* y32, float* lse, int batch, int heads,
+                          int length, int dim, int window, float scale, void* stream) {
   if (int rc = check_swa(q, k, v, meta, n_meta, batch, heads, length, dim, window)) return rc;
   if (!y || !lse) return fail(1, "swa_fwd: null output pointer");
-  return hip_status(lz::launch_swa_fwd(q, k, v, meta, n_meta, y, lse, batch * heads, length, dim,
-                                       window, scale, (hipStream_t)stream),
+  return hip_status(lz::launch_swa_fwd(q, k, v, meta, n_meta, y, y32, lse, batch * heads, length,
+                                       dim, window, scale, (hipStream_t)stream),
                     "swa_fwd");
 }
 
@@ -144,18 +144,18 @@ extern "C" size_t lz_swa_bwd_workspace_bytes(int batch, int heads, int length, i
 }
 
 extern "C" int lz_swa_bwd(const void* q, const void* k, const void* v, const float* meta,
-                          int n_meta, const void* y, const float* lse, const void* dy, void* dq,
+                          int n_meta, const float* y32, const float* lse, const void* dy, void* dq,
                           void* dk, void* dv, float* dmeta, int grad_bf16, int batch, int heads,
                           int length, int dim, int window, float scale, void* workspace,
                           size_t workspace_bytes, void* stream) {
   if (int rc = check_swa(q, k, v, meta, n_meta, batch, heads, length, dim, window)) return rc;
-  if (!y || !lse || !dy || !dq || !dk || !dv) return fail(1, "swa_bwd: null pointer");
+  if (!y32 || !lse || !dy || !dq || !dk || !dv) return fail(1, "swa_bwd: null pointer");
   if (n_meta > 0 && !dmeta) return fail(1, "swa_bwd: null dmeta pointer");
   const size_t need = lz_swa_bwd_workspace_bytes(batch, heads, length, dim, n_meta);
   if (need && (!workspace || workspace_bytes < need))
     return fail(1, "swa_bwd: workspace of %zu bytes given, %zu needed", workspace_bytes, need);
   hipStream_t st = (hipStream_t)stream;
-  hipError_t e = lz::launch_swa_bwd(q, k, v, meta, n_meta, y, lse, dy, dq, dk, dv, grad_bf16 != 0,
+  hipError_t e = lz::launch_swa_bwd(q, k, v, meta, n_meta, y32, lse, dy, dq, dk, dv, grad_bf16 != 0,
                                     (float*)workspace, batch * heads, length, dim, window, scale, st);
   if (e != hipSuccess || n_meta == 0) return hip_status(e, "swa_bwd");
   const int rows = batch * heads * ((length + 127) / 128);

@@ -6,12 +6,16 @@
 //   s_it = q_i . k_t / sqrt(d) for keys i-W < t <= i (t < L)
 //   y_i  = sum_t e^{s_it} v_t / (sum_j e^{meta_j} + sum_t e^{s_it})
 //   lse_i = log(sum_j e^{meta_j} + sum_t e^{s_it})
-// Backward with delta_i = dy_i . y_i (bf16 y, fp32 math, src/kernels/swa.py:164):
+// Backward with delta_i = dy_i . y_i (src/kernels/swa.py:164).  The reference
+// takes y from the bf16 output; here the forward also keeps y in fp32 (y32)
+// when a backward will follow, and delta uses it: with bf16 y the sink
+// gradient alone loses ~1 % to the rounding (it is a long signed sum of delta).
 //   p_it = e^{s_it - lse_i},  ds_it = p_it (dy_i . v_t - delta_i)
 //   dq_i = scale sum_t ds_it k_t,  dk_t = scale sum_i ds_it q_i,
 //   dv_t = sum_i p_it dy_i,  dmeta_j = -sum_i e^{meta_j - lse_i} delta_i
 //
-// Layout: q, k, v, y, dy are [BH, L, d] bf16 row-major; lse is [BH, L] fp32.
+// Layout: q, k, v, y, dy are [BH, L, d] bf16 row-major; y32 is [BH, L, d]
+// fp32; lse is [BH, L] fp32.
 // A workgroup is 4 waves; each wave owns a 32-row tile (queries in the
 // forward and dq role, keys in the dk/dv role) and keeps its own rows in
 // registers as MFMA operands.  The other side of each product is staged per
@@ -81,8 +85,8 @@ __device__ __forceinline__ bool in_window(int i, int t, int L, int W) {
 template <int DP>
 __global__ __launch_bounds__(256) void swa_fwd_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
-    const float* __restrict__ meta, int n_meta, bf16* __restrict__ y, float* __restrict__ lse,
-    int L, int d, int W, float scale) {
+    const float* __restrict__ meta, int n_meta, bf16* __restrict__ y, float* __restrict__ y32,
+    float* __restrict__ lse, int L, int d, int W, float scale) {
   using T = SwaTiles<DP>;
   extern __shared__ __align__(16) char smem[];
   bf16* kn = reinterpret_cast<bf16*>(smem);
@@ -161,8 +165,14 @@ __global__ __launch_bounds__(256) void swa_fwd_kernel(
     for (int t = 0; t < DP / 32; ++t)
 #pragma unroll
       for (int g = 0; g < 4; ++g)
-        store4<bf16>(y + base, qi, t * 32 + 8 * g + 4 * h, d, o[t][4 * g] * inv,
-                     o[t][4 * g + 1] * inv, o[t][4 * g + 2] * inv, o[t][4 * g + 3] * inv);
+      {
+        const int c = t * 32 + 8 * g + 4 * h;
+        store4<bf16>(y + base, qi, c, d, o[t][4 * g] * inv, o[t][4 * g + 1] * inv,
+                     o[t][4 * g + 2] * inv, o[t][4 * g + 3] * inv);
+        if (y32)
+          store4<float>(y32 + base, qi, c, d, o[t][4 * g] * inv, o[t][4 * g + 1] * inv,
+                        o[t][4 * g + 2] * inv, o[t][4 * g + 3] * inv);
+      }
     if (h == 0) lse[(size_t)bh * L + qi] = m_i + flog(l_i);
   }
 }
@@ -174,7 +184,7 @@ __global__ __launch_bounds__(256) void swa_fwd_kernel(
 template <int DP, typename OutT>
 __global__ __launch_bounds__(256) void swa_bwd_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
-    const float* __restrict__ meta, int n_meta, const bf16* __restrict__ y,
+    const float* __restrict__ meta, int n_meta, const float* __restrict__ y32,
     const float* __restrict__ lse, const bf16* __restrict__ dy, OutT* __restrict__ dq,
     OutT* __restrict__ dk, OutT* __restrict__ dv, float* __restrict__ dmeta_part, int L, int d,
     int W, float scale) {
@@ -198,15 +208,21 @@ __global__ __launch_bounds__(256) void swa_bwd_kernel(
     const int Q0 = blockIdx.x * 128;
     const int q0 = Q0 + wave * 32;
     const int qi = q0 + col;
-    bf16x8 qreg[DP / 16], dyreg[DP / 16], yreg[DP / 16];
+    bf16x8 qreg[DP / 16], dyreg[DP / 16];
     load_rows_operand<DP>(q + base, qi, L, d, h, qreg);
     load_rows_operand<DP>(dy + base, qi, L, d, h, dyreg);
-    load_rows_operand<DP>(y + base, qi, L, d, h, yreg);
+    // delta = dy . y32 over this lane's k-slots (columns 16kb + 8(j/4) + 4h + j%4)
     float delta = 0.f;
+    if (qi < L) {
+      const float* yr = y32 + base + (size_t)qi * d;
 #pragma unroll
-    for (int kb = 0; kb < DP / 16; ++kb)
+      for (int kb = 0; kb < DP / 16; ++kb)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) delta += to_f32(dyreg[kb][j]) * to_f32(yreg[kb][j]);
+        for (int j = 0; j < 8; ++j) {
+          const int c = 16 * kb + 8 * (j >> 2) + 4 * h + (j & 3);
+          if (c < d) delta += to_f32(dyreg[kb][j]) * yr[c];
+        }
+    }
     delta += xhalf(delta);
     const float lse_i = qi < L ? lse[(size_t)bh * L + qi] : 0.f;
 
@@ -295,9 +311,9 @@ __global__ __launch_bounds__(256) void swa_bwd_kernel(
       const int qrow = qq0 + r;
       float acc = 0.f;
       if (qrow < L) {
-        const bf16* yr = y + base + (size_t)qrow * d;
+        const float* yr = y32 + base + (size_t)qrow * d;
         const bf16* dr = dy + base + (size_t)qrow * d;
-        for (int c = part; c < d; c += 8) acc += to_f32(yr[c]) * to_f32(dr[c]);
+        for (int c = part; c < d; c += 8) acc += yr[c] * to_f32(dr[c]);
       }
       acc += __shfl_xor(acc, 1);
       acc += __shfl_xor(acc, 2);
@@ -366,8 +382,8 @@ static size_t swa_bwd_lds() {
 
 template <int DP>
 static hipError_t launch_swa_fwd_t(const void* q, const void* k, const void* v, const float* meta,
-                                   int n_meta, void* y, float* lse, int BH, int L, int d, int W,
-                                   float scale, hipStream_t st) {
+                                   int n_meta, void* y, float* y32, float* lse, int BH, int L,
+                                   int d, int W, float scale, hipStream_t st) {
   const size_t lds = swa_fwd_lds<DP>();
   auto kern = swa_fwd_kernel<DP>;
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -375,13 +391,13 @@ static hipError_t launch_swa_fwd_t(const void* q, const void* k, const void* v, 
   if (e != hipSuccess) return e;
   dim3 grid((L + 127) / 128, BH);
   hipLaunchKernelGGL(kern, grid, dim3(256), lds, st, (const bf16*)q, (const bf16*)k,
-                     (const bf16*)v, meta, n_meta, (bf16*)y, lse, L, d, W, scale);
+                     (const bf16*)v, meta, n_meta, (bf16*)y, y32, lse, L, d, W, scale);
   return hipGetLastError();
 }
 
 template <int DP, typename OutT>
 static hipError_t launch_swa_bwd_t(const void* q, const void* k, const void* v, const float* meta,
-                                   int n_meta, const void* y, const float* lse, const void* dy,
+                                   int n_meta, const float* y32, const float* lse, const void* dy,
                                    void* dq, void* dk, void* dv, float* dmeta_part, int BH, int L,
                                    int d, int W, float scale, hipStream_t st) {
   const size_t lds = swa_bwd_lds<DP>();
@@ -392,7 +408,7 @@ static hipError_t launch_swa_bwd_t(const void* q, const void* k, const void* v, 
   const int NB = (L + 127) / 128;
   dim3 grid(2 * NB, BH);
   hipLaunchKernelGGL(kern, grid, dim3(256), lds, st, (const bf16*)q, (const bf16*)k,
-                     (const bf16*)v, meta, n_meta, (const bf16*)y, lse, (const bf16*)dy,
+                     (const bf16*)v, meta, n_meta, y32, lse, (const bf16*)dy,
                      (OutT*)dq, (OutT*)dk, (OutT*)dv, dmeta_part, L, d, W, scale);
   return hipGetLastError();
 }
@@ -406,25 +422,25 @@ int swa_padded_dim(int d) {
 }
 
 hipError_t launch_swa_fwd(const void* q, const void* k, const void* v, const float* meta,
-                          int n_meta, void* y, float* lse, int BH, int L, int d, int W, float scale,
-                          hipStream_t st) {
+                          int n_meta, void* y, float* y32, float* lse, int BH, int L, int d, int W,
+                          float scale, hipStream_t st) {
   switch (swa_padded_dim(d)) {
-    case 32: return launch_swa_fwd_t<32>(q, k, v, meta, n_meta, y, lse, BH, L, d, W, scale, st);
-    case 64: return launch_swa_fwd_t<64>(q, k, v, meta, n_meta, y, lse, BH, L, d, W, scale, st);
-    case 128: return launch_swa_fwd_t<128>(q, k, v, meta, n_meta, y, lse, BH, L, d, W, scale, st);
-    case 256: return launch_swa_fwd_t<256>(q, k, v, meta, n_meta, y, lse, BH, L, d, W, scale, st);
+    case 32: return launch_swa_fwd_t<32>(q, k, v, meta, n_meta, y, y32, lse, BH, L, d, W, scale, st);
+    case 64: return launch_swa_fwd_t<64>(q, k, v, meta, n_meta, y, y32, lse, BH, L, d, W, scale, st);
+    case 128: return launch_swa_fwd_t<128>(q, k, v, meta, n_meta, y, y32, lse, BH, L, d, W, scale, st);
+    case 256: return launch_swa_fwd_t<256>(q, k, v, meta, n_meta, y, y32, lse, BH, L, d, W, scale, st);
     default: return hipErrorInvalidValue;
   }
 }
 
 hipError_t launch_swa_bwd(const void* q, const void* k, const void* v, const float* meta,
-                          int n_meta, const void* y, const float* lse, const void* dy, void* dq,
+                          int n_meta, const float* y32, const float* lse, const void* dy, void* dq,
                           void* dk, void* dv, bool grad_bf16, float* dmeta_part, int BH, int L,
                           int d, int W, float scale, hipStream_t st) {
 #define LZ_SWA_BWD(DPV)                                                                      \
-  return grad_bf16 ? launch_swa_bwd_t<DPV, bf16>(q, k, v, meta, n_meta, y, lse, dy, dq, dk, \
+  return grad_bf16 ? launch_swa_bwd_t<DPV, bf16>(q, k, v, meta, n_meta, y32, lse, dy, dq, dk, \
                                                  dv, dmeta_part, BH, L, d, W, scale, st)     \
-                   : launch_swa_bwd_t<DPV, float>(q, k, v, meta, n_meta, y, lse, dy, dq, dk, \
+                   : launch_swa_bwd_t<DPV, float>(q, k, v, meta, n_meta, y32, lse, dy, dq, dk, \
                                                   dv, dmeta_part, BH, L, d, W, scale, st)
   switch (swa_padded_dim(d)) {
     case 32: LZ_SWA_BWD(32);

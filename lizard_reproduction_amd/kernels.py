@@ -162,18 +162,22 @@ class _SWA(torch.autograd.Function):
         scale = 1.0 / math.sqrt(d)
         y = torch.empty_like(v)
         lse = torch.empty(b, h, length, device=v.device, dtype=torch.float32)
+        # fp32 copy of y for the backward's delta = dy . y (only when one follows)
+        y32 = torch.empty(v.shape, device=v.device, dtype=torch.float32) \
+            if any(ctx.needs_input_grad[:4]) else None
         if y.numel():
             lib = _lib.load()
             rc = lib.lz_swa_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(meta), meta.numel(), _ptr(y),
-                                _ptr(lse), b, h, length, d, window, scale, _stream(q))
+                                _ptr(y32), _ptr(lse), b, h, length, d, window, scale, _stream(q))
             _lib.check(rc, "lz_swa_fwd")
-        ctx.save_for_backward(q, k, v, meta, y, lse)
+        if y32 is not None:
+            ctx.save_for_backward(q, k, v, meta, y32, lse)
         ctx.window, ctx.scale = window, scale
         return y
 
     @staticmethod
     def backward(ctx, dy):
-        q, k, v, meta, y, lse = ctx.saved_tensors
+        q, k, v, meta, y32, lse = ctx.saved_tensors
         b, h, length, d = q.shape
         dy = _bf16(dy)
         gdt = torch.bfloat16 if all(x == torch.bfloat16 for x in ctx.dtypes[:3]) else torch.float32
@@ -186,7 +190,7 @@ class _SWA(torch.autograd.Function):
             n_meta = meta.numel()
             nbytes = lib.lz_swa_bwd_workspace_bytes(b, h, length, d, n_meta)
             ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
-            rc = lib.lz_swa_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(meta), n_meta, _ptr(y),
+            rc = lib.lz_swa_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(meta), n_meta, _ptr(y32),
                                 _ptr(lse), _ptr(dy), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dmeta),
                                 int(gdt == torch.bfloat16), b, h, length, d, ctx.window,
                                 ctx.scale, _ptr(ws), ws.numel(), _stream(q))
