@@ -29,13 +29,17 @@
 extern "C" {
 #endif
 
-#define LZ_ABI_VERSION 2
+#define LZ_ABI_VERSION 3
 
 /* ABI version of the loaded library (LZ_ABI_VERSION). */
 int lz_abi_version(void);
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* lz_last_error(void);
+
+/* Workspace bytes lz_gla_fwd needs for these sizes (0 when B*H alone fills the GPU). */
+size_t lz_gla_fwd_workspace_bytes(int batch, int heads, int length, int nf, int nd,
+                                  int gate_per_head, int chunk);
 
 /*
  * GLA forward.  Replaces kernels.gla's forward: the gate cumsum and head
@@ -49,13 +53,16 @@ const char* lz_last_error(void);
  *   chunk       tiling hint of the reference API (power of two >= 16); the
  *               kernels always walk 64-token chunks, results are
  *               chunk-independent up to rounding
+ *   workspace   device buffer of lz_gla_fwd_workspace_bytes() bytes (may be
+ *               NULL when that is 0): per-segment states when the sequence is
+ *               split into segments to fill the GPU
  * Supported sizes: nf <= 256, nd <= 128, and nd <= 64 when nf > 128.
  * Nothing is saved for the backward: lz_gla_bwd recomputes what it needs, so
  * the output is the same with and without autograd (tests/test_kernels.py:102-107).
  */
 int lz_gla_fwd(const void* fq, const void* fk, const void* v, const float* log_gamma, void* y,
                int batch, int heads, int length, int nf, int nd, int gate_per_head, int chunk,
-               void* stream);
+               void* workspace, size_t workspace_bytes, void* stream);
 
 /* Workspace bytes lz_gla_bwd needs for these sizes. */
 size_t lz_gla_bwd_workspace_bytes(int batch, int heads, int length, int nf, int nd,

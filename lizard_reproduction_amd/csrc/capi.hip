@@ -10,7 +10,9 @@
 
 namespace lz {
 hipError_t launch_gla_fwd(const void* fq, const void* fk, const void* v, const float* lg, void* y,
-                          int B, int H, int L, int F, int D, int gate_per_head, hipStream_t st);
+                          int B, int H, int L, int F, int D, int gate_per_head, float* ws,
+                          hipStream_t st);
+size_t gla_fwd_workspace(int B, int H, int L, int F, int D);
 hipError_t launch_gla_bwd(const void* fq, const void* fk, const void* v, const float* lg,
                           const void* dy, void* dfq, void* dfk, void* dv, float* dlg,
                           bool grad_bf16, int B, int H, int L, int F, int D, int gate_per_head,
@@ -78,13 +80,25 @@ static int check_gla(const void* fq, const void* fk, const void* v, const float*
   return 0;
 }
 
+extern "C" size_t lz_gla_fwd_workspace_bytes(int batch, int heads, int length, int nf, int nd,
+                                             int gate_per_head, int chunk) {
+  (void)gate_per_head; (void)chunk;
+  if (batch <= 0 || heads <= 0 || length <= 0 || !lz::gla_dims_supported(nf, nd)) return 0;
+  return lz::gla_fwd_workspace(batch, heads, length, nf, nd);
+}
+
 extern "C" int lz_gla_fwd(const void* fq, const void* fk, const void* v, const float* log_gamma,
                           void* y, int batch, int heads, int length, int nf, int nd,
-                          int gate_per_head, int chunk, void* stream) {
+                          int gate_per_head, int chunk, void* workspace, size_t workspace_bytes,
+                          void* stream) {
   if (int rc = check_gla(fq, fk, v, log_gamma, batch, heads, length, nf, nd, chunk)) return rc;
   if (!y) return fail(1, "gla_fwd: null output pointer");
+  const size_t need = lz::gla_fwd_workspace(batch, heads, length, nf, nd);
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(1, "gla_fwd: workspace of %zu bytes given, %zu needed", workspace_bytes, need);
   return hip_status(lz::launch_gla_fwd(fq, fk, v, log_gamma, y, batch, heads, length, nf, nd,
-                                       gate_per_head ? 1 : 0, (hipStream_t)stream),
+                                       gate_per_head ? 1 : 0, (float*)workspace,
+                                       (hipStream_t)stream),
                     "gla_fwd");
 }
 

@@ -125,4 +125,89 @@ __device__ __forceinline__ void store4(OutT* __restrict__ p, int row, int c, int
 // Exchange with the other half of the wave (lane ^ 32).
 __device__ __forceinline__ float xhalf(float x) { return __shfl_xor(x, 32); }
 
+// ---------------------------------------------------------------------------
+// LDS transpose reads (gfx950 ds_read_b64_tr_b16).
+//
+// Within each group of 16 lanes, lane i receives 16-bit element i%4 of the
+// 8 bytes addressed by lanes 4e + i/4 of its group, as its element e.  So if
+// the 16 lanes of a group address a block of 4 rows x 16 consecutive columns
+// of a row-major bf16 tile (lane 4e+q -> row e, columns 4q..4q+3), lane i
+// receives column i of those 4 rows: a column read, which is what an MFMA
+// operand whose k index runs down the rows of the tile needs.
+// ---------------------------------------------------------------------------
+typedef short short4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ bf16x4 lds_read_tr(const bf16* p) {
+  typedef __attribute__((address_space(3))) short4v* lds_ptr;
+  const short4v r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ptr)(const_cast<bf16*>(p)));
+  return __builtin_bit_cast(bf16x4, r);
+}
+
+// MFMA operand (A or B) whose 16 k-values run down the rows of a row-major
+// bf16 LDS tile with `pitch` elements per row: lane l gets column
+// col0 + l%32 at rows row0 + 4h + {0..3} (slots 0-3) and row0 + 8 + 4h + {0..3}
+// (slots 4-7), h = l/32 -- the accumulator row order of acc_row(), so the
+// operand pairs with accumulator-sourced operands.  col0 % 4 == 0 and
+// pitch % 4 == 0 keep every lane address 8-byte aligned.
+__device__ __forceinline__ bf16x8 tr_operand(const bf16* tile, int pitch, int row0, int col0,
+                                             int lane) {
+  const int g = lane >> 4, s = lane & 15;
+  const bf16* p = tile + (row0 + 4 * (g >> 1) + (s >> 2)) * pitch + col0 + 16 * (g & 1) + 4 * (s & 3);
+  const bf16x4 lo = lds_read_tr(p);
+  const bf16x4 hi = lds_read_tr(p + 8 * pitch);
+  return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// MFMA operand whose 16 k-values run along row `row` of a row-major tile, in
+// accumulator row order: columns col0 + 4h + {0..3} and col0 + 8 + 4h + {0..3}.
+__device__ __forceinline__ bf16x8 row_operand_acc(const bf16* tile, int pitch, int row, int col0,
+                                                  int h) {
+  const bf16* p = tile + row * pitch + col0 + 4 * h;
+  const bf16x4 lo = *reinterpret_cast<const bf16x4*>(p);
+  const bf16x4 hi = *reinterpret_cast<const bf16x4*>(p + 8);
+  return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// MFMA operand whose 16 k-values are the contiguous columns col0 + 8h + {0..7}
+// of row `row` (for products whose two operands both come from row-major tiles).
+__device__ __forceinline__ bf16x8 row_operand(const bf16* tile, int pitch, int row, int col0,
+                                              int h) {
+  return *reinterpret_cast<const bf16x8*>(tile + row * pitch + col0 + 8 * h);
+}
+
+// 16-byte global load of columns [c, c+8) of row `row` of a row-major
+// [nrows x ncols] bf16 matrix, zero outside it.  `vec` (ncols % 8 == 0)
+// selects the single vector load; otherwise elements are loaded one by one.
+__device__ __forceinline__ uint4 gload8(const bf16* __restrict__ base, int row, int c, int nrows,
+                                        int ncols, bool vec) {
+  if (row >= nrows) return make_uint4(0, 0, 0, 0);
+  const bf16* p = base + (size_t)row * ncols + c;
+  if (vec) {
+    if (c < ncols) return *reinterpret_cast<const uint4*>(p);
+    return make_uint4(0, 0, 0, 0);
+  }
+  bf16x8 v;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = (c + e < ncols) ? p[e] : to_bf16(0.f);
+  return __builtin_bit_cast(uint4, v);
+}
+
+__device__ __forceinline__ bf16x8 scale8(const bf16x8& x, float s) {
+  bf16x8 o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = to_bf16(to_f32(x[e]) * s);
+  return o;
+}
+
+// x[j] * s[j] for the 8 slots, rounded to bf16.
+__device__ __forceinline__ bf16x8 scale8v(const bf16x8& x, const f32x4& s_lo, const f32x4& s_hi) {
+  bf16x8 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    o[e] = to_bf16(to_f32(x[e]) * s_lo[e]);
+    o[4 + e] = to_bf16(to_f32(x[4 + e]) * s_hi[e]);
+  }
+  return o;
+}
+
 }  // namespace lz

@@ -7,144 +7,205 @@
 // chunk up to token j (so every absorbed factor exp(.) is <= 1):
 //   Q~_i = bf16(fq_i e^{lg_i}),  K~_t = bf16(fk_t e^{lg_end - lg_t})
 //   a_it = bf16((fq_i . fk_t) e^{lg_i - lg_t}) for t <= i
-//   o_i  = Q~_i S_n + sum_t a_it v_t,  den_i = Q~_i . z_n + sum_t a_it
+//   o_i  = Q~_i bf16(S_n) + sum_t a_it v_t,  den_i = Q~_i . z_n + sum_t a_it
 //   y_i  = o_i / max(den_i, FLT_MIN)
 //   S_{n+1} = e^{lg_end} S_n + K~^T V,   z_{n+1} = e^{lg_end} z_n + sum_t K~_t
 // The reference takes the same differences from a global cumsum G; the
 // chunk-local sums here are the same numbers without the cancellation.
 //
-// One workgroup (4 waves) per (b, h) walks the chunks in order.  The state
-// S (F x D, fp32) lives in MFMA accumulator registers for the whole walk and
-// is never written to HBM: HBM traffic is one read of fq, fk, v and the gate,
-// and one write of y.  Per chunk:
-//   1. stage fq, fk (natural, [token][f]) and fk, v (transposed, [f|d][token])
-//      in LDS; wave 0 scans the gate.
-//   2. each wave computes one 32x32 tile of s^T = fk fq^T (keys x queries),
-//      applies the causal decay in registers, rounds to bf16 and publishes
-//      the tile to LDS as ready-made MFMA B operands; partial row sums and
-//      Q~.z partials go to LDS.
-//   3. each wave forms o^T = S^T Q~^T + V^T P^T for its d-tile (S operands
-//      come straight from its accumulators), divides by den and stores y;
-//      then S <- e^{lg_end} S + K~^T V for its d-tile and z is updated.
-// Inputs: fq, fk [BH, L, F] bf16; v [BH, L, D] bf16; log_gamma fp32
-// [B, L] (gate_heads == 1) or [B, H, L] (gate_heads == H).  Output y bf16.
+// Work decomposition.  A workgroup (4 waves) walks the chunks of one segment
+// of one (b, h) in order, with the state S (F x D, fp32) in MFMA accumulator
+// registers for the whole walk: no state goes to HBM, so HBM traffic is one
+// read of fq, fk, v and the gate and one write of y.  When B*H alone cannot
+// fill the GPU, the sequence is cut into G segments per (b, h):
+//   1. gla_fwd_state_kernel: the state each segment (but the last) leaves
+//      when it starts from zero, its z and its total log decay;
+//   2. gla_segment_scan_kernel: exclusive scan over segments, giving the
+//      state entering each segment (S_g = e^{Lambda_{g-1}} S_{g-1} + dS_{g-1});
+//   3. gla_fwd_kernel: every segment walks its chunks from its entering state.
+// With G = 1 only step 3 runs.
+//
+// Per chunk, inside gla_fwd_kernel:
+//   * fq, fk, v sit in LDS as row-major [token][feature] tiles (16-byte
+//     stores); the next chunk is already in flight into registers.
+//   * phase 1: wave (kt, qt) computes one 32x32 tile of s^T = fk fq^T
+//     (keys x queries), applies the causal decay in registers and publishes
+//     the bf16 tile as ready-made MFMA operands; Q~.z partials and the
+//     partial sums of K~ for z go to LDS.
+//   * phase 2: a wave owns d-tiles of the output and the state: o^T = S^T Q~^T
+//     (S straight from its accumulators) + V^T P^T, y = o / den; then
+//     S <- e^{lg_end} S + K~^T V.  The operands that contract over tokens
+//     (V^T, K~^T, V) come from LDS transpose reads of the row-major tiles.
+//   * the prefetched chunk is written to LDS, the gate scan of the next chunk
+//     runs on wave 0, and z is updated.
 #include "common.hpp"
 
 namespace lz {
 
-template <int FP, int DP>
-struct GlaFwdCfg {
-  static constexpr int C = 64;
-  static constexpr int NPITCH = FP + 8;   // natural tiles [64][NPITCH]
-  static constexpr int TPITCH = C + 8;    // transposed tiles [FP|DP][TPITCH]
-  static constexpr int NFT = FP / 32, NDT = DP / 32;
-  static constexpr int DT_PER_WAVE = NDT >= 4 ? NDT / 4 : 1;
-  static constexpr int QT_PER_WAVE = NDT >= 4 ? 2 : 1;
-  // LDS carve-up (bytes)
-  static constexpr int OFF_FQN = 0;
-  static constexpr int OFF_FKN = OFF_FQN + C * NPITCH * 2;
-  static constexpr int OFF_FKT = OFF_FKN + C * NPITCH * 2;
-  static constexpr int OFF_VT = OFF_FKT + FP * TPITCH * 2;
-  static constexpr int OFF_PF = OFF_VT + DP * TPITCH * 2;          // [2 qt][4 kb][64][8] bf16
-  static constexpr int OFF_RS = OFF_PF + 2 * 4 * 64 * 16;          // [2][64] f32
-  static constexpr int OFF_QZ = OFF_RS + 2 * 64 * 4;               // [4][64] f32
-  static constexpr int OFF_LG = OFF_QZ + 4 * 64 * 4;               // [64] f32 chunk-local scan
-  static constexpr int OFF_QS = OFF_LG + 64 * 4;                   // [64] e^{lg}
-  static constexpr int OFF_KS = OFF_QS + 64 * 4;                   // [64] e^{end-lg}, slot order
-  static constexpr int OFF_Z = OFF_KS + 64 * 4;                    // [FP] z, slot order
-  static constexpr int OFF_R = OFF_Z + FP * 4;                     // chunk decay
-  static constexpr int BYTES = OFF_R + 16;
-};
+constexpr int GLA_C = 64;       // chunk length
+constexpr int GLA_TARGET_WG = 512;
 
 template <int FP, int DP>
-__global__ __launch_bounds__(256) void gla_fwd_kernel(
+struct GlaFwd {
+  static constexpr int C = GLA_C;
+  static constexpr int PF = FP + 16, PD = DP + 16;   // LDS row pitches (elements)
+  static constexpr int NFT = FP / 32, NDT = DP / 32;
+  static constexpr int NDW = NDT >= 4 ? NDT / 4 : 1;  // output d-tiles per wave
+  static constexpr int NQW = NDT >= 4 ? 2 : 1;        // output q-tiles per wave
+  static constexpr int ZPARTS = FP >= 256 ? 1 : 256 / FP;
+  static constexpr int NLF = C * FP / 8 / 256;        // 16-byte loads per thread, fq or fk
+  static constexpr int NLD = C * DP / 8 / 256;        // 16-byte loads per thread, v
+  static constexpr int OFF_FQ = 0;
+  static constexpr int OFF_FK = OFF_FQ + C * PF * 2;
+  static constexpr int OFF_V = OFF_FK + C * PF * 2;
+  static constexpr int OFF_PF = OFF_V + C * PD * 2;      // [2 qt][4 kb][64 lanes] bf16x8
+  static constexpr int OFF_RS = OFF_PF + 2 * 4 * 64 * 16; // [2 kt][64] row sums of a
+  static constexpr int OFF_QZ = OFF_RS + 2 * 64 * 4;      // [4 waves][64] Q~.z partials
+  static constexpr int OFF_LG = OFF_QZ + 4 * 64 * 4;      // [64] chunk-local lg
+  static constexpr int OFF_QS = OFF_LG + 64 * 4;          // [64] e^{lg}
+  static constexpr int OFF_KS = OFF_QS + 64 * 4;          // [64] e^{lg_end - lg}
+  static constexpr int OFF_Z = OFF_KS + 64 * 4;           // [FP] z
+  static constexpr int OFF_ZP = OFF_Z + FP * 4;           // [ZPARTS][FP] partial sums of K~
+  static constexpr int OFF_R = OFF_ZP + ZPARTS * FP * 4;  // e^{lg_end}, lg_end
+  static constexpr int BYTES = OFF_R + 16;
+  // per-(b,h,segment) state record in the workspace: S [FP][DP], then z [FP]
+  static constexpr int SEG = FP * DP + FP;
+};
+
+// Rows [t0, t0+64) of a [L x ncols] bf16 matrix into registers, 16 bytes per
+// load: thread slot idx = tid + 256 i covers row idx / (KP/8), columns
+// 8 * (idx % (KP/8)) .. +8.  Zero outside the matrix.
+template <int KP, int N>
+__device__ __forceinline__ void load_chunk(uint4 (&reg)[N], const bf16* __restrict__ base, int t0,
+                                           int L, int ncols, bool vec) {
+  constexpr int K8 = KP / 8;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const int idx = threadIdx.x + 256 * i;
+    reg[i] = gload8(base, t0 + idx / K8, (idx % K8) * 8, L, ncols, vec);
+  }
+}
+
+template <int KP, int N>
+__device__ __forceinline__ void store_chunk(const uint4 (&reg)[N], bf16* tile, int pitch) {
+  constexpr int K8 = KP / 8;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const int idx = threadIdx.x + 256 * i;
+    *reinterpret_cast<uint4*>(tile + (idx / K8) * pitch + (idx % K8) * 8) = reg[i];
+  }
+}
+
+// Chunk-local inclusive scan of the gate by one wave (lane = token): lg,
+// e^{lg}, e^{lg_end - lg}, and e^{lg_end}, lg_end in r[0], r[1].
+__device__ __forceinline__ void gate_scan(float g, int lane, float* lgs, float* qs, float* ks,
+                                          float* r) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const float o = __shfl_up(g, off);
+    if (lane >= off) g += o;
+  }
+  const float end = __shfl(g, 63);
+  lgs[lane] = g;
+  qs[lane] = fexp(g);
+  ks[lane] = fexp(end - g);
+  if (lane == 0) {
+    r[0] = fexp(end);
+    r[1] = end;
+  }
+}
+
+__device__ __forceinline__ float gate_at(const float* __restrict__ lgb, int t, int L) {
+  return t < L ? lgb[t] : 0.f;
+}
+
+// ----------------------------------------------------------------------------
+// fused forward walk over the chunks of one segment
+// ----------------------------------------------------------------------------
+template <int FP, int DP>
+__global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
     const bf16* __restrict__ fq, const bf16* __restrict__ fk, const bf16* __restrict__ v,
-    const float* __restrict__ log_gamma, bf16* __restrict__ y, int H, int L, int F, int D,
-    int gate_per_head) {
-  using Cfg = GlaFwdCfg<FP, DP>;
-  constexpr int C = Cfg::C, NP = Cfg::NPITCH, TP = Cfg::TPITCH;
-  constexpr int NFT = Cfg::NFT, NDT = Cfg::NDT;
+    const float* __restrict__ log_gamma, bf16* __restrict__ y,
+    const float* __restrict__ seg_state, int H, int L, int F, int D, int gate_per_head, int G,
+    int cps) {
+  using Cfg = GlaFwd<FP, DP>;
+  constexpr int C = Cfg::C, PF = Cfg::PF, PD = Cfg::PD;
+  constexpr int NFT = Cfg::NFT, NDT = Cfg::NDT, NDW = Cfg::NDW, NQW = Cfg::NQW;
   extern __shared__ __align__(16) char smem[];
-  bf16* fqn = reinterpret_cast<bf16*>(smem + Cfg::OFF_FQN);
-  bf16* fkn = reinterpret_cast<bf16*>(smem + Cfg::OFF_FKN);
-  bf16* fkt = reinterpret_cast<bf16*>(smem + Cfg::OFF_FKT);
-  bf16* vt = reinterpret_cast<bf16*>(smem + Cfg::OFF_VT);
-  bf16x8* pf = reinterpret_cast<bf16x8*>(smem + Cfg::OFF_PF);
+  bf16* fq_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_FQ);
+  bf16* fk_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_FK);
+  bf16* v_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_V);
+  bf16x8* pfrag = reinterpret_cast<bf16x8*>(smem + Cfg::OFF_PF);
   float* rs = reinterpret_cast<float*>(smem + Cfg::OFF_RS);
   float* qz = reinterpret_cast<float*>(smem + Cfg::OFF_QZ);
   float* lgs = reinterpret_cast<float*>(smem + Cfg::OFF_LG);
   float* qs = reinterpret_cast<float*>(smem + Cfg::OFF_QS);
-  float* kss = reinterpret_cast<float*>(smem + Cfg::OFF_KS);
+  float* ks = reinterpret_cast<float*>(smem + Cfg::OFF_KS);
   float* zs = reinterpret_cast<float*>(smem + Cfg::OFF_Z);
+  float* zp = reinterpret_cast<float*>(smem + Cfg::OFF_ZP);
   float* rdec = reinterpret_cast<float*>(smem + Cfg::OFF_R);
 
-  const int bh = blockIdx.x;
+  const int bh = blockIdx.x / G, seg = blockIdx.x % G;
+  const int NT = (L + C - 1) / C;
+  const int n0 = seg * cps, n1 = min(NT, n0 + cps);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int col = lane & 31, h = lane >> 5;
+  const bool vecF = (F & 7) == 0, vecD = (D & 7) == 0;
   const bf16* fqb = fq + (size_t)bh * L * F;
   const bf16* fkb = fk + (size_t)bh * L * F;
   const bf16* vb = v + (size_t)bh * L * D;
   bf16* yb = y + (size_t)bh * L * D;
   const float* lgb = log_gamma + (size_t)(gate_per_head ? bh : bh / H) * L;
+  const float* st = G > 1 ? seg_state + ((size_t)bh * G + seg) * Cfg::SEG : nullptr;
 
-  for (int f = tid; f < FP; f += 256) zs[f] = 0.f;
-
-  // wave -> (d-tiles, q-tiles) of the output; S tiles follow the d-tiles
+  // wave -> owned d-tiles (state and output) and output q-tiles
   const bool active = NDT >= 2 || wave < 2;
-  f32x16 S[Cfg::DT_PER_WAVE][NFT];
-#pragma unroll
-  for (int i = 0; i < Cfg::DT_PER_WAVE; ++i)
-#pragma unroll
-    for (int ft = 0; ft < NFT; ++ft) S[i][ft] = zero16();
+  auto dtile = [&](int i) { return NDT >= 4 ? wave + 4 * i : (NDT == 2 ? (wave & 1) : 0); };
+  auto qtile = [&](int j) { return NDT >= 4 ? j : (NDT == 2 ? (wave >> 1) : (wave & 1)); };
 
-  const int NT = (L + C - 1) / C;
-  for (int n = 0; n < NT; ++n) {
-    const int t0 = n * C;
-    __syncthreads();
-    // ---- 1. stage the chunk -------------------------------------------------
-    {
-      constexpr int F4 = FP / 4;
-      for (int idx = tid; idx < C * F4; idx += 256) {
-        const int r = idx / F4, c = (idx % F4) * 4;
-        const bf16x4 a = load4(fqb, t0 + r, c, L, F);
-        const bf16x4 b = load4(fkb, t0 + r, c, L, F);
-        *reinterpret_cast<bf16x4*>(fqn + r * NP + pidx(c)) = a;
-        *reinterpret_cast<bf16x4*>(fkn + r * NP + pidx(c)) = b;
+  f32x16 S[NDW][NFT];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) fkt[(c + e) * TP + pidx(r)] = b[e];
-      }
-      constexpr int D4 = DP / 4;
-      for (int idx = tid; idx < C * D4; idx += 256) {
-        const int r = idx / D4, c = (idx % D4) * 4;
-        const bf16x4 b = load4(vb, t0 + r, c, L, D);
+  for (int i = 0; i < NDW; ++i)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) vt[(c + e) * TP + pidx(r)] = b[e];
-      }
-      if (wave == 0) {
-        float g = (t0 + lane < L) ? lgb[t0 + lane] : 0.f;
+    for (int ft = 0; ft < NFT; ++ft) {
+      S[i][ft] = zero16();
+      if (st && active) {
 #pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-          const float o = __shfl_up(g, off);
-          if (lane >= off) g += o;
-        }
-        const float end = __shfl(g, 63);
-        lgs[lane] = g;
-        qs[lane] = fexp(g);
-        kss[pidx(lane)] = fexp(end - g);
-        if (lane == 0) rdec[0] = fexp(end);
+        for (int r = 0; r < 16; ++r)
+          S[i][ft][r] = st[(ft * 32 + acc_row(r, h)) * DP + dtile(i) * 32 + col];
       }
     }
-    __syncthreads();
-    // ---- 2. scores, P fragments, row sums, Q~.z partials ---------------------
+  for (int f = tid; f < FP; f += 256) zs[f] = st ? st[FP * DP + f] : 0.f;
+
+  uint4 rq[Cfg::NLF], rk[Cfg::NLF], rv[Cfg::NLD];
+  float rg;
+  load_chunk<FP>(rq, fqb, n0 * C, L, F, vecF);
+  load_chunk<FP>(rk, fkb, n0 * C, L, F, vecF);
+  load_chunk<DP>(rv, vb, n0 * C, L, D, vecD);
+  rg = gate_at(lgb, n0 * C + lane, L);
+  store_chunk<FP>(rq, fq_l, PF);
+  store_chunk<FP>(rk, fk_l, PF);
+  store_chunk<DP>(rv, v_l, PD);
+  if (wave == 0) gate_scan(rg, lane, lgs, qs, ks, rdec);
+  __syncthreads();
+
+  for (int n = n0; n < n1; ++n) {
+    const int t0 = n * C;
+    const bool more = n + 1 < n1;
+    if (more) {   // next chunk in flight while this one computes
+      load_chunk<FP>(rq, fqb, t0 + C, L, F, vecF);
+      load_chunk<FP>(rk, fkb, t0 + C, L, F, vecF);
+      load_chunk<DP>(rv, vb, t0 + C, L, D, vecD);
+      rg = gate_at(lgb, t0 + C + lane, L);
+    }
+    // ---- phase 1: scores -> P fragments and row sums; Q~.z; sums of K~ ------
     {
       const int kt = wave >> 1, qt = wave & 1;
       f32x16 s = zero16();
 #pragma unroll
-      for (int kb = 0; kb < FP / 16; ++kb) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(fkn + (kt * 32 + col) * NP + 16 * kb + 8 * h);
-        const bf16x8 b = *reinterpret_cast<const bf16x8*>(fqn + (qt * 32 + col) * NP + 16 * kb + 8 * h);
-        s = mfma(a, b, s);
-      }
+      for (int kb = 0; kb < FP / 16; ++kb)
+        s = mfma(row_operand(fk_l, PF, kt * 32 + col, 16 * kb, h),
+                 row_operand(fq_l, PF, qt * 32 + col, 16 * kb, h), s);
       const int qi = qt * 32 + col;
       const float lgq = lgs[qi];
       bf16x8 p[2];
@@ -158,46 +219,53 @@ __global__ __launch_bounds__(256) void gla_fwd_kernel(
         rsum += to_f32(pb);
       }
       rsum += xhalf(rsum);
-      pf[(qt * 4 + kt * 2 + 0) * 64 + lane] = p[0];
-      pf[(qt * 4 + kt * 2 + 1) * 64 + lane] = p[1];
+      pfrag[(qt * 4 + kt * 2 + 0) * 64 + lane] = p[0];
+      pfrag[(qt * 4 + kt * 2 + 1) * 64 + lane] = p[1];
       if (h == 0) rs[kt * 64 + qi] = rsum;
-      // Q~ . z partial over a quarter of the features; query = lane
-      constexpr int FQ = FP / 4;
+
+      constexpr int FQ = FP / 4;   // Q~ . z over a quarter of the features; query = lane
       const float qsv = qs[lane];
       float acc = 0.f;
-      for (int f = wave * FQ; f < (wave + 1) * FQ; ++f)
-        acc += to_f32(to_bf16(to_f32(fqn[lane * NP + f]) * qsv)) * zs[f];
+#pragma unroll
+      for (int c = 0; c < FQ; c += 8) {
+        const bf16x8 x = *reinterpret_cast<const bf16x8*>(fq_l + lane * PF + wave * FQ + c);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc += to_f32(to_bf16(to_f32(x[e]) * qsv)) * zs[wave * FQ + c + e];
+      }
       qz[wave * 64 + lane] = acc;
+
+      constexpr int TPP = C / Cfg::ZPARTS;   // tokens per partial sum of K~
+      const int f = tid % FP, part = tid / FP;
+      if (part < Cfg::ZPARTS) {
+        float za = 0.f;
+#pragma unroll 8
+        for (int t = part * TPP; t < (part + 1) * TPP; ++t)
+          za += to_f32(to_bf16(to_f32(fk_l[t * PF + f]) * ks[t]));
+        zp[part * FP + f] = za;
+      }
     }
     __syncthreads();
-    // ---- 3. outputs and state update ----------------------------------------
+    // ---- phase 2: outputs and state update ----------------------------------
     const float r_n = rdec[0];
     if (active) {
 #pragma unroll
-      for (int i = 0; i < Cfg::DT_PER_WAVE; ++i) {
-        const int dt = NDT >= 4 ? wave + 4 * i : (NDT == 2 ? (wave >> 1) : 0);
-        bf16x8 sa[FP / 16];
+      for (int i = 0; i < NDW; ++i) {
+        const int dt = dtile(i);
+        bf16x8 vop[4];   // V^T rows of this d-tile (A of V^T P^T) == V columns (B of K~^T V)
 #pragma unroll
-        for (int kb = 0; kb < FP / 16; ++kb) sa[kb] = acc_operand(S[i][kb >> 1], kb & 1);
+        for (int kb = 0; kb < 4; ++kb) vop[kb] = tr_operand(v_l, PD, 16 * kb, dt * 32, lane);
 #pragma unroll
-        for (int j = 0; j < Cfg::QT_PER_WAVE; ++j) {
-          const int qt = NDT >= 4 ? j : (wave & 1);
+        for (int j = 0; j < NQW; ++j) {
+          const int qt = qtile(j);
           const int qi = qt * 32 + col;
           const float qsv = qs[qi];
           f32x16 o = zero16();
 #pragma unroll
-          for (int kb = 0; kb < FP / 16; ++kb) {
-            const bf16x8 raw = *reinterpret_cast<const bf16x8*>(fqn + qi * NP + 16 * kb + 8 * h);
-            bf16x8 b;
+          for (int kb = 0; kb < FP / 16; ++kb)
+            o = mfma(acc_operand(S[i][kb >> 1], kb & 1),
+                     scale8(row_operand_acc(fq_l, PF, qi, 16 * kb, h), qsv), o);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) b[e] = to_bf16(to_f32(raw[e]) * qsv);
-            o = mfma(sa[kb], b, o);
-          }
-#pragma unroll
-          for (int kb = 0; kb < 4; ++kb) {
-            const bf16x8 a = *reinterpret_cast<const bf16x8*>(vt + (dt * 32 + col) * TP + 16 * kb + 8 * h);
-            o = mfma(a, pf[(qt * 4 + kb) * 64 + lane], o);
-          }
+          for (int kb = 0; kb < 4; ++kb) o = mfma(vop[kb], pfrag[(qt * 4 + kb) * 64 + lane], o);
           const float den = rs[qi] + rs[64 + qi] + qz[qi] + qz[64 + qi] + qz[128 + qi] + qz[192 + qi];
           const float inv = 1.f / fmaxf(den, TINY);
           const int tok = t0 + qi;
@@ -208,47 +276,173 @@ __global__ __launch_bounds__(256) void gla_fwd_kernel(
                            o[4 * g + 1] * inv, o[4 * g + 2] * inv, o[4 * g + 3] * inv);
           }
         }
-        // S <- e^{lg_end} S + K~^T V  (this wave's d-tile)
 #pragma unroll
         for (int ft = 0; ft < NFT; ++ft) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) S[i][ft][r] *= r_n;
 #pragma unroll
           for (int kb = 0; kb < 4; ++kb) {
-            const bf16x8 raw = *reinterpret_cast<const bf16x8*>(fkt + (ft * 32 + col) * TP + 16 * kb + 8 * h);
-            bf16x8 a;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) a[e] = to_bf16(to_f32(raw[e]) * kss[16 * kb + 8 * h + e]);
-            const bf16x8 b = *reinterpret_cast<const bf16x8*>(vt + (dt * 32 + col) * TP + 16 * kb + 8 * h);
-            S[i][ft] = mfma(a, b, S[i][ft]);
+            const f32x4 klo = *reinterpret_cast<const f32x4*>(ks + 16 * kb + 4 * h);
+            const f32x4 khi = *reinterpret_cast<const f32x4*>(ks + 16 * kb + 8 + 4 * h);
+            const bf16x8 a = scale8v(tr_operand(fk_l, PF, 16 * kb, ft * 32, lane), klo, khi);
+            S[i][ft] = mfma(a, vop[kb], S[i][ft]);
           }
         }
       }
     }
-    // z <- e^{lg_end} z + sum_t K~_t   (zs in slot order of f)
-    for (int fs = tid; fs < FP; fs += 256) {
-      const int f = pidx(fs);
-      float acc = 0.f;
-      for (int t = 0; t < C; ++t) acc += to_f32(to_bf16(to_f32(fkt[f * TP + t]) * kss[t]));
-      zs[fs] = zs[fs] * r_n + acc;
+    __syncthreads();
+    // ---- next chunk into LDS; z update ----------------------------------------
+    if (more) {
+      store_chunk<FP>(rq, fq_l, PF);
+      store_chunk<FP>(rk, fk_l, PF);
+      store_chunk<DP>(rv, v_l, PD);
+      if (wave == 0) gate_scan(rg, lane, lgs, qs, ks, rdec);
     }
+    if (tid < FP) {
+      float za = zs[tid] * r_n;
+#pragma unroll
+      for (int p = 0; p < Cfg::ZPARTS; ++p) za += zp[p * FP + tid];
+      zs[tid] = za;
+    }
+    __syncthreads();
   }
 }
 
+// ----------------------------------------------------------------------------
+// segment pass: state left by each segment g < G-1 starting from zero
+// ----------------------------------------------------------------------------
 template <int FP, int DP>
-static hipError_t launch_gla_fwd_t(const void* fq, const void* fk, const void* v,
-                                   const float* lg, void* y, int B, int H, int L, int F, int D,
-                                   int gate_per_head, hipStream_t st) {
-  using Cfg = GlaFwdCfg<FP, DP>;
-  auto kern = gla_fwd_kernel<FP, DP>;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::BYTES);
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(kern, dim3(B * H), dim3(256), Cfg::BYTES, st, (const bf16*)fq,
-                     (const bf16*)fk, (const bf16*)v, lg, (bf16*)y, H, L, F, D, gate_per_head);
-  return hipGetLastError();
+__global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_state_kernel(
+    const bf16* __restrict__ fk, const bf16* __restrict__ v, const float* __restrict__ log_gamma,
+    float* __restrict__ seg_state, float* __restrict__ seg_logdecay, int H, int L, int F, int D,
+    int gate_per_head, int G, int cps) {
+  using Cfg = GlaFwd<FP, DP>;
+  constexpr int C = Cfg::C, PF = Cfg::PF, PD = Cfg::PD;
+  constexpr int NFT = Cfg::NFT, NDT = Cfg::NDT;
+  constexpr int NTILE = NFT * NDT;
+  constexpr int TPW = (NTILE + 3) / 4;   // state tiles per wave
+  extern __shared__ __align__(16) char smem[];
+  bf16* fk_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_FK);
+  bf16* v_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_V);
+  float* lgs = reinterpret_cast<float*>(smem + Cfg::OFF_LG);
+  float* qs = reinterpret_cast<float*>(smem + Cfg::OFF_QS);
+  float* ks = reinterpret_cast<float*>(smem + Cfg::OFF_KS);
+  float* zs = reinterpret_cast<float*>(smem + Cfg::OFF_Z);
+  float* zp = reinterpret_cast<float*>(smem + Cfg::OFF_ZP);
+  float* rdec = reinterpret_cast<float*>(smem + Cfg::OFF_R);
+
+  const int bh = blockIdx.x / (G - 1), seg = blockIdx.x % (G - 1);
+  const int n0 = seg * cps, n1 = n0 + cps;   // segments before the last are full
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int col = lane & 31, h = lane >> 5;
+  const bool vecF = (F & 7) == 0, vecD = (D & 7) == 0;
+  const bf16* fkb = fk + (size_t)bh * L * F;
+  const bf16* vb = v + (size_t)bh * L * D;
+  const float* lgb = log_gamma + (size_t)(gate_per_head ? bh : bh / H) * L;
+
+  f32x16 S[TPW];
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) S[i] = zero16();
+  for (int f = tid; f < FP; f += 256) zs[f] = 0.f;
+  float lam = 0.f;   // total log decay of the segment (wave 0)
+
+  uint4 rk[Cfg::NLF], rv[Cfg::NLD];
+  float rg;
+  load_chunk<FP>(rk, fkb, n0 * C, L, F, vecF);
+  load_chunk<DP>(rv, vb, n0 * C, L, D, vecD);
+  rg = gate_at(lgb, n0 * C + lane, L);
+  store_chunk<FP>(rk, fk_l, PF);
+  store_chunk<DP>(rv, v_l, PD);
+  if (wave == 0) gate_scan(rg, lane, lgs, qs, ks, rdec);
+  __syncthreads();
+
+  for (int n = n0; n < n1; ++n) {
+    const int t0 = n * C;
+    const bool more = n + 1 < n1;
+    if (more) {
+      load_chunk<FP>(rk, fkb, t0 + C, L, F, vecF);
+      load_chunk<DP>(rv, vb, t0 + C, L, D, vecD);
+      rg = gate_at(lgb, t0 + C + lane, L);
+    }
+    const float r_n = rdec[0];
+    if (wave == 0) lam += rdec[1];
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+      const int ti = wave + 4 * i;
+      if (ti < NTILE) {
+        const int ft = ti / NDT, dt = ti % NDT;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) S[i][r] *= r_n;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+          const f32x4 klo = *reinterpret_cast<const f32x4*>(ks + 16 * kb + 4 * h);
+          const f32x4 khi = *reinterpret_cast<const f32x4*>(ks + 16 * kb + 8 + 4 * h);
+          const bf16x8 a = scale8v(tr_operand(fk_l, PF, 16 * kb, ft * 32, lane), klo, khi);
+          S[i] = mfma(a, tr_operand(v_l, PD, 16 * kb, dt * 32, lane), S[i]);
+        }
+      }
+    }
+    {
+      constexpr int TPP = C / Cfg::ZPARTS;
+      const int f = tid % FP, part = tid / FP;
+      if (part < Cfg::ZPARTS) {
+        float za = 0.f;
+#pragma unroll 8
+        for (int t = part * TPP; t < (part + 1) * TPP; ++t)
+          za += to_f32(to_bf16(to_f32(fk_l[t * PF + f]) * ks[t]));
+        zp[part * FP + f] = za;
+      }
+    }
+    __syncthreads();
+    if (more) {
+      store_chunk<FP>(rk, fk_l, PF);
+      store_chunk<DP>(rv, v_l, PD);
+      if (wave == 0) gate_scan(rg, lane, lgs, qs, ks, rdec);
+    }
+    if (tid < FP) {
+      float za = zs[tid] * r_n;
+#pragma unroll
+      for (int p = 0; p < Cfg::ZPARTS; ++p) za += zp[p * FP + tid];
+      zs[tid] = za;
+    }
+    __syncthreads();
+  }
+  float* out = seg_state + ((size_t)bh * G + seg) * Cfg::SEG;
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) {
+    const int ti = wave + 4 * i;
+    if (ti < NTILE) {
+      const int ft = ti / NDT, dt = ti % NDT;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) out[(ft * 32 + acc_row(r, h)) * DP + dt * 32 + col] = S[i][r];
+    }
+  }
+  for (int f = tid; f < FP; f += 256) out[FP * DP + f] = zs[f];
+  if (tid == 0) seg_logdecay[(size_t)bh * G + seg] = lam;
 }
 
+// ----------------------------------------------------------------------------
+// exclusive scan over segments, in place: record g <- state entering segment g
+// ----------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void gla_segment_scan_kernel(float* __restrict__ seg_state,
+                                                               const float* __restrict__ seg_logdecay,
+                                                               int G, int rec) {
+  const int bh = blockIdx.y;
+  const int e = blockIdx.x * 256 + threadIdx.x;
+  if (e >= rec) return;
+  float carry = 0.f;
+  for (int g = 0; g < G - 1; ++g) {
+    const size_t idx = ((size_t)bh * G + g) * rec + e;
+    const float d = seg_state[idx];
+    seg_state[idx] = carry;
+    carry = fexp(seg_logdecay[(size_t)bh * G + g]) * carry + d;
+  }
+  seg_state[((size_t)bh * G + G - 1) * rec + e] = carry;
+}
+
+// ----------------------------------------------------------------------------
+// host side
+// ----------------------------------------------------------------------------
 int gla_padded_dim(int n) {
   if (n <= 32) return 32;
   if (n <= 64) return 64;
@@ -257,24 +451,76 @@ int gla_padded_dim(int n) {
   return -1;
 }
 
+bool gla_dims_supported(int F, int D) {
+  const int fp = gla_padded_dim(F), dp = gla_padded_dim(D);
+  if (fp < 0 || dp < 0) return false;
+  return dp <= 128 && (fp <= 128 || dp <= 64);
+}
+
+// Segments per (b, h): enough (b, h, segment) workgroups to fill the GPU.
+void gla_segments(int BH, int L, int* G, int* cps) {
+  const int NT = (L + GLA_C - 1) / GLA_C;
+  int g = (GLA_TARGET_WG + BH - 1) / BH;
+  g = g < 1 ? 1 : (g > NT ? NT : g);
+  const int c = (NT + g - 1) / g;
+  *cps = c;
+  *G = (NT + c - 1) / c;
+}
+
+size_t gla_fwd_workspace(int B, int H, int L, int F, int D) {
+  int G, cps;
+  gla_segments(B * H, L, &G, &cps);
+  if (G <= 1) return 0;
+  const size_t rec = (size_t)gla_padded_dim(F) * gla_padded_dim(D) + gla_padded_dim(F);
+  return ((size_t)B * H * G * rec + (size_t)B * H * G) * sizeof(float);
+}
+
+template <int FP, int DP>
+static hipError_t launch_gla_fwd_t(const void* fq, const void* fk, const void* v,
+                                   const float* lg, void* y, int B, int H, int L, int F, int D,
+                                   int gate_per_head, float* ws, hipStream_t st) {
+  using Cfg = GlaFwd<FP, DP>;
+  const int BH = B * H;
+  int G, cps;
+  gla_segments(BH, L, &G, &cps);
+  float* seg_state = ws;
+  if (G > 1) {
+    float* seg_logdecay = ws + (size_t)BH * G * Cfg::SEG;
+    auto ks = gla_fwd_state_kernel<FP, DP>;
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(ks),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::BYTES);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(ks, dim3(BH * (G - 1)), dim3(256), Cfg::BYTES, st, (const bf16*)fk,
+                       (const bf16*)v, lg, seg_state, seg_logdecay, H, L, F, D, gate_per_head, G,
+                       cps);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL(gla_segment_scan_kernel, dim3((Cfg::SEG + 255) / 256, BH), dim3(256), 0,
+                       st, seg_state, (const float*)seg_logdecay, G, Cfg::SEG);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  auto kern = gla_fwd_kernel<FP, DP>;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::BYTES);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(kern, dim3(BH * G), dim3(256), Cfg::BYTES, st, (const bf16*)fq,
+                     (const bf16*)fk, (const bf16*)v, lg, (bf16*)y, (const float*)seg_state, H, L,
+                     F, D, gate_per_head, G, cps);
+  return hipGetLastError();
+}
+
 hipError_t launch_gla_fwd(const void* fq, const void* fk, const void* v, const float* lg, void* y,
-                          int B, int H, int L, int F, int D, int gate_per_head, hipStream_t st) {
+                          int B, int H, int L, int F, int D, int gate_per_head, float* ws,
+                          hipStream_t st) {
   const int fp = gla_padded_dim(F), dp = gla_padded_dim(D);
 #define LZ_GLA_FWD(FPV, DPV) \
   if (fp == FPV && dp == DPV) \
-    return launch_gla_fwd_t<FPV, DPV>(fq, fk, v, lg, y, B, H, L, F, D, gate_per_head, st);
+    return launch_gla_fwd_t<FPV, DPV>(fq, fk, v, lg, y, B, H, L, F, D, gate_per_head, ws, st);
   LZ_GLA_FWD(32, 32) LZ_GLA_FWD(32, 64) LZ_GLA_FWD(32, 128)
   LZ_GLA_FWD(64, 32) LZ_GLA_FWD(64, 64) LZ_GLA_FWD(64, 128)
   LZ_GLA_FWD(128, 32) LZ_GLA_FWD(128, 64) LZ_GLA_FWD(128, 128)
   LZ_GLA_FWD(256, 32) LZ_GLA_FWD(256, 64)
 #undef LZ_GLA_FWD
   return hipErrorInvalidValue;
-}
-
-bool gla_dims_supported(int F, int D) {
-  const int fp = gla_padded_dim(F), dp = gla_padded_dim(D);
-  if (fp < 0 || dp < 0) return false;
-  return dp <= 128 && (fp <= 128 || dp <= 64);
 }
 
 }  // namespace lz

@@ -84,8 +84,11 @@ class _GLA(torch.autograd.Function):
         y = torch.empty_like(v)
         if y.numel():
             lib = _lib.load()
+            per_head = int(lg.dim() == 3)
+            nbytes = lib.lz_gla_fwd_workspace_bytes(b, h, length, nf, nd, per_head, chunk)
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=fq.device) if nbytes else None
             rc = lib.lz_gla_fwd(_ptr(fq), _ptr(fk), _ptr(v), _ptr(lg), _ptr(y), b, h, length,
-                                nf, nd, int(lg.dim() == 3), chunk, _stream(fq))
+                                nf, nd, per_head, chunk, _ptr(ws), nbytes, _stream(fq))
             _lib.check(rc, "lz_gla_fwd")
         if any(ctx.needs_input_grad[:4]):
             ctx.save_for_backward(fq, fk, v, lg)

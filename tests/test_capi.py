@@ -43,7 +43,7 @@ def test_abi_version_and_error_string(lib):
 
 
 def test_null_pointers_are_rejected_with_a_message(lib):
-    rc = lib.lz_gla_fwd(None, None, None, None, None, 1, 1, 8, 16, 16, 0, 64, None)
+    rc = lib.lz_gla_fwd(None, None, None, None, None, 1, 1, 8, 16, 16, 0, 64, None, 0, None)
     assert rc != 0 and b"null" in lib.lz_last_error()
     rc = lib.lz_swa_fwd(None, None, None, None, 0, None, None, None, 1, 1, 8, 16, 4, 0.25, None)
     assert rc != 0 and b"null" in lib.lz_last_error()
@@ -51,9 +51,9 @@ def test_null_pointers_are_rejected_with_a_message(lib):
 
 def test_bad_sizes_are_rejected_before_any_launch(lib):
     p = ctypes.c_void_p(16)   # never dereferenced: validation fails first
-    rc = lib.lz_gla_fwd(p, p, p, p, p, 1, 1, 8, 300, 16, 0, 64, None)
+    rc = lib.lz_gla_fwd(p, p, p, p, p, 1, 1, 8, 300, 16, 0, 64, None, 0, None)
     assert rc != 0 and b"unsupported" in lib.lz_last_error()
-    rc = lib.lz_gla_fwd(p, p, p, p, p, 1, 1, 8, 16, 16, 0, 48, None)
+    rc = lib.lz_gla_fwd(p, p, p, p, p, 1, 1, 8, 16, 16, 0, 48, None, 0, None)
     assert rc != 0 and b"chunk" in lib.lz_last_error()
     rc = lib.lz_swa_fwd(p, p, p, p, 65, p, p, p, 1, 1, 8, 16, 4, 0.25, None)
     assert rc != 0 and b"n_meta" in lib.lz_last_error()

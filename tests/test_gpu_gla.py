@@ -118,3 +118,21 @@ def test_gla_baseline_config4_per_head_d128_chunked():
     # (pinned against the dense oracle in tests/test_oracle.py)
     _baseline_case(1, 4, 2048, 128, True, 2.0, 1.5,
                    lambda *a: lo.gla_chunked(*a, chunk=64, dtype=torch.float32))
+
+
+@pytest.mark.parametrize("batch, heads, length", [(8, 64, 200), (1, 512, 333)])
+def test_gla_single_segment_walk(batch, heads, length):
+    # B*H >= 512 fills the GPU with one workgroup per (b, h): every workgroup
+    # walks all chunks of its sequence (no segment split)
+    inputs = gla_inputs(length, batch=batch, heads=heads, features=32, dim=32)
+    grad = torch.randn(inputs[2].shape, generator=torch.Generator().manual_seed(1))
+    compare(gla_kernel(64), gla_reference, inputs, grad, label=f"B*H={batch * heads} L={length}")
+
+
+@pytest.mark.parametrize("length", [64 * 24, 64 * 24 + 17])
+def test_gla_segments_of_several_chunks(length):
+    # B*H = 64: the sequence is split into 8 (or 7) segments of 3 (or 4)
+    # chunks, whose entering states come from the segment pass and scan
+    inputs = gla_inputs(length, batch=4, heads=16, features=64, dim=64)
+    grad = torch.randn(inputs[2].shape, generator=torch.Generator().manual_seed(1))
+    compare(gla_kernel(64), gla_reference, inputs, grad, label=f"segments L={length}")
