@@ -17,7 +17,7 @@ hipError_t launch_gla_bwd(const void* fq, const void* fk, const void* v, const f
                           const void* dy, void* dfq, void* dfk, void* dv, float* dlg,
                           bool grad_bf16, int B, int H, int L, int F, int D, int gate_per_head,
                           float* ws, hipStream_t st);
-size_t gla_bwd_workspace(int B, int H, int L);
+size_t gla_bwd_workspace(int B, int H, int L, int F, int D, int gate_per_head);
 bool gla_dims_supported(int F, int D);
 int swa_padded_dim(int d);
 hipError_t launch_swa_fwd(const void* q, const void* k, const void* v, const float* meta,
@@ -104,9 +104,9 @@ extern "C" int lz_gla_fwd(const void* fq, const void* fk, const void* v, const f
 
 extern "C" size_t lz_gla_bwd_workspace_bytes(int batch, int heads, int length, int nf, int nd,
                                              int gate_per_head, int chunk) {
-  (void)nf; (void)nd; (void)gate_per_head; (void)chunk;
-  if (batch <= 0 || heads <= 0 || length <= 0) return 0;
-  return lz::gla_bwd_workspace(batch, heads, length);
+  (void)chunk;
+  if (batch <= 0 || heads <= 0 || length <= 0 || !lz::gla_dims_supported(nf, nd)) return 0;
+  return lz::gla_bwd_workspace(batch, heads, length, nf, nd, gate_per_head ? 1 : 0);
 }
 
 extern "C" int lz_gla_bwd(const void* fq, const void* fk, const void* v, const float* log_gamma,
@@ -116,7 +116,7 @@ extern "C" int lz_gla_bwd(const void* fq, const void* fk, const void* v, const f
                           void* stream) {
   if (int rc = check_gla(fq, fk, v, log_gamma, batch, heads, length, nf, nd, chunk)) return rc;
   if (!dy || !dfq || !dfk || !dv || !dlog_gamma) return fail(1, "gla_bwd: null pointer");
-  const size_t need = lz::gla_bwd_workspace(batch, heads, length);
+  const size_t need = lz::gla_bwd_workspace(batch, heads, length, nf, nd, gate_per_head ? 1 : 0);
   if (!workspace || workspace_bytes < need)
     return fail(1, "gla_bwd: workspace of %zu bytes given, %zu needed", workspace_bytes, need);
   return hip_status(lz::launch_gla_bwd(fq, fk, v, log_gamma, dy, dfq, dfk, dv, dlog_gamma,

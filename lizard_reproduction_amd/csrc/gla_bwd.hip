@@ -3,127 +3,97 @@
 // Reference: _GLA.backward and its kernels (src/kernels/gla.py:104-194,
 // 236-256), with the autograd steps of the gate path (gla.py:260-262).  With
 // the chunk-local notation of gla_fwd.hip (lg, qs = e^{lg}, ks = e^{lg_end-lg},
-// r = e^{lg_end}, decay_it = e^{lg_i - lg_t}) and the forward state S_n, z_n:
+// r = e^{lg_end}, decay_it = e^{lg_i - lg_t}), S_n, z_n the forward state
+// entering chunk n, and dS, dz the gradient state flowing back into chunk n
+// from the chunks after it:
 //   delta_i = dy_i . y_i                              (fp32 y)
 //   dA_it   = [t<=i] (dy_i . v_t - delta_i) / den_i,  dad = dA * decay
 //   dfq_i   = sum_t dad_it fk_t + (qs_i/den_i) (dy_i S_n^T - delta_i z_n)
-//   dfk_t   = sum_i dad_it fq_i + ks_t (v_t dS_n^T - dz_n)
-//   dv_t    = sum_i (a_it/den_i) dy_i + K~_t dS_n
-//   dS_n    = r_{n+1} dS_{n+1} + Q^_{n+1}^T dY_{n+1},  Q^_i = bf16(fq_i qs_i / den_i)
-//   dz_n    = r_{n+1} dz_{n+1} + sum_i Q^_i delta_i
+//   dfk_t   = sum_i dad_it fq_i + ks_t (v_t dS^T - dz)
+//   dv_t    = sum_i (a_it/den_i) dy_i + K~_t dS
+//   dS <- r_n dS + Q^_n^T dY_n,  Q^_i = bf16(fq_i qs_i / den_i)   (after chunk n)
+//   dz <- r_n dz + sum_i Q^_i delta_i
 //   dG_j    = fq_j . dfq_j - fk_j . dfk_j,  d log_gamma = reverse cumsum of dG
 //             (summed over heads for a per-token gate)
 //
-// Three launches, none of which writes a state to HBM:
-//   A (forward walk, one workgroup per (b,h)): carries S^T (d x f) in MFMA
-//     accumulators; recomputes den and delta -- delta_i = dy_i . o_i / den_i
-//     with dy_i . o_i = Q~_i . (S_n dy_i) + sum_t a_it (v_t . dy_i), both
-//     products it needs anyway -- and writes dfq, den, delta and fq.dfq.
-//   B (reverse walk, one workgroup per (b,h)): carries dS (f x d) and dS^T
-//     (d x f) in accumulators (dv contracts the state over f, dfk over d, and
-//     an accumulator can only be contracted over its rows); writes dv, dfk and
-//     dG.
-//   G: d log_gamma = reverse cumsum of dG (head-summed for per-token gates).
-#include "common.hpp"
+// Launches (G = segments per (b, h), as in the forward; no state goes to HBM
+// except the per-segment records when G > 1):
+//   [G > 1] forward segment pass + scan (gla_fwd.hip): S, z entering each segment
+//   A  gla_bwd_dq_kernel, forward walk per (b, h, segment): carries S^T in
+//      MFMA accumulators; recomputes den and delta -- delta_i = dy_i . o_i /
+//      den_i with dy_i . o_i = Q~_i . (S_n dy_i) + sum_t a_it (v_t . dy_i), both
+//      products it needs anyway -- and writes dfq, den, delta and fq . dfq.
+//   [G > 1] gla_bwd_state_kernel + reverse scan: dS, dz entering each segment
+//      from the right (needs den and delta from A).
+//   B  gla_bwd_dkv_kernel, reverse walk per (b, h, segment): carries dS in
+//      accumulators and publishes it as bf16 dS^T in LDS each chunk (dv
+//      contracts the state over f straight from the accumulators, dfk over d
+//      through LDS transpose reads); writes dv, dfk and dG.
+//   gate: d log_gamma = reverse cumsum of dG over L (head-summed for a
+//      per-token gate), two small launches (block totals, then block scans).
+// Operand staging follows gla_fwd.hip: row-major tiles in LDS, operands that
+// contract over tokens from LDS transpose reads, next chunk prefetched into
+// registers.
+#include "gla_common.hpp"
 
 namespace lz {
 
-constexpr int GC = 64;   // chunk length
-
-// Stage rows [t0, t0+64) of a [L x ncols] matrix: natural tile (slot order
-// along the columns) and/or transposed tile (slot order along the tokens).
-template <int KP>
-__device__ __forceinline__ void stage_chunk(const bf16* __restrict__ src, int t0, int L, int ncols,
-                                            bf16* nat, int npitch, bf16* tr, int tpitch) {
-  constexpr int K4 = KP / 4;
-  for (int idx = threadIdx.x; idx < GC * K4; idx += 256) {
-    const int r = idx / K4, c = (idx % K4) * 4;
-    const bf16x4 x = load4(src, t0 + r, c, L, ncols);
-    if (nat) *reinterpret_cast<bf16x4*>(nat + r * npitch + pidx(c)) = x;
-    if (tr) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) tr[(c + e) * tpitch + pidx(r)] = x[e];
-    }
-  }
-}
-
-// Chunk-local inclusive scan of the gate by one wave; writes lg[64],
-// e^{lg}[64] (natural order), e^{end-lg} in slot order, and e^{end}.
-__device__ __forceinline__ void scan_gate(const float* __restrict__ lgb, int t0, int L, int lane,
-                                          float* lgs, float* qs, float* kss, float* rdec) {
-  float g = (t0 + lane < L) ? lgb[t0 + lane] : 0.f;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const float o = __shfl_up(g, off);
-    if (lane >= off) g += o;
-  }
-  const float end = __shfl(g, 63);
-  lgs[lane] = g;
-  qs[lane] = fexp(g);
-  kss[pidx(lane)] = fexp(end - g);
-  if (lane == 0) rdec[0] = fexp(end);
-}
-
-// Which 32-wide tiles of a dimension with NT32 tiles a wave owns, and which
-// 32-token halves of the chunk it pairs them with.  Every (tile, half) pair
-// has exactly one owner; with fewer than 4 tiles a tile is owned by two waves
-// (one per half), which then both keep that tile's state.
-template <int NT32>
-struct Own {
-  static constexpr int TILES = NT32 >= 4 ? NT32 / 4 : 1;
-  static constexpr int HALVES = NT32 >= 4 ? 2 : 1;
-  __device__ static bool active(int wave) { return NT32 >= 2 || wave < 2; }
-  __device__ static int tile(int wave, int i) {
-    return NT32 >= 4 ? wave + 4 * i : (NT32 == 2 ? (wave >> 1) : 0);
-  }
-  __device__ static int half(int wave, int j) { return NT32 >= 4 ? j : (wave & 1); }
+template <int FP, int DP>
+struct BwdCommon {
+  static constexpr int C = GLA_C;
+  static constexpr int PF = FP + 16, PD = DP + 16;
+  static constexpr int NFT = FP / 32, NDT = DP / 32;
+  static constexpr int ZPARTS = FP >= 256 ? 1 : 256 / FP;
+  static constexpr int NLF = C * FP / 8 / 256, NLD = C * DP / 8 / 256;
+  static constexpr int SEG = SegRec<FP, DP>::SIZE;
 };
 
-// ----------------------------------------------------------------------------
+// ============================================================================
 // kernel A: forward walk -> dfq, den, delta, p = fq . dfq
-// ----------------------------------------------------------------------------
+// ============================================================================
 template <int FP, int DP>
-struct BwdACfg {
-  static constexpr int NPF = FP + 8, NPD = DP + 8, TP = GC + 8;
-  static constexpr int OFF_FQN = 0;
-  static constexpr int OFF_FKN = OFF_FQN + GC * NPF * 2;
-  static constexpr int OFF_FKT = OFF_FKN + GC * NPF * 2;
-  static constexpr int OFF_VN = OFF_FKT + FP * TP * 2;
-  static constexpr int OFF_VT = OFF_VN + GC * NPD * 2;
-  static constexpr int OFF_DYN = OFF_VT + DP * TP * 2;
-  static constexpr int OFF_FR = OFF_DYN + GC * NPD * 2;          // dad fragments [2][4][64] bf16x8
-  static constexpr int OFF_RA = OFF_FR + 2 * 4 * 64 * 16;         // [2][64] sum_t a
-  static constexpr int OFF_RAV = OFF_RA + 2 * 64 * 4;             // [2][64] sum_t a (v.dy)
-  static constexpr int OFF_QZ = OFF_RAV + 2 * 64 * 4;             // [4][64] Q~.z partials
-  static constexpr int OFF_NX = OFF_QZ + 4 * 64 * 4;              // [8][64] Q~.(S dy) partials
-  static constexpr int OFF_PP = OFF_NX + 8 * 64 * 4;              // [8][64] fq.dfq partials
-  static constexpr int OFF_DEN = OFF_PP + 8 * 64 * 4;             // [64]
-  static constexpr int OFF_DEL = OFF_DEN + 64 * 4;                // [64]
+struct BwdA : BwdCommon<FP, DP> {
+  using B_ = BwdCommon<FP, DP>;
+  static constexpr int C = B_::C, PF = B_::PF, PD = B_::PD, NFT = B_::NFT, ZPARTS = B_::ZPARTS;
+  static constexpr int OFF_FQ = 0;
+  static constexpr int OFF_FK = OFF_FQ + C * PF * 2;
+  static constexpr int OFF_V = OFF_FK + C * PF * 2;
+  static constexpr int OFF_DY = OFF_V + C * PD * 2;
+  static constexpr int OFF_FR = OFF_DY + C * PD * 2;       // dad fragments [2 qt][4 kb][64]
+  static constexpr int OFF_RA = OFF_FR + 2 * 4 * 64 * 16;  // [2][64] sum_t a
+  static constexpr int OFF_RAV = OFF_RA + 2 * 64 * 4;      // [2][64] sum_t a (v . dy)
+  static constexpr int OFF_QZ = OFF_RAV + 2 * 64 * 4;      // [4][64] Q~ . z partials
+  static constexpr int OFF_NX = OFF_QZ + 4 * 64 * 4;       // [NFT][64] Q~ . (S dy) partials
+  static constexpr int OFF_PP = OFF_NX + NFT * 64 * 4;     // [NFT][64] fq . dfq partials
+  static constexpr int OFF_DEN = OFF_PP + NFT * 64 * 4;
+  static constexpr int OFF_DEL = OFF_DEN + 64 * 4;
   static constexpr int OFF_LG = OFF_DEL + 64 * 4;
   static constexpr int OFF_QS = OFF_LG + 64 * 4;
   static constexpr int OFF_KS = OFF_QS + 64 * 4;
-  static constexpr int OFF_Z = OFF_KS + 64 * 4;                   // [FP] natural order
-  static constexpr int OFF_R = OFF_Z + FP * 4;
+  static constexpr int OFF_Z = OFF_KS + 64 * 4;
+  static constexpr int OFF_ZP = OFF_Z + FP * 4;
+  static constexpr int OFF_R = OFF_ZP + ZPARTS * FP * 4;
   static constexpr int BYTES = OFF_R + 16;
+  static constexpr int LB = (FP >= 256 || FP + DP >= 192) ? 1 : 2;
 };
 
 template <int FP, int DP, typename OutT>
-__global__ __launch_bounds__(256) void gla_bwd_a_kernel(
+__global__ __launch_bounds__(256, (BwdA<FP, DP>::LB)) void gla_bwd_dq_kernel(
     const bf16* __restrict__ fq, const bf16* __restrict__ fk, const bf16* __restrict__ v,
     const float* __restrict__ log_gamma, const bf16* __restrict__ dy, OutT* __restrict__ dfq,
-    float* __restrict__ den_out, float* __restrict__ delta_out, float* __restrict__ p_out, int H,
-    int L, int F, int D, int gate_per_head) {
-  using Cfg = BwdACfg<FP, DP>;
-  constexpr int NPF = Cfg::NPF, NPD = Cfg::NPD, TP = Cfg::TP;
-  constexpr int NFT = FP / 32, NDT = DP / 32;
-  using OF = Own<NFT>;
+    float* __restrict__ den_out, float* __restrict__ delta_out, float* __restrict__ p_out,
+    const float* __restrict__ seg_state, int H, int L, int F, int D, int gate_per_head, int G,
+    int cps) {
+  using Cfg = BwdA<FP, DP>;
+  constexpr int C = Cfg::C, PF = Cfg::PF, PD = Cfg::PD;
+  constexpr int NFT = Cfg::NFT, NDT = Cfg::NDT;
+  using RF = Roles<NFT>;
+  constexpr int NFW = RF::TILES, NQW = RF::HALVES;
   extern __shared__ __align__(16) char smem[];
-  bf16* fqn = reinterpret_cast<bf16*>(smem + Cfg::OFF_FQN);
-  bf16* fkn = reinterpret_cast<bf16*>(smem + Cfg::OFF_FKN);
-  bf16* fkt = reinterpret_cast<bf16*>(smem + Cfg::OFF_FKT);
-  bf16* vn = reinterpret_cast<bf16*>(smem + Cfg::OFF_VN);
-  bf16* vt = reinterpret_cast<bf16*>(smem + Cfg::OFF_VT);
-  bf16* dyn = reinterpret_cast<bf16*>(smem + Cfg::OFF_DYN);
+  bf16* fq_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_FQ);
+  bf16* fk_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_FK);
+  bf16* v_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_V);
+  bf16* dy_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_DY);
   bf16x8* fr = reinterpret_cast<bf16x8*>(smem + Cfg::OFF_FR);
   float* ra = reinterpret_cast<float*>(smem + Cfg::OFF_RA);
   float* rav = reinterpret_cast<float*>(smem + Cfg::OFF_RAV);
@@ -134,57 +104,73 @@ __global__ __launch_bounds__(256) void gla_bwd_a_kernel(
   float* dels = reinterpret_cast<float*>(smem + Cfg::OFF_DEL);
   float* lgs = reinterpret_cast<float*>(smem + Cfg::OFF_LG);
   float* qs = reinterpret_cast<float*>(smem + Cfg::OFF_QS);
-  float* kss = reinterpret_cast<float*>(smem + Cfg::OFF_KS);
+  float* ks = reinterpret_cast<float*>(smem + Cfg::OFF_KS);
   float* zs = reinterpret_cast<float*>(smem + Cfg::OFF_Z);
+  float* zp = reinterpret_cast<float*>(smem + Cfg::OFF_ZP);
   float* rdec = reinterpret_cast<float*>(smem + Cfg::OFF_R);
 
-  const int bh = blockIdx.x;
+  const int bh = blockIdx.x / G, seg = blockIdx.x % G;
+  const int NT = (L + C - 1) / C;
+  const int n0 = seg * cps, n1 = min(NT, n0 + cps);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int col = lane & 31, h = lane >> 5;
+  const bool vecF = (F & 7) == 0, vecD = (D & 7) == 0;
   const size_t offF = (size_t)bh * L * F, offD = (size_t)bh * L * D, offL = (size_t)bh * L;
   const float* lgb = log_gamma + (size_t)(gate_per_head ? bh : bh / H) * L;
+  const float* st = G > 1 ? seg_state + ((size_t)bh * G + seg) * Cfg::SEG : nullptr;
+  const bool active = RF::active(wave);
 
-  for (int f = tid; f < FP; f += 256) zs[f] = 0.f;
+  // S^T tiles (rows d, columns f) of the owned f-tiles, all d-tiles
+  f32x16 St[NFW][NDT];
+#pragma unroll
+  for (int i = 0; i < NFW; ++i)
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      St[i][dt] = zero16();
+      if (st && active) {
+        const int f = RF::tile(wave, i) * 32 + col;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) St[i][dt][r] = st[f * DP + dt * 32 + acc_row(r, h)];
+      }
+    }
+  for (int f = tid; f < FP; f += 256) zs[f] = st ? st[FP * DP + f] : 0.f;
 
-  // S^T[d-tile][owned f-tile]: rows d, cols f
-  f32x16 St[NDT][OF::TILES];
-#pragma unroll
-  for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-    for (int i = 0; i < OF::TILES; ++i) St[dt][i] = zero16();
+  uint4 rq[Cfg::NLF], rk[Cfg::NLF], rv[Cfg::NLD], rd[Cfg::NLD];
+  float rg;
+  load_chunk<FP>(rq, fq + offF, n0 * C, L, F, vecF);
+  load_chunk<FP>(rk, fk + offF, n0 * C, L, F, vecF);
+  load_chunk<DP>(rv, v + offD, n0 * C, L, D, vecD);
+  load_chunk<DP>(rd, dy + offD, n0 * C, L, D, vecD);
+  rg = gate_at(lgb, n0 * C + lane, L);
+  store_chunk<FP>(rq, fq_l, PF);
+  store_chunk<FP>(rk, fk_l, PF);
+  store_chunk<DP>(rv, v_l, PD);
+  store_chunk<DP>(rd, dy_l, PD);
+  if (wave == 0) gate_scan(rg, lane, lgs, qs, ks, rdec);
+  __syncthreads();
 
   const int kt = wave >> 1, qt = wave & 1;   // this wave's tile of the 64x64 score block
   const int qi = qt * 32 + col;               // chunk-local query of this lane
-  const int NT = (L + GC - 1) / GC;
-  for (int n = 0; n < NT; ++n) {
-    const int t0 = n * GC;
-    __syncthreads();
-    if (n > 0 && tid < 64 && t0 - GC + tid < L) {   // fq.dfq of the previous chunk
-      float s = 0.f;
-      for (int ft = 0; ft < NFT; ++ft) s += pp[ft * 64 + tid];
-      p_out[offL + t0 - GC + tid] = s;
+  for (int n = n0; n < n1; ++n) {
+    const int t0 = n * C;
+    const bool more = n + 1 < n1;
+    if (more) {
+      load_chunk<FP>(rq, fq + offF, t0 + C, L, F, vecF);
+      load_chunk<FP>(rk, fk + offF, t0 + C, L, F, vecF);
+      load_chunk<DP>(rv, v + offD, t0 + C, L, D, vecD);
+      load_chunk<DP>(rd, dy + offD, t0 + C, L, D, vecD);
+      rg = gate_at(lgb, t0 + C + lane, L);
     }
-    stage_chunk<FP>(fq + offF, t0, L, F, fqn, NPF, nullptr, 0);
-    stage_chunk<FP>(fk + offF, t0, L, F, fkn, NPF, fkt, TP);
-    stage_chunk<DP>(v + offD, t0, L, D, vn, NPD, vt, TP);
-    stage_chunk<DP>(dy + offD, t0, L, D, dyn, NPD, nullptr, 0);
-    if (wave == 0) scan_gate(lgb, t0, L, lane, lgs, qs, kss, rdec);
-    __syncthreads();
-
-    // ---- P1: a^T and (v dy^T) tile of this wave; X = S dy^T ----------------
+    // ---- phase 1: a^T and (v dy^T) tile; Q~.z; sums of K~; X = S dy^T --------
     f32x16 aT = zero16(), vdy = zero16();
 #pragma unroll
-    for (int kb = 0; kb < FP / 16; ++kb) {
-      const bf16x8 a = *reinterpret_cast<const bf16x8*>(fkn + (kt * 32 + col) * NPF + 16 * kb + 8 * h);
-      const bf16x8 b = *reinterpret_cast<const bf16x8*>(fqn + qi * NPF + 16 * kb + 8 * h);
-      aT = mfma(a, b, aT);
-    }
+    for (int kb = 0; kb < FP / 16; ++kb)
+      aT = mfma(row_operand(fk_l, PF, kt * 32 + col, 16 * kb, h),
+                row_operand(fq_l, PF, qi, 16 * kb, h), aT);
 #pragma unroll
-    for (int kb = 0; kb < DP / 16; ++kb) {
-      const bf16x8 a = *reinterpret_cast<const bf16x8*>(vn + (kt * 32 + col) * NPD + 16 * kb + 8 * h);
-      const bf16x8 b = *reinterpret_cast<const bf16x8*>(dyn + qi * NPD + 16 * kb + 8 * h);
-      vdy = mfma(a, b, vdy);
-    }
+    for (int kb = 0; kb < DP / 16; ++kb)
+      vdy = mfma(row_operand(v_l, PD, kt * 32 + col, 16 * kb, h),
+                 row_operand(dy_l, PD, qi, 16 * kb, h), vdy);
     const float lgq = lgs[qi];
     {
       float sa = 0.f, sav = 0.f;
@@ -202,34 +188,46 @@ __global__ __launch_bounds__(256) void gla_bwd_a_kernel(
         ra[kt * 64 + qi] = sa;
         rav[kt * 64 + qi] = sav;
       }
-      constexpr int FQ = FP / 4;   // Q~ . z over a quarter of the features, query = lane
+      constexpr int FQ = FP / 4;   // Q~ . z over a quarter of the features; query = lane
       const float qsv = qs[lane];
       float acc = 0.f;
-      for (int fs = wave * FQ; fs < (wave + 1) * FQ; ++fs)
-        acc += to_f32(to_bf16(to_f32(fqn[lane * NPF + fs]) * qsv)) * zs[pidx(fs)];
+#pragma unroll
+      for (int c = 0; c < FQ; c += 8) {
+        const bf16x8 x = *reinterpret_cast<const bf16x8*>(fq_l + lane * PF + wave * FQ + c);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc += to_f32(to_bf16(to_f32(x[e]) * qsv)) * zs[wave * FQ + c + e];
+      }
       qz[wave * 64 + lane] = acc;
+      constexpr int TPP = C / Cfg::ZPARTS;
+      const int f = tid % FP, part = tid / FP;
+      if (part < Cfg::ZPARTS) {
+        float za = 0.f;
+#pragma unroll 8
+        for (int t = part * TPP; t < (part + 1) * TPP; ++t)
+          za += to_f32(to_bf16(to_f32(fk_l[t * PF + f]) * ks[t]));
+        zp[part * FP + f] = za;
+      }
     }
-    f32x16 X[OF::TILES][OF::HALVES];
-    if (OF::active(wave)) {
+    f32x16 X[NFW][NQW];
+    if (active) {
 #pragma unroll
-      for (int i = 0; i < OF::TILES; ++i) {
-        const int ft = OF::tile(wave, i);
+      for (int i = 0; i < NFW; ++i) {
+        const int ft = RF::tile(wave, i);
 #pragma unroll
-        for (int j = 0; j < OF::HALVES; ++j) {
-          const int q = OF::half(wave, j) * 32 + col;
+        for (int j = 0; j < NQW; ++j) {
+          const int q = RF::half(wave, j) * 32 + col;
           f32x16 x = zero16();
 #pragma unroll
-          for (int kb = 0; kb < DP / 16; ++kb) {
-            const bf16x8 b = *reinterpret_cast<const bf16x8*>(dyn + q * NPD + 16 * kb + 8 * h);
-            x = mfma(acc_operand(St[kb >> 1][i], kb & 1), b, x);
-          }
+          for (int kb = 0; kb < DP / 16; ++kb)
+            x = mfma(acc_operand(St[i][kb >> 1], kb & 1), row_operand_acc(dy_l, PD, q, 16 * kb, h), x);
           X[i][j] = x;
           const float qsv = qs[q];
           float s = 0.f;
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int f = ft * 32 + acc_row(r, h);
-            s += to_f32(to_bf16(to_f32(fqn[q * NPF + pidx(f)]) * qsv)) * x[r];
+          for (int g4 = 0; g4 < 4; ++g4) {
+            const bf16x4 f4 = *reinterpret_cast<const bf16x4*>(fq_l + q * PF + ft * 32 + 8 * g4 + 4 * h);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) s += to_f32(to_bf16(to_f32(f4[e]) * qsv)) * x[4 * g4 + e];
           }
           s += xhalf(s);
           if (h == 0) nx[ft * 64 + q] = s;
@@ -237,11 +235,11 @@ __global__ __launch_bounds__(256) void gla_bwd_a_kernel(
       }
     }
     __syncthreads();
-
-    // ---- P2: den, delta and dad fragments -----------------------------------
+    // ---- phase 2: den, delta, dad fragments ------------------------------------
     {
       const float den = ra[qi] + ra[64 + qi] + qz[qi] + qz[64 + qi] + qz[128 + qi] + qz[192 + qi];
       float num = rav[qi] + rav[64 + qi];
+#pragma unroll
       for (int ft = 0; ft < NFT; ++ft) num += nx[ft * 64 + qi];
       const float dcl = fmaxf(den, TINY);
       const float delta = num / dcl;
@@ -265,199 +263,410 @@ __global__ __launch_bounds__(256) void gla_bwd_a_kernel(
       }
     }
     __syncthreads();
-
-    // ---- P3: dfq for owned (f-tile, half); S^T and z update -----------------
+    // ---- phase 3: dfq and fq . dfq for owned (f-tile, half); S^T update --------
     const float r_n = rdec[0];
-    if (OF::active(wave)) {
+    if (active) {
 #pragma unroll
-      for (int i = 0; i < OF::TILES; ++i) {
-        const int ft = OF::tile(wave, i);
+      for (int i = 0; i < NFW; ++i) {
+        const int ft = RF::tile(wave, i);
+        bf16x8 fkr[4];   // fk^T rows of this f-tile (A of fk^T dad^T); scaled by ks it is K~
 #pragma unroll
-        for (int j = 0; j < OF::HALVES; ++j) {
-          const int hq = OF::half(wave, j);
+        for (int kb = 0; kb < 4; ++kb) fkr[kb] = tr_operand(fk_l, PF, 16 * kb, ft * 32, lane);
+#pragma unroll
+        for (int j = 0; j < NQW; ++j) {
+          const int hq = RF::half(wave, j);
           const int q = hq * 32 + col;
           f32x16 g = zero16();
 #pragma unroll
-          for (int kb = 0; kb < 4; ++kb) {
-            const bf16x8 a = *reinterpret_cast<const bf16x8*>(fkt + (ft * 32 + col) * TP + 16 * kb + 8 * h);
-            g = mfma(a, fr[(hq * 4 + kb) * 64 + lane], g);
-          }
+          for (int kb = 0; kb < 4; ++kb) g = mfma(fkr[kb], fr[(hq * 4 + kb) * 64 + lane], g);
           const float dcl = fmaxf(dens[q], TINY);
           const float qsd = qs[q] / dcl;
           const float delta = dels[q];
           const int tok = t0 + q;
           float ps = 0.f;
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int f = ft * 32 + acc_row(r, h);
-            g[r] += qsd * (X[i][j][r] - zs[f] * delta);
-            ps += to_f32(fqn[q * NPF + pidx(f)]) * g[r];
+          for (int g4 = 0; g4 < 4; ++g4) {
+            const bf16x4 f4 = *reinterpret_cast<const bf16x4*>(fq_l + q * PF + ft * 32 + 8 * g4 + 4 * h);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int r = 4 * g4 + e, f = ft * 32 + 8 * g4 + 4 * h + e;
+              g[r] += qsd * (X[i][j][r] - zs[f] * delta);
+              ps += to_f32(f4[e]) * g[r];
+            }
           }
           ps += xhalf(ps);
           if (h == 0) pp[ft * 64 + q] = tok < L ? ps : 0.f;
           if (tok < L) {
 #pragma unroll
-            for (int gg = 0; gg < 4; ++gg)
-              store4<OutT>(dfq + offF, tok, ft * 32 + 8 * gg + 4 * h, F, g[4 * gg],
-                           g[4 * gg + 1], g[4 * gg + 2], g[4 * gg + 3]);
+            for (int g4 = 0; g4 < 4; ++g4)
+              store4<OutT>(dfq + offF, tok, ft * 32 + 8 * g4 + 4 * h, F, g[4 * g4],
+                           g[4 * g4 + 1], g[4 * g4 + 2], g[4 * g4 + 3]);
           }
         }
         // S^T[:, ft] <- r S^T + V^T K~
 #pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+          const f32x4 klo = *reinterpret_cast<const f32x4*>(ks + 16 * kb + 4 * h);
+          const f32x4 khi = *reinterpret_cast<const f32x4*>(ks + 16 * kb + 8 + 4 * h);
+          fkr[kb] = scale8v(fkr[kb], klo, khi);
+        }
+#pragma unroll
         for (int dt = 0; dt < NDT; ++dt) {
 #pragma unroll
-          for (int r = 0; r < 16; ++r) St[dt][i][r] *= r_n;
+          for (int r = 0; r < 16; ++r) St[i][dt][r] *= r_n;
 #pragma unroll
-          for (int kb = 0; kb < 4; ++kb) {
-            const bf16x8 a = *reinterpret_cast<const bf16x8*>(vt + (dt * 32 + col) * TP + 16 * kb + 8 * h);
-            const bf16x8 raw = *reinterpret_cast<const bf16x8*>(fkt + (ft * 32 + col) * TP + 16 * kb + 8 * h);
-            bf16x8 b;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) b[e] = to_bf16(to_f32(raw[e]) * kss[16 * kb + 8 * h + e]);
-            St[dt][i] = mfma(a, b, St[dt][i]);
-          }
+          for (int kb = 0; kb < 4; ++kb)
+            St[i][dt] = mfma(tr_operand(v_l, PD, 16 * kb, dt * 32, lane), fkr[kb], St[i][dt]);
         }
       }
     }
-    __syncthreads();   // z is read above (P3) before it is updated
-    for (int f = tid; f < FP; f += 256) {
-      float acc = 0.f;
-      for (int t = 0; t < GC; ++t) acc += to_f32(to_bf16(to_f32(fkt[f * TP + t]) * kss[t]));
-      zs[f] = zs[f] * r_n + acc;
-    }
-  }
-  __syncthreads();
-  {
-    const int t0 = (NT - 1) * GC;
+    __syncthreads();
+    // ---- next chunk into LDS; z update; fq . dfq of this chunk ------------------
     if (tid < 64 && t0 + tid < L) {
       float s = 0.f;
+#pragma unroll
       for (int ft = 0; ft < NFT; ++ft) s += pp[ft * 64 + tid];
       p_out[offL + t0 + tid] = s;
     }
+    if (more) {
+      store_chunk<FP>(rq, fq_l, PF);
+      store_chunk<FP>(rk, fk_l, PF);
+      store_chunk<DP>(rv, v_l, PD);
+      store_chunk<DP>(rd, dy_l, PD);
+      if (wave == 0) gate_scan(rg, lane, lgs, qs, ks, rdec);
+    }
+    if (tid < FP) {
+      float za = zs[tid] * r_n;
+#pragma unroll
+      for (int p = 0; p < Cfg::ZPARTS; ++p) za += zp[p * FP + tid];
+      zs[tid] = za;
+    }
+    __syncthreads();
   }
 }
 
-// ----------------------------------------------------------------------------
-// kernel B: reverse walk -> dv, dfk, dG = p - fk . dfk
-// ----------------------------------------------------------------------------
+// ============================================================================
+// per-token scalars of the reverse walks: the gate scan of a chunk plus
+// den (clamped), delta, p and Q^ scale qs/den, by one wave (lane = token)
+// ============================================================================
+__device__ __forceinline__ void bwd_scalars(float g, float den, float delta, float p, int lane,
+                                            float* lgs, float* qs, float* ks, float* r,
+                                            float* dens, float* dels, float* ps, float* qh) {
+  gate_scan(g, lane, lgs, qs, ks, r);
+  const float dcl = fmaxf(den, TINY);
+  dens[lane] = dcl;
+  dels[lane] = delta;
+  if (ps) ps[lane] = p;
+  qh[lane] = qs[lane] / dcl;
+}
+
+struct TokScalars {
+  float g, den, delta, p;
+};
+
+__device__ __forceinline__ TokScalars load_scalars(const float* __restrict__ lgb,
+                                                   const float* __restrict__ den_in,
+                                                   const float* __restrict__ delta_in,
+                                                   const float* __restrict__ p_in, size_t offL,
+                                                   int t, int L) {
+  TokScalars s;
+  const bool ok = t < L;
+  s.g = ok ? lgb[t] : 0.f;
+  s.den = ok ? den_in[offL + t] : 1.f;
+  s.delta = ok ? delta_in[offL + t] : 0.f;
+  s.p = (ok && p_in) ? p_in[offL + t] : 0.f;
+  return s;
+}
+
+// ============================================================================
+// reverse segment pass: gradient state left by segment g > 0 walking
+// backwards from zero
+// ============================================================================
 template <int FP, int DP>
-struct BwdBCfg {
-  static constexpr int NPF = FP + 8, NPD = DP + 8, TP = GC + 8;
-  static constexpr int OFF_FQN = 0;
-  static constexpr int OFF_FQT = OFF_FQN + GC * NPF * 2;
-  static constexpr int OFF_FKN = OFF_FQT + FP * TP * 2;
-  static constexpr int OFF_VN = OFF_FKN + GC * NPF * 2;
-  static constexpr int OFF_DYN = OFF_VN + GC * NPD * 2;
-  static constexpr int OFF_DYT = OFF_DYN + GC * NPD * 2;
-  static constexpr int OFF_FA = OFF_DYT + DP * TP * 2;           // a/den fragments [2 kt][4 qb][64]
-  static constexpr int OFF_FD = OFF_FA + 2 * 4 * 64 * 16;         // dad fragments
-  static constexpr int OFF_PK = OFF_FD + 2 * 4 * 64 * 16;         // [8][64] fk.dfk partials
-  static constexpr int OFF_DEN = OFF_PK + 8 * 64 * 4;             // [64] natural
-  static constexpr int OFF_DEL = OFF_DEN + 64 * 4;                // [64] natural
-  static constexpr int OFF_P = OFF_DEL + 64 * 4;                  // [64] fq.dfq
-  static constexpr int OFF_QH = OFF_P + 64 * 4;                   // [64] e^{lg}/den, slot order
-  static constexpr int OFF_LG = OFF_QH + 64 * 4;
+struct BwdS : BwdCommon<FP, DP> {
+  using B_ = BwdCommon<FP, DP>;
+  static constexpr int C = B_::C, PF = B_::PF, PD = B_::PD, ZPARTS = B_::ZPARTS;
+  static constexpr int OFF_FQ = 0;
+  static constexpr int OFF_DY = OFF_FQ + C * PF * 2;
+  static constexpr int OFF_LG = OFF_DY + C * PD * 2;
   static constexpr int OFF_QS = OFF_LG + 64 * 4;
-  static constexpr int OFF_KS = OFF_QS + 64 * 4;                  // slot order
-  static constexpr int OFF_KSN = OFF_KS + 64 * 4;                 // natural order
-  static constexpr int OFF_DZ = OFF_KSN + 64 * 4;                 // [2][FP] double-buffered dz
-  static constexpr int OFF_R = OFF_DZ + 2 * FP * 4;
+  static constexpr int OFF_KS = OFF_QS + 64 * 4;
+  static constexpr int OFF_DEN = OFF_KS + 64 * 4;
+  static constexpr int OFF_DEL = OFF_DEN + 64 * 4;
+  static constexpr int OFF_QH = OFF_DEL + 64 * 4;
+  static constexpr int OFF_DZ = OFF_QH + 64 * 4;
+  static constexpr int OFF_DZP = OFF_DZ + FP * 4;
+  static constexpr int OFF_R = OFF_DZP + ZPARTS * FP * 4;
   static constexpr int BYTES = OFF_R + 16;
 };
 
+template <int FP, int DP>
+__global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_bwd_state_kernel(
+    const bf16* __restrict__ fq, const bf16* __restrict__ dy, const float* __restrict__ log_gamma,
+    const float* __restrict__ den_in, const float* __restrict__ delta_in,
+    float* __restrict__ seg_state, float* __restrict__ seg_logdecay, int H, int L, int F, int D,
+    int gate_per_head, int G, int cps) {
+  using Cfg = BwdS<FP, DP>;
+  constexpr int C = Cfg::C, PF = Cfg::PF, PD = Cfg::PD;
+  constexpr int NFT = Cfg::NFT, NDT = Cfg::NDT, NTILE = NFT * NDT, TPW = (NTILE + 3) / 4;
+  extern __shared__ __align__(16) char smem[];
+  bf16* fq_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_FQ);
+  bf16* dy_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_DY);
+  float* lgs = reinterpret_cast<float*>(smem + Cfg::OFF_LG);
+  float* qs = reinterpret_cast<float*>(smem + Cfg::OFF_QS);
+  float* ks = reinterpret_cast<float*>(smem + Cfg::OFF_KS);
+  float* dens = reinterpret_cast<float*>(smem + Cfg::OFF_DEN);
+  float* dels = reinterpret_cast<float*>(smem + Cfg::OFF_DEL);
+  float* qh = reinterpret_cast<float*>(smem + Cfg::OFF_QH);
+  float* dzs = reinterpret_cast<float*>(smem + Cfg::OFF_DZ);
+  float* dzp = reinterpret_cast<float*>(smem + Cfg::OFF_DZP);
+  float* rdec = reinterpret_cast<float*>(smem + Cfg::OFF_R);
+
+  const int bh = blockIdx.x / (G - 1), seg = 1 + blockIdx.x % (G - 1);
+  const int NT = (L + C - 1) / C;
+  const int n0 = seg * cps, n1 = min(NT, n0 + cps);
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int col = lane & 31, h = lane >> 5;
+  const bool vecF = (F & 7) == 0, vecD = (D & 7) == 0;
+  const size_t offF = (size_t)bh * L * F, offD = (size_t)bh * L * D, offL = (size_t)bh * L;
+  const float* lgb = log_gamma + (size_t)(gate_per_head ? bh : bh / H) * L;
+
+  f32x16 dS[TPW];
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) dS[i] = zero16();
+  for (int f = tid; f < FP; f += 256) dzs[f] = 0.f;
+  float lam = 0.f;
+
+  uint4 rq[Cfg::NLF], rd[Cfg::NLD];
+  TokScalars sc;
+  load_chunk<FP>(rq, fq + offF, (n1 - 1) * C, L, F, vecF);
+  load_chunk<DP>(rd, dy + offD, (n1 - 1) * C, L, D, vecD);
+  sc = load_scalars(lgb, den_in, delta_in, nullptr, offL, (n1 - 1) * C + lane, L);
+  store_chunk<FP>(rq, fq_l, PF);
+  store_chunk<DP>(rd, dy_l, PD);
+  if (wave == 0)
+    bwd_scalars(sc.g, sc.den, sc.delta, 0.f, lane, lgs, qs, ks, rdec, dens, dels, nullptr, qh);
+  __syncthreads();
+
+  for (int n = n1 - 1; n >= n0; --n) {
+    const bool more = n - 1 >= n0;
+    if (more) {
+      load_chunk<FP>(rq, fq + offF, (n - 1) * C, L, F, vecF);
+      load_chunk<DP>(rd, dy + offD, (n - 1) * C, L, D, vecD);
+      sc = load_scalars(lgb, den_in, delta_in, nullptr, offL, (n - 1) * C + lane, L);
+    }
+    const float r_n = rdec[0];
+    if (wave == 0) lam += rdec[1];
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+      const int ti = wave + 4 * i;
+      if (ti < NTILE) {
+        const int ft = ti / NDT, dt = ti % NDT;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dS[i][r] *= r_n;
+#pragma unroll
+        for (int qb = 0; qb < 4; ++qb) {
+          const f32x4 qlo = *reinterpret_cast<const f32x4*>(qh + 16 * qb + 4 * h);
+          const f32x4 qhi = *reinterpret_cast<const f32x4*>(qh + 16 * qb + 8 + 4 * h);
+          dS[i] = mfma(scale8v(tr_operand(fq_l, PF, 16 * qb, ft * 32, lane), qlo, qhi),
+                       tr_operand(dy_l, PD, 16 * qb, dt * 32, lane), dS[i]);
+        }
+      }
+    }
+    {
+      constexpr int TPP = C / Cfg::ZPARTS;
+      const int f = tid % FP, part = tid / FP;
+      if (part < Cfg::ZPARTS) {
+        float za = 0.f;
+#pragma unroll 8
+        for (int t = part * TPP; t < (part + 1) * TPP; ++t)
+          za += to_f32(to_bf16(to_f32(fq_l[t * PF + f]) * qh[t])) * dels[t];
+        dzp[part * FP + f] = za;
+      }
+    }
+    __syncthreads();
+    if (more) {
+      store_chunk<FP>(rq, fq_l, PF);
+      store_chunk<DP>(rd, dy_l, PD);
+      if (wave == 0)
+        bwd_scalars(sc.g, sc.den, sc.delta, 0.f, lane, lgs, qs, ks, rdec, dens, dels, nullptr, qh);
+    }
+    if (tid < FP) {
+      float za = dzs[tid] * r_n;
+#pragma unroll
+      for (int p = 0; p < Cfg::ZPARTS; ++p) za += dzp[p * FP + tid];
+      dzs[tid] = za;
+    }
+    __syncthreads();
+  }
+  float* out = seg_state + ((size_t)bh * G + seg) * Cfg::SEG;
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) {
+    const int ti = wave + 4 * i;
+    if (ti < NTILE) {
+      const int ft = ti / NDT, dt = ti % NDT;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) out[(ft * 32 + acc_row(r, h)) * DP + dt * 32 + col] = dS[i][r];
+    }
+  }
+  for (int f = tid; f < FP; f += 256) out[FP * DP + f] = dzs[f];
+  if (tid == 0) seg_logdecay[(size_t)bh * G + seg] = lam;
+}
+
+// ============================================================================
+// kernel B: reverse walk -> dv, dfk, dG = p - fk . dfk
+// ============================================================================
+template <int FP, int DP>
+struct BwdB : BwdCommon<FP, DP> {
+  using B_ = BwdCommon<FP, DP>;
+  static constexpr int C = B_::C, PF = B_::PF, PD = B_::PD, NFT = B_::NFT, ZPARTS = B_::ZPARTS;
+  static constexpr int OFF_FQ = 0;
+  static constexpr int OFF_FK = OFF_FQ + C * PF * 2;
+  static constexpr int OFF_V = OFF_FK + C * PF * 2;
+  static constexpr int OFF_DY = OFF_V + C * PD * 2;
+  static constexpr int OFF_DST = OFF_DY + C * PD * 2;     // dS^T [DP][PF] bf16
+  static constexpr int OFF_FA = OFF_DST + DP * PF * 2;    // a/den fragments [2 kt][4 qb][64]
+  static constexpr int OFF_FD = OFF_FA + 2 * 4 * 64 * 16; // dad fragments
+  static constexpr int OFF_PK = OFF_FD + 2 * 4 * 64 * 16; // [NFT][64] fk . dfk partials
+  static constexpr int OFF_DEN = OFF_PK + NFT * 64 * 4;   // [2][64] (by chunk parity)
+  static constexpr int OFF_DEL = OFF_DEN + 2 * 64 * 4;
+  static constexpr int OFF_P = OFF_DEL + 2 * 64 * 4;
+  static constexpr int OFF_QH = OFF_P + 2 * 64 * 4;
+  static constexpr int OFF_LG = OFF_QH + 2 * 64 * 4;
+  static constexpr int OFF_QS = OFF_LG + 64 * 4;
+  static constexpr int OFF_KS = OFF_QS + 64 * 4;
+  static constexpr int OFF_DZ = OFF_KS + 64 * 4;
+  static constexpr int OFF_DZP = OFF_DZ + FP * 4;
+  static constexpr int OFF_R = OFF_DZP + ZPARTS * FP * 4;
+  static constexpr int BYTES = OFF_R + 16;
+  static constexpr int LB = (FP >= 256 || FP + DP >= 160) ? 1 : 2;
+};
+
 template <int FP, int DP, typename OutT>
-__global__ __launch_bounds__(256) void gla_bwd_b_kernel(
+__global__ __launch_bounds__(256, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_kernel(
     const bf16* __restrict__ fq, const bf16* __restrict__ fk, const bf16* __restrict__ v,
     const float* __restrict__ log_gamma, const bf16* __restrict__ dy,
     const float* __restrict__ den_in, const float* __restrict__ delta_in,
     const float* __restrict__ p_in, OutT* __restrict__ dfk, OutT* __restrict__ dv,
-    float* __restrict__ dG, int H, int L, int F, int D, int gate_per_head) {
-  using Cfg = BwdBCfg<FP, DP>;
-  constexpr int NPF = Cfg::NPF, NPD = Cfg::NPD, TP = Cfg::TP;
-  constexpr int NFT = FP / 32, NDT = DP / 32;
-  using OF = Own<NFT>;
-  using OD = Own<NDT>;
+    float* __restrict__ dG, const float* __restrict__ seg_state, int H, int L, int F, int D,
+    int gate_per_head, int G, int cps) {
+  using Cfg = BwdB<FP, DP>;
+  constexpr int C = Cfg::C, PF = Cfg::PF, PD = Cfg::PD;
+  constexpr int NFT = Cfg::NFT, NDT = Cfg::NDT;
+  using RD = Roles<NDT>;   // dv and the dS state by d-tile
+  using RF = Roles<NFT>;   // dfk by f-tile
   extern __shared__ __align__(16) char smem[];
-  bf16* fqn = reinterpret_cast<bf16*>(smem + Cfg::OFF_FQN);
-  bf16* fqt = reinterpret_cast<bf16*>(smem + Cfg::OFF_FQT);
-  bf16* fkn = reinterpret_cast<bf16*>(smem + Cfg::OFF_FKN);
-  bf16* vn = reinterpret_cast<bf16*>(smem + Cfg::OFF_VN);
-  bf16* dyn = reinterpret_cast<bf16*>(smem + Cfg::OFF_DYN);
-  bf16* dyt = reinterpret_cast<bf16*>(smem + Cfg::OFF_DYT);
+  bf16* fq_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_FQ);
+  bf16* fk_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_FK);
+  bf16* v_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_V);
+  bf16* dy_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_DY);
+  bf16* dst_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_DST);
   bf16x8* fa = reinterpret_cast<bf16x8*>(smem + Cfg::OFF_FA);
   bf16x8* fd = reinterpret_cast<bf16x8*>(smem + Cfg::OFF_FD);
   float* pk = reinterpret_cast<float*>(smem + Cfg::OFF_PK);
   float* dens = reinterpret_cast<float*>(smem + Cfg::OFF_DEN);
   float* dels = reinterpret_cast<float*>(smem + Cfg::OFF_DEL);
   float* ps = reinterpret_cast<float*>(smem + Cfg::OFF_P);
-  float* qhs = reinterpret_cast<float*>(smem + Cfg::OFF_QH);
+  float* qh = reinterpret_cast<float*>(smem + Cfg::OFF_QH);
   float* lgs = reinterpret_cast<float*>(smem + Cfg::OFF_LG);
   float* qs = reinterpret_cast<float*>(smem + Cfg::OFF_QS);
-  float* kss = reinterpret_cast<float*>(smem + Cfg::OFF_KS);
-  float* ksn = reinterpret_cast<float*>(smem + Cfg::OFF_KSN);
+  float* ks = reinterpret_cast<float*>(smem + Cfg::OFF_KS);
   float* dzs = reinterpret_cast<float*>(smem + Cfg::OFF_DZ);
+  float* dzp = reinterpret_cast<float*>(smem + Cfg::OFF_DZP);
   float* rdec = reinterpret_cast<float*>(smem + Cfg::OFF_R);
 
-  const int bh = blockIdx.x;
+  const int bh = blockIdx.x / G, seg = blockIdx.x % G;
+  const int NT = (L + C - 1) / C;
+  const int n0 = seg * cps, n1 = min(NT, n0 + cps);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int col = lane & 31, h = lane >> 5;
+  const bool vecF = (F & 7) == 0, vecD = (D & 7) == 0;
   const size_t offF = (size_t)bh * L * F, offD = (size_t)bh * L * D, offL = (size_t)bh * L;
   const float* lgb = log_gamma + (size_t)(gate_per_head ? bh : bh / H) * L;
+  const float* st = G > 1 ? seg_state + ((size_t)bh * G + seg) * Cfg::SEG : nullptr;
 
-  for (int f = tid; f < 2 * FP; f += 256) dzs[f] = 0.f;
+  // dS tiles (rows f, columns d) of the owned d-tiles
+  f32x16 dS[RD::TILES][NFT];
+#pragma unroll
+  for (int i = 0; i < RD::TILES; ++i)
+#pragma unroll
+    for (int ft = 0; ft < NFT; ++ft) {
+      dS[i][ft] = zero16();
+      if (st && RD::active(wave)) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          dS[i][ft][r] = st[(ft * 32 + acc_row(r, h)) * DP + RD::tile(wave, i) * 32 + col];
+      }
+    }
+  for (int f = tid; f < FP; f += 256) dzs[f] = st ? st[FP * DP + f] : 0.f;
 
-  // dS[f-tile][owned d-tile] (rows f, cols d); dS^T[d-tile][owned f-tile] (rows d, cols f)
-  f32x16 dS[NFT][OD::TILES];
-  f32x16 dSt[NDT][OF::TILES];
+  // publish dS as bf16 dS^T [d][f] (rows d = lane column, 4 consecutive f per store)
+  auto publish = [&]() {
+    if (RD::active(wave) && RD::primary(wave)) {
 #pragma unroll
-  for (int ft = 0; ft < NFT; ++ft)
+      for (int i = 0; i < RD::TILES; ++i) {
+        const int d = RD::tile(wave, i) * 32 + col;
 #pragma unroll
-    for (int i = 0; i < OD::TILES; ++i) dS[ft][i] = zero16();
+        for (int ft = 0; ft < NFT; ++ft)
 #pragma unroll
-  for (int dt = 0; dt < NDT; ++dt)
+          for (int g4 = 0; g4 < 4; ++g4) {
+            bf16x4 o;
 #pragma unroll
-    for (int i = 0; i < OF::TILES; ++i) dSt[dt][i] = zero16();
+            for (int e = 0; e < 4; ++e) o[e] = to_bf16(dS[i][ft][4 * g4 + e]);
+            *reinterpret_cast<bf16x4*>(dst_l + d * PF + ft * 32 + 8 * g4 + 4 * h) = o;
+          }
+      }
+    }
+  };
+
+  uint4 rq[Cfg::NLF], rk[Cfg::NLF], rv[Cfg::NLD], rd[Cfg::NLD];
+  TokScalars sc;
+  {
+    const int t0 = (n1 - 1) * C;
+    load_chunk<FP>(rq, fq + offF, t0, L, F, vecF);
+    load_chunk<FP>(rk, fk + offF, t0, L, F, vecF);
+    load_chunk<DP>(rv, v + offD, t0, L, D, vecD);
+    load_chunk<DP>(rd, dy + offD, t0, L, D, vecD);
+    sc = load_scalars(lgb, den_in, delta_in, p_in, offL, t0 + lane, L);
+    store_chunk<FP>(rq, fq_l, PF);
+    store_chunk<FP>(rk, fk_l, PF);
+    store_chunk<DP>(rv, v_l, PD);
+    store_chunk<DP>(rd, dy_l, PD);
+    const int b = (n1 - 1) & 1;
+    if (wave == 0)
+      bwd_scalars(sc.g, sc.den, sc.delta, sc.p, lane, lgs, qs, ks, rdec, dens + 64 * b,
+                  dels + 64 * b, ps + 64 * b, qh + 64 * b);
+    publish();
+  }
+  __syncthreads();
 
   const int qt = wave >> 1, kt = wave & 1;   // this wave's tile of the score block
-  const int ki = kt * 32 + col;               // chunk-local key of this lane (P1)
-  const int NT = (L + GC - 1) / GC;
-  int cur = 0;                                 // dz buffer holding dz_n
-  for (int n = NT - 1; n >= 0; --n) {
-    const int t0 = n * GC;
-    __syncthreads();
-    stage_chunk<FP>(fq + offF, t0, L, F, fqn, NPF, fqt, TP);
-    stage_chunk<FP>(fk + offF, t0, L, F, fkn, NPF, nullptr, 0);
-    stage_chunk<DP>(v + offD, t0, L, D, vn, NPD, nullptr, 0);
-    stage_chunk<DP>(dy + offD, t0, L, D, dyn, NPD, dyt, TP);
-    if (wave == 0) scan_gate(lgb, t0, L, lane, lgs, qs, kss, rdec);
-    if (wave == 1) {
-      const bool ok = t0 + lane < L;
-      const float den = ok ? fmaxf(den_in[offL + t0 + lane], TINY) : 1.f;
-      dens[lane] = den;
-      dels[lane] = ok ? delta_in[offL + t0 + lane] : 0.f;
-      ps[lane] = ok ? p_in[offL + t0 + lane] : 0.f;
+  const int ki = kt * 32 + col;               // chunk-local key of this lane (phase 1)
+  for (int n = n1 - 1; n >= n0; --n) {
+    const int t0 = n * C;
+    const bool more = n - 1 >= n0;
+    const int cur = n & 1;
+    const float* densc = dens + 64 * cur;
+    const float* delsc = dels + 64 * cur;
+    const float* qhc = qh + 64 * cur;
+    if (more) {
+      load_chunk<FP>(rq, fq + offF, t0 - C, L, F, vecF);
+      load_chunk<FP>(rk, fk + offF, t0 - C, L, F, vecF);
+      load_chunk<DP>(rv, v + offD, t0 - C, L, D, vecD);
+      load_chunk<DP>(rd, dy + offD, t0 - C, L, D, vecD);
+      sc = load_scalars(lgb, den_in, delta_in, p_in, offL, t0 - C + lane, L);
     }
-    __syncthreads();
-    if (tid < 64) {
-      qhs[pidx(tid)] = qs[tid] / dens[tid];
-      ksn[tid] = kss[pidx(tid)];
-    }
-
-    // ---- P1: s and (dy v^T) tile (queries x keys); a/den and dad fragments ----
+    // ---- phase 1: s and (dy v^T) tile (queries x keys) -> a/den, dad; dz sums ----
     {
       f32x16 s = zero16(), dyv = zero16();
 #pragma unroll
-      for (int kb = 0; kb < FP / 16; ++kb) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(fqn + (qt * 32 + col) * NPF + 16 * kb + 8 * h);
-        const bf16x8 b = *reinterpret_cast<const bf16x8*>(fkn + ki * NPF + 16 * kb + 8 * h);
-        s = mfma(a, b, s);
-      }
+      for (int kb = 0; kb < FP / 16; ++kb)
+        s = mfma(row_operand(fq_l, PF, qt * 32 + col, 16 * kb, h),
+                 row_operand(fk_l, PF, ki, 16 * kb, h), s);
 #pragma unroll
-      for (int kb = 0; kb < DP / 16; ++kb) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(dyn + (qt * 32 + col) * NPD + 16 * kb + 8 * h);
-        const bf16x8 b = *reinterpret_cast<const bf16x8*>(vn + ki * NPD + 16 * kb + 8 * h);
-        dyv = mfma(a, b, dyv);
-      }
+      for (int kb = 0; kb < DP / 16; ++kb)
+        dyv = mfma(row_operand(dy_l, PD, qt * 32 + col, 16 * kb, h),
+                   row_operand(v_l, PD, ki, 16 * kb, h), dyv);
       const float lgk = lgs[ki];
       bf16x8 fa8[2], fd8[2];
 #pragma unroll
@@ -465,230 +674,280 @@ __global__ __launch_bounds__(256) void gla_bwd_b_kernel(
         const int q = qt * 32 + acc_row(r, h);
         const bool c = ki <= q;
         const float dec = c ? fexp(lgs[q] - lgk) : 0.f;
-        const float den = dens[q];
+        const float den = densc[q];
         const float a = to_f32(to_bf16(s[r] * dec));
         fa8[r >> 3][r & 7] = to_bf16(a / den);
-        fd8[r >> 3][r & 7] = to_bf16(c ? (dyv[r] - dels[q]) / den * dec : 0.f);
+        fd8[r >> 3][r & 7] = to_bf16(c ? (dyv[r] - delsc[q]) / den * dec : 0.f);
       }
       fa[(kt * 4 + qt * 2 + 0) * 64 + lane] = fa8[0];
       fa[(kt * 4 + qt * 2 + 1) * 64 + lane] = fa8[1];
       fd[(kt * 4 + qt * 2 + 0) * 64 + lane] = fd8[0];
       fd[(kt * 4 + qt * 2 + 1) * 64 + lane] = fd8[1];
+      constexpr int TPP = C / Cfg::ZPARTS;
+      const int f = tid % FP, part = tid / FP;
+      if (part < Cfg::ZPARTS) {
+        float za = 0.f;
+#pragma unroll 8
+        for (int t = part * TPP; t < (part + 1) * TPP; ++t)
+          za += to_f32(to_bf16(to_f32(fq_l[t * PF + f]) * qhc[t])) * delsc[t];
+        dzp[part * FP + f] = za;
+      }
     }
     __syncthreads();
-
-    // ---- P2: dv (owned d-tiles), dfk (owned f-tiles), state updates ----------
     const float r_n = rdec[0];
-    const float* dz = dzs + cur * FP;
-    if (OD::active(wave)) {
+    // ---- phase 2: dv for owned (d-tile, key half); dS update --------------------
+    if (RD::active(wave)) {
 #pragma unroll
-      for (int i = 0; i < OD::TILES; ++i) {
-        const int dt = OD::tile(wave, i);
+      for (int i = 0; i < RD::TILES; ++i) {
+        const int dt = RD::tile(wave, i);
+        bf16x8 dyo[4];   // dY^T rows of this d-tile (A of dY^T (a/den)) == dY columns (B of Q^^T dY)
 #pragma unroll
-        for (int j = 0; j < OD::HALVES; ++j) {
-          const int hk = OD::half(wave, j);
-          const int key = hk * 32 + col;
-          const float ksv = ksn[key];
+        for (int qb = 0; qb < 4; ++qb) dyo[qb] = tr_operand(dy_l, PD, 16 * qb, dt * 32, lane);
+#pragma unroll
+        for (int j = 0; j < RD::HALVES; ++j) {
+          const int key = RD::half(wave, j) * 32 + col;
+          const float ksv = ks[key];
           f32x16 g = zero16();
 #pragma unroll
-          for (int qb = 0; qb < 4; ++qb) {
-            const bf16x8 a = *reinterpret_cast<const bf16x8*>(dyt + (dt * 32 + col) * TP + 16 * qb + 8 * h);
-            g = mfma(a, fa[(hk * 4 + qb) * 64 + lane], g);
-          }
+          for (int qb = 0; qb < 4; ++qb)
+            g = mfma(dyo[qb], fa[(RD::half(wave, j) * 4 + qb) * 64 + lane], g);
 #pragma unroll
-          for (int kb = 0; kb < FP / 16; ++kb) {
-            const bf16x8 raw = *reinterpret_cast<const bf16x8*>(fkn + key * NPF + 16 * kb + 8 * h);
-            bf16x8 b;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) b[e] = to_bf16(to_f32(raw[e]) * ksv);
-            g = mfma(acc_operand(dS[kb >> 1][i], kb & 1), b, g);
-          }
+          for (int kb = 0; kb < FP / 16; ++kb)
+            g = mfma(acc_operand(dS[i][kb >> 1], kb & 1),
+                     scale8(row_operand_acc(fk_l, PF, key, 16 * kb, h), ksv), g);
           const int tok = t0 + key;
           if (tok < L) {
 #pragma unroll
-            for (int gg = 0; gg < 4; ++gg)
-              store4<OutT>(dv + offD, tok, dt * 32 + 8 * gg + 4 * h, D, g[4 * gg],
-                           g[4 * gg + 1], g[4 * gg + 2], g[4 * gg + 3]);
+            for (int g4 = 0; g4 < 4; ++g4)
+              store4<OutT>(dv + offD, tok, dt * 32 + 8 * g4 + 4 * h, D, g[4 * g4],
+                           g[4 * g4 + 1], g[4 * g4 + 2], g[4 * g4 + 3]);
+          }
+        }
+#pragma unroll
+        for (int ft = 0; ft < NFT; ++ft) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) dS[i][ft][r] *= r_n;
+#pragma unroll
+          for (int qb = 0; qb < 4; ++qb) {
+            const f32x4 qlo = *reinterpret_cast<const f32x4*>(qhc + 16 * qb + 4 * h);
+            const f32x4 qhi = *reinterpret_cast<const f32x4*>(qhc + 16 * qb + 8 + 4 * h);
+            dS[i][ft] = mfma(scale8v(tr_operand(fq_l, PF, 16 * qb, ft * 32, lane), qlo, qhi),
+                             dyo[qb], dS[i][ft]);
           }
         }
       }
     }
-    if (OF::active(wave)) {
+    // ---- phase 2': dfk for owned (f-tile, key half), from the published dS^T ----
+    if (RF::active(wave)) {
 #pragma unroll
-      for (int i = 0; i < OF::TILES; ++i) {
-        const int ft = OF::tile(wave, i);
+      for (int i = 0; i < RF::TILES; ++i) {
+        const int ft = RF::tile(wave, i);
 #pragma unroll
-        for (int j = 0; j < OF::HALVES; ++j) {
-          const int hk = OF::half(wave, j);
+        for (int j = 0; j < RF::HALVES; ++j) {
+          const int hk = RF::half(wave, j);
           const int key = hk * 32 + col;
-          f32x16 x = zero16();
+          f32x16 x = zero16(), g = zero16();
 #pragma unroll
-          for (int kb = 0; kb < DP / 16; ++kb) {
-            const bf16x8 b = *reinterpret_cast<const bf16x8*>(vn + key * NPD + 16 * kb + 8 * h);
-            x = mfma(acc_operand(dSt[kb >> 1][i], kb & 1), b, x);
-          }
-          f32x16 g = zero16();
+          for (int kb = 0; kb < DP / 16; ++kb)
+            x = mfma(tr_operand(dst_l, PF, 16 * kb, ft * 32, lane),
+                     row_operand_acc(v_l, PD, key, 16 * kb, h), x);
 #pragma unroll
-          for (int qb = 0; qb < 4; ++qb) {
-            const bf16x8 a = *reinterpret_cast<const bf16x8*>(fqt + (ft * 32 + col) * TP + 16 * qb + 8 * h);
-            g = mfma(a, fd[(hk * 4 + qb) * 64 + lane], g);
-          }
-          const float ksv = ksn[key];
+          for (int qb = 0; qb < 4; ++qb)
+            g = mfma(tr_operand(fq_l, PF, 16 * qb, ft * 32, lane), fd[(hk * 4 + qb) * 64 + lane], g);
+          const float ksv = ks[key];
           const int tok = t0 + key;
           float pks = 0.f;
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int f = ft * 32 + acc_row(r, h);
-            g[r] += ksv * (x[r] - dz[f]);
-            pks += to_f32(fkn[key * NPF + pidx(f)]) * g[r];
+          for (int g4 = 0; g4 < 4; ++g4) {
+            const bf16x4 k4 = *reinterpret_cast<const bf16x4*>(fk_l + key * PF + ft * 32 + 8 * g4 + 4 * h);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int r = 4 * g4 + e, f = ft * 32 + 8 * g4 + 4 * h + e;
+              g[r] += ksv * (x[r] - dzs[f]);
+              pks += to_f32(k4[e]) * g[r];
+            }
           }
           pks += xhalf(pks);
           if (h == 0) pk[ft * 64 + key] = pks;
           if (tok < L) {
 #pragma unroll
-            for (int gg = 0; gg < 4; ++gg)
-              store4<OutT>(dfk + offF, tok, ft * 32 + 8 * gg + 4 * h, F, g[4 * gg],
-                           g[4 * gg + 1], g[4 * gg + 2], g[4 * gg + 3]);
+            for (int g4 = 0; g4 < 4; ++g4)
+              store4<OutT>(dfk + offF, tok, ft * 32 + 8 * g4 + 4 * h, F, g[4 * g4],
+                           g[4 * g4 + 1], g[4 * g4 + 2], g[4 * g4 + 3]);
           }
         }
       }
-    }
-    // dS <- r dS + Q^^T dY ; dS^T <- r dS^T + dY^T Q^   (after this chunk used them)
-    if (OD::active(wave)) {
-#pragma unroll
-      for (int i = 0; i < OD::TILES; ++i) {
-        const int dt = OD::tile(wave, i);
-#pragma unroll
-        for (int ft = 0; ft < NFT; ++ft) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) dS[ft][i][r] *= r_n;
-#pragma unroll
-          for (int qb = 0; qb < 4; ++qb) {
-            const bf16x8 raw = *reinterpret_cast<const bf16x8*>(fqt + (ft * 32 + col) * TP + 16 * qb + 8 * h);
-            bf16x8 a;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) a[e] = to_bf16(to_f32(raw[e]) * qhs[16 * qb + 8 * h + e]);
-            const bf16x8 b = *reinterpret_cast<const bf16x8*>(dyt + (dt * 32 + col) * TP + 16 * qb + 8 * h);
-            dS[ft][i] = mfma(a, b, dS[ft][i]);
-          }
-        }
-      }
-    }
-    if (OF::active(wave)) {
-#pragma unroll
-      for (int i = 0; i < OF::TILES; ++i) {
-        const int ft = OF::tile(wave, i);
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) dSt[dt][i][r] *= r_n;
-#pragma unroll
-          for (int qb = 0; qb < 4; ++qb) {
-            const bf16x8 a = *reinterpret_cast<const bf16x8*>(dyt + (dt * 32 + col) * TP + 16 * qb + 8 * h);
-            const bf16x8 raw = *reinterpret_cast<const bf16x8*>(fqt + (ft * 32 + col) * TP + 16 * qb + 8 * h);
-            bf16x8 b;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) b[e] = to_bf16(to_f32(raw[e]) * qhs[16 * qb + 8 * h + e]);
-            dSt[dt][i] = mfma(a, b, dSt[dt][i]);
-          }
-        }
-      }
-    }
-    // dz_{n-1} = r dz_n + sum_i Q^_i delta_i  into the other buffer
-    for (int f = tid; f < FP; f += 256) {
-      float acc = 0.f;
-      for (int t = 0; t < GC; ++t)
-        acc += to_f32(to_bf16(to_f32(fqt[f * TP + t]) * qhs[t])) * dels[pidx(t)];
-      dzs[(cur ^ 1) * FP + f] = dz[f] * r_n + acc;
     }
     __syncthreads();
+    // ---- dG of this chunk; publish dS; previous chunk into LDS; dz update -------
     if (tid < 64 && t0 + tid < L) {
       float s = 0.f;
+#pragma unroll
       for (int ft = 0; ft < NFT; ++ft) s += pk[ft * 64 + tid];
-      dG[offL + t0 + tid] = ps[tid] - s;
+      dG[offL + t0 + tid] = ps[64 * cur + tid] - s;
     }
-    cur ^= 1;
+    publish();
+    if (more) {
+      store_chunk<FP>(rq, fq_l, PF);
+      store_chunk<FP>(rk, fk_l, PF);
+      store_chunk<DP>(rv, v_l, PD);
+      store_chunk<DP>(rd, dy_l, PD);
+      const int b = cur ^ 1;
+      if (wave == 0)
+        bwd_scalars(sc.g, sc.den, sc.delta, sc.p, lane, lgs, qs, ks, rdec, dens + 64 * b,
+                    dels + 64 * b, ps + 64 * b, qh + 64 * b);
+    }
+    if (tid < FP) {
+      float za = dzs[tid] * r_n;
+#pragma unroll
+      for (int p = 0; p < Cfg::ZPARTS; ++p) za += dzp[p * FP + tid];
+      dzs[tid] = za;
+    }
+    __syncthreads();
   }
 }
 
-// ----------------------------------------------------------------------------
-// kernel G: d log_gamma[row, j] = sum_{j' >= j} value[row, j'], where value is
-// dG of that (b, h) row (per-head gate) or its sum over heads (per-token gate).
-// One workgroup per output row; deterministic order.
-// ----------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void gla_gate_grad_kernel(const float* __restrict__ dG,
-                                                            float* __restrict__ dlg, int H, int L,
-                                                            int gate_per_head) {
-  __shared__ float tot[256];
-  const int row = blockIdx.x, tid = threadIdx.x;
+// ============================================================================
+// d log_gamma[row, j] = sum_{j' >= j} value[row, j'], value = dG of that (b, h)
+// row (per-head gate) or its sum over the heads (per-token gate).  Two
+// launches over 256-token blocks, both in a fixed order: block totals, then
+// per block the sum of the later blocks' totals plus an in-block suffix scan.
+// ============================================================================
+constexpr int GG_BLK = 256;
+
+__device__ __forceinline__ float gate_value(const float* __restrict__ src, int nsum, int L, int j) {
+  float s = 0.f;
+  for (int hh = 0; hh < nsum; ++hh) s += src[(size_t)hh * L + j];
+  return s;
+}
+
+// Fixed-order tree sum of sh[0..255] (all 256 threads call it).
+__device__ __forceinline__ float block_sum256(float* sh, float x) {
+  const int tid = threadIdx.x;
+  sh[tid] = x;
+  __syncthreads();
+  for (int off = 128; off > 0; off >>= 1) {
+    if (tid < off) sh[tid] += sh[tid + off];
+    __syncthreads();
+  }
+  const float s = sh[0];
+  __syncthreads();
+  return s;
+}
+
+__global__ __launch_bounds__(256) void gla_gate_total_kernel(const float* __restrict__ dG,
+                                                             float* __restrict__ tot, int H, int L,
+                                                             int gate_per_head) {
+  __shared__ float sh[256];
+  const int row = blockIdx.y, blk = blockIdx.x;
   const int nsum = gate_per_head ? 1 : H;
   const float* src = dG + (size_t)row * nsum * L;
-  const int seg = (L + 255) / 256;
-  const int lo = min(L, tid * seg), hi = min(L, lo + seg);
-  auto value = [&](int j) {
-    float s = 0.f;
-    for (int hh = 0; hh < nsum; ++hh) s += src[(size_t)hh * L + j];
-    return s;
-  };
-  float t = 0.f;
-  for (int j = hi - 1; j >= lo; --j) t += value(j);
-  tot[tid] = t;
-  __syncthreads();
-  if (tid == 0) {
-    float acc = 0.f;
-    for (int i = 255; i >= 0; --i) {
-      const float x = tot[i];
-      tot[i] = acc;   // sum of the segments after i
-      acc += x;
-    }
-  }
-  __syncthreads();
-  float acc = tot[tid];
-  float* dst = dlg + (size_t)row * L;
-  for (int j = hi - 1; j >= lo; --j) {
-    acc += value(j);
-    dst[j] = acc;
-  }
+  const int j = blk * GG_BLK + threadIdx.x;
+  const float s = block_sum256(sh, j < L ? gate_value(src, nsum, L, j) : 0.f);
+  if (threadIdx.x == 0) tot[(size_t)row * gridDim.x + blk] = s;
 }
 
-// ----------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void gla_gate_scan_kernel(const float* __restrict__ dG,
+                                                            const float* __restrict__ tot,
+                                                            float* __restrict__ dlg, int H, int L,
+                                                            int gate_per_head) {
+  __shared__ float sh[256];
+  const int row = blockIdx.y, blk = blockIdx.x, nblk = gridDim.x, tid = threadIdx.x;
+  const int nsum = gate_per_head ? 1 : H;
+  const float* src = dG + (size_t)row * nsum * L;
+  float after = 0.f;
+  for (int b = blk + 1 + tid; b < nblk; b += 256) after += tot[(size_t)row * nblk + b];
+  after = block_sum256(sh, after);
+  const int j = blk * GG_BLK + tid;
+  sh[tid] = j < L ? gate_value(src, nsum, L, j) : 0.f;
+  __syncthreads();
+  for (int off = 1; off < 256; off <<= 1) {   // inclusive suffix scan
+    const float o = tid + off < 256 ? sh[tid + off] : 0.f;
+    __syncthreads();
+    sh[tid] += o;
+    __syncthreads();
+  }
+  if (j < L) dlg[(size_t)row * L + j] = after + sh[tid];
+}
+
+// ============================================================================
 // host launchers
-// ----------------------------------------------------------------------------
-int gla_padded_dim(int n);
+// ============================================================================
+static int gate_rows(int B, int H, int gate_per_head) { return gate_per_head ? B * H : B; }
+
+size_t gla_bwd_workspace(int B, int H, int L, int F, int D, int gate_per_head) {
+  const int BH = B * H;
+  int G, cps;
+  gla_segments(BH, L, &G, &cps);
+  const size_t nblk = (L + GG_BLK - 1) / GG_BLK;
+  return (4 * (size_t)BH * L + 2 * gla_segment_floats(BH, G, F, D) +
+          (size_t)gate_rows(B, H, gate_per_head) * nblk) * sizeof(float);
+}
+
+template <typename K>
+static hipError_t set_lds(K kern, int bytes) {
+  return hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                             hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+}
 
 template <int FP, int DP, typename OutT>
 static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v, const float* lg,
                                    const void* dy, void* dfq, void* dfk, void* dv, float* dlg,
                                    int B, int H, int L, int F, int D, int gate_per_head, float* ws,
                                    hipStream_t st) {
-  const size_t BHL = (size_t)B * H * L;
+  const int BH = B * H;
+  const size_t BHL = (size_t)BH * L;
+  int G, cps;
+  gla_segments(BH, L, &G, &cps);
+  constexpr int SEG = SegRec<FP, DP>::SIZE;
+  constexpr int LDS_A = BwdA<FP, DP>::BYTES, LDS_S = BwdS<FP, DP>::BYTES;
+  constexpr int LDS_B = BwdB<FP, DP>::BYTES;
   float* den = ws;
   float* delta = den + BHL;
   float* p = delta + BHL;
   float* dG = p + BHL;
-  auto ka = gla_bwd_a_kernel<FP, DP, OutT>;
-  auto kb = gla_bwd_b_kernel<FP, DP, OutT>;
-  constexpr int lds_a = BwdACfg<FP, DP>::BYTES, lds_b = BwdBCfg<FP, DP>::BYTES;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(ka),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, lds_a);
-  if (e != hipSuccess) return e;
-  e = hipFuncSetAttribute(reinterpret_cast<const void*>(kb),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, lds_b);
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(ka, dim3(B * H), dim3(256), lds_a, st, (const bf16*)fq,
+  const size_t segf = gla_segment_floats(BH, G, F, D);
+  float* fseg = dG + BHL;
+  float* rseg = fseg + segf;
+  float* gtot = rseg + segf;
+  hipError_t e;
+  if (G > 1) {
+    e = launch_gla_fwd_states(fk, v, lg, fseg, fseg + (size_t)BH * G * SEG, BH, H, L, F, D,
+                              gate_per_head, G, cps, st);
+    if (e != hipSuccess) return e;
+  }
+  auto ka = gla_bwd_dq_kernel<FP, DP, OutT>;
+  if ((e = set_lds(ka, LDS_A)) != hipSuccess) return e;
+  hipLaunchKernelGGL(ka, dim3(BH * G), dim3(256), LDS_A, st, (const bf16*)fq,
                      (const bf16*)fk, (const bf16*)v, lg, (const bf16*)dy, (OutT*)dfq, den, delta,
-                     p, H, L, F, D, gate_per_head);
+                     p, (const float*)fseg, H, L, F, D, gate_per_head, G, cps);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  hipLaunchKernelGGL(kb, dim3(B * H), dim3(256), lds_b, st, (const bf16*)fq,
-                     (const bf16*)fk, (const bf16*)v, lg, (const bf16*)dy, den, delta, p,
-                     (OutT*)dfk, (OutT*)dv, dG, H, L, F, D, gate_per_head);
+  if (G > 1) {
+    auto ks = gla_bwd_state_kernel<FP, DP>;
+    if ((e = set_lds(ks, LDS_S)) != hipSuccess) return e;
+    float* rlam = rseg + (size_t)BH * G * SEG;
+    hipLaunchKernelGGL(ks, dim3(BH * (G - 1)), dim3(256), LDS_S, st,
+                       (const bf16*)fq, (const bf16*)dy, lg, (const float*)den,
+                       (const float*)delta, rseg, rlam, H, L, F, D, gate_per_head, G, cps);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if ((e = launch_gla_segment_scan(rseg, rlam, BH, G, SEG, true, st)) != hipSuccess) return e;
+  }
+  auto kb = gla_bwd_dkv_kernel<FP, DP, OutT>;
+  if ((e = set_lds(kb, LDS_B)) != hipSuccess) return e;
+  hipLaunchKernelGGL(kb, dim3(BH * G), dim3(256), LDS_B, st, (const bf16*)fq,
+                     (const bf16*)fk, (const bf16*)v, lg, (const bf16*)dy, (const float*)den,
+                     (const float*)delta, (const float*)p, (OutT*)dfk, (OutT*)dv, dG,
+                     (const float*)rseg, H, L, F, D, gate_per_head, G, cps);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  hipLaunchKernelGGL(gla_gate_grad_kernel, dim3(gate_per_head ? B * H : B), dim3(256), 0, st, dG,
-                     dlg, H, L, gate_per_head);
+  const int nblk = (L + GG_BLK - 1) / GG_BLK;
+  const dim3 ggrid(nblk, gate_rows(B, H, gate_per_head));
+  hipLaunchKernelGGL(gla_gate_total_kernel, ggrid, dim3(256), 0, st, (const float*)dG, gtot, H, L,
+                     gate_per_head);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL(gla_gate_scan_kernel, ggrid, dim3(256), 0, st, (const float*)dG,
+                     (const float*)gtot, dlg, H, L, gate_per_head);
   return hipGetLastError();
 }
-
-size_t gla_bwd_workspace(int B, int H, int L) { return (size_t)4 * B * H * L * sizeof(float); }
 
 hipError_t launch_gla_bwd(const void* fq, const void* fk, const void* v, const float* lg,
                           const void* dy, void* dfq, void* dfk, void* dv, float* dlg,

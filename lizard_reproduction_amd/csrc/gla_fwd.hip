@@ -38,20 +38,15 @@
 //     (V^T, K~^T, V) come from LDS transpose reads of the row-major tiles.
 //   * the prefetched chunk is written to LDS, the gate scan of the next chunk
 //     runs on wave 0, and z is updated.
-#include "common.hpp"
+#include "gla_common.hpp"
 
 namespace lz {
-
-constexpr int GLA_C = 64;       // chunk length
-constexpr int GLA_TARGET_WG = 512;
 
 template <int FP, int DP>
 struct GlaFwd {
   static constexpr int C = GLA_C;
   static constexpr int PF = FP + 16, PD = DP + 16;   // LDS row pitches (elements)
   static constexpr int NFT = FP / 32, NDT = DP / 32;
-  static constexpr int NDW = NDT >= 4 ? NDT / 4 : 1;  // output d-tiles per wave
-  static constexpr int NQW = NDT >= 4 ? 2 : 1;        // output q-tiles per wave
   static constexpr int ZPARTS = FP >= 256 ? 1 : 256 / FP;
   static constexpr int NLF = C * FP / 8 / 256;        // 16-byte loads per thread, fq or fk
   static constexpr int NLD = C * DP / 8 / 256;        // 16-byte loads per thread, v
@@ -68,56 +63,8 @@ struct GlaFwd {
   static constexpr int OFF_ZP = OFF_Z + FP * 4;           // [ZPARTS][FP] partial sums of K~
   static constexpr int OFF_R = OFF_ZP + ZPARTS * FP * 4;  // e^{lg_end}, lg_end
   static constexpr int BYTES = OFF_R + 16;
-  // per-(b,h,segment) state record in the workspace: S [FP][DP], then z [FP]
-  static constexpr int SEG = FP * DP + FP;
+  static constexpr int SEG = SegRec<FP, DP>::SIZE;
 };
-
-// Rows [t0, t0+64) of a [L x ncols] bf16 matrix into registers, 16 bytes per
-// load: thread slot idx = tid + 256 i covers row idx / (KP/8), columns
-// 8 * (idx % (KP/8)) .. +8.  Zero outside the matrix.
-template <int KP, int N>
-__device__ __forceinline__ void load_chunk(uint4 (&reg)[N], const bf16* __restrict__ base, int t0,
-                                           int L, int ncols, bool vec) {
-  constexpr int K8 = KP / 8;
-#pragma unroll
-  for (int i = 0; i < N; ++i) {
-    const int idx = threadIdx.x + 256 * i;
-    reg[i] = gload8(base, t0 + idx / K8, (idx % K8) * 8, L, ncols, vec);
-  }
-}
-
-template <int KP, int N>
-__device__ __forceinline__ void store_chunk(const uint4 (&reg)[N], bf16* tile, int pitch) {
-  constexpr int K8 = KP / 8;
-#pragma unroll
-  for (int i = 0; i < N; ++i) {
-    const int idx = threadIdx.x + 256 * i;
-    *reinterpret_cast<uint4*>(tile + (idx / K8) * pitch + (idx % K8) * 8) = reg[i];
-  }
-}
-
-// Chunk-local inclusive scan of the gate by one wave (lane = token): lg,
-// e^{lg}, e^{lg_end - lg}, and e^{lg_end}, lg_end in r[0], r[1].
-__device__ __forceinline__ void gate_scan(float g, int lane, float* lgs, float* qs, float* ks,
-                                          float* r) {
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const float o = __shfl_up(g, off);
-    if (lane >= off) g += o;
-  }
-  const float end = __shfl(g, 63);
-  lgs[lane] = g;
-  qs[lane] = fexp(g);
-  ks[lane] = fexp(end - g);
-  if (lane == 0) {
-    r[0] = fexp(end);
-    r[1] = end;
-  }
-}
-
-__device__ __forceinline__ float gate_at(const float* __restrict__ lgb, int t, int L) {
-  return t < L ? lgb[t] : 0.f;
-}
 
 // ----------------------------------------------------------------------------
 // fused forward walk over the chunks of one segment
@@ -130,7 +77,9 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
     int cps) {
   using Cfg = GlaFwd<FP, DP>;
   constexpr int C = Cfg::C, PF = Cfg::PF, PD = Cfg::PD;
-  constexpr int NFT = Cfg::NFT, NDT = Cfg::NDT, NDW = Cfg::NDW, NQW = Cfg::NQW;
+  constexpr int NFT = Cfg::NFT, NDT = Cfg::NDT;
+  using RD = Roles<NDT>;   // wave -> owned d-tiles (state and output) x output q-tiles
+  constexpr int NDW = RD::TILES, NQW = RD::HALVES;
   extern __shared__ __align__(16) char smem[];
   bf16* fq_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_FQ);
   bf16* fk_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_FK);
@@ -158,10 +107,9 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
   const float* lgb = log_gamma + (size_t)(gate_per_head ? bh : bh / H) * L;
   const float* st = G > 1 ? seg_state + ((size_t)bh * G + seg) * Cfg::SEG : nullptr;
 
-  // wave -> owned d-tiles (state and output) and output q-tiles
-  const bool active = NDT >= 2 || wave < 2;
-  auto dtile = [&](int i) { return NDT >= 4 ? wave + 4 * i : (NDT == 2 ? (wave & 1) : 0); };
-  auto qtile = [&](int j) { return NDT >= 4 ? j : (NDT == 2 ? (wave >> 1) : (wave & 1)); };
+  const bool active = RD::active(wave);
+  auto dtile = [&](int i) { return RD::tile(wave, i); };
+  auto qtile = [&](int j) { return RD::half(wave, j); };
 
   f32x16 S[NDW][NFT];
 #pragma unroll
@@ -422,22 +370,42 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_state_kernel(
 }
 
 // ----------------------------------------------------------------------------
-// exclusive scan over segments, in place: record g <- state entering segment g
+// exclusive scan over segments, in place.  Forward (reverse == 0): record g
+// holds the state segment g leaves from zero (g < G-1) and becomes the state
+// entering segment g.  Reverse: record g holds the gradient state segment g
+// leaves (walking backwards) from zero (g > 0) and becomes the gradient state
+// entering segment g from the right.  seg_logdecay[g] is segment g's total
+// log decay.
 // ----------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void gla_segment_scan_kernel(float* __restrict__ seg_state,
                                                                const float* __restrict__ seg_logdecay,
-                                                               int G, int rec) {
+                                                               int G, int rec, int reverse) {
   const int bh = blockIdx.y;
   const int e = blockIdx.x * 256 + threadIdx.x;
   if (e >= rec) return;
+  float* base = seg_state + (size_t)bh * G * rec + e;
+  const float* lam = seg_logdecay + (size_t)bh * G;
   float carry = 0.f;
-  for (int g = 0; g < G - 1; ++g) {
-    const size_t idx = ((size_t)bh * G + g) * rec + e;
-    const float d = seg_state[idx];
-    seg_state[idx] = carry;
-    carry = fexp(seg_logdecay[(size_t)bh * G + g]) * carry + d;
+  // records are read in batches of 8 independent loads, then combined in order
+  for (int b0 = 0; b0 < G - 1; b0 += 8) {
+    float d[8], w[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int g = reverse ? G - 1 - (b0 + k) : b0 + k;
+      const bool ok = b0 + k < G - 1;
+      d[k] = ok ? base[(size_t)g * rec] : 0.f;
+      w[k] = ok ? fexp(lam[g]) : 0.f;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if (b0 + k < G - 1) {
+        const int g = reverse ? G - 1 - (b0 + k) : b0 + k;
+        base[(size_t)g * rec] = carry;
+        carry = w[k] * carry + d[k];
+      }
+    }
   }
-  seg_state[((size_t)bh * G + G - 1) * rec + e] = carry;
+  base[(size_t)(reverse ? 0 : G - 1) * rec] = carry;
 }
 
 // ----------------------------------------------------------------------------
@@ -467,12 +435,56 @@ void gla_segments(int BH, int L, int* G, int* cps) {
   *G = (NT + c - 1) / c;
 }
 
+// workspace floats of one segment-state set: records + log decays
+size_t gla_segment_floats(int BH, int G, int F, int D) {
+  if (G <= 1) return 0;
+  const size_t rec = (size_t)gla_padded_dim(F) * gla_padded_dim(D) + gla_padded_dim(F);
+  return (size_t)BH * G * rec + (size_t)BH * G;
+}
+
 size_t gla_fwd_workspace(int B, int H, int L, int F, int D) {
   int G, cps;
   gla_segments(B * H, L, &G, &cps);
-  if (G <= 1) return 0;
-  const size_t rec = (size_t)gla_padded_dim(F) * gla_padded_dim(D) + gla_padded_dim(F);
-  return ((size_t)B * H * G * rec + (size_t)B * H * G) * sizeof(float);
+  return gla_segment_floats(B * H, G, F, D) * sizeof(float);
+}
+
+hipError_t launch_gla_segment_scan(float* seg_state, const float* seg_logdecay, int BH, int G,
+                                   int rec, bool reverse, hipStream_t st) {
+  hipLaunchKernelGGL(gla_segment_scan_kernel, dim3((rec + 255) / 256, BH), dim3(256), 0, st,
+                     seg_state, seg_logdecay, G, rec, reverse ? 1 : 0);
+  return hipGetLastError();
+}
+
+template <int FP, int DP>
+static hipError_t launch_gla_fwd_states_t(const void* fk, const void* v, const float* lg,
+                                          float* seg_state, float* seg_logdecay, int BH, int H,
+                                          int L, int F, int D, int gate_per_head, int G, int cps,
+                                          hipStream_t st) {
+  using Cfg = GlaFwd<FP, DP>;
+  auto ks = gla_fwd_state_kernel<FP, DP>;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(ks),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::BYTES);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(ks, dim3(BH * (G - 1)), dim3(256), Cfg::BYTES, st, (const bf16*)fk,
+                     (const bf16*)v, lg, seg_state, seg_logdecay, H, L, F, D, gate_per_head, G, cps);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  return launch_gla_segment_scan(seg_state, seg_logdecay, BH, G, Cfg::SEG, false, st);
+}
+
+hipError_t launch_gla_fwd_states(const void* fk, const void* v, const float* lg, float* seg_state,
+                                 float* seg_logdecay, int BH, int H, int L, int F, int D,
+                                 int gate_per_head, int G, int cps, hipStream_t st) {
+  const int fp = gla_padded_dim(F), dp = gla_padded_dim(D);
+#define LZ_GLA_ST(FPV, DPV)                                                                   \
+  if (fp == FPV && dp == DPV)                                                                 \
+    return launch_gla_fwd_states_t<FPV, DPV>(fk, v, lg, seg_state, seg_logdecay, BH, H, L, F, \
+                                             D, gate_per_head, G, cps, st);
+  LZ_GLA_ST(32, 32) LZ_GLA_ST(32, 64) LZ_GLA_ST(32, 128)
+  LZ_GLA_ST(64, 32) LZ_GLA_ST(64, 64) LZ_GLA_ST(64, 128)
+  LZ_GLA_ST(128, 32) LZ_GLA_ST(128, 64) LZ_GLA_ST(128, 128)
+  LZ_GLA_ST(256, 32) LZ_GLA_ST(256, 64)
+#undef LZ_GLA_ST
+  return hipErrorInvalidValue;
 }
 
 template <int FP, int DP>
@@ -485,18 +497,10 @@ static hipError_t launch_gla_fwd_t(const void* fq, const void* fk, const void* v
   gla_segments(BH, L, &G, &cps);
   float* seg_state = ws;
   if (G > 1) {
-    float* seg_logdecay = ws + (size_t)BH * G * Cfg::SEG;
-    auto ks = gla_fwd_state_kernel<FP, DP>;
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(ks),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::BYTES);
+    hipError_t e = launch_gla_fwd_states_t<FP, DP>(fk, v, lg, seg_state,
+                                                   ws + (size_t)BH * G * Cfg::SEG, BH, H, L, F,
+                                                   D, gate_per_head, G, cps, st);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(ks, dim3(BH * (G - 1)), dim3(256), Cfg::BYTES, st, (const bf16*)fk,
-                       (const bf16*)v, lg, seg_state, seg_logdecay, H, L, F, D, gate_per_head, G,
-                       cps);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(gla_segment_scan_kernel, dim3((Cfg::SEG + 255) / 256, BH), dim3(256), 0,
-                       st, seg_state, (const float*)seg_logdecay, G, Cfg::SEG);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   auto kern = gla_fwd_kernel<FP, DP>;
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),

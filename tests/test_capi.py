@@ -62,12 +62,49 @@ def test_bad_sizes_are_rejected_before_any_launch(lib):
     rc = lib.lz_swa_fwd(p, p, p, p, 0, p, p, p, 1, 1, 8, 16, 0, 0.25, None)
     assert rc != 0 and b"window" in lib.lz_last_error()
     ws = lib.lz_gla_bwd_workspace_bytes(2, 3, 100, 24, 20, 0, 64)
+    assert ws > 0
     rc = lib.lz_gla_bwd(p, p, p, p, p, p, p, p, p, 0, 2, 3, 100, 24, 20, 0, 64, p, ws - 1, None)
     assert rc != 0 and b"workspace" in lib.lz_last_error()
 
 
-def test_workspace_sizes(lib):
-    assert lib.lz_gla_bwd_workspace_bytes(2, 3, 100, 24, 20, 0, 64) == 4 * 2 * 3 * 100 * 4
+def segments(bh, length, target=512, chunk=64):
+    """The library's split of each (b, h) sequence into segments (so that
+    B*H*segments fills the GPU): returns (segments, chunks per segment)."""
+    nt = -(-length // chunk)
+    g = min(max(-(-target // bh), 1), nt)
+    cps = -(-nt // g)
+    return -(-nt // cps), cps
+
+
+def padded(n):
+    return next(p for p in (32, 64, 128, 256) if n <= p)
+
+
+def seg_floats(bh, g, f, d):
+    return 0 if g <= 1 else bh * g * (padded(f) * padded(d) + padded(f)) + bh * g
+
+
+@pytest.mark.parametrize("b, h, length, f, d, per_head", [
+    (2, 3, 100, 24, 20, 0), (1, 32, 2048, 64, 64, 0), (16, 32, 2048, 128, 128, 1),
+    (4, 16, 1553, 64, 64, 1), (1, 4, 1, 256, 64, 0)])
+def test_workspace_sizes(lib, b, h, length, f, d, per_head):
+    bh = b * h
+    g, _ = segments(bh, length)
+    assert lib.lz_gla_fwd_workspace_bytes(b, h, length, f, d, per_head, 64) == \
+        4 * seg_floats(bh, g, f, d)
+    rows = bh if per_head else b
+    assert lib.lz_gla_bwd_workspace_bytes(b, h, length, f, d, per_head, 64) == \
+        4 * (4 * bh * length + 2 * seg_floats(bh, g, f, d) + rows * -(-length // 256))
+
+
+def test_segment_split():
+    assert segments(512, 2048) == (1, 32)       # B*H fills the GPU: one walk per (b, h)
+    assert segments(32, 2048) == (16, 2)        # training shape: 16 segments of 2 chunks
+    assert segments(64, 1553) == (7, 4)         # ragged: the last segment is shorter
+    assert segments(6, 1) == (1, 1)
+
+
+def test_swa_workspace_sizes(lib):
     assert lib.lz_swa_bwd_workspace_bytes(1, 32, 2048, 64, 4) == 32 * 16 * 4 * 4
     assert lib.lz_swa_bwd_workspace_bytes(1, 32, 2048, 64, 0) == 0
 
