@@ -77,6 +77,17 @@ def swa_flops(bh, length, d, window, backward):
     return (14 if backward else 4) * d * swa_weff(length, window) * bh * length
 
 
+def measured_traffic():
+    """HBM bytes per launch of the headline kernel from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE runs (scaled by a plain copy of known size), or None."""
+    path = os.path.join(ROOT, "profiles", "gla_fwd_headline_traffic.json")
+    try:
+        with open(path) as f:
+            return int(json.load(f)["traffic_bytes"])
+    except (OSError, ValueError, KeyError):
+        return None
+
+
 def parse_args():
     p = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     p.add_argument("--gpus", type=int, default=1)
@@ -86,6 +97,11 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="target CPU time of the cpu_baseline sample")
+    p.add_argument("--headline-only", action="store_true",
+                   help="time only the headline step (for profiler runs)")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="also run a plain 1 GiB device copy, the reference kernel that "
+                        "scales rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes")
     return p.parse_args()
 
 
@@ -236,6 +252,19 @@ def main():
         "attainable_tflops": round(attainable, 1),
         "attainable_frac": round(tflops / attainable, 4),
         "flops": flops, "bytes": nbytes}}
+    if args.copy_calibration:
+        src = torch.empty(1 << 29, dtype=torch.bfloat16, device="cuda").fill_(1.0)
+        dst = torch.empty_like(src)
+        t = median_ms(torch, lambda: dst.copy_(src), 10, 2)
+        extra["copy_calibration"] = {"bytes_read": src.numel() * 2, "bytes_written": dst.numel() * 2,
+                                     "ms": round(t, 4), "gbs": round(2 * src.numel() * 2 / t / 1e6, 1)}
+        print(f"[bench] copy calibration: {extra['copy_calibration']}", file=sys.stderr, flush=True)
+        del src, dst
+    if args.headline_only:
+        print(json.dumps({"metric": METRIC, "value": round(ms, 4), "unit": "ms",
+                          "ms_per_step": round(ms, 4), "steps": args.steps, "extra": extra}),
+              flush=True)
+        return
 
     iters = 50
     run, reset = fwd_bwd_fn(torch, kernels.gla, (fq, fk, v, lg), dy)
@@ -316,7 +345,7 @@ def main():
                    "gate": "per-head logsigmoid(N(2,1.5))", "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": None, "kernel": "gla_fwd_kernel<128,128>",
+                     "traffic": measured_traffic(), "kernel": "gla_fwd_kernel<128,128>",
                      "algorithmic_bytes": nbytes},
         "cpu_baseline": cpu,
         "extra": extra,

@@ -29,14 +29,24 @@ hipError_t launch_swa_bwd(const void* q, const void* k, const void* v, const flo
                           int d, int W, float scale, hipStream_t st);
 constexpr int MAX_META = 64;
 
-// Sum of the per-block dmeta partials [rows, n_meta] in a fixed order.
-__global__ void dmeta_reduce_kernel(const float* __restrict__ part, float* __restrict__ dmeta,
-                                    int rows, int n_meta) {
-  const int j = threadIdx.x;
-  if (j >= n_meta) return;
+// Sum of the per-block dmeta partials [rows, n_meta] in a fixed order: thread
+// (group g, sink j) sums rows g, g + groups, ...; thread j then sums the groups.
+__global__ __launch_bounds__(256) void dmeta_reduce_kernel(const float* __restrict__ part,
+                                                           float* __restrict__ dmeta, int rows,
+                                                           int n_meta) {
+  __shared__ float sh[256];
+  const int groups = 256 / n_meta;
+  const int j = threadIdx.x % n_meta, grp = threadIdx.x / n_meta;
   float s = 0.f;
-  for (int r = 0; r < rows; ++r) s += part[(size_t)r * n_meta + j];
-  dmeta[j] = s;
+  if (grp < groups)
+    for (int r = grp; r < rows; r += groups) s += part[(size_t)r * n_meta + j];
+  sh[threadIdx.x] = s;
+  __syncthreads();
+  if ((int)threadIdx.x < n_meta) {
+    float t = 0.f;
+    for (int g = 0; g < groups; ++g) t += sh[g * n_meta + threadIdx.x];
+    dmeta[threadIdx.x] = t;
+  }
 }
 }  // namespace lz
 
@@ -173,7 +183,7 @@ extern "C" int lz_swa_bwd(const void* q, const void* k, const void* v, const flo
                                     (float*)workspace, batch * heads, length, dim, window, scale, st);
   if (e != hipSuccess || n_meta == 0) return hip_status(e, "swa_bwd");
   const int rows = batch * heads * ((length + 127) / 128);
-  hipLaunchKernelGGL(lz::dmeta_reduce_kernel, dim3(1), dim3(64), 0, st, (const float*)workspace,
+  hipLaunchKernelGGL(lz::dmeta_reduce_kernel, dim3(1), dim3(256), 0, st, (const float*)workspace,
                      dmeta, rows, n_meta);
   return hip_status(hipGetLastError(), "swa_bwd dmeta");
 }
