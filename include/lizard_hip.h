@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define LZ_ABI_VERSION 3
+#define LZ_ABI_VERSION 5
 
 /* ABI version of the loaded library (LZ_ABI_VERSION). */
 int lz_abi_version(void);
@@ -72,15 +72,19 @@ size_t lz_gla_bwd_workspace_bytes(int batch, int heads, int length, int nf, int 
  * GLA backward.  Replaces _GLA.backward (src/kernels/gla.py:236-256): delta,
  * _gla_bwd_dh, _gla_bwd_dqkv, the dg reduction, and the autograd steps of
  * the gate path (expand-sum over heads, reverse cumsum, gla.py:260-262).
- *   dy          bf16 [BH, L, nd]      upstream gradient
- *   dfq, dfk    [BH, L, nf], dv [BH, L, nd]: bf16 if grad_bf16 else f32
- *   dlog_gamma  f32, same shape as log_gamma
+ *   dy            bf16 [BH, L, nd]      upstream gradient
+ *   dfq, dfk      [BH, L, nf], dv [BH, L, nd]: bf16 if grad_bf16 else f32
+ *   dlog_gamma    f32, same shape as log_gamma
+ *   fwd_workspace the workspace lz_gla_fwd used for these inputs, if the caller
+ *                 kept it (it then holds the state entering each segment and
+ *                 the backward skips recomputing it); may be NULL
  * The other arguments are those of lz_gla_fwd.
  */
 int lz_gla_bwd(const void* fq, const void* fk, const void* v, const float* log_gamma,
                const void* dy, void* dfq, void* dfk, void* dv, float* dlog_gamma, int grad_bf16,
                int batch, int heads, int length, int nf, int nd, int gate_per_head, int chunk,
-               void* workspace, size_t workspace_bytes, void* stream);
+               const void* fwd_workspace, size_t fwd_workspace_bytes, void* workspace,
+               size_t workspace_bytes, void* stream);
 
 /*
  * SWA forward.  Replaces _SWA.forward / _swa_fwd (src/kernels/swa.py:136-156,
@@ -88,32 +92,31 @@ int lz_gla_bwd(const void* fq, const void* fk, const void* v, const float* log_g
  *   q, k, v     bf16 [BH, L, dim]  (RoPE already applied to q and k)
  *   meta        f32 [n_meta] sink logits (n_meta may be 0; at most 64)
  *   y           bf16 [BH, L, dim] output
- *   y32         f32 [BH, L, dim] the same output before rounding, saved for
- *               lz_swa_bwd's delta = dy . y; may be NULL when no backward follows
- *               (y is bitwise the same either way)
  *   lse         f32 [BH, L] log of each row's softmax denominator (saved for backward)
  *   window      keys i-window < t <= i;  scale  usually 1/sqrt(dim)
  * Supported sizes: dim <= 256.
  */
 int lz_swa_fwd(const void* q, const void* k, const void* v, const float* meta, int n_meta,
-               void* y, float* y32, float* lse, int batch, int heads, int length, int dim,
-               int window, float scale, void* stream);
+               void* y, float* lse, int batch, int heads, int length, int dim, int window,
+               float scale, void* stream);
 
 /* Workspace bytes lz_swa_bwd needs for these sizes. */
 size_t lz_swa_bwd_workspace_bytes(int batch, int heads, int length, int dim, int n_meta);
 
 /*
  * SWA backward.  Replaces _SWA.backward (src/kernels/swa.py:158-179): delta,
- * _swa_bwd_q, _swa_bwd_kv and the dmeta reduction.  delta = dy . y32 (the
- * reference uses the bf16 y, swa.py:164; fp32 y halves the sink-gradient error).
- *   y32, lse    from lz_swa_fwd;  dy  bf16 [BH, L, dim]
+ * _swa_bwd_q, _swa_bwd_kv and the dmeta reduction.  delta_i = dy_i . y_i is
+ * formed in fp32 as sum_t p_it (dy_i . v_t) from the recomputed
+ * probabilities (the reference takes it from the bf16 output, swa.py:164),
+ * so the forward saves only lse.
+ *   lse         from lz_swa_fwd;  dy  bf16 [BH, L, dim]
  *   dq, dk, dv  [BH, L, dim]: bf16 if grad_bf16 else f32
  *   dmeta       f32 [n_meta] (untouched when n_meta == 0)
  */
 int lz_swa_bwd(const void* q, const void* k, const void* v, const float* meta, int n_meta,
-               const float* y32, const float* lse, const void* dy, void* dq, void* dk, void* dv,
-               float* dmeta, int grad_bf16, int batch, int heads, int length, int dim,
-               int window, float scale, void* workspace, size_t workspace_bytes, void* stream);
+               const float* lse, const void* dy, void* dq, void* dk, void* dv, float* dmeta,
+               int grad_bf16, int batch, int heads, int length, int dim, int window,
+               float scale, void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -16,17 +16,18 @@ size_t gla_fwd_workspace(int B, int H, int L, int F, int D);
 hipError_t launch_gla_bwd(const void* fq, const void* fk, const void* v, const float* lg,
                           const void* dy, void* dfq, void* dfk, void* dv, float* dlg,
                           bool grad_bf16, int B, int H, int L, int F, int D, int gate_per_head,
-                          float* ws, hipStream_t st);
+                          const float* fwd_ws, float* ws, hipStream_t st);
 size_t gla_bwd_workspace(int B, int H, int L, int F, int D, int gate_per_head);
 bool gla_dims_supported(int F, int D);
 int swa_padded_dim(int d);
+int swa_row_blocks(int L);
 hipError_t launch_swa_fwd(const void* q, const void* k, const void* v, const float* meta,
-                          int n_meta, void* y, float* y32, float* lse, int BH, int L, int d, int W,
+                          int n_meta, void* y, float* lse, int BH, int L, int d, int W,
                           float scale, hipStream_t st);
 hipError_t launch_swa_bwd(const void* q, const void* k, const void* v, const float* meta,
-                          int n_meta, const float* y32, const float* lse, const void* dy, void* dq,
-                          void* dk, void* dv, bool grad_bf16, float* dmeta_part, int BH, int L,
-                          int d, int W, float scale, hipStream_t st);
+                          int n_meta, const float* lse, const void* dy, void* dq, void* dk,
+                          void* dv, bool grad_bf16, float* delta, float* dmeta_part, int BH,
+                          int L, int d, int W, float scale, hipStream_t st);
 constexpr int MAX_META = 64;
 
 // Sum of the per-block dmeta partials [rows, n_meta] in a fixed order: thread
@@ -122,16 +123,27 @@ extern "C" size_t lz_gla_bwd_workspace_bytes(int batch, int heads, int length, i
 extern "C" int lz_gla_bwd(const void* fq, const void* fk, const void* v, const float* log_gamma,
                           const void* dy, void* dfq, void* dfk, void* dv, float* dlog_gamma,
                           int grad_bf16, int batch, int heads, int length, int nf, int nd,
-                          int gate_per_head, int chunk, void* workspace, size_t workspace_bytes,
+                          int gate_per_head, int chunk, const void* fwd_workspace,
+                          size_t fwd_workspace_bytes, void* workspace, size_t workspace_bytes,
                           void* stream) {
   if (int rc = check_gla(fq, fk, v, log_gamma, batch, heads, length, nf, nd, chunk)) return rc;
   if (!dy || !dfq || !dfk || !dv || !dlog_gamma) return fail(1, "gla_bwd: null pointer");
   const size_t need = lz::gla_bwd_workspace(batch, heads, length, nf, nd, gate_per_head ? 1 : 0);
   if (!workspace || workspace_bytes < need)
     return fail(1, "gla_bwd: workspace of %zu bytes given, %zu needed", workspace_bytes, need);
+  // the forward's workspace, if the caller kept it, already holds the state
+  // entering each segment; otherwise the backward recomputes it
+  const size_t fneed = lz::gla_fwd_workspace(batch, heads, length, nf, nd);
+  const float* fws = nullptr;
+  if (fwd_workspace && fneed) {
+    if (fwd_workspace_bytes < fneed)
+      return fail(1, "gla_bwd: forward workspace of %zu bytes given, %zu needed",
+                  fwd_workspace_bytes, fneed);
+    fws = (const float*)fwd_workspace;
+  }
   return hip_status(lz::launch_gla_bwd(fq, fk, v, log_gamma, dy, dfq, dfk, dv, dlog_gamma,
                                        grad_bf16 != 0, batch, heads, length, nf, nd,
-                                       gate_per_head ? 1 : 0, (float*)workspace,
+                                       gate_per_head ? 1 : 0, fws, (float*)workspace,
                                        (hipStream_t)stream),
                     "gla_bwd");
 }
@@ -150,40 +162,42 @@ static int check_swa(const void* q, const void* k, const void* v, const float* m
 }
 
 extern "C" int lz_swa_fwd(const void* q, const void* k, const void* v, const float* meta,
-                          int n_meta, void* y, float* y32, float* lse, int batch, int heads,
-                          int length, int dim, int window, float scale, void* stream) {
+                          int n_meta, void* y, float* lse, int batch, int heads, int length,
+                          int dim, int window, float scale, void* stream) {
   if (int rc = check_swa(q, k, v, meta, n_meta, batch, heads, length, dim, window)) return rc;
   if (!y || !lse) return fail(1, "swa_fwd: null output pointer");
-  return hip_status(lz::launch_swa_fwd(q, k, v, meta, n_meta, y, y32, lse, batch * heads, length,
-                                       dim, window, scale, (hipStream_t)stream),
+  return hip_status(lz::launch_swa_fwd(q, k, v, meta, n_meta, y, lse, batch * heads, length, dim,
+                                       window, scale, (hipStream_t)stream),
                     "swa_fwd");
 }
 
 extern "C" size_t lz_swa_bwd_workspace_bytes(int batch, int heads, int length, int dim,
                                              int n_meta) {
   (void)dim;
-  if (batch <= 0 || heads <= 0 || length <= 0 || n_meta <= 0) return 0;
-  const size_t nb = (size_t)(length + 127) / 128;
-  return (size_t)batch * heads * nb * n_meta * sizeof(float);
+  if (batch <= 0 || heads <= 0 || length <= 0 || n_meta < 0) return 0;
+  const size_t bh = (size_t)batch * heads;
+  return (bh * length + bh * lz::swa_row_blocks(length) * n_meta) * sizeof(float);
 }
 
 extern "C" int lz_swa_bwd(const void* q, const void* k, const void* v, const float* meta,
-                          int n_meta, const float* y32, const float* lse, const void* dy, void* dq,
-                          void* dk, void* dv, float* dmeta, int grad_bf16, int batch, int heads,
-                          int length, int dim, int window, float scale, void* workspace,
+                          int n_meta, const float* lse, const void* dy, void* dq, void* dk,
+                          void* dv, float* dmeta, int grad_bf16, int batch, int heads, int length,
+                          int dim, int window, float scale, void* workspace,
                           size_t workspace_bytes, void* stream) {
   if (int rc = check_swa(q, k, v, meta, n_meta, batch, heads, length, dim, window)) return rc;
-  if (!y32 || !lse || !dy || !dq || !dk || !dv) return fail(1, "swa_bwd: null pointer");
+  if (!lse || !dy || !dq || !dk || !dv) return fail(1, "swa_bwd: null pointer");
   if (n_meta > 0 && !dmeta) return fail(1, "swa_bwd: null dmeta pointer");
   const size_t need = lz_swa_bwd_workspace_bytes(batch, heads, length, dim, n_meta);
-  if (need && (!workspace || workspace_bytes < need))
+  if (!workspace || workspace_bytes < need)
     return fail(1, "swa_bwd: workspace of %zu bytes given, %zu needed", workspace_bytes, need);
   hipStream_t st = (hipStream_t)stream;
-  hipError_t e = lz::launch_swa_bwd(q, k, v, meta, n_meta, y32, lse, dy, dq, dk, dv, grad_bf16 != 0,
-                                    (float*)workspace, batch * heads, length, dim, window, scale, st);
+  float* delta = (float*)workspace;
+  float* part = delta + (size_t)batch * heads * length;
+  hipError_t e = lz::launch_swa_bwd(q, k, v, meta, n_meta, lse, dy, dq, dk, dv, grad_bf16 != 0,
+                                    delta, part, batch * heads, length, dim, window, scale, st);
   if (e != hipSuccess || n_meta == 0) return hip_status(e, "swa_bwd");
-  const int rows = batch * heads * ((length + 127) / 128);
-  hipLaunchKernelGGL(lz::dmeta_reduce_kernel, dim3(1), dim3(256), 0, st, (const float*)workspace,
+  const int rows = batch * heads * lz::swa_row_blocks(length);
+  hipLaunchKernelGGL(lz::dmeta_reduce_kernel, dim3(1), dim3(256), 0, st, (const float*)part,
                      dmeta, rows, n_meta);
   return hip_status(hipGetLastError(), "swa_bwd dmeta");
 }

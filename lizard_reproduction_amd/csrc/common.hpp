@@ -122,6 +122,17 @@ __device__ __forceinline__ void store4(OutT* __restrict__ p, int row, int c, int
   }
 }
 
+// Raise kernel Kern's dynamic-LDS limit to `bytes`, once per process: the
+// first launch of each kernel instantiation makes the runtime call (a
+// function-local static, initialised thread-safely), later launches reuse its
+// status.  Every instantiation asks for one fixed size, its LDS layout's.
+template <auto Kern>
+hipError_t ensure_lds(int bytes) {
+  static const hipError_t status = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(Kern), hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  return status;
+}
+
 // Exchange with the other half of the wave (lane ^ 32).
 __device__ __forceinline__ float xhalf(float x) { return __shfl_xor(x, 32); }
 

@@ -548,8 +548,8 @@ __global__ __launch_bounds__(256, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_kernel(
     const float* __restrict__ log_gamma, const bf16* __restrict__ dy,
     const float* __restrict__ den_in, const float* __restrict__ delta_in,
     const float* __restrict__ p_in, OutT* __restrict__ dfk, OutT* __restrict__ dv,
-    float* __restrict__ dG, const float* __restrict__ seg_state, int H, int L, int F, int D,
-    int gate_per_head, int G, int cps) {
+    float* __restrict__ dG, float* __restrict__ csum, const float* __restrict__ seg_state, int H,
+    int L, int F, int D, int gate_per_head, int G, int cps) {
   using Cfg = BwdB<FP, DP>;
   constexpr int C = Cfg::C, PF = Cfg::PF, PD = Cfg::PD;
   constexpr int NFT = Cfg::NFT, NDT = Cfg::NDT;
@@ -779,12 +779,19 @@ __global__ __launch_bounds__(256, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_kernel(
       }
     }
     __syncthreads();
-    // ---- dG of this chunk; publish dS; previous chunk into LDS; dz update -------
-    if (tid < 64 && t0 + tid < L) {
-      float s = 0.f;
+    // ---- dG of this chunk and its sum; publish dS; previous chunk; dz update ---
+    if (wave == 0) {
+      float g = 0.f;
+      if (t0 + lane < L) {
+        float s = 0.f;
 #pragma unroll
-      for (int ft = 0; ft < NFT; ++ft) s += pk[ft * 64 + tid];
-      dG[offL + t0 + tid] = ps[64 * cur + tid] - s;
+        for (int ft = 0; ft < NFT; ++ft) s += pk[ft * 64 + lane];
+        g = ps[64 * cur + lane] - s;
+        dG[offL + t0 + lane] = g;
+      }
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) g += __shfl_xor(g, off);
+      if (lane == 0) csum[(size_t)bh * NT + n] = g;
     }
     publish();
     if (more) {
@@ -809,19 +816,14 @@ __global__ __launch_bounds__(256, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_kernel(
 
 // ============================================================================
 // d log_gamma[row, j] = sum_{j' >= j} value[row, j'], value = dG of that (b, h)
-// row (per-head gate) or its sum over the heads (per-token gate).  Two
-// launches over 256-token blocks, both in a fixed order: block totals, then
-// per block the sum of the later blocks' totals plus an in-block suffix scan.
+// row (per-head gate) or its sum over the heads (per-token gate).  One launch
+// over 256-token blocks; a block adds the chunk sums of dG that the reverse
+// walk left for every chunk after it to an in-block suffix scan.  Fixed order
+// throughout.
 // ============================================================================
 constexpr int GG_BLK = 256;
 
-__device__ __forceinline__ float gate_value(const float* __restrict__ src, int nsum, int L, int j) {
-  float s = 0.f;
-  for (int hh = 0; hh < nsum; ++hh) s += src[(size_t)hh * L + j];
-  return s;
-}
-
-// Fixed-order tree sum of sh[0..255] (all 256 threads call it).
+// Fixed-order tree sum of one value per thread (all 256 threads call it).
 __device__ __forceinline__ float block_sum256(float* sh, float x) {
   const int tid = threadIdx.x;
   sh[tid] = x;
@@ -835,31 +837,28 @@ __device__ __forceinline__ float block_sum256(float* sh, float x) {
   return s;
 }
 
-__global__ __launch_bounds__(256) void gla_gate_total_kernel(const float* __restrict__ dG,
-                                                             float* __restrict__ tot, int H, int L,
-                                                             int gate_per_head) {
-  __shared__ float sh[256];
-  const int row = blockIdx.y, blk = blockIdx.x;
-  const int nsum = gate_per_head ? 1 : H;
-  const float* src = dG + (size_t)row * nsum * L;
-  const int j = blk * GG_BLK + threadIdx.x;
-  const float s = block_sum256(sh, j < L ? gate_value(src, nsum, L, j) : 0.f);
-  if (threadIdx.x == 0) tot[(size_t)row * gridDim.x + blk] = s;
-}
-
-__global__ __launch_bounds__(256) void gla_gate_scan_kernel(const float* __restrict__ dG,
-                                                            const float* __restrict__ tot,
+__global__ __launch_bounds__(256) void gla_gate_grad_kernel(const float* __restrict__ dG,
+                                                            const float* __restrict__ csum,
                                                             float* __restrict__ dlg, int H, int L,
                                                             int gate_per_head) {
   __shared__ float sh[256];
-  const int row = blockIdx.y, blk = blockIdx.x, nblk = gridDim.x, tid = threadIdx.x;
+  const int row = blockIdx.y, blk = blockIdx.x, tid = threadIdx.x;
+  const int NT = (L + GLA_C - 1) / GLA_C;
   const int nsum = gate_per_head ? 1 : H;
   const float* src = dG + (size_t)row * nsum * L;
+  const float* cs = csum + (size_t)row * nsum * NT;
+  const int c0 = (blk + 1) * (GG_BLK / GLA_C);   // first chunk after this block
   float after = 0.f;
-  for (int b = blk + 1 + tid; b < nblk; b += 256) after += tot[(size_t)row * nblk + b];
+  if (NT > c0) {
+    const int nc = NT - c0;
+    for (int idx = tid; idx < nc * nsum; idx += 256) after += cs[(size_t)(idx / nc) * NT + c0 + idx % nc];
+  }
   after = block_sum256(sh, after);
   const int j = blk * GG_BLK + tid;
-  sh[tid] = j < L ? gate_value(src, nsum, L, j) : 0.f;
+  float x = 0.f;
+  if (j < L)
+    for (int hh = 0; hh < nsum; ++hh) x += src[(size_t)hh * L + j];
+  sh[tid] = x;
   __syncthreads();
   for (int off = 1; off < 256; off <<= 1) {   // inclusive suffix scan
     const float o = tid + off < 256 ? sh[tid + off] : 0.f;
@@ -875,26 +874,23 @@ __global__ __launch_bounds__(256) void gla_gate_scan_kernel(const float* __restr
 // ============================================================================
 static int gate_rows(int B, int H, int gate_per_head) { return gate_per_head ? B * H : B; }
 
+// den, delta, p, dG [BH][L]; forward and reverse segment records; chunk sums
+// of dG [BH][NT]
 size_t gla_bwd_workspace(int B, int H, int L, int F, int D, int gate_per_head) {
+  (void)gate_per_head;
   const int BH = B * H;
   int G, cps;
   gla_segments(BH, L, &G, &cps);
-  const size_t nblk = (L + GG_BLK - 1) / GG_BLK;
-  return (4 * (size_t)BH * L + 2 * gla_segment_floats(BH, G, F, D) +
-          (size_t)gate_rows(B, H, gate_per_head) * nblk) * sizeof(float);
-}
-
-template <typename K>
-static hipError_t set_lds(K kern, int bytes) {
-  return hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                             hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  const size_t NT = (L + GLA_C - 1) / GLA_C;
+  return (4 * (size_t)BH * L + 2 * gla_segment_floats(BH, G, F, D) + (size_t)BH * NT) *
+         sizeof(float);
 }
 
 template <int FP, int DP, typename OutT>
 static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v, const float* lg,
                                    const void* dy, void* dfq, void* dfk, void* dv, float* dlg,
-                                   int B, int H, int L, int F, int D, int gate_per_head, float* ws,
-                                   hipStream_t st) {
+                                   int B, int H, int L, int F, int D, int gate_per_head,
+                                   const float* fwd_ws, float* ws, hipStream_t st) {
   const int BH = B * H;
   const size_t BHL = (size_t)BH * L;
   int G, cps;
@@ -907,24 +903,25 @@ static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v
   float* p = delta + BHL;
   float* dG = p + BHL;
   const size_t segf = gla_segment_floats(BH, G, F, D);
-  float* fseg = dG + BHL;
-  float* rseg = fseg + segf;
-  float* gtot = rseg + segf;
+  float* own_fseg = dG + BHL;
+  float* rseg = own_fseg + segf;
+  float* csum = rseg + segf;
+  const float* fseg = fwd_ws ? fwd_ws : own_fseg;   // the forward's records, when kept
   hipError_t e;
-  if (G > 1) {
-    e = launch_gla_fwd_states(fk, v, lg, fseg, fseg + (size_t)BH * G * SEG, BH, H, L, F, D,
-                              gate_per_head, G, cps, st);
+  if (G > 1 && !fwd_ws) {
+    e = launch_gla_fwd_states(fk, v, lg, own_fseg, own_fseg + (size_t)BH * G * SEG, BH, H, L, F,
+                              D, gate_per_head, G, cps, st);
     if (e != hipSuccess) return e;
   }
   auto ka = gla_bwd_dq_kernel<FP, DP, OutT>;
-  if ((e = set_lds(ka, LDS_A)) != hipSuccess) return e;
+  if ((e = ensure_lds<gla_bwd_dq_kernel<FP, DP, OutT>>(LDS_A)) != hipSuccess) return e;
   hipLaunchKernelGGL(ka, dim3(BH * G), dim3(256), LDS_A, st, (const bf16*)fq,
                      (const bf16*)fk, (const bf16*)v, lg, (const bf16*)dy, (OutT*)dfq, den, delta,
-                     p, (const float*)fseg, H, L, F, D, gate_per_head, G, cps);
+                     p, fseg, H, L, F, D, gate_per_head, G, cps);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   if (G > 1) {
     auto ks = gla_bwd_state_kernel<FP, DP>;
-    if ((e = set_lds(ks, LDS_S)) != hipSuccess) return e;
+    if ((e = ensure_lds<gla_bwd_state_kernel<FP, DP>>(LDS_S)) != hipSuccess) return e;
     float* rlam = rseg + (size_t)BH * G * SEG;
     hipLaunchKernelGGL(ks, dim3(BH * (G - 1)), dim3(256), LDS_S, st,
                        (const bf16*)fq, (const bf16*)dy, lg, (const float*)den,
@@ -933,33 +930,31 @@ static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v
     if ((e = launch_gla_segment_scan(rseg, rlam, BH, G, SEG, true, st)) != hipSuccess) return e;
   }
   auto kb = gla_bwd_dkv_kernel<FP, DP, OutT>;
-  if ((e = set_lds(kb, LDS_B)) != hipSuccess) return e;
+  if ((e = ensure_lds<gla_bwd_dkv_kernel<FP, DP, OutT>>(LDS_B)) != hipSuccess) return e;
   hipLaunchKernelGGL(kb, dim3(BH * G), dim3(256), LDS_B, st, (const bf16*)fq,
                      (const bf16*)fk, (const bf16*)v, lg, (const bf16*)dy, (const float*)den,
-                     (const float*)delta, (const float*)p, (OutT*)dfk, (OutT*)dv, dG,
+                     (const float*)delta, (const float*)p, (OutT*)dfk, (OutT*)dv, dG, csum,
                      (const float*)rseg, H, L, F, D, gate_per_head, G, cps);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  const int nblk = (L + GG_BLK - 1) / GG_BLK;
-  const dim3 ggrid(nblk, gate_rows(B, H, gate_per_head));
-  hipLaunchKernelGGL(gla_gate_total_kernel, ggrid, dim3(256), 0, st, (const float*)dG, gtot, H, L,
-                     gate_per_head);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
-  hipLaunchKernelGGL(gla_gate_scan_kernel, ggrid, dim3(256), 0, st, (const float*)dG,
-                     (const float*)gtot, dlg, H, L, gate_per_head);
+  const dim3 ggrid((L + GG_BLK - 1) / GG_BLK, gate_rows(B, H, gate_per_head));
+  hipLaunchKernelGGL(gla_gate_grad_kernel, ggrid, dim3(256), 0, st, (const float*)dG,
+                     (const float*)csum, dlg, H, L, gate_per_head);
   return hipGetLastError();
 }
 
 hipError_t launch_gla_bwd(const void* fq, const void* fk, const void* v, const float* lg,
                           const void* dy, void* dfq, void* dfk, void* dv, float* dlg,
                           bool grad_bf16, int B, int H, int L, int F, int D, int gate_per_head,
-                          float* ws, hipStream_t st) {
+                          const float* fwd_ws, float* ws, hipStream_t st) {
   const int fp = gla_padded_dim(F), dp = gla_padded_dim(D);
 #define LZ_GLA_BWD(FPV, DPV)                                                                   \
   if (fp == FPV && dp == DPV)                                                                  \
     return grad_bf16 ? launch_gla_bwd_t<FPV, DPV, bf16>(fq, fk, v, lg, dy, dfq, dfk, dv, dlg,  \
-                                                         B, H, L, F, D, gate_per_head, ws, st) \
+                                                         B, H, L, F, D, gate_per_head, fwd_ws, \
+                                                         ws, st)                               \
                      : launch_gla_bwd_t<FPV, DPV, float>(fq, fk, v, lg, dy, dfq, dfk, dv, dlg, \
-                                                          B, H, L, F, D, gate_per_head, ws, st);
+                                                          B, H, L, F, D, gate_per_head, fwd_ws, \
+                                                          ws, st);
   LZ_GLA_BWD(32, 32) LZ_GLA_BWD(32, 64) LZ_GLA_BWD(32, 128)
   LZ_GLA_BWD(64, 32) LZ_GLA_BWD(64, 64) LZ_GLA_BWD(64, 128)
   LZ_GLA_BWD(128, 32) LZ_GLA_BWD(128, 64) LZ_GLA_BWD(128, 128)

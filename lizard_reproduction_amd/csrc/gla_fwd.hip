@@ -462,8 +462,7 @@ static hipError_t launch_gla_fwd_states_t(const void* fk, const void* v, const f
                                           hipStream_t st) {
   using Cfg = GlaFwd<FP, DP>;
   auto ks = gla_fwd_state_kernel<FP, DP>;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(ks),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::BYTES);
+  hipError_t e = ensure_lds<gla_fwd_state_kernel<FP, DP>>(Cfg::BYTES);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(ks, dim3(BH * (G - 1)), dim3(256), Cfg::BYTES, st, (const bf16*)fk,
                      (const bf16*)v, lg, seg_state, seg_logdecay, H, L, F, D, gate_per_head, G, cps);
@@ -503,8 +502,7 @@ static hipError_t launch_gla_fwd_t(const void* fq, const void* fk, const void* v
     if (e != hipSuccess) return e;
   }
   auto kern = gla_fwd_kernel<FP, DP>;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::BYTES);
+  hipError_t e = ensure_lds<gla_fwd_kernel<FP, DP>>(Cfg::BYTES);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3(BH * G), dim3(256), Cfg::BYTES, st, (const bf16*)fq,
                      (const bf16*)fk, (const bf16*)v, lg, (bf16*)y, (const float*)seg_state, H, L,

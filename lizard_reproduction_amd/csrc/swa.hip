@@ -6,102 +6,113 @@
 //   s_it = q_i . k_t / sqrt(d) for keys i-W < t <= i (t < L)
 //   y_i  = sum_t e^{s_it} v_t / (sum_j e^{meta_j} + sum_t e^{s_it})
 //   lse_i = log(sum_j e^{meta_j} + sum_t e^{s_it})
-// Backward with delta_i = dy_i . y_i (src/kernels/swa.py:164).  The reference
-// takes y from the bf16 output; here the forward also keeps y in fp32 (y32)
-// when a backward will follow, and delta uses it: with bf16 y the sink
-// gradient alone loses ~1 % to the rounding (it is a long signed sum of delta).
-//   p_it = e^{s_it - lse_i},  ds_it = p_it (dy_i . v_t - delta_i)
+// Backward, with p_it = e^{s_it - lse_i}:
+//   delta_i = dy_i . y_i = sum_t p_it (dy_i . v_t)     (the sinks carry no value)
+//   ds_it = p_it (dy_i . v_t - delta_i)
 //   dq_i = scale sum_t ds_it k_t,  dk_t = scale sum_i ds_it q_i,
 //   dv_t = sum_i p_it dy_i,  dmeta_j = -sum_i e^{meta_j - lse_i} delta_i
+// The reference forms delta from the bf16 output (src/kernels/swa.py:164);
+// here it is the fp32 sum above, taken from the same p and dy.v the backward
+// computes anyway, so nothing beyond y and lse is saved by the forward.
 //
-// Layout: q, k, v, y, dy are [BH, L, d] bf16 row-major; y32 is [BH, L, d]
-// fp32; lse is [BH, L] fp32.
-// A workgroup is 4 waves; each wave owns a 32-row tile (queries in the
-// forward and dq role, keys in the dk/dv role) and keeps its own rows in
-// registers as MFMA operands.  The other side of each product is staged per
-// 32-row tile in LDS, both natural ([row][d], for contractions over d) and
-// transposed ([d][row], for contractions over rows).  Scores are computed
-// transposed (keys x queries in the forward) so that each lane owns one query
-// and the softmax statistics are per-lane scalars; P then feeds P*V straight
-// from the accumulator registers (see common.hpp).
+// Layout: q, k, v, y, dy, dq, dk, dv are [BH, L, d] row-major; lse, delta
+// [BH, L] fp32.  A workgroup is 4 waves and covers 128 rows of its own side
+// (queries in the forward and dq kernels, keys in the dk/dv kernel), 32 per
+// wave, held in registers as MFMA operands; the other side streams through
+// LDS in 64-row row-major tiles, the next tile prefetched into registers.
+// Operands that contract over rows of a staged tile (V^T, K^T, Q^T, dY^T)
+// come from LDS transpose reads.  Scores are computed with the staged side as
+// the MFMA A operand, so each lane owns one row of its own side and the
+// softmax statistics are per-lane scalars; P and dS then feed the next product
+// straight from the accumulator registers.  Consecutive workgroups of one
+// (b, h) are mapped to one XCD so that the tiles they share hit one L2.
 #include "common.hpp"
 
 namespace lz {
 
 constexpr int SWA_MAX_META = 64;
+constexpr int SWA_ROWS = 128;   // own-side rows per workgroup
+constexpr int SWA_TILE = 64;    // streamed rows per LDS tile
 
 template <int DP>
-struct SwaTiles {
-  static constexpr int NPITCH = DP + 8;   // natural tile [32][NPITCH]
-  static constexpr int TPITCH = 32 + 8;   // transposed tile [DP][TPITCH]
-  static constexpr int NAT_ELEMS = 32 * NPITCH;
-  static constexpr int TR_ELEMS = DP * TPITCH;
+struct SwaCfg {
+  static constexpr int P = DP + 16;                      // LDS row pitch (elements)
+  static constexpr int NL = SWA_TILE * DP / 8 / 256;     // 16-byte loads per thread per tile
+  static constexpr int TILE_BYTES = SWA_TILE * P * 2;
 };
 
-// Cooperatively stage rows [r0, r0+32) of a [nrows x ncols] matrix into a
-// natural tile (slot order along d) and/or a transposed tile (slot order
-// along rows).  256 threads.
-template <int DP, bool NAT, bool TR>
-__device__ __forceinline__ void stage_rows(const bf16* __restrict__ src, int r0, int nrows,
-                                           int ncols, bf16* nat, bf16* tr) {
-  using T = SwaTiles<DP>;
-  constexpr int C4 = DP / 4;
-  for (int idx = threadIdx.x; idx < 32 * C4; idx += 256) {
-    const int r = idx / C4, c = (idx % C4) * 4;
-    const bf16x4 x = load4(src, r0 + r, c, nrows, ncols);
-    if constexpr (NAT) *reinterpret_cast<bf16x4*>(nat + r * T::NPITCH + pidx(c)) = x;
-    if constexpr (TR) {
+// Logical block id for hardware block id i of a grid of 8 * per blocks: the
+// hardware deals consecutive ids round-robin over the 8 XCDs, this hands each
+// XCD a run of `per` consecutive logical blocks.
+__device__ __forceinline__ int xcd_block(int i, int per) { return (i & 7) * per + (i >> 3); }
+
+// rows [r0, r0+64) of a [L x d] matrix, 16 bytes per load (zero outside it)
+template <int DP>
+__device__ __forceinline__ void swa_load(uint4 (&reg)[SwaCfg<DP>::NL], const bf16* __restrict__ base,
+                                         int r0, int L, int d, bool vec) {
+  constexpr int K8 = DP / 8;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) tr[(c + e) * T::TPITCH + pidx(r)] = x[e];
-    }
+  for (int i = 0; i < SwaCfg<DP>::NL; ++i) {
+    const int idx = threadIdx.x + 256 * i;
+    reg[i] = gload8(base, r0 + idx / K8, (idx % K8) * 8, L, d, vec);
   }
 }
 
-// Operand registers for a 32-row tile held by the wave: lane (row r0+l%32,
-// half h) gets elements k = 16*kb + slot order, zero outside the matrix.
 template <int DP>
-__device__ __forceinline__ void load_rows_operand(const bf16* __restrict__ src, int row,
-                                                  int nrows, int ncols, int h,
-                                                  bf16x8 (&reg)[DP / 16]) {
+__device__ __forceinline__ void swa_store(const uint4 (&reg)[SwaCfg<DP>::NL], bf16* tile) {
+  constexpr int K8 = DP / 8;
 #pragma unroll
-  for (int kb = 0; kb < DP / 16; ++kb) {
-    const bf16x4 lo = load4(src, row, 16 * kb + 4 * h, nrows, ncols);
-    const bf16x4 hi = load4(src, row, 16 * kb + 8 + 4 * h, nrows, ncols);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      reg[kb][e] = lo[e];
-      reg[kb][4 + e] = hi[e];
-    }
+  for (int i = 0; i < SwaCfg<DP>::NL; ++i) {
+    const int idx = threadIdx.x + 256 * i;
+    *reinterpret_cast<uint4*>(tile + (idx / K8) * SwaCfg<DP>::P + (idx % K8) * 8) = reg[i];
   }
+}
+
+// The wave's own 32 rows as MFMA operands with contiguous k slots
+// (columns 16 kb + 8 h .. +8 of row `row`), zero outside the matrix.
+template <int DP>
+__device__ __forceinline__ void own_rows(const bf16* __restrict__ base, int row, int L, int d,
+                                         int h, bool vec, bf16x8 (&reg)[DP / 16]) {
+#pragma unroll
+  for (int kb = 0; kb < DP / 16; ++kb)
+    reg[kb] = __builtin_bit_cast(bf16x8, gload8(base, row, 16 * kb + 8 * h, L, d, vec));
 }
 
 __device__ __forceinline__ bool in_window(int i, int t, int L, int W) {
   return t <= i && i - t < W && t < L && i < L;
 }
 
+// Does key block [k0, k0+32) meet the windows of queries [q0, q0+32)?
+__device__ __forceinline__ bool blocks_meet(int q0, int k0, int L, int W) {
+  return q0 < L && k0 < L && k0 <= q0 + 31 && k0 + 31 >= q0 - W + 1;
+}
+
 // ----------------------------------------------------------------------------
-// forward: grid (ceil(L/128), BH), 256 threads
+// forward
 // ----------------------------------------------------------------------------
 template <int DP>
 __global__ __launch_bounds__(256) void swa_fwd_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
-    const float* __restrict__ meta, int n_meta, bf16* __restrict__ y, float* __restrict__ y32,
-    float* __restrict__ lse, int L, int d, int W, float scale) {
-  using T = SwaTiles<DP>;
+    const float* __restrict__ meta, int n_meta, bf16* __restrict__ y, float* __restrict__ lse,
+    int BH, int L, int d, int W, float scale, int per) {
+  using Cfg = SwaCfg<DP>;
+  constexpr int P = Cfg::P;
   extern __shared__ __align__(16) char smem[];
-  bf16* kn = reinterpret_cast<bf16*>(smem);
-  bf16* vt = kn + T::NAT_ELEMS;
+  bf16* k_l = reinterpret_cast<bf16*>(smem);
+  bf16* v_l = reinterpret_cast<bf16*>(smem + Cfg::TILE_BYTES);
 
-  const int bh = blockIdx.y;
+  const int nqb = (L + SWA_ROWS - 1) / SWA_ROWS;
+  const int lb = xcd_block(blockIdx.x, per);
+  if (lb >= BH * nqb) return;
+  const int bh = lb / nqb, Q0 = (lb % nqb) * SWA_ROWS;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int col = lane & 31, h = lane >> 5;
-  const int Q0 = blockIdx.x * 128;
-  const int q0 = Q0 + wave * 32;
+  const int q0 = Q0 + wave * 32, qi = q0 + col;
   const size_t base = (size_t)bh * L * d;
-  const int qi = q0 + col;
+  const bool vec = (d & 7) == 0;
 
   bf16x8 qreg[DP / 16];
-  load_rows_operand<DP>(q + base, qi, L, d, h, qreg);
+  own_rows<DP>(q + base, qi, L, d, h, vec, qreg);
 
   // running max and sum start from the sinks (src/kernels/swa.py:34-38)
   float m_i = -1e30f;
@@ -113,51 +124,63 @@ __global__ __launch_bounds__(256) void swa_fwd_kernel(
 #pragma unroll
   for (int t = 0; t < DP / 32; ++t) o[t] = zero16();
 
-  const int klo = max(0, Q0 - W + 1) & ~31;
-  const int khi = min(L, Q0 + 128);
-  for (int k0 = klo; k0 < khi; k0 += 32) {
-    __syncthreads();
-    stage_rows<DP, true, false>(k + base, k0, L, d, kn, nullptr);
-    stage_rows<DP, false, true>(v + base, k0, L, d, nullptr, vt);
-    __syncthreads();
-    if (q0 >= L || k0 > q0 + 31 || k0 + 31 < q0 - W + 1) continue;
-    f32x16 s = zero16();
-#pragma unroll
-    for (int kb = 0; kb < DP / 16; ++kb) {
-      const bf16x8 a = *reinterpret_cast<const bf16x8*>(kn + col * T::NPITCH + 16 * kb + 8 * h);
-      s = mfma(a, qreg[kb], s);
+  const int klo = (max(0, Q0 - W + 1) / SWA_TILE) * SWA_TILE;
+  const int khi = min(L, Q0 + SWA_ROWS);
+  uint4 rk[Cfg::NL], rv[Cfg::NL];
+  swa_load<DP>(rk, k + base, klo, L, d, vec);
+  swa_load<DP>(rv, v + base, klo, L, d, vec);
+  swa_store<DP>(rk, k_l);
+  swa_store<DP>(rv, v_l);
+  __syncthreads();
+  for (int t0 = klo; t0 < khi; t0 += SWA_TILE) {
+    const bool more = t0 + SWA_TILE < khi;
+    if (more) {
+      swa_load<DP>(rk, k + base, t0 + SWA_TILE, L, d, vec);
+      swa_load<DP>(rv, v + base, t0 + SWA_TILE, L, d, vec);
     }
-    float mx = NEG_INF;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int key = k0 + acc_row(r, h);
-      s[r] = in_window(qi, key, L, W) ? s[r] * scale : NEG_INF;
-      mx = fmaxf(mx, s[r]);
-    }
-    mx = fmaxf(mx, xhalf(mx));
-    const float m_new = fmaxf(m_i, mx);
-    const float alpha = fexp(m_i - m_new);
-    float ps = 0.f;
-    bf16x8 p[2];
+    for (int half = 0; half < 2; ++half) {
+      const int k0 = t0 + 32 * half;
+      if (!blocks_meet(q0, k0, L, W)) continue;
+      f32x16 s = zero16();
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float e = fexp(s[r] - m_new);
-      ps += e;
-      p[r >> 3][r & 7] = to_bf16(e);
-    }
-    ps += xhalf(ps);
-    l_i = l_i * alpha + ps;
+      for (int kb = 0; kb < DP / 16; ++kb)
+        s = mfma(row_operand(k_l, P, 32 * half + col, 16 * kb, h), qreg[kb], s);
+      float mx = NEG_INF;
 #pragma unroll
-    for (int t = 0; t < DP / 32; ++t) {
+      for (int r = 0; r < 16; ++r) {
+        s[r] = in_window(qi, k0 + acc_row(r, h), L, W) ? s[r] * scale : NEG_INF;
+        mx = fmaxf(mx, s[r]);
+      }
+      mx = fmaxf(mx, xhalf(mx));
+      const float m_new = fmaxf(m_i, mx);
+      const float alpha = fexp(m_i - m_new);
+      float ps = 0.f;
+      bf16x8 p[2];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) o[t][r] *= alpha;
+      for (int r = 0; r < 16; ++r) {
+        const float e = fexp(s[r] - m_new);
+        ps += e;
+        p[r >> 3][r & 7] = to_bf16(e);
+      }
+      ps += xhalf(ps);
+      l_i = l_i * alpha + ps;
+      m_i = m_new;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(vt + (t * 32 + col) * T::TPITCH + 16 * kb + 8 * h);
-        o[t] = mfma(a, p[kb], o[t]);
+      for (int t = 0; t < DP / 32; ++t) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[t][r] *= alpha;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+          o[t] = mfma(tr_operand(v_l, P, 32 * half + 16 * kb, t * 32, lane), p[kb], o[t]);
       }
     }
-    m_i = m_new;
+    if (more) {
+      __syncthreads();
+      swa_store<DP>(rk, k_l);
+      swa_store<DP>(rv, v_l);
+      __syncthreads();
+    }
   }
   if (qi < L) {
     const float inv = 1.f / l_i;
@@ -165,193 +188,226 @@ __global__ __launch_bounds__(256) void swa_fwd_kernel(
     for (int t = 0; t < DP / 32; ++t)
 #pragma unroll
       for (int g = 0; g < 4; ++g)
-      {
-        const int c = t * 32 + 8 * g + 4 * h;
-        store4<bf16>(y + base, qi, c, d, o[t][4 * g] * inv, o[t][4 * g + 1] * inv,
-                     o[t][4 * g + 2] * inv, o[t][4 * g + 3] * inv);
-        if (y32)
-          store4<float>(y32 + base, qi, c, d, o[t][4 * g] * inv, o[t][4 * g + 1] * inv,
-                        o[t][4 * g + 2] * inv, o[t][4 * g + 3] * inv);
-      }
+        store4<bf16>(y + base, qi, t * 32 + 8 * g + 4 * h, d, o[t][4 * g] * inv,
+                     o[t][4 * g + 1] * inv, o[t][4 * g + 2] * inv, o[t][4 * g + 3] * inv);
     if (h == 0) lse[(size_t)bh * L + qi] = m_i + flog(l_i);
   }
 }
 
 // ----------------------------------------------------------------------------
-// backward: grid (2*ceil(L/128), BH), 256 threads.  Blocks [0, NB) compute dq
-// (and the per-block dmeta partial), blocks [NB, 2NB) compute dk and dv.
+// backward, query side: delta (first pass over the window keys), dq (second
+// pass), and this block's partial of dmeta
 // ----------------------------------------------------------------------------
 template <int DP, typename OutT>
-__global__ __launch_bounds__(256) void swa_bwd_kernel(
+__global__ __launch_bounds__(256) void swa_bwd_dq_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
-    const float* __restrict__ meta, int n_meta, const float* __restrict__ y32,
-    const float* __restrict__ lse, const bf16* __restrict__ dy, OutT* __restrict__ dq,
-    OutT* __restrict__ dk, OutT* __restrict__ dv, float* __restrict__ dmeta_part, int L, int d,
-    int W, float scale) {
-  using T = SwaTiles<DP>;
+    const float* __restrict__ meta, int n_meta, const float* __restrict__ lse,
+    const bf16* __restrict__ dy, OutT* __restrict__ dq, float* __restrict__ delta_out,
+    float* __restrict__ dmeta_part, int BH, int L, int d, int W, float scale, int per) {
+  using Cfg = SwaCfg<DP>;
+  constexpr int P = Cfg::P;
   extern __shared__ __align__(16) char smem[];
-  bf16* nat0 = reinterpret_cast<bf16*>(smem);
-  bf16* nat1 = nat0 + T::NAT_ELEMS;
-  bf16* tr0 = nat1 + T::NAT_ELEMS;
-  bf16* tr1 = tr0 + T::TR_ELEMS;
-  float* rowv = reinterpret_cast<float*>(tr1 + T::TR_ELEMS);   // [2][32] lse, delta
-  float* red = rowv + 64;                                       // [4][SWA_MAX_META]
+  bf16* k_l = reinterpret_cast<bf16*>(smem);
+  bf16* v_l = reinterpret_cast<bf16*>(smem + Cfg::TILE_BYTES);
+  float* red = reinterpret_cast<float*>(smem + 2 * Cfg::TILE_BYTES);   // [4][SWA_MAX_META]
 
-  const int NB = (L + 127) / 128;
-  const int bh = blockIdx.y;
+  const int nqb = (L + SWA_ROWS - 1) / SWA_ROWS;
+  const int lb = xcd_block(blockIdx.x, per);
+  if (lb >= BH * nqb) return;
+  const int bh = lb / nqb, qb = lb % nqb, Q0 = qb * SWA_ROWS;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int col = lane & 31, h = lane >> 5;
+  const int q0 = Q0 + wave * 32, qi = q0 + col;
   const size_t base = (size_t)bh * L * d;
+  const bool vec = (d & 7) == 0;
 
-  if ((int)blockIdx.x < NB) {
-    // ---------------- dq role: this wave owns queries q0..q0+31 ----------------
-    const int Q0 = blockIdx.x * 128;
-    const int q0 = Q0 + wave * 32;
-    const int qi = q0 + col;
-    bf16x8 qreg[DP / 16], dyreg[DP / 16];
-    load_rows_operand<DP>(q + base, qi, L, d, h, qreg);
-    load_rows_operand<DP>(dy + base, qi, L, d, h, dyreg);
-    // delta = dy . y32 over this lane's k-slots (columns 16kb + 8(j/4) + 4h + j%4)
-    float delta = 0.f;
-    if (qi < L) {
-      const float* yr = y32 + base + (size_t)qi * d;
-#pragma unroll
-      for (int kb = 0; kb < DP / 16; ++kb)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int c = 16 * kb + 8 * (j >> 2) + 4 * h + (j & 3);
-          if (c < d) delta += to_f32(dyreg[kb][j]) * yr[c];
-        }
-    }
-    delta += xhalf(delta);
-    const float lse_i = qi < L ? lse[(size_t)bh * L + qi] : 0.f;
+  bf16x8 qreg[DP / 16], dyreg[DP / 16];
+  own_rows<DP>(q + base, qi, L, d, h, vec, qreg);
+  own_rows<DP>(dy + base, qi, L, d, h, vec, dyreg);
+  const float lse_i = qi < L ? lse[(size_t)bh * L + qi] : 0.f;
 
-    f32x16 dqa[DP / 32];
+  const int klo = (max(0, Q0 - W + 1) / SWA_TILE) * SWA_TILE;
+  const int khi = min(L, Q0 + SWA_ROWS);
+  float delta = 0.f;
+  f32x16 dqa[DP / 32];
 #pragma unroll
-    for (int t = 0; t < DP / 32; ++t) dqa[t] = zero16();
+  for (int t = 0; t < DP / 32; ++t) dqa[t] = zero16();
 
-    const int klo = max(0, Q0 - W + 1) & ~31;
-    const int khi = min(L, Q0 + 128);
-    for (int k0 = klo; k0 < khi; k0 += 32) {
-      __syncthreads();
-      stage_rows<DP, true, true>(k + base, k0, L, d, nat0, tr0);
-      stage_rows<DP, true, false>(v + base, k0, L, d, nat1, nullptr);
-      __syncthreads();
-      if (q0 >= L || k0 > q0 + 31 || k0 + 31 < q0 - W + 1) continue;
-      f32x16 s = zero16(), dp = zero16();
-#pragma unroll
-      for (int kb = 0; kb < DP / 16; ++kb) {
-        const bf16x8 ka = *reinterpret_cast<const bf16x8*>(nat0 + col * T::NPITCH + 16 * kb + 8 * h);
-        const bf16x8 va = *reinterpret_cast<const bf16x8*>(nat1 + col * T::NPITCH + 16 * kb + 8 * h);
-        s = mfma(ka, qreg[kb], s);
-        dp = mfma(va, dyreg[kb], dp);
-      }
-      bf16x8 ds[2];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = k0 + acc_row(r, h);
-        const float p = in_window(qi, key, L, W) ? fexp(s[r] * scale - lse_i) : 0.f;
-        ds[r >> 3][r & 7] = to_bf16(p * (dp[r] - delta));
-      }
-#pragma unroll
-      for (int t = 0; t < DP / 32; ++t)
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-          const bf16x8 a = *reinterpret_cast<const bf16x8*>(tr0 + (t * 32 + col) * T::TPITCH + 16 * kb + 8 * h);
-          dqa[t] = mfma(a, ds[kb], dqa[t]);
-        }
-    }
-    if (qi < L) {
-#pragma unroll
-      for (int t = 0; t < DP / 32; ++t)
-#pragma unroll
-        for (int g = 0; g < 4; ++g)
-          store4<OutT>(dq + base, qi, t * 32 + 8 * g + 4 * h, d, dqa[t][4 * g] * scale,
-                       dqa[t][4 * g + 1] * scale, dqa[t][4 * g + 2] * scale,
-                       dqa[t][4 * g + 3] * scale);
-    }
-    // dmeta partial of this block: -sum_i e^{meta_j - lse_i} delta_i
-    for (int j = 0; j < n_meta; ++j) {
-      float c = (qi < L && h == 0) ? fexp(meta[j] - lse_i) * delta : 0.f;
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) c += __shfl_xor(c, off);
-      if (lane == 0) red[wave * SWA_MAX_META + j] = c;
-    }
+  uint4 rk[Cfg::NL], rv[Cfg::NL];
+  // pass 0 accumulates delta = sum_t p dp; pass 1 forms ds and dq
+  for (int pass = 0; pass < 2; ++pass) {
+    swa_load<DP>(rk, k + base, klo, L, d, vec);
+    swa_load<DP>(rv, v + base, klo, L, d, vec);
     __syncthreads();
-    if ((int)threadIdx.x < n_meta) {
-      const int j = threadIdx.x;
-      const float c = red[j] + red[SWA_MAX_META + j] + red[2 * SWA_MAX_META + j] +
-                      red[3 * SWA_MAX_META + j];
-      dmeta_part[((size_t)bh * NB + blockIdx.x) * n_meta + j] = -c;
+    swa_store<DP>(rk, k_l);
+    swa_store<DP>(rv, v_l);
+    __syncthreads();
+    for (int t0 = klo; t0 < khi; t0 += SWA_TILE) {
+      const bool more = t0 + SWA_TILE < khi;
+      if (more) {
+        swa_load<DP>(rk, k + base, t0 + SWA_TILE, L, d, vec);
+        swa_load<DP>(rv, v + base, t0 + SWA_TILE, L, d, vec);
+      }
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const int k0 = t0 + 32 * half;
+        if (!blocks_meet(q0, k0, L, W)) continue;
+        f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+        for (int kb = 0; kb < DP / 16; ++kb) {
+          s = mfma(row_operand(k_l, P, 32 * half + col, 16 * kb, h), qreg[kb], s);
+          dp = mfma(row_operand(v_l, P, 32 * half + col, 16 * kb, h), dyreg[kb], dp);
+        }
+        if (pass == 0) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float p = in_window(qi, k0 + acc_row(r, h), L, W) ? fexp(s[r] * scale - lse_i) : 0.f;
+            delta += p * dp[r];
+          }
+        } else {
+          bf16x8 ds[2];
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float p = in_window(qi, k0 + acc_row(r, h), L, W) ? fexp(s[r] * scale - lse_i) : 0.f;
+            ds[r >> 3][r & 7] = to_bf16(p * (dp[r] - delta));
+          }
+#pragma unroll
+          for (int t = 0; t < DP / 32; ++t)
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+              dqa[t] = mfma(tr_operand(k_l, P, 32 * half + 16 * kb, t * 32, lane), ds[kb], dqa[t]);
+        }
+      }
+      if (more) {
+        __syncthreads();
+        swa_store<DP>(rk, k_l);
+        swa_store<DP>(rv, v_l);
+        __syncthreads();
+      }
     }
-    return;
+    if (pass == 0) delta += xhalf(delta);
   }
+  if (qi < L) {
+#pragma unroll
+    for (int t = 0; t < DP / 32; ++t)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        store4<OutT>(dq + base, qi, t * 32 + 8 * g + 4 * h, d, dqa[t][4 * g] * scale,
+                     dqa[t][4 * g + 1] * scale, dqa[t][4 * g + 2] * scale,
+                     dqa[t][4 * g + 3] * scale);
+    if (h == 0) delta_out[(size_t)bh * L + qi] = delta;
+  }
+  // dmeta partial of this block: -sum_i e^{meta_j - lse_i} delta_i
+  for (int j = 0; j < n_meta; ++j) {
+    float c = (qi < L && h == 0) ? fexp(meta[j] - lse_i) * delta : 0.f;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) c += __shfl_xor(c, off);
+    if (lane == 0) red[wave * SWA_MAX_META + j] = c;
+  }
+  __syncthreads();
+  if ((int)threadIdx.x < n_meta) {
+    const int j = threadIdx.x;
+    const float c = red[j] + red[SWA_MAX_META + j] + red[2 * SWA_MAX_META + j] +
+                    red[3 * SWA_MAX_META + j];
+    dmeta_part[((size_t)bh * nqb + qb) * n_meta + j] = -c;
+  }
+}
 
-  // ---------------- dk/dv role: this wave owns keys kk0..kk0+31 ----------------
-  const int K0 = (blockIdx.x - NB) * 128;
-  const int kk0 = K0 + wave * 32;
-  const int ti = kk0 + col;
+// ----------------------------------------------------------------------------
+// backward, key side: dk and dv over the queries whose windows hold the keys
+// ----------------------------------------------------------------------------
+template <int DP, typename OutT>
+__global__ __launch_bounds__(256) void swa_bwd_dkv_kernel(
+    const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
+    const float* __restrict__ lse, const float* __restrict__ delta_in,
+    const bf16* __restrict__ dy, OutT* __restrict__ dk, OutT* __restrict__ dv, int BH, int L,
+    int d, int W, float scale, int per) {
+  using Cfg = SwaCfg<DP>;
+  constexpr int P = Cfg::P;
+  extern __shared__ __align__(16) char smem[];
+  bf16* q_l = reinterpret_cast<bf16*>(smem);
+  bf16* dy_l = reinterpret_cast<bf16*>(smem + Cfg::TILE_BYTES);
+  float* lse_l = reinterpret_cast<float*>(smem + 2 * Cfg::TILE_BYTES);   // [64]
+  float* del_l = lse_l + SWA_TILE;                                        // [64]
+
+  const int nkb = (L + SWA_ROWS - 1) / SWA_ROWS;
+  const int lb = xcd_block(blockIdx.x, per);
+  if (lb >= BH * nkb) return;
+  const int bh = lb / nkb, K0 = (lb % nkb) * SWA_ROWS;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int col = lane & 31, h = lane >> 5;
+  const int k0 = K0 + wave * 32, ti = k0 + col;
+  const size_t base = (size_t)bh * L * d, lbase = (size_t)bh * L;
+  const bool vec = (d & 7) == 0;
+
   bf16x8 kreg[DP / 16], vreg[DP / 16];
-  load_rows_operand<DP>(k + base, ti, L, d, h, kreg);
-  load_rows_operand<DP>(v + base, ti, L, d, h, vreg);
+  own_rows<DP>(k + base, ti, L, d, h, vec, kreg);
+  own_rows<DP>(v + base, ti, L, d, h, vec, vreg);
   f32x16 dka[DP / 32], dva[DP / 32];
 #pragma unroll
   for (int t = 0; t < DP / 32; ++t) {
     dka[t] = zero16();
     dva[t] = zero16();
   }
-  const int qhi = min(L, K0 + 127 + W);
-  for (int qq0 = K0; qq0 < qhi; qq0 += 32) {
-    __syncthreads();
-    stage_rows<DP, true, true>(q + base, qq0, L, d, nat0, tr0);
-    stage_rows<DP, true, true>(dy + base, qq0, L, d, nat1, tr1);
-    {
-      // lse and delta of the 32 staged queries: 8 threads per query
-      const int r = threadIdx.x >> 3, part = threadIdx.x & 7;
-      const int qrow = qq0 + r;
-      float acc = 0.f;
-      if (qrow < L) {
-        const float* yr = y32 + base + (size_t)qrow * d;
-        const bf16* dr = dy + base + (size_t)qrow * d;
-        for (int c = part; c < d; c += 8) acc += yr[c] * to_f32(dr[c]);
-      }
-      acc += __shfl_xor(acc, 1);
-      acc += __shfl_xor(acc, 2);
-      acc += __shfl_xor(acc, 4);
-      if (part == 0) {
-        rowv[r] = qrow < L ? lse[(size_t)bh * L + qrow] : 0.f;
-        rowv[32 + r] = acc;
-      }
+
+  const int qlo = K0, qhi = min(L, K0 + SWA_ROWS - 1 + W);
+  uint4 rq[Cfg::NL], rd[Cfg::NL];
+  float rl = 0.f, rdl = 0.f;
+  auto load_rows = [&](int r0) {
+    swa_load<DP>(rq, q + base, r0, L, d, vec);
+    swa_load<DP>(rd, dy + base, r0, L, d, vec);
+    if (tid < SWA_TILE) {
+      const bool ok = r0 + tid < L;
+      rl = ok ? lse[lbase + r0 + tid] : 0.f;
+      rdl = ok ? delta_in[lbase + r0 + tid] : 0.f;
     }
-    __syncthreads();
-    if (kk0 >= L || qq0 + 31 < kk0 || qq0 > kk0 + 31 + W - 1) continue;
-    f32x16 s = zero16(), dp = zero16();
-#pragma unroll
-    for (int kb = 0; kb < DP / 16; ++kb) {
-      const bf16x8 qa = *reinterpret_cast<const bf16x8*>(nat0 + col * T::NPITCH + 16 * kb + 8 * h);
-      const bf16x8 da = *reinterpret_cast<const bf16x8*>(nat1 + col * T::NPITCH + 16 * kb + 8 * h);
-      s = mfma(qa, kreg[kb], s);
-      dp = mfma(da, vreg[kb], dp);
+  };
+  auto store_rows = [&]() {
+    swa_store<DP>(rq, q_l);
+    swa_store<DP>(rd, dy_l);
+    if (tid < SWA_TILE) {
+      lse_l[tid] = rl;
+      del_l[tid] = rdl;
     }
-    // s, dp: lane owns key ti, register r owns query qq0 + acc_row(r, h)
-    bf16x8 pb[2], dsb[2];
+  };
+  load_rows(qlo);
+  store_rows();
+  __syncthreads();
+  for (int t0 = qlo; t0 < qhi; t0 += SWA_TILE) {
+    const bool more = t0 + SWA_TILE < qhi;
+    if (more) load_rows(t0 + SWA_TILE);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int qr = acc_row(r, h);
-      const int qrow = qq0 + qr;
-      const float p = in_window(qrow, ti, L, W) ? fexp(s[r] * scale - rowv[qr]) : 0.f;
-      pb[r >> 3][r & 7] = to_bf16(p);
-      dsb[r >> 3][r & 7] = to_bf16(p * (dp[r] - rowv[32 + qr]));
-    }
+    for (int half = 0; half < 2; ++half) {
+      const int qq0 = t0 + 32 * half;
+      if (!blocks_meet(qq0, k0, L, W)) continue;
+      f32x16 s = zero16(), dp = zero16();
 #pragma unroll
-    for (int t = 0; t < DP / 32; ++t)
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const bf16x8 qa = *reinterpret_cast<const bf16x8*>(tr0 + (t * 32 + col) * T::TPITCH + 16 * kb + 8 * h);
-        const bf16x8 da = *reinterpret_cast<const bf16x8*>(tr1 + (t * 32 + col) * T::TPITCH + 16 * kb + 8 * h);
-        dva[t] = mfma(da, pb[kb], dva[t]);
-        dka[t] = mfma(qa, dsb[kb], dka[t]);
+      for (int kb = 0; kb < DP / 16; ++kb) {
+        s = mfma(row_operand(q_l, P, 32 * half + col, 16 * kb, h), kreg[kb], s);
+        dp = mfma(row_operand(dy_l, P, 32 * half + col, 16 * kb, h), vreg[kb], dp);
       }
+      // lane owns key ti; register r owns query qq0 + acc_row(r, h)
+      bf16x8 pb[2], dsb[2];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int qr = 32 * half + acc_row(r, h);
+        const float p = in_window(t0 + qr, ti, L, W) ? fexp(s[r] * scale - lse_l[qr]) : 0.f;
+        pb[r >> 3][r & 7] = to_bf16(p);
+        dsb[r >> 3][r & 7] = to_bf16(p * (dp[r] - del_l[qr]));
+      }
+#pragma unroll
+      for (int t = 0; t < DP / 32; ++t)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          dva[t] = mfma(tr_operand(dy_l, P, 32 * half + 16 * kb, t * 32, lane), pb[kb], dva[t]);
+          dka[t] = mfma(tr_operand(q_l, P, 32 * half + 16 * kb, t * 32, lane), dsb[kb], dka[t]);
+        }
+    }
+    if (more) {
+      __syncthreads();
+      store_rows();
+      __syncthreads();
+    }
   }
   if (ti < L) {
 #pragma unroll
@@ -370,49 +426,6 @@ __global__ __launch_bounds__(256) void swa_bwd_kernel(
 // ----------------------------------------------------------------------------
 // host launchers
 // ----------------------------------------------------------------------------
-template <int DP>
-static size_t swa_fwd_lds() {
-  return (SwaTiles<DP>::NAT_ELEMS + SwaTiles<DP>::TR_ELEMS) * sizeof(bf16);
-}
-template <int DP>
-static size_t swa_bwd_lds() {
-  return (2 * SwaTiles<DP>::NAT_ELEMS + 2 * SwaTiles<DP>::TR_ELEMS) * sizeof(bf16) +
-         (64 + 4 * SWA_MAX_META) * sizeof(float);
-}
-
-template <int DP>
-static hipError_t launch_swa_fwd_t(const void* q, const void* k, const void* v, const float* meta,
-                                   int n_meta, void* y, float* y32, float* lse, int BH, int L,
-                                   int d, int W, float scale, hipStream_t st) {
-  const size_t lds = swa_fwd_lds<DP>();
-  auto kern = swa_fwd_kernel<DP>;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-  if (e != hipSuccess) return e;
-  dim3 grid((L + 127) / 128, BH);
-  hipLaunchKernelGGL(kern, grid, dim3(256), lds, st, (const bf16*)q, (const bf16*)k,
-                     (const bf16*)v, meta, n_meta, (bf16*)y, y32, lse, L, d, W, scale);
-  return hipGetLastError();
-}
-
-template <int DP, typename OutT>
-static hipError_t launch_swa_bwd_t(const void* q, const void* k, const void* v, const float* meta,
-                                   int n_meta, const float* y32, const float* lse, const void* dy,
-                                   void* dq, void* dk, void* dv, float* dmeta_part, int BH, int L,
-                                   int d, int W, float scale, hipStream_t st) {
-  const size_t lds = swa_bwd_lds<DP>();
-  auto kern = swa_bwd_kernel<DP, OutT>;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-  if (e != hipSuccess) return e;
-  const int NB = (L + 127) / 128;
-  dim3 grid(2 * NB, BH);
-  hipLaunchKernelGGL(kern, grid, dim3(256), lds, st, (const bf16*)q, (const bf16*)k,
-                     (const bf16*)v, meta, n_meta, y32, lse, (const bf16*)dy,
-                     (OutT*)dq, (OutT*)dk, (OutT*)dv, dmeta_part, L, d, W, scale);
-  return hipGetLastError();
-}
-
 int swa_padded_dim(int d) {
   if (d <= 32) return 32;
   if (d <= 64) return 64;
@@ -421,27 +434,76 @@ int swa_padded_dim(int d) {
   return -1;
 }
 
+// blocks per (b, h) and the XCD-spread grid for BH * nblk logical blocks
+static void swa_grid(int BH, int L, int* per, int* grid) {
+  const int nblk = (L + SWA_ROWS - 1) / SWA_ROWS;
+  const int total = BH * nblk;
+  *per = (total + 7) / 8;
+  *grid = 8 * *per;
+}
+
+int swa_row_blocks(int L) { return (L + SWA_ROWS - 1) / SWA_ROWS; }
+
+template <int DP>
+static hipError_t launch_swa_fwd_t(const void* q, const void* k, const void* v, const float* meta,
+                                   int n_meta, void* y, float* lse, int BH, int L, int d, int W,
+                                   float scale, hipStream_t st) {
+  const size_t lds = 2 * SwaCfg<DP>::TILE_BYTES;
+  auto kern = swa_fwd_kernel<DP>;
+  hipError_t e = ensure_lds<swa_fwd_kernel<DP>>((int)lds);
+  if (e != hipSuccess) return e;
+  int per, grid;
+  swa_grid(BH, L, &per, &grid);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(256), lds, st, (const bf16*)q, (const bf16*)k,
+                     (const bf16*)v, meta, n_meta, (bf16*)y, lse, BH, L, d, W, scale, per);
+  return hipGetLastError();
+}
+
+template <int DP, typename OutT>
+static hipError_t launch_swa_bwd_t(const void* q, const void* k, const void* v, const float* meta,
+                                   int n_meta, const float* lse, const void* dy, void* dq,
+                                   void* dk, void* dv, float* delta, float* dmeta_part, int BH,
+                                   int L, int d, int W, float scale, hipStream_t st) {
+  int per, grid;
+  swa_grid(BH, L, &per, &grid);
+  const size_t lds_q = 2 * SwaCfg<DP>::TILE_BYTES + 4 * SWA_MAX_META * sizeof(float);
+  auto kq = swa_bwd_dq_kernel<DP, OutT>;
+  hipError_t e = ensure_lds<swa_bwd_dq_kernel<DP, OutT>>((int)lds_q);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(kq, dim3(grid), dim3(256), lds_q, st, (const bf16*)q, (const bf16*)k,
+                     (const bf16*)v, meta, n_meta, lse, (const bf16*)dy, (OutT*)dq, delta,
+                     dmeta_part, BH, L, d, W, scale, per);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  const size_t lds_k = 2 * SwaCfg<DP>::TILE_BYTES + 2 * SWA_TILE * sizeof(float);
+  auto kk = swa_bwd_dkv_kernel<DP, OutT>;
+  if ((e = ensure_lds<swa_bwd_dkv_kernel<DP, OutT>>((int)lds_k)) != hipSuccess) return e;
+  hipLaunchKernelGGL(kk, dim3(grid), dim3(256), lds_k, st, (const bf16*)q, (const bf16*)k,
+                     (const bf16*)v, lse, (const float*)delta, (const bf16*)dy, (OutT*)dk,
+                     (OutT*)dv, BH, L, d, W, scale, per);
+  return hipGetLastError();
+}
+
 hipError_t launch_swa_fwd(const void* q, const void* k, const void* v, const float* meta,
-                          int n_meta, void* y, float* y32, float* lse, int BH, int L, int d, int W,
+                          int n_meta, void* y, float* lse, int BH, int L, int d, int W,
                           float scale, hipStream_t st) {
   switch (swa_padded_dim(d)) {
-    case 32: return launch_swa_fwd_t<32>(q, k, v, meta, n_meta, y, y32, lse, BH, L, d, W, scale, st);
-    case 64: return launch_swa_fwd_t<64>(q, k, v, meta, n_meta, y, y32, lse, BH, L, d, W, scale, st);
-    case 128: return launch_swa_fwd_t<128>(q, k, v, meta, n_meta, y, y32, lse, BH, L, d, W, scale, st);
-    case 256: return launch_swa_fwd_t<256>(q, k, v, meta, n_meta, y, y32, lse, BH, L, d, W, scale, st);
+    case 32: return launch_swa_fwd_t<32>(q, k, v, meta, n_meta, y, lse, BH, L, d, W, scale, st);
+    case 64: return launch_swa_fwd_t<64>(q, k, v, meta, n_meta, y, lse, BH, L, d, W, scale, st);
+    case 128: return launch_swa_fwd_t<128>(q, k, v, meta, n_meta, y, lse, BH, L, d, W, scale, st);
+    case 256: return launch_swa_fwd_t<256>(q, k, v, meta, n_meta, y, lse, BH, L, d, W, scale, st);
     default: return hipErrorInvalidValue;
   }
 }
 
 hipError_t launch_swa_bwd(const void* q, const void* k, const void* v, const float* meta,
-                          int n_meta, const float* y32, const float* lse, const void* dy, void* dq,
-                          void* dk, void* dv, bool grad_bf16, float* dmeta_part, int BH, int L,
-                          int d, int W, float scale, hipStream_t st) {
-#define LZ_SWA_BWD(DPV)                                                                      \
-  return grad_bf16 ? launch_swa_bwd_t<DPV, bf16>(q, k, v, meta, n_meta, y32, lse, dy, dq, dk, \
-                                                 dv, dmeta_part, BH, L, d, W, scale, st)     \
-                   : launch_swa_bwd_t<DPV, float>(q, k, v, meta, n_meta, y32, lse, dy, dq, dk, \
-                                                  dv, dmeta_part, BH, L, d, W, scale, st)
+                          int n_meta, const float* lse, const void* dy, void* dq, void* dk,
+                          void* dv, bool grad_bf16, float* delta, float* dmeta_part, int BH,
+                          int L, int d, int W, float scale, hipStream_t st) {
+#define LZ_SWA_BWD(DPV)                                                                        \
+  return grad_bf16 ? launch_swa_bwd_t<DPV, bf16>(q, k, v, meta, n_meta, lse, dy, dq, dk, dv,   \
+                                                 delta, dmeta_part, BH, L, d, W, scale, st)    \
+                   : launch_swa_bwd_t<DPV, float>(q, k, v, meta, n_meta, lse, dy, dq, dk, dv,  \
+                                                  delta, dmeta_part, BH, L, d, W, scale, st)
   switch (swa_padded_dim(d)) {
     case 32: LZ_SWA_BWD(32);
     case 64: LZ_SWA_BWD(64);

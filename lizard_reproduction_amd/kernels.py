@@ -28,11 +28,12 @@ BWD_BLOCKS = (64, 64)
 
 
 def _stream(t):
-    return ctypes_ptr(torch.cuda.current_stream(t.device).cuda_stream)
-
-
-def ctypes_ptr(x):
-    return x if isinstance(x, int) else int(x)
+    """Raw hipStream_t of the current stream of t's device (launches go there,
+    as the reference's Triton launches go to torch's current stream)."""
+    try:
+        return torch._C._cuda_getCurrentRawStream(t.device.index)
+    except AttributeError:   # pragma: no cover - older torch without the raw accessor
+        return torch.cuda.current_stream(t.device).cuda_stream
 
 
 def _ptr(t):
@@ -90,8 +91,12 @@ class _GLA(torch.autograd.Function):
             rc = lib.lz_gla_fwd(_ptr(fq), _ptr(fk), _ptr(v), _ptr(lg), _ptr(y), b, h, length,
                                 nf, nd, per_head, chunk, _ptr(ws), nbytes, _stream(fq))
             _lib.check(rc, "lz_gla_fwd")
+        else:
+            ws = None
         if any(ctx.needs_input_grad[:4]):
             ctx.save_for_backward(fq, fk, v, lg)
+            # the state entering each segment, reused by the backward
+            ctx.fwd_ws = ws
         ctx.chunk = chunk
         return y
 
@@ -111,9 +116,11 @@ class _GLA(torch.autograd.Function):
             per_head = int(lg.dim() == 3)
             nbytes = lib.lz_gla_bwd_workspace_bytes(b, h, length, nf, nd, per_head, ctx.chunk)
             ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=fq.device)
+            fws = ctx.fwd_ws
             rc = lib.lz_gla_bwd(_ptr(fq), _ptr(fk), _ptr(v), _ptr(lg), _ptr(dy), _ptr(dfq),
                                 _ptr(dfk), _ptr(dv), _ptr(dlg), int(gdt == torch.bfloat16), b,
-                                h, length, nf, nd, per_head, ctx.chunk, _ptr(ws), ws.numel(),
+                                h, length, nf, nd, per_head, ctx.chunk, _ptr(fws),
+                                fws.numel() if fws is not None else 0, _ptr(ws), ws.numel(),
                                 _stream(fq))
             _lib.check(rc, "lz_gla_bwd")
         else:
@@ -165,41 +172,38 @@ class _SWA(torch.autograd.Function):
         scale = 1.0 / math.sqrt(d)
         y = torch.empty_like(v)
         lse = torch.empty(b, h, length, device=v.device, dtype=torch.float32)
-        # fp32 copy of y for the backward's delta = dy . y (only when one follows)
-        y32 = torch.empty(v.shape, device=v.device, dtype=torch.float32) \
-            if any(ctx.needs_input_grad[:4]) else None
         if y.numel():
             lib = _lib.load()
             rc = lib.lz_swa_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(meta), meta.numel(), _ptr(y),
-                                _ptr(y32), _ptr(lse), b, h, length, d, window, scale, _stream(q))
+                                _ptr(lse), b, h, length, d, window, scale, _stream(q))
             _lib.check(rc, "lz_swa_fwd")
-        if y32 is not None:
-            ctx.save_for_backward(q, k, v, meta, y32, lse)
+        if any(ctx.needs_input_grad[:4]):
+            ctx.save_for_backward(q, k, v, meta, lse)
         ctx.window, ctx.scale = window, scale
         return y
 
     @staticmethod
     def backward(ctx, dy):
-        q, k, v, meta, y32, lse = ctx.saved_tensors
+        q, k, v, meta, lse = ctx.saved_tensors
         b, h, length, d = q.shape
         dy = _bf16(dy)
         gdt = torch.bfloat16 if all(x == torch.bfloat16 for x in ctx.dtypes[:3]) else torch.float32
         dq = torch.empty(q.shape, device=q.device, dtype=gdt)
         dk = torch.empty_like(dq)
         dv = torch.empty_like(dq)
-        dmeta = torch.zeros(meta.shape, device=q.device, dtype=torch.float32)
+        dmeta = torch.empty(meta.shape, device=q.device, dtype=torch.float32)
         if dy.numel():
             lib = _lib.load()
             n_meta = meta.numel()
             nbytes = lib.lz_swa_bwd_workspace_bytes(b, h, length, d, n_meta)
             ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
-            rc = lib.lz_swa_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(meta), n_meta, _ptr(y32),
+            rc = lib.lz_swa_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(meta), n_meta,
                                 _ptr(lse), _ptr(dy), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dmeta),
                                 int(gdt == torch.bfloat16), b, h, length, d, ctx.window,
                                 ctx.scale, _ptr(ws), ws.numel(), _stream(q))
             _lib.check(rc, "lz_swa_bwd")
         else:
-            dq.zero_(), dk.zero_(), dv.zero_()
+            dq.zero_(), dk.zero_(), dv.zero_(), dmeta.zero_()
         grads = tuple(g.to(dt) for g, dt in zip((dq, dk, dv, dmeta), ctx.dtypes))
         return grads + (None, None, None)
 

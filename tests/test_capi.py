@@ -45,7 +45,7 @@ def test_abi_version_and_error_string(lib):
 def test_null_pointers_are_rejected_with_a_message(lib):
     rc = lib.lz_gla_fwd(None, None, None, None, None, 1, 1, 8, 16, 16, 0, 64, None, 0, None)
     assert rc != 0 and b"null" in lib.lz_last_error()
-    rc = lib.lz_swa_fwd(None, None, None, None, 0, None, None, None, 1, 1, 8, 16, 4, 0.25, None)
+    rc = lib.lz_swa_fwd(None, None, None, None, 0, None, None, 1, 1, 8, 16, 4, 0.25, None)
     assert rc != 0 and b"null" in lib.lz_last_error()
 
 
@@ -55,15 +55,16 @@ def test_bad_sizes_are_rejected_before_any_launch(lib):
     assert rc != 0 and b"unsupported" in lib.lz_last_error()
     rc = lib.lz_gla_fwd(p, p, p, p, p, 1, 1, 8, 16, 16, 0, 48, None, 0, None)
     assert rc != 0 and b"chunk" in lib.lz_last_error()
-    rc = lib.lz_swa_fwd(p, p, p, p, 65, p, p, p, 1, 1, 8, 16, 4, 0.25, None)
+    rc = lib.lz_swa_fwd(p, p, p, p, 65, p, p, 1, 1, 8, 16, 4, 0.25, None)
     assert rc != 0 and b"n_meta" in lib.lz_last_error()
-    rc = lib.lz_swa_fwd(p, p, p, p, 0, p, p, p, 1, 1, 8, 512, 4, 0.25, None)
+    rc = lib.lz_swa_fwd(p, p, p, p, 0, p, p, 1, 1, 8, 512, 4, 0.25, None)
     assert rc != 0 and b"dim" in lib.lz_last_error()
-    rc = lib.lz_swa_fwd(p, p, p, p, 0, p, p, p, 1, 1, 8, 16, 0, 0.25, None)
+    rc = lib.lz_swa_fwd(p, p, p, p, 0, p, p, 1, 1, 8, 16, 0, 0.25, None)
     assert rc != 0 and b"window" in lib.lz_last_error()
     ws = lib.lz_gla_bwd_workspace_bytes(2, 3, 100, 24, 20, 0, 64)
     assert ws > 0
-    rc = lib.lz_gla_bwd(p, p, p, p, p, p, p, p, p, 0, 2, 3, 100, 24, 20, 0, 64, p, ws - 1, None)
+    rc = lib.lz_gla_bwd(p, p, p, p, p, p, p, p, p, 0, 2, 3, 100, 24, 20, 0, 64, None, 0, p, ws - 1,
+                        None)
     assert rc != 0 and b"workspace" in lib.lz_last_error()
 
 
@@ -92,9 +93,8 @@ def test_workspace_sizes(lib, b, h, length, f, d, per_head):
     g, _ = segments(bh, length)
     assert lib.lz_gla_fwd_workspace_bytes(b, h, length, f, d, per_head, 64) == \
         4 * seg_floats(bh, g, f, d)
-    rows = bh if per_head else b
     assert lib.lz_gla_bwd_workspace_bytes(b, h, length, f, d, per_head, 64) == \
-        4 * (4 * bh * length + 2 * seg_floats(bh, g, f, d) + rows * -(-length // 256))
+        4 * (4 * bh * length + 2 * seg_floats(bh, g, f, d) + bh * -(-length // 64))
 
 
 def test_segment_split():
@@ -105,8 +105,9 @@ def test_segment_split():
 
 
 def test_swa_workspace_sizes(lib):
-    assert lib.lz_swa_bwd_workspace_bytes(1, 32, 2048, 64, 4) == 32 * 16 * 4 * 4
-    assert lib.lz_swa_bwd_workspace_bytes(1, 32, 2048, 64, 0) == 0
+    # delta [BH, L] plus dmeta partials [BH * ceil(L/128), n_meta]
+    assert lib.lz_swa_bwd_workspace_bytes(1, 32, 2048, 64, 4) == 4 * (32 * 2048 + 32 * 16 * 4)
+    assert lib.lz_swa_bwd_workspace_bytes(1, 32, 2048, 64, 0) == 4 * 32 * 2048
 
 
 def test_python_api_validates_shapes():

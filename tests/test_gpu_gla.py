@@ -136,3 +136,33 @@ def test_gla_segments_of_several_chunks(length):
     inputs = gla_inputs(length, batch=4, heads=16, features=64, dim=64)
     grad = torch.randn(inputs[2].shape, generator=torch.Generator().manual_seed(1))
     compare(gla_kernel(64), gla_reference, inputs, grad, label=f"segments L={length}")
+
+
+def test_gla_backward_without_forward_workspace_is_bitwise_equal():
+    # through the C ABI: lz_gla_bwd given no forward workspace recomputes the
+    # state entering each segment; the gradients must be the same bits as the
+    # autograd path, which hands it the forward's workspace
+    from lizard_reproduction_amd import _lib
+    fq, fk, v, z = gla_inputs(700, batch=1, heads=4, features=64, dim=64)
+    lg = F.logsigmoid(z)
+    leaves = [t.cuda().requires_grad_() for t in (fq, fk, v, lg)]
+    y = kernels.gla(*leaves)
+    dy = torch.randn(y.shape, generator=torch.Generator().manual_seed(3)).bfloat16().cuda()
+    y.backward(dy)
+    lib = _lib.load()
+    b, h, length, nf = fq.shape
+    nd = v.shape[-1]
+    assert lib.lz_gla_fwd_workspace_bytes(b, h, length, nf, nd, 0, 64) > 0   # segmented
+    ins = [t.detach().contiguous() for t in leaves]
+    dfq, dfk, dv = (torch.empty_like(t) for t in ins[:3])
+    dlg = torch.empty_like(ins[3])
+    n = lib.lz_gla_bwd_workspace_bytes(b, h, length, nf, nd, 0, 64)
+    ws = torch.empty(n, dtype=torch.uint8, device="cuda")
+    rc = lib.lz_gla_bwd(*(t.data_ptr() for t in ins), dy.data_ptr(), dfq.data_ptr(),
+                        dfk.data_ptr(), dv.data_ptr(), dlg.data_ptr(), 1, b, h, length, nf, nd,
+                        0, 64, None, 0, ws.data_ptr(), n,
+                        torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "lz_gla_bwd")
+    torch.cuda.synchronize()
+    for ours, ref in zip((dfq, dfk, dv, dlg), leaves):
+        assert torch.equal(ours, ref.grad)
