@@ -26,29 +26,11 @@ hipError_t launch_swa_fwd(const void* q, const void* k, const void* v, const flo
                           float scale, hipStream_t st);
 hipError_t launch_swa_bwd(const void* q, const void* k, const void* v, const float* meta,
                           int n_meta, const float* lse, const void* dy, void* dq, void* dk,
-                          void* dv, bool grad_bf16, float* delta, float* dmeta_part, int BH,
-                          int L, int d, int W, float scale, hipStream_t st);
+                          void* dv, bool grad_bf16, float* delta, float* dmeta_part,
+                          float* dmeta, int BH, int L, int d, int W, float scale,
+                          hipStream_t st);
 constexpr int MAX_META = 64;
 
-// Sum of the per-block dmeta partials [rows, n_meta] in a fixed order: thread
-// (group g, sink j) sums rows g, g + groups, ...; thread j then sums the groups.
-__global__ __launch_bounds__(256) void dmeta_reduce_kernel(const float* __restrict__ part,
-                                                           float* __restrict__ dmeta, int rows,
-                                                           int n_meta) {
-  __shared__ float sh[256];
-  const int groups = 256 / n_meta;
-  const int j = threadIdx.x % n_meta, grp = threadIdx.x / n_meta;
-  float s = 0.f;
-  if (grp < groups)
-    for (int r = grp; r < rows; r += groups) s += part[(size_t)r * n_meta + j];
-  sh[threadIdx.x] = s;
-  __syncthreads();
-  if ((int)threadIdx.x < n_meta) {
-    float t = 0.f;
-    for (int g = 0; g < groups; ++g) t += sh[g * n_meta + threadIdx.x];
-    dmeta[threadIdx.x] = t;
-  }
-}
 }  // namespace lz
 
 static thread_local std::string g_err;
@@ -193,11 +175,8 @@ extern "C" int lz_swa_bwd(const void* q, const void* k, const void* v, const flo
   hipStream_t st = (hipStream_t)stream;
   float* delta = (float*)workspace;
   float* part = delta + (size_t)batch * heads * length;
-  hipError_t e = lz::launch_swa_bwd(q, k, v, meta, n_meta, lse, dy, dq, dk, dv, grad_bf16 != 0,
-                                    delta, part, batch * heads, length, dim, window, scale, st);
-  if (e != hipSuccess || n_meta == 0) return hip_status(e, "swa_bwd");
-  const int rows = batch * heads * lz::swa_row_blocks(length);
-  hipLaunchKernelGGL(lz::dmeta_reduce_kernel, dim3(1), dim3(256), 0, st, (const float*)part,
-                     dmeta, rows, n_meta);
-  return hip_status(hipGetLastError(), "swa_bwd dmeta");
+  return hip_status(lz::launch_swa_bwd(q, k, v, meta, n_meta, lse, dy, dq, dk, dv,
+                                       grad_bf16 != 0, delta, part, dmeta, batch * heads, length,
+                                       dim, window, scale, st),
+                    "swa_bwd");
 }

@@ -22,7 +22,8 @@
 //   A  gla_bwd_dq_kernel, forward walk per (b, h, segment): carries S^T in
 //      MFMA accumulators; recomputes den and delta -- delta_i = dy_i . o_i /
 //      den_i with dy_i . o_i = Q~_i . (S_n dy_i) + sum_t a_it (v_t . dy_i), both
-//      products it needs anyway -- and writes dfq, den, delta and fq . dfq.
+//      products it needs anyway, Q~ = fq qs unrounded as in the forward -- and
+//      writes dfq, den, delta and fq . dfq.
 //   [G > 1] gla_bwd_state_kernel + reverse scan: dS, dz entering each segment
 //      from the right (needs den and delta from A).
 //   B  gla_bwd_dkv_kernel, reverse walk per (b, h, segment): carries dS in
@@ -74,7 +75,9 @@ struct BwdA : BwdCommon<FP, DP> {
   static constexpr int OFF_ZP = OFF_Z + FP * 4;
   static constexpr int OFF_R = OFF_ZP + ZPARTS * FP * 4;
   static constexpr int BYTES = OFF_R + 16;
-  static constexpr int LB = (FP >= 256 || FP + DP >= 192) ? 1 : 2;
+  static constexpr int LB = (FP >= 256 || FP + DP >= 160) ? 1 : 2;
+  // chunks prefetched ahead (1 or 2; two measured slower at the bench shapes)
+  static constexpr int DEPTH = 1;
 };
 
 template <int FP, int DP, typename OutT>
@@ -135,32 +138,40 @@ __global__ __launch_bounds__(256, (BwdA<FP, DP>::LB)) void gla_bwd_dq_kernel(
     }
   for (int f = tid; f < FP; f += 256) zs[f] = st ? st[FP * DP + f] : 0.f;
 
-  uint4 rq[Cfg::NLF], rk[Cfg::NLF], rv[Cfg::NLD], rd[Cfg::NLD];
-  float rg;
-  load_chunk<FP>(rq, fq + offF, n0 * C, L, F, vecF);
-  load_chunk<FP>(rk, fk + offF, n0 * C, L, F, vecF);
-  load_chunk<DP>(rv, v + offD, n0 * C, L, D, vecD);
-  load_chunk<DP>(rd, dy + offD, n0 * C, L, D, vecD);
-  rg = gate_at(lgb, n0 * C + lane, L);
-  store_chunk<FP>(rq, fq_l, PF);
-  store_chunk<FP>(rk, fk_l, PF);
-  store_chunk<DP>(rv, v_l, PD);
-  store_chunk<DP>(rd, dy_l, PD);
-  if (wave == 0) gate_scan(rg, lane, lgs, qs, ks, rdec);
+  // DEPTH register sets: while chunk n computes, chunks n+1 .. n+DEPTH are in flight
+  constexpr int DEPTH = Cfg::DEPTH;
+  uint4 rq[DEPTH][Cfg::NLF], rk[DEPTH][Cfg::NLF], rv[DEPTH][Cfg::NLD], rd[DEPTH][Cfg::NLD];
+  float rg[DEPTH];
+  auto issue = [&](auto set, int n) __attribute__((always_inline)) {
+    constexpr int S = decltype(set)::value;
+    if (n < n1) {
+      load_chunk<FP>(rq[S], fq + offF, n * C, L, F, vecF);
+      load_chunk<FP>(rk[S], fk + offF, n * C, L, F, vecF);
+      load_chunk<DP>(rv[S], v + offD, n * C, L, D, vecD);
+      load_chunk<DP>(rd[S], dy + offD, n * C, L, D, vecD);
+      rg[S] = gate_at(lgb, n * C + lane, L);
+    }
+  };
+  auto stage = [&](auto set) __attribute__((always_inline)) {
+    constexpr int S = decltype(set)::value;
+    store_chunk<FP>(rq[S], fq_l, PF);
+    store_chunk<FP>(rk[S], fk_l, PF);
+    store_chunk<DP>(rv[S], v_l, PD);
+    store_chunk<DP>(rd[S], dy_l, PD);
+    if (wave == 0) gate_scan(rg[S], lane, lgs, qs, ks, rdec);
+  };
+  issue(SET0, n0);
+  if constexpr (DEPTH == 2) issue(SET1, n0 + 1);
+  stage(SET0);
   __syncthreads();
 
   const int kt = wave >> 1, qt = wave & 1;   // this wave's tile of the 64x64 score block
   const int qi = qt * 32 + col;               // chunk-local query of this lane
-  for (int n = n0; n < n1; ++n) {
+  // chunk n is in LDS and register set `set` is free; the next set holds chunk n+1
+  auto step = [&](auto set, int n) __attribute__((always_inline)) {
+    constexpr int S = decltype(set)::value;
     const int t0 = n * C;
-    const bool more = n + 1 < n1;
-    if (more) {
-      load_chunk<FP>(rq, fq + offF, t0 + C, L, F, vecF);
-      load_chunk<FP>(rk, fk + offF, t0 + C, L, F, vecF);
-      load_chunk<DP>(rv, v + offD, t0 + C, L, D, vecD);
-      load_chunk<DP>(rd, dy + offD, t0 + C, L, D, vecD);
-      rg = gate_at(lgb, t0 + C + lane, L);
-    }
+    issue(set, n + DEPTH);
     // ---- phase 1: a^T and (v dy^T) tile; Q~.z; sums of K~; X = S dy^T --------
     f32x16 aT = zero16(), vdy = zero16();
 #pragma unroll
@@ -188,16 +199,15 @@ __global__ __launch_bounds__(256, (BwdA<FP, DP>::LB)) void gla_bwd_dq_kernel(
         ra[kt * 64 + qi] = sa;
         rav[kt * 64 + qi] = sav;
       }
-      constexpr int FQ = FP / 4;   // Q~ . z over a quarter of the features; query = lane
-      const float qsv = qs[lane];
+      constexpr int FQ = FP / 4;   // qs (fq . z) over a quarter of the features; query = lane
       float acc = 0.f;
 #pragma unroll
       for (int c = 0; c < FQ; c += 8) {
         const bf16x8 x = *reinterpret_cast<const bf16x8*>(fq_l + lane * PF + wave * FQ + c);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc += to_f32(to_bf16(to_f32(x[e]) * qsv)) * zs[wave * FQ + c + e];
+        for (int e = 0; e < 8; ++e) acc += to_f32(x[e]) * zs[wave * FQ + c + e];
       }
-      qz[wave * 64 + lane] = acc;
+      qz[wave * 64 + lane] = acc * qs[lane];
       constexpr int TPP = C / Cfg::ZPARTS;
       const int f = tid % FP, part = tid / FP;
       if (part < Cfg::ZPARTS) {
@@ -221,16 +231,15 @@ __global__ __launch_bounds__(256, (BwdA<FP, DP>::LB)) void gla_bwd_dq_kernel(
           for (int kb = 0; kb < DP / 16; ++kb)
             x = mfma(acc_operand(St[i][kb >> 1], kb & 1), row_operand_acc(dy_l, PD, q, 16 * kb, h), x);
           X[i][j] = x;
-          const float qsv = qs[q];
-          float s = 0.f;
+          float s = 0.f;   // qs (fq . S dy) over this f-tile
 #pragma unroll
           for (int g4 = 0; g4 < 4; ++g4) {
             const bf16x4 f4 = *reinterpret_cast<const bf16x4*>(fq_l + q * PF + ft * 32 + 8 * g4 + 4 * h);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) s += to_f32(to_bf16(to_f32(f4[e]) * qsv)) * x[4 * g4 + e];
+            for (int e = 0; e < 4; ++e) s += to_f32(f4[e]) * x[4 * g4 + e];
           }
           s += xhalf(s);
-          if (h == 0) nx[ft * 64 + q] = s;
+          if (h == 0) nx[ft * 64 + q] = s * qs[q];
         }
       }
     }
@@ -328,13 +337,7 @@ __global__ __launch_bounds__(256, (BwdA<FP, DP>::LB)) void gla_bwd_dq_kernel(
       for (int ft = 0; ft < NFT; ++ft) s += pp[ft * 64 + tid];
       p_out[offL + t0 + tid] = s;
     }
-    if (more) {
-      store_chunk<FP>(rq, fq_l, PF);
-      store_chunk<FP>(rk, fk_l, PF);
-      store_chunk<DP>(rv, v_l, PD);
-      store_chunk<DP>(rd, dy_l, PD);
-      if (wave == 0) gate_scan(rg, lane, lgs, qs, ks, rdec);
-    }
+    if (n + 1 < n1) stage(std::integral_constant<int, (S + 1) % DEPTH>{});
     if (tid < FP) {
       float za = zs[tid] * r_n;
 #pragma unroll
@@ -342,6 +345,11 @@ __global__ __launch_bounds__(256, (BwdA<FP, DP>::LB)) void gla_bwd_dq_kernel(
       zs[tid] = za;
     }
     __syncthreads();
+  };
+  for (int n = n0; n < n1; n += DEPTH) {
+    step(SET0, n);
+    if constexpr (DEPTH == 2)
+      if (n + 1 < n1) step(SET1, n + 1);
   }
 }
 
@@ -540,6 +548,7 @@ struct BwdB : BwdCommon<FP, DP> {
   static constexpr int OFF_R = OFF_DZP + ZPARTS * FP * 4;
   static constexpr int BYTES = OFF_R + 16;
   static constexpr int LB = (FP >= 256 || FP + DP >= 160) ? 1 : 2;
+  static constexpr int DEPTH = 1;
 };
 
 template <int FP, int DP, typename OutT>
@@ -619,43 +628,49 @@ __global__ __launch_bounds__(256, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_kernel(
     }
   };
 
-  uint4 rq[Cfg::NLF], rk[Cfg::NLF], rv[Cfg::NLD], rd[Cfg::NLD];
-  TokScalars sc;
-  {
-    const int t0 = (n1 - 1) * C;
-    load_chunk<FP>(rq, fq + offF, t0, L, F, vecF);
-    load_chunk<FP>(rk, fk + offF, t0, L, F, vecF);
-    load_chunk<DP>(rv, v + offD, t0, L, D, vecD);
-    load_chunk<DP>(rd, dy + offD, t0, L, D, vecD);
-    sc = load_scalars(lgb, den_in, delta_in, p_in, offL, t0 + lane, L);
-    store_chunk<FP>(rq, fq_l, PF);
-    store_chunk<FP>(rk, fk_l, PF);
-    store_chunk<DP>(rv, v_l, PD);
-    store_chunk<DP>(rd, dy_l, PD);
-    const int b = (n1 - 1) & 1;
+  // DEPTH register sets: while chunk n computes, chunks n-1 .. n-DEPTH are in flight
+  constexpr int DEPTH = Cfg::DEPTH;
+  uint4 rq[DEPTH][Cfg::NLF], rk[DEPTH][Cfg::NLF], rv[DEPTH][Cfg::NLD], rd[DEPTH][Cfg::NLD];
+  TokScalars sc[DEPTH];
+  auto issue = [&](auto set, int n) __attribute__((always_inline)) {
+    constexpr int S = decltype(set)::value;
+    if (n >= n0) {
+      load_chunk<FP>(rq[S], fq + offF, n * C, L, F, vecF);
+      load_chunk<FP>(rk[S], fk + offF, n * C, L, F, vecF);
+      load_chunk<DP>(rv[S], v + offD, n * C, L, D, vecD);
+      load_chunk<DP>(rd[S], dy + offD, n * C, L, D, vecD);
+      sc[S] = load_scalars(lgb, den_in, delta_in, p_in, offL, n * C + lane, L);
+    }
+  };
+  // chunk n's tiles and per-token scalars (scalars into the buffers of parity n & 1)
+  auto stage = [&](auto set, int n) __attribute__((always_inline)) {
+    constexpr int S = decltype(set)::value;
+    store_chunk<FP>(rq[S], fq_l, PF);
+    store_chunk<FP>(rk[S], fk_l, PF);
+    store_chunk<DP>(rv[S], v_l, PD);
+    store_chunk<DP>(rd[S], dy_l, PD);
+    const int b = n & 1;
     if (wave == 0)
-      bwd_scalars(sc.g, sc.den, sc.delta, sc.p, lane, lgs, qs, ks, rdec, dens + 64 * b,
-                  dels + 64 * b, ps + 64 * b, qh + 64 * b);
-    publish();
-  }
+      bwd_scalars(sc[S].g, sc[S].den, sc[S].delta, sc[S].p, lane, lgs, qs, ks, rdec,
+                  dens + 64 * b, dels + 64 * b, ps + 64 * b, qh + 64 * b);
+  };
+  issue(SET0, n1 - 1);
+  if constexpr (DEPTH == 2) issue(SET1, n1 - 2);
+  stage(SET0, n1 - 1);
+  publish();
   __syncthreads();
 
   const int qt = wave >> 1, kt = wave & 1;   // this wave's tile of the score block
   const int ki = kt * 32 + col;               // chunk-local key of this lane (phase 1)
-  for (int n = n1 - 1; n >= n0; --n) {
+  // chunk n is in LDS and register set `set` is free; the next set holds chunk n-1
+  auto step = [&](auto set, int n) __attribute__((always_inline)) {
+    constexpr int S = decltype(set)::value;
     const int t0 = n * C;
-    const bool more = n - 1 >= n0;
     const int cur = n & 1;
     const float* densc = dens + 64 * cur;
     const float* delsc = dels + 64 * cur;
     const float* qhc = qh + 64 * cur;
-    if (more) {
-      load_chunk<FP>(rq, fq + offF, t0 - C, L, F, vecF);
-      load_chunk<FP>(rk, fk + offF, t0 - C, L, F, vecF);
-      load_chunk<DP>(rv, v + offD, t0 - C, L, D, vecD);
-      load_chunk<DP>(rd, dy + offD, t0 - C, L, D, vecD);
-      sc = load_scalars(lgb, den_in, delta_in, p_in, offL, t0 - C + lane, L);
-    }
+    issue(set, n - DEPTH);
     // ---- phase 1: s and (dy v^T) tile (queries x keys) -> a/den, dad; dz sums ----
     {
       f32x16 s = zero16(), dyv = zero16();
@@ -794,16 +809,7 @@ __global__ __launch_bounds__(256, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_kernel(
       if (lane == 0) csum[(size_t)bh * NT + n] = g;
     }
     publish();
-    if (more) {
-      store_chunk<FP>(rq, fq_l, PF);
-      store_chunk<FP>(rk, fk_l, PF);
-      store_chunk<DP>(rv, v_l, PD);
-      store_chunk<DP>(rd, dy_l, PD);
-      const int b = cur ^ 1;
-      if (wave == 0)
-        bwd_scalars(sc.g, sc.den, sc.delta, sc.p, lane, lgs, qs, ks, rdec, dens + 64 * b,
-                    dels + 64 * b, ps + 64 * b, qh + 64 * b);
-    }
+    if (n - 1 >= n0) stage(std::integral_constant<int, (S + 1) % DEPTH>{}, n - 1);
     if (tid < FP) {
       float za = dzs[tid] * r_n;
 #pragma unroll
@@ -811,18 +817,21 @@ __global__ __launch_bounds__(256, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_kernel(
       dzs[tid] = za;
     }
     __syncthreads();
+  };
+  for (int n = n1 - 1; n >= n0; n -= DEPTH) {
+    step(SET0, n);
+    if constexpr (DEPTH == 2)
+      if (n - 1 >= n0) step(SET1, n - 1);
   }
 }
 
 // ============================================================================
 // d log_gamma[row, j] = sum_{j' >= j} value[row, j'], value = dG of that (b, h)
-// row (per-head gate) or its sum over the heads (per-token gate).  One launch
-// over 256-token blocks; a block adds the chunk sums of dG that the reverse
-// walk left for every chunk after it to an in-block suffix scan.  Fixed order
+// row (per-head gate) or its sum over the heads (per-token gate).  One block
+// per (row, 64-token chunk): the chunk sums of dG the reverse walk left for
+// every later chunk, plus a suffix scan inside the chunk.  Fixed order
 // throughout.
 // ============================================================================
-constexpr int GG_BLK = 256;
-
 // Fixed-order tree sum of one value per thread (all 256 threads call it).
 __device__ __forceinline__ float block_sum256(float* sh, float x) {
   const int tid = threadIdx.x;
@@ -842,31 +851,32 @@ __global__ __launch_bounds__(256) void gla_gate_grad_kernel(const float* __restr
                                                             float* __restrict__ dlg, int H, int L,
                                                             int gate_per_head) {
   __shared__ float sh[256];
-  const int row = blockIdx.y, blk = blockIdx.x, tid = threadIdx.x;
+  const int row = blockIdx.y, c = blockIdx.x, tid = threadIdx.x;
   const int NT = (L + GLA_C - 1) / GLA_C;
   const int nsum = gate_per_head ? 1 : H;
   const float* src = dG + (size_t)row * nsum * L;
   const float* cs = csum + (size_t)row * nsum * NT;
-  const int c0 = (blk + 1) * (GG_BLK / GLA_C);   // first chunk after this block
+  const int nc = NT - c - 1;   // chunks after this one
   float after = 0.f;
-  if (NT > c0) {
-    const int nc = NT - c0;
-    for (int idx = tid; idx < nc * nsum; idx += 256) after += cs[(size_t)(idx / nc) * NT + c0 + idx % nc];
-  }
+  for (int idx = tid; idx < nc * nsum; idx += 256)
+    after += cs[(size_t)(idx / nc) * NT + c + 1 + idx % nc];
   after = block_sum256(sh, after);
-  const int j = blk * GG_BLK + tid;
+  // token t of the chunk, heads hg, hg + 4, ... (four head groups per token)
+  const int t = tid & 63, hg = tid >> 6, j = c * GLA_C + t;
   float x = 0.f;
   if (j < L)
-    for (int hh = 0; hh < nsum; ++hh) x += src[(size_t)hh * L + j];
+    for (int hh = hg; hh < nsum; hh += 4) x += src[(size_t)hh * L + j];
   sh[tid] = x;
   __syncthreads();
-  for (int off = 1; off < 256; off <<= 1) {   // inclusive suffix scan
-    const float o = tid + off < 256 ? sh[tid + off] : 0.f;
-    __syncthreads();
-    sh[tid] += o;
-    __syncthreads();
+  if (tid < 64) {
+    float val = sh[t] + sh[64 + t] + sh[128 + t] + sh[192 + t];
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {   // inclusive suffix scan over the chunk
+      const float o = __shfl_down(val, off);
+      if (t + off < 64) val += o;
+    }
+    if (j < L) dlg[(size_t)row * L + j] = after + val;
   }
-  if (j < L) dlg[(size_t)row * L + j] = after + sh[tid];
 }
 
 // ============================================================================
@@ -936,7 +946,7 @@ static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v
                      (const float*)delta, (const float*)p, (OutT*)dfk, (OutT*)dv, dG, csum,
                      (const float*)rseg, H, L, F, D, gate_per_head, G, cps);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  const dim3 ggrid((L + GG_BLK - 1) / GG_BLK, gate_rows(B, H, gate_per_head));
+  const dim3 ggrid((L + GLA_C - 1) / GLA_C, gate_rows(B, H, gate_per_head));
   hipLaunchKernelGGL(gla_gate_grad_kernel, ggrid, dim3(256), 0, st, (const float*)dG,
                      (const float*)csum, dlg, H, L, gate_per_head);
   return hipGetLastError();

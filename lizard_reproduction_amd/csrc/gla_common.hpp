@@ -1,12 +1,18 @@
 // Pieces shared by the GLA forward and backward kernels: chunk staging,
 // the chunk-local gate scan, segment bookkeeping.
 #pragma once
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace lz {
 
 constexpr int GLA_C = 64;            // chunk length (tokens)
 constexpr int GLA_TARGET_WG = 512;   // (b, h, segment) workgroups wanted per launch
+
+// compile-time register-set selectors of the double-buffered chunk prefetch
+constexpr std::integral_constant<int, 0> SET0{};
+constexpr std::integral_constant<int, 1> SET1{};
 
 int gla_padded_dim(int n);
 bool gla_dims_supported(int F, int D);
@@ -35,6 +41,65 @@ __device__ __forceinline__ void store_chunk(const uint4 (&reg)[N], bf16* tile, i
     const int idx = threadIdx.x + 256 * i;
     *reinterpret_cast<uint4*>(tile + (idx / K8) * pitch + (idx % K8) * 8) = reg[i];
   }
+}
+
+// Row-scaled copy of a [64 x KP] row-major bf16 tile, bf16(x[t][c] * scale[t]),
+// spread over the 256 threads as 16-byte items: item i of a thread covers row
+// tid / (KP/8) + (2048/KP) i, columns 8 (tid % (KP/8)) .. +8 (KP/32 items).
+// The thread also writes the sums over its rows of the rounded values, per
+// column, to part[(tid / (KP/8)) * KP + column]: 2048/KP partial sums per
+// column (part holds 2048 floats), which a later pass adds up.
+template <int KP>
+struct RowItems {
+  static constexpr int K8 = KP / 8;
+  static constexpr int N = KP / 32;          // items per thread
+  static constexpr int RSTRIDE = 256 / K8;   // rows between a thread's items
+  static constexpr int PARTS = 256 / K8;     // partial sums per column
+};
+
+template <int KP>
+__device__ __forceinline__ void scale_rows(const bf16* tile, int pitch, const float* scale,
+                                           uint4 (&out)[RowItems<KP>::N], float* part) {
+  using R = RowItems<KP>;
+  const int cg = threadIdx.x % R::K8, r0 = threadIdx.x / R::K8;
+  float sum[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) sum[e] = 0.f;
+#pragma unroll
+  for (int i = 0; i < R::N; ++i) {
+    const int t = r0 + R::RSTRIDE * i;
+    const bf16x8 x = *reinterpret_cast<const bf16x8*>(tile + t * pitch + 8 * cg);
+    const float s = scale[t];
+    bf16x8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      o[e] = to_bf16(to_f32(x[e]) * s);
+      sum[e] += to_f32(o[e]);
+    }
+    out[i] = __builtin_bit_cast(uint4, o);
+  }
+  float* dst = part + r0 * KP + 8 * cg;
+  *reinterpret_cast<f32x4*>(dst) = f32x4{sum[0], sum[1], sum[2], sum[3]};
+  *reinterpret_cast<f32x4*>(dst + 4) = f32x4{sum[4], sum[5], sum[6], sum[7]};
+}
+
+template <int KP>
+__device__ __forceinline__ void store_rows(const uint4 (&in)[RowItems<KP>::N], bf16* tile,
+                                           int pitch) {
+  using R = RowItems<KP>;
+  const int cg = threadIdx.x % R::K8, r0 = threadIdx.x / R::K8;
+#pragma unroll
+  for (int i = 0; i < R::N; ++i)
+    *reinterpret_cast<uint4*>(tile + (r0 + R::RSTRIDE * i) * pitch + 8 * cg) = in[i];
+}
+
+// column c of the partial sums written by scale_rows (threads with tid < KP)
+template <int KP>
+__device__ __forceinline__ float sum_parts(const float* part, int c) {
+  float s = 0.f;
+#pragma unroll 8
+  for (int p = 0; p < RowItems<KP>::PARTS; ++p) s += part[p * KP + c];
+  return s;
 }
 
 // Chunk-local inclusive scan of the gate by one wave (lane = token): lg,

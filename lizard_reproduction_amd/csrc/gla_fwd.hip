@@ -5,13 +5,16 @@
 // src/lizard_attention.py:20-31).  Per (b, h), tokens are cut into 64-token
 // chunks.  Inside chunk n, lg_j is the inclusive sum of log_gamma over the
 // chunk up to token j (so every absorbed factor exp(.) is <= 1):
-//   Q~_i = bf16(fq_i e^{lg_i}),  K~_t = bf16(fk_t e^{lg_end - lg_t})
+//   Q~_i = fq_i e^{lg_i},  K~_t = bf16(fk_t e^{lg_end - lg_t})
 //   a_it = bf16((fq_i . fk_t) e^{lg_i - lg_t}) for t <= i
 //   o_i  = Q~_i bf16(S_n) + sum_t a_it v_t,  den_i = Q~_i . z_n + sum_t a_it
 //   y_i  = o_i / max(den_i, FLT_MIN)
 //   S_{n+1} = e^{lg_end} S_n + K~^T V,   z_{n+1} = e^{lg_end} z_n + sum_t K~_t
 // The reference takes the same differences from a global cumsum G; the
-// chunk-local sums here are the same numbers without the cancellation.
+// chunk-local sums here are the same numbers without the cancellation.  The
+// reference also rounds Q~ to bf16 before both of its products; here the row
+// scale e^{lg_i} multiplies the fp32 results of fq . S_n and fq . z_n instead
+// (one rounding fewer, the same Q~ in numerator and denominator).
 //
 // Work decomposition.  A workgroup (4 waves) walks the chunks of one segment
 // of one (b, h) in order, with the state S (F x D, fp32) in MFMA accumulator
@@ -30,11 +33,12 @@
 //     stores); the next chunk is already in flight into registers.
 //   * phase 1: wave (kt, qt) computes one 32x32 tile of s^T = fk fq^T
 //     (keys x queries), applies the causal decay in registers and publishes
-//     the bf16 tile as ready-made MFMA operands; Q~.z partials and the
-//     partial sums of K~ for z go to LDS.
-//   * phase 2: a wave owns d-tiles of the output and the state: o^T = S^T Q~^T
-//     (S straight from its accumulators) + V^T P^T, y = o / den; then
-//     S <- e^{lg_end} S + K~^T V.  The operands that contract over tokens
+//     the bf16 tile as ready-made MFMA operands; Q~.z partials go to LDS; the
+//     workgroup forms K~ = bf16(fk ks) once (16-byte row items, with their
+//     column sums for z) and writes it over fk, which the scores no longer need.
+//   * phase 2: a wave owns d-tiles of the output and the state: o^T = S^T fq^T
+//     (S straight from its accumulators) scaled by qs, + V^T P^T, y = o / den;
+//     then S <- e^{lg_end} S + K~^T V.  The operands that contract over tokens
 //     (V^T, K~^T, V) come from LDS transpose reads of the row-major tiles.
 //   * the prefetched chunk is written to LDS, the gate scan of the next chunk
 //     runs on wave 0, and z is updated.
@@ -60,8 +64,8 @@ struct GlaFwd {
   static constexpr int OFF_QS = OFF_LG + 64 * 4;          // [64] e^{lg}
   static constexpr int OFF_KS = OFF_QS + 64 * 4;          // [64] e^{lg_end - lg}
   static constexpr int OFF_Z = OFF_KS + 64 * 4;           // [FP] z
-  static constexpr int OFF_ZP = OFF_Z + FP * 4;           // [ZPARTS][FP] partial sums of K~
-  static constexpr int OFF_R = OFF_ZP + ZPARTS * FP * 4;  // e^{lg_end}, lg_end
+  static constexpr int OFF_ZP = OFF_Z + FP * 4;           // 2048 partial sums of K~
+  static constexpr int OFF_R = OFF_ZP + 2048 * 4;         // e^{lg_end}, lg_end
   static constexpr int BYTES = OFF_R + 16;
   static constexpr int SEG = SegRec<FP, DP>::SIZE;
 };
@@ -146,7 +150,8 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
       load_chunk<DP>(rv, vb, t0 + C, L, D, vecD);
       rg = gate_at(lgb, t0 + C + lane, L);
     }
-    // ---- phase 1: scores -> P fragments and row sums; Q~.z; sums of K~ ------
+    // ---- phase 1: scores -> P fragments and row sums; fq.z; K~ rows --------
+    uint4 kti[RowItems<FP>::N];   // this thread's rows of K~ = bf16(fk * ks)
     {
       const int kt = wave >> 1, qt = wave & 1;
       f32x16 s = zero16();
@@ -171,27 +176,19 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
       pfrag[(qt * 4 + kt * 2 + 1) * 64 + lane] = p[1];
       if (h == 0) rs[kt * 64 + qi] = rsum;
 
-      constexpr int FQ = FP / 4;   // Q~ . z over a quarter of the features; query = lane
-      const float qsv = qs[lane];
+      constexpr int FQ = FP / 4;   // qs (fq . z) over a quarter of the features; query = lane
       float acc = 0.f;
 #pragma unroll
       for (int c = 0; c < FQ; c += 8) {
         const bf16x8 x = *reinterpret_cast<const bf16x8*>(fq_l + lane * PF + wave * FQ + c);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc += to_f32(to_bf16(to_f32(x[e]) * qsv)) * zs[wave * FQ + c + e];
+        for (int e = 0; e < 8; ++e) acc += to_f32(x[e]) * zs[wave * FQ + c + e];
       }
-      qz[wave * 64 + lane] = acc;
-
-      constexpr int TPP = C / Cfg::ZPARTS;   // tokens per partial sum of K~
-      const int f = tid % FP, part = tid / FP;
-      if (part < Cfg::ZPARTS) {
-        float za = 0.f;
-#pragma unroll 8
-        for (int t = part * TPP; t < (part + 1) * TPP; ++t)
-          za += to_f32(to_bf16(to_f32(fk_l[t * PF + f]) * ks[t]));
-        zp[part * FP + f] = za;
-      }
+      qz[wave * 64 + lane] = acc * qs[lane];
+      scale_rows<FP>(fk_l, PF, ks, kti, zp);
     }
+    __syncthreads();
+    store_rows<FP>(kti, fk_l, PF);   // fk_l holds K~ from here to the end of the chunk
     __syncthreads();
     // ---- phase 2: outputs and state update ----------------------------------
     const float r_n = rdec[0];
@@ -206,12 +203,15 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
         for (int j = 0; j < NQW; ++j) {
           const int qt = qtile(j);
           const int qi = qt * 32 + col;
-          const float qsv = qs[qi];
+          // o^T = qs (S^T fq^T) + V^T P^T: the row scale of Q~ = fq qs is applied to the
+          // fp32 product (den uses the same unrounded Q~, so L = 1 still gives y = v)
           f32x16 o = zero16();
 #pragma unroll
           for (int kb = 0; kb < FP / 16; ++kb)
-            o = mfma(acc_operand(S[i][kb >> 1], kb & 1),
-                     scale8(row_operand_acc(fq_l, PF, qi, 16 * kb, h), qsv), o);
+            o = mfma(acc_operand(S[i][kb >> 1], kb & 1), row_operand_acc(fq_l, PF, qi, 16 * kb, h), o);
+          const float qsv = qs[qi];
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[r] *= qsv;
 #pragma unroll
           for (int kb = 0; kb < 4; ++kb) o = mfma(vop[kb], pfrag[(qt * 4 + kb) * 64 + lane], o);
           const float den = rs[qi] + rs[64 + qi] + qz[qi] + qz[64 + qi] + qz[128 + qi] + qz[192 + qi];
@@ -229,12 +229,8 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
 #pragma unroll
           for (int r = 0; r < 16; ++r) S[i][ft][r] *= r_n;
 #pragma unroll
-          for (int kb = 0; kb < 4; ++kb) {
-            const f32x4 klo = *reinterpret_cast<const f32x4*>(ks + 16 * kb + 4 * h);
-            const f32x4 khi = *reinterpret_cast<const f32x4*>(ks + 16 * kb + 8 + 4 * h);
-            const bf16x8 a = scale8v(tr_operand(fk_l, PF, 16 * kb, ft * 32, lane), klo, khi);
-            S[i][ft] = mfma(a, vop[kb], S[i][ft]);
-          }
+          for (int kb = 0; kb < 4; ++kb)
+            S[i][ft] = mfma(tr_operand(fk_l, PF, 16 * kb, ft * 32, lane), vop[kb], S[i][ft]);
         }
       }
     }
@@ -246,12 +242,7 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
       store_chunk<DP>(rv, v_l, PD);
       if (wave == 0) gate_scan(rg, lane, lgs, qs, ks, rdec);
     }
-    if (tid < FP) {
-      float za = zs[tid] * r_n;
-#pragma unroll
-      for (int p = 0; p < Cfg::ZPARTS; ++p) za += zp[p * FP + tid];
-      zs[tid] = za;
-    }
+    if (tid < FP) zs[tid] = zs[tid] * r_n + sum_parts<FP>(zp, tid);
     __syncthreads();
   }
 }

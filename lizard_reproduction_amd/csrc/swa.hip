@@ -320,7 +320,8 @@ template <int DP, typename OutT>
 __global__ __launch_bounds__(256) void swa_bwd_dkv_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ lse, const float* __restrict__ delta_in,
-    const bf16* __restrict__ dy, OutT* __restrict__ dk, OutT* __restrict__ dv, int BH, int L,
+    const bf16* __restrict__ dy, OutT* __restrict__ dk, OutT* __restrict__ dv,
+    const float* __restrict__ dmeta_part, float* __restrict__ dmeta, int n_meta, int BH, int L,
     int d, int W, float scale, int per) {
   using Cfg = SwaCfg<DP>;
   constexpr int P = Cfg::P;
@@ -333,6 +334,25 @@ __global__ __launch_bounds__(256) void swa_bwd_dkv_kernel(
   const int nkb = (L + SWA_ROWS - 1) / SWA_ROWS;
   const int lb = xcd_block(blockIdx.x, per);
   if (lb >= BH * nkb) return;
+  if (lb == 0 && n_meta > 0) {
+    // dmeta from the query-side blocks' partials (that launch has completed):
+    // thread (group g, sink j) sums partial rows g, g + groups, ...; thread j
+    // then sums the groups, in a fixed order
+    float* sh = reinterpret_cast<float*>(smem);
+    const int rows = BH * nkb, groups = 256 / n_meta;
+    const int j = threadIdx.x % n_meta, grp = threadIdx.x / n_meta;
+    float acc = 0.f;
+    if (grp < groups)
+      for (int r = grp; r < rows; r += groups) acc += dmeta_part[(size_t)r * n_meta + j];
+    sh[threadIdx.x] = acc;
+    __syncthreads();
+    if ((int)threadIdx.x < n_meta) {
+      float t = 0.f;
+      for (int g = 0; g < groups; ++g) t += sh[g * n_meta + threadIdx.x];
+      dmeta[threadIdx.x] = t;
+    }
+    __syncthreads();
+  }
   const int bh = lb / nkb, K0 = (lb % nkb) * SWA_ROWS;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int col = lane & 31, h = lane >> 5;
@@ -462,8 +482,9 @@ static hipError_t launch_swa_fwd_t(const void* q, const void* k, const void* v, 
 template <int DP, typename OutT>
 static hipError_t launch_swa_bwd_t(const void* q, const void* k, const void* v, const float* meta,
                                    int n_meta, const float* lse, const void* dy, void* dq,
-                                   void* dk, void* dv, float* delta, float* dmeta_part, int BH,
-                                   int L, int d, int W, float scale, hipStream_t st) {
+                                   void* dk, void* dv, float* delta, float* dmeta_part,
+                                   float* dmeta, int BH, int L, int d, int W, float scale,
+                                   hipStream_t st) {
   int per, grid;
   swa_grid(BH, L, &per, &grid);
   const size_t lds_q = 2 * SwaCfg<DP>::TILE_BYTES + 4 * SWA_MAX_META * sizeof(float);
@@ -479,7 +500,7 @@ static hipError_t launch_swa_bwd_t(const void* q, const void* k, const void* v, 
   if ((e = ensure_lds<swa_bwd_dkv_kernel<DP, OutT>>((int)lds_k)) != hipSuccess) return e;
   hipLaunchKernelGGL(kk, dim3(grid), dim3(256), lds_k, st, (const bf16*)q, (const bf16*)k,
                      (const bf16*)v, lse, (const float*)delta, (const bf16*)dy, (OutT*)dk,
-                     (OutT*)dv, BH, L, d, W, scale, per);
+                     (OutT*)dv, (const float*)dmeta_part, dmeta, n_meta, BH, L, d, W, scale, per);
   return hipGetLastError();
 }
 
@@ -497,13 +518,16 @@ hipError_t launch_swa_fwd(const void* q, const void* k, const void* v, const flo
 
 hipError_t launch_swa_bwd(const void* q, const void* k, const void* v, const float* meta,
                           int n_meta, const float* lse, const void* dy, void* dq, void* dk,
-                          void* dv, bool grad_bf16, float* delta, float* dmeta_part, int BH,
-                          int L, int d, int W, float scale, hipStream_t st) {
-#define LZ_SWA_BWD(DPV)                                                                        \
-  return grad_bf16 ? launch_swa_bwd_t<DPV, bf16>(q, k, v, meta, n_meta, lse, dy, dq, dk, dv,   \
-                                                 delta, dmeta_part, BH, L, d, W, scale, st)    \
-                   : launch_swa_bwd_t<DPV, float>(q, k, v, meta, n_meta, lse, dy, dq, dk, dv,  \
-                                                  delta, dmeta_part, BH, L, d, W, scale, st)
+                          void* dv, bool grad_bf16, float* delta, float* dmeta_part,
+                          float* dmeta, int BH, int L, int d, int W, float scale,
+                          hipStream_t st) {
+#define LZ_SWA_BWD(DPV)                                                                         \
+  return grad_bf16 ? launch_swa_bwd_t<DPV, bf16>(q, k, v, meta, n_meta, lse, dy, dq, dk, dv,    \
+                                                 delta, dmeta_part, dmeta, BH, L, d, W, scale,  \
+                                                 st)                                            \
+                   : launch_swa_bwd_t<DPV, float>(q, k, v, meta, n_meta, lse, dy, dq, dk, dv,   \
+                                                  delta, dmeta_part, dmeta, BH, L, d, W, scale, \
+                                                  st)
   switch (swa_padded_dim(d)) {
     case 32: LZ_SWA_BWD(32);
     case 64: LZ_SWA_BWD(64);

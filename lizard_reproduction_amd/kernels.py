@@ -16,6 +16,7 @@ kernels always use their own tiles (64-token GLA chunks, 32-row SWA tiles).
 Every call goes through the C ABI of ``liblizard_hip.so`` on the current HIP
 stream; there is no CPU or PyTorch fallback.
 """
+import functools
 import math
 
 import torch
@@ -38,6 +39,21 @@ def _stream(t):
 
 def _ptr(t):
     return t.data_ptr() if t is not None and t.numel() else None
+
+
+@functools.lru_cache(maxsize=256)
+def _gla_fwd_ws(b, h, length, nf, nd, per_head, chunk):
+    return _lib.load().lz_gla_fwd_workspace_bytes(b, h, length, nf, nd, per_head, chunk)
+
+
+@functools.lru_cache(maxsize=256)
+def _gla_bwd_ws(b, h, length, nf, nd, per_head, chunk):
+    return _lib.load().lz_gla_bwd_workspace_bytes(b, h, length, nf, nd, per_head, chunk)
+
+
+@functools.lru_cache(maxsize=256)
+def _swa_bwd_ws(b, h, length, d, n_meta):
+    return _lib.load().lz_swa_bwd_workspace_bytes(b, h, length, d, n_meta)
 
 
 def _require_gpu(*tensors):
@@ -86,7 +102,7 @@ class _GLA(torch.autograd.Function):
         if y.numel():
             lib = _lib.load()
             per_head = int(lg.dim() == 3)
-            nbytes = lib.lz_gla_fwd_workspace_bytes(b, h, length, nf, nd, per_head, chunk)
+            nbytes = _gla_fwd_ws(b, h, length, nf, nd, per_head, chunk)
             ws = torch.empty(nbytes, dtype=torch.uint8, device=fq.device) if nbytes else None
             rc = lib.lz_gla_fwd(_ptr(fq), _ptr(fk), _ptr(v), _ptr(lg), _ptr(y), b, h, length,
                                 nf, nd, per_head, chunk, _ptr(ws), nbytes, _stream(fq))
@@ -114,7 +130,7 @@ class _GLA(torch.autograd.Function):
         if dy.numel():
             lib = _lib.load()
             per_head = int(lg.dim() == 3)
-            nbytes = lib.lz_gla_bwd_workspace_bytes(b, h, length, nf, nd, per_head, ctx.chunk)
+            nbytes = _gla_bwd_ws(b, h, length, nf, nd, per_head, ctx.chunk)
             ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=fq.device)
             fws = ctx.fwd_ws
             rc = lib.lz_gla_bwd(_ptr(fq), _ptr(fk), _ptr(v), _ptr(lg), _ptr(dy), _ptr(dfq),
@@ -195,7 +211,7 @@ class _SWA(torch.autograd.Function):
         if dy.numel():
             lib = _lib.load()
             n_meta = meta.numel()
-            nbytes = lib.lz_swa_bwd_workspace_bytes(b, h, length, d, n_meta)
+            nbytes = _swa_bwd_ws(b, h, length, d, n_meta)
             ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
             rc = lib.lz_swa_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(meta), n_meta,
                                 _ptr(lse), _ptr(dy), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dmeta),

@@ -262,8 +262,10 @@ def gla_chunked(fq, fk, v, log_gamma, chunk=64, round_bf16=False, dtype=torch.fl
     The reference measures the same differences from a global cumsum
     (start = G[nC-1], end = G[last]); here they are chunk-local sums, which is
     what the HIP kernels do.  With ``round_bf16`` the kernel's bf16 MFMA
-    operands (Q~, K~, a and the state used by Q~ S) are rounded as the kernel
-    rounds them.  log_gamma: [B, L] or [B, H, L].  Returns [B, H, L, D].
+    operands (K~, a and the state used by Q~ S) are rounded as the kernel
+    rounds them; Q~ stays unrounded, as in the kernel, which applies the row
+    scale exp(lg_i) to the fp32 products fq . S and fq . z.
+    log_gamma: [B, L] or [B, H, L].  Returns [B, H, L, D].
     """
     batch, heads, length, nf = fq.shape
     nd = v.shape[-1]
@@ -280,7 +282,7 @@ def gla_chunked(fq, fk, v, log_gamma, chunk=64, round_bf16=False, dtype=torch.fl
         lg = torch.cumsum(lgam[..., c0:c1], dim=-1)           # [B,H,c]
         lg_end = lg[..., -1:]
         q, k, vv = fq[:, :, c0:c1], fk[:, :, c0:c1], v[:, :, c0:c1]
-        qt = rnd(q * torch.exp(lg)[..., None])
+        qt = q * torch.exp(lg)[..., None]
         kt = rnd(k * torch.exp(lg_end - lg)[..., None])
         n = c1 - c0
         causal = torch.ones(n, n, dtype=torch.bool).tril()
