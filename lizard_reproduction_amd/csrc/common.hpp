@@ -133,6 +133,13 @@ hipError_t ensure_lds(int bytes) {
   return status;
 }
 
+// Row pitch (elements) of a row-major bf16 LDS tile with x columns.  Rows are
+// read as 16-byte MFMA operands (8 lanes per LDS cycle) and, by the transpose
+// reads, as 4 rows x 32 bytes per 16-lane group; a pitch of 36 or 72 dwords
+// (mod 64 banks) keeps both conflict-free.  x + 8 gives 36 for x = 64,
+// x + 16 gives 72 for x = 128 (8 for x = 256, 24 for x = 32).
+__host__ __device__ constexpr int lds_pitch(int x) { return x + (x == 64 ? 8 : 16); }
+
 // Exchange with the other half of the wave (lane ^ 32).
 __device__ __forceinline__ float xhalf(float x) { return __shfl_xor(x, 32); }
 

@@ -10,9 +10,9 @@
 //   dA_it   = [t<=i] (dy_i . v_t - delta_i) / den_i,  dad = dA * decay
 //   dfq_i   = sum_t dad_it fk_t + (qs_i/den_i) (dy_i S_n^T - delta_i z_n)
 //   dfk_t   = sum_i dad_it fq_i + ks_t (v_t dS^T - dz)
-//   dv_t    = sum_i (a_it/den_i) dy_i + K~_t dS
-//   dS <- r_n dS + Q^_n^T dY_n,  Q^_i = bf16(fq_i qs_i / den_i)   (after chunk n)
-//   dz <- r_n dz + sum_i Q^_i delta_i
+//   dv_t    = sum_i (a_it/den_i) dy_i + ks_t (fk_t dS)
+//   dS <- r_n dS + fq_n^T dY^_n,  dY^_i = bf16(dy_i qs_i / den_i)   (after chunk n)
+//   dz <- r_n dz + sum_i fq_i (qs_i delta_i / den_i)
 //   dG_j    = fq_j . dfq_j - fk_j . dfk_j,  d log_gamma = reverse cumsum of dG
 //             (summed over heads for a per-token gate)
 //
@@ -42,7 +42,7 @@ namespace lz {
 template <int FP, int DP>
 struct BwdCommon {
   static constexpr int C = GLA_C;
-  static constexpr int PF = FP + 16, PD = DP + 16;
+  static constexpr int PF = lds_pitch(FP), PD = lds_pitch(DP);
   static constexpr int NFT = FP / 32, NDT = DP / 32;
   static constexpr int ZPARTS = FP >= 256 ? 1 : 256 / FP;
   static constexpr int NLF = C * FP / 8 / 256, NLD = C * DP / 8 / 256;
@@ -60,7 +60,8 @@ struct BwdA : BwdCommon<FP, DP> {
   static constexpr int OFF_FK = OFF_FQ + C * PF * 2;
   static constexpr int OFF_V = OFF_FK + C * PF * 2;
   static constexpr int OFF_DY = OFF_V + C * PD * 2;
-  static constexpr int OFF_FR = OFF_DY + C * PD * 2;       // dad fragments [2 qt][4 kb][64]
+  static constexpr int OFF_KT = OFF_DY + C * PD * 2;       // K~ = bf16(fk ks), row-major
+  static constexpr int OFF_FR = OFF_KT + C * PF * 2;       // dad fragments [2 qt][4 kb][64]
   static constexpr int OFF_RA = OFF_FR + 2 * 4 * 64 * 16;  // [2][64] sum_t a
   static constexpr int OFF_RAV = OFF_RA + 2 * 64 * 4;      // [2][64] sum_t a (v . dy)
   static constexpr int OFF_QZ = OFF_RAV + 2 * 64 * 4;      // [4][64] Q~ . z partials
@@ -72,8 +73,8 @@ struct BwdA : BwdCommon<FP, DP> {
   static constexpr int OFF_QS = OFF_LG + 64 * 4;
   static constexpr int OFF_KS = OFF_QS + 64 * 4;
   static constexpr int OFF_Z = OFF_KS + 64 * 4;
-  static constexpr int OFF_ZP = OFF_Z + FP * 4;
-  static constexpr int OFF_R = OFF_ZP + ZPARTS * FP * 4;
+  static constexpr int OFF_ZP = OFF_Z + FP * 4;            // 2048 partial sums of K~
+  static constexpr int OFF_R = OFF_ZP + 2048 * 4;
   static constexpr int BYTES = OFF_R + 16;
   static constexpr int LB = (FP >= 256 || FP + DP >= 160) ? 1 : 2;
   // chunks prefetched ahead (1 or 2; two measured slower at the bench shapes)
@@ -97,6 +98,7 @@ __global__ __launch_bounds__(256, (BwdA<FP, DP>::LB)) void gla_bwd_dq_kernel(
   bf16* fk_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_FK);
   bf16* v_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_V);
   bf16* dy_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_DY);
+  bf16* kt_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_KT);
   bf16x8* fr = reinterpret_cast<bf16x8*>(smem + Cfg::OFF_FR);
   float* ra = reinterpret_cast<float*>(smem + Cfg::OFF_RA);
   float* rav = reinterpret_cast<float*>(smem + Cfg::OFF_RAV);
@@ -183,13 +185,14 @@ __global__ __launch_bounds__(256, (BwdA<FP, DP>::LB)) void gla_bwd_dq_kernel(
       vdy = mfma(row_operand(v_l, PD, kt * 32 + col, 16 * kb, h),
                  row_operand(dy_l, PD, qi, 16 * kb, h), vdy);
     const float lgq = lgs[qi];
+    float dec[16];   // causal decay of this wave's score tile, reused in phase 2
     {
       float sa = 0.f, sav = 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int key = kt * 32 + acc_row(r, h);
-        const float dec = key <= qi ? fexp(lgq - lgs[key]) : 0.f;
-        aT[r] = to_f32(to_bf16(aT[r] * dec));   // a exactly as the forward rounds it
+        dec[r] = key <= qi ? fexp(lgq - lgs[key]) : 0.f;
+        aT[r] = to_f32(to_bf16(aT[r] * dec[r]));   // a exactly as the forward rounds it
         sa += aT[r];
         sav += aT[r] * vdy[r];
       }
@@ -208,15 +211,11 @@ __global__ __launch_bounds__(256, (BwdA<FP, DP>::LB)) void gla_bwd_dq_kernel(
         for (int e = 0; e < 8; ++e) acc += to_f32(x[e]) * zs[wave * FQ + c + e];
       }
       qz[wave * 64 + lane] = acc * qs[lane];
-      constexpr int TPP = C / Cfg::ZPARTS;
-      const int f = tid % FP, part = tid / FP;
-      if (part < Cfg::ZPARTS) {
-        float za = 0.f;
-#pragma unroll 8
-        for (int t = part * TPP; t < (part + 1) * TPP; ++t)
-          za += to_f32(to_bf16(to_f32(fk_l[t * PF + f]) * ks[t]));
-        zp[part * FP + f] = za;
-      }
+      // K~ = bf16(fk ks) once per chunk (the forward's rounding), with its
+      // column sums for z
+      uint4 kti[RowItems<FP>::N];
+      scale_rows<FP>(fk_l, PF, ks, kti, zp);
+      store_rows<FP>(kti, kt_l, PF);
     }
     f32x16 X[NFW][NQW];
     if (active) {
@@ -255,11 +254,7 @@ __global__ __launch_bounds__(256, (BwdA<FP, DP>::LB)) void gla_bwd_dq_kernel(
       const float inv = 1.f / dcl;
       bf16x8 d8[2];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = kt * 32 + acc_row(r, h);
-        const float dec = key <= qi ? fexp(lgq - lgs[key]) : 0.f;
-        d8[r >> 3][r & 7] = to_bf16((vdy[r] - delta) * inv * dec);
-      }
+      for (int r = 0; r < 16; ++r) d8[r >> 3][r & 7] = to_bf16((vdy[r] - delta) * inv * dec[r]);
       fr[(qt * 4 + kt * 2 + 0) * 64 + lane] = d8[0];
       fr[(qt * 4 + kt * 2 + 1) * 64 + lane] = d8[1];
       if (kt == 0 && h == 0) {
@@ -278,7 +273,7 @@ __global__ __launch_bounds__(256, (BwdA<FP, DP>::LB)) void gla_bwd_dq_kernel(
 #pragma unroll
       for (int i = 0; i < NFW; ++i) {
         const int ft = RF::tile(wave, i);
-        bf16x8 fkr[4];   // fk^T rows of this f-tile (A of fk^T dad^T); scaled by ks it is K~
+        bf16x8 fkr[4];   // fk^T rows of this f-tile (A of fk^T dad^T)
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) fkr[kb] = tr_operand(fk_l, PF, 16 * kb, ft * 32, lane);
 #pragma unroll
@@ -314,11 +309,7 @@ __global__ __launch_bounds__(256, (BwdA<FP, DP>::LB)) void gla_bwd_dq_kernel(
         }
         // S^T[:, ft] <- r S^T + V^T K~
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-          const f32x4 klo = *reinterpret_cast<const f32x4*>(ks + 16 * kb + 4 * h);
-          const f32x4 khi = *reinterpret_cast<const f32x4*>(ks + 16 * kb + 8 + 4 * h);
-          fkr[kb] = scale8v(fkr[kb], klo, khi);
-        }
+        for (int kb = 0; kb < 4; ++kb) fkr[kb] = tr_operand(kt_l, PF, 16 * kb, ft * 32, lane);
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) {
 #pragma unroll
@@ -338,12 +329,7 @@ __global__ __launch_bounds__(256, (BwdA<FP, DP>::LB)) void gla_bwd_dq_kernel(
       p_out[offL + t0 + tid] = s;
     }
     if (n + 1 < n1) stage(std::integral_constant<int, (S + 1) % DEPTH>{});
-    if (tid < FP) {
-      float za = zs[tid] * r_n;
-#pragma unroll
-      for (int p = 0; p < Cfg::ZPARTS; ++p) za += zp[p * FP + tid];
-      zs[tid] = za;
-    }
+    if (tid < FP) zs[tid] = zs[tid] * r_n + sum_parts<FP>(zp, tid);
     __syncthreads();
   };
   for (int n = n0; n < n1; n += DEPTH) {
@@ -359,13 +345,31 @@ __global__ __launch_bounds__(256, (BwdA<FP, DP>::LB)) void gla_bwd_dq_kernel(
 // ============================================================================
 __device__ __forceinline__ void bwd_scalars(float g, float den, float delta, float p, int lane,
                                             float* lgs, float* qs, float* ks, float* r,
-                                            float* dens, float* dels, float* ps, float* qh) {
+                                            float* invd, float* dels, float* ps, float* qh,
+                                            float* dw) {
   gate_scan(g, lane, lgs, qs, ks, r);
-  const float dcl = fmaxf(den, TINY);
-  dens[lane] = dcl;
+  const float inv = 1.f / fmaxf(den, TINY);
+  const float qhv = qs[lane] * inv;   // Q^_i = fq_i qs_i / den_i
+  invd[lane] = inv;
   dels[lane] = delta;
   if (ps) ps[lane] = p;
-  qh[lane] = qs[lane] / dcl;
+  qh[lane] = qhv;
+  dw[lane] = qhv * delta;             // dz = sum_i fq_i (qs_i delta_i / den_i)
+}
+
+// bf16(x[t][c] * scale[t]) for a [64 x KP] row-major tile, as 16-byte items
+// (the item layout of scale_rows), without column sums
+template <int KP>
+__device__ __forceinline__ void scale_rows_only(const bf16* tile, int pitch, const float* scale,
+                                                uint4 (&out)[RowItems<KP>::N]) {
+  using R = RowItems<KP>;
+  const int cg = threadIdx.x % R::K8, r0 = threadIdx.x / R::K8;
+#pragma unroll
+  for (int i = 0; i < R::N; ++i) {
+    const int t = r0 + R::RSTRIDE * i;
+    const bf16x8 x = *reinterpret_cast<const bf16x8*>(tile + t * pitch + 8 * cg);
+    out[i] = __builtin_bit_cast(uint4, scale8(x, scale[t]));
+  }
 }
 
 struct TokScalars {
@@ -396,13 +400,15 @@ struct BwdS : BwdCommon<FP, DP> {
   static constexpr int C = B_::C, PF = B_::PF, PD = B_::PD, ZPARTS = B_::ZPARTS;
   static constexpr int OFF_FQ = 0;
   static constexpr int OFF_DY = OFF_FQ + C * PF * 2;
-  static constexpr int OFF_LG = OFF_DY + C * PD * 2;
+  static constexpr int OFF_DYH = OFF_DY + C * PD * 2;     // dY^ = bf16(qh dy)
+  static constexpr int OFF_LG = OFF_DYH + C * PD * 2;
   static constexpr int OFF_QS = OFF_LG + 64 * 4;
   static constexpr int OFF_KS = OFF_QS + 64 * 4;
-  static constexpr int OFF_DEN = OFF_KS + 64 * 4;
-  static constexpr int OFF_DEL = OFF_DEN + 64 * 4;
+  static constexpr int OFF_INV = OFF_KS + 64 * 4;
+  static constexpr int OFF_DEL = OFF_INV + 64 * 4;
   static constexpr int OFF_QH = OFF_DEL + 64 * 4;
-  static constexpr int OFF_DZ = OFF_QH + 64 * 4;
+  static constexpr int OFF_DW = OFF_QH + 64 * 4;
+  static constexpr int OFF_DZ = OFF_DW + 64 * 4;
   static constexpr int OFF_DZP = OFF_DZ + FP * 4;
   static constexpr int OFF_R = OFF_DZP + ZPARTS * FP * 4;
   static constexpr int BYTES = OFF_R + 16;
@@ -420,12 +426,14 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_bwd_state_kernel(
   extern __shared__ __align__(16) char smem[];
   bf16* fq_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_FQ);
   bf16* dy_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_DY);
+  bf16* dyh_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_DYH);
   float* lgs = reinterpret_cast<float*>(smem + Cfg::OFF_LG);
   float* qs = reinterpret_cast<float*>(smem + Cfg::OFF_QS);
   float* ks = reinterpret_cast<float*>(smem + Cfg::OFF_KS);
-  float* dens = reinterpret_cast<float*>(smem + Cfg::OFF_DEN);
+  float* invd = reinterpret_cast<float*>(smem + Cfg::OFF_INV);
   float* dels = reinterpret_cast<float*>(smem + Cfg::OFF_DEL);
   float* qh = reinterpret_cast<float*>(smem + Cfg::OFF_QH);
+  float* dw = reinterpret_cast<float*>(smem + Cfg::OFF_DW);
   float* dzs = reinterpret_cast<float*>(smem + Cfg::OFF_DZ);
   float* dzp = reinterpret_cast<float*>(smem + Cfg::OFF_DZP);
   float* rdec = reinterpret_cast<float*>(smem + Cfg::OFF_R);
@@ -445,7 +453,7 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_bwd_state_kernel(
   for (int f = tid; f < FP; f += 256) dzs[f] = 0.f;
   float lam = 0.f;
 
-  uint4 rq[Cfg::NLF], rd[Cfg::NLD];
+  uint4 rq[Cfg::NLF], rd[Cfg::NLD], rh[RowItems<DP>::N];
   TokScalars sc;
   load_chunk<FP>(rq, fq + offF, (n1 - 1) * C, L, F, vecF);
   load_chunk<DP>(rd, dy + offD, (n1 - 1) * C, L, D, vecD);
@@ -453,7 +461,7 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_bwd_state_kernel(
   store_chunk<FP>(rq, fq_l, PF);
   store_chunk<DP>(rd, dy_l, PD);
   if (wave == 0)
-    bwd_scalars(sc.g, sc.den, sc.delta, 0.f, lane, lgs, qs, ks, rdec, dens, dels, nullptr, qh);
+    bwd_scalars(sc.g, sc.den, sc.delta, 0.f, lane, lgs, qs, ks, rdec, invd, dels, nullptr, qh, dw);
   __syncthreads();
 
   for (int n = n1 - 1; n >= n0; --n) {
@@ -463,6 +471,20 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_bwd_state_kernel(
       load_chunk<DP>(rd, dy + offD, (n - 1) * C, L, D, vecD);
       sc = load_scalars(lgb, den_in, delta_in, nullptr, offL, (n - 1) * C + lane, L);
     }
+    // dY^ = bf16(qh dy), formed once per chunk; dz partials sum_i fq_i (qh_i delta_i)
+    scale_rows_only<DP>(dy_l, PD, qh, rh);
+    store_rows<DP>(rh, dyh_l, PD);
+    {
+      constexpr int TPP = C / Cfg::ZPARTS;
+      const int f = tid % FP, part = tid / FP;
+      if (part < Cfg::ZPARTS) {
+        float za = 0.f;
+#pragma unroll 8
+        for (int t = part * TPP; t < (part + 1) * TPP; ++t) za += to_f32(fq_l[t * PF + f]) * dw[t];
+        dzp[part * FP + f] = za;
+      }
+    }
+    __syncthreads();
     const float r_n = rdec[0];
     if (wave == 0) lam += rdec[1];
 #pragma unroll
@@ -473,23 +495,9 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_bwd_state_kernel(
 #pragma unroll
         for (int r = 0; r < 16; ++r) dS[i][r] *= r_n;
 #pragma unroll
-        for (int qb = 0; qb < 4; ++qb) {
-          const f32x4 qlo = *reinterpret_cast<const f32x4*>(qh + 16 * qb + 4 * h);
-          const f32x4 qhi = *reinterpret_cast<const f32x4*>(qh + 16 * qb + 8 + 4 * h);
-          dS[i] = mfma(scale8v(tr_operand(fq_l, PF, 16 * qb, ft * 32, lane), qlo, qhi),
-                       tr_operand(dy_l, PD, 16 * qb, dt * 32, lane), dS[i]);
-        }
-      }
-    }
-    {
-      constexpr int TPP = C / Cfg::ZPARTS;
-      const int f = tid % FP, part = tid / FP;
-      if (part < Cfg::ZPARTS) {
-        float za = 0.f;
-#pragma unroll 8
-        for (int t = part * TPP; t < (part + 1) * TPP; ++t)
-          za += to_f32(to_bf16(to_f32(fq_l[t * PF + f]) * qh[t])) * dels[t];
-        dzp[part * FP + f] = za;
+        for (int qb = 0; qb < 4; ++qb)   // dS += fq^T dY^
+          dS[i] = mfma(tr_operand(fq_l, PF, 16 * qb, ft * 32, lane),
+                       tr_operand(dyh_l, PD, 16 * qb, dt * 32, lane), dS[i]);
       }
     }
     __syncthreads();
@@ -497,7 +505,8 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_bwd_state_kernel(
       store_chunk<FP>(rq, fq_l, PF);
       store_chunk<DP>(rd, dy_l, PD);
       if (wave == 0)
-        bwd_scalars(sc.g, sc.den, sc.delta, 0.f, lane, lgs, qs, ks, rdec, dens, dels, nullptr, qh);
+        bwd_scalars(sc.g, sc.den, sc.delta, 0.f, lane, lgs, qs, ks, rdec, invd, dels, nullptr, qh,
+                    dw);
     }
     if (tid < FP) {
       float za = dzs[tid] * r_n;
@@ -532,15 +541,17 @@ struct BwdB : BwdCommon<FP, DP> {
   static constexpr int OFF_FK = OFF_FQ + C * PF * 2;
   static constexpr int OFF_V = OFF_FK + C * PF * 2;
   static constexpr int OFF_DY = OFF_V + C * PD * 2;
-  static constexpr int OFF_DST = OFF_DY + C * PD * 2;     // dS^T [DP][PF] bf16
+  static constexpr int OFF_DYH = OFF_DY + C * PD * 2;     // dY^ = bf16(qh dy)
+  static constexpr int OFF_DST = OFF_DYH + C * PD * 2;    // dS^T [DP][PF] bf16
   static constexpr int OFF_FA = OFF_DST + DP * PF * 2;    // a/den fragments [2 kt][4 qb][64]
   static constexpr int OFF_FD = OFF_FA + 2 * 4 * 64 * 16; // dad fragments
   static constexpr int OFF_PK = OFF_FD + 2 * 4 * 64 * 16; // [NFT][64] fk . dfk partials
-  static constexpr int OFF_DEN = OFF_PK + NFT * 64 * 4;   // [2][64] (by chunk parity)
-  static constexpr int OFF_DEL = OFF_DEN + 2 * 64 * 4;
+  static constexpr int OFF_INV = OFF_PK + NFT * 64 * 4;   // per-token scalars, [2][64] by parity
+  static constexpr int OFF_DEL = OFF_INV + 2 * 64 * 4;
   static constexpr int OFF_P = OFF_DEL + 2 * 64 * 4;
   static constexpr int OFF_QH = OFF_P + 2 * 64 * 4;
-  static constexpr int OFF_LG = OFF_QH + 2 * 64 * 4;
+  static constexpr int OFF_DW = OFF_QH + 2 * 64 * 4;
+  static constexpr int OFF_LG = OFF_DW + 2 * 64 * 4;
   static constexpr int OFF_QS = OFF_LG + 64 * 4;
   static constexpr int OFF_KS = OFF_QS + 64 * 4;
   static constexpr int OFF_DZ = OFF_KS + 64 * 4;
@@ -569,14 +580,16 @@ __global__ __launch_bounds__(256, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_kernel(
   bf16* fk_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_FK);
   bf16* v_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_V);
   bf16* dy_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_DY);
+  bf16* dyh_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_DYH);
   bf16* dst_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_DST);
   bf16x8* fa = reinterpret_cast<bf16x8*>(smem + Cfg::OFF_FA);
   bf16x8* fd = reinterpret_cast<bf16x8*>(smem + Cfg::OFF_FD);
   float* pk = reinterpret_cast<float*>(smem + Cfg::OFF_PK);
-  float* dens = reinterpret_cast<float*>(smem + Cfg::OFF_DEN);
+  float* invd = reinterpret_cast<float*>(smem + Cfg::OFF_INV);
   float* dels = reinterpret_cast<float*>(smem + Cfg::OFF_DEL);
   float* ps = reinterpret_cast<float*>(smem + Cfg::OFF_P);
   float* qh = reinterpret_cast<float*>(smem + Cfg::OFF_QH);
+  float* dw = reinterpret_cast<float*>(smem + Cfg::OFF_DW);
   float* lgs = reinterpret_cast<float*>(smem + Cfg::OFF_LG);
   float* qs = reinterpret_cast<float*>(smem + Cfg::OFF_QS);
   float* ks = reinterpret_cast<float*>(smem + Cfg::OFF_KS);
@@ -652,7 +665,7 @@ __global__ __launch_bounds__(256, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_kernel(
     const int b = n & 1;
     if (wave == 0)
       bwd_scalars(sc[S].g, sc[S].den, sc[S].delta, sc[S].p, lane, lgs, qs, ks, rdec,
-                  dens + 64 * b, dels + 64 * b, ps + 64 * b, qh + 64 * b);
+                  invd + 64 * b, dels + 64 * b, ps + 64 * b, qh + 64 * b, dw + 64 * b);
   };
   issue(SET0, n1 - 1);
   if constexpr (DEPTH == 2) issue(SET1, n1 - 2);
@@ -667,9 +680,10 @@ __global__ __launch_bounds__(256, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_kernel(
     constexpr int S = decltype(set)::value;
     const int t0 = n * C;
     const int cur = n & 1;
-    const float* densc = dens + 64 * cur;
+    const float* invc = invd + 64 * cur;
     const float* delsc = dels + 64 * cur;
     const float* qhc = qh + 64 * cur;
+    const float* dwc = dw + 64 * cur;
     issue(set, n - DEPTH);
     // ---- phase 1: s and (dy v^T) tile (queries x keys) -> a/den, dad; dz sums ----
     {
@@ -689,22 +703,26 @@ __global__ __launch_bounds__(256, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_kernel(
         const int q = qt * 32 + acc_row(r, h);
         const bool c = ki <= q;
         const float dec = c ? fexp(lgs[q] - lgk) : 0.f;
-        const float den = densc[q];
+        const float inv = invc[q];
         const float a = to_f32(to_bf16(s[r] * dec));
-        fa8[r >> 3][r & 7] = to_bf16(a / den);
-        fd8[r >> 3][r & 7] = to_bf16(c ? (dyv[r] - delsc[q]) / den * dec : 0.f);
+        fa8[r >> 3][r & 7] = to_bf16(a * inv);
+        fd8[r >> 3][r & 7] = to_bf16(c ? (dyv[r] - delsc[q]) * inv * dec : 0.f);
       }
       fa[(kt * 4 + qt * 2 + 0) * 64 + lane] = fa8[0];
       fa[(kt * 4 + qt * 2 + 1) * 64 + lane] = fa8[1];
       fd[(kt * 4 + qt * 2 + 0) * 64 + lane] = fd8[0];
       fd[(kt * 4 + qt * 2 + 1) * 64 + lane] = fd8[1];
+      // dY^ = bf16(qh dy) once per chunk, for dS += fq^T dY^ (= Q^^T dY)
+      uint4 rh[RowItems<DP>::N];
+      scale_rows_only<DP>(dy_l, PD, qhc, rh);
+      store_rows<DP>(rh, dyh_l, PD);
+      // dz partials: sum_i fq_i (qh_i delta_i)
       constexpr int TPP = C / Cfg::ZPARTS;
       const int f = tid % FP, part = tid / FP;
       if (part < Cfg::ZPARTS) {
         float za = 0.f;
 #pragma unroll 8
-        for (int t = part * TPP; t < (part + 1) * TPP; ++t)
-          za += to_f32(to_bf16(to_f32(fq_l[t * PF + f]) * qhc[t])) * delsc[t];
+        for (int t = part * TPP; t < (part + 1) * TPP; ++t) za += to_f32(fq_l[t * PF + f]) * dwc[t];
         dzp[part * FP + f] = za;
       }
     }
@@ -715,21 +733,24 @@ __global__ __launch_bounds__(256, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_kernel(
 #pragma unroll
       for (int i = 0; i < RD::TILES; ++i) {
         const int dt = RD::tile(wave, i);
-        bf16x8 dyo[4];   // dY^T rows of this d-tile (A of dY^T (a/den)) == dY columns (B of Q^^T dY)
+        bf16x8 dyo[4];   // dY^T rows of this d-tile (A of dY^T (a/den))
 #pragma unroll
         for (int qb = 0; qb < 4; ++qb) dyo[qb] = tr_operand(dy_l, PD, 16 * qb, dt * 32, lane);
 #pragma unroll
         for (int j = 0; j < RD::HALVES; ++j) {
           const int key = RD::half(wave, j) * 32 + col;
-          const float ksv = ks[key];
+          // dv_t = ks_t (fk_t dS) + sum_i (a_it / den_i) dy_i: the row scale of
+          // K~ = fk ks multiplies the fp32 product
           f32x16 g = zero16();
+#pragma unroll
+          for (int kb = 0; kb < FP / 16; ++kb)
+            g = mfma(acc_operand(dS[i][kb >> 1], kb & 1), row_operand_acc(fk_l, PF, key, 16 * kb, h), g);
+          const float ksv = ks[key];
+#pragma unroll
+          for (int r = 0; r < 16; ++r) g[r] *= ksv;
 #pragma unroll
           for (int qb = 0; qb < 4; ++qb)
             g = mfma(dyo[qb], fa[(RD::half(wave, j) * 4 + qb) * 64 + lane], g);
-#pragma unroll
-          for (int kb = 0; kb < FP / 16; ++kb)
-            g = mfma(acc_operand(dS[i][kb >> 1], kb & 1),
-                     scale8(row_operand_acc(fk_l, PF, key, 16 * kb, h), ksv), g);
           const int tok = t0 + key;
           if (tok < L) {
 #pragma unroll
@@ -739,16 +760,14 @@ __global__ __launch_bounds__(256, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_kernel(
           }
         }
 #pragma unroll
+        for (int qb = 0; qb < 4; ++qb) dyo[qb] = tr_operand(dyh_l, PD, 16 * qb, dt * 32, lane);
+#pragma unroll
         for (int ft = 0; ft < NFT; ++ft) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) dS[i][ft][r] *= r_n;
 #pragma unroll
-          for (int qb = 0; qb < 4; ++qb) {
-            const f32x4 qlo = *reinterpret_cast<const f32x4*>(qhc + 16 * qb + 4 * h);
-            const f32x4 qhi = *reinterpret_cast<const f32x4*>(qhc + 16 * qb + 8 + 4 * h);
-            dS[i][ft] = mfma(scale8v(tr_operand(fq_l, PF, 16 * qb, ft * 32, lane), qlo, qhi),
-                             dyo[qb], dS[i][ft]);
-          }
+          for (int qb = 0; qb < 4; ++qb)
+            dS[i][ft] = mfma(tr_operand(fq_l, PF, 16 * qb, ft * 32, lane), dyo[qb], dS[i][ft]);
         }
       }
     }

@@ -36,7 +36,7 @@ constexpr int SWA_TILE = 64;    // streamed rows per LDS tile
 
 template <int DP>
 struct SwaCfg {
-  static constexpr int P = DP + 16;                      // LDS row pitch (elements)
+  static constexpr int P = lds_pitch(DP);                // LDS row pitch (elements)
   static constexpr int NL = SWA_TILE * DP / 8 / 256;     // 16-byte loads per thread per tile
   static constexpr int TILE_BYTES = SWA_TILE * P * 2;
 };
