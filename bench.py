@@ -20,7 +20,14 @@ reference (src/benchmark.py:57-66):
   * BASELINE config 3, SWA fwd and fwd+bwd (B=1, H=32, L=2048, d=64, W=64,
     4 sink logits, RoPE'd q and k);
   * BASELINE config 4 sweep, GLA fwd and fwd+bwd, B in {1,4,16},
-    L in {2K,4K,8K,16K}, d=128, per-head gate (skip with --no-sweep).
+    L in {2K,4K,8K,16K}, d=128, per-head gate (skip with --no-sweep);
+  * BASELINE config 5, a Llama-3.2-1B-shaped model (hidden 2048, 16 blocks,
+    32 query / 8 kv heads, head_dim 64, intermediate 8192, vocab 128256,
+    RoPE theta 500000, tied embeddings, random-init bf16 weights) with every
+    attention block a LizardAttention (hip backend: feature_dim 128 so F=256,
+    D=64, window 64, 4 sinks, per-token gate), one training step's
+    forward + cross-entropy backward at B=4, L=4096 on uniform random ids;
+    plus one such layer alone (skip with --no-layer).
 
 ``cpu_baseline`` times the dense fp32 PyTorch restatement of the reference's
 torch backend (oracle.lizard_oracle.gla_kernel_api, the math of
@@ -99,6 +106,9 @@ def parse_args():
                    help="target CPU time of the cpu_baseline sample")
     p.add_argument("--headline-only", action="store_true",
                    help="time only the headline step (for profiler runs)")
+    p.add_argument("--no-layer", action="store_true", help="skip the config-5 layer stack")
+    p.add_argument("--layer-only", action="store_true",
+                   help="run only the config-5 layer stack (for profiling)")
     p.add_argument("--copy-calibration", action="store_true",
                    help="also run a plain 1 GiB device copy, the reference kernel that "
                         "scales rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes")
@@ -169,6 +179,71 @@ def fwd_bwd_fn(torch, op, inputs, dy, extra=()):
     return run, reset
 
 
+def layer_stack(torch, steps, warmup):
+    """training step (forward, cross-entropy, backward) of
+    a Llama-3.2-1B-shaped model whose attention blocks are LizardAttention,
+    and of one such layer alone; medians of per-step events."""
+    from transformers import LlamaConfig, LlamaForCausalLM
+    from lizard_reproduction_amd.layer import LizardAttention, to_lizard
+    cfg = LlamaConfig(hidden_size=2048, intermediate_size=8192, num_hidden_layers=16,
+                      num_attention_heads=32, num_key_value_heads=8, head_dim=64,
+                      vocab_size=128256, rope_theta=500000.0, max_position_embeddings=4096,
+                      tie_word_embeddings=True, attn_implementation="eager")
+    batch, length = 4, 4096
+    opts = dict(window=64, num_meta=4, feature_dim=128)
+    out = {"shape": "Llama-3.2-1B shape: hidden 2048, 16 blocks, 32 q / 8 kv heads, "
+                    "head_dim 64, intermediate 8192, vocab 128256, tied embeddings; "
+                    "LizardAttention F=256 D=64 W=64 4 sinks; B=4 L=4096; bf16 random init",
+           "intermediate_size_used": 8192}
+    torch.manual_seed(0)
+    # one layer alone: hidden states in, fwd + bwd with a random upstream grad
+    layer = LizardAttention(cfg, 0, **opts).to("cuda", torch.bfloat16)
+    with torch.no_grad():
+        for p in (layer.W_gamma.weight, layer.meta_tokens):
+            p.normal_(0, 0.02)
+    from transformers.models.llama.modeling_llama import LlamaRotaryEmbedding
+    rotary = LlamaRotaryEmbedding(cfg).to("cuda")
+    x = torch.randn(batch, length, 2048, device="cuda", dtype=torch.bfloat16)
+    pos = torch.arange(length, device="cuda")[None].expand(batch, length)
+    rope = rotary(x, pos)
+    xg = x.detach().requires_grad_()
+    gy = torch.randn_like(x)
+
+    def layer_step():
+        y = layer(xg, rope)[0]
+        y.backward(gy)
+
+    def layer_reset():
+        xg.grad = None
+        layer.zero_grad(set_to_none=True)
+    with torch.no_grad():
+        out["one_layer_fwd_ms"] = round(median_ms(torch, lambda: layer(xg, rope), 5, 2), 3)
+    out["one_layer_fwd_bwd_ms"] = round(median_ms(torch, layer_step, 5, 2, layer_reset), 3)
+    del layer, xg, gy, rope, rotary
+    torch.cuda.empty_cache()
+    print(f"[bench] config5 one layer: {out}", file=sys.stderr, flush=True)
+
+    model = LlamaForCausalLM(cfg).to(torch.bfloat16)
+    to_lizard(model, **opts)
+    model = model.to("cuda")
+    model.train()
+    ids = torch.randint(0, cfg.vocab_size, (batch, length), device="cuda")
+
+    def step():
+        model(input_ids=ids, labels=ids).loss.backward()
+
+    def reset():
+        model.zero_grad(set_to_none=True)
+    t = median_ms(torch, step, max(1, steps), max(1, warmup), reset)
+    out["model_fwd_bwd_ms"] = round(t, 2)
+    out["tokens_per_s"] = round(batch * length / t * 1e3, 1)
+    out["peak_hbm_gib"] = round(torch.cuda.max_memory_allocated() / 2**30, 1)
+    del model, ids
+    torch.cuda.empty_cache()
+    print(f"[bench] config5 model: {out}", file=sys.stderr, flush=True)
+    return out
+
+
 def cpu_baseline(torch, fq, fk, v, lg, target_s):
     """Dense fp32 torch restatement (the reference's torch backend) on the host
     cores, on whole (b, h) slices of the headline inputs; returns the time
@@ -223,6 +298,9 @@ def main():
         sys.exit(1)
     _lib.load()
     torch.manual_seed(0)
+    if args.layer_only:
+        print(json.dumps({"extra": {"config5_layer_stack": layer_stack(torch, 3, 1)}}), flush=True)
+        return
 
     # ---- headline: GLA forward, B=16 H=32 L=2048 F=D=128, per-head gate -----
     B, H, L, D = 16, 32, 2048, 128
@@ -333,6 +411,10 @@ def main():
                 del fq, fk, v, lg, dy, run, reset
                 torch.cuda.empty_cache()
         extra["config4_sweep"] = sweep
+
+    # ---- config 5: layer stack ------------------------------------------------
+    if not args.no_layer:
+        extra["config5_layer_stack"] = layer_stack(torch, 3, 1)
 
     line = {
         "metric": METRIC, "value": round(ms, 4), "unit": "ms", "n_gpus": 1,

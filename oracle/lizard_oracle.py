@@ -38,6 +38,10 @@ swa_kernel_api      awa; empty meta == meta of -1e4 (tests/test_kernels.py:
 gla_chunked         == dense gla in fp64 for chunk 16/64, L in {1,77,150},
                     per-token and per-head gates, strong decay
 rope                rope_loop; relative-position invariance of q.k
+lizard_layer        lizard_layer_loop (fp64, 1e-10); with the GLA branch
+                    zeroed, no sinks and an unbounded window it equals
+                    transformers' LlamaAttention (a library routine);
+                    causal and batch independent
 ==================  =======================================================
 
 The loops are deliberately independent code paths (explicit Python loops over
@@ -296,3 +300,73 @@ def gla_chunked(fq, fk, v, log_gamma, chunk=64, round_bf16=False, dtype=torch.fl
         state = state * r + torch.matmul(kt.transpose(-1, -2), vv)
         norm = norm * r[..., 0] + kt.sum(-2)
     return out
+
+
+# ---------------------------------------------------------------------------
+# The whole attention layer (src/lizard_attention.py:47-97)
+# ---------------------------------------------------------------------------
+
+def lizard_layer(params, x, cos, sin, heads, kv_heads, window):
+    """Dense ``LizardAttention.forward`` of the reference's torch backend,
+    ``src/lizard_attention.py:73-97``, on a dict of its parameters (names as
+    ``named_parameters()`` gives them).
+
+    x [B, L, hidden]; cos, sin [B, L, head_dim] (transformers' rotary tables,
+    broadcast over heads as ``apply_rotary_pos_emb`` does with unsqueeze_dim
+    1).  Projections run in x's dtype, everything after them in
+    promote(x.dtype, fp32); heads are expanded from the kv heads by
+    repeat_interleave; y = gla(phi_q(q), phi_k(k), v, sigmoid(z)) +
+    alpha * awa(rope(q), rope(k), v, meta, window); out = o_proj(y).
+    """
+    batch, length, hidden = x.shape
+    head_dim = hidden // heads
+    dtype = torch.promote_types(x.dtype, torch.float32)
+
+    def heads_of(name, count):
+        y = torch.matmul(x, params[name].transpose(0, 1)).view(batch, length, count, head_dim)
+        return y.transpose(1, 2).repeat_interleave(heads // count, dim=1).to(dtype)
+
+    q = heads_of("q_proj.weight", heads)
+    k = heads_of("k_proj.weight", kv_heads)
+    v = heads_of("v_proj.weight", kv_heads)
+    z = torch.matmul(x, params["W_gamma.weight"].transpose(0, 1)).to(dtype).squeeze(-1)
+    fq = hedgehog(q, params["phi_q.weight"].to(dtype))
+    fk = hedgehog(k, params["phi_k.weight"].to(dtype))
+    c, s = cos.to(dtype).unsqueeze(1), sin.to(dtype).unsqueeze(1)
+    qr, kr = rope(q, c, s), rope(k, c, s)
+    alpha, meta = params["alpha_blend"].to(dtype), params["meta_tokens"].to(dtype)
+    y = gla(fq, fk, v, torch.sigmoid(z)) + alpha * awa(qr, kr, v, meta, window)
+    y = y.to(x.dtype).transpose(1, 2).reshape(batch, length, hidden)
+    return torch.matmul(y, params["o_proj.weight"].transpose(0, 1))
+
+
+def lizard_layer_loop(params, x, cos, sin, heads, kv_heads, window):
+    """The same layer composed from the closed-form loops (hedgehog_loop,
+    gla_loop, awa_loop, rope_loop), with the kv-head expansion written as an
+    explicit index map (head h reads kv head h // (heads / kv_heads)).  The
+    reference's own ground truth for its layer is this composition
+    (tests/test_lizard.py:72-91).  cos, sin [L, head_dim]."""
+    batch, length, hidden = x.shape
+    head_dim = hidden // heads
+    group = heads // kv_heads
+
+    def project(name, count):
+        w = params[name]
+        out = torch.empty(batch, heads, length, head_dim, dtype=x.dtype)
+        for h in range(heads):
+            src = h if count == heads else h // group
+            rows = w[src * head_dim:(src + 1) * head_dim]
+            out[:, h] = torch.matmul(x, rows.transpose(0, 1))
+        return out
+
+    q, k, v = (project(n, c) for n, c in (("q_proj.weight", heads),
+                                          ("k_proj.weight", kv_heads),
+                                          ("v_proj.weight", kv_heads)))
+    gamma = 1.0 / (1.0 + torch.exp(-torch.matmul(x, params["W_gamma.weight"][0])))
+    fq = hedgehog_loop(q, params["phi_q.weight"])
+    fk = hedgehog_loop(k, params["phi_k.weight"])
+    qr, kr = rope_loop(q, cos, sin), rope_loop(k, cos, sin)
+    y = gla_loop(fq, fk, v, gamma) + params["alpha_blend"] * awa_loop(
+        qr, kr, v, params["meta_tokens"], window)
+    y = y.transpose(1, 2).reshape(batch, length, hidden)
+    return torch.matmul(y, params["o_proj.weight"].transpose(0, 1))

@@ -1,0 +1,142 @@
+"""Whole-layer parity of the HIP LizardAttention against the oracle's dense
+layer, output and every parameter gradient (the reference's
+tests/test_kernels.py:137-156), and of a small Llama with every attention
+block swapped."""
+import pytest
+import torch
+import torch.nn as nn
+from transformers import LlamaForCausalLM
+
+from lizard_reproduction_amd import layer as hip_layer
+from oracle import lizard_oracle as lo
+from tests.helpers import GRAD_TOL, OUT_TOL, max_rel, norm_rel, ref_close
+from tests.test_layer import tiny_config, tiny_rope
+
+pytestmark = pytest.mark.gpu
+
+
+def random_layer(dtype, seed=0, window=16, feature_dim=8):
+    torch.manual_seed(seed)
+    layer = hip_layer.LizardAttention(tiny_config(), 0, window=window, feature_dim=feature_dim)
+    with torch.no_grad():
+        for p in layer.parameters():
+            p.normal_(0, 0.3)
+    return layer.to(dtype)
+
+
+class OracleAttention(nn.Module):
+    """The oracle's dense layer behind the layer's module interface, with
+    its own copies of a LizardAttention's parameters (CPU)."""
+
+    def __init__(self, layer):
+        super().__init__()
+        self.heads, self.kv_heads, self.window = layer.heads, layer.kv_heads, layer.window
+        self.params = nn.ParameterDict({n.replace(".", "__"): nn.Parameter(p.detach().cpu().clone())
+                                        for n, p in layer.named_parameters()})
+
+    def forward(self, hidden_states, position_embeddings, **kwargs):
+        params = {n.replace("__", "."): p for n, p in self.params.items()}
+        cos, sin = position_embeddings
+        return lo.lizard_layer(params, hidden_states, cos, sin, self.heads, self.kv_heads,
+                               self.window), None
+
+
+def report(label, pairs):
+    for k, (a, b) in pairs.items():
+        assert a is not None and b is not None, k
+    out = {k: max_rel(a, b) for k, (a, b) in pairs.items()}
+    print(f"[parity] {label}: " + " ".join(f"{k}={v:.2e}" for k, v in out.items()), flush=True)
+    return out
+
+
+@pytest.mark.parametrize("length", [40, 130])
+def test_layer_matches_oracle_layer(length):
+    """fp32 layer (the reference's whole-layer test shape, L=40, plus a
+    length that spans three GLA chunks); every parameter gradient and the
+    input gradient within the north-star bars."""
+    layer = random_layer(torch.float32)
+    oracle = OracleAttention(layer)
+    layer = layer.cuda()
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(2, length, 128, generator=g)
+    grad = torch.randn(2, length, 128, generator=g)
+    rope = tiny_rope(length, batch=2, dtype=torch.float32)
+    xg = x.detach().cuda().requires_grad_()
+    y = layer(xg, tuple(t.cuda() for t in rope))[0]
+    y.backward(grad.cuda())
+    xc = x.detach().clone().requires_grad_()
+    expected = oracle(xc, rope)[0]
+    expected.backward(grad)
+    torch.cuda.synchronize()
+    pairs = {"out": (y, expected), "dx": (xg.grad, xc.grad)}
+    for name, p in layer.named_parameters():
+        pairs[name] = (p.grad, oracle.params[name.replace(".", "__")].grad)
+    errs = report(f"layer L={length}", pairs)
+    assert y.dtype == torch.float32
+    assert errs["out"] <= OUT_TOL and norm_rel(y, expected) < 2 * OUT_TOL, errs
+    for name, (a, b) in pairs.items():
+        if name == "out":
+            continue
+        assert errs[name] <= GRAD_TOL, (name, errs)
+        assert ref_close(a, b), (name, errs)
+
+
+def test_bf16_layer_stays_bf16_and_close_to_oracle():
+    """bf16 weights and activations (the config-5 dtype): the output stays
+    bf16 and is within the reference's bf16 layer bar (2e-2 relative norm,
+    tests/test_lizard.py:244-253) of the fp64 oracle on the same bf16
+    parameters."""
+    layer = random_layer(torch.bfloat16)
+    params = {n: p.detach().double() for n, p in layer.named_parameters()}
+    layer = layer.cuda()
+    x = torch.randn(2, 40, 128, generator=torch.Generator().manual_seed(2)).bfloat16()
+    rope = tiny_rope(40, batch=2, dtype=torch.float32)
+    with torch.no_grad():
+        y = layer(x.cuda(), tuple(t.cuda().bfloat16() for t in rope))[0]
+    expected = lo.lizard_layer(params, x.double(), rope[0].bfloat16().double(),
+                               rope[1].bfloat16().double(), 4, 2, 16)
+    print(f"[parity] bf16 layer: norm={norm_rel(y, expected):.2e} "
+          f"max={max_rel(y, expected):.2e}", flush=True)
+    assert y.dtype == torch.bfloat16
+    assert norm_rel(y, expected) < 2e-2
+
+
+def test_small_llama_with_lizard_blocks_matches_oracle_model():
+    """A 2-block Llama (fp32) with every attention block swapped: logits and
+    the gradients of every parameter of the model after a cross-entropy
+    backward, HIP layers on the GPU vs oracle layers on the CPU."""
+    torch.manual_seed(0)
+    model = LlamaForCausalLM(tiny_config(layers=2))
+    hip_layer.to_lizard(model, window=16, feature_dim=8)
+    with torch.no_grad():
+        for block in model.model.layers:
+            for p in block.self_attn.parameters():
+                if p.dim() < 2 or p.shape[0] == 1 or p.shape[1] == 32:
+                    p.normal_(0, 0.3)   # lizard-only parameters away from their init
+    cpu = LlamaForCausalLM(tiny_config(layers=2))
+    cpu.load_state_dict({k: v for k, v in model.state_dict().items()
+                         if "self_attn" not in k}, strict=False)
+    for mine, theirs in zip(cpu.model.layers, model.model.layers):
+        mine.self_attn = OracleAttention(theirs.self_attn)
+    model = model.cuda()
+    ids = torch.randint(0, 100, (2, 96), generator=torch.Generator().manual_seed(3))
+    out = model(ids.cuda(), labels=ids.cuda())
+    out.loss.backward()
+    ref = cpu(ids, labels=ids)
+    ref.loss.backward()
+    torch.cuda.synchronize()
+    pairs = {"logits": (out.logits, ref.logits)}
+    cpu_params = dict(cpu.named_parameters())
+    for name, p in model.named_parameters():
+        if "self_attn" in name:
+            block, rest = name.split(".self_attn.")
+            theirs = cpu_params[f"{block}.self_attn.params.{rest.replace('.', '__')}"]
+        else:
+            theirs = cpu_params[name]
+        pairs[name] = (p.grad, theirs.grad)
+    errs = report("llama x2", pairs)
+    assert abs(out.loss.item() - ref.loss.item()) < 1e-3 * abs(ref.loss.item())
+    assert errs["logits"] <= OUT_TOL, errs
+    for name, (a, b) in pairs.items():
+        if name != "logits":
+            assert errs[name] <= GRAD_TOL, (name, errs)

@@ -1,0 +1,153 @@
+"""CPU checks of the layer: the oracle's dense layer is pinned by its loop
+composition and by transformers' LlamaAttention in the softmax limit (the
+reference's tests/test_lizard.py:224-288), and the HIP layer's module
+surface mirrors the reference's (parameters, init, from_llama, backend
+names) without running any kernel."""
+import pytest
+import torch
+from transformers import LlamaConfig, LlamaForCausalLM
+from transformers.models.llama.modeling_llama import LlamaAttention, LlamaRotaryEmbedding
+
+from lizard_reproduction_amd import layer as hip_layer
+from oracle import lizard_oracle as lo
+
+EXACT = 1e-10
+
+
+def rel_err(a, b):
+    a, b = a.double(), b.double()
+    return ((a - b).norm() / b.norm()).item()
+
+
+def tiny_config(layers=1):
+    """The reference's tiny Llama (tests/test_lizard.py:94-98)."""
+    return LlamaConfig(hidden_size=128, intermediate_size=256, num_hidden_layers=layers,
+                       num_attention_heads=4, num_key_value_heads=2, vocab_size=100,
+                       attn_implementation="eager")
+
+
+def tiny_rope(length, start=0, batch=1, dtype=torch.float64):
+    x = torch.zeros(1, length, 1, dtype=dtype)
+    positions = torch.arange(start, start + length)[None].expand(batch, length)
+    return LlamaRotaryEmbedding(tiny_config())(x, positions)
+
+
+def random_params(seed=0, dtype=torch.float64, window=16, feature_dim=8):
+    """Parameters of a layer built like the reference's random_layer
+    (tests/test_lizard.py:107-113): every parameter ~ N(0, 0.3)."""
+    torch.manual_seed(seed)
+    layer = hip_layer.LizardAttention(tiny_config(), 0, window=window, feature_dim=feature_dim)
+    with torch.no_grad():
+        for p in layer.parameters():
+            p.normal_(0, 0.3)
+    return {n: p.detach().to(dtype) for n, p in layer.named_parameters()}
+
+
+def dense(params, x, rope, window=16):
+    return lo.lizard_layer(params, x, rope[0], rope[1], 4, 2, window)
+
+
+def test_oracle_layer_matches_formula_loops():
+    params, rope = random_params(), tiny_rope(20)
+    x = torch.randn(2, 20, 128).double()
+    loop = lo.lizard_layer_loop(params, x, rope[0][0], rope[1][0], 4, 2, 16)
+    assert rel_err(dense(params, x, rope), loop) < EXACT
+
+
+def test_oracle_layer_window_rope_is_relative():
+    params = random_params()
+    x = torch.randn(2, 20, 128).double()
+    shifted = dense(params, x, tiny_rope(20, start=7))
+    assert rel_err(shifted, dense(params, x, tiny_rope(20))) < 1e-5
+
+
+def test_oracle_layer_is_causal_and_batch_independent():
+    params, rope = random_params(), tiny_rope(30)
+    x = torch.randn(3, 30, 128).double().requires_grad_()
+    y = dense(params, x, rope)
+    single = torch.cat([dense(params, x[i:i + 1], rope) for i in range(3)])
+    assert rel_err(y, single) < EXACT
+    y[:, 9].sum().backward()
+    assert (x.grad[:, 10:] == 0).all()
+
+
+def test_oracle_layer_in_the_softmax_limit_is_llama_attention(monkeypatch):
+    """GLA branch zeroed, sinks at -1e4, unbounded window: the layer is
+    Llama's eager causal attention (tests/test_lizard.py:270-288)."""
+    config = tiny_config()
+    torch.manual_seed(0)
+    llama = LlamaAttention(config, 0).double()
+    params = random_params()
+    for name in ("q_proj", "k_proj", "v_proj", "o_proj"):
+        params[f"{name}.weight"] = getattr(llama, name).weight.detach()
+    params["meta_tokens"] = torch.full((4,), -1e4, dtype=torch.float64)
+    params["alpha_blend"] = torch.ones((), dtype=torch.float64)
+    monkeypatch.setattr(lo, "gla", lambda fq, fk, v, g: torch.zeros_like(v))
+    x, rope = torch.randn(2, 30, 128).double(), tiny_rope(30, batch=2)
+    mask = torch.full((30, 30), float("-inf")).triu(1).double()[None, None]
+    expected, _ = llama(hidden_states=x, position_embeddings=rope, attention_mask=mask)
+    assert rel_err(dense(params, x, rope, window=10**6), expected) < 1e-6
+
+
+def test_oracle_layer_catches_a_wrong_kv_head_map():
+    """A planted mistake (kv heads tiled instead of repeated per group)
+    fails the loop check, so that check pins the GQA expansion."""
+    params, rope = random_params(), tiny_rope(12)
+    x = torch.randn(1, 12, 128).double()
+    loop = lo.lizard_layer_loop(params, x, rope[0][0], rope[1][0], 4, 2, 16)
+    good = torch.Tensor.repeat_interleave
+
+    def tiled(t, n, dim):
+        return t.repeat(*[n if d == dim else 1 for d in range(t.dim())])
+    try:
+        torch.Tensor.repeat_interleave = lambda t, n, dim: tiled(t, n, dim)
+        wrong = dense(params, x, rope)
+    finally:
+        torch.Tensor.repeat_interleave = good
+    assert rel_err(wrong, loop) > 1e-3
+    assert rel_err(dense(params, x, rope), loop) < EXACT
+
+
+# -- the HIP layer's module surface (no kernel runs here) ---------------------
+
+def reference_shapes(config, window, num_meta, feature_dim):
+    """Parameter names and shapes of src/lizard_attention.py:49-71."""
+    hidden, heads, kv = config.hidden_size, config.num_attention_heads, config.num_key_value_heads
+    hd = hidden // heads
+    return {"q_proj.weight": (hidden, hidden), "k_proj.weight": (kv * hd, hidden),
+            "v_proj.weight": (kv * hd, hidden), "o_proj.weight": (hidden, hidden),
+            "phi_q.weight": (feature_dim, hd), "phi_k.weight": (feature_dim, hd),
+            "W_gamma.weight": (1, hidden), "meta_tokens": (num_meta,), "alpha_blend": ()}
+
+
+def test_layer_parameters_and_init_mirror_the_reference():
+    layer = hip_layer.LizardAttention(tiny_config(), 3, window=16, num_meta=5, feature_dim=8)
+    shapes = {n: tuple(p.shape) for n, p in layer.named_parameters()}
+    assert shapes == reference_shapes(tiny_config(), 16, 5, 8)
+    assert (layer.W_gamma.weight == 0).all() and (layer.meta_tokens == 0).all()
+    assert layer.alpha_blend.item() == 1.0
+    assert 0.005 < layer.phi_q.weight.std().item() < 0.05
+    assert (layer.layer_idx, layer.window, layer.heads, layer.kv_heads, layer.head_dim) == \
+        (3, 16, 4, 2, 32)
+
+
+@pytest.mark.parametrize("backend", ["torch", "triton", "cuda"])
+def test_layer_rejects_other_backends(backend):
+    with pytest.raises(ValueError, match="backend"):
+        hip_layer.LizardAttention(tiny_config(), 0, backend=backend)
+
+
+def test_from_llama_copies_projections_and_keeps_dtype():
+    config = tiny_config()
+    llama = LlamaAttention(config, 0).to(torch.bfloat16)
+    layer = hip_layer.from_llama(llama, config, window=16, feature_dim=8)
+    assert all(p.dtype == torch.bfloat16 for p in layer.parameters())
+    for name in ("q_proj", "k_proj", "v_proj", "o_proj"):
+        assert torch.equal(getattr(layer, name).weight, getattr(llama, name).weight)
+
+
+def test_to_lizard_swaps_every_block():
+    model = LlamaForCausalLM(tiny_config(layers=2))
+    hip_layer.to_lizard(model, window=16, num_meta=4, feature_dim=8, backend="hip")
+    assert all(isinstance(b.self_attn, hip_layer.LizardAttention) for b in model.model.layers)
+    assert [b.self_attn.layer_idx for b in model.model.layers] == [0, 1]
