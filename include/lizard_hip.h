@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define LZ_ABI_VERSION 5
+#define LZ_ABI_VERSION 6
 
 /* ABI version of the loaded library (LZ_ABI_VERSION). */
 int lz_abi_version(void);
@@ -117,6 +117,77 @@ int lz_swa_bwd(const void* q, const void* k, const void* v, const float* meta, i
                const float* lse, const void* dy, void* dq, void* dk, void* dv, float* dmeta,
                int grad_bf16, int batch, int heads, int length, int dim, int window,
                float scale, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Layer prologue, forward.  Replaces the torch ops of LizardAttention.forward
+ * between the projections and the kernel calls (src/lizard_attention.py:73-88):
+ * split + repeat_interleave of q/k/v, the fp32 promotion, hedgehog(q, phi_q),
+ * hedgehog(k, phi_k) (:9-11) and apply_rotary_pos_emb (:88), plus the kernels'
+ * bf16 casts (src/kernels/gla.py:217, swa.py:139).
+ *   q           [B, L, heads, head_dim]     (the q_proj output)
+ *   k, v        [B, L, kv_heads, head_dim]  (k_proj, v_proj outputs)
+ *   wq, wk      [feature_dim, head_dim]     (phi_q.weight, phi_k.weight)
+ *   cos, sin    [B, L, head_dim] if cos_batched else [L, head_dim]
+ *   all of them bf16 if dtype_bf16 else f32.
+ *   fq, fk      bf16 [B, heads, L, 2 feature_dim]: [softmax(x W^T), softmax(-x W^T)]
+ *   qr, kr, v_out  bf16 [B, heads, L, head_dim]: rotate_half RoPE of q, k; v
+ *   (k, v rows of kv head g go to query heads g*G .. g*G+G-1, G = heads/kv_heads).
+ * Supported sizes: head_dim 32, 64 or 128; feature_dim a multiple of 4, at most
+ * 128 (64 when head_dim is 128).
+ */
+int lz_layer_prologue_fwd(const void* q, const void* k, const void* v, const void* wq,
+                          const void* wk, const void* cos, const void* sin, int cos_batched,
+                          void* fq, void* fk, void* qr, void* kr, void* v_out, int dtype_bf16,
+                          int batch, int length, int heads, int kv_heads, int head_dim,
+                          int feature_dim, void* stream);
+
+/* Workspace bytes lz_layer_prologue_bwd needs for these sizes. */
+size_t lz_layer_prologue_bwd_workspace_bytes(int batch, int length, int heads, int kv_heads,
+                                             int head_dim, int feature_dim);
+
+/*
+ * Layer prologue, backward: what autograd does for the same ops.
+ *   dfq, dfk         f32 [B, heads, L, 2 feature_dim]  (gradients of fq, fk)
+ *   dqr, dkr, dv     f32 [B, heads, L, head_dim]       (gradients of qr, kr, v_out)
+ *   dv2              NULL or a second f32 gradient of v_out, added to dv (v_out
+ *                    feeds both attention branches)
+ *   dq               [B, L, heads, head_dim];  dk, dv_out [B, L, kv_heads, head_dim]
+ *                    (summed over each kv head's query heads), bf16 if dtype_bf16 else f32
+ *   dwq, dwk         f32 [feature_dim, head_dim]  (summed over every row, deterministically)
+ * q, k, wq, wk, cos, sin as given to lz_layer_prologue_fwd.
+ */
+int lz_layer_prologue_bwd(const void* q, const void* k, const void* wq, const void* wk,
+                          const void* cos, const void* sin, int cos_batched, const float* dfq,
+                          const float* dfk, const float* dqr, const float* dkr, const float* dv,
+                          const float* dv2, void* dq, void* dk, void* dv_out, float* dwq,
+                          float* dwk,
+                          int dtype_bf16, int batch, int length, int heads, int kv_heads,
+                          int head_dim, int feature_dim, void* workspace, size_t workspace_bytes,
+                          void* stream);
+
+/*
+ * Layer epilogue, forward.  Replaces y = y_gla.to(dtype) + alpha * y_swa.to(dtype)
+ * and y.to(x.dtype).transpose(1, 2).flatten(2) (src/lizard_attention.py:94-97).
+ *   y_gla, y_swa  bf16 [B, heads, L, head_dim];  alpha  f32 [1] (device)
+ *   out           [B, L, heads * head_dim], bf16 if out_bf16 else f32
+ * head_dim a multiple of 8.
+ */
+int lz_layer_combine_fwd(const void* y_gla, const void* y_swa, const float* alpha, void* out,
+                         int out_bf16, int batch, int heads, int length, int head_dim,
+                         void* stream);
+
+/* Workspace bytes lz_layer_combine_bwd needs. */
+size_t lz_layer_combine_bwd_workspace_bytes(void);
+
+/*
+ * Layer epilogue, backward: dy_gla = bf16(dout), dy_swa = bf16(alpha dout)
+ * (bf16 [B, heads, L, head_dim]) and dalpha = sum(dout * y_swa) (f32 [1],
+ * summed in a fixed order).  dout as `out` of lz_layer_combine_fwd.
+ */
+int lz_layer_combine_bwd(const void* dout, const void* y_swa, const float* alpha, void* dy_gla,
+                         void* dy_swa, float* dalpha, int out_bf16, int batch, int heads,
+                         int length, int head_dim, void* workspace, size_t workspace_bytes,
+                         void* stream);
 
 #ifdef __cplusplus
 }

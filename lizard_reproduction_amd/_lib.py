@@ -8,7 +8,7 @@ import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "_lib", "liblizard_hip.so")
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -28,6 +28,14 @@ SIGNATURES = {
     "lz_swa_bwd_workspace_bytes": (_S, [_I, _I, _I, _I, _I]),
     "lz_swa_bwd": (_I, [_P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I,
                         _I, _I, _I, _I, _I, _F, _P, _S, _P]),
+    "lz_layer_prologue_fwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I,
+                                   _I, _I, _I, _I, _I, _I, _P]),
+    "lz_layer_prologue_bwd_workspace_bytes": (_S, [_I, _I, _I, _I, _I, _I]),
+    "lz_layer_prologue_bwd": (_I, [_P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P,
+                                   _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _S, _P]),
+    "lz_layer_combine_fwd": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
+    "lz_layer_combine_bwd_workspace_bytes": (_S, []),
+    "lz_layer_combine_bwd": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _S, _P]),
 }
 
 _lib = None

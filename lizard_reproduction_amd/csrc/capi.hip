@@ -30,6 +30,24 @@ hipError_t launch_swa_bwd(const void* q, const void* k, const void* v, const flo
                           float* dmeta, int BH, int L, int d, int W, float scale,
                           hipStream_t st);
 constexpr int MAX_META = 64;
+bool prologue_dims_supported(int hd, int f);
+size_t prologue_bwd_workspace(int B, int L, int H, int Hkv, int hd, int f);
+hipError_t launch_prologue_fwd(const void* q, const void* k, const void* v, const void* wq,
+                               const void* wk, const void* cos, const void* sin, void* fq,
+                               void* fk, void* qr, void* kr, void* vo, bool bf16_in, int B, int L,
+                               int H, int Hkv, int hd, int f, int cos_bstride, hipStream_t st);
+hipError_t launch_prologue_bwd(const void* q, const void* k, const void* wq, const void* wk,
+                               const void* cos, const void* sin, const float* dfq,
+                               const float* dfk, const float* dqr, const float* dkr,
+                               const float* dv, const float* dv2, void* dq, void* dk, void* dvo,
+                               float* dwq, float* dwk, bool bf16_in, int B, int L, int H, int Hkv,
+                               int hd, int f, int cos_bstride, float* ws, hipStream_t st);
+size_t combine_bwd_workspace();
+hipError_t launch_combine_fwd(const void* yg, const void* ys, const float* alpha, void* out,
+                              bool bf16_out, int B, int H, int L, int hd, hipStream_t st);
+hipError_t launch_combine_bwd(const void* dout, const void* ys, const float* alpha, void* dyg,
+                              void* dys, float* dalpha, bool bf16_out, int B, int H, int L,
+                              int hd, float* ws, hipStream_t st);
 
 }  // namespace lz
 
@@ -179,4 +197,112 @@ extern "C" int lz_swa_bwd(const void* q, const void* k, const void* v, const flo
                                        grad_bf16 != 0, delta, part, dmeta, batch * heads, length,
                                        dim, window, scale, st),
                     "swa_bwd");
+}
+
+// ---------------------------------------------------------------------------
+// layer prologue / epilogue
+// ---------------------------------------------------------------------------
+static int check_layer(int batch, int length, int heads, int kv_heads, int head_dim,
+                       int feature_dim) {
+  if (batch <= 0 || length <= 0 || heads <= 0 || kv_heads <= 0)
+    return fail(1, "layer: sizes must be positive (B=%d L=%d heads=%d kv_heads=%d)", batch,
+                length, heads, kv_heads);
+  if (heads % kv_heads)
+    return fail(1, "layer: heads (%d) must be a multiple of kv_heads (%d)", heads, kv_heads);
+  if (!lz::prologue_dims_supported(head_dim, feature_dim))
+    return fail(1, "layer: unsupported head_dim %d / feature_dim %d (head_dim 32, 64 or 128; "
+                   "feature_dim a multiple of 4 up to 128, up to 64 with head_dim 128)",
+                head_dim, feature_dim);
+  return 0;
+}
+
+extern "C" int lz_layer_prologue_fwd(const void* q, const void* k, const void* v, const void* wq,
+                                     const void* wk, const void* cos, const void* sin,
+                                     int cos_batched, void* fq, void* fk, void* qr, void* kr,
+                                     void* v_out, int dtype_bf16, int batch, int length,
+                                     int heads, int kv_heads, int head_dim, int feature_dim,
+                                     void* stream) {
+  if (int rc = check_layer(batch, length, heads, kv_heads, head_dim, feature_dim)) return rc;
+  if (!q || !k || !v || !wq || !wk || !cos || !sin)
+    return fail(1, "layer_prologue_fwd: null input pointer");
+  if (!fq || !fk || !qr || !kr || !v_out) return fail(1, "layer_prologue_fwd: null output pointer");
+  return hip_status(lz::launch_prologue_fwd(q, k, v, wq, wk, cos, sin, fq, fk, qr, kr, v_out,
+                                            dtype_bf16 != 0, batch, length, heads, kv_heads,
+                                            head_dim, feature_dim, cos_batched ? length : 0,
+                                            (hipStream_t)stream),
+                    "layer_prologue_fwd");
+}
+
+extern "C" size_t lz_layer_prologue_bwd_workspace_bytes(int batch, int length, int heads,
+                                                        int kv_heads, int head_dim,
+                                                        int feature_dim) {
+  if (batch <= 0 || length <= 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads ||
+      !lz::prologue_dims_supported(head_dim, feature_dim))
+    return 0;
+  return lz::prologue_bwd_workspace(batch, length, heads, kv_heads, head_dim, feature_dim);
+}
+
+extern "C" int lz_layer_prologue_bwd(const void* q, const void* k, const void* wq, const void* wk,
+                                     const void* cos, const void* sin, int cos_batched,
+                                     const float* dfq, const float* dfk, const float* dqr,
+                                     const float* dkr, const float* dv, const float* dv2,
+                                     void* dq, void* dk, void* dv_out, float* dwq, float* dwk,
+                                     int dtype_bf16,
+                                     int batch, int length, int heads, int kv_heads,
+                                     int head_dim, int feature_dim, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  if (int rc = check_layer(batch, length, heads, kv_heads, head_dim, feature_dim)) return rc;
+  if (!q || !k || !wq || !wk || !cos || !sin || !dfq || !dfk || !dqr || !dkr || !dv)
+    return fail(1, "layer_prologue_bwd: null input pointer");
+  if (!dq || !dk || !dv_out || !dwq || !dwk)
+    return fail(1, "layer_prologue_bwd: null output pointer");
+  const size_t need = lz_layer_prologue_bwd_workspace_bytes(batch, length, heads, kv_heads,
+                                                            head_dim, feature_dim);
+  if (!workspace || workspace_bytes < need)
+    return fail(1, "layer_prologue_bwd: workspace of %zu bytes given, %zu needed",
+                workspace_bytes, need);
+  return hip_status(lz::launch_prologue_bwd(q, k, wq, wk, cos, sin, dfq, dfk, dqr, dkr, dv, dv2,
+                                            dq, dk, dv_out, dwq, dwk, dtype_bf16 != 0, batch, length,
+                                            heads, kv_heads, head_dim, feature_dim,
+                                            cos_batched ? length : 0, (float*)workspace,
+                                            (hipStream_t)stream),
+                    "layer_prologue_bwd");
+}
+
+static int check_combine(int batch, int heads, int length, int head_dim) {
+  if (batch <= 0 || heads <= 0 || length <= 0 || head_dim <= 0)
+    return fail(1, "layer_combine: sizes must be positive (B=%d heads=%d L=%d hd=%d)", batch,
+                heads, length, head_dim);
+  if (head_dim % 8) return fail(1, "layer_combine: head_dim %d is not a multiple of 8", head_dim);
+  return 0;
+}
+
+extern "C" int lz_layer_combine_fwd(const void* y_gla, const void* y_swa, const float* alpha,
+                                    void* out, int out_bf16, int batch, int heads, int length,
+                                    int head_dim, void* stream) {
+  if (int rc = check_combine(batch, heads, length, head_dim)) return rc;
+  if (!y_gla || !y_swa || !alpha || !out) return fail(1, "layer_combine_fwd: null pointer");
+  return hip_status(lz::launch_combine_fwd(y_gla, y_swa, alpha, out, out_bf16 != 0, batch, heads,
+                                           length, head_dim, (hipStream_t)stream),
+                    "layer_combine_fwd");
+}
+
+extern "C" size_t lz_layer_combine_bwd_workspace_bytes(void) {
+  return lz::combine_bwd_workspace();
+}
+
+extern "C" int lz_layer_combine_bwd(const void* dout, const void* y_swa, const float* alpha,
+                                    void* dy_gla, void* dy_swa, float* dalpha, int out_bf16,
+                                    int batch, int heads, int length, int head_dim,
+                                    void* workspace, size_t workspace_bytes, void* stream) {
+  if (int rc = check_combine(batch, heads, length, head_dim)) return rc;
+  if (!dout || !y_swa || !alpha || !dy_gla || !dy_swa || !dalpha)
+    return fail(1, "layer_combine_bwd: null pointer");
+  if (!workspace || workspace_bytes < lz::combine_bwd_workspace())
+    return fail(1, "layer_combine_bwd: workspace of %zu bytes given, %zu needed",
+                workspace_bytes, lz::combine_bwd_workspace());
+  return hip_status(lz::launch_combine_bwd(dout, y_swa, alpha, dy_gla, dy_swa, dalpha,
+                                           out_bf16 != 0, batch, heads, length, head_dim,
+                                           (float*)workspace, (hipStream_t)stream),
+                    "layer_combine_bwd");
 }

@@ -86,6 +86,51 @@ def _check_gla(fq, fk, v, log_gamma, chunk):
     _require_gpu(fq, fk, v, log_gamma)
 
 
+def gla_forward(fq, fk, v, lg, keep_state=True, chunk=CHUNK):
+    """One ``lz_gla_fwd`` launch on bf16 contiguous fq, fk, v and fp32
+    contiguous log_gamma; returns (y, state), state being the workspace of
+    the states entering each sequence segment, which ``gla_backward`` reuses
+    (None when not kept or not needed)."""
+    b, h, length, nf = fq.shape
+    nd = v.shape[-1]
+    y = torch.empty_like(v)
+    ws = None
+    if y.numel():
+        lib = _lib.load()
+        per_head = int(lg.dim() == 3)
+        nbytes = _gla_fwd_ws(b, h, length, nf, nd, per_head, chunk)
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=fq.device) if nbytes else None
+        rc = lib.lz_gla_fwd(_ptr(fq), _ptr(fk), _ptr(v), _ptr(lg), _ptr(y), b, h, length,
+                            nf, nd, per_head, chunk, _ptr(ws), nbytes, _stream(fq))
+        _lib.check(rc, "lz_gla_fwd")
+    return y, (ws if keep_state else None)
+
+
+def gla_backward(fq, fk, v, lg, dy, state, grad_dtype, chunk=CHUNK):
+    """One ``lz_gla_bwd`` launch: (dfq, dfk, dv) in grad_dtype (bf16 or
+    fp32) and dlog_gamma fp32 in log_gamma's layout."""
+    b, h, length, nf = fq.shape
+    nd = v.shape[-1]
+    dfq = torch.empty(fq.shape, device=fq.device, dtype=grad_dtype)
+    dfk = torch.empty_like(dfq)
+    dv = torch.empty(v.shape, device=v.device, dtype=grad_dtype)
+    dlg = torch.empty_like(lg)
+    if dy.numel():
+        lib = _lib.load()
+        per_head = int(lg.dim() == 3)
+        nbytes = _gla_bwd_ws(b, h, length, nf, nd, per_head, chunk)
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=fq.device)
+        rc = lib.lz_gla_bwd(_ptr(fq), _ptr(fk), _ptr(v), _ptr(lg), _ptr(dy), _ptr(dfq),
+                            _ptr(dfk), _ptr(dv), _ptr(dlg), int(grad_dtype == torch.bfloat16),
+                            b, h, length, nf, nd, per_head, chunk, _ptr(state),
+                            state.numel() if state is not None else 0, _ptr(ws), ws.numel(),
+                            _stream(fq))
+        _lib.check(rc, "lz_gla_bwd")
+    else:
+        dfq.zero_(), dfk.zero_(), dv.zero_(), dlg.zero_()
+    return dfq, dfk, dv, dlg
+
+
 class _GLA(torch.autograd.Function):
     """Autograd node of ``gla``; mirrors ``_GLA`` (src/kernels/gla.py:213-256),
     but takes log_gamma itself: its cumsum, head expand and their gradients
@@ -96,53 +141,21 @@ class _GLA(torch.autograd.Function):
         ctx.dtypes = (fq.dtype, fk.dtype, v.dtype, log_gamma.dtype)
         fq, fk, v = _bf16(fq), _bf16(fk), _bf16(v)
         lg = log_gamma.float().contiguous()
-        b, h, length, nf = fq.shape
-        nd = v.shape[-1]
-        y = torch.empty_like(v)
-        if y.numel():
-            lib = _lib.load()
-            per_head = int(lg.dim() == 3)
-            nbytes = _gla_fwd_ws(b, h, length, nf, nd, per_head, chunk)
-            ws = torch.empty(nbytes, dtype=torch.uint8, device=fq.device) if nbytes else None
-            rc = lib.lz_gla_fwd(_ptr(fq), _ptr(fk), _ptr(v), _ptr(lg), _ptr(y), b, h, length,
-                                nf, nd, per_head, chunk, _ptr(ws), nbytes, _stream(fq))
-            _lib.check(rc, "lz_gla_fwd")
-        else:
-            ws = None
-        if any(ctx.needs_input_grad[:4]):
+        grad = any(ctx.needs_input_grad[:4])
+        y, state = gla_forward(fq, fk, v, lg, keep_state=grad, chunk=chunk)
+        if grad:
             ctx.save_for_backward(fq, fk, v, lg)
             # the state entering each segment, reused by the backward
-            ctx.fwd_ws = ws
+            ctx.fwd_ws = state
         ctx.chunk = chunk
         return y
 
     @staticmethod
     def backward(ctx, dy):
         fq, fk, v, lg = ctx.saved_tensors
-        b, h, length, nf = fq.shape
-        nd = v.shape[-1]
-        dy = _bf16(dy)
         gdt = torch.bfloat16 if all(d == torch.bfloat16 for d in ctx.dtypes[:3]) else torch.float32
-        dfq = torch.empty(fq.shape, device=fq.device, dtype=gdt)
-        dfk = torch.empty_like(dfq)
-        dv = torch.empty(v.shape, device=v.device, dtype=gdt)
-        dlg = torch.empty_like(lg)
-        if dy.numel():
-            lib = _lib.load()
-            per_head = int(lg.dim() == 3)
-            nbytes = _gla_bwd_ws(b, h, length, nf, nd, per_head, ctx.chunk)
-            ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=fq.device)
-            fws = ctx.fwd_ws
-            rc = lib.lz_gla_bwd(_ptr(fq), _ptr(fk), _ptr(v), _ptr(lg), _ptr(dy), _ptr(dfq),
-                                _ptr(dfk), _ptr(dv), _ptr(dlg), int(gdt == torch.bfloat16), b,
-                                h, length, nf, nd, per_head, ctx.chunk, _ptr(fws),
-                                fws.numel() if fws is not None else 0, _ptr(ws), ws.numel(),
-                                _stream(fq))
-            _lib.check(rc, "lz_gla_bwd")
-        else:
-            dfq.zero_(), dfk.zero_(), dv.zero_(), dlg.zero_()
-        grads = tuple(g.to(d) for g, d in zip((dfq, dfk, dv, dlg), ctx.dtypes))
-        return grads + (None,)
+        grads = gla_backward(fq, fk, v, lg, _bf16(dy), ctx.fwd_ws, gdt, ctx.chunk)
+        return tuple(g.to(d) for g, d in zip(grads, ctx.dtypes)) + (None,)
 
 
 def gla(fq, fk, v, log_gamma, chunk=CHUNK):
@@ -176,6 +189,42 @@ def _check_swa(q, k, v, meta, window, fwd_blocks, bwd_blocks):
         _require_gpu(meta)
 
 
+def swa_forward(q, k, v, meta, window):
+    """One ``lz_swa_fwd`` launch on bf16 contiguous q, k, v and fp32
+    contiguous meta; returns (y, lse)."""
+    b, h, length, d = q.shape
+    y = torch.empty_like(v)
+    lse = torch.empty(b, h, length, device=v.device, dtype=torch.float32)
+    if y.numel():
+        rc = _lib.load().lz_swa_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(meta), meta.numel(),
+                                    _ptr(y), _ptr(lse), b, h, length, d, window,
+                                    1.0 / math.sqrt(d), _stream(q))
+        _lib.check(rc, "lz_swa_fwd")
+    return y, lse
+
+
+def swa_backward(q, k, v, meta, lse, dy, window, grad_dtype):
+    """One ``lz_swa_bwd`` launch: (dq, dk, dv) in grad_dtype, dmeta fp32."""
+    b, h, length, d = q.shape
+    dq = torch.empty(q.shape, device=q.device, dtype=grad_dtype)
+    dk = torch.empty_like(dq)
+    dv = torch.empty_like(dq)
+    dmeta = torch.empty(meta.shape, device=q.device, dtype=torch.float32)
+    if dy.numel():
+        lib = _lib.load()
+        n_meta = meta.numel()
+        nbytes = _swa_bwd_ws(b, h, length, d, n_meta)
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
+        rc = lib.lz_swa_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(meta), n_meta,
+                            _ptr(lse), _ptr(dy), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dmeta),
+                            int(grad_dtype == torch.bfloat16), b, h, length, d, window,
+                            1.0 / math.sqrt(d), _ptr(ws), ws.numel(), _stream(q))
+        _lib.check(rc, "lz_swa_bwd")
+    else:
+        dq.zero_(), dk.zero_(), dv.zero_(), dmeta.zero_()
+    return dq, dk, dv, dmeta
+
+
 class _SWA(torch.autograd.Function):
     """Autograd node of ``swa``; mirrors ``_SWA`` (src/kernels/swa.py:136-179)."""
 
@@ -184,44 +233,18 @@ class _SWA(torch.autograd.Function):
         ctx.dtypes = (q.dtype, k.dtype, v.dtype, meta.dtype)
         q, k, v = _bf16(q), _bf16(k), _bf16(v)
         meta = meta.float().contiguous()
-        b, h, length, d = q.shape
-        scale = 1.0 / math.sqrt(d)
-        y = torch.empty_like(v)
-        lse = torch.empty(b, h, length, device=v.device, dtype=torch.float32)
-        if y.numel():
-            lib = _lib.load()
-            rc = lib.lz_swa_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(meta), meta.numel(), _ptr(y),
-                                _ptr(lse), b, h, length, d, window, scale, _stream(q))
-            _lib.check(rc, "lz_swa_fwd")
+        y, lse = swa_forward(q, k, v, meta, window)
         if any(ctx.needs_input_grad[:4]):
             ctx.save_for_backward(q, k, v, meta, lse)
-        ctx.window, ctx.scale = window, scale
+        ctx.window = window
         return y
 
     @staticmethod
     def backward(ctx, dy):
         q, k, v, meta, lse = ctx.saved_tensors
-        b, h, length, d = q.shape
-        dy = _bf16(dy)
         gdt = torch.bfloat16 if all(x == torch.bfloat16 for x in ctx.dtypes[:3]) else torch.float32
-        dq = torch.empty(q.shape, device=q.device, dtype=gdt)
-        dk = torch.empty_like(dq)
-        dv = torch.empty_like(dq)
-        dmeta = torch.empty(meta.shape, device=q.device, dtype=torch.float32)
-        if dy.numel():
-            lib = _lib.load()
-            n_meta = meta.numel()
-            nbytes = _swa_bwd_ws(b, h, length, d, n_meta)
-            ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
-            rc = lib.lz_swa_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(meta), n_meta,
-                                _ptr(lse), _ptr(dy), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dmeta),
-                                int(gdt == torch.bfloat16), b, h, length, d, ctx.window,
-                                ctx.scale, _ptr(ws), ws.numel(), _stream(q))
-            _lib.check(rc, "lz_swa_bwd")
-        else:
-            dq.zero_(), dk.zero_(), dv.zero_(), dmeta.zero_()
-        grads = tuple(g.to(dt) for g, dt in zip((dq, dk, dv, dmeta), ctx.dtypes))
-        return grads + (None, None, None)
+        grads = swa_backward(q, k, v, meta, lse, _bf16(dy), ctx.window, gdt)
+        return tuple(g.to(dt) for g, dt in zip(grads, ctx.dtypes)) + (None, None, None)
 
 
 def swa(q, k, v, meta, window, fwd_blocks=FWD_BLOCKS, bwd_blocks=BWD_BLOCKS):

@@ -5,8 +5,6 @@ Same constructor, parameter names, shapes and initialisation, same
 ``forward(hidden_states, position_embeddings) -> (out, None)`` and the same
 ``from_llama``, so a checkpoint or a ``LlamaForCausalLM`` whose attention
 blocks were swapped for the reference's layer loads into this one unchanged.
-The two attention branches run on ``kernels.gla`` and ``kernels.swa``
-(hand-written gfx950 kernels); the projections are torch GEMMs.
 
 The layer computes, per token (``src/lizard_attention.py:78-97``):
 
@@ -17,31 +15,182 @@ The layer computes, per token (``src/lizard_attention.py:78-97``):
     y       = gla(fq, fk, v, logsigmoid(z)) + alpha * swa(qr, kr, v, meta, window)
     out     = o_proj(y)
 
-with everything after the projections in promote(x.dtype, fp32), as the
-reference does.
+with everything after the projections in promote(x.dtype, fp32).  The
+projections and the gate logit are torch GEMMs; everything from the
+projection outputs to o_proj's input runs in four HIP launches (forward):
+the fused prologue (GQA expand, Hedgehog feature maps, RoPE and the bf16
+casts, one pass over q/k/v), the GLA and SWA kernels, and the fused blend +
+transpose.  The kernels hand fp32 gradients back to the prologue, as the
+reference's fp32 intermediates get them.
 """
+import functools
+
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from . import kernels
+from . import _lib, kernels
 
 BACKENDS = ("hip",)
 
 
-def hedgehog(x, weight):
-    """[softmax(x W^T), softmax(-x W^T)] over the features
-    (``src/lizard_attention.py:9-11``)."""
-    proj = torch.matmul(x, weight.transpose(0, 1))
-    return torch.cat([proj.softmax(-1), (-proj).softmax(-1)], dim=-1)
+def _stream(t):
+    return torch._C._cuda_getCurrentRawStream(t.device.index)
 
 
-def rotate(x, cos, sin):
-    """rotate_half RoPE with tables [B, L, d] broadcast over the heads (what
-    ``transformers``' ``apply_rotary_pos_emb`` does with unsqueeze_dim=1)."""
-    half = x.shape[-1] // 2
-    rotated = torch.cat([-x[..., half:], x[..., :half]], dim=-1)
-    return x * cos.unsqueeze(1) + rotated * sin.unsqueeze(1)
+@functools.lru_cache(maxsize=64)
+def _prologue_ws(b, length, heads, kv, hd, f):
+    return _lib.load().lz_layer_prologue_bwd_workspace_bytes(b, length, heads, kv, hd, f)
+
+
+def prologue_supported(head_dim, feature_dim):
+    """Shapes the fused prologue takes: head_dim 32, 64 or 128; feature_dim a
+    multiple of 4 up to 128, up to 64 with head_dim 128 (the GLA kernels
+    take F = 2 feature_dim <= 128 when D = 128)."""
+    return (head_dim in (32, 64, 128) and feature_dim > 0 and feature_dim % 4 == 0
+            and feature_dim <= (64 if head_dim == 128 else 128))
+
+
+def _tables(cos, sin, batch, length, head_dim, dtype):
+    """RoPE tables as contiguous [B, L, hd] or [L, hd] of ``dtype``; returns
+    (cos, sin, batched)."""
+    if cos.shape != sin.shape:
+        raise ValueError(f"LizardAttention: cos and sin shapes differ: {tuple(cos.shape)} "
+                         f"vs {tuple(sin.shape)}")
+    if cos.dim() == 3 and cos.shape[0] == 1:
+        cos, sin = cos[0], sin[0]
+    if cos.dim() == 2:
+        ok, batched = tuple(cos.shape) == (length, head_dim), 0
+    else:
+        ok, batched = tuple(cos.shape) == (batch, length, head_dim), 1
+    if not ok:
+        raise ValueError(f"LizardAttention: position embeddings of shape {tuple(cos.shape)} "
+                         f"do not match B={batch}, L={length}, head_dim={head_dim}")
+    return cos.to(dtype).contiguous(), sin.to(dtype).contiguous(), batched
+
+
+def prologue_forward(qp, kp, vp, wq, wk, cos, sin, heads, kv_heads):
+    """One ``lz_layer_prologue_fwd`` launch: the q/k/v projection outputs
+    ([B, L, heads * hd], [B, L, kv_heads * hd]) and phi weights ([f, hd]) to
+    the bf16 kernel operands fq, fk ([B, H, L, 2f]) and qr, kr, v
+    ([B, H, L, hd]).  Returns those five and the tuple ``prologue_backward``
+    needs."""
+    b, length, _ = qp.shape
+    hd = qp.shape[-1] // heads
+    f = wq.shape[0]
+    # bf16 arithmetic inputs only when every input is bf16; otherwise all are
+    # widened to fp32 (exactly), as the reference promotes them
+    dtype = torch.bfloat16 if all(t.dtype == torch.bfloat16
+                                  for t in (qp, kp, vp, wq, wk, cos, sin)) else torch.float32
+    qp, kp, vp, wq, wk = (t.to(dtype).contiguous() for t in (qp, kp, vp, wq, wk))
+    cos, sin, batched = _tables(cos, sin, b, length, hd, dtype)
+    dev = qp.device
+    fq = torch.empty(b, heads, length, 2 * f, device=dev, dtype=torch.bfloat16)
+    fk = torch.empty_like(fq)
+    qr = torch.empty(b, heads, length, hd, device=dev, dtype=torch.bfloat16)
+    kr, v = torch.empty_like(qr), torch.empty_like(qr)
+    rc = _lib.load().lz_layer_prologue_fwd(
+        qp.data_ptr(), kp.data_ptr(), vp.data_ptr(), wq.data_ptr(), wk.data_ptr(),
+        cos.data_ptr(), sin.data_ptr(), batched, fq.data_ptr(), fk.data_ptr(), qr.data_ptr(),
+        kr.data_ptr(), v.data_ptr(), int(dtype == torch.bfloat16), b, length, heads, kv_heads,
+        hd, f, _stream(qp))
+    _lib.check(rc, "lz_layer_prologue_fwd")
+    saved = (qp, kp, wq, wk, cos, sin, (b, length, heads, kv_heads, hd, f, batched))
+    return fq, fk, qr, kr, v, saved
+
+
+def prologue_backward(saved, dfq, dfk, dqr, dkr, dv, dv2=None):
+    """One ``lz_layer_prologue_bwd`` launch from fp32 gradients of fq, fk, qr,
+    kr and v (dv2: an optional second gradient of v); returns dq, dk, dv of
+    the projection outputs (in the arithmetic dtype) and dWq, dWk (fp32)."""
+    qp, kp, wq, wk, cos, sin, (b, length, heads, kv, hd, f, batched) = saved
+    grads = [None if g is None else g.float().contiguous() for g in (dfq, dfk, dqr, dkr, dv, dv2)]
+    dq, dk, dvp = torch.empty_like(qp), torch.empty_like(kp), torch.empty_like(kp)
+    dwq = torch.empty(wq.shape, device=wq.device, dtype=torch.float32)
+    dwk = torch.empty_like(dwq)
+    nbytes = _prologue_ws(b, length, heads, kv, hd, f)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=qp.device)
+    rc = _lib.load().lz_layer_prologue_bwd(
+        qp.data_ptr(), kp.data_ptr(), wq.data_ptr(), wk.data_ptr(), cos.data_ptr(),
+        sin.data_ptr(), batched, *(None if g is None else g.data_ptr() for g in grads),
+        dq.data_ptr(), dk.data_ptr(), dvp.data_ptr(), dwq.data_ptr(), dwk.data_ptr(),
+        int(qp.dtype == torch.bfloat16), b, length, heads, kv, hd, f, ws.data_ptr(), nbytes,
+        _stream(qp))
+    _lib.check(rc, "lz_layer_prologue_bwd")
+    return dq, dk, dvp, dwq, dwk
+
+
+def combine_forward(yg, ys, alpha, out_dtype):
+    """``lz_layer_combine_fwd``: y_gla + alpha * y_swa ([B, H, L, hd] bf16;
+    alpha fp32 [1]) as [B, L, H * hd] in out_dtype (bf16 or fp32)."""
+    b, heads, length, hd = yg.shape
+    out = torch.empty(b, length, heads * hd, device=yg.device, dtype=out_dtype)
+    rc = _lib.load().lz_layer_combine_fwd(yg.data_ptr(), ys.data_ptr(), alpha.data_ptr(),
+                                          out.data_ptr(), int(out_dtype == torch.bfloat16), b,
+                                          heads, length, hd, _stream(yg))
+    _lib.check(rc, "lz_layer_combine_fwd")
+    return out
+
+
+def combine_backward(dout, ys, alpha):
+    """``lz_layer_combine_bwd``: bf16 gradients of y_gla and y_swa and the
+    fp32 gradient of alpha ([1])."""
+    b, heads, length, hd = ys.shape
+    dyg, dys = torch.empty_like(ys), torch.empty_like(ys)
+    dalpha = torch.empty(1, device=ys.device, dtype=torch.float32)
+    lib = _lib.load()
+    nbytes = lib.lz_layer_combine_bwd_workspace_bytes()
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=ys.device)
+    rc = lib.lz_layer_combine_bwd(dout.data_ptr(), ys.data_ptr(), alpha.data_ptr(),
+                                  dyg.data_ptr(), dys.data_ptr(), dalpha.data_ptr(),
+                                  int(dout.dtype == torch.bfloat16), b, heads, length, hd,
+                                  ws.data_ptr(), nbytes, _stream(ys))
+    _lib.check(rc, "lz_layer_combine_bwd")
+    return dyg, dys, dalpha
+
+
+class _Core(torch.autograd.Function):
+    """Everything from the projection outputs to o_proj's input as one
+    autograd node (src/lizard_attention.py:73-97): prologue, GLA, SWA and
+    the blend, forward and backward.  Inside it the kernels pass each other
+    fp32 gradients of the fp32 intermediates the reference's layer has (its
+    fq, fk, q, k, v are fp32, so its kernels return fp32 gradients)."""
+
+    @staticmethod
+    def forward(ctx, qp, kp, vp, wq, wk, log_gamma, meta, alpha, cos, sin, heads, kv_heads,
+                window, out_dtype):
+        fq, fk, qr, kr, v, saved = prologue_forward(qp, kp, vp, wq, wk, cos, sin, heads,
+                                                    kv_heads)
+        lg = log_gamma.float().contiguous()
+        meta32 = meta.float().contiguous()
+        alpha32 = alpha.detach().float().reshape(1).contiguous()
+        grad = any(ctx.needs_input_grad[:8])
+        y_gla, state = kernels.gla_forward(fq, fk, v, lg, keep_state=grad)
+        y_swa, lse = kernels.swa_forward(qr, kr, v, meta32, window)
+        odt = torch.bfloat16 if out_dtype == torch.bfloat16 else torch.float32
+        out = combine_forward(y_gla, y_swa, alpha32, odt)
+        if grad:
+            ctx.save_for_backward(fq, fk, qr, kr, v, lg, meta32, lse, y_swa, alpha32,
+                                  *saved[:6])
+            ctx.state, ctx.sizes = state, saved[6]
+        ctx.window = window
+        ctx.dtypes = (qp.dtype, kp.dtype, vp.dtype, wq.dtype, wk.dtype, log_gamma.dtype,
+                      meta.dtype, alpha.dtype)
+        return out.to(out_dtype)
+
+    @staticmethod
+    def backward(ctx, dout):
+        fq, fk, qr, kr, v, lg, meta32, lse, y_swa, alpha32, *saved = ctx.saved_tensors
+        saved = tuple(saved) + (ctx.sizes,)
+        odt = torch.bfloat16 if dout.dtype == torch.bfloat16 else torch.float32
+        dyg, dys, dalpha = combine_backward(dout.to(odt).contiguous(), y_swa, alpha32)
+        f32 = torch.float32
+        dfq, dfk, dv_gla, dlg = kernels.gla_backward(fq, fk, v, lg, dyg, ctx.state, f32)
+        dqr, dkr, dv_swa, dmeta = kernels.swa_backward(qr, kr, v, meta32, lse, dys, ctx.window,
+                                                       f32)
+        dq, dk, dvp, dwq, dwk = prologue_backward(saved, dfq, dfk, dqr, dkr, dv_gla, dv_swa)
+        grads = (dq, dk, dvp, dwq, dwk, dlg, dmeta, dalpha.reshape(()))
+        return tuple(g.to(d) for g, d in zip(grads, ctx.dtypes)) + (None,) * 6
 
 
 class LizardAttention(nn.Module):
@@ -70,6 +219,10 @@ class LizardAttention(nn.Module):
             raise ValueError("LizardAttention: hidden_size must split into heads and "
                              "num_attention_heads into num_key_value_heads groups")
         self.head_dim = hidden // self.heads
+        if not prologue_supported(self.head_dim, feature_dim):
+            raise ValueError(f"LizardAttention: head_dim {self.head_dim} / feature_dim "
+                             f"{feature_dim} unsupported (head_dim 32, 64 or 128; feature_dim "
+                             "a multiple of 4 up to 128, up to 64 with head_dim 128)")
         self.window = window
         kv_dim = self.kv_heads * self.head_dim
         self.q_proj = nn.Linear(hidden, hidden, bias=False)
@@ -95,18 +248,14 @@ class LizardAttention(nn.Module):
     def forward(self, hidden_states, position_embeddings, **kwargs):
         x = hidden_states
         dtype = torch.promote_types(x.dtype, torch.float32)
-        q = self.split(self.q_proj(x), self.heads).to(dtype)
-        k = self.split(self.k_proj(x), self.kv_heads).to(dtype)
-        v = self.split(self.v_proj(x), self.kv_heads).to(dtype)
+        if x.device.type != "cuda":
+            raise ValueError("LizardAttention (hip backend) needs its input on a ROCm GPU")
         z = self.W_gamma(x).to(dtype).squeeze(-1)
-        fq = hedgehog(q, self.phi_q.weight.to(dtype))
-        fk = hedgehog(k, self.phi_k.weight.to(dtype))
-        cos, sin = (t.to(dtype) for t in position_embeddings)
-        qr, kr = rotate(q, cos, sin), rotate(k, cos, sin)
-        alpha, meta = self.alpha_blend.to(dtype), self.meta_tokens.to(dtype)
-        y = kernels.gla(fq, fk, v, F.logsigmoid(z)).to(dtype)
-        y = y + alpha * kernels.swa(qr, kr, v, meta, self.window).to(dtype)
-        return self.o_proj(y.to(x.dtype).transpose(1, 2).flatten(2)), None
+        cos, sin = position_embeddings
+        y = _Core.apply(self.q_proj(x), self.k_proj(x), self.v_proj(x), self.phi_q.weight,
+                        self.phi_k.weight, F.logsigmoid(z), self.meta_tokens, self.alpha_blend,
+                        cos, sin, self.heads, self.kv_heads, self.window, x.dtype)
+        return self.o_proj(y), None
 
 
 def from_llama(attention, config, **options):

@@ -68,6 +68,43 @@ def test_bad_sizes_are_rejected_before_any_launch(lib):
     assert rc != 0 and b"workspace" in lib.lz_last_error()
 
 
+def test_layer_entry_points_reject_bad_arguments(lib):
+    p = ctypes.c_void_p(16)   # never dereferenced: validation fails first
+    fwd = lib.lz_layer_prologue_fwd
+    # B, L, heads, kv_heads, head_dim, feature_dim
+    assert fwd(p, p, p, p, p, p, p, 1, p, p, p, p, p, 1, 2, 40, 4, 3, 32, 8, None) != 0
+    assert b"multiple of kv_heads" in lib.lz_last_error()
+    assert fwd(p, p, p, p, p, p, p, 1, p, p, p, p, p, 1, 2, 40, 4, 2, 48, 8, None) != 0
+    assert b"head_dim" in lib.lz_last_error()
+    assert fwd(p, p, p, p, p, p, p, 1, p, p, p, p, p, 1, 2, 40, 4, 2, 64, 6, None) != 0
+    assert b"feature_dim" in lib.lz_last_error()
+    assert fwd(p, p, p, p, p, p, p, 1, p, p, p, p, p, 1, 2, 40, 4, 2, 128, 128, None) != 0
+    assert fwd(None, p, p, p, p, p, p, 1, p, p, p, p, p, 1, 2, 40, 4, 2, 32, 8, None) != 0
+    assert b"null" in lib.lz_last_error()
+    ws = lib.lz_layer_prologue_bwd_workspace_bytes(2, 40, 4, 2, 32, 8)
+    assert ws > 0
+    rc = lib.lz_layer_prologue_bwd(p, p, p, p, p, p, 1, p, p, p, p, p, None, p, p, p, p, p, 1,
+                                   2, 40, 4, 2, 32, 8, p, ws - 1, None)
+    assert rc != 0 and b"workspace" in lib.lz_last_error()
+    assert lib.lz_layer_combine_fwd(p, p, p, p, 1, 2, 4, 40, 12, None) != 0
+    assert b"multiple of 8" in lib.lz_last_error()
+    cws = lib.lz_layer_combine_bwd_workspace_bytes()
+    rc = lib.lz_layer_combine_bwd(p, p, p, p, p, p, 1, 2, 4, 40, 32, p, cws - 1, None)
+    assert rc != 0 and b"workspace" in lib.lz_last_error()
+
+
+@pytest.mark.parametrize("b, length, heads, kv, hd, f", [
+    (2, 40, 4, 2, 32, 8), (4, 4096, 32, 8, 64, 128), (1, 7, 8, 8, 128, 64)])
+def test_layer_prologue_workspace_sizes(lib, b, length, heads, kv, hd, f):
+    """Per-workgroup partial dW tiles [32 ceil-tiles(f), hd] fp32: one
+    workgroup per 128 rows of each role (q rows, kv rows), at most 256."""
+    nq = min(-(-b * length * heads // 128), 256)
+    nk = min(-(-b * length * kv // 128), 256)
+    fp = 32 if f <= 32 else (64 if f <= 64 else 128)
+    assert lib.lz_layer_prologue_bwd_workspace_bytes(b, length, heads, kv, hd, f) == \
+        4 * (nq + nk) * fp * hd
+
+
 def segments(bh, length, target=512, chunk=64):
     """The library's split of each (b, h) sequence into segments (so that
     B*H*segments fills the GPU): returns (segments, chunks per segment)."""

@@ -140,3 +140,97 @@ def test_small_llama_with_lizard_blocks_matches_oracle_model():
     for name, (a, b) in pairs.items():
         if name != "logits":
             assert errs[name] <= GRAD_TOL, (name, errs)
+
+
+# -- the fused prologue and epilogue on their own ------------------------------
+
+def prologue_reference(qp, kp, vp, wq, wk, cos, sin, heads, kv_heads):
+    """The reference's ops between the projections and the kernels
+    (src/lizard_attention.py:73-88), from the oracle's hedgehog and rope."""
+    b, length, _ = qp.shape
+    hd = qp.shape[-1] // heads
+
+    def split(x, n):
+        return x.view(b, length, n, hd).transpose(1, 2).repeat_interleave(heads // n, dim=1)
+    q, k, v = split(qp, heads), split(kp, kv_heads), split(vp, kv_heads)
+    c, s = ((t if t.dim() == 3 else t[None]) for t in (cos, sin))
+    c, s = c.unsqueeze(1), s.unsqueeze(1)
+    return (lo.hedgehog(q, wq), lo.hedgehog(k, wk), lo.rope(q, c, s), lo.rope(k, c, s), v)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("b, length, heads, kv, hd, f, batched", [
+    (2, 40, 4, 2, 32, 8, True), (1, 300, 8, 2, 64, 128, False), (2, 77, 4, 4, 64, 64, True),
+    (1, 129, 8, 1, 128, 64, True), (1, 50, 6, 3, 32, 12, False), (1, 33, 4, 2, 64, 100, True)])
+def test_prologue_matches_reference_ops(dtype, b, length, heads, kv, hd, f, batched):
+    """The fused prologue's outputs and, from the same fp32 upstream
+    gradients (v's given as two parts, one per attention branch), every
+    input gradient, against autograd through the reference's ops in fp64."""
+    g = torch.Generator().manual_seed(hd + f + length)
+    qp = torch.randn(b, length, heads * hd, generator=g).to(dtype)
+    kp = torch.randn(b, length, kv * hd, generator=g).to(dtype)
+    vp = torch.randn(b, length, kv * hd, generator=g).to(dtype)
+    wq = (0.3 * torch.randn(f, hd, generator=g)).to(dtype)
+    wk = (0.3 * torch.randn(f, hd, generator=g)).to(dtype)
+    cos, sin = lo.rope_cos_sin(length + 3, hd)
+    cos, sin = cos[3:], sin[3:]
+    if batched:
+        cos, sin = cos[None].repeat(b, 1, 1), sin[None].repeat(b, 1, 1)
+    cos, sin = cos.to(dtype), sin.to(dtype)
+    ups = [torch.randn(b, heads, length, n, generator=g) for n in (2 * f, 2 * f, hd, hd, hd, hd)]
+    *outs, saved = hip_layer.prologue_forward(*(t.cuda() for t in (qp, kp, vp, wq, wk, cos, sin)),
+                                              heads, kv)
+    grads = hip_layer.prologue_backward(saved, *(u.cuda() for u in ups))
+    torch.cuda.synchronize()
+    theirs = [t.detach().double().requires_grad_() for t in (qp, kp, vp, wq, wk)]
+    refs = prologue_reference(*theirs, cos.double(), sin.double(), heads, kv)
+    ref_ups = [u.double() for u in ups[:4]] + [(ups[4] + ups[5]).double()]
+    torch.autograd.backward(refs, ref_ups)
+    pairs = {n: (a, r) for n, a, r in zip(("fq", "fk", "qr", "kr", "v"), outs, refs)}
+    for n, a, r in zip(("dq", "dk", "dv", "dwq", "dwk"), grads, theirs):
+        pairs[n] = (a, r.grad)
+    errs = report(f"prologue {dtype} b={b} L={length} H={heads}/{kv} hd={hd} f={f}", pairs)
+    for n in ("fq", "fk", "qr", "kr", "v"):
+        assert pairs[n][0].dtype == torch.bfloat16 and errs[n] <= OUT_TOL, (n, errs)
+    for n in ("dq", "dk", "dv"):
+        assert pairs[n][0].dtype == dtype, n
+    for n in ("dq", "dk", "dv", "dwq", "dwk"):
+        assert errs[n] <= GRAD_TOL, (n, errs)
+    if dtype == torch.float32:
+        # fp32 inputs: the split bf16 products keep the gradients near fp32 accuracy
+        assert max(errs[n] for n in ("dq", "dk", "dv", "dwq", "dwk")) < 1e-4, errs
+
+
+def test_prologue_is_deterministic():
+    g = torch.Generator().manual_seed(5)
+    args = [torch.randn(*s, generator=g).bfloat16().cuda()
+            for s in ((2, 256, 512), (2, 256, 128), (2, 256, 128), (128, 64), (128, 64))]
+    cos, sin = (t.bfloat16().cuda() for t in lo.rope_cos_sin(256, 64))
+    ups = [torch.randn(2, 8, 256, n, generator=g).cuda() for n in (256, 256, 64, 64, 64)]
+    runs = []
+    for _ in range(2):
+        *outs, saved = hip_layer.prologue_forward(*args, cos, sin, 8, 2)
+        runs.append(outs + list(hip_layer.prologue_backward(saved, *ups)))
+    for a, b in zip(*runs):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_combine_matches_reference_ops(dtype):
+    """The blend + transpose against the reference's torch ops
+    (src/lizard_attention.py:94-97): bitwise equal output and branch
+    gradients, alpha's gradient up to the order of its sum."""
+    g = torch.Generator().manual_seed(7)
+    yg = torch.randn(2, 4, 70, 32, generator=g).bfloat16()
+    ys = torch.randn(2, 4, 70, 32, generator=g).bfloat16()
+    alpha = torch.tensor(0.7)
+    dout = torch.randn(2, 70, 128, generator=g).to(dtype)
+    out = hip_layer.combine_forward(yg.cuda(), ys.cuda(), alpha.reshape(1).cuda(), dtype)
+    dyg, dys, dalpha = hip_layer.combine_backward(dout.cuda(), ys.cuda(), alpha.reshape(1).cuda())
+    leaves = [t.detach().clone().requires_grad_() for t in (yg, ys, alpha)]
+    ref = (leaves[0].float() + leaves[2] * leaves[1].float()).to(dtype).transpose(1, 2).flatten(2)
+    ref.backward(dout)
+    assert out.dtype == dtype and torch.equal(out.cpu(), ref)
+    assert torch.equal(dyg.cpu(), leaves[0].grad)
+    assert torch.equal(dys.cpu(), leaves[1].grad)
+    assert abs(dalpha.item() - leaves[2].grad.item()) <= 1e-5 * abs(leaves[2].grad.item())
