@@ -109,6 +109,8 @@ def parse_args():
     p.add_argument("--no-layer", action="store_true", help="skip the config-5 layer stack")
     p.add_argument("--layer-only", action="store_true",
                    help="run only the config-5 layer stack (for profiling)")
+    p.add_argument("--one-layer", action="store_true",
+                   help="with --layer-only: only the single-layer part (for profiling)")
     p.add_argument("--copy-calibration", action="store_true",
                    help="also run a plain 1 GiB device copy, the reference kernel that "
                         "scales rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes")
@@ -179,7 +181,7 @@ def fwd_bwd_fn(torch, op, inputs, dy, extra=()):
     return run, reset
 
 
-def layer_stack(torch, steps, warmup):
+def layer_stack(torch, steps, warmup, one_layer=False):
     """training step (forward, cross-entropy, backward) of
     a Llama-3.2-1B-shaped model whose attention blocks are LizardAttention,
     and of one such layer alone; medians of per-step events."""
@@ -222,6 +224,8 @@ def layer_stack(torch, steps, warmup):
     del layer, xg, gy, rope, rotary
     torch.cuda.empty_cache()
     print(f"[bench] config5 one layer: {out}", file=sys.stderr, flush=True)
+    if one_layer:
+        return out
 
     model = LlamaForCausalLM(cfg).to(torch.bfloat16)
     to_lizard(model, **opts)
@@ -299,7 +303,9 @@ def main():
     _lib.load()
     torch.manual_seed(0)
     if args.layer_only:
-        print(json.dumps({"extra": {"config5_layer_stack": layer_stack(torch, 3, 1)}}), flush=True)
+        print(json.dumps({"extra": {"config5_layer_stack": layer_stack(torch, 3, 1,
+                                                                       args.one_layer)}}),
+              flush=True)
         return
 
     # ---- headline: GLA forward, B=16 H=32 L=2048 F=D=128, per-head gate -----

@@ -147,19 +147,19 @@ size_t lz_layer_prologue_bwd_workspace_bytes(int batch, int length, int heads, i
 
 /*
  * Layer prologue, backward: what autograd does for the same ops.
- *   dfq, dfk         f32 [B, heads, L, 2 feature_dim]  (gradients of fq, fk)
- *   dqr, dkr, dv     f32 [B, heads, L, head_dim]       (gradients of qr, kr, v_out)
- *   dv2              NULL or a second f32 gradient of v_out, added to dv (v_out
- *                    feeds both attention branches)
+ *   dfq, dfk         bf16 [B, heads, L, 2 feature_dim]  (gradients of fq, fk)
+ *   dqr, dkr, dv     bf16 [B, heads, L, head_dim]       (gradients of qr, kr, v_out)
+ *   dv2              NULL or a second bf16 gradient of v_out, added to dv in
+ *                    fp32 (v_out feeds both attention branches)
  *   dq               [B, L, heads, head_dim];  dk, dv_out [B, L, kv_heads, head_dim]
  *                    (summed over each kv head's query heads), bf16 if dtype_bf16 else f32
  *   dwq, dwk         f32 [feature_dim, head_dim]  (summed over every row, deterministically)
  * q, k, wq, wk, cos, sin as given to lz_layer_prologue_fwd.
  */
 int lz_layer_prologue_bwd(const void* q, const void* k, const void* wq, const void* wk,
-                          const void* cos, const void* sin, int cos_batched, const float* dfq,
-                          const float* dfk, const float* dqr, const float* dkr, const float* dv,
-                          const float* dv2, void* dq, void* dk, void* dv_out, float* dwq,
+                          const void* cos, const void* sin, int cos_batched, const void* dfq,
+                          const void* dfk, const void* dqr, const void* dkr, const void* dv,
+                          const void* dv2, void* dq, void* dk, void* dv_out, float* dwq,
                           float* dwk,
                           int dtype_bf16, int batch, int length, int heads, int kv_heads,
                           int head_dim, int feature_dim, void* workspace, size_t workspace_bytes,

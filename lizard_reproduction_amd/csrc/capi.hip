@@ -37,9 +37,9 @@ hipError_t launch_prologue_fwd(const void* q, const void* k, const void* v, cons
                                void* fk, void* qr, void* kr, void* vo, bool bf16_in, int B, int L,
                                int H, int Hkv, int hd, int f, int cos_bstride, hipStream_t st);
 hipError_t launch_prologue_bwd(const void* q, const void* k, const void* wq, const void* wk,
-                               const void* cos, const void* sin, const float* dfq,
-                               const float* dfk, const float* dqr, const float* dkr,
-                               const float* dv, const float* dv2, void* dq, void* dk, void* dvo,
+                               const void* cos, const void* sin, const void* dfq,
+                               const void* dfk, const void* dqr, const void* dkr,
+                               const void* dv, const void* dv2, void* dq, void* dk, void* dvo,
                                float* dwq, float* dwk, bool bf16_in, int B, int L, int H, int Hkv,
                                int hd, int f, int cos_bstride, float* ws, hipStream_t st);
 size_t combine_bwd_workspace();
@@ -209,6 +209,9 @@ static int check_layer(int batch, int length, int heads, int kv_heads, int head_
                 length, heads, kv_heads);
   if (heads % kv_heads)
     return fail(1, "layer: heads (%d) must be a multiple of kv_heads (%d)", heads, kv_heads);
+  if ((long long)batch * length * heads > (1LL << 31) - (1LL << 20))
+    return fail(1, "layer: B*L*heads = %lld rows exceeds the 2^31 - 2^20 row limit",
+                (long long)batch * length * heads);
   if (!lz::prologue_dims_supported(head_dim, feature_dim))
     return fail(1, "layer: unsupported head_dim %d / feature_dim %d (head_dim 32, 64 or 128; "
                    "feature_dim a multiple of 4 up to 128, up to 64 with head_dim 128)",
@@ -244,8 +247,8 @@ extern "C" size_t lz_layer_prologue_bwd_workspace_bytes(int batch, int length, i
 
 extern "C" int lz_layer_prologue_bwd(const void* q, const void* k, const void* wq, const void* wk,
                                      const void* cos, const void* sin, int cos_batched,
-                                     const float* dfq, const float* dfk, const float* dqr,
-                                     const float* dkr, const float* dv, const float* dv2,
+                                     const void* dfq, const void* dfk, const void* dqr,
+                                     const void* dkr, const void* dv, const void* dv2,
                                      void* dq, void* dk, void* dv_out, float* dwq, float* dwk,
                                      int dtype_bf16,
                                      int batch, int length, int heads, int kv_heads,

@@ -13,7 +13,7 @@
 // inputs are split into bf16 hi + lo parts and the three significant partial
 // products summed (hi*hi + lo*hi + hi*lo), which keeps fp32-level accuracy.
 //
-// Backward: the softmax Jacobians give dxw = p (dp - <p,dp>) - n (dn - <n,dn>)
+// Backward (from bf16 gradients of the five outputs): the softmax Jacobians give dxw = p (dp - <p,dp>) - n (dn - <n,dn>)
 // (p, n recomputed from x W^T), dq = dxw W + rope^T(dqr), and
 // dW = sum over rows of dxw^T q, reduced deterministically: per-workgroup
 // partial tiles in a workspace, then one fixed-order sum.
@@ -129,7 +129,7 @@ struct ProFwdArgs {
 
 struct ProBwdArgs {
   const void *q, *k, *wq, *wk, *cos, *sin;
-  const float *dfq, *dfk, *dqr, *dkr, *dv, *dv2;   // dv2 may be null
+  const bf16 *dfq, *dfk, *dqr, *dkr, *dv, *dv2;   // dv2 may be null
   void *dq, *dk, *dvo;
   float* part;
   int B, L, H, Hkv, hd, f, cos_bstride, nq_wg;
@@ -149,56 +149,63 @@ __device__ void load_weight(const T* __restrict__ w, int f, bf16* hi, bf16* lo) 
   }
 }
 
-// x W^T for the 32 rows of a wave: acc[ft] holds features 32 ft + acc_row(r, h)
-// (registers) of row lane % 32 (lanes).
+// Tile ft of x W^T for the 32 rows of a wave: features 32 ft + acc_row(r, h)
+// (registers) of row lane % 32 (lanes).  The kernels recompute a tile in each
+// pass that needs it rather than keep all of them live: the MFMA work is
+// small next to the memory traffic, and the registers buy occupancy.
 template <typename T, int FT, int HT>
-__device__ __forceinline__ void project(f32x16 (&acc)[FT], const bf16x8 (&xh)[Pro<T, FT, HT>::HK],
-                                        const bf16x8 (&xl)[Pro<T, FT, HT>::HK],
-                                        const bf16* w_hi, const bf16* w_lo, int lane) {
+__device__ __forceinline__ f32x16 project_tile(int ft, const bf16x8 (&xh)[Pro<T, FT, HT>::HK],
+                                               const bf16x8 (&xl)[Pro<T, FT, HT>::HK],
+                                               const bf16* w_hi, const bf16* w_lo, int lane) {
   using C = Pro<T, FT, HT>;
   const int h = lane >> 5;
+  f32x16 acc = zero16();
 #pragma unroll
-  for (int ft = 0; ft < FT; ++ft) {
-    acc[ft] = zero16();
-#pragma unroll
-    for (int kb = 0; kb < C::HK; ++kb) {
-      const bf16x8 a = row_operand(w_hi, C::WP, 32 * ft + (lane & 31), 16 * kb, h);
-      acc[ft] = mfma(a, xh[kb], acc[ft]);
-      if constexpr (C::SPLIT) {
-        acc[ft] = mfma(a, xl[kb], acc[ft]);
-        acc[ft] = mfma(row_operand(w_lo, C::WP, 32 * ft + (lane & 31), 16 * kb, h), xh[kb],
-                       acc[ft]);
-      }
+  for (int kb = 0; kb < C::HK; ++kb) {
+    const bf16x8 a = row_operand(w_hi, C::WP, 32 * ft + (lane & 31), 16 * kb, h);
+    acc = mfma(a, xh[kb], acc);
+    if constexpr (C::SPLIT) {
+      acc = mfma(a, xl[kb], acc);
+      acc = mfma(row_operand(w_lo, C::WP, 32 * ft + (lane & 31), 16 * kb, h), xh[kb], acc);
     }
   }
+  return acc;
 }
 
 // Row statistics of the two softmaxes over the valid features (< f):
 // maxima and reciprocal sums, combined over both lane halves.
-template <int FT>
-__device__ __forceinline__ void softmax_stats(const f32x16 (&acc)[FT], int f, int h, float& mp,
-                                              float& mn, float& ip, float& in) {
+template <typename T, int FT, int HT>
+__device__ __forceinline__ void softmax_stats(const bf16x8 (&xh)[Pro<T, FT, HT>::HK],
+                                              const bf16x8 (&xl)[Pro<T, FT, HT>::HK],
+                                              const bf16* w_hi, const bf16* w_lo, int f,
+                                              int lane, float& mp, float& mn, float& ip,
+                                              float& in) {
+  const int h = lane >> 5;
   mp = NEG_INF;
   mn = NEG_INF;
 #pragma unroll
-  for (int ft = 0; ft < FT; ++ft)
+  for (int ft = 0; ft < FT; ++ft) {
+    const f32x16 acc = project_tile<T, FT, HT>(ft, xh, xl, w_hi, w_lo, lane);
 #pragma unroll
     for (int r = 0; r < 16; ++r)
       if (32 * ft + acc_row(r, h) < f) {
-        mp = fmaxf(mp, acc[ft][r]);
-        mn = fmaxf(mn, -acc[ft][r]);
+        mp = fmaxf(mp, acc[r]);
+        mn = fmaxf(mn, -acc[r]);
       }
+  }
   mp = fmaxf(mp, xhalf(mp));
   mn = fmaxf(mn, xhalf(mn));
   float sp = 0.f, sn = 0.f;
 #pragma unroll
-  for (int ft = 0; ft < FT; ++ft)
+  for (int ft = 0; ft < FT; ++ft) {
+    const f32x16 acc = project_tile<T, FT, HT>(ft, xh, xl, w_hi, w_lo, lane);
 #pragma unroll
     for (int r = 0; r < 16; ++r)
       if (32 * ft + acc_row(r, h) < f) {
-        sp += fexp(acc[ft][r] - mp);
-        sn += fexp(-acc[ft][r] - mn);
+        sp += fexp(acc[r] - mp);
+        sn += fexp(-acc[r] - mn);
       }
+  }
   sp += xhalf(sp);
   sn += xhalf(sn);
   ip = 1.f / sp;
@@ -209,14 +216,32 @@ struct RowPos {
   int b, l, head;
 };
 
-__device__ __forceinline__ RowPos decode(long row, int L, int heads) {
-  const long bl = row / heads;
-  return RowPos{(int)(bl / L), (int)(bl % L), (int)(row % heads)};
+// row = (b L + l) heads + head (row counts stay below 2^31, checked by the host)
+__device__ __forceinline__ RowPos decode(int row, int L, int heads) {
+  const unsigned bl = (unsigned)row / (unsigned)heads;
+  const unsigned b = bl / (unsigned)L;
+  return RowPos{(int)b, (int)(bl - b * L), (int)(row - bl * heads)};
 }
 
-// Offset of row (b, head, l) of a [B, H, L, width] tensor.
-__device__ __forceinline__ long out_row(const RowPos& p, int head, int H, int L, int width) {
-  return (((long)p.b * H + head) * L + p.l) * width;
+
+// Half `half` of the 2f-wide feature rows of a wave's 32 rows, staged in LDS
+// ([32][pitch] bf16), to the rows' output heads in chunks of CH elements.
+// Row r's output base row (the obase of lane r, split in two ints) comes
+// from lane r by a cross-lane read.
+template <int CH>
+__device__ __forceinline__ void copy_rows(const bf16* stage, int pitch, bf16* __restrict__ out,
+                                          int ob_lo, int ob_hi, int row0, int nrows, int f,
+                                          int half, int group, int L, int lane) {
+  typedef __bf16 chunk_t __attribute__((ext_vector_type(CH)));
+  const int cpr = f / CH;
+  for (int i = lane; i < PRO_ROWS * cpr; i += 64) {
+    const int r = i / cpr, c = CH * (i - r * cpr);
+    const long base = ((long)__shfl(ob_hi, r) << 32) | (unsigned)__shfl(ob_lo, r);
+    if (row0 + r >= nrows) continue;
+    const chunk_t val = *reinterpret_cast<const chunk_t*>(stage + r * pitch + c);
+    for (int g = 0; g < group; ++g)
+      *reinterpret_cast<chunk_t*>(out + (base + (long)g * L) * (2 * f) + half * f + c) = val;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -236,7 +261,7 @@ __global__ __launch_bounds__(256) void prologue_fwd_kernel(ProFwdArgs a) {
   const int nwg = kv ? gridDim.x - a.nq_wg : a.nq_wg;
   const int heads_in = kv ? a.Hkv : a.H;
   const int group = kv ? a.H / a.Hkv : 1;
-  const long nrows = (long)a.B * a.L * heads_in;
+  const int nrows = a.B * a.L * heads_in;
   const T* x = static_cast<const T*>(kv ? a.k : a.q);
   bf16* fout = kv ? a.fk : a.fq;
   bf16* rout = kv ? a.kr : a.qr;
@@ -247,97 +272,97 @@ __global__ __launch_bounds__(256) void prologue_fwd_kernel(ProFwdArgs a) {
   load_weight<T, FT, HT>(static_cast<const T*>(kv ? a.wk : a.wq), f, w_hi, w_lo);
   __syncthreads();
 
-  for (long blk = wg; blk * PRO_BLOCK < nrows; blk += nwg) {
-    const long row0 = blk * PRO_BLOCK + wave * PRO_ROWS;
-    const long row = row0 + (lane & 31);
+  for (int blk = wg; blk * PRO_BLOCK < nrows; blk += nwg) {
+    const int row0 = blk * PRO_BLOCK + wave * PRO_ROWS;
+    const int row = row0 + (lane & 31);
     const bool live = row < nrows;
     const RowPos pos = decode(live ? row : 0, a.L, heads_in);
+    // [B, H, L, .] row of this row's first output head; the group's next heads
+    // are L rows apart
+    const long obase = ((long)pos.b * a.H + pos.head * group) * a.L + pos.l;
 
-    float xf[C::HK][8];
     bf16x8 xh[C::HK], xl[C::HK];
+    {
+      float xf[C::HK][8];
 #pragma unroll
-    for (int kb = 0; kb < C::HK; ++kb) {
-      if (live) {
-        load8f(x + row * hd + 16 * kb + 8 * h, xf[kb]);
-      } else {
+      for (int kb = 0; kb < C::HK; ++kb) {
+        if (live) {
+          load8f(x + (long)row * hd + 16 * kb + 8 * h, xf[kb]);
+        } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) xf[kb][e] = 0.f;
+          for (int e = 0; e < 8; ++e) xf[kb][e] = 0.f;
+        }
       }
-      xh[kb] = to_bf8(xf[kb]);
-      if constexpr (C::SPLIT) xl[kb] = low8(xf[kb], xh[kb]);
+      // RoPE (and the kv heads' v) from the fp32 row values: column
+      // m = 16 kb + 8 h + e pairs with m + hd/2, the same column of kb + HK/2
+      if (live) {
+        const long tab = ((long)pos.b * a.cos_bstride + pos.l) * hd;
+#pragma unroll
+        for (int kb = 0; kb < C::HK / 2; ++kb) {
+          const int kb2 = kb + C::HK / 2;
+          float c1[8], s1[8], c2[8], s2[8];
+          load8f(cs + tab + 16 * kb + 8 * h, c1);
+          load8f(sn + tab + 16 * kb + 8 * h, s1);
+          load8f(cs + tab + 16 * kb2 + 8 * h, c2);
+          load8f(sn + tab + 16 * kb2 + 8 * h, s2);
+          bf16x8 o1, o2;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            o1[e] = to_bf16(xf[kb][e] * c1[e] - xf[kb2][e] * s1[e]);
+            o2[e] = to_bf16(xf[kb2][e] * c2[e] + xf[kb][e] * s2[e]);
+          }
+          for (int g = 0; g < group; ++g) {
+            bf16* dst = rout + (obase + (long)g * a.L) * hd;
+            *reinterpret_cast<bf16x8*>(dst + 16 * kb + 8 * h) = o1;
+            *reinterpret_cast<bf16x8*>(dst + 16 * kb2 + 8 * h) = o2;
+          }
+        }
+        if (kv) {
+          const T* vrow = static_cast<const T*>(a.v) + (long)row * hd;
+#pragma unroll
+          for (int kb = 0; kb < C::HK; ++kb) {
+            float vf[8];
+            load8f(vrow + 16 * kb + 8 * h, vf);
+            const bf16x8 o = to_bf8(vf);
+            for (int g = 0; g < group; ++g)
+              *reinterpret_cast<bf16x8*>(a.vo + (obase + (long)g * a.L) * hd + 16 * kb + 8 * h) =
+                  o;
+          }
+        }
+      }
+#pragma unroll
+      for (int kb = 0; kb < C::HK; ++kb) {
+        xh[kb] = to_bf8(xf[kb]);
+        if constexpr (C::SPLIT) xl[kb] = low8(xf[kb], xh[kb]);
+      }
     }
-    f32x16 acc[FT];
-    project<T, FT, HT>(acc, xh, xl, w_hi, w_lo, lane);
     float mp, mn, ip, in;
-    softmax_stats<FT>(acc, f, h, mp, mn, ip, in);
+    softmax_stats<T, FT, HT>(xh, xl, w_hi, w_lo, f, lane, mp, mn, ip, in);
 
     // the two halves of the feature row, staged through LDS for row-contiguous stores
+    const int ob_lo = (int)(obase & 0xffffffff), ob_hi = (int)(obase >> 32);
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
 #pragma unroll
-      for (int ft = 0; ft < FT; ++ft)
+      for (int ft = 0; ft < FT; ++ft) {
+        const f32x16 acc = project_tile<T, FT, HT>(ft, xh, xl, w_hi, w_lo, lane);
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4) {
           bf16x4 o;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const float s = acc[ft][4 * q4 + e];
+            const float s = acc[4 * q4 + e];
             o[e] = to_bf16(half == 0 ? fexp(s - mp) * ip : fexp(-s - mn) * in);
           }
           *reinterpret_cast<bf16x4*>(stage + (lane & 31) * C::SP + 32 * ft + 8 * q4 + 4 * h) = o;
         }
-      wave_sync();
-      const int cpr = f / 4;   // 4-element chunks per half row
-      for (int i = lane; i < PRO_ROWS * cpr; i += 64) {
-        const int r = i / cpr, c = 4 * (i % cpr);
-        const long grow = row0 + r;
-        if (grow >= nrows) continue;
-        const RowPos p = decode(grow, a.L, heads_in);
-        const bf16x4 val = *reinterpret_cast<const bf16x4*>(stage + r * C::SP + c);
-        for (int g = 0; g < group; ++g) {
-          bf16* dst = fout + out_row(p, p.head * group + g, a.H, a.L, F2) + half * f + c;
-          *reinterpret_cast<bf16x4*>(dst) = val;
-        }
       }
       wave_sync();
-    }
-
-    // RoPE (and the kv heads' v), from the fp32 row values held in registers:
-    // column m = 16 kb + 8 h + e pairs with m + hd/2 = column of kb + HK/2.
-    if (live) {
-      const long tab = ((long)pos.b * a.cos_bstride + pos.l) * hd;
-#pragma unroll
-      for (int kb = 0; kb < C::HK / 2; ++kb) {
-        const int kb2 = kb + C::HK / 2;
-        float c1[8], s1[8], c2[8], s2[8];
-        load8f(cs + tab + 16 * kb + 8 * h, c1);
-        load8f(sn + tab + 16 * kb + 8 * h, s1);
-        load8f(cs + tab + 16 * kb2 + 8 * h, c2);
-        load8f(sn + tab + 16 * kb2 + 8 * h, s2);
-        bf16x8 o1, o2;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          o1[e] = to_bf16(xf[kb][e] * c1[e] - xf[kb2][e] * s1[e]);
-          o2[e] = to_bf16(xf[kb2][e] * c2[e] + xf[kb][e] * s2[e]);
-        }
-        for (int g = 0; g < group; ++g) {
-          bf16* dst = rout + out_row(pos, pos.head * group + g, a.H, a.L, hd);
-          *reinterpret_cast<bf16x8*>(dst + 16 * kb + 8 * h) = o1;
-          *reinterpret_cast<bf16x8*>(dst + 16 * kb2 + 8 * h) = o2;
-        }
-      }
-      if (kv) {
-        const T* vrow = static_cast<const T*>(a.v) + row * hd;
-#pragma unroll
-        for (int kb = 0; kb < C::HK; ++kb) {
-          float vf[8];
-          load8f(vrow + 16 * kb + 8 * h, vf);
-          const bf16x8 o = to_bf8(vf);
-          for (int g = 0; g < group; ++g)
-            *reinterpret_cast<bf16x8*>(a.vo + out_row(pos, pos.head * group + g, a.H, a.L, hd) +
-                                       16 * kb + 8 * h) = o;
-        }
-      }
+      if (f % 8 == 0)
+        copy_rows<8>(stage, C::SP, fout, ob_lo, ob_hi, row0, nrows, f, half, group, a.L, lane);
+      else
+        copy_rows<4>(stage, C::SP, fout, ob_lo, ob_hi, row0, nrows, f, half, group, a.L, lane);
+      wave_sync();
     }
   }
 }
@@ -364,10 +389,10 @@ __global__ __launch_bounds__(256) void prologue_bwd_kernel(ProBwdArgs a) {
   const int nwg = kv ? gridDim.x - a.nq_wg : a.nq_wg;
   const int heads_in = kv ? a.Hkv : a.H;
   const int group = kv ? a.H / a.Hkv : 1;
-  const long nrows = (long)a.B * a.L * heads_in;
+  const int nrows = a.B * a.L * heads_in;
   const T* x = static_cast<const T*>(kv ? a.k : a.q);
-  const float* dphi = kv ? a.dfk : a.dfq;
-  const float* drope = kv ? a.dkr : a.dqr;
+  const bf16* dphi = kv ? a.dfk : a.dfq;
+  const bf16* drope = kv ? a.dkr : a.dqr;
   T* dx = static_cast<T*>(kv ? a.dk : a.dq);
   const T* cs = static_cast<const T*>(a.cos);
   const T* sn = static_cast<const T*>(a.sin);
@@ -379,17 +404,19 @@ __global__ __launch_bounds__(256) void prologue_bwd_kernel(ProBwdArgs a) {
 #pragma unroll
   for (int i = 0; i < OWN; ++i) dw[i] = zero16();
 
-  for (long blk = wg; blk * PRO_BLOCK < nrows; blk += nwg) {
-    const long row = blk * PRO_BLOCK + lrow;
+  for (int blk = wg; blk * PRO_BLOCK < nrows; blk += nwg) {
+    const int row = blk * PRO_BLOCK + lrow;
     const bool live = row < nrows;
     const RowPos pos = decode(live ? row : 0, a.L, heads_in);
+    // [B, H, L, .] row of this row's first head; the group's heads are L rows apart
+    const long obase = ((long)pos.b * a.H + pos.head * group) * a.L + pos.l;
 
     bf16x8 xh[C::HK], xl[C::HK];
 #pragma unroll
     for (int kb = 0; kb < C::HK; ++kb) {
       float xf[8];
       if (live) {
-        load8f(x + row * hd + 16 * kb + 8 * h, xf);
+        load8f(x + (long)row * hd + 16 * kb + 8 * h, xf);
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e) xf[e] = 0.f;
@@ -402,52 +429,56 @@ __global__ __launch_bounds__(256) void prologue_bwd_kernel(ProBwdArgs a) {
       }
     }
     __syncthreads();   // W tiles (first pass) and nothing else pending
-    f32x16 acc[FT];
-    project<T, FT, HT>(acc, xh, xl, w_hi, w_lo, lane);
     float mp, mn, ip, in;
-    softmax_stats<FT>(acc, f, h, mp, mn, ip, in);
+    softmax_stats<T, FT, HT>(xh, xl, w_hi, w_lo, f, lane, mp, mn, ip, in);
 
     // u = p dp - n dn per feature; s_p = <p, dp>, s_n = <n, dn>
     f32x16 dxw[FT];
     float s_p = 0.f, s_n = 0.f;
 #pragma unroll
-    for (int ft = 0; ft < FT; ++ft)
+    for (int ft = 0; ft < FT; ++ft) {
+      f32x4 dp[4], dn[4];
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
         const int c = 32 * ft + 8 * q4 + 4 * h;
-        f32x4 dp = {0.f, 0.f, 0.f, 0.f}, dn = dp;
+        dp[q4] = f32x4{0.f, 0.f, 0.f, 0.f};
+        dn[q4] = dp[q4];
         if (live && c < f) {
           for (int g = 0; g < group; ++g) {
-            const float* src = dphi + out_row(pos, pos.head * group + g, a.H, a.L, F2);
-            dp += *reinterpret_cast<const f32x4*>(src + c);
-            dn += *reinterpret_cast<const f32x4*>(src + f + c);
+            const bf16* src = dphi + (obase + (long)g * a.L) * F2;
+            dp[q4] += load4f(src + c);
+            dn[q4] += load4f(src + f + c);
           }
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int r = 4 * q4 + e;
-          float u = 0.f;
-          if (c < f) {
-            const float p = fexp(acc[ft][r] - mp) * ip;
-            const float n = fexp(-acc[ft][r] - mn) * in;
-            u = p * dp[e] - n * dn[e];
-            s_p += p * dp[e];
-            s_n += n * dn[e];
-          }
-          dxw[ft][r] = u;
         }
       }
+      const f32x16 acc = project_tile<T, FT, HT>(ft, xh, xl, w_hi, w_lo, lane);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float u = 0.f;
+        if (32 * ft + acc_row(r, h) < f) {
+          const float p = fexp(acc[r] - mp) * ip;
+          const float n = fexp(-acc[r] - mn) * in;
+          const float pd = p * dp[r >> 2][r & 3], nd = n * dn[r >> 2][r & 3];
+          u = pd - nd;
+          s_p += pd;
+          s_n += nd;
+        }
+        dxw[ft][r] = u;
+      }
+    }
     s_p += xhalf(s_p);
     s_n += xhalf(s_n);
 #pragma unroll
-    for (int ft = 0; ft < FT; ++ft)
+    for (int ft = 0; ft < FT; ++ft) {
+      const f32x16 acc = project_tile<T, FT, HT>(ft, xh, xl, w_hi, w_lo, lane);
 #pragma unroll
       for (int r = 0; r < 16; ++r)
         if (32 * ft + acc_row(r, h) < f) {
-          const float p = fexp(acc[ft][r] - mp) * ip;
-          const float n = fexp(-acc[ft][r] - mn) * in;
+          const float p = fexp(acc[r] - mp) * ip;
+          const float n = fexp(-acc[r] - mn) * in;
           dxw[ft][r] += n * s_n - p * s_p;
         }
+    }
 
     // dx_phi^T = W^T dxw^T: hd rows (registers), this wave's rows (lanes)
     f32x16 dacc[HT];
@@ -468,6 +499,23 @@ __global__ __launch_bounds__(256) void prologue_bwd_kernel(ProBwdArgs a) {
         }
     }
 
+    // dxw hi into the LDS tile now, lo kept as bf16 until the tile is free:
+    // the fp32 dxw dies here
+    bf16x4 dlo[FT][4];
+#pragma unroll
+    for (int ft = 0; ft < FT; ++ft)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        bf16x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float v = dxw[ft][4 * q4 + e];
+          o[e] = to_bf16(v);
+          dlo[ft][q4][e] = to_bf16(v - to_f32(o[e]));
+        }
+        *reinterpret_cast<bf16x4*>(d_l + lrow * C::DP + 32 * ft + 8 * q4 + 4 * h) = o;
+      }
+
     // dx = dx_phi + rope^T(drope): dx[m] = dr[m] cos[m] + dr[m + hd/2] sin[m + hd/2]
     // for m < hd/2, dr[m] cos[m] - dr[m - hd/2] sin[m - hd/2] otherwise
     // (drope summed over the group's heads); the kv rows also sum dv.
@@ -482,12 +530,12 @@ __global__ __launch_bounds__(256) void prologue_bwd_kernel(ProBwdArgs a) {
           const float sign = m < half_hd ? 1.f : -1.f;
           f32x4 dr = {0.f, 0.f, 0.f, 0.f}, dr2 = dr, dvs = dr;
           for (int g = 0; g < group; ++g) {
-            const long o = out_row(pos, pos.head * group + g, a.H, a.L, hd);
-            dr += *reinterpret_cast<const f32x4*>(drope + o + m);
-            dr2 += *reinterpret_cast<const f32x4*>(drope + o + mp2);
+            const long o = (obase + (long)g * a.L) * hd;
+            dr += load4f(drope + o + m);
+            dr2 += load4f(drope + o + mp2);
             if (kv) {
-              dvs += *reinterpret_cast<const f32x4*>(a.dv + o + m);
-              if (a.dv2) dvs += *reinterpret_cast<const f32x4*>(a.dv2 + o + m);
+              dvs += load4f(a.dv + o + m);
+              if (a.dv2) dvs += load4f(a.dv2 + o + m);
             }
           }
           const f32x4 c = load4f(cs + tab + m), s2 = load4f(sn + tab + mp2);
@@ -495,27 +543,22 @@ __global__ __launch_bounds__(256) void prologue_bwd_kernel(ProBwdArgs a) {
 #pragma unroll
           for (int e = 0; e < 4; ++e)
             out[e] = dacc[ht][4 * q4 + e] + dr[e] * c[e] + sign * dr2[e] * s2[e];
-          store4v(dx + row * hd + m, out);
-          if (kv) store4v(static_cast<T*>(a.dvo) + row * hd + m, dvs);
+          store4v(dx + (long)row * hd + m, out);
+          if (kv) store4v(static_cast<T*>(a.dvo) + (long)row * hd + m, dvs);
         }
     }
 
     // dW += dxw^T x over the workgroup's 128 rows: dxw hi, then lo, through LDS
 #pragma unroll
     for (int part = 0; part < 2; ++part) {
+      if (part == 1) {
 #pragma unroll
-      for (int ft = 0; ft < FT; ++ft)
+        for (int ft = 0; ft < FT; ++ft)
 #pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-          bf16x4 o;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float v = dxw[ft][4 * q4 + e];
-            const bf16 hi = to_bf16(v);
-            o[e] = part == 0 ? hi : to_bf16(v - to_f32(hi));
-          }
-          *reinterpret_cast<bf16x4*>(d_l + lrow * C::DP + 32 * ft + 8 * q4 + 4 * h) = o;
-        }
+          for (int q4 = 0; q4 < 4; ++q4)
+            *reinterpret_cast<bf16x4*>(d_l + lrow * C::DP + 32 * ft + 8 * q4 + 4 * h) =
+                dlo[ft][q4];
+      }
       __syncthreads();
 #pragma unroll
       for (int i = 0; i < OWN; ++i) {
@@ -549,22 +592,38 @@ __global__ __launch_bounds__(256) void prologue_bwd_kernel(ProBwdArgs a) {
   }
 }
 
-// dW[i][c] = sum over a role's workgroups of their partials, in workgroup order.
+// dW[i][c] = sum over a role's workgroups of their partials.  A block takes 64
+// consecutive (i, c) entries; its 4 waves sum interleaved quarters of the
+// workgroups (8 independent loads in flight per lane), then wave 0 adds the
+// four quarter sums in a fixed order: deterministic.
 __global__ __launch_bounds__(256) void prologue_dw_reduce_kernel(const float* __restrict__ part,
                                                                  float* __restrict__ dwq,
                                                                  float* __restrict__ dwk,
                                                                  int nq, int nk, int FP, int HP,
                                                                  int f, int hd) {
-  const int idx = blockIdx.x * 256 + threadIdx.x;
+  __shared__ float red[4][64];
   const bool kv = blockIdx.y == 1;
-  if (idx >= f * hd) return;
-  const int i = idx / hd, c = idx % hd;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int idx = blockIdx.x * 64 + lane;
   const int w0 = kv ? nq : 0, n = kv ? nk : nq;
   const size_t stride = (size_t)FP * HP;
-  const float* p = part + (size_t)w0 * stride + (size_t)i * HP + c;
   float s = 0.f;
-  for (int w = 0; w < n; ++w) s += p[w * stride];
-  (kv ? dwk : dwq)[idx] = s;
+  if (idx < f * hd) {
+    const int i = idx / hd, c = idx % hd;
+    const float* p = part + (size_t)w0 * stride + (size_t)i * HP + c;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    int w = wave;
+    for (; w + 28 < n; w += 32) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] += p[(size_t)(w + 4 * j) * stride];
+    }
+    for (int j = 0; w < n; w += 4, ++j) acc[j & 7] += p[(size_t)w * stride];
+    s = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+  }
+  red[wave][lane] = s;
+  __syncthreads();
+  if (wave == 0 && idx < f * hd)
+    (kv ? dwk : dwq)[idx] = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
 }
 
 // ---------------------------------------------------------------------------
@@ -705,7 +764,7 @@ static hipError_t launch_bwd_t(const ProBwdArgs& a, float* dwq, float* dwk, int 
                      a);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(prologue_dw_reduce_kernel, dim3((unsigned)ceil_div((long)a.f * a.hd, 256), 2),
+  hipLaunchKernelGGL(prologue_dw_reduce_kernel, dim3((unsigned)ceil_div((long)a.f * a.hd, 64), 2),
                      dim3(256), 0, st, a.part, dwq, dwk, nq, nk, C::FP, C::HP, a.f, a.hd);
   return hipGetLastError();
 }
@@ -755,14 +814,17 @@ hipError_t launch_prologue_fwd(const void* q, const void* k, const void* v, cons
 }
 
 hipError_t launch_prologue_bwd(const void* q, const void* k, const void* wq, const void* wk,
-                               const void* cos, const void* sin, const float* dfq,
-                               const float* dfk, const float* dqr, const float* dkr,
-                               const float* dv, const float* dv2, void* dq, void* dk, void* dvo,
+                               const void* cos, const void* sin, const void* dfq,
+                               const void* dfk, const void* dqr, const void* dkr,
+                               const void* dv, const void* dv2, void* dq, void* dk, void* dvo,
                                float* dwq, float* dwk, bool bf16_in, int B, int L, int H, int Hkv,
                                int hd, int f, int cos_bstride, float* ws, hipStream_t st) {
   int nq, nk;
   prologue_grid(B, L, H, Hkv, &nq, &nk);
-  ProBwdArgs a{q, k, wq, wk, cos, sin, dfq, dfk, dqr, dkr, dv, dv2, dq, dk, dvo, ws,
+  ProBwdArgs a{q, k, wq, wk, cos, sin, static_cast<const bf16*>(dfq),
+               static_cast<const bf16*>(dfk), static_cast<const bf16*>(dqr),
+               static_cast<const bf16*>(dkr), static_cast<const bf16*>(dv),
+               static_cast<const bf16*>(dv2), dq, dk, dvo, ws,
                B, L, H, Hkv, hd, f, cos_bstride, nq};
   return bf16_in ? dispatch_shape<bf16, BwdLaunch>(hd, f, a, dwq, dwk, nq, nk, st)
                  : dispatch_shape<float, BwdLaunch>(hd, f, a, dwq, dwk, nq, nk, st);

@@ -17,11 +17,10 @@ The layer computes, per token (``src/lizard_attention.py:78-97``):
 
 with everything after the projections in promote(x.dtype, fp32).  The
 projections and the gate logit are torch GEMMs; everything from the
-projection outputs to o_proj's input runs in four HIP launches (forward):
-the fused prologue (GQA expand, Hedgehog feature maps, RoPE and the bf16
-casts, one pass over q/k/v), the GLA and SWA kernels, and the fused blend +
-transpose.  The kernels hand fp32 gradients back to the prologue, as the
-reference's fp32 intermediates get them.
+projection outputs to o_proj's input runs on HIP kernels: the fused
+prologue (GQA expand, Hedgehog feature maps, RoPE and the bf16 casts, one
+pass over q/k/v), the GLA and SWA kernels, and the fused blend + transpose,
+one autograd node for all of them (``_Core``).
 """
 import functools
 
@@ -100,11 +99,13 @@ def prologue_forward(qp, kp, vp, wq, wk, cos, sin, heads, kv_heads):
 
 
 def prologue_backward(saved, dfq, dfk, dqr, dkr, dv, dv2=None):
-    """One ``lz_layer_prologue_bwd`` launch from fp32 gradients of fq, fk, qr,
-    kr and v (dv2: an optional second gradient of v); returns dq, dk, dv of
-    the projection outputs (in the arithmetic dtype) and dWq, dWk (fp32)."""
+    """One ``lz_layer_prologue_bwd`` launch from the gradients of fq, fk, qr,
+    kr and v (taken as bf16; dv2: an optional second gradient of v, added in
+    fp32); returns dq, dk, dv of the projection outputs (in the arithmetic
+    dtype) and dWq, dWk (fp32)."""
     qp, kp, wq, wk, cos, sin, (b, length, heads, kv, hd, f, batched) = saved
-    grads = [None if g is None else g.float().contiguous() for g in (dfq, dfk, dqr, dkr, dv, dv2)]
+    grads = [None if g is None else g.to(torch.bfloat16).contiguous()
+             for g in (dfq, dfk, dqr, dkr, dv, dv2)]
     dq, dk, dvp = torch.empty_like(qp), torch.empty_like(kp), torch.empty_like(kp)
     dwq = torch.empty(wq.shape, device=wq.device, dtype=torch.float32)
     dwk = torch.empty_like(dwq)
@@ -152,9 +153,11 @@ def combine_backward(dout, ys, alpha):
 class _Core(torch.autograd.Function):
     """Everything from the projection outputs to o_proj's input as one
     autograd node (src/lizard_attention.py:73-97): prologue, GLA, SWA and
-    the blend, forward and backward.  Inside it the kernels pass each other
-    fp32 gradients of the fp32 intermediates the reference's layer has (its
-    fq, fk, q, k, v are fp32, so its kernels return fp32 gradients)."""
+    the blend, forward and backward.  The kernels hand each other bf16
+    gradients of their bf16 operands (the reference's layer keeps fp32 ones
+    for its fp32 intermediates): half the bytes on the backward's largest
+    streams, for one extra bf16 rounding of each gradient (2^-9 relative,
+    the size of the rounding its bf16 projections already take)."""
 
     @staticmethod
     def forward(ctx, qp, kp, vp, wq, wk, log_gamma, meta, alpha, cos, sin, heads, kv_heads,
@@ -184,10 +187,10 @@ class _Core(torch.autograd.Function):
         saved = tuple(saved) + (ctx.sizes,)
         odt = torch.bfloat16 if dout.dtype == torch.bfloat16 else torch.float32
         dyg, dys, dalpha = combine_backward(dout.to(odt).contiguous(), y_swa, alpha32)
-        f32 = torch.float32
-        dfq, dfk, dv_gla, dlg = kernels.gla_backward(fq, fk, v, lg, dyg, ctx.state, f32)
+        bf = torch.bfloat16
+        dfq, dfk, dv_gla, dlg = kernels.gla_backward(fq, fk, v, lg, dyg, ctx.state, bf)
         dqr, dkr, dv_swa, dmeta = kernels.swa_backward(qr, kr, v, meta32, lse, dys, ctx.window,
-                                                       f32)
+                                                       bf)
         dq, dk, dvp, dwq, dwk = prologue_backward(saved, dfq, dfk, dqr, dkr, dv_gla, dv_swa)
         grads = (dq, dk, dvp, dwq, dwk, dlg, dmeta, dalpha.reshape(()))
         return tuple(g.to(d) for g, d in zip(grads, ctx.dtypes)) + (None,) * 6

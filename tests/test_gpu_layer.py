@@ -163,9 +163,9 @@ def prologue_reference(qp, kp, vp, wq, wk, cos, sin, heads, kv_heads):
     (2, 40, 4, 2, 32, 8, True), (1, 300, 8, 2, 64, 128, False), (2, 77, 4, 4, 64, 64, True),
     (1, 129, 8, 1, 128, 64, True), (1, 50, 6, 3, 32, 12, False), (1, 33, 4, 2, 64, 100, True)])
 def test_prologue_matches_reference_ops(dtype, b, length, heads, kv, hd, f, batched):
-    """The fused prologue's outputs and, from the same fp32 upstream
-    gradients (v's given as two parts, one per attention branch), every
-    input gradient, against autograd through the reference's ops in fp64."""
+    """The fused prologue's outputs and, from the same upstream gradients
+    (v's given as two parts, one per attention branch), every input
+    gradient, against autograd through the reference's ops in fp64."""
     g = torch.Generator().manual_seed(hd + f + length)
     qp = torch.randn(b, length, heads * hd, generator=g).to(dtype)
     kp = torch.randn(b, length, kv * hd, generator=g).to(dtype)
@@ -177,7 +177,9 @@ def test_prologue_matches_reference_ops(dtype, b, length, heads, kv, hd, f, batc
     if batched:
         cos, sin = cos[None].repeat(b, 1, 1), sin[None].repeat(b, 1, 1)
     cos, sin = cos.to(dtype), sin.to(dtype)
-    ups = [torch.randn(b, heads, length, n, generator=g) for n in (2 * f, 2 * f, hd, hd, hd, hd)]
+    # the prologue takes its upstream gradients in bf16: bf16-valued ones here
+    ups = [torch.randn(b, heads, length, n, generator=g).bfloat16().float()
+           for n in (2 * f, 2 * f, hd, hd, hd, hd)]
     *outs, saved = hip_layer.prologue_forward(*(t.cuda() for t in (qp, kp, vp, wq, wk, cos, sin)),
                                               heads, kv)
     grads = hip_layer.prologue_backward(saved, *(u.cuda() for u in ups))
