@@ -7,17 +7,16 @@
 //   B (16 x 32):  lane holds col  l % 32, k-slots j = 0..7
 //   D (32 x 32):  lane holds col  l % 32, register r holds row acc_row(r, h)
 // The hardware pairs k-slot j of A with k-slot j of B; which k index a slot
-// carries is a free choice as long as A and B agree.  This code uses
-//   slot j of lane half h  <->  k = 8*(j/4) + 4*h + (j%4)   (within a 16-block)
-// because that is exactly the row order of an accumulator: registers
-// 8*kb .. 8*kb+7 of a 32x32 accumulator are the A/B operand of the k-block kb
-// of a following product that contracts over the accumulator's rows.  So
-// scores never leave registers on their way to P*V, and the GLA state never
-// leaves registers on its way to Q~ S.
-//
-// LDS tiles store each 16-element k-block in "slot order" (storage position
-// pidx(k), bits 2 and 3 of k swapped), so one 16-byte read at storage offset
-// 16*kb + 8*h yields the operand of k-block kb for lane half h.
+// carries is a free choice as long as A and B agree.  Two orders are used:
+//   * accumulator order, slot j of lane half h <-> k = 8*(j/4) + 4*h + (j%4)
+//     (within a 16-block): the row order of an accumulator, so registers
+//     8*kb .. 8*kb+7 of a 32x32 accumulator are the operand of k-block kb of a
+//     following product that contracts over the accumulator's rows.  Scores
+//     never leave registers on their way to P*V, nor the GLA state on its way
+//     to Q~ S.  LDS operands paired with them come from row_operand_acc or,
+//     contracting down the rows of a tile, from tr_operand (transpose reads);
+//   * contiguous order, slot j <-> k = 8*h + j: row_operand, for products
+//     whose two operands both come from row-major tiles or global rows.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -43,11 +42,6 @@ __device__ __forceinline__ f32x16 mfma(const bf16x8& a, const bf16x8& b, const f
 // Row (M index) held by accumulator register r in lane half h.
 __host__ __device__ __forceinline__ constexpr int acc_row(int r, int h) {
   return ((r >> 2) << 3) + (h << 2) + (r & 3);
-}
-
-// Storage position of k inside its 16-block: swap bits 2 and 3 (an involution).
-__host__ __device__ __forceinline__ constexpr int pidx(int k) {
-  return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1);
 }
 
 __device__ __forceinline__ float fexp(float x) { return __builtin_amdgcn_exp2f(x * LOG2E); }

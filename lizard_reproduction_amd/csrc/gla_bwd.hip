@@ -31,7 +31,8 @@
 //      contracts the state over f straight from the accumulators, dfk over d
 //      through LDS transpose reads); writes dv, dfk and dG.
 //   gate: d log_gamma = reverse cumsum of dG over L (head-summed for a
-//      per-token gate), two small launches (block totals, then block scans).
+//      per-token gate), one launch (gla_gate_grad_kernel) from dG and the
+//      per-chunk dG totals kernel B writes.
 // Operand staging follows gla_fwd.hip: row-major tiles in LDS, operands that
 // contract over tokens from LDS transpose reads, next chunk prefetched into
 // registers.
