@@ -51,18 +51,72 @@ struct BwdCommon {
 };
 
 // ============================================================================
+// Both walks run eight waves (512 threads) per workgroup: a chunk's LDS
+// leaves room for one workgroup per CU, so the second wave per SIMD comes
+// from inside it.  Chunk tiles are loaded and stored by all 512 threads.
+// ============================================================================
+constexpr int B_WAVES = 8;
+constexpr int B_THREADS = 64 * B_WAVES;
+
+// Rows [t0, t0+64) of a [L x ncols] bf16 matrix into registers by B_THREADS
+// threads (item idx = tid + B_THREADS i: row idx / (KP/8), 8 columns), zero
+// outside the matrix; items past the tile are skipped.
+template <int KP, int N>
+__device__ __forceinline__ void load_tile8(uint4 (&reg)[N], const bf16* __restrict__ base, int t0,
+                                           int L, int ncols, bool vec) {
+  constexpr int K8 = KP / 8, ITEMS = GLA_C * K8;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const int idx = threadIdx.x + B_THREADS * i;
+    if (ITEMS % B_THREADS == 0 || idx < ITEMS)
+      reg[i] = gload8(base, t0 + idx / K8, (idx % K8) * 8, L, ncols, vec);
+  }
+}
+
+template <int KP, int N>
+__device__ __forceinline__ void store_tile8(const uint4 (&reg)[N], bf16* tile, int pitch) {
+  constexpr int K8 = KP / 8, ITEMS = GLA_C * K8;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const int idx = threadIdx.x + B_THREADS * i;
+    if (ITEMS % B_THREADS == 0 || idx < ITEMS)
+      *reinterpret_cast<uint4*>(tile + (idx / K8) * pitch + (idx % K8) * 8) = reg[i];
+  }
+}
+
+// ============================================================================
 // kernel A: forward walk -> dfq, den, delta, p = fq . dfq
+//
+//   phase 1  waves 0-3: the score tile (keys kt x queries qt) a^T and v dy^T,
+//            the decay, sum_t a and sum_t a (v . dy); waves 4-7: Q~ . z and
+//            K~ = bf16(fk ks) with its column sums; X jobs (f-tile, query
+//            half): X = S dy^T and qs fq . X, waves 4-7 first;
+//   phase 2  waves 0-3: den, delta, dad fragments;
+//   phase 3  X jobs: dfq and fq . dfq; S^T tiles: S^T <- r S^T + V^T K~;
+//   tail     p, next chunk, z update, publish S.
+// S lives in the accumulators of the waves that own its tiles.  With FP = 256
+// (eight f-tiles) wave w owns f-tile w across all d-tiles and contracts its X
+// jobs from its own registers; otherwise tile t = wave + 8 i is owned
+// (f-tile t % NFT, d-tile t / NFT) and the tiles are published as bf16 S
+// [f][d] in LDS each chunk, where the X jobs read them.
 // ============================================================================
 template <int FP, int DP>
 struct BwdA : BwdCommon<FP, DP> {
   using B_ = BwdCommon<FP, DP>;
-  static constexpr int C = B_::C, PF = B_::PF, PD = B_::PD, NFT = B_::NFT, ZPARTS = B_::ZPARTS;
+  static constexpr int C = B_::C, PF = B_::PF, PD = B_::PD, NFT = B_::NFT, NDT = B_::NDT;
+  static constexpr int ZPARTS = B_::ZPARTS;
+  static constexpr bool SREG = NFT >= B_WAVES;    // S by f-tile in registers, no LDS copy
+  static constexpr int S_OWN = SREG ? NDT * (NFT / B_WAVES) : (NFT * NDT + B_WAVES - 1) / B_WAVES;
+  static constexpr int XJ = SREG ? 2 * (NFT / B_WAVES) : 1;   // X jobs per wave
+  static constexpr int NLF = (C * FP / 8 + B_THREADS - 1) / B_THREADS;
+  static constexpr int NLD = (C * DP / 8 + B_THREADS - 1) / B_THREADS;
   static constexpr int OFF_FQ = 0;
   static constexpr int OFF_FK = OFF_FQ + C * PF * 2;
   static constexpr int OFF_V = OFF_FK + C * PF * 2;
   static constexpr int OFF_DY = OFF_V + C * PD * 2;
   static constexpr int OFF_KT = OFF_DY + C * PD * 2;       // K~ = bf16(fk ks), row-major
-  static constexpr int OFF_FR = OFF_KT + C * PF * 2;       // dad fragments [2 qt][4 kb][64]
+  static constexpr int OFF_SL = OFF_KT + C * PF * 2;       // S [f][d] bf16 (not SREG)
+  static constexpr int OFF_FR = OFF_SL + (SREG ? 0 : FP * PD * 2);   // dad fragments
   static constexpr int OFF_RA = OFF_FR + 2 * 4 * 64 * 16;  // [2][64] sum_t a
   static constexpr int OFF_RAV = OFF_RA + 2 * 64 * 4;      // [2][64] sum_t a (v . dy)
   static constexpr int OFF_QZ = OFF_RAV + 2 * 64 * 4;      // [4][64] Q~ . z partials
@@ -77,29 +131,65 @@ struct BwdA : BwdCommon<FP, DP> {
   static constexpr int OFF_ZP = OFF_Z + FP * 4;            // 2048 partial sums of K~
   static constexpr int OFF_R = OFF_ZP + 2048 * 4;
   static constexpr int BYTES = OFF_R + 16;
-  static constexpr int LB = (FP >= 256 || FP + DP >= 160) ? 1 : 2;
-  // chunks prefetched ahead (1 or 2; two measured slower at the bench shapes)
-  static constexpr int DEPTH = 1;
+  static_assert(BYTES <= 160 * 1024, "LDS budget");
 };
 
+// scale_rows (gla_common.hpp) for 256 threads numbered t (the upper half of
+// the workgroup here)
+template <int KP>
+__device__ __forceinline__ void scale_rows_t(const bf16* tile, int pitch, const float* scale,
+                                             uint4 (&out)[RowItems<KP>::N], float* part, int t) {
+  using R = RowItems<KP>;
+  const int cg = t % R::K8, r0 = t / R::K8;
+  float sum[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) sum[e] = 0.f;
+#pragma unroll
+  for (int i = 0; i < R::N; ++i) {
+    const int row = r0 + R::RSTRIDE * i;
+    const bf16x8 x = *reinterpret_cast<const bf16x8*>(tile + row * pitch + 8 * cg);
+    const float s = scale[row];
+    bf16x8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      o[e] = to_bf16(to_f32(x[e]) * s);
+      sum[e] += to_f32(o[e]);
+    }
+    out[i] = __builtin_bit_cast(uint4, o);
+  }
+  float* dst = part + r0 * KP + 8 * cg;
+  *reinterpret_cast<f32x4*>(dst) = f32x4{sum[0], sum[1], sum[2], sum[3]};
+  *reinterpret_cast<f32x4*>(dst + 4) = f32x4{sum[4], sum[5], sum[6], sum[7]};
+}
+
+template <int KP>
+__device__ __forceinline__ void store_rows_t(const uint4 (&in)[RowItems<KP>::N], bf16* tile,
+                                             int pitch, int t) {
+  using R = RowItems<KP>;
+  const int cg = t % R::K8, r0 = t / R::K8;
+#pragma unroll
+  for (int i = 0; i < R::N; ++i)
+    *reinterpret_cast<uint4*>(tile + (r0 + R::RSTRIDE * i) * pitch + 8 * cg) = in[i];
+}
+
 template <int FP, int DP, typename OutT>
-__global__ __launch_bounds__(256, (BwdA<FP, DP>::LB)) void gla_bwd_dq_kernel(
+__global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
     const bf16* __restrict__ fq, const bf16* __restrict__ fk, const bf16* __restrict__ v,
     const float* __restrict__ log_gamma, const bf16* __restrict__ dy, OutT* __restrict__ dfq,
     float* __restrict__ den_out, float* __restrict__ delta_out, float* __restrict__ p_out,
     const float* __restrict__ seg_state, int H, int L, int F, int D, int gate_per_head, int G,
-    int cps) {
+    int cps, int M) {
   using Cfg = BwdA<FP, DP>;
   constexpr int C = Cfg::C, PF = Cfg::PF, PD = Cfg::PD;
   constexpr int NFT = Cfg::NFT, NDT = Cfg::NDT;
-  using RF = Roles<NFT>;
-  constexpr int NFW = RF::TILES, NQW = RF::HALVES;
+  constexpr bool SREG = Cfg::SREG;
   extern __shared__ __align__(16) char smem[];
   bf16* fq_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_FQ);
   bf16* fk_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_FK);
   bf16* v_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_V);
   bf16* dy_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_DY);
   bf16* kt_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_KT);
+  bf16* s_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_SL);
   bf16x8* fr = reinterpret_cast<bf16x8*>(smem + Cfg::OFF_FR);
   float* ra = reinterpret_cast<float*>(smem + Cfg::OFF_RA);
   float* rav = reinterpret_cast<float*>(smem + Cfg::OFF_RAV);
@@ -115,87 +205,130 @@ __global__ __launch_bounds__(256, (BwdA<FP, DP>::LB)) void gla_bwd_dq_kernel(
   float* zp = reinterpret_cast<float*>(smem + Cfg::OFF_ZP);
   float* rdec = reinterpret_cast<float*>(smem + Cfg::OFF_R);
 
-  const int bh = blockIdx.x / G, seg = blockIdx.x % G;
-  const int NT = (L + C - 1) / C;
-  const int n0 = seg * cps, n1 = min(NT, n0 + cps);
+  // a workgroup walks M consecutive segments (seg .. seg + M - 1)
+  const int nwg = G / M;
+  const int bh = blockIdx.x / nwg, seg = (blockIdx.x % nwg) * M;
+  const int n0 = seg * cps, n1 = min((L + C - 1) / C, n0 + M * cps);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int col = lane & 31, h = lane >> 5;
   const bool vecF = (F & 7) == 0, vecD = (D & 7) == 0;
   const size_t offF = (size_t)bh * L * F, offD = (size_t)bh * L * D, offL = (size_t)bh * L;
   const float* lgb = log_gamma + (size_t)(gate_per_head ? bh : bh / H) * L;
   const float* st = G > 1 ? seg_state + ((size_t)bh * G + seg) * Cfg::SEG : nullptr;
-  const bool active = RF::active(wave);
 
-  // S^T tiles (rows d, columns f) of the owned f-tiles, all d-tiles
-  f32x16 St[NFW][NDT];
+  // owned S^T tiles (rows d, columns f): i -> (f-tile, d-tile)
+  auto s_tile = [&](int i, int& ft, int& dt) __attribute__((always_inline)) -> bool {
+    if constexpr (SREG) {
+      ft = wave * (NFT / B_WAVES) + i / NDT;
+      dt = i % NDT;
+      return true;
+    } else {
+      const int t = wave + B_WAVES * i;
+      ft = t % NFT;
+      dt = t / NFT;
+      return t < NFT * NDT;
+    }
+  };
+  // X jobs of this wave: j -> (f-tile, query half)
+  auto x_job = [&](int j, int& ft, int& hq) __attribute__((always_inline)) -> bool {
+    if constexpr (SREG) {
+      ft = wave * (NFT / B_WAVES) + (j >> 1);
+      hq = j & 1;
+      return true;
+    } else {
+      const int job = (wave + 4) & 7;   // waves 4-7 take jobs 0-3
+      ft = job >> 1;
+      hq = job & 1;
+      return job < 2 * NFT;
+    }
+  };
+  f32x16 St[Cfg::S_OWN];
 #pragma unroll
-  for (int i = 0; i < NFW; ++i)
+  for (int i = 0; i < Cfg::S_OWN; ++i) {
+    St[i] = zero16();
+    int ft, dt;
+    if (s_tile(i, ft, dt) && st) {
+      const int f = ft * 32 + col;
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-      St[i][dt] = zero16();
-      if (st && active) {
-        const int f = RF::tile(wave, i) * 32 + col;
+      for (int r = 0; r < 16; ++r) St[i][r] = st[f * DP + dt * 32 + acc_row(r, h)];
+    }
+  }
+  for (int f = tid; f < FP; f += B_THREADS) zs[f] = st ? st[FP * DP + f] : 0.f;
+  // bf16 S [f][d] for the X jobs (4 consecutive d per store)
+  auto publish = [&]() __attribute__((always_inline)) {
+    if constexpr (!SREG) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) St[i][dt][r] = st[f * DP + dt * 32 + acc_row(r, h)];
+      for (int i = 0; i < Cfg::S_OWN; ++i) {
+        int ft, dt;
+        if (s_tile(i, ft, dt)) {
+#pragma unroll
+          for (int g4 = 0; g4 < 4; ++g4) {
+            bf16x4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = to_bf16(St[i][4 * g4 + e]);
+            *reinterpret_cast<bf16x4*>(s_l + (ft * 32 + col) * PD + dt * 32 + 8 * g4 + 4 * h) = o;
+          }
+        }
       }
     }
-  for (int f = tid; f < FP; f += 256) zs[f] = st ? st[FP * DP + f] : 0.f;
+  };
 
-  // DEPTH register sets: while chunk n computes, chunks n+1 .. n+DEPTH are in flight
-  constexpr int DEPTH = Cfg::DEPTH;
-  uint4 rq[DEPTH][Cfg::NLF], rk[DEPTH][Cfg::NLF], rv[DEPTH][Cfg::NLD], rd[DEPTH][Cfg::NLD];
-  float rg[DEPTH];
-  auto issue = [&](auto set, int n) __attribute__((always_inline)) {
-    constexpr int S = decltype(set)::value;
+  uint4 rq[Cfg::NLF], rk[Cfg::NLF], rv[Cfg::NLD], rd[Cfg::NLD];
+  float rg = 0.f;
+  auto issue = [&](int n) __attribute__((always_inline)) {
     if (n < n1) {
-      load_chunk<FP>(rq[S], fq + offF, n * C, L, F, vecF);
-      load_chunk<FP>(rk[S], fk + offF, n * C, L, F, vecF);
-      load_chunk<DP>(rv[S], v + offD, n * C, L, D, vecD);
-      load_chunk<DP>(rd[S], dy + offD, n * C, L, D, vecD);
-      rg[S] = gate_at(lgb, n * C + lane, L);
+      load_tile8<FP>(rq, fq + offF, n * C, L, F, vecF);
+      load_tile8<FP>(rk, fk + offF, n * C, L, F, vecF);
+      load_tile8<DP>(rv, v + offD, n * C, L, D, vecD);
+      load_tile8<DP>(rd, dy + offD, n * C, L, D, vecD);
+      if (wave == 0) rg = gate_at(lgb, n * C + lane, L);
     }
   };
-  auto stage = [&](auto set) __attribute__((always_inline)) {
-    constexpr int S = decltype(set)::value;
-    store_chunk<FP>(rq[S], fq_l, PF);
-    store_chunk<FP>(rk[S], fk_l, PF);
-    store_chunk<DP>(rv[S], v_l, PD);
-    store_chunk<DP>(rd[S], dy_l, PD);
-    if (wave == 0) gate_scan(rg[S], lane, lgs, qs, ks, rdec);
+  auto stage = [&]() __attribute__((always_inline)) {
+    store_tile8<FP>(rq, fq_l, PF);
+    store_tile8<FP>(rk, fk_l, PF);
+    store_tile8<DP>(rv, v_l, PD);
+    store_tile8<DP>(rd, dy_l, PD);
+    if (wave == 0) gate_scan(rg, lane, lgs, qs, ks, rdec);
   };
-  issue(SET0, n0);
-  if constexpr (DEPTH == 2) issue(SET1, n0 + 1);
-  stage(SET0);
+  issue(n0);
+  stage();
+  publish();
   __syncthreads();
 
-  const int kt = wave >> 1, qt = wave & 1;   // this wave's tile of the 64x64 score block
-  const int qi = qt * 32 + col;               // chunk-local query of this lane
-  // chunk n is in LDS and register set `set` is free; the next set holds chunk n+1
-  auto step = [&](auto set, int n) __attribute__((always_inline)) {
-    constexpr int S = decltype(set)::value;
+  const bool scorer = wave < 4;
+  const int kt = (wave >> 1) & 1, qt = wave & 1;   // score tile of waves 0-3
+  const int qi = qt * 32 + col;                     // its query (lane)
+  for (int n = n0; n < n1; ++n) {
     const int t0 = n * C;
-    issue(set, n + DEPTH);
-    // ---- phase 1: a^T and (v dy^T) tile; Q~.z; sums of K~; X = S dy^T --------
-    f32x16 aT = zero16(), vdy = zero16();
+    issue(n + 1);
+    // ---- phase 1 ---------------------------------------------------------------
+    f32x16 vdy = zero16();
+    float dec[16];   // causal decay of the score tile, reused in phase 2
+    if (scorer) {
+      f32x16 aT = zero16();
 #pragma unroll
-    for (int kb = 0; kb < FP / 16; ++kb)
-      aT = mfma(row_operand(fk_l, PF, kt * 32 + col, 16 * kb, h),
-                row_operand(fq_l, PF, qi, 16 * kb, h), aT);
+      for (int kb = 0; kb < FP / 16; ++kb)
+        aT = mfma(row_operand(fk_l, PF, kt * 32 + col, 16 * kb, h),
+                  row_operand(fq_l, PF, qi, 16 * kb, h), aT);
 #pragma unroll
-    for (int kb = 0; kb < DP / 16; ++kb)
-      vdy = mfma(row_operand(v_l, PD, kt * 32 + col, 16 * kb, h),
-                 row_operand(dy_l, PD, qi, 16 * kb, h), vdy);
-    const float lgq = lgs[qi];
-    float dec[16];   // causal decay of this wave's score tile, reused in phase 2
-    {
+      for (int kb = 0; kb < DP / 16; ++kb)
+        vdy = mfma(row_operand(v_l, PD, kt * 32 + col, 16 * kb, h),
+                   row_operand(dy_l, PD, qi, 16 * kb, h), vdy);
+      const float lgq = lgs[qi];
       float sa = 0.f, sav = 0.f;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = kt * 32 + acc_row(r, h);
-        dec[r] = key <= qi ? fexp(lgq - lgs[key]) : 0.f;
-        aT[r] = to_f32(to_bf16(aT[r] * dec[r]));   // a exactly as the forward rounds it
-        sa += aT[r];
-        sav += aT[r] * vdy[r];
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int k0 = kt * 32 + 8 * g4 + 4 * h;   // keys of registers 4 g4 .. +4
+        const f32x4 lk = *reinterpret_cast<const f32x4*>(lgs + k0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * g4 + e;
+          dec[r] = k0 + e <= qi ? fexp(lgq - lk[e]) : 0.f;
+          aT[r] = to_f32(to_bf16(aT[r] * dec[r]));   // a exactly as the forward rounds it
+          sa += aT[r];
+          sav += aT[r] * vdy[r];
+        }
       }
       sa += xhalf(sa);
       sav += xhalf(sav);
@@ -203,49 +336,59 @@ __global__ __launch_bounds__(256, (BwdA<FP, DP>::LB)) void gla_bwd_dq_kernel(
         ra[kt * 64 + qi] = sa;
         rav[kt * 64 + qi] = sav;
       }
-      constexpr int FQ = FP / 4;   // qs (fq . z) over a quarter of the features; query = lane
+    } else {
+      // qs (fq . z) over a quarter of the features; query = lane
+      const int w4 = wave - 4;
+      constexpr int FQ = FP / 4;
       float acc = 0.f;
 #pragma unroll
       for (int c = 0; c < FQ; c += 8) {
-        const bf16x8 x = *reinterpret_cast<const bf16x8*>(fq_l + lane * PF + wave * FQ + c);
+        const bf16x8 x = *reinterpret_cast<const bf16x8*>(fq_l + lane * PF + w4 * FQ + c);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc += to_f32(x[e]) * zs[wave * FQ + c + e];
+        for (int e = 0; e < 8; ++e) acc += to_f32(x[e]) * zs[w4 * FQ + c + e];
       }
-      qz[wave * 64 + lane] = acc * qs[lane];
+      qz[w4 * 64 + lane] = acc * qs[lane];
       // K~ = bf16(fk ks) once per chunk (the forward's rounding), with its
       // column sums for z
       uint4 kti[RowItems<FP>::N];
-      scale_rows<FP>(fk_l, PF, ks, kti, zp);
-      store_rows<FP>(kti, kt_l, PF);
+      scale_rows_t<FP>(fk_l, PF, ks, kti, zp, tid - 256);
+      store_rows_t<FP>(kti, kt_l, PF, tid - 256);
     }
-    f32x16 X[NFW][NQW];
-    if (active) {
+    // X = S dy^T for this wave's jobs, and qs fq . X per query
+    f32x16 X[Cfg::XJ];
 #pragma unroll
-      for (int i = 0; i < NFW; ++i) {
-        const int ft = RF::tile(wave, i);
-#pragma unroll
-        for (int j = 0; j < NQW; ++j) {
-          const int q = RF::half(wave, j) * 32 + col;
-          f32x16 x = zero16();
+    for (int j = 0; j < Cfg::XJ; ++j) {
+      int ft, hq;
+      X[j] = zero16();
+      if (x_job(j, ft, hq)) {
+        const int q = hq * 32 + col;
+        f32x16 x = zero16();
+        if constexpr (SREG) {
 #pragma unroll
           for (int kb = 0; kb < DP / 16; ++kb)
-            x = mfma(acc_operand(St[i][kb >> 1], kb & 1), row_operand_acc(dy_l, PD, q, 16 * kb, h), x);
-          X[i][j] = x;
-          float s = 0.f;   // qs (fq . S dy) over this f-tile
+            x = mfma(acc_operand(St[(j >> 1) * NDT + (kb >> 1)], kb & 1),
+                     row_operand_acc(dy_l, PD, q, 16 * kb, h), x);
+        } else {
 #pragma unroll
-          for (int g4 = 0; g4 < 4; ++g4) {
-            const bf16x4 f4 = *reinterpret_cast<const bf16x4*>(fq_l + q * PF + ft * 32 + 8 * g4 + 4 * h);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) s += to_f32(f4[e]) * x[4 * g4 + e];
-          }
-          s += xhalf(s);
-          if (h == 0) nx[ft * 64 + q] = s * qs[q];
+          for (int kb = 0; kb < DP / 16; ++kb)
+            x = mfma(row_operand_acc(s_l, PD, ft * 32 + col, 16 * kb, h),
+                     row_operand_acc(dy_l, PD, q, 16 * kb, h), x);
         }
+        X[j] = x;
+        float s = 0.f;
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const bf16x4 f4 = *reinterpret_cast<const bf16x4*>(fq_l + q * PF + ft * 32 + 8 * g4 + 4 * h);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) s += to_f32(f4[e]) * x[4 * g4 + e];
+        }
+        s += xhalf(s);
+        if (h == 0) nx[ft * 64 + q] = s * qs[q];
       }
     }
     __syncthreads();
-    // ---- phase 2: den, delta, dad fragments ------------------------------------
-    {
+    // ---- phase 2: den, delta, dad fragments (waves 0-3) ------------------------
+    if (scorer) {
       const float den = ra[qi] + ra[64 + qi] + qz[qi] + qz[64 + qi] + qz[128 + qi] + qz[192 + qi];
       float num = rav[qi] + rav[64 + qi];
 #pragma unroll
@@ -268,75 +411,69 @@ __global__ __launch_bounds__(256, (BwdA<FP, DP>::LB)) void gla_bwd_dq_kernel(
       }
     }
     __syncthreads();
-    // ---- phase 3: dfq and fq . dfq for owned (f-tile, half); S^T update --------
+    // ---- phase 3: dfq and fq . dfq for the X jobs; S^T update ------------------
     const float r_n = rdec[0];
-    if (active) {
 #pragma unroll
-      for (int i = 0; i < NFW; ++i) {
-        const int ft = RF::tile(wave, i);
-        bf16x8 fkr[4];   // fk^T rows of this f-tile (A of fk^T dad^T)
+    for (int j = 0; j < Cfg::XJ; ++j) {
+      int ft, hq;
+      if (x_job(j, ft, hq)) {
+        const int q = hq * 32 + col;
+        f32x16 g = zero16();
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) fkr[kb] = tr_operand(fk_l, PF, 16 * kb, ft * 32, lane);
+        for (int kb = 0; kb < 4; ++kb)
+          g = mfma(tr_operand(fk_l, PF, 16 * kb, ft * 32, lane), fr[(hq * 4 + kb) * 64 + lane], g);
+        const float dcl = fmaxf(dens[q], TINY);
+        const float qsd = qs[q] / dcl;
+        const float delta = dels[q];
+        const int tok = t0 + q;
+        float ps = 0.f;
 #pragma unroll
-        for (int j = 0; j < NQW; ++j) {
-          const int hq = RF::half(wave, j);
-          const int q = hq * 32 + col;
-          f32x16 g = zero16();
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const int f0 = ft * 32 + 8 * g4 + 4 * h;
+          const bf16x4 f4 = *reinterpret_cast<const bf16x4*>(fq_l + q * PF + f0);
+          const f32x4 z4 = *reinterpret_cast<const f32x4*>(zs + f0);
 #pragma unroll
-          for (int kb = 0; kb < 4; ++kb) g = mfma(fkr[kb], fr[(hq * 4 + kb) * 64 + lane], g);
-          const float dcl = fmaxf(dens[q], TINY);
-          const float qsd = qs[q] / dcl;
-          const float delta = dels[q];
-          const int tok = t0 + q;
-          float ps = 0.f;
-#pragma unroll
-          for (int g4 = 0; g4 < 4; ++g4) {
-            const bf16x4 f4 = *reinterpret_cast<const bf16x4*>(fq_l + q * PF + ft * 32 + 8 * g4 + 4 * h);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int r = 4 * g4 + e, f = ft * 32 + 8 * g4 + 4 * h + e;
-              g[r] += qsd * (X[i][j][r] - zs[f] * delta);
-              ps += to_f32(f4[e]) * g[r];
-            }
-          }
-          ps += xhalf(ps);
-          if (h == 0) pp[ft * 64 + q] = tok < L ? ps : 0.f;
-          if (tok < L) {
-#pragma unroll
-            for (int g4 = 0; g4 < 4; ++g4)
-              store4<OutT>(dfq + offF, tok, ft * 32 + 8 * g4 + 4 * h, F, g[4 * g4],
-                           g[4 * g4 + 1], g[4 * g4 + 2], g[4 * g4 + 3]);
+          for (int e = 0; e < 4; ++e) {
+            const int r = 4 * g4 + e;
+            g[r] += qsd * (X[j][r] - z4[e] * delta);
+            ps += to_f32(f4[e]) * g[r];
           }
         }
-        // S^T[:, ft] <- r S^T + V^T K~
+        ps += xhalf(ps);
+        if (h == 0) pp[ft * 64 + q] = tok < L ? ps : 0.f;
+        if (tok < L) {
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) fkr[kb] = tr_operand(kt_l, PF, 16 * kb, ft * 32, lane);
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) St[i][dt][r] *= r_n;
-#pragma unroll
-          for (int kb = 0; kb < 4; ++kb)
-            St[i][dt] = mfma(tr_operand(v_l, PD, 16 * kb, dt * 32, lane), fkr[kb], St[i][dt]);
+          for (int g4 = 0; g4 < 4; ++g4)
+            store4<OutT>(dfq + offF, tok, ft * 32 + 8 * g4 + 4 * h, F, g[4 * g4], g[4 * g4 + 1],
+                         g[4 * g4 + 2], g[4 * g4 + 3]);
         }
       }
     }
+    // S^T <- r S^T + V^T K~ for the owned tiles
+#pragma unroll
+    for (int i = 0; i < Cfg::S_OWN; ++i) {
+      int ft, dt;
+      if (s_tile(i, ft, dt)) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) St[i][r] *= r_n;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+          St[i] = mfma(tr_operand(v_l, PD, 16 * kb, dt * 32, lane),
+                       tr_operand(kt_l, PF, 16 * kb, ft * 32, lane), St[i]);
+      }
+    }
     __syncthreads();
-    // ---- next chunk into LDS; z update; fq . dfq of this chunk ------------------
+    // ---- next chunk into LDS; z update; fq . dfq of this chunk; publish S ---------
     if (tid < 64 && t0 + tid < L) {
       float s = 0.f;
 #pragma unroll
       for (int ft = 0; ft < NFT; ++ft) s += pp[ft * 64 + tid];
       p_out[offL + t0 + tid] = s;
     }
-    if (n + 1 < n1) stage(std::integral_constant<int, (S + 1) % DEPTH>{});
+    if (n + 1 < n1) stage();
     if (tid < FP) zs[tid] = zs[tid] * r_n + sum_parts<FP>(zp, tid);
+    publish();
     __syncthreads();
-  };
-  for (int n = n0; n < n1; n += DEPTH) {
-    step(SET0, n);
-    if constexpr (DEPTH == 2)
-      if (n + 1 < n1) step(SET1, n + 1);
   }
 }
 
@@ -533,11 +670,30 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_bwd_state_kernel(
 
 // ============================================================================
 // kernel B: reverse walk -> dv, dfk, dG = p - fk . dfk
+//
+// Eight waves share one chunk (the LDS of a chunk leaves room for one
+// workgroup per CU, so the second wave per SIMD comes from inside it):
+//   phase 1  wave (kind, qt, kt): kind 0 the score tile s -> a/den, kind 1 the
+//            dy.v^T tile -> dad (both need only their own tile); all threads
+//            form dY^ = bf16(qh dy) and the dz partials;
+//   phase 2  dv jobs (d-tile, key half) contract dS over f from the published
+//            bf16 dS^T tile; dS tiles (f-tile, d-tile) are spread over the
+//            waves' accumulators and updated with fq^T dY^; dfk jobs
+//            (f-tile, key half) contract dS^T over d;
+//   tail     dG, publish dS^T, stage the prefetched chunk, dz update.
 // ============================================================================
 template <int FP, int DP>
 struct BwdB : BwdCommon<FP, DP> {
   using B_ = BwdCommon<FP, DP>;
-  static constexpr int C = B_::C, PF = B_::PF, PD = B_::PD, NFT = B_::NFT, ZPARTS = B_::ZPARTS;
+  static constexpr int C = B_::C, PF = B_::PF, PD = B_::PD, NFT = B_::NFT, NDT = B_::NDT;
+  static constexpr int ZP = 8;                                // dz partial sums per feature
+  static constexpr int S_OWN = (NFT * NDT + B_WAVES - 1) / B_WAVES;   // dS tiles per wave
+  static constexpr int DV_JOBS = 2 * NDT, DFK_JOBS = 2 * NFT;
+  static constexpr int DV_OWN = (DV_JOBS + B_WAVES - 1) / B_WAVES;
+  static constexpr int DFK_OWN = (DFK_JOBS + B_WAVES - 1) / B_WAVES;
+  // chunk tiles per thread (16-byte items), rounded up; the last may be partial
+  static constexpr int NLF = (C * FP / 8 + B_THREADS - 1) / B_THREADS;
+  static constexpr int NLD = (C * DP / 8 + B_THREADS - 1) / B_THREADS;
   static constexpr int OFF_FQ = 0;
   static constexpr int OFF_FK = OFF_FQ + C * PF * 2;
   static constexpr int OFF_V = OFF_FK + C * PF * 2;
@@ -557,25 +713,22 @@ struct BwdB : BwdCommon<FP, DP> {
   static constexpr int OFF_KS = OFF_QS + 64 * 4;
   static constexpr int OFF_DZ = OFF_KS + 64 * 4;
   static constexpr int OFF_DZP = OFF_DZ + FP * 4;
-  static constexpr int OFF_R = OFF_DZP + ZPARTS * FP * 4;
+  static constexpr int OFF_R = OFF_DZP + ZP * FP * 4;
   static constexpr int BYTES = OFF_R + 16;
-  static constexpr int LB = (FP >= 256 || FP + DP >= 160) ? 1 : 2;
-  static constexpr int DEPTH = 1;
+  static constexpr int LB = BYTES <= 80 * 1024 ? 2 : 1;
 };
 
 template <int FP, int DP, typename OutT>
-__global__ __launch_bounds__(256, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_kernel(
+__global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_kernel(
     const bf16* __restrict__ fq, const bf16* __restrict__ fk, const bf16* __restrict__ v,
     const float* __restrict__ log_gamma, const bf16* __restrict__ dy,
     const float* __restrict__ den_in, const float* __restrict__ delta_in,
     const float* __restrict__ p_in, OutT* __restrict__ dfk, OutT* __restrict__ dv,
     float* __restrict__ dG, float* __restrict__ csum, const float* __restrict__ seg_state, int H,
-    int L, int F, int D, int gate_per_head, int G, int cps) {
+    int L, int F, int D, int gate_per_head, int G, int cps, int M) {
   using Cfg = BwdB<FP, DP>;
   constexpr int C = Cfg::C, PF = Cfg::PF, PD = Cfg::PD;
-  constexpr int NFT = Cfg::NFT, NDT = Cfg::NDT;
-  using RD = Roles<NDT>;   // dv and the dS state by d-tile
-  using RF = Roles<NFT>;   // dfk by f-tile
+  constexpr int NFT = Cfg::NFT, NDT = Cfg::NDT, ZP = Cfg::ZP;
   extern __shared__ __align__(16) char smem[];
   bf16* fq_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_FQ);
   bf16* fk_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_FK);
@@ -598,9 +751,12 @@ __global__ __launch_bounds__(256, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_kernel(
   float* dzp = reinterpret_cast<float*>(smem + Cfg::OFF_DZP);
   float* rdec = reinterpret_cast<float*>(smem + Cfg::OFF_R);
 
-  const int bh = blockIdx.x / G, seg = blockIdx.x % G;
+  // a workgroup walks M consecutive segments (seg0 .. seg0 + M - 1) in reverse,
+  // entering with the state that flows into the last of them
+  const int nwg = G / M;
+  const int bh = blockIdx.x / nwg, seg0 = (blockIdx.x % nwg) * M, seg = seg0 + M - 1;
   const int NT = (L + C - 1) / C;
-  const int n0 = seg * cps, n1 = min(NT, n0 + cps);
+  const int n0 = seg0 * cps, n1 = min(NT, n0 + M * cps);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int col = lane & 31, h = lane >> 5;
   const bool vecF = (F & 7) == 0, vecD = (D & 7) == 0;
@@ -608,208 +764,223 @@ __global__ __launch_bounds__(256, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_kernel(
   const float* lgb = log_gamma + (size_t)(gate_per_head ? bh : bh / H) * L;
   const float* st = G > 1 ? seg_state + ((size_t)bh * G + seg) * Cfg::SEG : nullptr;
 
-  // dS tiles (rows f, columns d) of the owned d-tiles
-  f32x16 dS[RD::TILES][NFT];
+  // this wave's dS tiles t = wave + 8 i: f-tile t % NFT, d-tile t / NFT
+  // (lane = d column, registers = f rows)
+  f32x16 dS[Cfg::S_OWN];
 #pragma unroll
-  for (int i = 0; i < RD::TILES; ++i)
+  for (int i = 0; i < Cfg::S_OWN; ++i) {
+    dS[i] = zero16();
+    const int t = wave + B_WAVES * i;
+    if (st && t < NFT * NDT) {
+      const int ft = t % NFT, dt = t / NFT;
 #pragma unroll
-    for (int ft = 0; ft < NFT; ++ft) {
-      dS[i][ft] = zero16();
-      if (st && RD::active(wave)) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          dS[i][ft][r] = st[(ft * 32 + acc_row(r, h)) * DP + RD::tile(wave, i) * 32 + col];
-      }
+      for (int r = 0; r < 16; ++r) dS[i][r] = st[(ft * 32 + acc_row(r, h)) * DP + dt * 32 + col];
     }
-  for (int f = tid; f < FP; f += 256) dzs[f] = st ? st[FP * DP + f] : 0.f;
+  }
+  for (int f = tid; f < FP; f += B_THREADS) dzs[f] = st ? st[FP * DP + f] : 0.f;
 
-  // publish dS as bf16 dS^T [d][f] (rows d = lane column, 4 consecutive f per store)
+  // publish the owned dS tiles as bf16 dS^T [d][f] (4 consecutive f per store)
   auto publish = [&]() {
-    if (RD::active(wave) && RD::primary(wave)) {
 #pragma unroll
-      for (int i = 0; i < RD::TILES; ++i) {
-        const int d = RD::tile(wave, i) * 32 + col;
+    for (int i = 0; i < Cfg::S_OWN; ++i) {
+      const int t = wave + B_WAVES * i;
+      if (t < NFT * NDT) {
+        const int ft = t % NFT, d = (t / NFT) * 32 + col;
 #pragma unroll
-        for (int ft = 0; ft < NFT; ++ft)
+        for (int g4 = 0; g4 < 4; ++g4) {
+          bf16x4 o;
 #pragma unroll
-          for (int g4 = 0; g4 < 4; ++g4) {
-            bf16x4 o;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) o[e] = to_bf16(dS[i][ft][4 * g4 + e]);
-            *reinterpret_cast<bf16x4*>(dst_l + d * PF + ft * 32 + 8 * g4 + 4 * h) = o;
-          }
+          for (int e = 0; e < 4; ++e) o[e] = to_bf16(dS[i][4 * g4 + e]);
+          *reinterpret_cast<bf16x4*>(dst_l + d * PF + ft * 32 + 8 * g4 + 4 * h) = o;
+        }
       }
     }
   };
 
-  // DEPTH register sets: while chunk n computes, chunks n-1 .. n-DEPTH are in flight
-  constexpr int DEPTH = Cfg::DEPTH;
-  uint4 rq[DEPTH][Cfg::NLF], rk[DEPTH][Cfg::NLF], rv[DEPTH][Cfg::NLD], rd[DEPTH][Cfg::NLD];
-  TokScalars sc[DEPTH];
-  auto issue = [&](auto set, int n) __attribute__((always_inline)) {
-    constexpr int S = decltype(set)::value;
+  uint4 rq[Cfg::NLF], rk[Cfg::NLF], rv[Cfg::NLD], rd[Cfg::NLD];
+  TokScalars sc;
+  auto issue = [&](int n) __attribute__((always_inline)) {
     if (n >= n0) {
-      load_chunk<FP>(rq[S], fq + offF, n * C, L, F, vecF);
-      load_chunk<FP>(rk[S], fk + offF, n * C, L, F, vecF);
-      load_chunk<DP>(rv[S], v + offD, n * C, L, D, vecD);
-      load_chunk<DP>(rd[S], dy + offD, n * C, L, D, vecD);
-      sc[S] = load_scalars(lgb, den_in, delta_in, p_in, offL, n * C + lane, L);
+      load_tile8<FP>(rq, fq + offF, n * C, L, F, vecF);
+      load_tile8<FP>(rk, fk + offF, n * C, L, F, vecF);
+      load_tile8<DP>(rv, v + offD, n * C, L, D, vecD);
+      load_tile8<DP>(rd, dy + offD, n * C, L, D, vecD);
+      if (wave == 0) sc = load_scalars(lgb, den_in, delta_in, p_in, offL, n * C + lane, L);
     }
   };
   // chunk n's tiles and per-token scalars (scalars into the buffers of parity n & 1)
-  auto stage = [&](auto set, int n) __attribute__((always_inline)) {
-    constexpr int S = decltype(set)::value;
-    store_chunk<FP>(rq[S], fq_l, PF);
-    store_chunk<FP>(rk[S], fk_l, PF);
-    store_chunk<DP>(rv[S], v_l, PD);
-    store_chunk<DP>(rd[S], dy_l, PD);
+  auto stage = [&](int n) __attribute__((always_inline)) {
+    store_tile8<FP>(rq, fq_l, PF);
+    store_tile8<FP>(rk, fk_l, PF);
+    store_tile8<DP>(rv, v_l, PD);
+    store_tile8<DP>(rd, dy_l, PD);
     const int b = n & 1;
     if (wave == 0)
-      bwd_scalars(sc[S].g, sc[S].den, sc[S].delta, sc[S].p, lane, lgs, qs, ks, rdec,
-                  invd + 64 * b, dels + 64 * b, ps + 64 * b, qh + 64 * b, dw + 64 * b);
+      bwd_scalars(sc.g, sc.den, sc.delta, sc.p, lane, lgs, qs, ks, rdec, invd + 64 * b,
+                  dels + 64 * b, ps + 64 * b, qh + 64 * b, dw + 64 * b);
   };
-  issue(SET0, n1 - 1);
-  if constexpr (DEPTH == 2) issue(SET1, n1 - 2);
-  stage(SET0, n1 - 1);
+  issue(n1 - 1);
+  stage(n1 - 1);
   publish();
   __syncthreads();
 
-  const int qt = wave >> 1, kt = wave & 1;   // this wave's tile of the score block
-  const int ki = kt * 32 + col;               // chunk-local key of this lane (phase 1)
-  // chunk n is in LDS and register set `set` is free; the next set holds chunk n-1
-  auto step = [&](auto set, int n) __attribute__((always_inline)) {
-    constexpr int S = decltype(set)::value;
+  const int kind = wave >> 2, qt = (wave >> 1) & 1, kt = wave & 1;   // phase-1 tile
+  const int ki = kt * 32 + col;                                       // its key (lane)
+  for (int n = n1 - 1; n >= n0; --n) {
     const int t0 = n * C;
     const int cur = n & 1;
     const float* invc = invd + 64 * cur;
     const float* delsc = dels + 64 * cur;
     const float* qhc = qh + 64 * cur;
     const float* dwc = dw + 64 * cur;
-    issue(set, n - DEPTH);
-    // ---- phase 1: s and (dy v^T) tile (queries x keys) -> a/den, dad; dz sums ----
+    issue(n - 1);
+    // ---- phase 1: one 32x32 tile (queries x keys) of s or dy v^T per wave ----
     {
-      f32x16 s = zero16(), dyv = zero16();
+      f32x16 acc = zero16();
+      if (kind == 0) {
 #pragma unroll
-      for (int kb = 0; kb < FP / 16; ++kb)
-        s = mfma(row_operand(fq_l, PF, qt * 32 + col, 16 * kb, h),
-                 row_operand(fk_l, PF, ki, 16 * kb, h), s);
+        for (int kb = 0; kb < FP / 16; ++kb)
+          acc = mfma(row_operand(fq_l, PF, qt * 32 + col, 16 * kb, h),
+                     row_operand(fk_l, PF, ki, 16 * kb, h), acc);
+      } else {
 #pragma unroll
-      for (int kb = 0; kb < DP / 16; ++kb)
-        dyv = mfma(row_operand(dy_l, PD, qt * 32 + col, 16 * kb, h),
-                   row_operand(v_l, PD, ki, 16 * kb, h), dyv);
-      const float lgk = lgs[ki];
-      bf16x8 fa8[2], fd8[2];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int q = qt * 32 + acc_row(r, h);
-        const bool c = ki <= q;
-        const float dec = c ? fexp(lgs[q] - lgk) : 0.f;
-        const float inv = invc[q];
-        const float a = to_f32(to_bf16(s[r] * dec));
-        fa8[r >> 3][r & 7] = to_bf16(a * inv);
-        fd8[r >> 3][r & 7] = to_bf16(c ? (dyv[r] - delsc[q]) * inv * dec : 0.f);
+        for (int kb = 0; kb < DP / 16; ++kb)
+          acc = mfma(row_operand(dy_l, PD, qt * 32 + col, 16 * kb, h),
+                     row_operand(v_l, PD, ki, 16 * kb, h), acc);
       }
-      fa[(kt * 4 + qt * 2 + 0) * 64 + lane] = fa8[0];
-      fa[(kt * 4 + qt * 2 + 1) * 64 + lane] = fa8[1];
-      fd[(kt * 4 + qt * 2 + 0) * 64 + lane] = fd8[0];
-      fd[(kt * 4 + qt * 2 + 1) * 64 + lane] = fd8[1];
-      // dY^ = bf16(qh dy) once per chunk, for dS += fq^T dY^ (= Q^^T dY)
-      uint4 rh[RowItems<DP>::N];
-      scale_rows_only<DP>(dy_l, PD, qhc, rh);
-      store_rows<DP>(rh, dyh_l, PD);
-      // dz partials: sum_i fq_i (qh_i delta_i)
-      constexpr int TPP = C / Cfg::ZPARTS;
-      const int f = tid % FP, part = tid / FP;
-      if (part < Cfg::ZPARTS) {
-        float za = 0.f;
-#pragma unroll 8
-        for (int t = part * TPP; t < (part + 1) * TPP; ++t) za += to_f32(fq_l[t * PF + f]) * dwc[t];
-        dzp[part * FP + f] = za;
+      const float lgk = lgs[ki];
+      bf16x8 o8[2];
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int q0 = qt * 32 + 8 * g4 + 4 * h;   // queries of registers 4 g4 .. +4
+        const f32x4 lq = *reinterpret_cast<const f32x4*>(lgs + q0);
+        const f32x4 iv = *reinterpret_cast<const f32x4*>(invc + q0);
+        const f32x4 dl = *reinterpret_cast<const f32x4*>(delsc + q0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * g4 + e;
+          const bool c = ki <= q0 + e;
+          const float dec = c ? fexp(lq[e] - lgk) : 0.f;
+          float val;
+          if (kind == 0) val = to_f32(to_bf16(acc[r] * dec)) * iv[e];   // a / den
+          else val = c ? (acc[r] - dl[e]) * iv[e] * dec : 0.f;          // dad
+          o8[r >> 3][r & 7] = to_bf16(val);
+        }
+      }
+      bf16x8* frag = kind == 0 ? fa : fd;
+      frag[(kt * 4 + qt * 2 + 0) * 64 + lane] = o8[0];
+      frag[(kt * 4 + qt * 2 + 1) * 64 + lane] = o8[1];
+    }
+    // dY^ = bf16(qh dy), once per chunk, for dS += fq^T dY^
+    {
+      constexpr int K8 = DP / 8;
+      for (int idx = tid; idx < C * K8; idx += B_THREADS) {
+        const int t = idx / K8, c8 = 8 * (idx % K8);
+        const bf16x8 x = *reinterpret_cast<const bf16x8*>(dy_l + t * PD + c8);
+        *reinterpret_cast<bf16x8*>(dyh_l + t * PD + c8) = scale8(x, qhc[t]);
+      }
+    }
+    // dz partials: part p sums fq_t (qh_t delta_t) over tokens [8 p, 8 p + 8)
+    {
+      constexpr int K8 = FP / 8;
+      if (tid < ZP * K8) {
+        const int c8 = 8 * (tid % K8), part = tid / K8;
+        float za[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < C / ZP; ++j) {
+          const int t = part * (C / ZP) + j;
+          const bf16x8 x = *reinterpret_cast<const bf16x8*>(fq_l + t * PF + c8);
+          const float w = dwc[t];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) za[e] += to_f32(x[e]) * w;
+        }
+        float* dst = dzp + part * FP + c8;
+        *reinterpret_cast<f32x4*>(dst) = f32x4{za[0], za[1], za[2], za[3]};
+        *reinterpret_cast<f32x4*>(dst + 4) = f32x4{za[4], za[5], za[6], za[7]};
       }
     }
     __syncthreads();
     const float r_n = rdec[0];
-    // ---- phase 2: dv for owned (d-tile, key half); dS update --------------------
-    if (RD::active(wave)) {
+    // ---- phase 2: dv jobs from the published dS^T -----------------------------
 #pragma unroll
-      for (int i = 0; i < RD::TILES; ++i) {
-        const int dt = RD::tile(wave, i);
-        bf16x8 dyo[4];   // dY^T rows of this d-tile (A of dY^T (a/den))
+    for (int i = 0; i < Cfg::DV_OWN; ++i) {
+      const int job = wave + B_WAVES * i;
+      if (job < Cfg::DV_JOBS) {
+        const int dt = job >> 1, hk = job & 1;
+        const int key = hk * 32 + col;
+        // dv_t = ks_t (fk_t dS) + sum_i (a_it / den_i) dy_i: the row scale of
+        // K~ = fk ks multiplies the fp32 product
+        f32x16 g = zero16();
 #pragma unroll
-        for (int qb = 0; qb < 4; ++qb) dyo[qb] = tr_operand(dy_l, PD, 16 * qb, dt * 32, lane);
+        for (int kb = 0; kb < FP / 16; ++kb)
+          g = mfma(row_operand_acc(dst_l, PF, dt * 32 + col, 16 * kb, h),
+                   row_operand_acc(fk_l, PF, key, 16 * kb, h), g);
+        const float ksv = ks[key];
 #pragma unroll
-        for (int j = 0; j < RD::HALVES; ++j) {
-          const int key = RD::half(wave, j) * 32 + col;
-          // dv_t = ks_t (fk_t dS) + sum_i (a_it / den_i) dy_i: the row scale of
-          // K~ = fk ks multiplies the fp32 product
-          f32x16 g = zero16();
+        for (int r = 0; r < 16; ++r) g[r] *= ksv;
 #pragma unroll
-          for (int kb = 0; kb < FP / 16; ++kb)
-            g = mfma(acc_operand(dS[i][kb >> 1], kb & 1), row_operand_acc(fk_l, PF, key, 16 * kb, h), g);
-          const float ksv = ks[key];
+        for (int qb = 0; qb < 4; ++qb)
+          g = mfma(tr_operand(dy_l, PD, 16 * qb, dt * 32, lane), fa[(hk * 4 + qb) * 64 + lane], g);
+        const int tok = t0 + key;
+        if (tok < L) {
 #pragma unroll
-          for (int r = 0; r < 16; ++r) g[r] *= ksv;
-#pragma unroll
-          for (int qb = 0; qb < 4; ++qb)
-            g = mfma(dyo[qb], fa[(RD::half(wave, j) * 4 + qb) * 64 + lane], g);
-          const int tok = t0 + key;
-          if (tok < L) {
-#pragma unroll
-            for (int g4 = 0; g4 < 4; ++g4)
-              store4<OutT>(dv + offD, tok, dt * 32 + 8 * g4 + 4 * h, D, g[4 * g4],
-                           g[4 * g4 + 1], g[4 * g4 + 2], g[4 * g4 + 3]);
-          }
-        }
-#pragma unroll
-        for (int qb = 0; qb < 4; ++qb) dyo[qb] = tr_operand(dyh_l, PD, 16 * qb, dt * 32, lane);
-#pragma unroll
-        for (int ft = 0; ft < NFT; ++ft) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) dS[i][ft][r] *= r_n;
-#pragma unroll
-          for (int qb = 0; qb < 4; ++qb)
-            dS[i][ft] = mfma(tr_operand(fq_l, PF, 16 * qb, ft * 32, lane), dyo[qb], dS[i][ft]);
+          for (int g4 = 0; g4 < 4; ++g4)
+            store4<OutT>(dv + offD, tok, dt * 32 + 8 * g4 + 4 * h, D, g[4 * g4], g[4 * g4 + 1],
+                         g[4 * g4 + 2], g[4 * g4 + 3]);
         }
       }
     }
-    // ---- phase 2': dfk for owned (f-tile, key half), from the published dS^T ----
-    if (RF::active(wave)) {
+    // dS <- r_n dS + fq^T dY^ for the owned tiles
 #pragma unroll
-      for (int i = 0; i < RF::TILES; ++i) {
-        const int ft = RF::tile(wave, i);
+    for (int i = 0; i < Cfg::S_OWN; ++i) {
+      const int t = wave + B_WAVES * i;
+      if (t < NFT * NDT) {
+        const int ft = t % NFT, dt = t / NFT;
 #pragma unroll
-        for (int j = 0; j < RF::HALVES; ++j) {
-          const int hk = RF::half(wave, j);
-          const int key = hk * 32 + col;
-          f32x16 x = zero16(), g = zero16();
+        for (int r = 0; r < 16; ++r) dS[i][r] *= r_n;
 #pragma unroll
-          for (int kb = 0; kb < DP / 16; ++kb)
-            x = mfma(tr_operand(dst_l, PF, 16 * kb, ft * 32, lane),
-                     row_operand_acc(v_l, PD, key, 16 * kb, h), x);
+        for (int qb = 0; qb < 4; ++qb)
+          dS[i] = mfma(tr_operand(fq_l, PF, 16 * qb, ft * 32, lane),
+                       tr_operand(dyh_l, PD, 16 * qb, dt * 32, lane), dS[i]);
+      }
+    }
+    // ---- dfk jobs (f-tile, key half), from the published dS^T -----------------
 #pragma unroll
-          for (int qb = 0; qb < 4; ++qb)
-            g = mfma(tr_operand(fq_l, PF, 16 * qb, ft * 32, lane), fd[(hk * 4 + qb) * 64 + lane], g);
-          const float ksv = ks[key];
-          const int tok = t0 + key;
-          float pks = 0.f;
+    for (int i = 0; i < Cfg::DFK_OWN; ++i) {
+      const int job = wave + B_WAVES * i;
+      if (job < Cfg::DFK_JOBS) {
+        const int ft = job >> 1, hk = job & 1;
+        const int key = hk * 32 + col;
+        f32x16 x = zero16(), g = zero16();
 #pragma unroll
-          for (int g4 = 0; g4 < 4; ++g4) {
-            const bf16x4 k4 = *reinterpret_cast<const bf16x4*>(fk_l + key * PF + ft * 32 + 8 * g4 + 4 * h);
+        for (int kb = 0; kb < DP / 16; ++kb)
+          x = mfma(tr_operand(dst_l, PF, 16 * kb, ft * 32, lane),
+                   row_operand_acc(v_l, PD, key, 16 * kb, h), x);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int r = 4 * g4 + e, f = ft * 32 + 8 * g4 + 4 * h + e;
-              g[r] += ksv * (x[r] - dzs[f]);
-              pks += to_f32(k4[e]) * g[r];
-            }
+        for (int qb = 0; qb < 4; ++qb)
+          g = mfma(tr_operand(fq_l, PF, 16 * qb, ft * 32, lane), fd[(hk * 4 + qb) * 64 + lane], g);
+        const float ksv = ks[key];
+        const int tok = t0 + key;
+        float pks = 0.f;
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const int f0 = ft * 32 + 8 * g4 + 4 * h;
+          const bf16x4 k4 = *reinterpret_cast<const bf16x4*>(fk_l + key * PF + f0);
+          const f32x4 z4 = *reinterpret_cast<const f32x4*>(dzs + f0);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int r = 4 * g4 + e;
+            g[r] += ksv * (x[r] - z4[e]);
+            pks += to_f32(k4[e]) * g[r];
           }
-          pks += xhalf(pks);
-          if (h == 0) pk[ft * 64 + key] = pks;
-          if (tok < L) {
+        }
+        pks += xhalf(pks);
+        if (h == 0) pk[ft * 64 + key] = pks;
+        if (tok < L) {
 #pragma unroll
-            for (int g4 = 0; g4 < 4; ++g4)
-              store4<OutT>(dfk + offF, tok, ft * 32 + 8 * g4 + 4 * h, F, g[4 * g4],
-                           g[4 * g4 + 1], g[4 * g4 + 2], g[4 * g4 + 3]);
-          }
+          for (int g4 = 0; g4 < 4; ++g4)
+            store4<OutT>(dfk + offF, tok, ft * 32 + 8 * g4 + 4 * h, F, g[4 * g4],
+                         g[4 * g4 + 1], g[4 * g4 + 2], g[4 * g4 + 3]);
         }
       }
     }
@@ -829,19 +1000,14 @@ __global__ __launch_bounds__(256, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_kernel(
       if (lane == 0) csum[(size_t)bh * NT + n] = g;
     }
     publish();
-    if (n - 1 >= n0) stage(std::integral_constant<int, (S + 1) % DEPTH>{}, n - 1);
-    if (tid < FP) {
-      float za = dzs[tid] * r_n;
+    if (n - 1 >= n0) stage(n - 1);
+    for (int f = tid; f < FP; f += B_THREADS) {
+      float za = dzs[f] * r_n;
 #pragma unroll
-      for (int p = 0; p < Cfg::ZPARTS; ++p) za += dzp[p * FP + tid];
-      dzs[tid] = za;
+      for (int p = 0; p < ZP; ++p) za += dzp[p * FP + f];
+      dzs[f] = za;
     }
     __syncthreads();
-  };
-  for (int n = n1 - 1; n >= n0; n -= DEPTH) {
-    step(SET0, n);
-    if constexpr (DEPTH == 2)
-      if (n - 1 >= n0) step(SET1, n - 1);
   }
 }
 
@@ -943,11 +1109,14 @@ static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v
                               D, gate_per_head, G, cps, st);
     if (e != hipSuccess) return e;
   }
+  // the walks take two segments per workgroup while that still gives 256
+  // workgroups (one per CU): fewer, longer walks
+  const int M = (G % 2 == 0 && BH * G / 2 >= 256) ? 2 : 1;
   auto ka = gla_bwd_dq_kernel<FP, DP, OutT>;
   if ((e = ensure_lds<gla_bwd_dq_kernel<FP, DP, OutT>>(LDS_A)) != hipSuccess) return e;
-  hipLaunchKernelGGL(ka, dim3(BH * G), dim3(256), LDS_A, st, (const bf16*)fq,
+  hipLaunchKernelGGL(ka, dim3(BH * G / M), dim3(B_THREADS), LDS_A, st, (const bf16*)fq,
                      (const bf16*)fk, (const bf16*)v, lg, (const bf16*)dy, (OutT*)dfq, den, delta,
-                     p, fseg, H, L, F, D, gate_per_head, G, cps);
+                     p, fseg, H, L, F, D, gate_per_head, G, cps, M);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   if (G > 1) {
     auto ks = gla_bwd_state_kernel<FP, DP>;
@@ -961,10 +1130,10 @@ static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v
   }
   auto kb = gla_bwd_dkv_kernel<FP, DP, OutT>;
   if ((e = ensure_lds<gla_bwd_dkv_kernel<FP, DP, OutT>>(LDS_B)) != hipSuccess) return e;
-  hipLaunchKernelGGL(kb, dim3(BH * G), dim3(256), LDS_B, st, (const bf16*)fq,
+  hipLaunchKernelGGL(kb, dim3(BH * G / M), dim3(B_THREADS), LDS_B, st, (const bf16*)fq,
                      (const bf16*)fk, (const bf16*)v, lg, (const bf16*)dy, (const float*)den,
                      (const float*)delta, (const float*)p, (OutT*)dfk, (OutT*)dv, dG, csum,
-                     (const float*)rseg, H, L, F, D, gate_per_head, G, cps);
+                     (const float*)rseg, H, L, F, D, gate_per_head, G, cps, M);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   const dim3 ggrid((L + GLA_C - 1) / GLA_C, gate_rows(B, H, gate_per_head));
   hipLaunchKernelGGL(gla_gate_grad_kernel, ggrid, dim3(256), 0, st, (const float*)dG,
