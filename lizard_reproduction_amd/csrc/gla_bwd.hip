@@ -108,6 +108,9 @@ struct BwdA : BwdCommon<FP, DP> {
   static constexpr bool SREG = NFT >= B_WAVES;    // S by f-tile in registers, no LDS copy
   static constexpr int S_OWN = SREG ? NDT * (NFT / B_WAVES) : (NFT * NDT + B_WAVES - 1) / B_WAVES;
   static constexpr int XJ = SREG ? 2 * (NFT / B_WAVES) : 1;   // X jobs per wave
+  // chunks in flight while one computes (a second register set measured
+  // slower at the bench shapes, and spills at the largest tiles)
+  static constexpr int DEPTH = 1;
   static constexpr int NLF = (C * FP / 8 + B_THREADS - 1) / B_THREADS;
   static constexpr int NLD = (C * DP / 8 + B_THREADS - 1) / B_THREADS;
   static constexpr int OFF_FQ = 0;
@@ -273,35 +276,42 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
     }
   };
 
-  uint4 rq[Cfg::NLF], rk[Cfg::NLF], rv[Cfg::NLD], rd[Cfg::NLD];
-  float rg = 0.f;
-  auto issue = [&](int n) __attribute__((always_inline)) {
+  // DEPTH register sets: while chunk n computes, chunks n+1 .. n+DEPTH are in flight
+  constexpr int DEPTH = Cfg::DEPTH;
+  uint4 rq[DEPTH][Cfg::NLF], rk[DEPTH][Cfg::NLF], rv[DEPTH][Cfg::NLD], rd[DEPTH][Cfg::NLD];
+  float rg[DEPTH] = {};
+  auto issue = [&](auto set, int n) __attribute__((always_inline)) {
+    constexpr int S = decltype(set)::value;
     if (n < n1) {
-      load_tile8<FP>(rq, fq + offF, n * C, L, F, vecF);
-      load_tile8<FP>(rk, fk + offF, n * C, L, F, vecF);
-      load_tile8<DP>(rv, v + offD, n * C, L, D, vecD);
-      load_tile8<DP>(rd, dy + offD, n * C, L, D, vecD);
-      if (wave == 0) rg = gate_at(lgb, n * C + lane, L);
+      load_tile8<FP>(rq[S], fq + offF, n * C, L, F, vecF);
+      load_tile8<FP>(rk[S], fk + offF, n * C, L, F, vecF);
+      load_tile8<DP>(rv[S], v + offD, n * C, L, D, vecD);
+      load_tile8<DP>(rd[S], dy + offD, n * C, L, D, vecD);
+      if (wave == 0) rg[S] = gate_at(lgb, n * C + lane, L);
     }
   };
-  auto stage = [&]() __attribute__((always_inline)) {
-    store_tile8<FP>(rq, fq_l, PF);
-    store_tile8<FP>(rk, fk_l, PF);
-    store_tile8<DP>(rv, v_l, PD);
-    store_tile8<DP>(rd, dy_l, PD);
-    if (wave == 0) gate_scan(rg, lane, lgs, qs, ks, rdec);
+  auto stage = [&](auto set) __attribute__((always_inline)) {
+    constexpr int S = decltype(set)::value;
+    store_tile8<FP>(rq[S], fq_l, PF);
+    store_tile8<FP>(rk[S], fk_l, PF);
+    store_tile8<DP>(rv[S], v_l, PD);
+    store_tile8<DP>(rd[S], dy_l, PD);
+    if (wave == 0) gate_scan(rg[S], lane, lgs, qs, ks, rdec);
   };
-  issue(n0);
-  stage();
+  issue(SET0, n0);
+  if constexpr (DEPTH == 2) issue(SET1, n0 + 1);
+  stage(SET0);
   publish();
   __syncthreads();
 
   const bool scorer = wave < 4;
   const int kt = (wave >> 1) & 1, qt = wave & 1;   // score tile of waves 0-3
   const int qi = qt * 32 + col;                     // its query (lane)
-  for (int n = n0; n < n1; ++n) {
+  // chunk n is in LDS and register set `set` is free; the next set holds chunk n+1
+  auto step = [&](auto set, int n) __attribute__((always_inline)) {
+    constexpr int S = decltype(set)::value;
     const int t0 = n * C;
-    issue(n + 1);
+    issue(set, n + DEPTH);
     // ---- phase 1 ---------------------------------------------------------------
     f32x16 vdy = zero16();
     float dec[16];   // causal decay of the score tile, reused in phase 2
@@ -470,10 +480,15 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
       for (int ft = 0; ft < NFT; ++ft) s += pp[ft * 64 + tid];
       p_out[offL + t0 + tid] = s;
     }
-    if (n + 1 < n1) stage();
+    if (n + 1 < n1) stage(std::integral_constant<int, (S + 1) % DEPTH>{});
     if (tid < FP) zs[tid] = zs[tid] * r_n + sum_parts<FP>(zp, tid);
     publish();
     __syncthreads();
+  };
+  for (int n = n0; n < n1; n += DEPTH) {
+    step(SET0, n);
+    if constexpr (DEPTH == 2)
+      if (n + 1 < n1) step(SET1, n + 1);
   }
 }
 
@@ -691,6 +706,7 @@ struct BwdB : BwdCommon<FP, DP> {
   static constexpr int DV_JOBS = 2 * NDT, DFK_JOBS = 2 * NFT;
   static constexpr int DV_OWN = (DV_JOBS + B_WAVES - 1) / B_WAVES;
   static constexpr int DFK_OWN = (DFK_JOBS + B_WAVES - 1) / B_WAVES;
+  static constexpr int DEPTH = 1;   // as in BwdA
   // chunk tiles per thread (16-byte items), rounded up; the last may be partial
   static constexpr int NLF = (C * FP / 8 + B_THREADS - 1) / B_THREADS;
   static constexpr int NLD = (C * DP / 8 + B_THREADS - 1) / B_THREADS;
@@ -797,43 +813,50 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
     }
   };
 
-  uint4 rq[Cfg::NLF], rk[Cfg::NLF], rv[Cfg::NLD], rd[Cfg::NLD];
-  TokScalars sc;
-  auto issue = [&](int n) __attribute__((always_inline)) {
+  // DEPTH register sets: while chunk n computes, chunks n-1 .. n-DEPTH are in flight
+  constexpr int DEPTH = Cfg::DEPTH;
+  uint4 rq[DEPTH][Cfg::NLF], rk[DEPTH][Cfg::NLF], rv[DEPTH][Cfg::NLD], rd[DEPTH][Cfg::NLD];
+  TokScalars sc[DEPTH];
+  auto issue = [&](auto set, int n) __attribute__((always_inline)) {
+    constexpr int S = decltype(set)::value;
     if (n >= n0) {
-      load_tile8<FP>(rq, fq + offF, n * C, L, F, vecF);
-      load_tile8<FP>(rk, fk + offF, n * C, L, F, vecF);
-      load_tile8<DP>(rv, v + offD, n * C, L, D, vecD);
-      load_tile8<DP>(rd, dy + offD, n * C, L, D, vecD);
-      if (wave == 0) sc = load_scalars(lgb, den_in, delta_in, p_in, offL, n * C + lane, L);
+      load_tile8<FP>(rq[S], fq + offF, n * C, L, F, vecF);
+      load_tile8<FP>(rk[S], fk + offF, n * C, L, F, vecF);
+      load_tile8<DP>(rv[S], v + offD, n * C, L, D, vecD);
+      load_tile8<DP>(rd[S], dy + offD, n * C, L, D, vecD);
+      if (wave == 0) sc[S] = load_scalars(lgb, den_in, delta_in, p_in, offL, n * C + lane, L);
     }
   };
   // chunk n's tiles and per-token scalars (scalars into the buffers of parity n & 1)
-  auto stage = [&](int n) __attribute__((always_inline)) {
-    store_tile8<FP>(rq, fq_l, PF);
-    store_tile8<FP>(rk, fk_l, PF);
-    store_tile8<DP>(rv, v_l, PD);
-    store_tile8<DP>(rd, dy_l, PD);
+  auto stage = [&](auto set, int n) __attribute__((always_inline)) {
+    constexpr int S = decltype(set)::value;
+    store_tile8<FP>(rq[S], fq_l, PF);
+    store_tile8<FP>(rk[S], fk_l, PF);
+    store_tile8<DP>(rv[S], v_l, PD);
+    store_tile8<DP>(rd[S], dy_l, PD);
     const int b = n & 1;
     if (wave == 0)
-      bwd_scalars(sc.g, sc.den, sc.delta, sc.p, lane, lgs, qs, ks, rdec, invd + 64 * b,
-                  dels + 64 * b, ps + 64 * b, qh + 64 * b, dw + 64 * b);
+      bwd_scalars(sc[S].g, sc[S].den, sc[S].delta, sc[S].p, lane, lgs, qs, ks, rdec,
+                  invd + 64 * b, dels + 64 * b, ps + 64 * b, qh + 64 * b, dw + 64 * b);
   };
-  issue(n1 - 1);
-  stage(n1 - 1);
+  issue(SET0, n1 - 1);
+  if constexpr (DEPTH == 2) issue(SET1, n1 - 2);
+  stage(SET0, n1 - 1);
   publish();
   __syncthreads();
 
   const int kind = wave >> 2, qt = (wave >> 1) & 1, kt = wave & 1;   // phase-1 tile
   const int ki = kt * 32 + col;                                       // its key (lane)
-  for (int n = n1 - 1; n >= n0; --n) {
+  // chunk n is in LDS and register set `set` is free; the next set holds chunk n-1
+  auto step = [&](auto set, int n) __attribute__((always_inline)) {
+    constexpr int S = decltype(set)::value;
     const int t0 = n * C;
     const int cur = n & 1;
     const float* invc = invd + 64 * cur;
     const float* delsc = dels + 64 * cur;
     const float* qhc = qh + 64 * cur;
     const float* dwc = dw + 64 * cur;
-    issue(n - 1);
+    issue(set, n - DEPTH);
     // ---- phase 1: one 32x32 tile (queries x keys) of s or dy v^T per wave ----
     {
       f32x16 acc = zero16();
@@ -1000,7 +1023,7 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
       if (lane == 0) csum[(size_t)bh * NT + n] = g;
     }
     publish();
-    if (n - 1 >= n0) stage(n - 1);
+    if (n - 1 >= n0) stage(std::integral_constant<int, (S + 1) % DEPTH>{}, n - 1);
     for (int f = tid; f < FP; f += B_THREADS) {
       float za = dzs[f] * r_n;
 #pragma unroll
@@ -1008,6 +1031,11 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
       dzs[f] = za;
     }
     __syncthreads();
+  };
+  for (int n = n1 - 1; n >= n0; n -= DEPTH) {
+    step(SET0, n);
+    if constexpr (DEPTH == 2)
+      if (n - 1 >= n0) step(SET1, n - 1);
   }
 }
 
