@@ -1104,7 +1104,7 @@ size_t gla_bwd_workspace(int B, int H, int L, int F, int D, int gate_per_head) {
   (void)gate_per_head;
   const int BH = B * H;
   int G, cps;
-  gla_segments(BH, L, &G, &cps);
+  gla_segments(BH, L, F, &G, &cps);
   const size_t NT = (L + GLA_C - 1) / GLA_C;
   return (4 * (size_t)BH * L + 2 * gla_segment_floats(BH, G, F, D) + (size_t)BH * NT) *
          sizeof(float);
@@ -1118,7 +1118,7 @@ static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v
   const int BH = B * H;
   const size_t BHL = (size_t)BH * L;
   int G, cps;
-  gla_segments(BH, L, &G, &cps);
+  gla_segments(BH, L, F, &G, &cps);
   constexpr int SEG = SegRec<FP, DP>::SIZE;
   constexpr int LDS_A = BwdA<FP, DP>::BYTES, LDS_S = BwdS<FP, DP>::BYTES;
   constexpr int LDS_B = BwdB<FP, DP>::BYTES;

@@ -8,7 +8,7 @@
 namespace lz {
 
 constexpr int GLA_C = 64;            // chunk length (tokens)
-constexpr int GLA_TARGET_WG = 512;   // (b, h, segment) workgroups wanted per launch
+constexpr int GLA_TARGET_WG = 512;   // (b, h, segment) workgroups wanted per launch (F <= 128)
 
 // compile-time register-set selectors of the double-buffered chunk prefetch
 constexpr std::integral_constant<int, 0> SET0{};
@@ -16,7 +16,7 @@ constexpr std::integral_constant<int, 1> SET1{};
 
 int gla_padded_dim(int n);
 bool gla_dims_supported(int F, int D);
-void gla_segments(int BH, int L, int* G, int* cps);
+void gla_segments(int BH, int L, int F, int* G, int* cps);
 size_t gla_segment_floats(int BH, int G, int F, int D);
 
 // Rows [t0, t0+64) of a [L x ncols] bf16 matrix into registers, 16 bytes per

@@ -417,9 +417,12 @@ bool gla_dims_supported(int F, int D) {
 }
 
 // Segments per (b, h): enough (b, h, segment) workgroups to fill the GPU.
-void gla_segments(int BH, int L, int* G, int* cps) {
+// Segments per (b, h) so that B*H*G workgroups fill the GPU: two forward
+// workgroups per CU up to F = 128, one beyond (the LDS of a 256-wide chunk).
+void gla_segments(int BH, int L, int F, int* G, int* cps) {
   const int NT = (L + GLA_C - 1) / GLA_C;
-  int g = (GLA_TARGET_WG + BH - 1) / BH;
+  const int target = gla_padded_dim(F) > 128 ? GLA_TARGET_WG / 2 : GLA_TARGET_WG;
+  int g = (target + BH - 1) / BH;
   g = g < 1 ? 1 : (g > NT ? NT : g);
   const int c = (NT + g - 1) / g;
   *cps = c;
@@ -435,7 +438,7 @@ size_t gla_segment_floats(int BH, int G, int F, int D) {
 
 size_t gla_fwd_workspace(int B, int H, int L, int F, int D) {
   int G, cps;
-  gla_segments(B * H, L, &G, &cps);
+  gla_segments(B * H, L, F, &G, &cps);
   return gla_segment_floats(B * H, G, F, D) * sizeof(float);
 }
 
@@ -484,7 +487,7 @@ static hipError_t launch_gla_fwd_t(const void* fq, const void* fk, const void* v
   using Cfg = GlaFwd<FP, DP>;
   const int BH = B * H;
   int G, cps;
-  gla_segments(BH, L, &G, &cps);
+  gla_segments(BH, L, F, &G, &cps);
   float* seg_state = ws;
   if (G > 1) {
     hipError_t e = launch_gla_fwd_states_t<FP, DP>(fk, v, lg, seg_state,

@@ -105,9 +105,11 @@ def test_layer_prologue_workspace_sizes(lib, b, length, heads, kv, hd, f):
         4 * (nq + nk) * fp * hd
 
 
-def segments(bh, length, target=512, chunk=64):
+def segments(bh, length, f=64, chunk=64):
     """The library's split of each (b, h) sequence into segments (so that
-    B*H*segments fills the GPU): returns (segments, chunks per segment)."""
+    B*H*segments fills the GPU: 512 workgroups up to F = 128, 256 beyond):
+    returns (segments, chunks per segment)."""
+    target = 256 if padded(f) > 128 else 512
     nt = -(-length // chunk)
     g = min(max(-(-target // bh), 1), nt)
     cps = -(-nt // g)
@@ -127,7 +129,7 @@ def seg_floats(bh, g, f, d):
     (4, 16, 1553, 64, 64, 1), (1, 4, 1, 256, 64, 0)])
 def test_workspace_sizes(lib, b, h, length, f, d, per_head):
     bh = b * h
-    g, _ = segments(bh, length)
+    g, _ = segments(bh, length, f)
     assert lib.lz_gla_fwd_workspace_bytes(b, h, length, f, d, per_head, 64) == \
         4 * seg_floats(bh, g, f, d)
     assert lib.lz_gla_bwd_workspace_bytes(b, h, length, f, d, per_head, 64) == \
@@ -139,6 +141,7 @@ def test_segment_split():
     assert segments(32, 2048) == (16, 2)        # training shape: 16 segments of 2 chunks
     assert segments(64, 1553) == (7, 4)         # ragged: the last segment is shorter
     assert segments(6, 1) == (1, 1)
+    assert segments(128, 4096, f=256) == (2, 32)   # config-5 layer shape: one workgroup per CU
 
 
 def test_swa_workspace_sizes(lib):
