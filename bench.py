@@ -186,6 +186,7 @@ def layer_stack(torch, steps, warmup, one_layer=False):
     a Llama-3.2-1B-shaped model whose attention blocks are LizardAttention,
     and of one such layer alone; medians of per-step events."""
     from transformers import LlamaConfig, LlamaForCausalLM
+    from lizard_reproduction_amd import kernels
     from lizard_reproduction_amd.layer import LizardAttention, to_lizard
     cfg = LlamaConfig(hidden_size=2048, intermediate_size=8192, num_hidden_layers=16,
                       num_attention_heads=32, num_key_value_heads=8, head_dim=64,
@@ -226,6 +227,25 @@ def layer_stack(torch, steps, warmup, one_layer=False):
     print(f"[bench] config5 one layer: {out}", file=sys.stderr, flush=True)
     if one_layer:
         return out
+
+    # recurrent decode of the GLA branch at the layer's shape: one token per
+    # (b, h) after a 4096-token prefill (state [B, H, F*D + F] fp32 in HBM)
+    fq = torch.rand(batch, 32, length, 256, device="cuda").bfloat16()
+    fk = torch.rand_like(fq)
+    v = torch.randn(batch, 32, length, 64, device="cuda").bfloat16()
+    lg = torch.nn.functional.logsigmoid(torch.randn(batch, length, device="cuda") + 3)
+    _, state = kernels.gla_prefill(fq, fk, v, lg)
+    out["gla_prefill_ms"] = round(median_ms(torch, lambda: kernels.gla_prefill(fq, fk, v, lg),
+                                            5, 2), 3)
+    t_dec = median_ms(torch, lambda: kernels.gla_decode_step(fq[:, :, -1], fk[:, :, -1],
+                                                              v[:, :, -1], lg[:, -1], state),
+                      50, 5)
+    out["gla_decode_step_us"] = round(t_dec * 1e3, 2)
+    out["gla_decode_state_gbs"] = round(2 * state.numel() * 4 / (t_dec * 1e-3) / 1e9, 1)
+    del fq, fk, v, lg, state
+    torch.cuda.empty_cache()
+    print(f"[bench] config5 decode: prefill {out['gla_prefill_ms']} ms, step "
+          f"{out['gla_decode_step_us']} us", file=sys.stderr, flush=True)
 
     model = LlamaForCausalLM(cfg).to(torch.bfloat16)
     to_lizard(model, **opts)

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define LZ_ABI_VERSION 6
+#define LZ_ABI_VERSION 7
 
 /* ABI version of the loaded library (LZ_ABI_VERSION). */
 int lz_abi_version(void);
@@ -63,6 +63,31 @@ size_t lz_gla_fwd_workspace_bytes(int batch, int heads, int length, int nf, int 
 int lz_gla_fwd(const void* fq, const void* fk, const void* v, const float* log_gamma, void* y,
                int batch, int heads, int length, int nf, int nd, int gate_per_head, int chunk,
                void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * GLA prefill: lz_gla_fwd that also writes the recurrent state after the last
+ * token, for decoding.  No counterpart in the reference (it has no decode
+ * path); the state is that of its recurrent form (tests/test_lizard.py:41-52):
+ *   S_L = sum_t (prod_{s>t} gamma_s) fk_t v_t^T,  z_L = sum_t (prod_{s>t} gamma_s) fk_t
+ *   state  f32 [B, H, nf*nd + nf]: S row-major [nf][nd], then z [nf]
+ * Other arguments as lz_gla_fwd (same workspace).
+ */
+int lz_gla_prefill(const void* fq, const void* fk, const void* v, const float* log_gamma,
+                   void* y, float* state, int batch, int heads, int length, int nf, int nd,
+                   int gate_per_head, int chunk, void* workspace, size_t workspace_bytes,
+                   void* stream);
+
+/*
+ * GLA decode step: one new token per (b, h) on the recurrent form
+ * (tests/test_lizard.py:41-52), state updated in place:
+ *   S <- gamma S + fk v^T,  z <- gamma z + fk,  y = fq S / max(fq . z, FLT_MIN)
+ *   fq, fk  bf16 [B, H, nf];  v  bf16 [B, H, nd];  y  bf16 [B, H, nd]
+ *   log_gamma  f32 [B] (gate_per_head = 0) or [B, H];  gamma = exp(log_gamma)
+ *   state  f32 [B, H, nf*nd + nf] as written by lz_gla_prefill (zeros: empty prefix)
+ */
+int lz_gla_decode_step(const void* fq, const void* fk, const void* v, const float* log_gamma,
+                       float* state, void* y, int batch, int heads, int nf, int nd,
+                       int gate_per_head, void* stream);
 
 /* Workspace bytes lz_gla_bwd needs for these sizes. */
 size_t lz_gla_bwd_workspace_bytes(int batch, int heads, int length, int nf, int nd,

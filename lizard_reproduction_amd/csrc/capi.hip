@@ -11,7 +11,10 @@
 namespace lz {
 hipError_t launch_gla_fwd(const void* fq, const void* fk, const void* v, const float* lg, void* y,
                           int B, int H, int L, int F, int D, int gate_per_head, float* ws,
-                          hipStream_t st);
+                          float* final_state, hipStream_t st);
+hipError_t launch_gla_decode(const void* fq, const void* fk, const void* v, const float* lg,
+                             float* state, void* y, int B, int H, int F, int D,
+                             int gate_per_head, hipStream_t st);
 size_t gla_fwd_workspace(int B, int H, int L, int F, int D);
 hipError_t launch_gla_bwd(const void* fq, const void* fk, const void* v, const float* lg,
                           const void* dy, void* dfq, void* dfk, void* dv, float* dlg,
@@ -108,9 +111,35 @@ extern "C" int lz_gla_fwd(const void* fq, const void* fk, const void* v, const f
   if (need && (!workspace || workspace_bytes < need))
     return fail(1, "gla_fwd: workspace of %zu bytes given, %zu needed", workspace_bytes, need);
   return hip_status(lz::launch_gla_fwd(fq, fk, v, log_gamma, y, batch, heads, length, nf, nd,
-                                       gate_per_head ? 1 : 0, (float*)workspace,
+                                       gate_per_head ? 1 : 0, (float*)workspace, nullptr,
                                        (hipStream_t)stream),
                     "gla_fwd");
+}
+
+extern "C" int lz_gla_prefill(const void* fq, const void* fk, const void* v,
+                              const float* log_gamma, void* y, float* state, int batch, int heads,
+                              int length, int nf, int nd, int gate_per_head, int chunk,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+  if (int rc = check_gla(fq, fk, v, log_gamma, batch, heads, length, nf, nd, chunk)) return rc;
+  if (!y || !state) return fail(1, "gla_prefill: null output pointer");
+  const size_t need = lz::gla_fwd_workspace(batch, heads, length, nf, nd);
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(1, "gla_prefill: workspace of %zu bytes given, %zu needed", workspace_bytes,
+                need);
+  return hip_status(lz::launch_gla_fwd(fq, fk, v, log_gamma, y, batch, heads, length, nf, nd,
+                                       gate_per_head ? 1 : 0, (float*)workspace, state,
+                                       (hipStream_t)stream),
+                    "gla_prefill");
+}
+
+extern "C" int lz_gla_decode_step(const void* fq, const void* fk, const void* v,
+                                  const float* log_gamma, float* state, void* y, int batch,
+                                  int heads, int nf, int nd, int gate_per_head, void* stream) {
+  if (int rc = check_gla(fq, fk, v, log_gamma, batch, heads, 1, nf, nd, 64)) return rc;
+  if (!state || !y) return fail(1, "gla_decode_step: null state or output pointer");
+  return hip_status(lz::launch_gla_decode(fq, fk, v, log_gamma, state, y, batch, heads, nf, nd,
+                                          gate_per_head ? 1 : 0, (hipStream_t)stream),
+                    "gla_decode_step");
 }
 
 extern "C" size_t lz_gla_bwd_workspace_bytes(int batch, int heads, int length, int nf, int nd,

@@ -77,8 +77,8 @@ template <int FP, int DP>
 __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
     const bf16* __restrict__ fq, const bf16* __restrict__ fk, const bf16* __restrict__ v,
     const float* __restrict__ log_gamma, bf16* __restrict__ y,
-    const float* __restrict__ seg_state, int H, int L, int F, int D, int gate_per_head, int G,
-    int cps) {
+    const float* __restrict__ seg_state, float* __restrict__ final_state, int H, int L, int F,
+    int D, int gate_per_head, int G, int cps) {
   using Cfg = GlaFwd<FP, DP>;
   constexpr int C = Cfg::C, PF = Cfg::PF, PD = Cfg::PD;
   constexpr int NFT = Cfg::NFT, NDT = Cfg::NDT;
@@ -245,6 +245,99 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
     if (tid < FP) zs[tid] = zs[tid] * r_n + sum_parts<FP>(zp, tid);
     __syncthreads();
   }
+
+  // the state after the whole sequence, [F][D] fp32 then z [F], for decoding
+  if (final_state && seg == G - 1) {
+    float* fs = final_state + (size_t)bh * ((size_t)F * D + F);
+    if (active && RD::primary(wave)) {
+#pragma unroll
+      for (int i = 0; i < NDW; ++i) {
+        const int d = dtile(i) * 32 + col;
+#pragma unroll
+        for (int ft = 0; ft < NFT; ++ft)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int f = ft * 32 + acc_row(r, h);
+            if (f < F && d < D) fs[(size_t)f * D + d] = S[i][ft][r];
+          }
+      }
+    }
+    for (int f = tid; f < F; f += 256) fs[(size_t)F * D + f] = zs[f];
+  }
+}
+
+// ----------------------------------------------------------------------------
+// decode step: one token per (b, h) on the recurrent form
+//   S <- gamma S + fk v^T,  z <- gamma z + fk,  y = fq S / max(fq . z, FLT_MIN)
+// (tests/test_lizard.py:41-52 of the reference), state [F][D] fp32 then z [F]
+// per (b, h), updated in place.  Thread (g, d) of the 256 walks features
+// f = g, g + NG, ... of column d (NG = 256 / DP groups); the fq . S_new partial
+// sums of the groups meet in LDS.
+// ----------------------------------------------------------------------------
+template <int DP>
+__global__ __launch_bounds__(256) void gla_decode_kernel(
+    const bf16* __restrict__ fq, const bf16* __restrict__ fk, const bf16* __restrict__ v,
+    const float* __restrict__ log_gamma, float* __restrict__ state, bf16* __restrict__ y, int H,
+    int F, int D, int gate_per_head) {
+  constexpr int NG = 256 / DP;
+  __shared__ float fq_s[256], fk_s[256], part[256], red[4];
+  const int bh = blockIdx.x, tid = threadIdx.x;
+  const int g = tid / DP, d = tid % DP;
+  const float gam = fexp(log_gamma[gate_per_head ? bh : bh / H]);
+  const bf16* fqb = fq + (size_t)bh * F;
+  const bf16* fkb = fk + (size_t)bh * F;
+  float* Sb = state + (size_t)bh * ((size_t)F * D + F);
+  float* zb = Sb + (size_t)F * D;
+  for (int f = tid; f < F; f += 256) {
+    fq_s[f] = to_f32(fqb[f]);
+    fk_s[f] = to_f32(fkb[f]);
+  }
+  __syncthreads();
+  // z and fq . z
+  float qz = 0.f;
+  for (int f = tid; f < F; f += 256) {
+    const float zn = gam * zb[f] + fk_s[f];
+    zb[f] = zn;
+    qz += fq_s[f] * zn;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) qz += __shfl_xor(qz, off);
+  if ((tid & 63) == 0) red[tid >> 6] = qz;
+  // S and fq . S
+  float num = 0.f;
+  if (d < D) {
+    const float vd = to_f32(v[(size_t)bh * D + d]);
+    for (int f = g; f < F; f += NG) {
+      const float sn = gam * Sb[(size_t)f * D + d] + fk_s[f] * vd;
+      Sb[(size_t)f * D + d] = sn;
+      num += fq_s[f] * sn;
+    }
+  }
+  part[tid] = num;
+  __syncthreads();
+  if (g == 0 && d < D) {
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < NG; ++j) s += part[j * DP + d];
+    const float den = (red[0] + red[1]) + (red[2] + red[3]);
+    y[(size_t)bh * D + d] = to_bf16(s / fmaxf(den, TINY));
+  }
+}
+
+hipError_t launch_gla_decode(const void* fq, const void* fk, const void* v, const float* lg,
+                             float* state, void* y, int B, int H, int F, int D,
+                             int gate_per_head, hipStream_t st) {
+  const int dp = D <= 32 ? 32 : (D <= 64 ? 64 : (D <= 128 ? 128 : 256));
+#define LZ_GLA_DEC(DPV)                                                                       \
+  if (dp == DPV) {                                                                          \
+    hipLaunchKernelGGL(gla_decode_kernel<DPV>, dim3(B * H), dim3(256), 0, st,                 \
+                       (const bf16*)fq, (const bf16*)fk, (const bf16*)v, lg, state, (bf16*)y, \
+                       H, F, D, gate_per_head);                                               \
+    return hipGetLastError();                                                               \
+  }
+  LZ_GLA_DEC(32) LZ_GLA_DEC(64) LZ_GLA_DEC(128) LZ_GLA_DEC(256)
+#undef LZ_GLA_DEC
+  return hipErrorInvalidValue;
 }
 
 // ----------------------------------------------------------------------------
@@ -483,7 +576,8 @@ hipError_t launch_gla_fwd_states(const void* fk, const void* v, const float* lg,
 template <int FP, int DP>
 static hipError_t launch_gla_fwd_t(const void* fq, const void* fk, const void* v,
                                    const float* lg, void* y, int B, int H, int L, int F, int D,
-                                   int gate_per_head, float* ws, hipStream_t st) {
+                                   int gate_per_head, float* ws, float* final_state,
+                                   hipStream_t st) {
   using Cfg = GlaFwd<FP, DP>;
   const int BH = B * H;
   int G, cps;
@@ -499,18 +593,19 @@ static hipError_t launch_gla_fwd_t(const void* fq, const void* fk, const void* v
   hipError_t e = ensure_lds<gla_fwd_kernel<FP, DP>>(Cfg::BYTES);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3(BH * G), dim3(256), Cfg::BYTES, st, (const bf16*)fq,
-                     (const bf16*)fk, (const bf16*)v, lg, (bf16*)y, (const float*)seg_state, H, L,
-                     F, D, gate_per_head, G, cps);
+                     (const bf16*)fk, (const bf16*)v, lg, (bf16*)y, (const float*)seg_state,
+                     final_state, H, L, F, D, gate_per_head, G, cps);
   return hipGetLastError();
 }
 
 hipError_t launch_gla_fwd(const void* fq, const void* fk, const void* v, const float* lg, void* y,
                           int B, int H, int L, int F, int D, int gate_per_head, float* ws,
-                          hipStream_t st) {
+                          float* final_state, hipStream_t st) {
   const int fp = gla_padded_dim(F), dp = gla_padded_dim(D);
 #define LZ_GLA_FWD(FPV, DPV) \
   if (fp == FPV && dp == DPV) \
-    return launch_gla_fwd_t<FPV, DPV>(fq, fk, v, lg, y, B, H, L, F, D, gate_per_head, ws, st);
+    return launch_gla_fwd_t<FPV, DPV>(fq, fk, v, lg, y, B, H, L, F, D, gate_per_head, ws,   \
+                                      final_state, st);
   LZ_GLA_FWD(32, 32) LZ_GLA_FWD(32, 64) LZ_GLA_FWD(32, 128)
   LZ_GLA_FWD(64, 32) LZ_GLA_FWD(64, 64) LZ_GLA_FWD(64, 128)
   LZ_GLA_FWD(128, 32) LZ_GLA_FWD(128, 64) LZ_GLA_FWD(128, 128)

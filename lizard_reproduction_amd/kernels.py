@@ -158,6 +158,72 @@ class _GLA(torch.autograd.Function):
         return tuple(g.to(d) for g, d in zip(grads, ctx.dtypes)) + (None,)
 
 
+def gla_prefill(fq, fk, v, log_gamma, chunk=CHUNK):
+    """``gla`` forward (no autograd) that also returns the recurrent state
+    after the last token, for decoding: ``(y, state)``, state fp32
+    ``[B, H, F*D + F]`` (S row-major ``[F][D]``, then z ``[F]``; see
+    ``split_state``).  The reference has no decode path; the state is that of
+    its recurrent form (tests/test_lizard.py:41-52)."""
+    _check_gla(fq, fk, v, log_gamma, chunk)
+    fq, fk, v = _bf16(fq), _bf16(fk), _bf16(v)
+    lg = log_gamma.float().contiguous()
+    b, h, length, nf = fq.shape
+    nd = v.shape[-1]
+    y = torch.empty_like(v)
+    state = torch.zeros(b, h, nf * nd + nf, device=fq.device, dtype=torch.float32)
+    if y.numel():
+        lib = _lib.load()
+        per_head = int(lg.dim() == 3)
+        nbytes = _gla_fwd_ws(b, h, length, nf, nd, per_head, chunk)
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=fq.device) if nbytes else None
+        rc = lib.lz_gla_prefill(_ptr(fq), _ptr(fk), _ptr(v), _ptr(lg), _ptr(y), _ptr(state), b, h,
+                                length, nf, nd, per_head, chunk, _ptr(ws), nbytes, _stream(fq))
+        _lib.check(rc, "lz_gla_prefill")
+    return y, state
+
+
+def new_state(batch, heads, nf, nd, device):
+    """The recurrent state of an empty prefix (zeros), ``[B, H, F*D + F]`` fp32."""
+    return torch.zeros(batch, heads, nf * nd + nf, device=device, dtype=torch.float32)
+
+
+def split_state(state, nf, nd):
+    """Views (S ``[B, H, F, D]``, z ``[B, H, F]``) of a recurrent state."""
+    b, h, _ = state.shape
+    return state[..., :nf * nd].view(b, h, nf, nd), state[..., nf * nd:]
+
+
+def gla_decode_step(fq, fk, v, log_gamma, state):
+    """One token per (b, h) on the recurrent form, updating ``state`` in place
+    (tests/test_lizard.py:41-52): S <- gamma S + fk v^T, z <- gamma z + fk,
+    y = fq S / max(fq . z, FLT_MIN), gamma = exp(log_gamma).
+
+    fq, fk ``[B, H, F]``, v ``[B, H, D]`` (cast to bf16), log_gamma ``[B]``
+    or ``[B, H]`` fp32, state from ``gla_prefill`` or ``new_state``.
+    Returns bf16 ``[B, H, D]``; no autograd."""
+    if fq.dim() != 3 or fk.shape != fq.shape or v.dim() != 3 or v.shape[:2] != fq.shape[:2]:
+        raise ValueError(f"gla_decode_step: fq, fk must be [B, H, F] and v [B, H, D], got "
+                         f"{tuple(fq.shape)}, {tuple(fk.shape)}, {tuple(v.shape)}")
+    b, h, nf = fq.shape
+    nd = v.shape[-1]
+    if log_gamma.shape not in ((b,), (b, h)):
+        raise ValueError(f"gla_decode_step: log_gamma must be [B] or [B, H], got "
+                         f"{tuple(log_gamma.shape)}")
+    if state.shape != (b, h, nf * nd + nf) or state.dtype != torch.float32 or \
+            not state.is_contiguous():
+        raise ValueError(f"gla_decode_step: state must be contiguous fp32 "
+                         f"[B, H, F*D + F] = {(b, h, nf * nd + nf)}, got {tuple(state.shape)} "
+                         f"{state.dtype}")
+    _require_gpu(fq, fk, v, log_gamma, state)
+    fq, fk, v = _bf16(fq), _bf16(fk), _bf16(v)
+    lg = log_gamma.float().contiguous()
+    y = torch.empty_like(v)
+    rc = _lib.load().lz_gla_decode_step(_ptr(fq), _ptr(fk), _ptr(v), _ptr(lg), _ptr(state),
+                                        _ptr(y), b, h, nf, nd, int(lg.dim() == 2), _stream(fq))
+    _lib.check(rc, "lz_gla_decode_step")
+    return y
+
+
 def gla(fq, fk, v, log_gamma, chunk=CHUNK):
     """Chunked gated linear attention (``src/kernels/gla.py:259-263``).
 

@@ -37,6 +37,9 @@ swa_kernel_api      awa; empty meta == meta of -1e4 (tests/test_kernels.py:
                     127-134)
 gla_chunked         == dense gla in fp64 for chunk 16/64, L in {1,77,150},
                     per-token and per-head gates, strong decay
+gla_recurrent_state outputs == gla_recurrent and dense gla (fp64); its state
+                    == the chunked restatement's final state; S, z
+                    decompose: fq_i S_i / fq_i z_i over i gives the outputs
 rope                rope_loop; relative-position invariance of q.k
 lizard_layer        lizard_layer_loop (fp64, 1e-10); with the GLA branch
                     zeroed, no sinks and an unbounded window it equals
@@ -203,6 +206,25 @@ def gla_recurrent(fq, fk, v, gamma):
     return torch.stack(outs, dim=2)
 
 
+def gla_recurrent_state(fq, fk, v, gamma):
+    """The recurrent form of ``gla_recurrent`` returning also the state after
+    the last token: (out, S [B, H, F, D], z [B, H, F]).  gamma is [B, L]
+    (shared by heads) or [B, H, L]."""
+    b, h, n, f = fq.shape
+    state = torch.zeros(b, h, f, v.shape[-1], dtype=fq.dtype)
+    norm = torch.zeros(b, h, f, dtype=fq.dtype)
+    outs = []
+    for i in range(n):
+        g = gamma[..., i]
+        g = g.view(b, 1, 1) if g.dim() == 1 else g.view(b, h, 1)
+        state = g[..., None] * state + fk[:, :, i, :, None] * v[:, :, i, None, :]
+        norm = g * norm + fk[:, :, i]
+        num = (fq[:, :, i, :, None] * state).sum(-2)
+        den = (fq[:, :, i] * norm).sum(-1, keepdim=True)
+        outs.append(num / den.clamp_min(TINY))
+    return torch.stack(outs, dim=2), state, norm
+
+
 def awa_loop(q, k, v, meta, window):
     """y_i = sum_{i-W<t<=i} e^{s_it} v_t / (sum_j e^{meta_j} + sum_t e^{s_it}),
     s_it = q_i . k_t / sqrt(d)."""
@@ -252,7 +274,8 @@ def _bf16(t):
     return t.to(torch.bfloat16).to(t.dtype)
 
 
-def gla_chunked(fq, fk, v, log_gamma, chunk=64, round_bf16=False, dtype=torch.float64):
+def gla_chunked(fq, fk, v, log_gamma, chunk=64, round_bf16=False, dtype=torch.float64,
+                return_state=False):
     """Chunkwise GLA with gates measured from each chunk's boundary.
 
     Within chunk n (tokens [nC, nC+C)), lg_j is the inclusive sum of
@@ -269,7 +292,9 @@ def gla_chunked(fq, fk, v, log_gamma, chunk=64, round_bf16=False, dtype=torch.fl
     operands (K~, a and the state used by Q~ S) are rounded as the kernel
     rounds them; Q~ stays unrounded, as in the kernel, which applies the row
     scale exp(lg_i) to the fp32 products fq . S and fq . z.
-    log_gamma: [B, L] or [B, H, L].  Returns [B, H, L, D].
+    log_gamma: [B, L] or [B, H, L].  Returns [B, H, L, D]; with
+    ``return_state`` also the state after the last token (S [B, H, F, D],
+    z [B, H, F]).
     """
     batch, heads, length, nf = fq.shape
     nd = v.shape[-1]
@@ -299,6 +324,8 @@ def gla_chunked(fq, fk, v, log_gamma, chunk=64, round_bf16=False, dtype=torch.fl
         r = torch.exp(lg_end)[..., None]                       # [B,H,1,1]
         state = state * r + torch.matmul(kt.transpose(-1, -2), vv)
         norm = norm * r[..., 0] + kt.sum(-2)
+    if return_state:
+        return out, state, norm
     return out
 
 

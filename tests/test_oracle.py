@@ -277,3 +277,37 @@ def test_checks_catch_planted_mistakes(monkeypatch):
     lg = torch.log(gamma)
     dense = lo.gla_kernel_api(fq, fk, v, lg, dtype=torch.float64)
     assert rel_err(lo.gla_chunked(fq, fk, v, -lg.abs() * 0.5, 4), dense) > 1e-3
+
+
+# -- recurrent state (decode form) ----------------------------------------------
+
+@pytest.mark.parametrize("per_head", [False, True])
+def test_recurrent_state_matches_recurrent_form_and_chunked_state(per_head):
+    fq, fk, v, gamma = gla_inputs(70, features=12, dim=10)
+    if per_head:
+        gamma = torch.sigmoid(2 * torch.randn(2, 3, 70)).double()
+    out, S, z = lo.gla_recurrent_state(fq, fk, v, gamma)
+    lg = torch.log(gamma)
+    dense = lo.gla_kernel_api(fq, fk, v, lg, dtype=torch.float64)
+    assert rel_err(out, dense) < EXACT
+    if not per_head:
+        assert rel_err(out, lo.gla_recurrent(fq, fk, v, gamma)) < EXACT
+    for chunk in (16, 64):
+        c_out, c_S, c_z = lo.gla_chunked(fq, fk, v, lg, chunk, return_state=True)
+        assert rel_err(c_S, S) < EXACT and rel_err(c_z, z) < EXACT
+        assert rel_err(c_out, dense) < EXACT
+
+
+def test_recurrent_state_continues_a_prefix():
+    """Running the recurrence on a prefix, then on the rest from that state,
+    gives the whole sequence's outputs: what decoding after a prefill does."""
+    fq, fk, v, gamma = gla_inputs(40, features=8, dim=6)
+    full, S_full, z_full = lo.gla_recurrent_state(fq, fk, v, gamma)
+    _, S, z = lo.gla_recurrent_state(fq[:, :, :25], fk[:, :, :25], v[:, :, :25], gamma[:, :25])
+    for i in range(25, 40):
+        g = gamma[:, i].view(-1, 1, 1)
+        S = g[..., None] * S + fk[:, :, i, :, None] * v[:, :, i, None, :]
+        z = g * z + fk[:, :, i]
+        y = (fq[:, :, i, :, None] * S).sum(-2) / (fq[:, :, i] * z).sum(-1, keepdim=True)
+        assert rel_err(y, full[:, :, i]) < EXACT
+    assert rel_err(S, S_full) < EXACT and rel_err(z, z_full) < EXACT
