@@ -187,21 +187,147 @@ __device__ __forceinline__ bf16x8 row_operand(const bf16* tile, int pitch, int r
   return *reinterpret_cast<const bf16x8*>(tile + row * pitch + col0 + 8 * h);
 }
 
-// 16-byte global load of columns [c, c+8) of row `row` of a row-major
-// [nrows x ncols] bf16 matrix, zero outside it.  `vec` (ncols % 8 == 0)
-// selects the single vector load; otherwise elements are loaded one by one.
-__device__ __forceinline__ uint4 gload8(const bf16* __restrict__ base, int row, int c, int nrows,
-                                        int ncols, bool vec) {
-  if (row >= nrows) return make_uint4(0, 0, 0, 0);
-  const bf16* p = base + (size_t)row * ncols + c;
-  if (vec) {
-    if (c < ncols) return *reinterpret_cast<const uint4*>(p);
-    return make_uint4(0, 0, 0, 0);
-  }
+// Buffer resources.  A resource covers [base, base + bytes) of global memory;
+// a buffer load at a byte offset at or past `bytes` returns zeros and a
+// buffer store there is dropped (the hardware's range check), so tile edges
+// cost no branches.  Per-lane branches around loads are what this avoids: the
+// compiler waits for each such load to land before issuing the next.  Every
+// resource here spans one (batch, head) slab or one tensor of under 2 GiB
+// (the host entry points check), so OOB is past the end of all of them.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr uint32_t OOB = 0x80000000u;
+constexpr int RSRC_WORD3 = 0x00020000;   // gfx9 dword 3: 32-bit data format, no swizzle
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, size_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0,
+                                           (int)(uint32_t)(bytes < OOB ? bytes : OOB), RSRC_WORD3);
+}
+
+__device__ __forceinline__ uint4 bload16(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+__device__ __forceinline__ float bload_f32(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+
+// Columns [c, c+8) of row `row` of a row-major [nrows x ncols] bf16 matrix
+// behind resource r, zero outside it (rows < 0 or >= nrows included).
+// Vector form (ncols % 8 == 0): an item is wholly inside or outside a row.
+__device__ __forceinline__ uint4 bload8_vec(rsrc_t r, int row, int c, int ncols) {
+  return bload16(r, (row >= 0 && c < ncols) ? (uint32_t)(row * ncols + c) * 2u : OOB);
+}
+
+// Element form for any ncols: eight 2-byte loads.
+__device__ __forceinline__ uint4 bload8_elem(rsrc_t r, int row, int c, int ncols) {
   bf16x8 v;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) v[e] = (c + e < ncols) ? p[e] : to_bf16(0.f);
+  for (int e = 0; e < 8; ++e) {
+    const uint32_t off = (row >= 0 && c + e < ncols) ? (uint32_t)(row * ncols + c + e) * 2u : OOB;
+    v[e] = __builtin_bit_cast(bf16, __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
+  }
   return __builtin_bit_cast(uint4, v);
+}
+
+// One 8-column item; `vec` (ncols % 8 == 0, uniform) picks the vector form.
+__device__ __forceinline__ uint4 gload8(const bf16* __restrict__ base, int row, int c, int nrows,
+                                        int ncols, bool vec) {
+  const rsrc_t r = make_rsrc(base, (size_t)nrows * ncols * 2);
+  return vec ? bload8_vec(r, row, c, ncols) : bload8_elem(r, row, c, ncols);
+}
+
+// Row `row`, columns c0 .. c0+31 of a row-major [nrows x ncols] bf16 matrix
+// behind r, from one column of a 32x32 fp32 accumulator tile (lane l holds
+// tile column l % 32, register k the tile row acc_row(k, h), which is the
+// matrix column c0 + acc_row(k, h)), times `scale`; rows past nrows are
+// dropped.  A permlane32 swap between the two lane halves first gives half h
+// the runs c0 + 16 j + 8 h + {0..7} (j = 0, 1), so each lane writes two
+// 16-byte pieces (vec: ncols % 8 == 0) rather than four 8-byte ones.
+template <int AUX = 0>
+__device__ __forceinline__ void store_acc_row_bf16(rsrc_t r, int row, int c0, int ncols, bool vec,
+                                                   const f32x16& o, float scale, int h) {
+  uint32_t w[8];   // w[2g], w[2g+1]: rows 8g + 4h + {0..3} of the tile, as bf16 pairs
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const bf16x4 p = {to_bf16(o[4 * g] * scale), to_bf16(o[4 * g + 1] * scale),
+                      to_bf16(o[4 * g + 2] * scale), to_bf16(o[4 * g + 3] * scale)};
+    const uint2 u = __builtin_bit_cast(uint2, p);
+    w[2 * g] = u.x;
+    w[2 * g + 1] = u.y;
+  }
+  // lanes 32..63 of w[4j + k] <-> lanes 0..31 of w[4j + 2 + k]
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const auto sw = __builtin_amdgcn_permlane32_swap(w[4 * j + k], w[4 * j + 2 + k], false, false);
+      w[4 * j + k] = sw[0];
+      w[4 * j + 2 + k] = sw[1];
+    }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int col = c0 + 16 * j + 8 * h;
+    if (vec) {
+      typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+      const u32x4 v = {w[4 * j], w[4 * j + 1], w[4 * j + 2], w[4 * j + 3]};
+      __builtin_amdgcn_raw_buffer_store_b128(
+          v, r, (row >= 0 && col < ncols) ? (uint32_t)(row * ncols + col) * 2u : OOB, 0, AUX);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint16_t x = (uint16_t)(w[4 * j + (e >> 1)] >> (16 * (e & 1)));
+        __builtin_amdgcn_raw_buffer_store_b16(
+            x, r, (row >= 0 && col + e < ncols) ? (uint32_t)(row * ncols + col + e) * 2u : OOB, 0,
+            AUX);
+      }
+    }
+  }
+}
+
+// The same row of a [nrows x ncols] OutT matrix at base: bf16 through
+// store_acc_row_bf16; fp32 as four 16-byte stores per lane (already whole
+// 16-byte pieces).  Every lane of the wave must take part (the bf16 form
+// swaps registers between lane halves); rows at or past nrows are skipped.
+template <typename OutT>
+__device__ __forceinline__ void store_acc_row(OutT* __restrict__ base, int row, int c0, int nrows,
+                                              int ncols, const f32x16& g, float scale, int h) {
+  if constexpr (sizeof(OutT) == 2) {
+    store_acc_row_bf16(make_rsrc(base, (size_t)nrows * ncols * 2), row, c0, ncols,
+                       (ncols & 7) == 0, g, scale, h);
+  } else {
+    if (row < nrows) {
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4)
+        store4<OutT>(base, row, c0 + 8 * g4 + 4 * h, ncols, g[4 * g4] * scale,
+                     g[4 * g4 + 1] * scale, g[4 * g4 + 2] * scale, g[4 * g4 + 3] * scale);
+    }
+  }
+}
+
+// Items idx = threadIdx.x + NT i (i < N, idx < ITEMS) of a [rows x KP/8]
+// grid of 8-column items starting at row r0: item idx covers row
+// r0 + idx / (KP/8), columns 8 (idx % (KP/8)).  The uniform `vec` test sits
+// outside the unrolled loop, so the vector form is straight-line loads.
+template <int KP, int NT, int N, int ITEMS>
+__device__ __forceinline__ void load_items(uint4 (&reg)[N], const bf16* __restrict__ base, int r0,
+                                           int nrows, int ncols, bool vec) {
+  constexpr int K8 = KP / 8;
+  const rsrc_t r = make_rsrc(base, (size_t)nrows * ncols * 2);
+  if (vec) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int idx = threadIdx.x + NT * i;
+      if (ITEMS % NT == 0 || idx < ITEMS)
+        reg[i] = bload8_vec(r, r0 + idx / K8, (idx % K8) * 8, ncols);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int idx = threadIdx.x + NT * i;
+      if (ITEMS % NT == 0 || idx < ITEMS)
+        reg[i] = bload8_elem(r, r0 + idx / K8, (idx % K8) * 8, ncols);
+    }
+  }
 }
 
 __device__ __forceinline__ bf16x8 scale8(const bf16x8& x, float s) {

@@ -64,13 +64,7 @@ constexpr int B_THREADS = 64 * B_WAVES;
 template <int KP, int N>
 __device__ __forceinline__ void load_tile8(uint4 (&reg)[N], const bf16* __restrict__ base, int t0,
                                            int L, int ncols, bool vec) {
-  constexpr int K8 = KP / 8, ITEMS = GLA_C * K8;
-#pragma unroll
-  for (int i = 0; i < N; ++i) {
-    const int idx = threadIdx.x + B_THREADS * i;
-    if (ITEMS % B_THREADS == 0 || idx < ITEMS)
-      reg[i] = gload8(base, t0 + idx / K8, (idx % K8) * 8, L, ncols, vec);
-  }
+  load_items<KP, B_THREADS, N, GLA_C * KP / 8>(reg, base, t0, L, ncols, vec);
 }
 
 template <int KP, int N>
@@ -451,12 +445,7 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
         }
         ps += xhalf(ps);
         if (h == 0) pp[ft * 64 + q] = tok < L ? ps : 0.f;
-        if (tok < L) {
-#pragma unroll
-          for (int g4 = 0; g4 < 4; ++g4)
-            store4<OutT>(dfq + offF, tok, ft * 32 + 8 * g4 + 4 * h, F, g[4 * g4], g[4 * g4 + 1],
-                         g[4 * g4 + 2], g[4 * g4 + 3]);
-        }
+        store_acc_row<OutT>(dfq + offF, tok, ft * 32, L, F, g, 1.f, h);
       }
     }
     // S^T <- r S^T + V^T K~ for the owned tiles
@@ -944,13 +933,7 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
 #pragma unroll
         for (int qb = 0; qb < 4; ++qb)
           g = mfma(tr_operand(dy_l, PD, 16 * qb, dt * 32, lane), fa[(hk * 4 + qb) * 64 + lane], g);
-        const int tok = t0 + key;
-        if (tok < L) {
-#pragma unroll
-          for (int g4 = 0; g4 < 4; ++g4)
-            store4<OutT>(dv + offD, tok, dt * 32 + 8 * g4 + 4 * h, D, g[4 * g4], g[4 * g4 + 1],
-                         g[4 * g4 + 2], g[4 * g4 + 3]);
-        }
+        store_acc_row<OutT>(dv + offD, t0 + key, dt * 32, L, D, g, 1.f, h);
       }
     }
     // dS <- r_n dS + fq^T dY^ for the owned tiles
@@ -999,12 +982,7 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
         }
         pks += xhalf(pks);
         if (h == 0) pk[ft * 64 + key] = pks;
-        if (tok < L) {
-#pragma unroll
-          for (int g4 = 0; g4 < 4; ++g4)
-            store4<OutT>(dfk + offF, tok, ft * 32 + 8 * g4 + 4 * h, F, g[4 * g4],
-                         g[4 * g4 + 1], g[4 * g4 + 2], g[4 * g4 + 3]);
-        }
+        store_acc_row<OutT>(dfk + offF, tok, ft * 32, L, F, g, 1.f, h);
       }
     }
     __syncthreads();

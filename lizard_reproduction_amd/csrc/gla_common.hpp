@@ -25,12 +25,7 @@ size_t gla_segment_floats(int BH, int G, int F, int D);
 template <int KP, int N>
 __device__ __forceinline__ void load_chunk(uint4 (&reg)[N], const bf16* __restrict__ base, int t0,
                                            int L, int ncols, bool vec) {
-  constexpr int K8 = KP / 8;
-#pragma unroll
-  for (int i = 0; i < N; ++i) {
-    const int idx = threadIdx.x + 256 * i;
-    reg[i] = gload8(base, t0 + idx / K8, (idx % K8) * 8, L, ncols, vec);
-  }
+  load_items<KP, 256, N, 256 * N>(reg, base, t0, L, ncols, vec);
 }
 
 template <int KP, int N>
@@ -121,8 +116,9 @@ __device__ __forceinline__ void gate_scan(float g, int lane, float* lgs, float* 
   }
 }
 
+// log_gamma of token t of a gate row of length L, 0 past its end
 __device__ __forceinline__ float gate_at(const float* __restrict__ lgb, int t, int L) {
-  return t < L ? lgb[t] : 0.f;
+  return bload_f32(make_rsrc(lgb, (size_t)L * 4), (uint32_t)t * 4u);
 }
 
 // Which 32-wide tiles of a dimension with NT32 tiles a wave owns (i <

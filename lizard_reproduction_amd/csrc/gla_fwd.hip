@@ -107,7 +107,7 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
   const bf16* fqb = fq + (size_t)bh * L * F;
   const bf16* fkb = fk + (size_t)bh * L * F;
   const bf16* vb = v + (size_t)bh * L * D;
-  bf16* yb = y + (size_t)bh * L * D;
+  const rsrc_t yr = make_rsrc(y + (size_t)bh * L * D, (size_t)L * D * 2);
   const float* lgb = log_gamma + (size_t)(gate_per_head ? bh : bh / H) * L;
   const float* st = G > 1 ? seg_state + ((size_t)bh * G + seg) * Cfg::SEG : nullptr;
 
@@ -216,13 +216,7 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
           for (int kb = 0; kb < 4; ++kb) o = mfma(vop[kb], pfrag[(qt * 4 + kb) * 64 + lane], o);
           const float den = rs[qi] + rs[64 + qi] + qz[qi] + qz[64 + qi] + qz[128 + qi] + qz[192 + qi];
           const float inv = 1.f / fmaxf(den, TINY);
-          const int tok = t0 + qi;
-          if (tok < L) {
-#pragma unroll
-            for (int g = 0; g < 4; ++g)
-              store4<bf16>(yb, tok, dt * 32 + 8 * g + 4 * h, D, o[4 * g] * inv,
-                           o[4 * g + 1] * inv, o[4 * g + 2] * inv, o[4 * g + 3] * inv);
-          }
+          store_acc_row_bf16(yr, t0 + qi, dt * 32, D, vecD, o, inv, h);
         }
 #pragma unroll
         for (int ft = 0; ft < NFT; ++ft) {

@@ -50,12 +50,7 @@ __device__ __forceinline__ int xcd_block(int i, int per) { return (i & 7) * per 
 template <int DP>
 __device__ __forceinline__ void swa_load(uint4 (&reg)[SwaCfg<DP>::NL], const bf16* __restrict__ base,
                                          int r0, int L, int d, bool vec) {
-  constexpr int K8 = DP / 8;
-#pragma unroll
-  for (int i = 0; i < SwaCfg<DP>::NL; ++i) {
-    const int idx = threadIdx.x + 256 * i;
-    reg[i] = gload8(base, r0 + idx / K8, (idx % K8) * 8, L, d, vec);
-  }
+  load_items<DP, 256, SwaCfg<DP>::NL, 256 * SwaCfg<DP>::NL>(reg, base, r0, L, d, vec);
 }
 
 template <int DP>
@@ -182,16 +177,11 @@ __global__ __launch_bounds__(256) void swa_fwd_kernel(
       __syncthreads();
     }
   }
-  if (qi < L) {
-    const float inv = 1.f / l_i;
+  // every lane stores (rows past L are dropped): the row store swaps across lane halves
+  const float inv = 1.f / l_i;
 #pragma unroll
-    for (int t = 0; t < DP / 32; ++t)
-#pragma unroll
-      for (int g = 0; g < 4; ++g)
-        store4<bf16>(y + base, qi, t * 32 + 8 * g + 4 * h, d, o[t][4 * g] * inv,
-                     o[t][4 * g + 1] * inv, o[t][4 * g + 2] * inv, o[t][4 * g + 3] * inv);
-    if (h == 0) lse[(size_t)bh * L + qi] = m_i + flog(l_i);
-  }
+  for (int t = 0; t < DP / 32; ++t) store_acc_row<bf16>(y + base, qi, t * 32, L, d, o[t], inv, h);
+  if (qi < L && h == 0) lse[(size_t)bh * L + qi] = m_i + flog(l_i);
 }
 
 // ----------------------------------------------------------------------------
@@ -287,16 +277,9 @@ __global__ __launch_bounds__(256) void swa_bwd_dq_kernel(
     }
     if (pass == 0) delta += xhalf(delta);
   }
-  if (qi < L) {
 #pragma unroll
-    for (int t = 0; t < DP / 32; ++t)
-#pragma unroll
-      for (int g = 0; g < 4; ++g)
-        store4<OutT>(dq + base, qi, t * 32 + 8 * g + 4 * h, d, dqa[t][4 * g] * scale,
-                     dqa[t][4 * g + 1] * scale, dqa[t][4 * g + 2] * scale,
-                     dqa[t][4 * g + 3] * scale);
-    if (h == 0) delta_out[(size_t)bh * L + qi] = delta;
-  }
+  for (int t = 0; t < DP / 32; ++t) store_acc_row<OutT>(dq + base, qi, t * 32, L, d, dqa[t], scale, h);
+  if (qi < L && h == 0) delta_out[(size_t)bh * L + qi] = delta;
   // dmeta partial of this block: -sum_i e^{meta_j - lse_i} delta_i
   for (int j = 0; j < n_meta; ++j) {
     float c = (qi < L && h == 0) ? fexp(meta[j] - lse_i) * delta : 0.f;
@@ -429,17 +412,10 @@ __global__ __launch_bounds__(256) void swa_bwd_dkv_kernel(
       __syncthreads();
     }
   }
-  if (ti < L) {
 #pragma unroll
-    for (int t = 0; t < DP / 32; ++t)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int c = t * 32 + 8 * g + 4 * h;
-        store4<OutT>(dk + base, ti, c, d, dka[t][4 * g] * scale, dka[t][4 * g + 1] * scale,
-                     dka[t][4 * g + 2] * scale, dka[t][4 * g + 3] * scale);
-        store4<OutT>(dv + base, ti, c, d, dva[t][4 * g], dva[t][4 * g + 1], dva[t][4 * g + 2],
-                     dva[t][4 * g + 3]);
-      }
+  for (int t = 0; t < DP / 32; ++t) {
+    store_acc_row<OutT>(dk + base, ti, t * 32, L, d, dka[t], scale, h);
+    store_acc_row<OutT>(dv + base, ti, t * 32, L, d, dva[t], 1.f, h);
   }
 }
 
