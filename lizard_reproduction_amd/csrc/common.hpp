@@ -28,6 +28,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int WAVE = 64;
 constexpr float TINY = 1.1754943508222875e-38f;   // FLT_MIN, the reference's clamp
@@ -268,7 +269,6 @@ __device__ __forceinline__ void store_acc_row_bf16(rsrc_t r, int row, int c0, in
   for (int j = 0; j < 2; ++j) {
     const int col = c0 + 16 * j + 8 * h;
     if (vec) {
-      typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
       const u32x4 v = {w[4 * j], w[4 * j + 1], w[4 * j + 2], w[4 * j + 3]};
       __builtin_amdgcn_raw_buffer_store_b128(
           v, r, (row >= 0 && col < ncols) ? (uint32_t)(row * ncols + col) * 2u : OOB, 0, AUX);

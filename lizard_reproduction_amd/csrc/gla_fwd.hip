@@ -318,9 +318,100 @@ __global__ __launch_bounds__(256) void gla_decode_kernel(
   }
 }
 
+// Vector form of the decode step, for F % 4 == 0 and D a power of two in
+// [4, 128] (so S rows and each (b, h) state are 16-byte aligned and the
+// quads of a row divide a wave).  512 threads per (b, h): thread t owns
+// column quad q = t % (D/4) of rows f = t / (D/4) + i * RG (RG = 512 / (D/4)),
+// IPT rows in all.  Every state load of a thread is issued before any use,
+// through a range-checked buffer (rows past F read zeros, their stores drop).
+// fq . S_new sums over a wave's lanes of the same quad by xor shuffles, then
+// over the 8 waves in LDS.
+template <int IPT>
+__global__ __launch_bounds__(512) void gla_decode_vec_kernel(
+    const bf16* __restrict__ fq, const bf16* __restrict__ fk, const bf16* __restrict__ v,
+    const float* __restrict__ log_gamma, float* __restrict__ state, bf16* __restrict__ y, int H,
+    int F, int D, int gate_per_head) {
+  __shared__ float fq_s[256], fk_s[256], red[8];
+  __shared__ f32x4 part[8 * 32];
+  const int bh = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int NQ = D >> 2, RG = 512 / NQ;
+  const int q = tid % NQ, r0 = tid / NQ;
+  float* Sb = state + (size_t)bh * ((size_t)F * D + F);
+  float* zb = Sb + (size_t)F * D;
+  const rsrc_t sr = make_rsrc(Sb, (size_t)F * D * 4);
+  auto soff = [&](int i) {
+    const int f = r0 + i * RG;
+    return f < F ? (uint32_t)(f * D + 4 * q) * 4u : OOB;
+  };
+  f32x4 s[IPT];
+#pragma unroll
+  for (int i = 0; i < IPT; ++i) s[i] = __builtin_bit_cast(f32x4, bload16(sr, soff(i)));
+  const float gam = fexp(log_gamma[gate_per_head ? bh : bh / H]);
+  for (int f = tid; f < F; f += 512) {
+    fq_s[f] = to_f32(fq[(size_t)bh * F + f]);
+    fk_s[f] = to_f32(fk[(size_t)bh * F + f]);
+  }
+  const bf16x4 v4 = *reinterpret_cast<const bf16x4*>(v + (size_t)bh * D + 4 * q);
+  __syncthreads();
+  float qz = 0.f;
+  for (int f = tid; f < F; f += 512) {
+    const float zn = gam * zb[f] + fk_s[f];
+    zb[f] = zn;
+    qz += fq_s[f] * zn;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) qz += __shfl_xor(qz, off);
+  if (lane == 0) red[wave] = qz;
+  f32x4 num = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < IPT; ++i) {
+    const int f = min(r0 + i * RG, F - 1);   // rows past F: zeros in, store dropped
+    const float a = fk_s[f], b = fq_s[f];
+    f32x4 sn;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sn[e] = gam * s[i][e] + a * to_f32(v4[e]);
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sn), sr, soff(i), 0, 0);
+    if (r0 + i * RG < F) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) num[e] += b * sn[e];
+    }
+  }
+  for (int off = NQ; off < 64; off <<= 1)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) num[e] += __shfl_xor(num[e], off);
+  if (lane < NQ) part[wave * 32 + lane] = num;
+  __syncthreads();
+  if (tid < NQ) {
+    f32x4 t = part[tid];
+#pragma unroll
+    for (int w = 1; w < 8; ++w)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) t[e] += part[w * 32 + tid][e];
+    float den = red[0];
+#pragma unroll
+    for (int w = 1; w < 8; ++w) den += red[w];
+    const float inv = 1.f / fmaxf(den, TINY);
+    const bf16x4 o = {to_bf16(t[0] * inv), to_bf16(t[1] * inv), to_bf16(t[2] * inv),
+                      to_bf16(t[3] * inv)};
+    *reinterpret_cast<bf16x4*>(y + (size_t)bh * D + 4 * tid) = o;
+  }
+}
+
 hipError_t launch_gla_decode(const void* fq, const void* fk, const void* v, const float* lg,
                              float* state, void* y, int B, int H, int F, int D,
                              int gate_per_head, hipStream_t st) {
+  if (F % 4 == 0 && D >= 4 && D <= 128 && (D & (D - 1)) == 0) {
+    const int rg = 512 / (D / 4), need = (F + rg - 1) / rg;   // rows per thread
+#define LZ_GLA_DECV(IPTV)                                                                     \
+    if (need <= IPTV) {                                                                       \
+      hipLaunchKernelGGL(gla_decode_vec_kernel<IPTV>, dim3(B * H), dim3(512), 0, st,          \
+                         (const bf16*)fq, (const bf16*)fk, (const bf16*)v, lg, state,         \
+                         (bf16*)y, H, F, D, gate_per_head);                                   \
+      return hipGetLastError();                                                               \
+    }
+    LZ_GLA_DECV(1) LZ_GLA_DECV(2) LZ_GLA_DECV(4) LZ_GLA_DECV(8)
+#undef LZ_GLA_DECV
+  }
   const int dp = D <= 32 ? 32 : (D <= 64 ? 64 : (D <= 128 ? 128 : 256));
 #define LZ_GLA_DEC(DPV)                                                                       \
   if (dp == DPV) {                                                                          \

@@ -37,14 +37,18 @@ def test_prefill_state_matches_recurrent_form(length, per_head, nf, nd):
     assert max(errs.values()) <= OUT_TOL, errs
 
 
-@pytest.mark.parametrize("prefix, steps, per_head", [(100, 40, False), (0, 30, True),
-                                                     (64, 65, False)])
-def test_decode_steps_continue_the_sequence(prefix, steps, per_head):
+@pytest.mark.parametrize("prefix, steps, per_head, nf, nd", [
+    (100, 40, False, 24, 20), (0, 30, True, 24, 20), (64, 65, False, 24, 20),
+    # vector decode kernel (F % 4 == 0, D a power of two): 1, 2, 4 and 8 rows per thread
+    (70, 20, True, 32, 32), (30, 12, False, 64, 128), (50, 10, True, 128, 64),
+    (20, 8, False, 256, 64), (9, 5, True, 128, 128), (5, 3, False, 8, 4),
+    (40, 6, False, 64, 64)])
+def test_decode_steps_continue_the_sequence(prefix, steps, per_head, nf, nd):
     """Prefill on the first tokens, then one decode step per token: every
     step's output is the whole sequence's output at that position, and the
     final state is the whole sequence's."""
     n = prefix + steps
-    fq, fk, v, z = gla_inputs(n, gates=(3,) if per_head else (), features=24, dim=20, seed=3)
+    fq, fk, v, z = gla_inputs(n, gates=(3,) if per_head else (), features=nf, dim=nd, seed=3)
     lg = torch.nn.functional.logsigmoid(z)
     b, h = fq.shape[:2]
     dev = [t.cuda() for t in (fq, fk, v, lg)]
@@ -52,15 +56,15 @@ def test_decode_steps_continue_the_sequence(prefix, steps, per_head):
         _, state = kernels.gla_prefill(*(t[..., :prefix, :] for t in dev[:3]),
                                        dev[3][..., :prefix])
     else:
-        state = kernels.new_state(b, h, 24, 20, "cuda")
+        state = kernels.new_state(b, h, nf, nd, "cuda")
     ys = [kernels.gla_decode_step(dev[0][:, :, i], dev[1][:, :, i], dev[2][:, :, i],
                                   dev[3][..., i], state) for i in range(prefix, n)]
     out, S, zs = oracle_state(fq, fk, v, lg)
-    S_k, z_k = kernels.split_state(state, 24, 20)
+    S_k, z_k = kernels.split_state(state, nf, nd)
     torch.cuda.synchronize()
     errs = {"y": max_rel(torch.stack(ys, dim=2), out[:, :, prefix:]),
             "S": max_rel(S_k, S), "z": max_rel(z_k, zs)}
-    print(f"[parity] decode prefix={prefix} steps={steps} per_head={per_head}: " +
+    print(f"[parity] decode prefix={prefix} steps={steps} per_head={per_head} F={nf} D={nd}: " +
           " ".join(f"{k}={v:.2e}" for k, v in errs.items()), flush=True)
     assert all(y.dtype == torch.bfloat16 for y in ys)
     assert max(errs.values()) <= OUT_TOL, errs
