@@ -169,7 +169,7 @@ __device__ __forceinline__ void store_rows_t(const uint4 (&in)[RowItems<KP>::N],
     *reinterpret_cast<uint4*>(tile + (r0 + R::RSTRIDE * i) * pitch + 8 * cg) = in[i];
 }
 
-template <int FP, int DP, typename OutT>
+template <int FP, int DP, typename OutT, bool VEC>
 __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
     const bf16* __restrict__ fq, const bf16* __restrict__ fk, const bf16* __restrict__ v,
     const float* __restrict__ log_gamma, const bf16* __restrict__ dy, OutT* __restrict__ dfq,
@@ -208,7 +208,7 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
   const int n0 = seg * cps, n1 = min((L + C - 1) / C, n0 + M * cps);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int col = lane & 31, h = lane >> 5;
-  const bool vecF = (F & 7) == 0, vecD = (D & 7) == 0;
+  const bool vecF = VEC || (F & 7) == 0, vecD = VEC || (D & 7) == 0;
   const size_t offF = (size_t)bh * L * F, offD = (size_t)bh * L * D, offL = (size_t)bh * L;
   const float* lgb = log_gamma + (size_t)(gate_per_head ? bh : bh / H) * L;
   const float* st = G > 1 ? seg_state + ((size_t)bh * G + seg) * Cfg::SEG : nullptr;
@@ -556,7 +556,7 @@ struct BwdS : BwdCommon<FP, DP> {
   static constexpr int BYTES = OFF_R + 16;
 };
 
-template <int FP, int DP>
+template <int FP, int DP, bool VEC>
 __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_bwd_state_kernel(
     const bf16* __restrict__ fq, const bf16* __restrict__ dy, const float* __restrict__ log_gamma,
     const float* __restrict__ den_in, const float* __restrict__ delta_in,
@@ -585,7 +585,7 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_bwd_state_kernel(
   const int n0 = seg * cps, n1 = min(NT, n0 + cps);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int col = lane & 31, h = lane >> 5;
-  const bool vecF = (F & 7) == 0, vecD = (D & 7) == 0;
+  const bool vecF = VEC || (F & 7) == 0, vecD = VEC || (D & 7) == 0;
   const size_t offF = (size_t)bh * L * F, offD = (size_t)bh * L * D, offL = (size_t)bh * L;
   const float* lgb = log_gamma + (size_t)(gate_per_head ? bh : bh / H) * L;
 
@@ -723,7 +723,7 @@ struct BwdB : BwdCommon<FP, DP> {
   static constexpr int LB = BYTES <= 80 * 1024 ? 2 : 1;
 };
 
-template <int FP, int DP, typename OutT>
+template <int FP, int DP, typename OutT, bool VEC>
 __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_kernel(
     const bf16* __restrict__ fq, const bf16* __restrict__ fk, const bf16* __restrict__ v,
     const float* __restrict__ log_gamma, const bf16* __restrict__ dy,
@@ -764,7 +764,7 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
   const int n0 = seg0 * cps, n1 = min(NT, n0 + M * cps);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int col = lane & 31, h = lane >> 5;
-  const bool vecF = (F & 7) == 0, vecD = (D & 7) == 0;
+  const bool vecF = VEC || (F & 7) == 0, vecD = VEC || (D & 7) == 0;
   const size_t offF = (size_t)bh * L * F, offD = (size_t)bh * L * D, offL = (size_t)bh * L;
   const float* lgb = log_gamma + (size_t)(gate_per_head ? bh : bh / H) * L;
   const float* st = G > 1 ? seg_state + ((size_t)bh * G + seg) * Cfg::SEG : nullptr;
@@ -1088,7 +1088,7 @@ size_t gla_bwd_workspace(int B, int H, int L, int F, int D, int gate_per_head) {
          sizeof(float);
 }
 
-template <int FP, int DP, typename OutT>
+template <int FP, int DP, typename OutT, bool VEC>
 static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v, const float* lg,
                                    const void* dy, void* dfq, void* dfk, void* dv, float* dlg,
                                    int B, int H, int L, int F, int D, int gate_per_head,
@@ -1118,15 +1118,15 @@ static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v
   // the walks take two segments per workgroup while that still gives 256
   // workgroups (one per CU): fewer, longer walks
   const int M = (G % 2 == 0 && BH * G / 2 >= 256) ? 2 : 1;
-  auto ka = gla_bwd_dq_kernel<FP, DP, OutT>;
-  if ((e = ensure_lds<gla_bwd_dq_kernel<FP, DP, OutT>>(LDS_A)) != hipSuccess) return e;
+  auto ka = gla_bwd_dq_kernel<FP, DP, OutT, VEC>;
+  if ((e = ensure_lds<gla_bwd_dq_kernel<FP, DP, OutT, VEC>>(LDS_A)) != hipSuccess) return e;
   hipLaunchKernelGGL(ka, dim3(BH * G / M), dim3(B_THREADS), LDS_A, st, (const bf16*)fq,
                      (const bf16*)fk, (const bf16*)v, lg, (const bf16*)dy, (OutT*)dfq, den, delta,
                      p, fseg, H, L, F, D, gate_per_head, G, cps, M);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   if (G > 1) {
-    auto ks = gla_bwd_state_kernel<FP, DP>;
-    if ((e = ensure_lds<gla_bwd_state_kernel<FP, DP>>(LDS_S)) != hipSuccess) return e;
+    auto ks = gla_bwd_state_kernel<FP, DP, VEC>;
+    if ((e = ensure_lds<gla_bwd_state_kernel<FP, DP, VEC>>(LDS_S)) != hipSuccess) return e;
     float* rlam = rseg + (size_t)BH * G * SEG;
     hipLaunchKernelGGL(ks, dim3(BH * (G - 1)), dim3(256), LDS_S, st,
                        (const bf16*)fq, (const bf16*)dy, lg, (const float*)den,
@@ -1134,8 +1134,8 @@ static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if ((e = launch_gla_segment_scan(rseg, rlam, BH, G, SEG, true, st)) != hipSuccess) return e;
   }
-  auto kb = gla_bwd_dkv_kernel<FP, DP, OutT>;
-  if ((e = ensure_lds<gla_bwd_dkv_kernel<FP, DP, OutT>>(LDS_B)) != hipSuccess) return e;
+  auto kb = gla_bwd_dkv_kernel<FP, DP, OutT, VEC>;
+  if ((e = ensure_lds<gla_bwd_dkv_kernel<FP, DP, OutT, VEC>>(LDS_B)) != hipSuccess) return e;
   hipLaunchKernelGGL(kb, dim3(BH * G / M), dim3(B_THREADS), LDS_B, st, (const bf16*)fq,
                      (const bf16*)fk, (const bf16*)v, lg, (const bf16*)dy, (const float*)den,
                      (const float*)delta, (const float*)p, (OutT*)dfk, (OutT*)dv, dG, csum,
@@ -1152,19 +1152,22 @@ hipError_t launch_gla_bwd(const void* fq, const void* fk, const void* v, const f
                           bool grad_bf16, int B, int H, int L, int F, int D, int gate_per_head,
                           const float* fwd_ws, float* ws, hipStream_t st) {
   const int fp = gla_padded_dim(F), dp = gla_padded_dim(D);
-#define LZ_GLA_BWD(FPV, DPV)                                                                   \
-  if (fp == FPV && dp == DPV)                                                                  \
-    return grad_bf16 ? launch_gla_bwd_t<FPV, DPV, bf16>(fq, fk, v, lg, dy, dfq, dfk, dv, dlg,  \
-                                                         B, H, L, F, D, gate_per_head, fwd_ws, \
-                                                         ws, st)                               \
-                     : launch_gla_bwd_t<FPV, DPV, float>(fq, fk, v, lg, dy, dfq, dfk, dv, dlg, \
-                                                          B, H, L, F, D, gate_per_head, fwd_ws, \
-                                                          ws, st);
+  const bool vec = F % 8 == 0 && D % 8 == 0;
+#define LZ_GLA_BWD_V(FPV, DPV, OUT, V)                                                          \
+  launch_gla_bwd_t<FPV, DPV, OUT, V>(fq, fk, v, lg, dy, dfq, dfk, dv, dlg, B, H, L, F, D,      \
+                                     gate_per_head, fwd_ws, ws, st)
+#define LZ_GLA_BWD(FPV, DPV)                                                                    \
+  if (fp == FPV && dp == DPV)                                                                   \
+    return grad_bf16 ? (vec ? LZ_GLA_BWD_V(FPV, DPV, bf16, true)                                \
+                            : LZ_GLA_BWD_V(FPV, DPV, bf16, false))                              \
+                     : (vec ? LZ_GLA_BWD_V(FPV, DPV, float, true)                               \
+                            : LZ_GLA_BWD_V(FPV, DPV, float, false));
   LZ_GLA_BWD(32, 32) LZ_GLA_BWD(32, 64) LZ_GLA_BWD(32, 128)
   LZ_GLA_BWD(64, 32) LZ_GLA_BWD(64, 64) LZ_GLA_BWD(64, 128)
   LZ_GLA_BWD(128, 32) LZ_GLA_BWD(128, 64) LZ_GLA_BWD(128, 128)
   LZ_GLA_BWD(256, 32) LZ_GLA_BWD(256, 64)
 #undef LZ_GLA_BWD
+#undef LZ_GLA_BWD_V
   return hipErrorInvalidValue;
 }
 

@@ -73,7 +73,7 @@ struct GlaFwd {
 // ----------------------------------------------------------------------------
 // fused forward walk over the chunks of one segment
 // ----------------------------------------------------------------------------
-template <int FP, int DP>
+template <int FP, int DP, bool VEC>
 __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
     const bf16* __restrict__ fq, const bf16* __restrict__ fk, const bf16* __restrict__ v,
     const float* __restrict__ log_gamma, bf16* __restrict__ y,
@@ -103,7 +103,7 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
   const int n0 = seg * cps, n1 = min(NT, n0 + cps);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int col = lane & 31, h = lane >> 5;
-  const bool vecF = (F & 7) == 0, vecD = (D & 7) == 0;
+  const bool vecF = VEC || (F & 7) == 0, vecD = VEC || (D & 7) == 0;
   const bf16* fqb = fq + (size_t)bh * L * F;
   const bf16* fkb = fk + (size_t)bh * L * F;
   const bf16* vb = v + (size_t)bh * L * D;
@@ -428,7 +428,7 @@ hipError_t launch_gla_decode(const void* fq, const void* fk, const void* v, cons
 // ----------------------------------------------------------------------------
 // segment pass: state left by each segment g < G-1 starting from zero
 // ----------------------------------------------------------------------------
-template <int FP, int DP>
+template <int FP, int DP, bool VEC>
 __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_state_kernel(
     const bf16* __restrict__ fk, const bf16* __restrict__ v, const float* __restrict__ log_gamma,
     float* __restrict__ seg_state, float* __restrict__ seg_logdecay, int H, int L, int F, int D,
@@ -452,7 +452,7 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_state_kernel(
   const int n0 = seg * cps, n1 = n0 + cps;   // segments before the last are full
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int col = lane & 31, h = lane >> 5;
-  const bool vecF = (F & 7) == 0, vecD = (D & 7) == 0;
+  const bool vecF = VEC || (F & 7) == 0, vecD = VEC || (D & 7) == 0;
   const bf16* fkb = fk + (size_t)bh * L * F;
   const bf16* vb = v + (size_t)bh * L * D;
   const float* lgb = log_gamma + (size_t)(gate_per_head ? bh : bh / H) * L;
@@ -627,14 +627,14 @@ hipError_t launch_gla_segment_scan(float* seg_state, const float* seg_logdecay, 
   return hipGetLastError();
 }
 
-template <int FP, int DP>
+template <int FP, int DP, bool VEC>
 static hipError_t launch_gla_fwd_states_t(const void* fk, const void* v, const float* lg,
                                           float* seg_state, float* seg_logdecay, int BH, int H,
                                           int L, int F, int D, int gate_per_head, int G, int cps,
                                           hipStream_t st) {
   using Cfg = GlaFwd<FP, DP>;
-  auto ks = gla_fwd_state_kernel<FP, DP>;
-  hipError_t e = ensure_lds<gla_fwd_state_kernel<FP, DP>>(Cfg::BYTES);
+  auto ks = gla_fwd_state_kernel<FP, DP, VEC>;
+  hipError_t e = ensure_lds<gla_fwd_state_kernel<FP, DP, VEC>>(Cfg::BYTES);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(ks, dim3(BH * (G - 1)), dim3(256), Cfg::BYTES, st, (const bf16*)fk,
                      (const bf16*)v, lg, seg_state, seg_logdecay, H, L, F, D, gate_per_head, G, cps);
@@ -646,10 +646,15 @@ hipError_t launch_gla_fwd_states(const void* fk, const void* v, const float* lg,
                                  float* seg_logdecay, int BH, int H, int L, int F, int D,
                                  int gate_per_head, int G, int cps, hipStream_t st) {
   const int fp = gla_padded_dim(F), dp = gla_padded_dim(D);
+  const bool vec = F % 8 == 0 && D % 8 == 0;
 #define LZ_GLA_ST(FPV, DPV)                                                                   \
   if (fp == FPV && dp == DPV)                                                                 \
-    return launch_gla_fwd_states_t<FPV, DPV>(fk, v, lg, seg_state, seg_logdecay, BH, H, L, F, \
-                                             D, gate_per_head, G, cps, st);
+    return vec ? launch_gla_fwd_states_t<FPV, DPV, true>(fk, v, lg, seg_state, seg_logdecay,  \
+                                                         BH, H, L, F, D, gate_per_head, G,    \
+                                                         cps, st)                             \
+               : launch_gla_fwd_states_t<FPV, DPV, false>(fk, v, lg, seg_state, seg_logdecay, \
+                                                          BH, H, L, F, D, gate_per_head, G,   \
+                                                          cps, st);
   LZ_GLA_ST(32, 32) LZ_GLA_ST(32, 64) LZ_GLA_ST(32, 128)
   LZ_GLA_ST(64, 32) LZ_GLA_ST(64, 64) LZ_GLA_ST(64, 128)
   LZ_GLA_ST(128, 32) LZ_GLA_ST(128, 64) LZ_GLA_ST(128, 128)
@@ -658,7 +663,7 @@ hipError_t launch_gla_fwd_states(const void* fk, const void* v, const float* lg,
   return hipErrorInvalidValue;
 }
 
-template <int FP, int DP>
+template <int FP, int DP, bool VEC>
 static hipError_t launch_gla_fwd_t(const void* fq, const void* fk, const void* v,
                                    const float* lg, void* y, int B, int H, int L, int F, int D,
                                    int gate_per_head, float* ws, float* final_state,
@@ -669,13 +674,13 @@ static hipError_t launch_gla_fwd_t(const void* fq, const void* fk, const void* v
   gla_segments(BH, L, F, &G, &cps);
   float* seg_state = ws;
   if (G > 1) {
-    hipError_t e = launch_gla_fwd_states_t<FP, DP>(fk, v, lg, seg_state,
+    hipError_t e = launch_gla_fwd_states_t<FP, DP, VEC>(fk, v, lg, seg_state,
                                                    ws + (size_t)BH * G * Cfg::SEG, BH, H, L, F,
                                                    D, gate_per_head, G, cps, st);
     if (e != hipSuccess) return e;
   }
-  auto kern = gla_fwd_kernel<FP, DP>;
-  hipError_t e = ensure_lds<gla_fwd_kernel<FP, DP>>(Cfg::BYTES);
+  auto kern = gla_fwd_kernel<FP, DP, VEC>;
+  hipError_t e = ensure_lds<gla_fwd_kernel<FP, DP, VEC>>(Cfg::BYTES);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3(BH * G), dim3(256), Cfg::BYTES, st, (const bf16*)fq,
                      (const bf16*)fk, (const bf16*)v, lg, (bf16*)y, (const float*)seg_state,
@@ -687,10 +692,13 @@ hipError_t launch_gla_fwd(const void* fq, const void* fk, const void* v, const f
                           int B, int H, int L, int F, int D, int gate_per_head, float* ws,
                           float* final_state, hipStream_t st) {
   const int fp = gla_padded_dim(F), dp = gla_padded_dim(D);
-#define LZ_GLA_FWD(FPV, DPV) \
-  if (fp == FPV && dp == DPV) \
-    return launch_gla_fwd_t<FPV, DPV>(fq, fk, v, lg, y, B, H, L, F, D, gate_per_head, ws,   \
-                                      final_state, st);
+  const bool vec = F % 8 == 0 && D % 8 == 0;
+#define LZ_GLA_FWD(FPV, DPV)                                                                    \
+  if (fp == FPV && dp == DPV)                                                                   \
+    return vec ? launch_gla_fwd_t<FPV, DPV, true>(fq, fk, v, lg, y, B, H, L, F, D,              \
+                                                  gate_per_head, ws, final_state, st)           \
+               : launch_gla_fwd_t<FPV, DPV, false>(fq, fk, v, lg, y, B, H, L, F, D,             \
+                                                   gate_per_head, ws, final_state, st);
   LZ_GLA_FWD(32, 32) LZ_GLA_FWD(32, 64) LZ_GLA_FWD(32, 128)
   LZ_GLA_FWD(64, 32) LZ_GLA_FWD(64, 64) LZ_GLA_FWD(64, 128)
   LZ_GLA_FWD(128, 32) LZ_GLA_FWD(128, 64) LZ_GLA_FWD(128, 128)

@@ -85,7 +85,7 @@ __device__ __forceinline__ bool blocks_meet(int q0, int k0, int L, int W) {
 // ----------------------------------------------------------------------------
 // forward
 // ----------------------------------------------------------------------------
-template <int DP>
+template <int DP, bool VEC>
 __global__ __launch_bounds__(256) void swa_fwd_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ meta, int n_meta, bf16* __restrict__ y, float* __restrict__ lse,
@@ -104,7 +104,7 @@ __global__ __launch_bounds__(256) void swa_fwd_kernel(
   const int col = lane & 31, h = lane >> 5;
   const int q0 = Q0 + wave * 32, qi = q0 + col;
   const size_t base = (size_t)bh * L * d;
-  const bool vec = (d & 7) == 0;
+  const bool vec = VEC || (d & 7) == 0;
 
   bf16x8 qreg[DP / 16];
   own_rows<DP>(q + base, qi, L, d, h, vec, qreg);
@@ -188,7 +188,7 @@ __global__ __launch_bounds__(256) void swa_fwd_kernel(
 // backward, query side: delta (first pass over the window keys), dq (second
 // pass), and this block's partial of dmeta
 // ----------------------------------------------------------------------------
-template <int DP, typename OutT>
+template <int DP, typename OutT, bool VEC>
 __global__ __launch_bounds__(256) void swa_bwd_dq_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ meta, int n_meta, const float* __restrict__ lse,
@@ -209,7 +209,7 @@ __global__ __launch_bounds__(256) void swa_bwd_dq_kernel(
   const int col = lane & 31, h = lane >> 5;
   const int q0 = Q0 + wave * 32, qi = q0 + col;
   const size_t base = (size_t)bh * L * d;
-  const bool vec = (d & 7) == 0;
+  const bool vec = VEC || (d & 7) == 0;
 
   bf16x8 qreg[DP / 16], dyreg[DP / 16];
   own_rows<DP>(q + base, qi, L, d, h, vec, qreg);
@@ -299,7 +299,7 @@ __global__ __launch_bounds__(256) void swa_bwd_dq_kernel(
 // ----------------------------------------------------------------------------
 // backward, key side: dk and dv over the queries whose windows hold the keys
 // ----------------------------------------------------------------------------
-template <int DP, typename OutT>
+template <int DP, typename OutT, bool VEC>
 __global__ __launch_bounds__(256) void swa_bwd_dkv_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ lse, const float* __restrict__ delta_in,
@@ -341,7 +341,7 @@ __global__ __launch_bounds__(256) void swa_bwd_dkv_kernel(
   const int col = lane & 31, h = lane >> 5;
   const int k0 = K0 + wave * 32, ti = k0 + col;
   const size_t base = (size_t)bh * L * d, lbase = (size_t)bh * L;
-  const bool vec = (d & 7) == 0;
+  const bool vec = VEC || (d & 7) == 0;
 
   bf16x8 kreg[DP / 16], vreg[DP / 16];
   own_rows<DP>(k + base, ti, L, d, h, vec, kreg);
@@ -440,13 +440,13 @@ static void swa_grid(int BH, int L, int* per, int* grid) {
 
 int swa_row_blocks(int L) { return (L + SWA_ROWS - 1) / SWA_ROWS; }
 
-template <int DP>
+template <int DP, bool VEC>
 static hipError_t launch_swa_fwd_t(const void* q, const void* k, const void* v, const float* meta,
                                    int n_meta, void* y, float* lse, int BH, int L, int d, int W,
                                    float scale, hipStream_t st) {
   const size_t lds = 2 * SwaCfg<DP>::TILE_BYTES;
-  auto kern = swa_fwd_kernel<DP>;
-  hipError_t e = ensure_lds<swa_fwd_kernel<DP>>((int)lds);
+  auto kern = swa_fwd_kernel<DP, VEC>;
+  hipError_t e = ensure_lds<swa_fwd_kernel<DP, VEC>>((int)lds);
   if (e != hipSuccess) return e;
   int per, grid;
   swa_grid(BH, L, &per, &grid);
@@ -455,7 +455,7 @@ static hipError_t launch_swa_fwd_t(const void* q, const void* k, const void* v, 
   return hipGetLastError();
 }
 
-template <int DP, typename OutT>
+template <int DP, typename OutT, bool VEC>
 static hipError_t launch_swa_bwd_t(const void* q, const void* k, const void* v, const float* meta,
                                    int n_meta, const float* lse, const void* dy, void* dq,
                                    void* dk, void* dv, float* delta, float* dmeta_part,
@@ -464,16 +464,16 @@ static hipError_t launch_swa_bwd_t(const void* q, const void* k, const void* v, 
   int per, grid;
   swa_grid(BH, L, &per, &grid);
   const size_t lds_q = 2 * SwaCfg<DP>::TILE_BYTES + 4 * SWA_MAX_META * sizeof(float);
-  auto kq = swa_bwd_dq_kernel<DP, OutT>;
-  hipError_t e = ensure_lds<swa_bwd_dq_kernel<DP, OutT>>((int)lds_q);
+  auto kq = swa_bwd_dq_kernel<DP, OutT, VEC>;
+  hipError_t e = ensure_lds<swa_bwd_dq_kernel<DP, OutT, VEC>>((int)lds_q);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kq, dim3(grid), dim3(256), lds_q, st, (const bf16*)q, (const bf16*)k,
                      (const bf16*)v, meta, n_meta, lse, (const bf16*)dy, (OutT*)dq, delta,
                      dmeta_part, BH, L, d, W, scale, per);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   const size_t lds_k = 2 * SwaCfg<DP>::TILE_BYTES + 2 * SWA_TILE * sizeof(float);
-  auto kk = swa_bwd_dkv_kernel<DP, OutT>;
-  if ((e = ensure_lds<swa_bwd_dkv_kernel<DP, OutT>>((int)lds_k)) != hipSuccess) return e;
+  auto kk = swa_bwd_dkv_kernel<DP, OutT, VEC>;
+  if ((e = ensure_lds<swa_bwd_dkv_kernel<DP, OutT, VEC>>((int)lds_k)) != hipSuccess) return e;
   hipLaunchKernelGGL(kk, dim3(grid), dim3(256), lds_k, st, (const bf16*)q, (const bf16*)k,
                      (const bf16*)v, lse, (const float*)delta, (const bf16*)dy, (OutT*)dk,
                      (OutT*)dv, (const float*)dmeta_part, dmeta, n_meta, BH, L, d, W, scale, per);
@@ -483,13 +483,20 @@ static hipError_t launch_swa_bwd_t(const void* q, const void* k, const void* v, 
 hipError_t launch_swa_fwd(const void* q, const void* k, const void* v, const float* meta,
                           int n_meta, void* y, float* lse, int BH, int L, int d, int W,
                           float scale, hipStream_t st) {
+  const bool vec = d % 8 == 0;
+#define LZ_SWA_FWD(DPV)                                                                         \
+  return vec ? launch_swa_fwd_t<DPV, true>(q, k, v, meta, n_meta, y, lse, BH, L, d, W, scale,   \
+                                           st)                                                  \
+             : launch_swa_fwd_t<DPV, false>(q, k, v, meta, n_meta, y, lse, BH, L, d, W, scale,  \
+                                            st)
   switch (swa_padded_dim(d)) {
-    case 32: return launch_swa_fwd_t<32>(q, k, v, meta, n_meta, y, lse, BH, L, d, W, scale, st);
-    case 64: return launch_swa_fwd_t<64>(q, k, v, meta, n_meta, y, lse, BH, L, d, W, scale, st);
-    case 128: return launch_swa_fwd_t<128>(q, k, v, meta, n_meta, y, lse, BH, L, d, W, scale, st);
-    case 256: return launch_swa_fwd_t<256>(q, k, v, meta, n_meta, y, lse, BH, L, d, W, scale, st);
+    case 32: LZ_SWA_FWD(32);
+    case 64: LZ_SWA_FWD(64);
+    case 128: LZ_SWA_FWD(128);
+    case 256: LZ_SWA_FWD(256);
     default: return hipErrorInvalidValue;
   }
+#undef LZ_SWA_FWD
 }
 
 hipError_t launch_swa_bwd(const void* q, const void* k, const void* v, const float* meta,
@@ -497,13 +504,13 @@ hipError_t launch_swa_bwd(const void* q, const void* k, const void* v, const flo
                           void* dv, bool grad_bf16, float* delta, float* dmeta_part,
                           float* dmeta, int BH, int L, int d, int W, float scale,
                           hipStream_t st) {
+  const bool vec = d % 8 == 0;
+#define LZ_SWA_BWD_V(DPV, OUT, V)                                                               \
+  launch_swa_bwd_t<DPV, OUT, V>(q, k, v, meta, n_meta, lse, dy, dq, dk, dv, delta, dmeta_part, \
+                                dmeta, BH, L, d, W, scale, st)
 #define LZ_SWA_BWD(DPV)                                                                         \
-  return grad_bf16 ? launch_swa_bwd_t<DPV, bf16>(q, k, v, meta, n_meta, lse, dy, dq, dk, dv,    \
-                                                 delta, dmeta_part, dmeta, BH, L, d, W, scale,  \
-                                                 st)                                            \
-                   : launch_swa_bwd_t<DPV, float>(q, k, v, meta, n_meta, lse, dy, dq, dk, dv,   \
-                                                  delta, dmeta_part, dmeta, BH, L, d, W, scale, \
-                                                  st)
+  return grad_bf16 ? (vec ? LZ_SWA_BWD_V(DPV, bf16, true) : LZ_SWA_BWD_V(DPV, bf16, false))     \
+                   : (vec ? LZ_SWA_BWD_V(DPV, float, true) : LZ_SWA_BWD_V(DPV, float, false))
   switch (swa_padded_dim(d)) {
     case 32: LZ_SWA_BWD(32);
     case 64: LZ_SWA_BWD(64);
@@ -512,6 +519,7 @@ hipError_t launch_swa_bwd(const void* q, const void* k, const void* v, const flo
     default: return hipErrorInvalidValue;
   }
 #undef LZ_SWA_BWD
+#undef LZ_SWA_BWD_V
 }
 
 }  // namespace lz
