@@ -285,15 +285,17 @@ __device__ __forceinline__ void store_acc_row_bf16(rsrc_t r, int row, int c0, in
 }
 
 // The same row of a [nrows x ncols] OutT matrix at base: bf16 through
-// store_acc_row_bf16; fp32 as four 16-byte stores per lane (already whole
-// 16-byte pieces).  Every lane of the wave must take part (the bf16 form
-// swaps registers between lane halves); rows at or past nrows are skipped.
+// store_acc_row_bf16 (vec: ncols % 8 == 0); fp32 as four 16-byte stores per
+// lane (already whole 16-byte pieces).  Every lane of the wave must take part
+// (the bf16 form swaps registers between lane halves); rows at or past nrows
+// are skipped.
 template <typename OutT>
 __device__ __forceinline__ void store_acc_row(OutT* __restrict__ base, int row, int c0, int nrows,
-                                              int ncols, const f32x16& g, float scale, int h) {
+                                              int ncols, bool vec, const f32x16& g, float scale,
+                                              int h) {
   if constexpr (sizeof(OutT) == 2) {
-    store_acc_row_bf16(make_rsrc(base, (size_t)nrows * ncols * 2), row, c0, ncols,
-                       (ncols & 7) == 0, g, scale, h);
+    store_acc_row_bf16(make_rsrc(base, (size_t)nrows * ncols * 2), row, c0, ncols, vec, g, scale,
+                       h);
   } else {
     if (row < nrows) {
 #pragma unroll

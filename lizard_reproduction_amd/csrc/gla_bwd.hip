@@ -445,7 +445,7 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
         }
         ps += xhalf(ps);
         if (h == 0) pp[ft * 64 + q] = tok < L ? ps : 0.f;
-        store_acc_row<OutT>(dfq + offF, tok, ft * 32, L, F, g, 1.f, h);
+        store_acc_row<OutT>(dfq + offF, tok, ft * 32, L, F, vecF, g, 1.f, h);
       }
     }
     // S^T <- r S^T + V^T K~ for the owned tiles
@@ -933,7 +933,7 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
 #pragma unroll
         for (int qb = 0; qb < 4; ++qb)
           g = mfma(tr_operand(dy_l, PD, 16 * qb, dt * 32, lane), fa[(hk * 4 + qb) * 64 + lane], g);
-        store_acc_row<OutT>(dv + offD, t0 + key, dt * 32, L, D, g, 1.f, h);
+        store_acc_row<OutT>(dv + offD, t0 + key, dt * 32, L, D, vecD, g, 1.f, h);
       }
     }
     // dS <- r_n dS + fq^T dY^ for the owned tiles
@@ -982,7 +982,7 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
         }
         pks += xhalf(pks);
         if (h == 0) pk[ft * 64 + key] = pks;
-        store_acc_row<OutT>(dfk + offF, tok, ft * 32, L, F, g, 1.f, h);
+        store_acc_row<OutT>(dfk + offF, tok, ft * 32, L, F, vecF, g, 1.f, h);
       }
     }
     __syncthreads();

@@ -180,7 +180,7 @@ __global__ __launch_bounds__(256) void swa_fwd_kernel(
   // every lane stores (rows past L are dropped): the row store swaps across lane halves
   const float inv = 1.f / l_i;
 #pragma unroll
-  for (int t = 0; t < DP / 32; ++t) store_acc_row<bf16>(y + base, qi, t * 32, L, d, o[t], inv, h);
+  for (int t = 0; t < DP / 32; ++t) store_acc_row<bf16>(y + base, qi, t * 32, L, d, vec, o[t], inv, h);
   if (qi < L && h == 0) lse[(size_t)bh * L + qi] = m_i + flog(l_i);
 }
 
@@ -278,7 +278,7 @@ __global__ __launch_bounds__(256) void swa_bwd_dq_kernel(
     if (pass == 0) delta += xhalf(delta);
   }
 #pragma unroll
-  for (int t = 0; t < DP / 32; ++t) store_acc_row<OutT>(dq + base, qi, t * 32, L, d, dqa[t], scale, h);
+  for (int t = 0; t < DP / 32; ++t) store_acc_row<OutT>(dq + base, qi, t * 32, L, d, vec, dqa[t], scale, h);
   if (qi < L && h == 0) delta_out[(size_t)bh * L + qi] = delta;
   // dmeta partial of this block: -sum_i e^{meta_j - lse_i} delta_i
   for (int j = 0; j < n_meta; ++j) {
@@ -414,8 +414,8 @@ __global__ __launch_bounds__(256) void swa_bwd_dkv_kernel(
   }
 #pragma unroll
   for (int t = 0; t < DP / 32; ++t) {
-    store_acc_row<OutT>(dk + base, ti, t * 32, L, d, dka[t], scale, h);
-    store_acc_row<OutT>(dv + base, ti, t * 32, L, d, dva[t], 1.f, h);
+    store_acc_row<OutT>(dk + base, ti, t * 32, L, d, vec, dka[t], scale, h);
+    store_acc_row<OutT>(dv + base, ti, t * 32, L, d, vec, dva[t], 1.f, h);
   }
 }
 
