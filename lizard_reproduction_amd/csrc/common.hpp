@@ -128,12 +128,17 @@ hipError_t ensure_lds(int bytes) {
   return status;
 }
 
-// Row pitch (elements) of a row-major bf16 LDS tile with x columns.  Rows are
-// read as 16-byte MFMA operands (8 lanes per LDS cycle) and, by the transpose
-// reads, as 4 rows x 32 bytes per 16-lane group; a pitch of 36 or 72 dwords
-// (mod 64 banks) keeps both conflict-free.  x + 8 gives 36 for x = 64,
-// x + 16 gives 72 for x = 128 (8 for x = 256, 24 for x = 32).
-__host__ __device__ constexpr int lds_pitch(int x) { return x + (x == 64 ? 8 : 16); }
+// Row pitch (elements) of a row-major bf16 LDS tile with x columns.  Measured
+// bank-conflict cycles per instruction on gfx950 (64 banks; rocprofv3
+// SQ_LDS_BANK_CONFLICT over a probe of each access pattern):
+//   pitch (dwords mod 64)   16-byte rows   transpose reads   8-byte rows (acc order)
+//   8  (x=128: 144)         3.9            2.0               23.5
+//   12 (x=128: 152)         0              2.0               7.8
+//   36 (x=64: 72)           0              2.0               7.8
+// So x + 24 for x >= 128 (12 mod 64, 280 for x = 256 likewise), x + 8 for 64.
+__host__ __device__ constexpr int lds_pitch(int x) {
+  return x + (x == 64 ? 8 : (x >= 128 ? 24 : 16));
+}
 
 // Exchange with the other half of the wave (lane ^ 32).
 __device__ __forceinline__ float xhalf(float x) { return __shfl_xor(x, 32); }

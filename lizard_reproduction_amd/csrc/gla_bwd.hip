@@ -554,6 +554,7 @@ struct BwdS : BwdCommon<FP, DP> {
   static constexpr int OFF_DZP = OFF_DZ + FP * 4;
   static constexpr int OFF_R = OFF_DZP + ZPARTS * FP * 4;
   static constexpr int BYTES = OFF_R + 16;
+  static_assert(BYTES <= 160 * 1024, "LDS budget");
 };
 
 template <int FP, int DP, bool VEC>
@@ -690,7 +691,8 @@ template <int FP, int DP>
 struct BwdB : BwdCommon<FP, DP> {
   using B_ = BwdCommon<FP, DP>;
   static constexpr int C = B_::C, PF = B_::PF, PD = B_::PD, NFT = B_::NFT, NDT = B_::NDT;
-  static constexpr int ZP = 8;                                // dz partial sums per feature
+  // dz partial sums per feature (4 at FP = 256, where the chunk's LDS is tightest)
+  static constexpr int ZP = FP >= 256 ? 4 : 8;
   static constexpr int S_OWN = (NFT * NDT + B_WAVES - 1) / B_WAVES;   // dS tiles per wave
   static constexpr int DV_JOBS = 2 * NDT, DFK_JOBS = 2 * NFT;
   static constexpr int DV_OWN = (DV_JOBS + B_WAVES - 1) / B_WAVES;
@@ -721,6 +723,7 @@ struct BwdB : BwdCommon<FP, DP> {
   static constexpr int OFF_R = OFF_DZP + ZP * FP * 4;
   static constexpr int BYTES = OFF_R + 16;
   static constexpr int LB = BYTES <= 80 * 1024 ? 2 : 1;
+  static_assert(BYTES <= 160 * 1024, "LDS budget");
 };
 
 template <int FP, int DP, typename OutT, bool VEC>

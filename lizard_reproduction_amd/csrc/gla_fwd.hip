@@ -68,6 +68,8 @@ struct GlaFwd {
   static constexpr int OFF_R = OFF_ZP + 2048 * 4;         // e^{lg_end}, lg_end
   static constexpr int BYTES = OFF_R + 16;
   static constexpr int SEG = SegRec<FP, DP>::SIZE;
+  // two workgroups per CU up to F = 128 (the launch bounds ask for it), one beyond
+  static_assert(BYTES <= (FP >= 256 ? 160 : 80) * 1024, "LDS budget");
 };
 
 // ----------------------------------------------------------------------------
