@@ -30,7 +30,9 @@ namespace lz {
 constexpr int PRO_WAVES = 4;
 constexpr int PRO_ROWS = 32;                      // rows per wave and block
 constexpr int PRO_BLOCK = PRO_WAVES * PRO_ROWS;   // rows per workgroup iteration
-constexpr int PRO_WG_PER_ROLE = 256;              // backward workgroups per role (q, kv)
+constexpr int PRO_FWD_WG_PER_ROLE = 1024;         // forward workgroups per role (q, kv)
+constexpr int PRO_CUS = 256;                      // MI355X compute units
+constexpr int PRO_BWD_WG_PER_CU = 2;              // the most any backward instantiation asks for
 constexpr int CMB_BLOCKS = 1024;                  // epilogue backward partial sums
 
 __device__ __forceinline__ void wave_sync() {
@@ -114,11 +116,7 @@ struct Pro {
   static constexpr int W_ELEMS = FP * WP;
   static constexpr int SP = lds_pitch(FP);      // forward staging [32][SP] per wave
   static constexpr int FWD_LDS = (PARTS * W_ELEMS + PRO_WAVES * PRO_ROWS * SP) * 2;
-  static constexpr int DP = lds_pitch(FP);      // backward dxw tile [128][DP]
-  static constexpr int QP = lds_pitch(HP);      // backward x tile [128][QP] (per part)
-  static constexpr int BWD_LDS =
-      (PARTS * W_ELEMS + PRO_BLOCK * DP + PARTS * PRO_BLOCK * QP) * 2;
-  static_assert(BWD_LDS <= 160 * 1024 && FWD_LDS <= 160 * 1024, "LDS budget");
+  static_assert(FWD_LDS <= 160 * 1024, "LDS budget");
 };
 
 struct ProFwdArgs {
@@ -132,7 +130,8 @@ struct ProBwdArgs {
   const bf16 *dfq, *dfk, *dqr, *dkr, *dv, *dv2;   // dv2 may be null
   void *dq, *dk, *dvo;
   float* part;
-  int B, L, H, Hkv, hd, f, cos_bstride, nq_wg;
+  int B, L, H, Hkv, hd, f, cos_bstride;
+  int nbq, nbk;   // 128-row blocks of the q rows and of the kv rows
 };
 
 // W [f][hd] (type T) into LDS as bf16 hi (and lo) tiles [FP][WP], zero rows
@@ -369,186 +368,365 @@ __global__ __launch_bounds__(256) void prologue_fwd_kernel(ProFwdArgs a) {
 
 // ---------------------------------------------------------------------------
 // backward
+//
+// A workgroup takes blocks of 128 rows (a wave owns 32 of them, one per
+// lane column of its MFMA tiles).  Per block:
+//   1. x rows -> LDS (bf16 hi, and lo for fp32 inputs), coalesced; each lane
+//      reads its row's MFMA operands back;
+//   2. softmax statistics of both feature maps in one pass over the feature
+//      tiles (per-tile maxima, running rescaled sums);
+//   3. per feature tile ft: the gradient rows' 32 dp and 32 dn values of
+//      that tile, summed over the group's heads in fp32, are gathered by the
+//      whole workgroup with 16-byte loads into an fp32 LDS stage, and each
+//      lane forms A = p dp - n dn and the sums <p, dp>, <n, dn> from it;
+//   4. dxw = A + n <n,dn> - p <p,dp> per tile: dx_phi^T += W^T dxw^T (MFMA,
+//      hi and lo parts of dxw), dxw hi -> the dW tile in LDS;
+//   5. dW += dxw^T x over the block (hi, then lo), through LDS transpose reads;
+//   6. dx_phi -> LDS, and dx = dx_phi + rope^T(drope) (plus the summed dv for
+//      the kv rows) in a coalesced row layout, 8 columns per item.
+// The stage, the dW tile and the dx tile share one LDS buffer.
 // ---------------------------------------------------------------------------
+constexpr int imax(int a, int b) { return a > b ? a : b; }
+
 template <typename T, int FT, int HT>
-__global__ __launch_bounds__(256) void prologue_bwd_kernel(ProBwdArgs a) {
+struct ProBwd {
   using C = Pro<T, FT, HT>;
+  static constexpr int FP = C::FP, HP = C::HP, HK = C::HK, WP = C::WP, PARTS = C::PARTS;
+  static constexpr int QP = lds_pitch(HP);    // x tiles [128][QP] bf16
+  static constexpr int DP = lds_pitch(FP);    // dW tile [128][DP] bf16
+  static constexpr int SP = 64 + 4;           // stage [128][SP] fp32: 32 dp, then 32 dn
+  static constexpr int AP = HP + 4;           // dx tile [128][AP] fp32
+  static constexpr int BUF = imax(PRO_BLOCK * SP * 4, PRO_BLOCK * DP * 2);
+  static constexpr int OFF_X = PARTS * FP * WP * 2;
+  static constexpr int OFF_B = OFF_X + PARTS * PRO_BLOCK * QP * 2;
+  // the dx tile shares the buffer when it fits there, else it also spans the
+  // x tiles (then the next block waits for the epilogue before writing x)
+  static constexpr bool DX_OVER_X = PRO_BLOCK * AP * 4 > BUF;
+  static constexpr int OFF_DX = DX_OVER_X ? OFF_X : OFF_B;
+  static constexpr int LDS = imax(OFF_B + BUF, OFF_DX + PRO_BLOCK * AP * 4);
+  // workgroups per CU: two where the LDS and the registers (<= 256) allow it
+  static constexpr int OCC = LDS <= 80 * 1024 && FT <= 2 && HT <= 2 ? 2 : 1;
+  static constexpr int GI = PRO_BLOCK * 8 / 256;          // stage items per thread
+  // heads whose gradient loads are issued a tile ahead (none where two
+  // workgroups share a CU: their registers have no room for them)
+  static constexpr int GQ = OCC == 2 ? 0 : 4;
+  static constexpr int GQR = GQ > 0 ? GQ : 1;             // raw register sets held
+  static constexpr int XI = PRO_BLOCK * (HP / 8) / 256;   // x / dx items per thread
+  static_assert(LDS <= 160 * 1024, "LDS budget");
+};
+
+// 8 bf16 at p (16-byte aligned) added to acc in fp32; nothing when !ok (the
+// load then reads `safe`, a valid address, and its value is dropped, so the
+// loads of a loop stay branch-free and in flight together).
+__device__ __forceinline__ void add8(const bf16* p, const bf16* safe, bool ok, float (&acc)[8]) {
+  const bf16x8 v = *reinterpret_cast<const bf16x8*>(ok ? p : safe);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] += ok ? to_f32(v[e]) : 0.f;
+}
+
+// The same for two 4-element halves (8-byte aligned) with their own flags.
+__device__ __forceinline__ void add4x2(const bf16* p, const bf16* safe, bool ok0, bool ok1,
+                                       float (&acc)[8]) {
+  const bf16x4 v0 = *reinterpret_cast<const bf16x4*>(ok0 ? p : safe);
+  const bf16x4 v1 = *reinterpret_cast<const bf16x4*>(ok1 ? p + 4 : safe);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    acc[e] += ok0 ? to_f32(v0[e]) : 0.f;
+    acc[4 + e] += ok1 ? to_f32(v1[e]) : 0.f;
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void store8v(T* __restrict__ p, const float (&x)[8]) {
+  if constexpr (sizeof(T) == 2) {
+    bf16x8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = to_bf16(x[e]);
+    *reinterpret_cast<bf16x8*>(p) = o;
+  } else {
+    *reinterpret_cast<f32x4*>(p) = f32x4{x[0], x[1], x[2], x[3]};
+    *reinterpret_cast<f32x4*>(p + 4) = f32x4{x[4], x[5], x[6], x[7]};
+  }
+}
+
+// PART: f < 32 FT, so the last feature tile is partly padding and its
+// features past f are masked out (the instantiation without it carries no
+// masks at all).
+template <typename T, int FT, int HT, bool PART>
+__global__ __launch_bounds__(256, (ProBwd<T, FT, HT>::OCC)) void prologue_bwd_kernel(ProBwdArgs a) {
+  using K = ProBwd<T, FT, HT>;
+  constexpr int FP = K::FP, HP = K::HP, HK = K::HK, SP = K::SP, AP = K::AP;
+  constexpr bool SPLIT = Pro<T, FT, HT>::SPLIT;
   constexpr int TILES = FT * HT;
   constexpr int OWN = (TILES + PRO_WAVES - 1) / PRO_WAVES;   // dW tiles per wave
+  constexpr int H8 = HP / 8;                                 // 8-column items per hd row
   extern __shared__ __attribute__((aligned(16))) char smem[];
   bf16* w_hi = reinterpret_cast<bf16*>(smem);
-  bf16* w_lo = w_hi + C::W_ELEMS;
-  bf16* d_l = w_hi + C::PARTS * C::W_ELEMS;          // dxw tile [128][DP]
-  bf16* x_hi = d_l + PRO_BLOCK * C::DP;              // x tile [128][QP]
-  bf16* x_lo = x_hi + PRO_BLOCK * C::QP;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5;
+  bf16* w_lo = w_hi + FP * K::WP;
+  bf16* x_hi = reinterpret_cast<bf16*>(smem + K::OFF_X);
+  bf16* x_lo = x_hi + PRO_BLOCK * K::QP;
+  float* stage = reinterpret_cast<float*>(smem + K::OFF_B);
+  bf16* d_l = reinterpret_cast<bf16*>(smem + K::OFF_B);
+  float* dx_l = reinterpret_cast<float*>(smem + K::OFF_DX);
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, h = lane >> 5;
   const int lrow = wave * PRO_ROWS + (lane & 31);    // this lane's row in the LDS tiles
 
-  const bool kv = (int)blockIdx.x >= a.nq_wg;
-  const int wg = kv ? blockIdx.x - a.nq_wg : blockIdx.x;
-  const int nwg = kv ? gridDim.x - a.nq_wg : a.nq_wg;
-  const int heads_in = kv ? a.Hkv : a.H;
-  const int group = kv ? a.H / a.Hkv : 1;
-  const int nrows = a.B * a.L * heads_in;
-  const T* x = static_cast<const T*>(kv ? a.k : a.q);
-  const bf16* dphi = kv ? a.dfk : a.dfq;
-  const bf16* drope = kv ? a.dkr : a.dqr;
-  T* dx = static_cast<T*>(kv ? a.dk : a.dq);
   const T* cs = static_cast<const T*>(a.cos);
   const T* sn = static_cast<const T*>(a.sin);
-  const int f = a.f, hd = C::HP, half_hd = C::HP / 2, F2 = 2 * a.f;
+  const int f = a.f, hd = HP, half_hd = HP / 2, F2 = 2 * a.f;
+  const bool vec = (f & 7) == 0;   // gradient items are whole 16-byte pieces
 
-  load_weight<T, FT, HT>(static_cast<const T*>(kv ? a.wk : a.wq), f, w_hi, w_lo);
+  // stage items of this thread: rows (tid >> 3) + 32 i of a block, and the
+  // 8 features 8 (k & 3) .. +8 of tile ft of the dp (k < 4) or dn half
+  const int k8 = tid & 7, shalf = k8 >> 2, scol = 8 * (k8 & 3);
 
+  // this workgroup's partial dW [FP][HP] of role r: lane = column, registers = rows
+  auto flush = [&](const f32x16 (&acc)[OWN], int r, bool zero) {
+    float* part = a.part + ((size_t)r * gridDim.x + blockIdx.x) * FP * HP;
+#pragma unroll
+    for (int i = 0; i < OWN; ++i) {
+      const int t = wave + PRO_WAVES * i;
+      if (t < TILES) {
+        const int ft = t / HT, ht = t % HT;
+#pragma unroll
+        for (int r2 = 0; r2 < 16; ++r2)
+          part[(32 * ft + acc_row(r2, h)) * HP + 32 * ht + (lane & 31)] = zero ? 0.f : acc[i][r2];
+      }
+    }
+  };
+
+  // One grid over the q blocks, then the kv blocks: workgroup w takes blocks
+  // w, w + G, ... of that list, so it switches role at most once and every
+  // workgroup gets its share of both (kv blocks carry the group's gradients).
+  bool kv = false;
+  int role = -1, heads_in = 0, group = 1, nrows = 0;
+  const T* x = nullptr;
+  const bf16 *dphi = nullptr, *drope = nullptr;
+  T* dx = nullptr;
   f32x16 dw[OWN];
 #pragma unroll
   for (int i = 0; i < OWN; ++i) dw[i] = zero16();
 
-  for (int blk = wg; blk * PRO_BLOCK < nrows; blk += nwg) {
-    const int row = blk * PRO_BLOCK + lrow;
-    const bool live = row < nrows;
-    const RowPos pos = decode(live ? row : 0, a.L, heads_in);
-    // [B, H, L, .] row of this row's first head; the group's heads are L rows apart
-    const long obase = ((long)pos.b * a.H + pos.head * group) * a.L + pos.l;
-
-    bf16x8 xh[C::HK], xl[C::HK];
+  const int nb = a.nbq + a.nbk;
+  for (int j = blockIdx.x; j < nb; j += gridDim.x) {
+    const int r_j = j < a.nbq ? 0 : 1;
+    if (r_j != role) {   // uniform; the W tile's readers passed the last block's barriers
+      if (role == 0) {
+        flush(dw, 0, false);
 #pragma unroll
-    for (int kb = 0; kb < C::HK; ++kb) {
+        for (int i = 0; i < OWN; ++i) dw[i] = zero16();
+      } else {
+        flush(dw, 0, true);   // no q blocks here: a zero q partial
+      }
+      role = r_j;
+      kv = role == 1;
+      heads_in = kv ? a.Hkv : a.H;
+      group = kv ? a.H / a.Hkv : 1;
+      nrows = a.B * a.L * heads_in;
+      x = static_cast<const T*>(kv ? a.k : a.q);
+      dphi = kv ? a.dfk : a.dfq;
+      drope = kv ? a.dkr : a.dqr;
+      dx = static_cast<T*>(kv ? a.dk : a.dq);
+      load_weight<T, FT, HT>(static_cast<const T*>(kv ? a.wk : a.wq), f, w_hi, w_lo);
+    }
+    const int row0 = (kv ? j - a.nbq : j) * PRO_BLOCK;
+    // ---- 1. x rows -> LDS; this lane's operands ------------------------------
+#pragma unroll
+    for (int i = 0; i < K::XI; ++i) {
+      const int idx = tid + 256 * i, r = idx / H8, m0 = 8 * (idx % H8);
       float xf[8];
-      if (live) {
-        load8f(x + (long)row * hd + 16 * kb + 8 * h, xf);
+      if (row0 + r < nrows) {
+        load8f(x + (long)(row0 + r) * hd + m0, xf);
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e) xf[e] = 0.f;
       }
-      xh[kb] = to_bf8(xf);
-      *reinterpret_cast<bf16x8*>(x_hi + lrow * C::QP + 16 * kb + 8 * h) = xh[kb];
-      if constexpr (C::SPLIT) {
-        xl[kb] = low8(xf, xh[kb]);
-        *reinterpret_cast<bf16x8*>(x_lo + lrow * C::QP + 16 * kb + 8 * h) = xl[kb];
+      const bf16x8 hi = to_bf8(xf);
+      *reinterpret_cast<bf16x8*>(x_hi + r * K::QP + m0) = hi;
+      if constexpr (SPLIT) *reinterpret_cast<bf16x8*>(x_lo + r * K::QP + m0) = low8(xf, hi);
+    }
+    __syncthreads();   // x tiles (and, on the first block, W)
+    bf16x8 xh[HK], xl[HK];
+#pragma unroll
+    for (int kb = 0; kb < HK; ++kb) {
+      xh[kb] = row_operand(x_hi, K::QP, lrow, 16 * kb, h);
+      if constexpr (SPLIT) xl[kb] = row_operand(x_lo, K::QP, lrow, 16 * kb, h);
+    }
+
+    // rows of this thread's stage items: [B, H, L, 2f] element offset of
+    // their first head's gradient row (-1: row past the end)
+    long gbase[K::GI];
+#pragma unroll
+    for (int i = 0; i < K::GI; ++i) {
+      const int row = row0 + (tid >> 3) + 32 * i;
+      if (row < nrows) {
+        const RowPos pos = decode(row, a.L, heads_in);
+        gbase[i] = (((long)pos.b * a.H + pos.head * group) * a.L + pos.l) * F2 + shalf * f;
+      } else {
+        gbase[i] = -1;
       }
     }
-    __syncthreads();   // W tiles (first pass) and nothing else pending
-    float mp, mn, ip, in;
-    softmax_stats<T, FT, HT>(xh, xl, w_hi, w_lo, f, lane, mp, mn, ip, in);
+    // Gradient items of tile ft: the loads of the first GQ heads are issued a
+    // tile ahead (raw, 16 bytes each) and summed when the tile is staged;
+    // heads past GQ are loaded and added then.
+    auto item_ok = [&](int i, int c) { return gbase[i] >= 0 && c < f; };
+    auto issue = [&](int ft, uint4 (&raw)[K::GQR][K::GI]) {
+      const int c = 32 * ft + scol;
+#pragma unroll
+      for (int g = 0; g < K::GQ; ++g)
+#pragma unroll
+        for (int i = 0; i < K::GI; ++i)
+          if (g < group) {   // uniform
+            const bf16* p = dphi + (gbase[i] + (long)g * a.L * F2 + c);
+            if (vec) {
+              raw[g][i] = *reinterpret_cast<const uint4*>(item_ok(i, c) ? p : dphi);
+            } else {
+              const uint2 lo = *reinterpret_cast<const uint2*>(item_ok(i, c) ? p : dphi);
+              const uint2 hi = *reinterpret_cast<const uint2*>(item_ok(i, c + 4) ? p + 4 : dphi);
+              raw[g][i] = uint4{lo.x, lo.y, hi.x, hi.y};
+            }
+          }
+    };
+    auto gather = [&](int ft, const uint4 (&raw)[K::GQR][K::GI], float (&g8)[K::GI][8]) {
+      const int c = 32 * ft + scol;
+#pragma unroll
+      for (int i = 0; i < K::GI; ++i) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) g8[i][e] = 0.f;
+        const bool ok0 = item_ok(i, c), ok1 = item_ok(i, c + 4);
+#pragma unroll
+        for (int g = 0; g < K::GQ; ++g)
+          if (g < group) {
+            const bf16x8 v = __builtin_bit_cast(bf16x8, raw[g][i]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) g8[i][e] += (e < 4 ? ok0 : ok1) ? to_f32(v[e]) : 0.f;
+          }
+        for (int g = K::GQ; g < group; ++g) {
+          const bf16* p = dphi + (gbase[i] + (long)g * a.L * F2 + c);
+          if (vec)
+            add8(p, dphi, ok0, g8[i]);
+          else
+            add4x2(p, dphi, ok0, ok1, g8[i]);
+        }
+      }
+    };
+    uint4 raw[K::GQR][K::GI];
+    if constexpr (K::GQ > 0) issue(0, raw);
 
-    // u = p dp - n dn per feature; s_p = <p, dp>, s_n = <n, dn>
-    f32x16 dxw[FT];
+    // ---- 2. softmax statistics: maxima and sums in one pass -----------------
+    float mp = -1e30f, mn = -1e30f, sp = 0.f, sn_ = 0.f;
+#pragma unroll
+    for (int ft = 0; ft < FT; ++ft) {
+      const f32x16 acc = project_tile<T, FT, HT>(ft, xh, xl, w_hi, w_lo, lane);
+      // features past f (padding of the last tile) drop out through
+      // selects, not branches: their exponentials are of -inf
+      float tp = -1e30f, tn = -1e30f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const bool ok = !PART || 32 * ft + acc_row(r, h) < f;
+        tp = fmaxf(tp, ok ? acc[r] : -1e30f);
+        tn = fmaxf(tn, ok ? -acc[r] : -1e30f);
+      }
+      const float np = fmaxf(mp, tp), nn = fmaxf(mn, tn);
+      float ap = 0.f, an = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const bool ok = !PART || 32 * ft + acc_row(r, h) < f;
+        ap += fexp(ok ? acc[r] - np : NEG_INF);
+        an += fexp(ok ? -acc[r] - nn : NEG_INF);
+      }
+      sp = sp * fexp(mp - np) + ap;
+      sn_ = sn_ * fexp(mn - nn) + an;
+      mp = np;
+      mn = nn;
+    }
+    {   // the other lane half holds the row's other features
+      const float mpo = xhalf(mp), spo = xhalf(sp), mno = xhalf(mn), sno = xhalf(sn_);
+      const float mp2 = fmaxf(mp, mpo), mn2 = fmaxf(mn, mno);
+      sp = sp * fexp(mp - mp2) + spo * fexp(mpo - mp2);
+      sn_ = sn_ * fexp(mn - mn2) + sno * fexp(mno - mn2);
+      mp = mp2;
+      mn = mn2;
+    }
+    const float ip = 1.f / sp, in = 1.f / sn_;
+
+    // ---- 3. A = p dp - n dn per feature tile, <p, dp>, <n, dn> ---------------
+    f32x16 A[FT];
     float s_p = 0.f, s_n = 0.f;
 #pragma unroll
     for (int ft = 0; ft < FT; ++ft) {
-      f32x4 dp[4], dn[4];
+      float g8[K::GI][8];
+      gather(ft, raw, g8);
+      if (K::GQ > 0 && ft + 1 < FT) issue(ft + 1, raw);   // in flight while this tile computes
+      __syncthreads();   // the previous tile's (or block's) readers of the buffer are done
 #pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const int c = 32 * ft + 8 * q4 + 4 * h;
-        dp[q4] = f32x4{0.f, 0.f, 0.f, 0.f};
-        dn[q4] = dp[q4];
-        if (live && c < f) {
-          for (int g = 0; g < group; ++g) {
-            const bf16* src = dphi + (obase + (long)g * a.L) * F2;
-            dp[q4] += load4f(src + c);
-            dn[q4] += load4f(src + f + c);
-          }
-        }
+      for (int i = 0; i < K::GI; ++i) {
+        float* dst = stage + ((tid >> 3) + 32 * i) * SP + 32 * shalf + scol;
+        *reinterpret_cast<f32x4*>(dst) = f32x4{g8[i][0], g8[i][1], g8[i][2], g8[i][3]};
+        *reinterpret_cast<f32x4*>(dst + 4) = f32x4{g8[i][4], g8[i][5], g8[i][6], g8[i][7]};
       }
+      __syncthreads();
       const f32x16 acc = project_tile<T, FT, HT>(ft, xh, xl, w_hi, w_lo, lane);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float u = 0.f;
-        if (32 * ft + acc_row(r, h) < f) {
-          const float p = fexp(acc[r] - mp) * ip;
-          const float n = fexp(-acc[r] - mn) * in;
-          const float pd = p * dp[r >> 2][r & 3], nd = n * dn[r >> 2][r & 3];
-          u = pd - nd;
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const f32x4 dp = *reinterpret_cast<const f32x4*>(stage + lrow * SP + 8 * q4 + 4 * h);
+        const f32x4 dn = *reinterpret_cast<const f32x4*>(stage + lrow * SP + 32 + 8 * q4 + 4 * h);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * q4 + e;
+          const float pd = fexp(acc[r] - mp) * ip * dp[e];
+          const float nd = fexp(-acc[r] - mn) * in * dn[e];
+          A[ft][r] = pd - nd;
           s_p += pd;
           s_n += nd;
         }
-        dxw[ft][r] = u;
       }
     }
     s_p += xhalf(s_p);
     s_n += xhalf(s_n);
+
+    // ---- 4. dxw; dx_phi^T = W^T dxw^T; dxw hi -> the dW tile ----------------
+    __syncthreads();   // every lane is done with the stage
+    f32x16 dacc[HT];
+#pragma unroll
+    for (int ht = 0; ht < HT; ++ht) dacc[ht] = zero16();
+    bf16x4 dlo[FT][4];
 #pragma unroll
     for (int ft = 0; ft < FT; ++ft) {
       const f32x16 acc = project_tile<T, FT, HT>(ft, xh, xl, w_hi, w_lo, lane);
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        if (32 * ft + acc_row(r, h) < f) {
-          const float p = fexp(acc[r] - mp) * ip;
-          const float n = fexp(-acc[r] - mn) * in;
-          dxw[ft][r] += n * s_n - p * s_p;
-        }
-    }
-
-    // dx_phi^T = W^T dxw^T: hd rows (registers), this wave's rows (lanes)
-    f32x16 dacc[HT];
+      for (int r = 0; r < 16; ++r) {
+        const float p = fexp(acc[r] - mp) * ip;
+        const float n = fexp(-acc[r] - mn) * in;
+        A[ft][r] = !PART || 32 * ft + acc_row(r, h) < f ? A[ft][r] + n * s_n - p * s_p : 0.f;
+      }
 #pragma unroll
-    for (int ht = 0; ht < HT; ++ht) {
-      dacc[ht] = zero16();
+      for (int kb = 0; kb < 2; ++kb) {
+        const bf16x8 dh = acc_operand(A[ft], kb), dl = acc_operand_lo(A[ft], kb);
 #pragma unroll
-      for (int ft = 0; ft < FT; ++ft)
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-          const bf16x8 w = tr_operand(w_hi, C::WP, 32 * ft + 16 * kb, 32 * ht, lane);
-          const bf16x8 dh = acc_operand(dxw[ft], kb);
+        for (int ht = 0; ht < HT; ++ht) {
+          const bf16x8 w = tr_operand(w_hi, K::WP, 32 * ft + 16 * kb, 32 * ht, lane);
           dacc[ht] = mfma(w, dh, dacc[ht]);
-          dacc[ht] = mfma(w, acc_operand_lo(dxw[ft], kb), dacc[ht]);
-          if constexpr (C::SPLIT)
-            dacc[ht] = mfma(tr_operand(w_lo, C::WP, 32 * ft + 16 * kb, 32 * ht, lane), dh,
+          dacc[ht] = mfma(w, dl, dacc[ht]);
+          if constexpr (SPLIT)
+            dacc[ht] = mfma(tr_operand(w_lo, K::WP, 32 * ft + 16 * kb, 32 * ht, lane), dh,
                             dacc[ht]);
         }
-    }
-
-    // dxw hi into the LDS tile now, lo kept as bf16 until the tile is free:
-    // the fp32 dxw dies here
-    bf16x4 dlo[FT][4];
-#pragma unroll
-    for (int ft = 0; ft < FT; ++ft)
+      }
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
         bf16x4 o;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float v = dxw[ft][4 * q4 + e];
+          const float v = A[ft][4 * q4 + e];
           o[e] = to_bf16(v);
           dlo[ft][q4][e] = to_bf16(v - to_f32(o[e]));
         }
-        *reinterpret_cast<bf16x4*>(d_l + lrow * C::DP + 32 * ft + 8 * q4 + 4 * h) = o;
+        *reinterpret_cast<bf16x4*>(d_l + lrow * K::DP + 32 * ft + 8 * q4 + 4 * h) = o;
       }
-
-    // dx = dx_phi + rope^T(drope): dx[m] = dr[m] cos[m] + dr[m + hd/2] sin[m + hd/2]
-    // for m < hd/2, dr[m] cos[m] - dr[m - hd/2] sin[m - hd/2] otherwise
-    // (drope summed over the group's heads); the kv rows also sum dv.
-    if (live) {
-      const long tab = ((long)pos.b * a.cos_bstride + pos.l) * hd;
-#pragma unroll
-      for (int ht = 0; ht < HT; ++ht)
-#pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-          const int m = 32 * ht + 8 * q4 + 4 * h;
-          const int mp2 = m < half_hd ? m + half_hd : m - half_hd;
-          const float sign = m < half_hd ? 1.f : -1.f;
-          f32x4 dr = {0.f, 0.f, 0.f, 0.f}, dr2 = dr, dvs = dr;
-          for (int g = 0; g < group; ++g) {
-            const long o = (obase + (long)g * a.L) * hd;
-            dr += load4f(drope + o + m);
-            dr2 += load4f(drope + o + mp2);
-            if (kv) {
-              dvs += load4f(a.dv + o + m);
-              if (a.dv2) dvs += load4f(a.dv2 + o + m);
-            }
-          }
-          const f32x4 c = load4f(cs + tab + m), s2 = load4f(sn + tab + mp2);
-          f32x4 out;
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            out[e] = dacc[ht][4 * q4 + e] + dr[e] * c[e] + sign * dr2[e] * s2[e];
-          store4v(dx + (long)row * hd + m, out);
-          if (kv) store4v(static_cast<T*>(a.dvo) + (long)row * hd + m, dvs);
-        }
     }
 
-    // dW += dxw^T x over the workgroup's 128 rows: dxw hi, then lo, through LDS
+    // ---- 5. dW += dxw^T x over the block: dxw hi, then lo --------------------
 #pragma unroll
     for (int part = 0; part < 2; ++part) {
       if (part == 1) {
@@ -556,7 +734,7 @@ __global__ __launch_bounds__(256) void prologue_bwd_kernel(ProBwdArgs a) {
         for (int ft = 0; ft < FT; ++ft)
 #pragma unroll
           for (int q4 = 0; q4 < 4; ++q4)
-            *reinterpret_cast<bf16x4*>(d_l + lrow * C::DP + 32 * ft + 8 * q4 + 4 * h) =
+            *reinterpret_cast<bf16x4*>(d_l + lrow * K::DP + 32 * ft + 8 * q4 + 4 * h) =
                 dlo[ft][q4];
       }
       __syncthreads();
@@ -565,31 +743,68 @@ __global__ __launch_bounds__(256) void prologue_bwd_kernel(ProBwdArgs a) {
         const int t = wave + PRO_WAVES * i;
         if (t < TILES) {
           const int ft = t / HT, ht = t % HT;
-#pragma unroll
+#pragma unroll 2
           for (int ks = 0; ks < PRO_BLOCK / 16; ++ks) {
-            const bf16x8 d = tr_operand(d_l, C::DP, 16 * ks, 32 * ft, lane);
-            dw[i] = mfma(d, tr_operand(x_hi, C::QP, 16 * ks, 32 * ht, lane), dw[i]);
-            if (C::SPLIT && part == 0)
-              dw[i] = mfma(d, tr_operand(x_lo, C::QP, 16 * ks, 32 * ht, lane), dw[i]);
+            const bf16x8 d = tr_operand(d_l, K::DP, 16 * ks, 32 * ft, lane);
+            dw[i] = mfma(d, tr_operand(x_hi, K::QP, 16 * ks, 32 * ht, lane), dw[i]);
+            if (SPLIT && part == 0)
+              dw[i] = mfma(d, tr_operand(x_lo, K::QP, 16 * ks, 32 * ht, lane), dw[i]);
           }
         }
       }
       __syncthreads();
     }
-  }
 
-  // this workgroup's partial dW [FP][HP]: lane = column, registers = rows
-  float* part = a.part + (size_t)blockIdx.x * C::FP * C::HP;
+    // ---- 6. dx = dx_phi + rope^T(drope) (+ dv sums), coalesced ---------------
 #pragma unroll
-  for (int i = 0; i < OWN; ++i) {
-    const int t = wave + PRO_WAVES * i;
-    if (t < TILES) {
-      const int ft = t / HT, ht = t % HT;
+    for (int ht = 0; ht < HT; ++ht)
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        part[(32 * ft + acc_row(r, h)) * C::HP + 32 * ht + (lane & 31)] = dw[i][r];
+      for (int q4 = 0; q4 < 4; ++q4)
+        *reinterpret_cast<f32x4*>(dx_l + lrow * AP + 32 * ht + 8 * q4 + 4 * h) =
+            f32x4{dacc[ht][4 * q4], dacc[ht][4 * q4 + 1], dacc[ht][4 * q4 + 2],
+                  dacc[ht][4 * q4 + 3]};
+    __syncthreads();
+    // dx[m] = dr[m] cos[m] + dr[m + hd/2] sin[m + hd/2] for m < hd/2,
+    //         dr[m] cos[m] - dr[m - hd/2] sin[m - hd/2] otherwise (drope summed
+    // over the group's heads); the kv rows also sum dv (and dv2) over the group.
+#pragma unroll 1
+    for (int i = 0; i < K::XI; ++i) {
+      const int idx = tid + 256 * i, r = idx / H8, m0 = 8 * (idx % H8);
+      const int row = row0 + r;
+      if (row >= nrows) continue;
+      const RowPos pos = decode(row, a.L, heads_in);
+      const long obase = ((long)pos.b * a.H + pos.head * group) * a.L + pos.l;
+      const int mp2 = m0 < half_hd ? m0 + half_hd : m0 - half_hd;
+      const float sign = m0 < half_hd ? 1.f : -1.f;
+      float dr[8], dr2[8], dvs[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dr[e] = dr2[e] = dvs[e] = 0.f;
+#pragma unroll 4
+      for (int g = 0; g < group; ++g) {
+        const long o = (obase + (long)g * a.L) * hd;
+        add8(drope + o + m0, drope, true, dr);
+        add8(drope + o + mp2, drope, true, dr2);
+        if (kv) {
+          add8(a.dv + o + m0, a.dv, true, dvs);
+          if (a.dv2) add8(a.dv2 + o + m0, a.dv2, true, dvs);
+        }
+      }
+      const long tab = ((long)pos.b * a.cos_bstride + pos.l) * hd;
+      float c[8], s2[8], out[8];
+      load8f(cs + tab + m0, c);
+      load8f(sn + tab + mp2, s2);
+      const float* dxr = dx_l + r * AP + m0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) out[e] = dxr[e] + dr[e] * c[e] + sign * dr2[e] * s2[e];
+      store8v(dx + (long)row * hd + m0, out);
+      if (kv) store8v(static_cast<T*>(a.dvo) + (long)row * hd + m0, dvs);
     }
+    if constexpr (K::DX_OVER_X) __syncthreads();
   }
+  // the role in hand (its partial), and zeros for a role never taken
+  if (role == 0) flush(dw, 0, false);
+  if (role < 0) flush(dw, 0, true);
+  flush(dw, 1, role != 1);
 }
 
 // dW[i][c] = sum over a role's workgroups of their partials.  A block takes 64
@@ -732,16 +947,23 @@ bool prologue_dims_supported(int hd, int f) {
 
 static int feature_tiles(int f) { return f <= 32 ? 1 : (f <= 64 ? 2 : 4); }
 
-void prologue_grid(int B, int L, int H, int Hkv, int* nq, int* nk) {
-  const long rq = (long)B * L * H, rk = (long)B * L * Hkv;
-  *nq = (int)std::min<long>(ceil_div(rq, PRO_BLOCK), PRO_WG_PER_ROLE);
-  *nk = (int)std::min<long>(ceil_div(rk, PRO_BLOCK), PRO_WG_PER_ROLE);
+// Backward: 128-row blocks of each role, and the grid (at most
+// PRO_BWD_WG_PER_CU workgroups per CU on PRO_CUS CUs, no more than blocks).
+static void prologue_bwd_blocks(int B, int L, int H, int Hkv, int* nbq, int* nbk) {
+  *nbq = (int)ceil_div((long)B * L * H, PRO_BLOCK);
+  *nbk = (int)ceil_div((long)B * L * Hkv, PRO_BLOCK);
+}
+
+static int prologue_bwd_grid(int nbq, int nbk, int occ) {
+  return (int)std::min<long>((long)nbq + nbk, (long)PRO_CUS * occ);
 }
 
 size_t prologue_bwd_workspace(int B, int L, int H, int Hkv, int hd, int f) {
-  int nq, nk;
-  prologue_grid(B, L, H, Hkv, &nq, &nk);
-  return (size_t)(nq + nk) * (32 * feature_tiles(f)) * hd * sizeof(float);
+  int nbq, nbk;
+  prologue_bwd_blocks(B, L, H, Hkv, &nbq, &nbk);
+  // a q and a kv partial per workgroup, for the largest grid any instantiation uses
+  return (size_t)2 * prologue_bwd_grid(nbq, nbk, PRO_BWD_WG_PER_CU) *
+         (32 * feature_tiles(f)) * hd * sizeof(float);
 }
 
 template <typename T, int FT, int HT>
@@ -755,17 +977,27 @@ static hipError_t launch_fwd_t(const ProFwdArgs& a, int nq, int nk, hipStream_t 
 }
 
 template <typename T, int FT, int HT>
-static hipError_t launch_bwd_t(const ProBwdArgs& a, float* dwq, float* dwk, int nq, int nk,
-                               hipStream_t st) {
-  using C = Pro<T, FT, HT>;
-  hipError_t e = ensure_lds<prologue_bwd_kernel<T, FT, HT>>(C::BWD_LDS);
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((prologue_bwd_kernel<T, FT, HT>), dim3(nq + nk), dim3(256), C::BWD_LDS, st,
-                     a);
+static hipError_t launch_bwd_t(const ProBwdArgs& a, float* dwq, float* dwk, hipStream_t st) {
+  using C = ProBwd<T, FT, HT>;
+  static_assert(C::OCC <= PRO_BWD_WG_PER_CU, "workspace sized for fewer workgroups");
+  const int grid = prologue_bwd_grid(a.nbq, a.nbk, C::OCC);
+  hipError_t e;
+  if (a.f == C::FP) {
+    e = ensure_lds<prologue_bwd_kernel<T, FT, HT, false>>(C::LDS);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((prologue_bwd_kernel<T, FT, HT, false>), dim3(grid), dim3(256), C::LDS, st,
+                       a);
+  } else {
+    e = ensure_lds<prologue_bwd_kernel<T, FT, HT, true>>(C::LDS);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((prologue_bwd_kernel<T, FT, HT, true>), dim3(grid), dim3(256), C::LDS, st,
+                       a);
+  }
   e = hipGetLastError();
   if (e != hipSuccess) return e;
+  // partials: [q: grid][kv: grid] workgroups
   hipLaunchKernelGGL(prologue_dw_reduce_kernel, dim3((unsigned)ceil_div((long)a.f * a.hd, 64), 2),
-                     dim3(256), 0, st, a.part, dwq, dwk, nq, nk, C::FP, C::HP, a.f, a.hd);
+                     dim3(256), 0, st, a.part, dwq, dwk, grid, grid, C::FP, C::HP, a.f, a.hd);
   return hipGetLastError();
 }
 
@@ -790,9 +1022,8 @@ struct FwdLaunch {
 
 template <typename T, int FT, int HT>
 struct BwdLaunch {
-  static hipError_t run(const ProBwdArgs& a, float* dwq, float* dwk, int nq, int nk,
-                        hipStream_t st) {
-    return launch_bwd_t<T, FT, HT>(a, dwq, dwk, nq, nk, st);
+  static hipError_t run(const ProBwdArgs& a, float* dwq, float* dwk, hipStream_t st) {
+    return launch_bwd_t<T, FT, HT>(a, dwq, dwk, st);
   }
 };
 
@@ -800,11 +1031,9 @@ hipError_t launch_prologue_fwd(const void* q, const void* k, const void* v, cons
                                const void* wk, const void* cos, const void* sin, void* fq,
                                void* fk, void* qr, void* kr, void* vo, bool bf16_in, int B, int L,
                                int H, int Hkv, int hd, int f, int cos_bstride, hipStream_t st) {
-  int nq, nk;
-  prologue_grid(B, L, H, Hkv, &nq, &nk);
-  // the forward needs no partials: one workgroup per 128-row block, up to 4x the backward's
-  nq = (int)std::min<long>(ceil_div((long)B * L * H, PRO_BLOCK), 4 * PRO_WG_PER_ROLE);
-  nk = (int)std::min<long>(ceil_div((long)B * L * Hkv, PRO_BLOCK), 4 * PRO_WG_PER_ROLE);
+  // one workgroup per 128-row block, up to PRO_FWD_WG_PER_ROLE per role (grid-stride beyond)
+  const int nq = (int)std::min<long>(ceil_div((long)B * L * H, PRO_BLOCK), PRO_FWD_WG_PER_ROLE);
+  const int nk = (int)std::min<long>(ceil_div((long)B * L * Hkv, PRO_BLOCK), PRO_FWD_WG_PER_ROLE);
   ProFwdArgs a{q, k, v, wq, wk, cos, sin,
                static_cast<bf16*>(fq), static_cast<bf16*>(fk), static_cast<bf16*>(qr),
                static_cast<bf16*>(kr), static_cast<bf16*>(vo),
@@ -819,15 +1048,15 @@ hipError_t launch_prologue_bwd(const void* q, const void* k, const void* wq, con
                                const void* dv, const void* dv2, void* dq, void* dk, void* dvo,
                                float* dwq, float* dwk, bool bf16_in, int B, int L, int H, int Hkv,
                                int hd, int f, int cos_bstride, float* ws, hipStream_t st) {
-  int nq, nk;
-  prologue_grid(B, L, H, Hkv, &nq, &nk);
+  int nbq, nbk;
+  prologue_bwd_blocks(B, L, H, Hkv, &nbq, &nbk);
   ProBwdArgs a{q, k, wq, wk, cos, sin, static_cast<const bf16*>(dfq),
                static_cast<const bf16*>(dfk), static_cast<const bf16*>(dqr),
                static_cast<const bf16*>(dkr), static_cast<const bf16*>(dv),
                static_cast<const bf16*>(dv2), dq, dk, dvo, ws,
-               B, L, H, Hkv, hd, f, cos_bstride, nq};
-  return bf16_in ? dispatch_shape<bf16, BwdLaunch>(hd, f, a, dwq, dwk, nq, nk, st)
-                 : dispatch_shape<float, BwdLaunch>(hd, f, a, dwq, dwk, nq, nk, st);
+               B, L, H, Hkv, hd, f, cos_bstride, nbq, nbk};
+  return bf16_in ? dispatch_shape<bf16, BwdLaunch>(hd, f, a, dwq, dwk, st)
+                 : dispatch_shape<float, BwdLaunch>(hd, f, a, dwq, dwk, st);
 }
 
 size_t combine_bwd_workspace() { return CMB_BLOCKS * sizeof(float); }

@@ -96,13 +96,14 @@ def test_layer_entry_points_reject_bad_arguments(lib):
 @pytest.mark.parametrize("b, length, heads, kv, hd, f", [
     (2, 40, 4, 2, 32, 8), (4, 4096, 32, 8, 64, 128), (1, 7, 8, 8, 128, 64)])
 def test_layer_prologue_workspace_sizes(lib, b, length, heads, kv, hd, f):
-    """Per-workgroup partial dW tiles [32 ceil-tiles(f), hd] fp32: one
-    workgroup per 128 rows of each role (q rows, kv rows), at most 256."""
-    nq = min(-(-b * length * heads // 128), 256)
-    nk = min(-(-b * length * kv // 128), 256)
+    """Partial dW tiles [32 ceil-tiles(f), hd] fp32, a q and a kv one per
+    workgroup; the grid is one workgroup per 128-row block of both roles
+    together, at most 2 per CU on 256 CUs."""
+    blocks = -(-b * length * heads // 128) + -(-b * length * kv // 128)
+    grid = min(blocks, 512)
     fp = 32 if f <= 32 else (64 if f <= 64 else 128)
     assert lib.lz_layer_prologue_bwd_workspace_bytes(b, length, heads, kv, hd, f) == \
-        4 * (nq + nk) * fp * hd
+        4 * 2 * grid * fp * hd
 
 
 def segments(bh, length, f=64, chunk=64):
