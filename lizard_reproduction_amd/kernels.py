@@ -63,8 +63,23 @@ def _require_gpu(*tensors):
                              f"(got a tensor on {t.device})")
 
 
+# The casts below return their input unchanged when it already has the
+# dtype and layout (the common case): a dtype/contiguity test is far cheaper
+# per call than .to(...).contiguous(), and these wrappers run once per launch.
 def _bf16(t):
+    if t.dtype is torch.bfloat16 and t.is_contiguous():
+        return t
     return t.to(torch.bfloat16).contiguous()
+
+
+def _f32(t):
+    if t.dtype is torch.float32 and t.is_contiguous():
+        return t
+    return t.float().contiguous()
+
+
+def _cast_grads(grads, dtypes):
+    return tuple(g if g.dtype is d else g.to(d) for g, d in zip(grads, dtypes))
 
 
 # ---------------------------------------------------------------------------
@@ -140,7 +155,7 @@ class _GLA(torch.autograd.Function):
     def forward(ctx, fq, fk, v, log_gamma, chunk):
         ctx.dtypes = (fq.dtype, fk.dtype, v.dtype, log_gamma.dtype)
         fq, fk, v = _bf16(fq), _bf16(fk), _bf16(v)
-        lg = log_gamma.float().contiguous()
+        lg = _f32(log_gamma)
         grad = any(ctx.needs_input_grad[:4])
         y, state = gla_forward(fq, fk, v, lg, keep_state=grad, chunk=chunk)
         if grad:
@@ -155,7 +170,7 @@ class _GLA(torch.autograd.Function):
         fq, fk, v, lg = ctx.saved_tensors
         gdt = torch.bfloat16 if all(d == torch.bfloat16 for d in ctx.dtypes[:3]) else torch.float32
         grads = gla_backward(fq, fk, v, lg, _bf16(dy), ctx.fwd_ws, gdt, ctx.chunk)
-        return tuple(g.to(d) for g, d in zip(grads, ctx.dtypes)) + (None,)
+        return _cast_grads(grads, ctx.dtypes) + (None,)
 
 
 def gla_prefill(fq, fk, v, log_gamma, chunk=CHUNK):
@@ -298,7 +313,7 @@ class _SWA(torch.autograd.Function):
     def forward(ctx, q, k, v, meta, window, fwd_blocks, bwd_blocks):
         ctx.dtypes = (q.dtype, k.dtype, v.dtype, meta.dtype)
         q, k, v = _bf16(q), _bf16(k), _bf16(v)
-        meta = meta.float().contiguous()
+        meta = _f32(meta)
         y, lse = swa_forward(q, k, v, meta, window)
         if any(ctx.needs_input_grad[:4]):
             ctx.save_for_backward(q, k, v, meta, lse)
@@ -310,7 +325,7 @@ class _SWA(torch.autograd.Function):
         q, k, v, meta, lse = ctx.saved_tensors
         gdt = torch.bfloat16 if all(x == torch.bfloat16 for x in ctx.dtypes[:3]) else torch.float32
         grads = swa_backward(q, k, v, meta, lse, _bf16(dy), ctx.window, gdt)
-        return tuple(g.to(dt) for g, dt in zip(grads, ctx.dtypes)) + (None, None, None)
+        return _cast_grads(grads, ctx.dtypes) + (None, None, None)
 
 
 def swa(q, k, v, meta, window, fwd_blocks=FWD_BLOCKS, bwd_blocks=BWD_BLOCKS):
