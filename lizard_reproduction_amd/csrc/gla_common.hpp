@@ -97,16 +97,35 @@ __device__ __forceinline__ float sum_parts(const float* part, int c) {
   return s;
 }
 
+// x + (x of the lane DPP control CTRL names); lanes with no source and lanes
+// of rows outside ROW_MASK add 0.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add(float x) {
+  const int y = __builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROW_MASK, 0xf, false);
+  return x + __int_as_float(y);
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave: Hillis-Steele steps of 1,
+// 2, 4, 8 inside each 16-lane row (DPP row_shr), then the row totals carried
+// up by row_bcast:15 (row r's last lane into row r + 1, rows 1 and 3) and
+// row_bcast:31 (lane 31 into rows 2 and 3).  DPP moves need no LDS round
+// trip, unlike the ds_bpermute behind __shfl_up.
+__device__ __forceinline__ float wave_prefix_sum(float x) {
+  x = dpp_add<0x111, 0xf>(x);   // row_shr:1
+  x = dpp_add<0x112, 0xf>(x);   // row_shr:2
+  x = dpp_add<0x114, 0xf>(x);   // row_shr:4
+  x = dpp_add<0x118, 0xf>(x);   // row_shr:8
+  x = dpp_add<0x142, 0xa>(x);   // row_bcast:15
+  x = dpp_add<0x143, 0xc>(x);   // row_bcast:31
+  return x;
+}
+
 // Chunk-local inclusive scan of the gate by one wave (lane = token): lg,
 // e^{lg}, e^{lg_end - lg}, and e^{lg_end}, lg_end in r[0], r[1].
 __device__ __forceinline__ void gate_scan(float g, int lane, float* lgs, float* qs, float* ks,
                                           float* r) {
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const float o = __shfl_up(g, off);
-    if (lane >= off) g += o;
-  }
-  const float end = __shfl(g, 63);
+  g = wave_prefix_sum(g);
+  const float end = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(g), 63));
   lgs[lane] = g;
   qs[lane] = fexp(g);
   ks[lane] = fexp(end - g);

@@ -183,8 +183,12 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
 #pragma unroll
       for (int c = 0; c < FQ; c += 8) {
         const bf16x8 x = *reinterpret_cast<const bf16x8*>(fq_l + lane * PF + wave * FQ + c);
+        const f32x4 z0 = *reinterpret_cast<const f32x4*>(zs + wave * FQ + c);
+        const f32x4 z1 = *reinterpret_cast<const f32x4*>(zs + wave * FQ + c + 4);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc += to_f32(x[e]) * zs[wave * FQ + c + e];
+        for (int e = 0; e < 4; ++e) acc += to_f32(x[e]) * z0[e];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc += to_f32(x[4 + e]) * z1[e];
       }
       qz[wave * 64 + lane] = acc * qs[lane];
       scale_rows<FP>(fk_l, PF, ks, kti, zp);
