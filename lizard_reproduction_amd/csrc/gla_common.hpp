@@ -17,6 +17,7 @@ constexpr std::integral_constant<int, 1> SET1{};
 int gla_padded_dim(int n);
 bool gla_dims_supported(int F, int D);
 void gla_segments(int BH, int L, int F, int* G, int* cps);
+int gla_walk_segments(int BH, int G, int F);
 size_t gla_segment_floats(int BH, int G, int F, int D);
 
 // Rows [t0, t0+64) of a [L x ncols] bf16 matrix into registers, 16 bytes per

@@ -80,7 +80,7 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
     const bf16* __restrict__ fq, const bf16* __restrict__ fk, const bf16* __restrict__ v,
     const float* __restrict__ log_gamma, bf16* __restrict__ y,
     const float* __restrict__ seg_state, float* __restrict__ final_state, int H, int L, int F,
-    int D, int gate_per_head, int G, int cps) {
+    int D, int gate_per_head, int G, int cps, int M) {
   using Cfg = GlaFwd<FP, DP>;
   constexpr int C = Cfg::C, PF = Cfg::PF, PD = Cfg::PD;
   constexpr int NFT = Cfg::NFT, NDT = Cfg::NDT;
@@ -100,9 +100,12 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
   float* zp = reinterpret_cast<float*>(smem + Cfg::OFF_ZP);
   float* rdec = reinterpret_cast<float*>(smem + Cfg::OFF_R);
 
-  const int bh = blockIdx.x / G, seg = blockIdx.x % G;
+  // a workgroup walks M consecutive segments seg .. seg + M - 1 from the
+  // state entering the first
+  const int nwg = G / M;
+  const int bh = blockIdx.x / nwg, seg = (blockIdx.x % nwg) * M;
   const int NT = (L + C - 1) / C;
-  const int n0 = seg * cps, n1 = min(NT, n0 + cps);
+  const int n0 = seg * cps, n1 = min(NT, n0 + M * cps);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int col = lane & 31, h = lane >> 5;
   const bool vecF = VEC || (F & 7) == 0, vecD = VEC || (D & 7) == 0;
@@ -247,7 +250,7 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
   }
 
   // the state after the whole sequence, [F][D] fp32 then z [F], for decoding
-  if (final_state && seg == G - 1) {
+  if (final_state && seg + M == G) {
     float* fs = final_state + (size_t)bh * ((size_t)F * D + F);
     if (active && RD::primary(wave)) {
 #pragma unroll
@@ -434,12 +437,35 @@ hipError_t launch_gla_decode(const void* fq, const void* fk, const void* v, cons
 // ----------------------------------------------------------------------------
 // segment pass: state left by each segment g < G-1 starting from zero
 // ----------------------------------------------------------------------------
+// Its LDS: only the fk and v tiles of a chunk and the gate and z scratch
+// (no fq, no score fragments), so two workgroups fit a CU at every F.
+template <int FP, int DP>
+struct GlaState {
+  static constexpr int C = GLA_C;
+  static constexpr int PF = lds_pitch(FP), PD = lds_pitch(DP);
+  static constexpr int NFT = FP / 32, NDT = DP / 32;
+  static constexpr int ZPARTS = FP >= 256 ? 1 : 256 / FP;
+  static constexpr int NLF = C * FP / 8 / 256;        // 16-byte loads per thread, fk
+  static constexpr int NLD = C * DP / 8 / 256;        // 16-byte loads per thread, v
+  static constexpr int OFF_FK = 0;
+  static constexpr int OFF_V = OFF_FK + C * PF * 2;
+  static constexpr int OFF_LG = OFF_V + C * PD * 2;       // [64] chunk-local lg
+  static constexpr int OFF_QS = OFF_LG + 64 * 4;          // [64] e^{lg} (written by gate_scan)
+  static constexpr int OFF_KS = OFF_QS + 64 * 4;          // [64] e^{lg_end - lg}
+  static constexpr int OFF_Z = OFF_KS + 64 * 4;           // [FP] z
+  static constexpr int OFF_ZP = OFF_Z + FP * 4;           // [ZPARTS][FP] partial sums of K~
+  static constexpr int OFF_R = OFF_ZP + ZPARTS * FP * 4;  // e^{lg_end}, lg_end
+  static constexpr int BYTES = OFF_R + 16;
+  static constexpr int SEG = SegRec<FP, DP>::SIZE;
+  static_assert(BYTES <= 80 * 1024, "LDS budget: two workgroups per CU");
+};
+
 template <int FP, int DP, bool VEC>
-__global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_state_kernel(
+__global__ __launch_bounds__(256, 2) void gla_fwd_state_kernel(
     const bf16* __restrict__ fk, const bf16* __restrict__ v, const float* __restrict__ log_gamma,
     float* __restrict__ seg_state, float* __restrict__ seg_logdecay, int H, int L, int F, int D,
     int gate_per_head, int G, int cps) {
-  using Cfg = GlaFwd<FP, DP>;
+  using Cfg = GlaState<FP, DP>;
   constexpr int C = Cfg::C, PF = Cfg::PF, PD = Cfg::PD;
   constexpr int NFT = Cfg::NFT, NDT = Cfg::NDT;
   constexpr int NTILE = NFT * NDT;
@@ -605,12 +631,24 @@ bool gla_dims_supported(int F, int D) {
 // workgroups per CU up to F = 128, one beyond (the LDS of a 256-wide chunk).
 void gla_segments(int BH, int L, int F, int* G, int* cps) {
   const int NT = (L + GLA_C - 1) / GLA_C;
-  const int target = gla_padded_dim(F) > 128 ? GLA_TARGET_WG / 2 : GLA_TARGET_WG;
+  const bool wide = gla_padded_dim(F) > 128;   // walks run one workgroup per CU
+  const int target = wide ? GLA_TARGET_WG / 2 : GLA_TARGET_WG;
   int g = (target + BH - 1) / BH;
   g = g < 1 ? 1 : (g > NT ? NT : g);
+  // Wide walks: segments half as long as one walk, each walk taking two
+  // (gla_walk_segments).  The segment state passes, which fit two workgroups
+  // per CU, then run twice the workgroups at half the length.
+  if (wide && g > 1) g = 2 * g > NT ? NT : 2 * g;
   const int c = (NT + g - 1) / g;
   *cps = c;
   *G = (NT + c - 1) / c;
+}
+
+// Segments one walk workgroup takes in a row: two when each (b, h) has an
+// even number of segments and half as many workgroups still fill the GPU at
+// one per CU (wide walks; the segment split doubled for them).
+int gla_walk_segments(int BH, int G, int F) {
+  return gla_padded_dim(F) > 128 && G % 2 == 0 && BH * G / 2 >= GLA_TARGET_WG / 2 ? 2 : 1;
 }
 
 // workspace floats of one segment-state set: records + log decays
@@ -638,7 +676,7 @@ static hipError_t launch_gla_fwd_states_t(const void* fk, const void* v, const f
                                           float* seg_state, float* seg_logdecay, int BH, int H,
                                           int L, int F, int D, int gate_per_head, int G, int cps,
                                           hipStream_t st) {
-  using Cfg = GlaFwd<FP, DP>;
+  using Cfg = GlaState<FP, DP>;
   auto ks = gla_fwd_state_kernel<FP, DP, VEC>;
   hipError_t e = ensure_lds<gla_fwd_state_kernel<FP, DP, VEC>>(Cfg::BYTES);
   if (e != hipSuccess) return e;
@@ -688,9 +726,10 @@ static hipError_t launch_gla_fwd_t(const void* fq, const void* fk, const void* v
   auto kern = gla_fwd_kernel<FP, DP, VEC>;
   hipError_t e = ensure_lds<gla_fwd_kernel<FP, DP, VEC>>(Cfg::BYTES);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(kern, dim3(BH * G), dim3(256), Cfg::BYTES, st, (const bf16*)fq,
+  const int M = gla_walk_segments(BH, G, F);
+  hipLaunchKernelGGL(kern, dim3(BH * G / M), dim3(256), Cfg::BYTES, st, (const bf16*)fq,
                      (const bf16*)fk, (const bf16*)v, lg, (bf16*)y, (const float*)seg_state,
-                     final_state, H, L, F, D, gate_per_head, G, cps);
+                     final_state, H, L, F, D, gate_per_head, G, cps, M);
   return hipGetLastError();
 }
 

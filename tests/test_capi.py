@@ -108,11 +108,15 @@ def test_layer_prologue_workspace_sizes(lib, b, length, heads, kv, hd, f):
 
 def segments(bh, length, f=64, chunk=64):
     """The library's split of each (b, h) sequence into segments (so that
-    B*H*segments fills the GPU: 512 workgroups up to F = 128, 256 beyond):
+    B*H*segments fills the GPU: 512 workgroups up to F = 128, 256 beyond,
+    where the split is then doubled and each walk takes two segments):
     returns (segments, chunks per segment)."""
-    target = 256 if padded(f) > 128 else 512
+    wide = padded(f) > 128
+    target = 256 if wide else 512
     nt = -(-length // chunk)
     g = min(max(-(-target // bh), 1), nt)
+    if wide and g > 1:
+        g = min(2 * g, nt)
     cps = -(-nt // g)
     return -(-nt // cps), cps
 
@@ -142,7 +146,7 @@ def test_segment_split():
     assert segments(32, 2048) == (16, 2)        # training shape: 16 segments of 2 chunks
     assert segments(64, 1553) == (7, 4)         # ragged: the last segment is shorter
     assert segments(6, 1) == (1, 1)
-    assert segments(128, 4096, f=256) == (2, 32)   # config-5 layer shape: one workgroup per CU
+    assert segments(128, 4096, f=256) == (4, 16)   # config-5 layer shape: 2 segments per walk
 
 
 def test_swa_workspace_sizes(lib):
