@@ -139,7 +139,7 @@ struct ProBwdArgs {
 template <typename T, int FT, int HT>
 __device__ void load_weight(const T* __restrict__ w, int f, bf16* hi, bf16* lo) {
   using C = Pro<T, FT, HT>;
-  for (int i = threadIdx.x; i < C::FP * C::HP; i += 256) {
+  for (int i = threadIdx.x; i < C::FP * C::HP; i += blockDim.x) {
     const int r = i / C::HP, c = i % C::HP;
     const float x = r < f ? static_cast<float>(w[r * C::HP + c]) : 0.f;
     const bf16 h = to_bf16(x);
@@ -369,21 +369,29 @@ __global__ __launch_bounds__(256) void prologue_fwd_kernel(ProFwdArgs a) {
 // ---------------------------------------------------------------------------
 // backward
 //
-// A workgroup takes blocks of 128 rows (a wave owns 32 of them, one per
-// lane column of its MFMA tiles).  Per block:
+// A workgroup takes blocks of 128 rows.  Its 4 NWF waves are (row group rg,
+// feature group fh): wave (rg, fh) owns rows 32 rg .. 32 rg + 31 (one per lane
+// column of its MFMA tiles) and feature tiles fh FTW .. fh FTW + FTW - 1 of
+// both maps (FTW = FT / NWF).  Splitting a row's features over NWF = 2 waves
+// halves what a lane keeps in registers through the Jacobian, which is what
+// lets two waves share a SIMD at f = 128.  Per block:
 //   1. x rows -> LDS (bf16 hi, and lo for fp32 inputs), coalesced; each lane
 //      reads its row's MFMA operands back;
-//   2. softmax statistics of both feature maps in one pass over the feature
-//      tiles (per-tile maxima, running rescaled sums);
-//   3. per feature tile ft: the gradient rows' 32 dp and 32 dn values of
-//      that tile, summed over the group's heads in fp32, are gathered by the
-//      whole workgroup with 16-byte loads into an fp32 LDS stage, and each
-//      lane forms A = p dp - n dn and the sums <p, dp>, <n, dn> from it;
-//   4. dxw = A + n <n,dn> - p <p,dp> per tile: dx_phi^T += W^T dxw^T (MFMA,
-//      hi and lo parts of dxw), dxw hi -> the dW tile in LDS;
+//   2. softmax statistics of both feature maps over the wave's tiles in one
+//      pass (per-tile maxima, running rescaled sums), combined across the
+//      feature groups through LDS;
+//   3. per local tile s: the gradient rows' 32 dp and 32 dn values of tile s of
+//      every feature group, summed over the group's heads in fp32, are
+//      gathered by the whole workgroup with 16-byte loads into an fp32 LDS
+//      stage (the next tile's loads in flight meanwhile), and each lane forms
+//      A = p dp - n dn and its shares of <p, dp>, <n, dn> (summed across the
+//      feature groups through LDS afterwards);
+//   4. dxw = A + n <n,dn> - p <p,dp> per tile: the wave's share of
+//      dx_phi^T = W^T dxw^T (MFMA, hi and lo parts of dxw), dxw hi -> the dW
+//      tile in LDS;
 //   5. dW += dxw^T x over the block (hi, then lo), through LDS transpose reads;
-//   6. dx_phi -> LDS, and dx = dx_phi + rope^T(drope) (plus the summed dv for
-//      the kv rows) in a coalesced row layout, 8 columns per item.
+//   6. the dx_phi shares -> LDS, and dx = their sum + rope^T(drope) (plus the
+//      summed dv for the kv rows) in a coalesced row layout, 8 columns per item.
 // The stage, the dW tile and the dx tile share one LDS buffer.
 // ---------------------------------------------------------------------------
 constexpr int imax(int a, int b) { return a > b ? a : b; }
@@ -392,26 +400,38 @@ template <typename T, int FT, int HT>
 struct ProBwd {
   using C = Pro<T, FT, HT>;
   static constexpr int FP = C::FP, HP = C::HP, HK = C::HK, WP = C::WP, PARTS = C::PARTS;
+  // feature groups: two where a row has two or more feature tiles and the
+  // per-group dx shares fit the LDS (head_dim <= 64)
+  static constexpr int NWF = FT >= 2 && HT <= 2 ? 2 : 1;
+  static constexpr int FTW = FT / NWF;                   // feature tiles per wave
+  static constexpr int NW = PRO_WAVES * NWF, NT = 64 * NW;
   static constexpr int QP = lds_pitch(HP);    // x tiles [128][QP] bf16
   static constexpr int DP = lds_pitch(FP);    // dW tile [128][DP] bf16
-  static constexpr int SP = 64 + 4;           // stage [128][SP] fp32: 32 dp, then 32 dn
-  static constexpr int AP = HP + 4;           // dx tile [128][AP] fp32
+  static constexpr int SP = 64 * NWF + 4;     // stage [128][SP] fp32: per group 32 dp, 32 dn
+  static constexpr int AP = HP + 4;           // dx shares [NWF][128][AP] fp32
   static constexpr int BUF = imax(PRO_BLOCK * SP * 4, PRO_BLOCK * DP * 2);
   static constexpr int OFF_X = PARTS * FP * WP * 2;
   static constexpr int OFF_B = OFF_X + PARTS * PRO_BLOCK * QP * 2;
-  // the dx tile shares the buffer when it fits there, else it also spans the
-  // x tiles (then the next block waits for the epilogue before writing x)
-  static constexpr bool DX_OVER_X = PRO_BLOCK * AP * 4 > BUF;
+  // the dx shares take the buffer when they fit there, else they also span
+  // the x tiles (then the next block waits for the epilogue before writing x)
+  static constexpr int DX = NWF * PRO_BLOCK * AP * 4;
+  static constexpr bool DX_OVER_X = DX > BUF;
   static constexpr int OFF_DX = DX_OVER_X ? OFF_X : OFF_B;
-  static constexpr int LDS = imax(OFF_B + BUF, OFF_DX + PRO_BLOCK * AP * 4);
-  // workgroups per CU: two where the LDS and the registers (<= 256) allow it
-  static constexpr int OCC = LDS <= 80 * 1024 && FT <= 2 && HT <= 2 ? 2 : 1;
-  static constexpr int GI = PRO_BLOCK * 8 / 256;          // stage items per thread
-  // heads whose gradient loads are issued a tile ahead (none where two
-  // workgroups share a CU: their registers have no room for them)
-  static constexpr int GQ = OCC == 2 ? 0 : 4;
-  static constexpr int GQR = GQ > 0 ? GQ : 1;             // raw register sets held
-  static constexpr int XI = PRO_BLOCK * (HP / 8) / 256;   // x / dx items per thread
+  static constexpr int OFF_RED = imax(OFF_B + BUF, OFF_DX + DX);   // [NWF][4][128] row stats
+  static constexpr int LDS = OFF_RED + NWF * 4 * PRO_BLOCK * 4;
+  static constexpr int OCC = LDS <= 80 * 1024 && NW == 4 ? 2 : 1;   // workgroups per CU
+  static constexpr int IPR = 8 * NWF;                    // stage items per row
+  static constexpr int GI = PRO_BLOCK * IPR / NT;        // stage items per thread
+  static constexpr int RSTEP = NT / IPR;                 // rows between a thread's items
+  // heads whose gradient loads are issued a tile ahead: only where one wave
+  // per SIMD has the registers for them (the split and the two-workgroup
+  // forms have not: the loads' registers alone push them into spills, and
+  // their second wave per SIMD hides the load latency instead)
+  static constexpr int GQ = OCC == 1 && NWF == 1 ? 4 : 0;
+  static constexpr int GQR = GQ > 0 ? GQ : 1;            // raw register sets held
+  static constexpr int XI = PRO_BLOCK * (HP / 8) / NT;   // x / dx items per thread
+  static_assert(GI * RSTEP * IPR == PRO_BLOCK * IPR && RSTEP == 32, "item mapping");
+  static_assert(XI * NT == PRO_BLOCK * (HP / 8), "row items");
   static_assert(LDS <= 160 * 1024, "LDS budget");
 };
 
@@ -449,17 +469,26 @@ __device__ __forceinline__ void store8v(T* __restrict__ p, const float (&x)[8]) 
   }
 }
 
+// Two softmax statistics (running max m, sum s of e^{x - m}) of one row merged.
+__device__ __forceinline__ void merge_stats(float& m, float& s, float mo, float so) {
+  const float m2 = fmaxf(m, mo);
+  s = s * fexp(m - m2) + so * fexp(mo - m2);
+  m = m2;
+}
+
 // PART: f < 32 FT, so the last feature tile is partly padding and its
 // features past f are masked out (the instantiation without it carries no
 // masks at all).
 template <typename T, int FT, int HT, bool PART>
-__global__ __launch_bounds__(256, (ProBwd<T, FT, HT>::OCC)) void prologue_bwd_kernel(ProBwdArgs a) {
+__global__ __launch_bounds__((ProBwd<T, FT, HT>::NT), (ProBwd<T, FT, HT>::OCC)) void
+prologue_bwd_kernel(ProBwdArgs a) {
   using K = ProBwd<T, FT, HT>;
   constexpr int FP = K::FP, HP = K::HP, HK = K::HK, SP = K::SP, AP = K::AP;
+  constexpr int NWF = K::NWF, FTW = K::FTW, NW = K::NW, NT = K::NT;
   constexpr bool SPLIT = Pro<T, FT, HT>::SPLIT;
   constexpr int TILES = FT * HT;
-  constexpr int OWN = (TILES + PRO_WAVES - 1) / PRO_WAVES;   // dW tiles per wave
-  constexpr int H8 = HP / 8;                                 // 8-column items per hd row
+  constexpr int OWN = (TILES + NW - 1) / NW;   // dW tiles per wave
+  constexpr int H8 = HP / 8;                   // 8-column items per hd row
   extern __shared__ __attribute__((aligned(16))) char smem[];
   bf16* w_hi = reinterpret_cast<bf16*>(smem);
   bf16* w_lo = w_hi + FP * K::WP;
@@ -468,24 +497,29 @@ __global__ __launch_bounds__(256, (ProBwd<T, FT, HT>::OCC)) void prologue_bwd_ke
   float* stage = reinterpret_cast<float*>(smem + K::OFF_B);
   bf16* d_l = reinterpret_cast<bf16*>(smem + K::OFF_B);
   float* dx_l = reinterpret_cast<float*>(smem + K::OFF_DX);
+  float* red = reinterpret_cast<float*>(smem + K::OFF_RED);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, h = lane >> 5;
-  const int lrow = wave * PRO_ROWS + (lane & 31);    // this lane's row in the LDS tiles
+  const int rg = wave % PRO_WAVES, fh = wave / PRO_WAVES;   // row group, feature group
+  const int lrow = rg * PRO_ROWS + (lane & 31);             // this lane's row in the tiles
+  const int ft0 = fh * FTW;                                 // first feature tile of the wave
 
   const T* cs = static_cast<const T*>(a.cos);
   const T* sn = static_cast<const T*>(a.sin);
   const int f = a.f, hd = HP, half_hd = HP / 2, F2 = 2 * a.f;
   const bool vec = (f & 7) == 0;   // gradient items are whole 16-byte pieces
 
-  // stage items of this thread: rows (tid >> 3) + 32 i of a block, and the
-  // 8 features 8 (k & 3) .. +8 of tile ft of the dp (k < 4) or dn half
-  const int k8 = tid & 7, shalf = k8 >> 2, scol = 8 * (k8 & 3);
+  // stage items of this thread: rows tid / IPR + 32 i of a block; item k of a
+  // row covers features 8 (k & 3) .. +8 of tile (k / 8) FTW + s of the dp
+  // ((k / 4) & 1 == 0) or dn map, at stage column 8 k
+  const int k = tid % K::IPR, sgrp = k >> 3, shalf = (k >> 2) & 1, scol = 8 * (k & 3);
+  const int srow = tid / K::IPR;
 
   // this workgroup's partial dW [FP][HP] of role r: lane = column, registers = rows
   auto flush = [&](const f32x16 (&acc)[OWN], int r, bool zero) {
     float* part = a.part + ((size_t)r * gridDim.x + blockIdx.x) * FP * HP;
 #pragma unroll
     for (int i = 0; i < OWN; ++i) {
-      const int t = wave + PRO_WAVES * i;
+      const int t = wave + NW * i;
       if (t < TILES) {
         const int ft = t / HT, ht = t % HT;
 #pragma unroll
@@ -530,35 +564,13 @@ __global__ __launch_bounds__(256, (ProBwd<T, FT, HT>::OCC)) void prologue_bwd_ke
       load_weight<T, FT, HT>(static_cast<const T*>(kv ? a.wk : a.wq), f, w_hi, w_lo);
     }
     const int row0 = (kv ? j - a.nbq : j) * PRO_BLOCK;
-    // ---- 1. x rows -> LDS; this lane's operands ------------------------------
-#pragma unroll
-    for (int i = 0; i < K::XI; ++i) {
-      const int idx = tid + 256 * i, r = idx / H8, m0 = 8 * (idx % H8);
-      float xf[8];
-      if (row0 + r < nrows) {
-        load8f(x + (long)(row0 + r) * hd + m0, xf);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) xf[e] = 0.f;
-      }
-      const bf16x8 hi = to_bf8(xf);
-      *reinterpret_cast<bf16x8*>(x_hi + r * K::QP + m0) = hi;
-      if constexpr (SPLIT) *reinterpret_cast<bf16x8*>(x_lo + r * K::QP + m0) = low8(xf, hi);
-    }
-    __syncthreads();   // x tiles (and, on the first block, W)
-    bf16x8 xh[HK], xl[HK];
-#pragma unroll
-    for (int kb = 0; kb < HK; ++kb) {
-      xh[kb] = row_operand(x_hi, K::QP, lrow, 16 * kb, h);
-      if constexpr (SPLIT) xl[kb] = row_operand(x_lo, K::QP, lrow, 16 * kb, h);
-    }
 
     // rows of this thread's stage items: [B, H, L, 2f] element offset of
     // their first head's gradient row (-1: row past the end)
     long gbase[K::GI];
 #pragma unroll
     for (int i = 0; i < K::GI; ++i) {
-      const int row = row0 + (tid >> 3) + 32 * i;
+      const int row = row0 + srow + 32 * i;
       if (row < nrows) {
         const RowPos pos = decode(row, a.L, heads_in);
         gbase[i] = (((long)pos.b * a.H + pos.head * group) * a.L + pos.l) * F2 + shalf * f;
@@ -566,12 +578,12 @@ __global__ __launch_bounds__(256, (ProBwd<T, FT, HT>::OCC)) void prologue_bwd_ke
         gbase[i] = -1;
       }
     }
-    // Gradient items of tile ft: the loads of the first GQ heads are issued a
-    // tile ahead (raw, 16 bytes each) and summed when the tile is staged;
-    // heads past GQ are loaded and added then.
+    // Gradient items of local tile s: the loads of the first GQ heads are
+    // issued a tile ahead (raw, 16 bytes each) and summed when the tile is
+    // staged; heads past GQ are loaded and added then.
     auto item_ok = [&](int i, int c) { return gbase[i] >= 0 && c < f; };
-    auto issue = [&](int ft, uint4 (&raw)[K::GQR][K::GI]) {
-      const int c = 32 * ft + scol;
+    auto issue = [&](int s, uint4 (&raw)[K::GQR][K::GI]) {
+      const int c = 32 * (sgrp * FTW + s) + scol;
 #pragma unroll
       for (int g = 0; g < K::GQ; ++g)
 #pragma unroll
@@ -587,8 +599,8 @@ __global__ __launch_bounds__(256, (ProBwd<T, FT, HT>::OCC)) void prologue_bwd_ke
             }
           }
     };
-    auto gather = [&](int ft, const uint4 (&raw)[K::GQR][K::GI], float (&g8)[K::GI][8]) {
-      const int c = 32 * ft + scol;
+    auto gather = [&](int s, const uint4 (&raw)[K::GQR][K::GI], float (&g8)[K::GI][8]) {
+      const int c = 32 * (sgrp * FTW + s) + scol;
 #pragma unroll
       for (int i = 0; i < K::GI; ++i) {
 #pragma unroll
@@ -613,10 +625,34 @@ __global__ __launch_bounds__(256, (ProBwd<T, FT, HT>::OCC)) void prologue_bwd_ke
     uint4 raw[K::GQR][K::GI];
     if constexpr (K::GQ > 0) issue(0, raw);
 
+    // ---- 1. x rows -> LDS; this lane's operands ------------------------------
+#pragma unroll
+    for (int i = 0; i < K::XI; ++i) {
+      const int idx = tid + NT * i, r = idx / H8, m0 = 8 * (idx % H8);
+      float xf[8];
+      if (row0 + r < nrows) {
+        load8f(x + (long)(row0 + r) * hd + m0, xf);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xf[e] = 0.f;
+      }
+      const bf16x8 hi = to_bf8(xf);
+      *reinterpret_cast<bf16x8*>(x_hi + r * K::QP + m0) = hi;
+      if constexpr (SPLIT) *reinterpret_cast<bf16x8*>(x_lo + r * K::QP + m0) = low8(xf, hi);
+    }
+    __syncthreads();   // x tiles (and, after a role switch, W); the last block's epilogue is done
+    bf16x8 xh[HK], xl[HK];
+#pragma unroll
+    for (int kb = 0; kb < HK; ++kb) {
+      xh[kb] = row_operand(x_hi, K::QP, lrow, 16 * kb, h);
+      if constexpr (SPLIT) xl[kb] = row_operand(x_lo, K::QP, lrow, 16 * kb, h);
+    }
+
     // ---- 2. softmax statistics: maxima and sums in one pass -----------------
     float mp = -1e30f, mn = -1e30f, sp = 0.f, sn_ = 0.f;
 #pragma unroll
-    for (int ft = 0; ft < FT; ++ft) {
+    for (int s = 0; s < FTW; ++s) {
+      const int ft = ft0 + s;
       const f32x16 acc = project_tile<T, FT, HT>(ft, xh, xl, w_hi, w_lo, lane);
       // features past f (padding of the last tile) drop out through
       // selects, not branches: their exponentials are of -inf
@@ -640,43 +676,62 @@ __global__ __launch_bounds__(256, (ProBwd<T, FT, HT>::OCC)) void prologue_bwd_ke
       mp = np;
       mn = nn;
     }
-    {   // the other lane half holds the row's other features
-      const float mpo = xhalf(mp), spo = xhalf(sp), mno = xhalf(mn), sno = xhalf(sn_);
-      const float mp2 = fmaxf(mp, mpo), mn2 = fmaxf(mn, mno);
-      sp = sp * fexp(mp - mp2) + spo * fexp(mpo - mp2);
-      sn_ = sn_ * fexp(mn - mn2) + sno * fexp(mno - mn2);
-      mp = mp2;
-      mn = mn2;
+    // the other lane half holds other features of the row ...
+    merge_stats(mp, sp, xhalf(mp), xhalf(sp));
+    merge_stats(mn, sn_, xhalf(mn), xhalf(sn_));
+    if constexpr (NWF > 1) {   // ... and the other feature group the rest
+      float* mine = red + fh * 4 * PRO_BLOCK;
+      if (h == 0) {
+        mine[lrow] = mp;
+        mine[PRO_BLOCK + lrow] = sp;
+        mine[2 * PRO_BLOCK + lrow] = mn;
+        mine[3 * PRO_BLOCK + lrow] = sn_;
+      }
+      __syncthreads();
+      const float* other = red + (1 - fh) * 4 * PRO_BLOCK;
+      const float omp = other[lrow], osp = other[PRO_BLOCK + lrow];
+      const float omn = other[2 * PRO_BLOCK + lrow], osn = other[3 * PRO_BLOCK + lrow];
+      // both groups merge in the same order (group 0 first): identical results
+      if (fh == 0) {
+        merge_stats(mp, sp, omp, osp);
+        merge_stats(mn, sn_, omn, osn);
+      } else {
+        float m0 = omp, s0 = osp, n0 = omn, t0 = osn;
+        merge_stats(m0, s0, mp, sp);
+        merge_stats(n0, t0, mn, sn_);
+        mp = m0, sp = s0, mn = n0, sn_ = t0;
+      }
     }
     const float ip = 1.f / sp, in = 1.f / sn_;
 
     // ---- 3. A = p dp - n dn per feature tile, <p, dp>, <n, dn> ---------------
-    f32x16 A[FT];
+    f32x16 A[FTW];
     float s_p = 0.f, s_n = 0.f;
 #pragma unroll
-    for (int ft = 0; ft < FT; ++ft) {
+    for (int s = 0; s < FTW; ++s) {
       float g8[K::GI][8];
-      gather(ft, raw, g8);
-      if (K::GQ > 0 && ft + 1 < FT) issue(ft + 1, raw);   // in flight while this tile computes
-      __syncthreads();   // the previous tile's (or block's) readers of the buffer are done
+      gather(s, raw, g8);
+      if (K::GQ > 0 && s + 1 < FTW) issue(s + 1, raw);   // in flight while this tile computes
+      __syncthreads();   // the previous tile's readers of the buffer (and red) are done
 #pragma unroll
       for (int i = 0; i < K::GI; ++i) {
-        float* dst = stage + ((tid >> 3) + 32 * i) * SP + 32 * shalf + scol;
+        float* dst = stage + (srow + 32 * i) * SP + 8 * k;
         *reinterpret_cast<f32x4*>(dst) = f32x4{g8[i][0], g8[i][1], g8[i][2], g8[i][3]};
         *reinterpret_cast<f32x4*>(dst + 4) = f32x4{g8[i][4], g8[i][5], g8[i][6], g8[i][7]};
       }
       __syncthreads();
-      const f32x16 acc = project_tile<T, FT, HT>(ft, xh, xl, w_hi, w_lo, lane);
+      const f32x16 acc = project_tile<T, FT, HT>(ft0 + s, xh, xl, w_hi, w_lo, lane);
+      const float* srow_l = stage + lrow * SP + 64 * fh;
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
-        const f32x4 dp = *reinterpret_cast<const f32x4*>(stage + lrow * SP + 8 * q4 + 4 * h);
-        const f32x4 dn = *reinterpret_cast<const f32x4*>(stage + lrow * SP + 32 + 8 * q4 + 4 * h);
+        const f32x4 dp = *reinterpret_cast<const f32x4*>(srow_l + 8 * q4 + 4 * h);
+        const f32x4 dn = *reinterpret_cast<const f32x4*>(srow_l + 32 + 8 * q4 + 4 * h);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int r = 4 * q4 + e;
           const float pd = fexp(acc[r] - mp) * ip * dp[e];
           const float nd = fexp(-acc[r] - mn) * in * dn[e];
-          A[ft][r] = pd - nd;
+          A[s][r] = pd - nd;
           s_p += pd;
           s_n += nd;
         }
@@ -684,25 +739,38 @@ __global__ __launch_bounds__(256, (ProBwd<T, FT, HT>::OCC)) void prologue_bwd_ke
     }
     s_p += xhalf(s_p);
     s_n += xhalf(s_n);
+    if constexpr (NWF > 1) {
+      if (h == 0) {
+        red[fh * 4 * PRO_BLOCK + lrow] = s_p;
+        red[fh * 4 * PRO_BLOCK + PRO_BLOCK + lrow] = s_n;
+      }
+    }
+    __syncthreads();   // every lane is done with the stage (and the shares are in red)
+    if constexpr (NWF > 1) {   // group 0's share first, in both groups
+      const float p0 = red[lrow], p1 = red[4 * PRO_BLOCK + lrow];
+      const float n0 = red[PRO_BLOCK + lrow], n1 = red[5 * PRO_BLOCK + lrow];
+      s_p = p0 + p1;
+      s_n = n0 + n1;
+    }
 
-    // ---- 4. dxw; dx_phi^T = W^T dxw^T; dxw hi -> the dW tile ----------------
-    __syncthreads();   // every lane is done with the stage
+    // ---- 4. dxw; the wave's share of dx_phi^T = W^T dxw^T; dxw hi -> dW tile --
     f32x16 dacc[HT];
 #pragma unroll
     for (int ht = 0; ht < HT; ++ht) dacc[ht] = zero16();
-    bf16x4 dlo[FT][4];
+    bf16x4 dlo[FTW][4];
 #pragma unroll
-    for (int ft = 0; ft < FT; ++ft) {
+    for (int s = 0; s < FTW; ++s) {
+      const int ft = ft0 + s;
       const f32x16 acc = project_tile<T, FT, HT>(ft, xh, xl, w_hi, w_lo, lane);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const float p = fexp(acc[r] - mp) * ip;
         const float n = fexp(-acc[r] - mn) * in;
-        A[ft][r] = !PART || 32 * ft + acc_row(r, h) < f ? A[ft][r] + n * s_n - p * s_p : 0.f;
+        A[s][r] = !PART || 32 * ft + acc_row(r, h) < f ? A[s][r] + n * s_n - p * s_p : 0.f;
       }
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        const bf16x8 dh = acc_operand(A[ft], kb), dl = acc_operand_lo(A[ft], kb);
+        const bf16x8 dh = acc_operand(A[s], kb), dl = acc_operand_lo(A[s], kb);
 #pragma unroll
         for (int ht = 0; ht < HT; ++ht) {
           const bf16x8 w = tr_operand(w_hi, K::WP, 32 * ft + 16 * kb, 32 * ht, lane);
@@ -718,9 +786,9 @@ __global__ __launch_bounds__(256, (ProBwd<T, FT, HT>::OCC)) void prologue_bwd_ke
         bf16x4 o;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float v = A[ft][4 * q4 + e];
+          const float v = A[s][4 * q4 + e];
           o[e] = to_bf16(v);
-          dlo[ft][q4][e] = to_bf16(v - to_f32(o[e]));
+          dlo[s][q4][e] = to_bf16(v - to_f32(o[e]));
         }
         *reinterpret_cast<bf16x4*>(d_l + lrow * K::DP + 32 * ft + 8 * q4 + 4 * h) = o;
       }
@@ -731,16 +799,16 @@ __global__ __launch_bounds__(256, (ProBwd<T, FT, HT>::OCC)) void prologue_bwd_ke
     for (int part = 0; part < 2; ++part) {
       if (part == 1) {
 #pragma unroll
-        for (int ft = 0; ft < FT; ++ft)
+        for (int s = 0; s < FTW; ++s)
 #pragma unroll
           for (int q4 = 0; q4 < 4; ++q4)
-            *reinterpret_cast<bf16x4*>(d_l + lrow * K::DP + 32 * ft + 8 * q4 + 4 * h) =
-                dlo[ft][q4];
+            *reinterpret_cast<bf16x4*>(d_l + lrow * K::DP + 32 * (ft0 + s) + 8 * q4 + 4 * h) =
+                dlo[s][q4];
       }
       __syncthreads();
 #pragma unroll
       for (int i = 0; i < OWN; ++i) {
-        const int t = wave + PRO_WAVES * i;
+        const int t = wave + NW * i;
         if (t < TILES) {
           const int ft = t / HT, ht = t % HT;
 #pragma unroll 2
@@ -755,21 +823,24 @@ __global__ __launch_bounds__(256, (ProBwd<T, FT, HT>::OCC)) void prologue_bwd_ke
       __syncthreads();
     }
 
-    // ---- 6. dx = dx_phi + rope^T(drope) (+ dv sums), coalesced ---------------
+    // ---- 6. dx = sum of the dx_phi shares + rope^T(drope) (+ dv sums) --------
+    {
+      float* mine = dx_l + fh * PRO_BLOCK * AP;
 #pragma unroll
-    for (int ht = 0; ht < HT; ++ht)
+      for (int ht = 0; ht < HT; ++ht)
 #pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4)
-        *reinterpret_cast<f32x4*>(dx_l + lrow * AP + 32 * ht + 8 * q4 + 4 * h) =
-            f32x4{dacc[ht][4 * q4], dacc[ht][4 * q4 + 1], dacc[ht][4 * q4 + 2],
-                  dacc[ht][4 * q4 + 3]};
+        for (int q4 = 0; q4 < 4; ++q4)
+          *reinterpret_cast<f32x4*>(mine + lrow * AP + 32 * ht + 8 * q4 + 4 * h) =
+              f32x4{dacc[ht][4 * q4], dacc[ht][4 * q4 + 1], dacc[ht][4 * q4 + 2],
+                    dacc[ht][4 * q4 + 3]};
+    }
     __syncthreads();
     // dx[m] = dr[m] cos[m] + dr[m + hd/2] sin[m + hd/2] for m < hd/2,
     //         dr[m] cos[m] - dr[m - hd/2] sin[m - hd/2] otherwise (drope summed
     // over the group's heads); the kv rows also sum dv (and dv2) over the group.
 #pragma unroll 1
     for (int i = 0; i < K::XI; ++i) {
-      const int idx = tid + 256 * i, r = idx / H8, m0 = 8 * (idx % H8);
+      const int idx = tid + NT * i, r = idx / H8, m0 = 8 * (idx % H8);
       const int row = row0 + r;
       if (row >= nrows) continue;
       const RowPos pos = decode(row, a.L, heads_in);
@@ -793,9 +864,14 @@ __global__ __launch_bounds__(256, (ProBwd<T, FT, HT>::OCC)) void prologue_bwd_ke
       float c[8], s2[8], out[8];
       load8f(cs + tab + m0, c);
       load8f(sn + tab + mp2, s2);
-      const float* dxr = dx_l + r * AP + m0;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) out[e] = dxr[e] + dr[e] * c[e] + sign * dr2[e] * s2[e];
+      for (int e = 0; e < 8; ++e) out[e] = dr[e] * c[e] + sign * dr2[e] * s2[e];
+#pragma unroll
+      for (int g2 = 0; g2 < NWF; ++g2) {   // the shares in group order
+        const float* dxr = dx_l + (g2 * PRO_BLOCK + r) * AP + m0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) out[e] += dxr[e];
+      }
       store8v(dx + (long)row * hd + m0, out);
       if (kv) store8v(static_cast<T*>(a.dvo) + (long)row * hd + m0, dvs);
     }
@@ -985,13 +1061,13 @@ static hipError_t launch_bwd_t(const ProBwdArgs& a, float* dwq, float* dwk, hipS
   if (a.f == C::FP) {
     e = ensure_lds<prologue_bwd_kernel<T, FT, HT, false>>(C::LDS);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((prologue_bwd_kernel<T, FT, HT, false>), dim3(grid), dim3(256), C::LDS, st,
-                       a);
+    hipLaunchKernelGGL((prologue_bwd_kernel<T, FT, HT, false>), dim3(grid), dim3(C::NT), C::LDS,
+                       st, a);
   } else {
     e = ensure_lds<prologue_bwd_kernel<T, FT, HT, true>>(C::LDS);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((prologue_bwd_kernel<T, FT, HT, true>), dim3(grid), dim3(256), C::LDS, st,
-                       a);
+    hipLaunchKernelGGL((prologue_bwd_kernel<T, FT, HT, true>), dim3(grid), dim3(C::NT), C::LDS,
+                       st, a);
   }
   e = hipGetLastError();
   if (e != hipSuccess) return e;
