@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define LZ_ABI_VERSION 7
+#define LZ_ABI_VERSION 8
 
 /* ABI version of the loaded library (LZ_ABI_VERSION). */
 int lz_abi_version(void);
@@ -45,8 +45,12 @@ size_t lz_gla_fwd_workspace_bytes(int batch, int heads, int length, int nf, int 
  * GLA forward.  Replaces kernels.gla's forward: the gate cumsum and head
  * expand (src/kernels/gla.py:259-263) and the two launches of _GLA.forward,
  * _gla_fwd_h + _gla_fwd_o (src/kernels/gla.py:213-234).
- *   fq, fk      bf16 [BH, L, nf]      feature-mapped queries / keys
- *   v           bf16 [BH, L, nd]
+ *   fq          bf16 [BH, L, nf]      feature-mapped queries
+ *   fk          bf16 [B*kv_heads, L, nf]  feature-mapped keys
+ *   v           bf16 [B*kv_heads, L, nd]
+ *   kv_heads    heads of fk and v (divides heads): query head h reads kv head
+ *               h / (heads / kv_heads), grouped-query attention without
+ *               materialised copies; kv_heads = heads is the reference's layout
  *   log_gamma   f32  [B, L] (gate_per_head = 0) or [B, H, L] (gate_per_head = 1);
  *               log of the gate (<= 0), NOT its cumsum
  *   y           bf16 [BH, L, nd]      output
@@ -61,8 +65,8 @@ size_t lz_gla_fwd_workspace_bytes(int batch, int heads, int length, int nf, int 
  * the output is the same with and without autograd (tests/test_kernels.py:102-107).
  */
 int lz_gla_fwd(const void* fq, const void* fk, const void* v, const float* log_gamma, void* y,
-               int batch, int heads, int length, int nf, int nd, int gate_per_head, int chunk,
-               void* workspace, size_t workspace_bytes, void* stream);
+               int batch, int heads, int kv_heads, int length, int nf, int nd, int gate_per_head,
+               int chunk, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * GLA prefill: lz_gla_fwd that also writes the recurrent state after the last
@@ -73,8 +77,8 @@ int lz_gla_fwd(const void* fq, const void* fk, const void* v, const float* log_g
  * Other arguments as lz_gla_fwd (same workspace).
  */
 int lz_gla_prefill(const void* fq, const void* fk, const void* v, const float* log_gamma,
-                   void* y, float* state, int batch, int heads, int length, int nf, int nd,
-                   int gate_per_head, int chunk, void* workspace, size_t workspace_bytes,
+                   void* y, float* state, int batch, int heads, int kv_heads, int length, int nf,
+                   int nd, int gate_per_head, int chunk, void* workspace, size_t workspace_bytes,
                    void* stream);
 
 /*
@@ -98,7 +102,9 @@ size_t lz_gla_bwd_workspace_bytes(int batch, int heads, int length, int nf, int 
  * _gla_bwd_dh, _gla_bwd_dqkv, the dg reduction, and the autograd steps of
  * the gate path (expand-sum over heads, reverse cumsum, gla.py:260-262).
  *   dy            bf16 [BH, L, nd]      upstream gradient
- *   dfq, dfk      [BH, L, nf], dv [BH, L, nd]: bf16 if grad_bf16 else f32
+ *   dfq, dfk      [BH, L, nf], dv [BH, L, nd]: bf16 if grad_bf16 else f32; per
+ *                 query head also when kv_heads < heads (each query head's
+ *                 share; their sum over a group is the kv head's gradient)
  *   dlog_gamma    f32, same shape as log_gamma
  *   fwd_workspace the workspace lz_gla_fwd used for these inputs, if the caller
  *                 kept it (it then holds the state entering each segment and
@@ -107,14 +113,16 @@ size_t lz_gla_bwd_workspace_bytes(int batch, int heads, int length, int nf, int 
  */
 int lz_gla_bwd(const void* fq, const void* fk, const void* v, const float* log_gamma,
                const void* dy, void* dfq, void* dfk, void* dv, float* dlog_gamma, int grad_bf16,
-               int batch, int heads, int length, int nf, int nd, int gate_per_head, int chunk,
-               const void* fwd_workspace, size_t fwd_workspace_bytes, void* workspace,
+               int batch, int heads, int kv_heads, int length, int nf, int nd, int gate_per_head,
+               int chunk, const void* fwd_workspace, size_t fwd_workspace_bytes, void* workspace,
                size_t workspace_bytes, void* stream);
 
 /*
  * SWA forward.  Replaces _SWA.forward / _swa_fwd (src/kernels/swa.py:136-156,
  * 19-59).
- *   q, k, v     bf16 [BH, L, dim]  (RoPE already applied to q and k)
+ *   q           bf16 [BH, L, dim]  (RoPE already applied)
+ *   k, v        bf16 [B*kv_heads, L, dim]  (RoPE applied to k); kv_heads divides
+ *               heads, query head h reads kv head h / (heads / kv_heads)
  *   meta        f32 [n_meta] sink logits (n_meta may be 0; at most 64)
  *   y           bf16 [BH, L, dim] output
  *   lse         f32 [BH, L] log of each row's softmax denominator (saved for backward)
@@ -122,8 +130,8 @@ int lz_gla_bwd(const void* fq, const void* fk, const void* v, const float* log_g
  * Supported sizes: dim <= 256.
  */
 int lz_swa_fwd(const void* q, const void* k, const void* v, const float* meta, int n_meta,
-               void* y, float* lse, int batch, int heads, int length, int dim, int window,
-               float scale, void* stream);
+               void* y, float* lse, int batch, int heads, int kv_heads, int length, int dim,
+               int window, float scale, void* stream);
 
 /* Workspace bytes lz_swa_bwd needs for these sizes. */
 size_t lz_swa_bwd_workspace_bytes(int batch, int heads, int length, int dim, int n_meta);
@@ -135,12 +143,13 @@ size_t lz_swa_bwd_workspace_bytes(int batch, int heads, int length, int dim, int
  * probabilities (the reference takes it from the bf16 output, swa.py:164),
  * so the forward saves only lse.
  *   lse         from lz_swa_fwd;  dy  bf16 [BH, L, dim]
- *   dq, dk, dv  [BH, L, dim]: bf16 if grad_bf16 else f32
+ *   dq, dk, dv  [BH, L, dim]: bf16 if grad_bf16 else f32 (dk, dv per query head,
+ *               as lz_gla_bwd's dfk, dv)
  *   dmeta       f32 [n_meta] (untouched when n_meta == 0)
  */
 int lz_swa_bwd(const void* q, const void* k, const void* v, const float* meta, int n_meta,
                const float* lse, const void* dy, void* dq, void* dk, void* dv, float* dmeta,
-               int grad_bf16, int batch, int heads, int length, int dim, int window,
+               int grad_bf16, int batch, int heads, int kv_heads, int length, int dim, int window,
                float scale, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
@@ -154,9 +163,13 @@ int lz_swa_bwd(const void* q, const void* k, const void* v, const float* meta, i
  *   wq, wk      [feature_dim, head_dim]     (phi_q.weight, phi_k.weight)
  *   cos, sin    [B, L, head_dim] if cos_batched else [L, head_dim]
  *   all of them bf16 if dtype_bf16 else f32.
- *   fq, fk      bf16 [B, heads, L, 2 feature_dim]: [softmax(x W^T), softmax(-x W^T)]
- *   qr, kr, v_out  bf16 [B, heads, L, head_dim]: rotate_half RoPE of q, k; v
- *   (k, v rows of kv head g go to query heads g*G .. g*G+G-1, G = heads/kv_heads).
+ *   fq          bf16 [B, heads, L, 2 feature_dim]: [softmax(q Wq^T), softmax(-q Wq^T)]
+ *   fk          bf16 [B, kv_heads, L, 2 feature_dim]: the same of k with Wk
+ *   qr          bf16 [B, heads, L, head_dim]: rotate_half RoPE of q
+ *   kr, v_out   bf16 [B, kv_heads, L, head_dim]: RoPE of k; v
+ *   The k-side operands stay per kv head: lz_gla_* and lz_swa_* read them with
+ *   kv_heads < heads, which replaces the reference's repeat_interleave without
+ *   writing its copies.
  * Supported sizes: head_dim 32, 64 or 128; feature_dim a multiple of 4, at most
  * 128 (64 when head_dim is 128).
  */
@@ -172,8 +185,10 @@ size_t lz_layer_prologue_bwd_workspace_bytes(int batch, int length, int heads, i
 
 /*
  * Layer prologue, backward: what autograd does for the same ops.
- *   dfq, dfk         bf16 [B, heads, L, 2 feature_dim]  (gradients of fq, fk)
- *   dqr, dkr, dv     bf16 [B, heads, L, head_dim]       (gradients of qr, kr, v_out)
+ *   dfq, dfk         bf16 [B, heads, L, 2 feature_dim]  (gradients of fq, and of fk per
+ *                    query head, as lz_gla_bwd writes them)
+ *   dqr, dkr, dv     bf16 [B, heads, L, head_dim]       (gradients of qr, kr, v_out per
+ *                    query head, as lz_swa_bwd / lz_gla_bwd write them)
  *   dv2              NULL or a second bf16 gradient of v_out, added to dv in
  *                    fp32 (v_out feeds both attention branches)
  *   dq               [B, L, heads, head_dim];  dk, dv_out [B, L, kv_heads, head_dim]

@@ -8,7 +8,7 @@ import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "_lib", "liblizard_hip.so")
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -20,16 +20,17 @@ SIGNATURES = {
     "lz_abi_version": (_I, []),
     "lz_last_error": (ctypes.c_char_p, []),
     "lz_gla_fwd_workspace_bytes": (_S, [_I, _I, _I, _I, _I, _I, _I]),
-    "lz_gla_fwd": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _S, _P]),
-    "lz_gla_prefill": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _S, _P]),
+    "lz_gla_fwd": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _S, _P]),
+    "lz_gla_prefill": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _S,
+                            _P]),
     "lz_gla_decode_step": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "lz_gla_bwd_workspace_bytes": (_S, [_I, _I, _I, _I, _I, _I, _I]),
     "lz_gla_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I,
-                        _I, _I, _I, _I, _I, _I, _I, _P, _S, _P, _S, _P]),
-    "lz_swa_fwd": (_I, [_P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _F, _P]),
+                        _I, _I, _I, _I, _I, _I, _I, _I, _P, _S, _P, _S, _P]),
+    "lz_swa_fwd": (_I, [_P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P]),
     "lz_swa_bwd_workspace_bytes": (_S, [_I, _I, _I, _I, _I]),
     "lz_swa_bwd": (_I, [_P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I,
-                        _I, _I, _I, _I, _I, _F, _P, _S, _P]),
+                        _I, _I, _I, _I, _I, _I, _F, _P, _S, _P]),
     "lz_layer_prologue_fwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I,
                                    _I, _I, _I, _I, _I, _I, _P]),
     "lz_layer_prologue_bwd_workspace_bytes": (_S, [_I, _I, _I, _I, _I, _I]),

@@ -10,7 +10,7 @@
 
 namespace lz {
 hipError_t launch_gla_fwd(const void* fq, const void* fk, const void* v, const float* lg, void* y,
-                          int B, int H, int L, int F, int D, int gate_per_head, float* ws,
+                          int B, int H, int L, int F, int D, int gate_per_head, int KG, float* ws,
                           float* final_state, hipStream_t st);
 hipError_t launch_gla_decode(const void* fq, const void* fk, const void* v, const float* lg,
                              float* state, void* y, int B, int H, int F, int D,
@@ -19,18 +19,18 @@ size_t gla_fwd_workspace(int B, int H, int L, int F, int D);
 hipError_t launch_gla_bwd(const void* fq, const void* fk, const void* v, const float* lg,
                           const void* dy, void* dfq, void* dfk, void* dv, float* dlg,
                           bool grad_bf16, int B, int H, int L, int F, int D, int gate_per_head,
-                          const float* fwd_ws, float* ws, hipStream_t st);
+                          int KG, const float* fwd_ws, float* ws, hipStream_t st);
 size_t gla_bwd_workspace(int B, int H, int L, int F, int D, int gate_per_head);
 bool gla_dims_supported(int F, int D);
 int swa_padded_dim(int d);
 int swa_row_blocks(int L);
 hipError_t launch_swa_fwd(const void* q, const void* k, const void* v, const float* meta,
                           int n_meta, void* y, float* lse, int BH, int L, int d, int W,
-                          float scale, hipStream_t st);
+                          float scale, int KG, hipStream_t st);
 hipError_t launch_swa_bwd(const void* q, const void* k, const void* v, const float* meta,
                           int n_meta, const float* lse, const void* dy, void* dq, void* dk,
                           void* dv, bool grad_bf16, float* delta, float* dmeta_part,
-                          float* dmeta, int BH, int L, int d, int W, float scale,
+                          float* dmeta, int BH, int L, int d, int W, float scale, int KG,
                           hipStream_t st);
 constexpr int MAX_META = 64;
 bool prologue_dims_supported(int hd, int f);
@@ -94,6 +94,15 @@ static int check_gla(const void* fq, const void* fk, const void* v, const float*
   return 0;
 }
 
+// kv_heads heads of k-side operands (fk and v; k and v), each shared by
+// heads / kv_heads consecutive query heads (grouped-query attention)
+static int check_kv_heads(const char* what, int heads, int kv_heads) {
+  if (kv_heads <= 0 || heads % kv_heads)
+    return fail(1, "%s: kv_heads (%d) must be positive and divide heads (%d)", what, kv_heads,
+                heads);
+  return 0;
+}
+
 extern "C" size_t lz_gla_fwd_workspace_bytes(int batch, int heads, int length, int nf, int nd,
                                              int gate_per_head, int chunk) {
   (void)gate_per_head; (void)chunk;
@@ -102,33 +111,35 @@ extern "C" size_t lz_gla_fwd_workspace_bytes(int batch, int heads, int length, i
 }
 
 extern "C" int lz_gla_fwd(const void* fq, const void* fk, const void* v, const float* log_gamma,
-                          void* y, int batch, int heads, int length, int nf, int nd,
+                          void* y, int batch, int heads, int kv_heads, int length, int nf, int nd,
                           int gate_per_head, int chunk, void* workspace, size_t workspace_bytes,
                           void* stream) {
   if (int rc = check_gla(fq, fk, v, log_gamma, batch, heads, length, nf, nd, chunk)) return rc;
+  if (int rc = check_kv_heads("gla_fwd", heads, kv_heads)) return rc;
   if (!y) return fail(1, "gla_fwd: null output pointer");
   const size_t need = lz::gla_fwd_workspace(batch, heads, length, nf, nd);
   if (need && (!workspace || workspace_bytes < need))
     return fail(1, "gla_fwd: workspace of %zu bytes given, %zu needed", workspace_bytes, need);
   return hip_status(lz::launch_gla_fwd(fq, fk, v, log_gamma, y, batch, heads, length, nf, nd,
-                                       gate_per_head ? 1 : 0, (float*)workspace, nullptr,
-                                       (hipStream_t)stream),
+                                       gate_per_head ? 1 : 0, heads / kv_heads, (float*)workspace,
+                                       nullptr, (hipStream_t)stream),
                     "gla_fwd");
 }
 
 extern "C" int lz_gla_prefill(const void* fq, const void* fk, const void* v,
                               const float* log_gamma, void* y, float* state, int batch, int heads,
-                              int length, int nf, int nd, int gate_per_head, int chunk,
-                              void* workspace, size_t workspace_bytes, void* stream) {
+                              int kv_heads, int length, int nf, int nd, int gate_per_head,
+                              int chunk, void* workspace, size_t workspace_bytes, void* stream) {
   if (int rc = check_gla(fq, fk, v, log_gamma, batch, heads, length, nf, nd, chunk)) return rc;
+  if (int rc = check_kv_heads("gla_prefill", heads, kv_heads)) return rc;
   if (!y || !state) return fail(1, "gla_prefill: null output pointer");
   const size_t need = lz::gla_fwd_workspace(batch, heads, length, nf, nd);
   if (need && (!workspace || workspace_bytes < need))
     return fail(1, "gla_prefill: workspace of %zu bytes given, %zu needed", workspace_bytes,
                 need);
   return hip_status(lz::launch_gla_fwd(fq, fk, v, log_gamma, y, batch, heads, length, nf, nd,
-                                       gate_per_head ? 1 : 0, (float*)workspace, state,
-                                       (hipStream_t)stream),
+                                       gate_per_head ? 1 : 0, heads / kv_heads, (float*)workspace,
+                                       state, (hipStream_t)stream),
                     "gla_prefill");
 }
 
@@ -151,11 +162,12 @@ extern "C" size_t lz_gla_bwd_workspace_bytes(int batch, int heads, int length, i
 
 extern "C" int lz_gla_bwd(const void* fq, const void* fk, const void* v, const float* log_gamma,
                           const void* dy, void* dfq, void* dfk, void* dv, float* dlog_gamma,
-                          int grad_bf16, int batch, int heads, int length, int nf, int nd,
-                          int gate_per_head, int chunk, const void* fwd_workspace,
+                          int grad_bf16, int batch, int heads, int kv_heads, int length, int nf,
+                          int nd, int gate_per_head, int chunk, const void* fwd_workspace,
                           size_t fwd_workspace_bytes, void* workspace, size_t workspace_bytes,
                           void* stream) {
   if (int rc = check_gla(fq, fk, v, log_gamma, batch, heads, length, nf, nd, chunk)) return rc;
+  if (int rc = check_kv_heads("gla_bwd", heads, kv_heads)) return rc;
   if (!dy || !dfq || !dfk || !dv || !dlog_gamma) return fail(1, "gla_bwd: null pointer");
   const size_t need = lz::gla_bwd_workspace(batch, heads, length, nf, nd, gate_per_head ? 1 : 0);
   if (!workspace || workspace_bytes < need)
@@ -172,8 +184,8 @@ extern "C" int lz_gla_bwd(const void* fq, const void* fk, const void* v, const f
   }
   return hip_status(lz::launch_gla_bwd(fq, fk, v, log_gamma, dy, dfq, dfk, dv, dlog_gamma,
                                        grad_bf16 != 0, batch, heads, length, nf, nd,
-                                       gate_per_head ? 1 : 0, fws, (float*)workspace,
-                                       (hipStream_t)stream),
+                                       gate_per_head ? 1 : 0, heads / kv_heads, fws,
+                                       (float*)workspace, (hipStream_t)stream),
                     "gla_bwd");
 }
 
@@ -191,12 +203,13 @@ static int check_swa(const void* q, const void* k, const void* v, const float* m
 }
 
 extern "C" int lz_swa_fwd(const void* q, const void* k, const void* v, const float* meta,
-                          int n_meta, void* y, float* lse, int batch, int heads, int length,
-                          int dim, int window, float scale, void* stream) {
+                          int n_meta, void* y, float* lse, int batch, int heads, int kv_heads,
+                          int length, int dim, int window, float scale, void* stream) {
   if (int rc = check_swa(q, k, v, meta, n_meta, batch, heads, length, dim, window)) return rc;
+  if (int rc = check_kv_heads("swa_fwd", heads, kv_heads)) return rc;
   if (!y || !lse) return fail(1, "swa_fwd: null output pointer");
   return hip_status(lz::launch_swa_fwd(q, k, v, meta, n_meta, y, lse, batch * heads, length, dim,
-                                       window, scale, (hipStream_t)stream),
+                                       window, scale, heads / kv_heads, (hipStream_t)stream),
                     "swa_fwd");
 }
 
@@ -210,10 +223,11 @@ extern "C" size_t lz_swa_bwd_workspace_bytes(int batch, int heads, int length, i
 
 extern "C" int lz_swa_bwd(const void* q, const void* k, const void* v, const float* meta,
                           int n_meta, const float* lse, const void* dy, void* dq, void* dk,
-                          void* dv, float* dmeta, int grad_bf16, int batch, int heads, int length,
-                          int dim, int window, float scale, void* workspace,
-                          size_t workspace_bytes, void* stream) {
+                          void* dv, float* dmeta, int grad_bf16, int batch, int heads,
+                          int kv_heads, int length, int dim, int window, float scale,
+                          void* workspace, size_t workspace_bytes, void* stream) {
   if (int rc = check_swa(q, k, v, meta, n_meta, batch, heads, length, dim, window)) return rc;
+  if (int rc = check_kv_heads("swa_bwd", heads, kv_heads)) return rc;
   if (!lse || !dy || !dq || !dk || !dv) return fail(1, "swa_bwd: null pointer");
   if (n_meta > 0 && !dmeta) return fail(1, "swa_bwd: null dmeta pointer");
   const size_t need = lz_swa_bwd_workspace_bytes(batch, heads, length, dim, n_meta);
@@ -224,7 +238,7 @@ extern "C" int lz_swa_bwd(const void* q, const void* k, const void* v, const flo
   float* part = delta + (size_t)batch * heads * length;
   return hip_status(lz::launch_swa_bwd(q, k, v, meta, n_meta, lse, dy, dq, dk, dv,
                                        grad_bf16 != 0, delta, part, dmeta, batch * heads, length,
-                                       dim, window, scale, st),
+                                       dim, window, scale, heads / kv_heads, st),
                     "swa_bwd");
 }
 

@@ -175,7 +175,7 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
     const float* __restrict__ log_gamma, const bf16* __restrict__ dy, OutT* __restrict__ dfq,
     float* __restrict__ den_out, float* __restrict__ delta_out, float* __restrict__ p_out,
     const float* __restrict__ seg_state, int H, int L, int F, int D, int gate_per_head, int G,
-    int cps, int M) {
+    int cps, int M, int KG) {
   using Cfg = BwdA<FP, DP>;
   constexpr int C = Cfg::C, PF = Cfg::PF, PD = Cfg::PD;
   constexpr int NFT = Cfg::NFT, NDT = Cfg::NDT;
@@ -210,6 +210,8 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
   const int col = lane & 31, h = lane >> 5;
   const bool vecF = VEC || (F & 7) == 0, vecD = VEC || (D & 7) == 0;
   const size_t offF = (size_t)bh * L * F, offD = (size_t)bh * L * D, offL = (size_t)bh * L;
+  // fk and v of the kv head of this query head (KG query heads share one)
+  const size_t offFk = (size_t)(bh / KG) * L * F, offDv = (size_t)(bh / KG) * L * D;
   const float* lgb = log_gamma + (size_t)(gate_per_head ? bh : bh / H) * L;
   const float* st = G > 1 ? seg_state + ((size_t)bh * G + seg) * Cfg::SEG : nullptr;
 
@@ -278,8 +280,8 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
     constexpr int S = decltype(set)::value;
     if (n < n1) {
       load_tile8<FP>(rq[S], fq + offF, n * C, L, F, vecF);
-      load_tile8<FP>(rk[S], fk + offF, n * C, L, F, vecF);
-      load_tile8<DP>(rv[S], v + offD, n * C, L, D, vecD);
+      load_tile8<FP>(rk[S], fk + offFk, n * C, L, F, vecF);
+      load_tile8<DP>(rv[S], v + offDv, n * C, L, D, vecD);
       load_tile8<DP>(rd[S], dy + offD, n * C, L, D, vecD);
       if (wave == 0) rg[S] = gate_at(lgb, n * C + lane, L);
     }
@@ -733,7 +735,7 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
     const float* __restrict__ den_in, const float* __restrict__ delta_in,
     const float* __restrict__ p_in, OutT* __restrict__ dfk, OutT* __restrict__ dv,
     float* __restrict__ dG, float* __restrict__ csum, const float* __restrict__ seg_state, int H,
-    int L, int F, int D, int gate_per_head, int G, int cps, int M) {
+    int L, int F, int D, int gate_per_head, int G, int cps, int M, int KG) {
   using Cfg = BwdB<FP, DP>;
   constexpr int C = Cfg::C, PF = Cfg::PF, PD = Cfg::PD;
   constexpr int NFT = Cfg::NFT, NDT = Cfg::NDT, ZP = Cfg::ZP;
@@ -769,6 +771,8 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
   const int col = lane & 31, h = lane >> 5;
   const bool vecF = VEC || (F & 7) == 0, vecD = VEC || (D & 7) == 0;
   const size_t offF = (size_t)bh * L * F, offD = (size_t)bh * L * D, offL = (size_t)bh * L;
+  // fk and v of the kv head of this query head (KG query heads share one)
+  const size_t offFk = (size_t)(bh / KG) * L * F, offDv = (size_t)(bh / KG) * L * D;
   const float* lgb = log_gamma + (size_t)(gate_per_head ? bh : bh / H) * L;
   const float* st = G > 1 ? seg_state + ((size_t)bh * G + seg) * Cfg::SEG : nullptr;
 
@@ -813,8 +817,8 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
     constexpr int S = decltype(set)::value;
     if (n >= n0) {
       load_tile8<FP>(rq[S], fq + offF, n * C, L, F, vecF);
-      load_tile8<FP>(rk[S], fk + offF, n * C, L, F, vecF);
-      load_tile8<DP>(rv[S], v + offD, n * C, L, D, vecD);
+      load_tile8<FP>(rk[S], fk + offFk, n * C, L, F, vecF);
+      load_tile8<DP>(rv[S], v + offDv, n * C, L, D, vecD);
       load_tile8<DP>(rd[S], dy + offD, n * C, L, D, vecD);
       if (wave == 0) sc[S] = load_scalars(lgb, den_in, delta_in, p_in, offL, n * C + lane, L);
     }
@@ -1094,7 +1098,7 @@ size_t gla_bwd_workspace(int B, int H, int L, int F, int D, int gate_per_head) {
 template <int FP, int DP, typename OutT, bool VEC>
 static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v, const float* lg,
                                    const void* dy, void* dfq, void* dfk, void* dv, float* dlg,
-                                   int B, int H, int L, int F, int D, int gate_per_head,
+                                   int B, int H, int L, int F, int D, int gate_per_head, int KG,
                                    const float* fwd_ws, float* ws, hipStream_t st) {
   const int BH = B * H;
   const size_t BHL = (size_t)BH * L;
@@ -1115,7 +1119,7 @@ static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v
   hipError_t e;
   if (G > 1 && !fwd_ws) {
     e = launch_gla_fwd_states(fk, v, lg, own_fseg, own_fseg + (size_t)BH * G * SEG, BH, H, L, F,
-                              D, gate_per_head, G, cps, st);
+                              D, gate_per_head, G, cps, KG, st);
     if (e != hipSuccess) return e;
   }
   // the walks take two segments per workgroup while that still gives 256
@@ -1125,7 +1129,7 @@ static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v
   if ((e = ensure_lds<gla_bwd_dq_kernel<FP, DP, OutT, VEC>>(LDS_A)) != hipSuccess) return e;
   hipLaunchKernelGGL(ka, dim3(BH * G / M), dim3(B_THREADS), LDS_A, st, (const bf16*)fq,
                      (const bf16*)fk, (const bf16*)v, lg, (const bf16*)dy, (OutT*)dfq, den, delta,
-                     p, fseg, H, L, F, D, gate_per_head, G, cps, M);
+                     p, fseg, H, L, F, D, gate_per_head, G, cps, M, KG);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   if (G > 1) {
     auto ks = gla_bwd_state_kernel<FP, DP, VEC>;
@@ -1142,7 +1146,7 @@ static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v
   hipLaunchKernelGGL(kb, dim3(BH * G / M), dim3(B_THREADS), LDS_B, st, (const bf16*)fq,
                      (const bf16*)fk, (const bf16*)v, lg, (const bf16*)dy, (const float*)den,
                      (const float*)delta, (const float*)p, (OutT*)dfk, (OutT*)dv, dG, csum,
-                     (const float*)rseg, H, L, F, D, gate_per_head, G, cps, M);
+                     (const float*)rseg, H, L, F, D, gate_per_head, G, cps, M, KG);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   const dim3 ggrid((L + GLA_C - 1) / GLA_C, gate_rows(B, H, gate_per_head));
   hipLaunchKernelGGL(gla_gate_grad_kernel, ggrid, dim3(256), 0, st, (const float*)dG,
@@ -1153,12 +1157,12 @@ static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v
 hipError_t launch_gla_bwd(const void* fq, const void* fk, const void* v, const float* lg,
                           const void* dy, void* dfq, void* dfk, void* dv, float* dlg,
                           bool grad_bf16, int B, int H, int L, int F, int D, int gate_per_head,
-                          const float* fwd_ws, float* ws, hipStream_t st) {
+                          int KG, const float* fwd_ws, float* ws, hipStream_t st) {
   const int fp = gla_padded_dim(F), dp = gla_padded_dim(D);
   const bool vec = F % 8 == 0 && D % 8 == 0;
 #define LZ_GLA_BWD_V(FPV, DPV, OUT, V)                                                          \
   launch_gla_bwd_t<FPV, DPV, OUT, V>(fq, fk, v, lg, dy, dfq, dfk, dv, dlg, B, H, L, F, D,      \
-                                     gate_per_head, fwd_ws, ws, st)
+                                     gate_per_head, KG, fwd_ws, ws, st)
 #define LZ_GLA_BWD(FPV, DPV)                                                                    \
   if (fp == FPV && dp == DPV)                                                                   \
     return grad_bf16 ? (vec ? LZ_GLA_BWD_V(FPV, DPV, bf16, true)                                \

@@ -172,7 +172,7 @@ struct SegRec {
 // segments; used by the forward and by the backward's forward walk.
 hipError_t launch_gla_fwd_states(const void* fk, const void* v, const float* lg, float* seg_state,
                                  float* seg_logdecay, int BH, int H, int L, int F, int D,
-                                 int gate_per_head, int G, int cps, hipStream_t st);
+                                 int gate_per_head, int G, int cps, int KG, hipStream_t st);
 hipError_t launch_gla_segment_scan(float* seg_state, const float* seg_logdecay, int BH, int G,
                                    int rec, bool reverse, hipStream_t st);
 

@@ -80,7 +80,7 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
     const bf16* __restrict__ fq, const bf16* __restrict__ fk, const bf16* __restrict__ v,
     const float* __restrict__ log_gamma, bf16* __restrict__ y,
     const float* __restrict__ seg_state, float* __restrict__ final_state, int H, int L, int F,
-    int D, int gate_per_head, int G, int cps, int M) {
+    int D, int gate_per_head, int G, int cps, int M, int KG) {
   using Cfg = GlaFwd<FP, DP>;
   constexpr int C = Cfg::C, PF = Cfg::PF, PD = Cfg::PD;
   constexpr int NFT = Cfg::NFT, NDT = Cfg::NDT;
@@ -109,9 +109,10 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int col = lane & 31, h = lane >> 5;
   const bool vecF = VEC || (F & 7) == 0, vecD = VEC || (D & 7) == 0;
+  // fk and v belong to the kv head of this query head: KG query heads share one
   const bf16* fqb = fq + (size_t)bh * L * F;
-  const bf16* fkb = fk + (size_t)bh * L * F;
-  const bf16* vb = v + (size_t)bh * L * D;
+  const bf16* fkb = fk + (size_t)(bh / KG) * L * F;
+  const bf16* vb = v + (size_t)(bh / KG) * L * D;
   const rsrc_t yr = make_rsrc(y + (size_t)bh * L * D, (size_t)L * D * 2);
   const float* lgb = log_gamma + (size_t)(gate_per_head ? bh : bh / H) * L;
   const float* st = G > 1 ? seg_state + ((size_t)bh * G + seg) * Cfg::SEG : nullptr;
@@ -464,7 +465,7 @@ template <int FP, int DP, bool VEC>
 __global__ __launch_bounds__(256, 2) void gla_fwd_state_kernel(
     const bf16* __restrict__ fk, const bf16* __restrict__ v, const float* __restrict__ log_gamma,
     float* __restrict__ seg_state, float* __restrict__ seg_logdecay, int H, int L, int F, int D,
-    int gate_per_head, int G, int cps) {
+    int gate_per_head, int G, int cps, int KG) {
   using Cfg = GlaState<FP, DP>;
   constexpr int C = Cfg::C, PF = Cfg::PF, PD = Cfg::PD;
   constexpr int NFT = Cfg::NFT, NDT = Cfg::NDT;
@@ -485,8 +486,8 @@ __global__ __launch_bounds__(256, 2) void gla_fwd_state_kernel(
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int col = lane & 31, h = lane >> 5;
   const bool vecF = VEC || (F & 7) == 0, vecD = VEC || (D & 7) == 0;
-  const bf16* fkb = fk + (size_t)bh * L * F;
-  const bf16* vb = v + (size_t)bh * L * D;
+  const bf16* fkb = fk + (size_t)(bh / KG) * L * F;
+  const bf16* vb = v + (size_t)(bh / KG) * L * D;
   const float* lgb = log_gamma + (size_t)(gate_per_head ? bh : bh / H) * L;
 
   f32x16 S[TPW];
@@ -675,30 +676,31 @@ template <int FP, int DP, bool VEC>
 static hipError_t launch_gla_fwd_states_t(const void* fk, const void* v, const float* lg,
                                           float* seg_state, float* seg_logdecay, int BH, int H,
                                           int L, int F, int D, int gate_per_head, int G, int cps,
-                                          hipStream_t st) {
+                                          int KG, hipStream_t st) {
   using Cfg = GlaState<FP, DP>;
   auto ks = gla_fwd_state_kernel<FP, DP, VEC>;
   hipError_t e = ensure_lds<gla_fwd_state_kernel<FP, DP, VEC>>(Cfg::BYTES);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(ks, dim3(BH * (G - 1)), dim3(256), Cfg::BYTES, st, (const bf16*)fk,
-                     (const bf16*)v, lg, seg_state, seg_logdecay, H, L, F, D, gate_per_head, G, cps);
+                     (const bf16*)v, lg, seg_state, seg_logdecay, H, L, F, D, gate_per_head, G, cps,
+                     KG);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   return launch_gla_segment_scan(seg_state, seg_logdecay, BH, G, Cfg::SEG, false, st);
 }
 
 hipError_t launch_gla_fwd_states(const void* fk, const void* v, const float* lg, float* seg_state,
                                  float* seg_logdecay, int BH, int H, int L, int F, int D,
-                                 int gate_per_head, int G, int cps, hipStream_t st) {
+                                 int gate_per_head, int G, int cps, int KG, hipStream_t st) {
   const int fp = gla_padded_dim(F), dp = gla_padded_dim(D);
   const bool vec = F % 8 == 0 && D % 8 == 0;
 #define LZ_GLA_ST(FPV, DPV)                                                                   \
   if (fp == FPV && dp == DPV)                                                                 \
     return vec ? launch_gla_fwd_states_t<FPV, DPV, true>(fk, v, lg, seg_state, seg_logdecay,  \
                                                          BH, H, L, F, D, gate_per_head, G,    \
-                                                         cps, st)                             \
+                                                         cps, KG, st)                         \
                : launch_gla_fwd_states_t<FPV, DPV, false>(fk, v, lg, seg_state, seg_logdecay, \
                                                           BH, H, L, F, D, gate_per_head, G,   \
-                                                          cps, st);
+                                                          cps, KG, st);
   LZ_GLA_ST(32, 32) LZ_GLA_ST(32, 64) LZ_GLA_ST(32, 128)
   LZ_GLA_ST(64, 32) LZ_GLA_ST(64, 64) LZ_GLA_ST(64, 128)
   LZ_GLA_ST(128, 32) LZ_GLA_ST(128, 64) LZ_GLA_ST(128, 128)
@@ -710,7 +712,7 @@ hipError_t launch_gla_fwd_states(const void* fk, const void* v, const float* lg,
 template <int FP, int DP, bool VEC>
 static hipError_t launch_gla_fwd_t(const void* fq, const void* fk, const void* v,
                                    const float* lg, void* y, int B, int H, int L, int F, int D,
-                                   int gate_per_head, float* ws, float* final_state,
+                                   int gate_per_head, int KG, float* ws, float* final_state,
                                    hipStream_t st) {
   using Cfg = GlaFwd<FP, DP>;
   const int BH = B * H;
@@ -720,7 +722,7 @@ static hipError_t launch_gla_fwd_t(const void* fq, const void* fk, const void* v
   if (G > 1) {
     hipError_t e = launch_gla_fwd_states_t<FP, DP, VEC>(fk, v, lg, seg_state,
                                                    ws + (size_t)BH * G * Cfg::SEG, BH, H, L, F,
-                                                   D, gate_per_head, G, cps, st);
+                                                   D, gate_per_head, G, cps, KG, st);
     if (e != hipSuccess) return e;
   }
   auto kern = gla_fwd_kernel<FP, DP, VEC>;
@@ -729,21 +731,21 @@ static hipError_t launch_gla_fwd_t(const void* fq, const void* fk, const void* v
   const int M = gla_walk_segments(BH, G, F);
   hipLaunchKernelGGL(kern, dim3(BH * G / M), dim3(256), Cfg::BYTES, st, (const bf16*)fq,
                      (const bf16*)fk, (const bf16*)v, lg, (bf16*)y, (const float*)seg_state,
-                     final_state, H, L, F, D, gate_per_head, G, cps, M);
+                     final_state, H, L, F, D, gate_per_head, G, cps, M, KG);
   return hipGetLastError();
 }
 
 hipError_t launch_gla_fwd(const void* fq, const void* fk, const void* v, const float* lg, void* y,
-                          int B, int H, int L, int F, int D, int gate_per_head, float* ws,
+                          int B, int H, int L, int F, int D, int gate_per_head, int KG, float* ws,
                           float* final_state, hipStream_t st) {
   const int fp = gla_padded_dim(F), dp = gla_padded_dim(D);
   const bool vec = F % 8 == 0 && D % 8 == 0;
 #define LZ_GLA_FWD(FPV, DPV)                                                                    \
   if (fp == FPV && dp == DPV)                                                                   \
     return vec ? launch_gla_fwd_t<FPV, DPV, true>(fq, fk, v, lg, y, B, H, L, F, D,              \
-                                                  gate_per_head, ws, final_state, st)           \
+                                                  gate_per_head, KG, ws, final_state, st)       \
                : launch_gla_fwd_t<FPV, DPV, false>(fq, fk, v, lg, y, B, H, L, F, D,             \
-                                                   gate_per_head, ws, final_state, st);
+                                                   gate_per_head, KG, ws, final_state, st);
   LZ_GLA_FWD(32, 32) LZ_GLA_FWD(32, 64) LZ_GLA_FWD(32, 128)
   LZ_GLA_FWD(64, 32) LZ_GLA_FWD(64, 64) LZ_GLA_FWD(64, 128)
   LZ_GLA_FWD(128, 32) LZ_GLA_FWD(128, 64) LZ_GLA_FWD(128, 128)

@@ -6,10 +6,12 @@
 // rows ordered (b, l, head)):
 //   fq = [softmax(q Wq^T), softmax(-q Wq^T)]      (Hedgehog, :9-11, F = 2f)
 //   qr = rope(q)                                  (rotate_half RoPE, :88)
-//   fk, kr, v likewise from the kv heads, each written to the H / Hkv query
-//   heads of its group (the repeat_interleave of :73-76)
-// all in fp32 from the inputs' values, written once as the bf16 [B, H, L, .]
-// operands of the GLA and SWA kernels.  x W^T is a bf16 MFMA product; fp32
+//   fk, kr, v likewise from the kv heads
+// all in fp32 from the inputs' values, written once as the bf16 operands of
+// the GLA and SWA kernels: [B, H, L, .] for the query side, [B, Hkv, L, .]
+// for the key side.  The reference's repeat_interleave of k and v to the
+// H / Hkv query heads of a group (:73-76) is not materialised: the GLA and
+// SWA kernels read a query head's k-side operands from its kv head.  x W^T is a bf16 MFMA product; fp32
 // inputs are split into bf16 hi + lo parts and the three significant partial
 // products summed (hi*hi + lo*hi + hi*lo), which keeps fp32-level accuracy.
 //
@@ -224,13 +226,13 @@ __device__ __forceinline__ RowPos decode(int row, int L, int heads) {
 
 
 // Half `half` of the 2f-wide feature rows of a wave's 32 rows, staged in LDS
-// ([32][pitch] bf16), to the rows' output heads in chunks of CH elements.
-// Row r's output base row (the obase of lane r, split in two ints) comes
-// from lane r by a cross-lane read.
+// ([32][pitch] bf16), to the rows' output rows in chunks of CH elements.
+// Row r's output row (the obase of lane r, split in two ints) comes from
+// lane r by a cross-lane read.
 template <int CH>
 __device__ __forceinline__ void copy_rows(const bf16* stage, int pitch, bf16* __restrict__ out,
                                           int ob_lo, int ob_hi, int row0, int nrows, int f,
-                                          int half, int group, int L, int lane) {
+                                          int half, int lane) {
   typedef __bf16 chunk_t __attribute__((ext_vector_type(CH)));
   const int cpr = f / CH;
   for (int i = lane; i < PRO_ROWS * cpr; i += 64) {
@@ -238,8 +240,7 @@ __device__ __forceinline__ void copy_rows(const bf16* stage, int pitch, bf16* __
     const long base = ((long)__shfl(ob_hi, r) << 32) | (unsigned)__shfl(ob_lo, r);
     if (row0 + r >= nrows) continue;
     const chunk_t val = *reinterpret_cast<const chunk_t*>(stage + r * pitch + c);
-    for (int g = 0; g < group; ++g)
-      *reinterpret_cast<chunk_t*>(out + (base + (long)g * L) * (2 * f) + half * f + c) = val;
+    *reinterpret_cast<chunk_t*>(out + base * (2 * f) + half * f + c) = val;
   }
 }
 
@@ -259,7 +260,6 @@ __global__ __launch_bounds__(256) void prologue_fwd_kernel(ProFwdArgs a) {
   const int wg = kv ? blockIdx.x - a.nq_wg : blockIdx.x;
   const int nwg = kv ? gridDim.x - a.nq_wg : a.nq_wg;
   const int heads_in = kv ? a.Hkv : a.H;
-  const int group = kv ? a.H / a.Hkv : 1;
   const int nrows = a.B * a.L * heads_in;
   const T* x = static_cast<const T*>(kv ? a.k : a.q);
   bf16* fout = kv ? a.fk : a.fq;
@@ -276,9 +276,8 @@ __global__ __launch_bounds__(256) void prologue_fwd_kernel(ProFwdArgs a) {
     const int row = row0 + (lane & 31);
     const bool live = row < nrows;
     const RowPos pos = decode(live ? row : 0, a.L, heads_in);
-    // [B, H, L, .] row of this row's first output head; the group's next heads
-    // are L rows apart
-    const long obase = ((long)pos.b * a.H + pos.head * group) * a.L + pos.l;
+    // its [B, heads_in, L, .] output row
+    const long obase = ((long)pos.b * heads_in + pos.head) * a.L + pos.l;
 
     bf16x8 xh[C::HK], xl[C::HK];
     {
@@ -310,11 +309,9 @@ __global__ __launch_bounds__(256) void prologue_fwd_kernel(ProFwdArgs a) {
             o1[e] = to_bf16(xf[kb][e] * c1[e] - xf[kb2][e] * s1[e]);
             o2[e] = to_bf16(xf[kb2][e] * c2[e] + xf[kb][e] * s2[e]);
           }
-          for (int g = 0; g < group; ++g) {
-            bf16* dst = rout + (obase + (long)g * a.L) * hd;
-            *reinterpret_cast<bf16x8*>(dst + 16 * kb + 8 * h) = o1;
-            *reinterpret_cast<bf16x8*>(dst + 16 * kb2 + 8 * h) = o2;
-          }
+          bf16* dst = rout + obase * hd;
+          *reinterpret_cast<bf16x8*>(dst + 16 * kb + 8 * h) = o1;
+          *reinterpret_cast<bf16x8*>(dst + 16 * kb2 + 8 * h) = o2;
         }
         if (kv) {
           const T* vrow = static_cast<const T*>(a.v) + (long)row * hd;
@@ -322,10 +319,7 @@ __global__ __launch_bounds__(256) void prologue_fwd_kernel(ProFwdArgs a) {
           for (int kb = 0; kb < C::HK; ++kb) {
             float vf[8];
             load8f(vrow + 16 * kb + 8 * h, vf);
-            const bf16x8 o = to_bf8(vf);
-            for (int g = 0; g < group; ++g)
-              *reinterpret_cast<bf16x8*>(a.vo + (obase + (long)g * a.L) * hd + 16 * kb + 8 * h) =
-                  o;
+            *reinterpret_cast<bf16x8*>(a.vo + obase * hd + 16 * kb + 8 * h) = to_bf8(vf);
           }
         }
       }
@@ -358,9 +352,9 @@ __global__ __launch_bounds__(256) void prologue_fwd_kernel(ProFwdArgs a) {
       }
       wave_sync();
       if (f % 8 == 0)
-        copy_rows<8>(stage, C::SP, fout, ob_lo, ob_hi, row0, nrows, f, half, group, a.L, lane);
+        copy_rows<8>(stage, C::SP, fout, ob_lo, ob_hi, row0, nrows, f, half, lane);
       else
-        copy_rows<4>(stage, C::SP, fout, ob_lo, ob_hi, row0, nrows, f, half, group, a.L, lane);
+        copy_rows<4>(stage, C::SP, fout, ob_lo, ob_hi, row0, nrows, f, half, lane);
       wave_sync();
     }
   }

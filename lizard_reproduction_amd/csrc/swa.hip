@@ -89,7 +89,7 @@ template <int DP, bool VEC>
 __global__ __launch_bounds__(256) void swa_fwd_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ meta, int n_meta, bf16* __restrict__ y, float* __restrict__ lse,
-    int BH, int L, int d, int W, float scale, int per) {
+    int BH, int L, int d, int W, float scale, int per, int KG) {
   using Cfg = SwaCfg<DP>;
   constexpr int P = Cfg::P;
   extern __shared__ __align__(16) char smem[];
@@ -104,6 +104,7 @@ __global__ __launch_bounds__(256) void swa_fwd_kernel(
   const int col = lane & 31, h = lane >> 5;
   const int q0 = Q0 + wave * 32, qi = q0 + col;
   const size_t base = (size_t)bh * L * d;
+  const size_t kvbase = (size_t)(bh / KG) * L * d;   // k, v: the kv head (KG query heads share one)
   const bool vec = VEC || (d & 7) == 0;
 
   bf16x8 qreg[DP / 16];
@@ -122,16 +123,16 @@ __global__ __launch_bounds__(256) void swa_fwd_kernel(
   const int klo = (max(0, Q0 - W + 1) / SWA_TILE) * SWA_TILE;
   const int khi = min(L, Q0 + SWA_ROWS);
   uint4 rk[Cfg::NL], rv[Cfg::NL];
-  swa_load<DP>(rk, k + base, klo, L, d, vec);
-  swa_load<DP>(rv, v + base, klo, L, d, vec);
+  swa_load<DP>(rk, k + kvbase, klo, L, d, vec);
+  swa_load<DP>(rv, v + kvbase, klo, L, d, vec);
   swa_store<DP>(rk, k_l);
   swa_store<DP>(rv, v_l);
   __syncthreads();
   for (int t0 = klo; t0 < khi; t0 += SWA_TILE) {
     const bool more = t0 + SWA_TILE < khi;
     if (more) {
-      swa_load<DP>(rk, k + base, t0 + SWA_TILE, L, d, vec);
-      swa_load<DP>(rv, v + base, t0 + SWA_TILE, L, d, vec);
+      swa_load<DP>(rk, k + kvbase, t0 + SWA_TILE, L, d, vec);
+      swa_load<DP>(rv, v + kvbase, t0 + SWA_TILE, L, d, vec);
     }
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
@@ -193,7 +194,7 @@ __global__ __launch_bounds__(256) void swa_bwd_dq_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ meta, int n_meta, const float* __restrict__ lse,
     const bf16* __restrict__ dy, OutT* __restrict__ dq, float* __restrict__ delta_out,
-    float* __restrict__ dmeta_part, int BH, int L, int d, int W, float scale, int per) {
+    float* __restrict__ dmeta_part, int BH, int L, int d, int W, float scale, int per, int KG) {
   using Cfg = SwaCfg<DP>;
   constexpr int P = Cfg::P;
   extern __shared__ __align__(16) char smem[];
@@ -209,6 +210,7 @@ __global__ __launch_bounds__(256) void swa_bwd_dq_kernel(
   const int col = lane & 31, h = lane >> 5;
   const int q0 = Q0 + wave * 32, qi = q0 + col;
   const size_t base = (size_t)bh * L * d;
+  const size_t kvbase = (size_t)(bh / KG) * L * d;   // k, v: the kv head (KG query heads share one)
   const bool vec = VEC || (d & 7) == 0;
 
   bf16x8 qreg[DP / 16], dyreg[DP / 16];
@@ -226,8 +228,8 @@ __global__ __launch_bounds__(256) void swa_bwd_dq_kernel(
   uint4 rk[Cfg::NL], rv[Cfg::NL];
   // pass 0 accumulates delta = sum_t p dp; pass 1 forms ds and dq
   for (int pass = 0; pass < 2; ++pass) {
-    swa_load<DP>(rk, k + base, klo, L, d, vec);
-    swa_load<DP>(rv, v + base, klo, L, d, vec);
+    swa_load<DP>(rk, k + kvbase, klo, L, d, vec);
+    swa_load<DP>(rv, v + kvbase, klo, L, d, vec);
     __syncthreads();
     swa_store<DP>(rk, k_l);
     swa_store<DP>(rv, v_l);
@@ -235,8 +237,8 @@ __global__ __launch_bounds__(256) void swa_bwd_dq_kernel(
     for (int t0 = klo; t0 < khi; t0 += SWA_TILE) {
       const bool more = t0 + SWA_TILE < khi;
       if (more) {
-        swa_load<DP>(rk, k + base, t0 + SWA_TILE, L, d, vec);
-        swa_load<DP>(rv, v + base, t0 + SWA_TILE, L, d, vec);
+        swa_load<DP>(rk, k + kvbase, t0 + SWA_TILE, L, d, vec);
+        swa_load<DP>(rv, v + kvbase, t0 + SWA_TILE, L, d, vec);
       }
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
@@ -305,7 +307,7 @@ __global__ __launch_bounds__(256) void swa_bwd_dkv_kernel(
     const float* __restrict__ lse, const float* __restrict__ delta_in,
     const bf16* __restrict__ dy, OutT* __restrict__ dk, OutT* __restrict__ dv,
     const float* __restrict__ dmeta_part, float* __restrict__ dmeta, int n_meta, int BH, int L,
-    int d, int W, float scale, int per) {
+    int d, int W, float scale, int per, int KG) {
   using Cfg = SwaCfg<DP>;
   constexpr int P = Cfg::P;
   extern __shared__ __align__(16) char smem[];
@@ -341,11 +343,12 @@ __global__ __launch_bounds__(256) void swa_bwd_dkv_kernel(
   const int col = lane & 31, h = lane >> 5;
   const int k0 = K0 + wave * 32, ti = k0 + col;
   const size_t base = (size_t)bh * L * d, lbase = (size_t)bh * L;
+  const size_t kvbase = (size_t)(bh / KG) * L * d;   // k, v: the kv head (KG query heads share one)
   const bool vec = VEC || (d & 7) == 0;
 
   bf16x8 kreg[DP / 16], vreg[DP / 16];
-  own_rows<DP>(k + base, ti, L, d, h, vec, kreg);
-  own_rows<DP>(v + base, ti, L, d, h, vec, vreg);
+  own_rows<DP>(k + kvbase, ti, L, d, h, vec, kreg);
+  own_rows<DP>(v + kvbase, ti, L, d, h, vec, vreg);
   f32x16 dka[DP / 32], dva[DP / 32];
 #pragma unroll
   for (int t = 0; t < DP / 32; ++t) {
@@ -443,7 +446,7 @@ int swa_row_blocks(int L) { return (L + SWA_ROWS - 1) / SWA_ROWS; }
 template <int DP, bool VEC>
 static hipError_t launch_swa_fwd_t(const void* q, const void* k, const void* v, const float* meta,
                                    int n_meta, void* y, float* lse, int BH, int L, int d, int W,
-                                   float scale, hipStream_t st) {
+                                   float scale, int KG, hipStream_t st) {
   const size_t lds = 2 * SwaCfg<DP>::TILE_BYTES;
   auto kern = swa_fwd_kernel<DP, VEC>;
   hipError_t e = ensure_lds<swa_fwd_kernel<DP, VEC>>((int)lds);
@@ -451,7 +454,7 @@ static hipError_t launch_swa_fwd_t(const void* q, const void* k, const void* v, 
   int per, grid;
   swa_grid(BH, L, &per, &grid);
   hipLaunchKernelGGL(kern, dim3(grid), dim3(256), lds, st, (const bf16*)q, (const bf16*)k,
-                     (const bf16*)v, meta, n_meta, (bf16*)y, lse, BH, L, d, W, scale, per);
+                     (const bf16*)v, meta, n_meta, (bf16*)y, lse, BH, L, d, W, scale, per, KG);
   return hipGetLastError();
 }
 
@@ -459,7 +462,7 @@ template <int DP, typename OutT, bool VEC>
 static hipError_t launch_swa_bwd_t(const void* q, const void* k, const void* v, const float* meta,
                                    int n_meta, const float* lse, const void* dy, void* dq,
                                    void* dk, void* dv, float* delta, float* dmeta_part,
-                                   float* dmeta, int BH, int L, int d, int W, float scale,
+                                   float* dmeta, int BH, int L, int d, int W, float scale, int KG,
                                    hipStream_t st) {
   int per, grid;
   swa_grid(BH, L, &per, &grid);
@@ -469,26 +472,27 @@ static hipError_t launch_swa_bwd_t(const void* q, const void* k, const void* v, 
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kq, dim3(grid), dim3(256), lds_q, st, (const bf16*)q, (const bf16*)k,
                      (const bf16*)v, meta, n_meta, lse, (const bf16*)dy, (OutT*)dq, delta,
-                     dmeta_part, BH, L, d, W, scale, per);
+                     dmeta_part, BH, L, d, W, scale, per, KG);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   const size_t lds_k = 2 * SwaCfg<DP>::TILE_BYTES + 2 * SWA_TILE * sizeof(float);
   auto kk = swa_bwd_dkv_kernel<DP, OutT, VEC>;
   if ((e = ensure_lds<swa_bwd_dkv_kernel<DP, OutT, VEC>>((int)lds_k)) != hipSuccess) return e;
   hipLaunchKernelGGL(kk, dim3(grid), dim3(256), lds_k, st, (const bf16*)q, (const bf16*)k,
                      (const bf16*)v, lse, (const float*)delta, (const bf16*)dy, (OutT*)dk,
-                     (OutT*)dv, (const float*)dmeta_part, dmeta, n_meta, BH, L, d, W, scale, per);
+                     (OutT*)dv, (const float*)dmeta_part, dmeta, n_meta, BH, L, d, W, scale, per,
+                     KG);
   return hipGetLastError();
 }
 
 hipError_t launch_swa_fwd(const void* q, const void* k, const void* v, const float* meta,
                           int n_meta, void* y, float* lse, int BH, int L, int d, int W,
-                          float scale, hipStream_t st) {
+                          float scale, int KG, hipStream_t st) {
   const bool vec = d % 8 == 0;
 #define LZ_SWA_FWD(DPV)                                                                         \
   return vec ? launch_swa_fwd_t<DPV, true>(q, k, v, meta, n_meta, y, lse, BH, L, d, W, scale,   \
-                                           st)                                                  \
+                                           KG, st)                                              \
              : launch_swa_fwd_t<DPV, false>(q, k, v, meta, n_meta, y, lse, BH, L, d, W, scale,  \
-                                            st)
+                                            KG, st)
   switch (swa_padded_dim(d)) {
     case 32: LZ_SWA_FWD(32);
     case 64: LZ_SWA_FWD(64);
@@ -502,12 +506,12 @@ hipError_t launch_swa_fwd(const void* q, const void* k, const void* v, const flo
 hipError_t launch_swa_bwd(const void* q, const void* k, const void* v, const float* meta,
                           int n_meta, const float* lse, const void* dy, void* dq, void* dk,
                           void* dv, bool grad_bf16, float* delta, float* dmeta_part,
-                          float* dmeta, int BH, int L, int d, int W, float scale,
+                          float* dmeta, int BH, int L, int d, int W, float scale, int KG,
                           hipStream_t st) {
   const bool vec = d % 8 == 0;
 #define LZ_SWA_BWD_V(DPV, OUT, V)                                                               \
   launch_swa_bwd_t<DPV, OUT, V>(q, k, v, meta, n_meta, lse, dy, dq, dk, dv, delta, dmeta_part, \
-                                dmeta, BH, L, d, W, scale, st)
+                                dmeta, BH, L, d, W, scale, KG, st)
 #define LZ_SWA_BWD(DPV)                                                                         \
   return grad_bf16 ? (vec ? LZ_SWA_BWD_V(DPV, bf16, true) : LZ_SWA_BWD_V(DPV, bf16, false))     \
                    : (vec ? LZ_SWA_BWD_V(DPV, float, true) : LZ_SWA_BWD_V(DPV, float, false))

@@ -105,30 +105,33 @@ def gla_forward(fq, fk, v, lg, keep_state=True, chunk=CHUNK):
     """One ``lz_gla_fwd`` launch on bf16 contiguous fq, fk, v and fp32
     contiguous log_gamma; returns (y, state), state being the workspace of
     the states entering each sequence segment, which ``gla_backward`` reuses
-    (None when not kept or not needed)."""
+    (None when not kept or not needed).  fk and v may have fewer heads than
+    fq (a divisor: grouped-query attention, each kv head shared by
+    consecutive query heads)."""
     b, h, length, nf = fq.shape
     nd = v.shape[-1]
-    y = torch.empty_like(v)
+    y = torch.empty(b, h, length, nd, device=v.device, dtype=v.dtype)
     ws = None
     if y.numel():
         lib = _lib.load()
         per_head = int(lg.dim() == 3)
         nbytes = _gla_fwd_ws(b, h, length, nf, nd, per_head, chunk)
         ws = torch.empty(nbytes, dtype=torch.uint8, device=fq.device) if nbytes else None
-        rc = lib.lz_gla_fwd(_ptr(fq), _ptr(fk), _ptr(v), _ptr(lg), _ptr(y), b, h, length,
-                            nf, nd, per_head, chunk, _ptr(ws), nbytes, _stream(fq))
+        rc = lib.lz_gla_fwd(_ptr(fq), _ptr(fk), _ptr(v), _ptr(lg), _ptr(y), b, h, fk.shape[1],
+                            length, nf, nd, per_head, chunk, _ptr(ws), nbytes, _stream(fq))
         _lib.check(rc, "lz_gla_fwd")
     return y, (ws if keep_state else None)
 
 
 def gla_backward(fq, fk, v, lg, dy, state, grad_dtype, chunk=CHUNK):
     """One ``lz_gla_bwd`` launch: (dfq, dfk, dv) in grad_dtype (bf16 or
-    fp32) and dlog_gamma fp32 in log_gamma's layout."""
+    fp32) and dlog_gamma fp32 in log_gamma's layout.  dfk and dv are per
+    query head, also when fk and v have fewer (kv) heads."""
     b, h, length, nf = fq.shape
     nd = v.shape[-1]
     dfq = torch.empty(fq.shape, device=fq.device, dtype=grad_dtype)
     dfk = torch.empty_like(dfq)
-    dv = torch.empty(v.shape, device=v.device, dtype=grad_dtype)
+    dv = torch.empty(b, h, length, nd, device=v.device, dtype=grad_dtype)
     dlg = torch.empty_like(lg)
     if dy.numel():
         lib = _lib.load()
@@ -137,7 +140,7 @@ def gla_backward(fq, fk, v, lg, dy, state, grad_dtype, chunk=CHUNK):
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=fq.device)
         rc = lib.lz_gla_bwd(_ptr(fq), _ptr(fk), _ptr(v), _ptr(lg), _ptr(dy), _ptr(dfq),
                             _ptr(dfk), _ptr(dv), _ptr(dlg), int(grad_dtype == torch.bfloat16),
-                            b, h, length, nf, nd, per_head, chunk, _ptr(state),
+                            b, h, fk.shape[1], length, nf, nd, per_head, chunk, _ptr(state),
                             state.numel() if state is not None else 0, _ptr(ws), ws.numel(),
                             _stream(fq))
         _lib.check(rc, "lz_gla_bwd")
@@ -192,7 +195,8 @@ def gla_prefill(fq, fk, v, log_gamma, chunk=CHUNK):
         nbytes = _gla_fwd_ws(b, h, length, nf, nd, per_head, chunk)
         ws = torch.empty(nbytes, dtype=torch.uint8, device=fq.device) if nbytes else None
         rc = lib.lz_gla_prefill(_ptr(fq), _ptr(fk), _ptr(v), _ptr(lg), _ptr(y), _ptr(state), b, h,
-                                length, nf, nd, per_head, chunk, _ptr(ws), nbytes, _stream(fq))
+                                h, length, nf, nd, per_head, chunk, _ptr(ws), nbytes,
+                                _stream(fq))
         _lib.check(rc, "lz_gla_prefill")
     return y, state
 
@@ -272,20 +276,22 @@ def _check_swa(q, k, v, meta, window, fwd_blocks, bwd_blocks):
 
 def swa_forward(q, k, v, meta, window):
     """One ``lz_swa_fwd`` launch on bf16 contiguous q, k, v and fp32
-    contiguous meta; returns (y, lse)."""
+    contiguous meta; returns (y, lse).  k and v may have fewer heads than q
+    (a divisor, as in ``gla_forward``)."""
     b, h, length, d = q.shape
-    y = torch.empty_like(v)
+    y = torch.empty_like(q)
     lse = torch.empty(b, h, length, device=v.device, dtype=torch.float32)
     if y.numel():
         rc = _lib.load().lz_swa_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(meta), meta.numel(),
-                                    _ptr(y), _ptr(lse), b, h, length, d, window,
+                                    _ptr(y), _ptr(lse), b, h, k.shape[1], length, d, window,
                                     1.0 / math.sqrt(d), _stream(q))
         _lib.check(rc, "lz_swa_fwd")
     return y, lse
 
 
 def swa_backward(q, k, v, meta, lse, dy, window, grad_dtype):
-    """One ``lz_swa_bwd`` launch: (dq, dk, dv) in grad_dtype, dmeta fp32."""
+    """One ``lz_swa_bwd`` launch: (dq, dk, dv) in grad_dtype, dmeta fp32;
+    dk and dv per query head, also when k and v have fewer (kv) heads."""
     b, h, length, d = q.shape
     dq = torch.empty(q.shape, device=q.device, dtype=grad_dtype)
     dk = torch.empty_like(dq)
@@ -298,7 +304,7 @@ def swa_backward(q, k, v, meta, lse, dy, window, grad_dtype):
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
         rc = lib.lz_swa_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(meta), n_meta,
                             _ptr(lse), _ptr(dy), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dmeta),
-                            int(grad_dtype == torch.bfloat16), b, h, length, d, window,
+                            int(grad_dtype == torch.bfloat16), b, h, k.shape[1], length, d, window,
                             1.0 / math.sqrt(d), _ptr(ws), ws.numel(), _stream(q))
         _lib.check(rc, "lz_swa_bwd")
     else:

@@ -71,9 +71,11 @@ def _tables(cos, sin, batch, length, head_dim, dtype):
 def prologue_forward(qp, kp, vp, wq, wk, cos, sin, heads, kv_heads):
     """One ``lz_layer_prologue_fwd`` launch: the q/k/v projection outputs
     ([B, L, heads * hd], [B, L, kv_heads * hd]) and phi weights ([f, hd]) to
-    the bf16 kernel operands fq, fk ([B, H, L, 2f]) and qr, kr, v
-    ([B, H, L, hd]).  Returns those five and the tuple ``prologue_backward``
-    needs."""
+    the bf16 kernel operands fq ([B, heads, L, 2f]), qr ([B, heads, L, hd]),
+    fk ([B, kv_heads, L, 2f]) and kr, v ([B, kv_heads, L, hd]): the key side
+    stays per kv head, and the GLA and SWA kernels read each query head's
+    from its kv head (the reference's repeat_interleave, not materialised).
+    Returns those five and the tuple ``prologue_backward`` needs."""
     b, length, _ = qp.shape
     hd = qp.shape[-1] // heads
     f = wq.shape[0]
@@ -85,9 +87,10 @@ def prologue_forward(qp, kp, vp, wq, wk, cos, sin, heads, kv_heads):
     cos, sin, batched = _tables(cos, sin, b, length, hd, dtype)
     dev = qp.device
     fq = torch.empty(b, heads, length, 2 * f, device=dev, dtype=torch.bfloat16)
-    fk = torch.empty_like(fq)
+    fk = torch.empty(b, kv_heads, length, 2 * f, device=dev, dtype=torch.bfloat16)
     qr = torch.empty(b, heads, length, hd, device=dev, dtype=torch.bfloat16)
-    kr, v = torch.empty_like(qr), torch.empty_like(qr)
+    kr = torch.empty(b, kv_heads, length, hd, device=dev, dtype=torch.bfloat16)
+    v = torch.empty_like(kr)
     rc = _lib.load().lz_layer_prologue_fwd(
         qp.data_ptr(), kp.data_ptr(), vp.data_ptr(), wq.data_ptr(), wk.data_ptr(),
         cos.data_ptr(), sin.data_ptr(), batched, fq.data_ptr(), fk.data_ptr(), qr.data_ptr(),

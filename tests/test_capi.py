@@ -43,29 +43,34 @@ def test_abi_version_and_error_string(lib):
 
 
 def test_null_pointers_are_rejected_with_a_message(lib):
-    rc = lib.lz_gla_fwd(None, None, None, None, None, 1, 1, 8, 16, 16, 0, 64, None, 0, None)
+    rc = lib.lz_gla_fwd(None, None, None, None, None, 1, 1, 1, 8, 16, 16, 0, 64, None, 0, None)
     assert rc != 0 and b"null" in lib.lz_last_error()
-    rc = lib.lz_swa_fwd(None, None, None, None, 0, None, None, 1, 1, 8, 16, 4, 0.25, None)
+    rc = lib.lz_swa_fwd(None, None, None, None, 0, None, None, 1, 1, 1, 8, 16, 4, 0.25, None)
     assert rc != 0 and b"null" in lib.lz_last_error()
 
 
 def test_bad_sizes_are_rejected_before_any_launch(lib):
     p = ctypes.c_void_p(16)   # never dereferenced: validation fails first
-    rc = lib.lz_gla_fwd(p, p, p, p, p, 1, 1, 8, 300, 16, 0, 64, None, 0, None)
+    rc = lib.lz_gla_fwd(p, p, p, p, p, 1, 1, 1, 8, 300, 16, 0, 64, None, 0, None)
     assert rc != 0 and b"unsupported" in lib.lz_last_error()
-    rc = lib.lz_gla_fwd(p, p, p, p, p, 1, 1, 8, 16, 16, 0, 48, None, 0, None)
+    rc = lib.lz_gla_fwd(p, p, p, p, p, 1, 1, 1, 8, 16, 16, 0, 48, None, 0, None)
     assert rc != 0 and b"chunk" in lib.lz_last_error()
-    rc = lib.lz_swa_fwd(p, p, p, p, 65, p, p, 1, 1, 8, 16, 4, 0.25, None)
+    rc = lib.lz_swa_fwd(p, p, p, p, 65, p, p, 1, 1, 1, 8, 16, 4, 0.25, None)
     assert rc != 0 and b"n_meta" in lib.lz_last_error()
-    rc = lib.lz_swa_fwd(p, p, p, p, 0, p, p, 1, 1, 8, 512, 4, 0.25, None)
+    rc = lib.lz_swa_fwd(p, p, p, p, 0, p, p, 1, 1, 1, 8, 512, 4, 0.25, None)
     assert rc != 0 and b"dim" in lib.lz_last_error()
-    rc = lib.lz_swa_fwd(p, p, p, p, 0, p, p, 1, 1, 8, 16, 0, 0.25, None)
+    rc = lib.lz_swa_fwd(p, p, p, p, 0, p, p, 1, 1, 1, 8, 16, 0, 0.25, None)
     assert rc != 0 and b"window" in lib.lz_last_error()
     ws = lib.lz_gla_bwd_workspace_bytes(2, 3, 100, 24, 20, 0, 64)
     assert ws > 0
-    rc = lib.lz_gla_bwd(p, p, p, p, p, p, p, p, p, 0, 2, 3, 100, 24, 20, 0, 64, None, 0, p, ws - 1,
-                        None)
+    rc = lib.lz_gla_bwd(p, p, p, p, p, p, p, p, p, 0, 2, 3, 3, 100, 24, 20, 0, 64, None, 0, p,
+                        ws - 1, None)
     assert rc != 0 and b"workspace" in lib.lz_last_error()
+    # kv_heads must divide heads (grouped-query operands)
+    rc = lib.lz_gla_fwd(p, p, p, p, p, 1, 4, 3, 8, 16, 16, 0, 64, None, 0, None)
+    assert rc != 0 and b"kv_heads" in lib.lz_last_error()
+    rc = lib.lz_swa_fwd(p, p, p, p, 0, p, p, 1, 4, 0, 8, 16, 4, 0.25, None)
+    assert rc != 0 and b"kv_heads" in lib.lz_last_error()
 
 
 def test_layer_entry_points_reject_bad_arguments(lib):

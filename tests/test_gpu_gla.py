@@ -159,8 +159,8 @@ def test_gla_backward_without_forward_workspace_is_bitwise_equal():
     n = lib.lz_gla_bwd_workspace_bytes(b, h, length, nf, nd, 0, 64)
     ws = torch.empty(n, dtype=torch.uint8, device="cuda")
     rc = lib.lz_gla_bwd(*(t.data_ptr() for t in ins), dy.data_ptr(), dfq.data_ptr(),
-                        dfk.data_ptr(), dv.data_ptr(), dlg.data_ptr(), 1, b, h, length, nf, nd,
-                        0, 64, None, 0, ws.data_ptr(), n,
+                        dfk.data_ptr(), dv.data_ptr(), dlg.data_ptr(), 1, b, h, h, length, nf,
+                        nd, 0, 64, None, 0, ws.data_ptr(), n,
                         torch.cuda.current_stream().cuda_stream)
     _lib.check(rc, "lz_gla_bwd")
     torch.cuda.synchronize()

@@ -188,7 +188,14 @@ def test_prologue_matches_reference_ops(dtype, b, length, heads, kv, hd, f, batc
     refs = prologue_reference(*theirs, cos.double(), sin.double(), heads, kv)
     ref_ups = [u.double() for u in ups[:4]] + [(ups[4] + ups[5]).double()]
     torch.autograd.backward(refs, ref_ups)
-    pairs = {n: (a, r) for n, a, r in zip(("fq", "fk", "qr", "kr", "v"), outs, refs)}
+    # the key-side operands are written once per kv head: the reference's
+    # repeat_interleave copies them to the heads of each group, so its first
+    # head of every group is the one to compare with
+    group = heads // kv
+    pairs = {n: (a, r if n in ("fq", "qr") else r[:, ::group])
+             for n, a, r in zip(("fq", "fk", "qr", "kr", "v"), outs, refs)}
+    for n in ("fk", "kr", "v"):
+        assert pairs[n][0].shape[1] == kv, n
     for n, a, r in zip(("dq", "dk", "dv", "dwq", "dwk"), grads, theirs):
         pairs[n] = (a, r.grad)
     errs = report(f"prologue {dtype} b={b} L={length} H={heads}/{kv} hd={hd} f={f}", pairs)
