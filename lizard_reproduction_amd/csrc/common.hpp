@@ -140,6 +140,15 @@ __host__ __device__ constexpr int lds_pitch(int x) {
   return x + (x == 64 ? 8 : (x >= 128 ? 24 : 16));
 }
 
+// Workgroups are dispatched round-robin over the GPU's 8 XCDs (each with its
+// own L2): workgroup i runs on XCD i % 8.  xcd_block maps workgroup i to a
+// logical block so that each XCD takes a contiguous range of `per` logical
+// blocks: neighbouring logical blocks (the query heads of one kv head, the
+// row blocks of one (b, h)) share an L2.  Launch xcd_grid(total) workgroups
+// and skip logical blocks past `total`.
+__host__ __device__ constexpr int xcd_grid(int total) { return 8 * ((total + 7) / 8); }
+__device__ __forceinline__ int xcd_block(int i, int per) { return (i & 7) * per + (i >> 3); }
+
 // Exchange with the other half of the wave (lane ^ 32).
 __device__ __forceinline__ float xhalf(float x) { return __shfl_xor(x, 32); }
 

@@ -44,7 +44,6 @@ struct SwaCfg {
 // Logical block id for hardware block id i of a grid of 8 * per blocks: the
 // hardware deals consecutive ids round-robin over the 8 XCDs, this hands each
 // XCD a run of `per` consecutive logical blocks.
-__device__ __forceinline__ int xcd_block(int i, int per) { return (i & 7) * per + (i >> 3); }
 
 // rows [r0, r0+64) of a [L x d] matrix, 16 bytes per load (zero outside it)
 template <int DP>
@@ -436,9 +435,8 @@ int swa_padded_dim(int d) {
 // blocks per (b, h) and the XCD-spread grid for BH * nblk logical blocks
 static void swa_grid(int BH, int L, int* per, int* grid) {
   const int nblk = (L + SWA_ROWS - 1) / SWA_ROWS;
-  const int total = BH * nblk;
-  *per = (total + 7) / 8;
-  *grid = 8 * *per;
+  *grid = xcd_grid(BH * nblk);
+  *per = *grid / 8;
 }
 
 int swa_row_blocks(int L) { return (L + SWA_ROWS - 1) / SWA_ROWS; }
