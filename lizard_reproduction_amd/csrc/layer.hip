@@ -832,7 +832,8 @@ prologue_bwd_kernel(ProBwdArgs a) {
     // dx[m] = dr[m] cos[m] + dr[m + hd/2] sin[m + hd/2] for m < hd/2,
     //         dr[m] cos[m] - dr[m - hd/2] sin[m - hd/2] otherwise (drope summed
     // over the group's heads); the kv rows also sum dv (and dv2) over the group.
-#pragma unroll 1
+    // Two items' loads overlap (unrolled by 2): the Jacobian's registers are free here.
+#pragma unroll 2
     for (int i = 0; i < K::XI; ++i) {
       const int idx = tid + NT * i, r = idx / H8, m0 = 8 * (idx % H8);
       const int row = row0 + r;

@@ -101,6 +101,26 @@ def _check_gla(fq, fk, v, log_gamma, chunk):
     _require_gpu(fq, fk, v, log_gamma)
 
 
+def _check_kv(what, q, k, v, nk, nv):
+    """Shapes of the internal launch wrappers: q [B, H, L, nk]; k [B, Hkv,
+    L, nk] and v [B, Hkv, L, nv] with Hkv dividing H (the kernels index the
+    buffers from these sizes alone)."""
+    b, h, length = q.shape[:3]
+    hk = k.shape[1] if k.dim() == 4 else 0
+    if q.dim() != 4 or q.shape[3] != nk or tuple(k.shape) != (b, hk, length, nk) or \
+            tuple(v.shape) != (b, hk, length, nv) or hk <= 0 or h % hk:
+        raise ValueError(f"{what}: need q [B, H, L, {nk}], k [B, Hkv, L, {nk}], "
+                         f"v [B, Hkv, L, {nv}] with Hkv dividing H; got {tuple(q.shape)}, "
+                         f"{tuple(k.shape)}, {tuple(v.shape)}")
+
+
+def _check_gate(what, fq, lg):
+    b, h, length = fq.shape[:3]
+    if tuple(lg.shape) not in ((b, length), (b, h, length)):
+        raise ValueError(f"{what}: log_gamma must be {(b, length)} or {(b, h, length)}, "
+                         f"got {tuple(lg.shape)}")
+
+
 def gla_forward(fq, fk, v, lg, keep_state=True, chunk=CHUNK):
     """One ``lz_gla_fwd`` launch on bf16 contiguous fq, fk, v and fp32
     contiguous log_gamma; returns (y, state), state being the workspace of
@@ -108,6 +128,8 @@ def gla_forward(fq, fk, v, lg, keep_state=True, chunk=CHUNK):
     (None when not kept or not needed).  fk and v may have fewer heads than
     fq (a divisor: grouped-query attention, each kv head shared by
     consecutive query heads)."""
+    _check_kv("gla_forward", fq, fk, v, fq.shape[-1], v.shape[-1])
+    _check_gate("gla_forward", fq, lg)
     b, h, length, nf = fq.shape
     nd = v.shape[-1]
     y = torch.empty(b, h, length, nd, device=v.device, dtype=v.dtype)
@@ -127,8 +149,12 @@ def gla_backward(fq, fk, v, lg, dy, state, grad_dtype, chunk=CHUNK):
     """One ``lz_gla_bwd`` launch: (dfq, dfk, dv) in grad_dtype (bf16 or
     fp32) and dlog_gamma fp32 in log_gamma's layout.  dfk and dv are per
     query head, also when fk and v have fewer (kv) heads."""
+    _check_kv("gla_backward", fq, fk, v, fq.shape[-1], v.shape[-1])
+    _check_gate("gla_backward", fq, lg)
     b, h, length, nf = fq.shape
     nd = v.shape[-1]
+    if tuple(dy.shape) != (b, h, length, nd):
+        raise ValueError(f"gla_backward: dy must be {(b, h, length, nd)}, got {tuple(dy.shape)}")
     dfq = torch.empty(fq.shape, device=fq.device, dtype=grad_dtype)
     dfk = torch.empty_like(dfq)
     dv = torch.empty(b, h, length, nd, device=v.device, dtype=grad_dtype)
@@ -278,6 +304,7 @@ def swa_forward(q, k, v, meta, window):
     """One ``lz_swa_fwd`` launch on bf16 contiguous q, k, v and fp32
     contiguous meta; returns (y, lse).  k and v may have fewer heads than q
     (a divisor, as in ``gla_forward``)."""
+    _check_kv("swa_forward", q, k, v, q.shape[-1], q.shape[-1])
     b, h, length, d = q.shape
     y = torch.empty_like(q)
     lse = torch.empty(b, h, length, device=v.device, dtype=torch.float32)
@@ -292,7 +319,11 @@ def swa_forward(q, k, v, meta, window):
 def swa_backward(q, k, v, meta, lse, dy, window, grad_dtype):
     """One ``lz_swa_bwd`` launch: (dq, dk, dv) in grad_dtype, dmeta fp32;
     dk and dv per query head, also when k and v have fewer (kv) heads."""
+    _check_kv("swa_backward", q, k, v, q.shape[-1], q.shape[-1])
     b, h, length, d = q.shape
+    if tuple(dy.shape) != tuple(q.shape) or tuple(lse.shape) != (b, h, length):
+        raise ValueError(f"swa_backward: dy must be {tuple(q.shape)} and lse {(b, h, length)}, "
+                         f"got {tuple(dy.shape)} and {tuple(lse.shape)}")
     dq = torch.empty(q.shape, device=q.device, dtype=grad_dtype)
     dk = torch.empty_like(dq)
     dv = torch.empty_like(dq)

@@ -76,9 +76,19 @@ def prologue_forward(qp, kp, vp, wq, wk, cos, sin, heads, kv_heads):
     stays per kv head, and the GLA and SWA kernels read each query head's
     from its kv head (the reference's repeat_interleave, not materialised).
     Returns those five and the tuple ``prologue_backward`` needs."""
+    if qp.dim() != 3 or heads <= 0 or kv_heads <= 0 or heads % kv_heads or \
+            qp.shape[-1] % heads:
+        raise ValueError(f"prologue_forward: q must be [B, L, heads * head_dim] with kv_heads "
+                         f"dividing heads; got {tuple(qp.shape)}, heads={heads}, "
+                         f"kv_heads={kv_heads}")
     b, length, _ = qp.shape
     hd = qp.shape[-1] // heads
     f = wq.shape[0]
+    for name, t, shape in (("k", kp, (b, length, kv_heads * hd)),
+                           ("v", vp, (b, length, kv_heads * hd)),
+                           ("wq", wq, (f, hd)), ("wk", wk, (f, hd))):
+        if tuple(t.shape) != shape:
+            raise ValueError(f"prologue_forward: {name} must be {shape}, got {tuple(t.shape)}")
     # bf16 arithmetic inputs only when every input is bf16; otherwise all are
     # widened to fp32 (exactly), as the reference promotes them
     dtype = torch.bfloat16 if all(t.dtype == torch.bfloat16
@@ -107,6 +117,13 @@ def prologue_backward(saved, dfq, dfk, dqr, dkr, dv, dv2=None):
     fp32); returns dq, dk, dv of the projection outputs (in the arithmetic
     dtype) and dWq, dWk (fp32)."""
     qp, kp, wq, wk, cos, sin, (b, length, heads, kv, hd, f, batched) = saved
+    # every gradient is per query head (the kernels' gradients of the k-side
+    # operands are each query head's share; the kernel sums them per group)
+    for name, g, n in (("dfq", dfq, 2 * f), ("dfk", dfk, 2 * f), ("dqr", dqr, hd),
+                       ("dkr", dkr, hd), ("dv", dv, hd), ("dv2", dv2, hd)):
+        if g is not None and tuple(g.shape) != (b, heads, length, n):
+            raise ValueError(f"prologue_backward: {name} must be {(b, heads, length, n)}, got "
+                             f"{tuple(g.shape)}")
     grads = [None if g is None else g.to(torch.bfloat16).contiguous()
              for g in (dfq, dfk, dqr, dkr, dv, dv2)]
     dq, dk, dvp = torch.empty_like(qp), torch.empty_like(kp), torch.empty_like(kp)

@@ -195,3 +195,31 @@ def test_product_never_imports_the_oracle():
             if f.endswith((".py", ".hip", ".hpp", ".cpp")):
                 text = open(os.path.join(dirpath, f)).read()
                 assert not re.search(r"^\s*(from|import)\s+oracle", text, re.M), f
+
+
+def test_internal_wrappers_reject_mismatched_shapes_before_any_launch():
+    """The launch wrappers below the operator API (used by the layer) take
+    k-side operands with fewer heads; a shape they cannot index is refused
+    with ValueError before anything reaches the GPU."""
+    from lizard_reproduction_amd import layer
+    q = torch.zeros(1, 4, 8, 16)
+    k2, v2 = torch.zeros(1, 2, 8, 16), torch.zeros(1, 2, 8, 16)
+    with pytest.raises(ValueError, match="Hkv dividing H"):
+        kernels.gla_forward(q, torch.zeros(1, 3, 8, 16), v2, torch.zeros(1, 8))
+    with pytest.raises(ValueError, match="Hkv dividing H"):
+        kernels.swa_forward(q, k2, torch.zeros(1, 2, 9, 16), torch.zeros(4), 4)
+    with pytest.raises(ValueError, match="log_gamma"):
+        kernels.gla_forward(q, k2, v2, torch.zeros(1, 2, 8))
+    with pytest.raises(ValueError, match="dy must be"):
+        kernels.gla_backward(q, k2, v2, torch.zeros(1, 8), torch.zeros(1, 2, 8, 16), None,
+                             torch.bfloat16)
+    # the prologue backward wants per-query-head gradients of the k-side operands
+    saved = (None,) * 6 + ((1, 8, 4, 2, 32, 8, 0),)
+    per_q = [torch.zeros(1, 4, 8, n) for n in (16, 16, 32, 32, 32)]
+    with pytest.raises(ValueError, match="dfk must be"):
+        layer.prologue_backward(saved, per_q[0], torch.zeros(1, 2, 8, 16), *per_q[2:])
+    with pytest.raises(ValueError, match="dv must be"):
+        layer.prologue_backward(saved, *per_q[:4], torch.zeros(1, 2, 8, 32))
+    with pytest.raises(ValueError, match="k must be"):
+        layer.prologue_forward(torch.zeros(1, 8, 128), torch.zeros(1, 8, 32), torch.zeros(1, 8, 64),
+                               torch.zeros(8, 32), torch.zeros(8, 32), None, None, 4, 2)
