@@ -222,9 +222,36 @@ def layer_stack(torch, steps, warmup, one_layer=False):
     with torch.no_grad():
         out["one_layer_fwd_ms"] = round(median_ms(torch, lambda: layer(xg, rope), 5, 2), 3)
     out["one_layer_fwd_bwd_ms"] = round(median_ms(torch, layer_step, 5, 2, layer_reset), 3)
-    del layer, xg, gy, rope, rotary
-    torch.cuda.empty_cache()
     print(f"[bench] config5 one layer: {out}", file=sys.stderr, flush=True)
+
+    # layer-level decode: prefill the 4096-token prompts, then one token per
+    # sequence through LizardAttention.step (projections, one-token prologue,
+    # GLA and SWA decode kernels, blend, o_proj); and the SWA decode kernel
+    # alone, 64 back-to-back C-ABI calls between two HIP events
+    lib = _lib.load()
+    with torch.no_grad():
+        out["layer_prefill_ms"] = round(median_ms(torch, lambda: layer.prefill(x, rope), 5, 2), 3)
+        _, cache = layer.prefill(x, rope)
+        x1 = torch.randn(batch, 1, 2048, device="cuda", dtype=torch.bfloat16)
+        rope1 = rotary(x1, torch.full((batch, 1), length, device="cuda"))
+        out["layer_decode_step_ms"] = round(
+            median_ms(torch, lambda: layer.step(x1, rope1, cache), 20, 5), 4)
+        q1 = torch.randn(batch, 32, 64, device="cuda").bfloat16()
+        ys1 = torch.empty_like(q1)
+        meta = layer.meta_tokens.detach().float().contiguous()
+        sargs = [q1.data_ptr(), cache.k.data_ptr(), cache.v.data_ptr(), meta.data_ptr(), 4,
+                 ys1.data_ptr(), batch, 32, 8, opts["window"], 64, length, 0.125,
+                 torch.cuda.current_stream().cuda_stream]
+
+        def sdec64():
+            for _ in range(64):
+                lib.lz_swa_decode_step(*sargs)
+        out["swa_decode_step_us"] = round(median_ms(torch, sdec64, 5, 2) / 64 * 1e3, 2)
+    del layer, xg, gy, rope, rotary, cache, x1, rope1, q1, ys1
+    torch.cuda.empty_cache()
+    print(f"[bench] config5 layer decode: prefill {out['layer_prefill_ms']} ms, step "
+          f"{out['layer_decode_step_ms']} ms, SWA decode kernel {out['swa_decode_step_us']} us",
+          file=sys.stderr, flush=True)
     if one_layer:
         return out
 
@@ -244,9 +271,8 @@ def layer_stack(torch, steps, warmup, one_layer=False):
     tok = [t[:, :, -1].contiguous() for t in (fq, fk, v)]
     lg1 = lg[:, -1].contiguous()
     y1 = torch.empty_like(tok[2])
-    lib = _lib.load()
     args = [t.data_ptr() for t in tok] + [lg1.data_ptr(), state.data_ptr(), y1.data_ptr(),
-                                          batch, 32, 256, 64, 0,
+                                          batch, 32, 32, 256, 64, 0,
                                           torch.cuda.current_stream().cuda_stream]
 
     def dec64():

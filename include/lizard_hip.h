@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define LZ_ABI_VERSION 8
+#define LZ_ABI_VERSION 9
 
 /* ABI version of the loaded library (LZ_ABI_VERSION). */
 int lz_abi_version(void);
@@ -85,12 +85,13 @@ int lz_gla_prefill(const void* fq, const void* fk, const void* v, const float* l
  * GLA decode step: one new token per (b, h) on the recurrent form
  * (tests/test_lizard.py:41-52), state updated in place:
  *   S <- gamma S + fk v^T,  z <- gamma z + fk,  y = fq S / max(fq . z, FLT_MIN)
- *   fq, fk  bf16 [B, H, nf];  v  bf16 [B, H, nd];  y  bf16 [B, H, nd]
+ *   fq  bf16 [B, H, nf];  fk  bf16 [B, kv_heads, nf];  v  bf16 [B, kv_heads, nd]
+ *   (query head h reads kv head h / (heads / kv_heads));  y  bf16 [B, H, nd]
  *   log_gamma  f32 [B] (gate_per_head = 0) or [B, H];  gamma = exp(log_gamma)
  *   state  f32 [B, H, nf*nd + nf] as written by lz_gla_prefill (zeros: empty prefix)
  */
 int lz_gla_decode_step(const void* fq, const void* fk, const void* v, const float* log_gamma,
-                       float* state, void* y, int batch, int heads, int nf, int nd,
+                       float* state, void* y, int batch, int heads, int kv_heads, int nf, int nd,
                        int gate_per_head, void* stream);
 
 /* Workspace bytes lz_gla_bwd needs for these sizes. */
@@ -132,6 +133,22 @@ int lz_gla_bwd(const void* fq, const void* fk, const void* v, const float* log_g
 int lz_swa_fwd(const void* q, const void* k, const void* v, const float* meta, int n_meta,
                void* y, float* lse, int batch, int heads, int kv_heads, int length, int dim,
                int window, float scale, void* stream);
+
+/*
+ * SWA decode step: the forward's output row for one new query per (b, h), at
+ * absolute position pos, against a ring-buffered window cache.  No counterpart
+ * in the reference (it has no decode path); the row is that of _swa_fwd
+ * (src/kernels/swa.py:19-59) at i = pos:
+ *   q         bf16 [B, H, dim]  (RoPE at position pos applied)
+ *   k_cache, v_cache  bf16 [B, kv_heads, window, dim]; position p (RoPE applied
+ *             to k) in slot p % window; the caller writes position pos there
+ *             first, so slots of positions max(0, pos-window+1) .. pos are read
+ *   meta      f32 [n_meta] sink logits;  y  bf16 [B, H, dim]
+ *   window    at most 8192;  dim <= 256;  pos >= 0
+ */
+int lz_swa_decode_step(const void* q, const void* k_cache, const void* v_cache,
+                       const float* meta, int n_meta, void* y, int batch, int heads, int kv_heads,
+                       int window, int dim, int pos, float scale, void* stream);
 
 /* Workspace bytes lz_swa_bwd needs for these sizes. */
 size_t lz_swa_bwd_workspace_bytes(int batch, int heads, int length, int dim, int n_meta);

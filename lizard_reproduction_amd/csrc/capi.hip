@@ -14,7 +14,7 @@ hipError_t launch_gla_fwd(const void* fq, const void* fk, const void* v, const f
                           float* final_state, hipStream_t st);
 hipError_t launch_gla_decode(const void* fq, const void* fk, const void* v, const float* lg,
                              float* state, void* y, int B, int H, int F, int D,
-                             int gate_per_head, hipStream_t st);
+                             int gate_per_head, int KG, hipStream_t st);
 size_t gla_fwd_workspace(int B, int H, int L, int F, int D);
 hipError_t launch_gla_bwd(const void* fq, const void* fk, const void* v, const float* lg,
                           const void* dy, void* dfq, void* dfk, void* dv, float* dlg,
@@ -27,6 +27,10 @@ int swa_row_blocks(int L);
 hipError_t launch_swa_fwd(const void* q, const void* k, const void* v, const float* meta,
                           int n_meta, void* y, float* lse, int BH, int L, int d, int W,
                           float scale, int KG, hipStream_t st);
+constexpr int SWA_DEC_MAX_W = 8192;
+hipError_t launch_swa_decode(const void* q, const void* k_cache, const void* v_cache,
+                             const float* meta, int n_meta, void* y, int BH, int W, int d,
+                             int pos, float scale, int KG, hipStream_t st);
 hipError_t launch_swa_bwd(const void* q, const void* k, const void* v, const float* meta,
                           int n_meta, const float* lse, const void* dy, void* dq, void* dk,
                           void* dv, bool grad_bf16, float* delta, float* dmeta_part,
@@ -145,11 +149,14 @@ extern "C" int lz_gla_prefill(const void* fq, const void* fk, const void* v,
 
 extern "C" int lz_gla_decode_step(const void* fq, const void* fk, const void* v,
                                   const float* log_gamma, float* state, void* y, int batch,
-                                  int heads, int nf, int nd, int gate_per_head, void* stream) {
+                                  int heads, int kv_heads, int nf, int nd, int gate_per_head,
+                                  void* stream) {
   if (int rc = check_gla(fq, fk, v, log_gamma, batch, heads, 1, nf, nd, 64)) return rc;
+  if (int rc = check_kv_heads("gla_decode_step", heads, kv_heads)) return rc;
   if (!state || !y) return fail(1, "gla_decode_step: null state or output pointer");
   return hip_status(lz::launch_gla_decode(fq, fk, v, log_gamma, state, y, batch, heads, nf, nd,
-                                          gate_per_head ? 1 : 0, (hipStream_t)stream),
+                                          gate_per_head ? 1 : 0, heads / kv_heads,
+                                          (hipStream_t)stream),
                     "gla_decode_step");
 }
 
@@ -211,6 +218,23 @@ extern "C" int lz_swa_fwd(const void* q, const void* k, const void* v, const flo
   return hip_status(lz::launch_swa_fwd(q, k, v, meta, n_meta, y, lse, batch * heads, length, dim,
                                        window, scale, heads / kv_heads, (hipStream_t)stream),
                     "swa_fwd");
+}
+
+extern "C" int lz_swa_decode_step(const void* q, const void* k_cache, const void* v_cache,
+                                  const float* meta, int n_meta, void* y, int batch, int heads,
+                                  int kv_heads, int window, int dim, int pos, float scale,
+                                  void* stream) {
+  if (int rc = check_swa(q, k_cache, v_cache, meta, n_meta, batch, heads, 1, dim, window))
+    return rc;
+  if (int rc = check_kv_heads("swa_decode_step", heads, kv_heads)) return rc;
+  if (!y) return fail(1, "swa_decode_step: null output pointer");
+  if (window > lz::SWA_DEC_MAX_W)
+    return fail(1, "swa_decode_step: window %d > %d unsupported", window, lz::SWA_DEC_MAX_W);
+  if (pos < 0) return fail(1, "swa_decode_step: pos must be >= 0, got %d", pos);
+  return hip_status(lz::launch_swa_decode(q, k_cache, v_cache, meta, n_meta, y, batch * heads,
+                                          window, dim, pos, scale, heads / kv_heads,
+                                          (hipStream_t)stream),
+                    "swa_decode_step");
 }
 
 extern "C" size_t lz_swa_bwd_workspace_bytes(int batch, int heads, int length, int dim,

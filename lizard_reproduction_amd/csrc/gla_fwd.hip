@@ -274,7 +274,8 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
 // decode step: one token per (b, h) on the recurrent form
 //   S <- gamma S + fk v^T,  z <- gamma z + fk,  y = fq S / max(fq . z, FLT_MIN)
 // (tests/test_lizard.py:41-52 of the reference), state [F][D] fp32 then z [F]
-// per (b, h), updated in place.  Thread (g, d) of the 256 walks features
+// per (b, h), updated in place; fk and v of query head bh are row bh / KG
+// (its kv head).  Thread (g, d) of the 256 walks features
 // f = g, g + NG, ... of column d (NG = 256 / DP groups); the fq . S_new partial
 // sums of the groups meet in LDS.
 // ----------------------------------------------------------------------------
@@ -282,14 +283,14 @@ template <int DP>
 __global__ __launch_bounds__(256) void gla_decode_kernel(
     const bf16* __restrict__ fq, const bf16* __restrict__ fk, const bf16* __restrict__ v,
     const float* __restrict__ log_gamma, float* __restrict__ state, bf16* __restrict__ y, int H,
-    int F, int D, int gate_per_head) {
+    int F, int D, int gate_per_head, int KG) {
   constexpr int NG = 256 / DP;
   __shared__ float fq_s[256], fk_s[256], part[256], red[4];
   const int bh = blockIdx.x, tid = threadIdx.x;
   const int g = tid / DP, d = tid % DP;
   const float gam = fexp(log_gamma[gate_per_head ? bh : bh / H]);
   const bf16* fqb = fq + (size_t)bh * F;
-  const bf16* fkb = fk + (size_t)bh * F;
+  const bf16* fkb = fk + (size_t)(bh / KG) * F;
   float* Sb = state + (size_t)bh * ((size_t)F * D + F);
   float* zb = Sb + (size_t)F * D;
   for (int f = tid; f < F; f += 256) {
@@ -310,7 +311,7 @@ __global__ __launch_bounds__(256) void gla_decode_kernel(
   // S and fq . S
   float num = 0.f;
   if (d < D) {
-    const float vd = to_f32(v[(size_t)bh * D + d]);
+    const float vd = to_f32(v[(size_t)(bh / KG) * D + d]);
     for (int f = g; f < F; f += NG) {
       const float sn = gam * Sb[(size_t)f * D + d] + fk_s[f] * vd;
       Sb[(size_t)f * D + d] = sn;
@@ -340,7 +341,7 @@ template <int IPT>
 __global__ __launch_bounds__(512) void gla_decode_vec_kernel(
     const bf16* __restrict__ fq, const bf16* __restrict__ fk, const bf16* __restrict__ v,
     const float* __restrict__ log_gamma, float* __restrict__ state, bf16* __restrict__ y, int H,
-    int F, int D, int gate_per_head) {
+    int F, int D, int gate_per_head, int KG) {
   __shared__ float fq_s[256], fk_s[256], red[8];
   __shared__ f32x4 part[8 * 32];
   const int bh = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -359,9 +360,9 @@ __global__ __launch_bounds__(512) void gla_decode_vec_kernel(
   const float gam = fexp(log_gamma[gate_per_head ? bh : bh / H]);
   for (int f = tid; f < F; f += 512) {
     fq_s[f] = to_f32(fq[(size_t)bh * F + f]);
-    fk_s[f] = to_f32(fk[(size_t)bh * F + f]);
+    fk_s[f] = to_f32(fk[(size_t)(bh / KG) * F + f]);
   }
-  const bf16x4 v4 = *reinterpret_cast<const bf16x4*>(v + (size_t)bh * D + 4 * q);
+  const bf16x4 v4 = *reinterpret_cast<const bf16x4*>(v + (size_t)(bh / KG) * D + 4 * q);
   __syncthreads();
   float qz = 0.f;
   for (int f = tid; f < F; f += 512) {
@@ -409,14 +410,14 @@ __global__ __launch_bounds__(512) void gla_decode_vec_kernel(
 
 hipError_t launch_gla_decode(const void* fq, const void* fk, const void* v, const float* lg,
                              float* state, void* y, int B, int H, int F, int D,
-                             int gate_per_head, hipStream_t st) {
+                             int gate_per_head, int KG, hipStream_t st) {
   if (F % 4 == 0 && D >= 4 && D <= 128 && (D & (D - 1)) == 0) {
     const int rg = 512 / (D / 4), need = (F + rg - 1) / rg;   // rows per thread
 #define LZ_GLA_DECV(IPTV)                                                                     \
     if (need <= IPTV) {                                                                       \
       hipLaunchKernelGGL(gla_decode_vec_kernel<IPTV>, dim3(B * H), dim3(512), 0, st,          \
                          (const bf16*)fq, (const bf16*)fk, (const bf16*)v, lg, state,         \
-                         (bf16*)y, H, F, D, gate_per_head);                                   \
+                         (bf16*)y, H, F, D, gate_per_head, KG);                               \
       return hipGetLastError();                                                               \
     }
     LZ_GLA_DECV(1) LZ_GLA_DECV(2) LZ_GLA_DECV(4) LZ_GLA_DECV(8)
@@ -427,7 +428,7 @@ hipError_t launch_gla_decode(const void* fq, const void* fk, const void* v, cons
   if (dp == DPV) {                                                                          \
     hipLaunchKernelGGL(gla_decode_kernel<DPV>, dim3(B * H), dim3(256), 0, st,                 \
                        (const bf16*)fq, (const bf16*)fk, (const bf16*)v, lg, state, (bf16*)y, \
-                       H, F, D, gate_per_head);                                               \
+                       H, F, D, gate_per_head, KG);                                           \
     return hipGetLastError();                                                               \
   }
   LZ_GLA_DEC(32) LZ_GLA_DEC(64) LZ_GLA_DEC(128) LZ_GLA_DEC(256)

@@ -41,9 +41,6 @@ struct SwaCfg {
   static constexpr int TILE_BYTES = SWA_TILE * P * 2;
 };
 
-// Logical block id for hardware block id i of a grid of 8 * per blocks: the
-// hardware deals consecutive ids round-robin over the 8 XCDs, this hands each
-// XCD a run of `per` consecutive logical blocks.
 
 // rows [r0, r0+64) of a [L x d] matrix, 16 bytes per load (zero outside it)
 template <int DP>
@@ -522,6 +519,121 @@ hipError_t launch_swa_bwd(const void* q, const void* k, const void* v, const flo
   }
 #undef LZ_SWA_BWD
 #undef LZ_SWA_BWD_V
+}
+
+// ----------------------------------------------------------------------------
+// decode step: one new query per (b, h) against a ring-buffered window cache
+//   keys/values of absolute positions pos - n + 1 .. pos, n = min(pos + 1, W),
+//   position p in slot p % W of k_cache, v_cache [B*Hkv, W, d] (the caller
+//   has written position pos there);
+//   y = sum_p e^{s_p - m} v_p / (sum_j e^{meta_j - m} + sum_p e^{s_p - m}),
+//   s_p = scale q . k_p, m = max(max_p s_p, max_j meta_j) -- the forward's
+//   row at position pos (src/kernels/swa.py:19-59), with e^{s_p - m} rounded to
+//   bf16 before it weights v, as the forward's P is.
+// One workgroup per (b, h): thread t scores keys t, t + 256, ... (16-byte
+// loads of its key rows when d % 8 == 0 and the cache is 16-byte aligned); the
+// block takes the max and the sum; then thread (g, c) sums column c over keys
+// g, g + NG, ... (NG = 256 / d groups, v rows read coalesced) and the groups'
+// partial sums meet in LDS.
+// ----------------------------------------------------------------------------
+constexpr int SWA_DEC_MAX_W = 8192;
+
+__device__ __forceinline__ float block_max256(float* sh, float x) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x = fmaxf(x, __shfl_xor(x, off));
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = x;
+  __syncthreads();
+  x = fmaxf(fmaxf(sh[0], sh[1]), fmaxf(sh[2], sh[3]));
+  __syncthreads();
+  return x;
+}
+
+__device__ __forceinline__ float block_sum256(float* sh, float x) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off);
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = x;
+  __syncthreads();
+  x = (sh[0] + sh[1]) + (sh[2] + sh[3]);
+  __syncthreads();
+  return x;
+}
+
+__global__ __launch_bounds__(256) void swa_decode_kernel(
+    const bf16* __restrict__ q, const bf16* __restrict__ kc, const bf16* __restrict__ vc,
+    const float* __restrict__ meta, int n_meta, bf16* __restrict__ y, int W, int d, int pos,
+    float scale, int KG) {
+  extern __shared__ __align__(16) char smem[];
+  float* w = reinterpret_cast<float*>(smem);        // [W] bf16-rounded weights
+  float* qs = w + W;                                // [d] query
+  float* part = qs + ((d + 3) & ~3);                // [256] column partial sums
+  float* sh = part + 256;                           // [4] block reductions
+  const int bh = blockIdx.x, tid = threadIdx.x;
+  const int n = min(pos + 1, W);
+  const bf16* kb = kc + (size_t)(bh / KG) * W * d;
+  const bf16* vb = vc + (size_t)(bh / KG) * W * d;
+  const bool vec = (d & 7) == 0 && (reinterpret_cast<uintptr_t>(kb) & 15) == 0;
+  for (int c = tid; c < d; c += 256) qs[c] = to_f32(q[(size_t)bh * d + c]);
+  __syncthreads();
+  float mx = -1e30f;
+  for (int j = 0; j < n_meta; ++j) mx = fmaxf(mx, meta[j]);
+  // scores, key i = tid, tid + 256, ... (position pos - n + 1 + i)
+  for (int i = tid; i < n; i += 256) {
+    const bf16* kr = kb + (size_t)((pos - n + 1 + i) % W) * d;
+    float s = 0.f;
+    if (vec) {
+      for (int c = 0; c < d; c += 8) {
+        const bf16x8 k8 = *reinterpret_cast<const bf16x8*>(kr + c);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s += qs[c + e] * to_f32(k8[e]);
+      }
+    } else {
+      for (int c = 0; c < d; ++c) s += qs[c] * to_f32(kr[c]);
+    }
+    s *= scale;
+    w[i] = s;
+    mx = fmaxf(mx, s);
+  }
+  const float m = block_max256(sh, mx);
+  float l = 0.f;
+  for (int i = tid; i < n; i += 256) {
+    const float e = fexp(w[i] - m);
+    l += e;
+    w[i] = to_f32(to_bf16(e));
+  }
+  l = block_sum256(sh, l);   // also orders the weight writes before the reads below
+  float ls = 0.f;
+  for (int j = 0; j < n_meta; ++j) ls += fexp(meta[j] - m);
+  const float inv = 1.f / (ls + l);
+  const int NG = 256 / d, g = tid / d, c = tid - g * d;   // d <= 256: NG >= 1
+  float acc = 0.f;
+  if (g < NG) {
+#pragma unroll 4
+    for (int i = g; i < n; i += NG)
+      acc += w[i] * to_f32(vb[(size_t)((pos - n + 1 + i) % W) * d + c]);
+  }
+  part[tid] = acc;
+  __syncthreads();
+  if (tid < d) {
+    float t = part[tid];
+    for (int j = 1; j < NG; ++j) t += part[j * d + tid];
+    y[(size_t)bh * d + tid] = to_bf16(t * inv);
+  }
+}
+
+size_t swa_decode_lds(int W, int d) {
+  return ((size_t)W + ((d + 3) & ~3) + 256 + 4) * sizeof(float);
+}
+
+hipError_t launch_swa_decode(const void* q, const void* k_cache, const void* v_cache,
+                             const float* meta, int n_meta, void* y, int BH, int W, int d,
+                             int pos, float scale, int KG, hipStream_t st) {
+  const size_t lds = swa_decode_lds(W, d);
+  hipError_t e = ensure_lds<swa_decode_kernel>((int)swa_decode_lds(SWA_DEC_MAX_W, 256));
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(swa_decode_kernel, dim3(BH), dim3(256), lds, st, (const bf16*)q,
+                     (const bf16*)k_cache, (const bf16*)v_cache, meta, n_meta, (bf16*)y, W, d,
+                     pos, scale, KG);
+  return hipGetLastError();
 }
 
 }  // namespace lz

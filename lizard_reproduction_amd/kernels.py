@@ -207,13 +207,18 @@ def gla_prefill(fq, fk, v, log_gamma, chunk=CHUNK):
     after the last token, for decoding: ``(y, state)``, state fp32
     ``[B, H, F*D + F]`` (S row-major ``[F][D]``, then z ``[F]``; see
     ``split_state``).  The reference has no decode path; the state is that of
-    its recurrent form (tests/test_lizard.py:41-52)."""
-    _check_gla(fq, fk, v, log_gamma, chunk)
+    its recurrent form (tests/test_lizard.py:41-52).  fk and v may have fewer
+    heads than fq (a divisor, as in ``gla_forward``)."""
+    if not isinstance(chunk, int) or chunk < 16 or chunk & (chunk - 1):
+        raise ValueError(f"gla_prefill: chunk must be a power of two >= 16, got {chunk!r}")
+    _check_kv("gla_prefill", fq, fk, v, fq.shape[-1], v.shape[-1])
+    _check_gate("gla_prefill", fq, log_gamma)
+    _require_gpu(fq, fk, v, log_gamma)
     fq, fk, v = _bf16(fq), _bf16(fk), _bf16(v)
-    lg = log_gamma.float().contiguous()
+    lg = _f32(log_gamma)
     b, h, length, nf = fq.shape
     nd = v.shape[-1]
-    y = torch.empty_like(v)
+    y = torch.empty(b, h, length, nd, device=v.device, dtype=torch.bfloat16)
     state = torch.zeros(b, h, nf * nd + nf, device=fq.device, dtype=torch.float32)
     if y.numel():
         lib = _lib.load()
@@ -221,7 +226,7 @@ def gla_prefill(fq, fk, v, log_gamma, chunk=CHUNK):
         nbytes = _gla_fwd_ws(b, h, length, nf, nd, per_head, chunk)
         ws = torch.empty(nbytes, dtype=torch.uint8, device=fq.device) if nbytes else None
         rc = lib.lz_gla_prefill(_ptr(fq), _ptr(fk), _ptr(v), _ptr(lg), _ptr(y), _ptr(state), b, h,
-                                h, length, nf, nd, per_head, chunk, _ptr(ws), nbytes,
+                                fk.shape[1], length, nf, nd, per_head, chunk, _ptr(ws), nbytes,
                                 _stream(fq))
         _lib.check(rc, "lz_gla_prefill")
     return y, state
@@ -243,14 +248,20 @@ def gla_decode_step(fq, fk, v, log_gamma, state):
     (tests/test_lizard.py:41-52): S <- gamma S + fk v^T, z <- gamma z + fk,
     y = fq S / max(fq . z, FLT_MIN), gamma = exp(log_gamma).
 
-    fq, fk ``[B, H, F]``, v ``[B, H, D]`` (cast to bf16), log_gamma ``[B]``
-    or ``[B, H]`` fp32, state from ``gla_prefill`` or ``new_state``.
+    fq ``[B, H, F]``, fk ``[B, Hkv, F]``, v ``[B, Hkv, D]`` (cast to bf16;
+    Hkv divides H, query head h reads kv head h // (H // Hkv)), log_gamma
+    ``[B]`` or ``[B, H]`` fp32, state from ``gla_prefill`` or ``new_state``.
     Returns bf16 ``[B, H, D]``; no autograd."""
-    if fq.dim() != 3 or fk.shape != fq.shape or v.dim() != 3 or v.shape[:2] != fq.shape[:2]:
-        raise ValueError(f"gla_decode_step: fq, fk must be [B, H, F] and v [B, H, D], got "
-                         f"{tuple(fq.shape)}, {tuple(fk.shape)}, {tuple(v.shape)}")
+    if fq.dim() != 3 or fk.dim() != 3 or v.dim() != 3:
+        raise ValueError(f"gla_decode_step: fq [B, H, F], fk [B, Hkv, F] and v [B, Hkv, D] "
+                         f"expected, got {tuple(fq.shape)}, {tuple(fk.shape)}, {tuple(v.shape)}")
     b, h, nf = fq.shape
     nd = v.shape[-1]
+    hk = fk.shape[1]
+    if tuple(fk.shape) != (b, hk, nf) or tuple(v.shape) != (b, hk, nd) or hk <= 0 or h % hk:
+        raise ValueError(f"gla_decode_step: fq [B, H, F], fk [B, Hkv, F] and v [B, Hkv, D] with "
+                         f"Hkv dividing H expected, got {tuple(fq.shape)}, {tuple(fk.shape)}, "
+                         f"{tuple(v.shape)}")
     if log_gamma.shape not in ((b,), (b, h)):
         raise ValueError(f"gla_decode_step: log_gamma must be [B] or [B, H], got "
                          f"{tuple(log_gamma.shape)}")
@@ -262,9 +273,10 @@ def gla_decode_step(fq, fk, v, log_gamma, state):
     _require_gpu(fq, fk, v, log_gamma, state)
     fq, fk, v = _bf16(fq), _bf16(fk), _bf16(v)
     lg = log_gamma.float().contiguous()
-    y = torch.empty_like(v)
+    y = torch.empty(b, h, nd, device=v.device, dtype=torch.bfloat16)
     rc = _lib.load().lz_gla_decode_step(_ptr(fq), _ptr(fk), _ptr(v), _ptr(lg), _ptr(state),
-                                        _ptr(y), b, h, nf, nd, int(lg.dim() == 2), _stream(fq))
+                                        _ptr(y), b, h, hk, nf, nd, int(lg.dim() == 2),
+                                        _stream(fq))
     _lib.check(rc, "lz_gla_decode_step")
     return y
 
@@ -341,6 +353,44 @@ def swa_backward(q, k, v, meta, lse, dy, window, grad_dtype):
     else:
         dq.zero_(), dk.zero_(), dv.zero_(), dmeta.zero_()
     return dq, dk, dv, dmeta
+
+
+SWA_DECODE_MAX_WINDOW = 8192
+
+
+def swa_decode_step(q, k_cache, v_cache, meta, pos):
+    """The ``swa`` output row of one new query per (b, h) at absolute
+    position ``pos`` (src/kernels/swa.py:19-59 at i = pos), against a
+    ring-buffered window cache.  The reference has no decode path.
+
+    q ``[B, H, d]`` (RoPE applied), k_cache / v_cache ``[B, Hkv, W, d]``
+    holding position p in slot p % W (the caller has written position pos
+    there), meta ``[n_meta]`` fp32.  Returns bf16 ``[B, H, d]``; no autograd."""
+    if q.dim() != 3 or k_cache.dim() != 4 or tuple(v_cache.shape) != tuple(k_cache.shape):
+        raise ValueError(f"swa_decode_step: q [B, H, d] and k_cache, v_cache [B, Hkv, W, d] "
+                         f"expected, got {tuple(q.shape)}, {tuple(k_cache.shape)}, "
+                         f"{tuple(v_cache.shape)}")
+    b, h, d = q.shape
+    hk, window = k_cache.shape[1], k_cache.shape[2]
+    if k_cache.shape[0] != b or k_cache.shape[3] != d or hk <= 0 or h % hk:
+        raise ValueError(f"swa_decode_step: caches must be [B, Hkv, W, d] = [{b}, Hkv, W, {d}] "
+                         f"with Hkv dividing {h}, got {tuple(k_cache.shape)}")
+    if not 1 <= window <= SWA_DECODE_MAX_WINDOW:
+        raise ValueError(f"swa_decode_step: window must be in [1, {SWA_DECODE_MAX_WINDOW}], "
+                         f"got {window}")
+    if not isinstance(pos, int) or pos < 0:
+        raise ValueError(f"swa_decode_step: pos must be a non-negative int, got {pos!r}")
+    if meta.dim() != 1:
+        raise ValueError(f"swa_decode_step: meta must be 1-D, got {tuple(meta.shape)}")
+    _require_gpu(q, k_cache, v_cache)
+    q, kc, vc, meta = _bf16(q), _bf16(k_cache), _bf16(v_cache), _f32(meta)
+    y = torch.empty_like(q)
+    if y.numel():
+        rc = _lib.load().lz_swa_decode_step(_ptr(q), _ptr(kc), _ptr(vc), _ptr(meta),
+                                            meta.numel(), _ptr(y), b, h, hk, window, d, pos,
+                                            1.0 / math.sqrt(d), _stream(q))
+        _lib.check(rc, "lz_swa_decode_step")
+    return y
 
 
 class _SWA(torch.autograd.Function):

@@ -21,6 +21,13 @@ projection outputs to o_proj's input runs on HIP kernels: the fused
 prologue (GQA expand, Hedgehog feature maps, RoPE and the bf16 casts, one
 pass over q/k/v), the GLA and SWA kernels, and the fused blend + transpose,
 one autograd node for all of them (``_Core``).
+
+Decoding (no counterpart in the reference, which has no decode path):
+``prefill`` runs the forward over a prompt and returns a ``LizardCache`` --
+the GLA recurrent state after the prompt and a ring buffer of the last
+``window`` keys (RoPE applied) and values per kv head -- and ``step`` runs
+one token per sequence from it, each output equal (up to rounding) to the
+forward's row for that position.
 """
 import functools
 
@@ -216,6 +223,26 @@ class _Core(torch.autograd.Function):
         return tuple(g.to(d) for g, d in zip(grads, ctx.dtypes)) + (None,) * 6
 
 
+class LizardCache:
+    """Decode state of one layer: ``state`` fp32 [B, heads, F*hd + F] (the
+    GLA recurrent state S, z; F = 2 feature_dim), ``k`` and ``v`` bf16
+    [B, kv_heads, window, hd] (position p in slot p % window, RoPE applied
+    to k), ``pos`` the absolute position of the next token."""
+
+    def __init__(self, state, k, v, pos):
+        self.state, self.k, self.v, self.pos = state, k, v, pos
+
+    def put(self, kr, v, p0):
+        """Write positions p0 .. p0 + n - 1 of kr, v ([B, kv_heads, n, hd]);
+        only the last ``window`` of them stay."""
+        window = self.k.shape[2]
+        n = kr.shape[2]
+        first = max(0, n - window)
+        slots = torch.arange(p0 + first, p0 + n, device=kr.device) % window
+        self.k[:, :, slots] = kr[:, :, first:]
+        self.v[:, :, slots] = v[:, :, first:]
+
+
 class LizardAttention(nn.Module):
     """Hybrid GLA + sliding-window attention layer
     (``src/lizard_attention.py:47-97``).
@@ -279,6 +306,67 @@ class LizardAttention(nn.Module):
                         self.phi_k.weight, F.logsigmoid(z), self.meta_tokens, self.alpha_blend,
                         cos, sin, self.heads, self.kv_heads, self.window, x.dtype)
         return self.o_proj(y), None
+
+    # -- decoding -----------------------------------------------------------
+
+    def new_cache(self, batch, device=None):
+        """The cache of an empty prefix (zeros, pos 0)."""
+        device = device if device is not None else self.q_proj.weight.device
+        nf = 2 * self.phi_q.weight.shape[0]
+        state = kernels.new_state(batch, self.heads, nf, self.head_dim, device)
+        shape = (batch, self.kv_heads, self.window, self.head_dim)
+        k = torch.zeros(shape, device=device, dtype=torch.bfloat16)
+        return LizardCache(state, k, torch.zeros_like(k), 0)
+
+    def _operands(self, x, position_embeddings):
+        if x.device.type != "cuda":
+            raise ValueError("LizardAttention (hip backend) needs its input on a ROCm GPU")
+        dtype = torch.promote_types(x.dtype, torch.float32)
+        lg = F.logsigmoid(self.W_gamma(x).to(dtype).squeeze(-1)).float().contiguous()
+        cos, sin = position_embeddings
+        fq, fk, qr, kr, v, _ = prologue_forward(
+            self.q_proj(x), self.k_proj(x), self.v_proj(x), self.phi_q.weight,
+            self.phi_k.weight, cos, sin, self.heads, self.kv_heads)
+        return lg, fq, fk, qr, kr, v
+
+    def _out(self, y_gla, y_swa, x):
+        alpha = self.alpha_blend.detach().float().reshape(1).contiguous()
+        odt = torch.bfloat16 if x.dtype == torch.bfloat16 else torch.float32
+        return self.o_proj(combine_forward(y_gla, y_swa, alpha, odt).to(x.dtype))
+
+    @torch.no_grad()
+    def prefill(self, hidden_states, position_embeddings):
+        """``forward`` over a prompt [B, L, hidden] (no autograd) that also
+        returns the decode cache after it: ``(out, cache)``."""
+        x = hidden_states
+        lg, fq, fk, qr, kr, v = self._operands(x, position_embeddings)
+        y_gla, state = kernels.gla_prefill(fq, fk, v, lg)
+        y_swa, _ = kernels.swa_forward(qr, kr, v, self.meta_tokens.detach().float().contiguous(),
+                                       self.window)
+        cache = self.new_cache(x.shape[0], x.device)
+        cache.state = state
+        cache.put(kr, v, 0)
+        cache.pos = x.shape[1]
+        return self._out(y_gla, y_swa, x), cache
+
+    @torch.no_grad()
+    def step(self, hidden_states, position_embeddings, cache):
+        """One token per sequence: hidden_states [B, 1, hidden] at position
+        ``cache.pos`` (position_embeddings for that position, [B, 1, hd] or
+        [1, hd]); updates ``cache`` in place and returns out [B, 1, hidden]."""
+        x = hidden_states
+        if x.dim() != 3 or x.shape[1] != 1:
+            raise ValueError(f"LizardAttention.step: hidden_states must be [B, 1, hidden], got "
+                             f"{tuple(x.shape)}")
+        lg, fq, fk, qr, kr, v = self._operands(x, position_embeddings)
+        cache.put(kr, v, cache.pos)
+        y_gla = kernels.gla_decode_step(fq[:, :, 0], fk[:, :, 0], v[:, :, 0], lg[:, 0],
+                                        cache.state)
+        y_swa = kernels.swa_decode_step(qr[:, :, 0], cache.k, cache.v,
+                                        self.meta_tokens.detach().float().contiguous(),
+                                        cache.pos)
+        cache.pos += 1
+        return self._out(y_gla[:, :, None], y_swa[:, :, None], x)
 
 
 def from_llama(attention, config, **options):
