@@ -681,8 +681,10 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_bwd_state_kernel(
 // Eight waves share one chunk (the LDS of a chunk leaves room for one
 // workgroup per CU, so the second wave per SIMD comes from inside it):
 //   phase 1  wave (kind, qt, kt): kind 0 the score tile s -> a/den, kind 1 the
-//            dy.v^T tile -> dad (both need only their own tile); all threads
-//            form dY^ = bf16(qh dy) and the dz partials;
+//            dy.v^T tile -> dad (both need only their own tile).  The tiles of
+//            keys 32-63 x queries 0-31 are causally zero: their two waves
+//            form dY^ = bf16(qh dy) and the dz partials instead, and the
+//            phase-2 products skip those zero fragments;
 //   phase 2  dv jobs (d-tile, key half) contract dS over f from the published
 //            bf16 dS^T tile; dS tiles (f-tile, d-tile) are spread over the
 //            waves' accumulators and updated with fq^T dY^; dfk jobs
@@ -843,6 +845,10 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
 
   const int kind = wave >> 2, qt = (wave >> 1) & 1, kt = wave & 1;   // phase-1 tile
   const int ki = kt * 32 + col;                                       // its key (lane)
+  // waves 1 and 5 hold the causally zero tiles (kt = 1, qt = 0): they do the
+  // per-chunk staging work instead, as threads a = 0 .. 127
+  const bool stager = kt == 1 && qt == 0;
+  const int a = (kind << 6) + lane;
   // chunk n is in LDS and register set `set` is free; the next set holds chunk n-1
   auto step = [&](auto set, int n) __attribute__((always_inline)) {
     constexpr int S = decltype(set)::value;
@@ -854,7 +860,7 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
     const float* dwc = dw + 64 * cur;
     issue(set, n - DEPTH);
     // ---- phase 1: one 32x32 tile (queries x keys) of s or dy v^T per wave ----
-    {
+    if (!stager) {
       f32x16 acc = zero16();
       if (kind == 0) {
 #pragma unroll
@@ -891,9 +897,9 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
       frag[(kt * 4 + qt * 2 + 1) * 64 + lane] = o8[1];
     }
     // dY^ = bf16(qh dy), once per chunk, for dS += fq^T dY^
-    {
+    if (stager) {
       constexpr int K8 = DP / 8;
-      for (int idx = tid; idx < C * K8; idx += B_THREADS) {
+      for (int idx = a; idx < C * K8; idx += 128) {
         const int t = idx / K8, c8 = 8 * (idx % K8);
         const bf16x8 x = *reinterpret_cast<const bf16x8*>(dy_l + t * PD + c8);
         *reinterpret_cast<bf16x8*>(dyh_l + t * PD + c8) = scale8(x, qhc[t]);
@@ -902,8 +908,9 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
     // dz partials: part p sums fq_t (qh_t delta_t) over tokens [8 p, 8 p + 8)
     {
       constexpr int K8 = FP / 8;
-      if (tid < ZP * K8) {
-        const int c8 = 8 * (tid % K8), part = tid / K8;
+      static_assert(ZP * K8 <= 128, "dz partials: one per staging thread");
+      if (stager && a < ZP * K8) {
+        const int c8 = 8 * (a % K8), part = a / K8;
         float za[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < C / ZP; ++j) {
@@ -938,8 +945,9 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
 #pragma unroll
         for (int r = 0; r < 16; ++r) g[r] *= ksv;
 #pragma unroll
-        for (int qb = 0; qb < 4; ++qb)
-          g = mfma(tr_operand(dy_l, PD, 16 * qb, dt * 32, lane), fa[(hk * 4 + qb) * 64 + lane], g);
+        for (int qb = 0; qb < 4; ++qb)   // keys 32-63 have no queries in blocks 0, 1
+          if (hk == 0 || qb >= 2)
+            g = mfma(tr_operand(dy_l, PD, 16 * qb, dt * 32, lane), fa[(hk * 4 + qb) * 64 + lane], g);
         store_acc_row<OutT>(dv + offD, t0 + key, dt * 32, L, D, vecD, g, 1.f, h);
       }
     }
@@ -970,8 +978,9 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
           x = mfma(tr_operand(dst_l, PF, 16 * kb, ft * 32, lane),
                    row_operand_acc(v_l, PD, key, 16 * kb, h), x);
 #pragma unroll
-        for (int qb = 0; qb < 4; ++qb)
-          g = mfma(tr_operand(fq_l, PF, 16 * qb, ft * 32, lane), fd[(hk * 4 + qb) * 64 + lane], g);
+        for (int qb = 0; qb < 4; ++qb)   // keys 32-63 have no queries in blocks 0, 1
+          if (hk == 0 || qb >= 2)
+            g = mfma(tr_operand(fq_l, PF, 16 * qb, ft * 32, lane), fd[(hk * 4 + qb) * 64 + lane], g);
         const float ksv = ks[key];
         const int tok = t0 + key;
         float pks = 0.f;

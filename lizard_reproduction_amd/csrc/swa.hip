@@ -538,7 +538,7 @@ hipError_t launch_swa_bwd(const void* q, const void* k, const void* v, const flo
 // ----------------------------------------------------------------------------
 constexpr int SWA_DEC_MAX_W = 8192;
 
-__device__ __forceinline__ float block_max256(float* sh, float x) {
+__device__ __forceinline__ float decode_max256(float* sh, float x) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) x = fmaxf(x, __shfl_xor(x, off));
   if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = x;
@@ -548,7 +548,7 @@ __device__ __forceinline__ float block_max256(float* sh, float x) {
   return x;
 }
 
-__device__ __forceinline__ float block_sum256(float* sh, float x) {
+__device__ __forceinline__ float decode_sum256(float* sh, float x) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off);
   if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = x;
@@ -593,14 +593,14 @@ __global__ __launch_bounds__(256) void swa_decode_kernel(
     w[i] = s;
     mx = fmaxf(mx, s);
   }
-  const float m = block_max256(sh, mx);
+  const float m = decode_max256(sh, mx);
   float l = 0.f;
   for (int i = tid; i < n; i += 256) {
     const float e = fexp(w[i] - m);
     l += e;
     w[i] = to_f32(to_bf16(e));
   }
-  l = block_sum256(sh, l);   // also orders the weight writes before the reads below
+  l = decode_sum256(sh, l);   // also orders the weight writes before the reads below
   float ls = 0.f;
   for (int j = 0; j < n_meta; ++j) ls += fexp(meta[j] - m);
   const float inv = 1.f / (ls + l);

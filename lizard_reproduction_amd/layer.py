@@ -237,6 +237,10 @@ class LizardCache:
         only the last ``window`` of them stay."""
         window = self.k.shape[2]
         n = kr.shape[2]
+        if n == 1:   # a decode step: one slot, plain copies
+            self.k[:, :, p0 % window] = kr[:, :, 0]
+            self.v[:, :, p0 % window] = v[:, :, 0]
+            return
         first = max(0, n - window)
         slots = torch.arange(p0 + first, p0 + n, device=kr.device) % window
         self.k[:, :, slots] = kr[:, :, first:]

@@ -151,3 +151,25 @@ def test_to_lizard_swaps_every_block():
     hip_layer.to_lizard(model, window=16, num_meta=4, feature_dim=8, backend="hip")
     assert all(isinstance(b.self_attn, hip_layer.LizardAttention) for b in model.model.layers)
     assert [b.self_attn.layer_idx for b in model.model.layers] == [0, 1]
+
+
+@pytest.mark.parametrize("prompt, window", [(5, 8), (8, 8), (21, 8), (3, 1)])
+def test_cache_ring_holds_the_last_window_positions(prompt, window):
+    """LizardCache.put (plain torch, no kernels): after a prompt of any
+    length and then single-token writes, slot p % window holds position p for
+    the last `window` positions -- what the SWA decode kernel reads."""
+    b, kv, hd = 2, 3, 4
+    k = torch.zeros(b, kv, window, hd, dtype=torch.bfloat16)
+    cache = hip_layer.LizardCache(None, k, torch.zeros_like(k), 0)
+
+    def rows(p0, n):   # position p's key is filled with the value p, its value with -p
+        pos = torch.arange(p0, p0 + n, dtype=torch.float32).view(1, 1, n, 1)
+        return pos.expand(b, kv, n, hd).bfloat16(), (-pos).expand(b, kv, n, hd).bfloat16()
+    cache.put(*rows(0, prompt), 0)
+    end = prompt
+    for p in range(prompt, prompt + 5):
+        cache.put(*rows(p, 1), p)
+        end = p + 1
+        for q in range(max(0, end - window), end):
+            assert torch.all(cache.k[:, :, q % window] == q), (p, q)
+            assert torch.all(cache.v[:, :, q % window] == -q), (p, q)
