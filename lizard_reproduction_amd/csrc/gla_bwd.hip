@@ -82,7 +82,8 @@ __device__ __forceinline__ void store_tile8(const uint4 (&reg)[N], bf16* tile, i
 // kernel A: forward walk -> dfq, den, delta, p = fq . dfq
 //
 //   phase 1  waves 0-3: the score tile (keys kt x queries qt) a^T and v dy^T,
-//            the decay, sum_t a and sum_t a (v . dy); waves 4-7: Q~ . z and
+//            the decay, sum_t a and sum_t a (v . dy) (the tile of keys 32-63 x
+//            queries 0-31 is causally zero and skipped); waves 4-7: Q~ . z and
 //            K~ = bf16(fk ks) with its column sums; X jobs (f-tile, query
 //            half): X = S dy^T and qs fq . X, waves 4-7 first;
 //   phase 2  waves 0-3: den, delta, dad fragments;
@@ -303,6 +304,9 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
   const bool scorer = wave < 4;
   const int kt = (wave >> 1) & 1, qt = wave & 1;   // score tile of waves 0-3
   const int qi = qt * 32 + col;                     // its query (lane)
+  // keys 32-63 x queries 0-31 (wave 2) is causally zero: its row sums are 0,
+  // its dad fragments are never read (phase 3 skips them)
+  const bool live = scorer && !(kt == 1 && qt == 0);
   // chunk n is in LDS and register set `set` is free; the next set holds chunk n+1
   auto step = [&](auto set, int n) __attribute__((always_inline)) {
     constexpr int S = decltype(set)::value;
@@ -311,7 +315,12 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
     // ---- phase 1 ---------------------------------------------------------------
     f32x16 vdy = zero16();
     float dec[16];   // causal decay of the score tile, reused in phase 2
-    if (scorer) {
+    if (scorer && !live) {
+      if (h == 0) {
+        ra[kt * 64 + qi] = 0.f;
+        rav[kt * 64 + qi] = 0.f;
+      }
+    } else if (scorer) {
       f32x16 aT = zero16();
 #pragma unroll
       for (int kb = 0; kb < FP / 16; ++kb)
@@ -394,7 +403,7 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
     }
     __syncthreads();
     // ---- phase 2: den, delta, dad fragments (waves 0-3) ------------------------
-    if (scorer) {
+    if (live) {
       const float den = ra[qi] + ra[64 + qi] + qz[qi] + qz[64 + qi] + qz[128 + qi] + qz[192 + qi];
       float num = rav[qi] + rav[64 + qi];
 #pragma unroll
@@ -426,8 +435,9 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
         const int q = hq * 32 + col;
         f32x16 g = zero16();
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
-          g = mfma(tr_operand(fk_l, PF, 16 * kb, ft * 32, lane), fr[(hq * 4 + kb) * 64 + lane], g);
+        for (int kb = 0; kb < 4; ++kb)   // queries 0-31 have no keys in blocks 2, 3
+          if (hq == 1 || kb < 2)
+            g = mfma(tr_operand(fk_l, PF, 16 * kb, ft * 32, lane), fr[(hq * 4 + kb) * 64 + lane], g);
         const float dcl = fmaxf(dens[q], TINY);
         const float qsd = qs[q] / dcl;
         const float delta = dels[q];
