@@ -33,7 +33,9 @@
 //     stores); the next chunk is already in flight into registers.
 //   * phase 1: wave (kt, qt) computes one 32x32 tile of s^T = fk fq^T
 //     (keys x queries), applies the causal decay in registers and publishes
-//     the bf16 tile as ready-made MFMA operands; Q~.z partials go to LDS; the
+//     the bf16 tile as ready-made MFMA operands (the tile of keys 32-63 x
+//     queries 0-31 is causally zero: its wave takes most of the Q~.z work
+//     instead, and phase 2 skips its fragments); Q~.z partials go to LDS; the
 //     workgroup forms K~ = bf16(fk ks) once (16-byte row items, with their
 //     column sums for z) and writes it over fk, which the scores no longer need.
 //   * phase 2: a wave owns d-tiles of the output and the state: o^T = S^T fq^T
@@ -160,35 +162,45 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
     uint4 kti[RowItems<FP>::N];   // this thread's rows of K~ = bf16(fk * ks)
     {
       const int kt = wave >> 1, qt = wave & 1;
-      f32x16 s = zero16();
-#pragma unroll
-      for (int kb = 0; kb < FP / 16; ++kb)
-        s = mfma(row_operand(fk_l, PF, kt * 32 + col, 16 * kb, h),
-                 row_operand(fq_l, PF, qt * 32 + col, 16 * kb, h), s);
       const int qi = qt * 32 + col;
-      const float lgq = lgs[qi];
-      bf16x8 p[2];
-      float rsum = 0.f;
+      if (kt == 1 && qt == 0) {
+        // keys 32-63 x queries 0-31: causally zero (phase 2 skips its fragments)
+        if (h == 0) rs[64 + qi] = 0.f;
+      } else {
+        f32x16 s = zero16();
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = kt * 32 + acc_row(r, h);
-        const float val = key <= qi ? s[r] * fexp(lgq - lgs[key]) : 0.f;
-        const bf16 pb = to_bf16(val);
-        p[r >> 3][r & 7] = pb;
-        rsum += to_f32(pb);
+        for (int kb = 0; kb < FP / 16; ++kb)
+          s = mfma(row_operand(fk_l, PF, kt * 32 + col, 16 * kb, h),
+                   row_operand(fq_l, PF, qi, 16 * kb, h), s);
+        const float lgq = lgs[qi];
+        bf16x8 p[2];
+        float rsum = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kt * 32 + acc_row(r, h);
+          const float val = key <= qi ? s[r] * fexp(lgq - lgs[key]) : 0.f;
+          const bf16 pb = to_bf16(val);
+          p[r >> 3][r & 7] = pb;
+          rsum += to_f32(pb);
+        }
+        rsum += xhalf(rsum);
+        pfrag[(qt * 4 + kt * 2 + 0) * 64 + lane] = p[0];
+        pfrag[(qt * 4 + kt * 2 + 1) * 64 + lane] = p[1];
+        if (h == 0) rs[kt * 64 + qi] = rsum;
       }
-      rsum += xhalf(rsum);
-      pfrag[(qt * 4 + kt * 2 + 0) * 64 + lane] = p[0];
-      pfrag[(qt * 4 + kt * 2 + 1) * 64 + lane] = p[1];
-      if (h == 0) rs[kt * 64 + qi] = rsum;
 
-      constexpr int FQ = FP / 4;   // qs (fq . z) over a quarter of the features; query = lane
+      // qs (fq . z), query = lane, over 8-feature groups: wave 2 (no score
+      // tile) takes 5/8 of the groups, waves 0, 1, 3 a third of the rest each
+      constexpr int NG = FP / 8, G2 = NG * 5 / 8, GR = NG - G2;
+      const int wi = wave == 3 ? 2 : wave;
+      const int g0 = wave == 2 ? 0 : G2 + wi * GR / 3;
+      const int g1 = wave == 2 ? G2 : G2 + (wi + 1) * GR / 3;
       float acc = 0.f;
-#pragma unroll
-      for (int c = 0; c < FQ; c += 8) {
-        const bf16x8 x = *reinterpret_cast<const bf16x8*>(fq_l + lane * PF + wave * FQ + c);
-        const f32x4 z0 = *reinterpret_cast<const f32x4*>(zs + wave * FQ + c);
-        const f32x4 z1 = *reinterpret_cast<const f32x4*>(zs + wave * FQ + c + 4);
+#pragma unroll 2
+      for (int g = g0; g < g1; ++g) {
+        const bf16x8 x = *reinterpret_cast<const bf16x8*>(fq_l + lane * PF + 8 * g);
+        const f32x4 z0 = *reinterpret_cast<const f32x4*>(zs + 8 * g);
+        const f32x4 z1 = *reinterpret_cast<const f32x4*>(zs + 8 * g + 4);
 #pragma unroll
         for (int e = 0; e < 4; ++e) acc += to_f32(x[e]) * z0[e];
 #pragma unroll
@@ -223,7 +235,8 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
 #pragma unroll
           for (int r = 0; r < 16; ++r) o[r] *= qsv;
 #pragma unroll
-          for (int kb = 0; kb < 4; ++kb) o = mfma(vop[kb], pfrag[(qt * 4 + kb) * 64 + lane], o);
+          for (int kb = 0; kb < 4; ++kb)   // queries 0-31 have no keys in blocks 2, 3
+            if (qt == 1 || kb < 2) o = mfma(vop[kb], pfrag[(qt * 4 + kb) * 64 + lane], o);
           const float den = rs[qi] + rs[64 + qi] + qz[qi] + qz[64 + qi] + qz[128 + qi] + qz[192 + qi];
           const float inv = 1.f / fmaxf(den, TINY);
           store_acc_row_bf16(yr, t0 + qi, dt * 32, D, vecD, o, inv, h);
