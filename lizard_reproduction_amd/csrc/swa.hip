@@ -81,8 +81,16 @@ __device__ __forceinline__ bool blocks_meet(int q0, int k0, int L, int W) {
 // ----------------------------------------------------------------------------
 // forward
 // ----------------------------------------------------------------------------
+// Workgroups per CU the forward asks the compiler to fit in registers: at
+// d <= 64 four (122 VGPRs at d = 64 instead of 178 unconstrained), so four
+// waves per SIMD overlap each other's loads; two at d = 128 (no spills).
 template <int DP, bool VEC>
-__global__ __launch_bounds__(256) void swa_fwd_kernel(
+constexpr int swa_fwd_occupancy() {
+  return DP <= 32 ? 4 : DP <= 64 ? (VEC ? 4 : 3) : DP <= 128 ? 2 : 1;
+}
+
+template <int DP, bool VEC>
+__global__ __launch_bounds__(256, (swa_fwd_occupancy<DP, VEC>())) void swa_fwd_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ meta, int n_meta, bf16* __restrict__ y, float* __restrict__ lse,
     int BH, int L, int d, int W, float scale, int per, int KG) {
