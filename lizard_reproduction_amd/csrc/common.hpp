@@ -21,6 +21,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 namespace lz {
 
 typedef __bf16 bf16;
@@ -117,15 +119,25 @@ __device__ __forceinline__ void store4(OutT* __restrict__ p, int row, int c, int
   }
 }
 
-// Raise kernel Kern's dynamic-LDS limit to `bytes`, once per process: the
-// first launch of each kernel instantiation makes the runtime call (a
-// function-local static, initialised thread-safely), later launches reuse its
-// status.  Every instantiation asks for one fixed size, its LDS layout's.
+// Raise kernel Kern's dynamic-LDS limit to `bytes` on the current device,
+// once per device: the first launch of each kernel instantiation on a device
+// makes the runtime call (under a per-device std::call_once), later launches
+// reuse its status.  Every instantiation asks for one fixed size, its LDS
+// layout's.  Devices past the table's size make the call on every launch.
+constexpr int LDS_ATTR_DEVICES = 64;
 template <auto Kern>
 hipError_t ensure_lds(int bytes) {
-  static const hipError_t status = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(Kern), hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-  return status;
+  auto set = [bytes] {
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(Kern),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  };
+  int dev = 0;
+  if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
+  if (dev < 0 || dev >= LDS_ATTR_DEVICES) return set();
+  static std::once_flag once[LDS_ATTR_DEVICES];
+  static hipError_t status[LDS_ATTR_DEVICES];
+  std::call_once(once[dev], [&] { status[dev] = set(); });
+  return status[dev];
 }
 
 // Row pitch (elements) of a row-major bf16 LDS tile with x columns.  Measured
