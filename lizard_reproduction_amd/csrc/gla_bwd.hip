@@ -132,44 +132,6 @@ struct BwdA : BwdCommon<FP, DP> {
   static_assert(BYTES <= 160 * 1024, "LDS budget");
 };
 
-// scale_rows (gla_common.hpp) for 256 threads numbered t (the upper half of
-// the workgroup here)
-template <int KP>
-__device__ __forceinline__ void scale_rows_t(const bf16* tile, int pitch, const float* scale,
-                                             uint4 (&out)[RowItems<KP>::N], float* part, int t) {
-  using R = RowItems<KP>;
-  const int cg = t % R::K8, r0 = t / R::K8;
-  float sum[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) sum[e] = 0.f;
-#pragma unroll
-  for (int i = 0; i < R::N; ++i) {
-    const int row = r0 + R::RSTRIDE * i;
-    const bf16x8 x = *reinterpret_cast<const bf16x8*>(tile + row * pitch + 8 * cg);
-    const float s = scale[row];
-    bf16x8 o;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      o[e] = to_bf16(to_f32(x[e]) * s);
-      sum[e] += to_f32(o[e]);
-    }
-    out[i] = __builtin_bit_cast(uint4, o);
-  }
-  float* dst = part + r0 * KP + 8 * cg;
-  *reinterpret_cast<f32x4*>(dst) = f32x4{sum[0], sum[1], sum[2], sum[3]};
-  *reinterpret_cast<f32x4*>(dst + 4) = f32x4{sum[4], sum[5], sum[6], sum[7]};
-}
-
-template <int KP>
-__device__ __forceinline__ void store_rows_t(const uint4 (&in)[RowItems<KP>::N], bf16* tile,
-                                             int pitch, int t) {
-  using R = RowItems<KP>;
-  const int cg = t % R::K8, r0 = t / R::K8;
-#pragma unroll
-  for (int i = 0; i < R::N; ++i)
-    *reinterpret_cast<uint4*>(tile + (r0 + R::RSTRIDE * i) * pitch + 8 * cg) = in[i];
-}
-
 template <int FP, int DP, typename OutT, bool VEC>
 __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
     const bf16* __restrict__ fq, const bf16* __restrict__ fk, const bf16* __restrict__ v,

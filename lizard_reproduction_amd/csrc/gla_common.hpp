@@ -89,6 +89,44 @@ __device__ __forceinline__ void store_rows(const uint4 (&in)[RowItems<KP>::N], b
     *reinterpret_cast<uint4*>(tile + (r0 + R::RSTRIDE * i) * pitch + 8 * cg) = in[i];
 }
 
+// scale_rows for 256 threads numbered t (the upper half of an eight-wave
+// workgroup, t = tid - 256), and its store_rows
+template <int KP>
+__device__ __forceinline__ void scale_rows_t(const bf16* tile, int pitch, const float* scale,
+                                             uint4 (&out)[RowItems<KP>::N], float* part, int t) {
+  using R = RowItems<KP>;
+  const int cg = t % R::K8, r0 = t / R::K8;
+  float sum[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) sum[e] = 0.f;
+#pragma unroll
+  for (int i = 0; i < R::N; ++i) {
+    const int row = r0 + R::RSTRIDE * i;
+    const bf16x8 x = *reinterpret_cast<const bf16x8*>(tile + row * pitch + 8 * cg);
+    const float s = scale[row];
+    bf16x8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      o[e] = to_bf16(to_f32(x[e]) * s);
+      sum[e] += to_f32(o[e]);
+    }
+    out[i] = __builtin_bit_cast(uint4, o);
+  }
+  float* dst = part + r0 * KP + 8 * cg;
+  *reinterpret_cast<f32x4*>(dst) = f32x4{sum[0], sum[1], sum[2], sum[3]};
+  *reinterpret_cast<f32x4*>(dst + 4) = f32x4{sum[4], sum[5], sum[6], sum[7]};
+}
+
+template <int KP>
+__device__ __forceinline__ void store_rows_t(const uint4 (&in)[RowItems<KP>::N], bf16* tile,
+                                             int pitch, int t) {
+  using R = RowItems<KP>;
+  const int cg = t % R::K8, r0 = t / R::K8;
+#pragma unroll
+  for (int i = 0; i < R::N; ++i)
+    *reinterpret_cast<uint4*>(tile + (r0 + R::RSTRIDE * i) * pitch + 8 * cg) = in[i];
+}
+
 // column c of the partial sums written by scale_rows (threads with tid < KP)
 template <int KP>
 __device__ __forceinline__ float sum_parts(const float* part, int c) {

@@ -284,6 +284,277 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
 }
 
 // ----------------------------------------------------------------------------
+// F = 256: the same walk with eight waves per workgroup.  At F = 256 a chunk's
+// tiles leave room for one workgroup per CU, so the four-wave walk above runs
+// one wave per SIMD and its two waves per d-tile both carry (and update) that
+// tile's whole state.  Here 512 threads share the chunk, two waves per SIMD:
+//   * every (f-tile, d-tile) tile of S lives in exactly one wave's
+//     accumulators (tile t = wave + 8 i), and after each update the waves
+//     publish bf16 S^T [d][f] to LDS, where the output products read it: the
+//     same bf16(S) operands, in the same k order, as the register form above;
+//   * phase 1: waves 0, 1, 3 compute the three score tiles that are not
+//     causally zero; wave 2 takes 5/8 of the Q~.z feature groups, waves 4-7
+//     the rest and K~ = bf16(fk ks) with its column sums;
+//   * phase 2: waves 4-7 (4 - 4 + 2 NDT of them) compute the outputs of one
+//     (d-tile, query half) each; all waves update their state tiles;
+//   * then the waves publish S^T, stage the prefetched chunk, scan the next
+//     gate and update z.
+// ----------------------------------------------------------------------------
+constexpr int WIDE_THREADS = 512;
+
+template <int DP>
+struct GlaFwdWide {
+  static constexpr int FP = 256, C = GLA_C;
+  static constexpr int PF = lds_pitch(FP), PD = lds_pitch(DP);
+  static constexpr int NFT = FP / 32, NDT = DP / 32;
+  static constexpr int S_OWN = (NFT * NDT + 7) / 8;          // state tiles per wave
+  static constexpr int NLF = C * FP / 8 / WIDE_THREADS;       // 16-byte items per thread, fq or fk
+  static constexpr int NLD = (C * DP / 8 + WIDE_THREADS - 1) / WIDE_THREADS;
+  static constexpr int OFF_FQ = 0;
+  static constexpr int OFF_FK = OFF_FQ + C * PF * 2;
+  static constexpr int OFF_V = OFF_FK + C * PF * 2;
+  static constexpr int OFF_ST = OFF_V + C * PD * 2;           // bf16 S^T [DP][PF]
+  static constexpr int OFF_PF = OFF_ST + DP * PF * 2;         // [2 qt][4 kb][64 lanes] bf16x8
+  static constexpr int OFF_RS = OFF_PF + 2 * 4 * 64 * 16;     // [2 kt][64] row sums of a
+  static constexpr int OFF_QZ = OFF_RS + 2 * 64 * 4;          // [8 waves][64] Q~.z partials
+  static constexpr int OFF_LG = OFF_QZ + 8 * 64 * 4;
+  static constexpr int OFF_QS = OFF_LG + 64 * 4;
+  static constexpr int OFF_KS = OFF_QS + 64 * 4;
+  static constexpr int OFF_Z = OFF_KS + 64 * 4;
+  static constexpr int OFF_ZP = OFF_Z + FP * 4;               // K~ column partial sums
+  static constexpr int OFF_R = OFF_ZP + RowItems<FP>::PARTS * FP * 4;
+  static constexpr int BYTES = OFF_R + 16;
+  static_assert(BYTES <= 160 * 1024, "LDS budget");
+};
+
+// rows [t0, t0+64) of a [L x ncols] bf16 matrix by the 512 threads (item
+// idx = tid + 512 i: row idx / (KP/8), 8 columns), and their LDS stores
+template <int KP, int N>
+__device__ __forceinline__ void load_chunk512(uint4 (&reg)[N], const bf16* __restrict__ base,
+                                              int t0, int L, int ncols, bool vec) {
+  load_items<KP, WIDE_THREADS, N, GLA_C * KP / 8>(reg, base, t0, L, ncols, vec);
+}
+
+template <int KP, int N>
+__device__ __forceinline__ void store_chunk512(const uint4 (&reg)[N], bf16* tile, int pitch) {
+  constexpr int K8 = KP / 8, ITEMS = GLA_C * K8;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const int idx = threadIdx.x + WIDE_THREADS * i;
+    if (ITEMS % WIDE_THREADS == 0 || idx < ITEMS)
+      *reinterpret_cast<uint4*>(tile + (idx / K8) * pitch + (idx % K8) * 8) = reg[i];
+  }
+}
+
+template <int DP, bool VEC>
+__global__ __launch_bounds__(WIDE_THREADS, 1) void gla_fwd_wide_kernel(
+    const bf16* __restrict__ fq, const bf16* __restrict__ fk, const bf16* __restrict__ v,
+    const float* __restrict__ log_gamma, bf16* __restrict__ y,
+    const float* __restrict__ seg_state, float* __restrict__ final_state, int H, int L, int F,
+    int D, int gate_per_head, int G, int cps, int M, int KG) {
+  using Cfg = GlaFwdWide<DP>;
+  constexpr int FP = Cfg::FP, C = Cfg::C, PF = Cfg::PF, PD = Cfg::PD;
+  constexpr int NFT = Cfg::NFT, NDT = Cfg::NDT, S_OWN = Cfg::S_OWN;
+  extern __shared__ __align__(16) char smem[];
+  bf16* fq_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_FQ);
+  bf16* fk_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_FK);
+  bf16* v_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_V);
+  bf16* st_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_ST);
+  bf16x8* pfrag = reinterpret_cast<bf16x8*>(smem + Cfg::OFF_PF);
+  float* rs = reinterpret_cast<float*>(smem + Cfg::OFF_RS);
+  float* qz = reinterpret_cast<float*>(smem + Cfg::OFF_QZ);
+  float* lgs = reinterpret_cast<float*>(smem + Cfg::OFF_LG);
+  float* qs = reinterpret_cast<float*>(smem + Cfg::OFF_QS);
+  float* ks = reinterpret_cast<float*>(smem + Cfg::OFF_KS);
+  float* zs = reinterpret_cast<float*>(smem + Cfg::OFF_Z);
+  float* zp = reinterpret_cast<float*>(smem + Cfg::OFF_ZP);
+  float* rdec = reinterpret_cast<float*>(smem + Cfg::OFF_R);
+
+  const int nwg = G / M;
+  const int bh = blockIdx.x / nwg, seg = (blockIdx.x % nwg) * M;
+  const int NT = (L + C - 1) / C;
+  const int n0 = seg * cps, n1 = min(NT, n0 + M * cps);
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int col = lane & 31, h = lane >> 5;
+  const bool vecF = VEC || (F & 7) == 0, vecD = VEC || (D & 7) == 0;
+  const bf16* fqb = fq + (size_t)bh * L * F;
+  const bf16* fkb = fk + (size_t)(bh / KG) * L * F;   // fk, v: the kv head of this query head
+  const bf16* vb = v + (size_t)(bh / KG) * L * D;
+  const rsrc_t yr = make_rsrc(y + (size_t)bh * L * D, (size_t)L * D * 2);
+  const float* lgb = log_gamma + (size_t)(gate_per_head ? bh : bh / H) * L;
+  const float* st = G > 1 ? seg_state + ((size_t)bh * G + seg) * SegRec<FP, DP>::SIZE : nullptr;
+
+  // state tile i of this wave: t = wave + 8 i -> f-tile t % NFT, d-tile t / NFT
+  f32x16 S[S_OWN];
+#pragma unroll
+  for (int i = 0; i < S_OWN; ++i) {
+    S[i] = zero16();
+    const int t = wave + 8 * i, ft = t % NFT, dt = t / NFT;
+    if (st && t < NFT * NDT) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) S[i][r] = st[(ft * 32 + acc_row(r, h)) * DP + dt * 32 + col];
+    }
+  }
+  for (int f = tid; f < FP; f += WIDE_THREADS) zs[f] = st ? st[FP * DP + f] : 0.f;
+  // bf16 S^T [d][f] (4 consecutive f per store), read by the output products
+  auto publish = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < S_OWN; ++i) {
+      const int t = wave + 8 * i;
+      if (t < NFT * NDT) {
+        const int ft = t % NFT, d = (t / NFT) * 32 + col;
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          bf16x4 o;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[e] = to_bf16(S[i][4 * g4 + e]);
+          *reinterpret_cast<bf16x4*>(st_l + d * PF + ft * 32 + 8 * g4 + 4 * h) = o;
+        }
+      }
+    }
+  };
+
+  uint4 rq[Cfg::NLF], rk[Cfg::NLF], rv[Cfg::NLD];
+  float rg;
+  load_chunk512<FP>(rq, fqb, n0 * C, L, F, vecF);
+  load_chunk512<FP>(rk, fkb, n0 * C, L, F, vecF);
+  load_chunk512<DP>(rv, vb, n0 * C, L, D, vecD);
+  rg = gate_at(lgb, n0 * C + lane, L);
+  store_chunk512<FP>(rq, fq_l, PF);
+  store_chunk512<FP>(rk, fk_l, PF);
+  store_chunk512<DP>(rv, v_l, PD);
+  if (wave == 0) gate_scan(rg, lane, lgs, qs, ks, rdec);
+  publish();
+  __syncthreads();
+
+  // phase-1 roles: score tile (kt, qt) of waves 0, 1, 3; Q~.z groups of wave
+  // 2 (5/8 of them) and waves 4-7 (the rest, a quarter each)
+  constexpr int NG = FP / 8, G2 = NG * 5 / 8, GR = NG - G2;
+  const int g0 = wave == 2 ? 0 : G2 + (wave - 4) * GR / 4;
+  const int g1 = wave == 2 ? G2 : G2 + (wave - 3) * GR / 4;
+  const bool qz_wave = wave == 2 || wave >= 4;
+  for (int n = n0; n < n1; ++n) {
+    const int t0 = n * C;
+    const bool more = n + 1 < n1;
+    if (more) {   // next chunk in flight while this one computes
+      load_chunk512<FP>(rq, fqb, t0 + C, L, F, vecF);
+      load_chunk512<FP>(rk, fkb, t0 + C, L, F, vecF);
+      load_chunk512<DP>(rv, vb, t0 + C, L, D, vecD);
+      rg = gate_at(lgb, t0 + C + lane, L);
+    }
+    // ---- phase 1 ------------------------------------------------------------
+    uint4 kti[RowItems<FP>::N];   // waves 4-7: their rows of K~ = bf16(fk * ks)
+    if (wave < 4 && wave != 2) {
+      const int kt = wave >> 1, qt = wave & 1;
+      const int qi = qt * 32 + col;
+      f32x16 s = zero16();
+#pragma unroll
+      for (int kb = 0; kb < FP / 16; ++kb)
+        s = mfma(row_operand(fk_l, PF, kt * 32 + col, 16 * kb, h),
+                 row_operand(fq_l, PF, qi, 16 * kb, h), s);
+      const float lgq = lgs[qi];
+      bf16x8 p[2];
+      float rsum = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = kt * 32 + acc_row(r, h);
+        const float val = key <= qi ? s[r] * fexp(lgq - lgs[key]) : 0.f;
+        const bf16 pb = to_bf16(val);
+        p[r >> 3][r & 7] = pb;
+        rsum += to_f32(pb);
+      }
+      rsum += xhalf(rsum);
+      pfrag[(qt * 4 + kt * 2 + 0) * 64 + lane] = p[0];
+      pfrag[(qt * 4 + kt * 2 + 1) * 64 + lane] = p[1];
+      if (h == 0) rs[kt * 64 + qi] = rsum;
+    }
+    if (wave == 2 && h == 0) rs[64 + col] = 0.f;   // keys 32-63 x queries 0-31: zero
+    if (qz_wave) {
+      float acc = 0.f;
+#pragma unroll 2
+      for (int g = g0; g < g1; ++g) {
+        const bf16x8 x = *reinterpret_cast<const bf16x8*>(fq_l + lane * PF + 8 * g);
+        const f32x4 z0 = *reinterpret_cast<const f32x4*>(zs + 8 * g);
+        const f32x4 z1 = *reinterpret_cast<const f32x4*>(zs + 8 * g + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc += to_f32(x[e]) * z0[e];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc += to_f32(x[4 + e]) * z1[e];
+      }
+      qz[wave * 64 + lane] = acc * qs[lane];
+    }
+    if (wave >= 4) scale_rows_t<FP>(fk_l, PF, ks, kti, zp, tid - 256);
+    __syncthreads();
+    if (wave >= 4) store_rows_t<FP>(kti, fk_l, PF, tid - 256);   // fk_l holds K~ from here
+    __syncthreads();
+    // ---- phase 2: outputs (waves 4 .. 3 + 2 NDT), state update (all) ---------
+    const float r_n = rdec[0];
+    if (wave >= 4 && wave < 4 + 2 * NDT) {
+      const int dt = (wave - 4) >> 1, qt = (wave - 4) & 1;
+      const int qi = qt * 32 + col;
+      f32x16 o = zero16();
+#pragma unroll
+      for (int kb = 0; kb < FP / 16; ++kb)
+        o = mfma(row_operand_acc(st_l, PF, dt * 32 + col, 16 * kb, h),
+                 row_operand_acc(fq_l, PF, qi, 16 * kb, h), o);
+      const float qsv = qs[qi];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[r] *= qsv;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)   // queries 0-31 have no keys in blocks 2, 3
+        if (qt == 1 || kb < 2)
+          o = mfma(tr_operand(v_l, PD, 16 * kb, dt * 32, lane), pfrag[(qt * 4 + kb) * 64 + lane], o);
+      float den = rs[qi] + rs[64 + qi] + qz[2 * 64 + qi];
+#pragma unroll
+      for (int w = 4; w < 8; ++w) den += qz[w * 64 + qi];
+      const float inv = 1.f / fmaxf(den, TINY);
+      store_acc_row_bf16(yr, t0 + qi, dt * 32, D, vecD, o, inv, h);
+    }
+#pragma unroll
+    for (int i = 0; i < S_OWN; ++i) {
+      const int t = wave + 8 * i, ft = t % NFT, dt = t / NFT;
+      if (t < NFT * NDT) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) S[i][r] *= r_n;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+          S[i] = mfma(tr_operand(fk_l, PF, 16 * kb, ft * 32, lane),
+                      tr_operand(v_l, PD, 16 * kb, dt * 32, lane), S[i]);
+      }
+    }
+    __syncthreads();
+    // ---- publish S^T; next chunk into LDS; z update ---------------------------
+    publish();
+    if (more) {
+      store_chunk512<FP>(rq, fq_l, PF);
+      store_chunk512<FP>(rk, fk_l, PF);
+      store_chunk512<DP>(rv, v_l, PD);
+      if (wave == 0) gate_scan(rg, lane, lgs, qs, ks, rdec);
+    }
+    if (tid < FP) zs[tid] = zs[tid] * r_n + sum_parts<FP>(zp, tid);
+    __syncthreads();
+  }
+
+  // the state after the whole sequence, [F][D] fp32 then z [F], for decoding
+  if (final_state && seg + M == G) {
+    float* fs = final_state + (size_t)bh * ((size_t)F * D + F);
+#pragma unroll
+    for (int i = 0; i < S_OWN; ++i) {
+      const int t = wave + 8 * i, ft = t % NFT, dt = t / NFT;
+      if (t < NFT * NDT) {
+        const int d = dt * 32 + col;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int f = ft * 32 + acc_row(r, h);
+          if (f < F && d < D) fs[(size_t)f * D + d] = S[i][r];
+        }
+      }
+    }
+    for (int f = tid; f < F; f += WIDE_THREADS) fs[(size_t)F * D + f] = zs[f];
+  }
+}
+
+// ----------------------------------------------------------------------------
 // decode step: one token per (b, h) on the recurrent form
 //   S <- gamma S + fk v^T,  z <- gamma z + fk,  y = fq S / max(fq . z, FLT_MIN)
 // (tests/test_lizard.py:41-52 of the reference), state [F][D] fp32 then z [F]
@@ -739,14 +1010,26 @@ static hipError_t launch_gla_fwd_t(const void* fq, const void* fk, const void* v
                                                    D, gate_per_head, G, cps, KG, st);
     if (e != hipSuccess) return e;
   }
-  auto kern = gla_fwd_kernel<FP, DP, VEC>;
-  hipError_t e = ensure_lds<gla_fwd_kernel<FP, DP, VEC>>(Cfg::BYTES);
-  if (e != hipSuccess) return e;
   const int M = gla_walk_segments(BH, G, F);
-  hipLaunchKernelGGL(kern, dim3(BH * G / M), dim3(256), Cfg::BYTES, st, (const bf16*)fq,
-                     (const bf16*)fk, (const bf16*)v, lg, (bf16*)y, (const float*)seg_state,
-                     final_state, H, L, F, D, gate_per_head, G, cps, M, KG);
-  return hipGetLastError();
+  if constexpr (FP == 256) {   // eight waves per workgroup
+    using W = GlaFwdWide<DP>;
+    auto kern = gla_fwd_wide_kernel<DP, VEC>;
+    hipError_t e = ensure_lds<gla_fwd_wide_kernel<DP, VEC>>(W::BYTES);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(kern, dim3(BH * G / M), dim3(WIDE_THREADS), W::BYTES, st,
+                       (const bf16*)fq, (const bf16*)fk, (const bf16*)v, lg, (bf16*)y,
+                       (const float*)seg_state, final_state, H, L, F, D, gate_per_head, G, cps,
+                       M, KG);
+    return hipGetLastError();
+  } else {
+    auto kern = gla_fwd_kernel<FP, DP, VEC>;
+    hipError_t e = ensure_lds<gla_fwd_kernel<FP, DP, VEC>>(Cfg::BYTES);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(kern, dim3(BH * G / M), dim3(256), Cfg::BYTES, st, (const bf16*)fq,
+                       (const bf16*)fk, (const bf16*)v, lg, (bf16*)y, (const float*)seg_state,
+                       final_state, H, L, F, D, gate_per_head, G, cps, M, KG);
+    return hipGetLastError();
+  }
 }
 
 hipError_t launch_gla_fwd(const void* fq, const void* fk, const void* v, const float* lg, void* y,

@@ -50,7 +50,7 @@ def test_gla_with_strong_decay_matches_oracle():
 
 
 @pytest.mark.parametrize("features, dim", [(64, 64), (128, 128), (256, 64), (32, 128), (128, 32),
-                                           (40, 72)])
+                                           (40, 72), (256, 32), (232, 64), (256, 40)])
 def test_gla_feature_and_value_dims(features, dim):
     inputs = gla_inputs(150, batch=1, heads=2, features=features, dim=dim)
     grad = torch.randn(inputs[2].shape, generator=torch.Generator().manual_seed(1))
@@ -136,6 +136,18 @@ def test_gla_segments_of_several_chunks(length):
     inputs = gla_inputs(length, batch=4, heads=16, features=64, dim=64)
     grad = torch.randn(inputs[2].shape, generator=torch.Generator().manual_seed(1))
     compare(gla_kernel(64), gla_reference, inputs, grad, label=f"segments L={length}")
+
+
+@pytest.mark.parametrize("batch, heads, length, dim, per_head", [
+    (1, 2, 64 * 11 + 5, 64, True), (2, 3, 64 * 9, 32, False), (1, 1, 1, 64, False)])
+def test_gla_wide_features_segments(batch, heads, length, dim, per_head):
+    # F = 256 (the eight-wave walk): small B*H, so the sequence is split into
+    # segments and each walk workgroup takes two of them
+    inputs = gla_inputs(length, gates=(heads,) if per_head else (), batch=batch, heads=heads,
+                        features=256, dim=dim, seed=5)
+    grad = torch.randn(inputs[2].shape, generator=torch.Generator().manual_seed(1))
+    compare(gla_kernel(64), gla_reference, inputs, grad,
+            label=f"F=256 D={dim} B*H={batch * heads} L={length}")
 
 
 def test_gla_backward_without_forward_workspace_is_bitwise_equal():
