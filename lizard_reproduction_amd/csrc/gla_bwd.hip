@@ -513,7 +513,7 @@ __device__ __forceinline__ TokScalars load_scalars(const float* __restrict__ lgb
 template <int FP, int DP>
 struct BwdS : BwdCommon<FP, DP> {
   using B_ = BwdCommon<FP, DP>;
-  static constexpr int C = B_::C, PF = B_::PF, PD = B_::PD, ZPARTS = B_::ZPARTS;
+  static constexpr int C = B_::C, PF = B_::PF, PD = B_::PD;
   static constexpr int OFF_FQ = 0;
   static constexpr int OFF_DY = OFF_FQ + C * PF * 2;
   static constexpr int OFF_DYH = OFF_DY + C * PD * 2;     // dY^ = bf16(qh dy)
@@ -526,13 +526,13 @@ struct BwdS : BwdCommon<FP, DP> {
   static constexpr int OFF_DW = OFF_QH + 64 * 4;
   static constexpr int OFF_DZ = OFF_DW + 64 * 4;
   static constexpr int OFF_DZP = OFF_DZ + FP * 4;
-  static constexpr int OFF_R = OFF_DZP + ZPARTS * FP * 4;
+  static constexpr int OFF_R = OFF_DZP + 2048 * 4;        // 2048 partial sums (column_sums)
   static constexpr int BYTES = OFF_R + 16;
-  static_assert(BYTES <= 160 * 1024, "LDS budget");
+  static_assert(BYTES <= 80 * 1024, "LDS budget: two workgroups per CU");
 };
 
 template <int FP, int DP, bool VEC>
-__global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_bwd_state_kernel(
+__global__ __launch_bounds__(256, 2) void gla_bwd_state_kernel(
     const bf16* __restrict__ fq, const bf16* __restrict__ dy, const float* __restrict__ log_gamma,
     const float* __restrict__ den_in, const float* __restrict__ delta_in,
     float* __restrict__ seg_state, float* __restrict__ seg_logdecay, int H, int L, int F, int D,
@@ -591,16 +591,7 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_bwd_state_kernel(
     // dY^ = bf16(qh dy), formed once per chunk; dz partials sum_i fq_i (qh_i delta_i)
     scale_rows_only<DP>(dy_l, PD, qh, rh);
     store_rows<DP>(rh, dyh_l, PD);
-    {
-      constexpr int TPP = C / Cfg::ZPARTS;
-      const int f = tid % FP, part = tid / FP;
-      if (part < Cfg::ZPARTS) {
-        float za = 0.f;
-#pragma unroll 8
-        for (int t = part * TPP; t < (part + 1) * TPP; ++t) za += to_f32(fq_l[t * PF + f]) * dw[t];
-        dzp[part * FP + f] = za;
-      }
-    }
+    column_sums<FP, false>(fq_l, PF, dw, dzp);
     __syncthreads();
     const float r_n = rdec[0];
     if (wave == 0) lam += rdec[1];
@@ -625,12 +616,7 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_bwd_state_kernel(
         bwd_scalars(sc.g, sc.den, sc.delta, 0.f, lane, lgs, qs, ks, rdec, invd, dels, nullptr, qh,
                     dw);
     }
-    if (tid < FP) {
-      float za = dzs[tid] * r_n;
-#pragma unroll
-      for (int p = 0; p < Cfg::ZPARTS; ++p) za += dzp[p * FP + tid];
-      dzs[tid] = za;
-    }
+    if (tid < FP) dzs[tid] = dzs[tid] * r_n + sum_parts<FP>(dzp, tid);
     __syncthreads();
   }
   float* out = seg_state + ((size_t)bh * G + seg) * Cfg::SEG;

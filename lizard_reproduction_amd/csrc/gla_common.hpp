@@ -127,6 +127,34 @@ __device__ __forceinline__ void store_rows_t(const uint4 (&in)[RowItems<KP>::N],
     *reinterpret_cast<uint4*>(tile + (r0 + R::RSTRIDE * i) * pitch + 8 * cg) = in[i];
 }
 
+// The column sums of scale_rows alone, for a tile that is not rewritten:
+// thread tid sums x[t][c] * scale[t] (rounded to bf16 first if ROUND, as
+// scale_rows' values are) over its rows t = tid / (KP/8) + (2048/KP) i and its
+// 8 columns c, into the same part[] layout (16-byte reads).
+template <int KP, bool ROUND = true>
+__device__ __forceinline__ void column_sums(const bf16* tile, int pitch, const float* scale,
+                                            float* part) {
+  using R = RowItems<KP>;
+  const int cg = threadIdx.x % R::K8, r0 = threadIdx.x / R::K8;
+  float sum[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) sum[e] = 0.f;
+#pragma unroll
+  for (int i = 0; i < R::N; ++i) {
+    const int t = r0 + R::RSTRIDE * i;
+    const bf16x8 x = *reinterpret_cast<const bf16x8*>(tile + t * pitch + 8 * cg);
+    const float s = scale[t];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float p = to_f32(x[e]) * s;
+      sum[e] += ROUND ? to_f32(to_bf16(p)) : p;
+    }
+  }
+  float* dst = part + r0 * KP + 8 * cg;
+  *reinterpret_cast<f32x4*>(dst) = f32x4{sum[0], sum[1], sum[2], sum[3]};
+  *reinterpret_cast<f32x4*>(dst + 4) = f32x4{sum[4], sum[5], sum[6], sum[7]};
+}
+
 // column c of the partial sums written by scale_rows (threads with tid < KP)
 template <int KP>
 __device__ __forceinline__ float sum_parts(const float* part, int c) {

@@ -730,7 +730,6 @@ struct GlaState {
   static constexpr int C = GLA_C;
   static constexpr int PF = lds_pitch(FP), PD = lds_pitch(DP);
   static constexpr int NFT = FP / 32, NDT = DP / 32;
-  static constexpr int ZPARTS = FP >= 256 ? 1 : 256 / FP;
   static constexpr int NLF = C * FP / 8 / 256;        // 16-byte loads per thread, fk
   static constexpr int NLD = C * DP / 8 / 256;        // 16-byte loads per thread, v
   static constexpr int OFF_FK = 0;
@@ -739,8 +738,8 @@ struct GlaState {
   static constexpr int OFF_QS = OFF_LG + 64 * 4;          // [64] e^{lg} (written by gate_scan)
   static constexpr int OFF_KS = OFF_QS + 64 * 4;          // [64] e^{lg_end - lg}
   static constexpr int OFF_Z = OFF_KS + 64 * 4;           // [FP] z
-  static constexpr int OFF_ZP = OFF_Z + FP * 4;           // [ZPARTS][FP] partial sums of K~
-  static constexpr int OFF_R = OFF_ZP + ZPARTS * FP * 4;  // e^{lg_end}, lg_end
+  static constexpr int OFF_ZP = OFF_Z + FP * 4;           // 2048 partial sums of K~ (column_sums)
+  static constexpr int OFF_R = OFF_ZP + 2048 * 4;         // e^{lg_end}, lg_end
   static constexpr int BYTES = OFF_R + 16;
   static constexpr int SEG = SegRec<FP, DP>::SIZE;
   static_assert(BYTES <= 80 * 1024, "LDS budget: two workgroups per CU");
@@ -817,29 +816,14 @@ __global__ __launch_bounds__(256, 2) void gla_fwd_state_kernel(
         }
       }
     }
-    {
-      constexpr int TPP = C / Cfg::ZPARTS;
-      const int f = tid % FP, part = tid / FP;
-      if (part < Cfg::ZPARTS) {
-        float za = 0.f;
-#pragma unroll 8
-        for (int t = part * TPP; t < (part + 1) * TPP; ++t)
-          za += to_f32(to_bf16(to_f32(fk_l[t * PF + f]) * ks[t]));
-        zp[part * FP + f] = za;
-      }
-    }
+    column_sums<FP>(fk_l, PF, ks, zp);   // z's share of this chunk, as partial sums
     __syncthreads();
     if (more) {
       store_chunk<FP>(rk, fk_l, PF);
       store_chunk<DP>(rv, v_l, PD);
       if (wave == 0) gate_scan(rg, lane, lgs, qs, ks, rdec);
     }
-    if (tid < FP) {
-      float za = zs[tid] * r_n;
-#pragma unroll
-      for (int p = 0; p < Cfg::ZPARTS; ++p) za += zp[p * FP + tid];
-      zs[tid] = za;
-    }
+    if (tid < FP) zs[tid] = zs[tid] * r_n + sum_parts<FP>(zp, tid);
     __syncthreads();
   }
   float* out = seg_state + ((size_t)bh * G + seg) * Cfg::SEG;
