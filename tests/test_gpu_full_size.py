@@ -77,3 +77,41 @@ def test_headline_shape_is_deterministic():
         runs.append([y.detach()] + [t.grad for t in leaves])
     for a, b in zip(*runs):
         assert torch.equal(a, b)
+
+
+def test_config5_attention_shape_slices_match_chunked_oracle():
+    """The layer's GLA call at BASELINE config 5: B=4, H=32, L=4096, F=256
+    (Hedgehog maps [softmax(x), softmax(-x)] of 128 features), D=64, one gate
+    per token (logsigmoid(N(3, 1))); forward and backward on the whole batch,
+    sampled (b, h) slices against the chunked fp64 oracle."""
+    g = torch.Generator().manual_seed(9)
+    b, h, length = 4, 32, 4096
+
+    def hedgehog(x):
+        return torch.cat([x.softmax(-1), (-x).softmax(-1)], -1).bfloat16()
+    fq = hedgehog(torch.randn(b, h, length, 128, generator=g))
+    fk = hedgehog(torch.randn(b, h, length, 128, generator=g))
+    v = torch.randn(b, h, length, 64, generator=g).bfloat16()
+    lg = F.logsigmoid(3 + torch.randn(b, length, generator=g))
+    dy = torch.randn(b, h, length, 64, generator=g).bfloat16()
+    ours = [t.cuda().requires_grad_() for t in (fq, fk, v, lg)]
+    y = kernels.gla(*ours)
+    y.backward(dy.cuda())
+    torch.cuda.synchronize()
+    worst = {}
+    for bi, hi in [(0, 0), (2, 17), (3, 31)]:
+        sl = [t[bi:bi + 1, hi:hi + 1].double().requires_grad_() for t in (fq, fk, v)]
+        gl = lg[bi:bi + 1].double().requires_grad_()
+        ref = lo.gla_chunked(*sl, gl, 64)
+        ref.backward(dy[bi:bi + 1, hi:hi + 1].double())
+        pairs = {"y": (y[bi, hi], ref[0, 0]), "dfq": (ours[0].grad[bi, hi], sl[0].grad[0, 0]),
+                 "dfk": (ours[1].grad[bi, hi], sl[1].grad[0, 0]),
+                 "dv": (ours[2].grad[bi, hi], sl[2].grad[0, 0])}
+        for k, (a, r) in pairs.items():
+            worst[k] = max(worst.get(k, 0.0), max_rel(a, r))
+    print("[parity] config5 attention slices: " +
+          " ".join(f"{k}={v:.2e}" for k, v in worst.items()), flush=True)
+    assert worst["y"] <= OUT_TOL, worst
+    for k, e in worst.items():
+        if k != "y":
+            assert e <= GRAD_TOL, (k, worst)
