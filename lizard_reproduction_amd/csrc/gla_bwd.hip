@@ -993,56 +993,44 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
 
 // ============================================================================
 // d log_gamma[row, j] = sum_{j' >= j} value[row, j'], value = dG of that (b, h)
-// row (per-head gate) or its sum over the heads (per-token gate).  One block
-// per (row, 64-token chunk): the chunk sums of dG the reverse walk left for
-// every later chunk, plus a suffix scan inside the chunk.  Fixed order
-// throughout.
+// row (per-head gate) or its sum over the heads (per-token gate).  One wave
+// per (row, 64-token chunk), four chunks per workgroup, no barriers: the wave
+// sums the chunk totals of dG the reverse walk left for every later chunk
+// (lanes over (head, chunk) pairs, then a shuffle tree), and lane t holds
+// token t of the chunk summed over the heads for an inclusive suffix scan by
+// shuffles.  Fixed order throughout.
 // ============================================================================
-// Fixed-order tree sum of one value per thread (all 256 threads call it).
-__device__ __forceinline__ float block_sum256(float* sh, float x) {
-  const int tid = threadIdx.x;
-  sh[tid] = x;
-  __syncthreads();
-  for (int off = 128; off > 0; off >>= 1) {
-    if (tid < off) sh[tid] += sh[tid + off];
-    __syncthreads();
-  }
-  const float s = sh[0];
-  __syncthreads();
-  return s;
-}
+constexpr int GATE_CHUNKS_PER_WG = 4;
 
-__global__ __launch_bounds__(256) void gla_gate_grad_kernel(const float* __restrict__ dG,
-                                                            const float* __restrict__ csum,
-                                                            float* __restrict__ dlg, int H, int L,
-                                                            int gate_per_head) {
-  __shared__ float sh[256];
-  const int row = blockIdx.y, c = blockIdx.x, tid = threadIdx.x;
+__global__ __launch_bounds__(64 * GATE_CHUNKS_PER_WG) void gla_gate_grad_kernel(
+    const float* __restrict__ dG, const float* __restrict__ csum, float* __restrict__ dlg, int H,
+    int L, int gate_per_head) {
+  const int row = blockIdx.y, lane = threadIdx.x & 63;
   const int NT = (L + GLA_C - 1) / GLA_C;
+  const int c = blockIdx.x * GATE_CHUNKS_PER_WG + (threadIdx.x >> 6);
+  if (c >= NT) return;   // whole waves; nothing below synchronises across waves
   const int nsum = gate_per_head ? 1 : H;
   const float* src = dG + (size_t)row * nsum * L;
   const float* cs = csum + (size_t)row * nsum * NT;
   const int nc = NT - c - 1;   // chunks after this one
   float after = 0.f;
-  for (int idx = tid; idx < nc * nsum; idx += 256)
+#pragma unroll 4
+  for (int idx = lane; idx < nc * nsum; idx += 64)
     after += cs[(size_t)(idx / nc) * NT + c + 1 + idx % nc];
-  after = block_sum256(sh, after);
-  // token t of the chunk, heads hg, hg + 4, ... (four head groups per token)
-  const int t = tid & 63, hg = tid >> 6, j = c * GLA_C + t;
-  float x = 0.f;
-  if (j < L)
-    for (int hh = hg; hh < nsum; hh += 4) x += src[(size_t)hh * L + j];
-  sh[tid] = x;
-  __syncthreads();
-  if (tid < 64) {
-    float val = sh[t] + sh[64 + t] + sh[128 + t] + sh[192 + t];
 #pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {   // inclusive suffix scan over the chunk
-      const float o = __shfl_down(val, off);
-      if (t + off < 64) val += o;
-    }
-    if (j < L) dlg[(size_t)row * L + j] = after + val;
+  for (int off = 32; off >= 1; off >>= 1) after += __shfl_xor(after, off);
+  const int j = c * GLA_C + lane;
+  float val = 0.f;
+  if (j < L) {
+#pragma unroll 8
+    for (int hh = 0; hh < nsum; ++hh) val += src[(size_t)hh * L + j];
   }
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {   // inclusive suffix scan over the chunk
+    const float o = __shfl_down(val, off);
+    if (lane + off < 64) val += o;
+  }
+  if (j < L) dlg[(size_t)row * L + j] = after + val;
 }
 
 // ============================================================================
@@ -1115,8 +1103,11 @@ static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v
                      (const float*)delta, (const float*)p, (OutT*)dfk, (OutT*)dv, dG, csum,
                      (const float*)rseg, H, L, F, D, gate_per_head, G, cps, M, KG);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  const dim3 ggrid((L + GLA_C - 1) / GLA_C, gate_rows(B, H, gate_per_head));
-  hipLaunchKernelGGL(gla_gate_grad_kernel, ggrid, dim3(256), 0, st, (const float*)dG,
+  const int nt = (L + GLA_C - 1) / GLA_C;
+  const dim3 ggrid((nt + GATE_CHUNKS_PER_WG - 1) / GATE_CHUNKS_PER_WG,
+                   gate_rows(B, H, gate_per_head));
+  hipLaunchKernelGGL(gla_gate_grad_kernel, ggrid, dim3(64 * GATE_CHUNKS_PER_WG), 0, st,
+                     (const float*)dG,
                      (const float*)csum, dlg, H, L, gate_per_head);
   return hipGetLastError();
 }
