@@ -73,6 +73,33 @@ def test_bad_sizes_are_rejected_before_any_launch(lib):
     assert rc != 0 and b"kv_heads" in lib.lz_last_error()
 
 
+def test_decode_entry_points_reject_bad_arguments(lib):
+    p = ctypes.c_void_p(16)   # never dereferenced: validation fails first
+    # lz_swa_decode_step(q, k_cache, v_cache, meta, n_meta, y, B, H, kv_heads, window, dim,
+    #                    pos, scale, stream)
+    sd = lib.lz_swa_decode_step
+    assert sd(p, p, p, p, 4, None, 1, 4, 2, 64, 64, 0, 0.125, None) != 0
+    assert b"null" in lib.lz_last_error()
+    assert sd(p, p, p, p, 4, p, 1, 4, 3, 64, 64, 0, 0.125, None) != 0
+    assert b"kv_heads" in lib.lz_last_error()
+    assert sd(p, p, p, p, 4, p, 1, 4, 2, 8193, 64, 0, 0.125, None) != 0
+    assert b"window" in lib.lz_last_error()
+    assert sd(p, p, p, p, 4, p, 1, 4, 2, 64, 64, -1, 0.125, None) != 0
+    assert b"pos" in lib.lz_last_error()
+    assert sd(p, p, p, p, 4, p, 1, 4, 2, 64, 512, 0, 0.125, None) != 0
+    assert b"dim" in lib.lz_last_error()
+    assert sd(p, p, p, p, 65, p, 1, 4, 2, 64, 64, 0, 0.125, None) != 0
+    assert b"n_meta" in lib.lz_last_error()
+    # lz_gla_decode_step(fq, fk, v, log_gamma, state, y, B, H, kv_heads, F, D, per_head, stream)
+    gd = lib.lz_gla_decode_step
+    assert gd(p, p, p, p, p, p, 1, 4, 3, 64, 64, 0, None) != 0
+    assert b"kv_heads" in lib.lz_last_error()
+    assert gd(p, p, p, p, None, p, 1, 4, 2, 64, 64, 0, None) != 0
+    assert b"null" in lib.lz_last_error()
+    assert gd(p, p, p, p, p, p, 1, 4, 2, 300, 64, 0, None) != 0
+    assert b"unsupported" in lib.lz_last_error()
+
+
 def test_layer_entry_points_reject_bad_arguments(lib):
     p = ctypes.c_void_p(16)   # never dereferenced: validation fails first
     fwd = lib.lz_layer_prologue_fwd
