@@ -45,7 +45,6 @@ struct BwdCommon {
   static constexpr int C = GLA_C;
   static constexpr int PF = lds_pitch(FP), PD = lds_pitch(DP);
   static constexpr int NFT = FP / 32, NDT = DP / 32;
-  static constexpr int ZPARTS = FP >= 256 ? 1 : 256 / FP;
   static constexpr int NLF = C * FP / 8 / 256, NLD = C * DP / 8 / 256;
   static constexpr int SEG = SegRec<FP, DP>::SIZE;
 };
@@ -99,7 +98,6 @@ template <int FP, int DP>
 struct BwdA : BwdCommon<FP, DP> {
   using B_ = BwdCommon<FP, DP>;
   static constexpr int C = B_::C, PF = B_::PF, PD = B_::PD, NFT = B_::NFT, NDT = B_::NDT;
-  static constexpr int ZPARTS = B_::ZPARTS;
   static constexpr bool SREG = NFT >= B_WAVES;    // S by f-tile in registers, no LDS copy
   static constexpr int S_OWN = SREG ? NDT * (NFT / B_WAVES) : (NFT * NDT + B_WAVES - 1) / B_WAVES;
   static constexpr int XJ = SREG ? 2 * (NFT / B_WAVES) : 1;   // X jobs per wave

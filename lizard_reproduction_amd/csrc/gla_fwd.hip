@@ -53,7 +53,6 @@ struct GlaFwd {
   static constexpr int C = GLA_C;
   static constexpr int PF = lds_pitch(FP), PD = lds_pitch(DP);   // LDS row pitches
   static constexpr int NFT = FP / 32, NDT = DP / 32;
-  static constexpr int ZPARTS = FP >= 256 ? 1 : 256 / FP;
   static constexpr int NLF = C * FP / 8 / 256;        // 16-byte loads per thread, fq or fk
   static constexpr int NLD = C * DP / 8 / 256;        // 16-byte loads per thread, v
   static constexpr int OFF_FQ = 0;
