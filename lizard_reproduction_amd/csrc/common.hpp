@@ -313,8 +313,8 @@ __device__ __forceinline__ void store_acc_row_bf16(rsrc_t r, int row, int c0, in
 // The same row of a [nrows x ncols] OutT matrix at base: bf16 through
 // store_acc_row_bf16 (vec: ncols % 8 == 0); fp32 as four 16-byte stores per
 // lane (already whole 16-byte pieces).  Every lane of the wave must take part
-// (the bf16 form swaps registers between lane halves); rows at or past nrows
-// are skipped.
+// (the bf16 form swaps registers between lane halves); rows below 0 or at or
+// past nrows are skipped (bf16: dropped by the buffer range check).
 template <typename OutT>
 __device__ __forceinline__ void store_acc_row(OutT* __restrict__ base, int row, int c0, int nrows,
                                               int ncols, bool vec, const f32x16& g, float scale,
@@ -323,7 +323,7 @@ __device__ __forceinline__ void store_acc_row(OutT* __restrict__ base, int row, 
     store_acc_row_bf16(make_rsrc(base, (size_t)nrows * ncols * 2), row, c0, ncols, vec, g, scale,
                        h);
   } else {
-    if (row < nrows) {
+    if (row >= 0 && row < nrows) {
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4)
         store4<OutT>(base, row, c0 + 8 * g4 + 4 * h, ncols, g[4 * g4] * scale,
