@@ -438,6 +438,13 @@ def main():
         "fwd_bwd_ms": round(t_fb, 4),
         "fwd_tflops": round(gla_fwd_flops(32, 2048, 64, 64) / t_f / 1e9, 2),
         "fwd_bwd_tflops": round(gla_fwd_bwd_flops(32, 2048, 64, 64) / t_fb / 1e9, 2)}
+    # the same fwd+bwd as back-to-back C-ABI launches without autograd: what
+    # the kernels sustain when the host keeps ahead of them (the autograd
+    # figure above is bound by torch's host-side cost at this size)
+    def gla_launches():
+        _, state = kernels.gla_forward(fq, fk, v, lg, keep_state=True)
+        kernels.gla_backward(fq, fk, v, lg, dy, state, torch.bfloat16)
+    extra["config2_gla_train"]["fwd_bwd_launch_ms"] = round(median_ms(torch, gla_launches, 100, 10), 4)
     print(f"[bench] config2: {extra['config2_gla_train']}", file=sys.stderr, flush=True)
     del fq, fk, v, lg, dy, run, reset
 
@@ -454,6 +461,10 @@ def main():
         "fwd_tflops": round(swa_flops(32, 2048, 64, 64, False) / t_f / 1e9, 2),
         "fwd_bwd_tflops": round(swa_flops(32, 2048, 64, 64, True) / t_fb / 1e9, 2),
         "fwd_gbs": round(swa_bytes / t_f / 1e6, 1)}
+    def swa_launches():
+        _, lse = kernels.swa_forward(q, k, v, meta, 64)
+        kernels.swa_backward(q, k, v, meta, lse, dy, 64, torch.bfloat16)
+    extra["config3_swa"]["fwd_bwd_launch_ms"] = round(median_ms(torch, swa_launches, 100, 10), 4)
     print(f"[bench] config3: {extra['config3_swa']}", file=sys.stderr, flush=True)
     del q, k, v, meta, dy, run, reset
     torch.cuda.empty_cache()
