@@ -733,13 +733,14 @@ struct GlaState {
   static constexpr int NLD = C * DP / 8 / 256;        // 16-byte loads per thread, v
   static constexpr int OFF_FK = 0;
   static constexpr int OFF_V = OFF_FK + C * PF * 2;
-  static constexpr int OFF_LG = OFF_V + C * PD * 2;       // [64] chunk-local lg
-  static constexpr int OFF_QS = OFF_LG + 64 * 4;          // [64] e^{lg} (written by gate_scan)
-  static constexpr int OFF_KS = OFF_QS + 64 * 4;          // [64] e^{lg_end - lg}
-  static constexpr int OFF_Z = OFF_KS + 64 * 4;           // [FP] z
-  static constexpr int OFF_ZP = OFF_Z + FP * 4;           // 2048 partial sums of K~ (column_sums)
-  static constexpr int OFF_R = OFF_ZP + 2048 * 4;         // e^{lg_end}, lg_end
-  static constexpr int BYTES = OFF_R + 16;
+  // gate arrays, decays and K~ column sums, one set per chunk parity
+  static constexpr int OFF_LG = OFF_V + C * PD * 2;       // [2][64] chunk-local lg
+  static constexpr int OFF_QS = OFF_LG + 2 * 64 * 4;      // [2][64] e^{lg} (written by gate_scan)
+  static constexpr int OFF_KS = OFF_QS + 2 * 64 * 4;      // [2][64] e^{lg_end - lg}
+  static constexpr int OFF_Z = OFF_KS + 2 * 64 * 4;       // [FP] z
+  static constexpr int OFF_ZP = OFF_Z + FP * 4;           // [2][2048] partial sums of K~
+  static constexpr int OFF_R = OFF_ZP + 2 * 2048 * 4;     // [2][4] e^{lg_end}, lg_end
+  static constexpr int BYTES = OFF_R + 32;
   static constexpr int SEG = SegRec<FP, DP>::SIZE;
   static_assert(BYTES <= 80 * 1024, "LDS budget: two workgroups per CU");
 };
@@ -779,26 +780,62 @@ __global__ __launch_bounds__(256, 2) void gla_fwd_state_kernel(
   for (int f = tid; f < FP; f += 256) zs[f] = 0.f;
   float lam = 0.f;   // total log decay of the segment (wave 0)
 
+  // fk is staged as K~ = bf16(fk ks): each thread scales its prefetched
+  // 16-byte items (the item layout of scale_rows) by the staged chunk's ks
+  // and writes their column sums, so the state update reads ready operands.
+  // That needs the chunk's gate scan before it is staged: wave 0 scans the
+  // next chunk's gates while the current one updates the state, into the
+  // buffers of the other chunk parity.
+  using R = RowItems<FP>;
+  static_assert(Cfg::NLF == R::N, "chunk items follow the scale_rows layout");
+  const int cg = tid % R::K8, r0 = tid / R::K8;
+  auto stage_scaled = [&](const uint4 (&reg)[Cfg::NLF], const float* kss, float* part) {
+    float sum[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sum[e] = 0.f;
+#pragma unroll
+    for (int i = 0; i < R::N; ++i) {
+      const int t = r0 + R::RSTRIDE * i;
+      const bf16x8 x = __builtin_bit_cast(bf16x8, reg[i]);
+      const float sc = kss[t];
+      bf16x8 o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        o[e] = to_bf16(to_f32(x[e]) * sc);
+        sum[e] += to_f32(o[e]);
+      }
+      *reinterpret_cast<bf16x8*>(fk_l + t * PF + 8 * cg) = o;
+    }
+    float* dst = part + r0 * FP + 8 * cg;
+    *reinterpret_cast<f32x4*>(dst) = f32x4{sum[0], sum[1], sum[2], sum[3]};
+    *reinterpret_cast<f32x4*>(dst + 4) = f32x4{sum[4], sum[5], sum[6], sum[7]};
+  };
+
   uint4 rk[Cfg::NLF], rv[Cfg::NLD];
-  float rg;
+  float rg = gate_at(lgb, n0 * C + lane, L);   // the gate first: waited for alone
   load_chunk<FP>(rk, fkb, n0 * C, L, F, vecF);
   load_chunk<DP>(rv, vb, n0 * C, L, D, vecD);
-  rg = gate_at(lgb, n0 * C + lane, L);
-  store_chunk<FP>(rk, fk_l, PF);
-  store_chunk<DP>(rv, v_l, PD);
-  if (wave == 0) gate_scan(rg, lane, lgs, qs, ks, rdec);
-  __syncthreads();
+  {
+    const int pb = n0 & 1;
+    if (wave == 0) gate_scan(rg, lane, lgs + 64 * pb, qs + 64 * pb, ks + 64 * pb, rdec + 4 * pb);
+    __syncthreads();
+    stage_scaled(rk, ks + 64 * pb, zp + 2048 * pb);
+    store_chunk<DP>(rv, v_l, PD);
+    __syncthreads();
+  }
 
   for (int n = n0; n < n1; ++n) {
     const int t0 = n * C;
     const bool more = n + 1 < n1;
-    if (more) {
-      load_chunk<FP>(rk, fkb, t0 + C, L, F, vecF);
-      load_chunk<DP>(rv, vb, t0 + C, L, D, vecD);
-      rg = gate_at(lgb, t0 + C + lane, L);
-    }
-    const float r_n = rdec[0];
-    if (wave == 0) lam += rdec[1];
+    const int pc = n & 1, pn = pc ^ 1;   // this chunk's parity, the next one's
+    // unconditional loads (past the segment they read rows past L: zeros, no
+    // traffic), so the scan below waits for the gate alone
+    const int tn = more ? t0 + C : L;
+    rg = gate_at(lgb, tn + lane, L);
+    load_chunk<FP>(rk, fkb, tn, L, F, vecF);
+    load_chunk<DP>(rv, vb, tn, L, D, vecD);
+    const float r_n = rdec[4 * pc];
+    if (wave == 0) lam += rdec[4 * pc + 1];
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
       const int ti = wave + 4 * i;
@@ -807,22 +844,19 @@ __global__ __launch_bounds__(256, 2) void gla_fwd_state_kernel(
 #pragma unroll
         for (int r = 0; r < 16; ++r) S[i][r] *= r_n;
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-          const f32x4 klo = *reinterpret_cast<const f32x4*>(ks + 16 * kb + 4 * h);
-          const f32x4 khi = *reinterpret_cast<const f32x4*>(ks + 16 * kb + 8 + 4 * h);
-          const bf16x8 a = scale8v(tr_operand(fk_l, PF, 16 * kb, ft * 32, lane), klo, khi);
-          S[i] = mfma(a, tr_operand(v_l, PD, 16 * kb, dt * 32, lane), S[i]);
-        }
+        for (int kb = 0; kb < 4; ++kb)
+          S[i] = mfma(tr_operand(fk_l, PF, 16 * kb, ft * 32, lane),
+                      tr_operand(v_l, PD, 16 * kb, dt * 32, lane), S[i]);
       }
     }
-    column_sums<FP>(fk_l, PF, ks, zp);   // z's share of this chunk, as partial sums
+    if (more && wave == 0)
+      gate_scan(rg, lane, lgs + 64 * pn, qs + 64 * pn, ks + 64 * pn, rdec + 4 * pn);
     __syncthreads();
+    if (tid < FP) zs[tid] = zs[tid] * r_n + sum_parts<FP>(zp + 2048 * pc, tid);
     if (more) {
-      store_chunk<FP>(rk, fk_l, PF);
+      stage_scaled(rk, ks + 64 * pn, zp + 2048 * pn);
       store_chunk<DP>(rv, v_l, PD);
-      if (wave == 0) gate_scan(rg, lane, lgs, qs, ks, rdec);
     }
-    if (tid < FP) zs[tid] = zs[tid] * r_n + sum_parts<FP>(zp, tid);
     __syncthreads();
   }
   float* out = seg_state + ((size_t)bh * G + seg) * Cfg::SEG;
