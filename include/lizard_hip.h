@@ -15,6 +15,9 @@
  *     the call returns without synchronising;
  *   - return value 0 = success; otherwise an error code, with a message
  *     available from lz_last_error() on the calling thread.
+ *   - extents: one (batch, head) slab of fp32 rows, length x max(F, D) x 4
+ *     bytes, stays under 2 GiB, and batch*heads*length under 2^31 - 2^20; the
+ *     kernels address slabs with 32-bit offsets, and larger calls are refused.
  *
  * The reference (mahdikhashan/lizard-reproduction) is pure Python + Triton; the
  * functions below replace its Triton launches.  Each comment names the

@@ -85,6 +85,19 @@ extern "C" int lz_abi_version(void) { return LZ_ABI_VERSION; }
 
 extern "C" const char* lz_last_error(void) { return g_err.c_str(); }
 
+// The kernels address each (batch, head) slab through a buffer resource with a
+// 32-bit range and 32-bit offsets, and index rows (batch, head, token) with
+// 32-bit ints: a slab of fp32 rows must stay under 2 GiB, and B*H*L under 2^31.
+static int check_extent(const char* what, int batch, int heads, int length, int width) {
+  if ((long long)length * width * 4 >= (1LL << 31))
+    return fail(1, "%s: length %d x width %d exceeds the 2 GiB (batch, head) slab limit", what,
+                length, width);
+  if ((long long)batch * heads * length > (1LL << 31) - (1LL << 20))
+    return fail(1, "%s: B*H*L = %lld rows exceeds the 2^31 - 2^20 row limit", what,
+                (long long)batch * heads * length);
+  return 0;
+}
+
 static int check_gla(const void* fq, const void* fk, const void* v, const float* lg, int batch,
                      int heads, int length, int nf, int nd, int chunk) {
   if (!fq || !fk || !v || !lg) return fail(1, "gla: null input pointer");
@@ -95,7 +108,7 @@ static int check_gla(const void* fq, const void* fk, const void* v, const float*
   if (!lz::gla_dims_supported(nf, nd))
     return fail(1, "gla: unsupported feature/value dims F=%d D=%d (need F<=256, D<=128, "
                    "and D<=64 when F>128)", nf, nd);
-  return 0;
+  return check_extent("gla", batch, heads, length, nf > nd ? nf : nd);
 }
 
 // kv_heads heads of k-side operands (fk and v; k and v), each shared by
@@ -206,7 +219,7 @@ static int check_swa(const void* q, const void* k, const void* v, const float* m
     return fail(1, "swa: sizes must be positive (B=%d H=%d L=%d d=%d)", batch, heads, length, dim);
   if (window <= 0) return fail(1, "swa: window must be positive, got %d", window);
   if (lz::swa_padded_dim(dim) < 0) return fail(1, "swa: head dim %d > 256 unsupported", dim);
-  return 0;
+  return check_extent("swa", batch, heads, length, dim);
 }
 
 extern "C" int lz_swa_fwd(const void* q, const void* k, const void* v, const float* meta,

@@ -71,6 +71,17 @@ def test_bad_sizes_are_rejected_before_any_launch(lib):
     assert rc != 0 and b"kv_heads" in lib.lz_last_error()
     rc = lib.lz_swa_fwd(p, p, p, p, 0, p, p, 1, 4, 0, 8, 16, 4, 0.25, None)
     assert rc != 0 and b"kv_heads" in lib.lz_last_error()
+    # 32-bit addressing: a (batch, head) slab of fp32 rows under 2 GiB, B*H*L under 2^31
+    rc = lib.lz_gla_fwd(p, p, p, p, p, 1, 1, 1, 1 << 21, 256, 64, 0, 64, None, 0, None)
+    assert rc != 0 and b"slab" in lib.lz_last_error()
+    rc = lib.lz_gla_fwd(p, p, p, p, p, 1 << 12, 1 << 10, 1 << 10, 1 << 10, 64, 64, 0, 64, None,
+                        0, None)
+    assert rc != 0 and b"row limit" in lib.lz_last_error()
+    rc = lib.lz_swa_fwd(p, p, p, p, 0, p, p, 1, 1, 1, 1 << 22, 128, 64, 0.25, None)
+    assert rc != 0 and b"slab" in lib.lz_last_error()
+    rc = lib.lz_gla_bwd(p, p, p, p, p, p, p, p, p, 0, 1, 1, 1, 1 << 21, 256, 64, 0, 64, None, 0,
+                        p, 1, None)
+    assert rc != 0 and b"slab" in lib.lz_last_error()
 
 
 def test_decode_entry_points_reject_bad_arguments(lib):
