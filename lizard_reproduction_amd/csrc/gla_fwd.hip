@@ -157,6 +157,7 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
       load_chunk<DP>(rv, vb, t0 + C, L, D, vecD);
       rg = gate_at(lgb, t0 + C + lane, L);
     }
+    __builtin_amdgcn_s_setprio(0);
     // ---- phase 1: scores -> P fragments and row sums; fq.z; K~ rows --------
     uint4 kti[RowItems<FP>::N];   // this thread's rows of K~ = bf16(fk * ks)
     {
@@ -252,6 +253,10 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
     }
     __syncthreads();
     // ---- next chunk into LDS; z update ----------------------------------------
+    // the staging of the next chunk and the issue of the loads after it run at
+    // raised wave priority: the other workgroup on the CU is then usually in its
+    // compute phases, and the chunk's loads leave as early as they can
+    __builtin_amdgcn_s_setprio(1);
     if (more) {
       store_chunk<FP>(rq, fq_l, PF);
       store_chunk<FP>(rk, fk_l, PF);
