@@ -839,6 +839,7 @@ __global__ __launch_bounds__(256, 2) void gla_fwd_state_kernel(
     rg = gate_at(lgb, tn + lane, L);
     load_chunk<FP>(rk, fkb, tn, L, F, vecF);
     load_chunk<DP>(rv, vb, tn, L, D, vecD);
+    __builtin_amdgcn_s_setprio(0);
     const float r_n = rdec[4 * pc];
     if (wave == 0) lam += rdec[4 * pc + 1];
 #pragma unroll
@@ -857,6 +858,8 @@ __global__ __launch_bounds__(256, 2) void gla_fwd_state_kernel(
     if (more && wave == 0)
       gate_scan(rg, lane, lgs + 64 * pn, qs + 64 * pn, ks + 64 * pn, rdec + 4 * pn);
     __syncthreads();
+    // staging and the next loads at raised wave priority, as in the walk
+    __builtin_amdgcn_s_setprio(1);
     if (tid < FP) zs[tid] = zs[tid] * r_n + sum_parts<FP>(zp + 2048 * pc, tid);
     if (more) {
       stage_scaled(rk, ks + 64 * pn, zp + 2048 * pn);
