@@ -152,14 +152,45 @@ __host__ __device__ constexpr int lds_pitch(int x) {
   return x + (x == 64 ? 8 : (x >= 128 ? 24 : 16));
 }
 
-// Workgroups are dispatched round-robin over the GPU's 8 XCDs (each with its
-// own L2): workgroup i runs on XCD i % 8.  xcd_block maps workgroup i to a
-// logical block so that each XCD takes a contiguous range of `per` logical
+// Compute units and XCDs of the current HIP device, read once per device from
+// hipDeviceAttributeMultiprocessorCount and hipDeviceAttributeNumberOfXccs.
+// A whole MI355X shows 256 CUs over 8 XCDs; a partitioned one (CPX, say)
+// shows each HIP device its share.  Host-only queries made without a usable
+// device (workspace sizes on a machine with no GPU) get the whole chip's.
+struct DevGeom {
+  int cus, xcds;
+};
+constexpr DevGeom MI355X_GEOM = {256, 8};
+
+inline DevGeom device_geom() {
+  constexpr int MAXDEV = 64;
+  static std::once_flag once[MAXDEV];
+  static DevGeom geom[MAXDEV];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAXDEV) return MI355X_GEOM;
+  std::call_once(once[dev], [dev] {
+    int cus = 0, xcds = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = MI355X_GEOM.cus;
+    if (hipDeviceGetAttribute(&xcds, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess ||
+        xcds <= 0 || xcds > cus)
+      xcds = 1;
+    geom[dev] = DevGeom{cus, xcds};
+  });
+  return geom[dev];
+}
+
+// Workgroups are dispatched round-robin over the device's X XCDs (each with
+// its own L2): workgroup i runs on XCD i % X.  xcd_block maps workgroup i to
+// a logical block so that each XCD takes a contiguous range of `per` logical
 // blocks: neighbouring logical blocks (the query heads of one kv head, the
-// row blocks of one (b, h)) share an L2.  Launch xcd_grid(total) workgroups
-// and skip logical blocks past `total`.
-__host__ __device__ constexpr int xcd_grid(int total) { return 8 * ((total + 7) / 8); }
-__device__ __forceinline__ int xcd_block(int i, int per) { return (i & 7) * per + (i >> 3); }
+// row blocks of one (b, h)) share an L2.  Launch xcd_grid(total, X)
+// workgroups and skip logical blocks past `total`.
+__host__ __device__ constexpr int xcd_grid(int total, int X) { return X * ((total + X - 1) / X); }
+__device__ __forceinline__ int xcd_block(int i, int per, int X) {
+  return (i % X) * per + i / X;
+}
 
 // Exchange with the other half of the wave (lane ^ 32).
 __device__ __forceinline__ float xhalf(float x) { return __shfl_xor(x, 32); }

@@ -1075,9 +1075,9 @@ static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v
                               D, gate_per_head, G, cps, KG, st);
     if (e != hipSuccess) return e;
   }
-  // the walks take two segments per workgroup while that still gives 256
-  // workgroups (one per CU): fewer, longer walks
-  const int M = (G % 2 == 0 && BH * G / 2 >= 256) ? 2 : 1;
+  // the walks take two segments per workgroup while that still gives one
+  // workgroup per CU: fewer, longer walks
+  const int M = (G % 2 == 0 && BH * G / 2 >= device_geom().cus) ? 2 : 1;
   auto ka = gla_bwd_dq_kernel<FP, DP, OutT, VEC>;
   if ((e = ensure_lds<gla_bwd_dq_kernel<FP, DP, OutT, VEC>>(LDS_A)) != hipSuccess) return e;
   hipLaunchKernelGGL(ka, dim3(BH * G / M), dim3(B_THREADS), LDS_A, st, (const bf16*)fq,

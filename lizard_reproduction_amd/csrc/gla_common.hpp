@@ -8,7 +8,9 @@
 namespace lz {
 
 constexpr int GLA_C = 64;            // chunk length (tokens)
-constexpr int GLA_TARGET_WG = 512;   // (b, h, segment) workgroups wanted per launch (F <= 128)
+// (b, h, segment) workgroups wanted per launch at F <= 128: two per CU of
+// the current device (512 on a whole MI355X)
+inline int gla_target_wg() { return 2 * device_geom().cus; }
 
 // compile-time register-set selectors of the double-buffered chunk prefetch
 constexpr std::integral_constant<int, 0> SET0{};

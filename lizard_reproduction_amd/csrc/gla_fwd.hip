@@ -937,13 +937,12 @@ bool gla_dims_supported(int F, int D) {
   return dp <= 128 && (fp <= 128 || dp <= 64);
 }
 
-// Segments per (b, h): enough (b, h, segment) workgroups to fill the GPU.
 // Segments per (b, h) so that B*H*G workgroups fill the GPU: two forward
 // workgroups per CU up to F = 128, one beyond (the LDS of a 256-wide chunk).
 void gla_segments(int BH, int L, int F, int* G, int* cps) {
   const int NT = (L + GLA_C - 1) / GLA_C;
   const bool wide = gla_padded_dim(F) > 128;   // walks run one workgroup per CU
-  const int target = wide ? GLA_TARGET_WG / 2 : GLA_TARGET_WG;
+  const int target = wide ? gla_target_wg() / 2 : gla_target_wg();
   int g = (target + BH - 1) / BH;
   g = g < 1 ? 1 : (g > NT ? NT : g);
   // Wide walks: segments half as long as one walk, each walk taking two
@@ -959,7 +958,7 @@ void gla_segments(int BH, int L, int F, int* G, int* cps) {
 // even number of segments and half as many workgroups still fill the GPU at
 // one per CU (wide walks; the segment split doubled for them).
 int gla_walk_segments(int BH, int G, int F) {
-  return gla_padded_dim(F) > 128 && G % 2 == 0 && BH * G / 2 >= GLA_TARGET_WG / 2 ? 2 : 1;
+  return gla_padded_dim(F) > 128 && G % 2 == 0 && BH * G / 2 >= gla_target_wg() / 2 ? 2 : 1;
 }
 
 // workspace floats of one segment-state set: records + log decays

@@ -33,7 +33,6 @@ constexpr int PRO_WAVES = 4;
 constexpr int PRO_ROWS = 32;                      // rows per wave and block
 constexpr int PRO_BLOCK = PRO_WAVES * PRO_ROWS;   // rows per workgroup iteration
 constexpr int PRO_FWD_WG_PER_ROLE = 1024;         // forward workgroups per role (q, kv)
-constexpr int PRO_CUS = 256;                      // MI355X compute units
 constexpr int PRO_BWD_WG_PER_CU = 2;              // the most any backward instantiation asks for
 constexpr int CMB_BLOCKS = 1024;                  // epilogue backward partial sums
 
@@ -1019,14 +1018,14 @@ bool prologue_dims_supported(int hd, int f) {
 static int feature_tiles(int f) { return f <= 32 ? 1 : (f <= 64 ? 2 : 4); }
 
 // Backward: 128-row blocks of each role, and the grid (at most
-// PRO_BWD_WG_PER_CU workgroups per CU on PRO_CUS CUs, no more than blocks).
+// PRO_BWD_WG_PER_CU workgroups per CU on the device's CUs, no more than blocks).
 static void prologue_bwd_blocks(int B, int L, int H, int Hkv, int* nbq, int* nbk) {
   *nbq = (int)ceil_div((long)B * L * H, PRO_BLOCK);
   *nbk = (int)ceil_div((long)B * L * Hkv, PRO_BLOCK);
 }
 
 static int prologue_bwd_grid(int nbq, int nbk, int occ) {
-  return (int)std::min<long>((long)nbq + nbk, (long)PRO_CUS * occ);
+  return (int)std::min<long>((long)nbq + nbk, (long)device_geom().cus * occ);
 }
 
 size_t prologue_bwd_workspace(int B, int L, int H, int Hkv, int hd, int f) {

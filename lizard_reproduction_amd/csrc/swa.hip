@@ -93,7 +93,7 @@ template <int DP, bool VEC>
 __global__ __launch_bounds__(256, (swa_fwd_occupancy<DP, VEC>())) void swa_fwd_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ meta, int n_meta, bf16* __restrict__ y, float* __restrict__ lse,
-    int BH, int L, int d, int W, float scale, int per, int KG) {
+    int BH, int L, int d, int W, float scale, int per, int nx, int KG) {
   using Cfg = SwaCfg<DP>;
   constexpr int P = Cfg::P;
   extern __shared__ __align__(16) char smem[];
@@ -101,7 +101,7 @@ __global__ __launch_bounds__(256, (swa_fwd_occupancy<DP, VEC>())) void swa_fwd_k
   bf16* v_l = reinterpret_cast<bf16*>(smem + Cfg::TILE_BYTES);
 
   const int nqb = (L + SWA_ROWS - 1) / SWA_ROWS;
-  const int lb = xcd_block(blockIdx.x, per);
+  const int lb = xcd_block(blockIdx.x, per, nx);
   if (lb >= BH * nqb) return;
   const int bh = lb / nqb, Q0 = (lb % nqb) * SWA_ROWS;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -198,7 +198,8 @@ __global__ __launch_bounds__(256) void swa_bwd_dq_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ meta, int n_meta, const float* __restrict__ lse,
     const bf16* __restrict__ dy, OutT* __restrict__ dq, float* __restrict__ delta_out,
-    float* __restrict__ dmeta_part, int BH, int L, int d, int W, float scale, int per, int KG) {
+    float* __restrict__ dmeta_part, int BH, int L, int d, int W, float scale, int per, int nx,
+    int KG) {
   using Cfg = SwaCfg<DP>;
   constexpr int P = Cfg::P;
   extern __shared__ __align__(16) char smem[];
@@ -207,7 +208,7 @@ __global__ __launch_bounds__(256) void swa_bwd_dq_kernel(
   float* red = reinterpret_cast<float*>(smem + 2 * Cfg::TILE_BYTES);   // [4][SWA_MAX_META]
 
   const int nqb = (L + SWA_ROWS - 1) / SWA_ROWS;
-  const int lb = xcd_block(blockIdx.x, per);
+  const int lb = xcd_block(blockIdx.x, per, nx);
   if (lb >= BH * nqb) return;
   const int bh = lb / nqb, qb = lb % nqb, Q0 = qb * SWA_ROWS;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -311,7 +312,7 @@ __global__ __launch_bounds__(256) void swa_bwd_dkv_kernel(
     const float* __restrict__ lse, const float* __restrict__ delta_in,
     const bf16* __restrict__ dy, OutT* __restrict__ dk, OutT* __restrict__ dv,
     const float* __restrict__ dmeta_part, float* __restrict__ dmeta, int n_meta, int BH, int L,
-    int d, int W, float scale, int per, int KG) {
+    int d, int W, float scale, int per, int nx, int KG) {
   using Cfg = SwaCfg<DP>;
   constexpr int P = Cfg::P;
   extern __shared__ __align__(16) char smem[];
@@ -321,7 +322,7 @@ __global__ __launch_bounds__(256) void swa_bwd_dkv_kernel(
   float* del_l = lse_l + SWA_TILE;                                        // [64]
 
   const int nkb = (L + SWA_ROWS - 1) / SWA_ROWS;
-  const int lb = xcd_block(blockIdx.x, per);
+  const int lb = xcd_block(blockIdx.x, per, nx);
   if (lb >= BH * nkb) return;
   if (lb == 0 && n_meta > 0) {
     // dmeta from the query-side blocks' partials (that launch has completed):
@@ -438,10 +439,11 @@ int swa_padded_dim(int d) {
 }
 
 // blocks per (b, h) and the XCD-spread grid for BH * nblk logical blocks
-static void swa_grid(int BH, int L, int* per, int* grid) {
+static void swa_grid(int BH, int L, int* per, int* grid, int* nx) {
   const int nblk = (L + SWA_ROWS - 1) / SWA_ROWS;
-  *grid = xcd_grid(BH * nblk);
-  *per = *grid / 8;
+  *nx = device_geom().xcds;
+  *grid = xcd_grid(BH * nblk, *nx);
+  *per = *grid / *nx;
 }
 
 int swa_row_blocks(int L) { return (L + SWA_ROWS - 1) / SWA_ROWS; }
@@ -454,10 +456,11 @@ static hipError_t launch_swa_fwd_t(const void* q, const void* k, const void* v, 
   auto kern = swa_fwd_kernel<DP, VEC>;
   hipError_t e = ensure_lds<swa_fwd_kernel<DP, VEC>>((int)lds);
   if (e != hipSuccess) return e;
-  int per, grid;
-  swa_grid(BH, L, &per, &grid);
+  int per, grid, nx;
+  swa_grid(BH, L, &per, &grid, &nx);
   hipLaunchKernelGGL(kern, dim3(grid), dim3(256), lds, st, (const bf16*)q, (const bf16*)k,
-                     (const bf16*)v, meta, n_meta, (bf16*)y, lse, BH, L, d, W, scale, per, KG);
+                     (const bf16*)v, meta, n_meta, (bf16*)y, lse, BH, L, d, W, scale, per, nx,
+                     KG);
   return hipGetLastError();
 }
 
@@ -467,15 +470,15 @@ static hipError_t launch_swa_bwd_t(const void* q, const void* k, const void* v, 
                                    void* dk, void* dv, float* delta, float* dmeta_part,
                                    float* dmeta, int BH, int L, int d, int W, float scale, int KG,
                                    hipStream_t st) {
-  int per, grid;
-  swa_grid(BH, L, &per, &grid);
+  int per, grid, nx;
+  swa_grid(BH, L, &per, &grid, &nx);
   const size_t lds_q = 2 * SwaCfg<DP>::TILE_BYTES + 4 * SWA_MAX_META * sizeof(float);
   auto kq = swa_bwd_dq_kernel<DP, OutT, VEC>;
   hipError_t e = ensure_lds<swa_bwd_dq_kernel<DP, OutT, VEC>>((int)lds_q);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kq, dim3(grid), dim3(256), lds_q, st, (const bf16*)q, (const bf16*)k,
                      (const bf16*)v, meta, n_meta, lse, (const bf16*)dy, (OutT*)dq, delta,
-                     dmeta_part, BH, L, d, W, scale, per, KG);
+                     dmeta_part, BH, L, d, W, scale, per, nx, KG);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   const size_t lds_k = 2 * SwaCfg<DP>::TILE_BYTES + 2 * SWA_TILE * sizeof(float);
   auto kk = swa_bwd_dkv_kernel<DP, OutT, VEC>;
@@ -483,7 +486,7 @@ static hipError_t launch_swa_bwd_t(const void* q, const void* k, const void* v, 
   hipLaunchKernelGGL(kk, dim3(grid), dim3(256), lds_k, st, (const bf16*)q, (const bf16*)k,
                      (const bf16*)v, lse, (const float*)delta, (const bf16*)dy, (OutT*)dk,
                      (OutT*)dv, (const float*)dmeta_part, dmeta, n_meta, BH, L, d, W, scale, per,
-                     KG);
+                     nx, KG);
   return hipGetLastError();
 }
 

@@ -56,7 +56,21 @@ def _swa_bwd_ws(b, h, length, d, n_meta):
     return _lib.load().lz_swa_bwd_workspace_bytes(b, h, length, d, n_meta)
 
 
+def _refuse_capture(what):
+    """Refuse calls made while the current stream is being captured into a
+    HIP graph.  The wrappers allocate outputs and workspaces with torch on
+    every call, and the library sets a kernel's LDS limit with
+    hipFuncSetAttribute on its first launch on a device; a capture of a
+    whole fwd+bwd crashed the host process once (in the runtime's capture
+    end) and neither step has been cleared as its cause, so capture is not
+    offered."""
+    if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
+        raise RuntimeError(f"{what}: calls under HIP graph capture are not supported "
+                           "(run the kernels eagerly)")
+
+
 def _require_gpu(*tensors):
+    _refuse_capture("lizard_reproduction_amd kernels")
     for t in tensors:
         if not t.is_cuda:
             raise ValueError("lizard_reproduction_amd kernels need tensors on a ROCm GPU "

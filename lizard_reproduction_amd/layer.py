@@ -292,16 +292,10 @@ class LizardAttention(nn.Module):
         nn.init.normal_(self.phi_k.weight, std=0.02)
         nn.init.zeros_(self.W_gamma.weight)
 
-    def split(self, x, heads):
-        """[B, L, heads * head_dim] -> [B, self.heads, L, head_dim], each kv
-        head repeated for its group of query heads."""
-        b, n, _ = x.shape
-        x = x.view(b, n, heads, self.head_dim).transpose(1, 2)
-        return x.repeat_interleave(self.heads // heads, dim=1)
-
     def forward(self, hidden_states, position_embeddings, **kwargs):
         x = hidden_states
         dtype = torch.promote_types(x.dtype, torch.float32)
+        kernels._refuse_capture("LizardAttention")
         if x.device.type != "cuda":
             raise ValueError("LizardAttention (hip backend) needs its input on a ROCm GPU")
         z = self.W_gamma(x).to(dtype).squeeze(-1)
@@ -323,6 +317,7 @@ class LizardAttention(nn.Module):
         return LizardCache(state, k, torch.zeros_like(k), 0)
 
     def _operands(self, x, position_embeddings):
+        kernels._refuse_capture("LizardAttention")
         if x.device.type != "cuda":
             raise ValueError("LizardAttention (hip backend) needs its input on a ROCm GPU")
         dtype = torch.promote_types(x.dtype, torch.float32)

@@ -261,3 +261,30 @@ def test_internal_wrappers_reject_mismatched_shapes_before_any_launch():
     with pytest.raises(ValueError, match="k must be"):
         layer.prologue_forward(torch.zeros(1, 8, 128), torch.zeros(1, 8, 32), torch.zeros(1, 8, 64),
                                torch.zeros(8, 32), torch.zeros(8, 32), None, None, 4, 2)
+
+
+def test_calls_under_graph_capture_are_refused(monkeypatch):
+    """The operator API and the layer refuse to run while the current stream
+    is being captured into a HIP graph (their per-call torch allocations and
+    the library's first-launch LDS setup have not been cleared for capture),
+    before anything touches a GPU."""
+    import types
+
+    from lizard_reproduction_amd import layer
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: True)
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
+    x = torch.zeros(1, 2, 8, 16)
+    with pytest.raises(RuntimeError, match="graph capture"):
+        kernels.gla(x, x, x, torch.zeros(1, 8))
+    with pytest.raises(RuntimeError, match="graph capture"):
+        kernels.swa(x, x, x, torch.zeros(4), 4)
+    with pytest.raises(RuntimeError, match="graph capture"):
+        kernels.gla_prefill(x, x, x, torch.zeros(1, 8))
+    cfg = types.SimpleNamespace(hidden_size=64, num_attention_heads=2, num_key_value_heads=1)
+    mod = layer.LizardAttention(cfg, 0, window=8, feature_dim=8)
+    cos = torch.ones(8, 32)
+    with pytest.raises(RuntimeError, match="graph capture"):
+        mod(torch.zeros(1, 8, 64), (cos, cos))
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: False)
+    with pytest.raises(ValueError, match="ROCm GPU"):
+        kernels.gla(x, x, x, torch.zeros(1, 8))
