@@ -45,6 +45,10 @@ lizard_layer        lizard_layer_loop (fp64, 1e-10); with the GLA branch
                     zeroed, no sinks and an unbounded window it equals
                     transformers' LlamaAttention (a library routine);
                     causal and batch independent
+awa_banded          == awa in fp64 for windows 1 .. > L, ragged L, block
+                    sizes 16/64, empty meta, gradients included
+lizard_layer_banded == lizard_layer in fp64 (output and every gradient) at
+                    L <= 256, windows shorter and longer than a block
 ==================  =======================================================
 
 The loops are deliberately independent code paths (explicit Python loops over
@@ -363,6 +367,57 @@ def lizard_layer(params, x, cos, sin, heads, kv_heads, window):
     qr, kr = rope(q, c, s), rope(k, c, s)
     alpha, meta = params["alpha_blend"].to(dtype), params["meta_tokens"].to(dtype)
     y = gla(fq, fk, v, torch.sigmoid(z)) + alpha * awa(qr, kr, v, meta, window)
+    y = y.to(x.dtype).transpose(1, 2).reshape(batch, length, hidden)
+    return torch.matmul(y, params["o_proj.weight"].transpose(0, 1))
+
+
+def awa_banded(q, k, v, meta, window, block=64):
+    """``awa`` computed block by block over the queries, each block against
+    only the keys its window can reach (keys i0 - window + 1 .. i1 - 1 for
+    queries i0 .. i1 - 1), so memory is O(L (block + window)) instead of
+    O(L^2): the long-L form of the dense SWA oracle.  Same mask
+    (``window_mask``'s predicate), scale and ``sink_softmax``."""
+    length, dim = q.shape[-2], q.shape[-1]
+    outs = []
+    for i0 in range(0, length, block):
+        i1 = min(i0 + block, length)
+        t0 = max(0, i0 - window + 1)
+        rows = torch.arange(i0, i1).unsqueeze(1)
+        cols = torch.arange(t0, i1).unsqueeze(0)
+        mask = (cols <= rows) & ((rows - cols) < window)
+        scores = torch.matmul(q[..., i0:i1, :], k[..., t0:i1, :].transpose(-1, -2))
+        scores = (scores / math.sqrt(dim)).masked_fill(~mask, float("-inf"))
+        outs.append(torch.matmul(sink_softmax(scores, meta), v[..., t0:i1, :]))
+    return torch.cat(outs, dim=-2)
+
+
+def lizard_layer_banded(params, x, cos, sin, heads, kv_heads, window, chunk=64):
+    """``lizard_layer`` with its two O(L^2) pieces replaced by their long-L
+    forms: the GLA branch by ``gla_chunked`` on log_gamma = logsigmoid(z)
+    (exact in fp64, no rounding), the SWA branch by ``awa_banded``.  Same
+    projections, dtype promotion, repeat_interleave GQA expansion, Hedgehog
+    maps, RoPE and blend (``src/lizard_attention.py:73-97``).  Pinned against
+    ``lizard_layer`` at lengths the dense form holds; it is the oracle of the
+    layer at BASELINE config 5's sequence length."""
+    batch, length, hidden = x.shape
+    head_dim = hidden // heads
+    dtype = torch.promote_types(x.dtype, torch.float32)
+
+    def heads_of(name, count):
+        y = torch.matmul(x, params[name].transpose(0, 1)).view(batch, length, count, head_dim)
+        return y.transpose(1, 2).repeat_interleave(heads // count, dim=1).to(dtype)
+
+    q = heads_of("q_proj.weight", heads)
+    k = heads_of("k_proj.weight", kv_heads)
+    v = heads_of("v_proj.weight", kv_heads)
+    z = torch.matmul(x, params["W_gamma.weight"].transpose(0, 1)).to(dtype).squeeze(-1)
+    fq = hedgehog(q, params["phi_q.weight"].to(dtype))
+    fk = hedgehog(k, params["phi_k.weight"].to(dtype))
+    c, s = cos.to(dtype).unsqueeze(1), sin.to(dtype).unsqueeze(1)
+    qr, kr = rope(q, c, s), rope(k, c, s)
+    alpha, meta = params["alpha_blend"].to(dtype), params["meta_tokens"].to(dtype)
+    y_gla = gla_chunked(fq, fk, v, torch.nn.functional.logsigmoid(z), chunk, dtype=dtype)
+    y = y_gla + alpha * awa_banded(qr, kr, v, meta, window)
     y = y.to(x.dtype).transpose(1, 2).reshape(batch, length, hidden)
     return torch.matmul(y, params["o_proj.weight"].transpose(0, 1))
 

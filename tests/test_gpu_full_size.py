@@ -54,6 +54,25 @@ def test_config4_longest_slices_match_chunked_oracle():
     check_slices(16, 32, 16384, 128, True, 2.0, 1.5, [(3, 5), (12, 30)], "config4 L=16K")
 
 
+@pytest.mark.parametrize("batch, length, slices", [
+    (1, 4096, [(0, 0), (0, 17), (0, 31)]),      # 16 segments of 4 chunks
+    (1, 16384, [(0, 5), (0, 30)]),              # 16 segments of 16 chunks
+    (4, 2048, [(0, 0), (2, 9), (3, 31)]),       # 4 segments of 8 chunks
+    (4, 8192, [(1, 3), (3, 28)])])              # 4 segments of 32 chunks
+def test_config4_segmented_d128_walks_slices_match_chunked_oracle(batch, length, slices):
+    """The config-4 sweep points whose B*H (32, 128) cannot fill the GPU:
+    each (b, h) sequence is cut into segments of several chunks, so the
+    F=D=128 segment state pass, the forward and reverse segment scans and
+    the walks that start from a scanned state all run; output and every
+    gradient (d log_gamma per head) of sampled slices against the chunked
+    fp64 oracle."""
+    from lizard_reproduction_amd import _lib
+    lib = _lib.load()
+    assert lib.lz_gla_fwd_workspace_bytes(batch, 32, length, 128, 128, 1, 64) > 0  # segmented
+    check_slices(batch, 32, length, 128, True, 2.0, 1.5, slices,
+                 f"config4 segmented B={batch} L={length}")
+
+
 def test_headline_shape_constant_values_stay_constant_everywhere():
     """y_i is a normalised average of v, so a constant v comes back (up to
     the bf16 rounding of the state operand) at every position of every
@@ -79,11 +98,11 @@ def test_headline_shape_is_deterministic():
         assert torch.equal(a, b)
 
 
-def test_config5_attention_shape_slices_match_chunked_oracle():
+def config5_attention_inputs():
     """The layer's GLA call at BASELINE config 5: B=4, H=32, L=4096, F=256
     (Hedgehog maps [softmax(x), softmax(-x)] of 128 features), D=64, one gate
-    per token (logsigmoid(N(3, 1))); forward and backward on the whole batch,
-    sampled (b, h) slices against the chunked fp64 oracle."""
+    per token (logsigmoid(N(3, 1))), dO ~ N(0, 1); forward and backward of
+    the whole batch on the GPU.  Returns the CPU inputs, dO, y and the leaves."""
     g = torch.Generator().manual_seed(9)
     b, h, length = 4, 32, 4096
 
@@ -98,6 +117,13 @@ def test_config5_attention_shape_slices_match_chunked_oracle():
     y = kernels.gla(*ours)
     y.backward(dy.cuda())
     torch.cuda.synchronize()
+    return (fq, fk, v, lg), dy, y, ours
+
+
+def test_config5_attention_shape_slices_match_chunked_oracle():
+    """Sampled (b, h) slices of the config-5 attention call against the
+    chunked fp64 oracle: output, dfq, dfk, dv."""
+    (fq, fk, v, lg), dy, y, ours = config5_attention_inputs()
     worst = {}
     for bi, hi in [(0, 0), (2, 17), (3, 31)]:
         sl = [t[bi:bi + 1, hi:hi + 1].double().requires_grad_() for t in (fq, fk, v)]
@@ -115,3 +141,27 @@ def test_config5_attention_shape_slices_match_chunked_oracle():
     for k, e in worst.items():
         if k != "y":
             assert e <= GRAD_TOL, (k, worst)
+
+
+def test_config5_attention_shape_shared_gate_gradient_matches_chunked_oracle():
+    """One whole batch row (all 32 heads) of the config-5 attention call
+    against the chunked fp64 oracle, so that the gradient of the gate shared
+    by the heads -- summed over the heads and reverse-cumsummed over the 4096
+    tokens inside the kernels -- is compared too, with the output and the
+    other gradients of every head of the row."""
+    (fq, fk, v, lg), dy, y, ours = config5_attention_inputs()
+    bi = 2
+    sl = [t[bi:bi + 1].double().requires_grad_() for t in (fq, fk, v)]
+    gl = lg[bi:bi + 1].double().requires_grad_()
+    ref = lo.gla_chunked(*sl, gl, 64)
+    ref.backward(dy[bi:bi + 1].double())
+    errs = {"y": max_rel(y[bi], ref[0]), "dfq": max_rel(ours[0].grad[bi], sl[0].grad[0]),
+            "dfk": max_rel(ours[1].grad[bi], sl[1].grad[0]),
+            "dv": max_rel(ours[2].grad[bi], sl[2].grad[0]),
+            "dlg": max_rel(ours[3].grad[bi], gl.grad[0])}
+    print("[parity] config5 attention row 2, all heads: " +
+          " ".join(f"{k}={v:.2e}" for k, v in errs.items()), flush=True)
+    assert errs["y"] <= OUT_TOL, errs
+    for k, e in errs.items():
+        if k != "y":
+            assert e <= GRAD_TOL, (k, errs)

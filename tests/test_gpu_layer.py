@@ -243,3 +243,48 @@ def test_combine_matches_reference_ops(dtype):
     assert torch.equal(dyg.cpu(), leaves[0].grad)
     assert torch.equal(dys.cpu(), leaves[1].grad)
     assert abs(dalpha.item() - leaves[2].grad.item()) <= 1e-5 * abs(leaves[2].grad.item())
+
+
+def test_config5_layer_at_size_matches_banded_oracle_layer():
+    """One LizardAttention at BASELINE config 5's shape -- hidden 2048, 32
+    query / 8 kv heads, head_dim 64, feature_dim 128 (F = 256), window 64, 4
+    sinks, RoPE theta 500000 -- on a B=1 slice of its L=4096 sequences, fp32
+    parameters, against the long-L oracle layer (chunked GLA, banded SWA;
+    pinned against the dense layer in tests/test_layer.py) in fp64: output,
+    input gradient and every parameter gradient (the reference's whole-layer
+    test, tests/test_kernels.py:137-156, at the model's size)."""
+    import types
+    cfg = types.SimpleNamespace(hidden_size=2048, num_attention_heads=32, num_key_value_heads=8)
+    torch.manual_seed(0)
+    layer = hip_layer.LizardAttention(cfg, 0, window=64, num_meta=4, feature_dim=128)
+    with torch.no_grad():
+        layer.phi_q.weight.normal_(0, 0.3)
+        layer.phi_k.weight.normal_(0, 0.3)
+        layer.W_gamma.weight.normal_(0, 0.05)   # gates from ~0.1 to ~0.99
+        layer.meta_tokens.normal_(0, 1)
+        layer.alpha_blend.fill_(0.8)
+    params = {n: p.detach().double().requires_grad_() for n, p in layer.named_parameters()}
+    layer = layer.cuda()
+    batch, length = 1, 4096
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(batch, length, 2048, generator=g)
+    gy = torch.randn(batch, length, 2048, generator=g)
+    cos, sin = (t[None].expand(batch, length, 64) for t in lo.rope_cos_sin(length, 64))
+    xg = x.cuda().requires_grad_()
+    y = layer(xg, (cos.float().cuda(), sin.float().cuda()))[0]
+    y.backward(gy.cuda())
+    torch.cuda.synchronize()
+    xc = x.double().requires_grad_()
+    expected = lo.lizard_layer_banded(params, xc, cos, sin, 32, 8, 64)
+    expected.backward(gy.double())
+    pairs = {"out": (y, expected), "dx": (xg.grad, xc.grad)}
+    for name, p in layer.named_parameters():
+        pairs[name] = (p.grad, params[name].grad)
+    errs = report("config5 layer B=1 L=4096", pairs)
+    assert y.dtype == torch.float32
+    assert errs["out"] <= OUT_TOL and norm_rel(y, expected) < OUT_TOL, errs
+    for name, (a, b) in pairs.items():
+        if name == "out":
+            continue
+        assert errs[name] <= GRAD_TOL, (name, errs)
+        assert ref_close(a, b), (name, errs)

@@ -86,3 +86,18 @@ def test_swa_baseline_config3_dense():
           flush=True)
     assert errs[0] <= OUT_TOL, errs
     assert max(errs[1:]) <= GRAD_TOL, errs
+
+
+@pytest.mark.parametrize("dim", [20, 64])
+def test_swa_fp32_inputs_give_fp32_grads_matching_oracle(dim):
+    """fp32 q, k, v (what the reference's layer passes, src/lizard_attention.py:
+    80-96): the output is bf16 and dq, dk, dv, dmeta come back fp32 (the
+    kernels' fp32 gradient stores), within the bar of the fp32 oracle;
+    d = 20 takes the element-wise path, d = 64 the 16-byte one."""
+    inputs = swa_inputs(120, dim=dim)
+    inputs = [t.float() for t in inputs[:3]] + [inputs[3]]
+    grad = torch.randn(inputs[2].shape, generator=torch.Generator().manual_seed(1))
+    report = compare(lambda q, k, v, m: kernels.swa(q, k, v, m, 48),
+                     lambda q, k, v, m: lo.swa_kernel_api(q, k, v, m, 48, dtype=torch.float32),
+                     inputs, grad, label=f"fp32 inputs d={dim}")
+    assert {"grad0", "grad1", "grad2", "grad3"} <= set(report)

@@ -173,3 +173,69 @@ def test_cache_ring_holds_the_last_window_positions(prompt, window):
         for q in range(max(0, end - window), end):
             assert torch.all(cache.k[:, :, q % window] == q), (p, q)
             assert torch.all(cache.v[:, :, q % window] == -q), (p, q)
+
+
+# -- the long-L oracle layer (banded SWA, chunked GLA) -----------------------
+
+@pytest.mark.parametrize("length, window, block", [(1, 4, 64), (77, 16, 16), (150, 64, 64),
+                                                   (130, 1, 64), (97, 200, 16), (64, 64, 64)])
+def test_banded_swa_equals_dense_awa(length, window, block):
+    g = torch.Generator().manual_seed(length)
+    q, k, v = (torch.randn(2, 3, length, 20, generator=g, dtype=torch.float64)
+               .requires_grad_() for _ in range(3))
+    meta = torch.randn(4, generator=g, dtype=torch.float64).requires_grad_()
+    dy = torch.randn(2, 3, length, 20, generator=g, dtype=torch.float64)
+    dense_y = lo.awa(q, k, v, meta, window)
+    dense_y.backward(dy)
+    grads = [t.grad.clone() for t in (q, k, v, meta)]
+    for t in (q, k, v, meta):
+        t.grad = None
+    band = lo.awa_banded(q, k, v, meta, window, block=block)
+    band.backward(dy)
+    assert rel_err(band, dense_y) < EXACT
+    for t, ref in zip((q, k, v, meta), grads):
+        assert rel_err(t.grad, ref) < EXACT
+
+
+def test_banded_swa_without_sinks_equals_dense_awa():
+    g = torch.Generator().manual_seed(5)
+    q, k, v = (torch.randn(1, 2, 90, 16, generator=g, dtype=torch.float64) for _ in range(3))
+    meta = torch.empty(0, dtype=torch.float64)
+    assert rel_err(lo.awa_banded(q, k, v, meta, 32), lo.awa(q, k, v, meta, 32)) < EXACT
+
+
+@pytest.mark.parametrize("length, window", [(40, 16), (130, 16), (200, 100), (256, 64)])
+def test_banded_oracle_layer_equals_dense_layer(length, window):
+    """The long-L oracle layer (chunked GLA, banded SWA) against the dense
+    one in fp64: output, input gradient and every parameter gradient."""
+    params = random_params(window=window)
+    for p in params.values():
+        p.requires_grad_()
+    rope = tiny_rope(length, batch=2)
+    g = torch.Generator().manual_seed(length)
+    x = torch.randn(2, length, 128, generator=g, dtype=torch.float64).requires_grad_()
+    dy = torch.randn(2, length, 128, generator=g, dtype=torch.float64)
+    ref = lo.lizard_layer(params, x, rope[0], rope[1], 4, 2, window)
+    ref.backward(dy)
+    ref_grads = {n: p.grad.clone() for n, p in params.items()}
+    ref_dx = x.grad.clone()
+    for p in list(params.values()) + [x]:
+        p.grad = None
+    band = lo.lizard_layer_banded(params, x, rope[0], rope[1], 4, 2, window)
+    band.backward(dy)
+    assert rel_err(band, ref) < EXACT
+    assert rel_err(x.grad, ref_dx) < EXACT
+    for n, p in params.items():
+        assert rel_err(p.grad, ref_grads[n]) < EXACT, n
+
+
+def test_banded_oracle_layer_catches_a_window_off_by_one(monkeypatch):
+    """A planted mistake in the banded window (one key too many) fails the
+    check against the dense layer."""
+    params, rope = random_params(), tiny_rope(70)
+    x = torch.randn(1, 70, 128, dtype=torch.float64)
+    good = lo.awa_banded
+    monkeypatch.setattr(lo, "awa_banded", lambda q, k, v, m, w, block=64: good(q, k, v, m, w + 1,
+                                                                                block))
+    wrong = lo.lizard_layer_banded(params, x, rope[0], rope[1], 4, 2, 16)
+    assert rel_err(wrong, lo.lizard_layer(params, x, rope[0], rope[1], 4, 2, 16)) > 1e-4
