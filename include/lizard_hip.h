@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define LZ_ABI_VERSION 9
+#define LZ_ABI_VERSION 10
 
 /* ABI version of the loaded library (LZ_ABI_VERSION). */
 int lz_abi_version(void);
@@ -70,6 +70,26 @@ size_t lz_gla_fwd_workspace_bytes(int batch, int heads, int length, int nf, int 
 int lz_gla_fwd(const void* fq, const void* fk, const void* v, const float* log_gamma, void* y,
                int batch, int heads, int kv_heads, int length, int nf, int nd, int gate_per_head,
                int chunk, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * GLA forward that allocates nothing and takes no workspace.  No counterpart
+ * in the reference: it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments, sizes, result and kernels as lz_gla_fwd
+ * without the workspace: the per-segment states that lz_gla_fwd keeps in
+ * its workspace (when B*H alone cannot fill the GPU) live in a static device
+ * array of LZ_GLA_FWD_NOALLOC_MAX_BYTES per GPU, held until the process
+ * ends.  That covers every size the forward takes on a whole MI355X; sizes
+ * whose states would not fit are refused with an error.  Every call on one
+ * GPU shares that GPU's array: calls that overlap on one GPU (on different
+ * streams, or from different threads) race and must be serialised by the
+ * caller.  Nothing in the array needs to start at zero: each call writes
+ * every state it reads.
+ */
+#define LZ_GLA_FWD_NOALLOC_MAX_BYTES (66u << 20)
+int lz_gla_fwd_noalloc(const void* fq, const void* fk, const void* v, const float* log_gamma,
+                       void* y, int batch, int heads, int kv_heads, int length, int nf, int nd,
+                       int gate_per_head, int chunk, void* stream);
 
 /*
  * GLA prefill: lz_gla_fwd that also writes the recurrent state after the last

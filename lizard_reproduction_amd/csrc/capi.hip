@@ -3,6 +3,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
 #include <string>
 
 #include "../../include/lizard_hip.h"
@@ -207,6 +208,64 @@ extern "C" int lz_gla_bwd(const void* fq, const void* fk, const void* v, const f
                                        gate_per_head ? 1 : 0, heads / kv_heads, fws,
                                        (float*)workspace, (hipStream_t)stream),
                     "gla_bwd");
+}
+
+// ---------------------------------------------------------------------------
+// GLA forward without allocation: the segment records in a static array
+// ---------------------------------------------------------------------------
+// `scratch` holds the state records of lz_gla_fwd_noalloc's segment split
+// (the only device memory the forward needs beyond its inputs and output).
+// Its size covers every split the forward makes on a whole MI355X: the
+// largest, 64.75 MiB, is F = 256, D = 64 at B*H = 255.  Every GPU the library
+// runs on holds its own copy until the process ends.
+static_assert(LZ_GLA_FWD_NOALLOC_MAX_BYTES % 256 == 0, "scratch size");
+static __device__ __align__(256) float scratch[LZ_GLA_FWD_NOALLOC_MAX_BYTES / sizeof(float)];
+
+// Device address of the current device's copy of `scratch`, looked up once
+// per device with that device current.  In host code the array's name is
+// only a handle the runtime resolves; kernels get this address instead.
+static int scratch_address(float** out) {
+  constexpr int MAXDEV = 64;
+  static std::once_flag once[MAXDEV];
+  static float* addr[MAXDEV];
+  static hipError_t status[MAXDEV];
+  int dev = 0;
+  if (hipError_t e = hipGetDevice(&dev); e != hipSuccess)
+    return hip_status(e, "gla_fwd_noalloc: hipGetDevice");
+  if (dev < 0 || dev >= MAXDEV)
+    return fail(1, "gla_fwd_noalloc: device index %d beyond the %d this library tracks", dev,
+                MAXDEV);
+  std::call_once(once[dev], [dev] {
+    void* p = nullptr;
+    status[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    addr[dev] = static_cast<float*>(p);
+  });
+  if (status[dev] != hipSuccess)
+    return hip_status(status[dev], "gla_fwd_noalloc: hipGetSymbolAddress(scratch)");
+  if (!addr[dev]) return fail(1, "gla_fwd_noalloc: no device address for the scratch array");
+  *out = addr[dev];
+  return 0;
+}
+
+extern "C" int lz_gla_fwd_noalloc(const void* fq, const void* fk, const void* v,
+                                  const float* log_gamma, void* y, int batch, int heads,
+                                  int kv_heads, int length, int nf, int nd, int gate_per_head,
+                                  int chunk, void* stream) {
+  if (int rc = check_gla(fq, fk, v, log_gamma, batch, heads, length, nf, nd, chunk)) return rc;
+  if (int rc = check_kv_heads("gla_fwd_noalloc", heads, kv_heads)) return rc;
+  if (!y) return fail(1, "gla_fwd_noalloc: null output pointer");
+  const size_t need = lz::gla_fwd_workspace(batch, heads, length, nf, nd);
+  if (need > (size_t)LZ_GLA_FWD_NOALLOC_MAX_BYTES)
+    return fail(1, "gla_fwd_noalloc: these sizes need %zu bytes of segment records, more than "
+                   "the %zu-byte static scratch (use lz_gla_fwd with a workspace)",
+                need, (size_t)LZ_GLA_FWD_NOALLOC_MAX_BYTES);
+  float* ws = nullptr;
+  if (need)
+    if (int rc = scratch_address(&ws)) return rc;
+  return hip_status(lz::launch_gla_fwd(fq, fk, v, log_gamma, y, batch, heads, length, nf, nd,
+                                       gate_per_head ? 1 : 0, heads / kv_heads, ws, nullptr,
+                                       (hipStream_t)stream),
+                    "gla_fwd_noalloc");
 }
 
 static int check_swa(const void* q, const void* k, const void* v, const float* meta, int n_meta,
