@@ -20,7 +20,9 @@ reference (src/benchmark.py:57-66):
   * BASELINE config 3, SWA fwd and fwd+bwd (B=1, H=32, L=2048, d=64, W=64,
     4 sink logits, RoPE'd q and k);
   * BASELINE config 4 sweep, GLA fwd and fwd+bwd, B in {1,4,16},
-    L in {2K,4K,8K,16K}, d=128, per-head gate (skip with --no-sweep);
+    L in {2K,4K,8K,16K}, d=128, per-head gate (skip with --no-sweep); its
+    forward rows are timed like the headline (mean of back-to-back launches
+    after a short settle), so the B=16 L=2048 row is the headline again;
   * BASELINE config 5, a Llama-3.2-1B-shaped model (hidden 2048, 16 blocks,
     32 query / 8 kv heads, head_dim 64, intermediate 8192, vocab 128256,
     RoPE theta 500000, tied embeddings, random-init bf16 weights) with every
@@ -29,11 +31,27 @@ reference (src/benchmark.py:57-66):
     forward + cross-entropy backward at B=4, L=4096 on uniform random ids;
     plus one such layer alone (skip with --no-layer).
 
+Clocks: before its warm-up, the headline forward is launched untimed for
+--settle-seconds (2 s) of wall time, so that the GPU clocks have settled
+whatever --warmup the caller passes; the reported ``warmup`` is the W
+untimed steps that follow, as passed.
+
+Also in ``extra``: the algorithmic HBM bytes and HBM fraction of every fwd+bwd
+line, and at config 2 the analytic HBM floor of the reference's own
+two-kernel design (its per-chunk states and fp32 intermediates through HBM),
+the stand-in for its ROCm-Triton build, which cannot run on the GPU box.
+
 ``cpu_baseline`` times the dense fp32 PyTorch restatement of the reference's
-torch backend (oracle.lizard_oracle.gla_kernel_api, the math of
-src/lizard_attention.py:20-31) on the host cores, on a bounded sample of the
-headline workload (a few (b, h) slices at the full L), scaled linearly to all
-B*H slices (the dense algorithm is independent per slice).
+torch backend (oracle.lizard_oracle: gla_kernel_api, swa_kernel_api and
+lizard_layer, the math of src/lizard_attention.py:20-97) on the host cores
+(the CPU affinity, capped by a cgroup CPU quota; the count is reported),
+median of 5 after one warm-up, after the GPU work: the headline forward (its
+``value``) and fwd+bwd on a sample of (b, h) slices at the full L scaled to
+all B*H slices (each slice is an independent dense problem), configs 1-3
+whole, and one config-5 layer at B=1 (``extra.cpu_baselines``).
+
+``--only NAME`` runs one fwd+bwd workload (headline, config 2, config 3, or
+one config-5 layer) --steps times and nothing else, for rocprofv3 runs.
 
 Only one GPU is supported: --gpus N with N > 1 exits with a message.
 """
@@ -102,8 +120,14 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--no-sweep", action="store_true", help="skip the config-4 sweep")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--cpu-seconds", type=float, default=12.0,
-                   help="target CPU time of the cpu_baseline sample")
+    p.add_argument("--cpu-seconds", type=float, default=0.5,
+                   help="target CPU time of one headline cpu_baseline sample run")
+    p.add_argument("--settle-seconds", type=float, default=2.0,
+                   help="untimed launches of the headline (or of the --only workload) "
+                        "before its warmup, so clocks settle")
+    p.add_argument("--only", default=None,
+                   choices=["headline_fwd_bwd", "config2", "config3", "config5_layer"],
+                   help="run only this workload --steps times (for profiler runs)")
     p.add_argument("--headline-only", action="store_true",
                    help="time only the headline step (for profiler runs)")
     p.add_argument("--no-layer", action="store_true", help="skip the config-5 layer stack")
@@ -181,10 +205,11 @@ def fwd_bwd_fn(torch, op, inputs, dy, extra=()):
     return run, reset
 
 
-def layer_stack(torch, steps, warmup, one_layer=False):
+def layer_stack(torch, steps, warmup, one_layer=False, decode=True):
     """training step (forward, cross-entropy, backward) of
     a Llama-3.2-1B-shaped model whose attention blocks are LizardAttention,
-    and of one such layer alone; medians of per-step events."""
+    and of one such layer alone; medians of per-step events.  With
+    one_layer, only the single layer (and its decode, unless decode=False)."""
     from transformers import LlamaConfig, LlamaForCausalLM
     from lizard_reproduction_amd import _lib, kernels
     from lizard_reproduction_amd.layer import LizardAttention, to_lizard
@@ -221,8 +246,11 @@ def layer_stack(torch, steps, warmup, one_layer=False):
         layer.zero_grad(set_to_none=True)
     with torch.no_grad():
         out["one_layer_fwd_ms"] = round(median_ms(torch, lambda: layer(xg, rope), 5, 2), 3)
-    out["one_layer_fwd_bwd_ms"] = round(median_ms(torch, layer_step, 5, 2, layer_reset), 3)
+    out["one_layer_fwd_bwd_ms"] = round(median_ms(torch, layer_step, max(5, steps), 2,
+                                                  layer_reset), 3)
     print(f"[bench] config5 one layer: {out}", file=sys.stderr, flush=True)
+    if one_layer and not decode:
+        return out
 
     # layer-level decode: prefill the 4096-token prompts, then one token per
     # sequence through LizardAttention.step (projections, one-token prologue,
@@ -310,42 +338,243 @@ def layer_stack(torch, steps, warmup, one_layer=False):
     return out
 
 
-def cpu_baseline(torch, fq, fk, v, lg, target_s):
-    """Dense fp32 torch restatement (the reference's torch backend) on the host
-    cores, on whole (b, h) slices of the headline inputs; returns the time
-    scaled to all B*H slices."""
-    from oracle import lizard_oracle as lo
-    cores = max(1, min(16, len(os.sched_getaffinity(0))))
-    torch.set_num_threads(cores)
-    batch, heads = fq.shape[:2]
-    flat = [t.reshape(batch * heads, 1, *t.shape[2:]) for t in (fq, fk, v)]
-    lgf = lg.reshape(batch * heads, 1, lg.shape[-1])
+def host_cores():
+    """Host cores this process may use: its CPU affinity, capped by a cgroup
+    CPU quota when one is set (a GPU box's share of a larger host)."""
+    n = len(os.sched_getaffinity(0))
+    try:
+        quota, period = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        if quota != "max":
+            n = min(n, max(1, int(int(quota) // int(period))))
+    except (OSError, ValueError):
+        pass
+    return n
 
-    def run(n):
-        ins = [t[:n].cpu() for t in flat] + [lgf[:n].cpu()]
-        t0 = time.perf_counter()
-        with torch.no_grad():
-            lo.gla_kernel_api(*ins, dtype=torch.float32)
-        return time.perf_counter() - t0
-    run(1)                                   # warm-up
-    per = run(2) / 2
-    n = int(max(1, min(batch * heads, target_s / max(per, 1e-6))))
-    elapsed = run(n)
-    full_ms = elapsed / n * batch * heads * 1e3
-    cpu = platform.processor() or platform.machine()
+
+def host_cpu_name():
+    name = platform.processor() or platform.machine()
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
                 if line.startswith("model name"):
-                    cpu = line.split(":", 1)[1].strip()
-                    break
+                    return line.split(":", 1)[1].strip()
     except OSError:
         pass
-    return {"value": round(full_ms, 3), "unit": "ms", "cores": cores, "kind": "port",
-            "sample": (f"dense fp32 oracle gla_kernel_api (torch backend math) on {n} of "
-                       f"{batch * heads} (b,h) slices at L={fq.shape[2]}, F=D={fq.shape[3]}, "
-                       f"{elapsed:.1f} s, scaled x{batch * heads / n:.1f} to the full workload; "
-                       f"host CPU {cpu}")}
+    return name
+
+
+def cpu_median_s(fn, reps=5):
+    """Median wall time (s) of `reps` calls after one warm-up call."""
+    fn()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times)
+
+
+def cpu_baselines(torch, cpu_inputs, slice_target_s, with_layer):
+    """The reference's torch backend -- its dense L x L PyTorch math
+    (src/lizard_attention.py:20-44), restated as oracle.lizard_oracle
+    (gla_kernel_api, swa_kernel_api, lizard_layer) -- in fp32 on the host
+    cores, median of 5 after one warm-up, fwd and fwd+bwd, on the same
+    seeded inputs as the GPU lines.  The headline runs on a sample of its
+    B*H (b, h) slices (each slice is an independent dense problem) scaled to
+    all of them; configs 1-3 run whole; config 5 runs one layer at B=1,
+    median of 3 (the dense layer at B=4 needs ~4x the ~20 GB of B=1; rows are
+    independent, so B=4 is 4x the B=1 figure)."""
+    from oracle import lizard_oracle as lo
+    cores = host_cores()
+    torch.set_num_threads(cores)
+    out = {"cores": cores, "affinity_cpus": len(os.sched_getaffinity(0)),
+           "cpu": host_cpu_name(), "method": "median of 5 after 1 warm-up, fp32"}
+
+    def gla_fb(ins, dy):
+        leaves = [t.float().requires_grad_() for t in ins]
+        lo.gla_kernel_api(*leaves, dtype=torch.float32).backward(dy.float())
+
+    def swa_fb(ins, dy, window):
+        leaves = [t.float().requires_grad_() for t in ins]
+        lo.swa_kernel_api(*leaves, window, dtype=torch.float32).backward(dy.float())
+
+    # headline (B=16 H=32 L=2048 F=D=128, per-head gate) on whole (b, h) slices
+    fq, fk, v, lg, dy = cpu_inputs["headline"]
+    bh = fq.shape[0] * fq.shape[1]
+    flat = [t.reshape(bh, 1, *t.shape[2:]) for t in (fq, fk, v, dy)]
+    lgf = lg.reshape(bh, 1, lg.shape[-1])
+
+    def sl(n):
+        return [t[:n] for t in flat[:3]] + [lgf[:n]], flat[3][:n]
+    t0 = time.perf_counter()
+    with torch.no_grad():
+        lo.gla_kernel_api(*sl(2)[0], dtype=torch.float32)
+    per = max((time.perf_counter() - t0) / 2, 1e-4)
+    n = int(max(2, min(bh, slice_target_s / per)))
+    with torch.no_grad():
+        f = cpu_median_s(lambda: lo.gla_kernel_api(*sl(n)[0], dtype=torch.float32))
+    fb = cpu_median_s(lambda: gla_fb(*sl(n)))
+    out["headline_gla"] = {"fwd_ms": round(f / n * bh * 1e3, 1),
+                           "fwd_bwd_ms": round(fb / n * bh * 1e3, 1),
+                           "sample": f"{n} of {bh} (b, h) slices at L=2048 F=D=128, scaled "
+                                     f"x{bh / n:.1f}"}
+    print(f"[bench] cpu headline: {out['headline_gla']}", file=sys.stderr, flush=True)
+    # configs 1-3, whole workloads
+    for name, key in (("config1_gla_fwd", "config1"), ("config2_gla_train", "config2")):
+        fq, fk, v, lg, dy = cpu_inputs[key]
+        with torch.no_grad():
+            f = cpu_median_s(lambda: lo.gla_kernel_api(fq, fk, v, lg, dtype=torch.float32))
+        row = {"fwd_ms": round(f * 1e3, 2)}
+        if key == "config2":
+            row["fwd_bwd_ms"] = round(cpu_median_s(lambda: gla_fb((fq, fk, v, lg), dy)) * 1e3, 2)
+        out[name] = row
+    q, k, v, meta, dy = cpu_inputs["config3"]
+    with torch.no_grad():
+        f = cpu_median_s(lambda: lo.swa_kernel_api(q, k, v, meta, 64, dtype=torch.float32))
+    out["config3_swa"] = {"fwd_ms": round(f * 1e3, 2), "fwd_bwd_ms": round(
+        cpu_median_s(lambda: swa_fb((q, k, v, meta), dy, 64)) * 1e3, 2)}
+    print(f"[bench] cpu configs 1-3: {out['config1_gla_fwd']} {out['config2_gla_train']} "
+          f"{out['config3_swa']}", file=sys.stderr, flush=True)
+    if with_layer:
+        out["config5_one_layer_b1"] = cpu_layer(torch, lo)
+        print(f"[bench] cpu config5 layer: {out['config5_one_layer_b1']}", file=sys.stderr,
+              flush=True)
+    return out
+
+
+def cpu_layer(torch, lo):
+    """One config-5 LizardAttention (hidden 2048, 32 q / 8 kv heads, head_dim
+    64, feature_dim 128, W=64, 4 sinks) as the reference's dense torch
+    backend computes it (oracle.lizard_layer, src/lizard_attention.py:73-97),
+    fp32, B=1, L=4096: fwd and fwd+bwd."""
+    import types
+    from lizard_reproduction_amd.layer import LizardAttention
+    cfg = types.SimpleNamespace(hidden_size=2048, num_attention_heads=32, num_key_value_heads=8)
+    torch.manual_seed(0)
+    layer = LizardAttention(cfg, 0, window=64, num_meta=4, feature_dim=128)
+    params = {n: p.detach().float() for n, p in layer.named_parameters()}
+    length = 4096
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(1, length, 2048, generator=g)
+    gy = torch.randn(1, length, 2048, generator=g)
+    cos, sin = (t.float()[None] for t in lo.rope_cos_sin(length, 64))
+
+    def fwd():
+        with torch.no_grad():
+            lo.lizard_layer(params, x, cos, sin, 32, 8, 64)
+
+    def fwd_bwd():
+        ps = {n: p.clone().requires_grad_() for n, p in params.items()}
+        lo.lizard_layer(ps, x.clone().requires_grad_(), cos, sin, 32, 8, 64).backward(gy)
+    return {"fwd_ms": round(cpu_median_s(fwd, 3) * 1e3, 1),
+            "fwd_bwd_ms": round(cpu_median_s(fwd_bwd, 3) * 1e3, 1),
+            "method": "median of 3 after 1 warm-up (tens of seconds per call)",
+            "note": "B=1 L=4096; the B=4 model shape is 4 independent rows (4x), 16 layers"}
+
+
+def ref_design_bytes(nf, nd, chunk):
+    """HBM bytes per (token, head) of the reference's two-kernel GLA design
+    (src/kernels/gla.py:213-263), each kernel and torch op reading and
+    writing its operands exactly once: the analytic floor of that design.
+    Forward: cumsum + expand write G (4); _gla_fwd_h reads fk, v, G and writes
+    the per-chunk states S (bf16 F x D) and z (fp32 F) -- F D / C and F / C per
+    token; _gla_fwd_o reads fq, fk, v, G, S, z, writes y (bf16), y32 (fp32) and
+    den.  Backward: delta = sum dy . y32; _gla_bwd_dh reads fq, dy, den, delta,
+    G, writes dS, dz; _gla_bwd_dqkv reads fq, fk, v, dy, G, den, delta, S, z,
+    dS, dz and writes fp32 dfq, dfk, dv; dg = sum(fq dfq - fk dfk); the casts
+    of the fp32 grads to bf16; the gate gradient's reverse cumsum (4 + 4).
+    Returns (forward, backward) bytes."""
+    F, D, C = nf, nd, chunk
+    st, zz = 2 * F * D / C, 4 * F / C
+    gate = 4
+    fwd = gate + (2 * F + 2 * D + gate + st + zz) + \
+        (2 * F + 2 * F + 2 * D + gate + st + zz + 2 * D + 4 * D + 4)
+    bwd = (2 * D + 4 * D + 4) + \
+        (2 * F + 2 * D + 4 + 4 + gate + st + zz) + \
+        (2 * F + 2 * F + 2 * D + 2 * D + gate + 4 + 4 + 2 * st + 2 * zz + 4 * F + 4 * F + 4 * D) + \
+        (2 * F + 4 * F + 2 * F + 4 * F + 4) + \
+        (4 * F + 4 * F + 4 * D + 2 * F + 2 * F + 2 * D) + 8
+    return fwd, bwd
+
+
+def gla_fwd_bwd_bytes(bh, length, nf, nd, per_head):
+    """Algorithmic HBM bytes of one fwd+bwd: the forward's, then the backward
+    reading fq, fk, v, dy and the gate and writing bf16 dfq, dfk, dv and the
+    fp32 gate gradient (12F + 10D + 12 per token and head with a per-head
+    gate)."""
+    gate = 4 if per_head else 0
+    return gla_fwd_bytes(bh, length, nf, nd, per_head) + \
+        bh * length * (4 * nf + 4 * nd + gate + 4 * nf + 2 * nd + gate)
+
+
+def swa_fwd_bwd_bytes(bh, length, d):
+    """SWA fwd (read q, k, v; write y, lse) + bwd (read q, k, v, dy, lse;
+    write dq, dk, dv): 22d + 8 bytes per token and head."""
+    return bh * length * (22 * d + 8)
+
+
+def time_headline(torch, kernels, fq, fk, v, lg, steps, warmup, settle_s=2.0):
+    """Event-timed mean of `steps` back-to-back headline forwards on the
+    current stream, after launching the same forward untimed for `settle_s`
+    seconds of wall time (so the GPU's clocks have settled, whatever the
+    driver's --warmup) and then `warmup` more untimed steps."""
+    with torch.no_grad():
+        t_end = time.perf_counter() + settle_s
+        while time.perf_counter() < t_end:
+            for _ in range(20):
+                kernels.gla(fq, fk, v, lg)
+            torch.cuda.synchronize()
+        for _ in range(warmup):
+            kernels.gla(fq, fk, v, lg)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(steps):
+            kernels.gla(fq, fk, v, lg)
+        end.record()
+        torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def copy_calibration(torch):
+    """A plain 1 GiB device copy (torch's copy_, the runtime's copyBuffer
+    kernel): the kernel of known size whose rocprofv3 FETCH_SIZE and
+    WRITE_SIZE scale those counters to bytes."""
+    src = torch.empty(1 << 29, dtype=torch.bfloat16, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    t = median_ms(torch, lambda: dst.copy_(src), 10, 2)
+    out = {"bytes_read": src.numel() * 2, "bytes_written": dst.numel() * 2,
+           "ms": round(t, 4), "gbs": round(2 * src.numel() * 2 / t / 1e6, 1)}
+    print(f"[bench] copy calibration: {out}", file=sys.stderr, flush=True)
+    return out
+
+
+def profile_workload(torch, kernels, name, steps, settle_s):
+    """--only NAME: run one workload `steps` times after 3 warm-ups, for
+    counter and trace runs (rocprofv3) that should see those kernels alone;
+    with settle_s > 0 the workload first runs untimed for that many seconds
+    (steady clocks for trace runs; counter runs keep it 0, as every
+    dispatch under counters is recorded)."""
+    if name == "headline_fwd_bwd":
+        ins = gla_inputs(torch, 16, 32, 2048, 128, True, 2.0, 1.5)
+        run, reset = fwd_bwd_fn(torch, kernels.gla, ins[:4], ins[4])
+    elif name == "config2":
+        ins = gla_inputs(torch, 1, 32, 2048, 64, False, 3.0, 1.0)
+        run, reset = fwd_bwd_fn(torch, kernels.gla, ins[:4], ins[4])
+    elif name == "config3":
+        ins = swa_inputs(torch, 1, 32, 2048, 64)
+        run, reset = fwd_bwd_fn(torch, kernels.swa, ins[:4], ins[4], (64,))
+    elif name == "config5_layer":
+        return {"config5_layer": layer_stack(torch, steps, 1, one_layer=True, decode=False)}
+    else:
+        raise SystemExit(f"unknown --only workload {name!r}")
+    t_end = time.perf_counter() + settle_s
+    while time.perf_counter() < t_end:
+        run()
+        reset()
+        torch.cuda.synchronize()
+    t = median_ms(torch, run, steps, 3, reset)
+    return {name: {"fwd_bwd_ms": round(t, 4), "steps": steps}}
 
 
 def main():
@@ -369,21 +598,19 @@ def main():
                                                                        args.one_layer)}}),
               flush=True)
         return
+    if args.only:
+        extra = profile_workload(torch, kernels, args.only, args.steps, args.settle_seconds)
+        if args.copy_calibration:
+            extra["copy_calibration"] = copy_calibration(torch)
+        print(json.dumps({"extra": extra}), flush=True)
+        return
 
     # ---- headline: GLA forward, B=16 H=32 L=2048 F=D=128, per-head gate -----
     B, H, L, D = 16, 32, 2048, 128
     fq, fk, v, lg, dy = gla_inputs(torch, B, H, L, D, True, 2.0, 1.5)
-    with torch.no_grad():
-        for _ in range(args.warmup):
-            kernels.gla(fq, fk, v, lg)
-        torch.cuda.synchronize()
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record()
-        for _ in range(args.steps):
-            kernels.gla(fq, fk, v, lg)
-        end.record()
-        torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / args.steps
+    cpu_inputs = {"headline": [t.cpu() for t in (fq, fk, v, lg, dy)]}
+    ms = time_headline(torch, kernels, fq, fk, v, lg, args.steps, args.warmup,
+                       0.0 if args.headline_only else args.settle_seconds)
     flops = gla_fwd_flops(B * H, L, D, D)
     nbytes = gla_fwd_bytes(B * H, L, D, D, True)
     achieved_gbs = nbytes / (ms * 1e-3) / 1e9
@@ -397,15 +624,10 @@ def main():
         "mfma_peak_frac": round(tflops / MFMA_BF16_PEAK_TFS, 4),
         "attainable_tflops": round(attainable, 1),
         "attainable_frac": round(tflops / attainable, 4),
-        "flops": flops, "bytes": nbytes}}
+        "flops": flops, "bytes": nbytes,
+        "clock_settle_s": 0.0 if args.headline_only else args.settle_seconds}}
     if args.copy_calibration:
-        src = torch.empty(1 << 29, dtype=torch.bfloat16, device="cuda").fill_(1.0)
-        dst = torch.empty_like(src)
-        t = median_ms(torch, lambda: dst.copy_(src), 10, 2)
-        extra["copy_calibration"] = {"bytes_read": src.numel() * 2, "bytes_written": dst.numel() * 2,
-                                     "ms": round(t, 4), "gbs": round(2 * src.numel() * 2 / t / 1e6, 1)}
-        print(f"[bench] copy calibration: {extra['copy_calibration']}", file=sys.stderr, flush=True)
-        del src, dst
+        extra["copy_calibration"] = copy_calibration(torch)
     if args.headline_only:
         print(json.dumps({"metric": METRIC, "value": round(ms, 4), "unit": "ms",
                           "ms_per_step": round(ms, 4), "steps": args.steps, "extra": extra}),
@@ -416,28 +638,51 @@ def main():
     run, reset = fwd_bwd_fn(torch, kernels.gla, (fq, fk, v, lg), dy)
     t = median_ms(torch, run, iters, 5, reset)
     f = gla_fwd_bwd_flops(B * H, L, D, D)
-    extra["headline_gla_fwd_bwd"] = {"ms": round(t, 4), "tflops": round(f / t / 1e9, 2),
-                                     "mfma_peak_frac": round(f / t / 1e9 / MFMA_BF16_PEAK_TFS, 4)}
-    print(f"[bench] GLA fwd+bwd headline: {t:.4f} ms", file=sys.stderr, flush=True)
-
-    cpu = None
-    if not args.no_cpu_baseline:
-        cpu = cpu_baseline(torch, fq, fk, v, lg, args.cpu_seconds)
-        print(f"[bench] cpu baseline: {cpu}", file=sys.stderr, flush=True)
+    fbb = gla_fwd_bwd_bytes(B * H, L, D, D, True)
+    extra["headline_gla_fwd_bwd"] = {
+        "ms": round(t, 4), "tflops": round(f / t / 1e9, 2),
+        "mfma_peak_frac": round(f / t / 1e9 / MFMA_BF16_PEAK_TFS, 4),
+        "algorithmic_bytes": fbb, "gbs": round(fbb / t / 1e6, 1),
+        "hbm_frac": round(fbb / t / 1e6 / HBM_PEAK_GBS, 4),
+        "hbm_floor_ms": round(fbb / HBM_PEAK_GBS / 1e6, 4)}
+    print(f"[bench] GLA fwd+bwd headline: {extra['headline_gla_fwd_bwd']}", file=sys.stderr,
+          flush=True)
     del fq, fk, v, lg, dy, run, reset
     torch.cuda.empty_cache()
 
+    # ---- config 1: GLA forward (the reference's CPU-runnable case) -----------
+    ins = gla_inputs(torch, 1, 4, 256, 64, False, 3.0, 1.0)
+    cpu_inputs["config1"] = [t.cpu() for t in ins]
+    with torch.no_grad():
+        t_f = median_ms(torch, lambda: kernels.gla(*ins[:4]), 100, 10)
+    extra["config1_gla_fwd"] = {"shape": "B=1 H=4 L=256 F=D=64 per-token gate",
+                                "fwd_ms": round(t_f, 4)}
+    del ins
+
     # ---- config 2: GLA training shape, per-token gate -----------------------
     fq, fk, v, lg, dy = gla_inputs(torch, 1, 32, 2048, 64, False, 3.0, 1.0)
+    cpu_inputs["config2"] = [t.cpu() for t in (fq, fk, v, lg, dy)]
     with torch.no_grad():
         t_f = median_ms(torch, lambda: kernels.gla(fq, fk, v, lg), 100, 10)
     run, reset = fwd_bwd_fn(torch, kernels.gla, (fq, fk, v, lg), dy)
     t_fb = median_ms(torch, run, 100, 10, reset)
+    c2b = gla_fwd_bwd_bytes(32, 2048, 64, 64, False)
+    rf, rb = ref_design_bytes(64, 64, CHUNK)
+    units = 32 * 2048
     extra["config2_gla_train"] = {
         "shape": "B=1 H=32 L=2048 F=D=64 per-token gate", "fwd_ms": round(t_f, 4),
         "fwd_bwd_ms": round(t_fb, 4),
         "fwd_tflops": round(gla_fwd_flops(32, 2048, 64, 64) / t_f / 1e9, 2),
-        "fwd_bwd_tflops": round(gla_fwd_bwd_flops(32, 2048, 64, 64) / t_fb / 1e9, 2)}
+        "fwd_bwd_tflops": round(gla_fwd_bwd_flops(32, 2048, 64, 64) / t_fb / 1e9, 2),
+        "algorithmic_bytes": c2b, "hbm_floor_ms": round(c2b / HBM_PEAK_GBS / 1e6, 4),
+        "reference_design": {
+            "bytes_per_token_head": {"fwd": rf, "bwd": rb},
+            "fwd_bwd_bytes": int((rf + rb) * units),
+            "hbm_floor_fwd_ms": round(rf * units / HBM_PEAK_GBS / 1e6, 4),
+            "hbm_floor_fwd_bwd_ms": round((rf + rb) * units / HBM_PEAK_GBS / 1e6, 4),
+            "note": "analytic HBM floor of the reference's two-kernel Triton design "
+                    "(src/kernels/gla.py) at this shape; its ROCm-Triton build cannot run "
+                    "here (the reference's source may not travel to the GPU box)"}}
     # the same fwd+bwd as back-to-back C-ABI launches without autograd: what
     # the kernels sustain when the host keeps ahead of them (the autograd
     # figure above is bound by torch's host-side cost at this size)
@@ -450,17 +695,20 @@ def main():
 
     # ---- config 3: SWA with sinks -------------------------------------------
     q, k, v, meta, dy = swa_inputs(torch, 1, 32, 2048, 64)
+    cpu_inputs["config3"] = [t.cpu() for t in (q, k, v, meta, dy)]
     with torch.no_grad():
         t_f = median_ms(torch, lambda: kernels.swa(q, k, v, meta, 64), 100, 10)
     run, reset = fwd_bwd_fn(torch, kernels.swa, (q, k, v, meta), dy, (64,))
     t_fb = median_ms(torch, run, 100, 10, reset)
     swa_bytes = 32 * 2048 * (8 * 64 + 4)
+    c3b = swa_fwd_bwd_bytes(32, 2048, 64)
     extra["config3_swa"] = {
         "shape": "B=1 H=32 L=2048 d=64 W=64 4 sinks", "fwd_ms": round(t_f, 4),
         "fwd_bwd_ms": round(t_fb, 4),
         "fwd_tflops": round(swa_flops(32, 2048, 64, 64, False) / t_f / 1e9, 2),
         "fwd_bwd_tflops": round(swa_flops(32, 2048, 64, 64, True) / t_fb / 1e9, 2),
-        "fwd_gbs": round(swa_bytes / t_f / 1e6, 1)}
+        "fwd_gbs": round(swa_bytes / t_f / 1e6, 1),
+        "algorithmic_bytes": c3b, "hbm_floor_ms": round(c3b / HBM_PEAK_GBS / 1e6, 4)}
     def swa_launches():
         _, lse = kernels.swa_forward(q, k, v, meta, 64)
         kernels.swa_backward(q, k, v, meta, lse, dy, 64, torch.bfloat16)
@@ -475,8 +723,8 @@ def main():
         for b in (1, 4, 16):
             for length in (2048, 4096, 8192, 16384):
                 fq, fk, v, lg, dy = gla_inputs(torch, b, 32, length, 128, True, 2.0, 1.5)
-                with torch.no_grad():
-                    t_f = median_ms(torch, lambda: kernels.gla(fq, fk, v, lg), 20, 3)
+                # forward: mean of back-to-back launches, as the headline
+                t_f = time_headline(torch, kernels, fq, fk, v, lg, 20, 3, 0.3)
                 run, reset = fwd_bwd_fn(torch, kernels.gla, (fq, fk, v, lg), dy)
                 t_fb = median_ms(torch, run, 10, 2, reset)
                 ff = gla_fwd_flops(b * 32, length, 128, 128)
@@ -484,6 +732,8 @@ def main():
                 row = {"B": b, "L": length, "fwd_ms": round(t_f, 4), "fwd_bwd_ms": round(t_fb, 4),
                        "fwd_tflops": round(ff / t_f / 1e9, 1),
                        "fwd_mfma_frac": round(ff / t_f / 1e9 / MFMA_BF16_PEAK_TFS, 4),
+                       "fwd_hbm_frac": round(gla_fwd_bytes(b * 32, length, 128, 128, True) /
+                                             t_f / 1e6 / HBM_PEAK_GBS, 4),
                        "fwd_bwd_tflops": round(fb / t_fb / 1e9, 1)}
                 sweep.append(row)
                 print(f"[bench] sweep {row}", file=sys.stderr, flush=True)
@@ -494,6 +744,20 @@ def main():
     # ---- config 5: layer stack ------------------------------------------------
     if not args.no_layer:
         extra["config5_layer_stack"] = layer_stack(torch, 3, 1)
+
+    # ---- CPU baseline (the GPU is idle from here on) --------------------------
+    cpu = None
+    if not args.no_cpu_baseline:
+        base = cpu_baselines(torch, cpu_inputs, args.cpu_seconds, not args.no_layer)
+        extra["cpu_baselines"] = base
+        h = base["headline_gla"]
+        cpu = {"value": h["fwd_ms"], "unit": "ms", "cores": base["cores"], "kind": "port",
+               "sample": (f"dense fp32 torch-backend math (oracle.gla_kernel_api, "
+                          f"src/lizard_attention.py:20-31) of the headline forward on "
+                          f"{h['sample']}; {base['method']}; {base['cores']} threads "
+                          f"({base['affinity_cpus']} CPUs in the affinity mask) on "
+                          f"{base['cpu']}; fwd+bwd {h['fwd_bwd_ms']} ms; configs 1-3 and "
+                          f"config 5 in extra.cpu_baselines")}
 
     line = {
         "metric": METRIC, "value": round(ms, 4), "unit": "ms", "n_gpus": 1,
