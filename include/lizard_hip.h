@@ -32,7 +32,12 @@
 extern "C" {
 #endif
 
-#define LZ_ABI_VERSION 10
+#define LZ_ABI_VERSION 11
+
+/* Largest feature (nf) and value (nd) dim the GLA entry points take. */
+#define LZ_GLA_MAX_DIM 4096
+/* Most sink logits (n_meta) the SWA entry points take. */
+#define LZ_SWA_MAX_META 65536
 
 /* ABI version of the loaded library (LZ_ABI_VERSION). */
 int lz_abi_version(void);
@@ -63,7 +68,13 @@ size_t lz_gla_fwd_workspace_bytes(int batch, int heads, int length, int nf, int 
  *   workspace   device buffer of lz_gla_fwd_workspace_bytes() bytes (may be
  *               NULL when that is 0): per-segment states when the sequence is
  *               split into segments to fill the GPU
- * Supported sizes: nf <= 256, nd <= 128, and nd <= 64 when nf > 128.
+ * Sizes: any nf, nd up to LZ_GLA_MAX_DIM, as the reference's kernels loop
+ * over feature blocks (src/kernels/gla.py:74,154,171).  The walks take
+ * nf <= 256, nd <= 128 (nd <= 64 when nf > 128) directly; past that the
+ * library runs them on value tiles (exact) and, for nf > 256, on feature
+ * tiles whose unnormalised numerators and denominators it sums before the
+ * division (the bf16 weights a rounded per tile), with the workspace size
+ * that lz_gla_fwd_workspace_bytes reports.
  * Nothing is saved for the backward: lz_gla_bwd recomputes what it needs, so
  * the output is the same with and without autograd (tests/test_kernels.py:102-107).
  */
@@ -75,8 +86,9 @@ int lz_gla_fwd(const void* fq, const void* fk, const void* v, const float* log_g
  * GLA forward that allocates nothing and takes no workspace.  No counterpart
  * in the reference: it is for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc).  Same arguments, sizes, result and kernels as lz_gla_fwd
- * without the workspace: the per-segment states that lz_gla_fwd keeps in
+ * hipMalloc).  Same arguments, result and kernels as lz_gla_fwd without the
+ * workspace, at the walks' own sizes (nf <= 256, nd <= 128, nd <= 64 when
+ * nf > 128): the per-segment states that lz_gla_fwd keeps in
  * its workspace (when B*H alone cannot fill the GPU) live in a static device
  * array of LZ_GLA_FWD_NOALLOC_MAX_BYTES per GPU, held until the process
  * ends.  That covers every size the forward takes on a whole MI355X; sizes
@@ -97,7 +109,8 @@ int lz_gla_fwd_noalloc(const void* fq, const void* fk, const void* v, const floa
  * path); the state is that of its recurrent form (tests/test_lizard.py:41-52):
  *   S_L = sum_t (prod_{s>t} gamma_s) fk_t v_t^T,  z_L = sum_t (prod_{s>t} gamma_s) fk_t
  *   state  f32 [B, H, nf*nd + nf]: S row-major [nf][nd], then z [nf]
- * Other arguments as lz_gla_fwd (same workspace).
+ * Other arguments as lz_gla_fwd (same workspace), at the walks' own sizes:
+ * nf <= 256, nd <= 128, nd <= 64 when nf > 128.
  */
 int lz_gla_prefill(const void* fq, const void* fk, const void* v, const float* log_gamma,
                    void* y, float* state, int batch, int heads, int kv_heads, int length, int nf,
@@ -112,6 +125,7 @@ int lz_gla_prefill(const void* fq, const void* fk, const void* v, const float* l
  *   (query head h reads kv head h / (heads / kv_heads));  y  bf16 [B, H, nd]
  *   log_gamma  f32 [B] (gate_per_head = 0) or [B, H];  gamma = exp(log_gamma)
  *   state  f32 [B, H, nf*nd + nf] as written by lz_gla_prefill (zeros: empty prefix)
+ * Sizes as lz_gla_prefill.
  */
 int lz_gla_decode_step(const void* fq, const void* fk, const void* v, const float* log_gamma,
                        float* state, void* y, int batch, int heads, int kv_heads, int nf, int nd,
@@ -133,7 +147,7 @@ size_t lz_gla_bwd_workspace_bytes(int batch, int heads, int length, int nf, int 
  *   fwd_workspace the workspace lz_gla_fwd used for these inputs, if the caller
  *                 kept it (it then holds the state entering each segment and
  *                 the backward skips recomputing it); may be NULL
- * The other arguments are those of lz_gla_fwd.
+ * The other arguments are those of lz_gla_fwd, with its sizes.
  */
 int lz_gla_bwd(const void* fq, const void* fk, const void* v, const float* log_gamma,
                const void* dy, void* dfq, void* dfk, void* dv, float* dlog_gamma, int grad_bf16,
@@ -147,7 +161,7 @@ int lz_gla_bwd(const void* fq, const void* fk, const void* v, const float* log_g
  *   q           bf16 [BH, L, dim]  (RoPE already applied)
  *   k, v        bf16 [B*kv_heads, L, dim]  (RoPE applied to k); kv_heads divides
  *               heads, query head h reads kv head h / (heads / kv_heads)
- *   meta        f32 [n_meta] sink logits (n_meta may be 0; at most 64)
+ *   meta        f32 [n_meta] sink logits (n_meta may be 0; at most LZ_SWA_MAX_META)
  *   y           bf16 [BH, L, dim] output
  *   lse         f32 [BH, L] log of each row's softmax denominator (saved for backward)
  *   window      keys i-window < t <= i;  scale  usually 1/sqrt(dim)

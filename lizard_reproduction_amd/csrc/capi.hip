@@ -12,17 +12,27 @@
 namespace lz {
 hipError_t launch_gla_fwd(const void* fq, const void* fk, const void* v, const float* lg, void* y,
                           int B, int H, int L, int F, int D, int gate_per_head, int KG, float* ws,
-                          float* final_state, hipStream_t st);
+                          float* final_state, float* raw_den, hipStream_t st);
 hipError_t launch_gla_decode(const void* fq, const void* fk, const void* v, const float* lg,
                              float* state, void* y, int B, int H, int F, int D,
                              int gate_per_head, int KG, hipStream_t st);
 size_t gla_fwd_workspace(int B, int H, int L, int F, int D);
-hipError_t launch_gla_bwd(const void* fq, const void* fk, const void* v, const float* lg,
-                          const void* dy, void* dfq, void* dfk, void* dv, float* dlg,
-                          bool grad_bf16, int B, int H, int L, int F, int D, int gate_per_head,
-                          int KG, const float* fwd_ws, float* ws, hipStream_t st);
-size_t gla_bwd_workspace(int B, int H, int L, int F, int D, int gate_per_head);
 bool gla_dims_supported(int F, int D);
+struct GlaTiles {
+  int nF, Ft, nD, Dt;
+  bool native() const { return nF == 1 && nD == 1; }
+};
+GlaTiles gla_tiles(int F, int D);
+size_t gla_fwd_workspace_any(int B, int H, int L, int F, int D);
+size_t gla_bwd_workspace_any(int B, int H, int L, int F, int D, int gate_per_head);
+hipError_t launch_gla_fwd_any(const void* fq, const void* fk, const void* v, const float* lg,
+                              void* y, int B, int H, int L, int F, int D, int gate_per_head,
+                              int KG, void* ws, hipStream_t st);
+hipError_t launch_gla_bwd_any(const void* fq, const void* fk, const void* v, const float* lg,
+                              const void* dy, void* dfq, void* dfk, void* dv, float* dlg,
+                              bool grad_bf16, int B, int H, int L, int F, int D,
+                              int gate_per_head, int KG, const float* fwd_ws, void* ws,
+                              hipStream_t st);
 int swa_padded_dim(int d);
 int swa_row_blocks(int L);
 hipError_t launch_swa_fwd(const void* q, const void* k, const void* v, const float* meta,
@@ -37,7 +47,7 @@ hipError_t launch_swa_bwd(const void* q, const void* k, const void* v, const flo
                           void* dv, bool grad_bf16, float* delta, float* dmeta_part,
                           float* dmeta, int BH, int L, int d, int W, float scale, int KG,
                           hipStream_t st);
-constexpr int MAX_META = 64;
+constexpr int MAX_META = LZ_SWA_MAX_META;
 bool prologue_dims_supported(int hd, int f);
 size_t prologue_bwd_workspace(int B, int L, int H, int Hkv, int hd, int f);
 hipError_t launch_prologue_fwd(const void* q, const void* k, const void* v, const void* wq,
@@ -99,16 +109,22 @@ static int check_extent(const char* what, int batch, int heads, int length, int 
   return 0;
 }
 
+// `native`: the entry point runs the walks directly (prefill, decode, the
+// no-allocation forward), so F and D must be within their own sizes; the
+// forward and backward take any F and D (tiles of the walks past them).
 static int check_gla(const void* fq, const void* fk, const void* v, const float* lg, int batch,
-                     int heads, int length, int nf, int nd, int chunk) {
+                     int heads, int length, int nf, int nd, int chunk, bool native) {
   if (!fq || !fk || !v || !lg) return fail(1, "gla: null input pointer");
   if (batch <= 0 || heads <= 0 || length <= 0 || nf <= 0 || nd <= 0)
     return fail(1, "gla: sizes must be positive (B=%d H=%d L=%d F=%d D=%d)", batch, heads,
                 length, nf, nd);
   if (!pow2_at_least_16(chunk)) return fail(1, "gla: chunk must be a power of two >= 16, got %d", chunk);
-  if (!lz::gla_dims_supported(nf, nd))
-    return fail(1, "gla: unsupported feature/value dims F=%d D=%d (need F<=256, D<=128, "
-                   "and D<=64 when F>128)", nf, nd);
+  if (native && !lz::gla_dims_supported(nf, nd))
+    return fail(1, "gla: unsupported feature/value dims F=%d D=%d for this entry point (need "
+                   "F<=256, D<=128, and D<=64 when F>128)", nf, nd);
+  if (nf > LZ_GLA_MAX_DIM || nd > LZ_GLA_MAX_DIM)
+    return fail(1, "gla: feature/value dims F=%d D=%d beyond %d unsupported", nf, nd,
+                LZ_GLA_MAX_DIM);
   return check_extent("gla", batch, heads, length, nf > nd ? nf : nd);
 }
 
@@ -124,23 +140,26 @@ static int check_kv_heads(const char* what, int heads, int kv_heads) {
 extern "C" size_t lz_gla_fwd_workspace_bytes(int batch, int heads, int length, int nf, int nd,
                                              int gate_per_head, int chunk) {
   (void)gate_per_head; (void)chunk;
-  if (batch <= 0 || heads <= 0 || length <= 0 || !lz::gla_dims_supported(nf, nd)) return 0;
-  return lz::gla_fwd_workspace(batch, heads, length, nf, nd);
+  if (batch <= 0 || heads <= 0 || length <= 0 || nf <= 0 || nd <= 0 || nf > LZ_GLA_MAX_DIM ||
+      nd > LZ_GLA_MAX_DIM)
+    return 0;
+  return lz::gla_fwd_workspace_any(batch, heads, length, nf, nd);
 }
 
 extern "C" int lz_gla_fwd(const void* fq, const void* fk, const void* v, const float* log_gamma,
                           void* y, int batch, int heads, int kv_heads, int length, int nf, int nd,
                           int gate_per_head, int chunk, void* workspace, size_t workspace_bytes,
                           void* stream) {
-  if (int rc = check_gla(fq, fk, v, log_gamma, batch, heads, length, nf, nd, chunk)) return rc;
+  if (int rc = check_gla(fq, fk, v, log_gamma, batch, heads, length, nf, nd, chunk, false))
+    return rc;
   if (int rc = check_kv_heads("gla_fwd", heads, kv_heads)) return rc;
   if (!y) return fail(1, "gla_fwd: null output pointer");
-  const size_t need = lz::gla_fwd_workspace(batch, heads, length, nf, nd);
+  const size_t need = lz::gla_fwd_workspace_any(batch, heads, length, nf, nd);
   if (need && (!workspace || workspace_bytes < need))
     return fail(1, "gla_fwd: workspace of %zu bytes given, %zu needed", workspace_bytes, need);
-  return hip_status(lz::launch_gla_fwd(fq, fk, v, log_gamma, y, batch, heads, length, nf, nd,
-                                       gate_per_head ? 1 : 0, heads / kv_heads, (float*)workspace,
-                                       nullptr, (hipStream_t)stream),
+  return hip_status(lz::launch_gla_fwd_any(fq, fk, v, log_gamma, y, batch, heads, length, nf, nd,
+                                           gate_per_head ? 1 : 0, heads / kv_heads, workspace,
+                                           (hipStream_t)stream),
                     "gla_fwd");
 }
 
@@ -148,7 +167,8 @@ extern "C" int lz_gla_prefill(const void* fq, const void* fk, const void* v,
                               const float* log_gamma, void* y, float* state, int batch, int heads,
                               int kv_heads, int length, int nf, int nd, int gate_per_head,
                               int chunk, void* workspace, size_t workspace_bytes, void* stream) {
-  if (int rc = check_gla(fq, fk, v, log_gamma, batch, heads, length, nf, nd, chunk)) return rc;
+  if (int rc = check_gla(fq, fk, v, log_gamma, batch, heads, length, nf, nd, chunk, true))
+    return rc;
   if (int rc = check_kv_heads("gla_prefill", heads, kv_heads)) return rc;
   if (!y || !state) return fail(1, "gla_prefill: null output pointer");
   const size_t need = lz::gla_fwd_workspace(batch, heads, length, nf, nd);
@@ -157,7 +177,7 @@ extern "C" int lz_gla_prefill(const void* fq, const void* fk, const void* v,
                 need);
   return hip_status(lz::launch_gla_fwd(fq, fk, v, log_gamma, y, batch, heads, length, nf, nd,
                                        gate_per_head ? 1 : 0, heads / kv_heads, (float*)workspace,
-                                       state, (hipStream_t)stream),
+                                       state, nullptr, (hipStream_t)stream),
                     "gla_prefill");
 }
 
@@ -165,7 +185,7 @@ extern "C" int lz_gla_decode_step(const void* fq, const void* fk, const void* v,
                                   const float* log_gamma, float* state, void* y, int batch,
                                   int heads, int kv_heads, int nf, int nd, int gate_per_head,
                                   void* stream) {
-  if (int rc = check_gla(fq, fk, v, log_gamma, batch, heads, 1, nf, nd, 64)) return rc;
+  if (int rc = check_gla(fq, fk, v, log_gamma, batch, heads, 1, nf, nd, 64, true)) return rc;
   if (int rc = check_kv_heads("gla_decode_step", heads, kv_heads)) return rc;
   if (!state || !y) return fail(1, "gla_decode_step: null state or output pointer");
   return hip_status(lz::launch_gla_decode(fq, fk, v, log_gamma, state, y, batch, heads, nf, nd,
@@ -177,8 +197,10 @@ extern "C" int lz_gla_decode_step(const void* fq, const void* fk, const void* v,
 extern "C" size_t lz_gla_bwd_workspace_bytes(int batch, int heads, int length, int nf, int nd,
                                              int gate_per_head, int chunk) {
   (void)chunk;
-  if (batch <= 0 || heads <= 0 || length <= 0 || !lz::gla_dims_supported(nf, nd)) return 0;
-  return lz::gla_bwd_workspace(batch, heads, length, nf, nd, gate_per_head ? 1 : 0);
+  if (batch <= 0 || heads <= 0 || length <= 0 || nf <= 0 || nd <= 0 || nf > LZ_GLA_MAX_DIM ||
+      nd > LZ_GLA_MAX_DIM)
+    return 0;
+  return lz::gla_bwd_workspace_any(batch, heads, length, nf, nd, gate_per_head ? 1 : 0);
 }
 
 extern "C" int lz_gla_bwd(const void* fq, const void* fk, const void* v, const float* log_gamma,
@@ -187,15 +209,19 @@ extern "C" int lz_gla_bwd(const void* fq, const void* fk, const void* v, const f
                           int nd, int gate_per_head, int chunk, const void* fwd_workspace,
                           size_t fwd_workspace_bytes, void* workspace, size_t workspace_bytes,
                           void* stream) {
-  if (int rc = check_gla(fq, fk, v, log_gamma, batch, heads, length, nf, nd, chunk)) return rc;
+  if (int rc = check_gla(fq, fk, v, log_gamma, batch, heads, length, nf, nd, chunk, false))
+    return rc;
   if (int rc = check_kv_heads("gla_bwd", heads, kv_heads)) return rc;
   if (!dy || !dfq || !dfk || !dv || !dlog_gamma) return fail(1, "gla_bwd: null pointer");
-  const size_t need = lz::gla_bwd_workspace(batch, heads, length, nf, nd, gate_per_head ? 1 : 0);
+  const size_t need =
+      lz::gla_bwd_workspace_any(batch, heads, length, nf, nd, gate_per_head ? 1 : 0);
   if (!workspace || workspace_bytes < need)
     return fail(1, "gla_bwd: workspace of %zu bytes given, %zu needed", workspace_bytes, need);
   // the forward's workspace, if the caller kept it, already holds the state
-  // entering each segment; otherwise the backward recomputes it
-  const size_t fneed = lz::gla_fwd_workspace(batch, heads, length, nf, nd);
+  // entering each segment; otherwise the backward recomputes it (always for
+  // sizes past the walks', whose forward workspace holds tiles instead)
+  const bool native = lz::gla_dims_supported(nf, nd);
+  const size_t fneed = native ? lz::gla_fwd_workspace(batch, heads, length, nf, nd) : 0;
   const float* fws = nullptr;
   if (fwd_workspace && fneed) {
     if (fwd_workspace_bytes < fneed)
@@ -203,10 +229,10 @@ extern "C" int lz_gla_bwd(const void* fq, const void* fk, const void* v, const f
                   fwd_workspace_bytes, fneed);
     fws = (const float*)fwd_workspace;
   }
-  return hip_status(lz::launch_gla_bwd(fq, fk, v, log_gamma, dy, dfq, dfk, dv, dlog_gamma,
-                                       grad_bf16 != 0, batch, heads, length, nf, nd,
-                                       gate_per_head ? 1 : 0, heads / kv_heads, fws,
-                                       (float*)workspace, (hipStream_t)stream),
+  return hip_status(lz::launch_gla_bwd_any(fq, fk, v, log_gamma, dy, dfq, dfk, dv, dlog_gamma,
+                                           grad_bf16 != 0, batch, heads, length, nf, nd,
+                                           gate_per_head ? 1 : 0, heads / kv_heads, fws,
+                                           workspace, (hipStream_t)stream),
                     "gla_bwd");
 }
 
@@ -251,7 +277,8 @@ extern "C" int lz_gla_fwd_noalloc(const void* fq, const void* fk, const void* v,
                                   const float* log_gamma, void* y, int batch, int heads,
                                   int kv_heads, int length, int nf, int nd, int gate_per_head,
                                   int chunk, void* stream) {
-  if (int rc = check_gla(fq, fk, v, log_gamma, batch, heads, length, nf, nd, chunk)) return rc;
+  if (int rc = check_gla(fq, fk, v, log_gamma, batch, heads, length, nf, nd, chunk, true))
+    return rc;
   if (int rc = check_kv_heads("gla_fwd_noalloc", heads, kv_heads)) return rc;
   if (!y) return fail(1, "gla_fwd_noalloc: null output pointer");
   const size_t need = lz::gla_fwd_workspace(batch, heads, length, nf, nd);
@@ -264,7 +291,7 @@ extern "C" int lz_gla_fwd_noalloc(const void* fq, const void* fk, const void* v,
     if (int rc = scratch_address(&ws)) return rc;
   return hip_status(lz::launch_gla_fwd(fq, fk, v, log_gamma, y, batch, heads, length, nf, nd,
                                        gate_per_head ? 1 : 0, heads / kv_heads, ws, nullptr,
-                                       (hipStream_t)stream),
+                                       nullptr, (hipStream_t)stream),
                     "gla_fwd_noalloc");
 }
 

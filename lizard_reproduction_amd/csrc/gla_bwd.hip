@@ -130,7 +130,11 @@ struct BwdA : BwdCommon<FP, DP> {
   static_assert(BYTES <= 160 * 1024, "LDS budget");
 };
 
-template <int FP, int DP, typename OutT, bool VEC>
+// EXT (one F tile of a split feature dimension): den and delta are not
+// formed from this tile's features but read from den_out / delta_out, where
+// the caller has put those of the whole feature dimension; the kernel then
+// writes this tile's share of every gradient.
+template <int FP, int DP, typename OutT, bool VEC, bool EXT>
 __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
     const bf16* __restrict__ fq, const bf16* __restrict__ fk, const bf16* __restrict__ v,
     const float* __restrict__ log_gamma, const bf16* __restrict__ dy, OutT* __restrict__ dfq,
@@ -364,12 +368,19 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
     __syncthreads();
     // ---- phase 2: den, delta, dad fragments (waves 0-3) ------------------------
     if (live) {
-      const float den = ra[qi] + ra[64 + qi] + qz[qi] + qz[64 + qi] + qz[128 + qi] + qz[192 + qi];
-      float num = rav[qi] + rav[64 + qi];
+      float den, delta;
+      if constexpr (EXT) {
+        const bool ok = t0 + qi < L;
+        den = ok ? den_out[offL + t0 + qi] : 0.f;
+        delta = ok ? delta_out[offL + t0 + qi] : 0.f;
+      } else {
+        den = ra[qi] + ra[64 + qi] + qz[qi] + qz[64 + qi] + qz[128 + qi] + qz[192 + qi];
+        float num = rav[qi] + rav[64 + qi];
 #pragma unroll
-      for (int ft = 0; ft < NFT; ++ft) num += nx[ft * 64 + qi];
+        for (int ft = 0; ft < NFT; ++ft) num += nx[ft * 64 + qi];
+        delta = num / fmaxf(den, TINY);
+      }
       const float dcl = fmaxf(den, TINY);
-      const float delta = num / dcl;
       const float inv = 1.f / dcl;
       bf16x8 d8[2];
 #pragma unroll
@@ -379,7 +390,7 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
       if (kt == 0 && h == 0) {
         dens[qi] = den;
         dels[qi] = delta;
-        if (t0 + qi < L) {
+        if (!EXT && t0 + qi < L) {
           den_out[offL + t0 + qi] = den;
           delta_out[offL + t0 + qi] = delta;
         }
@@ -1052,7 +1063,8 @@ template <int FP, int DP, typename OutT, bool VEC>
 static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v, const float* lg,
                                    const void* dy, void* dfq, void* dfk, void* dv, float* dlg,
                                    int B, int H, int L, int F, int D, int gate_per_head, int KG,
-                                   const float* fwd_ws, float* ws, hipStream_t st) {
+                                   const float* fwd_ws, float* ws, const float* ext_den,
+                                   const float* ext_delta, hipStream_t st) {
   const int BH = B * H;
   const size_t BHL = (size_t)BH * L;
   int G, cps;
@@ -1060,9 +1072,12 @@ static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v
   constexpr int SEG = SegRec<FP, DP>::SIZE;
   constexpr int LDS_A = BwdA<FP, DP>::BYTES, LDS_S = BwdS<FP, DP>::BYTES;
   constexpr int LDS_B = BwdB<FP, DP>::BYTES;
-  float* den = ws;
-  float* delta = den + BHL;
-  float* p = delta + BHL;
+  // den and delta of the whole feature dimension, when given (ext_den), else
+  // kernel A forms them into the workspace
+  const bool ext = ext_den != nullptr;
+  float* den = ext ? const_cast<float*>(ext_den) : ws;
+  float* delta = ext ? const_cast<float*>(ext_delta) : ws + BHL;
+  float* p = ws + 2 * BHL;
   float* dG = p + BHL;
   const size_t segf = gla_segment_floats(BH, G, F, D);
   float* own_fseg = dG + BHL;
@@ -1078,11 +1093,20 @@ static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v
   // the walks take two segments per workgroup while that still gives one
   // workgroup per CU: fewer, longer walks
   const int M = (G % 2 == 0 && BH * G / 2 >= device_geom().cus) ? 2 : 1;
-  auto ka = gla_bwd_dq_kernel<FP, DP, OutT, VEC>;
-  if ((e = ensure_lds<gla_bwd_dq_kernel<FP, DP, OutT, VEC>>(LDS_A)) != hipSuccess) return e;
-  hipLaunchKernelGGL(ka, dim3(BH * G / M), dim3(B_THREADS), LDS_A, st, (const bf16*)fq,
-                     (const bf16*)fk, (const bf16*)v, lg, (const bf16*)dy, (OutT*)dfq, den, delta,
-                     p, fseg, H, L, F, D, gate_per_head, G, cps, M, KG);
+  auto launch_a = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3(BH * G / M), dim3(B_THREADS), LDS_A, st, (const bf16*)fq,
+                       (const bf16*)fk, (const bf16*)v, lg, (const bf16*)dy, (OutT*)dfq, den,
+                       delta, p, fseg, H, L, F, D, gate_per_head, G, cps, M, KG);
+  };
+  if (ext) {
+    if ((e = ensure_lds<gla_bwd_dq_kernel<FP, DP, OutT, VEC, true>>(LDS_A)) != hipSuccess)
+      return e;
+    launch_a(gla_bwd_dq_kernel<FP, DP, OutT, VEC, true>);
+  } else {
+    if ((e = ensure_lds<gla_bwd_dq_kernel<FP, DP, OutT, VEC, false>>(LDS_A)) != hipSuccess)
+      return e;
+    launch_a(gla_bwd_dq_kernel<FP, DP, OutT, VEC, false>);
+  }
   if ((e = hipGetLastError()) != hipSuccess) return e;
   if (G > 1) {
     auto ks = gla_bwd_state_kernel<FP, DP, VEC>;
@@ -1110,15 +1134,18 @@ static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v
   return hipGetLastError();
 }
 
+// ext_den / ext_delta: nullptr, or (one F tile of a split feature
+// dimension) den and delta [BH, L] of the whole feature dimension
 hipError_t launch_gla_bwd(const void* fq, const void* fk, const void* v, const float* lg,
                           const void* dy, void* dfq, void* dfk, void* dv, float* dlg,
                           bool grad_bf16, int B, int H, int L, int F, int D, int gate_per_head,
-                          int KG, const float* fwd_ws, float* ws, hipStream_t st) {
+                          int KG, const float* fwd_ws, float* ws, const float* ext_den,
+                          const float* ext_delta, hipStream_t st) {
   const int fp = gla_padded_dim(F), dp = gla_padded_dim(D);
   const bool vec = F % 8 == 0 && D % 8 == 0;
 #define LZ_GLA_BWD_V(FPV, DPV, OUT, V)                                                          \
   launch_gla_bwd_t<FPV, DPV, OUT, V>(fq, fk, v, lg, dy, dfq, dfk, dv, dlg, B, H, L, F, D,      \
-                                     gate_per_head, KG, fwd_ws, ws, st)
+                                     gate_per_head, KG, fwd_ws, ws, ext_den, ext_delta, st)
 #define LZ_GLA_BWD(FPV, DPV)                                                                    \
   if (fp == FPV && dp == DPV)                                                                   \
     return grad_bf16 ? (vec ? LZ_GLA_BWD_V(FPV, DPV, bf16, true)                                \

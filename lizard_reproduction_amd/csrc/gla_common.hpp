@@ -18,6 +18,38 @@ constexpr std::integral_constant<int, 1> SET1{};
 
 int gla_padded_dim(int n);
 bool gla_dims_supported(int F, int D);
+
+// Tiles of the (F, D) problem that the native walks take (gla_tiled.hip):
+// nF feature tiles of Ft (the last one the rest), nD value tiles of Dt.
+struct GlaTiles {
+  int nF, Ft, nD, Dt;
+  bool native() const { return nF == 1 && nD == 1; }
+};
+GlaTiles gla_tiles(int F, int D);
+
+// The native walks (F, D within gla_dims_supported).  raw_den: see
+// gla_fwd_kernel's RAW; ext_den / ext_delta: see gla_bwd_dq_kernel's EXT.
+size_t gla_fwd_workspace(int B, int H, int L, int F, int D);
+size_t gla_bwd_workspace(int B, int H, int L, int F, int D, int gate_per_head);
+hipError_t launch_gla_fwd(const void* fq, const void* fk, const void* v, const float* lg, void* y,
+                          int B, int H, int L, int F, int D, int gate_per_head, int KG, float* ws,
+                          float* final_state, float* raw_den, hipStream_t st);
+hipError_t launch_gla_bwd(const void* fq, const void* fk, const void* v, const float* lg,
+                          const void* dy, void* dfq, void* dfk, void* dv, float* dlg,
+                          bool grad_bf16, int B, int H, int L, int F, int D, int gate_per_head,
+                          int KG, const float* fwd_ws, float* ws, const float* ext_den,
+                          const float* ext_delta, hipStream_t st);
+// Any F and D: the native walks, or tiles of them (gla_tiled.hip).
+size_t gla_fwd_workspace_any(int B, int H, int L, int F, int D);
+size_t gla_bwd_workspace_any(int B, int H, int L, int F, int D, int gate_per_head);
+hipError_t launch_gla_fwd_any(const void* fq, const void* fk, const void* v, const float* lg,
+                              void* y, int B, int H, int L, int F, int D, int gate_per_head,
+                              int KG, void* ws, hipStream_t st);
+hipError_t launch_gla_bwd_any(const void* fq, const void* fk, const void* v, const float* lg,
+                              const void* dy, void* dfq, void* dfk, void* dv, float* dlg,
+                              bool grad_bf16, int B, int H, int L, int F, int D,
+                              int gate_per_head, int KG, const float* fwd_ws, void* ws,
+                              hipStream_t st);
 void gla_segments(int BH, int L, int F, int* G, int* cps);
 int gla_walk_segments(int BH, int G, int F);
 size_t gla_segment_floats(int BH, int G, int F, int D);

@@ -76,12 +76,16 @@ struct GlaFwd {
 // ----------------------------------------------------------------------------
 // fused forward walk over the chunks of one segment
 // ----------------------------------------------------------------------------
-template <int FP, int DP, bool VEC>
+// RAW (one F tile of a split feature dimension): instead of y, the walk writes
+// the unnormalised numerator o (fp32 [BH, L, D] at raw_num) and denominator
+// (fp32 [BH, L] at raw_den), which the caller sums over the F tiles.
+template <int FP, int DP, bool VEC, bool RAW>
 __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
     const bf16* __restrict__ fq, const bf16* __restrict__ fk, const bf16* __restrict__ v,
     const float* __restrict__ log_gamma, bf16* __restrict__ y,
     const float* __restrict__ seg_state, float* __restrict__ final_state, int H, int L, int F,
-    int D, int gate_per_head, int G, int cps, int M, int KG) {
+    int D, int gate_per_head, int G, int cps, int M, int KG, float* __restrict__ raw_num,
+    float* __restrict__ raw_den) {
   using Cfg = GlaFwd<FP, DP>;
   constexpr int C = Cfg::C, PF = Cfg::PF, PD = Cfg::PD;
   constexpr int NFT = Cfg::NFT, NDT = Cfg::NDT;
@@ -238,8 +242,14 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
           for (int kb = 0; kb < 4; ++kb)   // queries 0-31 have no keys in blocks 2, 3
             if (qt == 1 || kb < 2) o = mfma(vop[kb], pfrag[(qt * 4 + kb) * 64 + lane], o);
           const float den = rs[qi] + rs[64 + qi] + qz[qi] + qz[64 + qi] + qz[128 + qi] + qz[192 + qi];
-          const float inv = 1.f / fmaxf(den, TINY);
-          store_acc_row_bf16(yr, t0 + qi, dt * 32, D, vecD, o, inv, h);
+          if constexpr (RAW) {
+            store_acc_row<float>(raw_num + (size_t)bh * L * D, t0 + qi, dt * 32, L, D, vecD, o,
+                                 1.f, h);
+            if (dt == 0 && h == 0 && t0 + qi < L) raw_den[(size_t)bh * L + t0 + qi] = den;
+          } else {
+            const float inv = 1.f / fmaxf(den, TINY);
+            store_acc_row_bf16(yr, t0 + qi, dt * 32, D, vecD, o, inv, h);
+          }
         }
 #pragma unroll
         for (int ft = 0; ft < NFT; ++ft) {
@@ -350,12 +360,13 @@ __device__ __forceinline__ void store_chunk512(const uint4 (&reg)[N], bf16* tile
   }
 }
 
-template <int DP, bool VEC>
+template <int DP, bool VEC, bool RAW>
 __global__ __launch_bounds__(WIDE_THREADS, 1) void gla_fwd_wide_kernel(
     const bf16* __restrict__ fq, const bf16* __restrict__ fk, const bf16* __restrict__ v,
     const float* __restrict__ log_gamma, bf16* __restrict__ y,
     const float* __restrict__ seg_state, float* __restrict__ final_state, int H, int L, int F,
-    int D, int gate_per_head, int G, int cps, int M, int KG) {
+    int D, int gate_per_head, int G, int cps, int M, int KG, float* __restrict__ raw_num,
+    float* __restrict__ raw_den) {
   using Cfg = GlaFwdWide<DP>;
   constexpr int FP = Cfg::FP, C = Cfg::C, PF = Cfg::PF, PD = Cfg::PD;
   constexpr int NFT = Cfg::NFT, NDT = Cfg::NDT, S_OWN = Cfg::S_OWN;
@@ -511,8 +522,14 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void gla_fwd_wide_kernel(
       float den = rs[qi] + rs[64 + qi] + qz[2 * 64 + qi];
 #pragma unroll
       for (int w = 4; w < 8; ++w) den += qz[w * 64 + qi];
-      const float inv = 1.f / fmaxf(den, TINY);
-      store_acc_row_bf16(yr, t0 + qi, dt * 32, D, vecD, o, inv, h);
+      if constexpr (RAW) {   // as in gla_fwd_kernel
+        store_acc_row<float>(raw_num + (size_t)bh * L * D, t0 + qi, dt * 32, L, D, vecD, o, 1.f,
+                             h);
+        if (dt == 0 && h == 0 && t0 + qi < L) raw_den[(size_t)bh * L + t0 + qi] = den;
+      } else {
+        const float inv = 1.f / fmaxf(den, TINY);
+        store_acc_row_bf16(yr, t0 + qi, dt * 32, D, vecD, o, inv, h);
+      }
     }
 #pragma unroll
     for (int i = 0; i < S_OWN; ++i) {
@@ -1018,11 +1035,11 @@ hipError_t launch_gla_fwd_states(const void* fk, const void* v, const float* lg,
   return hipErrorInvalidValue;
 }
 
-template <int FP, int DP, bool VEC>
+template <int FP, int DP, bool VEC, bool RAW>
 static hipError_t launch_gla_fwd_t(const void* fq, const void* fk, const void* v,
                                    const float* lg, void* y, int B, int H, int L, int F, int D,
                                    int gate_per_head, int KG, float* ws, float* final_state,
-                                   hipStream_t st) {
+                                   float* raw_den, hipStream_t st) {
   using Cfg = GlaFwd<FP, DP>;
   const int BH = B * H;
   int G, cps;
@@ -1037,41 +1054,50 @@ static hipError_t launch_gla_fwd_t(const void* fq, const void* fk, const void* v
   const int M = gla_walk_segments(BH, G, F);
   if constexpr (FP == 256) {   // eight waves per workgroup
     using W = GlaFwdWide<DP>;
-    auto kern = gla_fwd_wide_kernel<DP, VEC>;
-    hipError_t e = ensure_lds<gla_fwd_wide_kernel<DP, VEC>>(W::BYTES);
+    auto kern = gla_fwd_wide_kernel<DP, VEC, RAW>;
+    hipError_t e = ensure_lds<gla_fwd_wide_kernel<DP, VEC, RAW>>(W::BYTES);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(kern, dim3(BH * G / M), dim3(WIDE_THREADS), W::BYTES, st,
                        (const bf16*)fq, (const bf16*)fk, (const bf16*)v, lg, (bf16*)y,
                        (const float*)seg_state, final_state, H, L, F, D, gate_per_head, G, cps,
-                       M, KG);
+                       M, KG, RAW ? (float*)y : nullptr, raw_den);
     return hipGetLastError();
   } else {
-    auto kern = gla_fwd_kernel<FP, DP, VEC>;
-    hipError_t e = ensure_lds<gla_fwd_kernel<FP, DP, VEC>>(Cfg::BYTES);
+    auto kern = gla_fwd_kernel<FP, DP, VEC, RAW>;
+    hipError_t e = ensure_lds<gla_fwd_kernel<FP, DP, VEC, RAW>>(Cfg::BYTES);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(kern, dim3(BH * G / M), dim3(256), Cfg::BYTES, st, (const bf16*)fq,
                        (const bf16*)fk, (const bf16*)v, lg, (bf16*)y, (const float*)seg_state,
-                       final_state, H, L, F, D, gate_per_head, G, cps, M, KG);
+                       final_state, H, L, F, D, gate_per_head, G, cps, M, KG,
+                       RAW ? (float*)y : nullptr, raw_den);
     return hipGetLastError();
   }
 }
 
+// raw_den == nullptr: y is the bf16 output; otherwise (one F tile of a split
+// feature dimension) y is the fp32 numerator [BH, L, D] and raw_den the fp32
+// denominator [BH, L] of this tile (see gla_fwd_kernel's RAW).
 hipError_t launch_gla_fwd(const void* fq, const void* fk, const void* v, const float* lg, void* y,
                           int B, int H, int L, int F, int D, int gate_per_head, int KG, float* ws,
-                          float* final_state, hipStream_t st) {
+                          float* final_state, float* raw_den, hipStream_t st) {
   const int fp = gla_padded_dim(F), dp = gla_padded_dim(D);
   const bool vec = F % 8 == 0 && D % 8 == 0;
+#define LZ_GLA_FWD_R(FPV, DPV, V)                                                               \
+  (raw_den ? launch_gla_fwd_t<FPV, DPV, V, true>(fq, fk, v, lg, y, B, H, L, F, D,               \
+                                                 gate_per_head, KG, ws, final_state, raw_den,   \
+                                                 st)                                            \
+           : launch_gla_fwd_t<FPV, DPV, V, false>(fq, fk, v, lg, y, B, H, L, F, D,              \
+                                                  gate_per_head, KG, ws, final_state, nullptr,  \
+                                                  st))
 #define LZ_GLA_FWD(FPV, DPV)                                                                    \
   if (fp == FPV && dp == DPV)                                                                   \
-    return vec ? launch_gla_fwd_t<FPV, DPV, true>(fq, fk, v, lg, y, B, H, L, F, D,              \
-                                                  gate_per_head, KG, ws, final_state, st)       \
-               : launch_gla_fwd_t<FPV, DPV, false>(fq, fk, v, lg, y, B, H, L, F, D,             \
-                                                   gate_per_head, KG, ws, final_state, st);
+    return vec ? LZ_GLA_FWD_R(FPV, DPV, true) : LZ_GLA_FWD_R(FPV, DPV, false);
   LZ_GLA_FWD(32, 32) LZ_GLA_FWD(32, 64) LZ_GLA_FWD(32, 128)
   LZ_GLA_FWD(64, 32) LZ_GLA_FWD(64, 64) LZ_GLA_FWD(64, 128)
   LZ_GLA_FWD(128, 32) LZ_GLA_FWD(128, 64) LZ_GLA_FWD(128, 128)
   LZ_GLA_FWD(256, 32) LZ_GLA_FWD(256, 64)
 #undef LZ_GLA_FWD
+#undef LZ_GLA_FWD_R
   return hipErrorInvalidValue;
 }
 

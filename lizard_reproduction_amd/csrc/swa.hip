@@ -30,7 +30,7 @@
 
 namespace lz {
 
-constexpr int SWA_MAX_META = 64;
+constexpr int SWA_META_BLOCK = 64;   // sinks per pass of a block's dmeta partials
 constexpr int SWA_ROWS = 128;   // own-side rows per workgroup
 constexpr int SWA_TILE = 64;    // streamed rows per LDS tile
 
@@ -205,7 +205,7 @@ __global__ __launch_bounds__(256) void swa_bwd_dq_kernel(
   extern __shared__ __align__(16) char smem[];
   bf16* k_l = reinterpret_cast<bf16*>(smem);
   bf16* v_l = reinterpret_cast<bf16*>(smem + Cfg::TILE_BYTES);
-  float* red = reinterpret_cast<float*>(smem + 2 * Cfg::TILE_BYTES);   // [4][SWA_MAX_META]
+  float* red = reinterpret_cast<float*>(smem + 2 * Cfg::TILE_BYTES);   // [4][SWA_META_BLOCK]
 
   const int nqb = (L + SWA_ROWS - 1) / SWA_ROWS;
   const int lb = xcd_block(blockIdx.x, per, nx);
@@ -287,19 +287,24 @@ __global__ __launch_bounds__(256) void swa_bwd_dq_kernel(
 #pragma unroll
   for (int t = 0; t < DP / 32; ++t) store_acc_row<OutT>(dq + base, qi, t * 32, L, d, vec, dqa[t], scale, h);
   if (qi < L && h == 0) delta_out[(size_t)bh * L + qi] = delta;
-  // dmeta partial of this block: -sum_i e^{meta_j - lse_i} delta_i
-  for (int j = 0; j < n_meta; ++j) {
-    float c = (qi < L && h == 0) ? fexp(meta[j] - lse_i) * delta : 0.f;
+  // dmeta partial of this block: -sum_i e^{meta_j - lse_i} delta_i, sinks in
+  // passes of SWA_META_BLOCK (one wave sum per sink, then the four waves')
+  for (int j0 = 0; j0 < n_meta; j0 += SWA_META_BLOCK) {
+    const int nj = min(SWA_META_BLOCK, n_meta - j0);
+    for (int jj = 0; jj < nj; ++jj) {
+      float c = (qi < L && h == 0) ? fexp(meta[j0 + jj] - lse_i) * delta : 0.f;
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) c += __shfl_xor(c, off);
-    if (lane == 0) red[wave * SWA_MAX_META + j] = c;
-  }
-  __syncthreads();
-  if ((int)threadIdx.x < n_meta) {
-    const int j = threadIdx.x;
-    const float c = red[j] + red[SWA_MAX_META + j] + red[2 * SWA_MAX_META + j] +
-                    red[3 * SWA_MAX_META + j];
-    dmeta_part[((size_t)bh * nqb + qb) * n_meta + j] = -c;
+      for (int off = 32; off >= 1; off >>= 1) c += __shfl_xor(c, off);
+      if (lane == 0) red[wave * SWA_META_BLOCK + jj] = c;
+    }
+    __syncthreads();
+    if ((int)threadIdx.x < nj) {
+      const int jj = threadIdx.x;
+      const float c = red[jj] + red[SWA_META_BLOCK + jj] + red[2 * SWA_META_BLOCK + jj] +
+                      red[3 * SWA_META_BLOCK + jj];
+      dmeta_part[((size_t)bh * nqb + qb) * n_meta + j0 + jj] = -c;
+    }
+    __syncthreads();
   }
 }
 
@@ -325,23 +330,26 @@ __global__ __launch_bounds__(256) void swa_bwd_dkv_kernel(
   const int lb = xcd_block(blockIdx.x, per, nx);
   if (lb >= BH * nkb) return;
   if (lb == 0 && n_meta > 0) {
-    // dmeta from the query-side blocks' partials (that launch has completed):
-    // thread (group g, sink j) sums partial rows g, g + groups, ...; thread j
-    // then sums the groups, in a fixed order
+    // dmeta from the query-side blocks' partials (that launch has completed),
+    // in passes of up to 256 sinks: thread (group g, sink j) sums partial rows
+    // g, g + groups, ...; thread j then sums the groups, in a fixed order
     float* sh = reinterpret_cast<float*>(smem);
-    const int rows = BH * nkb, groups = 256 / n_meta;
-    const int j = threadIdx.x % n_meta, grp = threadIdx.x / n_meta;
-    float acc = 0.f;
-    if (grp < groups)
-      for (int r = grp; r < rows; r += groups) acc += dmeta_part[(size_t)r * n_meta + j];
-    sh[threadIdx.x] = acc;
-    __syncthreads();
-    if ((int)threadIdx.x < n_meta) {
-      float t = 0.f;
-      for (int g = 0; g < groups; ++g) t += sh[g * n_meta + threadIdx.x];
-      dmeta[threadIdx.x] = t;
+    const int rows = BH * nkb, per = min(n_meta, 256), groups = 256 / per;
+    for (int j0 = 0; j0 < n_meta; j0 += per) {
+      const int nj = min(per, n_meta - j0);
+      const int j = threadIdx.x % per, grp = threadIdx.x / per;
+      float acc = 0.f;
+      if (grp < groups && j < nj)
+        for (int r = grp; r < rows; r += groups) acc += dmeta_part[(size_t)r * n_meta + j0 + j];
+      sh[threadIdx.x] = acc;
+      __syncthreads();
+      if ((int)threadIdx.x < nj) {
+        float t = 0.f;
+        for (int g = 0; g < groups; ++g) t += sh[g * per + threadIdx.x];
+        dmeta[j0 + threadIdx.x] = t;
+      }
+      __syncthreads();
     }
-    __syncthreads();
   }
   const int bh = lb / nkb, K0 = (lb % nkb) * SWA_ROWS;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -472,7 +480,7 @@ static hipError_t launch_swa_bwd_t(const void* q, const void* k, const void* v, 
                                    hipStream_t st) {
   int per, grid, nx;
   swa_grid(BH, L, &per, &grid, &nx);
-  const size_t lds_q = 2 * SwaCfg<DP>::TILE_BYTES + 4 * SWA_MAX_META * sizeof(float);
+  const size_t lds_q = 2 * SwaCfg<DP>::TILE_BYTES + 4 * SWA_META_BLOCK * sizeof(float);
   auto kq = swa_bwd_dq_kernel<DP, OutT, VEC>;
   hipError_t e = ensure_lds<swa_bwd_dq_kernel<DP, OutT, VEC>>((int)lds_q);
   if (e != hipSuccess) return e;

@@ -135,11 +135,23 @@ def _check_gate(what, fq, lg):
                          f"got {tuple(lg.shape)}")
 
 
+def _padded(n):
+    return next((p for p in (32, 64, 128, 256) if n <= p), None)
+
+
+def gla_native(nf, nd):
+    """Whether the GLA walks take (F, D) directly (F <= 256, D <= 128, D <= 64
+    when F > 128); past that the library runs them on tiles, and the
+    forward's workspace holds tiles rather than segment states."""
+    fp, dp = _padded(nf), _padded(nd)
+    return fp is not None and dp is not None and dp <= 128 and (fp <= 128 or dp <= 64)
+
+
 def gla_forward(fq, fk, v, lg, keep_state=True, chunk=CHUNK):
     """One ``lz_gla_fwd`` launch on bf16 contiguous fq, fk, v and fp32
     contiguous log_gamma; returns (y, state), state being the workspace of
     the states entering each sequence segment, which ``gla_backward`` reuses
-    (None when not kept or not needed).  fk and v may have fewer heads than
+    (None when not kept, not needed, or for tiled sizes past the walks').  fk and v may have fewer heads than
     fq (a divisor: grouped-query attention, each kv head shared by
     consecutive query heads)."""
     _check_kv("gla_forward", fq, fk, v, fq.shape[-1], v.shape[-1])
@@ -156,7 +168,7 @@ def gla_forward(fq, fk, v, lg, keep_state=True, chunk=CHUNK):
         rc = lib.lz_gla_fwd(_ptr(fq), _ptr(fk), _ptr(v), _ptr(lg), _ptr(y), b, h, fk.shape[1],
                             length, nf, nd, per_head, chunk, _ptr(ws), nbytes, _stream(fq))
         _lib.check(rc, "lz_gla_fwd")
-    return y, (ws if keep_state else None)
+    return y, (ws if keep_state and gla_native(nf, nd) else None)
 
 
 def gla_backward(fq, fk, v, lg, dy, state, grad_dtype, chunk=CHUNK):

@@ -51,11 +51,20 @@ def test_null_pointers_are_rejected_with_a_message(lib):
 
 def test_bad_sizes_are_rejected_before_any_launch(lib):
     p = ctypes.c_void_p(16)   # never dereferenced: validation fails first
+    # any F, D up to LZ_GLA_MAX_DIM (tiles past the walks' own sizes): F = 5000
+    # is refused; F = 300 is not refused for its size (here: for the workspace)
+    rc = lib.lz_gla_fwd(p, p, p, p, p, 1, 1, 1, 8, 5000, 16, 0, 64, None, 0, None)
+    assert rc != 0 and b"beyond" in lib.lz_last_error()
     rc = lib.lz_gla_fwd(p, p, p, p, p, 1, 1, 1, 8, 300, 16, 0, 64, None, 0, None)
+    assert rc != 0 and b"workspace" in lib.lz_last_error()
+    # entry points that run the walks directly keep their sizes
+    rc = lib.lz_gla_prefill(p, p, p, p, p, p, 1, 1, 1, 8, 300, 16, 0, 64, p, 1 << 20, None)
+    assert rc != 0 and b"unsupported" in lib.lz_last_error()
+    rc = lib.lz_gla_fwd_noalloc(p, p, p, p, p, 1, 1, 1, 8, 256, 128, 0, 64, None)
     assert rc != 0 and b"unsupported" in lib.lz_last_error()
     rc = lib.lz_gla_fwd(p, p, p, p, p, 1, 1, 1, 8, 16, 16, 0, 48, None, 0, None)
     assert rc != 0 and b"chunk" in lib.lz_last_error()
-    rc = lib.lz_swa_fwd(p, p, p, p, 65, p, p, 1, 1, 1, 8, 16, 4, 0.25, None)
+    rc = lib.lz_swa_fwd(p, p, p, p, 65537, p, p, 1, 1, 1, 8, 16, 4, 0.25, None)
     assert rc != 0 and b"n_meta" in lib.lz_last_error()
     rc = lib.lz_swa_fwd(p, p, p, p, 0, p, p, 1, 1, 1, 8, 512, 4, 0.25, None)
     assert rc != 0 and b"dim" in lib.lz_last_error()
@@ -99,7 +108,7 @@ def test_decode_entry_points_reject_bad_arguments(lib):
     assert b"pos" in lib.lz_last_error()
     assert sd(p, p, p, p, 4, p, 1, 4, 2, 64, 512, 0, 0.125, None) != 0
     assert b"dim" in lib.lz_last_error()
-    assert sd(p, p, p, p, 65, p, 1, 4, 2, 64, 64, 0, 0.125, None) != 0
+    assert sd(p, p, p, p, 65537, p, 1, 4, 2, 64, 64, 0, 0.125, None) != 0
     assert b"n_meta" in lib.lz_last_error()
     # lz_gla_decode_step(fq, fk, v, log_gamma, state, y, B, H, kv_heads, F, D, per_head, stream)
     gd = lib.lz_gla_decode_step
@@ -288,3 +297,30 @@ def test_calls_under_graph_capture_are_refused(monkeypatch):
     monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: False)
     with pytest.raises(ValueError, match="ROCm GPU"):
         kernels.gla(x, x, x, torch.zeros(1, 8))
+
+
+@pytest.mark.parametrize("f, d", [(256, 128), (512, 64), (300, 200), (24, 300), (1024, 128)])
+def test_tiled_gla_sizes_have_workspaces(lib, f, d):
+    """Sizes past the walks' own run on tiles: the forward and backward
+    report workspaces that hold at least the tiles' fp32 partial results."""
+    from lizard_reproduction_amd import kernels as k
+    assert not k.gla_native(f, d)
+    b, h, length = 2, 4, 300
+    fw = lib.lz_gla_fwd_workspace_bytes(b, h, length, f, d, 1, 64)
+    bw = lib.lz_gla_bwd_workspace_bytes(b, h, length, f, d, 1, 64)
+    rows = b * h * length
+    assert fw >= rows * 2 * min(d, 128) * 2          # at least a D tile of v and of y
+    assert bw >= rows * (2 * f + (d if f > 256 else 0)) * 4   # fp32 sums of dfq, dfk (dv)
+    assert lib.lz_gla_fwd_workspace_bytes(b, h, length, 5000, d, 1, 64) == 0
+
+
+def test_gla_native_predicate_matches_the_library(lib):
+    from lizard_reproduction_amd import kernels as k
+    for f in (8, 24, 64, 100, 128, 129, 200, 256, 257):
+        for d in (8, 20, 64, 65, 100, 128, 129):
+            # the no-allocation forward takes exactly the walks' sizes
+            p = ctypes.c_void_p(16)
+            rc = lib.lz_gla_fwd_noalloc(p, p, p, p, None, 1, 1, 1, 8, f, d, 0, 64, None)
+            msg = lib.lz_last_error()
+            assert rc != 0
+            assert (b"unsupported" not in msg) == k.gla_native(f, d), (f, d, msg)

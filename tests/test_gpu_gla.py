@@ -178,3 +178,49 @@ def test_gla_backward_without_forward_workspace_is_bitwise_equal():
     torch.cuda.synchronize()
     for ours, ref in zip((dfq, dfk, dv, dlg), leaves):
         assert torch.equal(ours, ref.grad)
+
+
+@pytest.mark.parametrize("features, dim, length, heads, gates", [
+    (256, 128, 150, 2, ()),      # head_dim-128 models at feature_dim 128: two D tiles of 64
+    (512, 64, 150, 2, ()),       # feature_dim 256: two F tiles, numerators summed
+    (300, 200, 130, 2, (2,)),    # ragged F and D tiles together, per-head gate
+    (24, 300, 77, 2, ()),        # D tiles of a small F
+    (512, 64, 1000, 3, (3,)),    # segmented walks inside each F tile (16 one-chunk segments)
+    (1024, 128, 200, 1, ()),     # eight F tiles of 128, one D tile
+])
+def test_gla_sizes_past_the_walks_match_oracle(features, dim, length, heads, gates):
+    """The reference's kernels take any F and D (src/kernels/gla.py:74,154,171,
+    203-210); past the walks' own sizes the library runs them on tiles."""
+    inputs = gla_inputs(length, gates=gates, batch=1, heads=heads, features=features, dim=dim)
+    assert not kernels.gla_native(features, dim)
+    grad = torch.randn(inputs[2].shape, generator=torch.Generator().manual_seed(1))
+    compare(gla_kernel(64), gla_reference, inputs, grad,
+            label=f"tiled F={features} D={dim} L={length}")
+
+
+def test_gla_tiled_sizes_fp32_grads_determinism_and_no_grad_equality():
+    fq, fk, v, z = gla_inputs(90, batch=1, heads=2, features=512, dim=64)
+    leaves = [t.float().cuda().requires_grad_() for t in (fq, fk, v)]
+    lg = F.logsigmoid(z).cuda().requires_grad_()
+    outs = []
+    for _ in range(2):
+        y = kernels.gla(*leaves, lg)
+        y.float().sum().backward()
+        outs.append([y.detach().clone()] + [t.grad.clone() for t in leaves + [lg]])
+        for t in leaves + [lg]:
+            t.grad = None
+    assert all(g.dtype == torch.float32 for g in outs[0][1:])
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+    with torch.no_grad():
+        assert torch.equal(kernels.gla(*[t.detach() for t in leaves], lg.detach()), outs[0][0])
+
+
+def test_gla_tiled_constant_values_stay_constant():
+    """y is a normalised average of v also when the numerator and the
+    denominator are sums over F tiles (each tile's bf16 weights feed both)."""
+    fq, fk, _, z = gla_inputs(300, batch=1, heads=2, features=600, dim=96)
+    v = torch.full((1, 2, 300, 96), -1.25, dtype=torch.bfloat16)
+    with torch.no_grad():
+        y = kernels.gla(fq.cuda(), fk.cuda(), v.cuda(), F.logsigmoid(z).cuda())
+    assert ((y.float() + 1.25).abs().max() / 1.25).item() <= OUT_TOL

@@ -20,6 +20,8 @@ def _expand(t, group):
     (2, 8, 2, 300, 64, 64, True),      # segmented walks (B*H small)
     (1, 32, 8, 777, 256, 64, False),   # the layer's wide features, two segments per walk
     (16, 32, 8, 130, 128, 128, True),  # B*H fills the GPU: one walk per (b, h)
+    (1, 8, 2, 300, 256, 128, False),   # past the walks' sizes: two D tiles
+    (1, 4, 2, 200, 512, 64, True),     # two F tiles (summed raw numerators)
 ])
 def test_gla_grouped_kv_equals_expanded(b, heads, kv, length, nf, nd, per_head):
     g = torch.Generator().manual_seed(nf + length)

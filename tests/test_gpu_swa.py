@@ -101,3 +101,16 @@ def test_swa_fp32_inputs_give_fp32_grads_matching_oracle(dim):
                      lambda q, k, v, m: lo.swa_kernel_api(q, k, v, m, 48, dtype=torch.float32),
                      inputs, grad, label=f"fp32 inputs d={dim}")
     assert {"grad0", "grad1", "grad2", "grad3"} <= set(report)
+
+
+@pytest.mark.parametrize("sinks, dim", [(100, 64), (300, 20)])
+def test_swa_many_sinks_match_oracle(sinks, dim):
+    """Any number of sink logits (the reference's BLOCK_S follows n_meta,
+    src/kernels/swa.py:151-152): dmeta partials in passes of 64 sinks, their
+    sum in passes of up to 256."""
+    inputs = swa_inputs(150, dim=dim, sinks=sinks)
+    inputs[3] = inputs[3] - 3.0   # keep the window's share of each row visible
+    grad = torch.randn(inputs[2].shape, generator=torch.Generator().manual_seed(1))
+    compare(lambda q, k, v, m: kernels.swa(q, k, v, m, 48),
+            lambda q, k, v, m: lo.swa_kernel_api(q, k, v, m, 48, dtype=torch.float32),
+            inputs, grad, label=f"{sinks} sinks d={dim}")
