@@ -225,7 +225,7 @@ int lz_swa_bwd(const void* q, const void* k, const void* v, const float* meta, i
  *   kv_heads < heads, which replaces the reference's repeat_interleave without
  *   writing its copies.
  * Supported sizes: head_dim 32, 64 or 128; feature_dim a multiple of 4, at most
- * 128 (64 when head_dim is 128).
+ * 128 (64 when head_dim is 128 and dtype_bf16 is 0).
  */
 int lz_layer_prologue_fwd(const void* q, const void* k, const void* v, const void* wq,
                           const void* wk, const void* cos, const void* sin, int cos_batched,

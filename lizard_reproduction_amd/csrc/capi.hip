@@ -48,7 +48,7 @@ hipError_t launch_swa_bwd(const void* q, const void* k, const void* v, const flo
                           float* dmeta, int BH, int L, int d, int W, float scale, int KG,
                           hipStream_t st);
 constexpr int MAX_META = LZ_SWA_MAX_META;
-bool prologue_dims_supported(int hd, int f);
+bool prologue_dims_supported(int hd, int f, bool bf16_in);
 size_t prologue_bwd_workspace(int B, int L, int H, int Hkv, int hd, int f);
 hipError_t launch_prologue_fwd(const void* q, const void* k, const void* v, const void* wq,
                                const void* wk, const void* cos, const void* sin, void* fq,
@@ -369,7 +369,7 @@ extern "C" int lz_swa_bwd(const void* q, const void* k, const void* v, const flo
 // layer prologue / epilogue
 // ---------------------------------------------------------------------------
 static int check_layer(int batch, int length, int heads, int kv_heads, int head_dim,
-                       int feature_dim) {
+                       int feature_dim, bool bf16_in) {
   if (batch <= 0 || length <= 0 || heads <= 0 || kv_heads <= 0)
     return fail(1, "layer: sizes must be positive (B=%d L=%d heads=%d kv_heads=%d)", batch,
                 length, heads, kv_heads);
@@ -378,9 +378,10 @@ static int check_layer(int batch, int length, int heads, int kv_heads, int head_
   if ((long long)batch * length * heads > (1LL << 31) - (1LL << 20))
     return fail(1, "layer: B*L*heads = %lld rows exceeds the 2^31 - 2^20 row limit",
                 (long long)batch * length * heads);
-  if (!lz::prologue_dims_supported(head_dim, feature_dim))
+  if (!lz::prologue_dims_supported(head_dim, feature_dim, bf16_in))
     return fail(1, "layer: unsupported head_dim %d / feature_dim %d (head_dim 32, 64 or 128; "
-                   "feature_dim a multiple of 4 up to 128, up to 64 with head_dim 128)",
+                   "feature_dim a multiple of 4 up to 128, up to 64 with head_dim 128 and "
+                   "fp32 inputs)",
                 head_dim, feature_dim);
   return 0;
 }
@@ -391,7 +392,9 @@ extern "C" int lz_layer_prologue_fwd(const void* q, const void* k, const void* v
                                      void* v_out, int dtype_bf16, int batch, int length,
                                      int heads, int kv_heads, int head_dim, int feature_dim,
                                      void* stream) {
-  if (int rc = check_layer(batch, length, heads, kv_heads, head_dim, feature_dim)) return rc;
+  if (int rc = check_layer(batch, length, heads, kv_heads, head_dim, feature_dim,
+                             dtype_bf16 != 0))
+    return rc;
   if (!q || !k || !v || !wq || !wk || !cos || !sin)
     return fail(1, "layer_prologue_fwd: null input pointer");
   if (!fq || !fk || !qr || !kr || !v_out) return fail(1, "layer_prologue_fwd: null output pointer");
@@ -406,7 +409,7 @@ extern "C" size_t lz_layer_prologue_bwd_workspace_bytes(int batch, int length, i
                                                         int kv_heads, int head_dim,
                                                         int feature_dim) {
   if (batch <= 0 || length <= 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads ||
-      !lz::prologue_dims_supported(head_dim, feature_dim))
+      !lz::prologue_dims_supported(head_dim, feature_dim, true))
     return 0;
   return lz::prologue_bwd_workspace(batch, length, heads, kv_heads, head_dim, feature_dim);
 }
@@ -420,7 +423,9 @@ extern "C" int lz_layer_prologue_bwd(const void* q, const void* k, const void* w
                                      int batch, int length, int heads, int kv_heads,
                                      int head_dim, int feature_dim, void* workspace,
                                      size_t workspace_bytes, void* stream) {
-  if (int rc = check_layer(batch, length, heads, kv_heads, head_dim, feature_dim)) return rc;
+  if (int rc = check_layer(batch, length, heads, kv_heads, head_dim, feature_dim,
+                             dtype_bf16 != 0))
+    return rc;
   if (!q || !k || !wq || !wk || !cos || !sin || !dfq || !dfk || !dqr || !dkr || !dv)
     return fail(1, "layer_prologue_bwd: null input pointer");
   if (!dq || !dk || !dv_out || !dwq || !dwk)

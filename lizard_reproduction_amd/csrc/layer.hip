@@ -420,12 +420,13 @@ struct ProBwd {
   // per SIMD has the registers for them (the split and the two-workgroup
   // forms have not: the loads' registers alone push them into spills, and
   // their second wave per SIMD hides the load latency instead)
-  static constexpr int GQ = OCC == 1 && NWF == 1 ? 4 : 0;
+  // (nor at FT = HT = 4, where a wave's own tiles already take every register)
+  static constexpr int GQ = OCC == 1 && NWF == 1 && FT * HT < 16 ? 4 : 0;
   static constexpr int GQR = GQ > 0 ? GQ : 1;            // raw register sets held
   static constexpr int XI = PRO_BLOCK * (HP / 8) / NT;   // x / dx items per thread
   static_assert(GI * RSTEP * IPR == PRO_BLOCK * IPR && RSTEP == 32, "item mapping");
   static_assert(XI * NT == PRO_BLOCK * (HP / 8), "row items");
-  static_assert(LDS <= 160 * 1024, "LDS budget");
+  static constexpr bool FITS = LDS <= 160 * 1024;   // instantiated for launch only when it fits
 };
 
 // 8 bf16 at p (16-byte aligned) added to acc in fp32; nothing when !ok (the
@@ -1009,10 +1010,10 @@ __global__ __launch_bounds__(256) void combine_alpha_reduce_kernel(const float* 
 static long ceil_div(long a, long b) { return (a + b - 1) / b; }
 
 // head_dim 32, 64 or 128; feature_dim a multiple of 4 up to 128, and up to 64
-// with head_dim 128 (the GLA kernels take F = 2 feature_dim <= 128 when D = 128).
-bool prologue_dims_supported(int hd, int f) {
+// with head_dim 128 when the inputs are fp32 (bf16 inputs take 128 there too).
+bool prologue_dims_supported(int hd, int f, bool bf16_in) {
   return (hd == 32 || hd == 64 || hd == 128) && f > 0 && f % 4 == 0 &&
-         f <= (hd == 128 ? 64 : 128);
+         f <= (hd == 128 && !bf16_in ? 64 : 128);
 }
 
 static int feature_tiles(int f) { return f <= 32 ? 1 : (f <= 64 ? 2 : 4); }
@@ -1049,6 +1050,7 @@ static hipError_t launch_fwd_t(const ProFwdArgs& a, int nq, int nk, hipStream_t 
 template <typename T, int FT, int HT>
 static hipError_t launch_bwd_t(const ProBwdArgs& a, float* dwq, float* dwk, hipStream_t st) {
   using C = ProBwd<T, FT, HT>;
+  static_assert(C::FITS, "LDS budget");
   static_assert(C::OCC <= PRO_BWD_WG_PER_CU, "workspace sized for fewer workgroups");
   const int grid = prologue_bwd_grid(a.nbq, a.nbk, C::OCC);
   hipError_t e;
@@ -1079,6 +1081,10 @@ static hipError_t dispatch_shape(int hd, int f, Args&&... args) {
   LZ_PRO_CASE(1, 32) LZ_PRO_CASE(1, 64) LZ_PRO_CASE(1, 128)
   LZ_PRO_CASE(2, 32) LZ_PRO_CASE(2, 64) LZ_PRO_CASE(2, 128)
   LZ_PRO_CASE(4, 32) LZ_PRO_CASE(4, 64)
+  // head_dim 128 with more than 64 features: bf16 only (the fp32 hi/lo
+  // operands double the backward's W and x tiles past the LDS)
+  if constexpr (sizeof(T) == 2)
+    if (ft == 4 && hd == 128) return Launch<T, 4, 4>::run(args...);
 #undef LZ_PRO_CASE
   return hipErrorInvalidValue;
 }

@@ -38,6 +38,8 @@ import torch.nn.functional as F
 from . import _lib, kernels
 
 BACKENDS = ("hip",)
+MAX_HEAD_DIM = 256       # lz_swa_*: dim <= 256
+MAX_FEATURE_DIM = 2048   # lz_gla_*: F = 2 feature_dim <= LZ_GLA_MAX_DIM
 
 
 def _stream(t):
@@ -49,12 +51,19 @@ def _prologue_ws(b, length, heads, kv, hd, f):
     return _lib.load().lz_layer_prologue_bwd_workspace_bytes(b, length, heads, kv, hd, f)
 
 
-def prologue_supported(head_dim, feature_dim):
+def prologue_supported(head_dim, feature_dim, bf16=True):
     """Shapes the fused prologue takes: head_dim 32, 64 or 128; feature_dim a
-    multiple of 4 up to 128, up to 64 with head_dim 128 (the GLA kernels
-    take F = 2 feature_dim <= 128 when D = 128)."""
+    multiple of 4 up to 128, up to 64 with head_dim 128 when its arithmetic
+    is fp32 (bf16 inputs take 128 there too).  Other shapes take the
+    reference's torch ops before the same GLA and SWA kernels."""
     return (head_dim in (32, 64, 128) and feature_dim > 0 and feature_dim % 4 == 0
-            and feature_dim <= (64 if head_dim == 128 else 128))
+            and feature_dim <= (64 if head_dim == 128 and not bf16 else 128))
+
+
+def _all_bf16(*tensors):
+    """The prologue's arithmetic is bf16 only when every input is bf16 (else
+    they are all widened to fp32, exactly, as the reference promotes them)."""
+    return all(t.dtype == torch.bfloat16 for t in tensors)
 
 
 def _tables(cos, sin, batch, length, head_dim, dtype):
@@ -96,10 +105,7 @@ def prologue_forward(qp, kp, vp, wq, wk, cos, sin, heads, kv_heads):
                            ("wq", wq, (f, hd)), ("wk", wk, (f, hd))):
         if tuple(t.shape) != shape:
             raise ValueError(f"prologue_forward: {name} must be {shape}, got {tuple(t.shape)}")
-    # bf16 arithmetic inputs only when every input is bf16; otherwise all are
-    # widened to fp32 (exactly), as the reference promotes them
-    dtype = torch.bfloat16 if all(t.dtype == torch.bfloat16
-                                  for t in (qp, kp, vp, wq, wk, cos, sin)) else torch.float32
+    dtype = torch.bfloat16 if _all_bf16(qp, kp, vp, wq, wk, cos, sin) else torch.float32
     qp, kp, vp, wq, wk = (t.to(dtype).contiguous() for t in (qp, kp, vp, wq, wk))
     cos, sin, batched = _tables(cos, sin, b, length, hd, dtype)
     dev = qp.device
@@ -273,10 +279,12 @@ class LizardAttention(nn.Module):
             raise ValueError("LizardAttention: hidden_size must split into heads and "
                              "num_attention_heads into num_key_value_heads groups")
         self.head_dim = hidden // self.heads
-        if not prologue_supported(self.head_dim, feature_dim):
+        if not 0 < self.head_dim <= MAX_HEAD_DIM or self.head_dim % 2 or \
+                not 0 < feature_dim <= MAX_FEATURE_DIM:
             raise ValueError(f"LizardAttention: head_dim {self.head_dim} / feature_dim "
-                             f"{feature_dim} unsupported (head_dim 32, 64 or 128; feature_dim "
-                             "a multiple of 4 up to 128, up to 64 with head_dim 128)")
+                             f"{feature_dim} unsupported (an even head_dim up to {MAX_HEAD_DIM}, "
+                             f"the SWA kernels' limit; feature_dim up to {MAX_FEATURE_DIM}, "
+                             "the GLA kernels' F = 2 feature_dim)")
         self.window = window
         kv_dim = self.kv_heads * self.head_dim
         self.q_proj = nn.Linear(hidden, hidden, bias=False)
@@ -292,6 +300,11 @@ class LizardAttention(nn.Module):
         nn.init.normal_(self.phi_k.weight, std=0.02)
         nn.init.zeros_(self.W_gamma.weight)
 
+    def _fused(self, x, cos, sin):
+        """Whether the fused prologue takes this layer's shapes and dtypes."""
+        return prologue_supported(self.head_dim, self.phi_q.weight.shape[0],
+                                  _all_bf16(x, self.q_proj.weight, self.phi_q.weight, cos, sin))
+
     def forward(self, hidden_states, position_embeddings, **kwargs):
         x = hidden_states
         dtype = torch.promote_types(x.dtype, torch.float32)
@@ -300,10 +313,42 @@ class LizardAttention(nn.Module):
             raise ValueError("LizardAttention (hip backend) needs its input on a ROCm GPU")
         z = self.W_gamma(x).to(dtype).squeeze(-1)
         cos, sin = position_embeddings
-        y = _Core.apply(self.q_proj(x), self.k_proj(x), self.v_proj(x), self.phi_q.weight,
-                        self.phi_k.weight, F.logsigmoid(z), self.meta_tokens, self.alpha_blend,
-                        cos, sin, self.heads, self.kv_heads, self.window, x.dtype)
+        qp, kp, vp = self.q_proj(x), self.k_proj(x), self.v_proj(x)
+        if not self._fused(x, cos, sin):
+            y = self._unfused(qp, kp, vp, F.logsigmoid(z), cos, sin, dtype).to(x.dtype)
+            return self.o_proj(y.transpose(1, 2).flatten(2)), None
+        y = _Core.apply(qp, kp, vp, self.phi_q.weight, self.phi_k.weight, F.logsigmoid(z),
+                        self.meta_tokens, self.alpha_blend, cos, sin, self.heads, self.kv_heads,
+                        self.window, x.dtype)
         return self.o_proj(y), None
+
+    def _unfused(self, qp, kp, vp, log_gamma, cos, sin, dtype):
+        """The layer between the projections and o_proj for shapes the fused
+        prologue does not take: the reference's own torch ops -- heads split
+        and repeated per group, Hedgehog maps, rotate_half RoPE, promotion to
+        ``dtype`` (src/lizard_attention.py:73-88) -- in front of the same HIP
+        GLA and SWA operators, blended as y_gla + alpha y_swa (:90-93)."""
+        b, n, _ = qp.shape
+
+        def heads_of(t, count):
+            t = t.view(b, n, count, self.head_dim).transpose(1, 2)
+            return t.repeat_interleave(self.heads // count, dim=1).to(dtype)
+
+        def hedgehog(t, w):
+            p = torch.matmul(t, w.to(dtype).transpose(0, 1))
+            return torch.cat([p.softmax(-1), (-p).softmax(-1)], dim=-1)
+
+        c, s = (t.to(dtype) for t in (cos, sin))
+        c, s = (t.unsqueeze(1) if t.dim() == 3 else t for t in (c, s))
+        half = self.head_dim // 2
+
+        def rope(t):
+            return t * c + torch.cat([-t[..., half:], t[..., :half]], dim=-1) * s
+        q, k, v = heads_of(qp, self.heads), heads_of(kp, self.kv_heads), heads_of(vp, self.kv_heads)
+        y_gla = kernels.gla(hedgehog(q, self.phi_q.weight), hedgehog(k, self.phi_k.weight), v,
+                            log_gamma).to(dtype)
+        y_swa = kernels.swa(rope(q), rope(k), v, self.meta_tokens.to(dtype), self.window)
+        return y_gla + self.alpha_blend.to(dtype) * y_swa.to(dtype)
 
     # -- decoding -----------------------------------------------------------
 
@@ -320,6 +365,12 @@ class LizardAttention(nn.Module):
         kernels._refuse_capture("LizardAttention")
         if x.device.type != "cuda":
             raise ValueError("LizardAttention (hip backend) needs its input on a ROCm GPU")
+        nf = 2 * self.phi_q.weight.shape[0]
+        if not self._fused(x, *position_embeddings) or not kernels.gla_native(nf, self.head_dim):
+            raise ValueError(f"LizardAttention.prefill/step: decoding takes the fused prologue's "
+                             f"shapes and the GLA decode kernels' (F = {nf}, D = "
+                             f"{self.head_dim} is not one: F <= 256, D <= 128, D <= 64 when "
+                             "F > 128)")
         dtype = torch.promote_types(x.dtype, torch.float32)
         lg = F.logsigmoid(self.W_gamma(x).to(dtype).squeeze(-1)).float().contiguous()
         cos, sin = position_embeddings

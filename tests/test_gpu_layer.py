@@ -166,6 +166,18 @@ def test_prologue_matches_reference_ops(dtype, b, length, heads, kv, hd, f, batc
     """The fused prologue's outputs and, from the same upstream gradients
     (v's given as two parts, one per attention branch), every input
     gradient, against autograd through the reference's ops in fp64."""
+    prologue_case(dtype, b, length, heads, kv, hd, f, batched)
+
+
+@pytest.mark.parametrize("b, length, heads, kv, batched", [(1, 200, 8, 2, True),
+                                                            (2, 70, 4, 4, False)])
+def test_prologue_head_dim_128_with_128_features_bf16(b, length, heads, kv, batched):
+    """head_dim 128 with feature_dim 128 (a head_dim-128 model at the
+    reference's default feature_dim): bf16 arithmetic only."""
+    prologue_case(torch.bfloat16, b, length, heads, kv, 128, 128, batched)
+
+
+def prologue_case(dtype, b, length, heads, kv, hd, f, batched):
     g = torch.Generator().manual_seed(hd + f + length)
     qp = torch.randn(b, length, heads * hd, generator=g).to(dtype)
     kp = torch.randn(b, length, kv * hd, generator=g).to(dtype)
@@ -288,3 +300,81 @@ def test_config5_layer_at_size_matches_banded_oracle_layer():
             continue
         assert errs[name] <= GRAD_TOL, (name, errs)
         assert ref_close(a, b), (name, errs)
+
+
+@pytest.mark.parametrize("hidden, heads, kv, feature_dim, length", [
+    (256, 2, 1, 128, 70),   # head_dim 128, feature_dim 128, fp32: F = 256, D = 128 tiles
+    (192, 2, 2, 24, 130),   # head_dim 96: not a fused-prologue head_dim
+])
+def test_layer_at_shapes_past_the_fused_prologue_matches_oracle(hidden, heads, kv, feature_dim,
+                                                                 length):
+    """fp32 layers whose shapes the fused prologue does not take run the
+    reference's torch ops before the HIP GLA and SWA operators: output,
+    input gradient and every parameter gradient against the dense oracle."""
+    import types
+    cfg = types.SimpleNamespace(hidden_size=hidden, num_attention_heads=heads,
+                                num_key_value_heads=kv)
+    torch.manual_seed(0)
+    layer = hip_layer.LizardAttention(cfg, 0, window=16, feature_dim=feature_dim)
+    hd = hidden // heads
+    # the reference's layer tests draw phi ~ N(0, 0.3) at head_dim 32 (tiny
+    # config); the feature logits q phi^T grow with sqrt(head_dim), so phi is
+    # scaled to keep that logit scale (at 0.3 and head_dim 128 the Hedgehog
+    # maps are nearly one-hot, and the gate weight's gradient -- a sum over
+    # tokens that mostly cancels -- turns the kernels' 4-6e-3 error in
+    # d log_gamma into 2.8e-2)
+    with torch.no_grad():
+        for n, p in layer.named_parameters():
+            kind = n.split(".")[0]
+            std = 0.1 if kind in ("q_proj", "k_proj", "v_proj", "o_proj") else 0.3
+            p.normal_(0, std * (32 / hd) ** 0.5 if kind in ("phi_q", "phi_k") else std)
+    assert not hip_layer.prologue_supported(hd, feature_dim, bf16=False)
+    oracle = OracleAttention(layer)
+    layer = layer.cuda()
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(2, length, hidden, generator=g)
+    grad = torch.randn(2, length, hidden, generator=g)
+    cos, sin = (t.float()[None].expand(2, length, hd) for t in lo.rope_cos_sin(length, hd))
+    xg = x.cuda().requires_grad_()
+    y = layer(xg, (cos.cuda(), sin.cuda()))[0]
+    y.backward(grad.cuda())
+    xc = x.clone().requires_grad_()
+    expected = oracle(xc, (cos, sin))[0]
+    expected.backward(grad)
+    torch.cuda.synchronize()
+    pairs = {"out": (y, expected), "dx": (xg.grad, xc.grad)}
+    for name, p in layer.named_parameters():
+        pairs[name] = (p.grad, oracle.params[name.replace(".", "__")].grad)
+    errs = report(f"unfused layer hidden={hidden} hd={hd} f={feature_dim}", pairs)
+    assert errs["out"] <= OUT_TOL, errs
+    for name in pairs:
+        if name != "out":
+            assert errs[name] <= GRAD_TOL, (name, errs)
+
+
+def test_bf16_layer_head_dim_128_with_128_features_close_to_oracle():
+    """The fused bf16 prologue at head_dim 128, feature_dim 128 in a whole
+    bf16 layer (F = 256, D = 128: the GLA on two D tiles), against the fp64
+    oracle on the same bf16 parameters (the reference's bf16 layer bar,
+    tests/test_lizard.py:244-253)."""
+    import types
+    cfg = types.SimpleNamespace(hidden_size=256, num_attention_heads=2, num_key_value_heads=1)
+    torch.manual_seed(1)
+    layer = hip_layer.LizardAttention(cfg, 0, window=16, feature_dim=128)
+    with torch.no_grad():
+        for n, p in layer.named_parameters():
+            p.normal_(0, 0.05 if n.split(".")[0] in ("q_proj", "k_proj", "v_proj", "o_proj")
+                      else 0.3)
+    layer = layer.to(torch.bfloat16)
+    params = {n: p.detach().double() for n, p in layer.named_parameters()}
+    layer = layer.cuda()
+    x = torch.randn(2, 90, 256, generator=torch.Generator().manual_seed(2)).bfloat16()
+    cos, sin = (t.bfloat16()[None].expand(2, 90, 128) for t in lo.rope_cos_sin(90, 128))
+    assert layer._fused(x, cos, sin)
+    with torch.no_grad():
+        y = layer(x.cuda(), (cos.cuda(), sin.cuda()))[0]
+    expected = lo.lizard_layer(params, x.double(), cos.double(), sin.double(), 2, 1, 16)
+    print(f"[parity] bf16 layer hd=128 f=128: norm={norm_rel(y, expected):.2e} "
+          f"max={max_rel(y, expected):.2e}", flush=True)
+    assert y.dtype == torch.bfloat16
+    assert norm_rel(y, expected) < 2e-2

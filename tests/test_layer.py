@@ -239,3 +239,26 @@ def test_banded_oracle_layer_catches_a_window_off_by_one(monkeypatch):
                                                                                 block))
     wrong = lo.lizard_layer_banded(params, x, rope[0], rope[1], 4, 2, 16)
     assert rel_err(wrong, lo.lizard_layer(params, x, rope[0], rope[1], 4, 2, 16)) > 1e-4
+
+
+def test_layer_takes_any_even_head_dim_up_to_the_swa_limit():
+    """The reference's layer takes any head_dim / feature_dim
+    (src/lizard_attention.py:47-66); the fused prologue covers head_dim 32,
+    64, 128 (feature_dim up to 128, bf16 at 128 x 128), the rest runs its
+    torch ops before the same kernels.  The SWA kernels bound head_dim."""
+    import types
+
+    def cfg(hidden, heads):
+        return types.SimpleNamespace(hidden_size=hidden, num_attention_heads=heads,
+                                     num_key_value_heads=1)
+    for hidden, heads, f in ((256, 2, 128), (192, 2, 24), (512, 2, 256)):
+        layer = hip_layer.LizardAttention(cfg(hidden, heads), 0, feature_dim=f)
+        assert layer.head_dim == hidden // heads
+    with pytest.raises(ValueError, match="head_dim"):
+        hip_layer.LizardAttention(cfg(1024, 2), 0)            # head_dim 512 > 256
+    with pytest.raises(ValueError, match="head_dim"):
+        hip_layer.LizardAttention(cfg(99, 3), 0)              # odd head_dim
+    assert hip_layer.prologue_supported(128, 128, bf16=True)
+    assert not hip_layer.prologue_supported(128, 128, bf16=False)
+    assert hip_layer.prologue_supported(128, 64, bf16=False)
+    assert not hip_layer.prologue_supported(96, 16)
