@@ -140,7 +140,7 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
     const float* __restrict__ log_gamma, const bf16* __restrict__ dy, OutT* __restrict__ dfq,
     float* __restrict__ den_out, float* __restrict__ delta_out, float* __restrict__ p_out,
     const float* __restrict__ seg_state, int H, int L, int F, int D, int gate_per_head, int G,
-    int cps, int M, int KG) {
+    int cps, int M, int KG, int xper, int nxcd, int nblk) {
   using Cfg = BwdA<FP, DP>;
   constexpr int C = Cfg::C, PF = Cfg::PF, PD = Cfg::PD;
   constexpr int NFT = Cfg::NFT, NDT = Cfg::NDT;
@@ -169,7 +169,9 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
 
   // a workgroup walks M consecutive segments (seg .. seg + M - 1)
   const int nwg = G / M;
-  const int bh = blockIdx.x / nwg, seg = (blockIdx.x % nwg) * M;
+  int blk;
+  if (!walk_block(xper, nxcd, nblk, blk)) return;
+  const int bh = blk / nwg, seg = (blk % nwg) * M;
   const int n0 = seg * cps, n1 = min((L + C - 1) / C, n0 + M * cps);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int col = lane & 31, h = lane >> 5;
@@ -704,7 +706,8 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
     const float* __restrict__ den_in, const float* __restrict__ delta_in,
     const float* __restrict__ p_in, OutT* __restrict__ dfk, OutT* __restrict__ dv,
     float* __restrict__ dG, float* __restrict__ csum, const float* __restrict__ seg_state, int H,
-    int L, int F, int D, int gate_per_head, int G, int cps, int M, int KG) {
+    int L, int F, int D, int gate_per_head, int G, int cps, int M, int KG, int xper, int nxcd,
+    int nblk) {
   using Cfg = BwdB<FP, DP>;
   constexpr int C = Cfg::C, PF = Cfg::PF, PD = Cfg::PD;
   constexpr int NFT = Cfg::NFT, NDT = Cfg::NDT, ZP = Cfg::ZP;
@@ -733,7 +736,9 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
   // a workgroup walks M consecutive segments (seg0 .. seg0 + M - 1) in reverse,
   // entering with the state that flows into the last of them
   const int nwg = G / M;
-  const int bh = blockIdx.x / nwg, seg0 = (blockIdx.x % nwg) * M, seg = seg0 + M - 1;
+  int blk;
+  if (!walk_block(xper, nxcd, nblk, blk)) return;
+  const int bh = blk / nwg, seg0 = (blk % nwg) * M, seg = seg0 + M - 1;
   const int NT = (L + C - 1) / C;
   const int n0 = seg0 * cps, n1 = min(NT, n0 + M * cps);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -1093,10 +1098,12 @@ static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v
   // the walks take two segments per workgroup while that still gives one
   // workgroup per CU: fewer, longer walks
   const int M = (G % 2 == 0 && BH * G / 2 >= device_geom().cus) ? 2 : 1;
+  const WalkGrid wg = walk_grid(BH * G / M, KG);
   auto launch_a = [&](auto kern) {
-    hipLaunchKernelGGL(kern, dim3(BH * G / M), dim3(B_THREADS), LDS_A, st, (const bf16*)fq,
+    hipLaunchKernelGGL(kern, dim3(wg.grid), dim3(B_THREADS), LDS_A, st, (const bf16*)fq,
                        (const bf16*)fk, (const bf16*)v, lg, (const bf16*)dy, (OutT*)dfq, den,
-                       delta, p, fseg, H, L, F, D, gate_per_head, G, cps, M, KG);
+                       delta, p, fseg, H, L, F, D, gate_per_head, G, cps, M, KG, wg.per, wg.nx,
+                       wg.nblk);
   };
   if (ext) {
     if ((e = ensure_lds<gla_bwd_dq_kernel<FP, DP, OutT, VEC, true>>(LDS_A)) != hipSuccess)
@@ -1120,10 +1127,11 @@ static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v
   }
   auto kb = gla_bwd_dkv_kernel<FP, DP, OutT, VEC>;
   if ((e = ensure_lds<gla_bwd_dkv_kernel<FP, DP, OutT, VEC>>(LDS_B)) != hipSuccess) return e;
-  hipLaunchKernelGGL(kb, dim3(BH * G / M), dim3(B_THREADS), LDS_B, st, (const bf16*)fq,
+  hipLaunchKernelGGL(kb, dim3(wg.grid), dim3(B_THREADS), LDS_B, st, (const bf16*)fq,
                      (const bf16*)fk, (const bf16*)v, lg, (const bf16*)dy, (const float*)den,
                      (const float*)delta, (const float*)p, (OutT*)dfk, (OutT*)dv, dG, csum,
-                     (const float*)rseg, H, L, F, D, gate_per_head, G, cps, M, KG);
+                     (const float*)rseg, H, L, F, D, gate_per_head, G, cps, M, KG, wg.per, wg.nx,
+                     wg.nblk);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   const int nt = (L + GLA_C - 1) / GLA_C;
   const dim3 ggrid((nt + GATE_CHUNKS_PER_WG - 1) / GATE_CHUNKS_PER_WG,

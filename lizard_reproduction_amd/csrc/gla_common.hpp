@@ -262,6 +262,28 @@ struct Roles {
   }
 };
 
+// Block order of the walks.  With kv heads shared by KG > 1 query heads, the
+// walks of one kv head's query heads read the same fk and v tiles: they are
+// placed on one XCD (one L2) by xcd_block, the grid padded to a multiple of
+// the XCD count.  With KG = 1 the launch order is kept (the grouped order
+// measured slower there).
+struct WalkGrid {
+  int grid, per, nx, nblk;   // per = 0: launch order
+};
+inline WalkGrid walk_grid(int nblk, int KG) {
+  if (KG <= 1) return WalkGrid{nblk, 0, 1, nblk};
+  const int nx = device_geom().xcds;
+  const int grid = xcd_grid(nblk, nx);
+  return WalkGrid{grid, grid / nx, nx, nblk};
+}
+
+// Logical block of this walk workgroup; false for the padding blocks of a
+// grouped grid (the whole workgroup returns before any barrier).
+__device__ __forceinline__ bool walk_block(int xper, int nx, int nblk, int& blk) {
+  blk = xper ? xcd_block((int)blockIdx.x, xper, nx) : (int)blockIdx.x;
+  return blk < nblk;
+}
+
 // Per-(b, h, segment) state record: S [FP][DP] fp32, then z [FP].
 template <int FP, int DP>
 struct SegRec {

@@ -85,7 +85,7 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
     const float* __restrict__ log_gamma, bf16* __restrict__ y,
     const float* __restrict__ seg_state, float* __restrict__ final_state, int H, int L, int F,
     int D, int gate_per_head, int G, int cps, int M, int KG, float* __restrict__ raw_num,
-    float* __restrict__ raw_den) {
+    float* __restrict__ raw_den, int xper, int nxcd, int nblk) {
   using Cfg = GlaFwd<FP, DP>;
   constexpr int C = Cfg::C, PF = Cfg::PF, PD = Cfg::PD;
   constexpr int NFT = Cfg::NFT, NDT = Cfg::NDT;
@@ -106,9 +106,11 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
   float* rdec = reinterpret_cast<float*>(smem + Cfg::OFF_R);
 
   // a workgroup walks M consecutive segments seg .. seg + M - 1 from the
-  // state entering the first
+  // state entering the first; logical block b = bh nwg + segment / M
   const int nwg = G / M;
-  const int bh = blockIdx.x / nwg, seg = (blockIdx.x % nwg) * M;
+  int blk;
+  if (!walk_block(xper, nxcd, nblk, blk)) return;
+  const int bh = blk / nwg, seg = (blk % nwg) * M;
   const int NT = (L + C - 1) / C;
   const int n0 = seg * cps, n1 = min(NT, n0 + M * cps);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -366,7 +368,7 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void gla_fwd_wide_kernel(
     const float* __restrict__ log_gamma, bf16* __restrict__ y,
     const float* __restrict__ seg_state, float* __restrict__ final_state, int H, int L, int F,
     int D, int gate_per_head, int G, int cps, int M, int KG, float* __restrict__ raw_num,
-    float* __restrict__ raw_den) {
+    float* __restrict__ raw_den, int xper, int nxcd, int nblk) {
   using Cfg = GlaFwdWide<DP>;
   constexpr int FP = Cfg::FP, C = Cfg::C, PF = Cfg::PF, PD = Cfg::PD;
   constexpr int NFT = Cfg::NFT, NDT = Cfg::NDT, S_OWN = Cfg::S_OWN;
@@ -386,7 +388,9 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void gla_fwd_wide_kernel(
   float* rdec = reinterpret_cast<float*>(smem + Cfg::OFF_R);
 
   const int nwg = G / M;
-  const int bh = blockIdx.x / nwg, seg = (blockIdx.x % nwg) * M;
+  int blk;
+  if (!walk_block(xper, nxcd, nblk, blk)) return;
+  const int bh = blk / nwg, seg = (blk % nwg) * M;
   const int NT = (L + C - 1) / C;
   const int n0 = seg * cps, n1 = min(NT, n0 + M * cps);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -1052,24 +1056,25 @@ static hipError_t launch_gla_fwd_t(const void* fq, const void* fk, const void* v
     if (e != hipSuccess) return e;
   }
   const int M = gla_walk_segments(BH, G, F);
+  const WalkGrid wg = walk_grid(BH * G / M, KG);
   if constexpr (FP == 256) {   // eight waves per workgroup
     using W = GlaFwdWide<DP>;
     auto kern = gla_fwd_wide_kernel<DP, VEC, RAW>;
     hipError_t e = ensure_lds<gla_fwd_wide_kernel<DP, VEC, RAW>>(W::BYTES);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(kern, dim3(BH * G / M), dim3(WIDE_THREADS), W::BYTES, st,
+    hipLaunchKernelGGL(kern, dim3(wg.grid), dim3(WIDE_THREADS), W::BYTES, st,
                        (const bf16*)fq, (const bf16*)fk, (const bf16*)v, lg, (bf16*)y,
                        (const float*)seg_state, final_state, H, L, F, D, gate_per_head, G, cps,
-                       M, KG, RAW ? (float*)y : nullptr, raw_den);
+                       M, KG, RAW ? (float*)y : nullptr, raw_den, wg.per, wg.nx, wg.nblk);
     return hipGetLastError();
   } else {
     auto kern = gla_fwd_kernel<FP, DP, VEC, RAW>;
     hipError_t e = ensure_lds<gla_fwd_kernel<FP, DP, VEC, RAW>>(Cfg::BYTES);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(kern, dim3(BH * G / M), dim3(256), Cfg::BYTES, st, (const bf16*)fq,
+    hipLaunchKernelGGL(kern, dim3(wg.grid), dim3(256), Cfg::BYTES, st, (const bf16*)fq,
                        (const bf16*)fk, (const bf16*)v, lg, (bf16*)y, (const float*)seg_state,
                        final_state, H, L, F, D, gate_per_head, G, cps, M, KG,
-                       RAW ? (float*)y : nullptr, raw_den);
+                       RAW ? (float*)y : nullptr, raw_den, wg.per, wg.nx, wg.nblk);
     return hipGetLastError();
   }
 }
