@@ -173,7 +173,7 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
   if (!walk_block(xper, nxcd, nblk, blk)) return;
   const int bh = blk / nwg, seg = (blk % nwg) * M;
   const int n0 = seg * cps, n1 = min((L + C - 1) / C, n0 + M * cps);
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int col = lane & 31, h = lane >> 5;
   const bool vecF = VEC || (F & 7) == 0, vecD = VEC || (D & 7) == 0;
   const size_t offF = (size_t)bh * L * F, offD = (size_t)bh * L * D, offL = (size_t)bh * L;
@@ -569,7 +569,7 @@ __global__ __launch_bounds__(256, 2) void gla_bwd_state_kernel(
   const int bh = blockIdx.x / (G - 1), seg = 1 + blockIdx.x % (G - 1);
   const int NT = (L + C - 1) / C;
   const int n0 = seg * cps, n1 = min(NT, n0 + cps);
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int col = lane & 31, h = lane >> 5;
   const bool vecF = VEC || (F & 7) == 0, vecD = VEC || (D & 7) == 0;
   const size_t offF = (size_t)bh * L * F, offD = (size_t)bh * L * D, offL = (size_t)bh * L;
@@ -741,7 +741,7 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
   const int bh = blk / nwg, seg0 = (blk % nwg) * M, seg = seg0 + M - 1;
   const int NT = (L + C - 1) / C;
   const int n0 = seg0 * cps, n1 = min(NT, n0 + M * cps);
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int col = lane & 31, h = lane >> 5;
   const bool vecF = VEC || (F & 7) == 0, vecD = VEC || (D & 7) == 0;
   const size_t offF = (size_t)bh * L * F, offD = (size_t)bh * L * D, offL = (size_t)bh * L;
@@ -847,21 +847,35 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
       }
       const float lgk = lgs[ki];
       bf16x8 o8[2];
+      // kind is uniform per wave: the test sits outside the element loops, so
+      // each wave runs one straight-line loop instead of a branch per element
+      if (kind == 0) {
 #pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        const int q0 = qt * 32 + 8 * g4 + 4 * h;   // queries of registers 4 g4 .. +4
-        const f32x4 lq = *reinterpret_cast<const f32x4*>(lgs + q0);
-        const f32x4 iv = *reinterpret_cast<const f32x4*>(invc + q0);
-        const f32x4 dl = *reinterpret_cast<const f32x4*>(delsc + q0);
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const int q0 = qt * 32 + 8 * g4 + 4 * h;   // queries of registers 4 g4 .. +4
+          const f32x4 lq = *reinterpret_cast<const f32x4*>(lgs + q0);
+          const f32x4 iv = *reinterpret_cast<const f32x4*>(invc + q0);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int r = 4 * g4 + e;
-          const bool c = ki <= q0 + e;
-          const float dec = c ? fexp(lq[e] - lgk) : 0.f;
-          float val;
-          if (kind == 0) val = to_f32(to_bf16(acc[r] * dec)) * iv[e];   // a / den
-          else val = c ? (acc[r] - dl[e]) * iv[e] * dec : 0.f;          // dad
-          o8[r >> 3][r & 7] = to_bf16(val);
+          for (int e = 0; e < 4; ++e) {
+            const int r = 4 * g4 + e;
+            const float dec = ki <= q0 + e ? fexp(lq[e] - lgk) : 0.f;
+            o8[r >> 3][r & 7] = to_bf16(to_f32(to_bf16(acc[r] * dec)) * iv[e]);   // a / den
+          }
+        }
+      } else {
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const int q0 = qt * 32 + 8 * g4 + 4 * h;
+          const f32x4 lq = *reinterpret_cast<const f32x4*>(lgs + q0);
+          const f32x4 iv = *reinterpret_cast<const f32x4*>(invc + q0);
+          const f32x4 dl = *reinterpret_cast<const f32x4*>(delsc + q0);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int r = 4 * g4 + e;
+            const bool c = ki <= q0 + e;
+            const float dec = c ? fexp(lq[e] - lgk) : 0.f;
+            o8[r >> 3][r & 7] = to_bf16(c ? (acc[r] - dl[e]) * iv[e] * dec : 0.f);   // dad
+          }
         }
       }
       bf16x8* frag = kind == 0 ? fa : fd;

@@ -236,6 +236,34 @@ __device__ __forceinline__ void gate_scan(float g, int lane, float* lgs, float* 
   }
 }
 
+// Causal decay of one 32 x 32 score tile s^T (keys kt*32 .. +32 x the query
+// qi of this lane's column): p = bf16(s e^{lg_q - lg_k}) where k <= q, else
+// 0, packed as the two MFMA fragments of the lane's 16 registers.  Returns
+// the lane's partial sum of the rounded p (its half of the tile's rows).  The
+// keys of registers 4 g .. 4 g + 3 are consecutive, so their gate logs come
+// in as four 16-byte LDS reads, and the mask is a select: written per
+// register with the key's log read under the condition, the compiler turned
+// each of the 16 into a branch around its own LDS round trip.
+__device__ __forceinline__ float decay_tile(const f32x16& s, const float* lgs, int kt, int qi,
+                                            int h, bf16x8 (&p)[2]) {
+  const float lgq = lgs[qi];
+  float rsum = 0.f;
+#pragma unroll
+  for (int g4 = 0; g4 < 4; ++g4) {
+    const int k0 = kt * 32 + 8 * g4 + 4 * h;   // keys of registers 4 g4 .. +4
+    const f32x4 lk = *reinterpret_cast<const f32x4*>(lgs + k0);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int r = 4 * g4 + e;
+      const float dec = k0 + e <= qi ? fexp(lgq - lk[e]) : 0.f;
+      const bf16 pb = to_bf16(s[r] * dec);
+      p[r >> 3][r & 7] = pb;
+      rsum += to_f32(pb);
+    }
+  }
+  return rsum;
+}
+
 // log_gamma of token t of a gate row of length L, 0 past its end
 __device__ __forceinline__ float gate_at(const float* __restrict__ lgb, int t, int L) {
   return bload_f32(make_rsrc(lgb, (size_t)L * 4), (uint32_t)t * 4u);

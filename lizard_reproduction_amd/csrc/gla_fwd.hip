@@ -113,7 +113,7 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
   const int bh = blk / nwg, seg = (blk % nwg) * M;
   const int NT = (L + C - 1) / C;
   const int n0 = seg * cps, n1 = min(NT, n0 + M * cps);
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int col = lane & 31, h = lane >> 5;
   const bool vecF = VEC || (F & 7) == 0, vecD = VEC || (D & 7) == 0;
   // fk and v belong to the kv head of this query head: KG query heads share one
@@ -178,17 +178,8 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
         for (int kb = 0; kb < FP / 16; ++kb)
           s = mfma(row_operand(fk_l, PF, kt * 32 + col, 16 * kb, h),
                    row_operand(fq_l, PF, qi, 16 * kb, h), s);
-        const float lgq = lgs[qi];
         bf16x8 p[2];
-        float rsum = 0.f;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = kt * 32 + acc_row(r, h);
-          const float val = key <= qi ? s[r] * fexp(lgq - lgs[key]) : 0.f;
-          const bf16 pb = to_bf16(val);
-          p[r >> 3][r & 7] = pb;
-          rsum += to_f32(pb);
-        }
+        float rsum = decay_tile(s, lgs, kt, qi, h, p);
         rsum += xhalf(rsum);
         pfrag[(qt * 4 + kt * 2 + 0) * 64 + lane] = p[0];
         pfrag[(qt * 4 + kt * 2 + 1) * 64 + lane] = p[1];
@@ -393,7 +384,7 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void gla_fwd_wide_kernel(
   const int bh = blk / nwg, seg = (blk % nwg) * M;
   const int NT = (L + C - 1) / C;
   const int n0 = seg * cps, n1 = min(NT, n0 + M * cps);
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int col = lane & 31, h = lane >> 5;
   const bool vecF = VEC || (F & 7) == 0, vecD = VEC || (D & 7) == 0;
   const bf16* fqb = fq + (size_t)bh * L * F;
@@ -471,17 +462,8 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void gla_fwd_wide_kernel(
       for (int kb = 0; kb < FP / 16; ++kb)
         s = mfma(row_operand(fk_l, PF, kt * 32 + col, 16 * kb, h),
                  row_operand(fq_l, PF, qi, 16 * kb, h), s);
-      const float lgq = lgs[qi];
       bf16x8 p[2];
-      float rsum = 0.f;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = kt * 32 + acc_row(r, h);
-        const float val = key <= qi ? s[r] * fexp(lgq - lgs[key]) : 0.f;
-        const bf16 pb = to_bf16(val);
-        p[r >> 3][r & 7] = pb;
-        rsum += to_f32(pb);
-      }
+      float rsum = decay_tile(s, lgs, kt, qi, h, p);
       rsum += xhalf(rsum);
       pfrag[(qt * 4 + kt * 2 + 0) * 64 + lane] = p[0];
       pfrag[(qt * 4 + kt * 2 + 1) * 64 + lane] = p[1];
@@ -793,7 +775,7 @@ __global__ __launch_bounds__(256, 2) void gla_fwd_state_kernel(
 
   const int bh = blockIdx.x / (G - 1), seg = blockIdx.x % (G - 1);
   const int n0 = seg * cps, n1 = n0 + cps;   // segments before the last are full
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int col = lane & 31, h = lane >> 5;
   const bool vecF = VEC || (F & 7) == 0, vecD = VEC || (D & 7) == 0;
   const bf16* fkb = fk + (size_t)(bh / KG) * L * F;
