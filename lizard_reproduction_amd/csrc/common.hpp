@@ -48,6 +48,12 @@ __host__ __device__ __forceinline__ constexpr int acc_row(int r, int h) {
 }
 
 __device__ __forceinline__ float fexp(float x) { return __builtin_amdgcn_exp2f(x * LOG2E); }
+// 1 / max(den, FLT_MIN) by the hardware reciprocal, the output scale of the
+// forward walks: within 1 ulp of fp32, far below the bf16 rounding of y that
+// follows, where an IEEE division costs ten VALU instructions more
+__device__ __forceinline__ float recip_den(float den) {
+  return __builtin_amdgcn_rcpf(fmaxf(den, TINY));
+}
 __device__ __forceinline__ float flog(float x) { return __builtin_amdgcn_logf(x) * LN2; }
 
 __device__ __forceinline__ bf16 to_bf16(float x) { return static_cast<bf16>(x); }

@@ -224,33 +224,55 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
           const int qi = qt * 32 + col;
           // o^T = qs (S^T fq^T) + V^T P^T: the row scale of Q~ = fq qs is applied to the
           // fp32 product (den uses the same unrounded Q~, so L = 1 still gives y = v)
+          // LDS operands are read a group ahead of the products that use them
+          constexpr int KB = FP / 16, KG4 = KB < 4 ? KB : 4;
           f32x16 o = zero16();
 #pragma unroll
-          for (int kb = 0; kb < FP / 16; ++kb)
-            o = mfma(acc_operand(S[i][kb >> 1], kb & 1), row_operand_acc(fq_l, PF, qi, 16 * kb, h), o);
+          for (int k4 = 0; k4 < KB / KG4; ++k4) {
+            bf16x8 fop[KG4];
+#pragma unroll
+            for (int u = 0; u < KG4; ++u)
+              fop[u] = row_operand_acc(fq_l, PF, qi, 16 * (KG4 * k4 + u), h);
+#pragma unroll
+            for (int u = 0; u < KG4; ++u) {
+              const int kb = KG4 * k4 + u;
+              o = mfma(acc_operand(S[i][kb >> 1], kb & 1), fop[u], o);
+            }
+          }
+          bf16x8 pop[4];
+#pragma unroll
+          for (int kb = 0; kb < 4; ++kb)   // queries 0-31 have no keys in blocks 2, 3
+            if (qt == 1 || kb < 2) pop[kb] = pfrag[(qt * 4 + kb) * 64 + lane];
           const float qsv = qs[qi];
+          const float d0 = rs[qi], d1 = rs[64 + qi], d2 = qz[qi], d3 = qz[64 + qi];
+          const float d4 = qz[128 + qi], d5 = qz[192 + qi];
 #pragma unroll
           for (int r = 0; r < 16; ++r) o[r] *= qsv;
 #pragma unroll
-          for (int kb = 0; kb < 4; ++kb)   // queries 0-31 have no keys in blocks 2, 3
-            if (qt == 1 || kb < 2) o = mfma(vop[kb], pfrag[(qt * 4 + kb) * 64 + lane], o);
-          const float den = rs[qi] + rs[64 + qi] + qz[qi] + qz[64 + qi] + qz[128 + qi] + qz[192 + qi];
+          for (int kb = 0; kb < 4; ++kb)
+            if (qt == 1 || kb < 2) o = mfma(vop[kb], pop[kb], o);
+          const float den = d0 + d1 + d2 + d3 + d4 + d5;
           if constexpr (RAW) {
             store_acc_row<float>(raw_num + (size_t)bh * L * D, t0 + qi, dt * 32, L, D, vecD, o,
                                  1.f, h);
             if (dt == 0 && h == 0 && t0 + qi < L) raw_den[(size_t)bh * L + t0 + qi] = den;
           } else {
-            const float inv = 1.f / fmaxf(den, TINY);
-            store_acc_row_bf16(yr, t0 + qi, dt * 32, D, vecD, o, inv, h);
+            store_acc_row_bf16(yr, t0 + qi, dt * 32, D, vecD, o, recip_den(den), h);
           }
         }
 #pragma unroll
         for (int ft = 0; ft < NFT; ++ft) {
+          // the four K~^T operands of this f-tile are read before its products
+          bf16x8 kop[4];
+#pragma unroll
+          for (int kb = 0; kb < 4; ++kb) kop[kb] = tr_operand(fk_l, PF, 16 * kb, ft * 32, lane);
 #pragma unroll
           for (int r = 0; r < 16; ++r) S[i][ft][r] *= r_n;
 #pragma unroll
-          for (int kb = 0; kb < 4; ++kb)
-            S[i][ft] = mfma(tr_operand(fk_l, PF, 16 * kb, ft * 32, lane), vop[kb], S[i][ft]);
+          for (int kb = 0; kb < 4; ++kb) S[i][ft] = mfma(kop[kb], vop[kb], S[i][ft]);
+          __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);   // the 8 transpose reads
+          __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);  // the decay of S
+          __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);   // the 4 products
         }
       }
     }
@@ -513,8 +535,7 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void gla_fwd_wide_kernel(
                              h);
         if (dt == 0 && h == 0 && t0 + qi < L) raw_den[(size_t)bh * L + t0 + qi] = den;
       } else {
-        const float inv = 1.f / fmaxf(den, TINY);
-        store_acc_row_bf16(yr, t0 + qi, dt * 32, D, vecD, o, inv, h);
+        store_acc_row_bf16(yr, t0 + qi, dt * 32, D, vecD, o, recip_den(den), h);
       }
     }
 #pragma unroll
