@@ -234,6 +234,33 @@ __device__ __forceinline__ bf16x8 tr_operand(const bf16* tile, int pitch, int ro
   return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
+// acc + sum_{k < K} A(k) B(k) on the MFMA as a software pipeline: the
+// operands of product k + P are read (from LDS) before product k issues.
+// Written product by product, the compiler gives the operands one register
+// set and waits for each read right before its MFMA, so the reads' latency
+// adds up along the chain; the scheduling fence after each batch of reads
+// keeps them ahead (only VALU and SALU work may move across it).
+template <int K, int P, class FA, class FB>
+__device__ __forceinline__ f32x16 mfma_chain(f32x16 acc, FA a_op, FB b_op) {
+  static_assert(P >= 1 && P <= 3, "pipeline depth");
+  bf16x8 a[P + 1], b[P + 1];
+#pragma unroll
+  for (int k = 0; k < P && k < K; ++k) {
+    a[k] = a_op(k);
+    b[k] = b_op(k);
+  }
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    if (k + P < K) {
+      a[(k + P) % (P + 1)] = a_op(k + P);
+      b[(k + P) % (P + 1)] = b_op(k + P);
+    }
+    __builtin_amdgcn_sched_barrier(0x0006);
+    acc = mfma(a[k % (P + 1)], b[k % (P + 1)], acc);
+  }
+  return acc;
+}
+
 // MFMA operand whose 16 k-values run along row `row` of a row-major tile, in
 // accumulator row order: columns col0 + 4h + {0..3} and col0 + 8 + 4h + {0..3}.
 __device__ __forceinline__ bf16x8 row_operand_acc(const bf16* tile, int pitch, int row, int col0,

@@ -144,6 +144,9 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
   using Cfg = BwdA<FP, DP>;
   constexpr int C = Cfg::C, PF = Cfg::PF, PD = Cfg::PD;
   constexpr int NFT = Cfg::NFT, NDT = Cfg::NDT;
+  // LDS operands are read PIPE products ahead of their MFMAs (one at F = 256,
+  // where two would spill)
+  constexpr int PIPE = FP >= 256 ? 1 : 2;
   constexpr bool SREG = Cfg::SREG;
   extern __shared__ __align__(16) char smem[];
   bf16* fq_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_FQ);
@@ -287,15 +290,12 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
         rav[kt * 64 + qi] = 0.f;
       }
     } else if (scorer) {
-      f32x16 aT = zero16();
-#pragma unroll
-      for (int kb = 0; kb < FP / 16; ++kb)
-        aT = mfma(row_operand(fk_l, PF, kt * 32 + col, 16 * kb, h),
-                  row_operand(fq_l, PF, qi, 16 * kb, h), aT);
-#pragma unroll
-      for (int kb = 0; kb < DP / 16; ++kb)
-        vdy = mfma(row_operand(v_l, PD, kt * 32 + col, 16 * kb, h),
-                   row_operand(dy_l, PD, qi, 16 * kb, h), vdy);
+      f32x16 aT = mfma_chain<FP / 16, PIPE>(
+          zero16(), [&](int kb) { return row_operand(fk_l, PF, kt * 32 + col, 16 * kb, h); },
+          [&](int kb) { return row_operand(fq_l, PF, qi, 16 * kb, h); });
+      vdy = mfma_chain<DP / 16, PIPE>(
+          vdy, [&](int kb) { return row_operand(v_l, PD, kt * 32 + col, 16 * kb, h); },
+          [&](int kb) { return row_operand(dy_l, PD, qi, 16 * kb, h); });
       const float lgq = lgs[qi];
       float sa = 0.f, sav = 0.f;
 #pragma unroll
@@ -345,15 +345,13 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
         const int q = hq * 32 + col;
         f32x16 x = zero16();
         if constexpr (SREG) {
-#pragma unroll
-          for (int kb = 0; kb < DP / 16; ++kb)
-            x = mfma(acc_operand(St[(j >> 1) * NDT + (kb >> 1)], kb & 1),
-                     row_operand_acc(dy_l, PD, q, 16 * kb, h), x);
+          x = mfma_chain<DP / 16, PIPE>(
+              x, [&](int kb) { return acc_operand(St[(j >> 1) * NDT + (kb >> 1)], kb & 1); },
+              [&](int kb) { return row_operand_acc(dy_l, PD, q, 16 * kb, h); });
         } else {
-#pragma unroll
-          for (int kb = 0; kb < DP / 16; ++kb)
-            x = mfma(row_operand_acc(s_l, PD, ft * 32 + col, 16 * kb, h),
-                     row_operand_acc(dy_l, PD, q, 16 * kb, h), x);
+          x = mfma_chain<DP / 16, PIPE>(
+              x, [&](int kb) { return row_operand_acc(s_l, PD, ft * 32 + col, 16 * kb, h); },
+              [&](int kb) { return row_operand_acc(dy_l, PD, q, 16 * kb, h); });
         }
         X[j] = x;
         float s = 0.f;
@@ -440,10 +438,9 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
       if (s_tile(i, ft, dt)) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) St[i][r] *= r_n;
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
-          St[i] = mfma(tr_operand(v_l, PD, 16 * kb, dt * 32, lane),
-                       tr_operand(kt_l, PF, 16 * kb, ft * 32, lane), St[i]);
+        St[i] = mfma_chain<4, PIPE>(
+            St[i], [&](int kb) { return tr_operand(v_l, PD, 16 * kb, dt * 32, lane); },
+            [&](int kb) { return tr_operand(kt_l, PF, 16 * kb, ft * 32, lane); });
       }
     }
     __syncthreads();
@@ -835,15 +832,13 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
     if (!stager) {
       f32x16 acc = zero16();
       if (kind == 0) {
-#pragma unroll
-        for (int kb = 0; kb < FP / 16; ++kb)
-          acc = mfma(row_operand(fq_l, PF, qt * 32 + col, 16 * kb, h),
-                     row_operand(fk_l, PF, ki, 16 * kb, h), acc);
+        acc = mfma_chain<FP / 16, 2>(
+            acc, [&](int kb) { return row_operand(fq_l, PF, qt * 32 + col, 16 * kb, h); },
+            [&](int kb) { return row_operand(fk_l, PF, ki, 16 * kb, h); });
       } else {
-#pragma unroll
-        for (int kb = 0; kb < DP / 16; ++kb)
-          acc = mfma(row_operand(dy_l, PD, qt * 32 + col, 16 * kb, h),
-                     row_operand(v_l, PD, ki, 16 * kb, h), acc);
+        acc = mfma_chain<DP / 16, 2>(
+            acc, [&](int kb) { return row_operand(dy_l, PD, qt * 32 + col, 16 * kb, h); },
+            [&](int kb) { return row_operand(v_l, PD, ki, 16 * kb, h); });
       }
       const float lgk = lgs[ki];
       bf16x8 o8[2];
@@ -923,10 +918,9 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
         // dv_t = ks_t (fk_t dS) + sum_i (a_it / den_i) dy_i: the row scale of
         // K~ = fk ks multiplies the fp32 product
         f32x16 g = zero16();
-#pragma unroll
-        for (int kb = 0; kb < FP / 16; ++kb)
-          g = mfma(row_operand_acc(dst_l, PF, dt * 32 + col, 16 * kb, h),
-                   row_operand_acc(fk_l, PF, key, 16 * kb, h), g);
+        g = mfma_chain<FP / 16, 2>(
+            g, [&](int kb) { return row_operand_acc(dst_l, PF, dt * 32 + col, 16 * kb, h); },
+            [&](int kb) { return row_operand_acc(fk_l, PF, key, 16 * kb, h); });
         const float ksv = ks[key];
 #pragma unroll
         for (int r = 0; r < 16; ++r) g[r] *= ksv;
@@ -945,10 +939,9 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
         const int ft = t % NFT, dt = t / NFT;
 #pragma unroll
         for (int r = 0; r < 16; ++r) dS[i][r] *= r_n;
-#pragma unroll
-        for (int qb = 0; qb < 4; ++qb)
-          dS[i] = mfma(tr_operand(fq_l, PF, 16 * qb, ft * 32, lane),
-                       tr_operand(dyh_l, PD, 16 * qb, dt * 32, lane), dS[i]);
+        dS[i] = mfma_chain<4, 2>(
+            dS[i], [&](int qb) { return tr_operand(fq_l, PF, 16 * qb, ft * 32, lane); },
+            [&](int qb) { return tr_operand(dyh_l, PD, 16 * qb, dt * 32, lane); });
       }
     }
     // ---- dfk jobs (f-tile, key half), from the published dS^T -----------------
@@ -959,10 +952,9 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
         const int ft = job >> 1, hk = job & 1;
         const int key = hk * 32 + col;
         f32x16 x = zero16(), g = zero16();
-#pragma unroll
-        for (int kb = 0; kb < DP / 16; ++kb)
-          x = mfma(tr_operand(dst_l, PF, 16 * kb, ft * 32, lane),
-                   row_operand_acc(v_l, PD, key, 16 * kb, h), x);
+        x = mfma_chain<DP / 16, 2>(
+            x, [&](int kb) { return tr_operand(dst_l, PF, 16 * kb, ft * 32, lane); },
+            [&](int kb) { return row_operand_acc(v_l, PD, key, 16 * kb, h); });
 #pragma unroll
         for (int qb = 0; qb < 4; ++qb)   // keys 32-63 have no queries in blocks 0, 1
           if (hk == 0 || qb >= 2)
