@@ -69,8 +69,13 @@ __device__ __forceinline__ void own_rows(const bf16* __restrict__ base, int row,
     reg[kb] = __builtin_bit_cast(bf16x8, gload8(base, row, 16 * kb + 8 * h, L, d, vec));
 }
 
-__device__ __forceinline__ bool in_window(int i, int t, int L, int W) {
-  return t <= i && i - t < W && t < L && i < L;
+// Is key t inside the window of query i (i - W < t <= i)?  One unsigned
+// compare.  The kernels need no t < L or i < L test: for a query row inside
+// the sequence the window test already gives t <= i < L, a query row past L
+// is never stored (and reads zero q and dy rows, so it adds exactly 0 to dk
+// and dv), and a key row past L is never stored either.
+__device__ __forceinline__ bool in_window(int i, int t, int W) {
+  return (unsigned)(i - t) < (unsigned)W;
 }
 
 // Does key block [k0, k0+32) meet the windows of queries [q0, q0+32)?
@@ -149,7 +154,7 @@ __global__ __launch_bounds__(256, (swa_fwd_occupancy<DP, VEC>())) void swa_fwd_k
       float mx = NEG_INF;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        s[r] = in_window(qi, k0 + acc_row(r, h), L, W) ? s[r] * scale : NEG_INF;
+        s[r] = in_window(qi, k0 + acc_row(r, h), W) ? s[r] * scale : NEG_INF;
         mx = fmaxf(mx, s[r]);
       }
       mx = fmaxf(mx, xhalf(mx));
@@ -189,12 +194,21 @@ __global__ __launch_bounds__(256, (swa_fwd_occupancy<DP, VEC>())) void swa_fwd_k
   if (qi < L && h == 0) lse[(size_t)bh * L + qi] = m_i + flog(l_i);
 }
 
+// Workgroups per CU the backward kernels ask the compiler to fit in
+// registers (VGPRs and AGPRs together): three at d <= 32, two at d <= 64
+// (about 200 VGPRs, no spills), one beyond, where two would spill.  Without
+// a bound the d = 64 kernels took 260-320 registers, one wave per SIMD.
+template <int DP>
+constexpr int swa_bwd_occupancy() {
+  return DP <= 32 ? 3 : DP <= 64 ? 2 : 1;
+}
+
 // ----------------------------------------------------------------------------
 // backward, query side: delta (first pass over the window keys), dq (second
 // pass), and this block's partial of dmeta
 // ----------------------------------------------------------------------------
 template <int DP, typename OutT, bool VEC>
-__global__ __launch_bounds__(256) void swa_bwd_dq_kernel(
+__global__ __launch_bounds__(256, (swa_bwd_occupancy<DP>())) void swa_bwd_dq_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ meta, int n_meta, const float* __restrict__ lse,
     const bf16* __restrict__ dy, OutT* __restrict__ dq, float* __restrict__ delta_out,
@@ -258,14 +272,14 @@ __global__ __launch_bounds__(256) void swa_bwd_dq_kernel(
         if (pass == 0) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const float p = in_window(qi, k0 + acc_row(r, h), L, W) ? fexp(s[r] * scale - lse_i) : 0.f;
+            const float p = in_window(qi, k0 + acc_row(r, h), W) ? fexp(s[r] * scale - lse_i) : 0.f;
             delta += p * dp[r];
           }
         } else {
           bf16x8 ds[2];
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const float p = in_window(qi, k0 + acc_row(r, h), L, W) ? fexp(s[r] * scale - lse_i) : 0.f;
+            const float p = in_window(qi, k0 + acc_row(r, h), W) ? fexp(s[r] * scale - lse_i) : 0.f;
             ds[r >> 3][r & 7] = to_bf16(p * (dp[r] - delta));
           }
 #pragma unroll
@@ -312,7 +326,7 @@ __global__ __launch_bounds__(256) void swa_bwd_dq_kernel(
 // backward, key side: dk and dv over the queries whose windows hold the keys
 // ----------------------------------------------------------------------------
 template <int DP, typename OutT, bool VEC>
-__global__ __launch_bounds__(256) void swa_bwd_dkv_kernel(
+__global__ __launch_bounds__(256, (swa_bwd_occupancy<DP>())) void swa_bwd_dkv_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ lse, const float* __restrict__ delta_in,
     const bf16* __restrict__ dy, OutT* __restrict__ dk, OutT* __restrict__ dv,
@@ -405,14 +419,22 @@ __global__ __launch_bounds__(256) void swa_bwd_dkv_kernel(
         s = mfma(row_operand(q_l, P, 32 * half + col, 16 * kb, h), kreg[kb], s);
         dp = mfma(row_operand(dy_l, P, 32 * half + col, 16 * kb, h), vreg[kb], dp);
       }
-      // lane owns key ti; register r owns query qq0 + acc_row(r, h)
+      // lane owns key ti; register r owns query qq0 + acc_row(r, h).  The
+      // queries of registers 4 g .. 4 g + 3 are consecutive: their lse and
+      // delta come in as 16-byte LDS reads, and the window is a select
       bf16x8 pb[2], dsb[2];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int qr = 32 * half + acc_row(r, h);
-        const float p = in_window(t0 + qr, ti, L, W) ? fexp(s[r] * scale - lse_l[qr]) : 0.f;
-        pb[r >> 3][r & 7] = to_bf16(p);
-        dsb[r >> 3][r & 7] = to_bf16(p * (dp[r] - del_l[qr]));
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int qr0 = 32 * half + 8 * g4 + 4 * h;
+        const f32x4 ls = *reinterpret_cast<const f32x4*>(lse_l + qr0);
+        const f32x4 dl = *reinterpret_cast<const f32x4*>(del_l + qr0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * g4 + e;
+          const float p = in_window(t0 + qr0 + e, ti, W) ? fexp(s[r] * scale - ls[e]) : 0.f;
+          pb[r >> 3][r & 7] = to_bf16(p);
+          dsb[r >> 3][r & 7] = to_bf16(p * (dp[r] - dl[e]));
+        }
       }
 #pragma unroll
       for (int t = 0; t < DP / 32; ++t)
