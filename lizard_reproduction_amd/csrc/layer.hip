@@ -593,26 +593,45 @@ prologue_bwd_kernel(ProBwdArgs a) {
             }
           }
     };
+    // Heads past GQ: per head, the loads of all GI items are issued before any
+    // is summed (each item's heads are still summed in head order), so GI
+    // loads per thread are in flight instead of one.
     auto gather = [&](int s, const uint4 (&raw)[K::GQR][K::GI], float (&g8)[K::GI][8]) {
       const int c = 32 * (sgrp * FTW + s) + scol;
+      bool ok0[K::GI], ok1[K::GI];
 #pragma unroll
       for (int i = 0; i < K::GI; ++i) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) g8[i][e] = 0.f;
-        const bool ok0 = item_ok(i, c), ok1 = item_ok(i, c + 4);
+        ok0[i] = item_ok(i, c);
+        ok1[i] = item_ok(i, c + 4);
 #pragma unroll
         for (int g = 0; g < K::GQ; ++g)
           if (g < group) {
             const bf16x8 v = __builtin_bit_cast(bf16x8, raw[g][i]);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) g8[i][e] += (e < 4 ? ok0 : ok1) ? to_f32(v[e]) : 0.f;
+            for (int e = 0; e < 8; ++e) g8[i][e] += (e < 4 ? ok0[i] : ok1[i]) ? to_f32(v[e]) : 0.f;
           }
-        for (int g = K::GQ; g < group; ++g) {
+      }
+      for (int g = K::GQ; g < group; ++g) {
+        uint4 v[K::GI];
+#pragma unroll
+        for (int i = 0; i < K::GI; ++i) {
           const bf16* p = dphi + (gbase[i] + (long)g * a.L * F2 + c);
-          if (vec)
-            add8(p, dphi, ok0, g8[i]);
-          else
-            add4x2(p, dphi, ok0, ok1, g8[i]);
+          if (vec) {
+            v[i] = *reinterpret_cast<const uint4*>(ok0[i] ? p : dphi);
+          } else {
+            const uint2 lo = *reinterpret_cast<const uint2*>(ok0[i] ? p : dphi);
+            const uint2 hi = *reinterpret_cast<const uint2*>(ok1[i] ? p + 4 : dphi);
+            v[i] = uint4{lo.x, lo.y, hi.x, hi.y};
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < K::GI; ++i) {
+          const bf16x8 x8 = __builtin_bit_cast(bf16x8, v[i]);
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            g8[i][e] += (e < 4 ? ok0[i] : ok1[i]) ? to_f32(x8[e]) : 0.f;
         }
       }
     };
