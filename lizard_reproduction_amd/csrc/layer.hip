@@ -429,27 +429,6 @@ struct ProBwd {
   static constexpr bool FITS = LDS <= 160 * 1024;   // instantiated for launch only when it fits
 };
 
-// 8 bf16 at p (16-byte aligned) added to acc in fp32; nothing when !ok (the
-// load then reads `safe`, a valid address, and its value is dropped, so the
-// loads of a loop stay branch-free and in flight together).
-__device__ __forceinline__ void add8(const bf16* p, const bf16* safe, bool ok, float (&acc)[8]) {
-  const bf16x8 v = *reinterpret_cast<const bf16x8*>(ok ? p : safe);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) acc[e] += ok ? to_f32(v[e]) : 0.f;
-}
-
-// The same for two 4-element halves (8-byte aligned) with their own flags.
-__device__ __forceinline__ void add4x2(const bf16* p, const bf16* safe, bool ok0, bool ok1,
-                                       float (&acc)[8]) {
-  const bf16x4 v0 = *reinterpret_cast<const bf16x4*>(ok0 ? p : safe);
-  const bf16x4 v1 = *reinterpret_cast<const bf16x4*>(ok1 ? p + 4 : safe);
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    acc[e] += ok0 ? to_f32(v0[e]) : 0.f;
-    acc[4 + e] += ok1 ? to_f32(v1[e]) : 0.f;
-  }
-}
-
 template <typename T>
 __device__ __forceinline__ void store8v(T* __restrict__ p, const float (&x)[8]) {
   if constexpr (sizeof(T) == 2) {
@@ -864,14 +843,23 @@ prologue_bwd_kernel(ProBwdArgs a) {
       float dr[8], dr2[8], dvs[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) dr[e] = dr2[e] = dvs[e] = 0.f;
-#pragma unroll 4
+      // a head's four loads issue before any of them is summed; the dv loads
+      // of a q row (and dv2's when there is none) read a valid address whose
+      // value is dropped, so there is no branch between them
+      const bool use_dv = kv, use_dv2 = kv && a.dv2 != nullptr;
+#pragma unroll 2
       for (int g = 0; g < group; ++g) {
         const long o = (obase + (long)g * a.L) * hd;
-        add8(drope + o + m0, drope, true, dr);
-        add8(drope + o + mp2, drope, true, dr2);
-        if (kv) {
-          add8(a.dv + o + m0, a.dv, true, dvs);
-          if (a.dv2) add8(a.dv2 + o + m0, a.dv2, true, dvs);
+        const bf16x8 r0 = *reinterpret_cast<const bf16x8*>(drope + o + m0);
+        const bf16x8 r1 = *reinterpret_cast<const bf16x8*>(drope + o + mp2);
+        const bf16x8 v0 = *reinterpret_cast<const bf16x8*>(use_dv ? a.dv + o + m0 : drope + o + m0);
+        const bf16x8 v1 = *reinterpret_cast<const bf16x8*>(use_dv2 ? a.dv2 + o + m0 : drope + o + m0);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          dr[e] += to_f32(r0[e]);
+          dr2[e] += to_f32(r1[e]);
+          dvs[e] += use_dv ? to_f32(v0[e]) : 0.f;
+          dvs[e] += use_dv2 ? to_f32(v1[e]) : 0.f;
         }
       }
       const long tab = ((long)pos.b * a.cos_bstride + pos.l) * hd;
