@@ -79,6 +79,37 @@ __device__ __forceinline__ void store4v(T* __restrict__ p, const f32x4& x) {
   }
 }
 
+// 8 elements of T at p as raw registers (16 bytes of bf16, 32 of fp32), to be
+// converted by cvt8 later: a row's loads can then all issue before any use.
+template <typename T>
+struct Raw8 {
+  uint4 r[sizeof(T) / 2];
+};
+
+template <typename T>
+__device__ __forceinline__ Raw8<T> load8r(const T* __restrict__ p) {
+  Raw8<T> o;
+#pragma unroll
+  for (int i = 0; i < (int)(sizeof(T) / 2); ++i) o.r[i] = reinterpret_cast<const uint4*>(p)[i];
+  return o;
+}
+
+template <typename T>
+__device__ __forceinline__ void cvt8(const Raw8<T>& v, float (&x)[8]) {
+  if constexpr (sizeof(T) == 2) {
+    const bf16x8 b = __builtin_bit_cast(bf16x8, v.r[0]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = to_f32(b[e]);
+  } else {
+    const f32x4 a = __builtin_bit_cast(f32x4, v.r[0]), b = __builtin_bit_cast(f32x4, v.r[1]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[e] = a[e];
+      x[4 + e] = b[e];
+    }
+  }
+}
+
 __device__ __forceinline__ bf16x8 to_bf8(const float (&x)[8]) {
   bf16x8 o;
 #pragma unroll
@@ -247,7 +278,7 @@ __device__ __forceinline__ void copy_rows(const bf16* stage, int pitch, bf16* __
 // forward
 // ---------------------------------------------------------------------------
 template <typename T, int FT, int HT>
-__global__ __launch_bounds__(256) void prologue_fwd_kernel(ProFwdArgs a) {
+__global__ __launch_bounds__(256, 2) void prologue_fwd_kernel(ProFwdArgs a) {
   using C = Pro<T, FT, HT>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   bf16* w_hi = reinterpret_cast<bf16*>(smem);
@@ -280,28 +311,40 @@ __global__ __launch_bounds__(256) void prologue_fwd_kernel(ProFwdArgs a) {
 
     bf16x8 xh[C::HK], xl[C::HK];
     {
-      float xf[C::HK][8];
+      // Every load of the row (x, the RoPE table rows, and for bf16 inputs v
+      // of kv rows) is issued before anything is stored: as far as the
+      // compiler knows the stores may alias the inputs, so a load written
+      // after a store waits for it.  (fp32 rows load v after the RoPE stores:
+      // its raw registers, twice the bf16 ones, would cost occupancy.)  A row
+      // past the end reads row 0 (valid) and stores nothing; q rows read
+      // their own x in place of v, unused.
+      const long rrow = live ? row : 0;
+      const long tab = ((long)pos.b * a.cos_bstride + pos.l) * hd + 8 * h;
+      const T* xrow = x + rrow * hd + 8 * h;
+      const T* vrow = (kv ? static_cast<const T*>(a.v) : x) + rrow * hd + 8 * h;
+      Raw8<T> xr[C::HK], cr[C::HK], sr[C::HK], vr[C::HK];
+#pragma unroll
+      for (int kb = 0; kb < C::HK; ++kb) xr[kb] = load8r(xrow + 16 * kb);
 #pragma unroll
       for (int kb = 0; kb < C::HK; ++kb) {
-        if (live) {
-          load8f(x + (long)row * hd + 16 * kb + 8 * h, xf[kb]);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) xf[kb][e] = 0.f;
-        }
+        cr[kb] = load8r(cs + tab + 16 * kb);
+        sr[kb] = load8r(sn + tab + 16 * kb);
+        if constexpr (sizeof(T) == 2) vr[kb] = load8r(vrow + 16 * kb);
       }
+      float xf[C::HK][8];
+#pragma unroll
+      for (int kb = 0; kb < C::HK; ++kb) cvt8(xr[kb], xf[kb]);
       // RoPE (and the kv heads' v) from the fp32 row values: column
       // m = 16 kb + 8 h + e pairs with m + hd/2, the same column of kb + HK/2
       if (live) {
-        const long tab = ((long)pos.b * a.cos_bstride + pos.l) * hd;
 #pragma unroll
         for (int kb = 0; kb < C::HK / 2; ++kb) {
           const int kb2 = kb + C::HK / 2;
           float c1[8], s1[8], c2[8], s2[8];
-          load8f(cs + tab + 16 * kb + 8 * h, c1);
-          load8f(sn + tab + 16 * kb + 8 * h, s1);
-          load8f(cs + tab + 16 * kb2 + 8 * h, c2);
-          load8f(sn + tab + 16 * kb2 + 8 * h, s2);
+          cvt8(cr[kb], c1);
+          cvt8(sr[kb], s1);
+          cvt8(cr[kb2], c2);
+          cvt8(sr[kb2], s2);
           bf16x8 o1, o2;
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
@@ -313,11 +356,14 @@ __global__ __launch_bounds__(256) void prologue_fwd_kernel(ProFwdArgs a) {
           *reinterpret_cast<bf16x8*>(dst + 16 * kb2 + 8 * h) = o2;
         }
         if (kv) {
-          const T* vrow = static_cast<const T*>(a.v) + (long)row * hd;
+          if constexpr (sizeof(T) != 2) {
+#pragma unroll
+            for (int kb = 0; kb < C::HK; ++kb) vr[kb] = load8r(vrow + 16 * kb);
+          }
 #pragma unroll
           for (int kb = 0; kb < C::HK; ++kb) {
             float vf[8];
-            load8f(vrow + 16 * kb + 8 * h, vf);
+            cvt8(vr[kb], vf);
             *reinterpret_cast<bf16x8*>(a.vo + obase * hd + 16 * kb + 8 * h) = to_bf8(vf);
           }
         }
