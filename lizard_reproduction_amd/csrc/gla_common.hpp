@@ -312,6 +312,14 @@ __device__ __forceinline__ bool walk_block(int xper, int nx, int nblk, int& blk)
   return blk < nblk;
 }
 
+// Forward segment records belong to kv heads when the gate is per token: the
+// KG query heads of a kv head then see the same fk, v and gate, hence the same
+// segment states, which the state pass computes once.  The record of query
+// head bh:
+__host__ __device__ inline int seg_owner(int bh, int KG, int gate_per_head) {
+  return gate_per_head ? bh : bh / KG;
+}
+
 // Per-(b, h, segment) state record: S [FP][DP] fp32, then z [FP].
 template <int FP, int DP>
 struct SegRec {

@@ -122,7 +122,8 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
   const bf16* vb = v + (size_t)(bh / KG) * L * D;
   const rsrc_t yr = make_rsrc(y + (size_t)bh * L * D, (size_t)L * D * 2);
   const float* lgb = log_gamma + (size_t)(gate_per_head ? bh : bh / H) * L;
-  const float* st = G > 1 ? seg_state + ((size_t)bh * G + seg) * Cfg::SEG : nullptr;
+  const float* st =
+      G > 1 ? seg_state + ((size_t)seg_owner(bh, KG, gate_per_head) * G + seg) * Cfg::SEG : nullptr;
 
   const bool active = RD::active(wave);
   auto dtile = [&](int i) { return RD::tile(wave, i); };
@@ -414,7 +415,9 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void gla_fwd_wide_kernel(
   const bf16* vb = v + (size_t)(bh / KG) * L * D;
   const rsrc_t yr = make_rsrc(y + (size_t)bh * L * D, (size_t)L * D * 2);
   const float* lgb = log_gamma + (size_t)(gate_per_head ? bh : bh / H) * L;
-  const float* st = G > 1 ? seg_state + ((size_t)bh * G + seg) * SegRec<FP, DP>::SIZE : nullptr;
+  const float* st = G > 1 ? seg_state + ((size_t)seg_owner(bh, KG, gate_per_head) * G + seg) *
+                                            SegRec<FP, DP>::SIZE
+                          : nullptr;
 
   // state tile i of this wave: t = wave + 8 i -> f-tile t % NFT, d-tile t / NFT
   f32x16 S[S_OWN];
@@ -1011,6 +1014,11 @@ static hipError_t launch_gla_fwd_states_t(const void* fk, const void* v, const f
                                           int L, int F, int D, int gate_per_head, int G, int cps,
                                           int KG, hipStream_t st) {
   using Cfg = GlaState<FP, DP>;
+  if (!gate_per_head && KG > 1) {   // one record per kv head (seg_owner)
+    BH /= KG;
+    H /= KG;
+    KG = 1;
+  }
   auto ks = gla_fwd_state_kernel<FP, DP, VEC>;
   hipError_t e = ensure_lds<gla_fwd_state_kernel<FP, DP, VEC>>(Cfg::BYTES);
   if (e != hipSuccess) return e;

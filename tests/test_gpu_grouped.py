@@ -18,6 +18,7 @@ def _expand(t, group):
 
 @pytest.mark.parametrize("b, heads, kv, length, nf, nd, per_head", [
     (2, 8, 2, 300, 64, 64, True),      # segmented walks (B*H small)
+    (2, 8, 2, 300, 64, 64, False),     # segmented, per-token gate: records per kv head
     (1, 32, 8, 777, 256, 64, False),   # the layer's wide features, two segments per walk
     (16, 32, 8, 130, 128, 128, True),  # B*H fills the GPU: one walk per (b, h)
     (1, 8, 2, 300, 256, 128, False),   # past the walks' sizes: two D tiles
@@ -37,10 +38,12 @@ def test_gla_grouped_kv_equals_expanded(b, heads, kv, length, nf, nd, per_head):
     y2, st2 = kernels.gla_forward(fq, fke, ve, lg, keep_state=True)
     g1 = kernels.gla_backward(fq, fk, v, lg, dy, st1, torch.bfloat16)
     g2 = kernels.gla_backward(fq, fke, ve, lg, dy, st2, torch.bfloat16)
+    # without the forward's segment records the backward recomputes them itself
+    g3 = kernels.gla_backward(fq, fk, v, lg, dy, None, torch.bfloat16)
     torch.cuda.synchronize()
     assert y1.shape == (b, heads, length, nd) and torch.equal(y1, y2)
-    for name, a, r in zip(("dfq", "dfk", "dv", "dlog_gamma"), g1, g2):
-        assert a.shape == r.shape and torch.equal(a, r), name
+    for name, a, r, c in zip(("dfq", "dfk", "dv", "dlog_gamma"), g1, g2, g3):
+        assert a.shape == r.shape and torch.equal(a, r) and torch.equal(a, c), name
 
 
 def test_gla_prefill_state_with_expanded_operands_matches_walk():
