@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define LZ_ABI_VERSION 11
+#define LZ_ABI_VERSION 12
 
 /* Largest feature (nf) and value (nd) dim the GLA entry points take. */
 #define LZ_GLA_MAX_DIM 4096
@@ -102,6 +102,17 @@ int lz_gla_fwd(const void* fq, const void* fk, const void* v, const float* log_g
 int lz_gla_fwd_noalloc(const void* fq, const void* fk, const void* v, const float* log_gamma,
                        void* y, int batch, int heads, int kv_heads, int length, int nf, int nd,
                        int gate_per_head, int chunk, void* stream);
+
+/*
+ * Set-up of lz_gla_fwd_noalloc on the current device, once per device: the
+ * device address of its static array, and the LDS limits
+ * (hipFuncSetAttribute) of every kernel it can launch.  No counterpart in the
+ * reference.  lz_gla_fwd_noalloc makes the same set-up on its first call on a
+ * device; callers that capture that call into a HIP graph call lz_init first,
+ * outside the capture, so that the captured call makes no runtime call but
+ * its kernel launches.  Returns 0 or an error code (lz_last_error).
+ */
+int lz_init(void);
 
 /*
  * GLA prefill: lz_gla_fwd that also writes the recurrent state after the last

@@ -8,7 +8,7 @@ import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "_lib", "liblizard_hip.so")
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -18,6 +18,7 @@ _S = ctypes.c_size_t
 # name -> (restype, argtypes); must match include/lizard_hip.h
 SIGNATURES = {
     "lz_abi_version": (_I, []),
+    "lz_init": (_I, []),
     "lz_last_error": (ctypes.c_char_p, []),
     "lz_gla_fwd_workspace_bytes": (_S, [_I, _I, _I, _I, _I, _I, _I]),
     "lz_gla_fwd": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _S, _P]),

@@ -17,6 +17,7 @@ hipError_t launch_gla_decode(const void* fq, const void* fk, const void* v, cons
                              float* state, void* y, int B, int H, int F, int D,
                              int gate_per_head, int KG, hipStream_t st);
 size_t gla_fwd_workspace(int B, int H, int L, int F, int D);
+hipError_t gla_fwd_prepare();
 bool gla_dims_supported(int F, int D);
 struct GlaTiles {
   int nF, Ft, nD, Dt;
@@ -273,6 +274,28 @@ static int scratch_address(float** out) {
   return 0;
 }
 
+// The no-allocation forward's set-up on the current device, once per device:
+// the scratch array's address and the LDS limits of the kernels it launches
+// (hipFuncSetAttribute, which the other entry points make on their first
+// launch of each kernel).  Made eagerly by lz_init, a later call under HIP
+// graph capture makes no runtime call but its kernel launches.
+static int noalloc_setup(float** ws) {
+  if (int rc = scratch_address(ws)) return rc;
+  constexpr int MAXDEV = 64;
+  static std::once_flag once[MAXDEV];
+  static hipError_t status[MAXDEV];
+  int dev = 0;
+  if (hipError_t e = hipGetDevice(&dev); e != hipSuccess)
+    return hip_status(e, "gla_fwd_noalloc: hipGetDevice");
+  std::call_once(once[dev], [dev] { status[dev] = lz::gla_fwd_prepare(); });
+  return hip_status(status[dev], "gla_fwd_noalloc: LDS limits of the forward kernels");
+}
+
+extern "C" int lz_init(void) {
+  float* ws = nullptr;
+  return noalloc_setup(&ws);
+}
+
 extern "C" int lz_gla_fwd_noalloc(const void* fq, const void* fk, const void* v,
                                   const float* log_gamma, void* y, int batch, int heads,
                                   int kv_heads, int length, int nf, int nd, int gate_per_head,
@@ -287,8 +310,8 @@ extern "C" int lz_gla_fwd_noalloc(const void* fq, const void* fk, const void* v,
                    "the %zu-byte static scratch (use lz_gla_fwd with a workspace)",
                 need, (size_t)LZ_GLA_FWD_NOALLOC_MAX_BYTES);
   float* ws = nullptr;
-  if (need)
-    if (int rc = scratch_address(&ws)) return rc;
+  if (int rc = noalloc_setup(&ws)) return rc;
+  if (!need) ws = nullptr;
   return hip_status(lz::launch_gla_fwd(fq, fk, v, log_gamma, y, batch, heads, length, nf, nd,
                                        gate_per_head ? 1 : 0, heads / kv_heads, ws, nullptr,
                                        nullptr, (hipStream_t)stream),

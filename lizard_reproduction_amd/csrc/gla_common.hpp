@@ -50,6 +50,9 @@ hipError_t launch_gla_bwd_any(const void* fq, const void* fk, const void* v, con
                               bool grad_bf16, int B, int H, int L, int F, int D,
                               int gate_per_head, int KG, const float* fwd_ws, void* ws,
                               hipStream_t st);
+// Sets, on the current device, the LDS limit of every kernel launch_gla_fwd
+// (without raw_den) and launch_gla_fwd_states can launch.
+hipError_t gla_fwd_prepare();
 void gla_segments(int BH, int L, int F, int* G, int* cps);
 int gla_walk_segments(int BH, int G, int F);
 size_t gla_segment_floats(int BH, int G, int F, int D);

@@ -1090,6 +1090,33 @@ static hipError_t launch_gla_fwd_t(const void* fq, const void* fk, const void* v
   }
 }
 
+// The LDS limit (hipFuncSetAttribute) of every kernel launch_gla_fwd and
+// launch_gla_fwd_states can launch at the walks' own sizes, set on the
+// current device; afterwards those launches make no other runtime call.
+template <int FP, int DP, bool VEC>
+static hipError_t prepare_fwd_t() {
+  hipError_t e;
+  if constexpr (FP == 256)
+    e = ensure_lds<gla_fwd_wide_kernel<DP, VEC, false>>(GlaFwdWide<DP>::BYTES);
+  else
+    e = ensure_lds<gla_fwd_kernel<FP, DP, VEC, false>>(GlaFwd<FP, DP>::BYTES);
+  if (e != hipSuccess) return e;
+  return ensure_lds<gla_fwd_state_kernel<FP, DP, VEC>>(GlaState<FP, DP>::BYTES);
+}
+
+hipError_t gla_fwd_prepare() {
+  hipError_t e;
+#define LZ_GLA_PREP(FPV, DPV)                                               \
+  if ((e = prepare_fwd_t<FPV, DPV, true>()) != hipSuccess) return e;        \
+  if ((e = prepare_fwd_t<FPV, DPV, false>()) != hipSuccess) return e;
+  LZ_GLA_PREP(32, 32) LZ_GLA_PREP(32, 64) LZ_GLA_PREP(32, 128)
+  LZ_GLA_PREP(64, 32) LZ_GLA_PREP(64, 64) LZ_GLA_PREP(64, 128)
+  LZ_GLA_PREP(128, 32) LZ_GLA_PREP(128, 64) LZ_GLA_PREP(128, 128)
+  LZ_GLA_PREP(256, 32) LZ_GLA_PREP(256, 64)
+#undef LZ_GLA_PREP
+  return hipSuccess;
+}
+
 // raw_den == nullptr: y is the bf16 output; otherwise (one F tile of a split
 // feature dimension) y is the fp32 numerator [BH, L, D] and raw_den the fp32
 // denominator [BH, L] of this tile (see gla_fwd_kernel's RAW).

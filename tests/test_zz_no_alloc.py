@@ -32,6 +32,18 @@ def _run(lib, fq, fk, v, lg, noalloc):
     return y
 
 
+def test_init_then_noalloc_forward():
+    """lz_init (the no-allocation forward's per-device set-up, made outside a
+    capture by callers that capture) succeeds, again when repeated, and the
+    forward after it matches the workspace forward."""
+    lib = _lib.load()
+    assert lib.lz_init() == 0, lib.lz_last_error()
+    assert lib.lz_init() == 0, lib.lz_last_error()
+    fq, fk, v, lg, _ = baseline_gla_inputs(1, 8, 700, 64, True, 2.0, 1.5, seed=5)
+    dev = [t.cuda().contiguous() for t in (fq, fk, v, lg)]
+    assert torch.equal(_run(lib, *dev, noalloc=True), _run(lib, *dev, noalloc=False))
+
+
 @pytest.mark.parametrize("order", ["noalloc_first", "workspace_first"])
 def test_noalloc_forward_equals_workspace_forward(order):
     lib = _lib.load()
