@@ -184,7 +184,7 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
   const size_t offFk = (size_t)(bh / KG) * L * F, offDv = (size_t)(bh / KG) * L * D;
   const float* lgb = log_gamma + (size_t)(gate_per_head ? bh : bh / H) * L;
   const float* st =
-      G > 1 ? seg_state + ((size_t)seg_owner(bh, KG, gate_per_head) * G + seg) * Cfg::SEG : nullptr;
+      G > 1 ? seg_state + ((size_t)seg_owner_uniform(bh, KG, gate_per_head) * G + seg) * Cfg::SEG : nullptr;
 
   // owned S^T tiles (rows d, columns f): i -> (f-tile, d-tile)
   auto s_tile = [&](int i, int& ft, int& dt) __attribute__((always_inline)) -> bool {

@@ -322,6 +322,13 @@ __device__ __forceinline__ bool walk_block(int xper, int nx, int nblk, int& blk)
 __host__ __device__ inline int seg_owner(int bh, int KG, int gate_per_head) {
   return gate_per_head ? bh : bh / KG;
 }
+// The same inside a walk, marked wave-uniform: used as written above in the
+// record pointer, it led the compiler to take the walks' chunk buffer
+// resources for divergent and to wrap every chunk load in a readfirstlane
+// loop.
+__device__ __forceinline__ int seg_owner_uniform(int bh, int KG, int gate_per_head) {
+  return __builtin_amdgcn_readfirstlane(seg_owner(bh, KG, gate_per_head));
+}
 
 // Per-(b, h, segment) state record: S [FP][DP] fp32, then z [FP].
 template <int FP, int DP>

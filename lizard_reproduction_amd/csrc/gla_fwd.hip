@@ -123,7 +123,7 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
   const rsrc_t yr = make_rsrc(y + (size_t)bh * L * D, (size_t)L * D * 2);
   const float* lgb = log_gamma + (size_t)(gate_per_head ? bh : bh / H) * L;
   const float* st =
-      G > 1 ? seg_state + ((size_t)seg_owner(bh, KG, gate_per_head) * G + seg) * Cfg::SEG : nullptr;
+      G > 1 ? seg_state + ((size_t)seg_owner_uniform(bh, KG, gate_per_head) * G + seg) * Cfg::SEG : nullptr;
 
   const bool active = RD::active(wave);
   auto dtile = [&](int i) { return RD::tile(wave, i); };
@@ -415,7 +415,7 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void gla_fwd_wide_kernel(
   const bf16* vb = v + (size_t)(bh / KG) * L * D;
   const rsrc_t yr = make_rsrc(y + (size_t)bh * L * D, (size_t)L * D * 2);
   const float* lgb = log_gamma + (size_t)(gate_per_head ? bh : bh / H) * L;
-  const float* st = G > 1 ? seg_state + ((size_t)seg_owner(bh, KG, gate_per_head) * G + seg) *
+  const float* st = G > 1 ? seg_state + ((size_t)seg_owner_uniform(bh, KG, gate_per_head) * G + seg) *
                                             SegRec<FP, DP>::SIZE
                           : nullptr;
 
