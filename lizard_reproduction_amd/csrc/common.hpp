@@ -15,8 +15,13 @@
 //     never leave registers on their way to P*V, nor the GLA state on its way
 //     to Q~ S.  LDS operands paired with them come from row_operand_acc or,
 //     contracting down the rows of a tile, from tr_operand (transpose reads);
-//   * contiguous order, slot j <-> k = 8*h + j: row_operand, for products
-//     whose two operands both come from row-major tiles or global rows.
+//   * contiguous order, slot j <-> k = 8*h + j: row_operand (one 16-byte
+//     read) and tr_operand_c, for products whose two operands both come from
+//     LDS tiles or global rows.  Where neither operand is an accumulator this
+//     order is the one to use: at the row pitches used here (72, 152, 280
+//     elements) the two 8-byte reads of row_operand_acc fall on the same
+//     banks for rows r and r + 16, and ran at a third of the 16-byte read's
+//     rate (64 against ~190 bytes per clock per CU, measured on gfx950).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -259,6 +264,17 @@ __device__ __forceinline__ f32x16 mfma_chain(f32x16 acc, FA a_op, FB b_op) {
     acc = mfma(a[k % (P + 1)], b[k % (P + 1)], acc);
   }
   return acc;
+}
+
+// The same k-values as tr_operand in contiguous order (slot j <-> row
+// row0 + 8h + j), to pair with row_operand.
+__device__ __forceinline__ bf16x8 tr_operand_c(const bf16* tile, int pitch, int row0, int col0,
+                                               int lane) {
+  const int g = lane >> 4, s = lane & 15;
+  const bf16* p = tile + (row0 + 8 * (g >> 1) + (s >> 2)) * pitch + col0 + 16 * (g & 1) + 4 * (s & 3);
+  const bf16x4 lo = lds_read_tr(p);
+  const bf16x4 hi = lds_read_tr(p + 4 * pitch);
+  return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
 // MFMA operand whose 16 k-values run along row `row` of a row-major tile, in

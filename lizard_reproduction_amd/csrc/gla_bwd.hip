@@ -82,9 +82,9 @@ __device__ __forceinline__ void store_tile8(const uint4 (&reg)[N], bf16* tile, i
 //
 //   phase 1  waves 0-3: the score tile (keys kt x queries qt) a^T and v dy^T,
 //            the decay, sum_t a and sum_t a (v . dy) (the tile of keys 32-63 x
-//            queries 0-31 is causally zero and skipped); waves 4-7: Q~ . z and
-//            K~ = bf16(fk ks) with its column sums; X jobs (f-tile, query
-//            half): X = S dy^T and qs fq . X, waves 4-7 first;
+//            queries 0-31 is causally zero: its wave forms Q~ . z instead);
+//            waves 4-7: K~ = bf16(fk ks) with its column sums; X jobs (f-tile,
+//            query half): X = S dy^T and qs fq . X, waves 4-7 first;
 //   phase 2  waves 0-3: den, delta, dad fragments;
 //   phase 3  X jobs: dfq and fq . dfq; S^T tiles: S^T <- r S^T + V^T K~;
 //   tail     p, next chunk, z update, publish S.
@@ -243,6 +243,9 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
     }
   };
 
+  // per-chunk single-wave work goes to waves whose tail is otherwise light:
+  // the gate to wave 3, fq . dfq to wave 2, the z update to the last FP threads
+  constexpr int GW = 3, PW = 2;
   // DEPTH register sets: while chunk n computes, chunks n+1 .. n+DEPTH are in flight
   constexpr int DEPTH = Cfg::DEPTH;
   uint4 rq[DEPTH][Cfg::NLF], rk[DEPTH][Cfg::NLF], rv[DEPTH][Cfg::NLD], rd[DEPTH][Cfg::NLD];
@@ -254,7 +257,7 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
       load_tile8<FP>(rk[S], fk + offFk, n * C, L, F, vecF);
       load_tile8<DP>(rv[S], v + offDv, n * C, L, D, vecD);
       load_tile8<DP>(rd[S], dy + offD, n * C, L, D, vecD);
-      if (wave == 0) rg[S] = gate_at(lgb, n * C + lane, L);
+      if (wave == GW) rg[S] = gate_at(lgb, n * C + lane, L);
     }
   };
   auto stage = [&](auto set) __attribute__((always_inline)) {
@@ -263,7 +266,7 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
     store_tile8<FP>(rk[S], fk_l, PF);
     store_tile8<DP>(rv[S], v_l, PD);
     store_tile8<DP>(rd[S], dy_l, PD);
-    if (wave == 0) gate_scan(rg[S], lane, lgs, qs, ks, rdec);
+    if (wave == GW) gate_scan(rg[S], lane, lgs, qs, ks, rdec);
   };
   issue(SET0, n0);
   if constexpr (DEPTH == 2) issue(SET1, n0 + 1);
@@ -281,7 +284,10 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
   auto step = [&](auto set, int n) __attribute__((always_inline)) {
     constexpr int S = decltype(set)::value;
     const int t0 = n * C;
-    issue(set, n + DEPTH);
+    // waves 0-3 load the chunk after next now, waves 4-7 once their phase-1
+    // work is done: issued together, the later waves' loads waited for free
+    // slots in the CU's memory queue and held back their phase-1 work
+    if (wave < 4) issue(set, n + DEPTH);
     // ---- phase 1 ---------------------------------------------------------------
     f32x16 vdy = zero16();
     float dec[16];   // causal decay of the score tile, reused in phase 2
@@ -289,6 +295,19 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
       if (h == 0) {
         ra[kt * 64 + qi] = 0.f;
         rav[kt * 64 + qi] = 0.f;
+      }
+      // qs (fq . z) by quarters of the features; query = lane
+      constexpr int FQ = FP / 4;
+#pragma unroll
+      for (int w4 = 0; w4 < 4; ++w4) {
+        float acc = 0.f;
+#pragma unroll
+        for (int c = 0; c < FQ; c += 8) {
+          const bf16x8 x = *reinterpret_cast<const bf16x8*>(fq_l + lane * PF + w4 * FQ + c);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc += to_f32(x[e]) * zs[w4 * FQ + c + e];
+        }
+        qz[w4 * 64 + lane] = acc * qs[lane];
       }
     } else if (scorer) {
       f32x16 aT = mfma_chain<FP / 16, PIPE>(
@@ -319,17 +338,6 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
         rav[kt * 64 + qi] = sav;
       }
     } else {
-      // qs (fq . z) over a quarter of the features; query = lane
-      const int w4 = wave - 4;
-      constexpr int FQ = FP / 4;
-      float acc = 0.f;
-#pragma unroll
-      for (int c = 0; c < FQ; c += 8) {
-        const bf16x8 x = *reinterpret_cast<const bf16x8*>(fq_l + lane * PF + w4 * FQ + c);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc += to_f32(x[e]) * zs[w4 * FQ + c + e];
-      }
-      qz[w4 * 64 + lane] = acc * qs[lane];
       // K~ = bf16(fk ks) once per chunk (the forward's rounding), with its
       // column sums for z
       uint4 kti[RowItems<FP>::N];
@@ -351,8 +359,8 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
               [&](int kb) { return row_operand_acc(dy_l, PD, q, 16 * kb, h); });
         } else {
           x = mfma_chain<DP / 16, PIPE>(
-              x, [&](int kb) { return row_operand_acc(s_l, PD, ft * 32 + col, 16 * kb, h); },
-              [&](int kb) { return row_operand_acc(dy_l, PD, q, 16 * kb, h); });
+              x, [&](int kb) { return row_operand(s_l, PD, ft * 32 + col, 16 * kb, h); },
+              [&](int kb) { return row_operand(dy_l, PD, q, 16 * kb, h); });
         }
         X[j] = x;
         float s = 0.f;
@@ -366,6 +374,7 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
         if (h == 0) nx[ft * 64 + q] = s * qs[q];
       }
     }
+    if (wave >= 4) issue(set, n + DEPTH);
     __syncthreads();
     // ---- phase 2: den, delta, dad fragments (waves 0-3) ------------------------
     if (live) {
@@ -446,14 +455,14 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
     }
     __syncthreads();
     // ---- next chunk into LDS; z update; fq . dfq of this chunk; publish S ---------
-    if (tid < 64 && t0 + tid < L) {
+    if (wave == PW && t0 + lane < L) {
       float s = 0.f;
 #pragma unroll
-      for (int ft = 0; ft < NFT; ++ft) s += pp[ft * 64 + tid];
-      p_out[offL + t0 + tid] = s;
+      for (int ft = 0; ft < NFT; ++ft) s += pp[ft * 64 + lane];
+      p_out[offL + t0 + lane] = s;
     }
     if (n + 1 < n1) stage(std::integral_constant<int, (S + 1) % DEPTH>{});
-    if (tid < FP) zs[tid] = zs[tid] * r_n + sum_parts<FP>(zp, tid);
+    if (const int f = tid - (B_THREADS - FP); f >= 0) zs[f] = zs[f] * r_n + sum_parts<FP>(zp, f);
     publish();
     __syncthreads();
   };
@@ -781,6 +790,9 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
     }
   };
 
+  // per-chunk single-wave work goes to waves whose tail is otherwise light:
+  // the token scalars to wave 3, dG to wave 2, the dz update to waves 4 and up
+  constexpr int SCW = 3, DGW = 2;
   // DEPTH register sets: while chunk n computes, chunks n-1 .. n-DEPTH are in flight
   constexpr int DEPTH = Cfg::DEPTH;
   uint4 rq[DEPTH][Cfg::NLF], rk[DEPTH][Cfg::NLF], rv[DEPTH][Cfg::NLD], rd[DEPTH][Cfg::NLD];
@@ -792,7 +804,7 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
       load_tile8<FP>(rk[S], fk + offFk, n * C, L, F, vecF);
       load_tile8<DP>(rv[S], v + offDv, n * C, L, D, vecD);
       load_tile8<DP>(rd[S], dy + offD, n * C, L, D, vecD);
-      if (wave == 0) sc[S] = load_scalars(lgb, den_in, delta_in, p_in, offL, n * C + lane, L);
+      if (wave == SCW) sc[S] = load_scalars(lgb, den_in, delta_in, p_in, offL, n * C + lane, L);
     }
   };
   // chunk n's tiles and per-token scalars (scalars into the buffers of parity n & 1)
@@ -803,7 +815,7 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
     store_tile8<DP>(rv[S], v_l, PD);
     store_tile8<DP>(rd[S], dy_l, PD);
     const int b = n & 1;
-    if (wave == 0)
+    if (wave == SCW)
       bwd_scalars(sc[S].g, sc[S].den, sc[S].delta, sc[S].p, lane, lgs, qs, ks, rdec,
                   invd + 64 * b, dels + 64 * b, ps + 64 * b, qh + 64 * b, dw + 64 * b);
   };
@@ -815,8 +827,8 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
 
   const int kind = wave >> 2, qt = (wave >> 1) & 1, kt = wave & 1;   // phase-1 tile
   const int ki = kt * 32 + col;                                       // its key (lane)
-  // waves 1 and 5 hold the causally zero tiles (kt = 1, qt = 0): they do the
-  // per-chunk staging work instead, as threads a = 0 .. 127
+  // waves 1 and 5 hold the causally zero tiles (kt = 1, qt = 0): they form the
+  // dz partial sums instead, as threads a = 0 .. 127 (dY^ is shared by all)
   const bool stager = kt == 1 && qt == 0;
   const int a = (kind << 6) + lane;
   // chunk n is in LDS and register set `set` is free; the next set holds chunk n-1
@@ -828,7 +840,10 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
     const float* delsc = dels + 64 * cur;
     const float* qhc = qh + 64 * cur;
     const float* dwc = dw + 64 * cur;
-    issue(set, n - DEPTH);
+    // waves 0-3 load the chunk after next now, waves 4-7 once their phase-1
+    // work is done: issued together, the later waves' loads waited for free
+    // slots in the CU's memory queue and held back their phase-1 products
+    if (wave < 4) issue(set, n - DEPTH);
     // ---- phase 1: one 32x32 tile (queries x keys) of s or dy v^T per wave ----
     if (!stager) {
       f32x16 acc = zero16();
@@ -878,10 +893,10 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
       frag[(kt * 4 + qt * 2 + 0) * 64 + lane] = o8[0];
       frag[(kt * 4 + qt * 2 + 1) * 64 + lane] = o8[1];
     }
-    // dY^ = bf16(qh dy), once per chunk, for dS += fq^T dY^
-    if (stager) {
+    // dY^ = bf16(qh dy), once per chunk, for dS += fq^T dY^, by all threads
+    {
       constexpr int K8 = DP / 8;
-      for (int idx = a; idx < C * K8; idx += 128) {
+      for (int idx = tid; idx < C * K8; idx += B_THREADS) {
         const int t = idx / K8, c8 = 8 * (idx % K8);
         const bf16x8 x = *reinterpret_cast<const bf16x8*>(dy_l + t * PD + c8);
         *reinterpret_cast<bf16x8*>(dyh_l + t * PD + c8) = scale8(x, qhc[t]);
@@ -907,6 +922,7 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
         *reinterpret_cast<f32x4*>(dst + 4) = f32x4{za[4], za[5], za[6], za[7]};
       }
     }
+    if (wave >= 4) issue(set, n - DEPTH);
     __syncthreads();
     const float r_n = rdec[0];
     // ---- phase 2: dv jobs from the published dS^T -----------------------------
@@ -920,8 +936,8 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
         // K~ = fk ks multiplies the fp32 product
         f32x16 g = zero16();
         g = mfma_chain<FP / 16, 2>(
-            g, [&](int kb) { return row_operand_acc(dst_l, PF, dt * 32 + col, 16 * kb, h); },
-            [&](int kb) { return row_operand_acc(fk_l, PF, key, 16 * kb, h); });
+            g, [&](int kb) { return row_operand(dst_l, PF, dt * 32 + col, 16 * kb, h); },
+            [&](int kb) { return row_operand(fk_l, PF, key, 16 * kb, h); });
         const float ksv = ks[key];
 #pragma unroll
         for (int r = 0; r < 16; ++r) g[r] *= ksv;
@@ -954,8 +970,8 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
         const int key = hk * 32 + col;
         f32x16 x = zero16(), g = zero16();
         x = mfma_chain<DP / 16, 2>(
-            x, [&](int kb) { return tr_operand(dst_l, PF, 16 * kb, ft * 32, lane); },
-            [&](int kb) { return row_operand_acc(v_l, PD, key, 16 * kb, h); });
+            x, [&](int kb) { return tr_operand_c(dst_l, PF, 16 * kb, ft * 32, lane); },
+            [&](int kb) { return row_operand(v_l, PD, key, 16 * kb, h); });
 #pragma unroll
         for (int qb = 0; qb < 4; ++qb)   // keys 32-63 have no queries in blocks 0, 1
           if (hk == 0 || qb >= 2)
@@ -982,7 +998,7 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
     }
     __syncthreads();
     // ---- dG of this chunk and its sum; publish dS; previous chunk; dz update ---
-    if (wave == 0) {
+    if (wave == DGW) {
       float g = 0.f;
       if (t0 + lane < L) {
         float s = 0.f;
@@ -997,7 +1013,7 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
     }
     publish();
     if (n - 1 >= n0) stage(std::integral_constant<int, (S + 1) % DEPTH>{}, n - 1);
-    for (int f = tid; f < FP; f += B_THREADS) {
+    for (int f = tid - 256; f >= 0 && f < FP; f += 256) {
       float za = dzs[f] * r_n;
 #pragma unroll
       for (int p = 0; p < ZP; ++p) za += dzp[p * FP + f];

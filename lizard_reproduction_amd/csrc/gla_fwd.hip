@@ -521,8 +521,8 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void gla_fwd_wide_kernel(
       f32x16 o = zero16();
 #pragma unroll
       for (int kb = 0; kb < FP / 16; ++kb)
-        o = mfma(row_operand_acc(st_l, PF, dt * 32 + col, 16 * kb, h),
-                 row_operand_acc(fq_l, PF, qi, 16 * kb, h), o);
+        o = mfma(row_operand(st_l, PF, dt * 32 + col, 16 * kb, h),
+                 row_operand(fq_l, PF, qi, 16 * kb, h), o);
       const float qsv = qs[qi];
 #pragma unroll
       for (int r = 0; r < 16; ++r) o[r] *= qsv;
