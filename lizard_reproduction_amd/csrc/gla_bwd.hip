@@ -82,12 +82,13 @@ __device__ __forceinline__ void store_tile8(const uint4 (&reg)[N], bf16* tile, i
 //
 //   phase 1  waves 0-3: the score tile (keys kt x queries qt) a^T and v dy^T,
 //            the decay, sum_t a and sum_t a (v . dy) (the tile of keys 32-63 x
-//            queries 0-31 is causally zero: its wave forms Q~ . z instead);
-//            waves 4-7: K~ = bf16(fk ks) with its column sums; X jobs (f-tile,
+//            queries 0-31 is causally zero: its wave forms half of Q~ . z
+//            instead); waves 4-7: the other half of Q~ . z, K~ = bf16(fk ks)
+//            with its column sums; X jobs (f-tile,
 //            query half): X = S dy^T and qs fq . X, waves 4-7 first;
-//   phase 2  waves 0-3: den, delta, dad fragments;
+//   phase 2  waves 0-3: den, delta, dad fragments; waves 4-7: the z update;
 //   phase 3  X jobs: dfq and fq . dfq; S^T tiles: S^T <- r S^T + V^T K~;
-//   tail     p, next chunk, z update, publish S.
+//   tail     p, next chunk, publish S.
 // S lives in the accumulators of the waves that own its tiles.  With FP = 256
 // (eight f-tiles) wave w owns f-tile w across all d-tiles and contracts its X
 // jobs from its own registers; otherwise tile t = wave + 8 i is owned
@@ -115,8 +116,8 @@ struct BwdA : BwdCommon<FP, DP> {
   static constexpr int OFF_FR = OFF_SL + (SREG ? 0 : FP * PD * 2);   // dad fragments
   static constexpr int OFF_RA = OFF_FR + 2 * 4 * 64 * 16;  // [2][64] sum_t a
   static constexpr int OFF_RAV = OFF_RA + 2 * 64 * 4;      // [2][64] sum_t a (v . dy)
-  static constexpr int OFF_QZ = OFF_RAV + 2 * 64 * 4;      // [4][64] Q~ . z partials
-  static constexpr int OFF_NX = OFF_QZ + 4 * 64 * 4;       // [NFT][64] Q~ . (S dy) partials
+  static constexpr int OFF_QZ = OFF_RAV + 2 * 64 * 4;      // [6][64] Q~ . z partials
+  static constexpr int OFF_NX = OFF_QZ + 6 * 64 * 4;       // [NFT][64] Q~ . (S dy) partials
   static constexpr int OFF_PP = OFF_NX + NFT * 64 * 4;     // [NFT][64] fq . dfq partials
   static constexpr int OFF_DEN = OFF_PP + NFT * 64 * 4;
   static constexpr int OFF_DEL = OFF_DEN + 64 * 4;
@@ -124,11 +125,42 @@ struct BwdA : BwdCommon<FP, DP> {
   static constexpr int OFF_QS = OFF_LG + 64 * 4;
   static constexpr int OFF_KS = OFF_QS + 64 * 4;
   static constexpr int OFF_Z = OFF_KS + 64 * 4;
-  static constexpr int OFF_ZP = OFF_Z + FP * 4;            // 2048 partial sums of K~
+  static constexpr int OFF_ZP = OFF_Z + 2 * FP * 4;        // 2048 partial sums of K~
   static constexpr int OFF_R = OFF_ZP + 2048 * 4;
   static constexpr int BYTES = OFF_R + 16;
   static_assert(BYTES <= 160 * 1024, "LDS budget");
 };
+
+// qz[lane] = qs_lane (fq_lane . z) over features [f0, f0 + NF) (query = lane)
+template <int NF>
+__device__ __forceinline__ void qz_part(const bf16* fq_l, int pitch, const float* zs,
+                                        const float* qs, float* qz, int lane, int f0) {
+  float acc = 0.f;
+#pragma unroll
+  for (int c = 0; c < NF; c += 8) {
+    const bf16x8 x = *reinterpret_cast<const bf16x8*>(fq_l + lane * pitch + f0 + c);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc += to_f32(x[e]) * zs[f0 + c + e];
+  }
+  qz[lane] = acc * qs[lane];
+}
+
+// z_next = r z + (column sums of K~) by 256 threads t: 256 / KP adjacent
+// threads per feature, each adding eight of scale_rows' partial sums, then
+// combined by lane exchanges
+template <int KP>
+__device__ __forceinline__ void z_update(float* zn, const float* zs, const float* part, float r,
+                                         int t) {
+  constexpr int TPF = 256 / KP, PER = RowItems<KP>::PARTS / TPF;
+  static_assert(PER == 8, "eight partial sums per thread");
+  const int f = t / TPF, sub = t % TPF;
+  float s = 0.f;
+#pragma unroll
+  for (int p = 0; p < PER; ++p) s += part[(sub * PER + p) * KP + f];
+#pragma unroll
+  for (int off = 1; off < TPF; off <<= 1) s += __shfl_xor(s, off);
+  if (sub == 0) zn[f] = zs[f] * r + s;
+}
 
 // EXT (one F tile of a split feature dimension): den and delta are not
 // formed from this tile's features but read from den_out / delta_out, where
@@ -166,7 +198,9 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
   float* lgs = reinterpret_cast<float*>(smem + Cfg::OFF_LG);
   float* qs = reinterpret_cast<float*>(smem + Cfg::OFF_QS);
   float* ks = reinterpret_cast<float*>(smem + Cfg::OFF_KS);
-  float* zs = reinterpret_cast<float*>(smem + Cfg::OFF_Z);
+  // z entering chunk n in zb + FP (n & 1): the update for chunk n + 1 is
+  // written while phase 3 still reads chunk n's
+  float* zb = reinterpret_cast<float*>(smem + Cfg::OFF_Z);
   float* zp = reinterpret_cast<float*>(smem + Cfg::OFF_ZP);
   float* rdec = reinterpret_cast<float*>(smem + Cfg::OFF_R);
 
@@ -223,7 +257,7 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
       for (int r = 0; r < 16; ++r) St[i][r] = st[f * DP + dt * 32 + acc_row(r, h)];
     }
   }
-  for (int f = tid; f < FP; f += B_THREADS) zs[f] = st ? st[FP * DP + f] : 0.f;
+  for (int f = tid; f < FP; f += B_THREADS) zb[FP * (n0 & 1) + f] = st ? st[FP * DP + f] : 0.f;
   // bf16 S [f][d] for the X jobs (4 consecutive d per store)
   auto publish = [&]() __attribute__((always_inline)) {
     if constexpr (!SREG) {
@@ -284,6 +318,7 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
   auto step = [&](auto set, int n) __attribute__((always_inline)) {
     constexpr int S = decltype(set)::value;
     const int t0 = n * C;
+    const float* zs = zb + FP * (n & 1);
     // waves 0-3 load the chunk after next now, waves 4-7 once their phase-1
     // work is done: issued together, the later waves' loads waited for free
     // slots in the CU's memory queue and held back their phase-1 work
@@ -296,19 +331,12 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
         ra[kt * 64 + qi] = 0.f;
         rav[kt * 64 + qi] = 0.f;
       }
-      // qs (fq . z) by quarters of the features; query = lane
-      constexpr int FQ = FP / 4;
+      // qs (fq . z) over the first two quarters of the features (all four
+      // at FP = 256, where two more partial sums in den made the kernel spill
+      // registers); query = lane
 #pragma unroll
-      for (int w4 = 0; w4 < 4; ++w4) {
-        float acc = 0.f;
-#pragma unroll
-        for (int c = 0; c < FQ; c += 8) {
-          const bf16x8 x = *reinterpret_cast<const bf16x8*>(fq_l + lane * PF + w4 * FQ + c);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) acc += to_f32(x[e]) * zs[w4 * FQ + c + e];
-        }
-        qz[w4 * 64 + lane] = acc * qs[lane];
-      }
+      for (int q4 = 0; q4 < (FP >= 256 ? 4 : 2); ++q4)
+        qz_part<FP / 4>(fq_l, PF, zs, qs, qz + 64 * q4, lane, q4 * (FP / 4));
     } else if (scorer) {
       f32x16 aT = mfma_chain<FP / 16, PIPE>(
           zero16(), [&](int kb) { return row_operand(fk_l, PF, kt * 32 + col, 16 * kb, h); },
@@ -340,9 +368,20 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
     } else {
       // K~ = bf16(fk ks) once per chunk (the forward's rounding), with its
       // column sums for z
-      uint4 kti[RowItems<FP>::N];
-      scale_rows_t<FP>(fk_l, PF, ks, kti, zp, tid - 256);
-      store_rows_t<FP>(kti, kt_l, PF, tid - 256);
+      {
+        uint4 kti[RowItems<FP>::N];
+        scale_rows_t<FP>(fk_l, PF, ks, kti, zp, tid - 256);
+        store_rows_t<FP>(kti, kt_l, PF, tid - 256);
+      }
+      // qs (fq . z) over an eighth of the features (the last two quarters; at
+      // FP = 32 waves 4 and 5 take a quarter each; none at FP = 256)
+      constexpr int NE = FP >= 64 ? FP / 8 : 8;
+      if constexpr (FP < 256) {
+        if (const int f0 = FP / 2 + (wave - 4) * NE; f0 < FP)
+          qz_part<NE>(fq_l, PF, zs, qs, qz + 64 * (wave - 2), lane, f0);
+        else
+          qz[64 * (wave - 2) + lane] = 0.f;
+      }
     }
     // X = S dy^T for this wave's jobs, and qs fq . X per query
     f32x16 X[Cfg::XJ];
@@ -385,6 +424,7 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
         delta = ok ? delta_out[offL + t0 + qi] : 0.f;
       } else {
         den = ra[qi] + ra[64 + qi] + qz[qi] + qz[64 + qi] + qz[128 + qi] + qz[192 + qi];
+        if constexpr (FP < 256) den += qz[256 + qi] + qz[320 + qi];
         float num = rav[qi] + rav[64 + qi];
 #pragma unroll
         for (int ft = 0; ft < NFT; ++ft) num += nx[ft * 64 + qi];
@@ -406,9 +446,11 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
         }
       }
     }
+    // z entering chunk n + 1, by waves 4-7, which have no phase-2 work
+    const float r_n = rdec[0];
+    if (tid >= 256) z_update<FP>(zb + FP * ((n + 1) & 1), zs, zp, r_n, tid - 256);
     __syncthreads();
     // ---- phase 3: dfq and fq . dfq for the X jobs; S^T update ------------------
-    const float r_n = rdec[0];
 #pragma unroll
     for (int j = 0; j < Cfg::XJ; ++j) {
       int ft, hq;
@@ -454,7 +496,7 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
       }
     }
     __syncthreads();
-    // ---- next chunk into LDS; z update; fq . dfq of this chunk; publish S ---------
+    // ---- next chunk into LDS; fq . dfq of this chunk; publish S --------------------
     if (wave == PW && t0 + lane < L) {
       float s = 0.f;
 #pragma unroll
@@ -462,7 +504,6 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
       p_out[offL + t0 + lane] = s;
     }
     if (n + 1 < n1) stage(std::integral_constant<int, (S + 1) % DEPTH>{});
-    if (const int f = tid - (B_THREADS - FP); f >= 0) zs[f] = zs[f] * r_n + sum_parts<FP>(zp, f);
     publish();
     __syncthreads();
   };
