@@ -32,7 +32,8 @@
 //      through LDS transpose reads); writes dv, dfk and dG.
 //   gate: d log_gamma = reverse cumsum of dG over L (head-summed for a
 //      per-token gate), one launch (gla_gate_grad_kernel) from dG and the
-//      per-chunk dG totals kernel B writes.
+//      per-chunk dG totals kernel B writes; with a per-head gate and G = 1
+//      kernel B, whose reverse walk sees the whole row, writes it instead.
 // Operand staging follows gla_fwd.hip: row-major tiles in LDS, operands that
 // contract over tokens from LDS transpose reads, next chunk prefetched into
 // registers.
@@ -753,7 +754,8 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
     const float* __restrict__ log_gamma, const bf16* __restrict__ dy,
     const float* __restrict__ den_in, const float* __restrict__ delta_in,
     const float* __restrict__ p_in, OutT* __restrict__ dfk, OutT* __restrict__ dv,
-    float* __restrict__ dG, float* __restrict__ csum, const float* __restrict__ seg_state, int H,
+    float* __restrict__ dG, float* __restrict__ csum, float* __restrict__ dlg_direct,
+    const float* __restrict__ seg_state, int H,
     int L, int F, int D, int gate_per_head, int G, int cps, int M, int KG, int xper, int nxcd,
     int nblk) {
   using Cfg = BwdB<FP, DP>;
@@ -872,6 +874,9 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
   // dz partial sums instead, as threads a = 0 .. 127 (dY^ is shared by all)
   const bool stager = kt == 1 && qt == 0;
   const int a = (kind << 6) + lane;
+  // with dlg_direct (a per-head gate, one segment: this walk sees all of its
+  // row), d log_gamma is written here; dlg_after sums dG of the chunks walked
+  float dlg_after = 0.f;
   // chunk n is in LDS and register set `set` is free; the next set holds chunk n-1
   auto step = [&](auto set, int n) __attribute__((always_inline)) {
     constexpr int S = decltype(set)::value;
@@ -1046,11 +1051,18 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
 #pragma unroll
         for (int ft = 0; ft < NFT; ++ft) s += pk[ft * 64 + lane];
         g = ps[64 * cur + lane] - s;
-        dG[offL + t0 + lane] = g;
+        if (!dlg_direct) dG[offL + t0 + lane] = g;
       }
+      if (dlg_direct) {
+        // d log_gamma of this chunk: the chunks after it are already summed
+        const float suf = wave_suffix_sum(g, lane);
+        if (t0 + lane < L) dlg_direct[offL + t0 + lane] = dlg_after + suf;
+        dlg_after += __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(suf)));
+      } else {
 #pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) g += __shfl_xor(g, off);
-      if (lane == 0) csum[(size_t)bh * NT + n] = g;
+        for (int off = 32; off >= 1; off >>= 1) g += __shfl_xor(g, off);
+        if (lane == 0) csum[(size_t)bh * NT + n] = g;
+      }
     }
     publish();
     if (n - 1 >= n0) stage(std::integral_constant<int, (S + 1) % DEPTH>{}, n - 1);
@@ -1189,14 +1201,18 @@ static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if ((e = launch_gla_segment_scan(rseg, rlam, BH, G, SEG, true, st)) != hipSuccess) return e;
   }
+  // a per-head gate in one segment: the reverse walk of (b, h) sees its whole
+  // gate row and writes d log_gamma itself (no gate launch, no dG)
+  const bool direct_dlg = gate_per_head && G == 1;
   auto kb = gla_bwd_dkv_kernel<FP, DP, OutT, VEC>;
   if ((e = ensure_lds<gla_bwd_dkv_kernel<FP, DP, OutT, VEC>>(LDS_B)) != hipSuccess) return e;
   hipLaunchKernelGGL(kb, dim3(wg.grid), dim3(B_THREADS), LDS_B, st, (const bf16*)fq,
                      (const bf16*)fk, (const bf16*)v, lg, (const bf16*)dy, (const float*)den,
                      (const float*)delta, (const float*)p, (OutT*)dfk, (OutT*)dv, dG, csum,
-                     (const float*)rseg, H, L, F, D, gate_per_head, G, cps, M, KG, wg.per, wg.nx,
-                     wg.nblk);
+                     direct_dlg ? dlg : nullptr, (const float*)rseg, H, L, F, D, gate_per_head, G,
+                     cps, M, KG, wg.per, wg.nx, wg.nblk);
   if ((e = hipGetLastError()) != hipSuccess) return e;
+  if (direct_dlg) return hipSuccess;
   const int nt = (L + GLA_C - 1) / GLA_C;
   const dim3 ggrid((nt + GATE_CHUNKS_PER_WG - 1) / GATE_CHUNKS_PER_WG,
                    gate_rows(B, H, gate_per_head));

@@ -224,6 +224,14 @@ __device__ __forceinline__ float wave_prefix_sum(float x) {
   return x;
 }
 
+// Inclusive suffix sum over the 64 lanes of a wave (lane l gets the sum of
+// lanes l .. 63): the prefix sum of the lane-reversed values, reversed back.
+__device__ __forceinline__ float wave_suffix_sum(float x, int lane) {
+  x = __shfl(x, 63 - lane);
+  x = wave_prefix_sum(x);
+  return __shfl(x, 63 - lane);
+}
+
 // Chunk-local inclusive scan of the gate by one wave (lane = token): lg,
 // e^{lg}, e^{lg_end - lg}, and e^{lg_end}, lg_end in r[0], r[1].
 __device__ __forceinline__ void gate_scan(float g, int lane, float* lgs, float* qs, float* ks,
