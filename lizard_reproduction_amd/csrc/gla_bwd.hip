@@ -1084,11 +1084,12 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
 // ============================================================================
 // d log_gamma[row, j] = sum_{j' >= j} value[row, j'], value = dG of that (b, h)
 // row (per-head gate) or its sum over the heads (per-token gate).  One wave
-// per (row, 64-token chunk), four chunks per workgroup, no barriers: the wave
-// sums the chunk totals of dG the reverse walk left for every later chunk
-// (lanes over (head, chunk) pairs, then a shuffle tree), and lane t holds
-// token t of the chunk summed over the heads for an inclusive suffix scan by
-// shuffles.  Fixed order throughout.
+// per (row, 64-token chunk), four chunks per workgroup, no barriers.  Lane t
+// holds token t of the chunk summed over the heads; the chunk totals of the
+// later chunks (lanes over chunks, summed over the heads) come in alongside.
+// Loads go out in batches of 16 buffer loads (zero past the end) so one
+// memory round trip covers 16 heads; the sums over lanes are DPP scans.  Fixed
+// order throughout.
 // ============================================================================
 constexpr int GATE_CHUNKS_PER_WG = 4;
 
@@ -1100,26 +1101,30 @@ __global__ __launch_bounds__(64 * GATE_CHUNKS_PER_WG) void gla_gate_grad_kernel(
   const int c = blockIdx.x * GATE_CHUNKS_PER_WG + (threadIdx.x >> 6);
   if (c >= NT) return;   // whole waves; nothing below synchronises across waves
   const int nsum = gate_per_head ? 1 : H;
-  const float* src = dG + (size_t)row * nsum * L;
-  const float* cs = csum + (size_t)row * nsum * NT;
-  const int nc = NT - c - 1;   // chunks after this one
-  float after = 0.f;
-#pragma unroll 4
-  for (int idx = lane; idx < nc * nsum; idx += 64)
-    after += cs[(size_t)(idx / nc) * NT + c + 1 + idx % nc];
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) after += __shfl_xor(after, off);
+  const rsrc_t src = make_rsrc(dG + (size_t)row * nsum * L, (size_t)nsum * L * 4);
+  const rsrc_t cs = make_rsrc(csum + (size_t)row * nsum * NT, (size_t)nsum * NT * 4);
   const int j = c * GLA_C + lane;
-  float val = 0.f;
-  if (j < L) {
-#pragma unroll 8
-    for (int hh = 0; hh < nsum; ++hh) val += src[(size_t)hh * L + j];
-  }
+  constexpr int BATCH = 16;
+  float val = 0.f, after = 0.f;
+  for (int h0 = 0; h0 < nsum; h0 += BATCH) {
+    float x[BATCH];
 #pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {   // inclusive suffix scan over the chunk
-    const float o = __shfl_down(val, off);
-    if (lane + off < 64) val += o;
+    for (int k = 0; k < BATCH; ++k)
+      x[k] = bload_f32(src, (h0 + k < nsum && j < L) ? (uint32_t)((h0 + k) * L + j) * 4u : OOB);
+    for (int c2 = c + 1 + lane; c2 - lane < NT; c2 += 64) {
+      float y[BATCH];
+#pragma unroll
+      for (int k = 0; k < BATCH; ++k)
+        y[k] = bload_f32(cs, (h0 + k < nsum && c2 < NT) ? (uint32_t)((h0 + k) * NT + c2) * 4u : OOB);
+#pragma unroll
+      for (int k = 0; k < BATCH; ++k) after += y[k];
+    }
+#pragma unroll
+    for (int k = 0; k < BATCH; ++k) val += x[k];
   }
+  after = wave_prefix_sum(after);
+  after = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(after), 63));
+  val = wave_suffix_sum(val, lane);   // inclusive suffix sum over the chunk
   if (j < L) dlg[(size_t)row * L + j] = after + val;
 }
 
