@@ -241,7 +241,9 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
       hq = j & 1;
       return true;
     } else {
-      const int job = (wave + 4) & 7;   // waves 4-7 take jobs 0-3
+      // waves 4-7 take jobs 0-3; the two waves of a SIMD (w, w + 4) take
+      // opposite query halves, whose phase-3 products differ in number
+      const int job = ((wave + 4) & 7) ^ (wave >> 2);
       ft = job >> 1;
       hq = job & 1;
       return job < 2 * NFT;
@@ -1010,7 +1012,9 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
     // ---- dfk jobs (f-tile, key half), from the published dS^T -----------------
 #pragma unroll
     for (int i = 0; i < Cfg::DFK_OWN; ++i) {
-      const int job = wave + B_WAVES * i;
+      // the other key half than this wave's dv job: a SIMD's two waves then
+      // carry one short (keys 32-63) and one long job of each kind
+      const int job = (wave ^ 1) + B_WAVES * i;
       if (job < Cfg::DFK_JOBS) {
         const int ft = job >> 1, hk = job & 1;
         const int key = hk * 32 + col;
