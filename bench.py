@@ -14,7 +14,9 @@ average is also the kernel's average duration, the basis of ``roofline``.
 Beside it (``extra``), each timed as the median of per-iteration HIP events
 after warm-up, like triton.testing.do_bench(return_mode="median") in the
 reference (src/benchmark.py:57-66):
-  * GLA fwd+bwd at the headline shape (grads reset each iteration);
+  * GLA fwd+bwd at the headline shape (grads reset each iteration; median
+    of 100 after 1 s of untimed fwd+bwd and 10 warm-ups, as the forward
+    settles below);
   * BASELINE config 2, GLA fwd and fwd+bwd at the training shape (B=1, H=32,
     L=2048, d=64, per-token gate logsigmoid(N(3,1)));
   * BASELINE config 3, SWA fwd and fwd+bwd (B=1, H=32, L=2048, d=64, W=64,
@@ -568,13 +570,18 @@ def profile_workload(torch, kernels, name, steps, settle_s):
         return {"config5_layer": layer_stack(torch, steps, 1, one_layer=True, decode=False)}
     else:
         raise SystemExit(f"unknown --only workload {name!r}")
-    t_end = time.perf_counter() + settle_s
+    settle(torch, run, reset, settle_s)
+    t = median_ms(torch, run, steps, 3, reset)
+    return {name: {"fwd_bwd_ms": round(t, 4), "steps": steps}}
+
+
+def settle(torch, run, reset, seconds):
+    """Run a fwd+bwd untimed for `seconds` of wall time (steady clocks)."""
+    t_end = time.perf_counter() + seconds
     while time.perf_counter() < t_end:
         run()
         reset()
         torch.cuda.synchronize()
-    t = median_ms(torch, run, steps, 3, reset)
-    return {name: {"fwd_bwd_ms": round(t, 4), "steps": steps}}
 
 
 def main():
@@ -634,9 +641,9 @@ def main():
               flush=True)
         return
 
-    iters = 50
     run, reset = fwd_bwd_fn(torch, kernels.gla, (fq, fk, v, lg), dy)
-    t = median_ms(torch, run, iters, 5, reset)
+    settle(torch, run, reset, 0.5 * args.settle_seconds)
+    t = median_ms(torch, run, 100, 10, reset)
     f = gla_fwd_bwd_flops(B * H, L, D, D)
     fbb = gla_fwd_bwd_bytes(B * H, L, D, D, True)
     extra["headline_gla_fwd_bwd"] = {
