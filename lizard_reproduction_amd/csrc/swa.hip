@@ -207,7 +207,13 @@ constexpr int swa_bwd_occupancy() {
 // backward, query side: delta (first pass over the window keys), dq (second
 // pass), and this block's partial of dmeta
 // ----------------------------------------------------------------------------
-template <int DP, typename OutT, bool VEC>
+// RES: the window's key tiles (at most SWA_RES of them) stay in LDS, one slot
+// each: pass 0 streams them in with one barrier per tile, pass 1 reads them
+// back with no loads and no barriers.  Otherwise both passes stream the tiles
+// through one k and one v buffer.
+constexpr int SWA_RES = 4;
+
+template <int DP, typename OutT, bool VEC, bool RES>
 __global__ __launch_bounds__(256, (swa_bwd_occupancy<DP>())) void swa_bwd_dq_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ meta, int n_meta, const float* __restrict__ lse,
@@ -216,10 +222,12 @@ __global__ __launch_bounds__(256, (swa_bwd_occupancy<DP>())) void swa_bwd_dq_ker
     int KG) {
   using Cfg = SwaCfg<DP>;
   constexpr int P = Cfg::P;
+  constexpr int NSLOT = RES ? SWA_RES : 1;
   extern __shared__ __align__(16) char smem[];
-  bf16* k_l = reinterpret_cast<bf16*>(smem);
-  bf16* v_l = reinterpret_cast<bf16*>(smem + Cfg::TILE_BYTES);
-  float* red = reinterpret_cast<float*>(smem + 2 * Cfg::TILE_BYTES);   // [4][SWA_META_BLOCK]
+  // k tile of slot i at smem + i TILE_BYTES, v tile at smem + (NSLOT + i) TILE_BYTES
+  auto kslot = [&](int i) { return reinterpret_cast<bf16*>(smem + i * Cfg::TILE_BYTES); };
+  auto vslot = [&](int i) { return reinterpret_cast<bf16*>(smem + (NSLOT + i) * Cfg::TILE_BYTES); };
+  float* red = reinterpret_cast<float*>(smem + 2 * NSLOT * Cfg::TILE_BYTES);   // [4][SWA_META_BLOCK]
 
   const int nqb = (L + SWA_ROWS - 1) / SWA_ROWS;
   const int lb = xcd_block(blockIdx.x, per, nx);
@@ -244,59 +252,90 @@ __global__ __launch_bounds__(256, (swa_bwd_occupancy<DP>())) void swa_bwd_dq_ker
 #pragma unroll
   for (int t = 0; t < DP / 32; ++t) dqa[t] = zero16();
 
+  // the work of one key tile (keys t0 .. t0+63 in k_l, v_l): pass 0 adds to
+  // delta = sum_t p dp, pass 1 forms ds and adds ds k to dq
+  auto tile = [&](int pass, const bf16* k_l, const bf16* v_l, int t0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const int k0 = t0 + 32 * half;
+      if (!blocks_meet(q0, k0, L, W)) continue;
+      f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+      for (int kb = 0; kb < DP / 16; ++kb) {
+        s = mfma(row_operand(k_l, P, 32 * half + col, 16 * kb, h), qreg[kb], s);
+        dp = mfma(row_operand(v_l, P, 32 * half + col, 16 * kb, h), dyreg[kb], dp);
+      }
+      if (pass == 0) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float p = in_window(qi, k0 + acc_row(r, h), W) ? fexp(s[r] * scale - lse_i) : 0.f;
+          delta += p * dp[r];
+        }
+      } else {
+        bf16x8 ds[2];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float p = in_window(qi, k0 + acc_row(r, h), W) ? fexp(s[r] * scale - lse_i) : 0.f;
+          ds[r >> 3][r & 7] = to_bf16(p * (dp[r] - delta));
+        }
+#pragma unroll
+        for (int t = 0; t < DP / 32; ++t)
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+            dqa[t] = mfma(tr_operand(k_l, P, 32 * half + 16 * kb, t * 32, lane), ds[kb], dqa[t]);
+      }
+    }
+  };
+
   uint4 rk[Cfg::NL], rv[Cfg::NL];
-  // pass 0 accumulates delta = sum_t p dp; pass 1 forms ds and dq
-  for (int pass = 0; pass < 2; ++pass) {
+  if constexpr (RES) {
+    const int nt = (khi - klo + SWA_TILE - 1) / SWA_TILE;   // <= SWA_RES (the launcher's test)
     swa_load<DP>(rk, k + kvbase, klo, L, d, vec);
     swa_load<DP>(rv, v + kvbase, klo, L, d, vec);
+    swa_store<DP>(rk, kslot(0));
+    swa_store<DP>(rv, vslot(0));
     __syncthreads();
-    swa_store<DP>(rk, k_l);
-    swa_store<DP>(rv, v_l);
-    __syncthreads();
-    for (int t0 = klo; t0 < khi; t0 += SWA_TILE) {
-      const bool more = t0 + SWA_TILE < khi;
+    for (int i = 0; i < nt; ++i) {
+      const int t0 = klo + i * SWA_TILE;
+      const bool more = i + 1 < nt;
       if (more) {
         swa_load<DP>(rk, k + kvbase, t0 + SWA_TILE, L, d, vec);
         swa_load<DP>(rv, v + kvbase, t0 + SWA_TILE, L, d, vec);
       }
-#pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        const int k0 = t0 + 32 * half;
-        if (!blocks_meet(q0, k0, L, W)) continue;
-        f32x16 s = zero16(), dp = zero16();
-#pragma unroll
-        for (int kb = 0; kb < DP / 16; ++kb) {
-          s = mfma(row_operand(k_l, P, 32 * half + col, 16 * kb, h), qreg[kb], s);
-          dp = mfma(row_operand(v_l, P, 32 * half + col, 16 * kb, h), dyreg[kb], dp);
-        }
-        if (pass == 0) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float p = in_window(qi, k0 + acc_row(r, h), W) ? fexp(s[r] * scale - lse_i) : 0.f;
-            delta += p * dp[r];
-          }
-        } else {
-          bf16x8 ds[2];
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float p = in_window(qi, k0 + acc_row(r, h), W) ? fexp(s[r] * scale - lse_i) : 0.f;
-            ds[r >> 3][r & 7] = to_bf16(p * (dp[r] - delta));
-          }
-#pragma unroll
-          for (int t = 0; t < DP / 32; ++t)
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-              dqa[t] = mfma(tr_operand(k_l, P, 32 * half + 16 * kb, t * 32, lane), ds[kb], dqa[t]);
-        }
-      }
-      if (more) {
-        __syncthreads();
-        swa_store<DP>(rk, k_l);
-        swa_store<DP>(rv, v_l);
+      tile(0, kslot(i), vslot(i), t0);
+      if (more) {   // slot i + 1 is not read before this barrier
+        swa_store<DP>(rk, kslot(i + 1));
+        swa_store<DP>(rv, vslot(i + 1));
         __syncthreads();
       }
     }
-    if (pass == 0) delta += xhalf(delta);
+    delta += xhalf(delta);
+    for (int i = 0; i < nt; ++i) tile(1, kslot(i), vslot(i), klo + i * SWA_TILE);
+  } else {
+    // pass 0 accumulates delta = sum_t p dp; pass 1 forms ds and dq
+    for (int pass = 0; pass < 2; ++pass) {
+      swa_load<DP>(rk, k + kvbase, klo, L, d, vec);
+      swa_load<DP>(rv, v + kvbase, klo, L, d, vec);
+      __syncthreads();
+      swa_store<DP>(rk, kslot(0));
+      swa_store<DP>(rv, vslot(0));
+      __syncthreads();
+      for (int t0 = klo; t0 < khi; t0 += SWA_TILE) {
+        const bool more = t0 + SWA_TILE < khi;
+        if (more) {
+          swa_load<DP>(rk, k + kvbase, t0 + SWA_TILE, L, d, vec);
+          swa_load<DP>(rv, v + kvbase, t0 + SWA_TILE, L, d, vec);
+        }
+        tile(pass, kslot(0), vslot(0), t0);
+        if (more) {
+          __syncthreads();
+          swa_store<DP>(rk, kslot(0));
+          swa_store<DP>(rv, vslot(0));
+          __syncthreads();
+        }
+      }
+      if (pass == 0) delta += xhalf(delta);
+    }
   }
 #pragma unroll
   for (int t = 0; t < DP / 32; ++t) store_acc_row<OutT>(dq + base, qi, t * 32, L, d, vec, dqa[t], scale, h);
@@ -502,13 +541,27 @@ static hipError_t launch_swa_bwd_t(const void* q, const void* k, const void* v, 
                                    hipStream_t st) {
   int per, grid, nx;
   swa_grid(BH, L, &per, &grid, &nx);
-  const size_t lds_q = 2 * SwaCfg<DP>::TILE_BYTES + 4 * SWA_META_BLOCK * sizeof(float);
-  auto kq = swa_bwd_dq_kernel<DP, OutT, VEC>;
-  hipError_t e = ensure_lds<swa_bwd_dq_kernel<DP, OutT, VEC>>((int)lds_q);
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(kq, dim3(grid), dim3(256), lds_q, st, (const bf16*)q, (const bf16*)k,
-                     (const bf16*)v, meta, n_meta, lse, (const bf16*)dy, (OutT*)dq, delta,
-                     dmeta_part, BH, L, d, W, scale, per, nx, KG);
+  // the window's key tiles fit the LDS slots of the resident form when a
+  // block's keys span at most SWA_RES tiles: klo >= Q0 - W - 62, khi <= Q0 +
+  // SWA_ROWS, so SWA_ROWS + W + 62 <= SWA_RES * SWA_TILE; and at d <= 64,
+  // where the slots leave the kernel's workgroups per CU in place
+  const bool res = DP <= 64 && SWA_ROWS + W + 62 <= SWA_RES * SWA_TILE;
+  hipError_t e;
+  const size_t lds_q = 2 * (res ? SWA_RES : 1) * SwaCfg<DP>::TILE_BYTES +
+                       4 * SWA_META_BLOCK * sizeof(float);
+  if (res) {
+    if ((e = ensure_lds<swa_bwd_dq_kernel<DP, OutT, VEC, true>>((int)lds_q)) != hipSuccess) return e;
+    hipLaunchKernelGGL((swa_bwd_dq_kernel<DP, OutT, VEC, true>), dim3(grid), dim3(256), lds_q, st,
+                       (const bf16*)q, (const bf16*)k, (const bf16*)v, meta, n_meta, lse,
+                       (const bf16*)dy, (OutT*)dq, delta, dmeta_part, BH, L, d, W, scale, per, nx,
+                       KG);
+  } else {
+    if ((e = ensure_lds<swa_bwd_dq_kernel<DP, OutT, VEC, false>>((int)lds_q)) != hipSuccess) return e;
+    hipLaunchKernelGGL((swa_bwd_dq_kernel<DP, OutT, VEC, false>), dim3(grid), dim3(256), lds_q, st,
+                       (const bf16*)q, (const bf16*)k, (const bf16*)v, meta, n_meta, lse,
+                       (const bf16*)dy, (OutT*)dq, delta, dmeta_part, BH, L, d, W, scale, per, nx,
+                       KG);
+  }
   if ((e = hipGetLastError()) != hipSuccess) return e;
   const size_t lds_k = 2 * SwaCfg<DP>::TILE_BYTES + 2 * SWA_TILE * sizeof(float);
   auto kk = swa_bwd_dkv_kernel<DP, OutT, VEC>;

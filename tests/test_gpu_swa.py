@@ -17,9 +17,12 @@ pytestmark = pytest.mark.gpu
 SMALL = ((16, 16), (16, 16))
 
 
+# W = 66 is the widest window whose key tiles the dq kernel keeps resident in
+# LDS (at d <= 64); W = 67 streams them twice
 @pytest.mark.parametrize("length, window, blocks", [(1, 8, SMALL), (77, 32, SMALL),
                                                     (150, 128, None), (300, 64, None),
-                                                    (130, 1, None), (97, 200, None)])
+                                                    (130, 1, None), (97, 200, None),
+                                                    (333, 66, None), (333, 67, None)])
 def test_swa_matches_oracle(length, window, blocks):
     inputs = swa_inputs(length)
     blocks = blocks or (kernels.FWD_BLOCKS, kernels.BWD_BLOCKS)
