@@ -85,8 +85,8 @@ __device__ __forceinline__ void store_tile8(const uint4 (&reg)[N], bf16* tile, i
 //            the decay, sum_t a and sum_t a (v . dy) (the tile of keys 32-63 x
 //            queries 0-31 is causally zero: its wave forms half of Q~ . z
 //            instead); waves 4-7: the other half of Q~ . z, K~ = bf16(fk ks)
-//            with its column sums; X jobs (f-tile,
-//            query half): X = S dy^T and qs fq . X, waves 4-7 first;
+//            with its column sums; X jobs (f-tile, query half): X = S dy^T
+//            and qs fq . X, waves 4-7 first;
 //   phase 2  waves 0-3: den, delta, dad fragments; waves 4-7: the z update;
 //   phase 3  X jobs: dfq and fq . dfq; S^T tiles: S^T <- r S^T + V^T K~;
 //   tail     p, next chunk, publish S.
@@ -281,7 +281,8 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
   };
 
   // per-chunk single-wave work goes to waves whose tail is otherwise light:
-  // the gate to wave 3, fq . dfq to wave 2, the z update to the last FP threads
+  // the gate to wave 3, fq . dfq to wave 2 (the z update runs in phase 2, on
+  // waves 4-7)
   constexpr int GW = 3, PW = 2;
   // DEPTH register sets: while chunk n computes, chunks n+1 .. n+DEPTH are in flight
   constexpr int DEPTH = Cfg::DEPTH;
@@ -322,9 +323,9 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
     constexpr int S = decltype(set)::value;
     const int t0 = n * C;
     const float* zs = zb + FP * (n & 1);
-    // waves 0-3 load the chunk after next now, waves 4-7 once their phase-1
-    // work is done: issued together, the later waves' loads waited for free
-    // slots in the CU's memory queue and held back their phase-1 work
+    // waves 0-3 load the next chunk now, waves 4-7 once their phase-1 work is
+    // done: issued together, the later waves' loads waited for free slots in
+    // the CU's memory queue and held back their phase-1 work
     if (wave < 4) issue(set, n + DEPTH);
     // ---- phase 1 ---------------------------------------------------------------
     f32x16 vdy = zero16();
@@ -888,9 +889,9 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
     const float* delsc = dels + 64 * cur;
     const float* qhc = qh + 64 * cur;
     const float* dwc = dw + 64 * cur;
-    // waves 0-3 load the chunk after next now, waves 4-7 once their phase-1
-    // work is done: issued together, the later waves' loads waited for free
-    // slots in the CU's memory queue and held back their phase-1 products
+    // waves 0-3 load the next chunk of the walk now, waves 4-7 once their
+    // phase-1 work is done: issued together, the later waves' loads waited for
+    // free slots in the CU's memory queue and held back their phase-1 products
     if (wave < 4) issue(set, n - DEPTH);
     // ---- phase 1: one 32x32 tile (queries x keys) of s or dy v^T per wave ----
     if (!stager) {
