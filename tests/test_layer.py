@@ -262,3 +262,31 @@ def test_layer_takes_any_even_head_dim_up_to_the_swa_limit():
     assert not hip_layer.prologue_supported(128, 128, bf16=False)
     assert hip_layer.prologue_supported(128, 64, bf16=False)
     assert not hip_layer.prologue_supported(96, 16)
+
+
+def test_rounding_model_of_the_layer_sweep_without_rounding_is_the_oracle_layer():
+    """The GPU layer sweep bounds cancelling gradients by what bf16 kernel
+    operands alone do, from a restatement of the oracle layer with optional
+    rounding; unrounded it must give lo.lizard_layer's gradients exactly, and
+    rounded it must move them (the rounding is really applied)."""
+    import types
+    from tests.test_gpu_random_shapes import _rounded_layer_grads
+    case = dict(heads=4, kv=2, window=5)
+    cfg = types.SimpleNamespace(hidden_size=4 * 24, num_attention_heads=4, num_key_value_heads=2)
+    torch.manual_seed(0)
+    layer = hip_layer.LizardAttention(cfg, 0, window=5, num_meta=3, feature_dim=12)
+    with torch.no_grad():
+        for p in layer.parameters():
+            p.normal_(0, 0.3)
+    g = torch.Generator().manual_seed(1)
+    x, grad = torch.randn(2, 30, 96, generator=g), torch.randn(2, 30, 96, generator=g)
+    cos, sin = (t.float()[None].expand(2, 30, 24) for t in lo.rope_cos_sin(30, 24))
+    params = {n: p.detach().double().requires_grad_() for n, p in layer.named_parameters()}
+    xd = x.double().requires_grad_()
+    lo.lizard_layer(params, xd, cos.double(), sin.double(), 4, 2, 5).backward(grad.double())
+    plain = _rounded_layer_grads(layer, x, grad, cos, sin, case, False)
+    rounded = _rounded_layer_grads(layer, x, grad, cos, sin, case, True)
+    assert rel_err(plain["dx"], xd.grad) < EXACT
+    for name, p in params.items():
+        assert rel_err(plain[name], p.grad) < EXACT, name
+        assert rel_err(rounded[name], p.grad) > 1e-5, name
