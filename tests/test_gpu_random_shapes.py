@@ -263,3 +263,80 @@ def _rounded_layer_grads(layer, x, grad, cos, sin, case, rnd):
     grads = {n: p.grad for n, p in params.items()}
     grads["dx"] = xd.grad
     return grads
+
+
+def _decode_cases(n, seed=77):
+    rng = random.Random(seed)
+    cases = []
+    for _ in range(n):
+        heads = rng.choice([1, 2, 4])
+        cases.append(dict(
+            batch=rng.choice([1, 2, 3]), heads=heads,
+            kv=rng.choice([d for d in (1, 2, 4) if heads % d == 0]),
+            prefix=rng.choice([0, 1, 63, 64, 65, rng.randint(2, 300)]), steps=rng.randint(1, 24),
+            features=rng.choice([4, 8, 24, 32, 64, 100, 128, 256]),
+            dim=rng.choice([4, 20, 32, 64, 72, 128]), per_head=rng.random() < 0.5,
+            window=rng.choice([1, 3, 16, 64, 100]), sinks=rng.choice([0, 1, 4, 9]),
+            seed=rng.randint(0, 10 ** 6)))
+    return cases
+
+
+DECODE_CASES = _decode_cases(16)
+
+
+@pytest.mark.parametrize("case", DECODE_CASES, ids=[_label(c) for c in DECODE_CASES])
+def test_decode_random_shape_continues_the_oracle(case):
+    """Prefill on a drawn prefix, then one decode step per token, for GLA
+    (kv-head k-side operands, either gate) and SWA (ring cache of the drawn
+    window, any sink count): every step's output against the oracle's row of
+    the whole sequence (GLA: the recurrent form in fp64 on the same bf16
+    inputs; SWA: the dense sliding-window softmax), and the final GLA state
+    against the recurrent form's."""
+    g = torch.Generator().manual_seed(case["seed"])
+    b, h, kv = case["batch"], case["heads"], case["kv"]
+    n, prefix, nf, nd = case["prefix"] + case["steps"], case["prefix"], case["features"], case["dim"]
+    group = h // kv
+    fq = torch.randn(b, h, n, nf, generator=g).softmax(-1).bfloat16()
+    fk = torch.randn(b, kv, n, nf, generator=g).softmax(-1).bfloat16()
+    v = torch.randn(b, kv, n, nd, generator=g).bfloat16()
+    lg = F.logsigmoid(2 * torch.randn(*((b, h, n) if case["per_head"] else (b, n)), generator=g)
+                      + 2)
+    dev = [t.cuda() for t in (fq, fk, v, lg)]
+    if prefix:
+        _, state = kernels.gla_prefill(dev[0][:, :, :prefix],
+                                       dev[1][:, :, :prefix].repeat_interleave(group, 1),
+                                       dev[2][:, :, :prefix].repeat_interleave(group, 1),
+                                       dev[3][..., :prefix])
+    else:
+        state = kernels.new_state(b, h, nf, nd, "cuda")
+    ys = [kernels.gla_decode_step(dev[0][:, :, i], dev[1][:, :, i], dev[2][:, :, i],
+                                  dev[3][..., i], state) for i in range(prefix, n)]
+    out, S, zs = lo.gla_recurrent_state(fq.double(), fk.double().repeat_interleave(group, 1),
+                                        v.double().repeat_interleave(group, 1),
+                                        torch.exp(lg.double()))
+    S_k, z_k = kernels.split_state(state, nf, nd)
+
+    # SWA on the same heads: q from fq's shape class, its own draws
+    d, w = nd, case["window"]
+    q = torch.randn(b, h, n, d, generator=g).bfloat16()
+    k = torch.randn(b, kv, n, d, generator=g).bfloat16()
+    sv = torch.randn(b, kv, n, d, generator=g).bfloat16()
+    meta = torch.randn(case["sinks"], generator=g)
+    expected = lo.swa_kernel_api(q, k.repeat_interleave(group, 1), sv.repeat_interleave(group, 1),
+                                 meta, w, torch.float64)
+    qd, kd, vd, md = q.cuda(), k.cuda(), sv.cuda(), meta.cuda()
+    kc = torch.zeros(b, kv, w, d, device="cuda", dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    rows = []
+    for p in range(n):
+        kc[:, :, p % w] = kd[:, :, p]
+        vc[:, :, p % w] = vd[:, :, p]
+        if p >= prefix:
+            rows.append(kernels.swa_decode_step(qd[:, :, p], kc, vc, md, p))
+    torch.cuda.synchronize()
+    errs = {"gla_y": max_rel(torch.stack(ys, dim=2), out[:, :, prefix:]),
+            "S": max_rel(S_k, S), "z": max_rel(z_k, zs),
+            "swa_y": max_rel(torch.stack(rows, dim=2), expected[:, :, prefix:])}
+    print(f"[parity] decode {_label(case)}: " + " ".join(f"{k}={x:.2e}" for k, x in errs.items()),
+          flush=True)
+    assert max(errs.values()) <= OUT_TOL, (case, errs)
