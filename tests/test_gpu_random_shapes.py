@@ -340,3 +340,73 @@ def test_decode_random_shape_continues_the_oracle(case):
     print(f"[parity] decode {_label(case)}: " + " ".join(f"{k}={x:.2e}" for k, x in errs.items()),
           flush=True)
     assert max(errs.values()) <= OUT_TOL, (case, errs)
+
+
+def _segmented_cases(n, seed=8192):
+    rng = random.Random(seed)
+    cases = []
+    for _ in range(n):
+        features, dim = rng.choice([(64, 64), (128, 128), (256, 64), (32, 128), (128, 32),
+                                    (100, 72), (256, 40)])
+        cases.append(dict(
+            batch=rng.choice([1, 2, 4]), heads=rng.choice([1, 3, 8, 32, 100]),
+            length=rng.randint(65, 5000), features=features, dim=dim,
+            per_head=rng.random() < 0.5, seed=rng.randint(0, 10 ** 6)))
+    return cases
+
+
+SEGMENTED_CASES = _segmented_cases(12)
+
+
+@pytest.mark.parametrize("case", SEGMENTED_CASES, ids=[_label(c) for c in SEGMENTED_CASES])
+def test_gla_random_segmented_walks_match_chunked_oracle(case):
+    """Mid-size GLA fwd+bwd where B*H is too small to fill the GPU, so each
+    sequence is cut into segments (state pass, scans, walks with several
+    chunks per segment, a ragged last one; F > 128 doubles the split): three
+    sampled (b, h) slices of the output and of dfq, dfk, dv, and the gate
+    gradient (per head, or for a per-token gate summed over all heads of one
+    batch row), against the chunked fp64 oracle with autograd.  Inputs as in
+    softplus features, N(0,1) values, logsigmoid(N(2,1.5))
+    gates."""
+    g = torch.Generator().manual_seed(case["seed"])
+    b, h, length, nf, nd = (case[k] for k in ("batch", "heads", "length", "features", "dim"))
+    fq = F.softplus(torch.randn(b, h, length, nf, generator=g)).bfloat16()
+    fk = F.softplus(torch.randn(b, h, length, nf, generator=g)).bfloat16()
+    v = torch.randn(b, h, length, nd, generator=g).bfloat16()
+    lg = F.logsigmoid(2 + 1.5 * torch.randn(*((b, h, length) if case["per_head"] else (b, length)),
+                                            generator=g))
+    dy = torch.randn(b, h, length, nd, generator=g).bfloat16()
+    ours = [t.cuda().requires_grad_() for t in (fq, fk, v, lg)]
+    y = kernels.gla(*ours)
+    y.backward(dy.cuda())
+    torch.cuda.synchronize()
+    rb, rh = case["seed"] % b, case["seed"] % h
+    slices = sorted({(0, 0), (b - 1, h - 1), (rb, rh)})
+    worst = {}
+
+    def oracle(bi, hi):
+        sl = [t[bi:bi + 1, hi:hi + 1].double().requires_grad_() for t in (fq, fk, v)]
+        gate = (lg[bi:bi + 1, hi:hi + 1] if case["per_head"] else lg[bi:bi + 1]).double() \
+            .requires_grad_()
+        ref = lo.gla_chunked(*sl, gate, 64)
+        ref.backward(dy[bi:bi + 1, hi:hi + 1].double())
+        return ref, sl, gate
+
+    for bi, hi in slices:
+        ref, sl, gate = oracle(bi, hi)
+        pairs = {"y": (y[bi, hi], ref[0, 0]), "dfq": (ours[0].grad[bi, hi], sl[0].grad[0, 0]),
+                 "dfk": (ours[1].grad[bi, hi], sl[1].grad[0, 0]),
+                 "dv": (ours[2].grad[bi, hi], sl[2].grad[0, 0])}
+        if case["per_head"]:
+            pairs["dlg"] = (ours[3].grad[bi, hi], gate.grad[0, 0])
+        for k, (a, r) in pairs.items():
+            worst[k] = max(worst.get(k, 0.0), max_rel(a, r))
+    if not case["per_head"] and h <= 8:   # the shared gate's gradient sums every head's share
+        total = sum(oracle(rb, hi)[2].grad[0] for hi in range(h))
+        worst["dlg_shared"] = max_rel(ours[3].grad[rb], total)
+    print(f"[parity] segmented {_label(case)} slices {slices}: " +
+          " ".join(f"{k}={x:.2e}" for k, x in worst.items()), flush=True)
+    assert worst["y"] <= OUT_TOL, (case, worst)
+    for k, e in worst.items():
+        if k != "y":
+            assert e <= GRAD_TOL, (case, k, worst)
