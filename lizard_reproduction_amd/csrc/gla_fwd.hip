@@ -777,7 +777,39 @@ struct GlaState {
   static_assert(BYTES <= 80 * 1024, "LDS budget: two workgroups per CU");
 };
 
-template <int FP, int DP, bool VEC>
+// Columns [0, ncols) of chunk rows t0 .. t0 + 63 of a row-major bf16 matrix
+// whose rows are `stride` elements apart, behind a buffer of `bytes` bytes from
+// `base` (rows past it read zeros); the item layout of load_chunk.
+template <int KP, int N>
+__device__ __forceinline__ void load_chunk_strided(uint4 (&reg)[N], const bf16* __restrict__ base,
+                                                   size_t bytes, int t0, int stride, int ncols,
+                                                   bool vec) {
+  constexpr int K8 = KP / 8;
+  const rsrc_t r = make_rsrc(base, bytes);
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const int idx = threadIdx.x + 256 * i;
+    const int row = t0 + idx / K8, c = (idx % K8) * 8;
+    if (vec) {
+      reg[i] = bload16(r, c < ncols ? (uint32_t)(row * stride + c) * 2u : OOB);
+    } else {
+      bf16x8 x;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t off = c + e < ncols ? (uint32_t)(row * stride + c + e) * 2u : OOB;
+        x[e] = __builtin_bit_cast(bf16, __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
+      }
+      reg[i] = __builtin_bit_cast(uint4, x);
+    }
+  }
+}
+
+// FR: the record's padded feature count.  FP < FR splits the state's feature
+// rows over FR / FP workgroups per segment: row f of S and z[f] depend only on
+// column f of fk, so each takes its slice of fk's columns (and all of v) and
+// writes its rows of the record.  Used when the segments alone leave most of
+// the GPU idle (few kv heads with a shared gate).
+template <int FP, int DP, bool VEC, int FR>
 __global__ __launch_bounds__(256, 2) void gla_fwd_state_kernel(
     const bf16* __restrict__ fk, const bf16* __restrict__ v, const float* __restrict__ log_gamma,
     float* __restrict__ seg_state, float* __restrict__ seg_logdecay, int H, int L, int F, int D,
@@ -797,14 +829,27 @@ __global__ __launch_bounds__(256, 2) void gla_fwd_state_kernel(
   float* zp = reinterpret_cast<float*>(smem + Cfg::OFF_ZP);
   float* rdec = reinterpret_cast<float*>(smem + Cfg::OFF_R);
 
-  const int bh = blockIdx.x / (G - 1), seg = blockIdx.x % (G - 1);
+  constexpr int NFS = FR / FP;
+  static_assert(FR % FP == 0, "feature slices divide the record");
+  const int fs = NFS > 1 ? (int)(blockIdx.x % NFS) : 0, f0 = fs * FP;
+  const int blk = NFS > 1 ? (int)(blockIdx.x / NFS) : (int)blockIdx.x;
+  const int bh = blk / (G - 1), seg = blk % (G - 1);
   const int n0 = seg * cps, n1 = n0 + cps;   // segments before the last are full
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int col = lane & 31, h = lane >> 5;
   const bool vecF = VEC || (F & 7) == 0, vecD = VEC || (D & 7) == 0;
-  const bf16* fkb = fk + (size_t)(bh / KG) * L * F;
+  // this workgroup's columns f0 .. f0 + FP - 1 of fk (rows F apart)
+  const bf16* fkb = fk + (size_t)(bh / KG) * L * F + f0;
+  const size_t fk_bytes = ((size_t)L * F - f0) * 2;
+  const int fcols = F - f0;   // valid columns from f0 (<= 0: none, the slice is zero)
   const bf16* vb = v + (size_t)(bh / KG) * L * D;
   const float* lgb = log_gamma + (size_t)(gate_per_head ? bh : bh / H) * L;
+  auto load_fk = [&](uint4 (&reg)[Cfg::NLF], int t) {
+    if constexpr (NFS == 1)
+      load_chunk<FP>(reg, fkb, t, L, F, vecF);
+    else
+      load_chunk_strided<FP>(reg, fkb, fk_bytes, t, F, fcols, vecF);
+  };
 
   f32x16 S[TPW];
 #pragma unroll
@@ -838,14 +883,31 @@ __global__ __launch_bounds__(256, 2) void gla_fwd_state_kernel(
       }
       *reinterpret_cast<bf16x8*>(fk_l + t * PF + 8 * cg) = o;
     }
-    float* dst = part + r0 * FP + 8 * cg;
-    *reinterpret_cast<f32x4*>(dst) = f32x4{sum[0], sum[1], sum[2], sum[3]};
-    *reinterpret_cast<f32x4*>(dst + 4) = f32x4{sum[4], sum[5], sum[6], sum[7]};
+    if constexpr (NFS == 1) {
+      float* dst = part + r0 * FP + 8 * cg;
+      *reinterpret_cast<f32x4*>(dst) = f32x4{sum[0], sum[1], sum[2], sum[3]};
+      *reinterpret_cast<f32x4*>(dst + 4) = f32x4{sum[4], sum[5], sum[6], sum[7]};
+    }
+  };
+  // A feature slice (NFS > 1) sums the staged chunk's K~ columns for z in the
+  // order the FR-wide layout does (RowItems<FR>: partial p over rows p, p + RS,
+  // p + 2 RS, ..., then the partials in turn), so that a record's bits do not
+  // depend on how its rows were split.
+  using RR = RowItems<FR>;
+  static_assert(RR::PARTS * FP <= 2048, "a slice's partial sums fit one parity of zp");
+  auto slice_parts = [&](float* part) {
+    for (int task = tid; task < RR::PARTS * FP; task += 256) {
+      const int p = task / FP, c = task % FP;
+      float q = 0.f;
+#pragma unroll
+      for (int i = 0; i < RR::N; ++i) q += to_f32(fk_l[(p + RR::RSTRIDE * i) * PF + c]);
+      part[p * FP + c] = q;
+    }
   };
 
   uint4 rk[Cfg::NLF], rv[Cfg::NLD];
   float rg = gate_at(lgb, n0 * C + lane, L);   // the gate first: waited for alone
-  load_chunk<FP>(rk, fkb, n0 * C, L, F, vecF);
+  load_fk(rk, n0 * C);
   load_chunk<DP>(rv, vb, n0 * C, L, D, vecD);
   {
     const int pb = n0 & 1;
@@ -864,7 +926,7 @@ __global__ __launch_bounds__(256, 2) void gla_fwd_state_kernel(
     // traffic), so the scan below waits for the gate alone
     const int tn = more ? t0 + C : L;
     rg = gate_at(lgb, tn + lane, L);
-    load_chunk<FP>(rk, fkb, tn, L, F, vecF);
+    load_fk(rk, tn);
     load_chunk<DP>(rv, vb, tn, L, D, vecD);
     __builtin_amdgcn_s_setprio(0);
     const float r_n = rdec[4 * pc];
@@ -882,30 +944,38 @@ __global__ __launch_bounds__(256, 2) void gla_fwd_state_kernel(
                       tr_operand(v_l, PD, 16 * kb, dt * 32, lane), S[i]);
       }
     }
+    if constexpr (NFS > 1) slice_parts(zp + 2048 * pc);
     if (more && wave == 0)
       gate_scan(rg, lane, lgs + 64 * pn, qs + 64 * pn, ks + 64 * pn, rdec + 4 * pn);
     __syncthreads();
     // staging and the next loads at raised wave priority, as in the walk
     __builtin_amdgcn_s_setprio(1);
-    if (tid < FP) zs[tid] = zs[tid] * r_n + sum_parts<FP>(zp + 2048 * pc, tid);
+    if constexpr (NFS == 1) {
+      if (tid < FP) zs[tid] = zs[tid] * r_n + sum_parts<FP>(zp + 2048 * pc, tid);
+    } else if (tid < FP) {
+      float zc = 0.f;
+      for (int p = 0; p < RR::PARTS; ++p) zc += zp[2048 * pc + p * FP + tid];
+      zs[tid] = zs[tid] * r_n + zc;
+    }
     if (more) {
       stage_scaled(rk, ks + 64 * pn, zp + 2048 * pn);
       store_chunk<DP>(rv, v_l, PD);
     }
     __syncthreads();
   }
-  float* out = seg_state + ((size_t)bh * G + seg) * Cfg::SEG;
+  float* out = seg_state + ((size_t)bh * G + seg) * SegRec<FR, DP>::SIZE;
 #pragma unroll
   for (int i = 0; i < TPW; ++i) {
     const int ti = wave + 4 * i;
     if (ti < NTILE) {
       const int ft = ti / NDT, dt = ti % NDT;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) out[(ft * 32 + acc_row(r, h)) * DP + dt * 32 + col] = S[i][r];
+      for (int r = 0; r < 16; ++r)
+        out[(f0 + ft * 32 + acc_row(r, h)) * DP + dt * 32 + col] = S[i][r];
     }
   }
-  for (int f = tid; f < FP; f += 256) out[FP * DP + f] = zs[f];
-  if (tid == 0) seg_logdecay[(size_t)bh * G + seg] = lam;
+  for (int f = tid; f < FP; f += 256) out[FR * DP + f0 + f] = zs[f];
+  if (tid == 0 && fs == 0) seg_logdecay[(size_t)bh * G + seg] = lam;
 }
 
 // ----------------------------------------------------------------------------
@@ -1008,25 +1078,66 @@ hipError_t launch_gla_segment_scan(float* seg_state, const float* seg_logdecay, 
   return hipGetLastError();
 }
 
+// the state pass with the record's FR feature rows in slices of FS per workgroup
+template <int FS, int FR, int DP, bool VEC>
+static hipError_t launch_state_slices(const void* fk, const void* v, const float* lg,
+                                      float* seg_state, float* seg_logdecay, int BH, int H, int L,
+                                      int F, int D, int gate_per_head, int G, int cps, int KG,
+                                      hipStream_t st) {
+  using Cfg = GlaState<FS, DP>;
+  auto ks = gla_fwd_state_kernel<FS, DP, VEC, FR>;
+  hipError_t e = ensure_lds<gla_fwd_state_kernel<FS, DP, VEC, FR>>(Cfg::BYTES);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(ks, dim3(BH * (G - 1) * (FR / FS)), dim3(256), Cfg::BYTES, st,
+                     (const bf16*)fk, (const bf16*)v, lg, seg_state, seg_logdecay, H, L, F, D,
+                     gate_per_head, G, cps, KG);
+  return hipGetLastError();
+}
+
+// Feature slices per segment: doubled while the state pass would still fill
+// at most half of the GPU's two workgroups per CU, down to 64 features.
+static int gla_state_slices(int workgroups, int FP) {
+  int n = 1;
+  while (n < FP / 64 && workgroups * n * 2 <= gla_target_wg()) n *= 2;
+  return n;
+}
+
 template <int FP, int DP, bool VEC>
 static hipError_t launch_gla_fwd_states_t(const void* fk, const void* v, const float* lg,
                                           float* seg_state, float* seg_logdecay, int BH, int H,
                                           int L, int F, int D, int gate_per_head, int G, int cps,
                                           int KG, hipStream_t st) {
-  using Cfg = GlaState<FP, DP>;
   if (!gate_per_head && KG > 1) {   // one record per kv head (seg_owner)
     BH /= KG;
     H /= KG;
     KG = 1;
   }
-  auto ks = gla_fwd_state_kernel<FP, DP, VEC>;
-  hipError_t e = ensure_lds<gla_fwd_state_kernel<FP, DP, VEC>>(Cfg::BYTES);
+  const int nfs = gla_state_slices(BH * (G - 1), FP);
+  hipError_t e;
+  if constexpr (FP == 256) {
+    if (nfs == 4)
+      e = launch_state_slices<64, FP, DP, VEC>(fk, v, lg, seg_state, seg_logdecay, BH, H, L, F,
+                                               D, gate_per_head, G, cps, KG, st);
+    else if (nfs == 2)
+      e = launch_state_slices<128, FP, DP, VEC>(fk, v, lg, seg_state, seg_logdecay, BH, H, L, F,
+                                                D, gate_per_head, G, cps, KG, st);
+    else
+      e = launch_state_slices<FP, FP, DP, VEC>(fk, v, lg, seg_state, seg_logdecay, BH, H, L, F,
+                                               D, gate_per_head, G, cps, KG, st);
+  } else if constexpr (FP == 128) {
+    if (nfs == 2)
+      e = launch_state_slices<64, FP, DP, VEC>(fk, v, lg, seg_state, seg_logdecay, BH, H, L, F,
+                                               D, gate_per_head, G, cps, KG, st);
+    else
+      e = launch_state_slices<FP, FP, DP, VEC>(fk, v, lg, seg_state, seg_logdecay, BH, H, L, F,
+                                               D, gate_per_head, G, cps, KG, st);
+  } else {
+    e = launch_state_slices<FP, FP, DP, VEC>(fk, v, lg, seg_state, seg_logdecay, BH, H, L, F, D,
+                                             gate_per_head, G, cps, KG, st);
+  }
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(ks, dim3(BH * (G - 1)), dim3(256), Cfg::BYTES, st, (const bf16*)fk,
-                     (const bf16*)v, lg, seg_state, seg_logdecay, H, L, F, D, gate_per_head, G, cps,
-                     KG);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
-  return launch_gla_segment_scan(seg_state, seg_logdecay, BH, G, Cfg::SEG, false, st);
+  return launch_gla_segment_scan(seg_state, seg_logdecay, BH, G, SegRec<FP, DP>::SIZE, false,
+                                 st);
 }
 
 hipError_t launch_gla_fwd_states(const void* fk, const void* v, const float* lg, float* seg_state,
@@ -1101,7 +1212,19 @@ static hipError_t prepare_fwd_t() {
   else
     e = ensure_lds<gla_fwd_kernel<FP, DP, VEC, false>>(GlaFwd<FP, DP>::BYTES);
   if (e != hipSuccess) return e;
-  return ensure_lds<gla_fwd_state_kernel<FP, DP, VEC>>(GlaState<FP, DP>::BYTES);
+  if constexpr (FP == 256) {   // the feature-sliced state passes
+    if ((e = ensure_lds<gla_fwd_state_kernel<64, DP, VEC, FP>>(GlaState<64, DP>::BYTES)) !=
+        hipSuccess)
+      return e;
+    if ((e = ensure_lds<gla_fwd_state_kernel<128, DP, VEC, FP>>(GlaState<128, DP>::BYTES)) !=
+        hipSuccess)
+      return e;
+  } else if constexpr (FP == 128) {
+    if ((e = ensure_lds<gla_fwd_state_kernel<64, DP, VEC, FP>>(GlaState<64, DP>::BYTES)) !=
+        hipSuccess)
+      return e;
+  }
+  return ensure_lds<gla_fwd_state_kernel<FP, DP, VEC, FP>>(GlaState<FP, DP>::BYTES);
 }
 
 hipError_t gla_fwd_prepare() {

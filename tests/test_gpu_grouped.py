@@ -20,6 +20,9 @@ def _expand(t, group):
     (2, 8, 2, 300, 64, 64, True),      # segmented walks (B*H small)
     (2, 8, 2, 300, 64, 64, False),     # segmented, per-token gate: records per kv head
     (1, 32, 8, 777, 256, 64, False),   # the layer's wide features, two segments per walk
+    # per-token gate, F = 128: the kv-head records' state pass splits its feature
+    # rows over two workgroups (120 segments), the expanded one does not (480)
+    (1, 32, 8, 2048, 128, 128, False),
     (16, 32, 8, 130, 128, 128, True),  # B*H fills the GPU: one walk per (b, h)
     (1, 8, 2, 300, 256, 128, False),   # past the walks' sizes: two D tiles
     (1, 4, 2, 200, 512, 64, True),     # two F tiles (summed raw numerators)
