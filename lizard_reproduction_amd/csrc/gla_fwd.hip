@@ -840,8 +840,8 @@ __global__ __launch_bounds__(256, 2) void gla_fwd_state_kernel(
   const bool vecF = VEC || (F & 7) == 0, vecD = VEC || (D & 7) == 0;
   // this workgroup's columns f0 .. f0 + FP - 1 of fk (rows F apart)
   const bf16* fkb = fk + (size_t)(bh / KG) * L * F + f0;
-  const size_t fk_bytes = ((size_t)L * F - f0) * 2;
   const int fcols = F - f0;   // valid columns from f0 (<= 0: none, the slice is zero)
+  const size_t fk_bytes = fcols > 0 ? ((size_t)L * F - f0) * 2 : 0;
   const bf16* vb = v + (size_t)(bh / KG) * L * D;
   const float* lgb = log_gamma + (size_t)(gate_per_head ? bh : bh / H) * L;
   auto load_fk = [&](uint4 (&reg)[Cfg::NLF], int t) {

@@ -138,6 +138,16 @@ def test_gla_segments_of_several_chunks(length):
     compare(gla_kernel(64), gla_reference, inputs, grad, label=f"segments L={length}")
 
 
+@pytest.mark.parametrize("features", [150, 200])
+def test_gla_state_pass_feature_slices_with_ragged_features(features):
+    # B*H = 2 and F in (128, 256]: the segment state pass splits the record's
+    # 256 feature rows over 4 workgroups of 64; at F = 150 the third slice
+    # holds 22 columns of fk and the fourth none (its record rows stay zero)
+    inputs = gla_inputs(700, batch=1, heads=2, features=features, dim=64, seed=9)
+    grad = torch.randn(inputs[2].shape, generator=torch.Generator().manual_seed(1))
+    compare(gla_kernel(64), gla_reference, inputs, grad, label=f"sliced state pass F={features}")
+
+
 @pytest.mark.parametrize("batch, heads, length, dim, per_head", [
     (1, 2, 64 * 11 + 5, 64, True), (2, 3, 64 * 9, 32, False), (1, 1, 1, 64, False)])
 def test_gla_wide_features_segments(batch, heads, length, dim, per_head):
