@@ -85,8 +85,11 @@ int lz_gla_fwd(const void* fq, const void* fk, const void* v, const float* log_g
 /*
  * GLA forward that allocates nothing and takes no workspace.  No counterpart
  * in the reference: it is for callers that cannot allocate device memory
- * (code under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc).  Same arguments, result and kernels as lz_gla_fwd without the
+ * (tight serving loops, harnesses that forbid hipMalloc).  Capturing it into
+ * a HIP graph is untested: the one capture this library's path ever ran (a
+ * whole fwd+bwd through the Python API) crashed the host process in the
+ * runtime's capture end, and that crash has no known cause, so capture is
+ * not recommended.  Same arguments, result and kernels as lz_gla_fwd without the
  * workspace, at the walks' own sizes (nf <= 256, nd <= 128, nd <= 64 when
  * nf > 128): the per-segment states that lz_gla_fwd keeps in
  * its workspace (when B*H alone cannot fill the GPU) live in a static device
@@ -105,12 +108,14 @@ int lz_gla_fwd_noalloc(const void* fq, const void* fk, const void* v, const floa
 
 /*
  * Set-up of lz_gla_fwd_noalloc on the current device, once per device: the
- * device address of its static array, and the LDS limits
- * (hipFuncSetAttribute) of every kernel it can launch.  No counterpart in the
- * reference.  lz_gla_fwd_noalloc makes the same set-up on its first call on a
- * device; callers that capture that call into a HIP graph call lz_init first,
- * outside the capture, so that the captured call makes no runtime call but
- * its kernel launches.  Returns 0 or an error code (lz_last_error).
+ * device address of its static array (hipGetSymbolAddress), and the LDS
+ * limits (hipFuncSetAttribute) of every kernel it can launch.  No
+ * counterpart in the reference.  lz_gla_fwd_noalloc makes the same set-up on
+ * its first call on a device.  After it, a call of lz_gla_fwd_noalloc still
+ * makes these runtime calls besides its kernel launches: hipGetDevice (to
+ * find the device's array and set-up), the device attribute queries of its
+ * first call on a device (CU and XCD counts), and hipGetLastError after the
+ * launches.  Returns 0 or an error code (lz_last_error).
  */
 int lz_init(void);
 

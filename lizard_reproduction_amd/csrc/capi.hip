@@ -277,8 +277,9 @@ static int scratch_address(float** out) {
 // The no-allocation forward's set-up on the current device, once per device:
 // the scratch array's address and the LDS limits of the kernels it launches
 // (hipFuncSetAttribute, which the other entry points make on their first
-// launch of each kernel).  Made eagerly by lz_init, a later call under HIP
-// graph capture makes no runtime call but its kernel launches.
+// launch of each kernel).  lz_init makes it eagerly.  Each call still makes
+// hipGetDevice calls here and in device_geom, and hipGetLastError after its
+// launches.
 static int noalloc_setup(float** ws) {
   if (int rc = scratch_address(ws)) return rc;
   constexpr int MAXDEV = 64;

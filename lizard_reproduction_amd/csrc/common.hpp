@@ -239,6 +239,25 @@ __device__ __forceinline__ bf16x8 tr_operand(const bf16* tile, int pitch, int ro
   return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
+// tr_operand with the tile's rows scaled by scale[row] and rounded to bf16
+// in registers: lane l's slots hold rows row0 + 4h + {0..3} and
+// row0 + 8 + 4h + {0..3}, so their scales are two 16-byte reads (row0 % 4 == 0
+// and a 16-byte aligned `scale` keep them aligned).
+__device__ __forceinline__ bf16x8 tr_operand_scaled(const bf16* tile, int pitch, int row0,
+                                                    int col0, int lane, const float* scale) {
+  const bf16x8 x = tr_operand(tile, pitch, row0, col0, lane);
+  const int h = lane >> 5;
+  const f32x4 s0 = *reinterpret_cast<const f32x4*>(scale + row0 + 4 * h);
+  const f32x4 s1 = *reinterpret_cast<const f32x4*>(scale + row0 + 8 + 4 * h);
+  bf16x8 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    o[e] = to_bf16(to_f32(x[e]) * s0[e]);
+    o[4 + e] = to_bf16(to_f32(x[4 + e]) * s1[e]);
+  }
+  return o;
+}
+
 // acc + sum_{k < K} A(k) B(k) on the MFMA as a software pipeline: the
 // operands of product k + P are read (from LDS) before product k issues.
 // Written product by product, the compiler gives the operands one register

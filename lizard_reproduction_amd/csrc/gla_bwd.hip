@@ -11,7 +11,7 @@
 //   dfq_i   = sum_t dad_it fk_t + (qs_i/den_i) (dy_i S_n^T - delta_i z_n)
 //   dfk_t   = sum_i dad_it fq_i + ks_t (v_t dS^T - dz)
 //   dv_t    = sum_i (a_it/den_i) dy_i + ks_t (fk_t dS)
-//   dS <- r_n dS + fq_n^T dY^_n,  dY^_i = bf16(dy_i qs_i / den_i)   (after chunk n)
+//   dS <- r_n dS + Q^_n^T dy_n,  Q^_i = bf16(fq_i qs_i / den_i)   (after chunk n)
 //   dz <- r_n dz + sum_i fq_i (qs_i delta_i / den_i)
 //   dG_j    = fq_j . dfq_j - fk_j . dfk_j,  d log_gamma = reverse cumsum of dG
 //             (summed over heads for a per-token gate)
@@ -579,8 +579,7 @@ struct BwdS : BwdCommon<FP, DP> {
   static constexpr int C = B_::C, PF = B_::PF, PD = B_::PD;
   static constexpr int OFF_FQ = 0;
   static constexpr int OFF_DY = OFF_FQ + C * PF * 2;
-  static constexpr int OFF_DYH = OFF_DY + C * PD * 2;     // dY^ = bf16(qh dy)
-  static constexpr int OFF_LG = OFF_DYH + C * PD * 2;
+  static constexpr int OFF_LG = OFF_DY + C * PD * 2;
   static constexpr int OFF_QS = OFF_LG + 64 * 4;
   static constexpr int OFF_KS = OFF_QS + 64 * 4;
   static constexpr int OFF_INV = OFF_KS + 64 * 4;
@@ -606,7 +605,6 @@ __global__ __launch_bounds__(256, 2) void gla_bwd_state_kernel(
   extern __shared__ __align__(16) char smem[];
   bf16* fq_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_FQ);
   bf16* dy_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_DY);
-  bf16* dyh_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_DYH);
   float* lgs = reinterpret_cast<float*>(smem + Cfg::OFF_LG);
   float* qs = reinterpret_cast<float*>(smem + Cfg::OFF_QS);
   float* ks = reinterpret_cast<float*>(smem + Cfg::OFF_KS);
@@ -633,7 +631,7 @@ __global__ __launch_bounds__(256, 2) void gla_bwd_state_kernel(
   for (int f = tid; f < FP; f += 256) dzs[f] = 0.f;
   float lam = 0.f;
 
-  uint4 rq[Cfg::NLF], rd[Cfg::NLD], rh[RowItems<DP>::N];
+  uint4 rq[Cfg::NLF], rd[Cfg::NLD];
   TokScalars sc;
   load_chunk<FP>(rq, fq + offF, (n1 - 1) * C, L, F, vecF);
   load_chunk<DP>(rd, dy + offD, (n1 - 1) * C, L, D, vecD);
@@ -651,24 +649,34 @@ __global__ __launch_bounds__(256, 2) void gla_bwd_state_kernel(
       load_chunk<DP>(rd, dy + offD, (n - 1) * C, L, D, vecD);
       sc = load_scalars(lgb, den_in, delta_in, nullptr, offL, (n - 1) * C + lane, L);
     }
-    // dY^ = bf16(qh dy), formed once per chunk; dz partials sum_i fq_i (qh_i delta_i)
-    scale_rows_only<DP>(dy_l, PD, qh, rh);
-    store_rows<DP>(rh, dyh_l, PD);
+    // dz partials sum_i fq_i (qh_i delta_i)
     column_sums<FP, false>(fq_l, PF, dw, dzp);
     __syncthreads();
     const float r_n = rdec[0];
     if (wave == 0) lam += rdec[1];
+    // dS += Q^T dy, Q^ = bf16(qh fq) formed in registers.  Tile ti = wave + 4 i
+    // has f-tile ti % NFT: one f-tile for all of a wave's tiles when NFT
+    // divides 4, two (i even, i odd) when NFT = 8, so the scaled operands are
+    // formed once per f-tile
+    constexpr int NQF = NFT <= 4 ? 1 : 2;
+    static_assert(NFT <= 8 && (NFT <= 4 || NFT % 4 == 0), "state pass f-tiles");
+    bf16x8 qf[NQF][4];
+#pragma unroll
+    for (int j = 0; j < NQF; ++j)
+      if (wave + 4 * j < NTILE)
+#pragma unroll
+        for (int qb = 0; qb < 4; ++qb)
+          qf[j][qb] = tr_operand_scaled(fq_l, PF, 16 * qb, ((wave + 4 * j) % NFT) * 32, lane, qh);
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
       const int ti = wave + 4 * i;
       if (ti < NTILE) {
-        const int ft = ti / NDT, dt = ti % NDT;
+        const int dt = ti / NFT;
 #pragma unroll
         for (int r = 0; r < 16; ++r) dS[i][r] *= r_n;
 #pragma unroll
-        for (int qb = 0; qb < 4; ++qb)   // dS += fq^T dY^
-          dS[i] = mfma(tr_operand(fq_l, PF, 16 * qb, ft * 32, lane),
-                       tr_operand(dyh_l, PD, 16 * qb, dt * 32, lane), dS[i]);
+        for (int qb = 0; qb < 4; ++qb)
+          dS[i] = mfma(qf[i % NQF][qb], tr_operand(dy_l, PD, 16 * qb, dt * 32, lane), dS[i]);
       }
     }
     __syncthreads();
@@ -687,7 +695,7 @@ __global__ __launch_bounds__(256, 2) void gla_bwd_state_kernel(
   for (int i = 0; i < TPW; ++i) {
     const int ti = wave + 4 * i;
     if (ti < NTILE) {
-      const int ft = ti / NDT, dt = ti % NDT;
+      const int ft = ti % NFT, dt = ti / NFT;
 #pragma unroll
       for (int r = 0; r < 16; ++r) out[(ft * 32 + acc_row(r, h)) * DP + dt * 32 + col] = dS[i][r];
     }
@@ -704,11 +712,13 @@ __global__ __launch_bounds__(256, 2) void gla_bwd_state_kernel(
 //   phase 1  wave (kind, qt, kt): kind 0 the score tile s -> a/den, kind 1 the
 //            dy.v^T tile -> dad (both need only their own tile).  The tiles of
 //            keys 32-63 x queries 0-31 are causally zero: their two waves
-//            form dY^ = bf16(qh dy) and the dz partials instead, and the
-//            phase-2 products skip those zero fragments;
+//            form the dz partials instead, and the phase-2 products skip
+//            those zero fragments;
 //   phase 2  dv jobs (d-tile, key half) contract dS over f from the published
 //            bf16 dS^T tile; dS tiles (f-tile, d-tile) are spread over the
-//            waves' accumulators and updated with fq^T dY^; dfk jobs
+//            waves' accumulators and updated with Q^T dy, Q^ = bf16(qh fq)
+//            formed in registers from fq's transpose reads (the reference
+//            rounds the same operand, src/kernels/gla.py:104-132); dfk jobs
 //            (f-tile, key half) contract dS^T over d;
 //   tail     dG, publish dS^T, stage the prefetched chunk, dz update.
 // ============================================================================
@@ -730,8 +740,7 @@ struct BwdB : BwdCommon<FP, DP> {
   static constexpr int OFF_FK = OFF_FQ + C * PF * 2;
   static constexpr int OFF_V = OFF_FK + C * PF * 2;
   static constexpr int OFF_DY = OFF_V + C * PD * 2;
-  static constexpr int OFF_DYH = OFF_DY + C * PD * 2;     // dY^ = bf16(qh dy)
-  static constexpr int OFF_DST = OFF_DYH + C * PD * 2;    // dS^T [DP][PF] bf16
+  static constexpr int OFF_DST = OFF_DY + C * PD * 2;     // dS^T [DP][PF] bf16
   static constexpr int OFF_FA = OFF_DST + DP * PF * 2;    // a/den fragments [2 kt][4 qb][64]
   static constexpr int OFF_FD = OFF_FA + 2 * 4 * 64 * 16; // dad fragments
   static constexpr int OFF_PK = OFF_FD + 2 * 4 * 64 * 16; // [NFT][64] fk . dfk partials
@@ -769,7 +778,6 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
   bf16* fk_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_FK);
   bf16* v_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_V);
   bf16* dy_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_DY);
-  bf16* dyh_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_DYH);
   bf16* dst_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_DST);
   bf16x8* fa = reinterpret_cast<bf16x8*>(smem + Cfg::OFF_FA);
   bf16x8* fd = reinterpret_cast<bf16x8*>(smem + Cfg::OFF_FD);
@@ -874,7 +882,7 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
   const int kind = wave >> 2, qt = (wave >> 1) & 1, kt = wave & 1;   // phase-1 tile
   const int ki = kt * 32 + col;                                       // its key (lane)
   // waves 1 and 5 hold the causally zero tiles (kt = 1, qt = 0): they form the
-  // dz partial sums instead, as threads a = 0 .. 127 (dY^ is shared by all)
+  // dz partial sums instead, as threads a = 0 .. 127
   const bool stager = kt == 1 && qt == 0;
   const int a = (kind << 6) + lane;
   // with dlg_direct (a per-head gate, one segment: this walk sees all of its
@@ -942,15 +950,6 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
       frag[(kt * 4 + qt * 2 + 0) * 64 + lane] = o8[0];
       frag[(kt * 4 + qt * 2 + 1) * 64 + lane] = o8[1];
     }
-    // dY^ = bf16(qh dy), once per chunk, for dS += fq^T dY^, by all threads
-    {
-      constexpr int K8 = DP / 8;
-      for (int idx = tid; idx < C * K8; idx += B_THREADS) {
-        const int t = idx / K8, c8 = 8 * (idx % K8);
-        const bf16x8 x = *reinterpret_cast<const bf16x8*>(dy_l + t * PD + c8);
-        *reinterpret_cast<bf16x8*>(dyh_l + t * PD + c8) = scale8(x, qhc[t]);
-      }
-    }
     // dz partials: part p sums fq_t (qh_t delta_t) over tokens [8 p, 8 p + 8)
     {
       constexpr int K8 = FP / 8;
@@ -997,17 +996,27 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
         store_acc_row<OutT>(dv + offD, t0 + key, dt * 32, L, D, vecD, g, 1.f, h);
       }
     }
-    // dS <- r_n dS + fq^T dY^ for the owned tiles
+    // dS <- r_n dS + Q^T dy for the owned tiles, Q^ = bf16(qh fq): the owned
+    // tiles t = wave + 8 i share the f-tile wave % NFT (8 is a multiple of
+    // NFT), so its four scaled operands are formed once per chunk
+    static_assert(B_WAVES % NFT == 0, "owned dS tiles share one f-tile");
+    if (wave < NFT * NDT) {
+      const int ft = wave % NFT;
+      bf16x8 qf[4];
 #pragma unroll
-    for (int i = 0; i < Cfg::S_OWN; ++i) {
-      const int t = wave + B_WAVES * i;
-      if (t < NFT * NDT) {
-        const int ft = t % NFT, dt = t / NFT;
+      for (int qb = 0; qb < 4; ++qb)
+        qf[qb] = tr_operand_scaled(fq_l, PF, 16 * qb, ft * 32, lane, qhc);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) dS[i][r] *= r_n;
-        dS[i] = mfma_chain<4, 2>(
-            dS[i], [&](int qb) { return tr_operand(fq_l, PF, 16 * qb, ft * 32, lane); },
-            [&](int qb) { return tr_operand(dyh_l, PD, 16 * qb, dt * 32, lane); });
+      for (int i = 0; i < Cfg::S_OWN; ++i) {
+        const int t = wave + B_WAVES * i;
+        if (t < NFT * NDT) {
+          const int dt = t / NFT;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) dS[i][r] *= r_n;
+          dS[i] = mfma_chain<4, 2>(
+              dS[i], [&](int qb) { return qf[qb]; },
+              [&](int qb) { return tr_operand(dy_l, PD, 16 * qb, dt * 32, lane); });
+        }
       }
     }
     // ---- dfk jobs (f-tile, key half), from the published dS^T -----------------

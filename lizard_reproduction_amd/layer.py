@@ -300,10 +300,13 @@ class LizardAttention(nn.Module):
         nn.init.normal_(self.phi_k.weight, std=0.02)
         nn.init.zeros_(self.W_gamma.weight)
 
-    def _fused(self, x, cos, sin):
-        """Whether the fused prologue takes this layer's shapes and dtypes."""
-        return prologue_supported(self.head_dim, self.phi_q.weight.shape[0],
-                                  _all_bf16(x, self.q_proj.weight, self.phi_q.weight, cos, sin))
+    def _fused(self, qp, kp, vp, cos, sin):
+        """Whether the fused prologue takes this layer's shapes and dtypes,
+        decided from the tensors ``prologue_forward`` itself reads (the
+        projection outputs, both phi weights and the RoPE tables), so that
+        the two never disagree on the arithmetic dtype."""
+        bf16 = _all_bf16(qp, kp, vp, self.phi_q.weight, self.phi_k.weight, cos, sin)
+        return prologue_supported(self.head_dim, self.phi_q.weight.shape[0], bf16)
 
     def forward(self, hidden_states, position_embeddings, **kwargs):
         x = hidden_states
@@ -314,7 +317,7 @@ class LizardAttention(nn.Module):
         z = self.W_gamma(x).to(dtype).squeeze(-1)
         cos, sin = position_embeddings
         qp, kp, vp = self.q_proj(x), self.k_proj(x), self.v_proj(x)
-        if not self._fused(x, cos, sin):
+        if not self._fused(qp, kp, vp, cos, sin):
             y = self._unfused(qp, kp, vp, F.logsigmoid(z), cos, sin, dtype).to(x.dtype)
             return self.o_proj(y.transpose(1, 2).flatten(2)), None
         y = _Core.apply(qp, kp, vp, self.phi_q.weight, self.phi_k.weight, F.logsigmoid(z),
@@ -366,17 +369,18 @@ class LizardAttention(nn.Module):
         if x.device.type != "cuda":
             raise ValueError("LizardAttention (hip backend) needs its input on a ROCm GPU")
         nf = 2 * self.phi_q.weight.shape[0]
-        if not self._fused(x, *position_embeddings) or not kernels.gla_native(nf, self.head_dim):
+        cos, sin = position_embeddings
+        qp, kp, vp = self.q_proj(x), self.k_proj(x), self.v_proj(x)
+        if not self._fused(qp, kp, vp, cos, sin) or not kernels.gla_native(nf, self.head_dim):
             raise ValueError(f"LizardAttention.prefill/step: decoding takes the fused prologue's "
                              f"shapes and the GLA decode kernels' (F = {nf}, D = "
                              f"{self.head_dim} is not one: F <= 256, D <= 128, D <= 64 when "
                              "F > 128)")
         dtype = torch.promote_types(x.dtype, torch.float32)
         lg = F.logsigmoid(self.W_gamma(x).to(dtype).squeeze(-1)).float().contiguous()
-        cos, sin = position_embeddings
-        fq, fk, qr, kr, v, _ = prologue_forward(
-            self.q_proj(x), self.k_proj(x), self.v_proj(x), self.phi_q.weight,
-            self.phi_k.weight, cos, sin, self.heads, self.kv_heads)
+        fq, fk, qr, kr, v, _ = prologue_forward(qp, kp, vp, self.phi_q.weight,
+                                                self.phi_k.weight, cos, sin, self.heads,
+                                                self.kv_heads)
         return lg, fq, fk, qr, kr, v
 
     def _out(self, y_gla, y_swa, x):

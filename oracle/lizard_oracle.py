@@ -49,6 +49,11 @@ awa_banded          == awa in fp64 for windows 1 .. > L, ragged L, block
                     sizes 16/64, empty meta, gradients included
 lizard_layer_banded == lizard_layer in fp64 (output and every gradient) at
                     L <= 256, windows shorter and longer than a block
+lizard_layer_       unrounded: == lizard_layer in fp64 (output and every
+  rounded           gradient, fp32- and bf16-layer modes); rounded: each
+                    rounding point moves the result (it is applied) and
+                    stays within bf16 error of the unrounded layer; its
+                    bf16 rounding is round-to-nearest-even (bf16 casts)
 ==================  =======================================================
 
 The loops are deliberately independent code paths (explicit Python loops over
@@ -309,25 +314,29 @@ def gla_chunked(fq, fk, v, log_gamma, chunk=64, round_bf16=False, dtype=torch.fl
     rnd = _bf16 if round_bf16 else (lambda t: t)
     state = torch.zeros(batch, heads, nf, nd, dtype=dtype)
     norm = torch.zeros(batch, heads, nf, dtype=dtype)
-    out = torch.empty(batch, heads, length, nd, dtype=dtype)
-    for c0 in range(0, length, chunk):
-        c1 = min(c0 + chunk, length)
-        lg = torch.cumsum(lgam[..., c0:c1], dim=-1)           # [B,H,c]
+    outs = []
+    # chunks by split and outputs joined by cat, so that autograd's backward
+    # stays linear in L (a slice's backward would fill a whole-length buffer)
+    if length == 0:
+        outs.append(torch.empty(batch, heads, 0, nd, dtype=dtype))
+    pieces = (torch.split(t, chunk, dim=2) for t in (fq, fk, v))
+    for q, k, vv, lgc in zip(*pieces, torch.split(lgam, chunk, dim=-1)):
+        lg = torch.cumsum(lgc, dim=-1)                         # [B,H,c]
         lg_end = lg[..., -1:]
-        q, k, vv = fq[:, :, c0:c1], fk[:, :, c0:c1], v[:, :, c0:c1]
         qt = q * torch.exp(lg)[..., None]
         kt = rnd(k * torch.exp(lg_end - lg)[..., None])
-        n = c1 - c0
+        n = q.shape[2]
         causal = torch.ones(n, n, dtype=torch.bool).tril()
         diff = lg[..., :, None] - lg[..., None, :]
         decay = torch.exp(torch.where(causal, diff, torch.full_like(diff, -math.inf)))
         a = rnd(torch.matmul(q, k.transpose(-1, -2)) * decay)
         o = torch.matmul(qt, rnd(state)) + torch.matmul(a, vv)
         den = (qt * norm[:, :, None, :]).sum(-1) + a.sum(-1)
-        out[:, :, c0:c1] = o / den.clamp_min(TINY)[..., None]
+        outs.append(o / den.clamp_min(TINY)[..., None])
         r = torch.exp(lg_end)[..., None]                       # [B,H,1,1]
         state = state * r + torch.matmul(kt.transpose(-1, -2), vv)
         norm = norm * r[..., 0] + kt.sum(-2)
+    out = torch.cat(outs, dim=2)
     if return_state:
         return out, state, norm
     return out
@@ -371,23 +380,110 @@ def lizard_layer(params, x, cos, sin, heads, kv_heads, window):
     return torch.matmul(y, params["o_proj.weight"].transpose(0, 1))
 
 
-def awa_banded(q, k, v, meta, window, block=64):
+class _RoundBF16(torch.autograd.Function):
+    """bf16 rounding of a value (kept in its dtype) whose gradient is rounded
+    the same way on the way back: what a bf16 tensor between two HIP kernels
+    does to both (autograd hands a bf16 output a bf16 upstream gradient)."""
+
+    @staticmethod
+    def forward(ctx, x):
+        return x.to(torch.bfloat16).to(x.dtype)
+
+    @staticmethod
+    def backward(ctx, g):
+        return g.to(torch.bfloat16).to(g.dtype)
+
+
+def round_bf16(t):
+    """``_RoundBF16`` applied to t."""
+    return _RoundBF16.apply(t)
+
+
+def lizard_layer_rounded(params, x, cos, sin, heads, kv_heads, window, rounded=True,
+                         bf16_layer=False, chunk=64):
+    """``lizard_layer`` in x's dtype (fp64 for a checker) with the bf16
+    rounding points of the HIP layer, forward and backward: the model of what
+    bf16 operands do to the layer, against which the HIP layer's output and
+    gradients are compared directly.
+
+    Rounding points (all with ``rounded``; none without, which leaves the
+    reference's layer, src/lizard_attention.py:73-97):
+
+    * the kernel operands fq, fk, rotated q and k, and v, and the two branch
+      outputs (the fused layer hands them over in bf16, both ways:
+      ``round_bf16``);
+    * inside the GLA branch, the chunked algorithm's bf16 MFMA operands
+      (``gla_chunked(round_bf16=True)``: K~, the weights a, the state used
+      by Q~ S), their gradients rounded the same way under autograd;
+    * inside the SWA branch, the probabilities P before P V in the forward
+      (the kernel's bf16 MFMA operand; ``awa_banded(round_p=True)``);
+    * with ``bf16_layer`` (a layer whose parameters and input are bf16):
+      the projection outputs q, k, v and the gate logit (torch's bf16
+      GEMMs), the blended y before o_proj, and the layer's output.
+
+    The GLA branch is ``gla_chunked`` on log_gamma = logsigmoid(z), the SWA
+    branch ``awa_banded``: unrounded, both equal the dense forms in fp64, so
+    long L fits.  cos, sin [B, L, hd] or [L, hd]."""
+    batch, length, hidden = x.shape
+    head_dim = hidden // heads
+    r = round_bf16 if rounded else (lambda t: t)
+    rp = r if bf16_layer else (lambda t: t)
+
+    def heads_of(name, count):
+        y = rp(torch.matmul(x, params[name].transpose(0, 1)))
+        y = y.view(batch, length, count, head_dim).transpose(1, 2)
+        return y.repeat_interleave(heads // count, dim=1)
+
+    q = heads_of("q_proj.weight", heads)
+    k = heads_of("k_proj.weight", kv_heads)
+    v = heads_of("v_proj.weight", kv_heads)
+    z = rp(torch.matmul(x, params["W_gamma.weight"].transpose(0, 1))).squeeze(-1)
+    fq, fk = hedgehog(q, params["phi_q.weight"]), hedgehog(k, params["phi_k.weight"])
+    c, s = cos.to(x.dtype), sin.to(x.dtype)
+    c, s = (c if c.dim() == 3 else c[None]).unsqueeze(1), (s if s.dim() == 3 else s[None]).unsqueeze(1)
+    qr, kr = rope(q, c, s), rope(k, c, s)
+    y_gla = r(gla_chunked(r(fq), r(fk), r(v), torch.nn.functional.logsigmoid(z), chunk,
+                          round_bf16=rounded, dtype=x.dtype))
+    y_swa = r(awa_banded(r(qr), r(kr), r(v), params["meta_tokens"], window, round_p=rounded))
+    y = rp(y_gla + params["alpha_blend"] * y_swa)
+    y = y.transpose(1, 2).reshape(batch, length, hidden)
+    return rp(torch.matmul(y, params["o_proj.weight"].transpose(0, 1)))
+
+
+def awa_banded(q, k, v, meta, window, block=64, round_p=False):
     """``awa`` computed block by block over the queries, each block against
     only the keys its window can reach (keys i0 - window + 1 .. i1 - 1 for
     queries i0 .. i1 - 1), so memory is O(L (block + window)) instead of
     O(L^2): the long-L form of the dense SWA oracle.  Same mask
-    (``window_mask``'s predicate), scale and ``sink_softmax``."""
+    (``window_mask``'s predicate), scale and ``sink_softmax``.  With
+    ``round_p`` the probabilities are rounded to bf16 before P V (the SWA
+    forward's MFMA operand) in the forward only: the gradient passes
+    unrounded, as the SWA backward recomputes P in fp32 for delta and the
+    sink gradient."""
     length, dim = q.shape[-2], q.shape[-1]
+    if length == 0:
+        return torch.empty_like(v)
+    # blocks by split and the keys a block reaches by cat, so that autograd's
+    # backward stays linear in L (a slice of the whole k would fill a
+    # whole-length buffer in its backward)
+    qb, kb, vb = (torch.split(t, block, dim=-2) for t in (q, k, v))
     outs = []
-    for i0 in range(0, length, block):
-        i1 = min(i0 + block, length)
+    for n, qq in enumerate(qb):
+        i0 = n * block
+        i1 = i0 + qq.shape[-2]
         t0 = max(0, i0 - window + 1)
+        first = t0 // block
+        kk = torch.cat(kb[first:n + 1], dim=-2)[..., t0 - first * block:, :]
+        vv = torch.cat(vb[first:n + 1], dim=-2)[..., t0 - first * block:, :]
         rows = torch.arange(i0, i1).unsqueeze(1)
         cols = torch.arange(t0, i1).unsqueeze(0)
         mask = (cols <= rows) & ((rows - cols) < window)
-        scores = torch.matmul(q[..., i0:i1, :], k[..., t0:i1, :].transpose(-1, -2))
+        scores = torch.matmul(qq, kk.transpose(-1, -2))
         scores = (scores / math.sqrt(dim)).masked_fill(~mask, float("-inf"))
-        outs.append(torch.matmul(sink_softmax(scores, meta), v[..., t0:i1, :]))
+        p = sink_softmax(scores, meta)
+        if round_p:
+            p = p + (p.detach().to(torch.bfloat16).to(p.dtype) - p.detach())
+        outs.append(torch.matmul(p, vv))
     return torch.cat(outs, dim=-2)
 
 

@@ -24,8 +24,12 @@ def _expand(t, group):
     # rows over two workgroups (120 segments), the expanded one does not (480)
     (1, 32, 8, 2048, 128, 128, False),
     (16, 32, 8, 130, 128, 128, True),  # B*H fills the GPU: one walk per (b, h)
-    (1, 8, 2, 300, 256, 128, False),   # past the walks' sizes: two D tiles
-    (1, 4, 2, 200, 512, 64, True),     # two F tiles (summed raw numerators)
+    # past the walks' sizes, both gate kinds: two D tiles (the fused bf16 layer
+    # at head_dim 128 x 128 features), two F tiles (summed raw numerators),
+    # and ragged F and D tiles
+    (1, 8, 2, 300, 256, 128, False), (1, 8, 2, 300, 256, 128, True),
+    (1, 4, 2, 200, 512, 64, True), (1, 4, 2, 200, 512, 64, False),
+    (1, 4, 2, 150, 300, 200, True), (2, 6, 3, 150, 300, 200, False),
 ])
 def test_gla_grouped_kv_equals_expanded(b, heads, kv, length, nf, nd, per_head):
     g = torch.Generator().manual_seed(nf + length)

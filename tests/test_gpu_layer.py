@@ -352,11 +352,39 @@ def test_layer_at_shapes_past_the_fused_prologue_matches_oracle(hidden, heads, k
             assert errs[name] <= GRAD_TOL, (name, errs)
 
 
+def _bf16_layer_case(layer, x, grad, cos, sin, heads, kv, window, label):
+    """A bf16 layer forward+backward on the GPU against the fp64 oracle on
+    the same bf16 parameters and inputs: the output within the reference's
+    bf16 layer bar (2e-2 relative norm, tests/test_lizard.py:244-253) of the
+    exact layer, and the output, input gradient and every parameter gradient
+    within the north-star bar of the layer with the HIP path's bf16 rounding
+    points (lo.lizard_layer_rounded, pinned to the exact layer in
+    tests/test_layer.py)."""
+    from tests.test_gpu_random_shapes import _oracle_layer_grads
+    params = {n: p.detach().double() for n, p in layer.named_parameters()}
+    layer = layer.cuda()
+    xg = x.cuda().requires_grad_()
+    y = layer(xg, (cos.cuda(), sin.cuda()))[0]
+    y.backward(grad.cuda())
+    torch.cuda.synchronize()
+    ours = {"out": y, "dx": xg.grad}
+    ours.update({n: p.grad for n, p in layer.named_parameters()})
+    model, exact = (_oracle_layer_grads(params, x, grad, cos, sin, heads, kv, window, rnd, True)
+                    for rnd in (True, False))
+    direct = report(label, {"rounding_model/" + n: (ours[n], model[n]) for n in ours})
+    report(label, {n: (ours[n], exact[n]) for n in ours})
+    err = norm_rel(y, exact["out"])
+    print(f"[parity] {label}: norm={err:.2e} max={max_rel(y, exact['out']):.2e}", flush=True)
+    assert all(t.dtype == torch.bfloat16 for t in ours.values())
+    assert err < 2e-2, err
+    for name, e in direct.items():
+        assert e <= (OUT_TOL if name.endswith("/out") else GRAD_TOL), (name, direct)
+
+
 def test_bf16_layer_head_dim_128_with_128_features_close_to_oracle():
     """The fused bf16 prologue at head_dim 128, feature_dim 128 in a whole
-    bf16 layer (F = 256, D = 128: the GLA on two D tiles), against the fp64
-    oracle on the same bf16 parameters (the reference's bf16 layer bar,
-    tests/test_lizard.py:244-253)."""
+    bf16 layer (F = 256, D = 128: the GLA on two D tiles, its k side read
+    per kv head), forward and backward."""
     import types
     cfg = types.SimpleNamespace(hidden_size=256, num_attention_heads=2, num_key_value_heads=1)
     torch.manual_seed(1)
@@ -366,15 +394,36 @@ def test_bf16_layer_head_dim_128_with_128_features_close_to_oracle():
             p.normal_(0, 0.05 if n.split(".")[0] in ("q_proj", "k_proj", "v_proj", "o_proj")
                       else 0.3)
     layer = layer.to(torch.bfloat16)
-    params = {n: p.detach().double() for n, p in layer.named_parameters()}
-    layer = layer.cuda()
-    x = torch.randn(2, 90, 256, generator=torch.Generator().manual_seed(2)).bfloat16()
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(2, 90, 256, generator=g).bfloat16()
+    grad = torch.randn(2, 90, 256, generator=g).bfloat16()
     cos, sin = (t.bfloat16()[None].expand(2, 90, 128) for t in lo.rope_cos_sin(90, 128))
-    assert layer._fused(x, cos, sin)
+    assert layer._fused(*(torch.empty(2, 90, n, dtype=torch.bfloat16) for n in (256, 128, 128)),
+                        cos, sin)
+    _bf16_layer_case(layer, x, grad, cos, sin, 2, 1, 16, "bf16 layer hd=128 f=128")
+
+
+def test_config5_bf16_layer_at_size_matches_oracle_layer():
+    """One LizardAttention at BASELINE config 5's shape in its own dtype:
+    bf16 parameters, input and RoPE tables (theta 500000), hidden 2048, 32
+    query / 8 kv heads, head_dim 64, feature_dim 128 (F = 256), window 64, 4
+    sinks, on a B=1 slice of its L=4096 sequences: the bf16 MFMA prologue,
+    the eight-wave GLA walk and the SWA kernels that bench.py times, forward
+    and backward, against the long-L oracle layer in fp64."""
+    import types
+    cfg = types.SimpleNamespace(hidden_size=2048, num_attention_heads=32, num_key_value_heads=8)
+    torch.manual_seed(0)
+    layer = hip_layer.LizardAttention(cfg, 0, window=64, num_meta=4, feature_dim=128)
     with torch.no_grad():
-        y = layer(x.cuda(), (cos.cuda(), sin.cuda()))[0]
-    expected = lo.lizard_layer(params, x.double(), cos.double(), sin.double(), 2, 1, 16)
-    print(f"[parity] bf16 layer hd=128 f=128: norm={norm_rel(y, expected):.2e} "
-          f"max={max_rel(y, expected):.2e}", flush=True)
-    assert y.dtype == torch.bfloat16
-    assert norm_rel(y, expected) < 2e-2
+        layer.phi_q.weight.normal_(0, 0.3)
+        layer.phi_k.weight.normal_(0, 0.3)
+        layer.W_gamma.weight.normal_(0, 0.05)   # gates from ~0.1 to ~0.99
+        layer.meta_tokens.normal_(0, 1)
+        layer.alpha_blend.fill_(0.8)
+    layer = layer.bfloat16()
+    batch, length = 1, 4096
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(batch, length, 2048, generator=g).bfloat16()
+    grad = torch.randn(batch, length, 2048, generator=g).bfloat16()
+    cos, sin = (t[None].expand(batch, length, 64).bfloat16() for t in lo.rope_cos_sin(length, 64))
+    _bf16_layer_case(layer, x, grad, cos, sin, 32, 8, 64, "config5 bf16 layer B=1 L=4096")

@@ -148,30 +148,36 @@ LAYER_CASES = _layer_cases(16)
 @pytest.mark.parametrize("case", LAYER_CASES, ids=[_label(c) for c in LAYER_CASES])
 def test_layer_random_shape_matches_oracle_layer(case):
     """LizardAttention at drawn shapes (fused prologue or the reference's torch
-    ops before the kernels, grouped kv heads, any window and sink count)
-    against the oracle's dense layer: fp32 layers output, input and every
-    parameter gradient within the bar; bf16 layers within the reference's
-    bf16 layer bar (2e-2 relative norm, tests/test_lizard.py:244-253) of the
-    fp64 oracle on the same bf16 parameters.
+    ops before the kernels, grouped kv heads, any window and sink count),
+    forward and backward, fp32 or bf16 parameters.
 
-    Some parameter gradients are small sums that mostly cancel: meta_tokens'
-    (sum over every query of sink probability times dy.y) and alpha_blend's.
-    There the bf16 operands the kernels take (fq, fk, rotated q, k, v, and
-    their bf16 outputs) alone move the result past the bar: the fp64 oracle
-    with just that rounding added (``_rounded_layer_grads``) departs from the
-    exact one by up to 7e-2 on these draws.  Each gradient is therefore held
-    to the bar or to 1.5 times what that rounding alone does, whichever is
-    larger: a kernel adding error of its own, or a wrong term, still fails."""
+    Every output and gradient is compared directly with the fp64 oracle
+    layer that applies the HIP layer's bf16 rounding points
+    (``lo.lizard_layer_rounded``: the kernels' bf16 operands and outputs, the
+    chunked GLA's internal roundings, SWA's bf16 P, and for a bf16 layer its
+    bf16 projections and output), at the north-star bar.  That model is
+    pinned to the exact oracle layer on the CPU (tests/test_layer.py).
+
+    Against the exact oracle layer (``lo.lizard_layer`` on the same
+    parameters): fp32 layers hold every quantity to the bar, except where
+    bf16 operands alone move the exact result by more than half of it (the
+    rounding model's own departure; it happens to the cancelling sink and
+    blend gradients on some draws) -- there the direct comparison above is
+    the check, and the exact-oracle error is printed.  bf16 layers hold the
+    output to the reference's bf16 layer bar (2e-2 relative norm,
+    tests/test_lizard.py:244-253)."""
     import types
     from lizard_reproduction_amd import layer as hip_layer
     from tests.helpers import norm_rel
-    from tests.test_gpu_layer import OracleAttention, report
+    from tests.test_gpu_layer import report
     b, hd, length = case["batch"], case["head_dim"], case["length"]
-    hidden = case["heads"] * hd
-    cfg = types.SimpleNamespace(hidden_size=hidden, num_attention_heads=case["heads"],
-                                num_key_value_heads=case["kv"])
+    heads, kv, window = case["heads"], case["kv"], case["window"]
+    hidden = heads * hd
+    bf16 = case["bf16"]
+    cfg = types.SimpleNamespace(hidden_size=hidden, num_attention_heads=heads,
+                                num_key_value_heads=kv)
     torch.manual_seed(case["seed"])
-    layer = hip_layer.LizardAttention(cfg, 0, window=case["window"], num_meta=case["sinks"],
+    layer = hip_layer.LizardAttention(cfg, 0, window=window, num_meta=case["sinks"],
                                       feature_dim=case["feature_dim"])
     # weights as in the fixed-shape layer tests: feature logits q phi^T kept
     # at the tiny config's scale whatever the head_dim
@@ -182,87 +188,50 @@ def test_layer_random_shape_matches_oracle_layer(case):
             p.normal_(0, std * (32 / hd) ** 0.5 if kind in ("phi_q", "phi_k") else std)
     g = torch.Generator().manual_seed(case["seed"] + 1)
     x = torch.randn(b, length, hidden, generator=g)
-    cos, sin = (t.float()[None].expand(b, length, hd) for t in lo.rope_cos_sin(length, hd))
-    label = "layer " + _label(case)
-    if case["bf16"]:
-        layer = layer.bfloat16()
-        params = {n: p.detach().double() for n, p in layer.named_parameters()}
-        layer = layer.cuda()
-        xb, cb, sb = x.bfloat16(), cos.bfloat16(), sin.bfloat16()
-        with torch.no_grad():
-            y = layer(xb.cuda(), (cb.cuda(), sb.cuda()))[0]
-        expected = lo.lizard_layer(params, xb.double(), cb.double(), sb.double(), case["heads"],
-                                   case["kv"], case["window"])
-        err = norm_rel(y, expected)
-        print(f"[parity] {label}: norm={err:.2e}", flush=True)
-        assert y.dtype == torch.bfloat16 and err < 2e-2, (label, err)
-        return
-    oracle = OracleAttention(layer)
-    layer = layer.cuda()
     grad = torch.randn(b, length, hidden, generator=g)
+    cos, sin = (t.float()[None].expand(b, length, hd) for t in lo.rope_cos_sin(length, hd))
+    dtype = torch.bfloat16 if bf16 else torch.float32
+    layer = layer.to(dtype)
+    x, grad, cos, sin = (t.to(dtype) for t in (x, grad, cos, sin))
+    params = {n: p.detach().double() for n, p in layer.named_parameters()}
+    layer = layer.cuda()
     xg = x.cuda().requires_grad_()
     y = layer(xg, (cos.cuda(), sin.cuda()))[0]
     y.backward(grad.cuda())
-    xc = x.clone().requires_grad_()
-    expected = oracle(xc, (cos, sin))[0]
-    expected.backward(grad)
     torch.cuda.synchronize()
-    pairs = {"out": (y, expected), "dx": (xg.grad, xc.grad)}
-    for name, p in layer.named_parameters():
-        pairs[name] = (p.grad, oracle.params[name.replace(".", "__")].grad)
-    errs = report(label, pairs)
-    assert errs["out"] <= OUT_TOL, (label, errs)
-    exact, rounded = (_rounded_layer_grads(layer, x, grad, cos, sin, case, rnd)
-                      for rnd in (False, True))
-    for name in pairs:
-        if name == "out":
-            continue
-        floor = max_rel(rounded[name], exact[name])
-        assert errs[name] <= max(GRAD_TOL, 1.5 * floor), (label, name, errs[name], floor)
+    ours = {"out": y, "dx": xg.grad}
+    ours.update({n: p.grad for n, p in layer.named_parameters()})
+    model, exact = (_oracle_layer_grads(params, x, grad, cos, sin, heads, kv, window, rnd, bf16)
+                    for rnd in (True, False))
+    label = "layer " + _label(case)
+    direct = report(label, {"rounding_model/" + n: (ours[n], model[n]) for n in ours})
+    errs = report(label, {n: (ours[n], exact[n]) for n in ours})
+    assert y.dtype == dtype and all(t.dtype == dtype for t in ours.values()), label
+    for name, e in direct.items():
+        assert e <= (OUT_TOL if name.endswith("/out") else GRAD_TOL), (label, name, direct)
+    if bf16:
+        err = norm_rel(y, exact["out"])
+        print(f"[parity] {label}: norm={err:.2e}", flush=True)
+        assert err < 2e-2, (label, err)
+        return
+    for name, e in errs.items():
+        tol = OUT_TOL if name == "out" else GRAD_TOL
+        if max_rel(model[name], exact[name]) <= tol / 2:
+            assert e <= tol, (label, name, errs)
 
 
-class _RoundBF16(torch.autograd.Function):
-    """bf16 rounding of a kernel operand or output, with the same rounding of
-    the gradient flowing back through it (autograd casts a bf16 output's
-    upstream gradient to bf16)."""
-
-    @staticmethod
-    def forward(ctx, x):
-        return x.to(torch.bfloat16).to(x.dtype)
-
-    @staticmethod
-    def backward(ctx, g):
-        return g.to(torch.bfloat16).to(g.dtype)
-
-
-def _rounded_layer_grads(layer, x, grad, cos, sin, case, rnd):
-    """Parameter and input gradients of the oracle layer in fp64, with (rnd)
-    or without the bf16 rounding of the operands and outputs of the GLA and
-    SWA calls (the steps of lo.lizard_layer, src/lizard_attention.py:78-97)."""
-    r = _RoundBF16.apply if rnd else (lambda t: t)
-    params = {n: p.detach().cpu().double().requires_grad_() for n, p in layer.named_parameters()}
-    xd = x.double().requires_grad_()
-    b, length, hidden = x.shape
-    heads, kv = case["heads"], case["kv"]
-    hd = hidden // heads
-
-    def heads_of(name, count):
-        y = (xd @ params[name].T).view(b, length, count, hd).transpose(1, 2)
-        return y.repeat_interleave(heads // count, dim=1)
-
-    q, k, v = heads_of("q_proj.weight", heads), heads_of("k_proj.weight", kv), \
-        heads_of("v_proj.weight", kv)
-    z = (xd @ params["W_gamma.weight"].T).squeeze(-1)
-    fq, fk = lo.hedgehog(q, params["phi_q.weight"]), lo.hedgehog(k, params["phi_k.weight"])
-    c, s = cos.double().unsqueeze(1), sin.double().unsqueeze(1)
-    qr, kr = lo.rope(q, c, s), lo.rope(k, c, s)
-    y = r(lo.gla(r(fq), r(fk), r(v), torch.sigmoid(z))) + params["alpha_blend"] * \
-        r(lo.awa(r(qr), r(kr), r(v), params["meta_tokens"], case["window"]))
-    out = y.transpose(1, 2).reshape(b, length, hidden) @ params["o_proj.weight"].T
-    out.backward(grad.double())
-    grads = {n: p.grad for n, p in params.items()}
-    grads["dx"] = xd.grad
-    return grads
+def _oracle_layer_grads(params, x, grad, cos, sin, heads, kv, window, rounded, bf16_layer):
+    """Output, input gradient and every parameter gradient of the oracle
+    layer in fp64 (lo.lizard_layer_rounded, with or without its bf16
+    rounding points) on the CPU."""
+    params = {n: p.detach().clone().requires_grad_() for n, p in params.items()}
+    xd = x.detach().double().requires_grad_()
+    y = lo.lizard_layer_rounded(params, xd, cos.double(), sin.double(), heads, kv, window,
+                                rounded=rounded, bf16_layer=bf16_layer)
+    y.backward(grad.double())
+    out = {n: p.grad for n, p in params.items()}
+    out["out"], out["dx"] = y.detach(), xd.grad
+    return out
 
 
 def _decode_cases(n, seed=77):

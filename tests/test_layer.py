@@ -264,29 +264,78 @@ def test_layer_takes_any_even_head_dim_up_to_the_swa_limit():
     assert not hip_layer.prologue_supported(96, 16)
 
 
-def test_rounding_model_of_the_layer_sweep_without_rounding_is_the_oracle_layer():
-    """The GPU layer sweep bounds cancelling gradients by what bf16 kernel
-    operands alone do, from a restatement of the oracle layer with optional
-    rounding; unrounded it must give lo.lizard_layer's gradients exactly, and
-    rounded it must move them (the rounding is really applied)."""
+def _sweep_layer(seed=0, heads=4, kv=2, hd=24, f=12, sinks=3, window=5):
     import types
-    from tests.test_gpu_random_shapes import _rounded_layer_grads
-    case = dict(heads=4, kv=2, window=5)
-    cfg = types.SimpleNamespace(hidden_size=4 * 24, num_attention_heads=4, num_key_value_heads=2)
-    torch.manual_seed(0)
-    layer = hip_layer.LizardAttention(cfg, 0, window=5, num_meta=3, feature_dim=12)
+    cfg = types.SimpleNamespace(hidden_size=heads * hd, num_attention_heads=heads,
+                                num_key_value_heads=kv)
+    torch.manual_seed(seed)
+    layer = hip_layer.LizardAttention(cfg, 0, window=window, num_meta=sinks, feature_dim=f)
     with torch.no_grad():
         for p in layer.parameters():
             p.normal_(0, 0.3)
-    g = torch.Generator().manual_seed(1)
-    x, grad = torch.randn(2, 30, 96, generator=g), torch.randn(2, 30, 96, generator=g)
-    cos, sin = (t.float()[None].expand(2, 30, 24) for t in lo.rope_cos_sin(30, 24))
-    params = {n: p.detach().double().requires_grad_() for n, p in layer.named_parameters()}
-    xd = x.double().requires_grad_()
-    lo.lizard_layer(params, xd, cos.double(), sin.double(), 4, 2, 5).backward(grad.double())
-    plain = _rounded_layer_grads(layer, x, grad, cos, sin, case, False)
-    rounded = _rounded_layer_grads(layer, x, grad, cos, sin, case, True)
-    assert rel_err(plain["dx"], xd.grad) < EXACT
-    for name, p in params.items():
-        assert rel_err(plain[name], p.grad) < EXACT, name
-        assert rel_err(rounded[name], p.grad) > 1e-5, name
+    return {n: p.detach().double() for n, p in layer.named_parameters()}
+
+
+def _layer_grads(fn, params, x, grad):
+    params = {n: p.detach().clone().requires_grad_() for n, p in params.items()}
+    xd = x.detach().clone().requires_grad_()
+    y = fn(params, xd)
+    y.backward(grad)
+    out = {n: p.grad for n, p in params.items()}
+    out["dx"], out["out"] = xd.grad, y.detach()
+    return out
+
+
+@pytest.mark.parametrize("bf16_layer", [False, True])
+@pytest.mark.parametrize("length, window", [(30, 5), (130, 100)])
+def test_rounded_oracle_layer_without_rounding_is_the_oracle_layer(bf16_layer, length, window):
+    """lo.lizard_layer_rounded with its rounding off is the dense oracle
+    layer: output, input gradient and every parameter gradient in fp64 (L =
+    130 spans three 64-token GLA chunks and, at window 5, several SWA
+    blocks), in both of its layer modes."""
+    params = _sweep_layer(window=window)
+    g = torch.Generator().manual_seed(length)
+    x = torch.randn(2, length, 96, generator=g, dtype=torch.float64)
+    grad = torch.randn(2, length, 96, generator=g, dtype=torch.float64)
+    cos, sin = (t[None].expand(2, length, 24) for t in lo.rope_cos_sin(length, 24))
+    dense_g = _layer_grads(lambda p, xd: lo.lizard_layer(p, xd, cos, sin, 4, 2, window),
+                           params, x, grad)
+    plain = _layer_grads(lambda p, xd: lo.lizard_layer_rounded(
+        p, xd, cos, sin, 4, 2, window, rounded=False, bf16_layer=bf16_layer), params, x, grad)
+    for name in dense_g:
+        assert rel_err(plain[name], dense_g[name]) < EXACT, name
+
+
+def test_rounded_oracle_layer_applies_its_rounding_points():
+    """With rounding on, every output and gradient moves off the exact layer
+    (the rounding is really applied), by bf16-sized amounts except the sink
+    gradient: there the sink probabilities exp(meta - lse_i) of this draw's
+    large scores (|q.k|/sqrt(d) ~ 40) move with the absolute error that the
+    bf16 q and k put into the scores, so that gradient is the rounding's own
+    (the HIP kernels take the same bf16 q and k, and are compared with this
+    model rather than with the exact layer for that reason).  The bf16-layer
+    mode adds its own rounding points (projections, blended y, output); the
+    SWA branch's P rounding moves its output; and round_bf16 is the bf16
+    cast both ways."""
+    params = _sweep_layer()
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(2, 70, 96, generator=g, dtype=torch.float64)
+    grad = torch.randn(2, 70, 96, generator=g, dtype=torch.float64)
+    cos, sin = (t[None].expand(2, 70, 24) for t in lo.rope_cos_sin(70, 24))
+    runs = {mode: _layer_grads(lambda p, xd: lo.lizard_layer_rounded(
+        p, xd, cos, sin, 4, 2, 5, rounded=mode != "exact", bf16_layer=mode == "bf16"),
+        params, x, grad) for mode in ("exact", "fp32", "bf16")}
+    for name in runs["exact"]:
+        d32 = rel_err(runs["fp32"][name], runs["exact"][name])
+        d16 = rel_err(runs["bf16"][name], runs["fp32"][name])
+        assert d32 > 1e-6 and (d32 < 2e-2 or name == "meta_tokens"), (name, d32)
+        assert d16 > 1e-6, (name, d16)
+    q, k, v = (torch.randn(1, 2, 90, 16, generator=g, dtype=torch.float64) for _ in range(3))
+    meta = torch.randn(3, generator=g, dtype=torch.float64)
+    exact, rnd = (lo.awa_banded(q, k, v, meta, 20, round_p=r) for r in (False, True))
+    assert 1e-6 < rel_err(rnd, exact) < 1e-2
+    t = torch.randn(1000, generator=g, dtype=torch.float64).requires_grad_()
+    up = torch.randn(1000, generator=g, dtype=torch.float64)
+    lo.round_bf16(t).backward(up)
+    assert torch.equal(lo.round_bf16(t).detach(), t.detach().bfloat16().double())
+    assert torch.equal(t.grad, up.bfloat16().double())
