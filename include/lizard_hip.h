@@ -32,7 +32,22 @@
 extern "C" {
 #endif
 
-#define LZ_ABI_VERSION 12
+#define LZ_ABI_VERSION 13
+
+/*
+ * gate_mode of the GLA entry points: a combination of
+ *   LZ_GATE_PER_HEAD  the gate is [B, H, L] (one per head); without it [B, L]
+ *                     (one per token, shared by the heads), the reference's
+ *                     two layouts (src/kernels/gla.py:259-263)
+ *   LZ_GATE_LOGIT     the gate buffer holds the logit z, and the kernels use
+ *                     log_gamma = logsigmoid(z), the reference layer's
+ *                     F.logsigmoid (src/lizard_attention.py:92); the gate
+ *                     gradient they write is then d/dz = d log_gamma *
+ *                     sigmoid(-z).  Without it the buffer holds log_gamma.
+ * Other bits are refused.
+ */
+#define LZ_GATE_PER_HEAD 1
+#define LZ_GATE_LOGIT 2
 
 /* Largest feature (nf) and value (nd) dim the GLA entry points take. */
 #define LZ_GLA_MAX_DIM 4096
@@ -47,7 +62,7 @@ const char* lz_last_error(void);
 
 /* Workspace bytes lz_gla_fwd needs for these sizes (0 when B*H alone fills the GPU). */
 size_t lz_gla_fwd_workspace_bytes(int batch, int heads, int length, int nf, int nd,
-                                  int gate_per_head, int chunk);
+                                  int gate_mode, int chunk);
 
 /*
  * GLA forward.  Replaces kernels.gla's forward: the gate cumsum and head
@@ -59,8 +74,9 @@ size_t lz_gla_fwd_workspace_bytes(int batch, int heads, int length, int nf, int 
  *   kv_heads    heads of fk and v (divides heads): query head h reads kv head
  *               h / (heads / kv_heads), grouped-query attention without
  *               materialised copies; kv_heads = heads is the reference's layout
- *   log_gamma   f32  [B, L] (gate_per_head = 0) or [B, H, L] (gate_per_head = 1);
- *               log of the gate (<= 0), NOT its cumsum
+ *   log_gamma   f32  [B, L], or [B, H, L] with LZ_GATE_PER_HEAD in gate_mode;
+ *               log of the gate (<= 0), NOT its cumsum, or with LZ_GATE_LOGIT
+ *               the gate's logit z (log_gamma = logsigmoid(z))
  *   y           bf16 [BH, L, nd]      output
  *   chunk       tiling hint of the reference API (power of two >= 16); the
  *               kernels always walk 64-token chunks, results are
@@ -79,7 +95,7 @@ size_t lz_gla_fwd_workspace_bytes(int batch, int heads, int length, int nf, int 
  * the output is the same with and without autograd (tests/test_kernels.py:102-107).
  */
 int lz_gla_fwd(const void* fq, const void* fk, const void* v, const float* log_gamma, void* y,
-               int batch, int heads, int kv_heads, int length, int nf, int nd, int gate_per_head,
+               int batch, int heads, int kv_heads, int length, int nf, int nd, int gate_mode,
                int chunk, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
@@ -104,7 +120,7 @@ int lz_gla_fwd(const void* fq, const void* fk, const void* v, const float* log_g
 #define LZ_GLA_FWD_NOALLOC_MAX_BYTES (66u << 20)
 int lz_gla_fwd_noalloc(const void* fq, const void* fk, const void* v, const float* log_gamma,
                        void* y, int batch, int heads, int kv_heads, int length, int nf, int nd,
-                       int gate_per_head, int chunk, void* stream);
+                       int gate_mode, int chunk, void* stream);
 
 /*
  * Set-up of lz_gla_fwd_noalloc on the current device, once per device: the
@@ -130,7 +146,7 @@ int lz_init(void);
  */
 int lz_gla_prefill(const void* fq, const void* fk, const void* v, const float* log_gamma,
                    void* y, float* state, int batch, int heads, int kv_heads, int length, int nf,
-                   int nd, int gate_per_head, int chunk, void* workspace, size_t workspace_bytes,
+                   int nd, int gate_mode, int chunk, void* workspace, size_t workspace_bytes,
                    void* stream);
 
 /*
@@ -139,17 +155,18 @@ int lz_gla_prefill(const void* fq, const void* fk, const void* v, const float* l
  *   S <- gamma S + fk v^T,  z <- gamma z + fk,  y = fq S / max(fq . z, FLT_MIN)
  *   fq  bf16 [B, H, nf];  fk  bf16 [B, kv_heads, nf];  v  bf16 [B, kv_heads, nd]
  *   (query head h reads kv head h / (heads / kv_heads));  y  bf16 [B, H, nd]
- *   log_gamma  f32 [B] (gate_per_head = 0) or [B, H];  gamma = exp(log_gamma)
+ *   log_gamma  f32 [B], or [B, H] with LZ_GATE_PER_HEAD;  gamma = exp(log_gamma)
+ *              (with LZ_GATE_LOGIT the logit z: log_gamma = logsigmoid(z))
  *   state  f32 [B, H, nf*nd + nf] as written by lz_gla_prefill (zeros: empty prefix)
  * Sizes as lz_gla_prefill.
  */
 int lz_gla_decode_step(const void* fq, const void* fk, const void* v, const float* log_gamma,
                        float* state, void* y, int batch, int heads, int kv_heads, int nf, int nd,
-                       int gate_per_head, void* stream);
+                       int gate_mode, void* stream);
 
 /* Workspace bytes lz_gla_bwd needs for these sizes. */
 size_t lz_gla_bwd_workspace_bytes(int batch, int heads, int length, int nf, int nd,
-                                  int gate_per_head, int chunk);
+                                  int gate_mode, int chunk);
 
 /*
  * GLA backward.  Replaces _GLA.backward (src/kernels/gla.py:236-256): delta,
@@ -159,7 +176,8 @@ size_t lz_gla_bwd_workspace_bytes(int batch, int heads, int length, int nf, int 
  *   dfq, dfk      [BH, L, nf], dv [BH, L, nd]: bf16 if grad_bf16 else f32; per
  *                 query head also when kv_heads < heads (each query head's
  *                 share; their sum over a group is the kv head's gradient)
- *   dlog_gamma    f32, same shape as log_gamma
+ *   dlog_gamma    f32, same shape as log_gamma (with LZ_GATE_LOGIT: the gradient of
+ *                 the logit z, d log_gamma * sigmoid(-z))
  *   fwd_workspace the workspace lz_gla_fwd used for these inputs, if the caller
  *                 kept it (it then holds the state entering each segment and
  *                 the backward skips recomputing it); may be NULL
@@ -167,7 +185,7 @@ size_t lz_gla_bwd_workspace_bytes(int batch, int heads, int length, int nf, int 
  */
 int lz_gla_bwd(const void* fq, const void* fk, const void* v, const float* log_gamma,
                const void* dy, void* dfq, void* dfk, void* dv, float* dlog_gamma, int grad_bf16,
-               int batch, int heads, int kv_heads, int length, int nf, int nd, int gate_per_head,
+               int batch, int heads, int kv_heads, int length, int nf, int nd, int gate_mode,
                int chunk, const void* fwd_workspace, size_t fwd_workspace_bytes, void* workspace,
                size_t workspace_bytes, void* stream);
 

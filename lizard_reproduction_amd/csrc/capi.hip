@@ -138,9 +138,20 @@ static int check_kv_heads(const char* what, int heads, int kv_heads) {
   return 0;
 }
 
+static_assert(LZ_GATE_PER_HEAD == lz::GATE_PER_HEAD && LZ_GATE_LOGIT == lz::GATE_LOGIT,
+              "gate mode bits");
+
+// gate_mode: LZ_GATE_PER_HEAD and LZ_GATE_LOGIT bits, nothing else
+static int check_gate_mode(const char* what, int gate_mode) {
+  if (gate_mode & ~(LZ_GATE_PER_HEAD | LZ_GATE_LOGIT))
+    return fail(1, "%s: gate_mode %d has bits other than LZ_GATE_PER_HEAD (1) and "
+                   "LZ_GATE_LOGIT (2)", what, gate_mode);
+  return 0;
+}
+
 extern "C" size_t lz_gla_fwd_workspace_bytes(int batch, int heads, int length, int nf, int nd,
-                                             int gate_per_head, int chunk) {
-  (void)gate_per_head; (void)chunk;
+                                             int gate_mode, int chunk) {
+  (void)gate_mode; (void)chunk;
   if (batch <= 0 || heads <= 0 || length <= 0 || nf <= 0 || nd <= 0 || nf > LZ_GLA_MAX_DIM ||
       nd > LZ_GLA_MAX_DIM)
     return 0;
@@ -149,73 +160,77 @@ extern "C" size_t lz_gla_fwd_workspace_bytes(int batch, int heads, int length, i
 
 extern "C" int lz_gla_fwd(const void* fq, const void* fk, const void* v, const float* log_gamma,
                           void* y, int batch, int heads, int kv_heads, int length, int nf, int nd,
-                          int gate_per_head, int chunk, void* workspace, size_t workspace_bytes,
+                          int gate_mode, int chunk, void* workspace, size_t workspace_bytes,
                           void* stream) {
   if (int rc = check_gla(fq, fk, v, log_gamma, batch, heads, length, nf, nd, chunk, false))
     return rc;
   if (int rc = check_kv_heads("gla_fwd", heads, kv_heads)) return rc;
+  if (int rc = check_gate_mode("gla_fwd", gate_mode)) return rc;
   if (!y) return fail(1, "gla_fwd: null output pointer");
   const size_t need = lz::gla_fwd_workspace_any(batch, heads, length, nf, nd);
   if (need && (!workspace || workspace_bytes < need))
     return fail(1, "gla_fwd: workspace of %zu bytes given, %zu needed", workspace_bytes, need);
   return hip_status(lz::launch_gla_fwd_any(fq, fk, v, log_gamma, y, batch, heads, length, nf, nd,
-                                           gate_per_head ? 1 : 0, heads / kv_heads, workspace,
+                                           gate_mode, heads / kv_heads, workspace,
                                            (hipStream_t)stream),
                     "gla_fwd");
 }
 
 extern "C" int lz_gla_prefill(const void* fq, const void* fk, const void* v,
                               const float* log_gamma, void* y, float* state, int batch, int heads,
-                              int kv_heads, int length, int nf, int nd, int gate_per_head,
+                              int kv_heads, int length, int nf, int nd, int gate_mode,
                               int chunk, void* workspace, size_t workspace_bytes, void* stream) {
   if (int rc = check_gla(fq, fk, v, log_gamma, batch, heads, length, nf, nd, chunk, true))
     return rc;
   if (int rc = check_kv_heads("gla_prefill", heads, kv_heads)) return rc;
+  if (int rc = check_gate_mode("gla_prefill", gate_mode)) return rc;
   if (!y || !state) return fail(1, "gla_prefill: null output pointer");
   const size_t need = lz::gla_fwd_workspace(batch, heads, length, nf, nd);
   if (need && (!workspace || workspace_bytes < need))
     return fail(1, "gla_prefill: workspace of %zu bytes given, %zu needed", workspace_bytes,
                 need);
   return hip_status(lz::launch_gla_fwd(fq, fk, v, log_gamma, y, batch, heads, length, nf, nd,
-                                       gate_per_head ? 1 : 0, heads / kv_heads, (float*)workspace,
+                                       gate_mode, heads / kv_heads, (float*)workspace,
                                        state, nullptr, (hipStream_t)stream),
                     "gla_prefill");
 }
 
 extern "C" int lz_gla_decode_step(const void* fq, const void* fk, const void* v,
                                   const float* log_gamma, float* state, void* y, int batch,
-                                  int heads, int kv_heads, int nf, int nd, int gate_per_head,
+                                  int heads, int kv_heads, int nf, int nd, int gate_mode,
                                   void* stream) {
   if (int rc = check_gla(fq, fk, v, log_gamma, batch, heads, 1, nf, nd, 64, true)) return rc;
   if (int rc = check_kv_heads("gla_decode_step", heads, kv_heads)) return rc;
+  if (int rc = check_gate_mode("gla_decode_step", gate_mode)) return rc;
   if (!state || !y) return fail(1, "gla_decode_step: null state or output pointer");
   return hip_status(lz::launch_gla_decode(fq, fk, v, log_gamma, state, y, batch, heads, nf, nd,
-                                          gate_per_head ? 1 : 0, heads / kv_heads,
+                                          gate_mode, heads / kv_heads,
                                           (hipStream_t)stream),
                     "gla_decode_step");
 }
 
 extern "C" size_t lz_gla_bwd_workspace_bytes(int batch, int heads, int length, int nf, int nd,
-                                             int gate_per_head, int chunk) {
+                                             int gate_mode, int chunk) {
   (void)chunk;
   if (batch <= 0 || heads <= 0 || length <= 0 || nf <= 0 || nd <= 0 || nf > LZ_GLA_MAX_DIM ||
       nd > LZ_GLA_MAX_DIM)
     return 0;
-  return lz::gla_bwd_workspace_any(batch, heads, length, nf, nd, gate_per_head ? 1 : 0);
+  return lz::gla_bwd_workspace_any(batch, heads, length, nf, nd, gate_mode);
 }
 
 extern "C" int lz_gla_bwd(const void* fq, const void* fk, const void* v, const float* log_gamma,
                           const void* dy, void* dfq, void* dfk, void* dv, float* dlog_gamma,
                           int grad_bf16, int batch, int heads, int kv_heads, int length, int nf,
-                          int nd, int gate_per_head, int chunk, const void* fwd_workspace,
+                          int nd, int gate_mode, int chunk, const void* fwd_workspace,
                           size_t fwd_workspace_bytes, void* workspace, size_t workspace_bytes,
                           void* stream) {
   if (int rc = check_gla(fq, fk, v, log_gamma, batch, heads, length, nf, nd, chunk, false))
     return rc;
   if (int rc = check_kv_heads("gla_bwd", heads, kv_heads)) return rc;
+  if (int rc = check_gate_mode("gla_bwd", gate_mode)) return rc;
   if (!dy || !dfq || !dfk || !dv || !dlog_gamma) return fail(1, "gla_bwd: null pointer");
   const size_t need =
-      lz::gla_bwd_workspace_any(batch, heads, length, nf, nd, gate_per_head ? 1 : 0);
+      lz::gla_bwd_workspace_any(batch, heads, length, nf, nd, gate_mode);
   if (!workspace || workspace_bytes < need)
     return fail(1, "gla_bwd: workspace of %zu bytes given, %zu needed", workspace_bytes, need);
   // the forward's workspace, if the caller kept it, already holds the state
@@ -232,7 +247,7 @@ extern "C" int lz_gla_bwd(const void* fq, const void* fk, const void* v, const f
   }
   return hip_status(lz::launch_gla_bwd_any(fq, fk, v, log_gamma, dy, dfq, dfk, dv, dlog_gamma,
                                            grad_bf16 != 0, batch, heads, length, nf, nd,
-                                           gate_per_head ? 1 : 0, heads / kv_heads, fws,
+                                           gate_mode, heads / kv_heads, fws,
                                            workspace, (hipStream_t)stream),
                     "gla_bwd");
 }
@@ -299,11 +314,12 @@ extern "C" int lz_init(void) {
 
 extern "C" int lz_gla_fwd_noalloc(const void* fq, const void* fk, const void* v,
                                   const float* log_gamma, void* y, int batch, int heads,
-                                  int kv_heads, int length, int nf, int nd, int gate_per_head,
+                                  int kv_heads, int length, int nf, int nd, int gate_mode,
                                   int chunk, void* stream) {
   if (int rc = check_gla(fq, fk, v, log_gamma, batch, heads, length, nf, nd, chunk, true))
     return rc;
   if (int rc = check_kv_heads("gla_fwd_noalloc", heads, kv_heads)) return rc;
+  if (int rc = check_gate_mode("gla_fwd_noalloc", gate_mode)) return rc;
   if (!y) return fail(1, "gla_fwd_noalloc: null output pointer");
   const size_t need = lz::gla_fwd_workspace(batch, heads, length, nf, nd);
   if (need > (size_t)LZ_GLA_FWD_NOALLOC_MAX_BYTES)
@@ -314,7 +330,7 @@ extern "C" int lz_gla_fwd_noalloc(const void* fq, const void* fk, const void* v,
   if (int rc = noalloc_setup(&ws)) return rc;
   if (!need) ws = nullptr;
   return hip_status(lz::launch_gla_fwd(fq, fk, v, log_gamma, y, batch, heads, length, nf, nd,
-                                       gate_per_head ? 1 : 0, heads / kv_heads, ws, nullptr,
+                                       gate_mode, heads / kv_heads, ws, nullptr,
                                        nullptr, (hipStream_t)stream),
                     "gla_fwd_noalloc");
 }

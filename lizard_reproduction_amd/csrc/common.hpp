@@ -37,6 +37,13 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// Gate mode of the GLA kernels (the C ABI's gate_mode): bit 0, one gate per
+// head ([B, H, L]) rather than per token ([B, L]); bit 1, the buffer holds the
+// gate logit z and log_gamma = logsigmoid(z) is formed where it is read (the
+// layer's F.logsigmoid, src/lizard_attention.py:92), and the gate gradient
+// written is d/dz = d log_gamma * sigmoid(-z).
+constexpr int GATE_PER_HEAD = 1, GATE_LOGIT = 2;
+
 constexpr int WAVE = 64;
 constexpr float TINY = 1.1754943508222875e-38f;   // FLT_MIN, the reference's clamp
 constexpr float LOG2E = 1.4426950408889634f;

@@ -172,7 +172,7 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
     const bf16* __restrict__ fq, const bf16* __restrict__ fk, const bf16* __restrict__ v,
     const float* __restrict__ log_gamma, const bf16* __restrict__ dy, OutT* __restrict__ dfq,
     float* __restrict__ den_out, float* __restrict__ delta_out, float* __restrict__ p_out,
-    const float* __restrict__ seg_state, int H, int L, int F, int D, int gate_per_head, int G,
+    const float* __restrict__ seg_state, int H, int L, int F, int D, int gate, int G,
     int cps, int M, int KG, int xper, int nxcd, int nblk) {
   using Cfg = BwdA<FP, DP>;
   constexpr int C = Cfg::C, PF = Cfg::PF, PD = Cfg::PD;
@@ -217,9 +217,9 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
   const size_t offF = (size_t)bh * L * F, offD = (size_t)bh * L * D, offL = (size_t)bh * L;
   // fk and v of the kv head of this query head (KG query heads share one)
   const size_t offFk = (size_t)(bh / KG) * L * F, offDv = (size_t)(bh / KG) * L * D;
-  const float* lgb = log_gamma + (size_t)(gate_per_head ? bh : bh / H) * L;
+  const float* lgb = log_gamma + (size_t)((gate & GATE_PER_HEAD) ? bh : bh / H) * L;
   const float* st =
-      G > 1 ? seg_state + ((size_t)seg_owner_uniform(bh, KG, gate_per_head) * G + seg) * Cfg::SEG : nullptr;
+      G > 1 ? seg_state + ((size_t)seg_owner_uniform(bh, KG, gate) * G + seg) * Cfg::SEG : nullptr;
 
   // owned S^T tiles (rows d, columns f): i -> (f-tile, d-tile)
   auto s_tile = [&](int i, int& ft, int& dt) __attribute__((always_inline)) -> bool {
@@ -288,6 +288,7 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
   constexpr int DEPTH = Cfg::DEPTH;
   uint4 rq[DEPTH][Cfg::NLF], rk[DEPTH][Cfg::NLF], rv[DEPTH][Cfg::NLD], rd[DEPTH][Cfg::NLD];
   float rg[DEPTH] = {};
+  bool rgok[DEPTH] = {};
   auto issue = [&](auto set, int n) __attribute__((always_inline)) {
     constexpr int S = decltype(set)::value;
     if (n < n1) {
@@ -295,7 +296,10 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
       load_tile8<FP>(rk[S], fk + offFk, n * C, L, F, vecF);
       load_tile8<DP>(rv[S], v + offDv, n * C, L, D, vecD);
       load_tile8<DP>(rd[S], dy + offD, n * C, L, D, vecD);
-      if (wave == GW) rg[S] = gate_at(lgb, n * C + lane, L);
+      if (wave == GW) {
+        rg[S] = gate_at(lgb, n * C + lane, L);
+        rgok[S] = n * C + lane < L;
+      }
     }
   };
   auto stage = [&](auto set) __attribute__((always_inline)) {
@@ -304,7 +308,7 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
     store_tile8<FP>(rk[S], fk_l, PF);
     store_tile8<DP>(rv[S], v_l, PD);
     store_tile8<DP>(rd[S], dy_l, PD);
-    if (wave == GW) gate_scan(rg[S], lane, lgs, qs, ks, rdec);
+    if (wave == GW) gate_scan(rg[S], lane, lgs, qs, ks, rdec, gate, rgok[S]);
   };
   issue(SET0, n0);
   if constexpr (DEPTH == 2) issue(SET1, n0 + 1);
@@ -521,12 +525,22 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
 // ============================================================================
 // per-token scalars of the reverse walks: the gate scan of a chunk plus
 // den (clamped), delta, p and Q^ scale qs/den, by one wave (lane = token)
+// one token's gate value (raw, see gate_scan), den, delta and p, as the
+// reverse walks load them; ok: the token is inside L
+struct TokScalars {
+  float g, den, delta, p;
+  bool ok;
+};
+
 // ============================================================================
-__device__ __forceinline__ void bwd_scalars(float g, float den, float delta, float p, int lane,
+__device__ __forceinline__ void bwd_scalars(const TokScalars& sc, int gate, int lane,
                                             float* lgs, float* qs, float* ks, float* r,
                                             float* invd, float* dels, float* ps, float* qh,
-                                            float* dw) {
-  gate_scan(g, lane, lgs, qs, ks, r);
+                                            float* dw, float* gz = nullptr) {
+  const float den = sc.den, delta = sc.delta, p = sc.p;
+  gate_scan(sc.g, lane, lgs, qs, ks, r, gate, sc.ok);
+  // d log_gamma -> the gate's own gradient (sigmoid(-z) for a logit, else 1)
+  if (gz) gz[lane] = (gate & GATE_LOGIT) ? sigmoid_neg(sc.g) : 1.f;
   const float inv = 1.f / fmaxf(den, TINY);
   const float qhv = qs[lane] * inv;   // Q^_i = fq_i qs_i / den_i
   invd[lane] = inv;
@@ -551,10 +565,6 @@ __device__ __forceinline__ void scale_rows_only(const bf16* tile, int pitch, con
   }
 }
 
-struct TokScalars {
-  float g, den, delta, p;
-};
-
 __device__ __forceinline__ TokScalars load_scalars(const float* __restrict__ lgb,
                                                    const float* __restrict__ den_in,
                                                    const float* __restrict__ delta_in,
@@ -562,6 +572,7 @@ __device__ __forceinline__ TokScalars load_scalars(const float* __restrict__ lgb
                                                    int t, int L) {
   TokScalars s;
   const bool ok = t < L;
+  s.ok = ok;
   s.g = ok ? lgb[t] : 0.f;
   s.den = ok ? den_in[offL + t] : 1.f;
   s.delta = ok ? delta_in[offL + t] : 0.f;
@@ -598,7 +609,7 @@ __global__ __launch_bounds__(256, 2) void gla_bwd_state_kernel(
     const bf16* __restrict__ fq, const bf16* __restrict__ dy, const float* __restrict__ log_gamma,
     const float* __restrict__ den_in, const float* __restrict__ delta_in,
     float* __restrict__ seg_state, float* __restrict__ seg_logdecay, int H, int L, int F, int D,
-    int gate_per_head, int G, int cps) {
+    int gate, int G, int cps) {
   using Cfg = BwdS<FP, DP>;
   constexpr int C = Cfg::C, PF = Cfg::PF, PD = Cfg::PD;
   constexpr int NFT = Cfg::NFT, NDT = Cfg::NDT, NTILE = NFT * NDT, TPW = (NTILE + 3) / 4;
@@ -623,7 +634,7 @@ __global__ __launch_bounds__(256, 2) void gla_bwd_state_kernel(
   const int col = lane & 31, h = lane >> 5;
   const bool vecF = VEC || (F & 7) == 0, vecD = VEC || (D & 7) == 0;
   const size_t offF = (size_t)bh * L * F, offD = (size_t)bh * L * D, offL = (size_t)bh * L;
-  const float* lgb = log_gamma + (size_t)(gate_per_head ? bh : bh / H) * L;
+  const float* lgb = log_gamma + (size_t)((gate & GATE_PER_HEAD) ? bh : bh / H) * L;
 
   f32x16 dS[TPW];
 #pragma unroll
@@ -639,7 +650,7 @@ __global__ __launch_bounds__(256, 2) void gla_bwd_state_kernel(
   store_chunk<FP>(rq, fq_l, PF);
   store_chunk<DP>(rd, dy_l, PD);
   if (wave == 0)
-    bwd_scalars(sc.g, sc.den, sc.delta, 0.f, lane, lgs, qs, ks, rdec, invd, dels, nullptr, qh, dw);
+    bwd_scalars(sc, gate, lane, lgs, qs, ks, rdec, invd, dels, nullptr, qh, dw);
   __syncthreads();
 
   for (int n = n1 - 1; n >= n0; --n) {
@@ -684,7 +695,7 @@ __global__ __launch_bounds__(256, 2) void gla_bwd_state_kernel(
       store_chunk<FP>(rq, fq_l, PF);
       store_chunk<DP>(rd, dy_l, PD);
       if (wave == 0)
-        bwd_scalars(sc.g, sc.den, sc.delta, 0.f, lane, lgs, qs, ks, rdec, invd, dels, nullptr, qh,
+        bwd_scalars(sc, gate, lane, lgs, qs, ks, rdec, invd, dels, nullptr, qh,
                     dw);
     }
     if (tid < FP) dzs[tid] = dzs[tid] * r_n + sum_parts<FP>(dzp, tid);
@@ -754,7 +765,8 @@ struct BwdB : BwdCommon<FP, DP> {
   static constexpr int OFF_KS = OFF_QS + 64 * 4;
   static constexpr int OFF_DZ = OFF_KS + 64 * 4;
   static constexpr int OFF_DZP = OFF_DZ + FP * 4;
-  static constexpr int OFF_R = OFF_DZP + ZP * FP * 4;
+  static constexpr int OFF_GZ = OFF_DZP + ZP * FP * 4;   // [2][64] d log_gamma scales
+  static constexpr int OFF_R = OFF_GZ + 2 * 64 * 4;
   static constexpr int BYTES = OFF_R + 16;
   static constexpr int LB = BYTES <= 80 * 1024 ? 2 : 1;
   static_assert(BYTES <= 160 * 1024, "LDS budget");
@@ -768,7 +780,7 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
     const float* __restrict__ p_in, OutT* __restrict__ dfk, OutT* __restrict__ dv,
     float* __restrict__ dG, float* __restrict__ csum, float* __restrict__ dlg_direct,
     const float* __restrict__ seg_state, int H,
-    int L, int F, int D, int gate_per_head, int G, int cps, int M, int KG, int xper, int nxcd,
+    int L, int F, int D, int gate, int G, int cps, int M, int KG, int xper, int nxcd,
     int nblk) {
   using Cfg = BwdB<FP, DP>;
   constexpr int C = Cfg::C, PF = Cfg::PF, PD = Cfg::PD;
@@ -792,6 +804,7 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
   float* ks = reinterpret_cast<float*>(smem + Cfg::OFF_KS);
   float* dzs = reinterpret_cast<float*>(smem + Cfg::OFF_DZ);
   float* dzp = reinterpret_cast<float*>(smem + Cfg::OFF_DZP);
+  float* gz = reinterpret_cast<float*>(smem + Cfg::OFF_GZ);
   float* rdec = reinterpret_cast<float*>(smem + Cfg::OFF_R);
 
   // a workgroup walks M consecutive segments (seg0 .. seg0 + M - 1) in reverse,
@@ -808,7 +821,7 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
   const size_t offF = (size_t)bh * L * F, offD = (size_t)bh * L * D, offL = (size_t)bh * L;
   // fk and v of the kv head of this query head (KG query heads share one)
   const size_t offFk = (size_t)(bh / KG) * L * F, offDv = (size_t)(bh / KG) * L * D;
-  const float* lgb = log_gamma + (size_t)(gate_per_head ? bh : bh / H) * L;
+  const float* lgb = log_gamma + (size_t)((gate & GATE_PER_HEAD) ? bh : bh / H) * L;
   const float* st = G > 1 ? seg_state + ((size_t)bh * G + seg) * Cfg::SEG : nullptr;
 
   // this wave's dS tiles t = wave + 8 i: f-tile t % NFT, d-tile t / NFT
@@ -870,8 +883,8 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
     store_tile8<DP>(rd[S], dy_l, PD);
     const int b = n & 1;
     if (wave == SCW)
-      bwd_scalars(sc[S].g, sc[S].den, sc[S].delta, sc[S].p, lane, lgs, qs, ks, rdec,
-                  invd + 64 * b, dels + 64 * b, ps + 64 * b, qh + 64 * b, dw + 64 * b);
+      bwd_scalars(sc[S], gate, lane, lgs, qs, ks, rdec, invd + 64 * b, dels + 64 * b,
+                  ps + 64 * b, qh + 64 * b, dw + 64 * b, dlg_direct ? gz + 64 * b : nullptr);
   };
   issue(SET0, n1 - 1);
   if constexpr (DEPTH == 2) issue(SET1, n1 - 2);
@@ -1070,7 +1083,7 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
       if (dlg_direct) {
         // d log_gamma of this chunk: the chunks after it are already summed
         const float suf = wave_suffix_sum(g, lane);
-        if (t0 + lane < L) dlg_direct[offL + t0 + lane] = dlg_after + suf;
+        if (t0 + lane < L) dlg_direct[offL + t0 + lane] = (dlg_after + suf) * gz[64 * cur + lane];
         dlg_after += __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(suf)));
       } else {
 #pragma unroll
@@ -1108,13 +1121,13 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
 constexpr int GATE_CHUNKS_PER_WG = 4;
 
 __global__ __launch_bounds__(64 * GATE_CHUNKS_PER_WG) void gla_gate_grad_kernel(
-    const float* __restrict__ dG, const float* __restrict__ csum, float* __restrict__ dlg, int H,
-    int L, int gate_per_head) {
+    const float* __restrict__ dG, const float* __restrict__ csum,
+    const float* __restrict__ gate_in, float* __restrict__ dlg, int H, int L, int gate) {
   const int row = blockIdx.y, lane = threadIdx.x & 63;
   const int NT = (L + GLA_C - 1) / GLA_C;
   const int c = blockIdx.x * GATE_CHUNKS_PER_WG + (threadIdx.x >> 6);
   if (c >= NT) return;   // whole waves; nothing below synchronises across waves
-  const int nsum = gate_per_head ? 1 : H;
+  const int nsum = (gate & GATE_PER_HEAD) ? 1 : H;
   const rsrc_t src = make_rsrc(dG + (size_t)row * nsum * L, (size_t)nsum * L * 4);
   const rsrc_t cs = make_rsrc(csum + (size_t)row * nsum * NT, (size_t)nsum * NT * 4);
   const int j = c * GLA_C + lane;
@@ -1139,18 +1152,22 @@ __global__ __launch_bounds__(64 * GATE_CHUNKS_PER_WG) void gla_gate_grad_kernel(
   after = wave_prefix_sum(after);
   after = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(after), 63));
   val = wave_suffix_sum(val, lane);   // inclusive suffix sum over the chunk
-  if (j < L) dlg[(size_t)row * L + j] = after + val;
+  if (j < L) {
+    const size_t at = (size_t)row * L + j;
+    // GATE_LOGIT: the gradient of the logit z, d log_gamma * sigmoid(-z)
+    dlg[at] = (gate & GATE_LOGIT) ? (after + val) * sigmoid_neg(gate_in[at]) : after + val;
+  }
 }
 
 // ============================================================================
 // host launchers
 // ============================================================================
-static int gate_rows(int B, int H, int gate_per_head) { return gate_per_head ? B * H : B; }
+static int gate_rows(int B, int H, int gate) { return (gate & GATE_PER_HEAD) ? B * H : B; }
 
 // den, delta, p, dG [BH][L]; forward and reverse segment records; chunk sums
 // of dG [BH][NT]
-size_t gla_bwd_workspace(int B, int H, int L, int F, int D, int gate_per_head) {
-  (void)gate_per_head;
+size_t gla_bwd_workspace(int B, int H, int L, int F, int D, int gate) {
+  (void)gate;
   const int BH = B * H;
   int G, cps;
   gla_segments(BH, L, F, &G, &cps);
@@ -1162,7 +1179,7 @@ size_t gla_bwd_workspace(int B, int H, int L, int F, int D, int gate_per_head) {
 template <int FP, int DP, typename OutT, bool VEC>
 static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v, const float* lg,
                                    const void* dy, void* dfq, void* dfk, void* dv, float* dlg,
-                                   int B, int H, int L, int F, int D, int gate_per_head, int KG,
+                                   int B, int H, int L, int F, int D, int gate, int KG,
                                    const float* fwd_ws, float* ws, const float* ext_den,
                                    const float* ext_delta, hipStream_t st) {
   const int BH = B * H;
@@ -1187,7 +1204,7 @@ static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v
   hipError_t e;
   if (G > 1 && !fwd_ws) {
     e = launch_gla_fwd_states(fk, v, lg, own_fseg, own_fseg + (size_t)BH * G * SEG, BH, H, L, F,
-                              D, gate_per_head, G, cps, KG, st);
+                              D, gate, G, cps, KG, st);
     if (e != hipSuccess) return e;
   }
   // the walks take two segments per workgroup while that still gives one
@@ -1197,7 +1214,7 @@ static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v
   auto launch_a = [&](auto kern) {
     hipLaunchKernelGGL(kern, dim3(wg.grid), dim3(B_THREADS), LDS_A, st, (const bf16*)fq,
                        (const bf16*)fk, (const bf16*)v, lg, (const bf16*)dy, (OutT*)dfq, den,
-                       delta, p, fseg, H, L, F, D, gate_per_head, G, cps, M, KG, wg.per, wg.nx,
+                       delta, p, fseg, H, L, F, D, gate, G, cps, M, KG, wg.per, wg.nx,
                        wg.nblk);
   };
   if (ext) {
@@ -1216,28 +1233,27 @@ static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v
     float* rlam = rseg + (size_t)BH * G * SEG;
     hipLaunchKernelGGL(ks, dim3(BH * (G - 1)), dim3(256), LDS_S, st,
                        (const bf16*)fq, (const bf16*)dy, lg, (const float*)den,
-                       (const float*)delta, rseg, rlam, H, L, F, D, gate_per_head, G, cps);
+                       (const float*)delta, rseg, rlam, H, L, F, D, gate, G, cps);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if ((e = launch_gla_segment_scan(rseg, rlam, BH, G, SEG, true, st)) != hipSuccess) return e;
   }
   // a per-head gate in one segment: the reverse walk of (b, h) sees its whole
   // gate row and writes d log_gamma itself (no gate launch, no dG)
-  const bool direct_dlg = gate_per_head && G == 1;
+  const bool direct_dlg = (gate & GATE_PER_HEAD) && G == 1;
   auto kb = gla_bwd_dkv_kernel<FP, DP, OutT, VEC>;
   if ((e = ensure_lds<gla_bwd_dkv_kernel<FP, DP, OutT, VEC>>(LDS_B)) != hipSuccess) return e;
   hipLaunchKernelGGL(kb, dim3(wg.grid), dim3(B_THREADS), LDS_B, st, (const bf16*)fq,
                      (const bf16*)fk, (const bf16*)v, lg, (const bf16*)dy, (const float*)den,
                      (const float*)delta, (const float*)p, (OutT*)dfk, (OutT*)dv, dG, csum,
-                     direct_dlg ? dlg : nullptr, (const float*)rseg, H, L, F, D, gate_per_head, G,
+                     direct_dlg ? dlg : nullptr, (const float*)rseg, H, L, F, D, gate, G,
                      cps, M, KG, wg.per, wg.nx, wg.nblk);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   if (direct_dlg) return hipSuccess;
   const int nt = (L + GLA_C - 1) / GLA_C;
   const dim3 ggrid((nt + GATE_CHUNKS_PER_WG - 1) / GATE_CHUNKS_PER_WG,
-                   gate_rows(B, H, gate_per_head));
+                   gate_rows(B, H, gate));
   hipLaunchKernelGGL(gla_gate_grad_kernel, ggrid, dim3(64 * GATE_CHUNKS_PER_WG), 0, st,
-                     (const float*)dG,
-                     (const float*)csum, dlg, H, L, gate_per_head);
+                     (const float*)dG, (const float*)csum, lg, dlg, H, L, gate);
   return hipGetLastError();
 }
 
@@ -1245,14 +1261,14 @@ static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v
 // dimension) den and delta [BH, L] of the whole feature dimension
 hipError_t launch_gla_bwd(const void* fq, const void* fk, const void* v, const float* lg,
                           const void* dy, void* dfq, void* dfk, void* dv, float* dlg,
-                          bool grad_bf16, int B, int H, int L, int F, int D, int gate_per_head,
+                          bool grad_bf16, int B, int H, int L, int F, int D, int gate,
                           int KG, const float* fwd_ws, float* ws, const float* ext_den,
                           const float* ext_delta, hipStream_t st) {
   const int fp = gla_padded_dim(F), dp = gla_padded_dim(D);
   const bool vec = F % 8 == 0 && D % 8 == 0;
 #define LZ_GLA_BWD_V(FPV, DPV, OUT, V)                                                          \
   launch_gla_bwd_t<FPV, DPV, OUT, V>(fq, fk, v, lg, dy, dfq, dfk, dv, dlg, B, H, L, F, D,      \
-                                     gate_per_head, KG, fwd_ws, ws, ext_den, ext_delta, st)
+                                     gate, KG, fwd_ws, ws, ext_den, ext_delta, st)
 #define LZ_GLA_BWD(FPV, DPV)                                                                    \
   if (fp == FPV && dp == DPV)                                                                   \
     return grad_bf16 ? (vec ? LZ_GLA_BWD_V(FPV, DPV, bf16, true)                                \

@@ -30,25 +30,25 @@ GlaTiles gla_tiles(int F, int D);
 // The native walks (F, D within gla_dims_supported).  raw_den: see
 // gla_fwd_kernel's RAW; ext_den / ext_delta: see gla_bwd_dq_kernel's EXT.
 size_t gla_fwd_workspace(int B, int H, int L, int F, int D);
-size_t gla_bwd_workspace(int B, int H, int L, int F, int D, int gate_per_head);
+size_t gla_bwd_workspace(int B, int H, int L, int F, int D, int gate);
 hipError_t launch_gla_fwd(const void* fq, const void* fk, const void* v, const float* lg, void* y,
-                          int B, int H, int L, int F, int D, int gate_per_head, int KG, float* ws,
+                          int B, int H, int L, int F, int D, int gate, int KG, float* ws,
                           float* final_state, float* raw_den, hipStream_t st);
 hipError_t launch_gla_bwd(const void* fq, const void* fk, const void* v, const float* lg,
                           const void* dy, void* dfq, void* dfk, void* dv, float* dlg,
-                          bool grad_bf16, int B, int H, int L, int F, int D, int gate_per_head,
+                          bool grad_bf16, int B, int H, int L, int F, int D, int gate,
                           int KG, const float* fwd_ws, float* ws, const float* ext_den,
                           const float* ext_delta, hipStream_t st);
 // Any F and D: the native walks, or tiles of them (gla_tiled.hip).
 size_t gla_fwd_workspace_any(int B, int H, int L, int F, int D);
-size_t gla_bwd_workspace_any(int B, int H, int L, int F, int D, int gate_per_head);
+size_t gla_bwd_workspace_any(int B, int H, int L, int F, int D, int gate);
 hipError_t launch_gla_fwd_any(const void* fq, const void* fk, const void* v, const float* lg,
-                              void* y, int B, int H, int L, int F, int D, int gate_per_head,
+                              void* y, int B, int H, int L, int F, int D, int gate,
                               int KG, void* ws, hipStream_t st);
 hipError_t launch_gla_bwd_any(const void* fq, const void* fk, const void* v, const float* lg,
                               const void* dy, void* dfq, void* dfk, void* dv, float* dlg,
                               bool grad_bf16, int B, int H, int L, int F, int D,
-                              int gate_per_head, int KG, const float* fwd_ws, void* ws,
+                              int gate, int KG, const float* fwd_ws, void* ws,
                               hipStream_t st);
 // Sets, on the current device, the LDS limit of every kernel launch_gla_fwd
 // (without raw_den) and launch_gla_fwd_states can launch.
@@ -232,10 +232,28 @@ __device__ __forceinline__ float wave_suffix_sum(float x, int lane) {
   return __shfl(x, 63 - lane);
 }
 
+
+// logsigmoid(z) = min(z, 0) - log1p(e^{-|z|}), no overflow for any z
+__device__ __forceinline__ float log_sigmoid(float z) {
+  return fminf(z, 0.f) - log1pf(__expf(-fabsf(z)));
+}
+
+// d logsigmoid(z) / dz = sigmoid(-z) = 1 / (1 + e^z) (0 when e^z overflows)
+__device__ __forceinline__ float sigmoid_neg(float z) { return 1.f / (1.f + __expf(z)); }
+
+// log_gamma from a gate buffer value of a token inside L, in mode `gate`
+__device__ __forceinline__ float gate_log(float g, int gate) {
+  return (gate & GATE_LOGIT) ? log_sigmoid(g) : g;
+}
+
 // Chunk-local inclusive scan of the gate by one wave (lane = token): lg,
-// e^{lg}, e^{lg_end - lg}, and e^{lg_end}, lg_end in r[0], r[1].
+// e^{lg}, e^{lg_end - lg}, and e^{lg_end}, lg_end in r[0], r[1].  g is the
+// lane's raw gate value (0 past L); in GATE_LOGIT mode it is the logit,
+// turned into logsigmoid(g) here (where it is used, so a prefetched gate is
+// not waited for at its load) and 0 for a token past L (`valid` false).
 __device__ __forceinline__ void gate_scan(float g, int lane, float* lgs, float* qs, float* ks,
-                                          float* r) {
+                                          float* r, int gate, bool valid) {
+  if (gate & GATE_LOGIT) g = valid ? log_sigmoid(g) : 0.f;
   g = wave_prefix_sum(g);
   const float end = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(g), 63));
   lgs[lane] = g;
@@ -275,7 +293,8 @@ __device__ __forceinline__ float decay_tile(const f32x16& s, const float* lgs, i
   return rsum;
 }
 
-// log_gamma of token t of a gate row of length L, 0 past its end
+// raw gate value of token t of a gate row of length L, 0 past its end (the
+// mode is applied where it is used: gate_scan)
 __device__ __forceinline__ float gate_at(const float* __restrict__ lgb, int t, int L) {
   return bload_f32(make_rsrc(lgb, (size_t)L * 4), (uint32_t)t * 4u);
 }
@@ -327,15 +346,15 @@ __device__ __forceinline__ bool walk_block(int xper, int nx, int nblk, int& blk)
 // KG query heads of a kv head then see the same fk, v and gate, hence the same
 // segment states, which the state pass computes once.  The record of query
 // head bh:
-__host__ __device__ inline int seg_owner(int bh, int KG, int gate_per_head) {
-  return gate_per_head ? bh : bh / KG;
+__host__ __device__ inline int seg_owner(int bh, int KG, int gate) {
+  return (gate & GATE_PER_HEAD) ? bh : bh / KG;
 }
 // The same inside a walk, marked wave-uniform: used as written above in the
 // record pointer, it led the compiler to take the walks' chunk buffer
 // resources for divergent and to wrap every chunk load in a readfirstlane
 // loop.
-__device__ __forceinline__ int seg_owner_uniform(int bh, int KG, int gate_per_head) {
-  return __builtin_amdgcn_readfirstlane(seg_owner(bh, KG, gate_per_head));
+__device__ __forceinline__ int seg_owner_uniform(int bh, int KG, int gate) {
+  return __builtin_amdgcn_readfirstlane(seg_owner(bh, KG, gate));
 }
 
 // Per-(b, h, segment) state record: S [FP][DP] fp32, then z [FP].
@@ -348,7 +367,7 @@ struct SegRec {
 // segments; used by the forward and by the backward's forward walk.
 hipError_t launch_gla_fwd_states(const void* fk, const void* v, const float* lg, float* seg_state,
                                  float* seg_logdecay, int BH, int H, int L, int F, int D,
-                                 int gate_per_head, int G, int cps, int KG, hipStream_t st);
+                                 int gate, int G, int cps, int KG, hipStream_t st);
 hipError_t launch_gla_segment_scan(float* seg_state, const float* seg_logdecay, int BH, int G,
                                    int rec, bool reverse, hipStream_t st);
 

@@ -84,7 +84,7 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
     const bf16* __restrict__ fq, const bf16* __restrict__ fk, const bf16* __restrict__ v,
     const float* __restrict__ log_gamma, bf16* __restrict__ y,
     const float* __restrict__ seg_state, float* __restrict__ final_state, int H, int L, int F,
-    int D, int gate_per_head, int G, int cps, int M, int KG, float* __restrict__ raw_num,
+    int D, int gate, int G, int cps, int M, int KG, float* __restrict__ raw_num,
     float* __restrict__ raw_den, int xper, int nxcd, int nblk) {
   using Cfg = GlaFwd<FP, DP>;
   constexpr int C = Cfg::C, PF = Cfg::PF, PD = Cfg::PD;
@@ -121,9 +121,9 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
   const bf16* fkb = fk + (size_t)(bh / KG) * L * F;
   const bf16* vb = v + (size_t)(bh / KG) * L * D;
   const rsrc_t yr = make_rsrc(y + (size_t)bh * L * D, (size_t)L * D * 2);
-  const float* lgb = log_gamma + (size_t)(gate_per_head ? bh : bh / H) * L;
+  const float* lgb = log_gamma + (size_t)((gate & GATE_PER_HEAD) ? bh : bh / H) * L;
   const float* st =
-      G > 1 ? seg_state + ((size_t)seg_owner_uniform(bh, KG, gate_per_head) * G + seg) * Cfg::SEG : nullptr;
+      G > 1 ? seg_state + ((size_t)seg_owner_uniform(bh, KG, gate) * G + seg) * Cfg::SEG : nullptr;
 
   const bool active = RD::active(wave);
   auto dtile = [&](int i) { return RD::tile(wave, i); };
@@ -152,7 +152,7 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
   store_chunk<FP>(rq, fq_l, PF);
   store_chunk<FP>(rk, fk_l, PF);
   store_chunk<DP>(rv, v_l, PD);
-  if (wave == 0) gate_scan(rg, lane, lgs, qs, ks, rdec);
+  if (wave == 0) gate_scan(rg, lane, lgs, qs, ks, rdec, gate, n0 * C + lane < L);
   __syncthreads();
 
   for (int n = n0; n < n1; ++n) {
@@ -287,7 +287,7 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
       store_chunk<FP>(rq, fq_l, PF);
       store_chunk<FP>(rk, fk_l, PF);
       store_chunk<DP>(rv, v_l, PD);
-      if (wave == 0) gate_scan(rg, lane, lgs, qs, ks, rdec);
+      if (wave == 0) gate_scan(rg, lane, lgs, qs, ks, rdec, gate, t0 + C + lane < L);
     }
     if (tid < FP) zs[tid] = zs[tid] * r_n + sum_parts<FP>(zp, tid);
     __syncthreads();
@@ -381,7 +381,7 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void gla_fwd_wide_kernel(
     const bf16* __restrict__ fq, const bf16* __restrict__ fk, const bf16* __restrict__ v,
     const float* __restrict__ log_gamma, bf16* __restrict__ y,
     const float* __restrict__ seg_state, float* __restrict__ final_state, int H, int L, int F,
-    int D, int gate_per_head, int G, int cps, int M, int KG, float* __restrict__ raw_num,
+    int D, int gate, int G, int cps, int M, int KG, float* __restrict__ raw_num,
     float* __restrict__ raw_den, int xper, int nxcd, int nblk) {
   using Cfg = GlaFwdWide<DP>;
   constexpr int FP = Cfg::FP, C = Cfg::C, PF = Cfg::PF, PD = Cfg::PD;
@@ -414,8 +414,8 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void gla_fwd_wide_kernel(
   const bf16* fkb = fk + (size_t)(bh / KG) * L * F;   // fk, v: the kv head of this query head
   const bf16* vb = v + (size_t)(bh / KG) * L * D;
   const rsrc_t yr = make_rsrc(y + (size_t)bh * L * D, (size_t)L * D * 2);
-  const float* lgb = log_gamma + (size_t)(gate_per_head ? bh : bh / H) * L;
-  const float* st = G > 1 ? seg_state + ((size_t)seg_owner_uniform(bh, KG, gate_per_head) * G + seg) *
+  const float* lgb = log_gamma + (size_t)((gate & GATE_PER_HEAD) ? bh : bh / H) * L;
+  const float* st = G > 1 ? seg_state + ((size_t)seg_owner_uniform(bh, KG, gate) * G + seg) *
                                             SegRec<FP, DP>::SIZE
                           : nullptr;
 
@@ -458,7 +458,7 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void gla_fwd_wide_kernel(
   store_chunk512<FP>(rq, fq_l, PF);
   store_chunk512<FP>(rk, fk_l, PF);
   store_chunk512<DP>(rv, v_l, PD);
-  if (wave == 0) gate_scan(rg, lane, lgs, qs, ks, rdec);
+  if (wave == 0) gate_scan(rg, lane, lgs, qs, ks, rdec, gate, n0 * C + lane < L);
   publish();
   __syncthreads();
 
@@ -560,7 +560,7 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void gla_fwd_wide_kernel(
       store_chunk512<FP>(rq, fq_l, PF);
       store_chunk512<FP>(rk, fk_l, PF);
       store_chunk512<DP>(rv, v_l, PD);
-      if (wave == 0) gate_scan(rg, lane, lgs, qs, ks, rdec);
+      if (wave == 0) gate_scan(rg, lane, lgs, qs, ks, rdec, gate, t0 + C + lane < L);
     }
     if (tid < FP) zs[tid] = zs[tid] * r_n + sum_parts<FP>(zp, tid);
     __syncthreads();
@@ -598,12 +598,12 @@ template <int DP>
 __global__ __launch_bounds__(256) void gla_decode_kernel(
     const bf16* __restrict__ fq, const bf16* __restrict__ fk, const bf16* __restrict__ v,
     const float* __restrict__ log_gamma, float* __restrict__ state, bf16* __restrict__ y, int H,
-    int F, int D, int gate_per_head, int KG) {
+    int F, int D, int gate, int KG) {
   constexpr int NG = 256 / DP;
   __shared__ float fq_s[256], fk_s[256], part[256], red[4];
   const int bh = blockIdx.x, tid = threadIdx.x;
   const int g = tid / DP, d = tid % DP;
-  const float gam = fexp(log_gamma[gate_per_head ? bh : bh / H]);
+  const float gam = fexp(gate_log(log_gamma[(gate & GATE_PER_HEAD) ? bh : bh / H], gate));
   const bf16* fqb = fq + (size_t)bh * F;
   const bf16* fkb = fk + (size_t)(bh / KG) * F;
   float* Sb = state + (size_t)bh * ((size_t)F * D + F);
@@ -656,7 +656,7 @@ template <int IPT>
 __global__ __launch_bounds__(512) void gla_decode_vec_kernel(
     const bf16* __restrict__ fq, const bf16* __restrict__ fk, const bf16* __restrict__ v,
     const float* __restrict__ log_gamma, float* __restrict__ state, bf16* __restrict__ y, int H,
-    int F, int D, int gate_per_head, int KG) {
+    int F, int D, int gate, int KG) {
   __shared__ float fq_s[256], fk_s[256], red[8];
   __shared__ f32x4 part[8 * 32];
   const int bh = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -672,7 +672,7 @@ __global__ __launch_bounds__(512) void gla_decode_vec_kernel(
   f32x4 s[IPT];
 #pragma unroll
   for (int i = 0; i < IPT; ++i) s[i] = __builtin_bit_cast(f32x4, bload16(sr, soff(i)));
-  const float gam = fexp(log_gamma[gate_per_head ? bh : bh / H]);
+  const float gam = fexp(gate_log(log_gamma[(gate & GATE_PER_HEAD) ? bh : bh / H], gate));
   for (int f = tid; f < F; f += 512) {
     fq_s[f] = to_f32(fq[(size_t)bh * F + f]);
     fk_s[f] = to_f32(fk[(size_t)(bh / KG) * F + f]);
@@ -725,14 +725,14 @@ __global__ __launch_bounds__(512) void gla_decode_vec_kernel(
 
 hipError_t launch_gla_decode(const void* fq, const void* fk, const void* v, const float* lg,
                              float* state, void* y, int B, int H, int F, int D,
-                             int gate_per_head, int KG, hipStream_t st) {
+                             int gate, int KG, hipStream_t st) {
   if (F % 4 == 0 && D >= 4 && D <= 128 && (D & (D - 1)) == 0) {
     const int rg = 512 / (D / 4), need = (F + rg - 1) / rg;   // rows per thread
 #define LZ_GLA_DECV(IPTV)                                                                     \
     if (need <= IPTV) {                                                                       \
       hipLaunchKernelGGL(gla_decode_vec_kernel<IPTV>, dim3(B * H), dim3(512), 0, st,          \
                          (const bf16*)fq, (const bf16*)fk, (const bf16*)v, lg, state,         \
-                         (bf16*)y, H, F, D, gate_per_head, KG);                               \
+                         (bf16*)y, H, F, D, gate, KG);                               \
       return hipGetLastError();                                                               \
     }
     LZ_GLA_DECV(1) LZ_GLA_DECV(2) LZ_GLA_DECV(4) LZ_GLA_DECV(8)
@@ -743,7 +743,7 @@ hipError_t launch_gla_decode(const void* fq, const void* fk, const void* v, cons
   if (dp == DPV) {                                                                          \
     hipLaunchKernelGGL(gla_decode_kernel<DPV>, dim3(B * H), dim3(256), 0, st,                 \
                        (const bf16*)fq, (const bf16*)fk, (const bf16*)v, lg, state, (bf16*)y, \
-                       H, F, D, gate_per_head, KG);                                           \
+                       H, F, D, gate, KG);                                           \
     return hipGetLastError();                                                               \
   }
   LZ_GLA_DEC(32) LZ_GLA_DEC(64) LZ_GLA_DEC(128) LZ_GLA_DEC(256)
@@ -813,7 +813,7 @@ template <int FP, int DP, bool VEC, int FR>
 __global__ __launch_bounds__(256, 2) void gla_fwd_state_kernel(
     const bf16* __restrict__ fk, const bf16* __restrict__ v, const float* __restrict__ log_gamma,
     float* __restrict__ seg_state, float* __restrict__ seg_logdecay, int H, int L, int F, int D,
-    int gate_per_head, int G, int cps, int KG) {
+    int gate, int G, int cps, int KG) {
   using Cfg = GlaState<FP, DP>;
   constexpr int C = Cfg::C, PF = Cfg::PF, PD = Cfg::PD;
   constexpr int NFT = Cfg::NFT, NDT = Cfg::NDT;
@@ -843,7 +843,7 @@ __global__ __launch_bounds__(256, 2) void gla_fwd_state_kernel(
   const int fcols = F - f0;   // valid columns from f0 (<= 0: none, the slice is zero)
   const size_t fk_bytes = fcols > 0 ? ((size_t)L * F - f0) * 2 : 0;
   const bf16* vb = v + (size_t)(bh / KG) * L * D;
-  const float* lgb = log_gamma + (size_t)(gate_per_head ? bh : bh / H) * L;
+  const float* lgb = log_gamma + (size_t)((gate & GATE_PER_HEAD) ? bh : bh / H) * L;
   auto load_fk = [&](uint4 (&reg)[Cfg::NLF], int t) {
     if constexpr (NFS == 1)
       load_chunk<FP>(reg, fkb, t, L, F, vecF);
@@ -911,7 +911,9 @@ __global__ __launch_bounds__(256, 2) void gla_fwd_state_kernel(
   load_chunk<DP>(rv, vb, n0 * C, L, D, vecD);
   {
     const int pb = n0 & 1;
-    if (wave == 0) gate_scan(rg, lane, lgs + 64 * pb, qs + 64 * pb, ks + 64 * pb, rdec + 4 * pb);
+    if (wave == 0)
+      gate_scan(rg, lane, lgs + 64 * pb, qs + 64 * pb, ks + 64 * pb, rdec + 4 * pb, gate,
+                n0 * C + lane < L);
     __syncthreads();
     stage_scaled(rk, ks + 64 * pb, zp + 2048 * pb);
     store_chunk<DP>(rv, v_l, PD);
@@ -946,7 +948,8 @@ __global__ __launch_bounds__(256, 2) void gla_fwd_state_kernel(
     }
     if constexpr (NFS > 1) slice_parts(zp + 2048 * pc);
     if (more && wave == 0)
-      gate_scan(rg, lane, lgs + 64 * pn, qs + 64 * pn, ks + 64 * pn, rdec + 4 * pn);
+      gate_scan(rg, lane, lgs + 64 * pn, qs + 64 * pn, ks + 64 * pn, rdec + 4 * pn, gate,
+                tn + lane < L);
     __syncthreads();
     // staging and the next loads at raised wave priority, as in the walk
     __builtin_amdgcn_s_setprio(1);
@@ -1082,7 +1085,7 @@ hipError_t launch_gla_segment_scan(float* seg_state, const float* seg_logdecay, 
 template <int FS, int FR, int DP, bool VEC>
 static hipError_t launch_state_slices(const void* fk, const void* v, const float* lg,
                                       float* seg_state, float* seg_logdecay, int BH, int H, int L,
-                                      int F, int D, int gate_per_head, int G, int cps, int KG,
+                                      int F, int D, int gate, int G, int cps, int KG,
                                       hipStream_t st) {
   using Cfg = GlaState<FS, DP>;
   auto ks = gla_fwd_state_kernel<FS, DP, VEC, FR>;
@@ -1090,7 +1093,7 @@ static hipError_t launch_state_slices(const void* fk, const void* v, const float
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(ks, dim3(BH * (G - 1) * (FR / FS)), dim3(256), Cfg::BYTES, st,
                      (const bf16*)fk, (const bf16*)v, lg, seg_state, seg_logdecay, H, L, F, D,
-                     gate_per_head, G, cps, KG);
+                     gate, G, cps, KG);
   return hipGetLastError();
 }
 
@@ -1105,9 +1108,9 @@ static int gla_state_slices(int workgroups, int FP) {
 template <int FP, int DP, bool VEC>
 static hipError_t launch_gla_fwd_states_t(const void* fk, const void* v, const float* lg,
                                           float* seg_state, float* seg_logdecay, int BH, int H,
-                                          int L, int F, int D, int gate_per_head, int G, int cps,
+                                          int L, int F, int D, int gate, int G, int cps,
                                           int KG, hipStream_t st) {
-  if (!gate_per_head && KG > 1) {   // one record per kv head (seg_owner)
+  if (!(gate & GATE_PER_HEAD) && KG > 1) {   // one record per kv head (seg_owner)
     BH /= KG;
     H /= KG;
     KG = 1;
@@ -1117,23 +1120,23 @@ static hipError_t launch_gla_fwd_states_t(const void* fk, const void* v, const f
   if constexpr (FP == 256) {
     if (nfs == 4)
       e = launch_state_slices<64, FP, DP, VEC>(fk, v, lg, seg_state, seg_logdecay, BH, H, L, F,
-                                               D, gate_per_head, G, cps, KG, st);
+                                               D, gate, G, cps, KG, st);
     else if (nfs == 2)
       e = launch_state_slices<128, FP, DP, VEC>(fk, v, lg, seg_state, seg_logdecay, BH, H, L, F,
-                                                D, gate_per_head, G, cps, KG, st);
+                                                D, gate, G, cps, KG, st);
     else
       e = launch_state_slices<FP, FP, DP, VEC>(fk, v, lg, seg_state, seg_logdecay, BH, H, L, F,
-                                               D, gate_per_head, G, cps, KG, st);
+                                               D, gate, G, cps, KG, st);
   } else if constexpr (FP == 128) {
     if (nfs == 2)
       e = launch_state_slices<64, FP, DP, VEC>(fk, v, lg, seg_state, seg_logdecay, BH, H, L, F,
-                                               D, gate_per_head, G, cps, KG, st);
+                                               D, gate, G, cps, KG, st);
     else
       e = launch_state_slices<FP, FP, DP, VEC>(fk, v, lg, seg_state, seg_logdecay, BH, H, L, F,
-                                               D, gate_per_head, G, cps, KG, st);
+                                               D, gate, G, cps, KG, st);
   } else {
     e = launch_state_slices<FP, FP, DP, VEC>(fk, v, lg, seg_state, seg_logdecay, BH, H, L, F, D,
-                                             gate_per_head, G, cps, KG, st);
+                                             gate, G, cps, KG, st);
   }
   if (e != hipSuccess) return e;
   return launch_gla_segment_scan(seg_state, seg_logdecay, BH, G, SegRec<FP, DP>::SIZE, false,
@@ -1142,16 +1145,16 @@ static hipError_t launch_gla_fwd_states_t(const void* fk, const void* v, const f
 
 hipError_t launch_gla_fwd_states(const void* fk, const void* v, const float* lg, float* seg_state,
                                  float* seg_logdecay, int BH, int H, int L, int F, int D,
-                                 int gate_per_head, int G, int cps, int KG, hipStream_t st) {
+                                 int gate, int G, int cps, int KG, hipStream_t st) {
   const int fp = gla_padded_dim(F), dp = gla_padded_dim(D);
   const bool vec = F % 8 == 0 && D % 8 == 0;
 #define LZ_GLA_ST(FPV, DPV)                                                                   \
   if (fp == FPV && dp == DPV)                                                                 \
     return vec ? launch_gla_fwd_states_t<FPV, DPV, true>(fk, v, lg, seg_state, seg_logdecay,  \
-                                                         BH, H, L, F, D, gate_per_head, G,    \
+                                                         BH, H, L, F, D, gate, G,    \
                                                          cps, KG, st)                         \
                : launch_gla_fwd_states_t<FPV, DPV, false>(fk, v, lg, seg_state, seg_logdecay, \
-                                                          BH, H, L, F, D, gate_per_head, G,   \
+                                                          BH, H, L, F, D, gate, G,   \
                                                           cps, KG, st);
   LZ_GLA_ST(32, 32) LZ_GLA_ST(32, 64) LZ_GLA_ST(32, 128)
   LZ_GLA_ST(64, 32) LZ_GLA_ST(64, 64) LZ_GLA_ST(64, 128)
@@ -1164,7 +1167,7 @@ hipError_t launch_gla_fwd_states(const void* fk, const void* v, const float* lg,
 template <int FP, int DP, bool VEC, bool RAW>
 static hipError_t launch_gla_fwd_t(const void* fq, const void* fk, const void* v,
                                    const float* lg, void* y, int B, int H, int L, int F, int D,
-                                   int gate_per_head, int KG, float* ws, float* final_state,
+                                   int gate, int KG, float* ws, float* final_state,
                                    float* raw_den, hipStream_t st) {
   using Cfg = GlaFwd<FP, DP>;
   const int BH = B * H;
@@ -1174,7 +1177,7 @@ static hipError_t launch_gla_fwd_t(const void* fq, const void* fk, const void* v
   if (G > 1) {
     hipError_t e = launch_gla_fwd_states_t<FP, DP, VEC>(fk, v, lg, seg_state,
                                                    ws + (size_t)BH * G * Cfg::SEG, BH, H, L, F,
-                                                   D, gate_per_head, G, cps, KG, st);
+                                                   D, gate, G, cps, KG, st);
     if (e != hipSuccess) return e;
   }
   const int M = gla_walk_segments(BH, G, F);
@@ -1186,7 +1189,7 @@ static hipError_t launch_gla_fwd_t(const void* fq, const void* fk, const void* v
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(kern, dim3(wg.grid), dim3(WIDE_THREADS), W::BYTES, st,
                        (const bf16*)fq, (const bf16*)fk, (const bf16*)v, lg, (bf16*)y,
-                       (const float*)seg_state, final_state, H, L, F, D, gate_per_head, G, cps,
+                       (const float*)seg_state, final_state, H, L, F, D, gate, G, cps,
                        M, KG, RAW ? (float*)y : nullptr, raw_den, wg.per, wg.nx, wg.nblk);
     return hipGetLastError();
   } else {
@@ -1195,7 +1198,7 @@ static hipError_t launch_gla_fwd_t(const void* fq, const void* fk, const void* v
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(kern, dim3(wg.grid), dim3(256), Cfg::BYTES, st, (const bf16*)fq,
                        (const bf16*)fk, (const bf16*)v, lg, (bf16*)y, (const float*)seg_state,
-                       final_state, H, L, F, D, gate_per_head, G, cps, M, KG,
+                       final_state, H, L, F, D, gate, G, cps, M, KG,
                        RAW ? (float*)y : nullptr, raw_den, wg.per, wg.nx, wg.nblk);
     return hipGetLastError();
   }
@@ -1244,16 +1247,16 @@ hipError_t gla_fwd_prepare() {
 // feature dimension) y is the fp32 numerator [BH, L, D] and raw_den the fp32
 // denominator [BH, L] of this tile (see gla_fwd_kernel's RAW).
 hipError_t launch_gla_fwd(const void* fq, const void* fk, const void* v, const float* lg, void* y,
-                          int B, int H, int L, int F, int D, int gate_per_head, int KG, float* ws,
+                          int B, int H, int L, int F, int D, int gate, int KG, float* ws,
                           float* final_state, float* raw_den, hipStream_t st) {
   const int fp = gla_padded_dim(F), dp = gla_padded_dim(D);
   const bool vec = F % 8 == 0 && D % 8 == 0;
 #define LZ_GLA_FWD_R(FPV, DPV, V)                                                               \
   (raw_den ? launch_gla_fwd_t<FPV, DPV, V, true>(fq, fk, v, lg, y, B, H, L, F, D,               \
-                                                 gate_per_head, KG, ws, final_state, raw_den,   \
+                                                 gate, KG, ws, final_state, raw_den,   \
                                                  st)                                            \
            : launch_gla_fwd_t<FPV, DPV, V, false>(fq, fk, v, lg, y, B, H, L, F, D,              \
-                                                  gate_per_head, KG, ws, final_state, nullptr,  \
+                                                  gate, KG, ws, final_state, nullptr,  \
                                                   st))
 #define LZ_GLA_FWD(FPV, DPV)                                                                    \
   if (fp == FPV && dp == DPV)                                                                   \

@@ -271,7 +271,7 @@ struct BwdBufs {
 };
 
 BwdBufs carve_bwd(Carve& c, const GlaTiles& t, int B, int H, int L, int F, int D, int gph) {
-  const size_t BHL = (size_t)B * H * L, NG = gph ? BHL : (size_t)B * L;
+  const size_t BHL = (size_t)B * H * L, NG = (gph & GATE_PER_HEAD) ? BHL : (size_t)B * L;
   BwdBufs b{};
   if (t.nF > 1) b.fwd = carve_fwd(c, t, B, H, L, F, D);
   b.vt = c.take<bf16>(BHL * t.Dt);
@@ -312,7 +312,7 @@ hipError_t launch_gla_bwd_any(const void* fq, const void* fk, const void* v, con
                           KG, fwd_ws, (float*)ws, nullptr, nullptr, st);
   Carve c{(char*)ws};
   const BwdBufs b = carve_bwd(c, t, B, H, L, F, D, gph);
-  const size_t BHL = (size_t)B * H * L, BHLk = BHL / KG, NG = gph ? BHL : (size_t)B * L;
+  const size_t BHL = (size_t)B * H * L, BHLk = BHL / KG, NG = (gph & GATE_PER_HEAD) ? BHL : (size_t)B * L;
   hipError_t e;
   if (t.nF > 1) {   // num, den of the whole feature dimension, then delta per D tile
     if ((e = raw_forward(t, b.fwd, fq, fk, v, lg, B, H, L, F, D, gph, KG, st))) return e;

@@ -147,13 +147,23 @@ def gla_native(nf, nd):
     return fp is not None and dp is not None and dp <= 128 and (fp <= 128 or dp <= 64)
 
 
-def gla_forward(fq, fk, v, lg, keep_state=True, chunk=CHUNK):
+# gate_mode bits of the C ABI (include/lizard_hip.h)
+GATE_PER_HEAD, GATE_LOGIT = 1, 2
+
+
+def _gate_mode(lg, gate_logit):
+    return (GATE_PER_HEAD if lg.dim() == 3 else 0) | (GATE_LOGIT if gate_logit else 0)
+
+
+def gla_forward(fq, fk, v, lg, keep_state=True, chunk=CHUNK, gate_logit=False):
     """One ``lz_gla_fwd`` launch on bf16 contiguous fq, fk, v and fp32
     contiguous log_gamma; returns (y, state), state being the workspace of
     the states entering each sequence segment, which ``gla_backward`` reuses
     (None when not kept, not needed, or for tiled sizes past the walks').  fk and v may have fewer heads than
     fq (a divisor: grouped-query attention, each kv head shared by
-    consecutive query heads)."""
+    consecutive query heads).  With ``gate_logit`` lg holds the gate's logit
+    z and the kernels use log_gamma = logsigmoid(z) (the layer's
+    F.logsigmoid, src/lizard_attention.py:92)."""
     _check_kv("gla_forward", fq, fk, v, fq.shape[-1], v.shape[-1])
     _check_gate("gla_forward", fq, lg)
     b, h, length, nf = fq.shape
@@ -162,19 +172,20 @@ def gla_forward(fq, fk, v, lg, keep_state=True, chunk=CHUNK):
     ws = None
     if y.numel():
         lib = _lib.load()
-        per_head = int(lg.dim() == 3)
-        nbytes = _gla_fwd_ws(b, h, length, nf, nd, per_head, chunk)
+        mode = _gate_mode(lg, gate_logit)
+        nbytes = _gla_fwd_ws(b, h, length, nf, nd, mode & GATE_PER_HEAD, chunk)
         ws = torch.empty(nbytes, dtype=torch.uint8, device=fq.device) if nbytes else None
         rc = lib.lz_gla_fwd(_ptr(fq), _ptr(fk), _ptr(v), _ptr(lg), _ptr(y), b, h, fk.shape[1],
-                            length, nf, nd, per_head, chunk, _ptr(ws), nbytes, _stream(fq))
+                            length, nf, nd, mode, chunk, _ptr(ws), nbytes, _stream(fq))
         _lib.check(rc, "lz_gla_fwd")
     return y, (ws if keep_state and gla_native(nf, nd) else None)
 
 
-def gla_backward(fq, fk, v, lg, dy, state, grad_dtype, chunk=CHUNK):
+def gla_backward(fq, fk, v, lg, dy, state, grad_dtype, chunk=CHUNK, gate_logit=False):
     """One ``lz_gla_bwd`` launch: (dfq, dfk, dv) in grad_dtype (bf16 or
-    fp32) and dlog_gamma fp32 in log_gamma's layout.  dfk and dv are per
-    query head, also when fk and v have fewer (kv) heads."""
+    fp32) and dlog_gamma fp32 in log_gamma's layout (with ``gate_logit``,
+    the gradient of the logit lg holds).  dfk and dv are per query head,
+    also when fk and v have fewer (kv) heads."""
     _check_kv("gla_backward", fq, fk, v, fq.shape[-1], v.shape[-1])
     _check_gate("gla_backward", fq, lg)
     b, h, length, nf = fq.shape
@@ -187,12 +198,12 @@ def gla_backward(fq, fk, v, lg, dy, state, grad_dtype, chunk=CHUNK):
     dlg = torch.empty_like(lg)
     if dy.numel():
         lib = _lib.load()
-        per_head = int(lg.dim() == 3)
-        nbytes = _gla_bwd_ws(b, h, length, nf, nd, per_head, chunk)
+        mode = _gate_mode(lg, gate_logit)
+        nbytes = _gla_bwd_ws(b, h, length, nf, nd, mode & GATE_PER_HEAD, chunk)
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=fq.device)
         rc = lib.lz_gla_bwd(_ptr(fq), _ptr(fk), _ptr(v), _ptr(lg), _ptr(dy), _ptr(dfq),
                             _ptr(dfk), _ptr(dv), _ptr(dlg), int(grad_dtype == torch.bfloat16),
-                            b, h, fk.shape[1], length, nf, nd, per_head, chunk, _ptr(state),
+                            b, h, fk.shape[1], length, nf, nd, mode, chunk, _ptr(state),
                             state.numel() if state is not None else 0, _ptr(ws), ws.numel(),
                             _stream(fq))
         _lib.check(rc, "lz_gla_bwd")
@@ -228,13 +239,14 @@ class _GLA(torch.autograd.Function):
         return _cast_grads(grads, ctx.dtypes) + (None,)
 
 
-def gla_prefill(fq, fk, v, log_gamma, chunk=CHUNK):
+def gla_prefill(fq, fk, v, log_gamma, chunk=CHUNK, gate_logit=False):
     """``gla`` forward (no autograd) that also returns the recurrent state
     after the last token, for decoding: ``(y, state)``, state fp32
     ``[B, H, F*D + F]`` (S row-major ``[F][D]``, then z ``[F]``; see
     ``split_state``).  The reference has no decode path; the state is that of
     its recurrent form (tests/test_lizard.py:41-52).  fk and v may have fewer
-    heads than fq (a divisor, as in ``gla_forward``)."""
+    heads than fq (a divisor, as in ``gla_forward``); ``gate_logit`` as
+    there."""
     if not isinstance(chunk, int) or chunk < 16 or chunk & (chunk - 1):
         raise ValueError(f"gla_prefill: chunk must be a power of two >= 16, got {chunk!r}")
     _check_kv("gla_prefill", fq, fk, v, fq.shape[-1], v.shape[-1])
@@ -248,11 +260,11 @@ def gla_prefill(fq, fk, v, log_gamma, chunk=CHUNK):
     state = torch.zeros(b, h, nf * nd + nf, device=fq.device, dtype=torch.float32)
     if y.numel():
         lib = _lib.load()
-        per_head = int(lg.dim() == 3)
-        nbytes = _gla_fwd_ws(b, h, length, nf, nd, per_head, chunk)
+        mode = _gate_mode(lg, gate_logit)
+        nbytes = _gla_fwd_ws(b, h, length, nf, nd, mode & GATE_PER_HEAD, chunk)
         ws = torch.empty(nbytes, dtype=torch.uint8, device=fq.device) if nbytes else None
         rc = lib.lz_gla_prefill(_ptr(fq), _ptr(fk), _ptr(v), _ptr(lg), _ptr(y), _ptr(state), b, h,
-                                fk.shape[1], length, nf, nd, per_head, chunk, _ptr(ws), nbytes,
+                                fk.shape[1], length, nf, nd, mode, chunk, _ptr(ws), nbytes,
                                 _stream(fq))
         _lib.check(rc, "lz_gla_prefill")
     return y, state
@@ -269,14 +281,15 @@ def split_state(state, nf, nd):
     return state[..., :nf * nd].view(b, h, nf, nd), state[..., nf * nd:]
 
 
-def gla_decode_step(fq, fk, v, log_gamma, state):
+def gla_decode_step(fq, fk, v, log_gamma, state, gate_logit=False):
     """One token per (b, h) on the recurrent form, updating ``state`` in place
     (tests/test_lizard.py:41-52): S <- gamma S + fk v^T, z <- gamma z + fk,
     y = fq S / max(fq . z, FLT_MIN), gamma = exp(log_gamma).
 
     fq ``[B, H, F]``, fk ``[B, Hkv, F]``, v ``[B, Hkv, D]`` (cast to bf16;
     Hkv divides H, query head h reads kv head h // (H // Hkv)), log_gamma
-    ``[B]`` or ``[B, H]`` fp32, state from ``gla_prefill`` or ``new_state``.
+    ``[B]`` or ``[B, H]`` fp32 (with ``gate_logit`` the gate's logit z,
+    log_gamma = logsigmoid(z)), state from ``gla_prefill`` or ``new_state``.
     Returns bf16 ``[B, H, D]``; no autograd."""
     if fq.dim() != 3 or fk.dim() != 3 or v.dim() != 3:
         raise ValueError(f"gla_decode_step: fq [B, H, F], fk [B, Hkv, F] and v [B, Hkv, D] "
@@ -301,7 +314,8 @@ def gla_decode_step(fq, fk, v, log_gamma, state):
     lg = log_gamma.float().contiguous()
     y = torch.empty(b, h, nd, device=v.device, dtype=torch.bfloat16)
     rc = _lib.load().lz_gla_decode_step(_ptr(fq), _ptr(fk), _ptr(v), _ptr(lg), _ptr(state),
-                                        _ptr(y), b, h, hk, nf, nd, int(lg.dim() == 2),
+                                        _ptr(y), b, h, hk, nf, nd,
+                                        int(lg.dim() == 2) | (GATE_LOGIT if gate_logit else 0),
                                         _stream(fq))
     _lib.check(rc, "lz_gla_decode_step")
     return y

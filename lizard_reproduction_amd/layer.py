@@ -19,8 +19,9 @@ with everything after the projections in promote(x.dtype, fp32).  The
 projections and the gate logit are torch GEMMs; everything from the
 projection outputs to o_proj's input runs on HIP kernels: the fused
 prologue (GQA expand, Hedgehog feature maps, RoPE and the bf16 casts, one
-pass over q/k/v), the GLA and SWA kernels, and the fused blend + transpose,
-one autograd node for all of them (``_Core``).
+pass over q/k/v), the GLA kernels (which take the logit z and form
+logsigmoid(z) and its derivative themselves) and the SWA kernels, and the
+fused blend + transpose, one autograd node for all of them (``_Core``).
 
 Decoding (no counterpart in the reference, which has no decode path):
 ``prefill`` runs the forward over a prompt and returns a ``LizardCache`` --
@@ -193,15 +194,18 @@ class _Core(torch.autograd.Function):
     the size of the rounding its bf16 projections already take)."""
 
     @staticmethod
-    def forward(ctx, qp, kp, vp, wq, wk, log_gamma, meta, alpha, cos, sin, heads, kv_heads,
+    def forward(ctx, qp, kp, vp, wq, wk, z, meta, alpha, cos, sin, heads, kv_heads,
                 window, out_dtype):
+        # z is the gate logit [B, L]: the GLA kernels form log_gamma =
+        # logsigmoid(z) where they read it and return the gradient of z
+        # (src/lizard_attention.py:92, F.logsigmoid, fused)
         fq, fk, qr, kr, v, saved = prologue_forward(qp, kp, vp, wq, wk, cos, sin, heads,
                                                     kv_heads)
-        lg = log_gamma.float().contiguous()
+        lg = z.float().contiguous()
         meta32 = meta.float().contiguous()
         alpha32 = alpha.detach().float().reshape(1).contiguous()
         grad = any(ctx.needs_input_grad[:8])
-        y_gla, state = kernels.gla_forward(fq, fk, v, lg, keep_state=grad)
+        y_gla, state = kernels.gla_forward(fq, fk, v, lg, keep_state=grad, gate_logit=True)
         y_swa, lse = kernels.swa_forward(qr, kr, v, meta32, window)
         odt = torch.bfloat16 if out_dtype == torch.bfloat16 else torch.float32
         out = combine_forward(y_gla, y_swa, alpha32, odt)
@@ -210,7 +214,7 @@ class _Core(torch.autograd.Function):
                                   *saved[:6])
             ctx.state, ctx.sizes = state, saved[6]
         ctx.window = window
-        ctx.dtypes = (qp.dtype, kp.dtype, vp.dtype, wq.dtype, wk.dtype, log_gamma.dtype,
+        ctx.dtypes = (qp.dtype, kp.dtype, vp.dtype, wq.dtype, wk.dtype, z.dtype,
                       meta.dtype, alpha.dtype)
         return out.to(out_dtype)
 
@@ -221,11 +225,12 @@ class _Core(torch.autograd.Function):
         odt = torch.bfloat16 if dout.dtype == torch.bfloat16 else torch.float32
         dyg, dys, dalpha = combine_backward(dout.to(odt).contiguous(), y_swa, alpha32)
         bf = torch.bfloat16
-        dfq, dfk, dv_gla, dlg = kernels.gla_backward(fq, fk, v, lg, dyg, ctx.state, bf)
+        dfq, dfk, dv_gla, dz = kernels.gla_backward(fq, fk, v, lg, dyg, ctx.state, bf,
+                                                    gate_logit=True)
         dqr, dkr, dv_swa, dmeta = kernels.swa_backward(qr, kr, v, meta32, lse, dys, ctx.window,
                                                        bf)
         dq, dk, dvp, dwq, dwk = prologue_backward(saved, dfq, dfk, dqr, dkr, dv_gla, dv_swa)
-        grads = (dq, dk, dvp, dwq, dwk, dlg, dmeta, dalpha.reshape(()))
+        grads = (dq, dk, dvp, dwq, dwk, dz, dmeta, dalpha.reshape(()))
         return tuple(g.to(d) for g, d in zip(grads, ctx.dtypes)) + (None,) * 6
 
 
@@ -320,9 +325,9 @@ class LizardAttention(nn.Module):
         if not self._fused(qp, kp, vp, cos, sin):
             y = self._unfused(qp, kp, vp, F.logsigmoid(z), cos, sin, dtype).to(x.dtype)
             return self.o_proj(y.transpose(1, 2).flatten(2)), None
-        y = _Core.apply(qp, kp, vp, self.phi_q.weight, self.phi_k.weight, F.logsigmoid(z),
-                        self.meta_tokens, self.alpha_blend, cos, sin, self.heads, self.kv_heads,
-                        self.window, x.dtype)
+        y = _Core.apply(qp, kp, vp, self.phi_q.weight, self.phi_k.weight, z, self.meta_tokens,
+                        self.alpha_blend, cos, sin, self.heads, self.kv_heads, self.window,
+                        x.dtype)
         return self.o_proj(y), None
 
     def _unfused(self, qp, kp, vp, log_gamma, cos, sin, dtype):
@@ -376,12 +381,12 @@ class LizardAttention(nn.Module):
                              f"shapes and the GLA decode kernels' (F = {nf}, D = "
                              f"{self.head_dim} is not one: F <= 256, D <= 128, D <= 64 when "
                              "F > 128)")
-        dtype = torch.promote_types(x.dtype, torch.float32)
-        lg = F.logsigmoid(self.W_gamma(x).to(dtype).squeeze(-1)).float().contiguous()
+        # the gate logit: the GLA kernels take logsigmoid of it themselves
+        z = self.W_gamma(x).float().squeeze(-1).contiguous()
         fq, fk, qr, kr, v, _ = prologue_forward(qp, kp, vp, self.phi_q.weight,
                                                 self.phi_k.weight, cos, sin, self.heads,
                                                 self.kv_heads)
-        return lg, fq, fk, qr, kr, v
+        return z, fq, fk, qr, kr, v
 
     def _out(self, y_gla, y_swa, x):
         alpha = self.alpha_blend.detach().float().reshape(1).contiguous()
@@ -393,8 +398,8 @@ class LizardAttention(nn.Module):
         """``forward`` over a prompt [B, L, hidden] (no autograd) that also
         returns the decode cache after it: ``(out, cache)``."""
         x = hidden_states
-        lg, fq, fk, qr, kr, v = self._operands(x, position_embeddings)
-        y_gla, state = kernels.gla_prefill(fq, fk, v, lg)
+        z, fq, fk, qr, kr, v = self._operands(x, position_embeddings)
+        y_gla, state = kernels.gla_prefill(fq, fk, v, z, gate_logit=True)
         y_swa, _ = kernels.swa_forward(qr, kr, v, self.meta_tokens.detach().float().contiguous(),
                                        self.window)
         cache = self.new_cache(x.shape[0], x.device)
@@ -412,10 +417,10 @@ class LizardAttention(nn.Module):
         if x.dim() != 3 or x.shape[1] != 1:
             raise ValueError(f"LizardAttention.step: hidden_states must be [B, 1, hidden], got "
                              f"{tuple(x.shape)}")
-        lg, fq, fk, qr, kr, v = self._operands(x, position_embeddings)
+        z, fq, fk, qr, kr, v = self._operands(x, position_embeddings)
         cache.put(kr, v, cache.pos)
-        y_gla = kernels.gla_decode_step(fq[:, :, 0], fk[:, :, 0], v[:, :, 0], lg[:, 0],
-                                        cache.state)
+        y_gla = kernels.gla_decode_step(fq[:, :, 0], fk[:, :, 0], v[:, :, 0], z[:, 0].contiguous(),
+                                        cache.state, gate_logit=True)
         y_swa = kernels.swa_decode_step(qr[:, :, 0], cache.k, cache.v,
                                         self.meta_tokens.detach().float().contiguous(),
                                         cache.pos)

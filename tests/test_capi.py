@@ -122,6 +122,22 @@ def test_bad_sizes_are_rejected_before_any_launch(lib):
 
 
 @no_gpu
+def test_gate_mode_bits_are_checked(lib):
+    """gate_mode takes LZ_GATE_PER_HEAD (1) and LZ_GATE_LOGIT (2) only."""
+    p = ctypes.c_void_p(16)   # never dereferenced: validation fails first
+    refused(lib, lib.lz_gla_fwd(p, p, p, p, p, 1, 1, 1, 8, 16, 16, 4, 64, None, 0, None),
+            b"gate_mode")
+    refused(lib, lib.lz_gla_decode_step(p, p, p, p, p, p, 1, 4, 2, 64, 64, 8, None), b"gate_mode")
+    ws = lib.lz_gla_bwd_workspace_bytes(1, 1, 8, 16, 16, 3, 64)
+    rc = lib.lz_gla_bwd(p, p, p, p, p, p, p, p, p, 0, 1, 1, 1, 8, 16, 16, -1, 64, None, 0, p, ws,
+                        None)
+    refused(lib, rc, b"gate_mode")
+    text = open(HEADER).read()
+    assert "#define LZ_GATE_PER_HEAD 1" in text and "#define LZ_GATE_LOGIT 2" in text
+    assert (kernels.GATE_PER_HEAD, kernels.GATE_LOGIT) == (1, 2)
+
+
+@no_gpu
 def test_decode_entry_points_reject_bad_arguments(lib):
     p = ctypes.c_void_p(16)   # never dereferenced: validation fails first
     # lz_swa_decode_step(q, k_cache, v_cache, meta, n_meta, y, B, H, kv_heads, window, dim,
