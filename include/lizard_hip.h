@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define LZ_ABI_VERSION 13
+#define LZ_ABI_VERSION 14
 
 /*
  * gate_mode of the GLA entry points: a combination of
@@ -150,6 +150,32 @@ int lz_gla_prefill(const void* fq, const void* fk, const void* v, const float* l
                    void* stream);
 
 /*
+ * GLA forward with the feature map of q formed inside the walk.  Replaces
+ * hedgehog(q, phi_q) (src/lizard_attention.py:9-11, 85) followed by
+ * kernels.gla's forward (src/kernels/gla.py:213-263), for a layer's
+ * forward without autograd (inference, prefill): fq is never written to
+ * memory; each chunk's fq = [softmax(q Wq^T), softmax(-q Wq^T)] is formed
+ * from the q rows and Wq in the walk, with the arithmetic of
+ * lz_layer_prologue_fwd (bf16 products, fp32 softmax, bf16 result).
+ *   q          bf16 [B, L, heads, head_dim]  (the q_proj output, not RoPE'd)
+ *   wq         bf16 [feature_dim, head_dim]  (phi_q.weight)
+ *   fk         bf16 [B, kv_heads, L, 2 feature_dim]  (lz_layer_prologue_fwd's fk)
+ *   v          bf16 [B, kv_heads, L, head_dim]
+ *   y          bf16 [B, heads, L, head_dim]
+ *   state      f32 [B, heads, nf*nd + nf] (nf = 2 feature_dim, nd = head_dim): the
+ *              recurrent state after the last token as lz_gla_prefill writes it,
+ *              or NULL
+ * Other arguments as lz_gla_fwd, whose workspace (lz_gla_fwd_workspace_bytes
+ * with nf = 2 feature_dim, nd = head_dim) this takes.  Sizes: head_dim 64,
+ * feature_dim 128 (the config of Llama-3.2-1B with the reference's default
+ * feature_dim); a batch row of q under 2 GiB.
+ */
+int lz_gla_fwd_phi(const void* q, const void* wq, const void* fk, const void* v,
+                   const float* log_gamma, void* y, float* state, int batch, int heads,
+                   int kv_heads, int length, int head_dim, int feature_dim, int gate_mode,
+                   int chunk, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * GLA decode step: one new token per (b, h) on the recurrent form
  * (tests/test_lizard.py:41-52), state updated in place:
  *   S <- gamma S + fk v^T,  z <- gamma z + fk,  y = fq S / max(fq . z, FLT_MIN)
@@ -251,7 +277,9 @@ int lz_swa_bwd(const void* q, const void* k, const void* v, const float* meta, i
  *   wq, wk      [feature_dim, head_dim]     (phi_q.weight, phi_k.weight)
  *   cos, sin    [B, L, head_dim] if cos_batched else [L, head_dim]
  *   all of them bf16 if dtype_bf16 else f32.
- *   fq          bf16 [B, heads, L, 2 feature_dim]: [softmax(q Wq^T), softmax(-q Wq^T)]
+ *   fq          bf16 [B, heads, L, 2 feature_dim]: [softmax(q Wq^T), softmax(-q Wq^T)],
+ *               or NULL: then the q rows are only rotated (qr), for lz_gla_fwd_phi,
+ *               which forms their feature map itself
  *   fk          bf16 [B, kv_heads, L, 2 feature_dim]: the same of k with Wk
  *   qr          bf16 [B, heads, L, head_dim]: rotate_half RoPE of q
  *   kr, v_out   bf16 [B, kv_heads, L, head_dim]: RoPE of k; v

@@ -8,7 +8,7 @@ import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "_lib", "liblizard_hip.so")
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -24,6 +24,8 @@ SIGNATURES = {
     "lz_gla_fwd": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _S, _P]),
     "lz_gla_fwd_noalloc": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "lz_gla_prefill": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _S,
+                            _P]),
+    "lz_gla_fwd_phi": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _S,
                             _P]),
     "lz_gla_decode_step": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
     "lz_gla_bwd_workspace_bytes": (_S, [_I, _I, _I, _I, _I, _I, _I]),

@@ -13,6 +13,9 @@ namespace lz {
 hipError_t launch_gla_fwd(const void* fq, const void* fk, const void* v, const float* lg, void* y,
                           int B, int H, int L, int F, int D, int gate_per_head, int KG, float* ws,
                           float* final_state, float* raw_den, hipStream_t st);
+hipError_t launch_gla_fwd_phi(const void* q, const void* wq, const void* fk, const void* v,
+                              const float* lg, void* y, int B, int H, int L, int gate, int KG,
+                              float* ws, float* final_state, hipStream_t st);
 hipError_t launch_gla_decode(const void* fq, const void* fk, const void* v, const float* lg,
                              float* state, void* y, int B, int H, int F, int D,
                              int gate_per_head, int KG, hipStream_t st);
@@ -193,6 +196,33 @@ extern "C" int lz_gla_prefill(const void* fq, const void* fk, const void* v,
                                        gate_mode, heads / kv_heads, (float*)workspace,
                                        state, nullptr, (hipStream_t)stream),
                     "gla_prefill");
+}
+
+extern "C" int lz_gla_fwd_phi(const void* q, const void* wq, const void* fk, const void* v,
+                              const float* log_gamma, void* y, float* state, int batch, int heads,
+                              int kv_heads, int length, int head_dim, int feature_dim,
+                              int gate_mode, int chunk, void* workspace, size_t workspace_bytes,
+                              void* stream) {
+  if (head_dim != 64 || feature_dim != 128)
+    return fail(1, "gla_fwd_phi: head_dim %d x feature_dim %d unsupported (the walk forms the "
+                   "feature map at head_dim 64, feature_dim 128)", head_dim, feature_dim);
+  const int nf = 2 * feature_dim, nd = head_dim;
+  if (int rc = check_gla(fk, fk, v, log_gamma, batch, heads, length, nf, nd, chunk, true))
+    return rc;
+  if (int rc = check_kv_heads("gla_fwd_phi", heads, kv_heads)) return rc;
+  if (int rc = check_gate_mode("gla_fwd_phi", gate_mode)) return rc;
+  if (!q || !wq || !y) return fail(1, "gla_fwd_phi: null q, wq or output pointer");
+  if ((size_t)length * heads * head_dim * 2 >= ((size_t)1 << 31))
+    return fail(1, "gla_fwd_phi: a batch row of q (%d x %d x %d bf16) must stay under 2 GiB",
+                length, heads, head_dim);
+  const size_t need = lz::gla_fwd_workspace(batch, heads, length, nf, nd);
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(1, "gla_fwd_phi: workspace of %zu bytes given, %zu needed", workspace_bytes,
+                need);
+  return hip_status(lz::launch_gla_fwd_phi(q, wq, fk, v, log_gamma, y, batch, heads, length,
+                                           gate_mode, heads / kv_heads, (float*)workspace,
+                                           state, (hipStream_t)stream),
+                    "gla_fwd_phi");
 }
 
 extern "C" int lz_gla_decode_step(const void* fq, const void* fk, const void* v,
@@ -437,7 +467,7 @@ extern "C" int lz_layer_prologue_fwd(const void* q, const void* k, const void* v
     return rc;
   if (!q || !k || !v || !wq || !wk || !cos || !sin)
     return fail(1, "layer_prologue_fwd: null input pointer");
-  if (!fq || !fk || !qr || !kr || !v_out) return fail(1, "layer_prologue_fwd: null output pointer");
+  if (!fk || !qr || !kr || !v_out) return fail(1, "layer_prologue_fwd: null output pointer");
   return hip_status(lz::launch_prologue_fwd(q, k, v, wq, wk, cos, sin, fq, fk, qr, kr, v_out,
                                             dtype_bf16 != 0, batch, length, heads, kv_heads,
                                             head_dim, feature_dim, cos_batched ? length : 0,

@@ -355,6 +355,13 @@ struct GlaFwdWide {
   static constexpr int OFF_R = OFF_ZP + RowItems<FP>::PARTS * FP * 4;
   static constexpr int BYTES = OFF_R + 16;
   static_assert(BYTES <= 160 * 1024, "LDS budget");
+  // PHI: softmax statistics of q W^T per (token tile, 32-feature tile, token),
+  // and W [128][PW] bf16 (head_dim 64)
+  static constexpr int PW = lds_pitch(64);
+  static constexpr int OFF_PS = BYTES;
+  static constexpr int OFF_W = OFF_PS + 2 * 4 * 32 * 16;
+  static constexpr int PHI_BYTES = OFF_W + 128 * PW * 2;
+  static_assert(PHI_BYTES <= 160 * 1024, "LDS budget");
 };
 
 // rows [t0, t0+64) of a [L x ncols] bf16 matrix by the 512 threads (item
@@ -376,13 +383,25 @@ __device__ __forceinline__ void store_chunk512(const uint4 (&reg)[N], bf16* tile
   }
 }
 
-template <int DP, bool VEC, bool RAW>
+// PHI: fq is not read.  The walk forms it from the q rows of the projection
+// output (qrow, [B, L, H, 64] bf16) and the feature weights (wphi, [128][64]
+// bf16) chunk by chunk: fq = [softmax(q W^T), softmax(-q W^T)] (the Hedgehog
+// map, src/lizard_attention.py:9-11, F = 256), as the layer prologue does:
+// the same bf16 MFMA product (A = W rows, B = q rows, k over head_dim in the
+// same order, so x W^T is bitwise the prologue's), fp32 softmax with the row
+// maximum subtracted, bf16 result.  Wave w forms 32-feature tile w >> 1 of
+// 32-token tile w & 1; the statistics of a token's four tiles meet in LDS
+// (written in phase 2, read in the tail, where the chunk is staged: no barrier
+// of its own), combined as max M and sum of s_j e^{m_j - M}.
+template <int DP, bool VEC, bool RAW, bool PHI>
 __global__ __launch_bounds__(WIDE_THREADS, 1) void gla_fwd_wide_kernel(
     const bf16* __restrict__ fq, const bf16* __restrict__ fk, const bf16* __restrict__ v,
     const float* __restrict__ log_gamma, bf16* __restrict__ y,
     const float* __restrict__ seg_state, float* __restrict__ final_state, int H, int L, int F,
     int D, int gate, int G, int cps, int M, int KG, float* __restrict__ raw_num,
-    float* __restrict__ raw_den, int xper, int nxcd, int nblk) {
+    float* __restrict__ raw_den, int xper, int nxcd, int nblk, const bf16* __restrict__ qrow,
+    const bf16* __restrict__ wphi) {
+  static_assert(!(PHI && RAW), "the feature map is formed for whole-F walks only");
   using Cfg = GlaFwdWide<DP>;
   constexpr int FP = Cfg::FP, C = Cfg::C, PF = Cfg::PF, PD = Cfg::PD;
   constexpr int NFT = Cfg::NFT, NDT = Cfg::NDT, S_OWN = Cfg::S_OWN;
@@ -449,17 +468,106 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void gla_fwd_wide_kernel(
     }
   };
 
+  // ---- PHI: the feature map of q, formed per chunk -------------------------
+  constexpr int PHD = 64, PHK = PHD / 16;   // head_dim of q and W; MFMA k-steps
+  const int ptt = wave & 1, pft = wave >> 1;
+  uint4 px[PHK];     // the next chunk's q rows of token tile ptt (B operand)
+  f32x16 pacc;       // q W^T tile: features 32 pft + acc_row (registers) x tokens (lanes)
+  f32x4* pst = reinterpret_cast<f32x4*>(smem + Cfg::OFF_PS);
+  bf16* w_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_W);   // W, for the whole walk
+  // q rows of this (b, h): token t at (t H) PHD elements past its first row
+  const rsrc_t qrs = make_rsrc(
+      PHI ? qrow + ((size_t)(bh / H) * L * H + (size_t)(bh % H)) * PHD : nullptr,
+      PHI ? ((size_t)(L - 1) * H + 1) * PHD * 2 : 0);
+  if constexpr (PHI) {
+    for (int i = tid; i < 128 * PHD / 8; i += WIDE_THREADS)
+      *reinterpret_cast<uint4*>(w_l + (i / (PHD / 8)) * Cfg::PW + 8 * (i % (PHD / 8))) =
+          reinterpret_cast<const uint4*>(wphi)[i];
+  }
+  auto phi_load = [&](int t) __attribute__((always_inline)) {   // chunk starting at t
+    const int row = t + 32 * ptt + col;
+#pragma unroll
+    for (int kb = 0; kb < PHK; ++kb)
+      px[kb] = bload16(qrs, row < L ? (uint32_t)((row * H * PHD + 16 * kb + 8 * h) * 2) : OOB);
+  };
+  // this wave's tile of q W^T and its per-token statistics (max and sum of
+  // e^{x - max} over the tile's 32 features, both signs) into LDS
+  auto phi_partial = [&]() __attribute__((always_inline)) {
+    pacc = zero16();
+#pragma unroll
+    for (int kb = 0; kb < PHK; ++kb)
+      pacc = mfma(row_operand(w_l, Cfg::PW, 32 * pft + col, 16 * kb, h),
+                  __builtin_bit_cast(bf16x8, px[kb]), pacc);
+    float mp = pacc[0], mn = -pacc[0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) {
+      mp = fmaxf(mp, pacc[r]);
+      mn = fmaxf(mn, -pacc[r]);
+    }
+    mp = fmaxf(mp, xhalf(mp));
+    mn = fmaxf(mn, xhalf(mn));
+    float sp = 0.f, sn = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      sp += fexp(pacc[r] - mp);
+      sn += fexp(-pacc[r] - mn);
+    }
+    sp += xhalf(sp);
+    sn += xhalf(sn);
+    if (h == 0) pst[(ptt * 4 + pft) * 32 + col] = f32x4{mp, sp, mn, sn};
+  };
+  // after a barrier: the token's statistics over all 128 features, and this
+  // wave's 32 features of both halves of its fq row into fq_l (zero past L)
+  auto phi_write = [&](int t) __attribute__((always_inline)) {
+    f32x4 g[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) g[j] = pst[(ptt * 4 + j) * 32 + col];
+    const float Mp = fmaxf(fmaxf(g[0][0], g[1][0]), fmaxf(g[2][0], g[3][0]));
+    const float Mn = fmaxf(fmaxf(g[0][2], g[1][2]), fmaxf(g[2][2], g[3][2]));
+    float Sp = 0.f, Sn = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      Sp += g[j][1] * fexp(g[j][0] - Mp);
+      Sn += g[j][3] * fexp(g[j][2] - Mn);
+    }
+    const float ip = 1.f / Sp, in = 1.f / Sn;
+    const int tok = 32 * ptt + col;
+    const bool live = t + tok < L;
+    bf16* row = fq_l + tok * PF + 32 * pft;
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      bf16x4 op, on;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float x = pacc[4 * q4 + e];
+        op[e] = to_bf16(live ? fexp(x - Mp) * ip : 0.f);
+        on[e] = to_bf16(live ? fexp(-x - Mn) * in : 0.f);
+      }
+      *reinterpret_cast<bf16x4*>(row + 8 * q4 + 4 * h) = op;
+      *reinterpret_cast<bf16x4*>(row + 128 + 8 * q4 + 4 * h) = on;
+    }
+  };
+
   uint4 rq[Cfg::NLF], rk[Cfg::NLF], rv[Cfg::NLD];
   float rg;
-  load_chunk512<FP>(rq, fqb, n0 * C, L, F, vecF);
+  if constexpr (PHI)
+    phi_load(n0 * C);
+  else
+    load_chunk512<FP>(rq, fqb, n0 * C, L, F, vecF);
   load_chunk512<FP>(rk, fkb, n0 * C, L, F, vecF);
   load_chunk512<DP>(rv, vb, n0 * C, L, D, vecD);
   rg = gate_at(lgb, n0 * C + lane, L);
-  store_chunk512<FP>(rq, fq_l, PF);
+  if constexpr (!PHI) store_chunk512<FP>(rq, fq_l, PF);
   store_chunk512<FP>(rk, fk_l, PF);
   store_chunk512<DP>(rv, v_l, PD);
   if (wave == 0) gate_scan(rg, lane, lgs, qs, ks, rdec, gate, n0 * C + lane < L);
   publish();
+  if constexpr (PHI) {
+    __syncthreads();   // W in LDS
+    phi_partial();
+    __syncthreads();
+    phi_write(n0 * C);
+  }
   __syncthreads();
 
   // phase-1 roles: score tile (kt, qt) of waves 0, 1, 3; Q~.z groups of wave
@@ -472,7 +580,10 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void gla_fwd_wide_kernel(
     const int t0 = n * C;
     const bool more = n + 1 < n1;
     if (more) {   // next chunk in flight while this one computes
-      load_chunk512<FP>(rq, fqb, t0 + C, L, F, vecF);
+      if constexpr (PHI)
+        phi_load(t0 + C);
+      else
+        load_chunk512<FP>(rq, fqb, t0 + C, L, F, vecF);
       load_chunk512<FP>(rk, fkb, t0 + C, L, F, vecF);
       load_chunk512<DP>(rv, vb, t0 + C, L, D, vecD);
       rg = gate_at(lgb, t0 + C + lane, L);
@@ -514,6 +625,11 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void gla_fwd_wide_kernel(
     if (wave >= 4) store_rows_t<FP>(kti, fk_l, PF, tid - 256);   // fk_l holds K~ from here
     __syncthreads();
     // ---- phase 2: outputs (waves 4 .. 3 + 2 NDT), state update (all) ---------
+    // PHI: the next chunk's q W^T tile and its statistics, waves 0-3 first
+    // (their phase 2 is the state update only), waves 4-7 after their outputs
+    if constexpr (PHI) {
+      if (more && wave < 4) phi_partial();
+    }
     const float r_n = rdec[0];
     if (wave >= 4 && wave < 4 + 2 * NDT) {
       const int dt = (wave - 4) >> 1, qt = (wave - 4) & 1;
@@ -553,11 +669,18 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void gla_fwd_wide_kernel(
                       tr_operand(v_l, PD, 16 * kb, dt * 32, lane), S[i]);
       }
     }
+    if constexpr (PHI) {
+      if (more && wave >= 4) phi_partial();
+    }
     __syncthreads();
-    // ---- publish S^T; next chunk into LDS; z update ---------------------------
+    // ---- publish S^T; next chunk into LDS (PHI: its fq from the statistics
+    // of phase 2); z update --------------------------------------------------
     publish();
     if (more) {
-      store_chunk512<FP>(rq, fq_l, PF);
+      if constexpr (PHI)
+        phi_write(t0 + C);
+      else
+        store_chunk512<FP>(rq, fq_l, PF);
       store_chunk512<FP>(rk, fk_l, PF);
       store_chunk512<DP>(rv, v_l, PD);
       if (wave == 0) gate_scan(rg, lane, lgs, qs, ks, rdec, gate, t0 + C + lane < L);
@@ -1184,13 +1307,14 @@ static hipError_t launch_gla_fwd_t(const void* fq, const void* fk, const void* v
   const WalkGrid wg = walk_grid(BH * G / M, KG);
   if constexpr (FP == 256) {   // eight waves per workgroup
     using W = GlaFwdWide<DP>;
-    auto kern = gla_fwd_wide_kernel<DP, VEC, RAW>;
-    hipError_t e = ensure_lds<gla_fwd_wide_kernel<DP, VEC, RAW>>(W::BYTES);
+    auto kern = gla_fwd_wide_kernel<DP, VEC, RAW, false>;
+    hipError_t e = ensure_lds<gla_fwd_wide_kernel<DP, VEC, RAW, false>>(W::BYTES);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(kern, dim3(wg.grid), dim3(WIDE_THREADS), W::BYTES, st,
                        (const bf16*)fq, (const bf16*)fk, (const bf16*)v, lg, (bf16*)y,
                        (const float*)seg_state, final_state, H, L, F, D, gate, G, cps,
-                       M, KG, RAW ? (float*)y : nullptr, raw_den, wg.per, wg.nx, wg.nblk);
+                       M, KG, RAW ? (float*)y : nullptr, raw_den, wg.per, wg.nx, wg.nblk,
+                       (const bf16*)nullptr, (const bf16*)nullptr);
     return hipGetLastError();
   } else {
     auto kern = gla_fwd_kernel<FP, DP, VEC, RAW>;
@@ -1211,7 +1335,7 @@ template <int FP, int DP, bool VEC>
 static hipError_t prepare_fwd_t() {
   hipError_t e;
   if constexpr (FP == 256)
-    e = ensure_lds<gla_fwd_wide_kernel<DP, VEC, false>>(GlaFwdWide<DP>::BYTES);
+    e = ensure_lds<gla_fwd_wide_kernel<DP, VEC, false, false>>(GlaFwdWide<DP>::BYTES);
   else
     e = ensure_lds<gla_fwd_kernel<FP, DP, VEC, false>>(GlaFwd<FP, DP>::BYTES);
   if (e != hipSuccess) return e;
@@ -1270,4 +1394,36 @@ hipError_t launch_gla_fwd(const void* fq, const void* fk, const void* v, const f
   return hipErrorInvalidValue;
 }
 
+// GLA forward with the feature map of q formed inside the walk (PHI): q rows
+// [B, L, H, 64] and W [128][64] bf16 in place of fq; fk [B, H/KG, L, 256],
+// v [B, H/KG, L, 64].  Segments, state pass and scan as launch_gla_fwd (the
+// state pass reads fk and v only).
+hipError_t launch_gla_fwd_phi(const void* q, const void* wq, const void* fk, const void* v,
+                              const float* lg, void* y, int B, int H, int L, int gate, int KG,
+                              float* ws, float* final_state, hipStream_t st) {
+  constexpr int FP = 256, DP = 64;
+  const int F = FP, D = DP, BH = B * H;
+  int G, cps;
+  gla_segments(BH, L, F, &G, &cps);
+  if (G > 1) {
+    hipError_t e = launch_gla_fwd_states_t<FP, DP, true>(
+        fk, v, lg, ws, ws + (size_t)BH * G * GlaFwd<FP, DP>::SEG, BH, H, L, F, D, gate, G, cps,
+        KG, st);
+    if (e != hipSuccess) return e;
+  }
+  const int M = gla_walk_segments(BH, G, F);
+  const WalkGrid wg = walk_grid(BH * G / M, KG);
+  using W = GlaFwdWide<DP>;
+  auto kern = gla_fwd_wide_kernel<DP, true, false, true>;
+  hipError_t e = ensure_lds<gla_fwd_wide_kernel<DP, true, false, true>>(W::PHI_BYTES);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(kern, dim3(wg.grid), dim3(WIDE_THREADS), W::PHI_BYTES, st,
+                     (const bf16*)nullptr, (const bf16*)fk, (const bf16*)v, lg, (bf16*)y,
+                     (const float*)ws, final_state, H, L, F, D, gate, G, cps, M, KG,
+                     (float*)nullptr, (float*)nullptr, wg.per, wg.nx, wg.nblk, (const bf16*)q,
+                     (const bf16*)wq);
+  return hipGetLastError();
+}
+
 }  // namespace lz
+

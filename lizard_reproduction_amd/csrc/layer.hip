@@ -374,6 +374,9 @@ __global__ __launch_bounds__(256, 2) void prologue_fwd_kernel(ProFwdArgs a) {
         if constexpr (C::SPLIT) xl[kb] = low8(xf[kb], xh[kb]);
       }
     }
+    // fq == nullptr: q rows stop at RoPE (the GLA walk forms their feature
+    // map itself, lz_gla_fwd_phi); fout is uniform per workgroup
+    if (fout == nullptr) continue;
     float mp, mn, ip, in;
     softmax_stats<T, FT, HT>(xh, xl, w_hi, w_lo, f, lane, mp, mn, ip, in);
 

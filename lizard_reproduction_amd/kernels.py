@@ -270,6 +270,46 @@ def gla_prefill(fq, fk, v, log_gamma, chunk=CHUNK, gate_logit=False):
     return y, state
 
 
+def gla_forward_phi(qp, wq, fk, v, lg, heads, gate_logit=False, final_state=False,
+                    chunk=CHUNK):
+    """One ``lz_gla_fwd_phi`` launch: the GLA forward with fq formed inside
+    the walk from the q projection rows and the feature weights --
+    fq = [softmax(q Wq^T), softmax(-q Wq^T)] (src/lizard_attention.py:9-11)
+    -- so fq never goes through memory.  qp bf16 ``[B, L, heads * 64]`` (the
+    q_proj output), wq bf16 ``[128, 64]``, fk bf16 ``[B, Hkv, L, 256]``, v
+    bf16 ``[B, Hkv, L, 64]``, lg as ``gla_forward`` (``gate_logit`` too).
+    Returns (y bf16 ``[B, heads, L, 64]``, the recurrent state after the last
+    token as ``gla_prefill`` returns it, or None)."""
+    if qp.dim() != 3 or heads <= 0 or qp.shape[-1] != heads * 64 or tuple(wq.shape) != (128, 64):
+        raise ValueError(f"gla_forward_phi: q [B, L, heads * 64] and wq [128, 64] expected, got "
+                         f"{tuple(qp.shape)} ({heads} heads) and {tuple(wq.shape)}")
+    b, length, _ = qp.shape
+    hk = fk.shape[1] if fk.dim() == 4 else 0
+    if tuple(fk.shape) != (b, hk, length, 256) or tuple(v.shape) != (b, hk, length, 64) or \
+            hk <= 0 or heads % hk:
+        raise ValueError(f"gla_forward_phi: fk [B, Hkv, L, 256] and v [B, Hkv, L, 64] with Hkv "
+                         f"dividing {heads} expected, got {tuple(fk.shape)}, {tuple(v.shape)}")
+    if tuple(lg.shape) not in ((b, length), (b, heads, length)):
+        raise ValueError(f"gla_forward_phi: log_gamma must be {(b, length)} or "
+                         f"{(b, heads, length)}, got {tuple(lg.shape)}")
+    _require_gpu(qp, wq, fk, v, lg)
+    for name, t in (("q", qp), ("wq", wq), ("fk", fk), ("v", v)):
+        if t.dtype is not torch.bfloat16 or not t.is_contiguous():
+            raise ValueError(f"gla_forward_phi: {name} must be contiguous bf16")
+    lg = _f32(lg)
+    y = torch.empty(b, heads, length, 64, device=qp.device, dtype=torch.bfloat16)
+    state = new_state(b, heads, 256, 64, qp.device) if final_state else None
+    if y.numel():
+        mode = _gate_mode(lg, gate_logit)
+        nbytes = _gla_fwd_ws(b, heads, length, 256, 64, mode & GATE_PER_HEAD, chunk)
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=qp.device) if nbytes else None
+        rc = _lib.load().lz_gla_fwd_phi(_ptr(qp), _ptr(wq), _ptr(fk), _ptr(v), _ptr(lg), _ptr(y),
+                                        _ptr(state), b, heads, hk, length, 64, 128, mode, chunk,
+                                        _ptr(ws), nbytes, _stream(qp))
+        _lib.check(rc, "lz_gla_fwd_phi")
+    return y, state
+
+
 def new_state(batch, heads, nf, nd, device):
     """The recurrent state of an empty prefix (zeros), ``[B, H, F*D + F]`` fp32."""
     return torch.zeros(batch, heads, nf * nd + nf, device=device, dtype=torch.float32)

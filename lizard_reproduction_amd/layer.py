@@ -85,14 +85,16 @@ def _tables(cos, sin, batch, length, head_dim, dtype):
     return cos.to(dtype).contiguous(), sin.to(dtype).contiguous(), batched
 
 
-def prologue_forward(qp, kp, vp, wq, wk, cos, sin, heads, kv_heads):
+def prologue_forward(qp, kp, vp, wq, wk, cos, sin, heads, kv_heads, with_fq=True):
     """One ``lz_layer_prologue_fwd`` launch: the q/k/v projection outputs
     ([B, L, heads * hd], [B, L, kv_heads * hd]) and phi weights ([f, hd]) to
     the bf16 kernel operands fq ([B, heads, L, 2f]), qr ([B, heads, L, hd]),
     fk ([B, kv_heads, L, 2f]) and kr, v ([B, kv_heads, L, hd]): the key side
     stays per kv head, and the GLA and SWA kernels read each query head's
     from its kv head (the reference's repeat_interleave, not materialised).
-    Returns those five and the tuple ``prologue_backward`` needs."""
+    Returns those five and the tuple ``prologue_backward`` needs; without
+    ``with_fq`` fq is None and not computed (``kernels.gla_forward_phi``
+    forms it inside the GLA walk)."""
     if qp.dim() != 3 or heads <= 0 or kv_heads <= 0 or heads % kv_heads or \
             qp.shape[-1] % heads:
         raise ValueError(f"prologue_forward: q must be [B, L, heads * head_dim] with kv_heads "
@@ -110,14 +112,16 @@ def prologue_forward(qp, kp, vp, wq, wk, cos, sin, heads, kv_heads):
     qp, kp, vp, wq, wk = (t.to(dtype).contiguous() for t in (qp, kp, vp, wq, wk))
     cos, sin, batched = _tables(cos, sin, b, length, hd, dtype)
     dev = qp.device
-    fq = torch.empty(b, heads, length, 2 * f, device=dev, dtype=torch.bfloat16)
+    fq = torch.empty(b, heads, length, 2 * f, device=dev, dtype=torch.bfloat16) if with_fq \
+        else None
     fk = torch.empty(b, kv_heads, length, 2 * f, device=dev, dtype=torch.bfloat16)
     qr = torch.empty(b, heads, length, hd, device=dev, dtype=torch.bfloat16)
     kr = torch.empty(b, kv_heads, length, hd, device=dev, dtype=torch.bfloat16)
     v = torch.empty_like(kr)
     rc = _lib.load().lz_layer_prologue_fwd(
         qp.data_ptr(), kp.data_ptr(), vp.data_ptr(), wq.data_ptr(), wk.data_ptr(),
-        cos.data_ptr(), sin.data_ptr(), batched, fq.data_ptr(), fk.data_ptr(), qr.data_ptr(),
+        cos.data_ptr(), sin.data_ptr(), batched, fq.data_ptr() if with_fq else None,
+        fk.data_ptr(), qr.data_ptr(),
         kr.data_ptr(), v.data_ptr(), int(dtype == torch.bfloat16), b, length, heads, kv_heads,
         hd, f, _stream(qp))
     _lib.check(rc, "lz_layer_prologue_fwd")
@@ -313,6 +317,33 @@ class LizardAttention(nn.Module):
         bf16 = _all_bf16(qp, kp, vp, self.phi_q.weight, self.phi_k.weight, cos, sin)
         return prologue_supported(self.head_dim, self.phi_q.weight.shape[0], bf16)
 
+    def _phi_walk(self, qp, kp, vp, cos, sin):
+        """Whether the GLA walk can form fq itself (``kernels.gla_forward_phi``):
+        a bf16 layer at head_dim 64 with feature_dim 128 (F = 256)."""
+        return (self.head_dim == 64 and self.phi_q.weight.shape[0] == 128 and
+                _all_bf16(qp, kp, vp, self.phi_q.weight, self.phi_k.weight, cos, sin))
+
+    def _needs_grad(self, x):
+        return torch.is_grad_enabled() and (
+            x.requires_grad or any(p.requires_grad for p in self.parameters()))
+
+    def _inference(self, qp, kp, vp, z, cos, sin, out_dtype, final_state=False):
+        """The forward without autograd with fq formed inside the GLA walk:
+        the prologue writes fk, qr, kr, v only; ``gla_forward_phi`` reads the
+        q projection rows and phi_q instead of fq.  Returns (out before
+        o_proj, the GLA state after the last token or None, kr, v)."""
+        _, fk, qr, kr, v, _ = prologue_forward(qp, kp, vp, self.phi_q.weight, self.phi_k.weight,
+                                               cos, sin, self.heads, self.kv_heads,
+                                               with_fq=False)
+        y_gla, state = kernels.gla_forward_phi(qp, self.phi_q.weight, fk, v,
+                                               z.float().contiguous(), self.heads,
+                                               gate_logit=True, final_state=final_state)
+        y_swa, _ = kernels.swa_forward(qr, kr, v, self.meta_tokens.detach().float().contiguous(),
+                                       self.window)
+        alpha = self.alpha_blend.detach().float().reshape(1).contiguous()
+        odt = torch.bfloat16 if out_dtype == torch.bfloat16 else torch.float32
+        return combine_forward(y_gla, y_swa, alpha, odt).to(out_dtype), state, kr, v
+
     def forward(self, hidden_states, position_embeddings, **kwargs):
         x = hidden_states
         dtype = torch.promote_types(x.dtype, torch.float32)
@@ -325,6 +356,8 @@ class LizardAttention(nn.Module):
         if not self._fused(qp, kp, vp, cos, sin):
             y = self._unfused(qp, kp, vp, F.logsigmoid(z), cos, sin, dtype).to(x.dtype)
             return self.o_proj(y.transpose(1, 2).flatten(2)), None
+        if not self._needs_grad(x) and self._phi_walk(qp, kp, vp, cos, sin):
+            return self.o_proj(self._inference(qp, kp, vp, z, cos, sin, x.dtype)[0]), None
         y = _Core.apply(qp, kp, vp, self.phi_q.weight, self.phi_k.weight, z, self.meta_tokens,
                         self.alpha_blend, cos, sin, self.heads, self.kv_heads, self.window,
                         x.dtype)
@@ -369,13 +402,13 @@ class LizardAttention(nn.Module):
         k = torch.zeros(shape, device=device, dtype=torch.bfloat16)
         return LizardCache(state, k, torch.zeros_like(k), 0)
 
-    def _operands(self, x, position_embeddings):
+    def _operands(self, x, position_embeddings, projections=None):
         kernels._refuse_capture("LizardAttention")
         if x.device.type != "cuda":
             raise ValueError("LizardAttention (hip backend) needs its input on a ROCm GPU")
         nf = 2 * self.phi_q.weight.shape[0]
         cos, sin = position_embeddings
-        qp, kp, vp = self.q_proj(x), self.k_proj(x), self.v_proj(x)
+        qp, kp, vp = projections or (self.q_proj(x), self.k_proj(x), self.v_proj(x))
         if not self._fused(qp, kp, vp, cos, sin) or not kernels.gla_native(nf, self.head_dim):
             raise ValueError(f"LizardAttention.prefill/step: decoding takes the fused prologue's "
                              f"shapes and the GLA decode kernels' (F = {nf}, D = "
@@ -398,15 +431,25 @@ class LizardAttention(nn.Module):
         """``forward`` over a prompt [B, L, hidden] (no autograd) that also
         returns the decode cache after it: ``(out, cache)``."""
         x = hidden_states
-        z, fq, fk, qr, kr, v = self._operands(x, position_embeddings)
-        y_gla, state = kernels.gla_prefill(fq, fk, v, z, gate_logit=True)
-        y_swa, _ = kernels.swa_forward(qr, kr, v, self.meta_tokens.detach().float().contiguous(),
-                                       self.window)
         cache = self.new_cache(x.shape[0], x.device)
+        cos, sin = position_embeddings
+        qp, kp, vp = self.q_proj(x), self.k_proj(x), self.v_proj(x)
+        if self._fused(qp, kp, vp, cos, sin) and self._phi_walk(qp, kp, vp, cos, sin):
+            kernels._refuse_capture("LizardAttention")
+            z = self.W_gamma(x).float().squeeze(-1)
+            y, state, kr, v = self._inference(qp, kp, vp, z, cos, sin, x.dtype, final_state=True)
+            out = self.o_proj(y)
+        else:
+            z, fq, fk, qr, kr, v = self._operands(x, position_embeddings, (qp, kp, vp))
+            y_gla, state = kernels.gla_prefill(fq, fk, v, z, gate_logit=True)
+            y_swa, _ = kernels.swa_forward(qr, kr, v,
+                                           self.meta_tokens.detach().float().contiguous(),
+                                           self.window)
+            out = self._out(y_gla, y_swa, x)
         cache.state = state
         cache.put(kr, v, 0)
         cache.pos = x.shape[1]
-        return self._out(y_gla, y_swa, x), cache
+        return out, cache
 
     @torch.no_grad()
     def step(self, hidden_states, position_embeddings, cache):

@@ -138,6 +138,30 @@ def test_gate_mode_bits_are_checked(lib):
 
 
 @no_gpu
+def test_phi_forward_rejects_bad_arguments(lib):
+    """lz_gla_fwd_phi takes head_dim 64 with feature_dim 128 only, and checks
+    its pointers, kv heads, gate mode and workspace like lz_gla_fwd."""
+    p = ctypes.c_void_p(16)   # never dereferenced: validation fails first
+    f = lib.lz_gla_fwd_phi
+    # q, wq, fk, v, log_gamma, y, state, B, H, kv_heads, L, head_dim, feature_dim, gate_mode,
+    # chunk, workspace, workspace_bytes, stream
+    refused(lib, f(p, p, p, p, p, p, None, 1, 4, 2, 64, 32, 128, 0, 64, p, 1 << 20, None),
+            b"unsupported")
+    refused(lib, f(p, p, p, p, p, p, None, 1, 4, 2, 64, 64, 64, 0, 64, p, 1 << 20, None),
+            b"unsupported")
+    refused(lib, f(None, p, p, p, p, p, None, 1, 4, 2, 64, 64, 128, 0, 64, p, 1 << 20, None),
+            b"null")
+    refused(lib, f(p, p, p, p, p, p, None, 1, 4, 3, 64, 64, 128, 0, 64, p, 1 << 20, None),
+            b"kv_heads")
+    refused(lib, f(p, p, p, p, p, p, None, 1, 4, 2, 64, 64, 128, 4, 64, p, 1 << 20, None),
+            b"gate_mode")
+    need = lib.lz_gla_fwd_workspace_bytes(1, 4, 4096, 256, 64, 0, 64)
+    assert need > 0
+    refused(lib, f(p, p, p, p, p, p, None, 1, 4, 2, 4096, 64, 128, 0, 64, p, need - 1, None),
+            b"workspace")
+
+
+@no_gpu
 def test_decode_entry_points_reject_bad_arguments(lib):
     p = ctypes.c_void_p(16)   # never dereferenced: validation fails first
     # lz_swa_decode_step(q, k_cache, v_cache, meta, n_meta, y, B, H, kv_heads, window, dim,
