@@ -233,13 +233,17 @@ __device__ __forceinline__ float wave_suffix_sum(float x, int lane) {
 }
 
 
-// logsigmoid(z) = min(z, 0) - log1p(e^{-|z|}), no overflow for any z
+// logsigmoid(z) = min(z, 0) - log(1 + e^{-|z|}), no overflow for any z, from
+// the hardware exp2 and log2 (a few instructions: it sits in the walks' gate
+// scan, where log1pf's longer sequence slowed the 256-register forward walk by
+// 6 %).  For |z| > 17, 1 + e^{-|z|} rounds to 1 and the result to min(z, 0):
+// an absolute error under 5e-8 in a log-gate.
 __device__ __forceinline__ float log_sigmoid(float z) {
-  return fminf(z, 0.f) - log1pf(__expf(-fabsf(z)));
+  return fminf(z, 0.f) - flog(1.f + fexp(-fabsf(z)));
 }
 
 // d logsigmoid(z) / dz = sigmoid(-z) = 1 / (1 + e^z) (0 when e^z overflows)
-__device__ __forceinline__ float sigmoid_neg(float z) { return 1.f / (1.f + __expf(z)); }
+__device__ __forceinline__ float sigmoid_neg(float z) { return 1.f / (1.f + fexp(z)); }
 
 // log_gamma from a gate buffer value of a token inside L, in mode `gate`
 __device__ __forceinline__ float gate_log(float g, int gate) {
@@ -253,7 +257,7 @@ __device__ __forceinline__ float gate_log(float g, int gate) {
 // not waited for at its load) and 0 for a token past L (`valid` false).
 __device__ __forceinline__ void gate_scan(float g, int lane, float* lgs, float* qs, float* ks,
                                           float* r, int gate, bool valid) {
-  if (gate & GATE_LOGIT) g = valid ? log_sigmoid(g) : 0.f;
+  if (__builtin_expect(gate & GATE_LOGIT, 0)) g = valid ? log_sigmoid(g) : 0.f;
   g = wave_prefix_sum(g);
   const float end = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(g), 63));
   lgs[lane] = g;

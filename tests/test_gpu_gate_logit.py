@@ -50,8 +50,9 @@ def test_gla_gate_logit_matches_oracle(b, h, kv, length, nf, nd, per_head):
           + " ".join(f"{k}={e:.2e}" for k, e in errs.items()), flush=True)
     assert dz.shape == z.shape and dz.dtype == torch.float32
     assert errs["y"] <= OUT_TOL and errs["dfq"] <= GRAD_TOL and errs["dz"] <= GRAD_TOL, errs
-    # the two kernel paths differ only by the fp32 rounding of logsigmoid
-    assert errs["y_vs_lg"] <= 4e-3 and errs["dz_vs_dlg"] <= 1e-3, errs
+    # the two kernel paths differ only by the fp32 rounding of logsigmoid, which
+    # can move a bf16 output by an ulp (2^-8 of the max-abs): two ulps allowed
+    assert errs["y_vs_lg"] <= 2 * 2 ** -8 and errs["dz_vs_dlg"] <= 1e-3, errs
     assert torch.isfinite(dz).all()
 
 
@@ -78,4 +79,4 @@ def test_gla_prefill_and_decode_take_the_gate_logit(per_head):
     errs = [max_rel(a, r) for a, r in zip(*outs)]
     print(f"[parity] gate logit prefill/decode per_head={per_head}: y={errs[0]:.2e} "
           f"steps={errs[1]:.2e} state={errs[2]:.2e}", flush=True)
-    assert max(errs) <= 4e-3, errs
+    assert max(errs) <= 2 * 2 ** -8, errs
