@@ -119,11 +119,14 @@ __global__ __launch_bounds__(256, (swa_fwd_occupancy<DP, VEC>())) void swa_fwd_k
   bf16x8 qreg[DP / 16];
   own_rows<DP>(q + base, qi, L, d, h, vec, qreg);
 
-  // running max and sum start from the sinks (src/kernels/swa.py:34-38)
+  // running max and sum start from the sinks (src/kernels/swa.py:34-38).  The
+  // max is kept in log2 units, u = s log2(e): a score's weight is then
+  // exp2(q.k c - m) with c = scale log2(e), one FMA and the hardware exp2.
+  const float c = scale * LOG2E;
   float m_i = -1e30f;
-  for (int j = 0; j < n_meta; ++j) m_i = fmaxf(m_i, meta[j]);
+  for (int j = 0; j < n_meta; ++j) m_i = fmaxf(m_i, meta[j] * LOG2E);
   float l_i = 0.f;
-  for (int j = 0; j < n_meta; ++j) l_i += fexp(meta[j] - m_i);
+  for (int j = 0; j < n_meta; ++j) l_i += __builtin_amdgcn_exp2f(meta[j] * LOG2E - m_i);
 
   f32x16 o[DP / 32];
 #pragma unroll
@@ -151,20 +154,28 @@ __global__ __launch_bounds__(256, (swa_fwd_occupancy<DP, VEC>())) void swa_fwd_k
 #pragma unroll
       for (int kb = 0; kb < DP / 16; ++kb)
         s = mfma(row_operand(k_l, P, 32 * half + col, 16 * kb, h), qreg[kb], s);
+      // only blocks that straddle the window's start or the diagonal are
+      // masked: keys [k0, k0 + 32) lie in every window of queries
+      // [q0, q0 + 32) when k0 + 31 <= q0 and k0 >= q0 + 32 - W (uniform per wave)
       float mx = NEG_INF;
+      if (k0 + 31 <= q0 && k0 >= q0 + 32 - W) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        s[r] = in_window(qi, k0 + acc_row(r, h), W) ? s[r] * scale : NEG_INF;
-        mx = fmaxf(mx, s[r]);
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[r]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          s[r] = in_window(qi, k0 + acc_row(r, h), W) ? s[r] : NEG_INF;
+          mx = fmaxf(mx, s[r]);
+        }
       }
       mx = fmaxf(mx, xhalf(mx));
-      const float m_new = fmaxf(m_i, mx);
-      const float alpha = fexp(m_i - m_new);
+      const float m_new = fmaxf(m_i, mx * c);
+      const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);
       float ps = 0.f;
       bf16x8 p[2];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float e = fexp(s[r] - m_new);
+        const float e = __builtin_amdgcn_exp2f(fmaf(s[r], c, -m_new));
         ps += e;
         p[r >> 3][r & 7] = to_bf16(e);
       }
@@ -191,7 +202,7 @@ __global__ __launch_bounds__(256, (swa_fwd_occupancy<DP, VEC>())) void swa_fwd_k
   const float inv = 1.f / l_i;
 #pragma unroll
   for (int t = 0; t < DP / 32; ++t) store_acc_row<bf16>(y + base, qi, t * 32, L, d, vec, o[t], inv, h);
-  if (qi < L && h == 0) lse[(size_t)bh * L + qi] = m_i + flog(l_i);
+  if (qi < L && h == 0) lse[(size_t)bh * L + qi] = m_i * LN2 + flog(l_i);
 }
 
 // Workgroups per CU the backward kernels ask the compiler to fit in

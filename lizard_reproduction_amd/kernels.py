@@ -166,6 +166,11 @@ def gla_forward(fq, fk, v, lg, keep_state=True, chunk=CHUNK, gate_logit=False):
     F.logsigmoid, src/lizard_attention.py:92)."""
     _check_kv("gla_forward", fq, fk, v, fq.shape[-1], v.shape[-1])
     _check_gate("gla_forward", fq, lg)
+    return _gla_fwd_launch(fq, fk, v, lg, keep_state, chunk, gate_logit)
+
+
+def _gla_fwd_launch(fq, fk, v, lg, keep_state, chunk, gate_logit):
+    """``gla_forward`` without its shape checks (for callers that made them)."""
     b, h, length, nf = fq.shape
     nd = v.shape[-1]
     y = torch.empty(b, h, length, nd, device=v.device, dtype=v.dtype)
@@ -192,6 +197,13 @@ def gla_backward(fq, fk, v, lg, dy, state, grad_dtype, chunk=CHUNK, gate_logit=F
     nd = v.shape[-1]
     if tuple(dy.shape) != (b, h, length, nd):
         raise ValueError(f"gla_backward: dy must be {(b, h, length, nd)}, got {tuple(dy.shape)}")
+    return _gla_bwd_launch(fq, fk, v, lg, dy, state, grad_dtype, chunk, gate_logit)
+
+
+def _gla_bwd_launch(fq, fk, v, lg, dy, state, grad_dtype, chunk, gate_logit):
+    """``gla_backward`` without its shape checks (for callers that made them)."""
+    b, h, length, nf = fq.shape
+    nd = v.shape[-1]
     dfq = torch.empty(fq.shape, device=fq.device, dtype=grad_dtype)
     dfk = torch.empty_like(dfq)
     dv = torch.empty(b, h, length, nd, device=v.device, dtype=grad_dtype)
@@ -223,7 +235,7 @@ class _GLA(torch.autograd.Function):
         fq, fk, v = _bf16(fq), _bf16(fk), _bf16(v)
         lg = _f32(log_gamma)
         grad = any(ctx.needs_input_grad[:4])
-        y, state = gla_forward(fq, fk, v, lg, keep_state=grad, chunk=chunk)
+        y, state = _gla_fwd_launch(fq, fk, v, lg, grad, chunk, False)
         if grad:
             ctx.save_for_backward(fq, fk, v, lg)
             # the state entering each segment, reused by the backward
@@ -235,7 +247,7 @@ class _GLA(torch.autograd.Function):
     def backward(ctx, dy):
         fq, fk, v, lg = ctx.saved_tensors
         gdt = torch.bfloat16 if all(d == torch.bfloat16 for d in ctx.dtypes[:3]) else torch.float32
-        grads = gla_backward(fq, fk, v, lg, _bf16(dy), ctx.fwd_ws, gdt, ctx.chunk)
+        grads = _gla_bwd_launch(fq, fk, v, lg, _bf16(dy), ctx.fwd_ws, gdt, ctx.chunk, False)
         return _cast_grads(grads, ctx.dtypes) + (None,)
 
 
@@ -369,6 +381,12 @@ def gla(fq, fk, v, log_gamma, chunk=CHUNK):
     Returns bf16 ``[B, H, L, D]``.
     """
     _check_gla(fq, fk, v, log_gamma, chunk)
+    if not (torch.is_grad_enabled() and (fq.requires_grad or fk.requires_grad or
+                                         v.requires_grad or log_gamma.requires_grad)):
+        # nothing to differentiate: the same forward launch without the
+        # autograd node (and the same bits as with it)
+        return _gla_fwd_launch(_bf16(fq), _bf16(fk), _bf16(v), _f32(log_gamma), False, chunk,
+                               False)[0]
     return _GLA.apply(fq, fk, v, log_gamma, chunk)
 
 
@@ -397,6 +415,11 @@ def swa_forward(q, k, v, meta, window):
     contiguous meta; returns (y, lse).  k and v may have fewer heads than q
     (a divisor, as in ``gla_forward``)."""
     _check_kv("swa_forward", q, k, v, q.shape[-1], q.shape[-1])
+    return _swa_fwd_launch(q, k, v, meta, window)
+
+
+def _swa_fwd_launch(q, k, v, meta, window):
+    """``swa_forward`` without its shape checks (for callers that made them)."""
     b, h, length, d = q.shape
     y = torch.empty_like(q)
     lse = torch.empty(b, h, length, device=v.device, dtype=torch.float32)
@@ -416,6 +439,12 @@ def swa_backward(q, k, v, meta, lse, dy, window, grad_dtype):
     if tuple(dy.shape) != tuple(q.shape) or tuple(lse.shape) != (b, h, length):
         raise ValueError(f"swa_backward: dy must be {tuple(q.shape)} and lse {(b, h, length)}, "
                          f"got {tuple(dy.shape)} and {tuple(lse.shape)}")
+    return _swa_bwd_launch(q, k, v, meta, lse, dy, window, grad_dtype)
+
+
+def _swa_bwd_launch(q, k, v, meta, lse, dy, window, grad_dtype):
+    """``swa_backward`` without its shape checks (for callers that made them)."""
+    b, h, length, d = q.shape
     dq = torch.empty(q.shape, device=q.device, dtype=grad_dtype)
     dk = torch.empty_like(dq)
     dv = torch.empty_like(dq)
@@ -481,7 +510,7 @@ class _SWA(torch.autograd.Function):
         ctx.dtypes = (q.dtype, k.dtype, v.dtype, meta.dtype)
         q, k, v = _bf16(q), _bf16(k), _bf16(v)
         meta = _f32(meta)
-        y, lse = swa_forward(q, k, v, meta, window)
+        y, lse = _swa_fwd_launch(q, k, v, meta, window)
         if any(ctx.needs_input_grad[:4]):
             ctx.save_for_backward(q, k, v, meta, lse)
         ctx.window = window
@@ -491,7 +520,7 @@ class _SWA(torch.autograd.Function):
     def backward(ctx, dy):
         q, k, v, meta, lse = ctx.saved_tensors
         gdt = torch.bfloat16 if all(x == torch.bfloat16 for x in ctx.dtypes[:3]) else torch.float32
-        grads = swa_backward(q, k, v, meta, lse, _bf16(dy), ctx.window, gdt)
+        grads = _swa_bwd_launch(q, k, v, meta, lse, _bf16(dy), ctx.window, gdt)
         return _cast_grads(grads, ctx.dtypes) + (None, None, None)
 
 
@@ -502,4 +531,8 @@ def swa(q, k, v, meta, window, fwd_blocks=FWD_BLOCKS, bwd_blocks=BWD_BLOCKS):
     s_it = q_i . k_t / sqrt(d).  Returns bf16 ``[B, H, L, d]``.
     """
     _check_swa(q, k, v, meta, window, fwd_blocks, bwd_blocks)
+    if not (torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or
+                                         v.requires_grad or meta.requires_grad)):
+        # nothing to differentiate: the forward launch without the autograd node
+        return _swa_fwd_launch(_bf16(q), _bf16(k), _bf16(v), _f32(meta), window)[0]
     return _SWA.apply(q, k, v, meta, window, tuple(fwd_blocks), tuple(bwd_blocks))
