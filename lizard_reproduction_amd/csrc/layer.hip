@@ -413,8 +413,8 @@ __global__ __launch_bounds__(256, 2) void prologue_fwd_kernel(ProFwdArgs a) {
 //
 // A workgroup takes blocks of 128 rows.  Its 4 NWF waves are (row group rg,
 // feature group fh): wave (rg, fh) owns rows 32 rg .. 32 rg + 31 (one per lane
-// column of its MFMA tiles) and feature tiles fh FTW .. fh FTW + FTW - 1 of
-// both maps (FTW = FT / NWF).  Splitting a row's features over NWF = 2 waves
+// column of its MFMA tiles) and feature tiles fh, fh + NWF, ... (FTW = FT / NWF
+// of them) of both maps.  Splitting a row's features over NWF = 2 waves
 // halves what a lane keeps in registers through the Jacobian, which is what
 // lets two waves share a SIMD at f = 128.  Per block:
 //   1. x rows -> LDS (bf16 hi, and lo for fp32 inputs), coalesced; each lane
@@ -523,7 +523,12 @@ prologue_bwd_kernel(ProBwdArgs a) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, h = lane >> 5;
   const int rg = wave % PRO_WAVES, fh = wave / PRO_WAVES;   // row group, feature group
   const int lrow = rg * PRO_ROWS + (lane & 31);             // this lane's row in the tiles
-  const int ft0 = fh * FTW;                                 // first feature tile of the wave
+  // local tile s of feature group g is feature tile s NWF + g: the groups'
+  // tiles interleave, so one pass over local tile s gathers the adjacent
+  // 32-feature tiles 2s and 2s + 1 of a gradient row, a whole 128-byte line of
+  // it (blocked tiles read half lines per pass, and the other halves came back
+  // from HBM a pass later, evicted meanwhile)
+  auto ftile = [](int g, int s) { return s * NWF + g; };
 
   const T* cs = static_cast<const T*>(a.cos);
   const T* sn = static_cast<const T*>(a.sin);
@@ -531,7 +536,7 @@ prologue_bwd_kernel(ProBwdArgs a) {
   const bool vec = (f & 7) == 0;   // gradient items are whole 16-byte pieces
 
   // stage items of this thread: rows tid / IPR + 32 i of a block; item k of a
-  // row covers features 8 (k & 3) .. +8 of tile (k / 8) FTW + s of the dp
+  // row covers features 8 (k & 3) .. +8 of tile ftile(k / 8, s) of the dp
   // ((k / 4) & 1 == 0) or dn map, at stage column 8 k
   const int k = tid % K::IPR, sgrp = k >> 3, shalf = (k >> 2) & 1, scol = 8 * (k & 3);
   const int srow = tid / K::IPR;
@@ -605,7 +610,7 @@ prologue_bwd_kernel(ProBwdArgs a) {
     // staged; heads past GQ are loaded and added then.
     auto item_ok = [&](int i, int c) { return gbase[i] >= 0 && c < f; };
     auto issue = [&](int s, uint4 (&raw)[K::GQR][K::GI]) {
-      const int c = 32 * (sgrp * FTW + s) + scol;
+      const int c = 32 * ftile(sgrp, s) + scol;
 #pragma unroll
       for (int g = 0; g < K::GQ; ++g)
 #pragma unroll
@@ -625,7 +630,7 @@ prologue_bwd_kernel(ProBwdArgs a) {
     // is summed (each item's heads are still summed in head order), so GI
     // loads per thread are in flight instead of one.
     auto gather = [&](int s, const uint4 (&raw)[K::GQR][K::GI], float (&g8)[K::GI][8]) {
-      const int c = 32 * (sgrp * FTW + s) + scol;
+      const int c = 32 * ftile(sgrp, s) + scol;
       bool ok0[K::GI], ok1[K::GI];
 #pragma unroll
       for (int i = 0; i < K::GI; ++i) {
@@ -693,7 +698,7 @@ prologue_bwd_kernel(ProBwdArgs a) {
     float mp = -1e30f, mn = -1e30f, sp = 0.f, sn_ = 0.f;
 #pragma unroll
     for (int s = 0; s < FTW; ++s) {
-      const int ft = ft0 + s;
+      const int ft = ftile(fh, s);
       const f32x16 acc = project_tile<T, FT, HT>(ft, xh, xl, w_hi, w_lo, lane);
       // features past f (padding of the last tile) drop out through
       // selects, not branches: their exponentials are of -inf
@@ -761,7 +766,7 @@ prologue_bwd_kernel(ProBwdArgs a) {
         *reinterpret_cast<f32x4*>(dst + 4) = f32x4{g8[i][4], g8[i][5], g8[i][6], g8[i][7]};
       }
       __syncthreads();
-      const f32x16 acc = project_tile<T, FT, HT>(ft0 + s, xh, xl, w_hi, w_lo, lane);
+      const f32x16 acc = project_tile<T, FT, HT>(ftile(fh, s), xh, xl, w_hi, w_lo, lane);
       const float* srow_l = stage + lrow * SP + 64 * fh;
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
@@ -801,7 +806,7 @@ prologue_bwd_kernel(ProBwdArgs a) {
     bf16x4 dlo[FTW][4];
 #pragma unroll
     for (int s = 0; s < FTW; ++s) {
-      const int ft = ft0 + s;
+      const int ft = ftile(fh, s);
       const f32x16 acc = project_tile<T, FT, HT>(ft, xh, xl, w_hi, w_lo, lane);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -843,7 +848,7 @@ prologue_bwd_kernel(ProBwdArgs a) {
         for (int s = 0; s < FTW; ++s)
 #pragma unroll
           for (int q4 = 0; q4 < 4; ++q4)
-            *reinterpret_cast<bf16x4*>(d_l + lrow * K::DP + 32 * (ft0 + s) + 8 * q4 + 4 * h) =
+            *reinterpret_cast<bf16x4*>(d_l + lrow * K::DP + 32 * ftile(fh, s) + 8 * q4 + 4 * h) =
                 dlo[s][q4];
       }
       __syncthreads();
