@@ -372,6 +372,30 @@ __global__ __launch_bounds__(256, (swa_bwd_occupancy<DP>())) void swa_bwd_dq_ker
   }
 }
 
+// dmeta[j] = sum over `rows` partial rows of part[row][j], by the first 256
+// threads of a workgroup, in passes of up to 256 sinks: thread (group g, sink
+// j) sums partial rows g, g + groups, ...; thread j then sums the groups, in a
+// fixed order.  sh: 256 floats of LDS.
+__device__ void dmeta_sum(const float* __restrict__ part, int rows, int n_meta,
+                          float* __restrict__ dmeta, float* sh) {
+  const int per = min(n_meta, 256), groups = 256 / per;
+  for (int j0 = 0; j0 < n_meta; j0 += per) {
+    const int nj = min(per, n_meta - j0);
+    const int j = threadIdx.x % per, grp = threadIdx.x / per;
+    float acc = 0.f;
+    if (threadIdx.x < 256 && grp < groups && j < nj)
+      for (int r = grp; r < rows; r += groups) acc += part[(size_t)r * n_meta + j0 + j];
+    if (threadIdx.x < 256) sh[threadIdx.x] = acc;
+    __syncthreads();
+    if ((int)threadIdx.x < nj) {
+      float t = 0.f;
+      for (int g = 0; g < groups; ++g) t += sh[g * per + threadIdx.x];
+      dmeta[j0 + threadIdx.x] = t;
+    }
+    __syncthreads();
+  }
+}
+
 // ----------------------------------------------------------------------------
 // backward, key side: dk and dv over the queries whose windows hold the keys
 // ----------------------------------------------------------------------------
@@ -393,28 +417,8 @@ __global__ __launch_bounds__(256, (swa_bwd_occupancy<DP>())) void swa_bwd_dkv_ke
   const int nkb = (L + SWA_ROWS - 1) / SWA_ROWS;
   const int lb = xcd_block(blockIdx.x, per, nx);
   if (lb >= BH * nkb) return;
-  if (lb == 0 && n_meta > 0) {
-    // dmeta from the query-side blocks' partials (that launch has completed),
-    // in passes of up to 256 sinks: thread (group g, sink j) sums partial rows
-    // g, g + groups, ...; thread j then sums the groups, in a fixed order
-    float* sh = reinterpret_cast<float*>(smem);
-    const int rows = BH * nkb, per = min(n_meta, 256), groups = 256 / per;
-    for (int j0 = 0; j0 < n_meta; j0 += per) {
-      const int nj = min(per, n_meta - j0);
-      const int j = threadIdx.x % per, grp = threadIdx.x / per;
-      float acc = 0.f;
-      if (grp < groups && j < nj)
-        for (int r = grp; r < rows; r += groups) acc += dmeta_part[(size_t)r * n_meta + j0 + j];
-      sh[threadIdx.x] = acc;
-      __syncthreads();
-      if ((int)threadIdx.x < nj) {
-        float t = 0.f;
-        for (int g = 0; g < groups; ++g) t += sh[g * per + threadIdx.x];
-        dmeta[j0 + threadIdx.x] = t;
-      }
-      __syncthreads();
-    }
-  }
+  // dmeta from the query-side blocks' partials (that launch has completed)
+  if (lb == 0 && n_meta > 0) dmeta_sum(dmeta_part, BH * nkb, n_meta, dmeta, reinterpret_cast<float*>(smem));
   const int bh = lb / nkb, K0 = (lb % nkb) * SWA_ROWS;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int col = lane & 31, h = lane >> 5;
@@ -508,6 +512,309 @@ __global__ __launch_bounds__(256, (swa_bwd_occupancy<DP>())) void swa_bwd_dkv_ke
 }
 
 // ----------------------------------------------------------------------------
+// backward in one pass, for windows W <= 64 at d <= 64 (padded to 64)
+//
+// With W <= 64 the queries of 64-row block i see keys of blocks i - 1 and i
+// only, and the keys of block j are seen by the queries of blocks j and j + 1.
+// A workgroup of eight waves walks a segment of blocks b0 .. b1 - 1 of one
+// (b, h); step i scores query block i against key blocks i - 1 and i once and
+// uses the scores three times:
+//   phase 1a  waves 0-5: pair (query half A, 32-key sub-block s), s = A .. A+2
+//             of the four sub-blocks of blocks i - 1, i: S, dP = dy v^T, p and
+//             the pair's part of delta = sum_t p dp (the fp32 form of the two
+//             kernels above, no delta buffer);
+//   phase 1b  delta = the three parts of the query half in key order;
+//             ds = p (dp - delta); p and ds to LDS as bf16 [query][key] tiles;
+//             the next block's rows (loaded a step ahead) to their LDS slots;
+//   phase 2   waves 0-3: dq tile (A, t) = scale ds K over the three
+//             sub-blocks: the query block is done, stored;
+//             waves 4-7: key half kh of the block of parity par in {i-1, i}
+//             accumulates dk += scale ds^T Q, dv += p^T dY; block i - 1 has
+//             seen all its queries and is stored.
+// The step past the segment (block b1, the next segment's first) runs for the
+// dk, dv of block b1 - 1 only; the first step reads block b0 - 1's keys for
+// the first queries' windows only.  Key tiles rotate through three LDS slots
+// (blocks i - 1 and i read, i + 1 written), query and dy tiles through two.
+// dmeta_j = -sum_i e^{meta_j - lse_i} delta_i = -e^{meta_j - m} T with
+// m = max_j meta_j and T = sum_i e^{m - lse_i} delta_i (both factors at most 1,
+// since lse_i >= m): a workgroup adds its queries' terms of T as it forms their
+// deltas, and a second launch sums the workgroups' T in a fixed order.
+// ----------------------------------------------------------------------------
+constexpr int SWA_WALK_MAX_NB = 32;   // blocks per segment
+constexpr int SWA_WALK_WAVES = 8;
+
+struct SwaWalk {
+  static constexpr int P = SwaCfg<64>::P;             // k, v, q, dy tiles [64][P]
+  static constexpr int TB = SwaCfg<64>::TILE_BYTES;
+  static constexpr int PP = lds_pitch(128);           // p, ds tiles [64 queries][PP]
+  static constexpr int OFF_K = 0;                     // three k slots
+  static constexpr int OFF_V = OFF_K + 3 * TB;        // three v slots
+  static constexpr int OFF_Q = OFF_V + 3 * TB;        // two q buffers
+  static constexpr int OFF_DY = OFF_Q + 2 * TB;       // two dy buffers
+  static constexpr int OFF_P = OFF_DY + 2 * TB;
+  static constexpr int OFF_DS = OFF_P + 64 * PP * 2;
+  static constexpr int OFF_LSE = OFF_DS + 64 * PP * 2;            // [2][64] f32
+  static constexpr int OFF_RED = OFF_LSE + 2 * 64 * 4;            // [6][32] f32
+  static constexpr int LDS = OFF_RED + 6 * 32 * 4;
+  static_assert(LDS <= 160 * 1024, "LDS budget");
+  static_assert(SWA_TILE == 64 && SwaCfg<64>::NL * 256 == 64 * 8, "tile items");
+};
+
+template <typename OutT, bool VEC>
+__global__ __launch_bounds__(64 * SWA_WALK_WAVES, 1) void swa_bwd_walk_kernel(
+    const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
+    const float* __restrict__ meta, int n_meta, const float* __restrict__ lse,
+    const bf16* __restrict__ dy, OutT* __restrict__ dq, OutT* __restrict__ dk,
+    OutT* __restrict__ dv, float* __restrict__ dmeta_part, int BH, int L, int d, int W,
+    float scale, int NB, int nseg, int per, int nx, int KG) {
+  using C = SwaWalk;
+  constexpr int P = C::P, PP = C::PP, NT = 64 * SWA_WALK_WAVES;
+  extern __shared__ __align__(16) char smem[];
+  auto kslot = [&](int j) { return reinterpret_cast<bf16*>(smem + C::OFF_K + ((j + 3) % 3) * C::TB); };
+  auto vslot = [&](int j) { return reinterpret_cast<bf16*>(smem + C::OFF_V + ((j + 3) % 3) * C::TB); };
+  auto qbuf = [&](int j) { return reinterpret_cast<bf16*>(smem + C::OFF_Q + (j & 1) * C::TB); };
+  auto dybuf = [&](int j) { return reinterpret_cast<bf16*>(smem + C::OFF_DY + (j & 1) * C::TB); };
+  auto lsebuf = [&](int j) { return reinterpret_cast<float*>(smem + C::OFF_LSE) + (j & 1) * 64; };
+  bf16* p_l = reinterpret_cast<bf16*>(smem + C::OFF_P);
+  bf16* ds_l = reinterpret_cast<bf16*>(smem + C::OFF_DS);
+  float* red = reinterpret_cast<float*>(smem + C::OFF_RED);
+
+  const int lb = xcd_block(blockIdx.x, per, nx);
+  if (lb >= BH * nseg) return;
+  const int bh = lb / nseg, seg = lb % nseg;
+  const int nblk = (L + SWA_TILE - 1) / SWA_TILE;
+  const int b0 = seg * NB, b1 = min(nblk, b0 + NB);
+  const int iend = min(b1, nblk - 1);   // the step past the segment, when there is a block
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, col = lane & 31, h = lane >> 5;
+  const size_t base = (size_t)bh * L * d, kvbase = (size_t)(bh / KG) * L * d;
+  const bf16 *qb = q + base, *dyb = dy + base, *kb = k + kvbase, *vb = v + kvbase;
+  const float* lseb = lse + (size_t)bh * L;
+  const bool vec = VEC || (d & 7) == 0;
+
+  // one 16-byte item per thread of a 64-row tile (row tid / 8, columns
+  // 8 (tid % 8)); rows outside [0, L) read zero
+  auto load_tile = [&](uint4& r, const bf16* src, int r0) {
+    uint4 t[1];
+    load_items<64, NT, 1, NT>(t, src, r0, L, d, vec);
+    r = t[0];
+  };
+  auto store_tile = [&](const uint4& r, bf16* tile) {
+    *reinterpret_cast<uint4*>(tile + (tid >> 3) * P + (tid & 7) * 8) = r;
+  };
+  // lse of a block's 64 rows: every thread loads row tid % 64 and writes it to
+  // LDS (eight equal writes per row), so neither the load nor the write sits
+  // under a branch: a branch there leaves the compiler unsure whether the load
+  // is still in flight, and its wait before the next one also drains the
+  // output stores issued in between
+  const rsrc_t lse_r = make_rsrc(lseb, (size_t)L * 4);
+  auto load_lse = [&](int r0) {
+    const int r = r0 + (tid & 63);
+    return bload_f32(lse_r, r < L ? (uint32_t)r * 4u : OOB);
+  };
+
+  // the first step's rows: key block b0 - 1 (zero rows before the sequence),
+  // block b0; the next block's rows stay in registers until step b0 stores them
+  uint4 pk, pv, pq, pd;
+  float pl;
+  {
+    uint4 k0r, v0r;
+    load_tile(k0r, kb, SWA_TILE * (b0 - 1));
+    load_tile(v0r, vb, SWA_TILE * (b0 - 1));
+    load_tile(pk, kb, SWA_TILE * b0);
+    load_tile(pv, vb, SWA_TILE * b0);
+    load_tile(pq, qb, SWA_TILE * b0);
+    load_tile(pd, dyb, SWA_TILE * b0);
+    pl = load_lse(SWA_TILE * b0);
+    store_tile(k0r, kslot(b0 - 1));
+    store_tile(v0r, vslot(b0 - 1));
+    store_tile(pk, kslot(b0));
+    store_tile(pv, vslot(b0));
+    store_tile(pq, qbuf(b0));
+    store_tile(pd, dybuf(b0));
+    lsebuf(b0)[tid & 63] = pl;
+    if (b0 + 1 <= iend) {
+      load_tile(pk, kb, SWA_TILE * (b0 + 1));
+      load_tile(pv, vb, SWA_TILE * (b0 + 1));
+      load_tile(pq, qb, SWA_TILE * (b0 + 1));
+      load_tile(pd, dyb, SWA_TILE * (b0 + 1));
+      pl = load_lse(SWA_TILE * (b0 + 1));
+    }
+  }
+  __syncthreads();
+
+  // phase-1 pair of this wave (waves 0-5) and phase-2 role
+  const int pA = wave / 3, psub = pA + wave % 3;
+  f32x16 acc[4];   // waves 0-3: acc[0] = dq tile; waves 4-7: dk tiles 0-1, dv tiles 0-1
+#pragma unroll
+  for (int t = 0; t < 4; ++t) acc[t] = zero16();
+  // this lane's terms of T (waves 0 and 3, lane half 0: one query row each)
+  float mmax = -1e30f;
+  for (int j = 0; j < n_meta; ++j) mmax = fmaxf(mmax, meta[j]);
+  float tpart = 0.f;
+  int out_row = -1;   // row of this lane's finished tile (dq: query, dk/dv: key); -1: none
+  auto flush = [&]() {
+    if (wave < 4) {
+      if (out_row >= 0)
+        store_acc_row<OutT>(dq + base, out_row, 32 * (wave & 1), L, d, vec, acc[0], scale, h);
+      acc[0] = zero16();
+    } else if (out_row >= 0) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        store_acc_row<OutT>(dk + base, out_row, 32 * t, L, d, vec, acc[t], scale, h);
+        store_acc_row<OutT>(dv + base, out_row, 32 * t, L, d, vec, acc[2 + t], 1.f, h);
+        acc[t] = zero16();
+        acc[2 + t] = zero16();
+      }
+    }
+    out_row = -1;
+  };
+
+  for (int i = b0; i <= iend; ++i) {
+    const bool own_q = i < b1;
+    // ---- 1a. scores of the wave's pair; its part of delta -------------------
+    const int key0 = SWA_TILE * (i - 1) + 32 * psub, q0 = SWA_TILE * i + 32 * pA, qi = q0 + col;
+    const bool pair = wave < 6 && key0 >= 0 && blocks_meet(q0, key0, L, W);
+    f32x16 pr = zero16(), dpr = zero16();
+    float dpart = 0.f;
+    const float lq = wave < 6 ? lsebuf(i)[32 * pA + col] : 0.f;
+    if (pair) {
+      const bf16* kt = psub < 2 ? kslot(i - 1) : kslot(i);
+      const bf16* vt = psub < 2 ? vslot(i - 1) : vslot(i);
+      const bf16* qt = qbuf(i);
+      const bf16* dyt = dybuf(i);
+      f32x16 s = zero16();
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        s = mfma(row_operand(kt, P, 32 * (psub & 1) + col, 16 * kk, h),
+                 row_operand(qt, P, 32 * pA + col, 16 * kk, h), s);
+        dpr = mfma(row_operand(vt, P, 32 * (psub & 1) + col, 16 * kk, h),
+                   row_operand(dyt, P, 32 * pA + col, 16 * kk, h), dpr);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const bool ok = qi < L && in_window(qi, key0 + acc_row(r, h), W);
+        pr[r] = ok ? fexp(s[r] * scale - lq) : 0.f;
+        dpart += pr[r] * dpr[r];
+      }
+      dpart += xhalf(dpart);
+    }
+    if (wave < 6 && h == 0) red[wave * 32 + col] = dpart;   // zero for an empty pair
+    __syncthreads();
+
+    // ---- 1b. delta; p and ds to LDS; the next block's rows to their slots ----
+    if (wave < 6) {
+      const float* rr = red + 3 * pA * 32 + col;
+      const float del = rr[0] + rr[32] + rr[64];
+      if (pair) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          bf16x4 p4, d4;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int r = 4 * g + e;
+            p4[e] = to_bf16(pr[r]);
+            d4[e] = to_bf16(pr[r] * (dpr[r] - del));
+          }
+          const int at = (32 * pA + col) * PP + 32 * psub + 8 * g + 4 * h;
+          *reinterpret_cast<bf16x4*>(p_l + at) = p4;
+          *reinterpret_cast<bf16x4*>(ds_l + at) = d4;
+        }
+      }
+      if (wave % 3 == 0 && h == 0 && own_q && qi < L) tpart += fexp(mmax - lq) * del;
+    }
+    if (i + 1 <= iend) {   // slots of blocks i - 2 and i - 1: their last readers passed the barrier
+      store_tile(pk, kslot(i + 1));
+      store_tile(pv, vslot(i + 1));
+      store_tile(pq, qbuf(i + 1));
+      store_tile(pd, dybuf(i + 1));
+      lsebuf(i + 1)[tid & 63] = pl;
+    }
+    if (i + 1 <= iend) {
+      if (i + 2 <= iend) {
+        load_tile(pk, kb, SWA_TILE * (i + 2));
+        load_tile(pv, vb, SWA_TILE * (i + 2));
+        load_tile(pq, qb, SWA_TILE * (i + 2));
+        load_tile(pd, dyb, SWA_TILE * (i + 2));
+        pl = load_lse(SWA_TILE * (i + 2));
+      }
+    }
+    __syncthreads();
+
+    // ---- 2. dq of query block i; dk, dv of key blocks i - 1 and i ------------
+    if (wave < 4) {
+      const int A = wave >> 1, t = wave & 1, qa = SWA_TILE * i + 32 * A;
+      if (own_q) {
+#pragma unroll
+        for (int s3 = 0; s3 < 3; ++s3) {
+          const int sub = A + s3, kk0 = SWA_TILE * (i - 1) + 32 * sub;
+          if (kk0 < 0 || !blocks_meet(qa, kk0, L, W)) continue;
+          const bf16* kt = sub < 2 ? kslot(i - 1) : kslot(i);
+#pragma unroll
+          for (int kk = 0; kk < 2; ++kk)
+            acc[0] = mfma(tr_operand_c(kt, P, 32 * (sub & 1) + 16 * kk, 32 * t, lane),
+                          row_operand(ds_l, PP, 32 * A + col, 32 * sub + 16 * kk, h), acc[0]);
+        }
+        out_row = qa + col;
+        flush();
+      }
+    } else {
+      const int par = (wave - 4) >> 1, kh = (wave - 4) & 1;
+      const int j = (i & 1) == par ? i : i - 1;
+      if (j >= b0 && j < b1) {   // a block of this segment
+        const int sub = (j == i ? 2 : 0) + kh, kk0 = SWA_TILE * j + 32 * kh;
+#pragma unroll
+        for (int A = 0; A < 2; ++A) {
+          if (sub < A || sub > A + 2 || !blocks_meet(SWA_TILE * i + 32 * A, kk0, L, W)) continue;
+#pragma unroll
+          for (int kk = 0; kk < 2; ++kk) {
+            const bf16x8 bds = tr_operand_c(ds_l, PP, 32 * A + 16 * kk, 32 * sub, lane);
+            const bf16x8 bp = tr_operand_c(p_l, PP, 32 * A + 16 * kk, 32 * sub, lane);
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+              acc[t] = mfma(tr_operand_c(qbuf(i), P, 32 * A + 16 * kk, 32 * t, lane), bds, acc[t]);
+              acc[2 + t] = mfma(tr_operand_c(dybuf(i), P, 32 * A + 16 * kk, 32 * t, lane), bp,
+                                acc[2 + t]);
+            }
+          }
+        }
+        if (j == i - 1 || j == nblk - 1) out_row = kk0 + col;   // every query of block j is in
+        flush();
+      }
+    }
+  }
+  flush();
+
+  // ---- this workgroup's T --------------------------------------------------
+  if (n_meta > 0) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) tpart += __shfl_xor(tpart, off);
+    __syncthreads();   // every reader of red is past it
+    if (lane == 0 && wave % 3 == 0 && wave < 6) red[wave / 3] = tpart;
+    __syncthreads();
+    if (tid == 0) dmeta_part[lb] = red[0] + red[1];
+  }
+}
+
+// dmeta_j = -e^{meta_j - m} sum_w T_w, the workgroups' T summed in a fixed
+// order (256 strided partial sums, then a halving tree).
+__global__ __launch_bounds__(256) void swa_dmeta_reduce_kernel(const float* __restrict__ part,
+                                                               int rows, const float* __restrict__ meta,
+                                                               int n_meta, float* __restrict__ dmeta) {
+  __shared__ float sh[256];
+  float acc = 0.f;
+  for (int r = threadIdx.x; r < rows; r += 256) acc += part[r];
+  sh[threadIdx.x] = acc;
+  __syncthreads();
+  for (int n = 128; n > 0; n >>= 1) {
+    if ((int)threadIdx.x < n) sh[threadIdx.x] += sh[threadIdx.x + n];
+    __syncthreads();
+  }
+  const float t = sh[0];
+  float mmax = -1e30f;
+  for (int j = 0; j < n_meta; ++j) mmax = fmaxf(mmax, meta[j]);
+  for (int j = threadIdx.x; j < n_meta; j += 256) dmeta[j] = -fexp(meta[j] - mmax) * t;
+}
+// ----------------------------------------------------------------------------
 // host launchers
 // ----------------------------------------------------------------------------
 int swa_padded_dim(int d) {
@@ -544,12 +851,51 @@ static hipError_t launch_swa_fwd_t(const void* q, const void* k, const void* v, 
   return hipGetLastError();
 }
 
+// Blocks per segment of the one-pass backward: enough segments for one
+// workgroup per CU where the rows allow, at least two blocks per segment when
+// there are two (so there are no more segments than the two-kernel form's
+// 128-row blocks, whose dmeta partial rows the workspace holds).
+static int swa_walk_blocks(int BH, int L) {
+  const int nblk = (L + SWA_TILE - 1) / SWA_TILE;
+  const int cus = device_geom().cus;
+  int nb = (BH * nblk + cus - 1) / cus;
+  nb = max(nb, nblk >= 2 ? 2 : 1);
+  return min(min(nb, SWA_WALK_MAX_NB), nblk);
+}
+
+template <typename OutT, bool VEC>
+static hipError_t launch_swa_bwd_walk(const void* q, const void* k, const void* v,
+                                      const float* meta, int n_meta, const float* lse,
+                                      const void* dy, void* dq, void* dk, void* dv,
+                                      float* dmeta_part, float* dmeta, int BH, int L, int d, int W,
+                                      float scale, int KG, hipStream_t st) {
+  const int nblk = (L + SWA_TILE - 1) / SWA_TILE;
+  const int NB = swa_walk_blocks(BH, L), nseg = (nblk + NB - 1) / NB;
+  const int nx = device_geom().xcds, grid = xcd_grid(BH * nseg, nx), per = grid / nx;
+  hipError_t e = ensure_lds<swa_bwd_walk_kernel<OutT, VEC>>(SwaWalk::LDS);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((swa_bwd_walk_kernel<OutT, VEC>), dim3(grid), dim3(64 * SWA_WALK_WAVES),
+                     SwaWalk::LDS, st, (const bf16*)q, (const bf16*)k, (const bf16*)v, meta,
+                     n_meta, lse, (const bf16*)dy, (OutT*)dq, (OutT*)dk, (OutT*)dv, dmeta_part, BH,
+                     L, d, W, scale, NB, nseg, per, nx, KG);
+  if ((e = hipGetLastError()) != hipSuccess || n_meta == 0) return e;
+  hipLaunchKernelGGL(swa_dmeta_reduce_kernel, dim3(1), dim3(256), 0, st,
+                     (const float*)dmeta_part, BH * nseg, meta, n_meta, dmeta);
+  return hipGetLastError();
+}
+
 template <int DP, typename OutT, bool VEC>
 static hipError_t launch_swa_bwd_t(const void* q, const void* k, const void* v, const float* meta,
                                    int n_meta, const float* lse, const void* dy, void* dq,
                                    void* dk, void* dv, float* delta, float* dmeta_part,
                                    float* dmeta, int BH, int L, int d, int W, float scale, int KG,
                                    hipStream_t st) {
+  // W <= 64 at d <= 64: the one-pass walk (no delta buffer)
+  if constexpr (DP == 64) {
+    if (W <= SWA_TILE)
+      return launch_swa_bwd_walk<OutT, VEC>(q, k, v, meta, n_meta, lse, dy, dq, dk, dv, dmeta_part,
+                                            dmeta, BH, L, d, W, scale, KG, st);
+  }
   int per, grid, nx;
   swa_grid(BH, L, &per, &grid, &nx);
   // the window's key tiles fit the LDS slots of the resident form when a
