@@ -94,16 +94,25 @@ constexpr int swa_fwd_occupancy() {
   return DP <= 32 ? 4 : DP <= 64 ? (VEC ? 4 : 3) : DP <= 128 ? 2 : 1;
 }
 
-template <int DP, bool VEC>
-__global__ __launch_bounds__(256, (swa_fwd_occupancy<DP, VEC>())) void swa_fwd_kernel(
+// RES: the window's key tiles (at most SWA_RES of them) are loaded at once,
+// each into its own LDS slot, behind one barrier, where the streaming form
+// waits for one tile per barrier: for grids of at most two workgroups per CU,
+// where each workgroup's chain of tile loads, not the CU's throughput, sets
+// the time.
+constexpr int SWA_RES = 4;
+
+template <int DP, bool VEC, bool RES>
+__global__ __launch_bounds__(256, (RES ? 2 : swa_fwd_occupancy<DP, VEC>())) void swa_fwd_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ meta, int n_meta, bf16* __restrict__ y, float* __restrict__ lse,
     int BH, int L, int d, int W, float scale, int per, int nx, int KG) {
   using Cfg = SwaCfg<DP>;
   constexpr int P = Cfg::P;
+  constexpr int NSLOT = RES ? SWA_RES : 1;
   extern __shared__ __align__(16) char smem[];
-  bf16* k_l = reinterpret_cast<bf16*>(smem);
-  bf16* v_l = reinterpret_cast<bf16*>(smem + Cfg::TILE_BYTES);
+  // k tile of slot i at smem + i TILE_BYTES, v tile at smem + (NSLOT + i) TILE_BYTES
+  auto kslot = [&](int i) { return reinterpret_cast<bf16*>(smem + i * Cfg::TILE_BYTES); };
+  auto vslot = [&](int i) { return reinterpret_cast<bf16*>(smem + (NSLOT + i) * Cfg::TILE_BYTES); };
 
   const int nqb = (L + SWA_ROWS - 1) / SWA_ROWS;
   const int lb = xcd_block(blockIdx.x, per, nx);
@@ -132,20 +141,8 @@ __global__ __launch_bounds__(256, (swa_fwd_occupancy<DP, VEC>())) void swa_fwd_k
 #pragma unroll
   for (int t = 0; t < DP / 32; ++t) o[t] = zero16();
 
-  const int klo = (max(0, Q0 - W + 1) / SWA_TILE) * SWA_TILE;
-  const int khi = min(L, Q0 + SWA_ROWS);
-  uint4 rk[Cfg::NL], rv[Cfg::NL];
-  swa_load<DP>(rk, k + kvbase, klo, L, d, vec);
-  swa_load<DP>(rv, v + kvbase, klo, L, d, vec);
-  swa_store<DP>(rk, k_l);
-  swa_store<DP>(rv, v_l);
-  __syncthreads();
-  for (int t0 = klo; t0 < khi; t0 += SWA_TILE) {
-    const bool more = t0 + SWA_TILE < khi;
-    if (more) {
-      swa_load<DP>(rk, k + kvbase, t0 + SWA_TILE, L, d, vec);
-      swa_load<DP>(rv, v + kvbase, t0 + SWA_TILE, L, d, vec);
-    }
+  // the work of one key tile (keys t0 .. t0+63 in k_l, v_l)
+  auto tile = [&](const bf16* k_l, const bf16* v_l, int t0) __attribute__((always_inline)) {
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
       const int k0 = t0 + 32 * half;
@@ -191,11 +188,47 @@ __global__ __launch_bounds__(256, (swa_fwd_occupancy<DP, VEC>())) void swa_fwd_k
           o[t] = mfma(tr_operand(v_l, P, 32 * half + 16 * kb, t * 32, lane), p[kb], o[t]);
       }
     }
-    if (more) {
-      __syncthreads();
-      swa_store<DP>(rk, k_l);
-      swa_store<DP>(rv, v_l);
-      __syncthreads();
+  };
+
+  const int klo = (max(0, Q0 - W + 1) / SWA_TILE) * SWA_TILE;
+  const int khi = min(L, Q0 + SWA_ROWS);
+  if constexpr (RES) {
+    const int nt = (khi - klo + SWA_TILE - 1) / SWA_TILE;   // <= SWA_RES (the launcher's test)
+    uint4 rk[SWA_RES][Cfg::NL], rv[SWA_RES][Cfg::NL];
+#pragma unroll
+    for (int i = 0; i < SWA_RES; ++i)
+      if (i < nt) {
+        swa_load<DP>(rk[i], k + kvbase, klo + i * SWA_TILE, L, d, vec);
+        swa_load<DP>(rv[i], v + kvbase, klo + i * SWA_TILE, L, d, vec);
+      }
+#pragma unroll
+    for (int i = 0; i < SWA_RES; ++i)
+      if (i < nt) {
+        swa_store<DP>(rk[i], kslot(i));
+        swa_store<DP>(rv[i], vslot(i));
+      }
+    __syncthreads();
+    for (int i = 0; i < nt; ++i) tile(kslot(i), vslot(i), klo + i * SWA_TILE);
+  } else {
+    uint4 rk[Cfg::NL], rv[Cfg::NL];
+    swa_load<DP>(rk, k + kvbase, klo, L, d, vec);
+    swa_load<DP>(rv, v + kvbase, klo, L, d, vec);
+    swa_store<DP>(rk, kslot(0));
+    swa_store<DP>(rv, vslot(0));
+    __syncthreads();
+    for (int t0 = klo; t0 < khi; t0 += SWA_TILE) {
+      const bool more = t0 + SWA_TILE < khi;
+      if (more) {
+        swa_load<DP>(rk, k + kvbase, t0 + SWA_TILE, L, d, vec);
+        swa_load<DP>(rv, v + kvbase, t0 + SWA_TILE, L, d, vec);
+      }
+      tile(kslot(0), vslot(0), t0);
+      if (more) {
+        __syncthreads();
+        swa_store<DP>(rk, kslot(0));
+        swa_store<DP>(rv, vslot(0));
+        __syncthreads();
+      }
     }
   }
   // every lane stores (rows past L are dropped): the row store swaps across lane halves
@@ -222,7 +255,6 @@ constexpr int swa_bwd_occupancy() {
 // each: pass 0 streams them in with one barrier per tile, pass 1 reads them
 // back with no loads and no barriers.  Otherwise both passes stream the tiles
 // through one k and one v buffer.
-constexpr int SWA_RES = 4;
 
 template <int DP, typename OutT, bool VEC, bool RES>
 __global__ __launch_bounds__(256, (swa_bwd_occupancy<DP>())) void swa_bwd_dq_kernel(
@@ -835,20 +867,36 @@ static void swa_grid(int BH, int L, int* per, int* grid, int* nx) {
 
 int swa_row_blocks(int L) { return (L + SWA_ROWS - 1) / SWA_ROWS; }
 
+template <int DP, bool VEC, bool RES>
+static hipError_t launch_swa_fwd_r(const void* q, const void* k, const void* v, const float* meta,
+                                   int n_meta, void* y, float* lse, int BH, int L, int d, int W,
+                                   float scale, int KG, hipStream_t st) {
+  const size_t lds = 2 * (RES ? SWA_RES : 1) * SwaCfg<DP>::TILE_BYTES;
+  hipError_t e = ensure_lds<swa_fwd_kernel<DP, VEC, RES>>((int)lds);
+  if (e != hipSuccess) return e;
+  int per, grid, nx;
+  swa_grid(BH, L, &per, &grid, &nx);
+  hipLaunchKernelGGL((swa_fwd_kernel<DP, VEC, RES>), dim3(grid), dim3(256), lds, st,
+                     (const bf16*)q, (const bf16*)k, (const bf16*)v, meta, n_meta, (bf16*)y, lse,
+                     BH, L, d, W, scale, per, nx, KG);
+  return hipGetLastError();
+}
+
 template <int DP, bool VEC>
 static hipError_t launch_swa_fwd_t(const void* q, const void* k, const void* v, const float* meta,
                                    int n_meta, void* y, float* lse, int BH, int L, int d, int W,
                                    float scale, int KG, hipStream_t st) {
-  const size_t lds = 2 * SwaCfg<DP>::TILE_BYTES;
-  auto kern = swa_fwd_kernel<DP, VEC>;
-  hipError_t e = ensure_lds<swa_fwd_kernel<DP, VEC>>((int)lds);
-  if (e != hipSuccess) return e;
-  int per, grid, nx;
-  swa_grid(BH, L, &per, &grid, &nx);
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(256), lds, st, (const bf16*)q, (const bf16*)k,
-                     (const bf16*)v, meta, n_meta, (bf16*)y, lse, BH, L, d, W, scale, per, nx,
-                     KG);
-  return hipGetLastError();
+  // resident tiles at d <= 64 when a block's keys span at most SWA_RES tiles
+  // (SWA_ROWS + W + 62 <= SWA_RES * SWA_TILE, as the dq kernel's) and the
+  // grid is at most two workgroups per CU (the slots allow two per CU)
+  if constexpr (DP <= 64) {
+    if (SWA_ROWS + W + 62 <= SWA_RES * SWA_TILE &&
+        BH * swa_row_blocks(L) <= 2 * device_geom().cus)
+      return launch_swa_fwd_r<DP, VEC, true>(q, k, v, meta, n_meta, y, lse, BH, L, d, W, scale,
+                                             KG, st);
+  }
+  return launch_swa_fwd_r<DP, VEC, false>(q, k, v, meta, n_meta, y, lse, BH, L, d, W, scale, KG,
+                                          st);
 }
 
 // Blocks per segment of the one-pass backward: enough segments for one
