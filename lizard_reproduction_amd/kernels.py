@@ -64,9 +64,21 @@ def _refuse_capture(what):
     whole fwd+bwd crashed the host process once (in the runtime's capture
     end) and neither step has been cleared as its cause, so capture is not
     offered."""
-    if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
+    if _gpu_present() and torch.cuda.is_current_stream_capturing():
         raise RuntimeError(f"{what}: calls under HIP graph capture are not supported "
                            "(run the kernels eagerly)")
+
+
+_GPU_SEEN = False
+
+
+def _gpu_present():
+    """torch.cuda.is_available(), remembered once true (it is asked on every
+    launch, and the query costs about a microsecond of host time)."""
+    global _GPU_SEEN
+    if not _GPU_SEEN:
+        _GPU_SEEN = torch.cuda.is_available()
+    return _GPU_SEEN
 
 
 def _require_gpu(*tensors):
@@ -403,6 +415,8 @@ def _check_swa(q, k, v, meta, window, fwd_blocks, bwd_blocks):
     if not isinstance(window, int) or window < 1:
         raise ValueError(f"swa: window must be a positive int, got {window!r}")
     for blocks in (fwd_blocks, bwd_blocks):
+        if blocks is FWD_BLOCKS or blocks is BWD_BLOCKS:   # the defaults, valid
+            continue
         if len(tuple(blocks)) != 2 or any(int(x) < 1 for x in blocks):
             raise ValueError(f"swa: blocks must be two positive ints, got {blocks!r}")
     _require_gpu(q, k, v)
