@@ -476,6 +476,11 @@ struct ProBwd {
   static_assert(GI * RSTEP * IPR == PRO_BLOCK * IPR && RSTEP == 32, "item mapping");
   static_assert(XI * NT == PRO_BLOCK * (HP / 8), "row items");
   static constexpr bool FITS = LDS <= 160 * 1024;   // instantiated for launch only when it fits
+  // the next block's x rows and the epilogue's first-head operands are issued
+  // a phase early (their latency then hides behind the dW passes): where one
+  // workgroup per CU leaves the registers for them (bf16, head_dim <= 64);
+  // elsewhere the held loads push the kernel into spills
+  static constexpr bool PRE = OCC == 1 && HT <= 2 && !C::SPLIT;
 };
 
 template <typename T>
@@ -533,7 +538,9 @@ prologue_bwd_kernel(ProBwdArgs a) {
   const T* cs = static_cast<const T*>(a.cos);
   const T* sn = static_cast<const T*>(a.sin);
   const int f = a.f, hd = HP, half_hd = HP / 2, F2 = 2 * a.f;
-  const bool vec = (f & 7) == 0;   // gradient items are whole 16-byte pieces
+  // gradient items are whole 16-byte pieces (always without a partial tile:
+  // then f is a multiple of 32)
+  const bool vec = !PART || (f & 7) == 0;
 
   // stage items of this thread: rows tid / IPR + 32 i of a block; item k of a
   // row covers features 8 (k & 3) .. +8 of tile ftile(k / 8, s) of the dp
@@ -561,7 +568,6 @@ prologue_bwd_kernel(ProBwdArgs a) {
   // workgroup gets its share of both (kv blocks carry the group's gradients).
   bool kv = false;
   int role = -1, heads_in = 0, group = 1, nrows = 0;
-  const T* x = nullptr;
   const bf16 *dphi = nullptr, *drope = nullptr;
   T* dx = nullptr;
   f32x16 dw[OWN];
@@ -569,7 +575,25 @@ prologue_bwd_kernel(ProBwdArgs a) {
   for (int i = 0; i < OWN; ++i) dw[i] = zero16();
 
   const int nb = a.nbq + a.nbk;
+  // x rows of block jb (this thread's XI items): with PRE issued during the
+  // previous block's dW passes, so the next block starts with its rows in
+  // registers; else at the block's start.  Rows past the end read the last
+  // row's address and are zeroed at use.
+  auto x_items = [&](int jb, Raw8<T> (&dst)[K::XI]) {
+    const bool kvb = jb >= a.nbq;
+    const T* xs = static_cast<const T*>(kvb ? a.k : a.q);
+    const int nr = a.B * a.L * (kvb ? a.Hkv : a.H);
+    const int r0 = (kvb ? jb - a.nbq : jb) * PRO_BLOCK;
+#pragma unroll
+    for (int i = 0; i < K::XI; ++i) {
+      const int idx = tid + NT * i, r = idx / H8, m0 = 8 * (idx % H8);
+      dst[i] = load8r(xs + (long)min(r0 + r, nr - 1) * hd + m0);
+    }
+  };
+  Raw8<T> xpre[K::XI];
+  if (K::PRE && (int)blockIdx.x < nb) x_items(blockIdx.x, xpre);
   for (int j = blockIdx.x; j < nb; j += gridDim.x) {
+    if constexpr (!K::PRE) x_items(j, xpre);
     const int r_j = j < a.nbq ? 0 : 1;
     if (r_j != role) {   // uniform; the W tile's readers passed the last block's barriers
       if (role == 0) {
@@ -584,7 +608,6 @@ prologue_bwd_kernel(ProBwdArgs a) {
       heads_in = kv ? a.Hkv : a.H;
       group = kv ? a.H / a.Hkv : 1;
       nrows = a.B * a.L * heads_in;
-      x = static_cast<const T*>(kv ? a.k : a.q);
       dphi = kv ? a.dfk : a.dfq;
       drope = kv ? a.dkr : a.dqr;
       dx = static_cast<T*>(kv ? a.dk : a.dq);
@@ -608,7 +631,7 @@ prologue_bwd_kernel(ProBwdArgs a) {
     // Gradient items of local tile s: the loads of the first GQ heads are
     // issued a tile ahead (raw, 16 bytes each) and summed when the tile is
     // staged; heads past GQ are loaded and added then.
-    auto item_ok = [&](int i, int c) { return gbase[i] >= 0 && c < f; };
+    auto item_ok = [&](int i, int c) { return gbase[i] >= 0 && (!PART || c < f); };
     auto issue = [&](int s, uint4 (&raw)[K::GQR][K::GI]) {
       const int c = 32 * ftile(sgrp, s) + scol;
 #pragma unroll
@@ -676,9 +699,8 @@ prologue_bwd_kernel(ProBwdArgs a) {
     for (int i = 0; i < K::XI; ++i) {
       const int idx = tid + NT * i, r = idx / H8, m0 = 8 * (idx % H8);
       float xf[8];
-      if (row0 + r < nrows) {
-        load8f(x + (long)(row0 + r) * hd + m0, xf);
-      } else {
+      cvt8(xpre[i], xf);
+      if (row0 + r >= nrows) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) xf[e] = 0.f;
       }
@@ -840,6 +862,39 @@ prologue_bwd_kernel(ProBwdArgs a) {
       }
     }
 
+    // ---- with PRE: the epilogue operands of the group's first head and the
+    // RoPE tables, issued before the dW passes, whose barriers and MFMA work
+    // then cover their latency (the later heads of a kv group load in phase
+    // 6), and the next block's x rows.  Rows past the end read the last row's
+    // addresses and are not stored.
+    // dx[m] = dr[m] cos[m] + dr[m + hd/2] sin[m + hd/2] for m < hd/2,
+    //         dr[m] cos[m] - dr[m - hd/2] sin[m - hd/2] otherwise (drope summed
+    // over the group's heads); the kv rows also sum dv (and dv2) over the group.
+    // The dv loads of a q row (and dv2's when there is none) read a valid
+    // address whose value is dropped, so there is no branch between them.
+    const bool use_dv = kv, use_dv2 = kv && a.dv2 != nullptr;
+    constexpr int EXI = K::PRE ? K::XI : 1;
+    long ebase[EXI];
+    Raw8<T> ec[EXI], es[EXI];
+    bf16x8 er0[EXI], er1[EXI], ev0[EXI], ev1[EXI];
+#pragma unroll
+    for (int i = 0; i < (K::PRE ? K::XI : 0); ++i) {
+      const int idx = tid + NT * i, r = idx / H8, m0 = 8 * (idx % H8);
+      const int row = min(row0 + r, nrows - 1);
+      const RowPos pos = decode(row, a.L, heads_in);
+      ebase[i] = ((long)pos.b * a.H + pos.head * group) * a.L + pos.l;
+      const int mp2 = m0 < half_hd ? m0 + half_hd : m0 - half_hd;
+      const long tab = ((long)pos.b * a.cos_bstride + pos.l) * hd;
+      const long o = ebase[i] * hd;
+      er0[i] = *reinterpret_cast<const bf16x8*>(drope + o + m0);
+      er1[i] = *reinterpret_cast<const bf16x8*>(drope + o + mp2);
+      ev0[i] = *reinterpret_cast<const bf16x8*>(use_dv ? a.dv + o + m0 : drope + o + m0);
+      ev1[i] = *reinterpret_cast<const bf16x8*>(use_dv2 ? a.dv2 + o + m0 : drope + o + m0);
+      ec[i] = load8r(cs + tab + m0);
+      es[i] = load8r(sn + tab + mp2);
+    }
+    if (K::PRE && j + (int)gridDim.x < nb) x_items(j + gridDim.x, xpre);
+
     // ---- 5. dW += dxw^T x over the block: dxw hi, then lo --------------------
 #pragma unroll
     for (int part = 0; part < 2; ++part) {
@@ -881,55 +936,100 @@ prologue_bwd_kernel(ProBwdArgs a) {
                     dacc[ht][4 * q4 + 3]};
     }
     __syncthreads();
-    // dx[m] = dr[m] cos[m] + dr[m + hd/2] sin[m + hd/2] for m < hd/2,
-    //         dr[m] cos[m] - dr[m - hd/2] sin[m - hd/2] otherwise (drope summed
-    // over the group's heads); the kv rows also sum dv (and dv2) over the group.
-    // Two items' loads overlap (unrolled by 2): the Jacobian's registers are free here.
-#pragma unroll 2
-    for (int i = 0; i < K::XI; ++i) {
-      const int idx = tid + NT * i, r = idx / H8, m0 = 8 * (idx % H8);
-      const int row = row0 + r;
-      if (row >= nrows) continue;
-      const RowPos pos = decode(row, a.L, heads_in);
-      const long obase = ((long)pos.b * a.H + pos.head * group) * a.L + pos.l;
-      const int mp2 = m0 < half_hd ? m0 + half_hd : m0 - half_hd;
-      const float sign = m0 < half_hd ? 1.f : -1.f;
-      float dr[8], dr2[8], dvs[8];
+    if constexpr (K::PRE) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) dr[e] = dr2[e] = dvs[e] = 0.f;
-      // a head's four loads issue before any of them is summed; the dv loads
-      // of a q row (and dv2's when there is none) read a valid address whose
-      // value is dropped, so there is no branch between them
-      const bool use_dv = kv, use_dv2 = kv && a.dv2 != nullptr;
-#pragma unroll 2
-      for (int g = 0; g < group; ++g) {
-        const long o = (obase + (long)g * a.L) * hd;
-        const bf16x8 r0 = *reinterpret_cast<const bf16x8*>(drope + o + m0);
-        const bf16x8 r1 = *reinterpret_cast<const bf16x8*>(drope + o + mp2);
-        const bf16x8 v0 = *reinterpret_cast<const bf16x8*>(use_dv ? a.dv + o + m0 : drope + o + m0);
-        const bf16x8 v1 = *reinterpret_cast<const bf16x8*>(use_dv2 ? a.dv2 + o + m0 : drope + o + m0);
+      for (int i = 0; i < K::XI; ++i) {
+        const int idx = tid + NT * i, r = idx / H8, m0 = 8 * (idx % H8);
+        const int row = row0 + r;
+        const int mp2 = m0 < half_hd ? m0 + half_hd : m0 - half_hd;
+        const float sign = m0 < half_hd ? 1.f : -1.f;
+        float dr[8], dr2[8], dvs[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          dr[e] += to_f32(r0[e]);
-          dr2[e] += to_f32(r1[e]);
-          dvs[e] += use_dv ? to_f32(v0[e]) : 0.f;
-          dvs[e] += use_dv2 ? to_f32(v1[e]) : 0.f;
+          dr[e] = to_f32(er0[i][e]);
+          dr2[e] = to_f32(er1[i][e]);
+          dvs[e] = use_dv ? to_f32(ev0[i][e]) : 0.f;
+          dvs[e] += use_dv2 ? to_f32(ev1[i][e]) : 0.f;
+        }
+        // the group's later heads: a head's four loads issue before any of them is summed
+#pragma unroll 2
+        for (int g = 1; g < group; ++g) {
+          const long o = (ebase[i] + (long)g * a.L) * hd;
+          const bf16x8 r0 = *reinterpret_cast<const bf16x8*>(drope + o + m0);
+          const bf16x8 r1 = *reinterpret_cast<const bf16x8*>(drope + o + mp2);
+          const bf16x8 v0 = *reinterpret_cast<const bf16x8*>(use_dv ? a.dv + o + m0 : drope + o + m0);
+          const bf16x8 v1 = *reinterpret_cast<const bf16x8*>(use_dv2 ? a.dv2 + o + m0 : drope + o + m0);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            dr[e] += to_f32(r0[e]);
+            dr2[e] += to_f32(r1[e]);
+            dvs[e] += use_dv ? to_f32(v0[e]) : 0.f;
+            dvs[e] += use_dv2 ? to_f32(v1[e]) : 0.f;
+          }
+        }
+        float c[8], s2[8], out[8];
+        cvt8(ec[i], c);
+        cvt8(es[i], s2);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) out[e] = dr[e] * c[e] + sign * dr2[e] * s2[e];
+#pragma unroll
+        for (int g2 = 0; g2 < NWF; ++g2) {   // the shares in group order
+          const float* dxr = dx_l + (g2 * PRO_BLOCK + r) * AP + m0;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) out[e] += dxr[e];
+        }
+        if (row < nrows) {
+          store8v(dx + (long)row * hd + m0, out);
+          if (kv) store8v(static_cast<T*>(a.dvo) + (long)row * hd + m0, dvs);
         }
       }
-      const long tab = ((long)pos.b * a.cos_bstride + pos.l) * hd;
-      float c[8], s2[8], out[8];
-      load8f(cs + tab + m0, c);
-      load8f(sn + tab + mp2, s2);
+    } else {
+      // Two items' loads overlap (unrolled by 2): the Jacobian's registers are free here.
+#pragma unroll 2
+      for (int i = 0; i < K::XI; ++i) {
+        const int idx = tid + NT * i, r = idx / H8, m0 = 8 * (idx % H8);
+        const int row = row0 + r;
+        if (row >= nrows) continue;
+        const RowPos pos = decode(row, a.L, heads_in);
+        const long obase = ((long)pos.b * a.H + pos.head * group) * a.L + pos.l;
+        const int mp2 = m0 < half_hd ? m0 + half_hd : m0 - half_hd;
+        const float sign = m0 < half_hd ? 1.f : -1.f;
+        float dr[8], dr2[8], dvs[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) out[e] = dr[e] * c[e] + sign * dr2[e] * s2[e];
+        for (int e = 0; e < 8; ++e) dr[e] = dr2[e] = dvs[e] = 0.f;
+        // a head's four loads issue before any of them is summed; the dv loads
+        // of a q row (and dv2's when there is none) read a valid address whose
+        // value is dropped, so there is no branch between them
+#pragma unroll 2
+        for (int g = 0; g < group; ++g) {
+          const long o = (obase + (long)g * a.L) * hd;
+          const bf16x8 r0 = *reinterpret_cast<const bf16x8*>(drope + o + m0);
+          const bf16x8 r1 = *reinterpret_cast<const bf16x8*>(drope + o + mp2);
+          const bf16x8 v0 = *reinterpret_cast<const bf16x8*>(use_dv ? a.dv + o + m0 : drope + o + m0);
+          const bf16x8 v1 = *reinterpret_cast<const bf16x8*>(use_dv2 ? a.dv2 + o + m0 : drope + o + m0);
 #pragma unroll
-      for (int g2 = 0; g2 < NWF; ++g2) {   // the shares in group order
-        const float* dxr = dx_l + (g2 * PRO_BLOCK + r) * AP + m0;
+          for (int e = 0; e < 8; ++e) {
+            dr[e] += to_f32(r0[e]);
+            dr2[e] += to_f32(r1[e]);
+            dvs[e] += use_dv ? to_f32(v0[e]) : 0.f;
+            dvs[e] += use_dv2 ? to_f32(v1[e]) : 0.f;
+          }
+        }
+        const long tab = ((long)pos.b * a.cos_bstride + pos.l) * hd;
+        float c[8], s2[8], out[8];
+        load8f(cs + tab + m0, c);
+        load8f(sn + tab + mp2, s2);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) out[e] += dxr[e];
+        for (int e = 0; e < 8; ++e) out[e] = dr[e] * c[e] + sign * dr2[e] * s2[e];
+#pragma unroll
+        for (int g2 = 0; g2 < NWF; ++g2) {   // the shares in group order
+          const float* dxr = dx_l + (g2 * PRO_BLOCK + r) * AP + m0;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) out[e] += dxr[e];
+        }
+        store8v(dx + (long)row * hd + m0, out);
+        if (kv) store8v(static_cast<T*>(a.dvo) + (long)row * hd + m0, dvs);
       }
-      store8v(dx + (long)row * hd + m0, out);
-      if (kv) store8v(static_cast<T*>(a.dvo) + (long)row * hd + m0, dvs);
     }
     if constexpr (K::DX_OVER_X) __syncthreads();
   }
