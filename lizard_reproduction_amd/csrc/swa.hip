@@ -828,24 +828,24 @@ __global__ __launch_bounds__(64 * SWA_WALK_WAVES, 1) void swa_bwd_walk_kernel(
 }
 
 // dmeta_j = -e^{meta_j - m} sum_w T_w, the workgroups' T summed in a fixed
-// order (256 strided partial sums, then a halving tree).
-__global__ __launch_bounds__(256) void swa_dmeta_reduce_kernel(const float* __restrict__ part,
-                                                               int rows, const float* __restrict__ meta,
-                                                               int n_meta, float* __restrict__ dmeta) {
-  __shared__ float sh[256];
-  float acc = 0.f;
-  for (int r = threadIdx.x; r < rows; r += 256) acc += part[r];
-  sh[threadIdx.x] = acc;
-  __syncthreads();
-  for (int n = 128; n > 0; n >>= 1) {
-    if ((int)threadIdx.x < n) sh[threadIdx.x] += sh[threadIdx.x + n];
-    __syncthreads();
-  }
-  const float t = sh[0];
+// order by one wave (strided lane sums, then a butterfly); the sinks' loads
+// issue first, so the kernel's one chain is a load and a wave reduction.
+__global__ __launch_bounds__(64) void swa_dmeta_reduce_kernel(const float* __restrict__ part,
+                                                              int rows, const float* __restrict__ meta,
+                                                              int n_meta, float* __restrict__ dmeta) {
+  const int lane = threadIdx.x;
   float mmax = -1e30f;
-  for (int j = 0; j < n_meta; ++j) mmax = fmaxf(mmax, meta[j]);
-  for (int j = threadIdx.x; j < n_meta; j += 256) dmeta[j] = -fexp(meta[j] - mmax) * t;
+  for (int j = lane; j < n_meta; j += 64) mmax = fmaxf(mmax, meta[j]);
+  float t = 0.f;
+  for (int r = lane; r < rows; r += 64) t += part[r];
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    t += __shfl_xor(t, off);
+    mmax = fmaxf(mmax, __shfl_xor(mmax, off));
+  }
+  for (int j = lane; j < n_meta; j += 64) dmeta[j] = -fexp(meta[j] - mmax) * t;
 }
+
 // ----------------------------------------------------------------------------
 // host launchers
 // ----------------------------------------------------------------------------
@@ -927,7 +927,7 @@ static hipError_t launch_swa_bwd_walk(const void* q, const void* k, const void* 
                      n_meta, lse, (const bf16*)dy, (OutT*)dq, (OutT*)dk, (OutT*)dv, dmeta_part, BH,
                      L, d, W, scale, NB, nseg, per, nx, KG);
   if ((e = hipGetLastError()) != hipSuccess || n_meta == 0) return e;
-  hipLaunchKernelGGL(swa_dmeta_reduce_kernel, dim3(1), dim3(256), 0, st,
+  hipLaunchKernelGGL(swa_dmeta_reduce_kernel, dim3(1), dim3(64), 0, st,
                      (const float*)dmeta_part, BH * nseg, meta, n_meta, dmeta);
   return hipGetLastError();
 }
