@@ -203,42 +203,54 @@ __device__ __forceinline__ f32x16 project_tile(int ft, const bf16x8 (&xh)[Pro<T,
   return acc;
 }
 
-// Row statistics of the two softmaxes over the valid features (< f):
-// maxima and reciprocal sums, combined over both lane halves.
-template <typename T, int FT, int HT>
+// Two softmax statistics (running max m, sum s of e^{x - m}) of one row merged.
+__device__ __forceinline__ void merge_stats(float& m, float& s, float mo, float so) {
+  const float m2 = fmaxf(m, mo);
+  s = s * fexp(m - m2) + so * fexp(mo - m2);
+  m = m2;
+}
+
+// Row statistics of the two softmaxes over the valid features (< f) in one
+// pass over the feature tiles: per tile its maxima, the running sums rescaled
+// to them (e^{x - m} as exp2 of one FMA), then the two lane halves' merged;
+// returns the maxima and the reciprocal sums.  PART: the last tile is partly
+// padding (f < 32 FT), masked; without it there are no masks.
+template <typename T, int FT, int HT, bool PART>
 __device__ __forceinline__ void softmax_stats(const bf16x8 (&xh)[Pro<T, FT, HT>::HK],
                                               const bf16x8 (&xl)[Pro<T, FT, HT>::HK],
                                               const bf16* w_hi, const bf16* w_lo, int f,
                                               int lane, float& mp, float& mn, float& ip,
                                               float& in) {
   const int h = lane >> 5;
-  mp = NEG_INF;
-  mn = NEG_INF;
-#pragma unroll
-  for (int ft = 0; ft < FT; ++ft) {
-    const f32x16 acc = project_tile<T, FT, HT>(ft, xh, xl, w_hi, w_lo, lane);
-#pragma unroll
-    for (int r = 0; r < 16; ++r)
-      if (32 * ft + acc_row(r, h) < f) {
-        mp = fmaxf(mp, acc[r]);
-        mn = fmaxf(mn, -acc[r]);
-      }
-  }
-  mp = fmaxf(mp, xhalf(mp));
-  mn = fmaxf(mn, xhalf(mn));
+  mp = -1e30f;
+  mn = -1e30f;
   float sp = 0.f, sn = 0.f;
 #pragma unroll
   for (int ft = 0; ft < FT; ++ft) {
     const f32x16 acc = project_tile<T, FT, HT>(ft, xh, xl, w_hi, w_lo, lane);
+    float tp = -1e30f, tn = -1e30f;
 #pragma unroll
-    for (int r = 0; r < 16; ++r)
-      if (32 * ft + acc_row(r, h) < f) {
-        sp += fexp(acc[r] - mp);
-        sn += fexp(-acc[r] - mn);
-      }
+    for (int r = 0; r < 16; ++r) {
+      const bool ok = !PART || 32 * ft + acc_row(r, h) < f;
+      tp = fmaxf(tp, ok ? acc[r] : -1e30f);
+      tn = fmaxf(tn, ok ? -acc[r] : -1e30f);
+    }
+    const float np = fmaxf(mp, tp), nn = fmaxf(mn, tn);
+    const float cp = -np * LOG2E, cn = -nn * LOG2E;
+    float ap = 0.f, an = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const bool ok = !PART || 32 * ft + acc_row(r, h) < f;
+      ap += ok ? __builtin_amdgcn_exp2f(fmaf(acc[r], LOG2E, cp)) : 0.f;
+      an += ok ? __builtin_amdgcn_exp2f(fmaf(acc[r], -LOG2E, cn)) : 0.f;
+    }
+    sp = sp * fexp(mp - np) + ap;
+    sn = sn * fexp(mn - nn) + an;
+    mp = np;
+    mn = nn;
   }
-  sp += xhalf(sp);
-  sn += xhalf(sn);
+  merge_stats(mp, sp, xhalf(mp), xhalf(sp));
+  merge_stats(mn, sn, xhalf(mn), xhalf(sn));
   ip = 1.f / sp;
   in = 1.f / sn;
 }
@@ -277,7 +289,7 @@ __device__ __forceinline__ void copy_rows(const bf16* stage, int pitch, bf16* __
 // ---------------------------------------------------------------------------
 // forward
 // ---------------------------------------------------------------------------
-template <typename T, int FT, int HT>
+template <typename T, int FT, int HT, bool PART>
 __global__ __launch_bounds__(256, 2) void prologue_fwd_kernel(ProFwdArgs a) {
   using C = Pro<T, FT, HT>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -378,7 +390,9 @@ __global__ __launch_bounds__(256, 2) void prologue_fwd_kernel(ProFwdArgs a) {
     // map itself, lz_gla_fwd_phi); fout is uniform per workgroup
     if (fout == nullptr) continue;
     float mp, mn, ip, in;
-    softmax_stats<T, FT, HT>(xh, xl, w_hi, w_lo, f, lane, mp, mn, ip, in);
+    softmax_stats<T, FT, HT, PART>(xh, xl, w_hi, w_lo, f, lane, mp, mn, ip, in);
+    // e^{x - m} / sum as exp2 of one FMA, times the reciprocal sum
+    const float cp = -mp * LOG2E, cn = -mn * LOG2E;
 
     // the two halves of the feature row, staged through LDS for row-contiguous stores
     const int ob_lo = (int)(obase & 0xffffffff), ob_hi = (int)(obase >> 32);
@@ -393,7 +407,8 @@ __global__ __launch_bounds__(256, 2) void prologue_fwd_kernel(ProFwdArgs a) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const float s = acc[4 * q4 + e];
-            o[e] = to_bf16(half == 0 ? fexp(s - mp) * ip : fexp(-s - mn) * in);
+            o[e] = to_bf16(half == 0 ? __builtin_amdgcn_exp2f(fmaf(s, LOG2E, cp)) * ip
+                                     : __builtin_amdgcn_exp2f(fmaf(s, -LOG2E, cn)) * in);
           }
           *reinterpret_cast<bf16x4*>(stage + (lane & 31) * C::SP + 32 * ft + 8 * q4 + 4 * h) = o;
         }
@@ -494,13 +509,6 @@ __device__ __forceinline__ void store8v(T* __restrict__ p, const float (&x)[8]) 
     *reinterpret_cast<f32x4*>(p) = f32x4{x[0], x[1], x[2], x[3]};
     *reinterpret_cast<f32x4*>(p + 4) = f32x4{x[4], x[5], x[6], x[7]};
   }
-}
-
-// Two softmax statistics (running max m, sum s of e^{x - m}) of one row merged.
-__device__ __forceinline__ void merge_stats(float& m, float& s, float mo, float so) {
-  const float m2 = fmaxf(m, mo);
-  s = s * fexp(m - m2) + so * fexp(mo - m2);
-  m = m2;
 }
 
 // PART: f < 32 FT, so the last feature tile is partly padding and its
@@ -1201,10 +1209,16 @@ size_t prologue_bwd_workspace(int B, int L, int H, int Hkv, int hd, int f) {
 template <typename T, int FT, int HT>
 static hipError_t launch_fwd_t(const ProFwdArgs& a, int nq, int nk, hipStream_t st) {
   using C = Pro<T, FT, HT>;
-  hipError_t e = ensure_lds<prologue_fwd_kernel<T, FT, HT>>(C::FWD_LDS);
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((prologue_fwd_kernel<T, FT, HT>), dim3(nq + nk), dim3(256), C::FWD_LDS, st,
-                     a);
+  hipError_t e;
+  if (a.f == C::FP) {
+    if ((e = ensure_lds<prologue_fwd_kernel<T, FT, HT, false>>(C::FWD_LDS)) != hipSuccess) return e;
+    hipLaunchKernelGGL((prologue_fwd_kernel<T, FT, HT, false>), dim3(nq + nk), dim3(256),
+                       C::FWD_LDS, st, a);
+  } else {
+    if ((e = ensure_lds<prologue_fwd_kernel<T, FT, HT, true>>(C::FWD_LDS)) != hipSuccess) return e;
+    hipLaunchKernelGGL((prologue_fwd_kernel<T, FT, HT, true>), dim3(nq + nk), dim3(256),
+                       C::FWD_LDS, st, a);
+  }
   return hipGetLastError();
 }
 
