@@ -213,18 +213,17 @@ __device__ __forceinline__ void merge_stats(float& m, float& s, float mo, float 
 // Row statistics of the two softmaxes over the valid features (< f) in one
 // pass over the feature tiles: per tile its maxima, the running sums rescaled
 // to them (e^{x - m} as exp2 of one FMA), then the two lane halves' merged;
-// returns the maxima and the reciprocal sums.  PART: the last tile is partly
-// padding (f < 32 FT), masked; without it there are no masks.
+// returns the exp2 offsets of the two maps, -(m log2e + log2 sum): a feature's
+// softmax value is then exp2(x log2e + offset) (for the negated map, of -x).
+// PART: the last tile is partly padding (f < 32 FT), masked; without it there
+// are no masks.
 template <typename T, int FT, int HT, bool PART>
 __device__ __forceinline__ void softmax_stats(const bf16x8 (&xh)[Pro<T, FT, HT>::HK],
                                               const bf16x8 (&xl)[Pro<T, FT, HT>::HK],
                                               const bf16* w_hi, const bf16* w_lo, int f,
-                                              int lane, float& mp, float& mn, float& ip,
-                                              float& in) {
+                                              int lane, float& op, float& on) {
   const int h = lane >> 5;
-  mp = -1e30f;
-  mn = -1e30f;
-  float sp = 0.f, sn = 0.f;
+  float mp = -1e30f, mn = -1e30f, sp = 0.f, sn = 0.f;
 #pragma unroll
   for (int ft = 0; ft < FT; ++ft) {
     const f32x16 acc = project_tile<T, FT, HT>(ft, xh, xl, w_hi, w_lo, lane);
@@ -251,8 +250,8 @@ __device__ __forceinline__ void softmax_stats(const bf16x8 (&xh)[Pro<T, FT, HT>:
   }
   merge_stats(mp, sp, xhalf(mp), xhalf(sp));
   merge_stats(mn, sn, xhalf(mn), xhalf(sn));
-  ip = 1.f / sp;
-  in = 1.f / sn;
+  op = -(mp * LOG2E + __builtin_amdgcn_logf(sp));
+  on = -(mn * LOG2E + __builtin_amdgcn_logf(sn));
 }
 
 struct RowPos {
@@ -389,10 +388,8 @@ __global__ __launch_bounds__(256, 2) void prologue_fwd_kernel(ProFwdArgs a) {
     // fq == nullptr: q rows stop at RoPE (the GLA walk forms their feature
     // map itself, lz_gla_fwd_phi); fout is uniform per workgroup
     if (fout == nullptr) continue;
-    float mp, mn, ip, in;
-    softmax_stats<T, FT, HT, PART>(xh, xl, w_hi, w_lo, f, lane, mp, mn, ip, in);
-    // e^{x - m} / sum as exp2 of one FMA, times the reciprocal sum
-    const float cp = -mp * LOG2E, cn = -mn * LOG2E;
+    float cp, cn;
+    softmax_stats<T, FT, HT, PART>(xh, xl, w_hi, w_lo, f, lane, cp, cn);
 
     // the two halves of the feature row, staged through LDS for row-contiguous stores
     const int ob_lo = (int)(obase & 0xffffffff), ob_hi = (int)(obase >> 32);
@@ -407,8 +404,8 @@ __global__ __launch_bounds__(256, 2) void prologue_fwd_kernel(ProFwdArgs a) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const float s = acc[4 * q4 + e];
-            o[e] = to_bf16(half == 0 ? __builtin_amdgcn_exp2f(fmaf(s, LOG2E, cp)) * ip
-                                     : __builtin_amdgcn_exp2f(fmaf(s, -LOG2E, cn)) * in);
+            o[e] = to_bf16(half == 0 ? __builtin_amdgcn_exp2f(fmaf(s, LOG2E, cp))
+                                     : __builtin_amdgcn_exp2f(fmaf(s, -LOG2E, cn)));
           }
           *reinterpret_cast<bf16x4*>(stage + (lane & 31) * C::SP + 32 * ft + 8 * q4 + 4 * h) = o;
         }
@@ -740,12 +737,13 @@ prologue_bwd_kernel(ProBwdArgs a) {
         tn = fmaxf(tn, ok ? -acc[r] : -1e30f);
       }
       const float np = fmaxf(mp, tp), nn = fmaxf(mn, tn);
+      const float cp = -np * LOG2E, cn = -nn * LOG2E;   // e^{x - m} = exp2(x log2e - m log2e)
       float ap = 0.f, an = 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const bool ok = !PART || 32 * ft + acc_row(r, h) < f;
-        ap += fexp(ok ? acc[r] - np : NEG_INF);
-        an += fexp(ok ? -acc[r] - nn : NEG_INF);
+        ap += ok ? __builtin_amdgcn_exp2f(fmaf(acc[r], LOG2E, cp)) : 0.f;
+        an += ok ? __builtin_amdgcn_exp2f(fmaf(acc[r], -LOG2E, cn)) : 0.f;
       }
       sp = sp * fexp(mp - np) + ap;
       sn_ = sn_ * fexp(mn - nn) + an;
@@ -778,7 +776,10 @@ prologue_bwd_kernel(ProBwdArgs a) {
         mp = m0, sp = s0, mn = n0, sn_ = t0;
       }
     }
-    const float ip = 1.f / sp, in = 1.f / sn_;
+    // p = e^{x - mp} / sp = exp2(x log2e - (mp log2e + log2 sp)), n likewise:
+    // one FMA and the hardware exp2 per feature
+    const float lp = -(mp * LOG2E + __builtin_amdgcn_logf(sp));
+    const float ln_ = -(mn * LOG2E + __builtin_amdgcn_logf(sn_));
 
     // ---- 3. A = p dp - n dn per feature tile, <p, dp>, <n, dn> ---------------
     f32x16 A[FTW];
@@ -805,8 +806,8 @@ prologue_bwd_kernel(ProBwdArgs a) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int r = 4 * q4 + e;
-          const float pd = fexp(acc[r] - mp) * ip * dp[e];
-          const float nd = fexp(-acc[r] - mn) * in * dn[e];
+          const float pd = __builtin_amdgcn_exp2f(fmaf(acc[r], LOG2E, lp)) * dp[e];
+          const float nd = __builtin_amdgcn_exp2f(fmaf(acc[r], -LOG2E, ln_)) * dn[e];
           A[s][r] = pd - nd;
           s_p += pd;
           s_n += nd;
@@ -840,8 +841,8 @@ prologue_bwd_kernel(ProBwdArgs a) {
       const f32x16 acc = project_tile<T, FT, HT>(ft, xh, xl, w_hi, w_lo, lane);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float p = fexp(acc[r] - mp) * ip;
-        const float n = fexp(-acc[r] - mn) * in;
+        const float p = __builtin_amdgcn_exp2f(fmaf(acc[r], LOG2E, lp));
+        const float n = __builtin_amdgcn_exp2f(fmaf(acc[r], -LOG2E, ln_));
         A[s][r] = !PART || 32 * ft + acc_row(r, h) < f ? A[s][r] + n * s_n - p * s_p : 0.f;
       }
 #pragma unroll
