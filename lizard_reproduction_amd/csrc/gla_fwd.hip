@@ -506,11 +506,13 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void gla_fwd_wide_kernel(
     }
     mp = fmaxf(mp, xhalf(mp));
     mn = fmaxf(mn, xhalf(mn));
+    // e^{x - m} as exp2 of one FMA
+    const float cp = -mp * LOG2E, cn = -mn * LOG2E;
     float sp = 0.f, sn = 0.f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      sp += fexp(pacc[r] - mp);
-      sn += fexp(-pacc[r] - mn);
+      sp += __builtin_amdgcn_exp2f(fmaf(pacc[r], LOG2E, cp));
+      sn += __builtin_amdgcn_exp2f(fmaf(pacc[r], -LOG2E, cn));
     }
     sp += xhalf(sp);
     sn += xhalf(sn);
@@ -530,7 +532,9 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void gla_fwd_wide_kernel(
       Sp += g[j][1] * fexp(g[j][0] - Mp);
       Sn += g[j][3] * fexp(g[j][2] - Mn);
     }
-    const float ip = 1.f / Sp, in = 1.f / Sn;
+    // e^{x - M} / S = exp2(x log2e - (M log2e + log2 S)): one FMA and exp2
+    const float op_ = -(Mp * LOG2E + __builtin_amdgcn_logf(Sp));
+    const float on_ = -(Mn * LOG2E + __builtin_amdgcn_logf(Sn));
     const int tok = 32 * ptt + col;
     const bool live = t + tok < L;
     bf16* row = fq_l + tok * PF + 32 * pft;
@@ -540,8 +544,8 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void gla_fwd_wide_kernel(
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float x = pacc[4 * q4 + e];
-        op[e] = to_bf16(live ? fexp(x - Mp) * ip : 0.f);
-        on[e] = to_bf16(live ? fexp(-x - Mn) * in : 0.f);
+        op[e] = to_bf16(live ? __builtin_amdgcn_exp2f(fmaf(x, LOG2E, op_)) : 0.f);
+        on[e] = to_bf16(live ? __builtin_amdgcn_exp2f(fmaf(x, -LOG2E, on_)) : 0.f);
       }
       *reinterpret_cast<bf16x4*>(row + 8 * q4 + 4 * h) = op;
       *reinterpret_cast<bf16x4*>(row + 128 + 8 * q4 + 4 * h) = on;
