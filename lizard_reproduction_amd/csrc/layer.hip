@@ -571,6 +571,10 @@ prologue_bwd_kernel(ProBwdArgs a) {
   // One grid over the q blocks, then the kv blocks: workgroup w takes blocks
   // w, w + G, ... of that list, so it switches role at most once and every
   // workgroup gets its share of both (kv blocks carry the group's gradients).
+  // Workgroups of odd index take theirs in reverse order, kv blocks first: at
+  // any time about half the CUs then walk kv blocks (four heads' gradients
+  // each, bandwidth-heavy) while the others walk q blocks (round-trip bound),
+  // where in list order all walked the q blocks and then all the kv blocks.
   bool kv = false;
   int role = -1, heads_in = 0, group = 1, nrows = 0;
   const bf16 *dphi = nullptr, *drope = nullptr;
@@ -595,18 +599,23 @@ prologue_bwd_kernel(ProBwdArgs a) {
       dst[i] = load8r(xs + (long)min(r0 + r, nr - 1) * hd + m0);
     }
   };
+  const int G = gridDim.x, w = blockIdx.x;
+  const int nmine = w < nb ? (nb - w + G - 1) / G : 0;   // this workgroup's blocks
+  const bool rev = (w & 1) != 0;
+  auto block_of = [&](int kk) { return w + (rev ? nmine - 1 - kk : kk) * G; };
+  bool taken[2] = {false, false};   // roles whose partial has been written
   Raw8<T> xpre[K::XI];
-  if (K::PRE && (int)blockIdx.x < nb) x_items(blockIdx.x, xpre);
-  for (int j = blockIdx.x; j < nb; j += gridDim.x) {
+  if (K::PRE && nmine > 0) x_items(block_of(0), xpre);
+  for (int kk = 0; kk < nmine; ++kk) {
+    const int j = block_of(kk);
     if constexpr (!K::PRE) x_items(j, xpre);
     const int r_j = j < a.nbq ? 0 : 1;
     if (r_j != role) {   // uniform; the W tile's readers passed the last block's barriers
-      if (role == 0) {
-        flush(dw, 0, false);
+      if (role >= 0) {   // the role in hand is done: its partial
+        flush(dw, role, false);
+        taken[role] = true;
 #pragma unroll
         for (int i = 0; i < OWN; ++i) dw[i] = zero16();
-      } else {
-        flush(dw, 0, true);   // no q blocks here: a zero q partial
       }
       role = r_j;
       kv = role == 1;
@@ -902,7 +911,7 @@ prologue_bwd_kernel(ProBwdArgs a) {
       ec[i] = load8r(cs + tab + m0);
       es[i] = load8r(sn + tab + mp2);
     }
-    if (K::PRE && j + (int)gridDim.x < nb) x_items(j + gridDim.x, xpre);
+    if (K::PRE && kk + 1 < nmine) x_items(block_of(kk + 1), xpre);
 
     // ---- 5. dW += dxw^T x over the block: dxw hi, then lo --------------------
 #pragma unroll
@@ -1043,9 +1052,12 @@ prologue_bwd_kernel(ProBwdArgs a) {
     if constexpr (K::DX_OVER_X) __syncthreads();
   }
   // the role in hand (its partial), and zeros for a role never taken
-  if (role == 0) flush(dw, 0, false);
-  if (role < 0) flush(dw, 0, true);
-  flush(dw, 1, role != 1);
+  if (role >= 0) {
+    flush(dw, role, false);
+    taken[role] = true;
+  }
+  if (!taken[0]) flush(dw, 0, true);
+  if (!taken[1]) flush(dw, 1, true);
 }
 
 // dW[i][c] = sum over a role's workgroups of their partials.  A block takes 64
