@@ -32,7 +32,6 @@ namespace lz {
 constexpr int PRO_WAVES = 4;
 constexpr int PRO_ROWS = 32;                      // rows per wave and block
 constexpr int PRO_BLOCK = PRO_WAVES * PRO_ROWS;   // rows per workgroup iteration
-constexpr int PRO_FWD_WG_PER_ROLE = 1024;         // forward workgroups per role (q, kv)
 constexpr int PRO_BWD_WG_PER_CU = 2;              // the most any backward instantiation asks for
 constexpr int CMB_BLOCKS = 1024;                  // epilogue backward partial sums
 
@@ -1295,9 +1294,13 @@ hipError_t launch_prologue_fwd(const void* q, const void* k, const void* v, cons
                                const void* wk, const void* cos, const void* sin, void* fq,
                                void* fk, void* qr, void* kr, void* vo, bool bf16_in, int B, int L,
                                int H, int Hkv, int hd, int f, int cos_bstride, hipStream_t st) {
-  // one workgroup per 128-row block, up to PRO_FWD_WG_PER_ROLE per role (grid-stride beyond)
-  const int nq = (int)std::min<long>(ceil_div((long)B * L * H, PRO_BLOCK), PRO_FWD_WG_PER_ROLE);
-  const int nk = (int)std::min<long>(ceil_div((long)B * L * Hkv, PRO_BLOCK), PRO_FWD_WG_PER_ROLE);
+  // one workgroup per 128-row block, up to two per CU and role when the q rows
+  // write their feature maps and one without them (grid-stride beyond).
+  // Measured at config 5 against 1, 1.5, 2, 2.5, 4, 8 and 16 per CU and role:
+  // 155 us with fq at 2 (159 at 4, 164 at 1), 75 us without at 1 (80 at 2, 90 at 4).
+  const long per_role = (long)device_geom().cus * (fq != nullptr ? 2 : 1);
+  const int nq = (int)std::min<long>(ceil_div((long)B * L * H, PRO_BLOCK), per_role);
+  const int nk = (int)std::min<long>(ceil_div((long)B * L * Hkv, PRO_BLOCK), per_role);
   ProFwdArgs a{q, k, v, wq, wk, cos, sin,
                static_cast<bf16*>(fq), static_cast<bf16*>(fk), static_cast<bf16*>(qr),
                static_cast<bf16*>(kr), static_cast<bf16*>(vo),
