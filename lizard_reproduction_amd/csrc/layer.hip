@@ -476,13 +476,6 @@ struct ProBwd {
   static constexpr int IPR = 8 * NWF;                    // stage items per row
   static constexpr int GI = PRO_BLOCK * IPR / NT;        // stage items per thread
   static constexpr int RSTEP = NT / IPR;                 // rows between a thread's items
-  // heads whose gradient loads are issued a tile ahead: only where one wave
-  // per SIMD has the registers for them (the split and the two-workgroup
-  // forms have not: the loads' registers alone push them into spills, and
-  // their second wave per SIMD hides the load latency instead)
-  // (nor at FT = HT = 4, where a wave's own tiles already take every register)
-  static constexpr int GQ = OCC == 1 && NWF == 1 && FT * HT < 16 ? 4 : 0;
-  static constexpr int GQR = GQ > 0 ? GQ : 1;            // raw register sets held
   static constexpr int XI = PRO_BLOCK * (HP / 8) / NT;   // x / dx items per thread
   static_assert(GI * RSTEP * IPR == PRO_BLOCK * IPR && RSTEP == 32, "item mapping");
   static_assert(XI * NT == PRO_BLOCK * (HP / 8), "row items");
@@ -492,6 +485,14 @@ struct ProBwd {
   // workgroup per CU leaves the registers for them (bf16, head_dim <= 64);
   // elsewhere the held loads push the kernel into spills
   static constexpr bool PRE = OCC == 1 && HT <= 2 && !C::SPLIT;
+  // heads whose gradient loads are issued a tile ahead: four where one wave
+  // per SIMD has the registers for them, one in the split form with PRE (the
+  // q blocks' only head: 1 % at config 5), none elsewhere (the two-workgroup
+  // forms' second wave per SIMD hides the load latency instead, and held
+  // loads push them into spills; nor at FT = HT = 4, where a wave's own tiles
+  // already take every register)
+  static constexpr int GQ = OCC == 1 && NWF == 1 && FT * HT < 16 ? 4 : (PRE ? 1 : 0);
+  static constexpr int GQR = GQ > 0 ? GQ : 1;            // raw register sets held
 };
 
 template <typename T>
