@@ -158,6 +158,13 @@ hipError_t ensure_lds(int bytes) {
   return status[dev];
 }
 
+// A kernel instantiation as a type, for launch helpers that pick one of
+// several at run time and need it as a template argument (ensure_lds).
+template <auto Kern>
+struct KernTag {
+  static constexpr auto value = Kern;
+};
+
 // Row pitch (elements) of a row-major bf16 LDS tile with x columns.  Measured
 // bank-conflict cycles per instruction on gfx950 (64 banks; rocprofv3
 // SQ_LDS_BANK_CONFLICT over a probe of each access pattern):

@@ -167,13 +167,13 @@ __device__ __forceinline__ void z_update(float* zn, const float* zs, const float
 // formed from this tile's features but read from den_out / delta_out, where
 // the caller has put those of the whole feature dimension; the kernel then
 // writes this tile's share of every gradient.
-template <int FP, int DP, typename OutT, bool VEC, bool EXT>
+template <int FP, int DP, typename OutT, bool VEC, bool EXT, bool FOLD = false>
 __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
     const bf16* __restrict__ fq, const bf16* __restrict__ fk, const bf16* __restrict__ v,
     const float* __restrict__ log_gamma, const bf16* __restrict__ dy, OutT* __restrict__ dfq,
     float* __restrict__ den_out, float* __restrict__ delta_out, float* __restrict__ p_out,
     const float* __restrict__ seg_state, int H, int L, int F, int D, int gate, int G,
-    int cps, int M, int KG, int xper, int nxcd, int nblk) {
+    int cps, int M, int KG, int xper, int nxcd, int nblk, const float* __restrict__ seg_lam) {
   using Cfg = BwdA<FP, DP>;
   constexpr int C = Cfg::C, PF = Cfg::PF, PD = Cfg::PD;
   constexpr int NFT = Cfg::NFT, NDT = Cfg::NDT;
@@ -218,8 +218,12 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
   // fk and v of the kv head of this query head (KG query heads share one)
   const size_t offFk = (size_t)(bh / KG) * L * F, offDv = (size_t)(bh / KG) * L * D;
   const float* lgb = log_gamma + (size_t)((gate & GATE_PER_HEAD) ? bh : bh / H) * L;
+  // the forward state entering segment seg: its scanned record, or (FOLD) the
+  // local records of segments 0 .. seg - 1 folded here (their total log
+  // decays at seg_lam)
+  const int own = seg_owner_uniform(bh, KG, gate);
   const float* st =
-      G > 1 ? seg_state + ((size_t)seg_owner_uniform(bh, KG, gate) * G + seg) * Cfg::SEG : nullptr;
+      G > 1 ? seg_state + ((size_t)own * G + (FOLD ? 0 : seg)) * Cfg::SEG : nullptr;
 
   // owned S^T tiles (rows d, columns f): i -> (f-tile, d-tile)
   auto s_tile = [&](int i, int& ft, int& dt) __attribute__((always_inline)) -> bool {
@@ -250,17 +254,39 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
     }
   };
   f32x16 St[Cfg::S_OWN];
+  if constexpr (FOLD) {   // folded in LDS, before the first chunk is staged there
+    static_assert(Cfg::SEG * 4 <= Cfg::BYTES, "a folded record fits the chunk's LDS");
+    float* fold_l = reinterpret_cast<float*>(smem);
+    if (seg > 0)
+      fold_records<B_THREADS, Cfg::SEG, 160>(fold_l, st, seg_lam + (size_t)own * G, 0, 1, seg);
+    __syncthreads();
 #pragma unroll
-  for (int i = 0; i < Cfg::S_OWN; ++i) {
-    St[i] = zero16();
-    int ft, dt;
-    if (s_tile(i, ft, dt) && st) {
-      const int f = ft * 32 + col;
+    for (int i = 0; i < Cfg::S_OWN; ++i) {
+      St[i] = zero16();
+      int ft, dt;
+      if (s_tile(i, ft, dt) && seg > 0) {
+        const int f = ft * 32 + col;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) St[i][r] = st[f * DP + dt * 32 + acc_row(r, h)];
+        for (int r = 0; r < 16; ++r) St[i][r] = fold_l[f * DP + dt * 32 + acc_row(r, h)];
+      }
     }
+    static_assert(FP <= B_THREADS, "one z element per thread");
+    const float zv = seg > 0 && tid < FP ? fold_l[FP * DP + tid] : 0.f;
+    __syncthreads();   // read before the LDS is reused
+    if (tid < FP) zb[FP * (n0 & 1) + tid] = zv;
+  } else {
+#pragma unroll
+    for (int i = 0; i < Cfg::S_OWN; ++i) {
+      St[i] = zero16();
+      int ft, dt;
+      if (s_tile(i, ft, dt) && st) {
+        const int f = ft * 32 + col;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) St[i][r] = st[f * DP + dt * 32 + acc_row(r, h)];
+      }
+    }
+    for (int f = tid; f < FP; f += B_THREADS) zb[FP * (n0 & 1) + f] = st ? st[FP * DP + f] : 0.f;
   }
-  for (int f = tid; f < FP; f += B_THREADS) zb[FP * (n0 & 1) + f] = st ? st[FP * DP + f] : 0.f;
   // bf16 S [f][d] for the X jobs (4 consecutive d per store)
   auto publish = [&]() __attribute__((always_inline)) {
     if constexpr (!SREG) {
@@ -772,7 +798,7 @@ struct BwdB : BwdCommon<FP, DP> {
   static_assert(BYTES <= 160 * 1024, "LDS budget");
 };
 
-template <int FP, int DP, typename OutT, bool VEC>
+template <int FP, int DP, typename OutT, bool VEC, bool FOLD = false>
 __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_kernel(
     const bf16* __restrict__ fq, const bf16* __restrict__ fk, const bf16* __restrict__ v,
     const float* __restrict__ log_gamma, const bf16* __restrict__ dy,
@@ -781,7 +807,7 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
     float* __restrict__ dG, float* __restrict__ csum, float* __restrict__ dlg_direct,
     const float* __restrict__ seg_state, int H,
     int L, int F, int D, int gate, int G, int cps, int M, int KG, int xper, int nxcd,
-    int nblk) {
+    int nblk, const float* __restrict__ seg_lam) {
   using Cfg = BwdB<FP, DP>;
   constexpr int C = Cfg::C, PF = Cfg::PF, PD = Cfg::PD;
   constexpr int NFT = Cfg::NFT, NDT = Cfg::NDT, ZP = Cfg::ZP;
@@ -822,22 +848,52 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
   // fk and v of the kv head of this query head (KG query heads share one)
   const size_t offFk = (size_t)(bh / KG) * L * F, offDv = (size_t)(bh / KG) * L * D;
   const float* lgb = log_gamma + (size_t)((gate & GATE_PER_HEAD) ? bh : bh / H) * L;
-  const float* st = G > 1 ? seg_state + ((size_t)bh * G + seg) * Cfg::SEG : nullptr;
+  // the gradient state entering segment seg from the right: its scanned
+  // record, or (FOLD) the local records of segments G - 1 .. seg + 1 folded
+  // here (their total log decays at seg_lam)
+  const float* st =
+      G > 1 ? seg_state + ((size_t)bh * G + (FOLD ? 0 : seg)) * Cfg::SEG : nullptr;
 
   // this wave's dS tiles t = wave + 8 i: f-tile t % NFT, d-tile t / NFT
   // (lane = d column, registers = f rows)
   f32x16 dS[Cfg::S_OWN];
+  if constexpr (FOLD) {   // folded in LDS, before the first chunk is staged there
+    static_assert(Cfg::SEG * 4 <= Cfg::BYTES, "a folded record fits the chunk's LDS");
+    float* fold_l = reinterpret_cast<float*>(smem);
+    const bool any = seg < G - 1;
+    if (any)
+      fold_records<B_THREADS, Cfg::SEG, 160>(fold_l, st, seg_lam + (size_t)bh * G, G - 1, -1,
+                                             G - 1 - seg);
+    __syncthreads();
 #pragma unroll
-  for (int i = 0; i < Cfg::S_OWN; ++i) {
-    dS[i] = zero16();
-    const int t = wave + B_WAVES * i;
-    if (st && t < NFT * NDT) {
-      const int ft = t % NFT, dt = t / NFT;
+    for (int i = 0; i < Cfg::S_OWN; ++i) {
+      dS[i] = zero16();
+      const int t = wave + B_WAVES * i;
+      if (any && t < NFT * NDT) {
+        const int ft = t % NFT, dt = t / NFT;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) dS[i][r] = st[(ft * 32 + acc_row(r, h)) * DP + dt * 32 + col];
+        for (int r = 0; r < 16; ++r)
+          dS[i][r] = fold_l[(ft * 32 + acc_row(r, h)) * DP + dt * 32 + col];
+      }
     }
+    static_assert(FP <= B_THREADS, "one dz element per thread");
+    const float zv = any && tid < FP ? fold_l[FP * DP + tid] : 0.f;
+    __syncthreads();   // read before the LDS is reused
+    if (tid < FP) dzs[tid] = zv;
+  } else {
+#pragma unroll
+    for (int i = 0; i < Cfg::S_OWN; ++i) {
+      dS[i] = zero16();
+      const int t = wave + B_WAVES * i;
+      if (st && t < NFT * NDT) {
+        const int ft = t % NFT, dt = t / NFT;
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          dS[i][r] = st[(ft * 32 + acc_row(r, h)) * DP + dt * 32 + col];
+      }
+    }
+    for (int f = tid; f < FP; f += B_THREADS) dzs[f] = st ? st[FP * DP + f] : 0.f;
   }
-  for (int f = tid; f < FP; f += B_THREADS) dzs[f] = st ? st[FP * DP + f] : 0.f;
 
   // publish the owned dS tiles as bf16 dS^T [d][f] (4 consecutive f per store)
   auto publish = [&]() {
@@ -1201,53 +1257,67 @@ static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v
   float* rseg = own_fseg + segf;
   float* csum = rseg + segf;
   const float* fseg = fwd_ws ? fwd_ws : own_fseg;   // the forward's records, when kept
+  // the walks fold the segment records themselves (the state passes, here
+  // and in the forward that kept them, leave them unscanned), or read the
+  // scanned ones
+  constexpr bool CAN_FOLD = gla_can_fold<FP, DP, VEC>();
+  const bool fold = CAN_FOLD && !ext && gla_fold_segments(G);
   hipError_t e;
   if (G > 1 && !fwd_ws) {
     e = launch_gla_fwd_states(fk, v, lg, own_fseg, own_fseg + (size_t)BH * G * SEG, BH, H, L, F,
-                              D, gate, G, cps, KG, st);
+                              D, gate, G, cps, KG, fold, st);
     if (e != hipSuccess) return e;
   }
   // the walks take two segments per workgroup while that still gives one
   // workgroup per CU: fewer, longer walks
   const int M = (G % 2 == 0 && BH * G / 2 >= device_geom().cus) ? 2 : 1;
   const WalkGrid wg = walk_grid(BH * G / M, KG);
-  auto launch_a = [&](auto kern) {
+  const float* flam = fseg + (size_t)BH * G * SEG;
+  auto launch_a = [&](auto tag) {
+    constexpr auto kern = decltype(tag)::value;
+    if (hipError_t e2 = ensure_lds<kern>(LDS_A); e2 != hipSuccess) return e2;
     hipLaunchKernelGGL(kern, dim3(wg.grid), dim3(B_THREADS), LDS_A, st, (const bf16*)fq,
                        (const bf16*)fk, (const bf16*)v, lg, (const bf16*)dy, (OutT*)dfq, den,
                        delta, p, fseg, H, L, F, D, gate, G, cps, M, KG, wg.per, wg.nx,
-                       wg.nblk);
+                       wg.nblk, flam);
+    return hipGetLastError();
   };
-  if (ext) {
-    if ((e = ensure_lds<gla_bwd_dq_kernel<FP, DP, OutT, VEC, true>>(LDS_A)) != hipSuccess)
-      return e;
-    launch_a(gla_bwd_dq_kernel<FP, DP, OutT, VEC, true>);
-  } else {
-    if ((e = ensure_lds<gla_bwd_dq_kernel<FP, DP, OutT, VEC, false>>(LDS_A)) != hipSuccess)
-      return e;
-    launch_a(gla_bwd_dq_kernel<FP, DP, OutT, VEC, false>);
-  }
-  if ((e = hipGetLastError()) != hipSuccess) return e;
+  if (ext)
+    e = launch_a(KernTag<gla_bwd_dq_kernel<FP, DP, OutT, VEC, true>>{});
+  else if (CAN_FOLD && fold)
+    e = launch_a(KernTag<gla_bwd_dq_kernel<FP, DP, OutT, VEC, false, CAN_FOLD>>{});
+  else
+    e = launch_a(KernTag<gla_bwd_dq_kernel<FP, DP, OutT, VEC, false>>{});
+  if (e != hipSuccess) return e;
+  float* rlam = rseg + (size_t)BH * G * SEG;
   if (G > 1) {
     auto ks = gla_bwd_state_kernel<FP, DP, VEC>;
     if ((e = ensure_lds<gla_bwd_state_kernel<FP, DP, VEC>>(LDS_S)) != hipSuccess) return e;
-    float* rlam = rseg + (size_t)BH * G * SEG;
     hipLaunchKernelGGL(ks, dim3(BH * (G - 1)), dim3(256), LDS_S, st,
                        (const bf16*)fq, (const bf16*)dy, lg, (const float*)den,
                        (const float*)delta, rseg, rlam, H, L, F, D, gate, G, cps);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    if ((e = launch_gla_segment_scan(rseg, rlam, BH, G, SEG, true, st)) != hipSuccess) return e;
+    if (!fold && (e = launch_gla_segment_scan(rseg, rlam, BH, G, SEG, true, st)) != hipSuccess)
+      return e;
   }
   // a per-head gate in one segment: the reverse walk of (b, h) sees its whole
   // gate row and writes d log_gamma itself (no gate launch, no dG)
   const bool direct_dlg = (gate & GATE_PER_HEAD) && G == 1;
-  auto kb = gla_bwd_dkv_kernel<FP, DP, OutT, VEC>;
-  if ((e = ensure_lds<gla_bwd_dkv_kernel<FP, DP, OutT, VEC>>(LDS_B)) != hipSuccess) return e;
-  hipLaunchKernelGGL(kb, dim3(wg.grid), dim3(B_THREADS), LDS_B, st, (const bf16*)fq,
-                     (const bf16*)fk, (const bf16*)v, lg, (const bf16*)dy, (const float*)den,
-                     (const float*)delta, (const float*)p, (OutT*)dfk, (OutT*)dv, dG, csum,
-                     direct_dlg ? dlg : nullptr, (const float*)rseg, H, L, F, D, gate, G,
-                     cps, M, KG, wg.per, wg.nx, wg.nblk);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
+  auto launch_b = [&](auto tag) {
+    constexpr auto kern = decltype(tag)::value;
+    if (hipError_t e2 = ensure_lds<kern>(LDS_B); e2 != hipSuccess) return e2;
+    hipLaunchKernelGGL(kern, dim3(wg.grid), dim3(B_THREADS), LDS_B, st, (const bf16*)fq,
+                       (const bf16*)fk, (const bf16*)v, lg, (const bf16*)dy, (const float*)den,
+                       (const float*)delta, (const float*)p, (OutT*)dfk, (OutT*)dv, dG, csum,
+                       direct_dlg ? dlg : nullptr, (const float*)rseg, H, L, F, D, gate, G,
+                       cps, M, KG, wg.per, wg.nx, wg.nblk, (const float*)rlam);
+    return hipGetLastError();
+  };
+  if (CAN_FOLD && fold)
+    e = launch_b(KernTag<gla_bwd_dkv_kernel<FP, DP, OutT, VEC, CAN_FOLD>>{});
+  else
+    e = launch_b(KernTag<gla_bwd_dkv_kernel<FP, DP, OutT, VEC>>{});
+  if (e != hipSuccess) return e;
   if (direct_dlg) return hipSuccess;
   const int nt = (L + GLA_C - 1) / GLA_C;
   const dim3 ggrid((nt + GATE_CHUNKS_PER_WG - 1) / GATE_CHUNKS_PER_WG,

@@ -367,11 +367,85 @@ struct SegRec {
   static constexpr int SIZE = FP * DP + FP;
 };
 
+// Records one pass of fold_records loads together: VREGS / 4 16-byte loads
+// in flight per thread, at least one record and at most 8.
+__host__ __device__ constexpr int fold_batch(int T, int REC, int VREGS) {
+  return (VREGS / 4 / ((REC / 4 + T - 1) / T)) < 1 ? 1
+         : (VREGS / 4 / ((REC / 4 + T - 1) / T)) > 8 ? 8
+                                                      : VREGS / 4 / ((REC / 4 + T - 1) / T);
+}
+
+// The state entering a segment, formed inside a walk from the local records
+// of the segments on its left (forward: records first, first + 1, ...) or on
+// its right (reverse: first, first - 1, ...), n records, in the order and with
+// the arithmetic of gla_segment_scan_kernel: carry = e^{lam_g} carry + R_g,
+// one fused multiply-add per element.  So the state has the bits the scan
+// would have written.  The T threads of the workgroup fold the REC floats of a
+// record as 16-byte groups and write the result to out (LDS, 16-byte aligned),
+// with VREGS registers of loads in flight per thread (the walk's own registers
+// bound it: its chunk loads are in flight meanwhile).
+template <int T, int REC, int VREGS>
+__device__ __forceinline__ void fold_records(float* __restrict__ out,
+                                             const float* __restrict__ base,
+                                             const float* __restrict__ lam, int first, int step,
+                                             int n) {
+  static_assert(REC % 4 == 0, "records are whole 16-byte groups");
+  constexpr int N4 = REC / 4, NG = (N4 + T - 1) / T, FB = fold_batch(T, REC, VREGS);
+  const int tid = threadIdx.x;
+  f32x4 carry[NG];
+#pragma unroll
+  for (int k = 0; k < NG; ++k) carry[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int g0 = 0; g0 < n; g0 += FB) {
+    f32x4 d[FB][NG];
+#pragma unroll
+    for (int b = 0; b < FB; ++b) {
+      const bool ok = g0 + b < n;   // wave-uniform
+      const float* rec = base + (size_t)(first + step * (g0 + b)) * REC;
+#pragma unroll
+      for (int k = 0; k < NG; ++k) {
+        const int i = tid + T * k;
+        d[b][k] = ok && (N4 % T == 0 || i < N4) ? *reinterpret_cast<const f32x4*>(rec + 4 * i)
+                                                : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < FB; ++b) {
+      if (g0 + b < n) {
+        const float w = fexp(lam[first + step * (g0 + b)]);
+#pragma unroll
+        for (int k = 0; k < NG; ++k)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) carry[k][c] = __builtin_fmaf(w, carry[k][c], d[b][k][c]);
+      }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < NG; ++k) {
+    const int i = tid + T * k;
+    if (N4 % T == 0 || i < N4) *reinterpret_cast<f32x4*>(out + 4 * i) = carry[k];
+  }
+}
+
+// Whether the walks fold the segment records themselves (no scan launch):
+// for at most 4 segments per row, in the walks that have a folding variant
+// (whole 16-byte rows, records of at least 128 x 64 floats).  Measured: with
+// 4 segments (F = D = 128, B = 4, L = 2048) and 3 (F = 256, D = 64, the
+// config-5 layer) the fold took 6-11 us off a fwd+bwd; with 16 (F = D = 64,
+// B = 1, L = 2048) its passes over 15 records of each walk cost more than
+// the scan launch.  The state passes leave the records unscanned exactly
+// when the walks that read them fold.
+template <int FP, int DP, bool VEC>
+constexpr bool gla_can_fold() {
+  return VEC && FP * DP >= 128 * 64;
+}
+inline bool gla_fold_segments(int G) { return G > 1 && G <= 4; }
+
 // Segment pass of the forward recurrence (gla_fwd.hip) and the scan over
 // segments; used by the forward and by the backward's forward walk.
+// fold: the walks fold the records (no scan).
 hipError_t launch_gla_fwd_states(const void* fk, const void* v, const float* lg, float* seg_state,
                                  float* seg_logdecay, int BH, int H, int L, int F, int D,
-                                 int gate, int G, int cps, int KG, hipStream_t st);
+                                 int gate, int G, int cps, int KG, bool fold, hipStream_t st);
 hipError_t launch_gla_segment_scan(float* seg_state, const float* seg_logdecay, int BH, int G,
                                    int rec, bool reverse, hipStream_t st);
 

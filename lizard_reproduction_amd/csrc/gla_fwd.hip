@@ -79,13 +79,13 @@ struct GlaFwd {
 // RAW (one F tile of a split feature dimension): instead of y, the walk writes
 // the unnormalised numerator o (fp32 [BH, L, D] at raw_num) and denominator
 // (fp32 [BH, L] at raw_den), which the caller sums over the F tiles.
-template <int FP, int DP, bool VEC, bool RAW>
+template <int FP, int DP, bool VEC, bool RAW, bool FOLD = false>
 __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
     const bf16* __restrict__ fq, const bf16* __restrict__ fk, const bf16* __restrict__ v,
     const float* __restrict__ log_gamma, bf16* __restrict__ y,
     const float* __restrict__ seg_state, float* __restrict__ final_state, int H, int L, int F,
     int D, int gate, int G, int cps, int M, int KG, float* __restrict__ raw_num,
-    float* __restrict__ raw_den, int xper, int nxcd, int nblk) {
+    float* __restrict__ raw_den, int xper, int nxcd, int nblk, const float* __restrict__ seg_lam) {
   using Cfg = GlaFwd<FP, DP>;
   constexpr int C = Cfg::C, PF = Cfg::PF, PD = Cfg::PD;
   constexpr int NFT = Cfg::NFT, NDT = Cfg::NDT;
@@ -122,26 +122,53 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
   const bf16* vb = v + (size_t)(bh / KG) * L * D;
   const rsrc_t yr = make_rsrc(y + (size_t)bh * L * D, (size_t)L * D * 2);
   const float* lgb = log_gamma + (size_t)((gate & GATE_PER_HEAD) ? bh : bh / H) * L;
+  // the state entering segment seg: its scanned record, or (FOLD) the local
+  // records of segments 0 .. seg - 1 folded here (their total log decays at
+  // seg_lam)
+  const int own = seg_owner_uniform(bh, KG, gate);
   const float* st =
-      G > 1 ? seg_state + ((size_t)seg_owner_uniform(bh, KG, gate) * G + seg) * Cfg::SEG : nullptr;
+      G > 1 ? seg_state + ((size_t)own * G + (FOLD ? 0 : seg)) * Cfg::SEG : nullptr;
 
   const bool active = RD::active(wave);
   auto dtile = [&](int i) { return RD::tile(wave, i); };
   auto qtile = [&](int j) { return RD::half(wave, j); };
 
   f32x16 S[NDW][NFT];
+  if constexpr (FOLD) {   // folded in LDS, before the first chunk is staged there
+    static_assert(Cfg::SEG * 4 <= Cfg::BYTES, "a folded record fits the chunk's LDS");
+    float* fold_l = reinterpret_cast<float*>(smem);
+    if (seg > 0)
+      fold_records<256, Cfg::SEG, 64>(fold_l, st, seg_lam + (size_t)own * G, 0, 1, seg);
+    __syncthreads();
 #pragma unroll
-  for (int i = 0; i < NDW; ++i)
+    for (int i = 0; i < NDW; ++i)
 #pragma unroll
-    for (int ft = 0; ft < NFT; ++ft) {
-      S[i][ft] = zero16();
-      if (st && active) {
+      for (int ft = 0; ft < NFT; ++ft) {
+        S[i][ft] = zero16();
+        if (seg > 0 && active) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          S[i][ft][r] = st[(ft * 32 + acc_row(r, h)) * DP + dtile(i) * 32 + col];
+          for (int r = 0; r < 16; ++r)
+            S[i][ft][r] = fold_l[(ft * 32 + acc_row(r, h)) * DP + dtile(i) * 32 + col];
+        }
       }
-    }
-  for (int f = tid; f < FP; f += 256) zs[f] = st ? st[FP * DP + f] : 0.f;
+    static_assert(FP <= 256, "one z element per thread");
+    const float zv = seg > 0 && tid < FP ? fold_l[FP * DP + tid] : 0.f;
+    __syncthreads();   // read before the LDS is reused
+    if (tid < FP) zs[tid] = zv;
+  } else {
+#pragma unroll
+    for (int i = 0; i < NDW; ++i)
+#pragma unroll
+      for (int ft = 0; ft < NFT; ++ft) {
+        S[i][ft] = zero16();
+        if (st && active) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            S[i][ft][r] = st[(ft * 32 + acc_row(r, h)) * DP + dtile(i) * 32 + col];
+        }
+      }
+    for (int f = tid; f < FP; f += 256) zs[f] = st ? st[FP * DP + f] : 0.f;
+  }
 
   uint4 rq[Cfg::NLF], rk[Cfg::NLF], rv[Cfg::NLD];
   float rg;
@@ -393,14 +420,14 @@ __device__ __forceinline__ void store_chunk512(const uint4 (&reg)[N], bf16* tile
 // 32-token tile w & 1; the statistics of a token's four tiles meet in LDS
 // (written in phase 2, read in the tail, where the chunk is staged: no barrier
 // of its own), combined as max M and sum of s_j e^{m_j - M}.
-template <int DP, bool VEC, bool RAW, bool PHI>
+template <int DP, bool VEC, bool RAW, bool PHI, bool FOLD = false>
 __global__ __launch_bounds__(WIDE_THREADS, 1) void gla_fwd_wide_kernel(
     const bf16* __restrict__ fq, const bf16* __restrict__ fk, const bf16* __restrict__ v,
     const float* __restrict__ log_gamma, bf16* __restrict__ y,
     const float* __restrict__ seg_state, float* __restrict__ final_state, int H, int L, int F,
     int D, int gate, int G, int cps, int M, int KG, float* __restrict__ raw_num,
     float* __restrict__ raw_den, int xper, int nxcd, int nblk, const bf16* __restrict__ qrow,
-    const bf16* __restrict__ wphi) {
+    const bf16* __restrict__ wphi, const float* __restrict__ seg_lam) {
   static_assert(!(PHI && RAW), "the feature map is formed for whole-F walks only");
   using Cfg = GlaFwdWide<DP>;
   constexpr int FP = Cfg::FP, C = Cfg::C, PF = Cfg::PF, PD = Cfg::PD;
@@ -434,22 +461,47 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void gla_fwd_wide_kernel(
   const bf16* vb = v + (size_t)(bh / KG) * L * D;
   const rsrc_t yr = make_rsrc(y + (size_t)bh * L * D, (size_t)L * D * 2);
   const float* lgb = log_gamma + (size_t)((gate & GATE_PER_HEAD) ? bh : bh / H) * L;
-  const float* st = G > 1 ? seg_state + ((size_t)seg_owner_uniform(bh, KG, gate) * G + seg) *
-                                            SegRec<FP, DP>::SIZE
-                          : nullptr;
+  // the state entering segment seg: its scanned record, or (FOLD) the local
+  // records of segments 0 .. seg - 1 folded here (their total log decays at
+  // seg_lam)
+  constexpr int SEG = SegRec<FP, DP>::SIZE;
+  const int own = seg_owner_uniform(bh, KG, gate);
+  const float* st = G > 1 ? seg_state + ((size_t)own * G + (FOLD ? 0 : seg)) * SEG : nullptr;
 
   // state tile i of this wave: t = wave + 8 i -> f-tile t % NFT, d-tile t / NFT
   f32x16 S[S_OWN];
+  if constexpr (FOLD) {   // folded in LDS, before the first chunk is staged there
+    static_assert(SEG * 4 <= Cfg::BYTES, "a folded record fits the chunk's LDS");
+    float* fold_l = reinterpret_cast<float*>(smem);
+    if (seg > 0)
+      fold_records<WIDE_THREADS, SEG, 160>(fold_l, st, seg_lam + (size_t)own * G, 0, 1, seg);
+    __syncthreads();
 #pragma unroll
-  for (int i = 0; i < S_OWN; ++i) {
-    S[i] = zero16();
-    const int t = wave + 8 * i, ft = t % NFT, dt = t / NFT;
-    if (st && t < NFT * NDT) {
+    for (int i = 0; i < S_OWN; ++i) {
+      S[i] = zero16();
+      const int t = wave + 8 * i, ft = t % NFT, dt = t / NFT;
+      if (seg > 0 && t < NFT * NDT) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) S[i][r] = st[(ft * 32 + acc_row(r, h)) * DP + dt * 32 + col];
+        for (int r = 0; r < 16; ++r)
+          S[i][r] = fold_l[(ft * 32 + acc_row(r, h)) * DP + dt * 32 + col];
+      }
     }
+    static_assert(FP <= WIDE_THREADS, "one z element per thread");
+    const float zv = seg > 0 && tid < FP ? fold_l[FP * DP + tid] : 0.f;
+    __syncthreads();   // read before the LDS is reused
+    if (tid < FP) zs[tid] = zv;
+  } else {
+#pragma unroll
+    for (int i = 0; i < S_OWN; ++i) {
+      S[i] = zero16();
+      const int t = wave + 8 * i, ft = t % NFT, dt = t / NFT;
+      if (st && t < NFT * NDT) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) S[i][r] = st[(ft * 32 + acc_row(r, h)) * DP + dt * 32 + col];
+      }
+    }
+    for (int f = tid; f < FP; f += WIDE_THREADS) zs[f] = st ? st[FP * DP + f] : 0.f;
   }
-  for (int f = tid; f < FP; f += WIDE_THREADS) zs[f] = st ? st[FP * DP + f] : 0.f;
   // bf16 S^T [d][f] (4 consecutive f per store), read by the output products
   auto publish = [&]() __attribute__((always_inline)) {
 #pragma unroll
@@ -479,11 +531,6 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void gla_fwd_wide_kernel(
   const rsrc_t qrs = make_rsrc(
       PHI ? qrow + ((size_t)(bh / H) * L * H + (size_t)(bh % H)) * PHD : nullptr,
       PHI ? ((size_t)(L - 1) * H + 1) * PHD * 2 : 0);
-  if constexpr (PHI) {
-    for (int i = tid; i < 128 * PHD / 8; i += WIDE_THREADS)
-      *reinterpret_cast<uint4*>(w_l + (i / (PHD / 8)) * Cfg::PW + 8 * (i % (PHD / 8))) =
-          reinterpret_cast<const uint4*>(wphi)[i];
-  }
   auto phi_load = [&](int t) __attribute__((always_inline)) {   // chunk starting at t
     const int row = t + 32 * ptt + col;
 #pragma unroll
@@ -561,6 +608,12 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void gla_fwd_wide_kernel(
   load_chunk512<FP>(rk, fkb, n0 * C, L, F, vecF);
   load_chunk512<DP>(rv, vb, n0 * C, L, D, vecD);
   rg = gate_at(lgb, n0 * C + lane, L);
+
+  if constexpr (PHI) {
+    for (int i = tid; i < 128 * PHD / 8; i += WIDE_THREADS)
+      *reinterpret_cast<uint4*>(w_l + (i / (PHD / 8)) * Cfg::PW + 8 * (i % (PHD / 8))) =
+          reinterpret_cast<const uint4*>(wphi)[i];
+  }
   if constexpr (!PHI) store_chunk512<FP>(rq, fq_l, PF);
   store_chunk512<FP>(rk, fk_l, PF);
   store_chunk512<DP>(rv, v_l, PD);
@@ -1140,7 +1193,7 @@ __global__ __launch_bounds__(256) void gla_segment_scan_kernel(float* __restrict
       if (b0 + k < G - 1) {
         const int g = reverse ? G - 1 - (b0 + k) : b0 + k;
         base[(size_t)g * rec] = carry;
-        carry = w[k] * carry + d[k];
+        carry = __builtin_fmaf(w[k], carry, d[k]);   // as fold_records
       }
     }
   }
@@ -1236,7 +1289,7 @@ template <int FP, int DP, bool VEC>
 static hipError_t launch_gla_fwd_states_t(const void* fk, const void* v, const float* lg,
                                           float* seg_state, float* seg_logdecay, int BH, int H,
                                           int L, int F, int D, int gate, int G, int cps,
-                                          int KG, hipStream_t st) {
+                                          int KG, bool fold, hipStream_t st) {
   if (!(gate & GATE_PER_HEAD) && KG > 1) {   // one record per kv head (seg_owner)
     BH /= KG;
     H /= KG;
@@ -1266,23 +1319,24 @@ static hipError_t launch_gla_fwd_states_t(const void* fk, const void* v, const f
                                              gate, G, cps, KG, st);
   }
   if (e != hipSuccess) return e;
+  if (fold) return hipSuccess;   // the walks fold the records
   return launch_gla_segment_scan(seg_state, seg_logdecay, BH, G, SegRec<FP, DP>::SIZE, false,
                                  st);
 }
 
 hipError_t launch_gla_fwd_states(const void* fk, const void* v, const float* lg, float* seg_state,
                                  float* seg_logdecay, int BH, int H, int L, int F, int D,
-                                 int gate, int G, int cps, int KG, hipStream_t st) {
+                                 int gate, int G, int cps, int KG, bool fold, hipStream_t st) {
   const int fp = gla_padded_dim(F), dp = gla_padded_dim(D);
   const bool vec = F % 8 == 0 && D % 8 == 0;
 #define LZ_GLA_ST(FPV, DPV)                                                                   \
   if (fp == FPV && dp == DPV)                                                                 \
     return vec ? launch_gla_fwd_states_t<FPV, DPV, true>(fk, v, lg, seg_state, seg_logdecay,  \
                                                          BH, H, L, F, D, gate, G,    \
-                                                         cps, KG, st)                         \
+                                                         cps, KG, fold, st)                   \
                : launch_gla_fwd_states_t<FPV, DPV, false>(fk, v, lg, seg_state, seg_logdecay, \
                                                           BH, H, L, F, D, gate, G,   \
-                                                          cps, KG, st);
+                                                          cps, KG, fold, st);
   LZ_GLA_ST(32, 32) LZ_GLA_ST(32, 64) LZ_GLA_ST(32, 128)
   LZ_GLA_ST(64, 32) LZ_GLA_ST(64, 64) LZ_GLA_ST(64, 128)
   LZ_GLA_ST(128, 32) LZ_GLA_ST(128, 64) LZ_GLA_ST(128, 128)
@@ -1300,35 +1354,48 @@ static hipError_t launch_gla_fwd_t(const void* fq, const void* fk, const void* v
   const int BH = B * H;
   int G, cps;
   gla_segments(BH, L, F, &G, &cps);
+  constexpr bool CAN_FOLD = gla_can_fold<FP, DP, VEC>() && !RAW;
+  const bool fold = CAN_FOLD && gla_fold_segments(G);
   float* seg_state = ws;
+  float* seg_lam = ws + (size_t)BH * G * Cfg::SEG;
   if (G > 1) {
-    hipError_t e = launch_gla_fwd_states_t<FP, DP, VEC>(fk, v, lg, seg_state,
-                                                   ws + (size_t)BH * G * Cfg::SEG, BH, H, L, F,
-                                                   D, gate, G, cps, KG, st);
+    hipError_t e = launch_gla_fwd_states_t<FP, DP, VEC>(fk, v, lg, seg_state, seg_lam, BH, H, L,
+                                                        F, D, gate, G, cps, KG, fold, st);
     if (e != hipSuccess) return e;
   }
   const int M = gla_walk_segments(BH, G, F);
   const WalkGrid wg = walk_grid(BH * G / M, KG);
   if constexpr (FP == 256) {   // eight waves per workgroup
     using W = GlaFwdWide<DP>;
-    auto kern = gla_fwd_wide_kernel<DP, VEC, RAW, false>;
-    hipError_t e = ensure_lds<gla_fwd_wide_kernel<DP, VEC, RAW, false>>(W::BYTES);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(kern, dim3(wg.grid), dim3(WIDE_THREADS), W::BYTES, st,
-                       (const bf16*)fq, (const bf16*)fk, (const bf16*)v, lg, (bf16*)y,
-                       (const float*)seg_state, final_state, H, L, F, D, gate, G, cps,
-                       M, KG, RAW ? (float*)y : nullptr, raw_den, wg.per, wg.nx, wg.nblk,
-                       (const bf16*)nullptr, (const bf16*)nullptr);
-    return hipGetLastError();
+    auto launch = [&](auto tag) {
+      constexpr auto kern = decltype(tag)::value;
+      hipError_t e = ensure_lds<kern>(W::BYTES);
+      if (e != hipSuccess) return e;
+      hipLaunchKernelGGL(kern, dim3(wg.grid), dim3(WIDE_THREADS), W::BYTES, st,
+                         (const bf16*)fq, (const bf16*)fk, (const bf16*)v, lg, (bf16*)y,
+                         (const float*)seg_state, final_state, H, L, F, D, gate, G, cps, M, KG,
+                         RAW ? (float*)y : nullptr, raw_den, wg.per, wg.nx, wg.nblk,
+                         (const bf16*)nullptr, (const bf16*)nullptr, (const float*)seg_lam);
+      return hipGetLastError();
+    };
+    if constexpr (CAN_FOLD)
+      if (fold) return launch(KernTag<gla_fwd_wide_kernel<DP, VEC, RAW, false, true>>{});
+    return launch(KernTag<gla_fwd_wide_kernel<DP, VEC, RAW, false>>{});
   } else {
-    auto kern = gla_fwd_kernel<FP, DP, VEC, RAW>;
-    hipError_t e = ensure_lds<gla_fwd_kernel<FP, DP, VEC, RAW>>(Cfg::BYTES);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(kern, dim3(wg.grid), dim3(256), Cfg::BYTES, st, (const bf16*)fq,
-                       (const bf16*)fk, (const bf16*)v, lg, (bf16*)y, (const float*)seg_state,
-                       final_state, H, L, F, D, gate, G, cps, M, KG,
-                       RAW ? (float*)y : nullptr, raw_den, wg.per, wg.nx, wg.nblk);
-    return hipGetLastError();
+    auto launch = [&](auto tag) {
+      constexpr auto kern = decltype(tag)::value;
+      hipError_t e = ensure_lds<kern>(Cfg::BYTES);
+      if (e != hipSuccess) return e;
+      hipLaunchKernelGGL(kern, dim3(wg.grid), dim3(256), Cfg::BYTES, st, (const bf16*)fq,
+                         (const bf16*)fk, (const bf16*)v, lg, (bf16*)y, (const float*)seg_state,
+                         final_state, H, L, F, D, gate, G, cps, M, KG,
+                         RAW ? (float*)y : nullptr, raw_den, wg.per, wg.nx, wg.nblk,
+                         (const float*)seg_lam);
+      return hipGetLastError();
+    };
+    if constexpr (CAN_FOLD)
+      if (fold) return launch(KernTag<gla_fwd_kernel<FP, DP, VEC, RAW, true>>{});
+    return launch(KernTag<gla_fwd_kernel<FP, DP, VEC, RAW>>{});
   }
 }
 
@@ -1343,6 +1410,13 @@ static hipError_t prepare_fwd_t() {
   else
     e = ensure_lds<gla_fwd_kernel<FP, DP, VEC, false>>(GlaFwd<FP, DP>::BYTES);
   if (e != hipSuccess) return e;
+  if constexpr (gla_can_fold<FP, DP, VEC>()) {   // the folding walks
+    if constexpr (FP == 256)
+      e = ensure_lds<gla_fwd_wide_kernel<DP, VEC, false, false, true>>(GlaFwdWide<DP>::BYTES);
+    else
+      e = ensure_lds<gla_fwd_kernel<FP, DP, VEC, false, true>>(GlaFwd<FP, DP>::BYTES);
+    if (e != hipSuccess) return e;
+  }
   if constexpr (FP == 256) {   // the feature-sliced state passes
     if ((e = ensure_lds<gla_fwd_state_kernel<64, DP, VEC, FP>>(GlaState<64, DP>::BYTES)) !=
         hipSuccess)
@@ -1409,24 +1483,30 @@ hipError_t launch_gla_fwd_phi(const void* q, const void* wq, const void* fk, con
   const int F = FP, D = DP, BH = B * H;
   int G, cps;
   gla_segments(BH, L, F, &G, &cps);
+  float* seg_lam = ws + (size_t)BH * G * GlaFwd<FP, DP>::SEG;
+  const bool fold = gla_fold_segments(G);   // the walk with phi has a folding variant
+  static_assert(gla_can_fold<FP, DP, true>(), "folding variant of the phi walk");
   if (G > 1) {
-    hipError_t e = launch_gla_fwd_states_t<FP, DP, true>(
-        fk, v, lg, ws, ws + (size_t)BH * G * GlaFwd<FP, DP>::SEG, BH, H, L, F, D, gate, G, cps,
-        KG, st);
+    hipError_t e = launch_gla_fwd_states_t<FP, DP, true>(fk, v, lg, ws, seg_lam, BH, H, L, F, D,
+                                                         gate, G, cps, KG, fold, st);
     if (e != hipSuccess) return e;
   }
   const int M = gla_walk_segments(BH, G, F);
   const WalkGrid wg = walk_grid(BH * G / M, KG);
   using W = GlaFwdWide<DP>;
-  auto kern = gla_fwd_wide_kernel<DP, true, false, true>;
-  hipError_t e = ensure_lds<gla_fwd_wide_kernel<DP, true, false, true>>(W::PHI_BYTES);
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(kern, dim3(wg.grid), dim3(WIDE_THREADS), W::PHI_BYTES, st,
-                     (const bf16*)nullptr, (const bf16*)fk, (const bf16*)v, lg, (bf16*)y,
-                     (const float*)ws, final_state, H, L, F, D, gate, G, cps, M, KG,
-                     (float*)nullptr, (float*)nullptr, wg.per, wg.nx, wg.nblk, (const bf16*)q,
-                     (const bf16*)wq);
-  return hipGetLastError();
+  auto launch = [&](auto tag) {
+    constexpr auto kern = decltype(tag)::value;
+    hipError_t e = ensure_lds<kern>(W::PHI_BYTES);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(kern, dim3(wg.grid), dim3(WIDE_THREADS), W::PHI_BYTES, st,
+                       (const bf16*)nullptr, (const bf16*)fk, (const bf16*)v, lg, (bf16*)y,
+                       (const float*)ws, final_state, H, L, F, D, gate, G, cps, M, KG,
+                       (float*)nullptr, (float*)nullptr, wg.per, wg.nx, wg.nblk, (const bf16*)q,
+                       (const bf16*)wq, (const float*)seg_lam);
+    return hipGetLastError();
+  };
+  if (fold) return launch(KernTag<gla_fwd_wide_kernel<DP, true, false, true, true>>{});
+  return launch(KernTag<gla_fwd_wide_kernel<DP, true, false, true>>{});
 }
 
 }  // namespace lz

@@ -160,6 +160,24 @@ def test_gla_wide_features_segments(batch, heads, length, dim, per_head):
             label=f"F=256 D={dim} B*H={batch * heads} L={length}")
 
 
+@pytest.mark.parametrize("batch, heads, length, features, dim, per_head", [
+    (2, 64, 64 * 7 + 13, 128, 128, False),   # B*H = 128: 4 segments of 2 chunks
+    (4, 50, 300, 128, 64, True),              # B*H = 200: 3 segments, the last short
+    (1, 128, 200, 64, 128, False),            # 4 one-chunk segments, the last ragged
+    (2, 64, 500, 256, 64, False),             # eight-wave walks, two segments each
+])
+def test_gla_walks_fold_few_segments(batch, heads, length, features, dim, per_head):
+    # at most 4 segments per (b, h) with records of at least 128 x 64 floats:
+    # the walks fold the segment records themselves (no scan launch), in the
+    # forward, the dq walk (left to right) and the dkv walk (right to left)
+    inputs = gla_inputs(length, gates=(heads,) if per_head else (), batch=batch, heads=heads,
+                        features=features, dim=dim, seed=13)
+    grad = torch.randn(inputs[2].shape, generator=torch.Generator().manual_seed(2))
+    compare(gla_kernel(64), lambda *a: lo.gla_chunked(*a[:3], F.logsigmoid(a[3]), chunk=64,
+                                                      dtype=torch.float32),
+            inputs, grad, label=f"folded segments F={features} D={dim} B*H={batch * heads}")
+
+
 def test_gla_backward_without_forward_workspace_is_bitwise_equal():
     # through the C ABI: lz_gla_bwd given no forward workspace recomputes the
     # state entering each segment; the gradients must be the same bits as the

@@ -24,6 +24,10 @@ def _expand(t, group):
     # rows over two workgroups (120 segments), the expanded one does not (480)
     (1, 32, 8, 2048, 128, 128, False),
     (16, 32, 8, 130, 128, 128, True),  # B*H fills the GPU: one walk per (b, h)
+    # at most 4 segments: the walks fold the segment records (kv-head records
+    # with a per-token gate; two segments per eight-wave walk at F = 256)
+    (2, 64, 16, 500, 256, 64, False), (2, 64, 16, 500, 256, 64, True),
+    (2, 64, 16, 461, 128, 128, False),
     # past the walks' sizes, both gate kinds: two D tiles (the fused bf16 layer
     # at head_dim 128 x 128 features), two F tiles (summed raw numerators),
     # and ragged F and D tiles
