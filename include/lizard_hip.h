@@ -205,8 +205,10 @@ size_t lz_gla_bwd_workspace_bytes(int batch, int heads, int length, int nf, int 
  *   dlog_gamma    f32, same shape as log_gamma (with LZ_GATE_LOGIT: the gradient of
  *                 the logit z, d log_gamma * sigmoid(-z))
  *   fwd_workspace the workspace lz_gla_fwd used for these inputs, if the caller
- *                 kept it (it then holds the state entering each segment and
- *                 the backward skips recomputing it); may be NULL
+ *                 kept it (it then holds the segment state records, scanned
+ *                 into the state entering each segment or, for at most 4
+ *                 segments, left for the walks to combine, and the backward
+ *                 skips recomputing them); may be NULL
  * The other arguments are those of lz_gla_fwd, with its sizes.
  */
 int lz_gla_bwd(const void* fq, const void* fk, const void* v, const float* log_gamma,

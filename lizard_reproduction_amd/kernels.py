@@ -170,7 +170,7 @@ def _gate_mode(lg, gate_logit):
 def gla_forward(fq, fk, v, lg, keep_state=True, chunk=CHUNK, gate_logit=False):
     """One ``lz_gla_fwd`` launch on bf16 contiguous fq, fk, v and fp32
     contiguous log_gamma; returns (y, state), state being the workspace of
-    the states entering each sequence segment, which ``gla_backward`` reuses
+    the sequence segments' state records, which ``gla_backward`` reuses
     (None when not kept, not needed, or for tiled sizes past the walks').  fk and v may have fewer heads than
     fq (a divisor: grouped-query attention, each kv head shared by
     consecutive query heads).  With ``gate_logit`` lg holds the gate's logit
@@ -250,7 +250,7 @@ class _GLA(torch.autograd.Function):
         y, state = _gla_fwd_launch(fq, fk, v, lg, grad, chunk, False)
         if grad:
             ctx.save_for_backward(fq, fk, v, lg)
-            # the state entering each segment, reused by the backward
+            # the segments' state records, reused by the backward
             ctx.fwd_ws = state
         ctx.chunk = chunk
         return y
