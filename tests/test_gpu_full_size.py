@@ -57,15 +57,16 @@ def test_config4_longest_slices_match_chunked_oracle():
 @pytest.mark.parametrize("batch, length, slices", [
     (1, 4096, [(0, 0), (0, 17), (0, 31)]),      # 16 segments of 4 chunks
     (1, 16384, [(0, 5), (0, 30)]),              # 16 segments of 16 chunks
-    (4, 2048, [(0, 0), (2, 9), (3, 31)]),       # 4 segments of 8 chunks
-    (4, 8192, [(1, 3), (3, 28)])])              # 4 segments of 32 chunks
+    (4, 2048, [(0, 0), (2, 9), (3, 31)]),       # 4 segments of 8 chunks (records folded)
+    (4, 8192, [(1, 3), (3, 28)])])              # 4 segments of 32 chunks (records folded)
 def test_config4_segmented_d128_walks_slices_match_chunked_oracle(batch, length, slices):
     """The config-4 sweep points whose B*H (32, 128) cannot fill the GPU:
     each (b, h) sequence is cut into segments of several chunks, so the
-    F=D=128 segment state pass, the forward and reverse segment scans and
-    the walks that start from a scanned state all run; output and every
-    gradient (d log_gamma per head) of sampled slices against the chunked
-    fp64 oracle."""
+    F=D=128 segment state passes run, then either the forward and reverse
+    segment scans and walks that start from a scanned state (16 segments)
+    or walks that fold the records themselves (4 segments); output and
+    every gradient (d log_gamma per head) of sampled slices against the
+    chunked fp64 oracle."""
     from lizard_reproduction_amd import _lib
     lib = _lib.load()
     assert lib.lz_gla_fwd_workspace_bytes(batch, 32, length, 128, 128, 1, 64) > 0  # segmented
