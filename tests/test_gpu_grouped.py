@@ -28,6 +28,7 @@ def _expand(t, group):
     # with a per-token gate; two segments per eight-wave walk at F = 256)
     (2, 64, 16, 500, 256, 64, False), (2, 64, 16, 500, 256, 64, True),
     (2, 64, 16, 461, 128, 128, False),
+    (2, 64, 16, 300, 256, 128, True),   # two D tiles, each folding its records
     # past the walks' sizes, both gate kinds: two D tiles (the fused bf16 layer
     # at head_dim 128 x 128 features), two F tiles (summed raw numerators),
     # and ragged F and D tiles
