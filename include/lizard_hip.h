@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define LZ_ABI_VERSION 14
+#define LZ_ABI_VERSION 15
 
 /*
  * gate_mode of the GLA entry points: a combination of
@@ -44,10 +44,19 @@ extern "C" {
  *                     F.logsigmoid (src/lizard_attention.py:92); the gate
  *                     gradient they write is then d/dz = d log_gamma *
  *                     sigmoid(-z).  Without it the buffer holds log_gamma.
+ *   LZ_GLA_NO_REUSE   a hint: nothing reads fq, fk and v again soon (no
+ *                     backward follows this forward), so the forward walk may
+ *                     load them nontemporally.  Used by lz_gla_fwd,
+ *                     lz_gla_prefill and lz_gla_fwd_noalloc (for one segment
+ *                     per row and kv_heads == heads), ignored by the other
+ *                     GLA entry points; the results are the same bits with or
+ *                     without it.  No counterpart in the reference (a cache
+ *                     policy of this build's loads).
  * Other bits are refused.
  */
 #define LZ_GATE_PER_HEAD 1
 #define LZ_GATE_LOGIT 2
+#define LZ_GLA_NO_REUSE 4
 
 /* Largest feature (nf) and value (nd) dim the GLA entry points take. */
 #define LZ_GLA_MAX_DIM 4096

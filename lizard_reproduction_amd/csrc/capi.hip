@@ -141,14 +141,16 @@ static int check_kv_heads(const char* what, int heads, int kv_heads) {
   return 0;
 }
 
-static_assert(LZ_GATE_PER_HEAD == lz::GATE_PER_HEAD && LZ_GATE_LOGIT == lz::GATE_LOGIT,
+static_assert(LZ_GATE_PER_HEAD == lz::GATE_PER_HEAD && LZ_GATE_LOGIT == lz::GATE_LOGIT &&
+                  LZ_GLA_NO_REUSE == lz::GATE_NO_REUSE,
               "gate mode bits");
 
-// gate_mode: LZ_GATE_PER_HEAD and LZ_GATE_LOGIT bits, nothing else
+// gate_mode: LZ_GATE_PER_HEAD, LZ_GATE_LOGIT and LZ_GLA_NO_REUSE bits,
+// nothing else (the entry points that do not walk forward ignore the hint)
 static int check_gate_mode(const char* what, int gate_mode) {
-  if (gate_mode & ~(LZ_GATE_PER_HEAD | LZ_GATE_LOGIT))
-    return fail(1, "%s: gate_mode %d has bits other than LZ_GATE_PER_HEAD (1) and "
-                   "LZ_GATE_LOGIT (2)", what, gate_mode);
+  if (gate_mode & ~(LZ_GATE_PER_HEAD | LZ_GATE_LOGIT | LZ_GLA_NO_REUSE))
+    return fail(1, "%s: gate_mode %d has bits other than LZ_GATE_PER_HEAD (1), "
+                   "LZ_GATE_LOGIT (2) and LZ_GLA_NO_REUSE (4)", what, gate_mode);
   return 0;
 }
 

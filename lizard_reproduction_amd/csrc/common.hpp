@@ -42,7 +42,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // gate logit z and log_gamma = logsigmoid(z) is formed where it is read (the
 // layer's F.logsigmoid, src/lizard_attention.py:92), and the gate gradient
 // written is d/dz = d log_gamma * sigmoid(-z).
-constexpr int GATE_PER_HEAD = 1, GATE_LOGIT = 2;
+constexpr int GATE_PER_HEAD = 1, GATE_LOGIT = 2, GATE_NO_REUSE = 4;
 
 constexpr int WAVE = 64;
 constexpr float TINY = 1.1754943508222875e-38f;   // FLT_MIN, the reference's clamp
@@ -343,8 +343,12 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base, size_t bytes) {
                                            (int)(uint32_t)(bytes < OOB ? bytes : OOB), RSRC_WORD3);
 }
 
+// AUX: the load's cache policy (LOAD_NT: nontemporal, for data that nothing
+// reads again soon)
+constexpr int LOAD_NT = 2;
+template <int AUX = 0>
 __device__ __forceinline__ uint4 bload16(rsrc_t r, uint32_t off) {
-  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, AUX));
 }
 
 __device__ __forceinline__ float bload_f32(rsrc_t r, uint32_t off) {
@@ -354,8 +358,9 @@ __device__ __forceinline__ float bload_f32(rsrc_t r, uint32_t off) {
 // Columns [c, c+8) of row `row` of a row-major [nrows x ncols] bf16 matrix
 // behind resource r, zero outside it (rows < 0 or >= nrows included).
 // Vector form (ncols % 8 == 0): an item is wholly inside or outside a row.
+template <int AUX = 0>
 __device__ __forceinline__ uint4 bload8_vec(rsrc_t r, int row, int c, int ncols) {
-  return bload16(r, (row >= 0 && c < ncols) ? (uint32_t)(row * ncols + c) * 2u : OOB);
+  return bload16<AUX>(r, (row >= 0 && c < ncols) ? (uint32_t)(row * ncols + c) * 2u : OOB);
 }
 
 // Element form for any ncols: eight 2-byte loads.
@@ -449,7 +454,7 @@ __device__ __forceinline__ void store_acc_row(OutT* __restrict__ base, int row, 
 // grid of 8-column items starting at row r0: item idx covers row
 // r0 + idx / (KP/8), columns 8 (idx % (KP/8)).  The uniform `vec` test sits
 // outside the unrolled loop, so the vector form is straight-line loads.
-template <int KP, int NT, int N, int ITEMS>
+template <int KP, int NT, int N, int ITEMS, int AUX = 0>
 __device__ __forceinline__ void load_items(uint4 (&reg)[N], const bf16* __restrict__ base, int r0,
                                            int nrows, int ncols, bool vec) {
   constexpr int K8 = KP / 8;
@@ -459,7 +464,7 @@ __device__ __forceinline__ void load_items(uint4 (&reg)[N], const bf16* __restri
     for (int i = 0; i < N; ++i) {
       const int idx = threadIdx.x + NT * i;
       if (ITEMS % NT == 0 || idx < ITEMS)
-        reg[i] = bload8_vec(r, r0 + idx / K8, (idx % K8) * 8, ncols);
+        reg[i] = bload8_vec<AUX>(r, r0 + idx / K8, (idx % K8) * 8, ncols);
     }
   } else {
 #pragma unroll

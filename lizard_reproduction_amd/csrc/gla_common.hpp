@@ -60,10 +60,10 @@ size_t gla_segment_floats(int BH, int G, int F, int D);
 // Rows [t0, t0+64) of a [L x ncols] bf16 matrix into registers, 16 bytes per
 // load: thread slot idx = tid + 256 i covers row idx / (KP/8), columns
 // 8 * (idx % (KP/8)) .. +8.  Zero outside the matrix.
-template <int KP, int N>
+template <int KP, int N, int AUX = 0>
 __device__ __forceinline__ void load_chunk(uint4 (&reg)[N], const bf16* __restrict__ base, int t0,
                                            int L, int ncols, bool vec) {
-  load_items<KP, 256, N, 256 * N>(reg, base, t0, L, ncols, vec);
+  load_items<KP, 256, N, 256 * N, AUX>(reg, base, t0, L, ncols, vec);
 }
 
 template <int KP, int N>

@@ -79,7 +79,7 @@ struct GlaFwd {
 // RAW (one F tile of a split feature dimension): instead of y, the walk writes
 // the unnormalised numerator o (fp32 [BH, L, D] at raw_num) and denominator
 // (fp32 [BH, L] at raw_den), which the caller sums over the F tiles.
-template <int FP, int DP, bool VEC, bool RAW, bool FOLD = false>
+template <int FP, int DP, bool VEC, bool RAW, bool FOLD = false, bool NTL = false>
 __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
     const bf16* __restrict__ fq, const bf16* __restrict__ fk, const bf16* __restrict__ v,
     const float* __restrict__ log_gamma, bf16* __restrict__ y,
@@ -90,6 +90,9 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
   constexpr int C = Cfg::C, PF = Cfg::PF, PD = Cfg::PD;
   constexpr int NFT = Cfg::NFT, NDT = Cfg::NDT;
   using RD = Roles<NDT>;   // wave -> owned d-tiles (state and output) x output q-tiles
+  // NTL: the chunk loads are nontemporal (one segment, no shared kv heads:
+  // nothing reads these rows again during the walk)
+  constexpr int AUX = NTL ? LOAD_NT : 0;
   constexpr int NDW = RD::TILES, NQW = RD::HALVES;
   extern __shared__ __align__(16) char smem[];
   bf16* fq_l = reinterpret_cast<bf16*>(smem + Cfg::OFF_FQ);
@@ -172,9 +175,9 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
 
   uint4 rq[Cfg::NLF], rk[Cfg::NLF], rv[Cfg::NLD];
   float rg;
-  load_chunk<FP>(rq, fqb, n0 * C, L, F, vecF);
-  load_chunk<FP>(rk, fkb, n0 * C, L, F, vecF);
-  load_chunk<DP>(rv, vb, n0 * C, L, D, vecD);
+  load_chunk<FP, Cfg::NLF, AUX>(rq, fqb, n0 * C, L, F, vecF);
+  load_chunk<FP, Cfg::NLF, AUX>(rk, fkb, n0 * C, L, F, vecF);
+  load_chunk<DP, Cfg::NLD, AUX>(rv, vb, n0 * C, L, D, vecD);
   rg = gate_at(lgb, n0 * C + lane, L);
   store_chunk<FP>(rq, fq_l, PF);
   store_chunk<FP>(rk, fk_l, PF);
@@ -186,9 +189,9 @@ __global__ __launch_bounds__(256, FP >= 256 ? 1 : 2) void gla_fwd_kernel(
     const int t0 = n * C;
     const bool more = n + 1 < n1;
     if (more) {   // next chunk in flight while this one computes
-      load_chunk<FP>(rq, fqb, t0 + C, L, F, vecF);
-      load_chunk<FP>(rk, fkb, t0 + C, L, F, vecF);
-      load_chunk<DP>(rv, vb, t0 + C, L, D, vecD);
+      load_chunk<FP, Cfg::NLF, AUX>(rq, fqb, t0 + C, L, F, vecF);
+      load_chunk<FP, Cfg::NLF, AUX>(rk, fkb, t0 + C, L, F, vecF);
+      load_chunk<DP, Cfg::NLD, AUX>(rv, vb, t0 + C, L, D, vecD);
       rg = gate_at(lgb, t0 + C + lane, L);
     }
     __builtin_amdgcn_s_setprio(0);
@@ -1395,6 +1398,15 @@ static hipError_t launch_gla_fwd_t(const void* fq, const void* fk, const void* v
     };
     if constexpr (CAN_FOLD)
       if (fold) return launch(KernTag<gla_fwd_kernel<FP, DP, VEC, RAW, true>>{});
+    // the caller reads fq, fk, v no more (GATE_NO_REUSE: no backward
+    // follows), and with one segment and no kv head shared by query heads
+    // this walk reads each row once: its chunk loads go nontemporal
+    // (headline forward 216.9 -> 208.8 us).  Where a state pass or other
+    // heads' walks read the rows again, as at config 2, such loads were 15 %
+    // slower, and before a backward the fwd+bwd was 0.5 % slower.
+    if constexpr (VEC && !RAW)
+      if ((gate & GATE_NO_REUSE) && G == 1 && KG == 1)
+        return launch(KernTag<gla_fwd_kernel<FP, DP, VEC, RAW, false, true>>{});
     return launch(KernTag<gla_fwd_kernel<FP, DP, VEC, RAW>>{});
   }
 }
@@ -1415,6 +1427,10 @@ static hipError_t prepare_fwd_t() {
       e = ensure_lds<gla_fwd_wide_kernel<DP, VEC, false, false, true>>(GlaFwdWide<DP>::BYTES);
     else
       e = ensure_lds<gla_fwd_kernel<FP, DP, VEC, false, true>>(GlaFwd<FP, DP>::BYTES);
+    if (e != hipSuccess) return e;
+  }
+  if constexpr (FP < 256 && VEC) {   // the walk with nontemporal chunk loads
+    e = ensure_lds<gla_fwd_kernel<FP, DP, VEC, false, false, true>>(GlaFwd<FP, DP>::BYTES);
     if (e != hipSuccess) return e;
   }
   if constexpr (FP == 256) {   // the feature-sliced state passes

@@ -160,7 +160,7 @@ def gla_native(nf, nd):
 
 
 # gate_mode bits of the C ABI (include/lizard_hip.h)
-GATE_PER_HEAD, GATE_LOGIT = 1, 2
+GATE_PER_HEAD, GATE_LOGIT, GLA_NO_REUSE = 1, 2, 4
 
 
 def _gate_mode(lg, gate_logit):
@@ -171,7 +171,9 @@ def gla_forward(fq, fk, v, lg, keep_state=True, chunk=CHUNK, gate_logit=False):
     """One ``lz_gla_fwd`` launch on bf16 contiguous fq, fk, v and fp32
     contiguous log_gamma; returns (y, state), state being the workspace of
     the sequence segments' state records, which ``gla_backward`` reuses
-    (None when not kept, not needed, or for tiled sizes past the walks').  fk and v may have fewer heads than
+    (None when not kept, not needed, or for tiled sizes past the walks').
+    Not keeping it also tells the kernels that nothing reads fq, fk, v again
+    soon (``LZ_GLA_NO_REUSE``: no backward follows).  fk and v may have fewer heads than
     fq (a divisor: grouped-query attention, each kv head shared by
     consecutive query heads).  With ``gate_logit`` lg holds the gate's logit
     z and the kernels use log_gamma = logsigmoid(z) (the layer's
@@ -189,7 +191,7 @@ def _gla_fwd_launch(fq, fk, v, lg, keep_state, chunk, gate_logit):
     ws = None
     if y.numel():
         lib = _lib.load()
-        mode = _gate_mode(lg, gate_logit)
+        mode = _gate_mode(lg, gate_logit) | (0 if keep_state else GLA_NO_REUSE)
         nbytes = _gla_fwd_ws(b, h, length, nf, nd, mode & GATE_PER_HEAD, chunk)
         ws = torch.empty(nbytes, dtype=torch.uint8, device=fq.device) if nbytes else None
         rc = lib.lz_gla_fwd(_ptr(fq), _ptr(fk), _ptr(v), _ptr(lg), _ptr(y), b, h, fk.shape[1],
@@ -284,7 +286,7 @@ def gla_prefill(fq, fk, v, log_gamma, chunk=CHUNK, gate_logit=False):
     state = torch.zeros(b, h, nf * nd + nf, device=fq.device, dtype=torch.float32)
     if y.numel():
         lib = _lib.load()
-        mode = _gate_mode(lg, gate_logit)
+        mode = _gate_mode(lg, gate_logit) | GLA_NO_REUSE   # inference: no backward
         nbytes = _gla_fwd_ws(b, h, length, nf, nd, mode & GATE_PER_HEAD, chunk)
         ws = torch.empty(nbytes, dtype=torch.uint8, device=fq.device) if nbytes else None
         rc = lib.lz_gla_prefill(_ptr(fq), _ptr(fk), _ptr(v), _ptr(lg), _ptr(y), _ptr(state), b, h,

@@ -123,9 +123,10 @@ def test_bad_sizes_are_rejected_before_any_launch(lib):
 
 @no_gpu
 def test_gate_mode_bits_are_checked(lib):
-    """gate_mode takes LZ_GATE_PER_HEAD (1) and LZ_GATE_LOGIT (2) only."""
+    """gate_mode takes LZ_GATE_PER_HEAD (1), LZ_GATE_LOGIT (2) and the hint
+    LZ_GLA_NO_REUSE (4) only."""
     p = ctypes.c_void_p(16)   # never dereferenced: validation fails first
-    refused(lib, lib.lz_gla_fwd(p, p, p, p, p, 1, 1, 1, 8, 16, 16, 4, 64, None, 0, None),
+    refused(lib, lib.lz_gla_fwd(p, p, p, p, p, 1, 1, 1, 8, 16, 16, 8, 64, None, 0, None),
             b"gate_mode")
     refused(lib, lib.lz_gla_decode_step(p, p, p, p, p, p, 1, 4, 2, 64, 64, 8, None), b"gate_mode")
     ws = lib.lz_gla_bwd_workspace_bytes(1, 1, 8, 16, 16, 3, 64)
@@ -134,7 +135,8 @@ def test_gate_mode_bits_are_checked(lib):
     refused(lib, rc, b"gate_mode")
     text = open(HEADER).read()
     assert "#define LZ_GATE_PER_HEAD 1" in text and "#define LZ_GATE_LOGIT 2" in text
-    assert (kernels.GATE_PER_HEAD, kernels.GATE_LOGIT) == (1, 2)
+    assert "#define LZ_GLA_NO_REUSE 4" in text
+    assert (kernels.GATE_PER_HEAD, kernels.GATE_LOGIT, kernels.GLA_NO_REUSE) == (1, 2, 4)
 
 
 @no_gpu
@@ -153,7 +155,7 @@ def test_phi_forward_rejects_bad_arguments(lib):
             b"null")
     refused(lib, f(p, p, p, p, p, p, None, 1, 4, 3, 64, 64, 128, 0, 64, p, 1 << 20, None),
             b"kv_heads")
-    refused(lib, f(p, p, p, p, p, p, None, 1, 4, 2, 64, 64, 128, 4, 64, p, 1 << 20, None),
+    refused(lib, f(p, p, p, p, p, p, None, 1, 4, 2, 64, 64, 128, 8, 64, p, 1 << 20, None),
             b"gate_mode")
     need = lib.lz_gla_fwd_workspace_bytes(1, 4, 4096, 256, 64, 0, 64)
     assert need > 0
