@@ -777,7 +777,7 @@ def main():
                    "gate": "per-head logsigmoid(N(2,1.5))", "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(), "kernel": "gla_fwd_kernel<128,128,true,false,false>",
+                     "traffic": measured_traffic(), "kernel": "gla_fwd_kernel<128,128,true,false,false,true>",
                      "algorithmic_bytes": nbytes},
         "cpu_baseline": cpu,
         "extra": extra,
