@@ -592,7 +592,10 @@ struct SwaWalk {
   static_assert(SWA_TILE == 64 && SwaCfg<64>::NL * 256 == 64 * 8, "tile items");
 };
 
-template <typename OutT, bool VEC>
+// NTQ: the q and dy tiles load nontemporally (each is read by one walk),
+// which leaves the caches to the k and v tiles that KG > 1 query heads share
+// (config 5: 103.6 -> 98.2 us; at config 3, KG = 1, it read 21.6 -> 22.0 us)
+template <typename OutT, bool VEC, bool NTQ = false>
 __global__ __launch_bounds__(64 * SWA_WALK_WAVES, 1) void swa_bwd_walk_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ meta, int n_meta, const float* __restrict__ lse,
@@ -630,6 +633,11 @@ __global__ __launch_bounds__(64 * SWA_WALK_WAVES, 1) void swa_bwd_walk_kernel(
     load_items<64, NT, 1, NT>(t, src, r0, L, d, vec);
     r = t[0];
   };
+  auto load_qd = [&](uint4& r, const bf16* src, int r0) {   // a q or dy tile
+    uint4 t[1];
+    load_items<64, NT, 1, NT, NTQ ? LOAD_NT : 0>(t, src, r0, L, d, vec);
+    r = t[0];
+  };
   auto store_tile = [&](const uint4& r, bf16* tile) {
     *reinterpret_cast<uint4*>(tile + (tid >> 3) * P + (tid & 7) * 8) = r;
   };
@@ -654,8 +662,8 @@ __global__ __launch_bounds__(64 * SWA_WALK_WAVES, 1) void swa_bwd_walk_kernel(
     load_tile(v0r, vb, SWA_TILE * (b0 - 1));
     load_tile(pk, kb, SWA_TILE * b0);
     load_tile(pv, vb, SWA_TILE * b0);
-    load_tile(pq, qb, SWA_TILE * b0);
-    load_tile(pd, dyb, SWA_TILE * b0);
+    load_qd(pq, qb, SWA_TILE * b0);
+    load_qd(pd, dyb, SWA_TILE * b0);
     pl = load_lse(SWA_TILE * b0);
     store_tile(k0r, kslot(b0 - 1));
     store_tile(v0r, vslot(b0 - 1));
@@ -667,8 +675,8 @@ __global__ __launch_bounds__(64 * SWA_WALK_WAVES, 1) void swa_bwd_walk_kernel(
     if (b0 + 1 <= iend) {
       load_tile(pk, kb, SWA_TILE * (b0 + 1));
       load_tile(pv, vb, SWA_TILE * (b0 + 1));
-      load_tile(pq, qb, SWA_TILE * (b0 + 1));
-      load_tile(pd, dyb, SWA_TILE * (b0 + 1));
+      load_qd(pq, qb, SWA_TILE * (b0 + 1));
+      load_qd(pd, dyb, SWA_TILE * (b0 + 1));
       pl = load_lse(SWA_TILE * (b0 + 1));
     }
   }
@@ -765,8 +773,8 @@ __global__ __launch_bounds__(64 * SWA_WALK_WAVES, 1) void swa_bwd_walk_kernel(
       if (i + 2 <= iend) {
         load_tile(pk, kb, SWA_TILE * (i + 2));
         load_tile(pv, vb, SWA_TILE * (i + 2));
-        load_tile(pq, qb, SWA_TILE * (i + 2));
-        load_tile(pd, dyb, SWA_TILE * (i + 2));
+        load_qd(pq, qb, SWA_TILE * (i + 2));
+        load_qd(pd, dyb, SWA_TILE * (i + 2));
         pl = load_lse(SWA_TILE * (i + 2));
       }
     }
@@ -920,13 +928,18 @@ static hipError_t launch_swa_bwd_walk(const void* q, const void* k, const void* 
   const int nblk = (L + SWA_TILE - 1) / SWA_TILE;
   const int NB = swa_walk_blocks(BH, L), nseg = (nblk + NB - 1) / NB;
   const int nx = device_geom().xcds, grid = xcd_grid(BH * nseg, nx), per = grid / nx;
-  hipError_t e = ensure_lds<swa_bwd_walk_kernel<OutT, VEC>>(SwaWalk::LDS);
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((swa_bwd_walk_kernel<OutT, VEC>), dim3(grid), dim3(64 * SWA_WALK_WAVES),
-                     SwaWalk::LDS, st, (const bf16*)q, (const bf16*)k, (const bf16*)v, meta,
-                     n_meta, lse, (const bf16*)dy, (OutT*)dq, (OutT*)dk, (OutT*)dv, dmeta_part, BH,
-                     L, d, W, scale, NB, nseg, per, nx, KG);
-  if ((e = hipGetLastError()) != hipSuccess || n_meta == 0) return e;
+  auto launch = [&](auto tag) {
+    constexpr auto kern = decltype(tag)::value;
+    if (hipError_t e2 = ensure_lds<kern>(SwaWalk::LDS); e2 != hipSuccess) return e2;
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * SWA_WALK_WAVES), SwaWalk::LDS, st,
+                       (const bf16*)q, (const bf16*)k, (const bf16*)v, meta, n_meta, lse,
+                       (const bf16*)dy, (OutT*)dq, (OutT*)dk, (OutT*)dv, dmeta_part, BH, L, d, W,
+                       scale, NB, nseg, per, nx, KG);
+    return hipGetLastError();
+  };
+  hipError_t e = KG > 1 ? launch(KernTag<swa_bwd_walk_kernel<OutT, VEC, true>>{})
+                        : launch(KernTag<swa_bwd_walk_kernel<OutT, VEC>>{});
+  if (e != hipSuccess || n_meta == 0) return e;
   hipLaunchKernelGGL(swa_dmeta_reduce_kernel, dim3(1), dim3(64), 0, st,
                      (const float*)dmeta_part, BH * nseg, meta, n_meta, dmeta);
   return hipGetLastError();
