@@ -241,8 +241,11 @@ hipError_t launch_gla_fwd_any(const void* fq, const void* fk, const void* v, con
   if (t.nF == 1) {   // D tiles of the native walk, each its own columns of y
     for (int d = 0; d < t.nD; ++d) {
       const int dw = width_of(d, t.nD, t.Dt, D);
+      // every D tile reads fq and fk again: only the last may load them as
+      // read no more (GATE_NO_REUSE)
+      const int gd = d + 1 < t.nD ? gph & ~GATE_NO_REUSE : gph;
       if ((e = copy_bf16(b.vt, dw, 0, (const bf16*)v, D, d * t.Dt, dw, BHLk, st))) return e;
-      if ((e = launch_gla_fwd(fq, fk, b.vt, lg, b.yt, B, H, L, F, dw, gph, KG, b.inner, nullptr,
+      if ((e = launch_gla_fwd(fq, fk, b.vt, lg, b.yt, B, H, L, F, dw, gd, KG, b.inner, nullptr,
                               nullptr, st)))
         return e;
       if ((e = copy_bf16((bf16*)y, D, d * t.Dt, b.yt, dw, 0, dw, BHL, st))) return e;
