@@ -807,7 +807,7 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
     float* __restrict__ dG, float* __restrict__ csum, float* __restrict__ dlg_direct,
     const float* __restrict__ seg_state, int H,
     int L, int F, int D, int gate, int G, int cps, int M, int KG, int xper, int nxcd,
-    int nblk, const float* __restrict__ seg_lam) {
+    int nblk, const float* __restrict__ seg_lam, int rev) {
   using Cfg = BwdB<FP, DP>;
   constexpr int C = Cfg::C, PF = Cfg::PF, PD = Cfg::PD;
   constexpr int NFT = Cfg::NFT, NDT = Cfg::NDT, ZP = Cfg::ZP;
@@ -837,7 +837,7 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
   // entering with the state that flows into the last of them
   const int nwg = G / M;
   int blk;
-  if (!walk_block(xper, nxcd, nblk, blk)) return;
+  if (!walk_block(xper, nxcd, nblk, blk, rev != 0)) return;
   const int bh = blk / nwg, seg0 = (blk % nwg) * M, seg = seg0 + M - 1;
   const int NT = (L + C - 1) / C;
   const int n0 = seg0 * cps, n1 = min(NT, n0 + M * cps);
@@ -1303,6 +1303,11 @@ static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v
   // a per-head gate in one segment: the reverse walk of (b, h) sees its whole
   // gate row and writes d log_gamma itself (no gate launch, no dG)
   const bool direct_dlg = (gate & GATE_PER_HEAD) && G == 1;
+  // more workgroups than CUs (one walk workgroup per CU): the dkv walk runs in
+  // rounds, and takes its blocks in reverse so that its first round starts on
+  // the rows the dq walk read last (headline fwd+bwd -0.9 %, B=16 L=4096
+  // -0.7 %; a one-round launch gains nothing from the order)
+  const int rev = wg.grid > device_geom().cus;
   auto launch_b = [&](auto tag) {
     constexpr auto kern = decltype(tag)::value;
     if (hipError_t e2 = ensure_lds<kern>(LDS_B); e2 != hipSuccess) return e2;
@@ -1310,7 +1315,7 @@ static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v
                        (const bf16*)fk, (const bf16*)v, lg, (const bf16*)dy, (const float*)den,
                        (const float*)delta, (const float*)p, (OutT*)dfk, (OutT*)dv, dG, csum,
                        direct_dlg ? dlg : nullptr, (const float*)rseg, H, L, F, D, gate, G,
-                       cps, M, KG, wg.per, wg.nx, wg.nblk, (const float*)rlam);
+                       cps, M, KG, wg.per, wg.nx, wg.nblk, (const float*)rlam, rev);
     return hipGetLastError();
   };
   if (CAN_FOLD && fold)

@@ -330,10 +330,10 @@ struct Roles {
 // the XCD count.  With KG = 1 the launch order is kept (the grouped order
 // measured slower there).
 struct WalkGrid {
-  int grid, per, nx, nblk;   // per = 0: launch order
+  int grid, per, nx, nblk;   // per = 0: launch order; nx = the device's XCDs
 };
 inline WalkGrid walk_grid(int nblk, int KG) {
-  if (KG <= 1) return WalkGrid{nblk, 0, 1, nblk};
+  if (KG <= 1) return WalkGrid{nblk, 0, device_geom().xcds, nblk};
   const int nx = device_geom().xcds;
   const int grid = xcd_grid(nblk, nx);
   return WalkGrid{grid, grid / nx, nx, nblk};
@@ -341,8 +341,19 @@ inline WalkGrid walk_grid(int nblk, int KG) {
 
 // Logical block of this walk workgroup; false for the padding blocks of a
 // grouped grid (the whole workgroup returns before any barrier).
-__device__ __forceinline__ bool walk_block(int xper, int nx, int nblk, int& blk) {
-  blk = xper ? xcd_block((int)blockIdx.x, xper, nx) : (int)blockIdx.x;
+// rev: the workgroups of each XCD (workgroup i runs on XCD i % nx) take that
+// XCD's blocks in reverse launch order, each block kept on its XCD.  A walk
+// launched in more than one round of workgroups after a walk over the same
+// rows in launch order then starts on the rows that walk read last, which the
+// memory-side cache (and for the last chunks the XCD's L2) still holds.
+__device__ __forceinline__ bool walk_block(int xper, int nx, int nblk, int& blk,
+                                           bool rev = false) {
+  int b = (int)blockIdx.x;
+  if (rev) {
+    const int full = (int)gridDim.x - (int)gridDim.x % nx;
+    if (b < full) b = full - nx - (b - b % nx) + b % nx;
+  }
+  blk = xper ? xcd_block(b, xper, nx) : b;
   return blk < nblk;
 }
 

@@ -99,6 +99,36 @@ def test_headline_shape_is_deterministic():
         assert torch.equal(a, b)
 
 
+def test_headline_shape_every_row_matches_per_row_calls():
+    """At the headline shape each backward walk launches twice as many
+    workgroups as there are CUs, so it runs in two rounds, and the dkv walk
+    takes its blocks in reverse launch order per XCD.  Every (b, h) of the
+    output and of every gradient is compared with the same call made one
+    batch row at a time (32 (b, h) per call: segmented walks in one round,
+    whose parity the segmented tests above pin), so a block that the order
+    skipped or computed twice fails somewhere in the whole tensors."""
+    fq, fk, v, lg, dy = baseline_gla_inputs(16, 32, 2048, 128, True, 2.0, 1.5)
+    leaves = [t.cuda().requires_grad_() for t in (fq, fk, v, lg)]
+    y = kernels.gla(*leaves)
+    y.backward(dy.cuda())
+    worst = {}
+    for b in range(16):
+        row = [t[b:b + 1].cuda().requires_grad_() for t in (fq, fk, v, lg)]
+        yr = kernels.gla(*row)
+        yr.backward(dy[b:b + 1].cuda())
+        pairs = {"y": (y[b], yr[0])}
+        for name, full, part in zip(("dfq", "dfk", "dv", "dlg"), leaves, row):
+            pairs[name] = (full.grad[b], part.grad[0])
+        for k, (a, r) in pairs.items():
+            worst[k] = max(worst.get(k, 0.0), max_rel(a, r))
+    print("[parity] headline whole batch vs per-row calls: " +
+          " ".join(f"{k}={e:.2e}" for k, e in worst.items()), flush=True)
+    assert worst["y"] <= OUT_TOL, worst
+    for k, e in worst.items():
+        if k != "y":
+            assert e <= GRAD_TOL, (k, worst)
+
+
 def config5_attention_inputs():
     """The layer's GLA call at BASELINE config 5: B=4, H=32, L=4096, F=256
     (Hedgehog maps [softmax(x), softmax(-x)] of 128 features), D=64, one gate
