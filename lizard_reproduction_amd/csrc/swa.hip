@@ -836,22 +836,38 @@ __global__ __launch_bounds__(64 * SWA_WALK_WAVES, 1) void swa_bwd_walk_kernel(
 }
 
 // dmeta_j = -e^{meta_j - m} sum_w T_w, the workgroups' T summed in a fixed
-// order by one wave (strided lane sums, then a butterfly); the sinks' loads
-// issue first, so the kernel's one chain is a load and a wave reduction.
+// order by one wave (strided lane sums, then a butterfly).  The lane's sink
+// logit and its first 16 partials are loaded together, before any is used
+// (buffer loads, zero past the end), so the kernel waits one memory round
+// trip for up to 1024 partials, not one per 64; each lane still adds its
+// partials in row order, from zero.
 __global__ __launch_bounds__(64) void swa_dmeta_reduce_kernel(const float* __restrict__ part,
                                                               int rows, const float* __restrict__ meta,
                                                               int n_meta, float* __restrict__ dmeta) {
   const int lane = threadIdx.x;
-  float mmax = -1e30f;
-  for (int j = lane; j < n_meta; j += 64) mmax = fmaxf(mmax, meta[j]);
+  constexpr int U = 16;
+  const rsrc_t src = make_rsrc(part, (size_t)rows * 4);
+  const float m0 = lane < n_meta ? meta[lane] : -1e30f;
   float t = 0.f;
-  for (int r = lane; r < rows; r += 64) t += part[r];
+  for (int r0 = 0; r0 < rows; r0 += 64 * U) {
+    float x[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int r = r0 + 64 * u + lane;
+      x[u] = bload_f32(src, r < rows ? (uint32_t)r * 4u : OOB);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) t += x[u];
+  }
+  float mmax = fmaxf(-1e30f, m0);
+  for (int j = lane + 64; j < n_meta; j += 64) mmax = fmaxf(mmax, meta[j]);
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
     t += __shfl_xor(t, off);
     mmax = fmaxf(mmax, __shfl_xor(mmax, off));
   }
-  for (int j = lane; j < n_meta; j += 64) dmeta[j] = -fexp(meta[j] - mmax) * t;
+  if (lane < n_meta) dmeta[lane] = -fexp(m0 - mmax) * t;
+  for (int j = lane + 64; j < n_meta; j += 64) dmeta[j] = -fexp(meta[j] - mmax) * t;
 }
 
 // ----------------------------------------------------------------------------
