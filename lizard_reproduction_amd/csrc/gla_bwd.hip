@@ -1167,15 +1167,18 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
 // ============================================================================
 // d log_gamma[row, j] = sum_{j' >= j} value[row, j'], value = dG of that (b, h)
 // row (per-head gate) or its sum over the heads (per-token gate).  One wave
-// per (row, 64-token chunk), four chunks per workgroup, no barriers.  Lane t
+// per (row, 64-token chunk) and per workgroup, so the loads of a small grid
+// spread over as many CUs as there are chunks; no barriers.  Lane t
 // holds token t of the chunk summed over the heads; the chunk totals of the
 // later chunks (lanes over chunks, summed over the heads) come in alongside.
-// Loads go out in batches of 16 buffer loads (zero past the end) so one
-// memory round trip covers 16 heads; the sums over lanes are DPP scans.  Fixed
+// Loads go out in batches of BATCH buffer loads (zero past the end; BATCH
+// is the number of heads summed, rounded up to 8, at most 16), the gate
+// logit with the first batch; the sums over lanes are DPP scans.  Fixed
 // order throughout.
 // ============================================================================
-constexpr int GATE_CHUNKS_PER_WG = 4;
+constexpr int GATE_CHUNKS_PER_WG = 1;
 
+template <int BATCH>
 __global__ __launch_bounds__(64 * GATE_CHUNKS_PER_WG) void gla_gate_grad_kernel(
     const float* __restrict__ dG, const float* __restrict__ csum,
     const float* __restrict__ gate_in, float* __restrict__ dlg, int H, int L, int gate) {
@@ -1187,7 +1190,12 @@ __global__ __launch_bounds__(64 * GATE_CHUNKS_PER_WG) void gla_gate_grad_kernel(
   const rsrc_t src = make_rsrc(dG + (size_t)row * nsum * L, (size_t)nsum * L * 4);
   const rsrc_t cs = make_rsrc(csum + (size_t)row * nsum * NT, (size_t)nsum * NT * 4);
   const int j = c * GLA_C + lane;
-  constexpr int BATCH = 16;
+  const size_t at = (size_t)row * L + j;
+  // a buffer load (zero past the end, none without GATE_LOGIT): no branch
+  // around it, so nothing waits for it before the batches go out
+  const bool logit = (gate & GATE_LOGIT) != 0;
+  const rsrc_t gz = make_rsrc(logit ? gate_in + (size_t)row * L : nullptr, logit ? (size_t)L * 4 : 0);
+  const float z = bload_f32(gz, j < L ? (uint32_t)j * 4u : OOB);
   float val = 0.f, after = 0.f;
   for (int h0 = 0; h0 < nsum; h0 += BATCH) {
     float x[BATCH];
@@ -1208,11 +1216,8 @@ __global__ __launch_bounds__(64 * GATE_CHUNKS_PER_WG) void gla_gate_grad_kernel(
   after = wave_prefix_sum(after);
   after = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(after), 63));
   val = wave_suffix_sum(val, lane);   // inclusive suffix sum over the chunk
-  if (j < L) {
-    const size_t at = (size_t)row * L + j;
-    // GATE_LOGIT: the gradient of the logit z, d log_gamma * sigmoid(-z)
-    dlg[at] = (gate & GATE_LOGIT) ? (after + val) * sigmoid_neg(gate_in[at]) : after + val;
-  }
+  // GATE_LOGIT: the gradient of the logit z, d log_gamma * sigmoid(-z)
+  if (j < L) dlg[at] = (gate & GATE_LOGIT) ? (after + val) * sigmoid_neg(z) : after + val;
 }
 
 // ============================================================================
@@ -1327,7 +1332,12 @@ static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v
   const int nt = (L + GLA_C - 1) / GLA_C;
   const dim3 ggrid((nt + GATE_CHUNKS_PER_WG - 1) / GATE_CHUNKS_PER_WG,
                    gate_rows(B, H, gate));
-  hipLaunchKernelGGL(gla_gate_grad_kernel, ggrid, dim3(64 * GATE_CHUNKS_PER_WG), 0, st,
+  // loads per batch: the heads summed, rounded up to 8, at most 16
+  const int nsum = (gate & GATE_PER_HEAD) ? 1 : H;
+  auto kg = nsum == 1 ? gla_gate_grad_kernel<1>
+          : nsum <= 8 ? gla_gate_grad_kernel<8>
+          : gla_gate_grad_kernel<16>;
+  hipLaunchKernelGGL(kg, ggrid, dim3(64 * GATE_CHUNKS_PER_WG), 0, st,
                      (const float*)dG, (const float*)csum, lg, dlg, H, L, gate);
   return hipGetLastError();
 }
