@@ -23,7 +23,9 @@ def _expand(t, group):
     # per-token gate, F = 128: the kv-head records' state pass splits its feature
     # rows over two workgroups (120 segments), the expanded one does not (480)
     (1, 32, 8, 2048, 128, 128, False),
-    (16, 32, 8, 130, 128, 128, True),  # B*H fills the GPU: one walk per (b, h)
+    # B*H fills the GPU: one walk per (b, h); 512 walks run in two rounds, the
+    # dkv walk's blocks reversed per XCD, grouped (XCD-mapped) and expanded
+    (16, 32, 8, 130, 128, 128, True),
     # at most 4 segments: the walks fold the segment records (kv-head records
     # with a per-token gate; two segments per eight-wave walk at F = 256)
     (2, 64, 16, 500, 256, 64, False), (2, 64, 16, 500, 256, 64, True),
