@@ -64,6 +64,21 @@ def test_gla_without_grad_gives_the_same_output():
         assert torch.equal(kernels.gla(fq, fk, v, F.logsigmoid(z), 16), y)
 
 
+@pytest.mark.parametrize("gates", [(), (32,)])
+def test_gla_no_grad_walk_with_nontemporal_loads_gives_the_same_output(gates):
+    """Enough (b, h) to fill the GPU without segments (no forward workspace):
+    there the no-grad forward passes the no-reuse hint and its walk loads the
+    chunks nontemporally, while a forward kept for a backward loads them
+    normally.  The cache policy must not change a bit of y."""
+    from lizard_reproduction_amd import _lib
+    assert _lib.load().lz_gla_fwd_workspace_bytes(16, 32, 200, 128, 128, len(gates), 64) == 0
+    fq, fk, v, z = (t.cuda() for t in gla_inputs(200, gates=gates, batch=16, heads=32,
+                                                 features=128, dim=128))
+    y = kernels.gla(fq, fk, v.requires_grad_(), F.logsigmoid(z))
+    with torch.no_grad():
+        assert torch.equal(kernels.gla(fq, fk, v, F.logsigmoid(z)), y)
+
+
 def test_gla_is_deterministic():
     fq, fk, v, z = (t.cuda().requires_grad_() for t in gla_inputs(150, gates=(3,)))
     outs = []
