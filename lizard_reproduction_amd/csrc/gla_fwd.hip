@@ -992,7 +992,7 @@ __device__ __forceinline__ void load_chunk_strided(uint4 (&reg)[N], const bf16* 
 // column f of fk, so each takes its slice of fk's columns (and all of v) and
 // writes its rows of the record.  Used when the segments alone leave most of
 // the GPU idle (few kv heads with a shared gate).
-template <int FP, int DP, bool VEC, int FR>
+template <int FP, int DP, bool VEC, int FR, bool REV = false>
 __global__ __launch_bounds__(256, 2) void gla_fwd_state_kernel(
     const bf16* __restrict__ fk, const bf16* __restrict__ v, const float* __restrict__ log_gamma,
     float* __restrict__ seg_state, float* __restrict__ seg_logdecay, int H, int L, int F, int D,
@@ -1088,28 +1088,38 @@ __global__ __launch_bounds__(256, 2) void gla_fwd_state_kernel(
     }
   };
 
+  // REV walks the segment from its last chunk to its first: the record is
+  // S = sum_n dec_n K~_n^T V_n with dec_n the decay from the end of chunk n to
+  // the end of the segment (the product of the later chunks' decays), so each
+  // chunk's product is formed from zero and added scaled by dec_n.  The walk
+  // that follows reads each segment from its first chunk, which this pass then
+  // read last: when the segments' rows are more than the memory-side cache
+  // holds, those rows are the ones still in it as the walk starts (read in the
+  // walk's order, the walk's first rows are the first ones evicted).
   uint4 rk[Cfg::NLF], rv[Cfg::NLD];
-  float rg = gate_at(lgb, n0 * C + lane, L);   // the gate first: waited for alone
-  load_fk(rk, n0 * C);
-  load_chunk<DP>(rv, vb, n0 * C, L, D, vecD);
+  const int nf = REV ? n1 - 1 : n0;   // the first chunk this pass reads
+  float rg = gate_at(lgb, nf * C + lane, L);   // the gate first: waited for alone
+  load_fk(rk, nf * C);
+  load_chunk<DP>(rv, vb, nf * C, L, D, vecD);
   {
-    const int pb = n0 & 1;
+    const int pb = nf & 1;
     if (wave == 0)
       gate_scan(rg, lane, lgs + 64 * pb, qs + 64 * pb, ks + 64 * pb, rdec + 4 * pb, gate,
-                n0 * C + lane < L);
+                nf * C + lane < L);
     __syncthreads();
     stage_scaled(rk, ks + 64 * pb, zp + 2048 * pb);
     store_chunk<DP>(rv, v_l, PD);
     __syncthreads();
   }
 
-  for (int n = n0; n < n1; ++n) {
+  float dec = 1.f;   // REV: decay from the end of chunk n to the end of the segment
+  for (int n = nf; REV ? n >= n0 : n < n1; n += REV ? -1 : 1) {
     const int t0 = n * C;
-    const bool more = n + 1 < n1;
+    const bool more = REV ? n > n0 : n + 1 < n1;
     const int pc = n & 1, pn = pc ^ 1;   // this chunk's parity, the next one's
     // unconditional loads (past the segment they read rows past L: zeros, no
     // traffic), so the scan below waits for the gate alone
-    const int tn = more ? t0 + C : L;
+    const int tn = more ? (REV ? t0 - C : t0 + C) : L;
     rg = gate_at(lgb, tn + lane, L);
     load_fk(rk, tn);
     load_chunk<DP>(rv, vb, tn, L, D, vecD);
@@ -1121,12 +1131,22 @@ __global__ __launch_bounds__(256, 2) void gla_fwd_state_kernel(
       const int ti = wave + 4 * i;
       if (ti < NTILE) {
         const int ft = ti / NDT, dt = ti % NDT;
+        if constexpr (REV) {
+          f32x16 T = zero16();
 #pragma unroll
-        for (int r = 0; r < 16; ++r) S[i][r] *= r_n;
+          for (int kb = 0; kb < 4; ++kb)
+            T = mfma(tr_operand(fk_l, PF, 16 * kb, ft * 32, lane),
+                     tr_operand(v_l, PD, 16 * kb, dt * 32, lane), T);
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
-          S[i] = mfma(tr_operand(fk_l, PF, 16 * kb, ft * 32, lane),
-                      tr_operand(v_l, PD, 16 * kb, dt * 32, lane), S[i]);
+          for (int r = 0; r < 16; ++r) S[i][r] = __builtin_fmaf(dec, T[r], S[i][r]);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) S[i][r] *= r_n;
+#pragma unroll
+          for (int kb = 0; kb < 4; ++kb)
+            S[i] = mfma(tr_operand(fk_l, PF, 16 * kb, ft * 32, lane),
+                        tr_operand(v_l, PD, 16 * kb, dt * 32, lane), S[i]);
+        }
       }
     }
     if constexpr (NFS > 1) slice_parts(zp + 2048 * pc);
@@ -1137,12 +1157,18 @@ __global__ __launch_bounds__(256, 2) void gla_fwd_state_kernel(
     // staging and the next loads at raised wave priority, as in the walk
     __builtin_amdgcn_s_setprio(1);
     if constexpr (NFS == 1) {
-      if (tid < FP) zs[tid] = zs[tid] * r_n + sum_parts<FP>(zp + 2048 * pc, tid);
+      if (tid < FP) {
+        if constexpr (REV)
+          zs[tid] = __builtin_fmaf(dec, sum_parts<FP>(zp + 2048 * pc, tid), zs[tid]);
+        else
+          zs[tid] = zs[tid] * r_n + sum_parts<FP>(zp + 2048 * pc, tid);
+      }
     } else if (tid < FP) {
       float zc = 0.f;
       for (int p = 0; p < RR::PARTS; ++p) zc += zp[2048 * pc + p * FP + tid];
-      zs[tid] = zs[tid] * r_n + zc;
+      zs[tid] = REV ? __builtin_fmaf(dec, zc, zs[tid]) : zs[tid] * r_n + zc;
     }
+    if constexpr (REV) dec *= r_n;
     if (more) {
       stage_scaled(rk, ks + 64 * pn, zp + 2048 * pn);
       store_chunk<DP>(rv, v_l, PD);
@@ -1264,20 +1290,32 @@ hipError_t launch_gla_segment_scan(float* seg_state, const float* seg_logdecay, 
   return hipGetLastError();
 }
 
-// the state pass with the record's FR feature rows in slices of FS per workgroup
+// The state pass reads its segments' chunks from the last to the first (REV)
+// when those rows are more than half of the memory-side cache (256 MB on
+// MI355X), so that the walk starts on rows still cached; below that both
+// orders leave the rows cached and the forward loop is the cheaper one.
+constexpr size_t GLA_STATE_REV_BYTES = size_t(128) << 20;
+
+// the state pass with the record's FR feature rows in slices of FS per
+// workgroup; rev: the reverse chunk order (unsliced passes only: a sliced pass
+// has few segments, whose rows the cache holds)
 template <int FS, int FR, int DP, bool VEC>
 static hipError_t launch_state_slices(const void* fk, const void* v, const float* lg,
                                       float* seg_state, float* seg_logdecay, int BH, int H, int L,
-                                      int F, int D, int gate, int G, int cps, int KG,
+                                      int F, int D, int gate, int G, int cps, int KG, bool rev,
                                       hipStream_t st) {
   using Cfg = GlaState<FS, DP>;
-  auto ks = gla_fwd_state_kernel<FS, DP, VEC, FR>;
-  hipError_t e = ensure_lds<gla_fwd_state_kernel<FS, DP, VEC, FR>>(Cfg::BYTES);
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(ks, dim3(BH * (G - 1) * (FR / FS)), dim3(256), Cfg::BYTES, st,
-                     (const bf16*)fk, (const bf16*)v, lg, seg_state, seg_logdecay, H, L, F, D,
-                     gate, G, cps, KG);
-  return hipGetLastError();
+  auto launch = [&](auto tag) {
+    constexpr auto kern = decltype(tag)::value;
+    if (hipError_t e = ensure_lds<kern>(Cfg::BYTES); e != hipSuccess) return e;
+    hipLaunchKernelGGL(kern, dim3(BH * (G - 1) * (FR / FS)), dim3(256), Cfg::BYTES, st,
+                       (const bf16*)fk, (const bf16*)v, lg, seg_state, seg_logdecay, H, L, F, D,
+                       gate, G, cps, KG);
+    return hipGetLastError();
+  };
+  if constexpr (FS == FR)
+    if (rev) return launch(KernTag<gla_fwd_state_kernel<FS, DP, VEC, FR, true>>{});
+  return launch(KernTag<gla_fwd_state_kernel<FS, DP, VEC, FR>>{});
 }
 
 // Feature slices per segment: doubled while the state pass would still fill
@@ -1299,27 +1337,30 @@ static hipError_t launch_gla_fwd_states_t(const void* fk, const void* v, const f
     KG = 1;
   }
   const int nfs = gla_state_slices(BH * (G - 1), FP);
+  // the fk and v rows the pass reads (all segments but the last)
+  const size_t rows_bytes = (size_t)BH * (G - 1) * cps * GLA_C * (size_t)(F + D) * 2;
+  const bool rev = rows_bytes > GLA_STATE_REV_BYTES;
   hipError_t e;
   if constexpr (FP == 256) {
     if (nfs == 4)
       e = launch_state_slices<64, FP, DP, VEC>(fk, v, lg, seg_state, seg_logdecay, BH, H, L, F,
-                                               D, gate, G, cps, KG, st);
+                                               D, gate, G, cps, KG, rev, st);
     else if (nfs == 2)
       e = launch_state_slices<128, FP, DP, VEC>(fk, v, lg, seg_state, seg_logdecay, BH, H, L, F,
-                                                D, gate, G, cps, KG, st);
+                                                D, gate, G, cps, KG, rev, st);
     else
       e = launch_state_slices<FP, FP, DP, VEC>(fk, v, lg, seg_state, seg_logdecay, BH, H, L, F,
-                                               D, gate, G, cps, KG, st);
+                                               D, gate, G, cps, KG, rev, st);
   } else if constexpr (FP == 128) {
     if (nfs == 2)
       e = launch_state_slices<64, FP, DP, VEC>(fk, v, lg, seg_state, seg_logdecay, BH, H, L, F,
-                                               D, gate, G, cps, KG, st);
+                                               D, gate, G, cps, KG, rev, st);
     else
       e = launch_state_slices<FP, FP, DP, VEC>(fk, v, lg, seg_state, seg_logdecay, BH, H, L, F,
-                                               D, gate, G, cps, KG, st);
+                                               D, gate, G, cps, KG, rev, st);
   } else {
     e = launch_state_slices<FP, FP, DP, VEC>(fk, v, lg, seg_state, seg_logdecay, BH, H, L, F, D,
-                                             gate, G, cps, KG, st);
+                                             gate, G, cps, KG, rev, st);
   }
   if (e != hipSuccess) return e;
   if (fold) return hipSuccess;   // the walks fold the records
@@ -1445,6 +1486,9 @@ static hipError_t prepare_fwd_t() {
         hipSuccess)
       return e;
   }
+  if ((e = ensure_lds<gla_fwd_state_kernel<FP, DP, VEC, FP, true>>(GlaState<FP, DP>::BYTES)) !=
+      hipSuccess)   // the reverse-order pass
+    return e;
   return ensure_lds<gla_fwd_state_kernel<FP, DP, VEC, FP>>(GlaState<FP, DP>::BYTES);
 }
 

@@ -74,6 +74,23 @@ def test_config4_segmented_d128_walks_slices_match_chunked_oracle(batch, length,
                  f"config4 segmented B={batch} L={length}")
 
 
+@pytest.mark.parametrize("batch, length", [(1, 16384), (4, 8192)])
+def test_reverse_order_state_pass_gives_the_backward_the_same_records(batch, length):
+    """At these shapes the forward state pass reads more than 128 MB of fk
+    and v (251 and 403 MB), so it walks each segment from its last chunk to
+    its first.  The backward given the forward's records and the backward
+    that recomputes them must agree bit for bit; the slices above check the
+    same shapes against the oracle."""
+    fq, fk, v, lg, dy = baseline_gla_inputs(batch, 32, length, 128, True, 2.0, 1.5)
+    fq, fk, v, lg, dy = (t.cuda() for t in (fq, fk, v, lg, dy))
+    _, state = kernels.gla_forward(fq, fk, v, lg, keep_state=True)
+    assert state is not None   # segmented
+    kept = kernels.gla_backward(fq, fk, v, lg, dy, state, torch.bfloat16)
+    again = kernels.gla_backward(fq, fk, v, lg, dy, None, torch.bfloat16)
+    for name, a, b in zip(("dfq", "dfk", "dv", "dlog_gamma"), kept, again):
+        assert torch.equal(a, b), name
+
+
 def test_headline_shape_constant_values_stay_constant_everywhere():
     """y_i is a normalised average of v, so a constant v comes back (up to
     the bf16 rounding of the state operand) at every position of every
