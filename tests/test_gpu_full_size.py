@@ -74,6 +74,15 @@ def test_config4_segmented_d128_walks_slices_match_chunked_oracle(batch, length,
                  f"config4 segmented B={batch} L={length}")
 
 
+def test_reverse_order_state_pass_with_a_shared_gate_matches_chunked_oracle():
+    """B=1 L=16384 F=D=128 with one gate per token (config 2's gate on the
+    config-4 shape): the forward state pass walks its segments from the last
+    chunk (251 MB of fk and v rows), scanning the shared gate row backwards;
+    output and gradients of sampled slices against the chunked fp64 oracle."""
+    check_slices(1, 32, 16384, 128, False, 3.0, 1.0, [(0, 2), (0, 27)],
+                 "config4 shape, per-token gate, B=1 L=16384")
+
+
 @pytest.mark.parametrize("batch, length", [(1, 16384), (4, 8192)])
 def test_reverse_order_state_pass_gives_the_backward_the_same_records(batch, length):
     """At these shapes the forward state pass reads more than 128 MB of fk
