@@ -34,6 +34,9 @@
 //      per-token gate), one launch (gla_gate_grad_kernel) from dG and the
 //      per-chunk dG totals kernel B writes; with a per-head gate and G = 1
 //      kernel B, whose reverse walk sees the whole row, writes it instead.
+//   With G = 1, A and B of a (b, h) run in one workgroup, B right after A
+//   (gla_bwd_fused_kernel): B then needs only that workgroup's den, delta and
+//   p, and starts on the chunks A read last.
 // Operand staging follows gla_fwd.hip: row-major tiles in LDS, operands that
 // contract over tokens from LDS transpose reads, next chunk prefetched into
 // registers.
@@ -168,7 +171,7 @@ __device__ __forceinline__ void z_update(float* zn, const float* zs, const float
 // the caller has put those of the whole feature dimension; the kernel then
 // writes this tile's share of every gradient.
 template <int FP, int DP, typename OutT, bool VEC, bool EXT, bool FOLD = false>
-__global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
+__device__ __forceinline__ void gla_bwd_dq_body(
     const bf16* __restrict__ fq, const bf16* __restrict__ fk, const bf16* __restrict__ v,
     const float* __restrict__ log_gamma, const bf16* __restrict__ dy, OutT* __restrict__ dfq,
     float* __restrict__ den_out, float* __restrict__ delta_out, float* __restrict__ p_out,
@@ -548,6 +551,18 @@ __global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
   }
 }
 
+template <int FP, int DP, typename OutT, bool VEC, bool EXT, bool FOLD = false>
+__global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_dq_kernel(
+    const bf16* __restrict__ fq, const bf16* __restrict__ fk, const bf16* __restrict__ v,
+    const float* __restrict__ log_gamma, const bf16* __restrict__ dy, OutT* __restrict__ dfq,
+    float* __restrict__ den_out, float* __restrict__ delta_out, float* __restrict__ p_out,
+    const float* __restrict__ seg_state, int H, int L, int F, int D, int gate, int G,
+    int cps, int M, int KG, int xper, int nxcd, int nblk, const float* __restrict__ seg_lam) {
+  gla_bwd_dq_body<FP, DP, OutT, VEC, EXT, FOLD>(fq, fk, v, log_gamma, dy, dfq, den_out, delta_out,
+                                                 p_out, seg_state, H, L, F, D, gate, G, cps, M,
+                                                 KG, xper, nxcd, nblk, seg_lam);
+}
+
 // ============================================================================
 // per-token scalars of the reverse walks: the gate scan of a chunk plus
 // den (clamped), delta, p and Q^ scale qs/den, by one wave (lane = token)
@@ -799,7 +814,7 @@ struct BwdB : BwdCommon<FP, DP> {
 };
 
 template <int FP, int DP, typename OutT, bool VEC, bool FOLD = false>
-__global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_kernel(
+__device__ __forceinline__ void gla_bwd_dkv_body(
     const bf16* __restrict__ fq, const bf16* __restrict__ fk, const bf16* __restrict__ v,
     const float* __restrict__ log_gamma, const bf16* __restrict__ dy,
     const float* __restrict__ den_in, const float* __restrict__ delta_in,
@@ -1164,6 +1179,43 @@ __global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_ker
   }
 }
 
+template <int FP, int DP, typename OutT, bool VEC, bool FOLD = false>
+__global__ __launch_bounds__(B_THREADS, (BwdB<FP, DP>::LB)) void gla_bwd_dkv_kernel(
+    const bf16* __restrict__ fq, const bf16* __restrict__ fk, const bf16* __restrict__ v,
+    const float* __restrict__ log_gamma, const bf16* __restrict__ dy,
+    const float* __restrict__ den_in, const float* __restrict__ delta_in,
+    const float* __restrict__ p_in, OutT* __restrict__ dfk, OutT* __restrict__ dv,
+    float* __restrict__ dG, float* __restrict__ csum, float* __restrict__ dlg_direct,
+    const float* __restrict__ seg_state, int H,
+    int L, int F, int D, int gate, int G, int cps, int M, int KG, int xper, int nxcd,
+    int nblk, const float* __restrict__ seg_lam, int rev) {
+  gla_bwd_dkv_body<FP, DP, OutT, VEC, FOLD>(fq, fk, v, log_gamma, dy, den_in, delta_in, p_in, dfk,
+                                            dv, dG, csum, dlg_direct, seg_state, H, L, F, D, gate,
+                                            G, cps, M, KG, xper, nxcd, nblk, seg_lam, rev);
+}
+
+// One segment per (b, h): the dq walk and then the dkv walk of the same
+// (b, h) in one workgroup.  The dkv walk starts on the chunks the dq walk
+// read last, still in the caches, and needs only this workgroup's own den,
+// delta and p rows (a workgroup-scope fence and barrier order them).
+template <int FP, int DP, typename OutT, bool VEC>
+__global__ __launch_bounds__(B_THREADS, 1) void gla_bwd_fused_kernel(
+    const bf16* __restrict__ fq, const bf16* __restrict__ fk, const bf16* __restrict__ v,
+    const float* __restrict__ log_gamma, const bf16* __restrict__ dy, OutT* __restrict__ dfq,
+    OutT* __restrict__ dfk, OutT* __restrict__ dv, float* __restrict__ den,
+    float* __restrict__ delta, float* __restrict__ p, float* __restrict__ dG,
+    float* __restrict__ csum, float* __restrict__ dlg_direct, int H, int L, int F, int D,
+    int gate, int cps, int KG, int xper, int nxcd, int nblk) {
+  gla_bwd_dq_body<FP, DP, OutT, VEC, false>(fq, fk, v, log_gamma, dy, dfq, den, delta, p, nullptr,
+                                            H, L, F, D, gate, 1, cps, 1, KG, xper, nxcd, nblk,
+                                            nullptr);
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+  __syncthreads();
+  gla_bwd_dkv_body<FP, DP, OutT, VEC>(fq, fk, v, log_gamma, dy, den, delta, p, dfk, dv, dG, csum,
+                                      dlg_direct, nullptr, H, L, F, D, gate, 1, cps, 1, KG, xper,
+                                      nxcd, nblk, nullptr, 0);
+}
+
 // ============================================================================
 // d log_gamma[row, j] = sum_{j' >= j} value[row, j'], value = dG of that (b, h)
 // row (per-head gate) or its sum over the heads (per-token gate).  One wave
@@ -1278,6 +1330,31 @@ static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v
   const int M = (G % 2 == 0 && BH * G / 2 >= device_geom().cus) ? 2 : 1;
   const WalkGrid wg = walk_grid(BH * G / M, KG);
   const float* flam = fseg + (size_t)BH * G * SEG;
+  // One segment per (b, h): the dq and dkv walks of a (b, h) run in one
+  // workgroup, one after the other (gla_bwd_fused_kernel): one launch, and
+  // the dkv walk starts on the chunks the dq walk read last, in every round
+  // of workgroups (headline fwd+bwd 0.8808 -> 0.8628 ms, same bits).
+  if (G == 1 && !ext) {
+    const bool direct = (gate & GATE_PER_HEAD) != 0;
+    auto kf = gla_bwd_fused_kernel<FP, DP, OutT, VEC>;
+    constexpr int LDS_F = LDS_A > LDS_B ? LDS_A : LDS_B;
+    if ((e = ensure_lds<gla_bwd_fused_kernel<FP, DP, OutT, VEC>>(LDS_F)) != hipSuccess) return e;
+    hipLaunchKernelGGL(kf, dim3(wg.grid), dim3(B_THREADS), LDS_F, st, (const bf16*)fq,
+                       (const bf16*)fk, (const bf16*)v, lg, (const bf16*)dy, (OutT*)dfq,
+                       (OutT*)dfk, (OutT*)dv, den, delta, p, dG, csum, direct ? dlg : nullptr,
+                       H, L, F, D, gate, cps, KG, wg.per, wg.nx, wg.nblk);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if (direct) return hipSuccess;
+    const int nt = (L + GLA_C - 1) / GLA_C;
+    const dim3 ggrid((nt + GATE_CHUNKS_PER_WG - 1) / GATE_CHUNKS_PER_WG, gate_rows(B, H, gate));
+    const int nsum = (gate & GATE_PER_HEAD) ? 1 : H;
+    auto kg = nsum == 1 ? gla_gate_grad_kernel<1>
+            : nsum <= 8 ? gla_gate_grad_kernel<8>
+            : gla_gate_grad_kernel<16>;
+    hipLaunchKernelGGL(kg, ggrid, dim3(64 * GATE_CHUNKS_PER_WG), 0, st,
+                       (const float*)dG, (const float*)csum, lg, dlg, H, L, gate);
+    return hipGetLastError();
+  }
   auto launch_a = [&](auto tag) {
     constexpr auto kern = decltype(tag)::value;
     if (hipError_t e2 = ensure_lds<kern>(LDS_A); e2 != hipSuccess) return e2;
@@ -1310,8 +1387,9 @@ static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v
   const bool direct_dlg = (gate & GATE_PER_HEAD) && G == 1;
   // more workgroups than CUs (one walk workgroup per CU): the dkv walk runs in
   // rounds, and takes its blocks in reverse so that its first round starts on
-  // the rows the dq walk read last (headline fwd+bwd -0.9 %, B=16 L=4096
-  // -0.7 %; a one-round launch gains nothing from the order)
+  // the rows the dq walk read last (measured on the unsegmented headline
+  // before those ran fused: fwd+bwd -0.9 %; a one-round launch gains nothing
+  // from the order)
   const int rev = wg.grid > device_geom().cus;
   auto launch_b = [&](auto tag) {
     constexpr auto kern = decltype(tag)::value;

@@ -193,6 +193,17 @@ def test_gla_walks_fold_few_segments(batch, heads, length, features, dim, per_he
             inputs, grad, label=f"folded segments F={features} D={dim} B*H={batch * heads}")
 
 
+def test_gla_segmented_dkv_walk_in_rounds_matches_oracle():
+    # B*H = 100 with 10 chunks: 5 segments of 2 chunks per (b, h) and 500
+    # dkv-walk workgroups at one per CU, so that walk runs in rounds and takes
+    # its blocks in reverse launch order per XCD
+    inputs = gla_inputs(600, gates=(50,), batch=2, heads=50, features=64, dim=64, seed=17)
+    grad = torch.randn(inputs[2].shape, generator=torch.Generator().manual_seed(4))
+    compare(gla_kernel(64), lambda *a: lo.gla_chunked(*a[:3], F.logsigmoid(a[3]), chunk=64,
+                                                      dtype=torch.float32),
+            inputs, grad, label="dkv walk in rounds B*H=100 L=600")
+
+
 def test_gla_backward_without_forward_workspace_is_bitwise_equal():
     # through the C ABI: lz_gla_bwd given no forward workspace recomputes the
     # state entering each segment; the gradients must be the same bits as the

@@ -23,9 +23,12 @@ def _expand(t, group):
     # per-token gate, F = 128: the kv-head records' state pass splits its feature
     # rows over two workgroups (120 segments), the expanded one does not (480)
     (1, 32, 8, 2048, 128, 128, False),
-    # B*H fills the GPU: one walk per (b, h); 512 walks run in two rounds, the
-    # dkv walk's blocks reversed per XCD, grouped (XCD-mapped) and expanded
+    # B*H fills the GPU: one segment per (b, h), whose dq and dkv walks run in
+    # one workgroup (512 of them, two rounds), grouped (XCD-mapped) and expanded
     (16, 32, 8, 130, 128, 128, True),
+    # 5 segments per (b, h) and 500 dkv-walk workgroups at one per CU: the
+    # dkv walk runs in rounds and takes its blocks in reverse per XCD
+    (2, 50, 10, 600, 64, 64, False),
     # at most 4 segments: the walks fold the segment records (kv-head records
     # with a per-token gate; two segments per eight-wave walk at F = 256)
     (2, 64, 16, 500, 256, 64, False), (2, 64, 16, 500, 256, 64, True),
