@@ -1289,6 +1289,21 @@ size_t gla_bwd_workspace(int B, int H, int L, int F, int D, int gate) {
          sizeof(float);
 }
 
+// d log_gamma from dG and the per-chunk dG totals: one wave per (row,
+// chunk), BATCH loads per batch (the heads summed, rounded up to 8, at most 16)
+static hipError_t launch_gate_grad(const float* dG, const float* csum, const float* lg,
+                                   float* dlg, int B, int H, int L, int gate, hipStream_t st) {
+  const int nt = (L + GLA_C - 1) / GLA_C;
+  const dim3 ggrid((nt + GATE_CHUNKS_PER_WG - 1) / GATE_CHUNKS_PER_WG, gate_rows(B, H, gate));
+  const int nsum = (gate & GATE_PER_HEAD) ? 1 : H;
+  auto kg = nsum == 1 ? gla_gate_grad_kernel<1>
+          : nsum <= 8 ? gla_gate_grad_kernel<8>
+          : gla_gate_grad_kernel<16>;
+  hipLaunchKernelGGL(kg, ggrid, dim3(64 * GATE_CHUNKS_PER_WG), 0, st, dG, csum, lg, dlg, H, L,
+                     gate);
+  return hipGetLastError();
+}
+
 template <int FP, int DP, typename OutT, bool VEC>
 static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v, const float* lg,
                                    const void* dy, void* dfq, void* dfk, void* dv, float* dlg,
@@ -1334,26 +1349,20 @@ static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v
   // workgroup, one after the other (gla_bwd_fused_kernel): one launch, and
   // the dkv walk starts on the chunks the dq walk read last, in every round
   // of workgroups (headline fwd+bwd 0.8808 -> 0.8628 ms, same bits).
+  // a per-head gate in one segment: the reverse walk of (b, h) sees its whole
+  // gate row and writes d log_gamma itself (no gate launch, no dG)
+  const bool direct_dlg = (gate & GATE_PER_HEAD) && G == 1;
   if (G == 1 && !ext) {
-    const bool direct = (gate & GATE_PER_HEAD) != 0;
     auto kf = gla_bwd_fused_kernel<FP, DP, OutT, VEC>;
     constexpr int LDS_F = LDS_A > LDS_B ? LDS_A : LDS_B;
     if ((e = ensure_lds<gla_bwd_fused_kernel<FP, DP, OutT, VEC>>(LDS_F)) != hipSuccess) return e;
     hipLaunchKernelGGL(kf, dim3(wg.grid), dim3(B_THREADS), LDS_F, st, (const bf16*)fq,
                        (const bf16*)fk, (const bf16*)v, lg, (const bf16*)dy, (OutT*)dfq,
-                       (OutT*)dfk, (OutT*)dv, den, delta, p, dG, csum, direct ? dlg : nullptr,
-                       H, L, F, D, gate, cps, KG, wg.per, wg.nx, wg.nblk);
+                       (OutT*)dfk, (OutT*)dv, den, delta, p, dG, csum,
+                       direct_dlg ? dlg : nullptr, H, L, F, D, gate, cps, KG, wg.per, wg.nx,
+                       wg.nblk);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    if (direct) return hipSuccess;
-    const int nt = (L + GLA_C - 1) / GLA_C;
-    const dim3 ggrid((nt + GATE_CHUNKS_PER_WG - 1) / GATE_CHUNKS_PER_WG, gate_rows(B, H, gate));
-    const int nsum = (gate & GATE_PER_HEAD) ? 1 : H;
-    auto kg = nsum == 1 ? gla_gate_grad_kernel<1>
-            : nsum <= 8 ? gla_gate_grad_kernel<8>
-            : gla_gate_grad_kernel<16>;
-    hipLaunchKernelGGL(kg, ggrid, dim3(64 * GATE_CHUNKS_PER_WG), 0, st,
-                       (const float*)dG, (const float*)csum, lg, dlg, H, L, gate);
-    return hipGetLastError();
+    return direct_dlg ? hipSuccess : launch_gate_grad(dG, csum, lg, dlg, B, H, L, gate, st);
   }
   auto launch_a = [&](auto tag) {
     constexpr auto kern = decltype(tag)::value;
@@ -1382,9 +1391,6 @@ static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v
     if (!fold && (e = launch_gla_segment_scan(rseg, rlam, BH, G, SEG, true, st)) != hipSuccess)
       return e;
   }
-  // a per-head gate in one segment: the reverse walk of (b, h) sees its whole
-  // gate row and writes d log_gamma itself (no gate launch, no dG)
-  const bool direct_dlg = (gate & GATE_PER_HEAD) && G == 1;
   // more workgroups than CUs (one walk workgroup per CU): the dkv walk runs in
   // rounds, and takes its blocks in reverse so that its first round starts on
   // the rows the dq walk read last (measured on the unsegmented headline
@@ -1406,18 +1412,7 @@ static hipError_t launch_gla_bwd_t(const void* fq, const void* fk, const void* v
   else
     e = launch_b(KernTag<gla_bwd_dkv_kernel<FP, DP, OutT, VEC>>{});
   if (e != hipSuccess) return e;
-  if (direct_dlg) return hipSuccess;
-  const int nt = (L + GLA_C - 1) / GLA_C;
-  const dim3 ggrid((nt + GATE_CHUNKS_PER_WG - 1) / GATE_CHUNKS_PER_WG,
-                   gate_rows(B, H, gate));
-  // loads per batch: the heads summed, rounded up to 8, at most 16
-  const int nsum = (gate & GATE_PER_HEAD) ? 1 : H;
-  auto kg = nsum == 1 ? gla_gate_grad_kernel<1>
-          : nsum <= 8 ? gla_gate_grad_kernel<8>
-          : gla_gate_grad_kernel<16>;
-  hipLaunchKernelGGL(kg, ggrid, dim3(64 * GATE_CHUNKS_PER_WG), 0, st,
-                     (const float*)dG, (const float*)csum, lg, dlg, H, L, gate);
-  return hipGetLastError();
+  return direct_dlg ? hipSuccess : launch_gate_grad(dG, csum, lg, dlg, B, H, L, gate, st);
 }
 
 // ext_den / ext_delta: nullptr, or (one F tile of a split feature
