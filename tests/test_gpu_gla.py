@@ -102,6 +102,20 @@ def test_gla_fp32_inputs_give_fp32_grads():
     assert all(t.grad.dtype == torch.float32 for t in leaves + [lg])
 
 
+@pytest.mark.parametrize("gates", [(64,), ()])
+def test_gla_one_segment_fp32_grads_match_oracle(gates):
+    # B*H = 512 fills the GPU without segments: the dq and dkv walks of each
+    # (b, h) run in one workgroup, here writing fp32 gradients (fp32 inputs)
+    inputs = gla_inputs(100, gates=gates, batch=8, heads=64, features=32, dim=32, seed=23)
+    inputs = [t.float() if t.dtype == torch.bfloat16 else t for t in inputs]
+    grad = torch.randn(inputs[2].shape, generator=torch.Generator().manual_seed(5))
+    from lizard_reproduction_amd import _lib
+    assert _lib.load().lz_gla_fwd_workspace_bytes(8, 64, 100, 32, 32, len(gates), 64) == 0
+    compare(gla_kernel(64), lambda *a: lo.gla_chunked(*a[:3], F.logsigmoid(a[3]), chunk=64,
+                                                      dtype=torch.float32),
+            inputs, grad, label=f"one segment fp32 grads gates={gates}")
+
+
 def _baseline_case(batch, heads, length, dim, per_head, gate_mean, gate_std, oracle):
     fq, fk, v, lg, dy = baseline_gla_inputs(batch, heads, length, dim, per_head,
                                             gate_mean, gate_std)
