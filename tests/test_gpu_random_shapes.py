@@ -379,3 +379,34 @@ def test_gla_random_segmented_walks_match_chunked_oracle(case):
     for k, e in worst.items():
         if k != "y":
             assert e <= GRAD_TOL, (case, k, worst)
+
+
+def _wide_and_long_cases(seed=16384):
+    """Draws past the segmented range: B*H of 512-1024 (one segment per row,
+    so the dq and dkv walks of a row run in one workgroup) and single batch
+    rows of 32 heads with L of 12000-16384 (fk and v rows past half the
+    memory-side cache, so the forward state pass walks its segments from the
+    last chunk)."""
+    rng = random.Random(seed)
+    cases = []
+    for _ in range(4):
+        features, dim = rng.choice([(64, 64), (128, 128), (256, 64), (32, 128), (100, 72)])
+        b = rng.choice([1, 2, 4, 8])
+        cases.append(dict(batch=b, heads=rng.choice([512, 768, 1024]) // b,
+                          length=rng.randint(40, 700), features=features, dim=dim,
+                          per_head=rng.random() < 0.5, seed=rng.randint(0, 10 ** 6)))
+    for _ in range(2):
+        features, dim = rng.choice([(128, 128), (128, 64), (64, 128)])
+        cases.append(dict(batch=1, heads=32, length=rng.randint(12000, 16384),
+                          features=features, dim=dim, per_head=rng.random() < 0.5,
+                          seed=rng.randint(0, 10 ** 6)))
+    return cases
+
+
+WIDE_AND_LONG_CASES = _wide_and_long_cases()
+
+
+@pytest.mark.parametrize("case", WIDE_AND_LONG_CASES, ids=[_label(c) for c in WIDE_AND_LONG_CASES])
+def test_gla_random_one_segment_and_long_rows_match_chunked_oracle(case):
+    """The check above on the draws of ``_wide_and_long_cases``."""
+    test_gla_random_segmented_walks_match_chunked_oracle(case)
